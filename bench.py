@@ -1,0 +1,221 @@
+"""Benchmark of the Kandle hot path on one MI355X.
+
+Headline (BASELINE.json metric): causal GQA flash-attention prefill TFLOP/s on config C3
+(B=4, Hq=16, Hkv=8, S=4096, D=128, bf16, fp32 accumulate).  A "step" is one prefill call over that
+batch with inputs resident in HBM.  The same run also measures decode attention (config C4: B=8,
+Hq=16, Hkv=8, D=128, per-sequence KV lengths ~ U[8192, 32768]) in HBM GB/s and the fused RMSNorm +
+qk-norm + RoPE (config C2) in GB/s, each against its roofline, and times the CPU oracle's flash
+algorithm on a bounded sample as the CPU baseline.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--only prefill|decode|norm]
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+METRIC = "flash-attn prefill TFLOP/s (%MFMA peak) S=4096; decode-attn HBM GB/s @32k KV"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def bf16_tensor(seed, shape):
+    from kandle_amd import Tensor
+    from kandle_amd import synthetic as syn
+
+    bits, _ = syn.bf16(syn.normal(seed, shape))
+    return Tensor(bits, dtype="bfloat16")
+
+
+def time_calls(fn, steps, warmup):
+    """(wall ms per call, device ms per call from HIP events on the library stream)."""
+    from kandle_amd import _lib
+
+    for _ in range(warmup):
+        fn()
+    _lib.synchronize()
+    e0, e1 = _lib.Event(), _lib.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    _lib.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_ms(e1) / steps
+
+
+def bench_prefill(steps, warmup):
+    from kandle_amd import HipTensorHandle, kernels
+
+    B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
+    q = bf16_tensor(301, (B, Hq, S, D))
+    k = bf16_tensor(302, (B, Hkv, S, D))
+    v = bf16_tensor(303, (B, Hkv, S, D))
+    o = HipTensorHandle.create_new((B, Hq, S, D), "bfloat16")
+    scale = 1.0 / np.sqrt(D)
+    fn = lambda: kernels.flash_attention(q.handle, k.handle, v.handle, o, scale, True)  # noqa: E731
+    wall_ms, dev_ms = time_calls(fn, steps, warmup)
+    flops = 4.0 * B * Hq * S * S * D / 2.0
+    out = o.data_async()
+    assert np.all(np.isfinite(out)), "prefill produced non-finite values"
+    for t in (q, k, v):
+        t.dispose()
+    o.dispose()
+    return {"B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D, "flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+
+def bench_decode(steps, warmup):
+    from kandle_amd import HipTensorHandle, Tensor, kernels
+    from kandle_amd import synthetic as syn
+
+    B, Hq, Hkv, D, ML = 8, 16, 8, 128, 32768
+    lens = syn.randint(2024, (B,), 8192, 32769)
+    q = bf16_tensor(401, (B, Hq, D))
+    kc = bf16_tensor(402, (B, Hkv, ML, D))
+    vc = bf16_tensor(403, (B, Hkv, ML, D))
+    sl = Tensor(lens, dtype="int32")
+    o = HipTensorHandle.create_new((B, Hq, D), "bfloat16")
+    scale = 1.0 / np.sqrt(D)
+    fn = lambda: kernels.decode_attention(q.handle, kc.handle, vc.handle, sl.handle, o, scale)  # noqa: E731
+    wall_ms, dev_ms = time_calls(fn, steps, warmup)
+    kv_bytes = float(lens.sum()) * Hkv * D * 2 * 2
+    for t in (q, kc, vc, sl):
+        t.dispose()
+    o.dispose()
+    return {"B": B, "sum_len": int(lens.sum()), "bytes": kv_bytes, "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+
+def bench_norm_rope(steps, warmup):
+    from kandle_amd import HipTensorHandle, Tensor, kernels
+    from kandle_amd import synthetic as syn
+
+    T, Hq, Hkv, D, H = 8192, 16, 8, 128, 1024
+    x = bf16_tensor(501, (T, H))
+    q = bf16_tensor(502, (1, T, Hq, D))
+    k = bf16_tensor(503, (1, T, Hkv, D))
+    w = Tensor(syn.bf16(syn.uniform(504, (H,), 0.5, 1.5))[0], dtype="bfloat16")
+    wq = Tensor(syn.bf16(syn.uniform(505, (D,), 0.5, 1.5))[0], dtype="bfloat16")
+    wk = Tensor(syn.bf16(syn.uniform(506, (D,), 0.5, 1.5))[0], dtype="bfloat16")
+    half = D // 2
+    inv = np.array([1.0 / (1e6 ** (i / half)) for i in range(half)], np.float64).astype(np.float32)
+    invt = Tensor(inv)
+    pos = Tensor(np.arange(T, dtype=np.int32), dtype="int32")
+    y = HipTensorHandle.create_new((T, H), "bfloat16")
+    qo = HipTensorHandle.create_new((1, Hq, T, D), "bfloat16")
+    ko = HipTensorHandle.create_new((1, Hkv, T, D), "bfloat16")
+    params = {"q_weight": wq.handle, "k_weight": wk.handle, "inv_freq": invt.handle, "positions": pos.handle,
+              "eps": 1e-6, "q_out": qo, "k_out": ko}
+    norm_params = {"normalized_shape": [H], "eps": 1e-6, "weight": w.handle, "out": y}
+
+    def fn():
+        kernels.rms_norm([x.handle], norm_params)
+        kernels.rms_norm_rope(q.handle, k.handle, params)
+
+    wall_ms, dev_ms = time_calls(fn, steps, warmup)
+    bytes_ = 2 * T * H * 2 + H * 2 + 2 * (T * Hq * D + T * Hkv * D) * 2 + 2 * D * 2
+    return {"T": T, "bytes": float(bytes_), "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+
+def cpu_baseline_prefill(n_slices=1):
+    """The oracle's float32 port of the reference flash algorithm on n (b, head) slices of C3."""
+    import oracle
+    from kandle_amd import synthetic as syn
+
+    S, D = 4096, 128
+    q = syn.normal(601, (1, 1, S, D))
+    k = syn.normal(602, (1, 1, S, D))
+    v = syn.normal(603, (1, 1, S, D))
+    t0 = time.perf_counter()
+    for _ in range(n_slices):
+        oracle.flash_f32(q, k, v, causal=True)
+    dt = time.perf_counter() - t0
+    flops = n_slices * 4.0 * S * S * D / 2.0
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{n_slices} of 64 (batch, q-head) slices of C3 at full S=4096, causal, fp32, "
+                      f"single thread ({dt:.1f} s); host has {os.cpu_count()} cores"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode", "norm"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from kandle_amd import HipBackend
+
+    HipBackend.create(0)
+    res = {}
+    if args.only in (None, "prefill"):
+        log("prefill C3 ...")
+        res["prefill"] = bench_prefill(args.steps, args.warmup)
+    if args.only in (None, "decode"):
+        log("decode C4 ...")
+        res["decode"] = bench_decode(args.steps, args.warmup)
+    if args.only in (None, "norm"):
+        log("norm+rope C2 ...")
+        res["norm"] = bench_norm_rope(args.steps, args.warmup)
+    cpu = None
+    if not args.no_cpu_baseline and args.only in (None, "prefill"):
+        log("cpu baseline ...")
+        cpu = cpu_baseline_prefill(1)
+
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded Philox N(0,1))"}
+    if "prefill" in res:
+        p = res["prefill"]
+        tflops = p["flops"] / (p["wall_ms"] * 1e-3) / 1e12
+        achieved = p["flops"] / (p["dev_ms"] * 1e-3) / 1e12
+        line.update({
+            "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(p["wall_ms"], 4),
+            "config": {"workload": "C3 causal GQA flash-attention prefill", "batch": p["B"], "q_heads": p["Hq"],
+                       "kv_heads": p["Hkv"], "seq_len": p["S"], "head_dim": p["D"]},
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                         "kernel": "flash_fwd_bf16_d128_kernel", "kernel_ms": round(p["dev_ms"], 4)},
+        })
+    if "decode" in res:
+        d = res["decode"]
+        gbps = d["bytes"] / (d["dev_ms"] * 1e-3) / 1e9
+        line["decode"] = {"workload": "C4 decode attention, B=8, Hq=16, Hkv=8, D=128, L~U[8192,32768]",
+                          "sum_len": d["sum_len"], "bytes": d["bytes"], "ms": round(d["dev_ms"], 4),
+                          "wall_ms": round(d["wall_ms"], 4), "GB/s": round(gbps, 1),
+                          "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
+                                       "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4)}}
+        if "value" not in line:
+            line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(d["wall_ms"], 4),
+                         "config": {"workload": "C4 decode attention"}})
+    if "norm" in res:
+        n = res["norm"]
+        gbps = n["bytes"] / (n["dev_ms"] * 1e-3) / 1e9
+        line["norm_rope"] = {"workload": "C2 RMSNorm + qk-norm + RoPE, T=8192, bf16", "bytes": n["bytes"],
+                             "ms": round(n["dev_ms"], 4), "GB/s": round(gbps, 1),
+                             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
+                                          "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4)}}
+        if "value" not in line:
+            line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(n["wall_ms"], 4),
+                         "config": {"workload": "C2 norm + rope"}})
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

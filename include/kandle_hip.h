@@ -1,0 +1,190 @@
+/*
+ * kandle_hip.h — C ABI of the MI355X (gfx950) backend for Kandle's transformer hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and element strides (no torch or
+ * Node types), enqueues its work on the library's single HIP stream and returns 0 on success or a
+ * non-zero error code whose text `kh_last_error()` returns.  Work is asynchronous: only
+ * `kh_memcpy_d2h` and `kh_synchronize` wait for the device, mirroring Kandle's "kernels enqueue,
+ * readback syncs" contract (reference: packages/backend-webgpu/src/kernels/attention/executor.ts:162-168
+ * submits without waiting; packages/backend-webgpu/src/base/storage.ts:191-229 is the only wait).
+ *
+ * Strides and offsets are in ELEMENTS, as in Kandle's ITensorHandle
+ * (reference: packages/types/src/tensor.ts:6-55; packages/backend-webgpu/src/kernels/matrix/executor.ts:141).
+ * The innermost dimension of every tensor argument is contiguous (stride 1): host code materialises
+ * any other view with kh_copy_strided first.
+ *
+ * dtype codes: KH_F32 = 0, KH_BF16 = 1, KH_I32 = 2.  bf16 is an extension of the reference API,
+ * which has no bfloat16 DType (reference: packages/types/src/base.ts:5-25); it is the 16 high bits
+ * of an IEEE float32, rounded to nearest even.
+ */
+#ifndef KANDLE_HIP_H
+#define KANDLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KH_F32 0
+#define KH_BF16 1
+#define KH_I32 2
+
+#define KH_OK 0
+#define KH_ERR_INVALID 1   /* bad argument: shape, dtype, stride or pointer */
+#define KH_ERR_HIP 2       /* a HIP runtime call failed */
+#define KH_ERR_NOT_INIT 3  /* kh_init was not called */
+#define KH_ERR_OOM 4       /* device allocation failed even after emptying the cache */
+
+/* ------------------------------------------------------------------ runtime ------------------ */
+
+/* Selects `device`, creates the library stream (default priority) and its events.
+ * Replaces WebGPUDeviceManager.init (reference: packages/backend-webgpu/src/base/device.ts:95-176)
+ * as called from WebGPUBackend.create (packages/backend-webgpu/src/index.ts:73-85). */
+int kh_init(int device);
+
+/* Number of visible HIP devices (0 on a host without a GPU; never fails for lack of a GPU). */
+int kh_device_count(int* count);
+
+/* Text of the most recent error on the calling thread ("" when none). */
+const char* kh_last_error(void);
+
+/* Caching device allocator (size classes, stream-ordered reuse on the single library stream).
+ * Replaces WebGPUStorage's GPUBuffer creation/destroy and its buffer pooling
+ * (reference: packages/backend-webgpu/src/base/storage.ts:68-106, :114-143). */
+int kh_alloc(void** ptr, size_t bytes);
+int kh_free(void* ptr);
+int kh_empty_cache(void);
+
+typedef struct kh_alloc_stats {
+  uint64_t live_bytes;    /* bytes handed out and not yet freed */
+  uint64_t cached_bytes;  /* bytes held in the free lists */
+  uint64_t peak_bytes;    /* maximum of live_bytes */
+  uint64_t n_device_allocs;  /* hipMalloc calls made */
+  uint64_t n_cache_hits;     /* kh_alloc calls served from the free lists */
+} kh_alloc_stats;
+/* Mirrors the live-bytes statistics of the reference storage (packages/backend-webgpu/src/base/storage.ts:16-58). */
+int kh_get_alloc_stats(kh_alloc_stats* out);
+
+/* Copies on the library stream.  h2d returns after the source may be reused; d2h waits for the
+ * stream (replaces WebGPUStorage.toRawDataAsync, packages/backend-webgpu/src/base/storage.ts:191-229). */
+int kh_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int kh_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int kh_memcpy_d2d(void* dst, const void* src, size_t bytes);
+int kh_synchronize(void);
+
+/* Stream events for timing (the reference has none; its timing is wall-clock only,
+ * playground-node/src/qwen3/index.ts:253-261). */
+int kh_event_create(void** event);
+int kh_event_destroy(void* event);
+int kh_event_record(void* event);
+int kh_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ------------------------------------------------------------------ support ops -------------- */
+
+/* dst[i] = value for n elements of `dtype` (a fill kernel, never hipMemsetAsync).
+ * Replaces the `zeros`/`fill` factory kernels (reference: packages/backend-webgpu/src/kernels/factory/index.ts:22-46). */
+int kh_fill(void* dst, int64_t n, float value, int dtype);
+
+/* Gathers a strided view of up to 6 dims into a contiguous buffer, converting dtype_src→dtype_dst
+ * (f32/bf16 either way; i32→i32).  `src` points at storage element 0; `src_offset` is the view offset.
+ * Replaces the `copy` kernel behind contiguous/clone/cast/copy_
+ * (reference: packages/core/src/dispatch/handlers/copy.ts:40-71, :123-138; packages/backend-webgpu/src/kernels/copy/index.ts:13-33). */
+int kh_copy_strided(const void* src, int64_t src_offset, void* dst, int ndim, const int64_t* shape,
+                    const int64_t* src_strides, int dtype_src, int dtype_dst);
+
+/* out[i] = a[i] (op) b[i] for contiguous same-shape operands; op 0 = add, 1 = mul, 2 = sub.
+ * Replaces the `add`/`mul`/`sub` pointwise iterator kernels for the contiguous case
+ * (reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:329 mul, :437 add). */
+int kh_binary(int op, const void* a, const void* b, void* out, int64_t n, int dtype);
+
+/* out[i] = silu(x[i]) with silu(x) = x / (1 + exp(-clamp(x, -88, 88))).
+ * Replaces the `silu` pointwise kernel (reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:299). */
+int kh_silu(const void* x, void* out, int64_t n, int dtype);
+
+/* out[r, i] = silu(gate[r, i]) * up[r, i] over rows x n, rows strided by the given element strides.
+ * Fuses SwiGLUMLP's silu and mul (reference: packages/model-utils/src/mlp/swiglu.ts:119-134;
+ * ops.ts:299 silu, :329 mul). */
+int kh_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,
+                void* out, int64_t out_row_stride, int64_t rows, int64_t n, int dtype);
+
+/* out[i, :] = table[idx[i], :] for n_idx rows of row_elems elements; idx is device int32 and must
+ * lie in [0, n_rows) (checked on device: an out-of-range id yields a zero row and sets *bad_count).
+ * Replaces index_select behind embedding (reference: packages/core/src/dispatch/handlers/composite.ts:149-245;
+ * packages/backend-webgpu/src/kernels/gather/index.ts:14-23). */
+int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64_t n_idx, int64_t row_elems,
+                    void* out, int dtype);
+
+/* out[r] = the lowest index of the maximum of row r (rows x n, contiguous), int32.
+ * Replaces argmax (reference: packages/backend-webgpu/src/kernels/reduction/argShaderBuilder.ts:205-240)
+ * with the greedy tie rule of sample() (packages/model-utils/src/sampling/index.ts:132,138). */
+int kh_argmax(const void* x, int64_t rows, int64_t n, int32_t* out, int dtype);
+
+/* ------------------------------------------------------------------ hot path ----------------- */
+
+/* y[r, :] = x[r, :] * (1 / sqrt(mean(x[r, :]^2) + eps)) * w[:] (w may be NULL), fp32 math,
+ * rows x n, x and y row-strided (contiguous rows).  Replaces the `rms_norm` kernel
+ * (reference: packages/core/src/dispatch/handlers/normalize.ts:46-95;
+ * packages/backend-webgpu/src/kernels/normalize/executor.ts:26-183; shaderBuilder.ts:343-414). */
+int kh_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* y, int64_t y_row_stride,
+                int64_t rows, int64_t n, float eps, int dtype);
+
+/* Per-head RMSNorm (qk-norm) followed by rotary embedding, for q and k in one launch.
+ * Token t of a [n_batch, seq_len] grid has position positions[t]; head h of q is read at
+ *   q + b*s[0] + t_in_seq*s[1] + h*s[2]   and written at   q_out + b*s[6] + t_in_seq*s[7] + h*s[8],
+ * k likewise with s[3..5] (read) and s[9..11] (write) — `strides` holds these 12 element strides.
+ * Math per head row x (head_dim D): n = x / sqrt(mean(x^2)+eps) * w; then, with
+ * f_i = float(positions[t]) * inv_freq[i mod D/2] (float32 product) and rotate_half(n) = cat(-n2, n1),
+ *   out = n * cos(f) + rotate_half(n) * sin(f).
+ * If v/v_out are non-NULL, v rows (k's head count and strides s[12..14] read, s[15..17] write;
+ * `strides` then holds 18 values) are copied unchanged in the same launch (fused KV-cache write).
+ * Replaces q_norm/k_norm + _permuteToHeadsFirst + applyRotaryPosEmbDirect + kvCache.update
+ * (reference: packages/model-utils/src/attention/gqa.ts:279-309; packages/model-utils/src/rope.ts:159-261, :546-644;
+ * packages/model-utils/src/kv-cache.ts:164-212). */
+int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out,
+                    const void* v, void* v_out,
+                    const void* wq, const void* wk, const float* inv_freq, const int32_t* positions,
+                    int64_t n_batch, int64_t seq_len, int n_q_heads, int n_kv_heads, int head_dim,
+                    const int64_t* strides, float eps, int dtype);
+
+/* Scaled dot-product attention O = softmax(scale * Q K^T + causal) V with GQA
+ * (query head h reads kv head h / (hq / hkv)); causal masks key j > query i (top-left aligned).
+ * Shapes q [batch, hq, lq, d], k/v [batch, hkv, lk, d], o [batch, hq, lq, d]; `strides` holds 12
+ * element strides: q (batch, head, seq), k (…), v (…), o (…); the d axis is contiguous.
+ * bf16 with d == 128 runs the MFMA flash kernel; lq == 1 runs split-K decode; otherwise a
+ * LDS-tiled fp32-math kernel (d <= 256).  Replaces the `flash_attention` kernel
+ * (reference signature packages/types/src/backend/register.ts:102-109; semantics
+ * packages/backend-webgpu/src/kernels/attention/builder.ts:138-329; called from
+ * packages/core/src/dispatch/handlers/composite.ts:312-316). */
+int kh_flash_attention(const void* q, const void* k, const void* v, void* o,
+                       int batch, int hq, int hkv, int64_t lq, int64_t lk, int d,
+                       const int64_t* strides, float scale, int causal, int dtype);
+
+/* Decode attention for one query token per sequence against a KV cache with per-sequence
+ * lengths seq_lens[b] (device int32, each in [1, max_len]); no mask (the caller turns causal off
+ * for 1-token decode, reference packages/model-utils/src/attention/gqa.ts:333-336).
+ * q [batch, hq, d], o [batch, hq, d] (strides: batch, head), caches [batch, hkv, max_len, d]
+ * (strides: batch, head, seq).  `strides` holds 10 values: q (b, h), k (b, h, s), v (b, h, s),
+ * o (b, h).  Split-K over the sequence with a log-sum-exp merge; bf16 or f32.
+ * Varlen extension of flash_attention for StaticKVCache views
+ * (reference: packages/model-utils/src/kv-cache.ts:197-211; register.ts:102-109). */
+int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
+                        const int32_t* seq_lens, int batch, int hq, int hkv, int d, int64_t max_len,
+                        const int64_t* strides, float scale, int dtype);
+
+/* C[m, n] = alpha * sum_k A[m, k] * B'[k, n] + beta * Cin[m, n] (+ bias[n]), fp32 accumulate,
+ * where B' = B^T with B stored [n, k] (trans_b = 1, the nn.Linear weight layout) or B' = B stored
+ * [k, n] (trans_b = 0).  Row strides lda/ldb/ldc/ldcin in elements; cin/bias may be NULL and may
+ * alias c.  Replaces the `matmul` kernel's mm path with its alpha/beta/C epilogue
+ * (reference: packages/core/src/dispatch/matmulOps.ts:32-125, :408-496, :649-814;
+ * packages/core/src/dispatch/handlers/composite.ts:55-77; packages/backend-webgpu/src/kernels/matrix/executor.ts:438-598). */
+int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
+            const void* cin, int64_t ldcin, const void* bias,
+            int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b, int dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KANDLE_HIP_H */

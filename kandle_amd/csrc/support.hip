@@ -1,0 +1,350 @@
+// Support kernels of the hot path: fill, strided copy/cast, binary add/mul/sub, silu, silu*mul,
+// index_select (embedding rows) and argmax.  All are HBM-bound; contiguous ones move 16 bytes per
+// lane per access when the pointers allow it.
+#include <cfloat>
+
+#include "common.h"
+
+using namespace kh;
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline int grid_for(int64_t work, int per_block = kThreads, int cap = 65536) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (int)g;
+}
+
+// ---- fill ---------------------------------------------------------------------------------
+template <typename T>
+__global__ void fill_kernel(T* dst, int64_t n, float value) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(dst, i, value);
+}
+__global__ void fill_i32_kernel(int32_t* dst, int64_t n, int32_t value) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = value;
+}
+
+// ---- strided copy / cast ------------------------------------------------------------------
+struct StridedDesc {
+  int ndim;
+  int64_t shape[6];
+  int64_t stride[6];
+};
+
+template <typename S, typename D>
+__global__ void copy_strided_kernel(const S* __restrict__ src, int64_t src_offset, D* __restrict__ dst,
+                                    int64_t n, StridedDesc desc) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t rem = i, off = src_offset;
+    for (int d = desc.ndim - 1; d >= 0; --d) {
+      const int64_t c = rem % desc.shape[d];
+      rem /= desc.shape[d];
+      off += c * desc.stride[d];
+    }
+    Elem<D>::store(dst, i, Elem<S>::load(src, off));
+  }
+}
+__global__ void copy_strided_i32_kernel(const int32_t* __restrict__ src, int64_t src_offset,
+                                        int32_t* __restrict__ dst, int64_t n, StridedDesc desc) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t rem = i, off = src_offset;
+    for (int d = desc.ndim - 1; d >= 0; --d) {
+      const int64_t c = rem % desc.shape[d];
+      rem /= desc.shape[d];
+      off += c * desc.stride[d];
+    }
+    dst[i] = src[off];
+  }
+}
+
+// ---- binary / unary ---------------------------------------------------------------------------
+__device__ __forceinline__ float apply_binary(int op, float a, float b) {
+  return op == 0 ? a + b : (op == 1 ? a * b : a - b);
+}
+
+// Reference silu: x / (1 + exp(-clamp(x, -88, 88)))  (pointwise/ops.ts:299).
+__device__ __forceinline__ float silu_f(float x) {
+  const float c = fminf(fmaxf(x, -88.0f), 88.0f);
+  return x / (1.0f + expf(-c));
+}
+
+template <typename T>
+__global__ void binary_kernel(int op, const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ out,
+                              int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(out, i, apply_binary(op, Elem<T>::load(a, i), Elem<T>::load(b, i)));
+}
+
+// bf16, 8 elements per lane per step (16-byte accesses).
+__global__ void binary_bf16x8_kernel(int op, const uint4* __restrict__ a, const uint4* __restrict__ b,
+                                     uint4* __restrict__ out, int64_t n8) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint4 va = a[i], vb = b[i];
+    const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
+    const uint32_t wb[4] = {vb.x, vb.y, vb.z, vb.w};
+    uint32_t wo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      wo[j] = pack_bf16x2(apply_binary(op, lo_bf16(wa[j]), lo_bf16(wb[j])),
+                          apply_binary(op, hi_bf16(wa[j]), hi_bf16(wb[j])));
+    out[i] = make_uint4(wo[0], wo[1], wo[2], wo[3]);
+  }
+}
+
+template <typename T>
+__global__ void silu_kernel(const T* __restrict__ x, T* __restrict__ out, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(out, i, silu_f(Elem<T>::load(x, i)));
+}
+
+template <typename T>
+__global__ void silu_mul_kernel(const T* __restrict__ g, int64_t gs, const T* __restrict__ u, int64_t us,
+                                T* __restrict__ out, int64_t os, int64_t rows, int64_t n) {
+  const int64_t total = rows * n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / n, c = i - r * n;
+    const float gv = Elem<T>::load(g, r * gs + c);
+    const float uv = Elem<T>::load(u, r * us + c);
+    Elem<T>::store(out, r * os + c, silu_f(gv) * uv);
+  }
+}
+
+// bf16 silu*mul with 8 elements per lane (n % 8 == 0, 16-byte aligned rows).
+__global__ void silu_mul_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t gs, const uint16_t* __restrict__ u,
+                                       int64_t us, uint16_t* __restrict__ out, int64_t os, int64_t rows,
+                                       int64_t n8) {
+  const int64_t total = rows * n8;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / n8, c = (i - r * n8) * 8;
+    const uint4 vg = *reinterpret_cast<const uint4*>(g + r * gs + c);
+    const uint4 vu = *reinterpret_cast<const uint4*>(u + r * us + c);
+    const uint32_t wg[4] = {vg.x, vg.y, vg.z, vg.w};
+    const uint32_t wu[4] = {vu.x, vu.y, vu.z, vu.w};
+    uint32_t wo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      wo[j] = pack_bf16x2(silu_f(lo_bf16(wg[j])) * lo_bf16(wu[j]), silu_f(hi_bf16(wg[j])) * hi_bf16(wu[j]));
+    *reinterpret_cast<uint4*>(out + r * os + c) = make_uint4(wo[0], wo[1], wo[2], wo[3]);
+  }
+}
+
+// ---- index_select -------------------------------------------------------------------------
+template <typename T>
+__global__ void index_select_kernel(const T* __restrict__ table, int64_t n_rows, const int32_t* __restrict__ idx,
+                                    int64_t row_elems, T* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const int32_t id = idx[r];
+  const bool ok = id >= 0 && id < n_rows;
+  const T* src = table + (ok ? (int64_t)id : 0) * row_elems;
+  T* dst = out + r * row_elems;
+  for (int64_t c = threadIdx.x; c < row_elems; c += blockDim.x) dst[c] = ok ? src[c] : T(0);
+}
+
+// ---- argmax (lowest index among maxima; NaN never wins; init -FLT_MAX at index 0) ----------
+template <typename T>
+__global__ void argmax_kernel(const T* __restrict__ x, int64_t n, int32_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const T* row = x + r * n;
+  // A candidate must be strictly greater than -FLT_MAX (the reference's initial value); a row
+  // with none yields index 0, as the reference's initial best_idx does.
+  float best = -FLT_MAX;
+  int32_t bidx = INT32_MAX;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = Elem<T>::load(row, i);
+    if (v > best) {
+      best = v;
+      bidx = (int32_t)i;
+    }
+  }
+  __shared__ float sv[kThreads];
+  __shared__ int32_t si[kThreads];
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bidx;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      const float ov = sv[threadIdx.x + s];
+      const int32_t oi = si[threadIdx.x + s];
+      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[r] = si[0] == INT32_MAX ? 0 : si[0];
+}
+
+}  // namespace
+
+extern "C" {
+
+int kh_fill(void* dst, int64_t n, float value, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(n >= 0, "kh_fill: negative count");
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(dst != nullptr, "kh_fill: null pointer");
+  const int g = grid_for(n);
+  if (dtype == KH_F32)
+    fill_kernel<float><<<g, kThreads, 0, stream()>>>((float*)dst, n, value);
+  else if (dtype == KH_BF16)
+    fill_kernel<uint16_t><<<g, kThreads, 0, stream()>>>((uint16_t*)dst, n, value);
+  else if (dtype == KH_I32)
+    fill_i32_kernel<<<g, kThreads, 0, stream()>>>((int32_t*)dst, n, (int32_t)value);
+  else
+    KH_REQUIRE(false, "kh_fill: unsupported dtype %d", dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_copy_strided(const void* src, int64_t src_offset, void* dst, int ndim, const int64_t* shape,
+                    const int64_t* src_strides, int dtype_src, int dtype_dst) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(ndim >= 0 && ndim <= 6, "kh_copy_strided: ndim %d outside [0, 6]", ndim);
+  KH_REQUIRE(ndim == 0 || (shape && src_strides), "kh_copy_strided: null shape/strides");
+  StridedDesc desc{};
+  desc.ndim = ndim;
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) {
+    KH_REQUIRE(shape[d] >= 0, "kh_copy_strided: negative extent");
+    desc.shape[d] = shape[d];
+    desc.stride[d] = src_strides[d];
+    n *= shape[d];
+  }
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(src && dst, "kh_copy_strided: null pointer");
+  const int g = grid_for(n);
+  if (dtype_src == KH_I32 || dtype_dst == KH_I32) {
+    KH_REQUIRE(dtype_src == KH_I32 && dtype_dst == KH_I32, "kh_copy_strided: int32 copies cannot cast");
+    copy_strided_i32_kernel<<<g, kThreads, 0, stream()>>>((const int32_t*)src, src_offset, (int32_t*)dst, n, desc);
+  } else if (dtype_src == KH_F32 && dtype_dst == KH_F32) {
+    copy_strided_kernel<float, float><<<g, kThreads, 0, stream()>>>((const float*)src, src_offset, (float*)dst, n, desc);
+  } else if (dtype_src == KH_F32 && dtype_dst == KH_BF16) {
+    copy_strided_kernel<float, uint16_t><<<g, kThreads, 0, stream()>>>((const float*)src, src_offset, (uint16_t*)dst, n, desc);
+  } else if (dtype_src == KH_BF16 && dtype_dst == KH_F32) {
+    copy_strided_kernel<uint16_t, float><<<g, kThreads, 0, stream()>>>((const uint16_t*)src, src_offset, (float*)dst, n, desc);
+  } else if (dtype_src == KH_BF16 && dtype_dst == KH_BF16) {
+    copy_strided_kernel<uint16_t, uint16_t><<<g, kThreads, 0, stream()>>>((const uint16_t*)src, src_offset, (uint16_t*)dst, n, desc);
+  } else {
+    KH_REQUIRE(false, "kh_copy_strided: unsupported dtypes %d -> %d", dtype_src, dtype_dst);
+  }
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_binary(int op, const void* a, const void* b, void* out, int64_t n, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(op >= 0 && op <= 2, "kh_binary: unknown op %d", op);
+  KH_REQUIRE(n >= 0, "kh_binary: negative count");
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(a && b && out, "kh_binary: null pointer");
+  if (dtype == KH_BF16 && n % 8 == 0 && aligned16(a) && aligned16(b) && aligned16(out)) {
+    binary_bf16x8_kernel<<<grid_for(n / 8), kThreads, 0, stream()>>>(op, (const uint4*)a, (const uint4*)b,
+                                                                     (uint4*)out, n / 8);
+  } else if (dtype == KH_BF16) {
+    binary_kernel<uint16_t><<<grid_for(n), kThreads, 0, stream()>>>(op, (const uint16_t*)a, (const uint16_t*)b,
+                                                                    (uint16_t*)out, n);
+  } else if (dtype == KH_F32) {
+    binary_kernel<float><<<grid_for(n), kThreads, 0, stream()>>>(op, (const float*)a, (const float*)b,
+                                                                 (float*)out, n);
+  } else {
+    KH_REQUIRE(false, "kh_binary: unsupported dtype %d", dtype);
+  }
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_silu(const void* x, void* out, int64_t n, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(n >= 0, "kh_silu: negative count");
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(x && out, "kh_silu: null pointer");
+  if (dtype == KH_F32)
+    silu_kernel<float><<<grid_for(n), kThreads, 0, stream()>>>((const float*)x, (float*)out, n);
+  else if (dtype == KH_BF16)
+    silu_kernel<uint16_t><<<grid_for(n), kThreads, 0, stream()>>>((const uint16_t*)x, (uint16_t*)out, n);
+  else
+    KH_REQUIRE(false, "kh_silu: unsupported dtype %d", dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride, void* out,
+                int64_t out_row_stride, int64_t rows, int64_t n, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(rows >= 0 && n >= 0, "kh_silu_mul: negative extent");
+  if (rows == 0 || n == 0) return KH_OK;
+  KH_REQUIRE(gate && up && out, "kh_silu_mul: null pointer");
+  KH_REQUIRE(gate_row_stride >= n && up_row_stride >= n && out_row_stride >= n,
+             "kh_silu_mul: row strides must be >= n");
+  if (dtype == KH_BF16) {
+    const bool vec = n % 8 == 0 && gate_row_stride % 8 == 0 && up_row_stride % 8 == 0 && out_row_stride % 8 == 0 &&
+                     aligned16(gate) && aligned16(up) && aligned16(out);
+    if (vec)
+      silu_mul_bf16x8_kernel<<<grid_for(rows * (n / 8)), kThreads, 0, stream()>>>(
+          (const uint16_t*)gate, gate_row_stride, (const uint16_t*)up, up_row_stride, (uint16_t*)out, out_row_stride,
+          rows, n / 8);
+    else
+      silu_mul_kernel<uint16_t><<<grid_for(rows * n), kThreads, 0, stream()>>>(
+          (const uint16_t*)gate, gate_row_stride, (const uint16_t*)up, up_row_stride, (uint16_t*)out, out_row_stride,
+          rows, n);
+  } else if (dtype == KH_F32) {
+    silu_mul_kernel<float><<<grid_for(rows * n), kThreads, 0, stream()>>>(
+        (const float*)gate, gate_row_stride, (const float*)up, up_row_stride, (float*)out, out_row_stride, rows, n);
+  } else {
+    KH_REQUIRE(false, "kh_silu_mul: unsupported dtype %d", dtype);
+  }
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64_t n_idx, int64_t row_elems,
+                    void* out, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(n_rows > 0 && n_idx >= 0 && row_elems > 0, "kh_index_select: bad extents");
+  if (n_idx == 0) return KH_OK;
+  KH_REQUIRE(n_idx <= INT32_MAX, "kh_index_select: too many indices");
+  KH_REQUIRE(table && idx && out, "kh_index_select: null pointer");
+  if (dtype == KH_BF16)
+    index_select_kernel<uint16_t><<<(int)n_idx, kThreads, 0, stream()>>>((const uint16_t*)table, n_rows, idx,
+                                                                         row_elems, (uint16_t*)out);
+  else if (dtype == KH_F32)
+    index_select_kernel<float><<<(int)n_idx, kThreads, 0, stream()>>>((const float*)table, n_rows, idx, row_elems,
+                                                                      (float*)out);
+  else
+    KH_REQUIRE(false, "kh_index_select: unsupported dtype %d", dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_argmax(const void* x, int64_t rows, int64_t n, int32_t* out, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(rows >= 0 && n > 0, "kh_argmax: bad extents (rows %lld, n %lld)", (long long)rows, (long long)n);
+  if (rows == 0) return KH_OK;
+  KH_REQUIRE(rows <= INT32_MAX && n <= INT32_MAX, "kh_argmax: extents too large");
+  KH_REQUIRE(x && out, "kh_argmax: null pointer");
+  if (dtype == KH_F32)
+    argmax_kernel<float><<<(int)rows, kThreads, 0, stream()>>>((const float*)x, n, out);
+  else if (dtype == KH_BF16)
+    argmax_kernel<uint16_t><<<(int)rows, kThreads, 0, stream()>>>((const uint16_t*)x, n, out);
+  else
+    KH_REQUIRE(false, "kh_argmax: unsupported dtype %d", dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+}  // extern "C"

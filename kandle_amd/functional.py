@@ -1,0 +1,341 @@
+"""User-facing ops for the hot path (Tensor in, Tensor out), restating Kandle's dispatch layer.
+
+Each op validates and routes exactly as the reference dispatcher does, allocates its output through
+the active backend and calls the kernel it finds BY NAME in the backend's registry (a missing kernel
+raises: there is no fallback implementation here):
+  scaled_dot_product_attention  packages/core/src/dispatch/handlers/composite.ts:247-348
+  linear                        packages/core/src/dispatch/handlers/composite.ts:55-77
+  matmul                        packages/core/src/dispatch/matmulOps.ts:408-496, :649-814
+  rms_norm                      packages/core/src/dispatch/handlers/normalize.ts:46-95
+  silu / mul / add              packages/core/src/dispatch/handlers/iterator.ts:24-135
+  contiguous / cast / copy_     packages/core/src/dispatch/handlers/copy.ts:40-71, :123-138
+  embedding                     packages/core/src/dispatch/handlers/composite.ts:149-245
+  views                         packages/core/src/dispatch/handlers/shape.ts (metadata only)
+"""
+from __future__ import annotations
+
+import math
+import warnings
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import env
+from .kernels import MatmulDispatchResult, TensorIterator
+from .tensor import HipTensorHandle, Tensor, contiguous_strides, numel_of
+
+
+def _backend(t: Tensor):
+    return env.get_backend(t.device)
+
+
+def _kernel(t: Tensor, name: str):
+    k = _backend(t).operators.find(name)
+    if k is None:
+        raise RuntimeError(f"kernel {name!r} is not registered for device {t.device}")
+    return k
+
+
+def _new(t: Tensor, shape, dtype=None) -> HipTensorHandle:
+    return _backend(t).create_tensor_handle(tuple(shape), dtype or t.dtype)
+
+
+def _wrap(h: HipTensorHandle) -> Tensor:
+    return Tensor(handle=h)
+
+
+# ---------------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------------
+def scaled_dot_product_attention(query: Tensor, key: Tensor, value: Tensor, attn_mask: Optional[Tensor] = None,
+                                 dropout_p: float = 0.0, is_causal: bool = False,
+                                 scale: Optional[float] = None, out: Optional[Tensor] = None) -> Tensor:
+    """softmax(scale * Q K^T [+ causal]) V.  q (..., L, E), k (..., S, E), v (..., S, Ev) -> (..., L, Ev).
+
+    Like the reference: dropout_p > 0 is warned about and ignored (inference), the default scale is
+    1/sqrt(E), and the `flash_attention` kernel is found by name."""
+    if dropout_p > 0:
+        warnings.warn("SDPA: dropout_p > 0 is not supported in inference mode, ignoring")
+    E = query.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(E)
+    if attn_mask is not None:
+        # The reference routes explicit masks to matmul -> add -> softmax -> matmul; this backend
+        # has no softmax kernel on the hot path, so an explicit mask is rejected rather than faked.
+        raise NotImplementedError("scaled_dot_product_attention: explicit attn_mask is not supported by the HIP backend")
+    out_shape = tuple(query.shape[:-1]) + (value.shape[-1],)
+    output = out.handle if out is not None else _new(query, out_shape)
+    _kernel(query, "flash_attention")(query.handle, key.handle, value.handle, output, float(scale), bool(is_causal))
+    return out if out is not None else _wrap(output)
+
+
+def decode_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, seq_lens: Tensor,
+                     scale: Optional[float] = None) -> Tensor:
+    """Varlen 1-token decode: q [B, Hq, D] against caches [B, Hkv, max_len, D] with seq_lens [B]."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    output = _new(q, q.shape)
+    _kernel(q, "decode_attention")(q.handle, k_cache.handle, v_cache.handle, seq_lens.handle, output, float(scale))
+    return _wrap(output)
+
+
+# ---------------------------------------------------------------------------------------------
+# matmul / linear
+# ---------------------------------------------------------------------------------------------
+def dispatch_matmul(a: Tensor, b: Tensor, c: Optional[Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
+                    out: Optional[Tensor] = None, transpose_a: bool = False, transpose_b: bool = False,
+                    bias: Optional[Tensor] = None) -> Tensor:
+    """out = alpha * a @ op(b) + beta * c (+ bias).  With transpose_b, b is stored [..., N, K]."""
+    if a.device != b.device:
+        raise RuntimeError(f"matmul requires tensors on same device, got {a.device} and {b.device}")
+    for t, nm in ((a, "a"), (b, "b")):
+        if t.dtype not in ("float32", "bfloat16"):
+            raise TypeError(f"matmul does not support dtype {t.dtype}")
+    if beta != 0.0 and c is None:
+        raise ValueError(f"matmul: beta={beta} requires inputC to be provided")
+    if transpose_a:
+        a = transpose(a, -1, -2)
+    ash, bsh = list(a.shape), list(b.shape)
+    if len(ash) < 1 or len(bsh) < 1:
+        raise ValueError("matmul: scalars are not matrices")
+    a2 = ash if len(ash) >= 2 else [1] + ash
+    if transpose_b:
+        b2 = bsh if len(bsh) >= 2 else bsh + [1]
+        N, Kb = b2[-2], b2[-1]
+    else:
+        b2 = bsh if len(bsh) >= 2 else bsh + [1]
+        Kb, N = b2[-2], b2[-1]
+    M, K = a2[-2], a2[-1]
+    if K != Kb:
+        raise ValueError(f"matmul: inner dimensions differ ({K} vs {Kb}) for {tuple(ash)} @ {tuple(bsh)}")
+    batch_shape = list(np.broadcast_shapes(tuple(a2[:-2]), tuple(b2[:-2])))
+    out_shape = batch_shape + [M, N]
+    if len(ash) == 1:
+        out_shape.pop(-2)
+    if len(bsh) == 1:
+        out_shape.pop(-1)
+    if out is not None:
+        if tuple(out.shape) != tuple(out_shape):
+            raise ValueError(f"matmul: out shape {out.shape} != {tuple(out_shape)}")
+        output = out.handle
+    else:
+        output = _new(a, out_shape)
+    variant = "mm" if not batch_shape else "bmm"
+    cfg = MatmulDispatchResult(variant=variant, output=output, M=M, K=K, N=N, batch_shape=tuple(batch_shape),
+                               batch_size=int(np.prod(batch_shape)) if batch_shape else 1, transpose_a=False,
+                               transpose_b=bool(transpose_b), alpha=float(alpha), beta=float(beta),
+                               input_c=c.handle if c is not None else None,
+                               bias=bias.handle if bias is not None else None)
+    ah = a.handle if len(ash) >= 2 else _view_handle(a.handle, [1] + ash, [0] + list(a.strides))
+    bh = b.handle
+    if len(bsh) == 1:
+        bh = _view_handle(b.handle, bsh + [1], list(b.strides) + [1]) if not transpose_b else \
+            _view_handle(b.handle, [1] + bsh, [0] + list(b.strides))
+    try:
+        _kernel(a, "matmul")(cfg, ah, bh)
+    finally:
+        if ah is not a.handle:
+            ah.dispose()
+        if bh is not b.handle:
+            bh.dispose()
+    return out if out is not None else _wrap(output)
+
+
+def matmul(a: Tensor, b: Tensor) -> Tensor:
+    return dispatch_matmul(a, b)
+
+
+def linear(input: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+    """y = input @ weight^T + bias with weight [out_features, in_features] (nn.Linear layout)."""
+    return dispatch_matmul(input, weight, transpose_b=True, bias=bias)
+
+
+# ---------------------------------------------------------------------------------------------
+# normalisation and pointwise
+# ---------------------------------------------------------------------------------------------
+def rms_norm(input: Tensor, normalized_shape: Sequence[int], weight: Optional[Tensor] = None,
+             eps: Optional[float] = None) -> Tensor:
+    params = {"normalized_shape": list(normalized_shape), "eps": eps,
+              "weight": weight.handle if weight is not None else None}
+    return _wrap(_kernel(input, "rms_norm")([input.handle], params))
+
+
+def _broadcast_pair(a: Tensor, b: Tensor):
+    shape = tuple(np.broadcast_shapes(tuple(a.shape), tuple(b.shape)))
+    ha = a.handle if tuple(a.shape) == shape and a.handle.is_contiguous() else _materialize_expand(a, shape)
+    hb = b.handle if tuple(b.shape) == shape and b.handle.is_contiguous() else _materialize_expand(b, shape)
+    return shape, ha, hb
+
+
+def _materialize_expand(t: Tensor, shape) -> HipTensorHandle:
+    v = expand(t, shape) if tuple(t.shape) != tuple(shape) else t
+    h = _kernel(t, "contiguous")(v.handle, {})
+    if v is not t:
+        v.dispose()
+    return h
+
+
+def _binary(name: str, a: Tensor, b: Tensor) -> Tensor:
+    if a.dtype != b.dtype:
+        raise TypeError(f"{name}: dtype mismatch {a.dtype} vs {b.dtype}")
+    shape, ha, hb = _broadcast_pair(a, b)
+    out = _new(a, shape)
+    try:
+        _kernel(a, name)(TensorIterator([ha, hb], [out]))
+    finally:
+        if ha is not a.handle:
+            ha.dispose()
+        if hb is not b.handle:
+            hb.dispose()
+    return _wrap(out)
+
+
+def add(a: Tensor, b: Tensor) -> Tensor:
+    return _binary("add", a, b)
+
+
+def mul(a: Tensor, b: Tensor) -> Tensor:
+    return _binary("mul", a, b)
+
+
+def sub(a: Tensor, b: Tensor) -> Tensor:
+    return _binary("sub", a, b)
+
+
+def silu(x: Tensor) -> Tensor:
+    hx = x.handle if x.handle.is_contiguous() else _kernel(x, "contiguous")(x.handle, {})
+    out = _new(x, x.shape)
+    try:
+        _kernel(x, "silu")(TensorIterator([hx], [out]))
+    finally:
+        if hx is not x.handle:
+            hx.dispose()
+    return _wrap(out)
+
+
+def silu_mul(gate: Tensor, up: Tensor) -> Tensor:
+    out = _new(gate, gate.shape)
+    _kernel(gate, "silu_mul")(gate.handle, up.handle, out)
+    return _wrap(out)
+
+
+# ---------------------------------------------------------------------------------------------
+# copies, gathers, reductions
+# ---------------------------------------------------------------------------------------------
+def contiguous(x: Tensor) -> Tensor:
+    """Zero-copy when already contiguous at its offset (copy.ts:123-138), else a materialising copy."""
+    if x.handle.is_contiguous():
+        x.handle.storage.inc_ref()
+        return _wrap(HipTensorHandle(x.handle.storage, x.shape, x.dtype, x.strides, x.offset))
+    return _wrap(_kernel(x, "contiguous")(x.handle, {}))
+
+
+def cast(x: Tensor, dtype: str) -> Tensor:
+    return _wrap(_kernel(x, "cast")(x.handle, {"target_dtype": dtype}))
+
+
+def copy_(dst: Tensor, src: Tensor) -> Tensor:
+    _kernel(dst, "copy_")(dst.handle, src.handle)
+    return dst
+
+
+def embedding(input_ids: Tensor, weight: Tensor) -> Tensor:
+    """weight[input_ids] with ids int32 of any shape -> ids.shape + [hidden]."""
+    ids = input_ids if input_ids.handle.is_contiguous() else contiguous(input_ids)
+    out = _new(weight, tuple(input_ids.shape) + tuple(weight.shape[1:]))
+    _kernel(weight, "index_select")(weight.handle, ids.handle, {"dim": 0}, out)
+    if ids is not input_ids:
+        ids.dispose()
+    return _wrap(out)
+
+
+def argmax(x: Tensor, dim: int = -1) -> Tensor:
+    if dim not in (-1, len(x.shape) - 1):
+        raise NotImplementedError("argmax: only the last dim is implemented")
+    out = _new(x, x.shape[:-1], "int32")
+    _kernel(x, "argmax")(TensorIterator([x.handle], [out]))
+    return _wrap(out)
+
+
+def zeros(shape, dtype: str = "float32") -> Tensor:
+    b = env.get_backend("hip")
+    h = b.create_tensor_handle(tuple(shape), dtype)
+    b.operators.find("zeros")(h)
+    return _wrap(h)
+
+
+# ---------------------------------------------------------------------------------------------
+# views (metadata only; the storage is shared and incRef'd)
+# ---------------------------------------------------------------------------------------------
+def _view_handle(h: HipTensorHandle, shape, strides, offset=None) -> HipTensorHandle:
+    return HipTensorHandle.create_view(h.storage, shape, h.dtype, strides, h.offset if offset is None else offset)
+
+
+def view(x: Tensor, shape) -> Tensor:
+    shape = list(shape)
+    if -1 in shape:
+        i = shape.index(-1)
+        rest = numel_of([s for j, s in enumerate(shape) if j != i])
+        shape[i] = x.numel // rest if rest else 0
+    if numel_of(shape) != x.numel:
+        raise ValueError(f"view: {tuple(x.shape)} cannot become {tuple(shape)}")
+    if not x.handle.is_contiguous():
+        raise ValueError("view: input must be contiguous (use reshape)")
+    return _wrap(_view_handle(x.handle, shape, contiguous_strides(shape)))
+
+
+def reshape(x: Tensor, shape) -> Tensor:
+    if x.handle.is_contiguous():
+        return view(x, shape)
+    c = contiguous(x)
+    try:
+        return view(c, shape)
+    finally:
+        c.dispose()
+
+
+def permute(x: Tensor, dims) -> Tensor:
+    nd = len(x.shape)
+    dims = [d % nd for d in dims]
+    return _wrap(_view_handle(x.handle, [x.shape[d] for d in dims], [x.strides[d] for d in dims]))
+
+
+def transpose(x: Tensor, d0: int, d1: int) -> Tensor:
+    nd = len(x.shape)
+    dims = list(range(nd))
+    dims[d0 % nd], dims[d1 % nd] = dims[d1 % nd], dims[d0 % nd]
+    return permute(x, dims)
+
+
+def narrow(x: Tensor, dim: int, start: int, length: int) -> Tensor:
+    dim %= len(x.shape)
+    if start < 0 or start + length > x.shape[dim]:
+        raise ValueError(f"narrow: [{start}, {start + length}) outside dim {dim} of size {x.shape[dim]}")
+    shape = list(x.shape)
+    shape[dim] = length
+    return _wrap(_view_handle(x.handle, shape, x.strides, x.offset + start * x.strides[dim]))
+
+
+def unsqueeze(x: Tensor, dim: int) -> Tensor:
+    nd = len(x.shape) + 1
+    dim %= nd
+    shape, strides = list(x.shape), list(x.strides)
+    inner = strides[dim] * shape[dim] if dim < len(shape) else 1
+    shape.insert(dim, 1)
+    strides.insert(dim, inner)
+    return _wrap(_view_handle(x.handle, shape, strides))
+
+
+def expand(x: Tensor, shape) -> Tensor:
+    shape = list(shape)
+    pad = len(shape) - len(x.shape)
+    xs, xst = [1] * pad + list(x.shape), [0] * pad + list(x.strides)
+    strides = []
+    for s, xs_i, st in zip(shape, xs, xst):
+        if xs_i == s:
+            strides.append(st)
+        elif xs_i == 1:
+            strides.append(0)
+        else:
+            raise ValueError(f"expand: cannot expand {tuple(x.shape)} to {tuple(shape)}")
+    return _wrap(_view_handle(x.handle, shape, strides))

@@ -1,0 +1,511 @@
+"""Kernel implementations registered by HipBackend, with the reference kernel signatures.
+
+Each function validates shapes on the host, materialises views the kernels cannot take, and calls
+one C-ABI entry point of libkandle_hip.so.  There is no CPU or WebGPU fallback: a shape or dtype the
+HIP kernels do not take raises.
+
+Signatures follow packages/types/src/backend/register.ts:
+  flash_attention(query, key, value, output, scale, is_causal) -> None            (:102-109)
+  matmul(config, a, b) -> None  (config = MatmulDispatchResult)                   (core/src/dispatch/matmulOps.ts:486-493)
+  rms_norm(inputs, params) -> handle  (NormalizeKernelImpl)                        (:52-55)
+  silu / mul / add / sub (iter) -> None  (IteratorKernelImpl)                       (:9)
+  copy(input, options) -> handle  (CopyKernelImpl: contiguous / cast)              (:14-25)
+  index_select(self, index, params, output) -> None  (GatherKernelImpl)            (:64-69)
+  argmax(iter) -> None
+New fused names (no reference schema; the reference composes them from the ops above):
+  rms_norm_rope(q, k, params) -> (q_out, k_out)   qk-norm + RoPE (+ V cache write)
+  silu_mul(gate, up, output) -> None              SwiGLU activation
+  decode_attention(q, k_cache, v_cache, seq_lens, output, scale) -> None   varlen split-K decode
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from .dtypes import BFLOAT16, FLOAT32, INT32
+from .tensor import HipTensorHandle, copy_into, contiguous_strides
+
+_vp = C.c_void_p
+
+
+def _materialize(h: HipTensorHandle, dtype: Optional[str] = None) -> HipTensorHandle:
+    """Contiguous handle with the same logical data (a new one unless already contiguous)."""
+    dtype = dtype or h.dtype
+    if h.is_contiguous() and dtype == h.dtype:
+        h.storage.inc_ref()
+        return HipTensorHandle(h.storage, h.shape, h.dtype, h.strides, h.offset)
+    out = HipTensorHandle.create_new(h.shape, dtype)
+    copy_into(h, out)
+    return out
+
+
+def _last_dim_contiguous(h: HipTensorHandle) -> bool:
+    return h.strides[-1] == 1 or h.shape[-1] == 1
+
+
+def _as_4d(h: HipTensorHandle):
+    """[B,H,L,D] view parameters (shape, strides) of a 2/3/4-D handle (attention/executor.ts:198-220)."""
+    shape, strides = list(h.shape), list(h.strides)
+    if len(shape) == 4:
+        return shape, strides
+    if len(shape) == 3:
+        return [1] + shape, [0] + strides
+    if len(shape) == 2:
+        return [1, 1] + shape, [0, 0] + strides
+    raise ValueError(f"attention expects a 2-D, 3-D or 4-D tensor, got shape {tuple(h.shape)}")
+
+
+# ---------------------------------------------------------------------------------------------
+# flash_attention
+# ---------------------------------------------------------------------------------------------
+def flash_attention(query, key, value, output, scale: float, is_causal: bool) -> None:
+    """O = softmax(scale * Q K^T + causal) V with native GQA; output preallocated by the caller."""
+    for name, h in (("query", query), ("key", key), ("value", value), ("output", output)):
+        if h.dtype not in (FLOAT32, BFLOAT16):
+            raise TypeError(f"flash_attention: {name} dtype {h.dtype} not supported")
+    if not (query.dtype == key.dtype == value.dtype == output.dtype):
+        raise TypeError("flash_attention: query/key/value/output dtypes differ")
+    tmp = []
+    try:
+        hs = []
+        for h in (query, key, value):
+            if not _last_dim_contiguous(h):
+                h = _materialize(h)
+                tmp.append(h)
+            hs.append(h)
+        q, k, v = hs
+        qs, qst = _as_4d(q)
+        ks, kst = _as_4d(k)
+        vs, vst = _as_4d(v)
+        os_, ost = _as_4d(output)
+        B, Hq, Lq, D = qs
+        Bk, Hkv, Lk, Dk = ks
+        if Bk != B or vs[0] != B or Dk != D or vs[1] != Hkv or vs[2] != Lk:
+            raise ValueError(f"flash_attention: incompatible shapes q{qs} k{ks} v{vs}")
+        if vs[3] != D:
+            raise ValueError("flash_attention: value head_dim must equal query head_dim")
+        if Hq % Hkv != 0:
+            raise ValueError(f"flash_attention: numHeadsQ ({Hq}) must be divisible by numHeadsKV ({Hkv})")
+        if tuple(os_) != (B, Hq, Lq, D) or ost[3] != 1:
+            raise ValueError(f"flash_attention: output must be [B,Hq,Lq,D] with a contiguous last dim, got {os_}")
+        strides = _lib.i64_array(qst[:3] + kst[:3] + vst[:3] + ost[:3])
+        _lib.call(
+            "kh_flash_attention",
+            _vp(q.data_ptr()), _vp(k.data_ptr()), _vp(v.data_ptr()), _vp(output.data_ptr()),
+            B, Hq, Hkv, Lq, Lk, D, strides, C.c_float(scale), int(bool(is_causal)), q.kh_dtype,
+        )
+    finally:
+        for t in tmp:
+            t.dispose()
+
+
+def decode_attention(q, k_cache, v_cache, seq_lens, output, scale: float) -> None:
+    """One query token per sequence against [B, Hkv, max_len, D] caches with per-sequence lengths.
+
+    q/output: [B, Hq, D] or [B, Hq, 1, D]; seq_lens: int32 device handle [B] (values in [1, max_len])."""
+    qs, qst = list(q.shape), list(q.strides)
+    os_, ost = list(output.shape), list(output.strides)
+    if len(qs) == 4:
+        qs, qst = qs[:2] + qs[3:], qst[:2] + qst[3:]
+    if len(os_) == 4:
+        os_, ost = os_[:2] + os_[3:], ost[:2] + ost[3:]
+    B, Hq, D = qs
+    _, Hkv, L, Dk = k_cache.shape
+    if seq_lens.dtype != INT32 or seq_lens.shape != (B,):
+        raise ValueError("decode_attention: seq_lens must be an int32 tensor of shape [B]")
+    if Dk != D or tuple(v_cache.shape) != tuple(k_cache.shape) or os_ != [B, Hq, D]:
+        raise ValueError("decode_attention: incompatible shapes")
+    if qst[2] != 1 or ost[2] != 1 or k_cache.strides[3] != 1 or v_cache.strides[3] != 1:
+        raise ValueError("decode_attention: the head_dim axis must be contiguous")
+    strides = _lib.i64_array(qst[:2] + list(k_cache.strides[:3]) + list(v_cache.strides[:3]) + ost[:2])
+    _lib.call(
+        "kh_decode_attention",
+        _vp(q.data_ptr()), _vp(k_cache.data_ptr()), _vp(v_cache.data_ptr()), _vp(output.data_ptr()),
+        _vp(seq_lens.data_ptr()), B, Hq, Hkv, D, L, strides, C.c_float(scale), q.kh_dtype,
+    )
+
+
+# ---------------------------------------------------------------------------------------------
+# matmul
+# ---------------------------------------------------------------------------------------------
+@dataclass
+class MatmulDispatchResult:
+    """Subset of the reference MatmulDispatchResult (packages/core/src/dispatch/matmulOps.ts:32-125)
+    the kernel reads, plus `bias` (fused linear bias)."""
+
+    variant: str
+    output: HipTensorHandle
+    M: int
+    K: int
+    N: int
+    batch_shape: Sequence[int] = field(default_factory=tuple)
+    batch_size: int = 1
+    transpose_a: bool = False
+    transpose_b: bool = False
+    alpha: float = 1.0
+    beta: float = 0.0
+    input_c: Optional[HipTensorHandle] = None
+    bias: Optional[HipTensorHandle] = None
+
+
+def matmul(config: MatmulDispatchResult, a: HipTensorHandle, b: HipTensorHandle) -> None:
+    """out[..., M, N] = alpha * A[..., M, K] op(B) + beta * C (+ bias), one GEMM per batch entry.
+
+    `b` is [..., K, N] (transpose_b False) or [..., N, K] (transpose_b True, the nn.Linear weight)."""
+    out = config.output
+    if a.dtype != b.dtype or a.dtype != out.dtype:
+        raise TypeError(f"matmul: dtype mismatch {a.dtype}, {b.dtype} -> {out.dtype}")
+    if a.dtype not in (FLOAT32, BFLOAT16):
+        raise TypeError(f"matmul does not support dtype {a.dtype}")
+    if config.transpose_a:
+        raise NotImplementedError("matmul: transpose_a is materialised by the dispatcher")
+    M, K, N = config.M, config.K, config.N
+    tmp = []
+    try:
+        A = a if (a.strides[-1] == 1 or K == 1) else _materialize(a)
+        if A is not a:
+            tmp.append(A)
+        Bm = b if (b.strides[-1] == 1 or b.shape[-1] == 1) else _materialize(b)
+        if Bm is not b:
+            tmp.append(Bm)
+        if not out.is_contiguous():
+            raise ValueError("matmul: output must be contiguous")
+        batch = int(np.prod(config.batch_shape)) if len(config.batch_shape) else 1
+        a_rows = A.numel // K if K else 0
+        # Fold batch into M when A is a contiguous stack and B is shared (x W^T of a 3-D activation).
+        b_batched = len(Bm.shape) > 2 and int(np.prod(Bm.shape[:-2])) > 1
+        if not b_batched and A.is_contiguous():
+            _gemm_call(A, K, Bm, out, N, config, rows=a_rows, a_off=0, b_off=0, c_off=0)
+            return
+        a_bs = _batch_offsets(A, config.batch_shape, 2)
+        b_bs = _batch_offsets(Bm, config.batch_shape, 2)
+        for i in range(batch):
+            _gemm_call(A, A.strides[-2], Bm, out, N, config, rows=M, a_off=a_bs[i], b_off=b_bs[i], c_off=i * M * N)
+    finally:
+        for t in tmp:
+            t.dispose()
+
+
+def _batch_offsets(h: HipTensorHandle, batch_shape, mat_dims: int):
+    """Element offsets of each broadcast batch entry of h over batch_shape."""
+    bshape = list(batch_shape)
+    hb_shape = list(h.shape[:-mat_dims])
+    hb_str = list(h.strides[:-mat_dims])
+    pad = len(bshape) - len(hb_shape)
+    hb_shape = [1] * pad + hb_shape
+    hb_str = [0] * pad + hb_str
+    offs = []
+    for idx in np.ndindex(*bshape) if bshape else [()]:
+        off = 0
+        for d, i in enumerate(idx):
+            off += (0 if hb_shape[d] == 1 else i) * hb_str[d]
+        offs.append(off)
+    return offs
+
+
+def _gemm_call(A, lda, Bm, out, N, config, rows, a_off, b_off, c_off):
+    K = config.K
+    isz = A.itemsize
+    # [.., N, K] (transpose_b) or [.., K, N]: either way the row stride of the stored matrix.
+    ldb = Bm.strides[-2] if len(Bm.shape) >= 2 else Bm.shape[-1]
+    cin = config.input_c
+    cin_ptr, ldcin = None, N
+    if cin is not None and config.beta != 0.0:
+        if tuple(cin.shape[-2:]) != (config.M, N) or not cin.is_contiguous() or cin.dtype != out.dtype:
+            raise ValueError("matmul: inputC must be a contiguous [.., M, N] tensor of the output dtype")
+        cin_ptr = cin.data_ptr() + c_off * isz
+    bias_ptr = None
+    if config.bias is not None:
+        if config.bias.shape != (N,) or not config.bias.is_contiguous():
+            raise ValueError("matmul: bias must be a contiguous [N] tensor")
+        bias_ptr = config.bias.data_ptr()
+    lda_eff = lda if lda else K
+    _lib.call(
+        "kh_gemm",
+        _vp(A.data_ptr() + a_off * isz), lda_eff,
+        _vp(Bm.data_ptr() + b_off * isz), ldb,
+        _vp(out.data_ptr() + c_off * isz), N,
+        _vp(cin_ptr) if cin_ptr else None, ldcin,
+        _vp(bias_ptr) if bias_ptr else None,
+        rows, N, K, C.c_float(config.alpha), C.c_float(config.beta), int(bool(config.transpose_b)), A.kh_dtype,
+    )
+
+
+# ---------------------------------------------------------------------------------------------
+# normalisation / fused qk-norm + RoPE
+# ---------------------------------------------------------------------------------------------
+def rms_norm(inputs, params) -> HipTensorHandle:
+    """NormalizeKernelImpl: inputs = [x], params = {normalized_shape, eps, weight?, out?}.
+
+    Normalises over the trailing dims given by normalized_shape; output is contiguous
+    (packages/backend-webgpu/src/kernels/normalize/executor.ts:121-122).  The kernel default eps is
+    1e-5 (executor.ts:58)."""
+    x = inputs[0]
+    ns = params.get("normalized_shape") or params.get("normalizedShape")
+    if ns is None:
+        raise ValueError("rms_norm: normalized_shape is required")
+    ns = [int(v) for v in (ns if isinstance(ns, (list, tuple)) else [ns])]
+    if list(x.shape[len(x.shape) - len(ns):]) != ns:
+        raise ValueError(f"rms_norm: normalized_shape {ns} does not match input shape {x.shape}")
+    eps = params.get("eps")
+    eps = 1e-5 if eps is None else float(eps)
+    w = params.get("weight")
+    if params.get("bias") is not None:
+        raise ValueError("rms_norm: bias is not part of RMSNorm")
+    n = int(np.prod(ns))
+    xs = x if x.is_contiguous() else _materialize(x)
+    try:
+        rows = xs.numel // n if n else 0
+        out = params.get("out") or HipTensorHandle.create_new(x.shape, x.dtype)
+        if w is not None:
+            if w.numel != n or w.dtype != x.dtype:
+                raise ValueError("rms_norm: weight must have normalized_shape elements and the input dtype")
+            wc = w if w.is_contiguous() else _materialize(w)
+        else:
+            wc = None
+        try:
+            _lib.call(
+                "kh_rms_norm", _vp(xs.data_ptr()), n, _vp(wc.data_ptr()) if wc is not None else None,
+                _vp(out.data_ptr()), n, rows, n, C.c_float(eps), x.kh_dtype,
+            )
+        finally:
+            if wc is not None and wc is not w:
+                wc.dispose()
+        return out
+    finally:
+        if xs is not x:
+            xs.dispose()
+
+
+def rms_norm_rope(q, k, params):
+    """Fused per-head RMSNorm + RoPE (+ optional V cache write) for q [B,S,Hq,D] and k [B,S,Hkv,D].
+
+    params: q_weight, k_weight (handles [D]), inv_freq (float32 handle [D/2]), positions (int32 handle
+    [B*S]), eps, and optional q_out / k_out (default: new [B,Hq,S,D] / [B,Hkv,S,D] tensors, i.e. the
+    heads-first layout the attention consumes), v / v_out.  Returns (q_out, k_out)."""
+    if q.dtype != k.dtype or q.dtype not in (FLOAT32, BFLOAT16):
+        raise TypeError("rms_norm_rope: q and k must share a float dtype")
+    if len(q.shape) != 4 or len(k.shape) != 4:
+        raise ValueError("rms_norm_rope: q and k must be [B, S, H, D]")
+    B, S, Hq, D = q.shape
+    _, _, Hkv, _ = k.shape
+    q_out = params.get("q_out") or HipTensorHandle.create_new((B, Hq, S, D), q.dtype)
+    k_out = params.get("k_out") or HipTensorHandle.create_new((B, Hkv, S, D), k.dtype)
+
+    def bsh(h, heads_first):
+        st = h.strides
+        if h.strides[-1] != 1:
+            raise ValueError("rms_norm_rope: head_dim must be contiguous")
+        # heads_first tensors are [B, H, S, D]; the kernel wants (batch, seq, head) strides
+        return [st[0], st[2], st[1]] if heads_first else [st[0], st[1], st[2]]
+
+    v, v_out = params.get("v"), params.get("v_out")
+    s = bsh(q, False) + bsh(k, False) + bsh(q_out, True) + bsh(k_out, True)
+    if v is not None:
+        s += bsh(v, False) + bsh(v_out, True)
+    pos, inv_freq = params["positions"], params["inv_freq"]
+    if pos.dtype != INT32 or pos.numel != B * S:
+        raise ValueError("rms_norm_rope: positions must be int32 with B*S entries")
+    if inv_freq.dtype != FLOAT32 or inv_freq.numel != D // 2:
+        raise ValueError("rms_norm_rope: inv_freq must be float32 [D/2]")
+    _lib.call(
+        "kh_qk_norm_rope",
+        _vp(q.data_ptr()), _vp(k.data_ptr()), _vp(q_out.data_ptr()), _vp(k_out.data_ptr()),
+        _vp(v.data_ptr()) if v is not None else None, _vp(v_out.data_ptr()) if v is not None else None,
+        _vp(params["q_weight"].data_ptr()), _vp(params["k_weight"].data_ptr()),
+        _vp(inv_freq.data_ptr()), _vp(pos.data_ptr()),
+        B, S, Hq, Hkv, D, _lib.i64_array(s), C.c_float(float(params.get("eps", 1e-6))), q.kh_dtype,
+    )
+    return q_out, k_out
+
+
+# ---------------------------------------------------------------------------------------------
+# pointwise (iterator kernels for the same-shape contiguous case the dispatcher prepares)
+# ---------------------------------------------------------------------------------------------
+@dataclass
+class TensorIterator:
+    """Minimal stand-in for ITensorIterator (packages/types/src/tensor.ts:395-569): the dispatcher
+    broadcasts / materialises so every operand is contiguous with the output's shape."""
+
+    inputs: list
+    outputs: list
+
+    def input(self, i: int = 0) -> HipTensorHandle:
+        return self.inputs[i]
+
+    def output(self, i: int = 0) -> HipTensorHandle:
+        return self.outputs[i]
+
+
+def _binary(op: int, it: TensorIterator) -> None:
+    a, b, o = it.input(0), it.input(1), it.output()
+    if not (a.numel == b.numel == o.numel) or not (a.is_contiguous() and b.is_contiguous() and o.is_contiguous()):
+        raise ValueError("binary kernel: operands must be contiguous and of equal size")
+    _lib.call("kh_binary", op, _vp(a.data_ptr()), _vp(b.data_ptr()), _vp(o.data_ptr()), o.numel, o.kh_dtype)
+
+
+def add(it: TensorIterator) -> None:
+    _binary(0, it)
+
+
+def mul(it: TensorIterator) -> None:
+    _binary(1, it)
+
+
+def sub(it: TensorIterator) -> None:
+    _binary(2, it)
+
+
+def silu(it: TensorIterator) -> None:
+    x, o = it.input(0), it.output()
+    if not (x.is_contiguous() and o.is_contiguous()) or x.numel != o.numel:
+        raise ValueError("silu: operands must be contiguous and of equal size")
+    _lib.call("kh_silu", _vp(x.data_ptr()), _vp(o.data_ptr()), o.numel, o.kh_dtype)
+
+
+def silu_mul(gate: HipTensorHandle, up: HipTensorHandle, output: HipTensorHandle) -> None:
+    """output = silu(gate) * up over [..., n]; rows may be strided (e.g. halves of a fused gate/up)."""
+    n = gate.shape[-1]
+    if up.shape != gate.shape or output.shape != gate.shape:
+        raise ValueError("silu_mul: shapes differ")
+    for h in (gate, up, output):
+        if h.strides[-1] != 1:
+            raise ValueError("silu_mul: last dim must be contiguous")
+    rows = gate.numel // n if n else 0
+
+    def row_stride(h):
+        if len(h.shape) == 1:
+            return n
+        # rows must be evenly spaced: all leading dims flatten into one row index
+        lead = [(s, st) for s, st in zip(h.shape[:-1], h.strides[:-1]) if s != 1]
+        rs = lead[-1][1] if lead else n
+        acc = rs
+        for s, st in reversed(lead):
+            if st != acc:
+                raise ValueError("silu_mul: leading dims must flatten to one row stride")
+            acc = st * s
+        return rs
+
+    _lib.call(
+        "kh_silu_mul", _vp(gate.data_ptr()), row_stride(gate), _vp(up.data_ptr()), row_stride(up),
+        _vp(output.data_ptr()), row_stride(output), rows, n, output.kh_dtype,
+    )
+
+
+# ---------------------------------------------------------------------------------------------
+# copy / gather / argmax / factory
+# ---------------------------------------------------------------------------------------------
+def copy(input: HipTensorHandle, options: dict) -> HipTensorHandle:
+    """CopyKernelImpl: contiguous copy of any view, casting to options['target_dtype'] if given."""
+    target = (options or {}).get("target_dtype") or input.dtype
+    out = HipTensorHandle.create_new(input.shape, target)
+    copy_into(input, out)
+    return out
+
+
+def copy_(dst: HipTensorHandle, src: HipTensorHandle) -> None:
+    """In-place copy into a (possibly strided) destination view, e.g. a KV-cache slice
+    (packages/model-utils/src/kv-cache.ts:180-188).  The destination's last dim must be contiguous and
+    its rows evenly described by (batch, head, seq) strides; the source is materialised first."""
+    if dst.shape != src.shape:
+        raise ValueError(f"copy_: shape mismatch {dst.shape} vs {src.shape}")
+    if dst.is_contiguous():
+        copy_into(src, dst)
+        return
+    s = src if (src.is_contiguous() and src.dtype == dst.dtype) else _materialize(src, dst.dtype)
+    try:
+        # Scatter: copy row-blocks of the contiguous source into the strided destination with
+        # strided copies whose *source* is the destination layout read backwards is not expressible;
+        # instead treat the destination as the "source view" of a gather from a contiguous buffer.
+        _scatter_rows(s, dst)
+    finally:
+        if s is not src:
+            s.dispose()
+
+
+def _scatter_rows(src: HipTensorHandle, dst: HipTensorHandle) -> None:
+    # A strided destination is written one contiguous run of its innermost dims at a time.
+    shape, strides = list(dst.shape), list(dst.strides)
+    inner = 1
+    k = len(shape)
+    while k > 0 and strides[k - 1] == inner:
+        inner *= shape[k - 1]
+        k -= 1
+    outer_shape = shape[:k]
+    isz = dst.itemsize
+    for n, idx in enumerate(np.ndindex(*outer_shape) if outer_shape else [()]):
+        off = dst.offset + sum(i * st for i, st in zip(idx, strides[:k]))
+        _lib.call(
+            "kh_memcpy_d2d", _vp(dst.storage.ptr + off * isz), _vp(src.data_ptr() + n * inner * isz), inner * isz
+        )
+
+
+def index_select(self_: HipTensorHandle, index: HipTensorHandle, params: dict, output: HipTensorHandle) -> None:
+    """GatherKernelImpl for dim 0 of a contiguous table (embedding lookup)."""
+    dim = int((params or {}).get("dim", 0))
+    if dim != 0:
+        raise NotImplementedError("index_select: only dim 0 (embedding rows) is implemented")
+    if index.dtype != INT32 or not index.is_contiguous():
+        raise TypeError("index_select: index must be a contiguous int32 tensor")
+    t = self_ if self_.is_contiguous() else _materialize(self_)
+    try:
+        row = int(np.prod(t.shape[1:])) if len(t.shape) > 1 else 1
+        _lib.call(
+            "kh_index_select", _vp(t.data_ptr()), t.shape[0], _vp(index.data_ptr()), index.numel, row,
+            _vp(output.data_ptr()), t.kh_dtype,
+        )
+    finally:
+        if t is not self_:
+            t.dispose()
+
+
+def argmax(it: TensorIterator) -> None:
+    """Row-wise argmax over the last dim (lowest index among maxima), int32 output."""
+    x, o = it.input(0), it.output()
+    xs = x if x.is_contiguous() else _materialize(x)
+    try:
+        n = x.shape[-1]
+        _lib.call("kh_argmax", _vp(xs.data_ptr()), xs.numel // n, n, _vp(o.data_ptr()), xs.kh_dtype)
+    finally:
+        if xs is not x:
+            xs.dispose()
+
+
+def fill(output: HipTensorHandle, value: float) -> None:
+    if not output.is_contiguous():
+        raise ValueError("fill: output must be contiguous")
+    _lib.call("kh_fill", _vp(output.data_ptr()), output.numel, C.c_float(value), output.kh_dtype)
+
+
+def zeros(output: HipTensorHandle) -> None:
+    fill(output, 0.0)
+
+
+KERNELS = {
+    "flash_attention": flash_attention,
+    "decode_attention": decode_attention,
+    "matmul": matmul,
+    "mm": matmul,
+    "bmm": matmul,
+    "addmm": matmul,
+    "baddbmm": matmul,
+    "rms_norm": rms_norm,
+    "rms_norm_rope": rms_norm_rope,
+    "silu": silu,
+    "mul": mul,
+    "add": add,
+    "sub": sub,
+    "silu_mul": silu_mul,
+    "copy": copy,
+    "contiguous": copy,
+    "cast": copy,
+    "copy_": copy_,
+    "index_select": index_select,
+    "argmax": argmax,
+    "fill": fill,
+    "zeros": zeros,
+}

@@ -1,0 +1,161 @@
+"""GPU parity of attention (flash prefill, decode, generic) against the CPU oracle.
+
+Tolerances (from the task's parity bar): fp32 kernels within 1e-4 relative (max-abs error over
+max-abs value); bf16 kernels with fp32 accumulation within 2e-2 absolute on attention outputs.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import dev, max_rel, seeded
+from kandle_amd import Tensor
+from kandle_amd import functional as F
+from kandle_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+BF16_ATOL = 2e-2
+F32_RTOL = 1e-4
+
+
+def _sdpa_gpu(q, k, v, causal, scale=None):
+    o = F.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)
+    out = o.numpy()
+    o.dispose()
+    return out
+
+
+def test_c1_fp32_sdpa_full_size(hip):
+    """Config C1: B=1, Hq=16, Hkv=8, S=256, D=128, causal, scale 1/sqrt(128), fp32."""
+    q, qh = seeded(11, (1, 16, 256, 128))
+    k, kh = seeded(12, (1, 8, 256, 128))
+    v, vh = seeded(13, (1, 8, 256, 128))
+    out = _sdpa_gpu(q, k, v, True)
+    ref = oracle.sdpa(qh, kh, vh, causal=True)
+    assert max_rel(out, ref) < F32_RTOL
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(1, 16, 8, 512), (2, 4, 4, 300), (1, 8, 2, 77), (1, 8, 1, 130),
+                                        (1, 4, 4, 1000)])
+def test_flash_bf16_mfma_matches_oracle(hip, B, Hq, Hkv, S, causal):
+    q, qh = seeded(21, (B, Hq, S, 128), "bfloat16")
+    k, kh = seeded(22, (B, Hkv, S, 128), "bfloat16")
+    v, vh = seeded(23, (B, Hkv, S, 128), "bfloat16")
+    out = _sdpa_gpu(q, k, v, causal)
+    ref = oracle.sdpa(qh, kh, vh, causal=causal)
+    err = float(np.max(np.abs(out - ref)))
+    assert err < BF16_ATOL, err
+
+
+def test_flash_bf16_rectangular_noncausal(hip):
+    """Lq != Lk (prefix attention without a mask)."""
+    q, qh = seeded(31, (1, 4, 40, 128), "bfloat16")
+    k, kh = seeded(32, (1, 2, 200, 128), "bfloat16")
+    v, vh = seeded(33, (1, 2, 200, 128), "bfloat16")
+    out = _sdpa_gpu(q, k, v, False, scale=0.05)
+    ref = oracle.sdpa(qh, kh, vh, scale=0.05)
+    assert np.max(np.abs(out - ref)) < BF16_ATOL
+
+
+def test_flash_bf16_strided_kv_cache_view(hip):
+    """K/V as the [:, :, :end, :] slice of a longer cache (StaticKVCache.update returns such views)."""
+    cache_k, ckh = seeded(41, (1, 2, 512, 128), "bfloat16")
+    cache_v, cvh = seeded(42, (1, 2, 512, 128), "bfloat16")
+    q, qh = seeded(43, (1, 4, 300, 128), "bfloat16")
+    k = F.narrow(cache_k, 2, 0, 300)
+    v = F.narrow(cache_v, 2, 0, 300)
+    out = _sdpa_gpu(q, k, v, True)
+    ref = oracle.sdpa(qh, ckh[:, :, :300], cvh[:, :, :300], causal=True)
+    assert np.max(np.abs(out - ref)) < BF16_ATOL
+
+
+def test_generic_kernel_fp32_small_dims(hip):
+    """Generic path: fp32, D=64, GQA 6/3, ragged lengths, causal."""
+    q, qh = seeded(51, (2, 6, 33, 64))
+    k, kh = seeded(52, (2, 3, 33, 64))
+    v, vh = seeded(53, (2, 3, 33, 64))
+    out = _sdpa_gpu(q, k, v, True)
+    assert max_rel(out, oracle.sdpa(qh, kh, vh, causal=True)) < F32_RTOL
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_sdpa_single_query_routes_to_decode(hip, dtype):
+    """Lq = 1 without a mask (the caller's decode step) through the SDPA entry point."""
+    q, qh = seeded(61, (2, 16, 1, 128), dtype)
+    k, kh = seeded(62, (2, 8, 1000, 128), dtype)
+    v, vh = seeded(63, (2, 8, 1000, 128), dtype)
+    out = _sdpa_gpu(q, k, v, False)
+    ref = oracle.sdpa(qh, kh, vh)
+    if dtype == "float32":
+        assert max_rel(out, ref) < F32_RTOL
+    else:
+        assert np.max(np.abs(out - ref)) < BF16_ATOL
+
+
+def test_single_query_causal_sees_key0_only(hip):
+    """Top-left causal with Lq = 1 masks every key but the first (reference mask k > q)."""
+    q, qh = seeded(64, (1, 2, 1, 128), "bfloat16")
+    k, kh = seeded(65, (1, 1, 50, 128), "bfloat16")
+    v, vh = seeded(66, (1, 1, 50, 128), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    np.testing.assert_allclose(out[0, :, 0], np.repeat(vh[0, :, 0], 2, axis=0), atol=1e-2)
+
+
+def test_decode_varlen_matches_oracle(hip):
+    """Per-sequence KV lengths in one launch, caches [B, Hkv, max_len, D]."""
+    B, Hq, Hkv, D, ML = 4, 16, 8, 128, 3000
+    lens = np.array([1, 257, 1024, 2999], np.int32)
+    q, qh = seeded(71, (B, Hq, D), "bfloat16")
+    kc, kch = seeded(72, (B, Hkv, ML, D), "bfloat16")
+    vc, vch = seeded(73, (B, Hkv, ML, D), "bfloat16")
+    sl = Tensor(lens, dtype="int32")
+    o = F.decode_attention(q, kc, vc, sl).numpy()
+    ref = oracle.sdpa(qh[:, :, None, :], kch, vch, kv_len=lens)[:, :, 0, :]
+    assert np.max(np.abs(o - ref)) < BF16_ATOL
+
+
+def test_decode_c4_full_size(hip):
+    """Config C4 at full size: B=8, Hq=16, Hkv=8, D=128, L_b ~ U[8192, 32768], bf16."""
+    B, Hq, Hkv, D, ML = 8, 16, 8, 128, 32768
+    lens = syn.randint(2024, (B,), 8192, 32769)
+    q, qh = seeded(81, (B, Hq, D), "bfloat16")
+    kc, kch = seeded(82, (B, Hkv, ML, D), "bfloat16")
+    vc, vch = seeded(83, (B, Hkv, ML, D), "bfloat16")
+    sl = Tensor(lens, dtype="int32")
+    o = F.decode_attention(q, kc, vc, sl).numpy()
+    ref = oracle.sdpa(qh[:, :, None, :], kch, vch, kv_len=lens)[:, :, 0, :]
+    assert np.max(np.abs(o - ref)) < BF16_ATOL
+    for t in (q, kc, vc, sl):
+        t.dispose()
+
+
+def test_flash_c3_full_size_sampled_rows(hip):
+    """Config C3 at full size (B=4, Hq=16, Hkv=8, S=4096, D=128, causal, bf16): 48 query rows,
+    including the first and last of each sampled head, are checked exactly against the oracle."""
+    B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
+    q, qh = seeded(91, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(92, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(93, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    assert np.all(np.isfinite(out))
+    r = np.random.default_rng(7)
+    rows = [(0, 0, 0), (3, 15, S - 1), (1, 7, 4095), (2, 8, 1)] + [
+        (int(r.integers(B)), int(r.integers(Hq)), int(r.integers(S))) for _ in range(44)]
+    for b, h, i in rows:
+        hk = h // (Hq // Hkv)
+        ref = oracle.sdpa(qh[b:b + 1, h:h + 1, i:i + 1], kh[b:b + 1, hk:hk + 1, :i + 1],
+                          vh[b:b + 1, hk:hk + 1, :i + 1])
+        err = float(np.max(np.abs(out[b, h, i] - ref[0, 0, 0])))
+        assert err < BF16_ATOL, (b, h, i, err)
+    for t in (q, k, v):
+        t.dispose()
+
+
+def test_flash_rejects_bad_gqa(hip):
+    q, _ = seeded(1, (1, 6, 8, 128), "bfloat16")
+    k, _ = seeded(2, (1, 4, 8, 128), "bfloat16")
+    with pytest.raises(ValueError):
+        F.scaled_dot_product_attention(q, k, k)

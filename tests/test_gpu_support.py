@@ -1,0 +1,126 @@
+"""GPU parity of the support kernels (pointwise, copies, gather, argmax, GEMM) and the allocator."""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import max_rel, seeded
+from kandle_amd import HipBackend, Tensor
+from kandle_amd import functional as F
+from kandle_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_add_mul_broadcast(hip, dtype):
+    a, ah = seeded(201, (3, 5, 64), dtype)
+    b, bh = seeded(202, (5, 64), dtype)
+    s = F.add(a, b).numpy()
+    m = F.mul(a, b).numpy()
+    rs, rm = ah + bh, ah * bh
+    if dtype == "bfloat16":
+        rs, rm = oracle.bf16_round(rs), oracle.bf16_round(rm)
+    np.testing.assert_allclose(s, rs, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(m, rm, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_silu_mul(hip, dtype):
+    g, gh = seeded(210, (7, 3072), dtype, std=4.0)
+    u, uh = seeded(211, (7, 3072), dtype)
+    y = F.silu_mul(g, u).numpy()
+    ref = oracle.silu_mul(gh, uh)
+    if dtype == "float32":
+        assert max_rel(y, ref) < 1e-5
+    else:
+        assert np.all(np.abs(y - ref) <= 2 ** -8 * np.abs(ref) + 1e-6)
+    s = F.silu(g).numpy()
+    refs = oracle.silu_mul(gh)
+    tol = 1e-5 if dtype == "float32" else 2 ** -8
+    assert np.all(np.abs(s - refs) <= tol * np.abs(refs) + 1e-6)
+
+
+def test_silu_mul_strided_halves_of_fused_gate_up(hip):
+    gu, guh = seeded(212, (5, 2 * 256), "bfloat16")
+    g = F.narrow(gu, 1, 0, 256)
+    u = F.narrow(gu, 1, 256, 256)
+    y = F.silu_mul(g, u).numpy()
+    ref = oracle.silu_mul(guh[:, :256], guh[:, 256:])
+    assert np.all(np.abs(y - ref) <= 2 ** -8 * np.abs(ref) + 1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_contiguous_cast_of_permuted_view(hip, dtype):
+    x, xh = seeded(220, (2, 3, 4, 8), dtype)
+    p = F.permute(x, (0, 2, 1, 3))
+    np.testing.assert_array_equal(F.contiguous(p).numpy(), np.transpose(xh, (0, 2, 1, 3)))
+    other = "float32" if dtype == "bfloat16" else "bfloat16"
+    c = F.cast(p, other).numpy()
+    ref = np.transpose(xh, (0, 2, 1, 3))
+    np.testing.assert_array_equal(c, oracle.bf16_round(ref) if other == "bfloat16" else ref)
+
+
+def test_copy_into_strided_cache_slice(hip):
+    cache = F.zeros((1, 2, 16, 8), "float32")
+    src, sh = seeded(221, (1, 2, 3, 8))
+    F.copy_(F.narrow(cache, 2, 5, 3), src)
+    c = cache.numpy()
+    np.testing.assert_array_equal(c[:, :, 5:8], sh)
+    assert np.all(c[:, :, :5] == 0) and np.all(c[:, :, 8:] == 0)
+
+
+def test_embedding_and_argmax(hip):
+    V, H = 1000, 64
+    table, th = seeded(230, (V, H), "bfloat16")
+    ids = syn.randint(231, (2, 7), 0, V)
+    e = F.embedding(Tensor(ids, dtype="int32"), table).numpy()
+    np.testing.assert_array_equal(e, th[ids])
+    x = syn.normal(232, (3, 151936))
+    x[1, 5] = x[1, 77] = 100.0  # tie: lowest index wins
+    x[2, :] = -np.inf
+    x[2, 9] = np.nan
+    a = F.argmax(Tensor(x)).numpy()
+    np.testing.assert_array_equal(a, oracle.argmax(x))
+    assert a[1] == 5 and a[2] == 0
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 1024), (130, 200, 72), (8, 3000, 1024), (1, 151936, 1024),
+                                   (3, 100, 30), (600, 4096, 2048)])
+def test_linear_bf16(hip, M, N, K):
+    x, xh = seeded(240, (M, K), "bfloat16")
+    w, wh = seeded(241, (N, K), "bfloat16", std=0.02)
+    y = F.linear(x, w).numpy()
+    ref = oracle.linear(xh, wh)
+    err = np.abs(y - ref)
+    # one bf16 rounding of the output plus fp32 accumulation-order noise
+    assert np.all(err <= 2 ** -8 * np.abs(ref) + 1e-4 * np.sqrt(K) * 0.02 * 4), float(err.max())
+
+
+def test_linear_fp32_bias_and_residual_epilogue(hip):
+    x, xh = seeded(250, (33, 96))
+    w, wh = seeded(251, (40, 96))
+    b, bh = seeded(252, (40,))
+    c, ch = seeded(253, (33, 40))
+    y = F.linear(x, w, b).numpy()
+    assert max_rel(y, oracle.linear(xh, wh, bias=bh)) < 1e-5
+    z = F.dispatch_matmul(x, w, c=c, alpha=0.5, beta=2.0, transpose_b=True).numpy()
+    assert max_rel(z, oracle.linear(xh, wh, cin=ch, alpha=0.5, beta=2.0)) < 1e-5
+
+
+def test_matmul_batched_fp32(hip):
+    a, ah = seeded(260, (3, 17, 24))
+    b, bh = seeded(261, (3, 24, 9))
+    y = F.matmul(a, b).numpy()
+    assert max_rel(y, np.einsum("bmk,bkn->bmn", ah.astype(np.float64), bh)) < 1e-5
+
+
+def test_allocator_reuses_freed_blocks(hip):
+    before = HipBackend.memory_stats()
+    t = Tensor(np.zeros(1 << 20, np.float32))
+    live = HipBackend.memory_stats()["live_bytes"]
+    t.dispose()
+    t2 = Tensor(np.zeros(1 << 20, np.float32))
+    after = HipBackend.memory_stats()
+    assert after["n_cache_hits"] > before["n_cache_hits"]
+    assert after["live_bytes"] == live
+    t2.dispose()
