@@ -90,6 +90,18 @@ struct Elem<uint16_t> {
   }
 };
 
+// Raw buffer access: a load at a byte offset >= `bytes` returns zero instead of touching memory,
+// so bounds checks need no branch (and no divergent vmcnt bookkeeping).  0x00020000 is the gfx9
+// family's buffer-resource word 3 (32-bit data format, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// 2^x with the hardware instruction (denormal results flush to 0: fine for softmax weights <= 1).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Wave-wide (64 lanes) reductions via cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
