@@ -128,6 +128,37 @@ def bench_norm_rope(steps, warmup):
     return {"T": T, "bytes": float(bytes_), "wall_ms": wall_ms, "dev_ms": dev_ms}
 
 
+def bench_copy(steps, warmup):
+    """Calibration workload for the HBM-traffic counters: a contiguous 1 GiB device-to-device copy
+    through the library's strided-copy kernel (1 GiB read + 1 GiB written per call)."""
+    from kandle_amd import HipTensorHandle, kernels
+
+    n = 1 << 29  # bf16 elements = 1 GiB
+    src = HipTensorHandle.create_new((n,), "bfloat16")
+    kernels.zeros(src)
+    dst = HipTensorHandle.create_new((n,), "bfloat16")
+    from kandle_amd.tensor import copy_into
+
+    wall_ms, dev_ms = time_calls(lambda: copy_into(src, dst), steps, warmup)
+    src.dispose()
+    dst.dispose()
+    return {"bytes": float(2 * n * 2), "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurements
+    (profiles/traffic.json), scaled by the copy-kernel calibration factors; None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        k = t["kernels"][workload]
+        cal = t["calibration"]
+        return float(k["fetch_kib"] * 1024 * cal["fetch_factor"] + k["write_kib"] * 1024 * cal["write_factor"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline_prefill(n_slices=1):
     """The oracle's float32 port of the reference flash algorithm on n (b, head) slices of C3."""
     import oracle
@@ -153,7 +184,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "norm", "copy"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -173,10 +204,13 @@ def main():
     if args.only in (None, "norm"):
         log("norm+rope C2 ...")
         res["norm"] = bench_norm_rope(args.steps, args.warmup)
+    if args.only == "copy":
+        log("copy calibration ...")
+        res["copy"] = bench_copy(args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
-        cpu = cpu_baseline_prefill(1)
+        cpu = cpu_baseline_prefill(16)
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded Philox N(0,1))"}
@@ -189,8 +223,9 @@ def main():
             "config": {"workload": "C3 causal GQA flash-attention prefill", "batch": p["B"], "q_heads": p["Hq"],
                        "kv_heads": p["Hkv"], "seq_len": p["S"], "head_dim": p["D"]},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                         "kernel": "flash_fwd_bf16_d128_kernel", "kernel_ms": round(p["dev_ms"], 4)},
+                         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                         "traffic": measured_traffic("prefill"),
+                         "kernel": "flash_fwd_kernel<64, 8, 1, true>", "kernel_ms": round(p["dev_ms"], 4)},
         })
     if "decode" in res:
         d = res["decode"]
@@ -199,7 +234,8 @@ def main():
                           "sum_len": d["sum_len"], "bytes": d["bytes"], "ms": round(d["dev_ms"], 4),
                           "wall_ms": round(d["wall_ms"], 4), "GB/s": round(gbps, 1),
                           "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
-                                       "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4)}}
+                                       "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                                       "traffic": measured_traffic("decode")}}
         if "value" not in line:
             line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(d["wall_ms"], 4),
                          "config": {"workload": "C4 decode attention"}})
@@ -209,10 +245,16 @@ def main():
         line["norm_rope"] = {"workload": "C2 RMSNorm + qk-norm + RoPE, T=8192, bf16", "bytes": n["bytes"],
                              "ms": round(n["dev_ms"], 4), "GB/s": round(gbps, 1),
                              "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
-                                          "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4)}}
+                                          "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                                          "traffic": measured_traffic("norm")}}
         if "value" not in line:
             line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(n["wall_ms"], 4),
                          "config": {"workload": "C2 norm + rope"}})
+    if "copy" in res:
+        c = res["copy"]
+        gbps = c["bytes"] / (c["dev_ms"] * 1e-3) / 1e9
+        line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(c["wall_ms"], 4),
+                     "config": {"workload": "1 GiB device copy (traffic-counter calibration)"}})
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 
