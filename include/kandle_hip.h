@@ -109,12 +109,13 @@ int kh_silu(const void* x, void* out, int64_t n, int dtype);
 int kh_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,
                 void* out, int64_t out_row_stride, int64_t rows, int64_t n, int dtype);
 
-/* out[i, :] = table[idx[i], :] for n_idx rows of row_elems elements; idx is device int32 and must
- * lie in [0, n_rows) (checked on device: an out-of-range id yields a zero row and sets *bad_count).
+/* out[i, :] = table[idx[i], :] for n_idx rows of row_elems elements; idx is device int32; an id
+ * outside [0, n_rows) yields a zero row (checked on device, never read out of bounds).  The table
+ * has `dtype`, the output `out_dtype` (the same, or float32 from bfloat16).
  * Replaces index_select behind embedding (reference: packages/core/src/dispatch/handlers/composite.ts:149-245;
  * packages/backend-webgpu/src/kernels/gather/index.ts:14-23). */
 int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64_t n_idx, int64_t row_elems,
-                    void* out, int dtype);
+                    void* out, int dtype, int out_dtype);
 
 /* out[r] = the lowest index of the maximum of row r (rows x n, contiguous), int32.
  * Replaces argmax (reference: packages/backend-webgpu/src/kernels/reduction/argShaderBuilder.ts:205-240)
@@ -124,11 +125,12 @@ int kh_argmax(const void* x, int64_t rows, int64_t n, int32_t* out, int dtype);
 /* ------------------------------------------------------------------ hot path ----------------- */
 
 /* y[r, :] = x[r, :] * (1 / sqrt(mean(x[r, :]^2) + eps)) * w[:] (w may be NULL), fp32 math,
- * rows x n, x and y row-strided (contiguous rows).  Replaces the `rms_norm` kernel
+ * rows x n, x and y row-strided (contiguous rows).  x has `dtype`; y and w have `out_dtype` (the
+ * same, or bfloat16 from a float32 residual stream).  Replaces the `rms_norm` kernel
  * (reference: packages/core/src/dispatch/handlers/normalize.ts:46-95;
  * packages/backend-webgpu/src/kernels/normalize/executor.ts:26-183; shaderBuilder.ts:343-414). */
 int kh_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* y, int64_t y_row_stride,
-                int64_t rows, int64_t n, float eps, int dtype);
+                int64_t rows, int64_t n, float eps, int dtype, int out_dtype);
 
 /* Per-head RMSNorm (qk-norm) followed by rotary embedding, for q and k in one launch.
  * Token t of a [n_batch, seq_len] grid has position positions[t]; head h of q is read at
@@ -175,13 +177,15 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
 
 /* C[m, n] = alpha * sum_k A[m, k] * B'[k, n] + beta * Cin[m, n] (+ bias[n]), fp32 accumulate,
  * where B' = B^T with B stored [n, k] (trans_b = 1, the nn.Linear weight layout) or B' = B stored
- * [k, n] (trans_b = 0).  Row strides lda/ldb/ldc/ldcin in elements; cin/bias may be NULL and may
- * alias c.  Replaces the `matmul` kernel's mm path with its alpha/beta/C epilogue
+ * [k, n] (trans_b = 0).  A and B have `dtype`; C, Cin and bias have `out_dtype` (bf16 inputs may
+ * produce fp32 output, e.g. logits; fp32 inputs produce fp32).  Row strides lda/ldb/ldc/ldcin in
+ * elements; cin/bias may be NULL and cin may alias c (in-place residual add).  Replaces the
+ * `matmul` kernel's mm path with its alpha/beta/C epilogue
  * (reference: packages/core/src/dispatch/matmulOps.ts:32-125, :408-496, :649-814;
  * packages/core/src/dispatch/handlers/composite.ts:55-77; packages/backend-webgpu/src/kernels/matrix/executor.ts:438-598). */
 int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
             const void* cin, int64_t ldcin, const void* bias,
-            int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b, int dtype);
+            int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b, int dtype, int out_dtype);
 
 #ifdef __cplusplus
 }

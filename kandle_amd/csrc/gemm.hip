@@ -1,8 +1,10 @@
 // GEMM for the projections: C = alpha * A * B' + beta * Cin (+ bias), fp32 accumulate.
 //
-//  * bf16, trans_b = 1 (nn.Linear weight [n, k]), m > 8: MFMA tile kernel (v_mfma_f32_32x32x16_bf16).
-//  * m <= 8, trans_b = 1: GEMV-style kernel that streams each weight row once (decode, lm_head).
+//  * bf16 inputs, trans_b = 1 (nn.Linear weight [n, k]), m > 8: MFMA tile kernel
+//    (v_mfma_f32_32x32x16_bf16).
+//  * m <= 8, trans_b = 1: weight-streaming kernel that reads each weight row once (decode, lm_head).
 //  * anything else: LDS-tiled fp32-math kernel.
+// The output (and Cin / bias) may be bf16 or fp32 independently of bf16 inputs, e.g. fp32 logits.
 //
 // Reference semantics: out = alpha * op(A) op(B) + beta * C (packages/core/src/dispatch/matmulOps.ts:32-125;
 // epilogue packages/backend-webgpu/src/kernels/matrix/builder.ts:152-218); linear = x W^T + b
@@ -15,20 +17,38 @@ namespace {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-template <typename T>
-__device__ __forceinline__ float epilogue(float acc, float alpha, float beta, const T* cin, int64_t ldcin,
-                                          const T* bias, int64_t m, int64_t n) {
+template <typename TO>
+__device__ __forceinline__ float epilogue(float acc, float alpha, float beta, const TO* cin, int64_t ldcin,
+                                          const TO* bias, int64_t m, int64_t n) {
   float v = alpha * acc;
-  if (cin != nullptr && beta != 0.f) v += beta * Elem<T>::load(cin, m * ldcin + n);
-  if (bias != nullptr) v += Elem<T>::load(bias, n);
+  if (cin != nullptr && beta != 0.f) v += beta * Elem<TO>::load(cin, m * ldcin + n);
+  if (bias != nullptr) v += Elem<TO>::load(bias, n);
   return v;
+}
+
+// Four consecutive outputs of one row, vectorised when the row start allows it.
+template <typename TO>
+__device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], bool vec, int valid) {
+  if (vec && valid == 4) {
+    if constexpr (sizeof(TO) == 2) {
+      uint2 w;
+      w.x = pack_bf16x2(v[0], v[1]);
+      w.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(C + off) = w;
+    } else {
+      *reinterpret_cast<float4*>(C + off) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  } else {
+    for (int e = 0; e < valid; ++e) Elem<TO>::store(C, off + e, v[e]);
+  }
 }
 
 // =============================================================================================
 // MFMA tile kernel.  Workgroup tile 128 (m) x 128 (n), k-step 64, 4 waves in a 2 x 2 layout, each
 // wave 64 x 64 = 2 x 2 tiles of 32 x 32.  The product is formed as C^T = B A^T so that each lane
-// owns one m row and 4 consecutive n per register group (8-byte stores): A-operand = B rows (n),
-// B-operand = A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered.
+// owns one m row and 4 consecutive n per register group: A-operand = B rows (n), B-operand = A rows
+// (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are raw buffer loads
+// (rows past M / N and columns past K read as zero without a branch).
 // =============================================================================================
 constexpr int GM = 128, GN = 128, GK = 64;
 constexpr int G_THREADS = 256;
@@ -36,29 +56,35 @@ constexpr int G_STR = GK + 8;  // LDS row stride (elements), keeps 16-byte align
 constexpr int G_ATILE = GM * G_STR;
 constexpr int G_BTILE = GN * G_STR;
 
+template <typename TO>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
-    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, uint16_t* C,
-    int64_t ldc, const uint16_t* cin, int64_t ldcin, const uint16_t* __restrict__ bias, int M, int N, int K,
-    float alpha, float beta, int tiles_n) {
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
+    const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
+    int tiles_n) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (G_ATILE + G_BTILE)];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, g = lane >> 5;
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
   const int m0 = tm * GM, n0 = tn * GN;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
 
-  // Staging: each of A and B tiles is 128 rows x 64 k = 1024 chunks of 16 B, 4 per thread.
+  // Byte ranges of this tile's rows; a row past the matrix or a column past K reads zero.
+  const int mrows = min(GM, M - m0), nrows = min(GN, N - n0);
+  const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * 2));
+  const auto rb = make_rsrc(B + (int64_t)n0 * ldb, (uint32_t)(((int64_t)(nrows - 1) * ldb + K) * 2));
+
+  // Staging: each of the A and B tiles is 128 rows x 64 k = 1024 chunks of 16 B, 4 per thread.
   uint4 ast[4], bst[4];
   auto load_tile = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = tid + G_THREADS * i;
-      const int row = id >> 3, kc = 8 * (id & 7);
-      const int kk = kt + kc;
-      ast[i] = make_uint4(0, 0, 0, 0);
-      bst[i] = make_uint4(0, 0, 0, 0);
-      if (m0 + row < M && kk < K) ast[i] = *reinterpret_cast<const uint4*>(A + (int64_t)(m0 + row) * lda + kk);
-      if (n0 + row < N && kk < K) bst[i] = *reinterpret_cast<const uint4*>(B + (int64_t)(n0 + row) * ldb + kk);
+      const int row = id >> 3, kc = kt + 8 * (id & 7);
+      // Columns >= K map past the range (K % 8 == 0, so a chunk is all in or all out).
+      const int64_t ao = kc < K ? (int64_t)row * lda + kc : (int64_t)1 << 40;
+      const int64_t bo = kc < K ? (int64_t)row * ldb + kc : (int64_t)1 << 40;
+      ast[i] = buf_load16(ra, (uint32_t)min<int64_t>(ao * 2, 0xffffffffLL));
+      bst[i] = buf_load16(rb, (uint32_t)min<int64_t>(bo * 2, 0xffffffffLL));
     }
   };
   auto store_tile = [&](int buf) {
@@ -84,6 +110,7 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   const int nk = (K + GK - 1) / GK;
   load_tile(0);
   store_tile(0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int t = 0; t < nk; ++t) {
     const int buf = t & 1;
@@ -110,8 +137,7 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   }
 
   // Epilogue: acc[a][b] lane holds m = m0 + wm + 32b + r, n = n0 + wn + 32a + 8(j/4) + 4g + j%4.
-  // 8-byte stores need an 8-byte aligned C row start (n is a multiple of 4).
-  const bool vec_store = ((reinterpret_cast<uintptr_t>(C) & 7u) == 0) && ((ldc & 3) == 0);
+  const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     const int m = m0 + wm + 32 * b + r;
@@ -121,34 +147,27 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
+        if (n >= N) continue;
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          v[e] = (n + e < N) ? epilogue<uint16_t>(acc[a][b][4 * q + e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
-        if (n + 3 < N && vec_store) {
-          uint2 w;
-          w.x = pack_bf16x2(v[0], v[1]);
-          w.y = pack_bf16x2(v[2], v[3]);
-          *reinterpret_cast<uint2*>(C + (int64_t)m * ldc + n) = w;
-        } else {
-          for (int e = 0; e < 4; ++e)
-            if (n + e < N) C[(int64_t)m * ldc + n + e] = (uint16_t)f32_to_bf16_bits(v[e]);
-        }
+          v[e] = (n + e < N) ? epilogue<TO>(acc[a][b][4 * q + e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
+        store4<TO>(C, (int64_t)m * ldc + n, v, vec, min(4, N - n));
       }
   }
 }
 
 // =============================================================================================
 // Skinny kernel for m <= 8 (trans_b = 1): each wave owns output columns n and streams weight row n
-// once with 16-byte loads; the m rows of A are kept in LDS.
+// once with 16-byte loads; the m rows of A are kept in LDS as fp32.
 // =============================================================================================
 constexpr int SK_MAXM = 8;
 constexpr int SK_ROWS_PER_WAVE = 4;  // weight rows in flight per wave step
 
-template <typename T>
+template <typename T, typename TO>
 __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
-                                                      int64_t ldb, T* C, int64_t ldc, const T* cin, int64_t ldcin,
-                                                      const T* __restrict__ bias, int M, int N, int K, float alpha,
+                                                      int64_t ldb, TO* C, int64_t ldc, const TO* cin, int64_t ldcin,
+                                                      const TO* __restrict__ bias, int M, int N, int K, float alpha,
                                                       float beta) {
   extern __shared__ float xs[];  // [M][K] fp32
   for (int i = threadIdx.x; i < M * K; i += blockDim.x) {
@@ -219,20 +238,20 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
           const float s = wave_sum(acc[rr][mm]);
           const int n = n0 + rr;
           if (lane == 0 && n < N)
-            Elem<T>::store(C, (int64_t)mm * ldc + n, epilogue<T>(s, alpha, beta, cin, ldcin, bias, mm, n));
+            Elem<TO>::store(C, (int64_t)mm * ldc + n, epilogue<TO>(s, alpha, beta, cin, ldcin, bias, mm, n));
         }
       }
   }
 }
 
 // =============================================================================================
-// Generic tiled kernel (f32 or bf16 storage, trans_b 0/1): 16 x 16 threads, 64 x 64 tile,
-// each thread 4 x 4 outputs, fp32 math.
+// Generic tiled kernel (f32 or bf16 storage, trans_b 0/1): 16 x 16 threads, 64 x 64 tile, each
+// thread 4 x 4 outputs, fp32 math.
 // =============================================================================================
-template <typename T>
+template <typename T, typename TO>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__ A, int64_t lda,
-                                                           const T* __restrict__ B, int64_t ldb, T* C, int64_t ldc,
-                                                           const T* cin, int64_t ldcin, const T* __restrict__ bias,
+                                                           const T* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
+                                                           const TO* cin, int64_t ldcin, const TO* __restrict__ bias,
                                                            int M, int N, int K, float alpha, float beta, int trans_b) {
   __shared__ float As[16][64 + 1];
   __shared__ float Bs[16][64 + 1];
@@ -246,7 +265,8 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
       As[kk][mm] = (gm < M && gk < K) ? Elem<T>::load(A, (int64_t)gm * lda + gk) : 0.f;
       const int gn = n0 + mm;
       float bv = 0.f;
-      if (gn < N && gk < K) bv = trans_b ? Elem<T>::load(B, (int64_t)gn * ldb + gk) : Elem<T>::load(B, (int64_t)gk * ldb + gn);
+      if (gn < N && gk < K)
+        bv = trans_b ? Elem<T>::load(B, (int64_t)gn * ldb + gk) : Elem<T>::load(B, (int64_t)gk * ldb + gn);
       Bs[kk][mm] = bv;
     }
     __syncthreads();
@@ -263,8 +283,47 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
-      if (m < M && n < N) Elem<T>::store(C, (int64_t)m * ldc + n, epilogue<T>(acc[i][j], alpha, beta, cin, ldcin, bias, m, n));
+      if (m < M && n < N)
+        Elem<TO>::store(C, (int64_t)m * ldc + n, epilogue<TO>(acc[i][j], alpha, beta, cin, ldcin, bias, m, n));
     }
+}
+
+template <typename T, typename TO>
+int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, const void* cin,
+                int64_t ldcin, const void* bias, int M, int N, int K, float alpha, float beta, int trans_b) {
+  const T* A = (const T*)a;
+  const T* B = (const T*)b;
+  TO* C = (TO*)c;
+  const TO* CI = (const TO*)cin;
+  const TO* BI = (const TO*)bias;
+  constexpr bool is_bf16 = sizeof(T) == 2;
+  const int64_t lim = int64_t(1) << 31;
+  if (is_bf16 && trans_b && M > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) &&
+      aligned16(b) && (int64_t)GM * lda * 2 < lim && (int64_t)GN * ldb * 2 < lim) {
+    const int tiles_m = (M + GM - 1) / GM, tiles_n = (N + GN - 1) / GN;
+    const int64_t nblk = (int64_t)tiles_m * tiles_n;
+    KH_REQUIRE(nblk <= INT32_MAX, "kh_gemm: grid too large");
+    if constexpr (is_bf16)
+      gemm_bf16_nt_kernel<TO><<<(int)nblk, G_THREADS, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K,
+                                                                     alpha, beta, tiles_n);
+    KH_CHECK_LAUNCH();
+    return KH_OK;
+  }
+  if (trans_b && M <= SK_MAXM && (size_t)M * K * sizeof(float) <= 64 * 1024 && aligned16(b)) {
+    const int waves_needed = (N + SK_ROWS_PER_WAVE - 1) / SK_ROWS_PER_WAVE;
+    int grid = (waves_needed + 3) / 4;
+    if (grid > 4096) grid = 4096;
+    const size_t shm = (size_t)M * K * sizeof(float);
+    gemv_nt_kernel<T, TO><<<grid, 256, shm, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta);
+    KH_CHECK_LAUNCH();
+    return KH_OK;
+  }
+  dim3 grid((N + 63) / 64, (M + 63) / 64);
+  KH_REQUIRE(grid.y <= 65535, "kh_gemm: m too large for the generic kernel");
+  gemm_generic_kernel<T, TO><<<grid, 256, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
+                                                         trans_b);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 }  // namespace
@@ -273,55 +332,23 @@ extern "C" {
 
 int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, const void* cin,
             int64_t ldcin, const void* bias, int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b,
-            int dtype) {
+            int dtype, int out_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(m >= 0 && n >= 0 && k >= 0, "kh_gemm: negative extent");
   KH_REQUIRE(m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX, "kh_gemm: extent too large");
   KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_gemm: unsupported dtype %d", dtype);
+  KH_REQUIRE(out_dtype == KH_BF16 || out_dtype == KH_F32, "kh_gemm: unsupported output dtype %d", out_dtype);
+  KH_REQUIRE(!(dtype == KH_F32 && out_dtype == KH_BF16), "kh_gemm: fp32 inputs with a bf16 output are not supported");
   if (m == 0 || n == 0) return KH_OK;
   KH_REQUIRE(a && b && c, "kh_gemm: null pointer");
   KH_REQUIRE(lda >= k && ldc >= n && (trans_b ? ldb >= k : ldb >= n), "kh_gemm: leading dimension too small");
   KH_REQUIRE(cin == nullptr || ldcin >= n, "kh_gemm: ldcin too small");
   const int M = (int)m, N = (int)n, K = (int)k;
-  if (dtype == KH_BF16 && trans_b && m > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) &&
-      aligned16(b)) {
-    const int tiles_m = (M + GM - 1) / GM, tiles_n = (N + GN - 1) / GN;
-    const int64_t nblk = (int64_t)tiles_m * tiles_n;
-    KH_REQUIRE(nblk <= INT32_MAX, "kh_gemm: grid too large");
-    gemm_bf16_nt_kernel<<<(int)nblk, G_THREADS, 0, stream()>>>(
-        (const uint16_t*)a, lda, (const uint16_t*)b, ldb, (uint16_t*)c, ldc, (const uint16_t*)cin, ldcin,
-        (const uint16_t*)bias, M, N, K, alpha, beta, tiles_n);
-    KH_CHECK_LAUNCH();
-    return KH_OK;
-  }
-  if (trans_b && m <= SK_MAXM && (size_t)m * k * sizeof(float) <= 64 * 1024 && aligned16(b)) {
-    const int waves_needed = (N + SK_ROWS_PER_WAVE - 1) / SK_ROWS_PER_WAVE;
-    int grid = (waves_needed + 3) / 4;
-    if (grid > 4096) grid = 4096;
-    const size_t shm = (size_t)m * k * sizeof(float);
-    if (dtype == KH_BF16)
-      gemv_nt_kernel<uint16_t><<<grid, 256, shm, stream()>>>((const uint16_t*)a, lda, (const uint16_t*)b, ldb,
-                                                             (uint16_t*)c, ldc, (const uint16_t*)cin, ldcin,
-                                                             (const uint16_t*)bias, M, N, K, alpha, beta);
-    else
-      gemv_nt_kernel<float><<<grid, 256, shm, stream()>>>((const float*)a, lda, (const float*)b, ldb, (float*)c, ldc,
-                                                          (const float*)cin, ldcin, (const float*)bias, M, N, K, alpha,
-                                                          beta);
-    KH_CHECK_LAUNCH();
-    return KH_OK;
-  }
-  dim3 grid((N + 63) / 64, (M + 63) / 64);
-  KH_REQUIRE(grid.y <= 65535, "kh_gemm: m too large for the generic kernel");
+  if (dtype == KH_BF16 && out_dtype == KH_BF16)
+    return launch_gemm<uint16_t, uint16_t>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
   if (dtype == KH_BF16)
-    gemm_generic_kernel<uint16_t><<<grid, 256, 0, stream()>>>((const uint16_t*)a, lda, (const uint16_t*)b, ldb,
-                                                              (uint16_t*)c, ldc, (const uint16_t*)cin, ldcin,
-                                                              (const uint16_t*)bias, M, N, K, alpha, beta, trans_b);
-  else
-    gemm_generic_kernel<float><<<grid, 256, 0, stream()>>>((const float*)a, lda, (const float*)b, ldb, (float*)c, ldc,
-                                                           (const float*)cin, ldcin, (const float*)bias, M, N, K, alpha,
-                                                           beta, trans_b);
-  KH_CHECK_LAUNCH();
-  return KH_OK;
+    return launch_gemm<uint16_t, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
+  return launch_gemm<float, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
 }
 
 }  // extern "C"

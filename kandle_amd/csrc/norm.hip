@@ -40,22 +40,23 @@ struct Vec8<float> {
 };
 
 // ---- RMSNorm: one wave per row, row kept in registers (n <= 64 * 8 * CPL) -----------------
-template <typename T, int CPL>
-__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const T* __restrict__ x, int64_t xs,
-                                                            const T* __restrict__ w, T* __restrict__ y,
+// x has element type TI; w and y have TO (e.g. a float32 residual stream normalised into bf16).
+template <typename TI, typename TO, int CPL>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const TI* __restrict__ x, int64_t xs,
+                                                            const TO* __restrict__ w, TO* __restrict__ y,
                                                             int64_t ys, int64_t rows, int n, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nchunks = n >> 3;
-  const T* xr = x + row * xs;
+  const TI* xr = x + row * xs;
   float v[CPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = lane + 64 * c;
     if (ch < nchunks) {
-      Vec8<T>::load(xr + ch * 8, v[c]);
+      Vec8<TI>::load(xr + ch * 8, v[c]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
     }
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(const T* __restrict__
   ss = wave_sum(ss);
   const float rms = sqrtf(ss / (float)n + eps);
   const float inv = 1.0f / rms;
-  T* yr = y + row * ys;
+  TO* yr = y + row * ys;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = lane + 64 * c;
@@ -71,39 +72,39 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(const T* __restrict__
       float o[8];
       if (w != nullptr) {
         float wv[8];
-        Vec8<T>::load(w + ch * 8, wv);
+        Vec8<TO>::load(w + ch * 8, wv);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (v[c][j] * inv) * wv[j];
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = v[c][j] * inv;
       }
-      Vec8<T>::store(yr + ch * 8, o);
+      Vec8<TO>::store(yr + ch * 8, o);
     }
   }
 }
 
 // Generic RMSNorm (any n, any alignment): one wave per row, two passes over the row.
-template <typename T>
-__global__ __launch_bounds__(256) void rms_norm_generic_kernel(const T* __restrict__ x, int64_t xs,
-                                                                const T* __restrict__ w, T* __restrict__ y,
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void rms_norm_generic_kernel(const TI* __restrict__ x, int64_t xs,
+                                                                const TO* __restrict__ w, TO* __restrict__ y,
                                                                 int64_t ys, int64_t rows, int64_t n, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const T* xr = x + row * xs;
+  const TI* xr = x + row * xs;
   float ss = 0.f;
   for (int64_t i = lane; i < n; i += 64) {
-    const float v = Elem<T>::load(xr, i);
+    const float v = Elem<TI>::load(xr, i);
     ss += v * v;
   }
   ss = wave_sum(ss);
   const float rms = sqrtf(ss / (float)n + eps);
   const float inv = 1.0f / rms;
-  T* yr = y + row * ys;
+  TO* yr = y + row * ys;
   for (int64_t i = lane; i < n; i += 64) {
-    const float nv = Elem<T>::load(xr, i) * inv;
-    Elem<T>::store(yr, i, w != nullptr ? nv * Elem<T>::load(w, i) : nv);
+    const float nv = Elem<TI>::load(xr, i) * inv;
+    Elem<TO>::store(yr, i, w != nullptr ? nv * Elem<TO>::load(w, i) : nv);
   }
 }
 
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
-template <typename T>
+template <typename TI, typename TO>
 int launch_rms_norm(const void* x, int64_t xs, const void* w, void* y, int64_t ys, int64_t rows, int64_t n,
                     float eps) {
   const int waves = 4;
@@ -209,19 +210,19 @@ int launch_rms_norm(const void* x, int64_t xs, const void* w, void* y, int64_t y
   KH_REQUIRE(grid <= INT32_MAX, "kh_rms_norm: too many rows");
   const bool vec = n % 8 == 0 && xs % 8 == 0 && ys % 8 == 0 && aligned16(x) && aligned16(y) &&
                    (w == nullptr || aligned16(w));
-  const T* xp = (const T*)x;
-  const T* wp = (const T*)w;
-  T* yp = (T*)y;
+  const TI* xp = (const TI*)x;
+  const TO* wp = (const TO*)w;
+  TO* yp = (TO*)y;
   if (vec && n <= 64 * 8 * 1)
-    rms_norm_vec_kernel<T, 1><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
+    rms_norm_vec_kernel<TI, TO, 1><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
   else if (vec && n <= 64 * 8 * 2)
-    rms_norm_vec_kernel<T, 2><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
+    rms_norm_vec_kernel<TI, TO, 2><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
   else if (vec && n <= 64 * 8 * 4)
-    rms_norm_vec_kernel<T, 4><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
+    rms_norm_vec_kernel<TI, TO, 4><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
   else if (vec && n <= 64 * 8 * 8)
-    rms_norm_vec_kernel<T, 8><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
+    rms_norm_vec_kernel<TI, TO, 8><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, (int)n, eps);
   else
-    rms_norm_generic_kernel<T><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, n, eps);
+    rms_norm_generic_kernel<TI, TO><<<(int)grid, 64 * waves, 0, stream()>>>(xp, xs, wp, yp, ys, rows, n, eps);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
@@ -231,15 +232,21 @@ int launch_rms_norm(const void* x, int64_t xs, const void* w, void* y, int64_t y
 extern "C" {
 
 int kh_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* y, int64_t y_row_stride, int64_t rows,
-                int64_t n, float eps, int dtype) {
+                int64_t n, float eps, int dtype, int out_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(rows >= 0 && n > 0, "kh_rms_norm: bad extents (rows %lld, n %lld)", (long long)rows, (long long)n);
   if (rows == 0) return KH_OK;
   KH_REQUIRE(x && y, "kh_rms_norm: null pointer");
   KH_REQUIRE(x_row_stride >= n && y_row_stride >= n, "kh_rms_norm: row strides must be >= n");
-  if (dtype == KH_BF16) return launch_rms_norm<uint16_t>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
-  if (dtype == KH_F32) return launch_rms_norm<float>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
-  KH_REQUIRE(false, "kh_rms_norm: unsupported dtype %d", dtype);
+  if (dtype == KH_BF16 && out_dtype == KH_BF16)
+    return launch_rms_norm<uint16_t, uint16_t>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
+  if (dtype == KH_F32 && out_dtype == KH_F32)
+    return launch_rms_norm<float, float>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
+  if (dtype == KH_F32 && out_dtype == KH_BF16)
+    return launch_rms_norm<float, uint16_t>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
+  if (dtype == KH_BF16 && out_dtype == KH_F32)
+    return launch_rms_norm<uint16_t, float>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
+  KH_REQUIRE(false, "kh_rms_norm: unsupported dtypes (in %d, out %d)", dtype, out_dtype);
 }
 
 int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out, const void* v, void* v_out,

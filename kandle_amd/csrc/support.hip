@@ -143,15 +143,18 @@ __global__ void silu_mul_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t g
 }
 
 // ---- index_select -------------------------------------------------------------------------
-template <typename T>
+// Rows of `table` (element type T) gathered into `out` (element type D, converted through fp32);
+// an id outside [0, n_rows) yields a zero row.
+template <typename T, typename D>
 __global__ void index_select_kernel(const T* __restrict__ table, int64_t n_rows, const int32_t* __restrict__ idx,
-                                    int64_t row_elems, T* __restrict__ out) {
+                                    int64_t row_elems, D* __restrict__ out) {
   const int64_t r = blockIdx.x;
   const int32_t id = idx[r];
   const bool ok = id >= 0 && id < n_rows;
   const T* src = table + (ok ? (int64_t)id : 0) * row_elems;
-  T* dst = out + r * row_elems;
-  for (int64_t c = threadIdx.x; c < row_elems; c += blockDim.x) dst[c] = ok ? src[c] : T(0);
+  D* dst = out + r * row_elems;
+  for (int64_t c = threadIdx.x; c < row_elems; c += blockDim.x)
+    Elem<D>::store(dst, c, ok ? Elem<T>::load(src, c) : 0.0f);
 }
 
 // ---- argmax (lowest index among maxima; NaN never wins; init -FLT_MAX at index 0) ----------
@@ -313,20 +316,27 @@ int kh_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64
 }
 
 int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64_t n_idx, int64_t row_elems,
-                    void* out, int dtype) {
+                    void* out, int dtype, int out_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(n_rows > 0 && n_idx >= 0 && row_elems > 0, "kh_index_select: bad extents");
   if (n_idx == 0) return KH_OK;
   KH_REQUIRE(n_idx <= INT32_MAX, "kh_index_select: too many indices");
   KH_REQUIRE(table && idx && out, "kh_index_select: null pointer");
-  if (dtype == KH_BF16)
-    index_select_kernel<uint16_t><<<(int)n_idx, kThreads, 0, stream()>>>((const uint16_t*)table, n_rows, idx,
-                                                                         row_elems, (uint16_t*)out);
-  else if (dtype == KH_F32)
-    index_select_kernel<float><<<(int)n_idx, kThreads, 0, stream()>>>((const float*)table, n_rows, idx, row_elems,
-                                                                      (float*)out);
+  const dim3 grid((unsigned)n_idx), block(kThreads);
+  if (dtype == KH_BF16 && out_dtype == KH_BF16)
+    index_select_kernel<uint16_t, uint16_t><<<grid, block, 0, stream()>>>((const uint16_t*)table, n_rows, idx,
+                                                                          row_elems, (uint16_t*)out);
+  else if (dtype == KH_BF16 && out_dtype == KH_F32)
+    index_select_kernel<uint16_t, float><<<grid, block, 0, stream()>>>((const uint16_t*)table, n_rows, idx,
+                                                                       row_elems, (float*)out);
+  else if (dtype == KH_F32 && out_dtype == KH_F32)
+    index_select_kernel<float, float><<<grid, block, 0, stream()>>>((const float*)table, n_rows, idx, row_elems,
+                                                                    (float*)out);
+  else if (dtype == KH_F32 && out_dtype == KH_BF16)
+    index_select_kernel<float, uint16_t><<<grid, block, 0, stream()>>>((const float*)table, n_rows, idx,
+                                                                       row_elems, (uint16_t*)out);
   else
-    KH_REQUIRE(false, "kh_index_select: unsupported dtype %d", dtype);
+    KH_REQUIRE(false, "kh_index_select: unsupported dtypes (table %d, out %d)", dtype, out_dtype);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

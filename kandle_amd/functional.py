@@ -84,8 +84,9 @@ def decode_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, seq_lens: Tens
 # ---------------------------------------------------------------------------------------------
 def dispatch_matmul(a: Tensor, b: Tensor, c: Optional[Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
                     out: Optional[Tensor] = None, transpose_a: bool = False, transpose_b: bool = False,
-                    bias: Optional[Tensor] = None) -> Tensor:
-    """out = alpha * a @ op(b) + beta * c (+ bias).  With transpose_b, b is stored [..., N, K]."""
+                    bias: Optional[Tensor] = None, out_dtype: Optional[str] = None) -> Tensor:
+    """out = alpha * a @ op(b) + beta * c (+ bias).  With transpose_b, b is stored [..., N, K].
+    out_dtype (default: the input dtype) may be float32 for bfloat16 inputs."""
     if a.device != b.device:
         raise RuntimeError(f"matmul requires tensors on same device, got {a.device} and {b.device}")
     for t, nm in ((a, "a"), (b, "b")):
@@ -119,7 +120,7 @@ def dispatch_matmul(a: Tensor, b: Tensor, c: Optional[Tensor] = None, alpha: flo
             raise ValueError(f"matmul: out shape {out.shape} != {tuple(out_shape)}")
         output = out.handle
     else:
-        output = _new(a, out_shape)
+        output = _new(a, out_shape, out_dtype)
     variant = "mm" if not batch_shape else "bmm"
     cfg = MatmulDispatchResult(variant=variant, output=output, M=M, K=K, N=N, batch_shape=tuple(batch_shape),
                                batch_size=int(np.prod(batch_shape)) if batch_shape else 1, transpose_a=False,
@@ -145,18 +146,20 @@ def matmul(a: Tensor, b: Tensor) -> Tensor:
     return dispatch_matmul(a, b)
 
 
-def linear(input: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+def linear(input: Tensor, weight: Tensor, bias: Optional[Tensor] = None, out_dtype: Optional[str] = None) -> Tensor:
     """y = input @ weight^T + bias with weight [out_features, in_features] (nn.Linear layout)."""
-    return dispatch_matmul(input, weight, transpose_b=True, bias=bias)
+    return dispatch_matmul(input, weight, transpose_b=True, bias=bias, out_dtype=out_dtype)
 
 
 # ---------------------------------------------------------------------------------------------
 # normalisation and pointwise
 # ---------------------------------------------------------------------------------------------
 def rms_norm(input: Tensor, normalized_shape: Sequence[int], weight: Optional[Tensor] = None,
-             eps: Optional[float] = None) -> Tensor:
+             eps: Optional[float] = None, out_dtype: Optional[str] = None) -> Tensor:
+    """RMSNorm over the trailing normalized_shape dims; out_dtype (default: the input dtype) is the
+    dtype of the result and of the weight."""
     params = {"normalized_shape": list(normalized_shape), "eps": eps,
-              "weight": weight.handle if weight is not None else None}
+              "weight": weight.handle if weight is not None else None, "out_dtype": out_dtype}
     return _wrap(_kernel(input, "rms_norm")([input.handle], params))
 
 
@@ -239,10 +242,11 @@ def copy_(dst: Tensor, src: Tensor) -> Tensor:
     return dst
 
 
-def embedding(input_ids: Tensor, weight: Tensor) -> Tensor:
-    """weight[input_ids] with ids int32 of any shape -> ids.shape + [hidden]."""
+def embedding(input_ids: Tensor, weight: Tensor, out_dtype: Optional[str] = None) -> Tensor:
+    """weight[input_ids] with ids int32 of any shape -> ids.shape + [hidden], in out_dtype
+    (default: the table's dtype); ids outside the table give zero rows."""
     ids = input_ids if input_ids.handle.is_contiguous() else contiguous(input_ids)
-    out = _new(weight, tuple(input_ids.shape) + tuple(weight.shape[1:]))
+    out = _new(weight, tuple(input_ids.shape) + tuple(weight.shape[1:]), out_dtype)
     _kernel(weight, "index_select")(weight.handle, ids.handle, {"dim": 0}, out)
     if ids is not input_ids:
         ids.dispose()

@@ -157,10 +157,12 @@ def matmul(config: MatmulDispatchResult, a: HipTensorHandle, b: HipTensorHandle)
 
     `b` is [..., K, N] (transpose_b False) or [..., N, K] (transpose_b True, the nn.Linear weight)."""
     out = config.output
-    if a.dtype != b.dtype or a.dtype != out.dtype:
-        raise TypeError(f"matmul: dtype mismatch {a.dtype}, {b.dtype} -> {out.dtype}")
+    if a.dtype != b.dtype:
+        raise TypeError(f"matmul: dtype mismatch {a.dtype} vs {b.dtype}")
     if a.dtype not in (FLOAT32, BFLOAT16):
         raise TypeError(f"matmul does not support dtype {a.dtype}")
+    if out.dtype != a.dtype and not (a.dtype == BFLOAT16 and out.dtype == FLOAT32):
+        raise TypeError(f"matmul: {a.dtype} inputs cannot produce a {out.dtype} output")
     if config.transpose_a:
         raise NotImplementedError("matmul: transpose_a is materialised by the dispatcher")
     M, K, N = config.M, config.K, config.N
@@ -210,6 +212,7 @@ def _batch_offsets(h: HipTensorHandle, batch_shape, mat_dims: int):
 def _gemm_call(A, lda, Bm, out, N, config, rows, a_off, b_off, c_off):
     K = config.K
     isz = A.itemsize
+    osz = out.itemsize
     # [.., N, K] (transpose_b) or [.., K, N]: either way the row stride of the stored matrix.
     ldb = Bm.strides[-2] if len(Bm.shape) >= 2 else Bm.shape[-1]
     cin = config.input_c
@@ -217,21 +220,22 @@ def _gemm_call(A, lda, Bm, out, N, config, rows, a_off, b_off, c_off):
     if cin is not None and config.beta != 0.0:
         if tuple(cin.shape[-2:]) != (config.M, N) or not cin.is_contiguous() or cin.dtype != out.dtype:
             raise ValueError("matmul: inputC must be a contiguous [.., M, N] tensor of the output dtype")
-        cin_ptr = cin.data_ptr() + c_off * isz
+        cin_ptr = cin.data_ptr() + c_off * osz
     bias_ptr = None
     if config.bias is not None:
-        if config.bias.shape != (N,) or not config.bias.is_contiguous():
-            raise ValueError("matmul: bias must be a contiguous [N] tensor")
+        if config.bias.shape != (N,) or not config.bias.is_contiguous() or config.bias.dtype != out.dtype:
+            raise ValueError("matmul: bias must be a contiguous [N] tensor of the output dtype")
         bias_ptr = config.bias.data_ptr()
     lda_eff = lda if lda else K
     _lib.call(
         "kh_gemm",
         _vp(A.data_ptr() + a_off * isz), lda_eff,
         _vp(Bm.data_ptr() + b_off * isz), ldb,
-        _vp(out.data_ptr() + c_off * isz), N,
+        _vp(out.data_ptr() + c_off * osz), N,
         _vp(cin_ptr) if cin_ptr else None, ldcin,
         _vp(bias_ptr) if bias_ptr else None,
         rows, N, K, C.c_float(config.alpha), C.c_float(config.beta), int(bool(config.transpose_b)), A.kh_dtype,
+        out.kh_dtype,
     )
 
 
@@ -239,11 +243,12 @@ def _gemm_call(A, lda, Bm, out, N, config, rows, a_off, b_off, c_off):
 # normalisation / fused qk-norm + RoPE
 # ---------------------------------------------------------------------------------------------
 def rms_norm(inputs, params) -> HipTensorHandle:
-    """NormalizeKernelImpl: inputs = [x], params = {normalized_shape, eps, weight?, out?}.
+    """NormalizeKernelImpl: inputs = [x], params = {normalized_shape, eps, weight?, out?, out_dtype?}.
 
     Normalises over the trailing dims given by normalized_shape; output is contiguous
     (packages/backend-webgpu/src/kernels/normalize/executor.ts:121-122).  The kernel default eps is
-    1e-5 (executor.ts:58)."""
+    1e-5 (executor.ts:58).  out_dtype (default: the input dtype) lets a float32 residual stream be
+    normalised straight into a bfloat16 activation; the weight then has out_dtype."""
     x = inputs[0]
     ns = params.get("normalized_shape") or params.get("normalizedShape")
     if ns is None:
@@ -260,17 +265,22 @@ def rms_norm(inputs, params) -> HipTensorHandle:
     xs = x if x.is_contiguous() else _materialize(x)
     try:
         rows = xs.numel // n if n else 0
-        out = params.get("out") or HipTensorHandle.create_new(x.shape, x.dtype)
+        out_dtype = params.get("out").dtype if params.get("out") is not None else (params.get("out_dtype") or x.dtype)
+        if out_dtype not in (FLOAT32, BFLOAT16) or x.dtype not in (FLOAT32, BFLOAT16):
+            raise TypeError(f"rms_norm: unsupported dtypes {x.dtype} -> {out_dtype}")
+        out = params.get("out") or HipTensorHandle.create_new(x.shape, out_dtype)
+        if not out.is_contiguous() or tuple(out.shape) != tuple(x.shape):
+            raise ValueError("rms_norm: out must be a contiguous tensor of the input's shape")
         if w is not None:
-            if w.numel != n or w.dtype != x.dtype:
-                raise ValueError("rms_norm: weight must have normalized_shape elements and the input dtype")
+            if w.numel != n or w.dtype != out_dtype:
+                raise ValueError("rms_norm: weight must have normalized_shape elements and the output dtype")
             wc = w if w.is_contiguous() else _materialize(w)
         else:
             wc = None
         try:
             _lib.call(
                 "kh_rms_norm", _vp(xs.data_ptr()), n, _vp(wc.data_ptr()) if wc is not None else None,
-                _vp(out.data_ptr()), n, rows, n, C.c_float(eps), x.kh_dtype,
+                _vp(out.data_ptr()), n, rows, n, C.c_float(eps), x.kh_dtype, out.kh_dtype,
             )
         finally:
             if wc is not None and wc is not w:
@@ -451,12 +461,16 @@ def index_select(self_: HipTensorHandle, index: HipTensorHandle, params: dict, o
         raise NotImplementedError("index_select: only dim 0 (embedding rows) is implemented")
     if index.dtype != INT32 or not index.is_contiguous():
         raise TypeError("index_select: index must be a contiguous int32 tensor")
+    if not output.is_contiguous() or output.dtype not in (FLOAT32, BFLOAT16) or self_.dtype not in (FLOAT32, BFLOAT16):
+        raise TypeError("index_select: table and output must be float tensors; output contiguous")
     t = self_ if self_.is_contiguous() else _materialize(self_)
     try:
         row = int(np.prod(t.shape[1:])) if len(t.shape) > 1 else 1
+        if output.numel != index.numel * row:
+            raise ValueError("index_select: output must hold len(index) rows of the table")
         _lib.call(
             "kh_index_select", _vp(t.data_ptr()), t.shape[0], _vp(index.data_ptr()), index.numel, row,
-            _vp(output.data_ptr()), t.kh_dtype,
+            _vp(output.data_ptr()), t.kh_dtype, output.kh_dtype,
         )
     finally:
         if t is not self_:

@@ -27,6 +27,18 @@ def test_rms_norm_bf16_no_weight_default_eps(hip):
     assert np.max(np.abs(y - ref)) <= 2 ** -7 * np.max(np.abs(ref))
 
 
+@pytest.mark.parametrize("rows,n", [(9, 1024), (3, 130)])
+def test_rms_norm_fp32_in_bf16_out(hip, rows, n):
+    """A float32 residual row normalised straight into bf16 with a bf16 weight: exactly the oracle's
+    fp32 result rounded once (within one bf16 ulp of rounding-boundary noise)."""
+    x, xh = seeded(105, (rows, n))
+    w = oracle.bf16_round(syn.uniform(106, (n,), 0.5, 1.5))
+    y = F.rms_norm(x, [n], Tensor(w, dtype="bfloat16"), eps=1e-6, out_dtype="bfloat16")
+    assert y.dtype == "bfloat16"
+    ref = oracle.bf16_round(oracle.rms_norm(xh, w, 1e-6))
+    assert np.max(np.abs(y.numpy() - ref)) <= 2 ** -7 * np.max(np.abs(ref))
+
+
 def test_rms_norm_on_permuted_view(hip):
     """Strided input is materialised; the output is contiguous (normalize/executor.ts:121-122)."""
     x, xh = seeded(104, (6, 4, 128))

@@ -75,6 +75,12 @@ def test_embedding_and_argmax(hip):
     ids = syn.randint(231, (2, 7), 0, V)
     e = F.embedding(Tensor(ids, dtype="int32"), table).numpy()
     np.testing.assert_array_equal(e, th[ids])
+    ids_bad = np.array([3, -1, V, 0], np.int32)      # ids outside the table give zero rows
+    e32 = F.embedding(Tensor(ids_bad, dtype="int32"), table, out_dtype="float32")
+    assert e32.dtype == "float32"
+    ref = th[np.clip(ids_bad, 0, V - 1)].copy()
+    ref[1:3] = 0.0
+    np.testing.assert_array_equal(e32.numpy(), ref)
     x = syn.normal(232, (3, 151936))
     x[1, 5] = x[1, 77] = 100.0  # tie: lowest index wins
     x[2, :] = -np.inf
