@@ -7,7 +7,12 @@ Hq=16, Hkv=8, D=128, per-sequence KV lengths ~ U[8192, 32768]) in HBM GB/s and t
 qk-norm + RoPE (config C2) in GB/s, each against its roofline, and times the CPU oracle's flash
 algorithm on a bounded sample as the CPU baseline.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--only prefill|decode|norm]
+It also runs the full Qwen3-0.6B model of config C5 (512-token prefill, 128 greedy decode steps)
+and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against their rooflines.
+`--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+                    [--only prefill|decode|norm|model|copy]
 Prints ONE JSON line.
 """
 import argparse
@@ -128,6 +133,43 @@ def bench_norm_rope(steps, warmup):
     return {"T": T, "bytes": float(bytes_), "wall_ms": wall_ms, "dev_ms": dev_ms}
 
 
+def bench_model(steps, warmup, new_tokens=128, prompt_len=512, use_graph=True):
+    """Config C5: Qwen3-0.6B architecture, random N(0, 0.02) bf16 weights, a 512-token prefill of
+    uniform-random ids, then 128 greedy decode steps (the decode step captured once as a HIP graph
+    and replayed).  One warm-up generation of 8 tokens precedes the timed one."""
+    from kandle_amd.model_utils import Qwen3Config, Qwen3ForCausalLM, init_qwen3_weights
+    from kandle_amd import synthetic as syn
+
+    cfg = Qwen3Config()
+    t0 = time.perf_counter()
+    w = init_qwen3_weights(cfg, seed=7)
+    log(f"model weights generated in {time.perf_counter() - t0:.1f} s")
+    prompt = syn.randint(8, (prompt_len,), 0, cfg.vocab_size)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=prompt_len + new_tokens)
+    del w
+    model.generate(prompt, 8, use_graph=use_graph)
+    timing = {}
+    toks = model.generate(prompt, new_tokens, timing=timing, use_graph=use_graph)
+    if not use_graph:  # every step eager: time all of them
+        timing["replay_ms"], timing["replay_steps"] = timing["decode_ms"], new_tokens
+    model.dispose()
+    H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    Hq, Hkv, Lyr = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
+    layer_w = H * (Hq + 2 * Hkv) * D + Hq * D * H + 3 * H * I            # projection weights per layer
+    prefill_flops = (2.0 * prompt_len * layer_w * Lyr                      # projections, all rows
+                     + 2.0 * cfg.vocab_size * H                            # lm_head, last row
+                     + Lyr * 4.0 * Hq * prompt_len * prompt_len * D / 2)   # causal attention
+    # bytes a decode step must read: every weight once (tied embedding as lm_head), plus the KV
+    # cache rows attended; the mean attended length over the timed replays
+    weight_bytes = 2.0 * (Lyr * (layer_w + 2 * H + 2 * D) + cfg.vocab_size * H + H)
+    steps_r = timing.get("replay_steps", 0)
+    mean_len = prompt_len + 1 + (new_tokens + 1) / 2.0
+    kv_bytes = Lyr * 2 * Hkv * D * 2 * mean_len
+    return {"prefill_ms": timing["prefill_ms"], "prefill_flops": prefill_flops, "prompt_len": prompt_len,
+            "new_tokens": new_tokens, "replay_ms": timing.get("replay_ms"), "replay_steps": steps_r,
+            "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8]}
+
+
 def bench_copy(steps, warmup):
     """Calibration workload for the HBM-traffic counters: a contiguous 1 GiB device-to-device copy
     through the library's strided-copy kernel (1 GiB read + 1 GiB written per call)."""
@@ -184,7 +226,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm", "copy"], default=None)
+    ap.add_argument("--eager-decode", action="store_true",
+                    help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
+    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -204,6 +248,9 @@ def main():
     if args.only in (None, "norm"):
         log("norm+rope C2 ...")
         res["norm"] = bench_norm_rope(args.steps, args.warmup)
+    if args.only in (None, "model"):
+        log("Qwen3-0.6B C5 ...")
+        res["model"] = bench_model(args.steps, args.warmup, use_graph=not args.eager_decode)
     if args.only == "copy":
         log("copy calibration ...")
         res["copy"] = bench_copy(args.steps, args.warmup)
@@ -250,6 +297,27 @@ def main():
         if "value" not in line:
             line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(n["wall_ms"], 4),
                          "config": {"workload": "C2 norm + rope"}})
+    if "model" in res:
+        m = res["model"]
+        p_tps = m["prompt_len"] / (m["prefill_ms"] * 1e-3)
+        p_tf = m["prefill_flops"] / (m["prefill_ms"] * 1e-3) / 1e12
+        d_ms = m["replay_ms"] / m["replay_steps"]
+        d_gbps = m["step_bytes"] / (d_ms * 1e-3) / 1e9
+        line["model"] = {
+            "workload": "C5 Qwen3-0.6B (28 layers, hidden 1024, 16/8 heads, vocab 151936, random bf16 weights): "
+                        f"{m['prompt_len']}-token prefill + {m['new_tokens']} greedy decode steps",
+            "prefill_ms": round(m["prefill_ms"], 3), "prefill_tokens_per_s": round(p_tps, 1),
+            "prefill": {"bound": "mfma", "achieved": round(p_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(p_tf / PEAK_BF16_TFLOPS, 4), "flops": m["prefill_flops"]},
+            "decode_ms_per_token": round(d_ms, 4), "decode_tokens_per_s": round(1e3 / d_ms, 1),
+            "decode": {"bound": "hbm", "achieved": round(d_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                       "frac": round(d_gbps / PEAK_HBM_GBPS, 4), "bytes_per_step": m["step_bytes"]},
+            "decode_steps_timed": m["replay_steps"], "decode_total_ms": round(m["decode_ms"], 3),
+            "decode_issue": "eager" if args.eager_decode else "hip graph replay",
+            "first_tokens": m["tokens"]}
+        if "value" not in line:
+            line.update({"value": round(1e3 / d_ms, 1), "unit": "tokens/s", "ms_per_step": round(d_ms, 4),
+                         "config": {"workload": "C5 Qwen3-0.6B greedy decode"}})
     if "copy" in res:
         c = res["copy"]
         gbps = c["bytes"] / (c["dev_ms"] * 1e-3) / 1e9

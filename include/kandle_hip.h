@@ -81,6 +81,19 @@ int kh_event_destroy(void* event);
 int kh_event_record(void* event);
 int kh_event_elapsed_ms(void* start, void* stop, float* ms);
 
+/* Graphs of library launches.  Between kh_graph_begin_capture and kh_graph_end_capture, calls
+ * that enqueue work are recorded instead of run; kh_graph_launch replays the recording on the
+ * library stream.  Device blocks allocated or freed while the capture is open belong to the
+ * graph until kh_graph_destroy (which waits for the stream), so a replay never touches memory
+ * handed to other work.  Host-synchronous calls (kh_memcpy_h2d/d2h, kh_synchronize,
+ * kh_empty_cache) fail while a capture is open.  No counterpart in the reference, whose decode
+ * loop dispatches every op from the host per token (reference:
+ * packages/model-utils/src/qwen3/for_causal_lm.ts:475-508); this replaces that per-token dispatch. */
+int kh_graph_begin_capture(void);
+int kh_graph_end_capture(void** graph);
+int kh_graph_launch(void* graph);
+int kh_graph_destroy(void* graph);
+
 /* ------------------------------------------------------------------ support ops -------------- */
 
 /* dst[i] = value for n elements of `dtype` (a fill kernel, never hipMemsetAsync).
@@ -122,6 +135,16 @@ int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64
  * with the greedy tie rule of sample() (packages/model-utils/src/sampling/index.ts:132,138). */
 int kh_argmax(const void* x, int64_t rows, int64_t n, int32_t* out, int dtype);
 
+/* Device-side bookkeeping of one greedy decode step, one thread: with p = *position,
+ *   token_log[p + 1 - log_base] = *next_token  (if that index lies in [0, log_cap)),
+ *   *position = p + 1,  *seq_len = p + 2.
+ * next_token is the argmax just written for position p + 1; seq_len is the KV length the next
+ * step attends over.  Keeps generateWithKVCache's loop state (reference:
+ * packages/model-utils/src/qwen3/for_causal_lm.ts:475-508: append the token, advance the
+ * position) on the device, so a captured decode step replays with no host round trip. */
+int kh_greedy_advance(const int32_t* next_token, int32_t* position, int32_t* seq_len, int32_t* token_log,
+                      int64_t log_base, int64_t log_cap);
+
 /* ------------------------------------------------------------------ hot path ----------------- */
 
 /* y[r, :] = x[r, :] * (1 / sqrt(mean(x[r, :]^2) + eps)) * w[:] (w may be NULL), fp32 math,
@@ -141,6 +164,10 @@ int kh_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* y, int
  *   out = n * cos(f) + rotate_half(n) * sin(f).
  * If v/v_out are non-NULL, v rows (k's head count and strides s[12..14] read, s[15..17] write;
  * `strides` then holds 18 values) are copied unchanged in the same launch (fused KV-cache write).
+ * kv_cache_len > 0 selects cache addressing for k_out and v_out: token t is written at sequence
+ * index positions[t] instead of t_in_seq, and a token whose position lies outside
+ * [0, kv_cache_len) writes no K/V row; q_out keeps t_in_seq.  With positions held on the device,
+ * one captured launch then serves every decode step.
  * Replaces q_norm/k_norm + _permuteToHeadsFirst + applyRotaryPosEmbDirect + kvCache.update
  * (reference: packages/model-utils/src/attention/gqa.ts:279-309; packages/model-utils/src/rope.ts:159-261, :546-644;
  * packages/model-utils/src/kv-cache.ts:164-212). */
@@ -148,7 +175,7 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out,
                     const void* v, void* v_out,
                     const void* wq, const void* wk, const float* inv_freq, const int32_t* positions,
                     int64_t n_batch, int64_t seq_len, int n_q_heads, int n_kv_heads, int head_dim,
-                    const int64_t* strides, float eps, int dtype);
+                    const int64_t* strides, float eps, int dtype, int64_t kv_cache_len);
 
 /* Scaled dot-product attention O = softmax(scale * Q K^T + causal) V with GQA
  * (query head h reads kv head h / (hq / hkv)); causal masks key j > query i (top-left aligned).
@@ -186,6 +213,21 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
 int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc,
             const void* cin, int64_t ldcin, const void* bias,
             int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b, int dtype, int out_dtype);
+
+/* One-row projection (decode) with the producing op fused in front of it:
+ *   c[j] = alpha * sum_i x'[i] * w[j, i] + beta * cin[j] (+ bias[j]),  j < n, i < k,
+ * w bf16 [n, k] with row stride ldw (the nn.Linear weight), c/cin/bias of out_dtype, where x' is
+ * the activation row exactly as the unfused producer would have stored it (rounded to bf16):
+ *   prologue 0: x' = x (bf16 [k]) — plain linear (reference: packages/core/src/nn/modules/linear/Linear.ts:135-137);
+ *   prologue 1: x' = rms_norm(x, norm_w, eps) with x the fp32 residual row [k] and norm_w bf16 [k]
+ *               — RMSNorm then linear (reference: packages/core/src/nn/modules/normalization/RMSNorm.ts:92-99;
+ *               packages/model-utils/src/qwen3/decoder_layer.ts:191-241);
+ *   prologue 2: x' = silu(x) * x2 with x, x2 bf16 [k] (gate and up) — the SwiGLU product then
+ *               down_proj (reference: packages/model-utils/src/mlp/swiglu.ts:119-134).
+ * Needs k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w and k <= 16384.  cin may alias c. */
+int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps,
+                  const void* w, int64_t ldw, void* c, const void* cin, const void* bias,
+                  int64_t n, int64_t k, float alpha, float beta, int out_dtype);
 
 #ifdef __cplusplus
 }

@@ -30,6 +30,7 @@ class AllocStats(C.Structure):
 # name -> (restype, argtypes); every entry point returns int (0 = success) unless stated.
 _vp, _i, _i64, _f, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
 _i64p = C.POINTER(C.c_int64)
+_vpp = C.POINTER(C.c_void_p)
 SIGNATURES = {
     "kh_init": [_i],
     "kh_device_count": [C.POINTER(C.c_int)],
@@ -53,10 +54,17 @@ SIGNATURES = {
     "kh_index_select": [_vp, _i64, _vp, _i64, _i64, _vp, _i, _i],
     "kh_argmax": [_vp, _i64, _i64, _vp, _i],
     "kh_rms_norm": [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _f, _i, _i],
-    "kh_qk_norm_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i, _i, _i, _i64p, _f, _i],
+    "kh_qk_norm_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i, _i, _i, _i64p, _f, _i,
+                        _i64],
+    "kh_greedy_advance": [_vp, _vp, _vp, _vp, _i64, _i64],
+    "kh_graph_begin_capture": [],
+    "kh_graph_end_capture": [_vpp],
+    "kh_graph_launch": [_vp],
+    "kh_graph_destroy": [_vp],
     "kh_flash_attention": [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i64p, _f, _i, _i],
     "kh_decode_attention": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
     "kh_gemm": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _f, _f, _i, _i, _i],
+    "kh_gemv_fused": [_i, _vp, _vp, _vp, _f, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _f, _f, _i],
 }
 
 _lib = None

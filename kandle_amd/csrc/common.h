@@ -18,6 +18,11 @@ bool initialized();
 void* scratch_alloc(size_t bytes);
 void scratch_free(void* p);
 
+// A library-owned array of at least n uint32 counters, all zero whenever no kernel is running:
+// a kernel that counts in it must return every counter it touched to zero before it exits.
+// nullptr if n exceeds the array (allocated and cleared once, in kh_init).
+uint32_t* zeroed_counters(size_t n);
+
 #define KH_CHECK_HIP(expr)                                                              \
   do {                                                                                  \
     hipError_t _e = (expr);                                                             \
@@ -101,6 +106,16 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t b
 }
 // 2^x with the hardware instruction (denormal results flush to 0: fine for softmax weights <= 1).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// silu(x) = x / (1 + exp(-clamp(x, -88, 88))), the reference's pointwise silu (the clamp keeps
+// exp finite for large |x|; reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:299).
+__device__ __forceinline__ float silu_ref(float x) {
+  const float c = fminf(fmaxf(x, -88.0f), 88.0f);
+  return x / (1.0f + expf(-c));
+}
+
+// Round a float to the nearest bf16 value (kept in a float register).
+__device__ __forceinline__ float round_bf16(float v) { return __uint_as_float(f32_to_bf16_bits(v) << 16); }
 
 // Wave-wide (64 lanes) reductions via cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -9,6 +9,8 @@
 // Reference semantics: out = alpha * op(A) op(B) + beta * C (packages/core/src/dispatch/matmulOps.ts:32-125;
 // epilogue packages/backend-webgpu/src/kernels/matrix/builder.ts:152-218); linear = x W^T + b
 // (packages/core/src/dispatch/handlers/composite.ts:55-77).
+#include <type_traits>
+
 #include "common.h"
 
 using namespace kh;
@@ -245,6 +247,181 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
 }
 
 // =============================================================================================
+// One-row GEMV (decode: m = 1, bf16 weight [n, k], trans_b = 1) with an optional fused prologue
+// that forms the activation row the way the unfused ops would have stored it (bf16):
+//   PRO_NONE      x' = x                               (x bf16)
+//   PRO_RMSNORM   x' = bf16(rms_norm(x, norm_w, eps))  (x fp32 residual row, norm_w bf16)
+//   PRO_SILU_MUL  x' = bf16(silu(x) * x2)              (x, x2 bf16: gate and up halves)
+// Each workgroup forms x' once in LDS (fp32, zero past k); each wave then owns U weight rows and
+// streams them with raw 16-byte buffer loads, CB chunks of 512 columns per row in flight (rows past
+// n read as zero), and reduces each row across the wave.  Every weight byte is read once.
+// =============================================================================================
+constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2;
+constexpr int GV_CHUNK = 512;  // columns per wave-wide 16-byte load (64 lanes x 8 bf16)
+
+template <int PRO>
+__device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const uint16_t* x2, const uint16_t* nw,
+                                              float eps, int K, int kpad) {
+  const int tid = threadIdx.x;
+  if constexpr (PRO == PRO_RMSNORM) {
+    // Rows of up to 8 * blockDim elements stay in registers between the two passes.
+    constexpr int PR = 8;
+    __shared__ float red[4];
+    const float* xf = (const float*)x;
+    const bool in_regs = kpad <= PR * (int)blockDim.x;
+    float xv[PR], wv[PR];
+    float ss = 0.f;
+    if (in_regs) {
+#pragma unroll
+      for (int j = 0; j < PR; ++j) {
+        const int i = tid + j * blockDim.x;
+        xv[j] = i < K ? xf[i] : 0.f;
+        wv[j] = i < K ? bf16_bits_to_f32(nw[i]) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < PR; ++j) ss += xv[j] * xv[j];
+    } else {
+      for (int i = tid; i < K; i += blockDim.x) ss += xf[i] * xf[i];
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    if (in_regs) {
+#pragma unroll
+      for (int j = 0; j < PR; ++j) {
+        const int i = tid + j * blockDim.x;
+        if (i < kpad) xs[i] = i < K ? round_bf16((xv[j] * inv) * wv[j]) : 0.f;
+      }
+    } else {
+      for (int i = tid; i < kpad; i += blockDim.x)
+        xs[i] = i < K ? round_bf16((xf[i] * inv) * bf16_bits_to_f32(nw[i])) : 0.f;
+    }
+  } else if constexpr (PRO == PRO_SILU_MUL) {
+    const uint16_t* g = (const uint16_t*)x;
+    for (int i = tid; i < kpad; i += blockDim.x)
+      xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(g[i])) * bf16_bits_to_f32(x2[i])) : 0.f;
+  } else {
+    const uint16_t* xb = (const uint16_t*)x;
+    for (int i = tid; i < kpad; i += blockDim.x) xs[i] = i < K ? bf16_bits_to_f32(xb[i]) : 0.f;
+  }
+  __syncthreads();
+}
+
+template <int U, int PRO, typename TO>
+__global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, const uint16_t* __restrict__ x2,
+                                                    const uint16_t* __restrict__ nw, float eps,
+                                                    const uint16_t* __restrict__ W, int64_t ldw, uint32_t w_bytes,
+                                                    TO* C, const TO* cin, const TO* __restrict__ bias, int N, int K,
+                                                    int nch, float alpha, float beta) {
+  constexpr int CB = 8 / U;  // 16-byte loads in flight per row per lane
+  extern __shared__ float xs[];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(W, w_bytes);
+  const int64_t stride = (int64_t)gridDim.x * (blockDim.x >> 6) * U;
+  int64_t n0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + w) * U;
+
+  // Weight loads of batch (row group n, chunks [c0, c0 + CB)); columns past K (row padding when
+  // ldw > K) and rows past N read as zero (offset w_bytes is out of range).
+  uint4 wv[U][CB];
+  auto issue = [&](int64_t n, int c0) {
+#pragma unroll
+    for (int cc = 0; cc < CB; ++cc)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + cc;
+        const int k = c * GV_CHUNK + lane * 8;
+        const uint32_t off = k < K ? (uint32_t)(((n + u) * ldw + k) * 2) : w_bytes;
+        wv[u][cc] = c < nch ? buf_load16(rsrc, off) : make_uint4(0, 0, 0, 0);
+      }
+  };
+  // The first batch is in flight while the workgroup forms x'.
+  if (n0 < N) issue(n0, 0);
+  gemv_prologue<PRO>(xs, x, x2, nw, eps, K, nch * GV_CHUNK);
+
+  for (; n0 < N; n0 += stride) {
+    float acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      uint4 cur[U][CB];
+#pragma unroll
+      for (int cc = 0; cc < CB; ++cc)
+#pragma unroll
+        for (int u = 0; u < U; ++u) cur[u][cc] = wv[u][cc];
+      // prefetch the next batch: the rest of this row group, else the next row group
+      if (c0 + CB < nch)
+        issue(n0, c0 + CB);
+      else if (n0 + stride < N)
+        issue(n0 + stride, 0);
+#pragma unroll
+      for (int cc = 0; cc < CB; ++cc) {
+        if (c0 + cc < nch) {
+          const float4* xp = reinterpret_cast<const float4*>(xs + (c0 + cc) * GV_CHUNK + lane * 8);
+          const float4 xa = xp[0], xb = xp[1];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const uint4 q = cur[u][cc];
+            float s = acc[u];
+            s += lo_bf16(q.x) * xa.x;
+            s += hi_bf16(q.x) * xa.y;
+            s += lo_bf16(q.y) * xa.z;
+            s += hi_bf16(q.y) * xa.w;
+            s += lo_bf16(q.z) * xb.x;
+            s += hi_bf16(q.z) * xb.y;
+            s += lo_bf16(q.w) * xb.z;
+            s += hi_bf16(q.w) * xb.w;
+            acc[u] = s;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float sum = wave_sum(acc[u]);
+      const int64_t n = n0 + u;
+      if (lane == 0 && n < N) Elem<TO>::store(C, n, epilogue<TO>(sum, alpha, beta, cin, 0, bias, 0, n));
+    }
+  }
+}
+
+// Launches gemv1_kernel; returns false (nothing launched) when the operands do not fit its
+// assumptions (16-byte aligned weight rows, 32-bit byte offsets, x' within 64 KiB of LDS).
+template <int U, int PRO, typename TO>
+void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw,
+              uint32_t w_bytes, TO* C, const TO* cin, const TO* bias, int N, int K, int nch, float alpha, float beta) {
+  const int64_t waves = (N + U - 1) / U;
+  int64_t grid = (waves + 3) / 4;
+  if (grid > 8192) grid = 8192;  // waves then stride over the remaining rows
+  const size_t shm = (size_t)nch * GV_CHUNK * sizeof(float);
+  gemv1_kernel<U, PRO, TO><<<(int)grid, 256, shm, stream()>>>(x, (const uint16_t*)x2, (const uint16_t*)nw, eps, W,
+                                                              ldw, w_bytes, C, cin, bias, N, K, nch, alpha, beta);
+}
+
+template <int PRO, typename TO>
+bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw, TO* C,
+                  const TO* cin, const TO* bias, int N, int K, float alpha, float beta) {
+  if (N <= 0 || K <= 0) return false;
+  const int nch = (K + GV_CHUNK - 1) / GV_CHUNK;
+  const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
+  // largest offset formed: a row index up to N + 3 (rows past N read as zero)
+  const int64_t max_off = ((int64_t)(N + 4) * ldw) * 2;
+  if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || max_off >= (int64_t(1) << 32) ||
+      (size_t)nch * GV_CHUNK * sizeof(float) > 64 * 1024)
+    return false;
+  const uint32_t wb = (uint32_t)w_bytes;
+  if (N >= 16384)
+    gemv1_go<4, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta);
+  else if (N >= 2048)
+    gemv1_go<2, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta);
+  else
+    gemv1_go<1, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta);
+  return true;
+}
+
+// =============================================================================================
 // Generic tiled kernel (f32 or bf16 storage, trans_b 0/1): 16 x 16 threads, 64 x 64 tile, each
 // thread 4 x 4 outputs, fp32 math.
 // =============================================================================================
@@ -309,6 +486,14 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
     KH_CHECK_LAUNCH();
     return KH_OK;
   }
+  if constexpr (is_bf16) {
+    if (trans_b && M == 1) {
+      if (launch_gemv1<PRO_NONE, TO>(a, nullptr, nullptr, 0.f, B, ldb, C, CI, BI, N, K, alpha, beta)) {
+        KH_CHECK_LAUNCH();
+        return KH_OK;
+      }
+    }
+  }
   if (trans_b && M <= SK_MAXM && (size_t)M * K * sizeof(float) <= 64 * 1024 && aligned16(b)) {
     const int waves_needed = (N + SK_ROWS_PER_WAVE - 1) / SK_ROWS_PER_WAVE;
     int grid = (waves_needed + 3) / 4;
@@ -349,6 +534,40 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
   if (dtype == KH_BF16)
     return launch_gemm<uint16_t, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
   return launch_gemm<float, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
+}
+
+int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps, const void* w,
+                  int64_t ldw, void* c, const void* cin, const void* bias, int64_t n, int64_t k, float alpha,
+                  float beta, int out_dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(prologue >= PRO_NONE && prologue <= PRO_SILU_MUL, "kh_gemv_fused: unknown prologue %d", prologue);
+  KH_REQUIRE(n >= 0 && k > 0 && n <= INT32_MAX && k <= INT32_MAX, "kh_gemv_fused: bad extents");
+  KH_REQUIRE(out_dtype == KH_BF16 || out_dtype == KH_F32, "kh_gemv_fused: unsupported output dtype %d", out_dtype);
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(x && w && c, "kh_gemv_fused: null pointer");
+  KH_REQUIRE(prologue != PRO_RMSNORM || norm_w != nullptr, "kh_gemv_fused: the RMSNorm prologue needs norm_w");
+  KH_REQUIRE(prologue != PRO_SILU_MUL || x2 != nullptr, "kh_gemv_fused: the silu*mul prologue needs x2");
+  KH_REQUIRE(ldw >= k, "kh_gemv_fused: ldw < k");
+  const int N = (int)n, K = (int)k;
+  const uint16_t* W = (const uint16_t*)w;
+  bool ok = false;
+  auto run = [&](auto* C, auto* CI, auto* BI) {
+    using TO = std::remove_const_t<std::remove_pointer_t<decltype(CI)>>;
+    if (prologue == PRO_RMSNORM)
+      ok = launch_gemv1<PRO_RMSNORM, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+    else if (prologue == PRO_SILU_MUL)
+      ok = launch_gemv1<PRO_SILU_MUL, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+    else
+      ok = launch_gemv1<PRO_NONE, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+  };
+  if (out_dtype == KH_F32)
+    run((float*)c, (const float*)cin, (const float*)bias);
+  else
+    run((uint16_t*)c, (const uint16_t*)cin, (const uint16_t*)bias);
+  KH_REQUIRE(ok, "kh_gemv_fused: unsupported operands (need k %% 8 == 0, ldw %% 8 == 0, a 16-byte aligned weight, "
+                 "k <= 16384 and byte offsets below 4 GiB)");
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 }  // extern "C"

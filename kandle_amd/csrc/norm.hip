@@ -116,82 +116,103 @@ struct QkStrides {
   int64_t s[18];
 };
 
+// A wave handles `spw` consecutive row steps of one token: steps [0, qk_steps) are RPW q/k head
+// rows each (q heads first), steps [qk_steps, qk_steps + v_steps) copy RPW V rows each.  The host
+// gives a long sequence one wave per token (spw = all steps: the angles are computed once per
+// token) and a short one (decode) one step per wave, so a single token still spreads over waves.
 template <typename T>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo, T* __restrict__ ko,
     const T* __restrict__ v, T* __restrict__ vo, const T* __restrict__ wq, const T* __restrict__ wk,
     const float* __restrict__ inv_freq, const int32_t* __restrict__ positions, int64_t n_tokens, int64_t seq_len,
-    int hq, int hkv, int D, QkStrides st, float eps) {
+    int hq, int hkv, int D, QkStrides st, float eps, int64_t kv_cache_len, int spw) {
   const int lane = threadIdx.x & 63;
-  const int64_t tok = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (tok >= n_tokens) return;
-  const int64_t b = tok / seq_len, s = tok - b * seq_len;
   const int LPR = D >> 4;            // lanes per row
   const int RPW = 64 / LPR;          // rows per wave step
+  const int qk_steps = (hq + hkv + RPW - 1) / RPW;
+  const int v_steps = v != nullptr ? (hkv + RPW - 1) / RPW : 0;
+  const int total_steps = qk_steps + v_steps;
+  const int groups = (total_steps + spw - 1) / spw;
+  const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t tok = gw / groups;
+  if (tok >= n_tokens) return;
+  const int step0 = (int)(gw - tok * groups) * spw;
+  const int step1 = min(step0 + spw, total_steps);
+  const int64_t b = tok / seq_len, s = tok - b * seq_len;
   const int t = lane % LPR;          // chunk index inside the row
   const int rsub = lane / LPR;       // row slot inside the step
   const int half = D >> 1;
 
-  // cos/sin of f = float(pos) * inv_freq[i] for i = 8t..8t+7.
-  const float pos = (float)positions[tok];
-  float cs[8], sn[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float f = pos * inv_freq[8 * t + j];
-    sincosf(f, &sn[j], &cs[j]);
-  }
-  float wqa[8], wqb[8], wka[8], wkb[8];
-  Vec8<T>::load(wq + 8 * t, wqa);
-  Vec8<T>::load(wq + half + 8 * t, wqb);
-  Vec8<T>::load(wk + 8 * t, wka);
-  Vec8<T>::load(wk + half + 8 * t, wkb);
+  // K/V destination row: the token's index in its sequence, or (cache addressing) its position,
+  // in which case a position outside the cache writes no K/V row.
+  const int32_t ipos = positions[tok];
+  const bool cache_mode = kv_cache_len > 0;
+  const int64_t kv_row = cache_mode ? (int64_t)ipos : s;
+  const bool kv_ok = !cache_mode || (ipos >= 0 && (int64_t)ipos < kv_cache_len);
 
-  const int total_rows = hq + hkv;
-  for (int r0 = 0; r0 < total_rows; r0 += RPW) {
-    const int r = r0 + rsub;
-    const bool active = r < total_rows;
-    const bool isq = r < hq;
-    const int h = isq ? r : r - hq;
-    const T* src;
-    T* dst;
-    if (isq) {
-      src = q + b * st.s[0] + s * st.s[1] + (int64_t)h * st.s[2];
-      dst = qo + b * st.s[6] + s * st.s[7] + (int64_t)h * st.s[8];
-    } else {
-      src = k + b * st.s[3] + s * st.s[4] + (int64_t)h * st.s[5];
-      dst = ko + b * st.s[9] + s * st.s[10] + (int64_t)h * st.s[11];
-    }
-    float a[8], c[8];
-    float ss = 0.f;
-    if (active) {
-      Vec8<T>::load(src + 8 * t, a);
-      Vec8<T>::load(src + half + 8 * t, c);
+  if (step0 < qk_steps) {
+    // cos/sin of f = float(pos) * inv_freq[i] for i = 8t..8t+7.
+    const float pos = (float)ipos;
+    float cs[8], sn[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss += a[j] * a[j] + c[j] * c[j];
+    for (int j = 0; j < 8; ++j) {
+      const float f = pos * inv_freq[8 * t + j];
+      sincosf(f, &sn[j], &cs[j]);
     }
-    // Reduce over the LPR lanes of this row (LPR is a power of two <= 16).
-    for (int o = LPR >> 1; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if (active) {
-      const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-      float oa[8], oc[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float na = (a[j] * inv) * (isq ? wqa[j] : wka[j]);
-        const float nc = (c[j] * inv) * (isq ? wqb[j] : wkb[j]);
-        oa[j] = na * cs[j] + (-nc) * sn[j];
-        oc[j] = nc * cs[j] + na * sn[j];
+    float wqa[8], wqb[8], wka[8], wkb[8];
+    Vec8<T>::load(wq + 8 * t, wqa);
+    Vec8<T>::load(wq + half + 8 * t, wqb);
+    Vec8<T>::load(wk + 8 * t, wka);
+    Vec8<T>::load(wk + half + 8 * t, wkb);
+
+    const int total_rows = hq + hkv;
+    const int qk_end = min(step1, qk_steps);
+    for (int step = step0; step < qk_end; ++step) {
+      const int r = step * RPW + rsub;
+      const bool isq = r < hq;
+      const bool active = r < total_rows && (isq || kv_ok);
+      const int h = isq ? r : r - hq;
+      const T* src;
+      T* dst;
+      if (isq) {
+        src = q + b * st.s[0] + s * st.s[1] + (int64_t)h * st.s[2];
+        dst = qo + b * st.s[6] + s * st.s[7] + (int64_t)h * st.s[8];
+      } else {
+        src = k + b * st.s[3] + s * st.s[4] + (int64_t)h * st.s[5];
+        dst = ko + b * st.s[9] + kv_row * st.s[10] + (int64_t)h * st.s[11];
       }
-      Vec8<T>::store(dst + 8 * t, oa);
-      Vec8<T>::store(dst + half + 8 * t, oc);
+      float a[8], c[8];
+      float ss = 0.f;
+      if (active) {
+        Vec8<T>::load(src + 8 * t, a);
+        Vec8<T>::load(src + half + 8 * t, c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += a[j] * a[j] + c[j] * c[j];
+      }
+      // Reduce over the LPR lanes of this row (LPR is a power of two <= 16).
+      for (int o = LPR >> 1; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      if (active) {
+        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+        float oa[8], oc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float na = (a[j] * inv) * (isq ? wqa[j] : wka[j]);
+          const float nc = (c[j] * inv) * (isq ? wqb[j] : wkb[j]);
+          oa[j] = na * cs[j] + (-nc) * sn[j];
+          oc[j] = nc * cs[j] + na * sn[j];
+        }
+        Vec8<T>::store(dst + 8 * t, oa);
+        Vec8<T>::store(dst + half + 8 * t, oc);
+      }
     }
   }
-  if (v != nullptr) {
+  if (kv_ok) {
     // Fused KV-cache write of V rows (unchanged values).
-    for (int r0 = 0; r0 < hkv; r0 += RPW) {
-      const int h = r0 + rsub;
+    for (int step = max(step0, qk_steps); step < step1; ++step) {
+      const int h = (step - qk_steps) * RPW + rsub;
       if (h < hkv) {
         const T* src = v + b * st.s[12] + s * st.s[13] + (int64_t)h * st.s[14];
-        T* dst = vo + b * st.s[15] + s * st.s[16] + (int64_t)h * st.s[17];
+        T* dst = vo + b * st.s[15] + kv_row * st.s[16] + (int64_t)h * st.s[17];
         float a[8], c[8];
         Vec8<T>::load(src + 8 * t, a);
         Vec8<T>::load(src + half + 8 * t, c);
@@ -252,9 +273,10 @@ int kh_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* y, int
 int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out, const void* v, void* v_out,
                     const void* wq, const void* wk, const float* inv_freq, const int32_t* positions,
                     int64_t n_batch, int64_t seq_len, int n_q_heads, int n_kv_heads, int head_dim,
-                    const int64_t* strides, float eps, int dtype) {
+                    const int64_t* strides, float eps, int dtype, int64_t kv_cache_len) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(n_batch >= 0 && seq_len >= 0, "kh_qk_norm_rope: negative extent");
+  KH_REQUIRE(kv_cache_len >= 0, "kh_qk_norm_rope: negative kv_cache_len");
   KH_REQUIRE(n_q_heads > 0 && n_kv_heads > 0, "kh_qk_norm_rope: head counts must be positive");
   KH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256,
              "kh_qk_norm_rope: head_dim %d not in {32, 64, 128, 256}", head_dim);
@@ -275,19 +297,24 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out, cons
   const void* ptrs[8] = {q, k, q_out, k_out, wq, wk, v, v_out};
   for (int i = 0; i < 8; ++i)
     KH_REQUIRE(ptrs[i] == nullptr || aligned16(ptrs[i]), "kh_qk_norm_rope: pointer %d not 16-byte aligned", i);
+  // Long sequences: one wave per token (angles once per token).  Short ones: one row step per wave.
+  const int rpw = 64 / (head_dim / 16);
+  const int total_steps = (n_q_heads + n_kv_heads + rpw - 1) / rpw + (v ? (n_kv_heads + rpw - 1) / rpw : 0);
+  const int spw = n_tokens >= 2048 ? total_steps : 1;
+  const int groups = (total_steps + spw - 1) / spw;
   const int waves = 4;
-  const int64_t grid = (n_tokens + waves - 1) / waves;
+  const int64_t grid = (n_tokens * groups + waves - 1) / waves;
   KH_REQUIRE(grid <= INT32_MAX, "kh_qk_norm_rope: too many tokens");
   if (dtype == KH_BF16)
     qk_norm_rope_kernel<uint16_t><<<(int)grid, 64 * waves, 0, stream()>>>(
         (const uint16_t*)q, (const uint16_t*)k, (uint16_t*)q_out, (uint16_t*)k_out, (const uint16_t*)v,
         (uint16_t*)v_out, (const uint16_t*)wq, (const uint16_t*)wk, inv_freq, positions, n_tokens, seq_len,
-        n_q_heads, n_kv_heads, head_dim, st, eps);
+        n_q_heads, n_kv_heads, head_dim, st, eps, kv_cache_len, spw);
   else
     qk_norm_rope_kernel<float><<<(int)grid, 64 * waves, 0, stream()>>>(
         (const float*)q, (const float*)k, (float*)q_out, (float*)k_out, (const float*)v, (float*)v_out,
         (const float*)wq, (const float*)wk, inv_freq, positions, n_tokens, seq_len, n_q_heads, n_kv_heads, head_dim,
-        st, eps);
+        st, eps, kv_cache_len, spw);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

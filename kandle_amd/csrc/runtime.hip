@@ -18,11 +18,17 @@ namespace {
 
 thread_local char g_err[1024] = {0};
 
+struct Pool;
+struct GraphObj;
+
 struct State {
   bool init = false;
   int device = -1;
   hipStream_t stream = nullptr;
+  GraphObj* capturing = nullptr;  // graph whose stream capture is open
+  uint32_t* counters = nullptr;   // zeroed_counters() array
 };
+constexpr size_t kCounterCap = 65536;
 State g_state;
 
 // Size classes: requests up to 1 MiB round to 512 B, larger ones to 2 MiB.
@@ -36,44 +42,66 @@ size_t round_size(size_t bytes) {
   return (bytes + kLargeRound - 1) / kLargeRound * kLargeRound;
 }
 
+// Blocks that belong to one captured graph.  While a capture is open, every allocation comes from
+// the capture's pool and every block freed (whoever allocated it) joins that pool, so no address a
+// graph replays can be handed to other work before the graph is destroyed.
+struct Pool {
+  std::multimap<size_t, void*> free_blocks;
+  std::unordered_map<void*, size_t> owned;  // every block of the pool, free or live
+};
+
 struct Allocator {
   std::mutex mu;
   std::multimap<size_t, void*> free_blocks;   // size -> block
   std::unordered_map<void*, size_t> live;     // block -> size
+  std::unordered_map<void*, Pool*> pool_of;   // block -> graph pool (absent: global cache)
+  Pool* capture = nullptr;                    // pool of the open capture, if any
   kh_alloc_stats stats{};
+
+  static bool take(std::multimap<size_t, void*>& fl, size_t sz, void** p, size_t* bsz) {
+    // The smallest cached block that fits and wastes at most half of itself.
+    auto it = fl.lower_bound(sz);
+    if (it == fl.end() || it->first > 2 * sz) return false;
+    *p = it->second;
+    *bsz = it->first;
+    fl.erase(it);
+    return true;
+  }
+
+  void note_live(void* p, size_t bsz) {
+    live[p] = bsz;
+    stats.live_bytes += bsz;
+    if (stats.live_bytes > stats.peak_bytes) stats.peak_bytes = stats.live_bytes;
+  }
 
   int alloc(void** out, size_t bytes) {
     std::lock_guard<std::mutex> lock(mu);
     const size_t sz = round_size(bytes);
-    // Reuse the smallest cached block that fits and wastes at most half of itself.
-    auto it = free_blocks.lower_bound(sz);
-    if (it != free_blocks.end() && it->first <= 2 * sz) {
-      void* p = it->second;
-      const size_t bsz = it->first;
-      free_blocks.erase(it);
+    void* p = nullptr;
+    size_t bsz = 0;
+    if (take(capture ? capture->free_blocks : free_blocks, sz, &p, &bsz)) {
       stats.cached_bytes -= bsz;
-      live[p] = bsz;
-      stats.live_bytes += bsz;
-      if (stats.live_bytes > stats.peak_bytes) stats.peak_bytes = stats.live_bytes;
+      note_live(p, bsz);
       stats.n_cache_hits++;
       *out = p;
       return KH_OK;
     }
-    void* p = nullptr;
     hipError_t e = hipMalloc(&p, sz);
-    if (e != hipSuccess) {
+    if (e != hipSuccess && capture == nullptr) {
       (void)hipGetLastError();
       release_cached_locked();
       e = hipMalloc(&p, sz);
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        set_error("kh_alloc: out of device memory for %zu bytes (%s)", sz, hipGetErrorString(e));
-        return KH_ERR_OOM;
-      }
     }
-    live[p] = sz;
-    stats.live_bytes += sz;
-    if (stats.live_bytes > stats.peak_bytes) stats.peak_bytes = stats.live_bytes;
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      set_error("kh_alloc: out of device memory for %zu bytes (%s)", sz, hipGetErrorString(e));
+      return KH_ERR_OOM;
+    }
+    if (capture) {
+      capture->owned[p] = sz;
+      pool_of[p] = capture;
+    }
+    note_live(p, sz);
     stats.n_device_allocs++;
     *out = p;
     return KH_OK;
@@ -90,20 +118,56 @@ struct Allocator {
     const size_t sz = it->second;
     live.erase(it);
     stats.live_bytes -= sz;
-    free_blocks.emplace(sz, p);
     stats.cached_bytes += sz;
+    auto po = pool_of.find(p);
+    Pool* pool = po != pool_of.end() ? po->second : capture;
+    if (pool == nullptr) {
+      free_blocks.emplace(sz, p);
+      return KH_OK;
+    }
+    if (po == pool_of.end()) {  // a global block released inside a capture joins the capture's pool
+      pool->owned[p] = sz;
+      pool_of[p] = pool;
+    }
+    pool->free_blocks.emplace(sz, p);
     return KH_OK;
   }
 
   // Caller holds `mu`.  Waits for the stream so no queued kernel still uses a released block.
   void release_cached_locked() {
     if (g_state.stream) (void)hipStreamSynchronize(g_state.stream);
-    for (auto& kv : free_blocks) (void)hipFree(kv.second);
+    for (auto& kv : free_blocks) {
+      (void)hipFree(kv.second);
+      stats.cached_bytes -= kv.first;
+    }
     free_blocks.clear();
-    stats.cached_bytes = 0;
+  }
+
+  // Caller holds `mu` and has synchronised the stream.  Frees the pool's idle blocks; blocks still
+  // live (tensors the caller kept) become ordinary blocks that a later kh_free returns to the cache.
+  void release_pool_locked(Pool* pool) {
+    for (auto& kv : pool->owned) {
+      pool_of.erase(kv.first);
+      if (live.find(kv.first) == live.end()) {
+        (void)hipFree(kv.first);
+        stats.cached_bytes -= kv.second;
+      }
+    }
+    pool->owned.clear();
+    pool->free_blocks.clear();
   }
 };
 Allocator g_alloc;
+
+// A captured, instantiated sequence of library launches plus the device blocks it addresses.
+struct GraphObj {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  Pool pool;
+};
+
+#define KH_REQUIRE_NO_CAPTURE(name) \
+  KH_REQUIRE(g_state.capturing == nullptr, name ": not allowed while a graph capture is open")
 
 }  // namespace
 
@@ -123,6 +187,8 @@ void* scratch_alloc(size_t bytes) {
   return p;
 }
 void scratch_free(void* p) { (void)g_alloc.free(p); }
+
+uint32_t* zeroed_counters(size_t n) { return n <= kCounterCap ? g_state.counters : nullptr; }
 
 }  // namespace kh
 
@@ -159,6 +225,9 @@ int kh_init(int device) {
   }
   KH_CHECK_HIP(hipSetDevice(device));
   KH_CHECK_HIP(hipStreamCreateWithFlags(&g_state.stream, hipStreamNonBlocking));
+  KH_CHECK_HIP(hipMalloc(&g_state.counters, kCounterCap * sizeof(uint32_t)));
+  KH_CHECK_HIP(hipMemset(g_state.counters, 0, kCounterCap * sizeof(uint32_t)));  // once, outside any graph
+  KH_CHECK_HIP(hipDeviceSynchronize());
   g_state.device = device;
   g_state.init = true;
   return KH_OK;
@@ -179,6 +248,7 @@ int kh_free(void* ptr) {
 
 int kh_empty_cache(void) {
   KH_REQUIRE_INIT();
+  KH_REQUIRE_NO_CAPTURE("kh_empty_cache");
   std::lock_guard<std::mutex> lock(g_alloc.mu);
   g_alloc.release_cached_locked();
   return KH_OK;
@@ -193,6 +263,7 @@ int kh_get_alloc_stats(kh_alloc_stats* out) {
 
 int kh_memcpy_h2d(void* dst, const void* src, size_t bytes) {
   KH_REQUIRE_INIT();
+  KH_REQUIRE_NO_CAPTURE("kh_memcpy_h2d");
   if (bytes == 0) return KH_OK;
   KH_REQUIRE(dst && src, "kh_memcpy_h2d: null pointer");
   KH_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_state.stream));
@@ -203,6 +274,7 @@ int kh_memcpy_h2d(void* dst, const void* src, size_t bytes) {
 
 int kh_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   KH_REQUIRE_INIT();
+  KH_REQUIRE_NO_CAPTURE("kh_memcpy_d2h");
   if (bytes == 0) return KH_OK;
   KH_REQUIRE(dst && src, "kh_memcpy_d2h: null pointer");
   KH_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_state.stream));
@@ -220,6 +292,7 @@ int kh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
 
 int kh_synchronize(void) {
   KH_REQUIRE_INIT();
+  KH_REQUIRE_NO_CAPTURE("kh_synchronize");
   KH_CHECK_HIP(hipStreamSynchronize(g_state.stream));
   return KH_OK;
 }
@@ -251,6 +324,72 @@ int kh_event_elapsed_ms(void* start, void* stop, float* ms) {
   KH_REQUIRE(start && stop && ms, "kh_event_elapsed_ms: null argument");
   KH_CHECK_HIP(hipEventSynchronize((hipEvent_t)stop));
   KH_CHECK_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return KH_OK;
+}
+
+int kh_graph_begin_capture(void) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE_NO_CAPTURE("kh_graph_begin_capture");
+  GraphObj* g = new GraphObj();
+  {
+    std::lock_guard<std::mutex> lock(g_alloc.mu);
+    g_alloc.capture = &g->pool;
+  }
+  const hipError_t e = hipStreamBeginCapture(g_state.stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) {
+    std::lock_guard<std::mutex> lock(g_alloc.mu);
+    g_alloc.capture = nullptr;
+    delete g;
+    set_error("kh_graph_begin_capture: hipStreamBeginCapture failed: %s", hipGetErrorString(e));
+    return KH_ERR_HIP;
+  }
+  g_state.capturing = g;
+  return KH_OK;
+}
+
+int kh_graph_end_capture(void** graph) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(g_state.capturing != nullptr, "kh_graph_end_capture: no capture is open");
+  GraphObj* g = g_state.capturing;
+  g_state.capturing = nullptr;
+  hipError_t e = hipStreamEndCapture(g_state.stream, &g->graph);
+  {
+    std::lock_guard<std::mutex> lock(g_alloc.mu);
+    g_alloc.capture = nullptr;
+  }
+  if (e == hipSuccess && graph == nullptr) e = hipErrorInvalidValue;
+  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    kh_graph_destroy(g);
+    set_error("kh_graph_end_capture: capture or instantiation failed: %s", hipGetErrorString(e));
+    return KH_ERR_HIP;
+  }
+  *graph = g;
+  return KH_OK;
+}
+
+int kh_graph_launch(void* graph) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE_NO_CAPTURE("kh_graph_launch");
+  KH_REQUIRE(graph != nullptr && ((GraphObj*)graph)->exec != nullptr, "kh_graph_launch: not an instantiated graph");
+  KH_CHECK_HIP(hipGraphLaunch(((GraphObj*)graph)->exec, g_state.stream));
+  return KH_OK;
+}
+
+int kh_graph_destroy(void* graph) {
+  KH_REQUIRE_INIT();
+  if (graph == nullptr) return KH_OK;
+  KH_REQUIRE(graph != (void*)g_state.capturing, "kh_graph_destroy: the graph's capture is still open");
+  GraphObj* g = (GraphObj*)graph;
+  KH_CHECK_HIP(hipStreamSynchronize(g_state.stream));
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  {
+    std::lock_guard<std::mutex> lock(g_alloc.mu);
+    g_alloc.release_pool_locked(&g->pool);
+  }
+  delete g;
   return KH_OK;
 }
 

@@ -71,11 +71,6 @@ __device__ __forceinline__ float apply_binary(int op, float a, float b) {
   return op == 0 ? a + b : (op == 1 ? a * b : a - b);
 }
 
-// Reference silu: x / (1 + exp(-clamp(x, -88, 88)))  (pointwise/ops.ts:299).
-__device__ __forceinline__ float silu_f(float x) {
-  const float c = fminf(fmaxf(x, -88.0f), 88.0f);
-  return x / (1.0f + expf(-c));
-}
 
 template <typename T>
 __global__ void binary_kernel(int op, const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ out,
@@ -106,7 +101,7 @@ template <typename T>
 __global__ void silu_kernel(const T* __restrict__ x, T* __restrict__ out, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
-    Elem<T>::store(out, i, silu_f(Elem<T>::load(x, i)));
+    Elem<T>::store(out, i, silu_ref(Elem<T>::load(x, i)));
 }
 
 template <typename T>
@@ -118,7 +113,7 @@ __global__ void silu_mul_kernel(const T* __restrict__ g, int64_t gs, const T* __
     const int64_t r = i / n, c = i - r * n;
     const float gv = Elem<T>::load(g, r * gs + c);
     const float uv = Elem<T>::load(u, r * us + c);
-    Elem<T>::store(out, r * os + c, silu_f(gv) * uv);
+    Elem<T>::store(out, r * os + c, silu_ref(gv) * uv);
   }
 }
 
@@ -137,7 +132,7 @@ __global__ void silu_mul_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t g
     uint32_t wo[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      wo[j] = pack_bf16x2(silu_f(lo_bf16(wg[j])) * lo_bf16(wu[j]), silu_f(hi_bf16(wg[j])) * hi_bf16(wu[j]));
+      wo[j] = pack_bf16x2(silu_ref(lo_bf16(wg[j])) * lo_bf16(wu[j]), silu_ref(hi_bf16(wg[j])) * hi_bf16(wu[j]));
     *reinterpret_cast<uint4*>(out + r * os + c) = make_uint4(wo[0], wo[1], wo[2], wo[3]);
   }
 }
@@ -157,39 +152,104 @@ __global__ void index_select_kernel(const T* __restrict__ table, int64_t n_rows,
     Elem<D>::store(dst, c, ok ? Elem<T>::load(src, c) : 0.0f);
 }
 
+// ---- greedy decode bookkeeping (one thread) ------------------------------------------------
+__global__ void greedy_advance_kernel(const int32_t* __restrict__ next_token, int32_t* __restrict__ position,
+                                      int32_t* __restrict__ seq_len, int32_t* __restrict__ token_log,
+                                      int64_t log_base, int64_t log_cap) {
+  const int32_t p = *position;
+  const int64_t slot = (int64_t)p + 1 - log_base;
+  if (token_log != nullptr && slot >= 0 && slot < log_cap) token_log[slot] = *next_token;
+  *position = p + 1;
+  *seq_len = p + 2;
+}
+
 // ---- argmax (lowest index among maxima; NaN never wins; init -FLT_MAX at index 0) ----------
+// A candidate must be strictly greater than -FLT_MAX (the reference's initial value); a row with
+// none yields index 0, as the reference's initial best_idx does.  Pass 1: block (c, r) scans
+// columns [c * AM_CHUNK, (c + 1) * AM_CHUNK) of row r with all its loads issued up front; pass 2
+// combines the per-chunk (value, index) pairs of a row.  A row of one chunk finishes in pass 1.
+constexpr int AM_PER_THREAD = 16;
+constexpr int AM_CHUNK = kThreads * AM_PER_THREAD;
+
+__device__ __forceinline__ bool am_better(float v, int32_t i, float bv, int32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Block-wide (value, index) reduction; every thread returns the block's best pair.
+__device__ __forceinline__ void am_block_reduce(float& best, int32_t& bidx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int32_t oi = __shfl_xor(bidx, o, 64);
+    if (am_better(ov, oi, best, bidx)) {
+      best = ov;
+      bidx = oi;
+    }
+  }
+  __shared__ float sv[kThreads / 64];
+  __shared__ int32_t si[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = best;
+    si[threadIdx.x >> 6] = bidx;
+  }
+  __syncthreads();
+  best = sv[0];
+  bidx = si[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+    if (am_better(sv[w], si[w], best, bidx)) {
+      best = sv[w];
+      bidx = si[w];
+    }
+}
+
 template <typename T>
-__global__ void argmax_kernel(const T* __restrict__ x, int64_t n, int32_t* __restrict__ out) {
-  const int64_t r = blockIdx.x;
+__global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const T* __restrict__ x, int64_t n,
+                                                                  float* __restrict__ pv, int32_t* __restrict__ pi,
+                                                                  int32_t* __restrict__ out) {
+  const int64_t r = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * AM_CHUNK;
   const T* row = x + r * n;
-  // A candidate must be strictly greater than -FLT_MAX (the reference's initial value); a row
-  // with none yields index 0, as the reference's initial best_idx does.
+  float v[AM_PER_THREAD];
+#pragma unroll
+  for (int j = 0; j < AM_PER_THREAD; ++j) {
+    const int64_t i = c0 + j * kThreads + threadIdx.x;
+    v[j] = i < n ? Elem<T>::load(row, i) : -FLT_MAX;
+  }
   float best = -FLT_MAX;
   int32_t bidx = INT32_MAX;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = Elem<T>::load(row, i);
-    if (v > best) {
+#pragma unroll
+  for (int j = 0; j < AM_PER_THREAD; ++j)  // increasing column order: strict > keeps the first
+    if (v[j] > best) {
+      best = v[j];
+      bidx = (int32_t)(c0 + j * kThreads + threadIdx.x);
+    }
+  am_block_reduce(best, bidx);
+  if (threadIdx.x == 0) {
+    if (gridDim.x == 1) {
+      out[r] = bidx == INT32_MAX ? 0 : bidx;
+    } else {
+      pv[r * gridDim.x + blockIdx.x] = best;
+      pi[r * gridDim.x + blockIdx.x] = bidx;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_final_kernel(const float* __restrict__ pv,
+                                                                const int32_t* __restrict__ pi, int nchunks,
+                                                                int32_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  float best = -FLT_MAX;
+  int32_t bidx = INT32_MAX;
+  for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
+    const float v = pv[r * nchunks + c];
+    const int32_t i = pi[r * nchunks + c];
+    if (am_better(v, i, best, bidx)) {
       best = v;
-      bidx = (int32_t)i;
+      bidx = i;
     }
   }
-  __shared__ float sv[kThreads];
-  __shared__ int32_t si[kThreads];
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bidx;
-  __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      const float ov = sv[threadIdx.x + s];
-      const int32_t oi = si[threadIdx.x + s];
-      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) out[r] = si[0] == INT32_MAX ? 0 : si[0];
+  am_block_reduce(best, bidx);
+  if (threadIdx.x == 0) out[r] = bidx == INT32_MAX ? 0 : bidx;
 }
 
 }  // namespace
@@ -341,18 +401,48 @@ int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64
   return KH_OK;
 }
 
+int kh_greedy_advance(const int32_t* next_token, int32_t* position, int32_t* seq_len, int32_t* token_log,
+                      int64_t log_base, int64_t log_cap) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(next_token && position && seq_len, "kh_greedy_advance: null pointer");
+  KH_REQUIRE(log_cap >= 0 && (log_cap == 0 || token_log != nullptr), "kh_greedy_advance: bad token log");
+  greedy_advance_kernel<<<1, 1, 0, stream()>>>(next_token, position, seq_len, token_log, log_base, log_cap);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
 int kh_argmax(const void* x, int64_t rows, int64_t n, int32_t* out, int dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(rows >= 0 && n > 0, "kh_argmax: bad extents (rows %lld, n %lld)", (long long)rows, (long long)n);
   if (rows == 0) return KH_OK;
   KH_REQUIRE(rows <= INT32_MAX && n <= INT32_MAX, "kh_argmax: extents too large");
   KH_REQUIRE(x && out, "kh_argmax: null pointer");
-  if (dtype == KH_F32)
-    argmax_kernel<float><<<(int)rows, kThreads, 0, stream()>>>((const float*)x, n, out);
-  else if (dtype == KH_BF16)
-    argmax_kernel<uint16_t><<<(int)rows, kThreads, 0, stream()>>>((const uint16_t*)x, n, out);
-  else
-    KH_REQUIRE(false, "kh_argmax: unsupported dtype %d", dtype);
+  KH_REQUIRE(dtype == KH_F32 || dtype == KH_BF16, "kh_argmax: unsupported dtype %d", dtype);
+  const int64_t nchunks = (n + AM_CHUNK - 1) / AM_CHUNK;
+  float* pv = nullptr;
+  int32_t* pi = nullptr;
+  void* part = nullptr;
+  if (nchunks > 1) {
+    part = scratch_alloc((size_t)rows * nchunks * 8);
+    KH_REQUIRE(part != nullptr, "kh_argmax: out of device memory for partials");
+    pv = (float*)part;
+    pi = (int32_t*)(pv + rows * nchunks);
+  }
+  const size_t esz = dtype == KH_F32 ? 4 : 2;
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {  // grid.y holds at most 65535 rows per launch
+    const int64_t nr = rows - r0 < 65535 ? rows - r0 : 65535;
+    const dim3 grid((unsigned)nchunks, (unsigned)nr);
+    const void* xr = (const char*)x + (size_t)r0 * n * esz;
+    float* pvr = pv ? pv + r0 * nchunks : nullptr;
+    int32_t* pir = pi ? pi + r0 * nchunks : nullptr;
+    if (dtype == KH_F32)
+      argmax_partial_kernel<float><<<grid, kThreads, 0, stream()>>>((const float*)xr, n, pvr, pir, out + r0);
+    else
+      argmax_partial_kernel<uint16_t><<<grid, kThreads, 0, stream()>>>((const uint16_t*)xr, n, pvr, pir, out + r0);
+    if (nchunks > 1)
+      argmax_final_kernel<<<(unsigned)nr, kThreads, 0, stream()>>>(pvr, pir, (int)nchunks, out + r0);
+  }
+  if (part) scratch_free(part);  // stream-ordered reuse only
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

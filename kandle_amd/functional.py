@@ -151,6 +151,31 @@ def linear(input: Tensor, weight: Tensor, bias: Optional[Tensor] = None, out_dty
     return dispatch_matmul(input, weight, transpose_b=True, bias=bias, out_dtype=out_dtype)
 
 
+def linear_fused(prologue: str, x: Tensor, weight: Tensor, norm_weight: Optional[Tensor] = None,
+                 eps: float = 1e-6, x2: Optional[Tensor] = None, residual: Optional[Tensor] = None,
+                 out_dtype: Optional[str] = None) -> Tensor:
+    """One-row linear with its producer fused in front (decode).  prologue 'rms_norm': x is the
+    fp32 residual row and the input is rms_norm(x, norm_weight, eps); 'silu_mul': the input is
+    silu(x) * x2; 'none': the input is x.  With `residual` the result is added into it in place
+    (residual += input @ weight^T) and returned; otherwise a new [1, out_features] tensor of
+    out_dtype (default bf16)."""
+    params = {"eps": eps}
+    if norm_weight is not None:
+        params["norm_weight"] = norm_weight.handle
+    if x2 is not None:
+        params["x2"] = x2.handle
+    if residual is not None:
+        params["cin"] = residual.handle
+        params["beta"] = 1.0
+        out = residual.handle
+    else:
+        out = _new(weight, (1, weight.shape[0]), out_dtype or "bfloat16")
+    _kernel(weight, "gemv_fused")(prologue, x.handle, weight.handle, out, params)
+    if residual is not None:
+        return residual
+    return _wrap(out)
+
+
 # ---------------------------------------------------------------------------------------------
 # normalisation and pointwise
 # ---------------------------------------------------------------------------------------------

@@ -296,7 +296,10 @@ def rms_norm_rope(q, k, params):
 
     params: q_weight, k_weight (handles [D]), inv_freq (float32 handle [D/2]), positions (int32 handle
     [B*S]), eps, and optional q_out / k_out (default: new [B,Hq,S,D] / [B,Hkv,S,D] tensors, i.e. the
-    heads-first layout the attention consumes), v / v_out.  Returns (q_out, k_out)."""
+    heads-first layout the attention consumes), v / v_out.  With cache_positions=True, k_out and
+    v_out are whole KV caches [B, Hkv, max_seq, D] and token t is written at sequence index
+    positions[t] (positions outside [0, max_seq) write nothing), so the write location can live on
+    the device (kv-cache.ts:164-212 writes the slice [pos, pos+S)).  Returns (q_out, k_out)."""
     if q.dtype != k.dtype or q.dtype not in (FLOAT32, BFLOAT16):
         raise TypeError("rms_norm_rope: q and k must share a float dtype")
     if len(q.shape) != 4 or len(k.shape) != 4:
@@ -314,6 +317,11 @@ def rms_norm_rope(q, k, params):
         return [st[0], st[2], st[1]] if heads_first else [st[0], st[1], st[2]]
 
     v, v_out = params.get("v"), params.get("v_out")
+    kv_cache_len = 0
+    if params.get("cache_positions"):
+        kv_cache_len = k_out.shape[2]
+        if v_out is not None and v_out.shape[2] != kv_cache_len:
+            raise ValueError("rms_norm_rope: K and V caches must have the same length")
     s = bsh(q, False) + bsh(k, False) + bsh(q_out, True) + bsh(k_out, True)
     if v is not None:
         s += bsh(v, False) + bsh(v_out, True)
@@ -329,6 +337,7 @@ def rms_norm_rope(q, k, params):
         _vp(params["q_weight"].data_ptr()), _vp(params["k_weight"].data_ptr()),
         _vp(inv_freq.data_ptr()), _vp(pos.data_ptr()),
         B, S, Hq, Hkv, D, _lib.i64_array(s), C.c_float(float(params.get("eps", 1e-6))), q.kh_dtype,
+        kv_cache_len,
     )
     return q_out, k_out
 
@@ -499,6 +508,61 @@ def zeros(output: HipTensorHandle) -> None:
     fill(output, 0.0)
 
 
+GEMV_PROLOGUES = {"none": 0, "rms_norm": 1, "silu_mul": 2}
+
+
+def gemv_fused(prologue: str, x, w, out, params=None) -> None:
+    """One-row projection with its producer fused in front (decode): out[1, n] = alpha * x' W^T
+    + beta * cin (+ bias) for the bf16 weight W [n, k] (nn.Linear layout), where x' is
+      'none'     -> x (bf16 [k]);
+      'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row x, rounded to bf16;
+      'silu_mul' -> silu(x) * x2 of the bf16 gate/up rows, rounded to bf16.
+    params: norm_weight, eps, x2, cin, alpha, beta, bias.  out may alias cin (residual add).
+    Fuses RMSNorm.ts:92-99 or swiglu.ts:119-134 into Linear.ts:135-137."""
+    params = params or {}
+    code = GEMV_PROLOGUES[prologue]
+    n, k = w.shape
+    if w.dtype != BFLOAT16 or w.strides[1] != 1:
+        raise TypeError("gemv_fused: the weight must be bf16 with contiguous rows")
+    want = FLOAT32 if prologue == "rms_norm" else BFLOAT16
+    x2 = params.get("x2")
+    for h, nm in ((x, "x"), (x2, "x2")):
+        if h is None:
+            continue
+        if h.dtype != want or h.numel != k or (len(h.shape) > 0 and h.strides[-1] != 1):
+            raise ValueError(f"gemv_fused: {nm} must be one contiguous {want} row of {k} elements")
+    if prologue == "silu_mul" and x2 is None:
+        raise ValueError("gemv_fused: silu_mul needs x2")
+    nw = params.get("norm_weight")
+    if prologue == "rms_norm" and (nw is None or nw.dtype != BFLOAT16 or nw.numel != k):
+        raise ValueError("gemv_fused: rms_norm needs a bf16 norm_weight of k elements")
+    if out.numel != n or not out.is_contiguous() or out.dtype not in (FLOAT32, BFLOAT16):
+        raise ValueError("gemv_fused: out must be a contiguous float row of n elements")
+    cin, bias = params.get("cin"), params.get("bias")
+    for h, nm in ((cin, "cin"), (bias, "bias")):
+        if h is not None and (h.numel != n or not h.is_contiguous() or h.dtype != out.dtype):
+            raise ValueError(f"gemv_fused: {nm} must be a contiguous row of n elements in the output dtype")
+    beta = float(params.get("beta", 1.0 if cin is not None else 0.0))
+    _lib.call(
+        "kh_gemv_fused", code, _vp(x.data_ptr()), _vp(x2.data_ptr()) if x2 is not None else None,
+        _vp(nw.data_ptr()) if nw is not None else None, C.c_float(float(params.get("eps", 1e-6))),
+        _vp(w.data_ptr()), w.strides[0], _vp(out.data_ptr()), _vp(cin.data_ptr()) if cin is not None else None,
+        _vp(bias.data_ptr()) if bias is not None else None, n, k, C.c_float(float(params.get("alpha", 1.0))),
+        C.c_float(beta), out.kh_dtype,
+    )
+
+
+def greedy_advance(next_token, position, seq_len, token_log, log_base: int) -> None:
+    """Device-side step of the greedy loop (for_causal_lm.ts:475-508): with p = position[0],
+    token_log[p + 1 - log_base] = next_token[0] (when inside the log), position = p + 1,
+    seq_len = p + 2.  All operands are int32 device tensors."""
+    for h in (next_token, position, seq_len, token_log):
+        if h.dtype != INT32 or not h.is_contiguous():
+            raise TypeError("greedy_advance: operands must be contiguous int32 tensors")
+    _lib.call("kh_greedy_advance", _vp(next_token.data_ptr()), _vp(position.data_ptr()), _vp(seq_len.data_ptr()),
+              _vp(token_log.data_ptr()), int(log_base), token_log.numel)
+
+
 KERNELS = {
     "flash_attention": flash_attention,
     "decode_attention": decode_attention,
@@ -520,6 +584,8 @@ KERNELS = {
     "copy_": copy_,
     "index_select": index_select,
     "argmax": argmax,
+    "greedy_advance": greedy_advance,
+    "gemv_fused": gemv_fused,
     "fill": fill,
     "zeros": zeros,
 }

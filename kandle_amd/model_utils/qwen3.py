@@ -22,6 +22,7 @@ read fp32 x and write bf16 h); math inside kernels is fp32.
 """
 from __future__ import annotations
 
+import time
 from dataclasses import dataclass
 from typing import Dict, List, Optional
 
@@ -30,6 +31,8 @@ import numpy as np
 from .. import env
 from .. import functional as F
 from .. import synthetic as syn
+from ..graphs import HipGraph
+from ..kernels import TensorIterator
 from ..tensor import HipTensorHandle, Tensor
 from .kv_cache import StaticKVCache
 from .rope import RotaryEmbedding
@@ -116,61 +119,114 @@ class Qwen3ForCausalLM:
         self.cache = StaticKVCache(cfg.num_hidden_layers, 1, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
         self.scale = 1.0 / np.sqrt(cfg.head_dim)
 
+    # -- decoder body shared by the prefill and the device-resident decode step -------------------
+    def _decoder(self, x: Tensor, S: int, positions: Tensor, attend) -> Tensor:
+        """Runs every decoder layer over the fp32 residual rows x [S, hidden] in place and returns
+        the fp32 logits of the last position [1, vocab].  positions: int32 [S] device tensor
+        (RoPE angles and KV-cache rows); attend(layer, q_heads, out_view) writes attention for
+        q_heads [1, Hq, S, D] into out_view [1, Hq, S, D].  A single row (decode) runs each norm
+        and the SwiGLU product inside the projection that consumes it (linear_fused)."""
+        cfg = self.cfg
+        Hq, Hkv, D, Hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
+        nq, nkv, I = Hq * D, Hkv * D, cfg.intermediate_size
+        eps = cfg.rms_norm_eps
+        one = S == 1
+        for li, L in enumerate(self.layers):
+            if one:
+                qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
+            else:
+                h = F.rms_norm(x, [Hd], L["in_norm"], eps, out_dtype="bfloat16")
+                qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
+                h.dispose()
+            q = _split_heads(qkv, 0, S, Hq, D)
+            k = _split_heads(qkv, nq, S, Hkv, D)
+            v = _split_heads(qkv, nq + nkv, S, Hkv, D)
+            q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+            # K (normed + rotated) and V land in the cache rows given by `positions`.
+            self.ops.find("rms_norm_rope")(q.handle, k.handle, {
+                "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
+                "positions": positions.handle, "eps": eps, "q_out": q_heads,
+                "k_out": self.cache.key_cache[li].handle, "v": v.handle, "v_out": self.cache.value_cache[li].handle,
+                "cache_positions": True})
+            for t in (q, k, v, qkv):
+                t.dispose()
+            attn = HipTensorHandle.create_new((S, nq), "bfloat16")
+            # [1, Hq, S, D] view of the [S, Hq*D] buffer: o_proj then reads it as a plain matrix.
+            attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
+            attend(li, q_heads, attn_view)
+            attn_view.dispose()
+            q_heads.dispose()
+            attn_t = Tensor(handle=attn)
+            if one:
+                F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
+            else:
+                F.dispatch_matmul(attn_t, L["w_o"], c=x, beta=1.0, out=x, transpose_b=True)
+            attn_t.dispose()
+            if one:
+                gu = F.linear_fused("rms_norm", x, L["w_gu"], L["post_norm"], eps)     # [1, 2I]
+            else:
+                h = F.rms_norm(x, [Hd], L["post_norm"], eps, out_dtype="bfloat16")
+                gu = F.linear(h, L["w_gu"])                                            # [S, 2I]
+                h.dispose()
+            g, u = F.narrow(gu, 1, 0, I), F.narrow(gu, 1, I, I)
+            if one:
+                F.linear_fused("silu_mul", g, L["w_down"], x2=u, residual=x)           # x += a W_d^T
+            else:
+                a = F.silu_mul(g, u)
+                F.dispatch_matmul(a, L["w_down"], c=x, beta=1.0, out=x, transpose_b=True)
+                a.dispose()
+            for t in (g, u, gu):
+                t.dispose()
+        last = F.narrow(x, 0, S - 1, 1)
+        if one:
+            logits = F.linear_fused("rms_norm", last, self.embed, self.final_norm, eps, out_dtype="float32")
+        else:
+            xf = F.rms_norm(last, [Hd], self.final_norm, eps, out_dtype="bfloat16")
+            logits = F.linear(xf, self.embed, out_dtype="float32")                     # [1, vocab] fp32
+            xf.dispose()
+        last.dispose()
+        return logits
+
     # -- one forward over S new tokens at cache position `pos` -------------------------------------
     def forward(self, input_ids: np.ndarray, pos: int) -> Tensor:
         """Runs the decoder over input_ids (int32 [S]) appended at `pos`; returns fp32 logits of the
         last position [1, vocab] (the only row greedy decoding reads)."""
-        cfg = self.cfg
         S = int(len(input_ids))
-        Hq, Hkv, D, Hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
-        nq, nkv = Hq * D, Hkv * D
         end = self.cache.check_write(pos, S)
         ids = Tensor(np.asarray(input_ids, np.int32), dtype="int32")
         x = F.embedding(ids, self.embed, out_dtype="float32")     # [S, Hd] fp32 residual stream
         positions = RotaryEmbedding.get_position_ids(S, pos)
-        eps = cfg.rms_norm_eps
-        for li, L in enumerate(self.layers):
-            h = F.rms_norm(x, [Hd], L["in_norm"], eps, out_dtype="bfloat16")
-            qkv = F.linear(h, L["w_qkv"])                          # [S, nq + 2 nkv]
-            h.dispose()
-            q = _split_heads(qkv, 0, S, Hq, D)
-            k = _split_heads(qkv, nq, S, Hkv, D)
-            v = _split_heads(qkv, nq + nkv, S, Hkv, D)
-            k_dst, v_dst = self.cache.write_slices(li, pos, S)
-            q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
-            self.ops.find("rms_norm_rope")(q.handle, k.handle, {
-                "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
-                "positions": positions.handle, "eps": eps, "q_out": q_heads, "k_out": k_dst.handle,
-                "v": v.handle, "v_out": v_dst.handle})
-            for t in (q, k, v, k_dst, v_dst):
-                t.dispose()
-            qkv.dispose()
+
+        def attend(li, q_heads, out_view):
             kc, vc = self.cache.valid_slices(li, end)
-            attn = HipTensorHandle.create_new((S, nq), "bfloat16")
-            # [1, Hq, S, D] view of the [S, Hq*D] buffer: o_proj then reads it as a plain matrix.
-            attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
-            self.ops.find("flash_attention")(q_heads, kc.handle, vc.handle, attn_view, self.scale, S > 1)
-            attn_view.dispose()
-            q_heads.dispose()
+            # causal for a multi-token chunk; off for one new token (gqa.ts:333-336)
+            self.ops.find("flash_attention")(q_heads, kc.handle, vc.handle, out_view, self.scale, S > 1)
             kc.dispose()
             vc.dispose()
-            attn_t = Tensor(handle=attn)
-            F.dispatch_matmul(attn_t, L["w_o"], c=x, beta=1.0, out=x, transpose_b=True)   # x += o W_o^T
-            attn_t.dispose()
-            h = F.rms_norm(x, [Hd], L["post_norm"], eps, out_dtype="bfloat16")
-            gu = F.linear(h, L["w_gu"])                            # [S, 2I]
-            h.dispose()
-            I = cfg.intermediate_size
-            a = F.silu_mul(F.narrow(gu, 1, 0, I), F.narrow(gu, 1, I, I))
-            gu.dispose()
-            F.dispatch_matmul(a, L["w_down"], c=x, beta=1.0, out=x, transpose_b=True)     # x += a W_d^T
-            a.dispose()
+
+        logits = self._decoder(x, S, positions, attend)
         self.cache.mark_written(end)
-        last = F.narrow(x, 0, S - 1, 1)
-        xf = F.rms_norm(last, [Hd], self.final_norm, eps, out_dtype="bfloat16")
-        logits = F.linear(xf, self.embed, out_dtype="float32")     # [1, vocab] fp32
-        for t in (last, xf, x, ids, positions):
+        for t in (x, ids, positions):
             t.dispose()
+        return logits
+
+    # -- device-resident greedy decode step ---------------------------------------------------------
+    def _decode_step(self, st: "DecodeState") -> Tensor:
+        """One greedy step that reads every changing value from device memory: the token st.ids at
+        position st.pos attends over st.lens cached rows; the argmax of its logits overwrites st.ids
+        and greedy_advance logs it and moves st.pos / st.lens on.  The same launches run eagerly
+        or replayed from a captured graph.  Returns the step's fp32 logits [1, vocab]."""
+        x = F.embedding(st.ids, self.embed, out_dtype="float32")  # [1, Hd]
+
+        def attend(li, q_heads, out_view):
+            self.ops.find("decode_attention")(q_heads, self.cache.key_cache[li].handle,
+                                               self.cache.value_cache[li].handle, st.lens.handle, out_view,
+                                               self.scale)
+
+        logits = self._decoder(x, 1, st.pos, attend)
+        x.dispose()
+        self.ops.find("argmax")(TensorIterator([logits.handle], [st.ids.handle]))
+        self.ops.find("greedy_advance")(st.ids.handle, st.pos.handle, st.lens.handle, st.log.handle, st.base)
         return logits
 
     def greedy(self, logits: Tensor) -> int:
@@ -179,22 +235,65 @@ class Qwen3ForCausalLM:
         tok.dispose()
         return v
 
-    def generate(self, prompt_ids: np.ndarray, max_new_tokens: int, return_logits: bool = False):
-        """Prefill the prompt, then greedy-decode max_new_tokens tokens (for_causal_lm.ts:475-508)."""
+    def generate(self, prompt_ids: np.ndarray, max_new_tokens: int, return_logits: bool = False,
+                 use_graph: bool = True, timing: Optional[dict] = None):
+        """Prefill the prompt, then greedy-decode (for_causal_lm.ts:475-508): max_new_tokens token
+        ids, each the lowest-index argmax of the previous logits, after max_new_tokens decode
+        forwards as in the reference loop.  The decode steps run on device state; with use_graph
+        the step is captured once and replayed.  return_logits adds the fp32 logits each token was
+        chosen from.  timing (a dict) receives wall times: prefill_ms, decode_ms (all decode steps,
+        including the eager first step and the capture) and, with a graph, replay_ms over the
+        replay_steps = max_new_tokens - 1 replayed steps."""
+        from .. import _lib
+
+        P, N = int(len(prompt_ids)), int(max_new_tokens)
         self.cache.reset()
+        self.cache.check_write(0, P + N)
+        t0 = time.perf_counter()
         logits = self.forward(prompt_ids, 0)
-        pos = len(prompt_ids)
-        out, all_logits = [], []
-        for _ in range(max_new_tokens):
-            if return_logits:
-                all_logits.append(logits.numpy()[0])
-            nxt = self.greedy(logits)
-            logits.dispose()
-            out.append(nxt)
-            logits = self.forward(np.array([nxt], np.int32), pos)
-            pos += 1
+        st = DecodeState.start(logits, P, N + 1, self.ops)
+        if timing is not None:
+            _lib.synchronize()
+            timing["prefill_ms"] = (time.perf_counter() - t0) * 1e3
+        all_logits = [logits.numpy()[0]] if return_logits else []
         logits.dispose()
-        return (out, all_logits) if return_logits else out
+        graph, g_logits = None, None
+        t1 = time.perf_counter()
+        t_replay = None
+        try:
+            for i in range(N):
+                if not use_graph or i == 0:
+                    lg = self._decode_step(st)
+                    if return_logits and i + 1 < N:
+                        all_logits.append(lg.numpy()[0])
+                    lg.dispose()
+                    if use_graph and N > 1:
+                        # Capture records the step without running it; replays 1..N-1 run it.
+                        graph = HipGraph()
+                        with graph.capture():
+                            g_logits = self._decode_step(st)
+                        if timing is not None:
+                            _lib.synchronize()
+                            t_replay = time.perf_counter()
+                else:
+                    graph.replay()
+                    if return_logits and i + 1 < N:
+                        all_logits.append(g_logits.numpy()[0])
+            toks = st.log.numpy()[:N].tolist()   # waits for the last step
+            t2 = time.perf_counter()
+        finally:
+            if g_logits is not None:
+                g_logits.dispose()
+            if graph is not None:
+                graph.dispose()
+            st.dispose()
+        if timing is not None:
+            timing["decode_ms"] = (t2 - t1) * 1e3
+            if t_replay is not None:
+                timing["replay_ms"] = (t2 - t_replay) * 1e3
+                timing["replay_steps"] = N - 1
+        self.cache.mark_written(P + N)
+        return (toks, all_logits) if return_logits else toks
 
     def dispose(self) -> None:
         self.cache.dispose()
@@ -208,3 +307,29 @@ def _split_heads(qkv: Tensor, col0: int, S: int, H: int, D: int) -> Tensor:
     h = HipTensorHandle.create_view(qkv.handle.storage, (1, S, H, D), qkv.dtype, (S * ncols, ncols, D, 1),
                                     qkv.offset + col0)
     return Tensor(handle=h)
+
+
+class DecodeState:
+    """Device-resident greedy-loop state: ids (int32 [1], the token to feed), pos (int32 [1], its
+    position), lens (int32 [1], KV rows attended = pos + 1) and log (int32 [cap], the generated
+    tokens; log[i] is the token for position base + i)."""
+
+    def __init__(self, ids: Tensor, pos: Tensor, lens: Tensor, log: Tensor, base: int):
+        self.ids, self.pos, self.lens, self.log, self.base = ids, pos, lens, log, base
+
+    @classmethod
+    def start(cls, prefill_logits: Tensor, prompt_len: int, cap: int, ops) -> "DecodeState":
+        """State after the prefill: ids = argmax(prefill logits) (also log[0]), pos = prompt_len."""
+        ids = F.zeros((1,), "int32")
+        log = F.zeros((cap,), "int32")
+        ops.find("argmax")(TensorIterator([prefill_logits.handle], [ids.handle]))
+        head = F.narrow(log, 0, 0, 1)
+        F.copy_(head, ids)
+        head.dispose()
+        pos = Tensor(np.array([prompt_len], np.int32), dtype="int32")
+        lens = Tensor(np.array([prompt_len + 1], np.int32), dtype="int32")
+        return cls(ids, pos, lens, log, prompt_len)
+
+    def dispose(self) -> None:
+        for t in (self.ids, self.pos, self.lens, self.log):
+            t.dispose()

@@ -117,6 +117,24 @@ def test_decode_varlen_matches_oracle(hip):
     assert np.max(np.abs(o - ref)) < BF16_ATOL
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (16, 2)])
+def test_decode_single_launch_merge(hip, Hq, Hkv):
+    """Caches of at most 8 chunks merge in the decode launch itself (the last chunk's block, via a
+    counter it returns to zero): varlen including an empty and a one-key sequence, and three
+    launches in a row giving identical results (the counters start at zero every time)."""
+    B, D, ML = 5, 128, 2048
+    lens = np.array([0, 1, 256, 700, 2048], np.int32)
+    q, qh = seeded(74, (B, Hq, D), "bfloat16")
+    kc, kch = seeded(75, (B, Hkv, ML, D), "bfloat16")
+    vc, vch = seeded(76, (B, Hkv, ML, D), "bfloat16")
+    sl = Tensor(lens, dtype="int32")
+    outs = [F.decode_attention(q, kc, vc, sl).numpy() for _ in range(3)]
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert np.all(outs[0][0] == 0.0)
+    ref = oracle.sdpa(qh[1:, :, None, :], kch[1:], vch[1:], kv_len=lens[1:])[:, :, 0, :]
+    assert np.max(np.abs(outs[0][1:] - ref)) < BF16_ATOL
+
+
 def test_decode_c4_full_size(hip):
     """Config C4 at full size: B=8, Hq=16, Hkv=8, D=128, L_b ~ U[8192, 32768], bf16."""
     B, Hq, Hkv, D, ML = 8, 16, 8, 128, 32768

@@ -107,3 +107,34 @@ def test_qk_norm_rope_fused_v_copy(hip):
     c = cache.numpy()
     np.testing.assert_array_equal(c[0, :, 10:10 + T], vh[0].transpose(1, 0, 2))
     assert np.all(c[0, :, :10] == 0) and np.all(c[0, :, 10 + T:] == 0)
+
+
+def test_qk_norm_rope_cache_positions(hip):
+    """Cache addressing: K/V of token t land in cache row positions[t]; a position outside the
+    cache writes nothing; rows no token names keep their contents; q keeps token order."""
+    T, Hq, Hkv, D, L = 5, 4, 2, 128, 8
+    pos = np.array([3, 0, 7, 9, 1], np.int32)
+    q, qh = seeded(130, (1, T, Hq, D))
+    k, kh = seeded(131, (1, T, Hkv, D))
+    v, vh = seeded(132, (1, T, Hkv, D))
+    wq = syn.uniform(133, (D,), 0.5, 1.5)
+    wk = syn.uniform(134, (D,), 0.5, 1.5)
+    inv = oracle.rope_inv_freq(D, 1e6)
+    kc = Tensor(np.full((1, Hkv, L, D), 7.0, np.float32))
+    vc = Tensor(np.full((1, Hkv, L, D), 7.0, np.float32))
+    params = {"q_weight": Tensor(wq).handle, "k_weight": Tensor(wk).handle, "inv_freq": Tensor(inv).handle,
+              "positions": Tensor(pos, dtype="int32").handle, "eps": 1e-6, "k_out": kc.handle,
+              "v": v.handle, "v_out": vc.handle, "cache_positions": True}
+    qo, _ = kernels.rms_norm_rope(q.handle, k.handle, params)
+    rq = oracle.qk_norm_rope(qh[0], wq, pos, inv, 1e-6)          # [T, Hq, D]
+    rk = oracle.qk_norm_rope(kh[0], wk, pos, inv, 1e-6)          # [T, Hkv, D]
+    assert max_rel(qo.data_async()[0].transpose(1, 0, 2), rq) < 1e-4
+    gk, gv = kc.numpy()[0], vc.numpy()[0]                          # [Hkv, L, D]
+    written = {int(p_): t for t, p_ in enumerate(pos) if 0 <= p_ < L}
+    for row in range(L):
+        if row in written:
+            t = written[row]
+            assert max_rel(gk[:, row], rk[t]) < 1e-4
+            np.testing.assert_array_equal(gv[:, row], vh[0, t])
+        else:
+            assert np.all(gk[:, row] == 7.0) and np.all(gv[:, row] == 7.0)
