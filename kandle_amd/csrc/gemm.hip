@@ -46,40 +46,43 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 }
 
 // =============================================================================================
-// MFMA tile kernel.  Workgroup tile 128 (m) x 128 (n), k-step 64, 4 waves in a 2 x 2 layout, each
-// wave 64 x 64 = 2 x 2 tiles of 32 x 32.  The product is formed as C^T = B A^T so that each lane
-// owns one m row and 4 consecutive n per register group: A-operand = B rows (n), B-operand = A rows
-// (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are raw buffer loads
-// (rows past M / N and columns past K read as zero without a branch).
+// MFMA tile kernel.  Workgroup tile (64 WT) x (64 WT), k-step 64, 4 waves in a 2 x 2 layout, each
+// wave (32 WT) x (32 WT) = WT x WT tiles of 32 x 32: WT = 2 (128 x 128) for large problems, WT = 1
+// (64 x 64) when 128-tiles would leave CUs idle.  The product is formed as C^T = B A^T so that each
+// lane owns one m row and 4 consecutive n per register group: A-operand = B rows (n), B-operand =
+// A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are raw
+// buffer loads (rows past M / N and columns past K read as zero without a branch).
 // =============================================================================================
-constexpr int GM = 128, GN = 128, GK = 64;
+constexpr int GK = 64;
 constexpr int G_THREADS = 256;
 constexpr int G_STR = GK + 8;  // LDS row stride (elements), keeps 16-byte alignment, breaks bank aliasing
-constexpr int G_ATILE = GM * G_STR;
-constexpr int G_BTILE = GN * G_STR;
+constexpr int g_tile(int wt) { return 64 * wt; }
 
-template <typename TO>
+template <typename TO, int WT>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
     int tiles_n) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (G_ATILE + G_BTILE)];
+  constexpr int GM = g_tile(WT), GN = g_tile(WT);
+  constexpr int ATILE = GM * G_STR, BTILE = GN * G_STR;
+  constexpr int CPT = GM * (GK / 8) / G_THREADS;  // 16-byte chunks per thread per tile
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ATILE + BTILE)];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, g = lane >> 5;
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
   const int m0 = tm * GM, n0 = tn * GN;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int wm = (wave >> 1) * 32 * WT, wn = (wave & 1) * 32 * WT;
 
   // Byte ranges of this tile's rows; a row past the matrix or a column past K reads zero.
   const int mrows = min(GM, M - m0), nrows = min(GN, N - n0);
   const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * 2));
   const auto rb = make_rsrc(B + (int64_t)n0 * ldb, (uint32_t)(((int64_t)(nrows - 1) * ldb + K) * 2));
 
-  // Staging: each of the A and B tiles is 128 rows x 64 k = 1024 chunks of 16 B, 4 per thread.
-  uint4 ast[4], bst[4];
+  // Staging: each of the A and B tiles is GM rows x 64 k = GM * 8 chunks of 16 B, CPT per thread.
+  uint4 ast[CPT], bst[CPT];
   auto load_tile = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int id = tid + G_THREADS * i;
       const int row = id >> 3, kc = kt + 8 * (id & 7);
       // Columns >= K map past the range (K % 8 == 0, so a chunk is all in or all out).
@@ -90,10 +93,10 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     }
   };
   auto store_tile = [&](int buf) {
-    uint16_t* as = smem + buf * (G_ATILE + G_BTILE);
-    uint16_t* bs = as + G_ATILE;
+    uint16_t* as = smem + buf * (ATILE + BTILE);
+    uint16_t* bs = as + ATILE;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int id = tid + G_THREADS * i;
       const int row = id >> 3, kc = 8 * (id & 7);
       *reinterpret_cast<uint4*>(as + row * G_STR + kc) = ast[i];
@@ -101,11 +104,11 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     }
   };
 
-  f32x16 acc[2][2];  // [n tile][m tile]
+  f32x16 acc[WT][WT];  // [n tile][m tile]
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < WT; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < WT; ++b)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
 
@@ -118,20 +121,20 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const int buf = t & 1;
     const bool has_next = t + 1 < nk;
     if (has_next) load_tile((t + 1) * GK);
-    const uint16_t* as = smem + buf * (G_ATILE + G_BTILE);
-    const uint16_t* bs = as + G_ATILE;
+    const uint16_t* as = smem + buf * (ATILE + BTILE);
+    const uint16_t* bs = as + ATILE;
 #pragma unroll
     for (int kc = 0; kc < GK / 16; ++kc) {
-      bf16x8 av[2], bv[2];
+      bf16x8 av[WT], bv[WT];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < WT; ++i) {
         av[i] = as_bf16x8(*reinterpret_cast<const uint4*>(as + (wm + 32 * i + r) * G_STR + 16 * kc + 8 * g));
         bv[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn + 32 * i + r) * G_STR + 16 * kc + 8 * g));
       }
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < WT; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < WT; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv[a], av[b], acc[a][b], 0, 0, 0);
     }
     if (has_next) store_tile(buf ^ 1);
@@ -141,11 +144,11 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   // Epilogue: acc[a][b] lane holds m = m0 + wm + 32b + r, n = n0 + wn + 32a + 8(j/4) + 4g + j%4.
   const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
+  for (int b = 0; b < WT; ++b) {
     const int m = m0 + wm + 32 * b + r;
     if (m >= M) continue;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < WT; ++a)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
@@ -476,13 +479,22 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
   constexpr bool is_bf16 = sizeof(T) == 2;
   const int64_t lim = int64_t(1) << 31;
   if (is_bf16 && trans_b && M > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) &&
-      aligned16(b) && (int64_t)GM * lda * 2 < lim && (int64_t)GN * ldb * 2 < lim) {
-    const int tiles_m = (M + GM - 1) / GM, tiles_n = (N + GN - 1) / GN;
+      aligned16(b) && (int64_t)g_tile(2) * lda * 2 < lim && (int64_t)g_tile(2) * ldb * 2 < lim) {
+    // 128-tiles when they fill the chip (256 CUs), else 64-tiles for 4x the workgroups.
+    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    const int wt = t128 >= 256 ? 2 : 1;
+    const int gt = g_tile(wt);
+    const int tiles_m = (M + gt - 1) / gt, tiles_n = (N + gt - 1) / gt;
     const int64_t nblk = (int64_t)tiles_m * tiles_n;
     KH_REQUIRE(nblk <= INT32_MAX, "kh_gemm: grid too large");
-    if constexpr (is_bf16)
-      gemm_bf16_nt_kernel<TO><<<(int)nblk, G_THREADS, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K,
-                                                                     alpha, beta, tiles_n);
+    if constexpr (is_bf16) {
+      if (wt == 2)
+        gemm_bf16_nt_kernel<TO, 2><<<(int)nblk, G_THREADS, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N,
+                                                                          K, alpha, beta, tiles_n);
+      else
+        gemm_bf16_nt_kernel<TO, 1><<<(int)nblk, G_THREADS, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N,
+                                                                          K, alpha, beta, tiles_n);
+    }
     KH_CHECK_LAUNCH();
     return KH_OK;
   }

@@ -118,6 +118,7 @@ class Qwen3ForCausalLM:
         self.rope = RotaryEmbedding(cfg.head_dim, cfg.rope_theta)
         self.cache = StaticKVCache(cfg.num_hidden_layers, 1, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
         self.scale = 1.0 / np.sqrt(cfg.head_dim)
+        self._prefill_graphs: Dict[int, tuple] = {}   # prompt length -> (graph, ids, positions, logits)
 
     # -- decoder body shared by the prefill and the device-resident decode step -------------------
     def _decoder(self, x: Tensor, S: int, positions: Tensor, attend) -> Tensor:
@@ -188,14 +189,11 @@ class Qwen3ForCausalLM:
         return logits
 
     # -- one forward over S new tokens at cache position `pos` -------------------------------------
-    def forward(self, input_ids: np.ndarray, pos: int) -> Tensor:
-        """Runs the decoder over input_ids (int32 [S]) appended at `pos`; returns fp32 logits of the
-        last position [1, vocab] (the only row greedy decoding reads)."""
-        S = int(len(input_ids))
-        end = self.cache.check_write(pos, S)
-        ids = Tensor(np.asarray(input_ids, np.int32), dtype="int32")
+    def _forward_dev(self, ids: Tensor, positions: Tensor, end: int) -> Tensor:
+        """Forward over the device token ids [S] at device positions [S] (cache rows), attending
+        over the first `end` cache rows; returns fp32 logits of the last position [1, vocab]."""
+        S = ids.shape[0]
         x = F.embedding(ids, self.embed, out_dtype="float32")     # [S, Hd] fp32 residual stream
-        positions = RotaryEmbedding.get_position_ids(S, pos)
 
         def attend(li, q_heads, out_view):
             kc, vc = self.cache.valid_slices(li, end)
@@ -205,10 +203,44 @@ class Qwen3ForCausalLM:
             vc.dispose()
 
         logits = self._decoder(x, S, positions, attend)
+        x.dispose()
+        return logits
+
+    def forward(self, input_ids: np.ndarray, pos: int) -> Tensor:
+        """Runs the decoder over input_ids (int32 [S]) appended at `pos`; returns fp32 logits of the
+        last position [1, vocab] (the only row greedy decoding reads)."""
+        S = int(len(input_ids))
+        end = self.cache.check_write(pos, S)
+        ids = Tensor(np.asarray(input_ids, np.int32), dtype="int32")
+        positions = RotaryEmbedding.get_position_ids(S, pos)
+        logits = self._forward_dev(ids, positions, end)
         self.cache.mark_written(end)
-        for t in (x, ids, positions):
+        for t in (ids, positions):
             t.dispose()
         return logits
+
+    def _prefill(self, prompt_ids: np.ndarray, use_graph: bool):
+        """(logits, owned) of the prompt at position 0.  With use_graph, the first prompt of a given
+        length runs eagerly and is then captured; later prompts of that length are copied into the
+        graph's device ids buffer and replayed (owned = False: the logits buffer is the graph's)."""
+        S = int(len(prompt_ids))
+        if not use_graph:
+            return self.forward(prompt_ids, 0), True
+        entry = self._prefill_graphs.get(S)
+        if entry is None:
+            logits = self.forward(prompt_ids, 0)
+            ids_buf = Tensor(np.zeros(S, np.int32), dtype="int32")
+            pos_buf = RotaryEmbedding.get_position_ids(S, 0)
+            graph = HipGraph()
+            with graph.capture():
+                g_logits = self._forward_dev(ids_buf, pos_buf, S)
+            self._prefill_graphs[S] = (graph, ids_buf, pos_buf, g_logits)
+            return logits, True
+        graph, ids_buf, _, g_logits = entry
+        ids_buf.handle.storage.upload(np.ascontiguousarray(prompt_ids, dtype=np.int32))
+        graph.replay()
+        self.cache.mark_written(S)
+        return g_logits, False
 
     # -- device-resident greedy decode step ---------------------------------------------------------
     def _decode_step(self, st: "DecodeState") -> Tensor:
@@ -250,13 +282,15 @@ class Qwen3ForCausalLM:
         self.cache.reset()
         self.cache.check_write(0, P + N)
         t0 = time.perf_counter()
-        logits = self.forward(prompt_ids, 0)
+        logits, owned = self._prefill(prompt_ids, use_graph)
         st = DecodeState.start(logits, P, N + 1, self.ops)
         if timing is not None:
             _lib.synchronize()
             timing["prefill_ms"] = (time.perf_counter() - t0) * 1e3
+            timing["prefill_issue"] = "eager" if owned else "hip graph replay"
         all_logits = [logits.numpy()[0]] if return_logits else []
-        logits.dispose()
+        if owned:
+            logits.dispose()
         graph, g_logits = None, None
         t1 = time.perf_counter()
         t_replay = None
@@ -296,6 +330,12 @@ class Qwen3ForCausalLM:
         return (toks, all_logits) if return_logits else toks
 
     def dispose(self) -> None:
+        for graph, ids_buf, pos_buf, g_logits in self._prefill_graphs.values():
+            g_logits.dispose()
+            graph.dispose()
+            ids_buf.dispose()
+            pos_buf.dispose()
+        self._prefill_graphs = {}
         self.cache.dispose()
         for t in [self.embed, self.final_norm] + [v for L in self.layers for v in L.values()]:
             t.dispose()

@@ -27,18 +27,20 @@ def _run(cfg, seed, prompt_len, steps, max_seq):
 
 
 def test_decode_graph_replays_match_eager(hip):
-    """The captured decode step, replayed with readbacks (host syncs) between replays, gives the
-    same logits bit for bit as the same step run eagerly, and the oracle's tokens."""
+    """The captured decode step, replayed with readbacks (host syncs) between replays, and the
+    captured prefill, replayed on a second generation, give the same logits bit for bit as the
+    same launches run eagerly, and the oracle's tokens."""
     cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
     w = init_qwen3_weights(cfg, seed=5)
     prompt = syn.randint(6, (40,), 0, cfg.vocab_size)
     model = Qwen3ForCausalLM(cfg, w, max_seq_len=64)
     etoks, elog = model.generate(prompt, 6, return_logits=True, use_graph=False)
-    gtoks, glog = model.generate(prompt, 6, return_logits=True, use_graph=True)
+    gtoks, glog = model.generate(prompt, 6, return_logits=True, use_graph=True)     # captures the prefill
+    g2toks, g2log = model.generate(prompt, 6, return_logits=True, use_graph=True)   # replays it
     model.dispose()
-    assert etoks == gtoks
-    for i, (a, b) in enumerate(zip(elog, glog)):
-        assert np.array_equal(a, b), i
+    assert etoks == gtoks == g2toks
+    for i, (a, b, c) in enumerate(zip(elog, glog, g2log)):
+        assert np.array_equal(a, b) and np.array_equal(a, c), i
     rtoks, _ = Qwen3Oracle(cfg, w, max_seq_len=64).generate(prompt, 6)
     assert gtoks == rtoks
 

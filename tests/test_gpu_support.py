@@ -91,7 +91,7 @@ def test_embedding_and_argmax(hip):
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 1024, 1024), (130, 200, 72), (8, 3000, 1024), (1, 151936, 1024),
-                                   (3, 100, 30), (600, 4096, 2048)])
+                                   (3, 100, 30), (600, 4096, 2048), (2048, 2048, 256), (1000, 4100, 136)])
 def test_linear_bf16(hip, M, N, K):
     x, xh = seeded(240, (M, K), "bfloat16")
     w, wh = seeded(241, (N, K), "bfloat16", std=0.02)
