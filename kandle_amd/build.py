@@ -32,6 +32,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions.  flash_prefill.hip is written NaN-free (masked scores are -inf, never NaN)
+# and assumes no NaNs so that its row maxima compile to plain v_max3 without canonicalisation.
+EXTRA_FLAGS = {"flash_prefill.hip": ["-fno-honor-nans"]}
+
+
 def _hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(exe):
@@ -40,7 +45,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless, filtered.
     noise = "'-packed-fp32-ops' is not a recognized feature"

@@ -6,21 +6,24 @@
 //
 // A workgroup of WAVES waves shares one kv head: wave w serves query head g = w / (WAVES/G) of the
 // G query heads that read this kv head (G = hq / hkv) and 32 query rows of a BMQ = 32 * WAVES / G row
-// block.  K/V tiles of BN keys are staged in LDS (double buffered) and shared by all waves.
+// block.  K/V tiles of BN keys (128 by default) are staged in LDS (double buffered, one barrier per
+// tile) and shared by all waves, which compute them in chunks of 64 keys.
 //
-// Per wave and tile, with v_mfma_f32_32x32x16_bf16:
+// Per wave and chunk, with v_mfma_f32_32x32x16_bf16:
 //   S^T (keys x queries) = K Q^T : A = K rows from LDS, B = Q held in registers for the whole loop.
-//   O^T (d x queries)   += V^T P^T: A = V^T rows from LDS (V is transposed when staged), B = P.
-// Each lane owns one query column: the row max / sum of the softmax are in-lane over BN/2 scores
+//   O^T (d x queries)   += V^T P^T: A = V^T fragments, B = P.
+// Each lane owns one query column: the row max / sum of the softmax are in-lane over 32 scores
 // plus one exchange with lane ^ 32.  K rows are stored in LDS in the order "swap bits 2 and 3 of
 // the key index", which makes S^T accumulator registers j = 0..7 of lane group g hold keys 8g + j
 // (j = 8..15: keys 16 + 8g + j - 8) -- exactly the B-operand layout of the PV product, so P never
 // leaves registers.
 //
-// Global loads are raw buffer loads (out-of-range rows read as zero without a branch); V^T rows are
-// stored with the 8-key block index XOR-swizzled by (d / 16) % 8 so that both the transposing
-// 4-byte writes and the 16-byte operand reads spread over all LDS banks.  The softmax uses a
-// thresholded reference max (see Softmax), so the O accumulators are rescaled on a few tiles only.
+// V is staged row-major like K and its V^T operand fragments are read with the gfx950 transposing
+// LDS read (ds_read_b64_tr_b16) at a per-lane base plus compile-time offsets.  (A variant stages V
+// transposed, with the 8-key block index XOR-swizzled by (d / 16) % 8 so that the transposing
+// 4-byte writes and the 16-byte operand reads spread over all LDS banks.)  Global loads are raw
+// buffer loads (out-of-range rows read as zero without a branch).  The softmax uses a thresholded
+// reference max (see Softmax), so the O accumulators are rescaled on a few tiles only.
 #include <cstdlib>
 
 #include "attention.h"
@@ -33,25 +36,42 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int FA_D = 128;
 constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
-template <int BN, int WAVES>
+// VTR: V is staged row-major (keys x d, like K) and the PV operand is read with the gfx950
+// transposing LDS read; otherwise V is staged transposed (d x keys).
+template <int BN, int WAVES, bool VTR = false>
 struct Cfg {
   static constexpr int THREADS = WAVES * 64;
-  static constexpr int VSTR = BN + 8;                // V^T row stride (elements)
+  // V row stride (elements).  Row-major: 288 B = 8 banks apart per row, so the 4 rows x 32 B that
+  // a 16-lane group of a transposing read touches cover 32 distinct banks.
+  static constexpr int VSTR = VTR ? FA_D + 16 : BN + 8;
   static constexpr int KTILE = BN * FA_KSTR;         // elements
-  static constexpr int VTILE = FA_D * VSTR;          // elements
+  static constexpr int VTILE = VTR ? BN * VSTR : FA_D * VSTR;  // elements
   static constexpr int NK = BN * 16 / THREADS;       // 16-byte K chunks per thread per tile
   static constexpr int PAIRS = THREADS / 16;         // V key pairs staged per pass
-  static constexpr int NVG = BN / (2 * PAIRS);       // V passes per tile
-  static constexpr int NSUB = BN / 32;               // 32-key S^T subtiles
+  static constexpr int NVG = BN / (2 * PAIRS);       // V passes per tile (transposed V)
+  // Compute works on 64-key chunks; a staged tile holds NCH of them (transposed V: one).
+  static constexpr int BNC = 64;
+  static constexpr int NCH = BN / BNC;
+  static constexpr int NSUB = BNC / 32;              // 32-key S^T subtiles per chunk
+  static_assert(BN % BNC == 0 && (VTR || NCH == 1), "multi-chunk tiles need row-major V");
   static_assert(NK >= 1 && NVG >= 1, "tile too small for the workgroup");
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+
+// gfx950 ds_read_b64_tr_b16: within each 16-lane group, element k of lane j is element (j & 3)
+// of the four bf16 at the address of lane 4k + (j >> 2).
+__device__ __forceinline__ v4i16 lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
+}
+
 // Shared per-workgroup setup and staging helpers.
-template <int BN, int WAVES>
+template <int BN, int WAVES, bool VTR = false>
 struct Flash {
-  using C = Cfg<BN, WAVES>;
+  using C = Cfg<BN, WAVES, VTR>;
   int G, BMQ, tid, wave, lane, r, g, b, hk, hqi, q0, qw0, qi, ntiles, wave_last_q, wave_tiles, dcol;
   __amdgpu_buffer_rsrc_t rk, rv;
   AttnStrides st;
@@ -78,8 +98,10 @@ struct Flash {
     qi = qw0 + r;
     const int kv_end = causal ? min(lk, q0 + BMQ) : lk;
     ntiles = (kv_end + BN - 1) / BN;
+    // wave_tiles counts 64-key compute chunks (C::BNC)
+    const int nchunks = (kv_end + C::BNC - 1) / C::BNC;
     wave_last_q = min(qw0 + 31, lq - 1);
-    wave_tiles = qw0 >= lq ? 0 : (causal ? min(ntiles, wave_last_q / BN + 1) : ntiles);
+    wave_tiles = qw0 >= lq ? 0 : (causal ? min(nchunks, wave_last_q / C::BNC + 1) : nchunks);
     rk = make_rsrc(K + b * s.kb + hk * s.kh, (uint32_t)(((int64_t)(lk - 1) * s.ks + FA_D) * 2));
     rv = make_rsrc(V + b * s.vb + hk * s.vh, (uint32_t)(((int64_t)(lk - 1) * s.vs + FA_D) * 2));
     dcol = 8 * (tid & 15);
@@ -103,6 +125,37 @@ struct Flash {
       const int key = t * BN + ((tid + C::THREADS * i) >> 4);
       kst[i] = buf_load16(rk, (uint32_t)(((int64_t)key * st.ks + dcol) * 2));
     }
+  }
+  // V row-major (VTR): the K chunk pattern, chunk id = tid + THREADS i -> key id / 16, d 8 (id % 16).
+  __device__ __forceinline__ void load_v_rows(int t, uint4 (&vst)[C::NK]) const {
+#pragma unroll
+    for (int i = 0; i < C::NK; ++i) {
+      const int key = t * BN + ((tid + C::THREADS * i) >> 4);
+      vst[i] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + dcol) * 2));
+    }
+  }
+  __device__ __forceinline__ void store_v_rows(uint16_t* vs, const uint4 (&vst)[C::NK]) const {
+#pragma unroll
+    for (int i = 0; i < C::NK; ++i)
+      *reinterpret_cast<uint4*>(vs + ((tid + C::THREADS * i) >> 4) * C::VSTR + dcol) = vst[i];
+  }
+  // O^T += V^T P^T with V row-major in LDS.  The A operand of chunk kc (lane: d = 32 dt + r, keys
+  // 16 kc + 8 g + e) is two transposing reads: lane l = 16 G + L supplies row 16 kc + 8 g + L / 4
+  // (+ 4 for the second read), columns 32 dt + 16 (G & 1) + 4 (L & 3) .. + 3 -- a per-lane base
+  // plus compile-time offsets.
+  __device__ __forceinline__ void pv_tr(const uint16_t* vs, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[4]) const {
+    const int L = lane & 15, Gq = lane >> 4;
+    const uint16_t* vbase = vs + (8 * (Gq >> 1) + (L >> 2)) * C::VSTR + 16 * (Gq & 1) + 4 * (L & 3);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 2 * C::NSUB; ++kc) {
+        const uint16_t* p0 = vbase + 16 * kc * C::VSTR + 32 * dt;
+        const v4i16 lo = lds_read_tr16(p0);
+        const v4i16 hi = lds_read_tr16(p0 + 4 * C::VSTR);
+        const v8i16 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, both), pk[kc], oacc[dt], 0, 0, 0);
+      }
   }
   // V: pass vg stages key pair p = tid / 16 + PAIRS vg (keys 2p, 2p + 1), d 8 * (tid % 16) .. + 8.
   __device__ __forceinline__ void load_v(int t, uint4 (&vst)[C::NVG][2]) const {
@@ -154,8 +207,8 @@ struct Flash {
   // Causal / length mask of tile t (only tiles crossing the diagonal or the sequence end).
   template <bool CAUSAL>
   __device__ __forceinline__ void mask(int t, int lk, f32x16 (&sc)[C::NSUB]) const {
-    const int kt = t * BN;
-    if ((kt + BN > lk) || (CAUSAL && kt + BN - 1 > qw0)) {
+    const int kt = t * C::BNC;  // t counts 64-key compute chunks
+    if ((kt + C::BNC > lk) || (CAUSAL && kt + C::BNC - 1 > qw0)) {
       const int lim = (CAUSAL ? min(lk, qi + 1) : lk) - kt - 8 * g;
 #pragma unroll
       for (int s = 0; s < C::NSUB; ++s)
@@ -223,11 +276,13 @@ struct Softmax {
 #pragma unroll
     for (int i = 1; i < NSUB * 4; ++i) mx = fmaxf(mx, m4[i]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // (-inf) - (-inf) is NaN, so a row with nothing unmasked yet never asks for a raise.
-    const bool need = (mx - m_ref) * c2 > kRescaleLog2;
+    // NaN-free by construction (this file is compiled assuming no NaNs, so that fmaxf needs no
+    // canonicalisation): a row with nothing unmasked (mx = -inf) never asks for a raise, and
+    // m_ref = -inf only before the first raise, where alpha = 2^-inf = 0 clears the empty O and l.
+    const bool need = mx != -INFINITY && (m_ref == -INFINITY || (mx - m_ref) * c2 > kRescaleLog2);
     if (__any(need)) {
-      const float m_new = fmaxf(m_ref, mx);
-      const float alpha = fast_exp2((m_ref - (m_new == -INFINITY ? 0.f : m_new)) * c2);
+      const float m_new = need ? fmaxf(m_ref, mx) : m_ref;
+      const float alpha = m_ref == -INFINITY ? 0.f : fast_exp2((m_ref - m_new) * c2);
       m_ref = m_new;
       l_run *= alpha;
 #pragma unroll
@@ -260,20 +315,29 @@ struct Softmax {
 // =============================================================================================
 // Tile-synchronous kernel.
 // =============================================================================================
-template <int BN, int WAVES, int MINB, bool CAUSAL>
+template <int BN, int WAVES, int MINB, bool CAUSAL, bool VTR = false>
 __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale,
     int n_qblocks) {
-  using C = Cfg<BN, WAVES>;
+  using C = Cfg<BN, WAVES, VTR>;
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
-  Flash<BN, WAVES> F;
+  Flash<BN, WAVES, VTR> F;
   F.init(batch, hq, hkv, lq, lk, st, CAUSAL, n_qblocks, K, V);
   bf16x8 qreg[8];
   F.load_q(Q, lq, qreg);
 
-  uint4 kst[C::NK], vst[C::NVG][2];
+  // V staging registers: row-major chunks (VTR) or transposing key pairs.
+  using VStage = std::conditional_t<VTR, uint4[C::NK], uint4[C::NVG][2]>;
+  uint4 kst[C::NK];
+  VStage vst;
+  auto load_v = [&](int t) {
+    if constexpr (VTR) F.load_v_rows(t, vst); else F.load_v(t, vst);
+  };
+  auto store_v = [&](uint16_t* vs) {
+    if constexpr (VTR) F.store_v_rows(vs, vst); else F.store_v(vs, vst);
+  };
   f32x16 oacc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -285,9 +349,9 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
 
   if (ntiles > 0) {
     F.load_k(0, kst);
-    F.load_v(0, vst);
+    load_v(0);
     F.store_k(smem, kst);
-    F.store_v(smem + C::KTILE, vst);
+    store_v(smem + C::KTILE);
   }
   // Retire every outstanding load (Q included) before the loop, so the compiler's wait counting
   // inside the loop only ever covers the next tile's prefetch and never stalls QK^T on it.
@@ -298,22 +362,29 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     const bool has_next = t + 1 < ntiles;
     if (has_next) {
       F.load_k(t + 1, kst);
-      F.load_v(t + 1, vst);
+      load_v(t + 1);
     }
     const uint16_t* ks = smem + (t & 1) * STAGE;
-    if (t < F.wave_tiles) {
-      f32x16 sacc[C::NSUB];
-      F.qk(ks, qreg, sacc);
-      F.template mask<CAUSAL>(t, lk, sacc);
-      sm.update(sacc, c2, oacc);
-      bf16x8 pk[2 * C::NSUB];
-      sm.exponentiate(sacc, c2, pk);
-      F.pv(ks + C::KTILE, pk, oacc);
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) {
+      const int tc = t * C::NCH + c;  // 64-key compute chunk
+      if (tc < F.wave_tiles) {
+        f32x16 sacc[C::NSUB];
+        F.qk(ks + c * C::BNC * FA_KSTR, qreg, sacc);
+        F.template mask<CAUSAL>(tc, lk, sacc);
+        sm.update(sacc, c2, oacc);
+        bf16x8 pk[2 * C::NSUB];
+        sm.exponentiate(sacc, c2, pk);
+        if constexpr (VTR)
+          F.pv_tr(ks + C::KTILE + c * C::BNC * C::VSTR, pk, oacc);
+        else
+          F.pv(ks + C::KTILE, pk, oacc);
+      }
     }
     if (has_next) {
       uint16_t* nxt = smem + ((t + 1) & 1) * STAGE;
       F.store_k(nxt, kst);
-      F.store_v(nxt + C::KTILE, vst);
+      store_v(nxt + C::KTILE);
     }
     __syncthreads();
   }
@@ -321,27 +392,28 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
 }
 
 int flash_variant() {
-  // 0: 8 waves, one workgroup per CU (default, fastest measured); 1: 4 waves, two workgroups per
-  // CU.  KANDLE_FLASH_VARIANT selects one for sweeps.
+  // 0: 128-key stages, row-major V read with transposing loads (default, fastest measured);
+  // 1: 64-key stages, V staged transposed; 2: 64-key stages, row-major V; 3: as 1 with 4 waves
+  // and two workgroups per CU.  KANDLE_FLASH_VARIANT selects one for sweeps.
   static int v = [] {
     const char* e = getenv("KANDLE_FLASH_VARIANT");
     const int x = e ? atoi(e) : 0;
-    return (x == 0 || x == 1) ? x : 0;
+    return (x >= 0 && x <= 3) ? x : 0;
   }();
   return v;
 }
 
-template <int BN, int WAVES, int MINB>
+template <int BN, int WAVES, int MINB, bool VTR = false>
 void launch_sync(bool causal, const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
                  int lq, int lk, const AttnStrides& st, float scale, int nqb, int nblk) {
   const uint16_t *Q = (const uint16_t*)q, *K = (const uint16_t*)k, *V = (const uint16_t*)v;
   uint16_t* O = (uint16_t*)o;
   if (causal)
-    flash_fwd_kernel<BN, WAVES, MINB, true><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
-                                                                              st, scale, nqb);
+    flash_fwd_kernel<BN, WAVES, MINB, true, VTR><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq,
+                                                                                   lk, st, scale, nqb);
   else
-    flash_fwd_kernel<BN, WAVES, MINB, false><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
-                                                                               st, scale, nqb);
+    flash_fwd_kernel<BN, WAVES, MINB, false, VTR><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq,
+                                                                                    lk, st, scale, nqb);
 }
 
 }  // namespace
@@ -367,14 +439,18 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
                               int lq, int lk, const AttnStrides& st, float scale, bool causal) {
   const int G = hq / hkv;
   const int var = flash_variant();
-  const int waves = var == 0 ? 8 : 4;
+  const int waves = var == 3 ? 4 : 8;
   const int BMQ = 32 * (waves / G);
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
   const int nblk = (int)nblk64;
   if (var == 0)
+    launch_sync<128, 8, 1, true>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
+  else if (var == 1)
     launch_sync<64, 8, 1>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
+  else if (var == 2)
+    launch_sync<64, 8, 1, true>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
   else
     launch_sync<64, 4, 2>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
   KH_CHECK_LAUNCH();
