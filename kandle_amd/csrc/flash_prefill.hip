@@ -33,6 +33,7 @@ using namespace kh;
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
 constexpr int FA_D = 128;
 constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
@@ -87,9 +88,16 @@ struct Flash {
     lane = tid & 63;
     r = lane & 31;
     g = lane >> 5;
-    // Heaviest (last) query blocks first for causal load balance; (b, kv head) fastest-varying.
-    const int bh = blockIdx.x % (batch * hkv);
-    const int qblk = n_qblocks - 1 - blockIdx.x / (batch * hkv);
+    // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCD i % 8), each XCD
+    // with its own L2.  Renumber so that XCD x runs a contiguous range of logical blocks, ordered
+    // (b, kv head)-major and, inside a head, heaviest (last) query block first: at any time an
+    // XCD's CUs work on one or two heads, whose K/V stay resident in its L2.
+    const int nblk = batch * hkv * n_qblocks;
+    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int base = nblk / kXcds, extra = nblk % kXcds;  // XCD x runs base + (x < extra) blocks
+    const int logical = xcd * base + min(xcd, extra) + j;
+    const int bh = logical / n_qblocks;
+    const int qblk = n_qblocks - 1 - logical % n_qblocks;
     b = bh / hkv;
     hk = bh % hkv;
     hqi = hk * G + wave / wpg;
@@ -431,7 +439,8 @@ bool flash_prefill_supported(const void* q, const void* k, const void* v, const 
   if (st.ob % 4 || st.oh % 4 || st.os % 4) return false;
   // Per-head byte offsets (including the zero-filled rows past the end) must fit 31 bits.
   const int64_t lim = int64_t(1) << 31;
-  if ((lq + 256) * st.qs * 2 >= lim || (lk + 256) * st.ks * 2 >= lim || (lk + 256) * st.vs * 2 >= lim) return false;
+  // (Tiles are prefetched up to two ahead: keys up to lk + 383 are addressed and read as zero.)
+  if ((lq + 512) * st.qs * 2 >= lim || (lk + 512) * st.ks * 2 >= lim || (lk + 512) * st.vs * 2 >= lim) return false;
   return true;
 }
 
