@@ -22,8 +22,12 @@ from . import bf16_round, from_bf16_bits, qk_norm_rope, rms_norm, rope_inv_freq
 
 
 class Qwen3Oracle:
-    def __init__(self, cfg, weights_bits, max_seq_len: int = 1024):
+    """exact=True drops the bf16 rounding points (every intermediate stays float32/float64): the
+    form checked against an independent float32 implementation of the architecture."""
+
+    def __init__(self, cfg, weights_bits, max_seq_len: int = 1024, exact: bool = False):
         self.cfg = cfg
+        self.r = (lambda a: np.asarray(a, np.float32)) if exact else bf16_round  # noqa: E731
         f = lambda n: from_bf16_bits(weights_bits[n])  # noqa: E731
         self.embed = f("model.embed_tokens.weight")
         self.final_norm = f("model.norm.weight")
@@ -68,26 +72,26 @@ class Qwen3Oracle:
         x = self.embed[np.asarray(ids)].astype(np.float32)                    # fp32 residual [S, Hd]
         positions = np.arange(pos, end, dtype=np.int32)
         for li, L in enumerate(self.layers):
-            h = bf16_round(rms_norm(x, L["in_norm"], eps))
-            q = bf16_round(h @ L["q"].T).reshape(S, Hq, D)
-            k = bf16_round(h @ L["k"].T).reshape(S, Hkv, D)
-            v = bf16_round(h @ L["v"].T).reshape(S, Hkv, D)
-            qh = bf16_round(qk_norm_rope(q, L["q_norm"], positions, self.inv_freq, eps)).transpose(1, 0, 2)
-            kh = bf16_round(qk_norm_rope(k, L["k_norm"], positions, self.inv_freq, eps)).transpose(1, 0, 2)
+            h = self.r(rms_norm(x, L["in_norm"], eps))
+            q = self.r(h @ L["q"].T).reshape(S, Hq, D)
+            k = self.r(h @ L["k"].T).reshape(S, Hkv, D)
+            v = self.r(h @ L["v"].T).reshape(S, Hkv, D)
+            qh = self.r(qk_norm_rope(q, L["q_norm"], positions, self.inv_freq, eps)).transpose(1, 0, 2)
+            kh = self.r(qk_norm_rope(k, L["k_norm"], positions, self.inv_freq, eps)).transpose(1, 0, 2)
             self.k_cache[li][:, pos:end] = kh
             self.v_cache[li][:, pos:end] = v.transpose(1, 0, 2)
             o = self._sdpa(qh, self.k_cache[li][:, :end], self.v_cache[li][:, :end], 1.0 / np.sqrt(D), S > 1)
-            o = bf16_round(o.transpose(1, 0, 2).reshape(S, Hq * D).astype(np.float32))
+            o = self.r(o.transpose(1, 0, 2).reshape(S, Hq * D).astype(np.float32))
             x = (x + (o @ L["o"].T)).astype(np.float32)
-            h = bf16_round(rms_norm(x, L["post_norm"], eps))
+            h = self.r(rms_norm(x, L["post_norm"], eps))
             g = h @ L["gate"].T
             u = h @ L["up"].T
-            g = bf16_round(g)
-            u = bf16_round(u)
+            g = self.r(g)
+            u = self.r(u)
             c = np.clip(g.astype(np.float64), -88.0, 88.0)
-            a = bf16_round((g / (1.0 + np.exp(-c)) * u).astype(np.float32))
+            a = self.r((g / (1.0 + np.exp(-c)) * u).astype(np.float32))
             x = (x + (a @ L["down"].T)).astype(np.float32)
-        xf = bf16_round(rms_norm(x[-1:], self.final_norm, eps))
+        xf = self.r(rms_norm(x[-1:], self.final_norm, eps))
         return (xf @ self.embed.T)[0].astype(np.float32)
 
     def generate(self, prompt_ids, max_new_tokens: int):

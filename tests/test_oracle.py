@@ -190,3 +190,24 @@ def test_argmax_tie_and_nan_rules():
     x = np.array([[1.0, 3.0, 3.0, 2.0], [np.nan, 1.0, np.nan, 0.5], [-np.inf, -np.inf, -np.inf, -np.inf]],
                  np.float32)
     assert list(oracle.argmax(x)) == [1, 1, 0]
+
+
+# ---------------------------------------------------------------------------------------- Qwen3 composition
+def test_qwen3_oracle_matches_transformers_float32():
+    """The model oracle without its bf16 rounding points reproduces Hugging Face transformers'
+    Qwen3ForCausalLM (float32) on a tiny config: prefill logits, then the logits after each greedy
+    token appended through the KV cache (tests/golden/make_qwen3_golden.py)."""
+    from kandle_amd.model_utils.qwen3 import Qwen3Config
+    from oracle.qwen3 import Qwen3Oracle
+
+    Z = np.load(Path(__file__).resolve().parent / "golden" / "qwen3_tiny.npz")
+    cfg = Qwen3Config(vocab_size=97, hidden_size=64, intermediate_size=96, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16, rms_norm_eps=1e-6, rope_theta=1e6)
+    weights = {k[2:]: Z[k] for k in Z.files if k.startswith("w:")}
+    ids, P = [int(i) for i in Z["ids"]], int(Z["prompt_len"])
+    ref = Qwen3Oracle(cfg, weights, max_seq_len=32, exact=True)
+    steps = len(ids) - P
+    toks, logits = ref.generate(ids[:P], steps + 1)
+    assert toks[:steps] == ids[P:]
+    for i in range(steps + 1):
+        np.testing.assert_allclose(logits[i], Z["logits"][i], rtol=0, atol=2e-4 * np.abs(Z["logits"][i]).max())
