@@ -102,19 +102,14 @@ __device__ __forceinline__ int decode_len(const int32_t* lens, int uniform_len, 
   return L < 0 ? 0 : (L > max_len ? max_len : L);
 }
 
-// Chunk counts up to which the last chunk's block merges the partials itself.
-constexpr int kFusedMergeChunks = 8;
-
 template <typename T, int G>
 __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                              const T* __restrict__ V, const int32_t* __restrict__ lens,
                                                              int uniform_len, int max_len, int hq, int hkv,
                                                              AttnStrides st, float scale, int max_chunks,
-                                                             float* __restrict__ part, uint32_t* counters,
-                                                             T* __restrict__ O) {
-  // Layout of `part`: [b][hq][max_chunks][2 + 128] floats (m, l, o[0..127]), valid chunks only.
-  // With `counters`, the block that finishes a (b, kv head)'s last chunk merges its partials into
-  // O (see below); without, decode_merge_kernel does it in a second launch.
+                                                             float* __restrict__ part) {
+  // Layout of `part`: [b][hq][max_chunks][2 + 128] floats (m, l, o[0..127]), valid chunks only;
+  // decode_merge_kernel combines them.
   constexpr int D = 128;
   constexpr int EPL = 16 / (int)sizeof(T);            // elements per 16-byte load
   constexpr int LPK = D / EPL;                        // lanes per key row (16 bf16, 32 f32)
@@ -130,10 +125,6 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
   const int L = decode_len(lens, uniform_len, b, max_len);
-  if (L == 0 && counters != nullptr && chunk == 0) {  // empty cache: the output is zero
-    for (int t = threadIdx.x; t < G * D; t += blockDim.x)
-      Elem<T>::store(O + b * st.ob + (int64_t)(hk * G + t / D) * st.oh, t % D, 0.f);
-  }
   if (chunk * CHUNK >= L) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int sub = lane % LPK;          // 16-byte column inside the row
@@ -253,48 +244,6 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
     }
     pp[2 + d] = Os;
   }
-  if (counters == nullptr) return;
-
-  // Count this chunk for (b, hk); the block that brings the count to nch merges.  Release: every
-  // thread's partial stores are made device-visible before thread 0 counts; acquire: the merging
-  // block fences again before it reads the other chunks' partials.
-  __shared__ uint32_t s_ticket;
-  __threadfence();
-  __syncthreads();
-  uint32_t* cnt = counters + (int64_t)b * hkv + hk;
-  if (threadIdx.x == 0) s_ticket = atomicAdd(cnt, 1u);
-  __syncthreads();
-  const int nch = (L + CHUNK - 1) / CHUNK;
-  if (s_ticket != (uint32_t)(nch - 1)) return;
-  __threadfence();
-  // nch <= kFusedMergeChunks (the host only passes counters then): every partial of a column is
-  // loaded in one round trip.
-  for (int t = threadIdx.x; t < G * D; t += blockDim.x) {
-    const int gi = t / D, d = t % D;
-    const float* pp = part + ((int64_t)b * hq + hk * G + gi) * max_chunks * (2 + D);
-    float mc[kFusedMergeChunks], lc[kFusedMergeChunks], oc[kFusedMergeChunks];
-#pragma unroll
-    for (int c = 0; c < kFusedMergeChunks; ++c) {
-      const bool in = c < nch;
-      const float* pc = pp + (int64_t)(in ? c : 0) * (2 + D);
-      mc[c] = in ? pc[0] : -INFINITY;
-      lc[c] = in ? pc[1] : 0.f;
-      oc[c] = in ? pc[2 + d] : 0.f;
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < kFusedMergeChunks; ++c) M = fmaxf(M, mc[c]);
-    const float mu = M == -INFINITY ? 0.f : M;
-    float Ls = 0.f, Os = 0.f;
-#pragma unroll
-    for (int c = 0; c < kFusedMergeChunks; ++c) {
-      const float f = c < nch ? __expf(mc[c] - mu) : 0.f;
-      Ls += lc[c] * f;
-      Os += oc[c] * f;
-    }
-    Elem<T>::store(O + b * st.ob + (int64_t)(hk * G + gi) * st.oh, d, Ls > 0.f ? Os / Ls : 0.f);
-  }
-  if (threadIdx.x == 0) atomicExch(cnt, 0u);  // back to zero for the next launch
 }
 
 // Merge of one (b, query head): 256 threads.  The chunk maxima and weighted denominators are
@@ -378,13 +327,10 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   const T* Q = (const T*)q;
   const T* K = (const T*)k;
   const T* V = (const T*)v;
-  // Short caches (few chunks): one launch, the last chunk's block merges.  Long ones: partials,
-  // then the parallel merge kernel (a single block walking many chunks would be the tail).
-  uint32_t* counters = max_chunks <= kFusedMergeChunks ? zeroed_counters((size_t)batch * hkv) : nullptr;
 #define KH_DECODE_CASE(GG)                                                                               \
   case GG:                                                                                               \
     decode_partial_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st, \
-                                                              scale, max_chunks, part, counters, (T*)o); \
+                                                              scale, max_chunks, part);                  \
     break;
   switch (G) {
     KH_DECODE_CASE(1)
@@ -394,7 +340,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   }
 #undef KH_DECODE_CASE
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess && counters == nullptr) {
+  if (e == hipSuccess) {
     decode_merge_kernel<T><<<dim3(hq, batch), 256, 0, stream()>>>(part, lens, uniform_len, ml, hq, max_chunks, st,
                                                                   (T*)o);
     e = hipGetLastError();

@@ -18,11 +18,6 @@ bool initialized();
 void* scratch_alloc(size_t bytes);
 void scratch_free(void* p);
 
-// A library-owned array of at least n uint32 counters, all zero whenever no kernel is running:
-// a kernel that counts in it must return every counter it touched to zero before it exits.
-// nullptr if n exceeds the array (allocated and cleared once, in kh_init).
-uint32_t* zeroed_counters(size_t n);
-
 #define KH_CHECK_HIP(expr)                                                              \
   do {                                                                                  \
     hipError_t _e = (expr);                                                             \

@@ -46,48 +46,57 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 }
 
 // =============================================================================================
-// MFMA tile kernel.  Workgroup tile (64 WT) x (64 WT), k-step 64, 4 waves in a 2 x 2 layout, each
+// MFMA tile kernel.  Workgroup tile (64 WT) x (64 WT), k-step KS, 4 waves in a 2 x 2 layout, each
 // wave (32 WT) x (32 WT) = WT x WT tiles of 32 x 32: WT = 2 (128 x 128) for large problems, WT = 1
-// (64 x 64) when 128-tiles would leave CUs idle.  The product is formed as C^T = B A^T so that each
-// lane owns one m row and 4 consecutive n per register group: A-operand = B rows (n), B-operand =
-// A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are raw
-// buffer loads (rows past M / N and columns past K read as zero without a branch).
+// (64 x 64, k-step 128) when 128-tiles would leave CUs idle.  The product is formed as C^T = B A^T
+// so that each lane owns one m row and 4 consecutive n per register group: A-operand = B rows (n),
+// B-operand = A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are
+// raw buffer loads (rows past M / N and columns past the k range read as zero without a branch).
+//
+// SPLIT: S workgroups share one output tile, each summing K / S of the products.  Each writes its
+// fp32 accumulators to a workspace and counts itself in a library counter; the last one adds the S
+// partials in split order (deterministic whichever finishes last), applies the epilogue and resets
+// the counter to zero.
 // =============================================================================================
-constexpr int GK = 64;
 constexpr int G_THREADS = 256;
-constexpr int G_STR = GK + 8;  // LDS row stride (elements), keeps 16-byte alignment, breaks bank aliasing
+constexpr int kMaxSplits = 8;
 constexpr int g_tile(int wt) { return 64 * wt; }
 
-template <typename TO, int WT>
+template <typename TO, int WT, int KS, bool SPLIT>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
-    int tiles_n) {
+    int tiles_n, int splits, int kchunk, float* __restrict__ part) {
   constexpr int GM = g_tile(WT), GN = g_tile(WT);
-  constexpr int ATILE = GM * G_STR, BTILE = GN * G_STR;
-  constexpr int CPT = GM * (GK / 8) / G_THREADS;  // 16-byte chunks per thread per tile
+  constexpr int STR = KS + 8;  // LDS row stride (elements): 16-byte aligned, breaks bank aliasing
+  constexpr int ATILE = GM * STR, BTILE = GN * STR;
+  constexpr int CPR = KS / 8;                      // 16-byte chunks per row per k-step
+  constexpr int CPT = GM * CPR / G_THREADS;        // chunks per thread per tile
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ATILE + BTILE)];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, g = lane >> 5;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int tile = SPLIT ? blockIdx.x / splits : blockIdx.x;
+  const int split = SPLIT ? blockIdx.x % splits : 0;
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int m0 = tm * GM, n0 = tn * GN;
   const int wm = (wave >> 1) * 32 * WT, wn = (wave & 1) * 32 * WT;
+  const int kbeg = split * kchunk, kend = min(K, kbeg + kchunk);
 
-  // Byte ranges of this tile's rows; a row past the matrix or a column past K reads zero.
+  // Byte ranges of this tile's rows; a row past the matrix or a column past the range reads zero.
   const int mrows = min(GM, M - m0), nrows = min(GN, N - n0);
   const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * 2));
   const auto rb = make_rsrc(B + (int64_t)n0 * ldb, (uint32_t)(((int64_t)(nrows - 1) * ldb + K) * 2));
 
-  // Staging: each of the A and B tiles is GM rows x 64 k = GM * 8 chunks of 16 B, CPT per thread.
+  // Staging: each of the A and B tiles is GM rows x KS k = GM * CPR chunks of 16 B, CPT per thread.
   uint4 ast[CPT], bst[CPT];
   auto load_tile = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + G_THREADS * i;
-      const int row = id >> 3, kc = kt + 8 * (id & 7);
-      // Columns >= K map past the range (K % 8 == 0, so a chunk is all in or all out).
-      const int64_t ao = kc < K ? (int64_t)row * lda + kc : (int64_t)1 << 40;
-      const int64_t bo = kc < K ? (int64_t)row * ldb + kc : (int64_t)1 << 40;
+      const int row = id / CPR, kc = kt + 8 * (id % CPR);
+      // Columns past kend map past the range (K % 8 == 0, so a chunk is all in or all out).
+      const int64_t ao = kc < kend ? (int64_t)row * lda + kc : (int64_t)1 << 40;
+      const int64_t bo = kc < kend ? (int64_t)row * ldb + kc : (int64_t)1 << 40;
       ast[i] = buf_load16(ra, (uint32_t)min<int64_t>(ao * 2, 0xffffffffLL));
       bst[i] = buf_load16(rb, (uint32_t)min<int64_t>(bo * 2, 0xffffffffLL));
     }
@@ -98,9 +107,9 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + G_THREADS * i;
-      const int row = id >> 3, kc = 8 * (id & 7);
-      *reinterpret_cast<uint4*>(as + row * G_STR + kc) = ast[i];
-      *reinterpret_cast<uint4*>(bs + row * G_STR + kc) = bst[i];
+      const int row = id / CPR, kc = 8 * (id % CPR);
+      *reinterpret_cast<uint4*>(as + row * STR + kc) = ast[i];
+      *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[i];
     }
   };
 
@@ -112,24 +121,26 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
 
-  const int nk = (K + GK - 1) / GK;
-  load_tile(0);
-  store_tile(0);
+  const int nk = kend > kbeg ? (kend - kbeg + KS - 1) / KS : 0;
+  if (nk > 0) {
+    load_tile(kbeg);
+    store_tile(0);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int t = 0; t < nk; ++t) {
     const int buf = t & 1;
     const bool has_next = t + 1 < nk;
-    if (has_next) load_tile((t + 1) * GK);
+    if (has_next) load_tile(kbeg + (t + 1) * KS);
     const uint16_t* as = smem + buf * (ATILE + BTILE);
     const uint16_t* bs = as + ATILE;
 #pragma unroll
-    for (int kc = 0; kc < GK / 16; ++kc) {
+    for (int kc = 0; kc < KS / 16; ++kc) {
       bf16x8 av[WT], bv[WT];
 #pragma unroll
       for (int i = 0; i < WT; ++i) {
-        av[i] = as_bf16x8(*reinterpret_cast<const uint4*>(as + (wm + 32 * i + r) * G_STR + 16 * kc + 8 * g));
-        bv[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn + 32 * i + r) * G_STR + 16 * kc + 8 * g));
+        av[i] = as_bf16x8(*reinterpret_cast<const uint4*>(as + (wm + 32 * i + r) * STR + 16 * kc + 8 * g));
+        bv[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn + 32 * i + r) * STR + 16 * kc + 8 * g));
       }
 #pragma unroll
       for (int a = 0; a < WT; ++a)
@@ -139,6 +150,23 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     }
     if (has_next) store_tile(buf ^ 1);
     __syncthreads();
+  }
+
+  if constexpr (SPLIT) {
+    // Raw fp32 partial of this split: part[tile][split][m - m0][n - n0]; the reduction kernel adds
+    // the splits in order and applies the epilogue.
+    float* mine = part + ((int64_t)tile * splits + split) * (GM * GN);
+#pragma unroll
+    for (int b = 0; b < WT; ++b)
+#pragma unroll
+      for (int a = 0; a < WT; ++a)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int ml = wm + 32 * b + r, nl = wn + 32 * a + 8 * q + 4 * g;
+          *reinterpret_cast<float4*>(mine + ml * GN + nl) =
+              make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+        }
+    return;
   }
 
   // Epilogue: acc[a][b] lane holds m = m0 + wm + 32b + r, n = n0 + wn + 32a + 8(j/4) + 4g + j%4.
@@ -159,6 +187,41 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
           v[e] = (n + e < N) ? epilogue<TO>(acc[a][b][4 * q + e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
         store4<TO>(C, (int64_t)m * ldc + n, v, vec, min(4, N - n));
       }
+  }
+}
+
+// Split-K reduction: one workgroup per output tile, four consecutive outputs per thread and step;
+// all splits' partials are loaded before they are added (in split order), then the epilogue.
+template <typename TO, int GT>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                  TO* C, int64_t ldc, const TO* cin, int64_t ldcin,
+                                                                  const TO* __restrict__ bias, int M, int N,
+                                                                  float alpha, float beta, int tiles_n) {
+  const int tile = blockIdx.x;
+  const int m0 = (tile / tiles_n) * GT, n0 = (tile % tiles_n) * GT;
+  const float* tp = part + (int64_t)tile * splits * (GT * GT);
+  const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
+  for (int idx = threadIdx.x * 4; idx < GT * GT; idx += blockDim.x * 4) {
+    const int ml = idx / GT, nl = idx % GT;
+    const int m = m0 + ml, n = n0 + nl;
+    float4 pv[kMaxSplits];
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxSplits; ++s2)
+      pv[s2] = s2 < splits ? *reinterpret_cast<const float4*>(tp + (int64_t)s2 * (GT * GT) + idx)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxSplits; ++s2) {
+      v[0] += pv[s2].x;
+      v[1] += pv[s2].y;
+      v[2] += pv[s2].z;
+      v[3] += pv[s2].w;
+    }
+    if (m >= M || n >= N) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = (n + e < N) ? epilogue<TO>(v[e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
+    store4<TO>(C, (int64_t)m * ldc + n, v, vec, min(4, N - n));
   }
 }
 
@@ -480,21 +543,52 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
   const int64_t lim = int64_t(1) << 31;
   if (is_bf16 && trans_b && M > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) &&
       aligned16(b) && (int64_t)g_tile(2) * lda * 2 < lim && (int64_t)g_tile(2) * ldb * 2 < lim) {
-    // 128-tiles when they fill the chip (256 CUs), else 64-tiles for 4x the workgroups.
+    // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the
+    // workgroups, and when even those leave CUs idle and K is long, split K over up to 8 workgroups.
     const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
     const int wt = t128 >= 256 ? 2 : 1;
     const int gt = g_tile(wt);
     const int tiles_m = (M + gt - 1) / gt, tiles_n = (N + gt - 1) / gt;
-    const int64_t nblk = (int64_t)tiles_m * tiles_n;
-    KH_REQUIRE(nblk <= INT32_MAX, "kh_gemm: grid too large");
-    if constexpr (is_bf16) {
-      if (wt == 2)
-        gemm_bf16_nt_kernel<TO, 2><<<(int)nblk, G_THREADS, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N,
-                                                                          K, alpha, beta, tiles_n);
-      else
-        gemm_bf16_nt_kernel<TO, 1><<<(int)nblk, G_THREADS, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N,
-                                                                          K, alpha, beta, tiles_n);
+    const int64_t tiles = (int64_t)tiles_m * tiles_n;
+    KH_REQUIRE(tiles <= INT32_MAX / 8, "kh_gemm: grid too large");
+    int splits = 1;
+    if (wt == 1 && tiles < 256 && K >= 1024) {
+      const int64_t want = 512 / tiles;
+      splits = want < 1 ? 1 : (want > kMaxSplits ? kMaxSplits : (int)want);
     }
+    int kchunk = K;
+    float* part = nullptr;
+    if (splits > 1) {
+      kchunk = ((K + splits - 1) / splits + 127) / 128 * 128;
+      splits = (K + kchunk - 1) / kchunk;
+      part = (float*)scratch_alloc((size_t)splits * tiles * gt * gt * sizeof(float));
+      if (!part) {
+        splits = 1;
+        kchunk = K;
+      }
+    }
+    // k-step 128 doubles the bytes per round trip but also the LDS per workgroup (70 KB: two per
+    // CU); with more than two tiles per CU the 64 k-step's occupancy (four per CU) wins.
+    const bool ks128 = tiles * splits <= 512;
+    const int nblk = (int)(tiles * splits);
+    if constexpr (is_bf16) {
+      if (wt == 2) {
+        gemm_bf16_nt_kernel<TO, 2, 64, false><<<nblk, G_THREADS, 0, stream()>>>(
+            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
+      } else if (splits > 1) {
+        gemm_bf16_nt_kernel<TO, 1, 128, true><<<nblk, G_THREADS, 0, stream()>>>(
+            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
+        gemm_splitk_reduce_kernel<TO, 64><<<(int)tiles, 256, 0, stream()>>>(part, splits, C, ldc, CI, ldcin, BI, M,
+                                                                            N, alpha, beta, tiles_n);
+      } else if (ks128) {
+        gemm_bf16_nt_kernel<TO, 1, 128, false><<<nblk, G_THREADS, 0, stream()>>>(
+            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
+      } else {
+        gemm_bf16_nt_kernel<TO, 1, 64, false><<<nblk, G_THREADS, 0, stream()>>>(
+            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
+      }
+    }
+    if (part) scratch_free(part);  // stream-ordered reuse only
     KH_CHECK_LAUNCH();
     return KH_OK;
   }

@@ -26,9 +26,7 @@ struct State {
   int device = -1;
   hipStream_t stream = nullptr;
   GraphObj* capturing = nullptr;  // graph whose stream capture is open
-  uint32_t* counters = nullptr;   // zeroed_counters() array
 };
-constexpr size_t kCounterCap = 65536;
 State g_state;
 
 // Size classes: requests up to 1 MiB round to 512 B, larger ones to 2 MiB.
@@ -188,8 +186,6 @@ void* scratch_alloc(size_t bytes) {
 }
 void scratch_free(void* p) { (void)g_alloc.free(p); }
 
-uint32_t* zeroed_counters(size_t n) { return n <= kCounterCap ? g_state.counters : nullptr; }
-
 }  // namespace kh
 
 using namespace kh;
@@ -225,9 +221,6 @@ int kh_init(int device) {
   }
   KH_CHECK_HIP(hipSetDevice(device));
   KH_CHECK_HIP(hipStreamCreateWithFlags(&g_state.stream, hipStreamNonBlocking));
-  KH_CHECK_HIP(hipMalloc(&g_state.counters, kCounterCap * sizeof(uint32_t)));
-  KH_CHECK_HIP(hipMemset(g_state.counters, 0, kCounterCap * sizeof(uint32_t)));  // once, outside any graph
-  KH_CHECK_HIP(hipDeviceSynchronize());
   g_state.device = device;
   g_state.init = true;
   return KH_OK;

@@ -118,10 +118,9 @@ def test_decode_varlen_matches_oracle(hip):
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(16, 8), (16, 2)])
-def test_decode_single_launch_merge(hip, Hq, Hkv):
-    """Caches of at most 8 chunks merge in the decode launch itself (the last chunk's block, via a
-    counter it returns to zero): varlen including an empty and a one-key sequence, and three
-    launches in a row giving identical results (the counters start at zero every time)."""
+def test_decode_short_caches_repeatable(hip, Hq, Hkv):
+    """Short varlen caches (at most 8 chunks) including an empty and a one-key sequence, GQA 2 and
+    8, three launches in a row giving identical results (the empty one yields zeros)."""
     B, D, ML = 5, 128, 2048
     lens = np.array([0, 1, 256, 700, 2048], np.int32)
     q, qh = seeded(74, (B, Hq, D), "bfloat16")

@@ -102,6 +102,25 @@ def test_linear_bf16(hip, M, N, K):
     assert np.all(err <= 2 ** -8 * np.abs(ref) + 1e-4 * np.sqrt(K) * 0.02 * 4), float(err.max())
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 3072), (100, 520, 2048)])
+def test_linear_split_k_residual_deterministic(hip, M, N, K):
+    """Few output tiles and a long K: workgroups split K and the last one of each tile adds the
+    partials in a fixed order -- fp32 output with the residual added in place, and bit-identical
+    results when run twice."""
+    x, xh = seeded(245, (M, K), "bfloat16")
+    w, wh = seeded(246, (N, K), "bfloat16", std=0.02)
+    r0 = syn.normal(247, (M, N))
+    outs = []
+    for _ in range(2):
+        r = Tensor(r0.copy())
+        F.dispatch_matmul(x, w, c=r, beta=1.0, out=r, transpose_b=True)
+        outs.append(r.numpy())
+        r.dispose()
+    assert np.array_equal(outs[0], outs[1])
+    ref = oracle.linear(xh, wh) + r0
+    assert max_rel(outs[0], ref) < 1e-4
+
+
 def test_linear_fp32_bias_and_residual_epilogue(hip):
     x, xh = seeded(250, (33, 96))
     w, wh = seeded(251, (40, 96))
