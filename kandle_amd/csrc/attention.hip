@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
                                                              AttnStrides st, float scale, int max_chunks,
                                                              float* __restrict__ part) {
   // Layout of `part`: [b][hq][max_chunks][2 + 128] floats (m, l, o[0..127]), valid chunks only;
-  // decode_merge_kernel combines them.
+  // decode_merge_cols_kernel combines them.
   constexpr int D = 128;
   constexpr int EPL = 16 / (int)sizeof(T);            // elements per 16-byte load
   constexpr int LPK = D / EPL;                        // lanes per key row (16 bf16, 32 f32)
@@ -246,57 +246,209 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
   }
 }
 
-// Merge of one (b, query head): 256 threads.  The chunk maxima and weighted denominators are
-// reduced block-wide first; then two groups of 128 threads (one per output column) each sum half
-// of the chunks' rescaled partial outputs, unrolled so several partial rows are in flight.
+// ---- bf16 decode partials with in-row DPP reductions ------------------------------------------
+// gfx9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2), row_half_mirror
+// (lane i <-> 7 - i in each group of 8), row_mirror (lane i <-> 15 - i in each row of 16).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the 16 lanes of a DPP row; every lane of the row receives it.  VALU only (no LDS).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return v;
+}
+
+// Same unit of work and output as decode_partial_kernel, for bf16: the 16 lanes of a DPP row hold
+// one key row (8 columns each), so a score is an in-lane dot product plus a 4-step DPP row sum, and
+// the 4 rows of a wave (key slots kk) keep separate softmax states (m, l, o) -- no cross-row
+// shuffles.  The 16 states of the workgroup (4 waves x 4 rows) are combined once through LDS.
+template <int G>
+__global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t* __restrict__ Q,
+                                                                  const uint16_t* __restrict__ K,
+                                                                  const uint16_t* __restrict__ V,
+                                                                  const int32_t* __restrict__ lens, int uniform_len,
+                                                                  int max_len, int hq, int hkv, AttnStrides st,
+                                                                  float scale, int max_chunks,
+                                                                  float* __restrict__ part) {
+  constexpr int D = 128, NI = 16, KPI = 4, KPW = NI * KPI, CHUNK = DC_WAVES * KPW, NS = DC_WAVES * KPI;
+  static_assert(CHUNK == dc_chunk<uint16_t>(), "chunk size shared with the merge");
+  __shared__ float red_m[NS][G];
+  __shared__ float red_l[NS][G];
+  __shared__ float red_o[NS][G][D];
+
+  const int chunk = blockIdx.x;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const int L = decode_len(lens, uniform_len, b, max_len);
+  if (chunk * CHUNK >= L) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int sub = lane & 15;  // 16-byte column of the key row
+  const int kk = lane >> 4;   // key slot (DPP row) inside a load instruction
+  const int key0 = chunk * CHUNK + w * KPW;
+
+  float qv[G][8];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    const uint4 u = *reinterpret_cast<const uint4*>(Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * 8);
+    const uint32_t wq[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      qv[gi][2 * e] = lo_bf16(wq[e]) * scale;
+      qv[gi][2 * e + 1] = hi_bf16(wq[e]) * scale;
+    }
+  }
+  // Byte ranges end at the sequence length: keys >= L read as zero.
+  const auto rk = make_rsrc(K + b * st.kb + hk * st.kh, (uint32_t)(((int64_t)(L - 1) * st.ks + D) * 2));
+  const auto rv = make_rsrc(V + b * st.vb + hk * st.vh, (uint32_t)(((int64_t)(L - 1) * st.vs + D) * 2));
+  uint4 kr[NI], vr[NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int key = key0 + it * KPI + kk;
+    kr[it] = buf_load16(rk, (uint32_t)(((int64_t)key * st.ks + sub * 8) * 2));
+  }
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int key = key0 + it * KPI + kk;
+    vr[it] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + sub * 8) * 2));
+  }
+
+  float sc[G][NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const uint32_t wk[4] = {kr[it].x, kr[it].y, kr[it].z, kr[it].w};
+    const bool valid = key0 + it * KPI + kk < L;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d += qv[gi][2 * e] * lo_bf16(wk[e]);
+        d += qv[gi][2 * e + 1] * hi_bf16(wk[e]);
+      }
+      d = row16_sum(d);
+      sc[gi][it] = valid ? d : -INFINITY;
+    }
+  }
+  const int s_id = w * KPI + kk;
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    float mx = sc[gi][0];
+#pragma unroll
+    for (int it = 1; it < NI; ++it) mx = fmaxf(mx, sc[gi][it]);
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float ls = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const float p = __expf(sc[gi][it] - mu);
+      ls += p;
+      const uint32_t wv[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[2 * e] += p * lo_bf16(wv[e]);
+        o[2 * e + 1] += p * hi_bf16(wv[e]);
+      }
+    }
+    if (sub == 0) {
+      red_m[s_id][gi] = mx;
+      red_l[s_id][gi] = ls;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red_o[s_id][gi][sub * 8 + e] = o[e];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < G * D; t += blockDim.x) {
+    const int gi = t / D, d = t % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) M = fmaxf(M, red_m[s2][gi]);
+    const float mu = M == -INFINITY ? 0.f : M;
+    float Ls = 0.f, Os = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+      const float f = __expf(red_m[s2][gi] - mu);
+      Ls += red_l[s2][gi] * f;
+      Os += red_o[s2][gi][d] * f;
+    }
+    float* pp = part + (((int64_t)b * hq + hk * G + gi) * max_chunks + chunk) * (2 + D);
+    if (d == 0) {
+      pp[0] = M;
+      pp[1] = Ls;
+    }
+    pp[2 + d] = Os;
+  }
+}
+
+// Merge by column groups: workgroup (cg, h, b) produces columns 32 cg .. 32 cg + 31 of query head
+// h.  8 groups of 32 threads (one per column) each run one online log-sum-exp pass over every 8th
+// chunk (running max, denominator and column sum, rescaled when the max grows; four chunks' loads in
+// flight), and the 8 group states are combined through LDS.
 template <typename T>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part,
-                                                           const int32_t* __restrict__ lens, int uniform_len,
-                                                           int max_len, int hq, int max_chunks, AttnStrides st,
-                                                           T* __restrict__ O) {
-  constexpr int D = 128;
-  constexpr int ROW = 2 + D;
-  __shared__ float red[8];
-  __shared__ float osum[D];
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+__global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __restrict__ part,
+                                                                const int32_t* __restrict__ lens, int uniform_len,
+                                                                int max_len, int hq, int max_chunks, AttnStrides st,
+                                                                T* __restrict__ O) {
+  constexpr int D = 128, ROW = 2 + D, COLS = 32, NG = 8;
+  __shared__ float gm[NG], gl[NG];
+  __shared__ float gacc[NG][COLS];
+  const int cg = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int col = tid & (COLS - 1), grp = tid >> 5;
+  const int d = cg * COLS + col;
   const int L = decode_len(lens, uniform_len, b, max_len);
   const int nch = (L + dc_chunk<T>() - 1) / dc_chunk<T>();
   const float* pp = part + ((int64_t)b * hq + h) * max_chunks * ROW;
 
-  float mloc = -INFINITY;
-  for (int c = tid; c < nch; c += 256) mloc = fmaxf(mloc, pp[(int64_t)c * ROW]);
-  mloc = wave_max(mloc);
-  if (lane == 0) red[w] = mloc;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float mu = M == -INFINITY ? 0.f : M;
-  float lloc = 0.f;
-  for (int c = tid; c < nch; c += 256) lloc += pp[(int64_t)c * ROW + 1] * __expf(pp[(int64_t)c * ROW] - mu);
-  lloc = wave_sum(lloc);
-  __syncthreads();
-  if (lane == 0) red[4 + w] = lloc;
-  __syncthreads();
-  const float Ls = red[4] + red[5] + red[6] + red[7];
-
-  const int grp = tid >> 7, d = tid & 127;
-  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+  float m = -INFINITY, l = 0.f, acc = 0.f;
+  // Fold chunk (mc, lc, oc) into the running state.
+  auto fold = [&](float mc, float lc, float oc) {
+    const float mn = fmaxf(m, mc);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float a = __expf(m - mu), p = __expf(mc - mu);
+    l = l * a + lc * p;
+    acc = acc * a + oc * p;
+    m = mn;
+  };
   int c = grp;
-  for (; c + 6 < nch; c += 8) {
-    const float* p0 = pp + (int64_t)c * ROW;
-    const float* p1 = p0 + 2 * ROW;
-    const float* p2 = p0 + 4 * ROW;
-    const float* p3 = p0 + 6 * ROW;
-    acc0 += __expf(p0[0] - mu) * p0[2 + d];
-    acc1 += __expf(p1[0] - mu) * p1[2 + d];
-    acc2 += __expf(p2[0] - mu) * p2[2 + d];
-    acc3 += __expf(p3[0] - mu) * p3[2 + d];
+  for (; c + 3 * NG < nch; c += 4 * NG) {
+    float mc[4], lc[4], oc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* pc = pp + (int64_t)(c + u * NG) * ROW;
+      mc[u] = pc[0];
+      lc[u] = pc[1];
+      oc[u] = pc[2 + d];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fold(mc[u], lc[u], oc[u]);
   }
-  for (; c < nch; c += 2) acc0 += __expf(pp[(int64_t)c * ROW] - mu) * pp[(int64_t)c * ROW + 2 + d];
-  const float acc = (acc0 + acc1) + (acc2 + acc3);
-  if (grp == 1) osum[d] = acc;
+  for (; c < nch; c += NG) {
+    const float* pc = pp + (int64_t)c * ROW;
+    fold(pc[0], pc[1], pc[2 + d]);
+  }
+  if (col == 0) {
+    gm[grp] = m;
+    gl[grp] = l;
+  }
+  gacc[grp][col] = acc;
   __syncthreads();
-  if (grp == 0) Elem<T>::store(O + b * st.ob + h * st.oh, d, Ls > 0.f ? (acc + osum[d]) / Ls : 0.f);
+  if (grp == 0) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2) M = fmaxf(M, gm[g2]);
+    const float mu = M == -INFINITY ? 0.f : M;
+    float Ls = 0.f, tot = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2) {
+      const float f = __expf(gm[g2] - mu);
+      Ls += gl[g2] * f;
+      tot += gacc[g2][col] * f;
+    }
+    Elem<T>::store(O + b * st.ob + h * st.oh, d, Ls > 0.f ? tot / Ls : 0.f);
+  }
 }
 
 AttnStrides load_strides(const int64_t* s) {
@@ -327,10 +479,14 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   const T* Q = (const T*)q;
   const T* K = (const T*)k;
   const T* V = (const T*)v;
-#define KH_DECODE_CASE(GG)                                                                               \
-  case GG:                                                                                               \
-    decode_partial_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st, \
-                                                              scale, max_chunks, part);                  \
+#define KH_DECODE_CASE(GG)                                                                                 \
+  case GG:                                                                                                 \
+    if constexpr (sizeof(T) == 2)                                                                          \
+      decode_partial_bf16_kernel<GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st, \
+                                                                 scale, max_chunks, part);                 \
+    else                                                                                                   \
+      decode_partial_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st,  \
+                                                                scale, max_chunks, part);                  \
     break;
   switch (G) {
     KH_DECODE_CASE(1)
@@ -341,7 +497,8 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
 #undef KH_DECODE_CASE
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
-    decode_merge_kernel<T><<<dim3(hq, batch), 256, 0, stream()>>>(part, lens, uniform_len, ml, hq, max_chunks, st,
+    decode_merge_cols_kernel<T><<<dim3(4, hq, batch), 256, 0, stream()>>>(part, lens, uniform_len, ml, hq,
+                                                                          max_chunks, st,
                                                                   (T*)o);
     e = hipGetLastError();
   }
