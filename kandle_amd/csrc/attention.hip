@@ -102,14 +102,26 @@ __device__ __forceinline__ int decode_len(const int32_t* lens, int uniform_len, 
   return L < 0 ? 0 : (L > max_len ? max_len : L);
 }
 
+// Split-K partials: the column sums o of a (sequence, query head, chunk) as one 512-byte row, so the
+// merge reads whole 128-byte lines of it, and the (max, denominator) pairs in an array of their own.
+// Both kernels run on a grid whose z extent is the batch.
+__device__ __forceinline__ float* decode_part_o(float* part) { return part; }
+__device__ __forceinline__ const float* decode_part_o(const float* part) { return part; }
+__device__ __forceinline__ float2* decode_part_ml(float* part, int hq, int max_chunks) {
+  return reinterpret_cast<float2*>(part + (int64_t)gridDim.z * hq * max_chunks * 128);
+}
+__device__ __forceinline__ const float2* decode_part_ml(const float* part, int hq, int max_chunks) {
+  return reinterpret_cast<const float2*>(part + (int64_t)gridDim.z * hq * max_chunks * 128);
+}
+
 template <typename T, int G>
 __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                              const T* __restrict__ V, const int32_t* __restrict__ lens,
                                                              int uniform_len, int max_len, int hq, int hkv,
                                                              AttnStrides st, float scale, int max_chunks,
                                                              float* __restrict__ part) {
-  // Layout of `part`: [b][hq][max_chunks][2 + 128] floats (m, l, o[0..127]), valid chunks only;
-  // decode_merge_cols_kernel combines them.
+  // Layout of `part` (decode_part_o / decode_part_ml): o[b][hq][max_chunks][128] floats, then
+  // (m, l)[b][hq][max_chunks] float pairs; valid chunks only.  decode_merge_cols_kernel combines them.
   constexpr int D = 128;
   constexpr int EPL = 16 / (int)sizeof(T);            // elements per 16-byte load
   constexpr int LPK = D / EPL;                        // lanes per key row (16 bf16, 32 f32)
@@ -237,30 +249,13 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
       Ls += red_l[ww][gi] * f;
       Os += red_o[ww][gi][d] * f;
     }
-    float* pp = part + (((int64_t)b * hq + hk * G + gi) * max_chunks + chunk) * (2 + D);
-    if (d == 0) {
-      pp[0] = M;
-      pp[1] = Ls;
-    }
-    pp[2 + d] = Os;
+    const int64_t row = ((int64_t)b * hq + hk * G + gi) * max_chunks + chunk;
+    if (d == 0) decode_part_ml(part, hq, max_chunks)[row] = make_float2(M, Ls);
+    decode_part_o(part)[row * D + d] = Os;
   }
 }
 
 // ---- bf16 decode partials with in-row DPP reductions ------------------------------------------
-// gfx9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2), row_half_mirror
-// (lane i <-> 7 - i in each group of 8), row_mirror (lane i <-> 15 - i in each row of 16).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-// Sum over the 16 lanes of a DPP row; every lane of the row receives it.  VALU only (no LDS).
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_f<0xB1>(v);
-  v += dpp_f<0x4E>(v);
-  v += dpp_f<0x141>(v);
-  v += dpp_f<0x140>(v);
-  return v;
-}
 
 // Same unit of work and output as decode_partial_kernel, for bf16: the 16 lanes of a DPP row hold
 // one key row (8 columns each), so a score is an in-lane dot product plus a 4-step DPP row sum, and
@@ -373,25 +368,22 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
       Ls += red_l[s2][gi] * f;
       Os += red_o[s2][gi][d] * f;
     }
-    float* pp = part + (((int64_t)b * hq + hk * G + gi) * max_chunks + chunk) * (2 + D);
-    if (d == 0) {
-      pp[0] = M;
-      pp[1] = Ls;
-    }
-    pp[2 + d] = Os;
+    const int64_t row = ((int64_t)b * hq + hk * G + gi) * max_chunks + chunk;
+    if (d == 0) decode_part_ml(part, hq, max_chunks)[row] = make_float2(M, Ls);
+    decode_part_o(part)[row * D + d] = Os;
   }
 }
 
 // Merge by column groups: workgroup (cg, h, b) produces columns 32 cg .. 32 cg + 31 of query head
 // h.  8 groups of 32 threads (one per column) each run one online log-sum-exp pass over every 8th
-// chunk (running max, denominator and column sum, rescaled when the max grows; four chunks' loads in
-// flight), and the 8 group states are combined through LDS.
+// chunk (running max, denominator and column sum, rescaled when the max grows), and the 8 group
+// states are combined through LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __restrict__ part,
                                                                 const int32_t* __restrict__ lens, int uniform_len,
                                                                 int max_len, int hq, int max_chunks, AttnStrides st,
                                                                 T* __restrict__ O) {
-  constexpr int D = 128, ROW = 2 + D, COLS = 32, NG = 8;
+  constexpr int D = 128, COLS = 32, NG = 8;
   __shared__ float gm[NG], gl[NG];
   __shared__ float gacc[NG][COLS];
   const int cg = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -400,7 +392,9 @@ __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __r
   const int d = cg * COLS + col;
   const int L = decode_len(lens, uniform_len, b, max_len);
   const int nch = (L + dc_chunk<T>() - 1) / dc_chunk<T>();
-  const float* pp = part + ((int64_t)b * hq + h) * max_chunks * ROW;
+  const int64_t row0 = ((int64_t)b * hq + h) * max_chunks;
+  const float* po = decode_part_o(part) + row0 * D + d;
+  const float2* pml = decode_part_ml(part, hq, max_chunks) + row0;
 
   float m = -INFINITY, l = 0.f, acc = 0.f;
   // Fold chunk (mc, lc, oc) into the running state.
@@ -412,22 +406,21 @@ __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __r
     acc = acc * a + oc * p;
     m = mn;
   };
-  int c = grp;
-  for (; c + 3 * NG < nch; c += 4 * NG) {
-    float mc[4], lc[4], oc[4];
+  // Up to 16 chunks per thread and pass, all loads issued first; indices past the last chunk are
+  // clamped to it and folded as empty (max -inf, weight 0).
+  constexpr int U = 16;
+  for (int c = grp; c < nch; c += U * NG) {
+    float mc[U], lc[U], oc[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float* pc = pp + (int64_t)(c + u * NG) * ROW;
-      mc[u] = pc[0];
-      lc[u] = pc[1];
-      oc[u] = pc[2 + d];
+    for (int u = 0; u < U; ++u) {
+      const int cc = min(c + u * NG, nch - 1);
+      const float2 mlc = pml[cc];
+      mc[u] = mlc.x;
+      lc[u] = mlc.y;
+      oc[u] = po[(int64_t)cc * D];
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) fold(mc[u], lc[u], oc[u]);
-  }
-  for (; c < nch; c += NG) {
-    const float* pc = pp + (int64_t)c * ROW;
-    fold(pc[0], pc[1], pc[2 + d]);
+    for (int u = 0; u < U; ++u) fold(c + u * NG < nch ? mc[u] : -INFINITY, lc[u], oc[u]);
   }
   if (col == 0) {
     gm[grp] = m;
@@ -472,7 +465,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   const int ml = (int)max_len;
   const int max_chunks = (ml + dc_chunk<T>() - 1) / dc_chunk<T>();
   KH_REQUIRE(max_chunks <= 65535 * 64, "kh_decode_attention: max_len too large");
-  const size_t part_bytes = (size_t)batch * hq * max_chunks * (2 + 128) * sizeof(float);
+  const size_t part_bytes = (size_t)batch * hq * max_chunks * (128 + 2) * sizeof(float);  // o rows + (m, l)
   float* part = (float*)scratch_alloc(part_bytes);
   if (!part) return KH_ERR_OOM;
   dim3 grid(max_chunks, hkv, batch);

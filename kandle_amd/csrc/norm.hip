@@ -16,11 +16,14 @@ template <typename T>
 struct Vec8;
 template <>
 struct Vec8<uint16_t> {
-  static __device__ __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
-    const uint4 w = *reinterpret_cast<const uint4*>(p);
+  // Raw form: the loaded bytes, converted later (so that several loads can be in flight).
+  using Raw = uint4;
+  static __device__ __forceinline__ Raw ld(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ void cvt(const Raw& w, float (&v)[8]) {
     v[0] = lo_bf16(w.x); v[1] = hi_bf16(w.x); v[2] = lo_bf16(w.y); v[3] = hi_bf16(w.y);
     v[4] = lo_bf16(w.z); v[5] = hi_bf16(w.z); v[6] = lo_bf16(w.w); v[7] = hi_bf16(w.w);
   }
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&v)[8]) { cvt(ld(p), v); }
   static __device__ __forceinline__ void store(uint16_t* p, const float (&v)[8]) {
     *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
                                               pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
@@ -28,11 +31,16 @@ struct Vec8<uint16_t> {
 };
 template <>
 struct Vec8<float> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0];
-    const float4 b = reinterpret_cast<const float4*>(p)[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  struct Raw {
+    float4 a, b;
+  };
+  static __device__ __forceinline__ Raw ld(const float* p) {
+    return Raw{reinterpret_cast<const float4*>(p)[0], reinterpret_cast<const float4*>(p)[1]};
   }
+  static __device__ __forceinline__ void cvt(const Raw& r, float (&v)[8]) {
+    v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w; v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+  }
+  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) { cvt(ld(p), v); }
   static __device__ __forceinline__ void store(float* p, const float (&v)[8]) {
     reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
     reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -41,22 +49,31 @@ struct Vec8<float> {
 
 // ---- RMSNorm: one wave per row, row kept in registers (n <= 64 * 8 * CPL) -----------------
 // x has element type TI; w and y have TO (e.g. a float32 residual stream normalised into bf16).
+// Every load of the row and of the weights is issued before any math (lanes past the row end load
+// the last chunk again and ignore it), so a wave waits for one memory round trip, not one per chunk.
 template <typename TI, typename TO, int CPL>
 __global__ __launch_bounds__(256) void rms_norm_vec_kernel(const TI* __restrict__ x, int64_t xs,
                                                             const TO* __restrict__ w, TO* __restrict__ y,
                                                             int64_t ys, int64_t rows, int n, float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= rows) return;
   const int nchunks = n >> 3;
   const TI* xr = x + row * xs;
+  typename Vec8<TI>::Raw rx[CPL];
+  typename Vec8<TO>::Raw rw[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) rx[c] = Vec8<TI>::ld(xr + min(lane + 64 * c, nchunks - 1) * 8);
+  if (w != nullptr) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) rw[c] = Vec8<TO>::ld(w + min(lane + 64 * c, nchunks - 1) * 8);
+  }
   float v[CPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < nchunks) {
-      Vec8<TI>::load(xr + ch * 8, v[c]);
+    Vec8<TI>::cvt(rx[c], v[c]);
+    if (lane + 64 * c < nchunks) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
     }
@@ -72,7 +89,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(const TI* __restrict_
       float o[8];
       if (w != nullptr) {
         float wv[8];
-        Vec8<TO>::load(w + ch * 8, wv);
+        Vec8<TO>::cvt(rw[c], wv);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (v[c][j] * inv) * wv[j];
       } else {
@@ -111,7 +128,9 @@ __global__ __launch_bounds__(256) void rms_norm_generic_kernel(const TI* __restr
 // ---- fused qk-norm + RoPE ---------------------------------------------------------------
 // One wave per token.  A head row of D elements is owned by LPR = D/16 lanes; lane t of a row holds
 // elements [8t, 8t+8) and [D/2 + 8t, D/2 + 8t + 8), so rotate_half pairs stay inside the lane and
-// each lane needs cos/sin for frequencies 8t..8t+7 only (computed once per token).
+// each lane needs cos/sin for frequencies 8t..8t+7 only.  Each frequency's sincosf is evaluated by
+// one lane and read by the others (a full-range sincosf is ~200 VALU instructions; eight per lane
+// made the kernel VALU bound).
 struct QkStrides {
   int64_t s[18];
 };
@@ -120,106 +139,183 @@ struct QkStrides {
 // rows each (q heads first), steps [qk_steps, qk_steps + v_steps) copy RPW V rows each.  The host
 // gives a long sequence one wave per token (spw = all steps: the angles are computed once per
 // token) and a short one (decode) one step per wave, so a single token still spreads over waves.
-template <typename T>
+// Token and step indices are wave-uniform (scalar registers); the host bounds them below 2^32.
+template <typename T, int D, int NB>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo, T* __restrict__ ko,
     const T* __restrict__ v, T* __restrict__ vo, const T* __restrict__ wq, const T* __restrict__ wk,
-    const float* __restrict__ inv_freq, const int32_t* __restrict__ positions, int64_t n_tokens, int64_t seq_len,
-    int hq, int hkv, int D, QkStrides st, float eps, int64_t kv_cache_len, int spw) {
+    const float* __restrict__ inv_freq, const int32_t* __restrict__ positions, uint32_t n_tokens,
+    uint32_t seq_len, int hq, int hkv, QkStrides st, float eps, int64_t kv_cache_len, int spw) {
+  constexpr int LPR = D / 16;        // lanes per row
+  constexpr int RPW = 64 / LPR;      // rows per wave step
+  constexpr int HALF = D / 2;
   const int lane = threadIdx.x & 63;
-  const int LPR = D >> 4;            // lanes per row
-  const int RPW = 64 / LPR;          // rows per wave step
   const int qk_steps = (hq + hkv + RPW - 1) / RPW;
   const int v_steps = v != nullptr ? (hkv + RPW - 1) / RPW : 0;
   const int total_steps = qk_steps + v_steps;
-  const int groups = (total_steps + spw - 1) / spw;
-  const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t tok = gw / groups;
+  const uint32_t groups = (uint32_t)((total_steps + spw - 1) / spw);
+  const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t tok = gw / groups;
   if (tok >= n_tokens) return;
   const int step0 = (int)(gw - tok * groups) * spw;
   const int step1 = min(step0 + spw, total_steps);
-  const int64_t b = tok / seq_len, s = tok - b * seq_len;
+  const uint32_t b = tok / seq_len, s = tok - b * seq_len;
   const int t = lane % LPR;          // chunk index inside the row
   const int rsub = lane / LPR;       // row slot inside the step
-  const int half = D >> 1;
+  const int total_rows = hq + hkv;
 
   // K/V destination row: the token's index in its sequence, or (cache addressing) its position,
   // in which case a position outside the cache writes no K/V row.
   const int32_t ipos = positions[tok];
   const bool cache_mode = kv_cache_len > 0;
-  const int64_t kv_row = cache_mode ? (int64_t)ipos : s;
+  const int64_t kv_row = cache_mode ? (int64_t)ipos : (int64_t)s;
   const bool kv_ok = !cache_mode || (ipos >= 0 && (int64_t)ipos < kv_cache_len);
+  const T* qt = q + b * st.s[0] + s * st.s[1];
+  const T* kt = k + b * st.s[3] + s * st.s[4];
+  const T* vt = v ? v + b * st.s[12] + s * st.s[13] : v;
+  T* qot = qo + b * st.s[6] + s * st.s[7];
+  T* kot = ko + b * st.s[9] + kv_row * st.s[10];
+  T* vot = vo ? vo + b * st.s[15] + kv_row * st.s[16] : vo;
 
+  // Row steps are processed in batches of NB (the host picks NB = min(4, spw)): every load of a
+  // batch is issued, unconditionally, before any math, so a wave keeps NB * 32 bytes per lane in
+  // flight.  Rows past the end of a partial step or batch load a valid clamped row and store nothing.
+  float cs[8], sn[8];
+  // The frequencies are loaded before the rows (loads complete in order, so the angles can then be
+  // computed while the row loads are in flight); the weights after them.
+  typename Vec8<T>::Raw rwqa, rwqb, rwka, rwkb;
+  float f0 = 0.f, f1 = 0.f;
   if (step0 < qk_steps) {
-    // cos/sin of f = float(pos) * inv_freq[i] for i = 8t..8t+7.
-    const float pos = (float)ipos;
-    float cs[8], sn[8];
+    if (lane < HALF) f0 = inv_freq[lane];
+    if (HALF > 64 && lane + 64 < HALF) f1 = inv_freq[lane + 64];
+  }
+  for (int base = step0; base < step1; base += NB) {
+    typename Vec8<T>::Raw ra[NB], rc[NB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float f = pos * inv_freq[8 * t + j];
-      sincosf(f, &sn[j], &cs[j]);
-    }
-    float wqa[8], wqb[8], wka[8], wkb[8];
-    Vec8<T>::load(wq + 8 * t, wqa);
-    Vec8<T>::load(wq + half + 8 * t, wqb);
-    Vec8<T>::load(wk + 8 * t, wka);
-    Vec8<T>::load(wk + half + 8 * t, wkb);
-
-    const int total_rows = hq + hkv;
-    const int qk_end = min(step1, qk_steps);
-    for (int step = step0; step < qk_end; ++step) {
-      const int r = step * RPW + rsub;
-      const bool isq = r < hq;
-      const bool active = r < total_rows && (isq || kv_ok);
-      const int h = isq ? r : r - hq;
+    for (int u = 0; u < NB; ++u) {
+      const int step = min(base + u, step1 - 1);
       const T* src;
-      T* dst;
-      if (isq) {
-        src = q + b * st.s[0] + s * st.s[1] + (int64_t)h * st.s[2];
-        dst = qo + b * st.s[6] + s * st.s[7] + (int64_t)h * st.s[8];
+      if (step < qk_steps) {
+        const int r = min(step * RPW + rsub, total_rows - 1);
+        src = r < hq ? qt + (int64_t)r * st.s[2] : kt + (int64_t)(r - hq) * st.s[5];
       } else {
-        src = k + b * st.s[3] + s * st.s[4] + (int64_t)h * st.s[5];
-        dst = ko + b * st.s[9] + kv_row * st.s[10] + (int64_t)h * st.s[11];
+        const int h = min((step - qk_steps) * RPW + rsub, hkv - 1);
+        src = vt + (int64_t)h * st.s[14];
       }
-      float a[8], c[8];
-      float ss = 0.f;
-      if (active) {
-        Vec8<T>::load(src + 8 * t, a);
-        Vec8<T>::load(src + half + 8 * t, c);
+      ra[u] = Vec8<T>::ld(src + 8 * t);
+      rc[u] = Vec8<T>::ld(src + HALF + 8 * t);
+    }
+    if (base == step0 && step0 < qk_steps) {
+      rwqa = Vec8<T>::ld(wq + 8 * t);
+      rwqb = Vec8<T>::ld(wq + HALF + 8 * t);
+      rwka = Vec8<T>::ld(wk + 8 * t);
+      rwkb = Vec8<T>::ld(wk + HALF + 8 * t);
+      // Keeps the angle computation below the row loads (the compiler would otherwise hoist it,
+      // and its wait for the frequencies, above them).
+      asm volatile("" : "+v"(f0), "+v"(f1));
+      // cos/sin of f = float(pos) * inv_freq[i]: lane i evaluates frequencies i and i + 64 once,
+      // then each lane gathers its eight (i = 8t .. 8t+7) from the lanes that hold them.
+      const float pos = (float)ipos;
+      float c0 = 1.f, s0 = 0.f;
+      if (lane < HALF) sincosf(pos * f0, &s0, &c0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss += a[j] * a[j] + c[j] * c[j];
+      for (int j = 0; j < 8; ++j) {
+        const int i = 8 * t + j;
+        cs[j] = __shfl(c0, i & 63, 64);
+        sn[j] = __shfl(s0, i & 63, 64);
       }
-      // Reduce over the LPR lanes of this row (LPR is a power of two <= 16).
-      for (int o = LPR >> 1; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      if (active) {
-        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-        float oa[8], oc[8];
+      if (HALF > 64) {
+        float c1 = 1.f, s1 = 0.f;
+        if (lane + 64 < HALF) sincosf(pos * f1, &s1, &c1);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float na = (a[j] * inv) * (isq ? wqa[j] : wka[j]);
-          const float nc = (c[j] * inv) * (isq ? wqb[j] : wkb[j]);
-          oa[j] = na * cs[j] + (-nc) * sn[j];
-          oc[j] = nc * cs[j] + na * sn[j];
+          const int i = 8 * t + j;
+          const float c1j = __shfl(c1, i & 63, 64), s1j = __shfl(s1, i & 63, 64);
+          if (i >= 64) {
+            cs[j] = c1j;
+            sn[j] = s1j;
+          }
         }
-        Vec8<T>::store(dst + 8 * t, oa);
-        Vec8<T>::store(dst + half + 8 * t, oc);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int step = base + u;
+      if (step >= step1) break;
+      float a[8], c[8];
+      Vec8<T>::cvt(ra[u], a);
+      Vec8<T>::cvt(rc[u], c);
+      if (step < qk_steps) {
+        const int r = step * RPW + rsub;
+        const bool isq = r < hq;
+        const bool active = r < total_rows && (isq || kv_ok);
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += a[j] * a[j] + c[j] * c[j];
+        ss = group_sum<LPR>(ss);
+        // Weights of this lane's row: whole steps of q rows or of k rows select them uniformly.
+        float wa[8], wb[8];
+        if (step * RPW + RPW <= hq) {
+          Vec8<T>::cvt(rwqa, wa);
+          Vec8<T>::cvt(rwqb, wb);
+        } else if (step * RPW >= hq) {
+          Vec8<T>::cvt(rwka, wa);
+          Vec8<T>::cvt(rwkb, wb);
+        } else {
+          float xa[8], xb[8];
+          Vec8<T>::cvt(rwqa, wa);
+          Vec8<T>::cvt(rwqb, wb);
+          Vec8<T>::cvt(rwka, xa);
+          Vec8<T>::cvt(rwkb, xb);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            wa[j] = isq ? wa[j] : xa[j];
+            wb[j] = isq ? wb[j] : xb[j];
+          }
+        }
+        if (active) {
+          const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+          float oa[8], oc[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float na = (a[j] * inv) * wa[j];
+            const float nc = (c[j] * inv) * wb[j];
+            oa[j] = na * cs[j] + (-nc) * sn[j];
+            oc[j] = nc * cs[j] + na * sn[j];
+          }
+          T* dst = isq ? qot + (int64_t)r * st.s[8] : kot + (int64_t)(r - hq) * st.s[11];
+          Vec8<T>::store(dst + 8 * t, oa);
+          Vec8<T>::store(dst + HALF + 8 * t, oc);
+        }
+      } else {
+        // Fused KV-cache write of V rows (unchanged values).
+        const int h = (step - qk_steps) * RPW + rsub;
+        if (h < hkv && kv_ok) {
+          T* dst = vot + (int64_t)h * st.s[17];
+          Vec8<T>::store(dst + 8 * t, a);
+          Vec8<T>::store(dst + HALF + 8 * t, c);
+        }
       }
     }
   }
-  if (kv_ok) {
-    // Fused KV-cache write of V rows (unchanged values).
-    for (int step = max(step0, qk_steps); step < step1; ++step) {
-      const int h = (step - qk_steps) * RPW + rsub;
-      if (h < hkv) {
-        const T* src = v + b * st.s[12] + s * st.s[13] + (int64_t)h * st.s[14];
-        T* dst = vo + b * st.s[15] + kv_row * st.s[16] + (int64_t)h * st.s[17];
-        float a[8], c[8];
-        Vec8<T>::load(src + 8 * t, a);
-        Vec8<T>::load(src + half + 8 * t, c);
-        Vec8<T>::store(dst + 8 * t, a);
-        Vec8<T>::store(dst + half + 8 * t, c);
-      }
-    }
+}
+
+template <typename T, int D, typename... Args>
+void launch_qk_norm_rope_d(int nb, int grid, int block, Args... args) {
+  switch (nb) {
+    case 1: qk_norm_rope_kernel<T, D, 1><<<grid, block, 0, stream()>>>(args...); break;
+    case 2: qk_norm_rope_kernel<T, D, 2><<<grid, block, 0, stream()>>>(args...); break;
+    case 3: qk_norm_rope_kernel<T, D, 3><<<grid, block, 0, stream()>>>(args...); break;
+    default: qk_norm_rope_kernel<T, D, 4><<<grid, block, 0, stream()>>>(args...); break;
+  }
+}
+template <typename T, typename... Args>
+void launch_qk_norm_rope(int head_dim, int nb, int grid, int block, Args... args) {
+  switch (head_dim) {
+    case 32: launch_qk_norm_rope_d<T, 32>(nb, grid, block, args...); break;
+    case 64: launch_qk_norm_rope_d<T, 64>(nb, grid, block, args...); break;
+    case 128: launch_qk_norm_rope_d<T, 128>(nb, grid, block, args...); break;
+    default: launch_qk_norm_rope_d<T, 256>(nb, grid, block, args...); break;
   }
 }
 
@@ -302,19 +398,21 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out, cons
   const int total_steps = (n_q_heads + n_kv_heads + rpw - 1) / rpw + (v ? (n_kv_heads + rpw - 1) / rpw : 0);
   const int spw = n_tokens >= 2048 ? total_steps : 1;
   const int groups = (total_steps + spw - 1) / spw;
+  const int nb = spw < 4 ? spw : 4;
   const int waves = 4;
   const int64_t grid = (n_tokens * groups + waves - 1) / waves;
-  KH_REQUIRE(grid <= INT32_MAX, "kh_qk_norm_rope: too many tokens");
+  KH_REQUIRE(grid * waves <= (int64_t)UINT32_MAX && seq_len <= (int64_t)UINT32_MAX,
+             "kh_qk_norm_rope: too many tokens");
   if (dtype == KH_BF16)
-    qk_norm_rope_kernel<uint16_t><<<(int)grid, 64 * waves, 0, stream()>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (uint16_t*)q_out, (uint16_t*)k_out, (const uint16_t*)v,
-        (uint16_t*)v_out, (const uint16_t*)wq, (const uint16_t*)wk, inv_freq, positions, n_tokens, seq_len,
-        n_q_heads, n_kv_heads, head_dim, st, eps, kv_cache_len, spw);
+    launch_qk_norm_rope<uint16_t>(head_dim, nb, (int)grid, 64 * waves, (const uint16_t*)q, (const uint16_t*)k,
+                                  (uint16_t*)q_out, (uint16_t*)k_out, (const uint16_t*)v, (uint16_t*)v_out,
+                                  (const uint16_t*)wq, (const uint16_t*)wk, inv_freq, positions, (uint32_t)n_tokens,
+                                  (uint32_t)seq_len, n_q_heads, n_kv_heads, st, eps, kv_cache_len, spw);
   else
-    qk_norm_rope_kernel<float><<<(int)grid, 64 * waves, 0, stream()>>>(
-        (const float*)q, (const float*)k, (float*)q_out, (float*)k_out, (const float*)v, (float*)v_out,
-        (const float*)wq, (const float*)wk, inv_freq, positions, n_tokens, seq_len, n_q_heads, n_kv_heads, head_dim,
-        st, eps, kv_cache_len, spw);
+    launch_qk_norm_rope<float>(head_dim, nb, (int)grid, 64 * waves, (const float*)q, (const float*)k, (float*)q_out,
+                               (float*)k_out, (const float*)v, (float*)v_out, (const float*)wq, (const float*)wk,
+                               inv_freq, positions, (uint32_t)n_tokens, (uint32_t)seq_len, n_q_heads, n_kv_heads, st,
+                               eps, kv_cache_len, spw);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

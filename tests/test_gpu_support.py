@@ -49,6 +49,23 @@ def test_silu_mul_strided_halves_of_fused_gate_up(hip):
     assert np.all(np.abs(y - ref) <= 2 ** -8 * np.abs(ref) + 1e-6)
 
 
+def test_cast_to_bf16_rounding_edge_cases(hip):
+    """The device float32 -> bf16 conversion (one v_cvt_pk_bf16_f32 per pair) rounds to nearest even
+    bit for bit like the oracle: ties both ways, carries into the exponent, overflow to infinity,
+    subnormals, signed zeros; NaN stays NaN."""
+    tie = np.float32(1.0) + np.float32(2.0 ** -8)            # exactly half an ulp above 1 -> 1
+    vals = np.array([0.0, -0.0, 1.0, tie, 1.0 + 3 * 2.0 ** -8, 1.0 + 2 ** -8 + 2 ** -20, -tie,
+                     1.9999999, 3.3895e38, 3.4028235e38, -3.4028235e38, np.inf, -np.inf,
+                     1e-40, -3e-39, 9.18e-41, 1.1754942e-38, 1.17549435e-38, 5.9e-39, 65504.0, 1e10,
+                     np.nan, -np.nan], np.float32)
+    x = np.concatenate([vals, syn.normal(225, (997,)) * np.float32(1e3)]).astype(np.float32)
+    y = F.cast(Tensor(x), "bfloat16").numpy()
+    ref = oracle.bf16_round(x)
+    nan = np.isnan(x)
+    np.testing.assert_array_equal(np.isnan(y), nan)
+    np.testing.assert_array_equal(y[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
 def test_contiguous_cast_of_permuted_view(hip, dtype):
     x, xh = seeded(220, (2, 3, 4, 8), dtype)
