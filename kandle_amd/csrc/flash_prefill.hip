@@ -42,9 +42,12 @@ constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keep
 template <int BN, int WAVES, bool VTR = false>
 struct Cfg {
   static constexpr int THREADS = WAVES * 64;
-  // V row stride (elements).  Row-major: 288 B = 8 banks apart per row, so the 4 rows x 32 B that
-  // a 16-lane group of a transposing read touches cover 32 distinct banks.
-  static constexpr int VSTR = VTR ? FA_D + 16 : BN + 8;
+  // V row stride (elements).  Row-major: 320 B = 80 dwords = 16 banks (mod 64) apart per row.  The
+  // LDS has 64 banks and serves a transposing read 32 lanes per clock: the two 16-lane groups of a
+  // clock read the same 4 rows at column offsets 8 banks apart, so rows must be 16 banks apart for
+  // the 64 dwords to fall on 64 distinct banks (a 288-byte stride gave 2-way conflicts on 28 % of
+  // the LDS-active cycles).
+  static constexpr int VSTR = VTR ? FA_D + 32 : BN + 8;
   static constexpr int KTILE = BN * FA_KSTR;         // elements
   static constexpr int VTILE = VTR ? BN * VSTR : FA_D * VSTR;  // elements
   static constexpr int NK = BN * 16 / THREADS;       // 16-byte K chunks per thread per tile
@@ -272,8 +275,10 @@ struct Softmax {
   float m_ref = -INFINITY;  // reference max of raw scores (q . k) for this row
   float l_run = 0.f;        // partial denominator of this lane's keys, relative to m_ref
 
+  // Raises the reference max when this tile needs it (rescaling O and l); true (wave-uniform) if
+  // any lane did, in which case P must be recomputed.
   template <int NSUB>
-  __device__ __forceinline__ void update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4]) {
+  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4]) {
     float m4[NSUB * 4];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
@@ -297,10 +302,13 @@ struct Softmax {
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+      return true;
     }
+    return false;
   }
+  // P = 2^(s c2 - m_ref c2) as bf16 operands; returns this lane's sum of the fp32 values.
   template <int NSUB>
-  __device__ __forceinline__ void exponentiate(const f32x16 (&sc)[NSUB], float c2, bf16x8 (&pk)[2 * NSUB]) {
+  __device__ __forceinline__ float exponentiate(const f32x16 (&sc)[NSUB], float c2, bf16x8 (&pk)[2 * NSUB]) const {
     const float mb = (m_ref == -INFINITY ? 0.f : m_ref) * c2;
     float ps[2] = {0.f, 0.f};
 #pragma unroll
@@ -316,7 +324,7 @@ struct Softmax {
         }
         pk[2 * s + h] = pv;
       }
-    l_run += ps[0] + ps[1];
+    return ps[0] + ps[1];
   }
 };
 
@@ -380,9 +388,13 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
         f32x16 sacc[C::NSUB];
         F.qk(ks + c * C::BNC * FA_KSTR, qreg, sacc);
         F.template mask<CAUSAL>(tc, lk, sacc);
-        sm.update(sacc, c2, oacc);
+        // P is computed with the current reference max while the tile max is checked (the two are
+        // independent, so their instructions interleave); a raise, rare after the first tile,
+        // rescales O and l and recomputes P.
         bf16x8 pk[2 * C::NSUB];
-        sm.exponentiate(sacc, c2, pk);
+        float ps = sm.exponentiate(sacc, c2, pk);
+        if (sm.update(sacc, c2, oacc)) ps = sm.exponentiate(sacc, c2, pk);
+        sm.l_run += ps;
         if constexpr (VTR)
           F.pv_tr(ks + C::KTILE + c * C::BNC * C::VSTR, pk, oacc);
         else
