@@ -72,6 +72,23 @@ __device__ __forceinline__ v4i16 lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
 }
 
+// Operand reads of a block of NM MFMAs (RPM LDS reads each): the reads of the first kReadsAhead
+// MFMAs are issued first and each MFMA is followed by the reads of the one kReadsAhead places later,
+// so several operands are in flight while the matrix core works (the default schedule keeps one or
+// two).  Placed after the block's code; it orders the DS reads and MFMAs of the basic block.
+constexpr int kReadsAhead = 4;
+template <int NM, int RPM>
+__device__ __forceinline__ void sched_reads_ahead() {
+  constexpr int AHEAD = kReadsAhead < NM ? kReadsAhead : NM;
+  __builtin_amdgcn_sched_group_barrier(0x100, AHEAD * RPM, 0);  // DS reads
+#pragma unroll
+  for (int i = 0; i < NM - AHEAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);        // the reads of a later one
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+}
+
 // Shared per-workgroup setup and staging helpers.
 template <int BN, int WAVES, bool VTR = false>
 struct Flash {
@@ -157,16 +174,24 @@ struct Flash {
   __device__ __forceinline__ void pv_tr(const uint16_t* vs, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[4]) const {
     const int L = lane & 15, Gq = lane >> 4;
     const uint16_t* vbase = vs + (8 * (Gq >> 1) + (L >> 2)) * C::VSTR + 16 * (Gq & 1) + 4 * (L & 3);
+    constexpr int KC = 2 * C::NSUB;
+    v8i16 af[4 * KC];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int kc = 0; kc < 2 * C::NSUB; ++kc) {
+      for (int kc = 0; kc < KC; ++kc) {
         const uint16_t* p0 = vbase + 16 * kc * C::VSTR + 32 * dt;
         const v4i16 lo = lds_read_tr16(p0);
         const v4i16 hi = lds_read_tr16(p0 + 4 * C::VSTR);
-        const v8i16 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, both), pk[kc], oacc[dt], 0, 0, 0);
+        af[dt * KC + kc] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[dt * KC + kc]), pk[kc],
+                                                           oacc[dt], 0, 0, 0);
+    sched_reads_ahead<4 * KC, 2>();
   }
   // V: pass vg stages key pair p = tid / 16 + PAIRS vg (keys 2p, 2p + 1), d 8 * (tid % 16) .. + 8.
   __device__ __forceinline__ void load_v(int t, uint4 (&vst)[C::NVG][2]) const {
@@ -203,17 +228,21 @@ struct Flash {
   }
   // S^T subtiles of one K tile in LDS.
   __device__ __forceinline__ void qk(const uint16_t* ks, const bf16x8 (&qreg)[8], f32x16 (&sacc)[C::NSUB]) const {
+    bf16x8 kf[C::NSUB * 8];
+#pragma unroll
+    for (int s = 0; s < C::NSUB; ++s) {
+      const uint16_t* krp = ks + (32 * s + r) * FA_KSTR + 8 * g;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) kf[s * 8 + c] = as_bf16x8(*reinterpret_cast<const uint4*>(krp + 16 * c));
+    }
 #pragma unroll
     for (int s = 0; s < C::NSUB; ++s) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) sacc[s][j] = 0.f;
-      const uint16_t* krp = ks + (32 * s + r) * FA_KSTR + 8 * g;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const bf16x8 kv = as_bf16x8(*reinterpret_cast<const uint4*>(krp + 16 * c));
-        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qreg[c], sacc[s], 0, 0, 0);
-      }
+      for (int c = 0; c < 8; ++c) sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8 + c], qreg[c], sacc[s], 0, 0, 0);
     }
+    sched_reads_ahead<C::NSUB * 8, 1>();
   }
   // Causal / length mask of tile t (only tiles crossing the diagonal or the sequence end).
   template <bool CAUSAL>
