@@ -191,6 +191,53 @@ def bench_copy(steps, warmup):
     return {"bytes": float(2 * n * 2), "wall_ms": wall_ms, "dev_ms": dev_ms}
 
 
+def bench_load():
+    """Native-bf16 checkpoint load: the C5 Qwen3-0.6B weights (random N(0, 0.02) bf16) written as a
+    two-shard safetensors checkpoint with config.json into a temporary directory, then
+    Qwen3ForCausalLM.from_pretrained timed from the call to the last weight resident in HBM (the
+    files were just written, so they are read from the page cache).  A short greedy generation
+    checks the loaded model against one built from the same in-memory weights."""
+    import dataclasses
+    import tempfile
+
+    import torch
+    from safetensors.torch import save_file
+
+    from kandle_amd import _lib
+    from kandle_amd.model_utils import Qwen3Config, Qwen3ForCausalLM, init_qwen3_weights
+    from kandle_amd import synthetic as syn
+
+    cfg = Qwen3Config()
+    w = init_qwen3_weights(cfg, seed=7)
+    names = list(w)
+    nbytes = sum(v.nbytes for v in w.values())
+    with tempfile.TemporaryDirectory() as d:
+        half = len(names) // 2
+        wm = {}
+        for i, keys in enumerate((names[:half], names[half:])):
+            shard = f"model-0000{i + 1}-of-00002.safetensors"
+            save_file({k: torch.from_numpy(w[k].astype(np.int16)).view(torch.bfloat16) for k in keys},
+                      os.path.join(d, shard))
+            wm.update({k: shard for k in keys})
+        with open(os.path.join(d, "model.safetensors.index.json"), "w") as fh:
+            json.dump({"metadata": {"total_size": nbytes}, "weight_map": wm}, fh)
+        with open(os.path.join(d, "config.json"), "w") as fh:
+            json.dump(dataclasses.asdict(cfg), fh)
+        log(f"checkpoint written ({nbytes / 1e9:.2f} GB)")
+        _lib.synchronize()
+        t0 = time.perf_counter()
+        model = Qwen3ForCausalLM.from_pretrained(d, max_seq_len=64)
+        _lib.synchronize()
+        load_s = time.perf_counter() - t0
+    prompt = syn.randint(8, (16,), 0, cfg.vocab_size)
+    toks = model.generate(prompt, 4)
+    model.dispose()
+    ref = Qwen3ForCausalLM(cfg, w, max_seq_len=64)
+    rtoks = ref.generate(prompt, 4)
+    ref.dispose()
+    return {"bytes": nbytes, "load_s": load_s, "tokens_match": toks == rtoks}
+
+
 def measured_traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurements
     (profiles/traffic.json), scaled by the copy-kernel calibration factors; None if absent."""
@@ -232,7 +279,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -258,6 +305,9 @@ def main():
     if args.only == "copy":
         log("copy calibration ...")
         res["copy"] = bench_copy(args.steps, args.warmup)
+    if args.only == "load":
+        log("checkpoint load ...")
+        res["load"] = bench_load()
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
@@ -323,6 +373,11 @@ def main():
         if "value" not in line:
             line.update({"value": round(1e3 / d_ms, 1), "unit": "tokens/s", "ms_per_step": round(d_ms, 4),
                          "config": {"workload": "C5 Qwen3-0.6B greedy decode"}})
+    if "load" in res:
+        ld = res["load"]
+        line.update({"value": round(ld["bytes"] / ld["load_s"] / 1e9, 2), "unit": "GB/s", "ms_per_step": round(ld["load_s"] * 1e3, 1),
+                     "config": {"workload": "Qwen3-0.6B bf16 safetensors (2 shards, page cache) -> HBM via from_pretrained",
+                                "bytes": ld["bytes"], "tokens_match_in_memory_model": ld["tokens_match"]}})
     if "copy" in res:
         c = res["copy"]
         gbps = c["bytes"] / (c["dev_ms"] * 1e-3) / 1e9

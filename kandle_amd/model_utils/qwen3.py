@@ -55,6 +55,22 @@ class Qwen3Config:
     max_position_embeddings: int = 40960
     tie_word_embeddings: bool = True
 
+    @classmethod
+    def from_dict(cls, d: dict) -> "Qwen3Config":
+        """From a Hugging Face config.json mapping (unknown keys ignored; head_dim defaults to
+        hidden_size / num_attention_heads as in the transformers Qwen3 config)."""
+        kw = {f: d[f] for f in cls.__dataclass_fields__ if f in d and d[f] is not None}
+        if "head_dim" not in kw and "hidden_size" in kw and "num_attention_heads" in kw:
+            kw["head_dim"] = kw["hidden_size"] // kw["num_attention_heads"]
+        return cls(**kw)
+
+    @classmethod
+    def from_json_file(cls, path: str) -> "Qwen3Config":
+        import json
+
+        with open(path, "r", encoding="utf-8") as fh:
+            return cls.from_dict(json.load(fh))
+
 
 def weight_names(cfg: Qwen3Config) -> List[str]:
     names = ["model.embed_tokens.weight"]
@@ -92,6 +108,56 @@ def init_qwen3_weights(cfg: Qwen3Config, seed: int = 0, std: float = 0.02) -> Di
     return out
 
 
+@dataclass
+class LoadStateDictResult:
+    """Outcome of loading a checkpoint (reference: nn/module.ts LoadStateDictResult)."""
+
+    loaded_keys: List[str]
+    missing_keys: List[str]
+    unexpected_keys: List[str]
+
+
+def qwen3_weights_from_safetensor(group, cfg: Qwen3Config, strict: bool = True, key_mapper=None):
+    """(weights, result): the model's tensors from a safetensors group as bf16 bit patterns (uint16
+    arrays; BF16 layers are views of the file's memory map, F32/F16 layers are rounded to nearest
+    even), keyed by the Hugging Face names of weight_names(cfg), plus "lm_head.weight" for an untied
+    head.  Follows Module.loadFromSafetensor (nn/module.ts:572-660): key_mapper maps checkpoint names
+    to model names; strict raises on missing or unexpected keys, with the same message."""
+    from ..io.safetensors import host_array
+
+    key_mapper = key_mapper or (lambda k: k)
+    expected = weight_names(cfg)
+    if not cfg.tie_word_embeddings:
+        expected = expected + ["lm_head.weight"]
+    expected_set = set(expected)
+    tied_extra = {"lm_head.weight"} if cfg.tie_word_embeddings else set()   # a tied head may be stored too
+    by_model_key = {}
+    unexpected = []
+    for name in group.layers:
+        mk = key_mapper(name)
+        if mk in expected_set:
+            by_model_key.setdefault(mk, name)
+        elif mk not in tied_extra:
+            unexpected.append(name)
+    weights, loaded, missing = {}, [], []
+    for key in expected:
+        name = by_model_key.get(key)
+        if name is None:
+            missing.append(key)
+            continue
+        layer = group.get_layer(name)
+        want = tuple(weight_shape(cfg, key)) if key != "lm_head.weight" else (cfg.vocab_size, cfg.hidden_size)
+        if tuple(layer.shape) != want:
+            raise ValueError(f"{name}: checkpoint shape {list(layer.shape)} does not match the model's {list(want)}")
+        weights[key] = host_array(layer, "bfloat16")
+        loaded.append(key)
+    if strict and (missing or unexpected):
+        raise ValueError("Error(s) in loading state_dict:\n"
+                         f"  Missing keys: [{', '.join(missing)}]\n"
+                         f"  Unexpected keys: [{', '.join(unexpected)}]")
+    return weights, LoadStateDictResult(loaded, missing, unexpected)
+
+
 class Qwen3ForCausalLM:
     def __init__(self, cfg: Qwen3Config, weights: Dict[str, np.ndarray], max_seq_len: int = 1024):
         self.cfg = cfg
@@ -99,6 +165,9 @@ class Qwen3ForCausalLM:
         self.ops = env.get_backend("hip").operators
         up = lambda a: Tensor(a, dtype="bfloat16")  # noqa: E731  (uint16 bits -> bf16 tensor)
         self.embed = up(weights["model.embed_tokens.weight"])
+        # Tied embeddings (for_causal_lm.ts:121-125): the lm_head is the embedding matrix itself.
+        untied = not cfg.tie_word_embeddings and "lm_head.weight" in weights
+        self.lm_head = up(weights["lm_head.weight"]) if untied else self.embed
         self.final_norm = up(weights["model.norm.weight"])
         self.layers = []
         for i in range(cfg.num_hidden_layers):
@@ -121,6 +190,26 @@ class Qwen3ForCausalLM:
         self._prefill_graphs: Dict[int, tuple] = {}   # prompt length -> (graph, ids, positions, logits)
 
     # -- decoder body shared by the prefill and the device-resident decode step -------------------
+    @classmethod
+    def from_pretrained(cls, path: str, max_seq_len: int = 1024, cfg: Optional[Qwen3Config] = None,
+                        strict: bool = True) -> "Qwen3ForCausalLM":
+        """A model from a Hugging Face-layout checkpoint: `path` is a directory holding config.json and
+        model.safetensors (or model.safetensors.index.json and its shards), or a .safetensors /
+        index file with `cfg` given.  Weights go to the device as bf16 without an fp32 copy."""
+        import os
+
+        from ..io.safetensors import load_safetensor
+
+        if cfg is None:
+            root = path if os.path.isdir(path) else os.path.dirname(os.path.abspath(path))
+            cfg = Qwen3Config.from_json_file(os.path.join(root, "config.json"))
+        with load_safetensor(path) as group:
+            weights, result = qwen3_weights_from_safetensor(group, cfg, strict=strict)
+            model = cls(cfg, weights, max_seq_len=max_seq_len)
+            del weights   # views of the memory maps: released before the files close
+        model.load_result = result
+        return model
+
     def _decoder(self, x: Tensor, S: int, positions: Tensor, attend) -> Tensor:
         """Runs every decoder layer over the fp32 residual rows x [S, hidden] in place and returns
         the fp32 logits of the last position [1, vocab].  positions: int32 [S] device tensor
@@ -180,10 +269,10 @@ class Qwen3ForCausalLM:
                 t.dispose()
         last = F.narrow(x, 0, S - 1, 1)
         if one:
-            logits = F.linear_fused("rms_norm", last, self.embed, self.final_norm, eps, out_dtype="float32")
+            logits = F.linear_fused("rms_norm", last, self.lm_head, self.final_norm, eps, out_dtype="float32")
         else:
             xf = F.rms_norm(last, [Hd], self.final_norm, eps, out_dtype="bfloat16")
-            logits = F.linear(xf, self.embed, out_dtype="float32")                     # [1, vocab] fp32
+            logits = F.linear(xf, self.lm_head, out_dtype="float32")                   # [1, vocab] fp32
             xf.dispose()
         last.dispose()
         return logits
@@ -337,7 +426,8 @@ class Qwen3ForCausalLM:
             pos_buf.dispose()
         self._prefill_graphs = {}
         self.cache.dispose()
-        for t in [self.embed, self.final_norm] + [v for L in self.layers for v in L.values()]:
+        heads = [self.lm_head] if self.lm_head is not self.embed else []
+        for t in [self.embed, self.final_norm] + heads + [v for L in self.layers for v in L.values()]:
             t.dispose()
 
 

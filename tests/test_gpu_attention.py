@@ -134,6 +134,24 @@ def test_decode_short_caches_repeatable(hip, Hq, Hkv):
     assert np.max(np.abs(outs[0][1:] - ref)) < BF16_ATOL
 
 
+@pytest.mark.parametrize("Hq,Hkv,lens", [(8, 4, [0, 1, 2048]), (4, 4, [65, 513, 1500]), (16, 8, [63, 640])])
+def test_decode_short_caches_gqa_1_and_2(hip, Hq, Hkv, lens):
+    """Short caches (few split-K chunks): GQA 1 and 2, an empty sequence (zeros), lengths off the
+    256-key chunk edges, the C5 decode shape (16/8 heads, 640 keys); repeatable."""
+    lens = np.array(lens, np.int32)
+    B, D, ML = len(lens), 128, int(max(lens.max(), 1))
+    q, qh = seeded(77, (B, Hq, D), "bfloat16")
+    kc, kch = seeded(78, (B, Hkv, ML, D), "bfloat16")
+    vc, vch = seeded(79, (B, Hkv, ML, D), "bfloat16")
+    sl = Tensor(lens, dtype="int32")
+    outs = [F.decode_attention(q, kc, vc, sl).numpy() for _ in range(2)]
+    assert np.array_equal(outs[0], outs[1])
+    nz = lens > 0
+    assert np.all(outs[0][~nz] == 0.0)
+    ref = oracle.sdpa(qh[nz][:, :, None, :], kch[nz], vch[nz], kv_len=lens[nz])[:, :, 0, :]
+    assert np.max(np.abs(outs[0][nz] - ref)) < BF16_ATOL
+
+
 def test_decode_c4_full_size(hip):
     """Config C4 at full size: B=8, Hq=16, Hkv=8, D=128, L_b ~ U[8192, 32768], bf16."""
     B, Hq, Hkv, D, ML = 8, 16, 8, 128, 32768

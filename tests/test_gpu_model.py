@@ -72,3 +72,48 @@ def test_qwen3_0p6b_greedy_32_steps(hip):
     assert err0 < LOGIT_ATOL
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, rtoks)) if a != b), None)
     assert first_diff is None, (first_diff, toks[first_diff], rtoks[first_diff], _margin(rlogits[first_diff]))
+
+
+def test_from_pretrained_sharded_checkpoint_matches_in_memory(hip, tmp_path):
+    """A 2-layer Qwen3 (vocab 4096) saved as a two-shard bf16 safetensors checkpoint with config.json
+    (written by the safetensors package) and loaded with Qwen3ForCausalLM.from_pretrained: device
+    weights carry the checkpoint's bits, generation matches the model built from the in-memory
+    weights bit for bit, and the oracle's tokens."""
+    import dataclasses
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    from kandle_amd.dtypes import bf16_bits_to_f32
+
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
+    w = init_qwen3_weights(cfg, seed=11)
+    names = list(w)
+    shards = {"model-00001-of-00002.safetensors": names[: len(names) // 2],
+              "model-00002-of-00002.safetensors": names[len(names) // 2:]}
+    wm = {}
+    for shard, keys in shards.items():
+        save_file({k: torch.from_numpy(w[k].astype(np.int16)).view(torch.bfloat16) for k in keys},
+                  str(tmp_path / shard))
+        wm.update({k: shard for k in keys})
+    with open(tmp_path / "model.safetensors.index.json", "w") as fh:
+        json.dump({"metadata": {}, "weight_map": wm}, fh)
+    with open(tmp_path / "config.json", "w") as fh:
+        json.dump(dataclasses.asdict(cfg), fh)
+
+    prompt = syn.randint(12, (30,), 0, cfg.vocab_size)
+    model = Qwen3ForCausalLM.from_pretrained(str(tmp_path), max_seq_len=64)
+    assert model.cfg == cfg and not model.load_result.missing_keys and not model.load_result.unexpected_keys
+    np.testing.assert_array_equal(model.embed.numpy(), bf16_bits_to_f32(w["model.embed_tokens.weight"]).reshape(
+        cfg.vocab_size, cfg.hidden_size))
+    toks, logits = model.generate(prompt, 6, return_logits=True)
+    model.dispose()
+    ref = Qwen3ForCausalLM(cfg, w, max_seq_len=64)
+    rtoks, rlogits = ref.generate(prompt, 6, return_logits=True)
+    ref.dispose()
+    assert toks == rtoks
+    for a, b in zip(logits, rlogits):
+        assert np.array_equal(a, b)
+    otoks, _ = Qwen3Oracle(cfg, w, max_seq_len=64).generate(prompt, 6)
+    assert toks == otoks
