@@ -12,7 +12,7 @@ and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against th
 `--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy]
+                    [--only prefill|decode|norm|model|copy|load|sample]
 Prints ONE JSON line.
 """
 import argparse
@@ -238,6 +238,40 @@ def bench_load():
     return {"bytes": nbytes, "load_s": load_s, "tokens_match": toks == rtoks}
 
 
+def bench_sample(steps, warmup):
+    """On-device sampling of one token from a Qwen3 logits row (vocab 151936, float32): kh_sample
+    per call for greedy, an unfiltered draw, and temperature 0.7 with top-k 50 and top-p 0.9 (the
+    counter stays in device memory; its value changes r, not the work)."""
+    from kandle_amd import Tensor
+    from kandle_amd.model_utils.sampling import SamplerConfig, sample_device
+
+    V = 151936
+    x = (np.random.default_rng(21).normal(size=V) * 3).astype(np.float32)
+    lg = Tensor(x, dtype="float32")
+    ctr = Tensor(np.zeros(1, np.int32), dtype="int32")
+    tok = Tensor(np.zeros(1, np.int32), dtype="int32")
+    out = {"vocab": V}
+    for name, cfg in (("greedy", SamplerConfig(do_sample=False)), ("plain", SamplerConfig()),
+                      ("t0.7_k50_p0.9", SamplerConfig(temperature=0.7, top_k=50, top_p=0.9))):
+        wall, dev = time_calls(lambda cfg=cfg: sample_device(lg, cfg, 1234, ctr, tok), steps, warmup)
+        out[name] = {"wall_us": round(wall * 1e3, 2), "dev_us": round(dev * 1e3, 2)}
+    for t in (lg, ctr, tok):
+        t.dispose()
+    return out
+
+
+def cpu_baseline_sample(reps=20):
+    """The oracle's numpy restatement of sample() (temperature 0.7, top-k 50, top-p 0.9) on the same
+    row, single thread: the reference's per-token host work (sort, softmax, filters, draw)."""
+    from oracle.sampling import sample_reference
+
+    x = (np.random.default_rng(21).normal(size=151936) * 3).astype(np.float32)
+    t0 = time.perf_counter()
+    for i in range(reps):
+        sample_reference(x, 0.7, 50, 0.9, (i + 0.5) / reps, 10)
+    return (time.perf_counter() - t0) * 1e6 / reps
+
+
 def measured_traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurements
     (profiles/traffic.json), scaled by the copy-kernel calibration factors; None if absent."""
@@ -279,7 +313,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample"],
+                    default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -308,6 +343,11 @@ def main():
     if args.only == "load":
         log("checkpoint load ...")
         res["load"] = bench_load()
+    if args.only in (None, "sample"):
+        log("sampling ...")
+        res["sample"] = bench_sample(args.steps, args.warmup)
+        if args.only == "sample" and not args.no_cpu_baseline:
+            res["sample"]["cpu_oracle_us"] = round(cpu_baseline_sample(), 1)
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
@@ -383,6 +423,13 @@ def main():
         gbps = c["bytes"] / (c["dev_ms"] * 1e-3) / 1e9
         line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(c["wall_ms"], 4),
                      "config": {"workload": "1 GiB device copy (traffic-counter calibration)"}})
+    if "sample" in res:
+        line["sample"] = dict(res["sample"], workload="kh_sample, one float32 logits row, vocab 151936")
+        if "value" not in line:
+            sm = res["sample"]["t0.7_k50_p0.9"]
+            line.update({"value": round(1e6 / sm["wall_us"], 1), "unit": "draws/s",
+                         "ms_per_step": round(sm["wall_us"] * 1e-3, 4),
+                         "config": {"workload": "on-device sampling, T=0.7, top-k 50, top-p 0.9, vocab 151936"}})
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 

@@ -145,6 +145,25 @@ int kh_argmax(const void* x, int64_t rows, int64_t n, int32_t* out, int dtype);
 int kh_greedy_advance(const int32_t* next_token, int32_t* position, int32_t* seq_len, int32_t* token_log,
                       int64_t log_base, int64_t log_cap);
 
+/* One token chosen from a row of float32 logits [vocab] on the device.  do_sample != 0: temperature,
+ * top-k (top_k <= 0: off), top-p (top_p >= 1: off), renormalisation, and a draw that walks the kept
+ * probabilities in id order against r = (word 0 of philox4x32-10(key = seed, counter = (*counter, 0,
+ * 0, 0)) >> 8) * 2^-24.  do_sample == 0 (greedy): the lowest id of the largest logit, with the
+ * unfiltered softmax(logits / T) as its probabilities (counter may then be NULL).
+ * Writes the token (int32), log(q_token + 1e-10) (logprob_out may be NULL) and the first display_k
+ * ids of the descending logit order with their probabilities (NULL to skip).
+ * counter is a device int32 (a generation loop advances it on the device).  Not capturable.
+ * Replaces sample() (reference: packages/model-utils/src/sampling/index.ts:103-243, softmaxCPU
+ * :268-291, sampleFromProbs :294-311); the reference draws r with Math.random(). */
+int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperature, int top_k, double top_p,
+              uint64_t seed, const int32_t* counter, int32_t* token_out, float* logprob_out, int display_k, int32_t* display_ids,
+              float* display_probs);
+
+/* out[4i .. 4i+3] = philox4x32-10(counters[4i .. 4i+3], key = (low, high 32 bits of seed)) for n
+ * counters (device arrays).  The generator kh_sample draws from (Salmon et al., SC'11); no
+ * reference counterpart (the reference draws with Math.random). */
+int kh_philox4x32_10(uint64_t seed, const uint32_t* counters, int64_t n, uint32_t* out);
+
 /* ------------------------------------------------------------------ hot path ----------------- */
 
 /* y[r, :] = x[r, :] * (1 / sqrt(mean(x[r, :]^2) + eps)) * w[:] (w may be NULL), fp32 math,

@@ -563,7 +563,45 @@ def greedy_advance(next_token, position, seq_len, token_log, log_base: int) -> N
               _vp(token_log.data_ptr()), int(log_base), token_log.numel)
 
 
+def sample(logits, params: dict):
+    """Choose one token from a [vocab] (or [1, vocab]) float32 logits row on the device
+    (sampling/index.ts:103-243).  params: do_sample (True; False = greedy), temperature (1.0),
+    top_k (0 = off), top_p (1.0 = off), seed (int), counter (int32 device tensor [1]; r comes from
+    philox4x32-10(seed, counter); unused when greedy), display_k (0), and the outputs token (int32 [1]),
+    logprob (float32 [1], optional), display_ids (int32 [display_k], optional) and display_probs
+    (float32 [display_k], optional)."""
+    if logits.dtype != FLOAT32 or not logits.is_contiguous():
+        raise TypeError("sample: logits must be a contiguous float32 tensor")
+    vocab = logits.shape[-1]
+    if logits.numel != vocab:
+        raise ValueError(f"sample: one row of logits expected, got shape {list(logits.shape)}")
+    do_sample = bool(params.get("do_sample", True))
+    ctr, tok = params.get("counter"), params["token"]
+    for name, h in (("counter", ctr), ("token", tok)):
+        if h is None and name == "counter" and not do_sample:
+            continue
+        if h is None or h.dtype != INT32 or h.numel < 1:
+            raise TypeError(f"sample: {name} must be an int32 tensor with one element")
+    dk = int(params.get("display_k", 0))
+    ptr = lambda h: _vp(h.data_ptr()) if h is not None else _vp(0)  # noqa: E731
+    dids, dprobs = params.get("display_ids"), params.get("display_probs")
+    if dk and ((dids is not None and dids.numel < dk) or (dprobs is not None and dprobs.numel < dk)):
+        raise ValueError("sample: display outputs shorter than display_k")
+    _lib.call("kh_sample", _vp(logits.data_ptr()), vocab, int(do_sample), float(params.get("temperature", 1.0)),
+              int(params.get("top_k", 0)), float(params.get("top_p", 1.0)), C.c_uint64(int(params.get("seed", 0))),
+              ptr(ctr), _vp(tok.data_ptr()), ptr(params.get("logprob")), dk, ptr(dids), ptr(dprobs))
+
+
+def philox4x32_10(seed: int, counters, out) -> None:
+    """out[i] = philox4x32-10(counters[i], key = seed) for uint32 [n, 4] device tensors (int32 storage)."""
+    if counters.numel % 4 or out.numel != counters.numel:
+        raise ValueError("philox4x32_10: counters and out must be [n, 4]")
+    _lib.call("kh_philox4x32_10", C.c_uint64(int(seed)), _vp(counters.data_ptr()), counters.numel // 4,
+              _vp(out.data_ptr()))
+
+
 KERNELS = {
+    "sample": sample,
     "flash_attention": flash_attention,
     "decode_attention": decode_attention,
     "matmul": matmul,

@@ -1,0 +1,131 @@
+"""GPU parity of on-device sampling (kh_sample, kh_philox4x32_10) with the CPU restatement of
+sample() (packages/model-utils/src/sampling/index.ts:103-311) in oracle/sampling.py.
+
+Bar: display ids and greedy tokens bit-exact; the drawn token exact unless r lies within 1e-12 of a
+running sum (the device sums in another order than the reference's loop, so ties at that distance
+are rounding, not semantics; no case here comes that close, and the test says so if one does);
+probabilities within 2e-6 relative (f64 sums in another order may move an f32 quotient by one ulp);
+log-probabilities within 2e-6 absolute."""
+import numpy as np
+import pytest
+
+from kandle_amd import Tensor
+from kandle_amd import kernels
+from kandle_amd.model_utils.sampling import SamplerConfig, sample, sample_device, sample_greedy
+from oracle.sampling import draw_margin, philox4x32_10, sample_reference, topp_margin, uniform24
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 151936
+
+
+def _logits(seed, n=VOCAB, scale=3.0):
+    return (np.random.default_rng(seed).normal(size=n) * scale).astype(np.float32)
+
+
+def _check(x, cfg, seed, counter, display_k=10):
+    lg = Tensor(x, dtype="float32")
+    res = sample(lg, cfg, display_k, seed=seed, counter=counter)
+    lg.dispose()
+    r = uniform24(seed, counter)
+    tok, lp, ids, probs = sample_reference(x, cfg.temperature, cfg.top_k, cfg.top_p, r, display_k, cfg.do_sample)
+    assert res.top_k_token_ids == [int(i) for i in ids]
+    np.testing.assert_allclose(res.top_k_probs, probs, rtol=2e-6, atol=1e-30)
+    near = cfg.do_sample and (topp_margin(x, cfg.temperature, cfg.top_k, cfg.top_p) <= 1e-12
+                              or draw_margin(x, cfg.temperature, cfg.top_k, cfg.top_p, r) <= 1e-12)
+    if near:   # r or top_p within rounding of a running sum: either neighbour is a correct draw
+        print(f"[sample] seed={seed} counter={counter}: boundary within 1e-12, token not compared")
+        return res
+    assert res.token_id == tok
+    assert res.log_prob == pytest.approx(lp, abs=2e-6)
+    return res
+
+
+KAT = {  # Random123 known answers: (seed as key low | high << 32, counter row) -> output
+    0: (0, (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+    0xffffffff_ffffffff: (1, (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+    0x299f31d0_a4093822: (2, (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1)),
+}
+
+
+def test_philox_device_matches_kat_and_oracle(hip):
+    ctr = np.array([[0, 0, 0, 0], [0xffffffff] * 4, [0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344]],
+                   np.uint32)
+    rng = np.random.default_rng(5)
+    ctr = np.concatenate([ctr, rng.integers(0, 2 ** 32, size=(997, 4), dtype=np.uint32)])
+    for seed in (0, 0xffffffff_ffffffff, 0x299f31d0_a4093822, 123456789):
+        c = Tensor(ctr.view(np.int32), dtype="int32")
+        o = Tensor(np.zeros_like(ctr).view(np.int32), dtype="int32")
+        kernels.philox4x32_10(seed, c.handle, o.handle)
+        got = o.numpy().view(np.uint32)
+        c.dispose()
+        o.dispose()
+        if seed in KAT:
+            row, answer = KAT[seed]
+            assert tuple(int(v) for v in got[row]) == answer
+        want = np.array([philox4x32_10(row, (seed & 0xffffffff, seed >> 32)) for row in ctr], np.uint32)
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("cfg", [
+    SamplerConfig(),                                          # plain softmax draw
+    SamplerConfig(temperature=0.7, top_k=50),
+    SamplerConfig(temperature=0.7, top_p=0.9),
+    SamplerConfig(temperature=1.3, top_k=40, top_p=0.95),
+    SamplerConfig(temperature=0.5, top_p=0.5),
+    SamplerConfig(temperature=2.0, top_k=1),
+], ids=["plain", "t0.7k50", "t0.7p0.9", "t1.3k40p0.95", "t0.5p0.5", "t2k1"])
+def test_sample_matches_reference_full_vocab(hip, cfg):
+    x = _logits(11)
+    for seed, counter in ((0, 0), (42, 1), (42, 2), (2 ** 40 + 3, 77), (7, 123456)):
+        _check(x, cfg, seed, counter)
+
+
+def test_sample_peaked_and_flat_rows(hip):
+    # a peaked row (top-p keeps few ids) and a flat one (the draw walks far into the vocabulary)
+    peaked = _logits(12, scale=8.0)
+    flat = _logits(13, scale=0.05)
+    for seed in range(4):
+        _check(peaked, SamplerConfig(top_p=0.8), seed, seed)
+        _check(flat, SamplerConfig(temperature=1.5), seed, seed)
+        _check(flat, SamplerConfig(top_k=1000, top_p=0.3), seed, seed)
+
+
+@pytest.mark.parametrize("t", [1.0, 0.6, 1.7])
+def test_greedy_matches_reference(hip, t):
+    x = _logits(14)
+    x[[100, 5000, 90000]] = x.max() + 1.0                      # a three-way tie for the maximum
+    res = _check(x, SamplerConfig(temperature=t, do_sample=False), 0, 0)
+    assert res.token_id == 100
+    g = sample_greedy(Tensor(x, dtype="float32"), 5)
+    assert g.token_id == 100 and g.top_k_token_ids[:3] == [100, 5000, 90000]
+
+
+def test_small_vocab_ties_and_signed_zero(hip):
+    x = np.array([1.0, 5.0, 5.0, 0.0, 5.0, -0.0, 0.0, -3.0], np.float32)
+    for cfg in (SamplerConfig(top_k=2), SamplerConfig(top_p=0.5), SamplerConfig(temperature=0.3),
+                SamplerConfig(do_sample=False)):
+        for c in range(6):
+            _check(x, cfg, 9, c, display_k=8)
+    one = np.array([2.5], np.float32)
+    res = _check(one, SamplerConfig(temperature=0.9, top_p=0.2), 1, 1, display_k=1)
+    assert res.token_id == 0
+
+
+def test_counter_read_on_device_and_2d_logits(hip):
+    x = _logits(15, n=4096, scale=2.0)
+    lg = Tensor(x.reshape(1, -1), dtype="float32")
+    ctr = Tensor(np.array([3], np.int32), dtype="int32")
+    tok = Tensor(np.zeros(1, np.int32), dtype="int32")
+    sample_device(lg, SamplerConfig(temperature=0.8), 99, ctr, tok)
+    want = sample_reference(x, 0.8, 0, 1.0, uniform24(99, 3), 0)[0]
+    assert int(tok.numpy()[0]) == want
+    for t in (lg, ctr, tok):
+        t.dispose()
+
+
+def test_sample_argument_errors(hip):
+    lg = Tensor(_logits(16, n=64), dtype="float32")
+    with pytest.raises(Exception, match="temperature"):
+        sample(lg, SamplerConfig(temperature=0.0))
+    lg.dispose()
