@@ -21,10 +21,11 @@
 // bits (word 0 >> 8, times 2^-24), with the counter read from device memory so a generation loop can
 // advance it on the device.
 //
-// The sort is hipCUB's stable LSD radix sort; the f64 sums are two-pass block reductions and
-// hipCUB inclusive scans (deterministic for a given size).  hipCUB may clear its temporary storage
+// The sort is rocPRIM's stable radix sort; the f64 sums are two-pass block reductions
+// and hipCUB inclusive scans (deterministic for a given size).  hipCUB may clear its temporary storage
 // with memsets, so kh_sample refuses to run under stream capture.
 #include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include "common.h"
 
@@ -164,15 +165,20 @@ __global__ void scatter_q_kernel(const float* __restrict__ p, const int32_t* __r
 }
 
 // sel[0] = min id with r < cum[id]; sel[1] = max id with q[id] > 0 (the fallback); r from Philox.
+// One atomic per wave: the wave's lowest (highest) qualifying id, found from a ballot.
 __global__ void draw_kernel(const double* __restrict__ cum, const float* __restrict__ q, int n, uint64_t seed,
                             const int32_t* __restrict__ counter, int* __restrict__ sel) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+  const int lane = threadIdx.x & 63;
   uint32_t c[4] = {(uint32_t)*counter, 0u, 0u, 0u};
   philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
   const double r = (double)(c[0] >> 8) * (1.0 / 16777216.0);
-  if (r < cum[i]) atomicMin(&sel[0], i);
-  if (q[i] > 0.f) atomicMax(&sel[1], i);
+  const bool in = i < n;
+  const uint64_t hit = __ballot(in && r < cum[in ? i : 0]);
+  const uint64_t pos = __ballot(in && q[in ? i : 0] > 0.f);
+  const int base = i - lane;
+  if (lane == 0 && hit) atomicMin(&sel[0], base + __ffsll((unsigned long long)hit) - 1);
+  if (lane == 0 && pos) atomicMax(&sel[1], base + 63 - __clzll((unsigned long long)pos));
 }
 
 // token: greedy -> the first id of the order; sampling -> the draw, else the fallback, else 0.
@@ -199,6 +205,13 @@ __global__ void init_sel_kernel(int* __restrict__ sel, int n) {
 }
 
 inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+// rocPRIM's stable radix sort with its default configuration (for a 151,936-id row: a block sort
+// and merge passes, measured faster here than forcing onesweep).
+inline hipError_t sort_desc(void* tmp, size_t& bytes, const float* k_in, float* k_out, const int32_t* v_in,
+                            int32_t* v_out, int n, hipStream_t s) {
+  return rocprim::radix_sort_pairs_desc(tmp, bytes, k_in, k_out, v_in, v_out, n, 0, 32, s);
+}
 
 }  // namespace
 
@@ -234,9 +247,7 @@ int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperat
 
   // temporary storage sizes of the hipCUB calls
   size_t sort_bytes = 0, scan_bytes = 0;
-  KH_CHECK_HIP(hipcub::DeviceRadixSort::SortPairsDescending(nullptr, sort_bytes, (const float*)nullptr, (float*)nullptr,
-                                                            (const int32_t*)nullptr, (int32_t*)nullptr, n, 0, 32,
-                                                            stream()));
+  KH_CHECK_HIP(sort_desc(nullptr, sort_bytes, nullptr, nullptr, nullptr, nullptr, n, stream()));
   KH_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, (const double*)nullptr, (double*)nullptr, n,
                                                 stream()));
   const size_t cub_bytes = sort_bytes > scan_bytes ? sort_bytes : scan_bytes;
@@ -268,8 +279,7 @@ int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperat
   iota_keys_kernel<<<nb, kThreads, 0, stream()>>>(logits, n, keys, ids);
   ok(hipGetLastError());
   size_t sb = sort_bytes;
-  ok(hipcub::DeviceRadixSort::SortPairsDescending(cub_tmp, sb, keys, sorted_logits, ids, sorted_ids, n, 0, 32,
-                                                  stream()));
+  ok(sort_desc(cub_tmp, sb, keys, sorted_logits, ids, sorted_ids, n, stream()));
   exp_kernel<<<nb, kThreads, 0, stream()>>>(sorted_logits, n, inv_t, greedy, e, part);
   final_sum_kernel<<<1, kThreads, 0, stream()>>>(part, nb, Z);
   prob_kernel<<<nb, kThreads, 0, stream()>>>(e, n, Z, e, p64);

@@ -23,7 +23,7 @@ read fp32 x and write bf16 h); math inside kernels is fp32.
 from __future__ import annotations
 
 import time
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
 import numpy as np
@@ -332,11 +332,10 @@ class Qwen3ForCausalLM:
         return g_logits, False
 
     # -- device-resident greedy decode step ---------------------------------------------------------
-    def _decode_step(self, st: "DecodeState") -> Tensor:
-        """One greedy step that reads every changing value from device memory: the token st.ids at
-        position st.pos attends over st.lens cached rows; the argmax of its logits overwrites st.ids
-        and greedy_advance logs it and moves st.pos / st.lens on.  The same launches run eagerly
-        or replayed from a captured graph.  Returns the step's fp32 logits [1, vocab]."""
+    def _step_logits(self, st: "DecodeState") -> Tensor:
+        """The fp32 logits [1, vocab] of the token st.ids at position st.pos, attending over st.lens
+        cached rows (its K/V row is written at st.pos); every changing value is read from device
+        memory, so the same launches run eagerly or replayed from a captured graph."""
         x = F.embedding(st.ids, self.embed, out_dtype="float32")  # [1, Hd]
 
         def attend(li, q_heads, out_view):
@@ -346,6 +345,13 @@ class Qwen3ForCausalLM:
 
         logits = self._decoder(x, 1, st.pos, attend)
         x.dispose()
+        return logits
+
+    def _decode_step(self, st: "DecodeState") -> Tensor:
+        """One greedy step on device state: the logits of st.ids (_step_logits), whose argmax
+        overwrites st.ids, and greedy_advance logs it and moves st.pos / st.lens on.  Returns the
+        step's fp32 logits [1, vocab]."""
+        logits = self._step_logits(st)
         self.ops.find("argmax")(TensorIterator([logits.handle], [st.ids.handle]))
         self.ops.find("greedy_advance")(st.ids.handle, st.pos.handle, st.lens.handle, st.log.handle, st.base)
         return logits
@@ -418,6 +424,67 @@ class Qwen3ForCausalLM:
         self.cache.mark_written(P + N)
         return (toks, all_logits) if return_logits else toks
 
+    def generate_stream(self, input_ids, config: Optional["GeneratorConfig"] = None, seed: int = 0,
+                        use_graph: bool = True):
+        """generateStream (for_causal_lm.ts:354-440): a generator that prefills the prompt, then per
+        step samples a token on the device (sample(), temperature / top-k / top-p or greedy) and
+        yields a GenerationStep with the token, its log-probability and the display_top_k most
+        likely ids.  `generator.send(token_id)` overrides the token fed back (None keeps the
+        sampled one); generation stops after max_new_tokens steps or at an EOS token.
+
+        The draw of step i uses r = philox4x32-10(seed, counter = i), so a (seed, prompt, config)
+        triple replays the same tokens (the reference draws with Math.random()).  With use_graph the
+        one-token forward is captured once and replayed with the token, position and KV length in
+        device memory.  The reference's extra forward after the last step (its result unused) is
+        not run."""
+        from .sampling import SamplerConfig, sample
+
+        cfg = config or GeneratorConfig()
+        prompt = np.asarray(input_ids, np.int32).reshape(-1)
+        P, N = int(prompt.size), int(cfg.max_new_tokens)
+        eos = set(int(t) for t in cfg.eos_token_ids)
+        sampler = SamplerConfig(cfg.temperature, cfg.top_k, cfg.top_p, cfg.do_sample)
+        self.cache.reset()
+        self.cache.check_write(0, P + max(N, 1))
+        logits, owned = self._prefill(prompt, use_graph)
+        st = DecodeState(*(Tensor(np.zeros(1, np.int32), dtype="int32") for _ in range(3)),
+                         Tensor(np.zeros(1, np.int32), dtype="int32"), P)
+        graph, g_logits = None, None
+        try:
+            for i in range(N):
+                res = sample(logits, sampler, cfg.display_top_k, seed=seed, counter=i)
+                if owned:
+                    logits.dispose()
+                logits, owned = None, False
+                override = yield GenerationStep(res.token_id, res.log_prob, res.top_k_token_ids, res.top_k_probs,
+                                                res.token_id in eos, P + i, i + 1)
+                tok = int(override) if override is not None else res.token_id
+                if tok in eos or i + 1 == N:
+                    break
+                if not 0 <= tok < self.cfg.vocab_size:
+                    raise ValueError(f"generate_stream: token id {tok} outside [0, {self.cfg.vocab_size})")
+                for t, v in ((st.ids, tok), (st.pos, P + i), (st.lens, P + i + 1)):
+                    t.handle.storage.upload(np.array([v], np.int32))
+                if not use_graph:
+                    logits, owned = self._step_logits(st), True
+                elif graph is None:
+                    logits, owned = self._step_logits(st), True
+                    graph = HipGraph()
+                    with graph.capture():
+                        g_logits = self._step_logits(st)
+                else:
+                    graph.replay()
+                    logits = g_logits
+                self.cache.mark_written(P + i + 1)
+        finally:
+            if owned and logits is not None:
+                logits.dispose()
+            if g_logits is not None:
+                g_logits.dispose()
+            if graph is not None:
+                graph.dispose()
+            st.dispose()
+
     def dispose(self) -> None:
         for graph, ids_buf, pos_buf, g_logits in self._prefill_graphs.values():
             g_logits.dispose()
@@ -429,6 +496,32 @@ class Qwen3ForCausalLM:
         heads = [self.lm_head] if self.lm_head is not self.embed else []
         for t in [self.embed, self.final_norm] + heads + [v for L in self.layers for v in L.values()]:
             t.dispose()
+
+
+@dataclass
+class GeneratorConfig:
+    """GeneratorConfig and DEFAULT_GENERATOR_CONFIG (for_causal_lm.ts:47-78)."""
+
+    max_new_tokens: int = 256
+    eos_token_ids: List[int] = field(default_factory=list)
+    display_top_k: int = 10
+    temperature: float = 1.0
+    top_k: int = 0
+    top_p: float = 1.0
+    do_sample: bool = True
+
+
+@dataclass
+class GenerationStep:
+    """One yielded step of generate_stream (for_causal_lm.ts:24-41)."""
+
+    token_id: int
+    log_prob: float
+    top_k_token_ids: List[int]
+    top_k_probs: np.ndarray
+    is_eos: bool
+    cache_position: int
+    generated_count: int
 
 
 def _split_heads(qkv: Tensor, col0: int, S: int, H: int, D: int) -> Tensor:

@@ -129,3 +129,102 @@ def test_sample_argument_errors(hip):
     with pytest.raises(Exception, match="temperature"):
         sample(lg, SamplerConfig(temperature=0.0))
     lg.dispose()
+
+
+# ---- generateStream (for_causal_lm.ts:354-440) on the device sampler -------------------------------
+
+def _small_model(seed=5, max_seq=96):
+    from kandle_amd.model_utils import Qwen3Config, Qwen3ForCausalLM, init_qwen3_weights
+
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
+    w = init_qwen3_weights(cfg, seed=seed)
+    return cfg, w, Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq)
+
+
+def _drive(gen, overrides=None):
+    """Run a generate_stream generator to the end, sending overrides[i] after step i."""
+    steps, send = [], None
+    overrides = overrides or {}
+    while True:
+        try:
+            st = gen.send(send) if steps else next(gen)
+        except StopIteration:
+            return steps
+        steps.append(st)
+        send = overrides.get(len(steps) - 1)
+
+
+def test_generate_stream_sampled_steps_follow_reference(hip, monkeypatch):
+    """Each step is sample() of the logits the oracle gives for the tokens actually fed (sampled or
+    overridden), drawn with r = philox(seed, step)."""
+    from kandle_amd import synthetic as syn
+    from kandle_amd.model_utils import GeneratorConfig
+    from kandle_amd.model_utils import sampling as S
+    from oracle.qwen3 import Qwen3Oracle
+
+    cfg, w, model = _small_model()
+    prompt = syn.randint(6, (40,), 0, cfg.vocab_size)
+    seen = []
+    real = S.sample
+
+    def spy(logits, config=None, display_top_k=10, seed=0, counter=0):
+        seen.append((logits.numpy().reshape(-1).copy(), seed, counter))
+        return real(logits, config, display_top_k, seed, counter)
+
+    monkeypatch.setattr(S, "sample", spy)
+    gc = GeneratorConfig(max_new_tokens=6, temperature=0.8, top_k=50, top_p=0.9, display_top_k=5)
+    steps = _drive(model.generate_stream(prompt, gc, seed=7), overrides={2: 123})
+    model.dispose()
+    assert len(steps) == 6 and len(seen) == 6
+    fed = [s.token_id for s in steps]
+    fed[2] = 123
+    ref = Qwen3Oracle(cfg, w, max_seq_len=96)
+    rl = ref.forward(prompt, 0)
+    for i, (st, (lg, seed, ctr)) in enumerate(zip(steps, seen)):
+        assert (seed, ctr) == (7, i) and st.cache_position == 40 + i and st.generated_count == i + 1
+        assert float(np.max(np.abs(lg - rl))) < 2e-2, i
+        r = uniform24(7, i)
+        tok, lp, ids, probs = sample_reference(lg, 0.8, 50, 0.9, r, 5)
+        assert st.top_k_token_ids == [int(x) for x in ids]
+        np.testing.assert_allclose(st.top_k_probs, probs, rtol=2e-6)
+        if topp_margin(lg, 0.8, 50, 0.9) > 1e-12 and draw_margin(lg, 0.8, 50, 0.9, r) > 1e-12:
+            assert st.token_id == tok and st.log_prob == pytest.approx(lp, abs=2e-6)
+        if i + 1 < len(steps):
+            rl = ref.forward([fed[i]], 40 + i)
+
+
+def test_generate_stream_greedy_matches_generate_and_stops_at_eos(hip):
+    from kandle_amd import synthetic as syn
+    from kandle_amd.model_utils import GeneratorConfig
+
+    cfg, w, model = _small_model(seed=8)
+    prompt = syn.randint(9, (33,), 0, cfg.vocab_size)
+    want = model.generate(prompt, 6)
+    for use_graph in (False, True):
+        steps = _drive(model.generate_stream(prompt, GeneratorConfig(max_new_tokens=6, do_sample=False),
+                                             use_graph=use_graph))
+        assert [s.token_id for s in steps] == want
+        assert all(s.top_k_token_ids[0] == s.token_id for s in steps)
+    eos = want[2]
+    first = want.index(eos)
+    steps = _drive(model.generate_stream(prompt, GeneratorConfig(max_new_tokens=6, do_sample=False,
+                                                                 eos_token_ids=[eos])))
+    model.dispose()
+    assert len(steps) == first + 1 and steps[-1].is_eos and not any(s.is_eos for s in steps[:-1])
+
+
+def test_generate_stream_graph_replay_matches_eager(hip):
+    from kandle_amd import synthetic as syn
+    from kandle_amd.model_utils import GeneratorConfig
+
+    cfg, w, model = _small_model(seed=10)
+    prompt = syn.randint(11, (24,), 0, cfg.vocab_size)
+    gc = GeneratorConfig(max_new_tokens=8, temperature=1.1, top_p=0.95, display_top_k=4)
+    a = _drive(model.generate_stream(prompt, gc, seed=3, use_graph=False))
+    b = _drive(model.generate_stream(prompt, gc, seed=3, use_graph=True))
+    c = _drive(model.generate_stream(prompt, gc, seed=4, use_graph=True))
+    model.dispose()
+    assert [s.token_id for s in a] == [s.token_id for s in b]
+    for x, y in zip(a, b):
+        assert x.top_k_token_ids == y.top_k_token_ids and np.array_equal(x.top_k_probs, y.top_k_probs)
+    assert [s.token_id for s in c] != [s.token_id for s in a]   # another seed, another draw
