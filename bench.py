@@ -12,7 +12,7 @@ and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against th
 `--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy|load|sample]
+                    [--only prefill|decode|norm|model|copy|load|sample|stream]
 Prints ONE JSON line.
 """
 import argparse
@@ -251,13 +251,56 @@ def bench_sample(steps, warmup):
     ctr = Tensor(np.zeros(1, np.int32), dtype="int32")
     tok = Tensor(np.zeros(1, np.int32), dtype="int32")
     out = {"vocab": V}
+    from kandle_amd.graphs import HipGraph
+
     for name, cfg in (("greedy", SamplerConfig(do_sample=False)), ("plain", SamplerConfig()),
-                      ("t0.7_k50_p0.9", SamplerConfig(temperature=0.7, top_k=50, top_p=0.9))):
+                      ("t0.7_k50_p0.9", SamplerConfig(temperature=0.7, top_k=50, top_p=0.9)),
+                      ("t0.7_p0.9_fullsort", SamplerConfig(temperature=0.7, top_p=0.9))):
         wall, dev = time_calls(lambda cfg=cfg: sample_device(lg, cfg, 1234, ctr, tok), steps, warmup)
         out[name] = {"wall_us": round(wall * 1e3, 2), "dev_us": round(dev * 1e3, 2)}
+        if "fullsort" in name:
+            continue
+        # device time without the host: one draw captured in a graph, replayed
+        g = HipGraph()
+        with g.capture():
+            sample_device(lg, cfg, 1234, ctr, tok)
+        _, gdev = time_calls(g.replay, steps, warmup)
+        g.dispose()
+        out[name]["graph_replay_us"] = round(gdev * 1e3, 2)
     for t in (lg, ctr, tok):
         t.dispose()
     return out
+
+
+def bench_stream(new_tokens=64, prompt_len=512):
+    """Config C5 model driven through generate_stream with Qwen3's sampling settings (temperature
+    0.6, top-k 20, top-p 0.95, 10 display candidates): per-token wall time of the whole interactive
+    step -- device sampling, the host reading the step back, and the captured one-token forward --
+    beside greedy generate()'s replayed step."""
+    from kandle_amd.model_utils import GeneratorConfig, Qwen3Config, Qwen3ForCausalLM, init_qwen3_weights
+    from kandle_amd import synthetic as syn
+
+    cfg = Qwen3Config()
+    w = init_qwen3_weights(cfg, seed=7)
+    prompt = syn.randint(8, (prompt_len,), 0, cfg.vocab_size)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=prompt_len + new_tokens + 8)
+    del w
+    gc = GeneratorConfig(max_new_tokens=new_tokens, temperature=0.6, top_k=20, top_p=0.95, display_top_k=10)
+    for _ in model.generate_stream(prompt, GeneratorConfig(max_new_tokens=4)):   # capture the prefill
+        pass
+    times = []
+    t = time.perf_counter()
+    for _ in model.generate_stream(prompt, gc, seed=1):
+        now = time.perf_counter()
+        times.append(now - t)
+        t = now
+    timing = {}
+    model.generate(prompt, new_tokens, timing=timing)
+    model.dispose()
+    steady = times[2:]   # after the prefill step and the step that captures the forward
+    return {"new_tokens": new_tokens, "first_step_ms": round(times[0] * 1e3, 3),
+            "stream_ms_per_token": round(float(np.mean(steady)) * 1e3, 4),
+            "greedy_replay_ms_per_token": round(timing["replay_ms"] / timing["replay_steps"], 4)}
 
 
 def cpu_baseline_sample(reps=20):
@@ -313,7 +356,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample"],
+    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream"],
                     default=None)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -348,6 +391,9 @@ def main():
         res["sample"] = bench_sample(args.steps, args.warmup)
         if args.only == "sample" and not args.no_cpu_baseline:
             res["sample"]["cpu_oracle_us"] = round(cpu_baseline_sample(), 1)
+    if args.only == "stream":
+        log("generate_stream ...")
+        res["stream"] = bench_stream()
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
@@ -430,6 +476,12 @@ def main():
             line.update({"value": round(1e6 / sm["wall_us"], 1), "unit": "draws/s",
                          "ms_per_step": round(sm["wall_us"] * 1e-3, 4),
                          "config": {"workload": "on-device sampling, T=0.7, top-k 50, top-p 0.9, vocab 151936"}})
+    if "stream" in res:
+        st = res["stream"]
+        line.update({"value": round(1e3 / st["stream_ms_per_token"], 1), "unit": "tokens/s",
+                     "ms_per_step": st["stream_ms_per_token"],
+                     "config": {"workload": "C5 Qwen3-0.6B generate_stream, T=0.6 top-k 20 top-p 0.95, 512-token "
+                                            "prompt", **st}})
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 

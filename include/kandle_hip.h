@@ -152,12 +152,19 @@ int kh_greedy_advance(const int32_t* next_token, int32_t* position, int32_t* seq
  * unfiltered softmax(logits / T) as its probabilities (counter may then be NULL).
  * Writes the token (int32), log(q_token + 1e-10) (logprob_out may be NULL) and the first display_k
  * ids of the descending logit order with their probabilities (NULL to skip).
- * counter is a device int32 (a generation loop advances it on the device).  Not capturable.
+ * counter is a device int32 (a generation loop advances it on the device).  Capturable into a
+ * graph except for top-p without top-k, top_k > 1024 or display_k > 1024 (full-sort path).
  * Replaces sample() (reference: packages/model-utils/src/sampling/index.ts:103-243, softmaxCPU
  * :268-291, sampleFromProbs :294-311); the reference draws r with Math.random(). */
 int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperature, int top_k, double top_p,
               uint64_t seed, const int32_t* counter, int32_t* token_out, float* logprob_out, int display_k, int32_t* display_ids,
               float* display_probs);
+
+/* Which kh_sample implementation runs: 0 (default) the selection path wherever it applies (greedy,
+ * top-k <= 1024 with or without top-p, no filter; display_k <= 1024), 1 the full-sort path for
+ * every call.  Both give the same results; the switch lets tests compare them.  No reference
+ * counterpart.  Process-wide, not thread-safe. */
+int kh_sample_set_path(int path);
 
 /* out[4i .. 4i+3] = philox4x32-10(counters[4i .. 4i+3], key = (low, high 32 bits of seed)) for n
  * counters (device arrays).  The generator kh_sample draws from (Salmon et al., SC'11); no

@@ -59,6 +59,7 @@ SIGNATURES = {
     "kh_greedy_advance": [_vp, _vp, _vp, _vp, _i64, _i64],
     "kh_sample": [_vp, _i64, _i, C.c_double, _i, C.c_double, C.c_uint64, _vp, _vp, _vp, _i, _vp, _vp],
     "kh_philox4x32_10": [C.c_uint64, _vp, _i64, _vp],
+    "kh_sample_set_path": [_i],
     "kh_graph_begin_capture": [],
     "kh_graph_end_capture": [_vpp],
     "kh_graph_launch": [_vp],

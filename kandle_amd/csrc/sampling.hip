@@ -21,9 +21,12 @@
 // bits (word 0 >> 8, times 2^-24), with the counter read from device memory so a generation loop can
 // advance it on the device.
 //
-// The sort is rocPRIM's stable radix sort; the f64 sums are two-pass block reductions
-// and hipCUB inclusive scans (deterministic for a given size).  hipCUB may clear its temporary storage
-// with memsets, so kh_sample refuses to run under stream capture.
+// Two implementations give the same results.  The selection path (greedy, top-k <= 1024 with or
+// without top-p, the unfiltered draw; display_k <= 1024) builds only the needed prefix of the order
+// by bitonic selection and runs under graph capture.  Top-p without top-k may cut anywhere in the
+// order, so it (and longer prefixes) takes the full-sort path: rocPRIM's stable radix sort, f64
+// block reductions and hipCUB scans; hipCUB may clear its temporary storage with memsets, so that
+// path refuses to run under stream capture.
 #include <hipcub/hipcub.hpp>
 #include <rocprim/device/device_radix_sort.hpp>
 
@@ -206,6 +209,429 @@ __global__ void init_sel_kernel(int* __restrict__ sel, int n) {
 
 inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
+int g_sample_path = 0;   // 0: selection path where it applies; 1: always the full sort (kh_sample_set_path)
+
+// ---- selection path: the sorted prefix of length m <= kMaxPrefix without sorting the row --------
+//
+// Each id gets a 64-bit key whose descending order is the reference's order: the logit mapped to an
+// order-preserving uint32 in the high word (-0.0 as +0.0), 0xffffffff - id in the low word (lower id
+// first among equal logits).  Keys are distinct, so any sort yields the same order.  A block sorts
+// 1024 or 4096 keys (bitonic, in registers) and keeps its first m; blocks of those survivors are reduced the same
+// way until one block remains: its first m keys are the first m ids of the order.
+
+// Selection blocks sort 1024 keys with 256 threads while m <= 256 (many blocks, short sorts), and
+// 4096 keys with 1024 threads for longer prefixes; each level shrinks the key count 4x or more.
+constexpr int kSelSmall = 1024, kSelSmallThreads = 256;
+constexpr int kSelLarge = 4096, kSelLargeThreads = 1024;
+constexpr int kMaxPrefix = 1024;    // longest prefix the selection path produces
+constexpr int kIdThreads = 512;     // id-order passes: ids per block
+
+__device__ __forceinline__ uint32_t order_bits(float x) {
+  const uint32_t b = __float_as_uint(x == 0.f ? 0.f : x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float order_value(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+__device__ __forceinline__ uint64_t order_key(float x, int id) {
+  return ((uint64_t)order_bits(x) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
+__device__ __forceinline__ float key_logit(uint64_t k) { return order_value((uint32_t)(k >> 32)); }
+
+// x of lane (lane ^ X) within the wave.  Distances 1, 2, 4 and 8 stay inside a 16-lane row and use
+// DPP moves (quad_perm, row_half_mirror then a quad reversal, row_ror:8), which do not occupy the
+// LDS crossbar; 16 and 32 use ds_bpermute.
+template <int X>
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t x) {
+  if constexpr (X == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  } else if constexpr (X == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  } else if constexpr (X == 4) {
+    // row_half_mirror: lane i reads 7 - i (within 8); then quad_perm [3,2,1,0]: lane i reads
+    // i ^ 3; composed, lane i reads 7 - (i ^ 3) = i ^ 4 (within 8)
+    const int h = __builtin_amdgcn_update_dpp((int)x, (int)x, 0x141, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(h, h, 0x1B, 0xF, 0xF, false);
+  } else if constexpr (X == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else {
+    return (uint32_t)__shfl_xor((int)x, X, 64);
+  }
+}
+
+template <int X>
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t x) {
+  return ((uint64_t)lane_xor_u32<X>((uint32_t)(x >> 32)) << 32) | lane_xor_u32<X>((uint32_t)x);
+}
+
+// One compare-exchange against the partner value p: the lower index of the pair keeps the larger
+// value when the pair ends larger-first, the upper index the smaller (branch-free selects).
+template <bool DESC>
+__device__ __forceinline__ uint64_t cx_keep(uint64_t a, uint64_t p, int i, int j, int k) {
+  const bool keep_max = ((i & j) == 0) == (((i & k) == 0) == DESC);
+  return ((a > p) == keep_max) ? a : p;   // one 64-bit compare, two selects
+}
+
+// The in-register and lane-shuffle steps of one (k, j) stage.
+template <int E, int T, bool DESC, int K, int J>
+__device__ __forceinline__ void bitonic_step(uint64_t (&v)[E], uint64_t* lds, int t, int& half) {
+  if constexpr (J < E) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (e & J) continue;
+      const bool up = (((t * E + e) & K) == 0) == DESC;   // the pair ends larger-first
+      const uint64_t a = v[e], b = v[e | J];
+      const bool swap = (a < b) == up;
+      v[e] = swap ? b : a;
+      v[e | J] = swap ? a : b;
+    }
+  } else if constexpr (J < 64 * E) {
+    uint64_t p[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) p[e] = lane_xor_u64<J / E>(v[e]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = cx_keep<DESC>(v[e], p[e], t * E + e, J, K);
+  } else {
+    constexpr int N = E * T;
+    uint64_t* sb = lds + half * N;
+#pragma unroll
+    for (int e = 0; e < E; ++e) sb[t * E + e] = v[e];
+    __syncthreads();
+    uint64_t p[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) p[e] = sb[(t * E + e) ^ J];
+    half ^= 1;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = cx_keep<DESC>(v[e], p[e], t * E + e, J, K);
+  }
+}
+
+template <int E, int T, bool DESC, int K, int J>
+__device__ __forceinline__ void bitonic_merge(uint64_t (&v)[E], uint64_t* lds, int t, int& half) {
+  bitonic_step<E, T, DESC, K, J>(v, lds, t, half);
+  if constexpr (J > 1) bitonic_merge<E, T, DESC, K, J / 2>(v, lds, t, half);
+}
+
+template <int E, int T, bool DESC, int K>
+__device__ __forceinline__ void bitonic_phases(uint64_t (&v)[E], uint64_t* lds, int t, int& half) {
+  bitonic_merge<E, T, DESC, K, K / 2>(v, lds, t, half);
+  if constexpr (K < E * T) bitonic_phases<E, T, DESC, K * 2>(v, lds, t, half);
+}
+
+// Bitonic sort of N = E * T distinct 64-bit values, descending when DESC, by T threads holding E
+// values each in registers (element i = t * E + e in v[e]).  Partners within a thread are swapped in
+// registers, partners within a wave exchanged across lanes, and only partners in other waves
+// (j >= 64 E) go through LDS (lds: 2 N values; consecutive LDS steps alternate halves, so one
+// barrier per step suffices).  When N <= 64 E no barrier is executed and a single wave may call it.
+template <int E, int T, bool DESC>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&v)[E], uint64_t* lds) {
+  int half = 0;
+  bitonic_phases<E, T, DESC, 2>(v, lds, (int)(threadIdx.x % T), half);
+}
+
+// out[blockIdx.x * m + t] (t < m): the m largest keys of chunk blockIdx.x (CHUNK keys), in order.
+// The chunk is logits[base, base + CHUNK) (FROM_LOGITS) or in[base, base + CHUNK); missing entries
+// are key 0, which is below every real key (a real key's low word is 0xffffffff - id > 0).
+template <bool FROM_LOGITS, int CHUNK, int THREADS>
+__global__ __launch_bounds__(THREADS) void select_kernel(const float* __restrict__ logits,
+                                                         const uint64_t* __restrict__ in, int n, int m,
+                                                         uint64_t* __restrict__ out) {
+  constexpr int E = CHUNK / THREADS;
+  __shared__ uint64_t s[2 * CHUNK];
+  const int base = blockIdx.x * CHUNK + threadIdx.x * E;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = base + e;
+    v[e] = 0;
+    if (i < n) v[e] = FROM_LOGITS ? order_key(logits[i], i) : in[i];
+  }
+  bitonic_sort<E, THREADS, true>(v, s);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int r = threadIdx.x * E + e;
+    if (r < m) out[(size_t)blockIdx.x * m + r] = v[e];
+  }
+}
+
+// e_i in id order (stored when e != nullptr) and per-block f64 sums of e, with the largest logit
+// taken from the selected prefix (top[0]).
+__global__ __launch_bounds__(kIdThreads) void exp_ids_kernel(const float* __restrict__ logits, int n,
+                                                             const uint64_t* __restrict__ top, double inv_t,
+                                                             int greedy, float* __restrict__ e,
+                                                             double* __restrict__ part) {
+  __shared__ double red[kIdThreads / 64];
+  const int i = blockIdx.x * kIdThreads + threadIdx.x;
+  const float x0 = key_logit(top[0]);
+  double v = 0.0;
+  if (i < n) {
+    const float x = logits[i];
+    const double arg = greedy ? ((double)x - (double)x0) * inv_t
+                              : (double)scaled_logit(x, inv_t) - (double)scaled_logit(x0, inv_t);
+    const float ef = (float)exp(arg);
+    if (e) e[i] = ef;
+    v = (double)ef;
+  }
+  v = block_sum_f64(v, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = v;
+}
+
+// Sum of part[0..nb) in a fixed order (the same in every block that calls it).
+__device__ __forceinline__ double sum_parts(const double* __restrict__ part, int nb, double* red) {
+  double v = 0.0;
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) v += part[i];
+  return block_sum_f64(v, red);
+}
+
+// Top-k (with or without top-p) and greedy on the selected prefix, one block of kMaxPrefix threads.
+// Every sum the reference runs sequentially is run sequentially here, in the reference's order:
+// the top-p running sum over the order, the kept mass and the draw over ids (ids outside the kept
+// set add exact zeros in the reference).  Only the softmax total Z is a tree sum.
+__global__ __launch_bounds__(kMaxPrefix) void finish_prefix_kernel(
+    const uint64_t* __restrict__ top, int m, const double* __restrict__ part, int nb, double inv_t, int greedy,
+    int k_eff, double top_p, uint64_t seed, const int32_t* __restrict__ counter, int display_k,
+    int32_t* __restrict__ token, float* __restrict__ logprob, int32_t* __restrict__ disp_ids,
+    float* __restrict__ disp_p) {
+  __shared__ double red[kMaxPrefix / 64];
+  __shared__ float p_s[kMaxPrefix];
+  __shared__ int id_s[kMaxPrefix];
+  __shared__ uint64_t by_id[kMaxPrefix];
+  __shared__ uint64_t sort_lds[2 * kMaxPrefix];
+  __shared__ float v_s[kMaxPrefix];
+  __shared__ int cut_s;
+  __shared__ double P_s;
+  const int t = threadIdx.x;
+  const double Z = sum_parts(part, nb, red);
+  const float x0 = key_logit(top[0]);
+  if (t < m) {
+    const uint64_t k = top[t];
+    const float x = key_logit(k);
+    const double arg = greedy ? ((double)x - (double)x0) * inv_t
+                              : (double)scaled_logit(x, inv_t) - (double)scaled_logit(x0, inv_t);
+    const float ef = (float)exp(arg);
+    p_s[t] = (float)((double)ef / Z);
+    id_s[t] = key_id(k);
+  }
+  __syncthreads();
+  if (greedy) {
+    if (t == 0) {
+      *token = id_s[0];
+      if (logprob) *logprob = (float)log((double)p_s[0] + 1e-10);
+    }
+    if (t < display_k) {
+      if (disp_ids) disp_ids[t] = id_s[t];
+      if (disp_p) disp_p[t] = p_s[t];
+    }
+    return;
+  }
+  if (t == 0) {
+    int cut = k_eff;
+    if (top_p < 1.0) {
+      double cum = 0.0;
+#pragma unroll 8
+      for (int j = 0; j < k_eff; ++j) {
+        cum += (double)p_s[j];
+        if (cum >= top_p) {
+          cut = j + 1;
+          break;
+        }
+      }
+    }
+    cut_s = cut;
+  }
+  __syncthreads();
+  const int cut = cut_s;
+  // the kept positions in id order: by_id[j] = (id << 32) | position, ascending; the rest after
+  {
+    uint64_t kv[1] = {t < cut ? (((uint64_t)(uint32_t)id_s[t] << 32) | (uint32_t)t) : ~0ull};
+    if (cut <= 64) {
+      if (t < 64) bitonic_sort<1, 64, false>(kv, nullptr);
+    } else {
+      bitonic_sort<1, kMaxPrefix, false>(kv, sort_lds);
+    }
+    by_id[t] = kv[0];
+  }
+  __syncthreads();
+  // p of the kept ids in id order, summed sequentially (the reference's probs.reduce)
+  if (t < cut) v_s[t] = p_s[(uint32_t)by_id[t]];
+  __syncthreads();
+  if (t == 0) {
+    double P = 0.0;
+#pragma unroll 8
+    for (int j = 0; j < cut; ++j) P += (double)v_s[j];
+    P_s = P;
+  }
+  __syncthreads();
+  const double P = P_s;
+  float q = 0.f;
+  if (t < cut) q = P > 0.0 ? (float)((double)p_s[t] / P) : p_s[t];
+  __syncthreads();   // every p_s read above is done before q replaces it
+  if (t < m) p_s[t] = t < cut ? q : 0.f;
+  __syncthreads();
+  if (t < cut) v_s[t] = p_s[(uint32_t)by_id[t]];   // q of the kept ids in id order
+  __syncthreads();
+  if (t == 0) {
+    uint32_t c[4] = {(uint32_t)*counter, 0u, 0u, 0u};
+    philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    const double r = (double)(c[0] >> 8) * (1.0 / 16777216.0);
+    int pick = -1;
+    double cum = 0.0;
+#pragma unroll 8
+    for (int j = 0; j < cut; ++j) {
+      cum += (double)v_s[j];
+      if (r < cum) {
+        pick = j;
+        break;
+      }
+    }
+    if (pick < 0)   // the last kept id with q > 0
+      for (int j = cut - 1; j >= 0; --j)
+        if (v_s[j] > 0.f) {
+          pick = j;
+          break;
+        }
+    // nothing kept with q > 0: id 0, whose q is then 0 (id 0 is kept only with q == 0)
+    const int pos = pick >= 0 ? (int)(uint32_t)by_id[pick] : -1;
+    *token = pos >= 0 ? id_s[pos] : 0;
+    if (logprob) *logprob = (float)log((double)(pos >= 0 ? p_s[pos] : 0.f) + 1e-10);
+  }
+  if (t < display_k) {
+    if (disp_ids) disp_ids[t] = id_s[t];
+    if (disp_p) disp_p[t] = p_s[t];
+  }
+}
+
+// No filter (top_k off, top_p >= 1): every id is kept, so the renormalisation and the draw run
+// over the whole row in id order.
+// p_i = f32(e_i / Z) in place, per-block f64 sums of p.
+__global__ __launch_bounds__(kIdThreads) void prob_ids_kernel(float* e, int n, const double* __restrict__ zpart,
+                                                              int nb, double* __restrict__ part) {
+  __shared__ double red[kIdThreads / 64];
+  const double Z = sum_parts(zpart, nb, red);
+  const int i = blockIdx.x * kIdThreads + threadIdx.x;
+  double v = 0.0;
+  if (i < n) {
+    const float p = (float)((double)e[i] / Z);
+    e[i] = p;
+    v = (double)p;
+  }
+  v = block_sum_f64(v, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = v;
+}
+
+// q_i = f32(p_i / P) in place; per block the exact sum of q in 2^-62 fixed point (the draw's running
+// sum, exact in any order) and the last id with q > 0 (-1 if none).
+constexpr double kFix = 4611686018427387904.0;   // 2^62
+__global__ __launch_bounds__(kIdThreads) void q_ids_kernel(float* p, int n, const double* __restrict__ ppart, int nb,
+                                                           unsigned long long* __restrict__ qfix_sum,
+                                                           int* __restrict__ last_pos) {
+  __shared__ double red[kIdThreads / 64];
+  __shared__ unsigned long long ured[kIdThreads / 64];
+  __shared__ int lred[kIdThreads / 64];
+  const double P = sum_parts(ppart, nb, red);
+  const int i = blockIdx.x * kIdThreads + threadIdx.x;
+  unsigned long long f = 0;
+  int last = -1;
+  if (i < n) {
+    const float q = P > 0.0 ? (float)((double)p[i] / P) : p[i];
+    p[i] = q;
+    f = (unsigned long long)((double)q * kFix);
+    if (q > 0.f) last = i;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    f += __shfl_xor(f, o, 64);
+    last = max(last, __shfl_xor(last, o, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    ured[threadIdx.x >> 6] = f;
+    lred[threadIdx.x >> 6] = last;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long tot = 0;
+    int l = -1;
+    for (int w = 0; w < kIdThreads / 64; ++w) {
+      tot += ured[w];
+      l = max(l, lred[w]);
+    }
+    qfix_sum[blockIdx.x] = tot;
+    last_pos[blockIdx.x] = l;
+  }
+}
+
+// The draw over the whole row: the first id whose running fixed-point sum of q exceeds
+// r * 2^62, else the last id with q > 0, else 0; one block of 1024 threads.
+__global__ __launch_bounds__(1024) void draw_ids_kernel(const float* __restrict__ q, int n,
+                                                        const unsigned long long* __restrict__ qfix_sum,
+                                                        const int* __restrict__ last_pos, int nb,
+                                                        const uint64_t* __restrict__ top, uint64_t seed,
+                                                        const int32_t* __restrict__ counter, int display_k,
+                                                        int32_t* __restrict__ token, float* __restrict__ logprob,
+                                                        int32_t* __restrict__ disp_ids, float* __restrict__ disp_p) {
+  __shared__ unsigned long long pre[1024];
+  __shared__ int blk_s, pick_s, last_s;
+  const int t = threadIdx.x;
+  uint32_t c[4] = {(uint32_t)*counter, 0u, 0u, 0u};
+  philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+  const unsigned long long R = (unsigned long long)(c[0] >> 8) << 38;   // r * 2^62, exact
+  if (t == 0) {
+    blk_s = nb;
+    pick_s = n;
+    last_s = -1;
+  }
+  // block totals, prefix-summed in chunks of 1024 blocks
+  unsigned long long carry = 0;
+  int blk = -1;
+  for (int b0 = 0; b0 < nb && blk < 0; b0 += 1024) {
+    const int b = b0 + t;
+    pre[t] = b < nb ? qfix_sum[b] : 0ull;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {   // inclusive Hillis-Steele scan (exact integers)
+      const unsigned long long v = t >= o ? pre[t - o] : 0ull;
+      __syncthreads();
+      pre[t] += v;
+      __syncthreads();
+    }
+    if (b < nb && carry + pre[t] > R && (t == 0 || carry + pre[t - 1] <= R)) blk_s = b;
+    if (b < nb) atomicMax(&last_s, last_pos[b]);
+    __syncthreads();
+    if (blk_s < nb) {
+      blk = blk_s;
+      carry += blk == b0 ? 0ull : pre[blk - b0 - 1];
+    } else {
+      carry += pre[1023];
+    }
+    __syncthreads();
+  }
+  if (blk >= 0) {
+    // inside block blk: ids blk*kIdThreads + u
+    const int base = blk * kIdThreads;
+    const int i = base + t;
+    pre[t] = (t < kIdThreads && i < n) ? (unsigned long long)((double)q[i] * kFix) : 0ull;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      const unsigned long long v = t >= o ? pre[t - o] : 0ull;
+      __syncthreads();
+      pre[t] += v;
+      __syncthreads();
+    }
+    if (t < kIdThreads && i < n && carry + pre[t] > R) atomicMin(&pick_s, i);
+    __syncthreads();
+  }
+  if (t == 0) {
+    const int tok = pick_s < n ? pick_s : (last_s >= 0 ? last_s : 0);
+    *token = tok;
+    if (logprob) *logprob = (float)log((double)q[tok] + 1e-10);
+  }
+  if (t < display_k) {
+    const int id = key_id(top[t]);
+    if (disp_ids) disp_ids[t] = id;
+    if (disp_p) disp_p[t] = q[id];
+  }
+}
+
 // rocPRIM's stable radix sort with its default configuration (for a 151,936-id row: a block sort
 // and merge passes, measured faster here than forcing onesweep).
 inline hipError_t sort_desc(void* tmp, size_t& bytes, const float* k_in, float* k_out, const int32_t* v_in,
@@ -216,6 +642,12 @@ inline hipError_t sort_desc(void* tmp, size_t& bytes, const float* k_in, float* 
 }  // namespace
 
 extern "C" {
+
+int kh_sample_set_path(int path) {
+  KH_REQUIRE(path == 0 || path == 1, "kh_sample_set_path: path must be 0 (automatic) or 1 (full sort)");
+  g_sample_path = path;
+  return KH_OK;
+}
 
 int kh_philox4x32_10(uint64_t seed, const uint32_t* counters, int64_t n, uint32_t* out) {
   KH_REQUIRE_INIT();
@@ -228,6 +660,71 @@ int kh_philox4x32_10(uint64_t seed, const uint32_t* counters, int64_t n, uint32_
   return KH_OK;
 }
 
+// The selection path (prefix of m <= kMaxPrefix ids; see select_kernel): greedy, top-k with or
+// without top-p, and the unfiltered draw.
+static int sample_selected(const float* logits, int n, int greedy, double inv_t, int k_eff, double top_p, int m,
+                           uint64_t seed, const int32_t* counter, int32_t* token_out, float* logprob_out,
+                           int display_k, int32_t* display_ids, float* display_probs) {
+  const bool small = m <= kSelSmall / 4;
+  const int chunk = small ? kSelSmall : kSelLarge;
+  const int nsel = (n + chunk - 1) / chunk;
+  const int nb = (n + kIdThreads - 1) / kIdThreads;
+  const bool plain = !greedy && k_eff == n && top_p >= 1.0;
+  const size_t sz_sel = align256((size_t)nsel * m * 8), sz_nb = align256((size_t)nb * 8);
+  const size_t total = 2 * sz_sel + (plain ? align256((size_t)n * 4) + 3 * sz_nb + align256((size_t)nb * 4) : sz_nb);
+  char* ws = (char*)scratch_alloc(total);
+  if (!ws) return KH_ERR_OOM;
+  char* cur = ws;
+  auto take = [&](size_t b) { char* p = cur; cur += b; return p; };
+  uint64_t* src = (uint64_t*)take(sz_sel);
+  uint64_t* dst = (uint64_t*)take(sz_sel);
+  double* zpart = (double*)take(sz_nb);
+
+  if (small)
+    select_kernel<true, kSelSmall, kSelSmallThreads><<<nsel, kSelSmallThreads, 0, stream()>>>(logits, nullptr, n, m,
+                                                                                              src);
+  else
+    select_kernel<true, kSelLarge, kSelLargeThreads><<<nsel, kSelLargeThreads, 0, stream()>>>(logits, nullptr, n, m,
+                                                                                              src);
+  for (int blocks = nsel; blocks > 1;) {
+    const int cnt = blocks * m;
+    blocks = (cnt + chunk - 1) / chunk;
+    if (small)
+      select_kernel<false, kSelSmall, kSelSmallThreads><<<blocks, kSelSmallThreads, 0, stream()>>>(nullptr, src, cnt,
+                                                                                                   m, dst);
+    else
+      select_kernel<false, kSelLarge, kSelLargeThreads><<<blocks, kSelLargeThreads, 0, stream()>>>(nullptr, src, cnt,
+                                                                                                   m, dst);
+    uint64_t* t = src;
+    src = dst;
+    dst = t;
+  }
+  const uint64_t* top = src;   // the first m ids of the order
+  if (!plain) {
+    exp_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(logits, n, top, inv_t, greedy, nullptr, zpart);
+    finish_prefix_kernel<<<1, kMaxPrefix, 0, stream()>>>(top, m, zpart, nb, inv_t, greedy, k_eff, top_p, seed, counter,
+                                                         display_k, token_out, logprob_out, display_ids,
+                                                         display_probs);
+  } else {
+    float* e = (float*)take(align256((size_t)n * 4));   // e, then p, then q (id order)
+    double* ppart = (double*)take(sz_nb);
+    unsigned long long* qfix = (unsigned long long*)take(sz_nb);
+    int* last = (int*)take(align256((size_t)nb * 4));
+    exp_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(logits, n, top, inv_t, 0, e, zpart);
+    prob_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(e, n, zpart, nb, ppart);
+    q_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(e, n, ppart, nb, qfix, last);
+    draw_ids_kernel<<<1, 1024, 0, stream()>>>(e, n, qfix, last, nb, top, seed, counter, display_k, token_out,
+                                              logprob_out, display_ids, display_probs);
+  }
+  const hipError_t err = hipGetLastError();
+  scratch_free(ws);  // stream-ordered: reused only by later work on the same stream
+  if (err != hipSuccess) {
+    set_error("kh_sample: launch failed: %s", hipGetErrorString(err));
+    return KH_ERR_HIP;
+  }
+  return KH_OK;
+}
+
 int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperature, int top_k, double top_p,
               uint64_t seed, const int32_t* counter, int32_t* token_out, float* logprob_out, int display_k, int32_t* display_ids,
               float* display_probs) {
@@ -236,14 +733,26 @@ int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperat
   KH_REQUIRE(logits && token_out && (counter || !do_sample), "kh_sample: null pointer");
   KH_REQUIRE(temperature > 0.0, "kh_sample: temperature must be positive (got %g)", temperature);
   KH_REQUIRE(display_k >= 0 && display_k <= vocab, "kh_sample: display_k %d out of [0, vocab]", display_k);
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  KH_CHECK_HIP(hipStreamIsCapturing(stream(), &cap));
-  KH_REQUIRE(cap == hipStreamCaptureStatusNone, "kh_sample: not supported under stream capture");
   const int n = (int)vocab;
   const int nb = (n + kThreads - 1) / kThreads;
   const int greedy = do_sample ? 0 : 1;
   const int k_eff = (!greedy && top_k > 0 && top_k < n) ? top_k : n;
   const double inv_t = 1.0 / temperature;
+  // The selection path needs the order only up to m = max(display_k, 1, top-k); top-p without
+  // top-k may cut anywhere in the order and takes the full sort below.
+  int m = display_k > 1 ? display_k : 1;
+  if (k_eff < n && k_eff > m) m = k_eff;
+  const bool topp_only = !greedy && k_eff == n && top_p < 1.0;
+  if (!topp_only && m <= kMaxPrefix && g_sample_path != 1)
+    return sample_selected(logits, n, greedy, inv_t, k_eff, top_p, m, seed, counter, token_out, logprob_out,
+                           display_k, display_ids, display_probs);
+  // The full-sort path calls rocPRIM / hipCUB, which may clear their temporary storage with
+  // memsets: it is not captured into graphs.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  KH_CHECK_HIP(hipStreamIsCapturing(stream(), &cap));
+  KH_REQUIRE(cap == hipStreamCaptureStatusNone,
+             "kh_sample: top-p without top-k, top-k > 1024 or display_k > 1024 is not supported under stream "
+             "capture");
 
   // temporary storage sizes of the hipCUB calls
   size_t sort_bytes = 0, scan_bytes = 0;

@@ -592,6 +592,12 @@ def sample(logits, params: dict):
               ptr(ctr), _vp(tok.data_ptr()), ptr(params.get("logprob")), dk, ptr(dids), ptr(dprobs))
 
 
+def sample_set_path(path: int) -> None:
+    """Select kh_sample's implementation: 0 the selection path where it applies (default), 1 the
+    full sort for every call (both give the same results; used by tests)."""
+    _lib.call("kh_sample_set_path", int(path))
+
+
 def philox4x32_10(seed: int, counters, out) -> None:
     """out[i] = philox4x32-10(counters[i], key = seed) for uint32 [n, 4] device tensors (int32 storage)."""
     if counters.numel % 4 or out.numel != counters.numel:

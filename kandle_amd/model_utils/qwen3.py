@@ -433,29 +433,41 @@ class Qwen3ForCausalLM:
         sampled one); generation stops after max_new_tokens steps or at an EOS token.
 
         The draw of step i uses r = philox4x32-10(seed, counter = i), so a (seed, prompt, config)
-        triple replays the same tokens (the reference draws with Math.random()).  With use_graph the
-        one-token forward is captured once and replayed with the token, position and KV length in
-        device memory.  The reference's extra forward after the last step (its result unused) is
-        not run."""
-        from .sampling import SamplerConfig, sample
+        triple replays the same tokens (the reference draws with Math.random()).  The token fed
+        back, its position, the KV length and the counter live in one device buffer written with
+        one copy per step; the step's outputs are read back with one copy.  With use_graph the
+        one-token forward and the draw are captured together once and replayed (except for top-p
+        without top-k and prefixes over 1024 ids, whose full sort is not capturable: then only the
+        forward is captured).  The reference's extra forward after the last step (its result
+        unused) is not run."""
+        from .sampling import SampleOutputs, SamplerConfig, sample_device
 
         cfg = config or GeneratorConfig()
         prompt = np.asarray(input_ids, np.int32).reshape(-1)
         P, N = int(prompt.size), int(cfg.max_new_tokens)
         eos = set(int(t) for t in cfg.eos_token_ids)
+        k = min(int(cfg.display_top_k), self.cfg.vocab_size)
         sampler = SamplerConfig(cfg.temperature, cfg.top_k, cfg.top_p, cfg.do_sample)
+        top_p_only = cfg.do_sample and cfg.top_p < 1.0 and not 0 < cfg.top_k < self.cfg.vocab_size
+        capture_draw = not top_p_only and k <= 1024 and not (cfg.do_sample and cfg.top_k > 1024)
         self.cache.reset()
         self.cache.check_write(0, P + max(N, 1))
         logits, owned = self._prefill(prompt, use_graph)
-        st = DecodeState(*(Tensor(np.zeros(1, np.int32), dtype="int32") for _ in range(3)),
-                         Tensor(np.zeros(1, np.int32), dtype="int32"), P)
+        state = Tensor(np.zeros(4, np.int32), dtype="int32")   # token, position, KV length, counter
+        ids, pos, lens, ctr = (F.narrow(state, 0, i, 1) for i in range(4))
+        st = DecodeState(ids, pos, lens, None, P)
+        out = SampleOutputs(k)
+        draw = lambda lg: sample_device(lg, sampler, seed, ctr, out.token, k, out.logprob, out.ids,  # noqa: E731
+                                        out.probs)
         graph, g_logits = None, None
         try:
             for i in range(N):
-                res = sample(logits, sampler, cfg.display_top_k, seed=seed, counter=i)
-                if owned:
-                    logits.dispose()
-                logits, owned = None, False
+                if logits is not None:   # eager step (or a replay whose draw is not captured)
+                    draw(logits)
+                    if owned:
+                        logits.dispose()
+                    logits, owned = None, False
+                res = out.read()
                 override = yield GenerationStep(res.token_id, res.log_prob, res.top_k_token_ids, res.top_k_probs,
                                                 res.token_id in eos, P + i, i + 1)
                 tok = int(override) if override is not None else res.token_id
@@ -463,18 +475,18 @@ class Qwen3ForCausalLM:
                     break
                 if not 0 <= tok < self.cfg.vocab_size:
                     raise ValueError(f"generate_stream: token id {tok} outside [0, {self.cfg.vocab_size})")
-                for t, v in ((st.ids, tok), (st.pos, P + i), (st.lens, P + i + 1)):
-                    t.handle.storage.upload(np.array([v], np.int32))
-                if not use_graph:
+                state.handle.storage.upload(np.array([tok, P + i, P + i + 1, i + 1], np.int32))
+                if not use_graph or graph is None:
                     logits, owned = self._step_logits(st), True
-                elif graph is None:
-                    logits, owned = self._step_logits(st), True
-                    graph = HipGraph()
-                    with graph.capture():
-                        g_logits = self._step_logits(st)
+                    if use_graph:   # capture records without running: replays serve the next steps
+                        graph = HipGraph()
+                        with graph.capture():
+                            g_logits = self._step_logits(st)
+                            if capture_draw:
+                                draw(g_logits)
                 else:
                     graph.replay()
-                    logits = g_logits
+                    logits = None if capture_draw else g_logits
                 self.cache.mark_written(P + i + 1)
         finally:
             if owned and logits is not None:
@@ -483,7 +495,9 @@ class Qwen3ForCausalLM:
                 g_logits.dispose()
             if graph is not None:
                 graph.dispose()
-            st.dispose()
+            out.dispose()
+            for t in (ids, pos, lens, ctr, state):
+                t.dispose()
 
     def dispose(self) -> None:
         for graph, ids_buf, pos_buf, g_logits in self._prefill_graphs.values():

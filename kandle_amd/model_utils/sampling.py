@@ -74,32 +74,51 @@ def sample_device(logits: Tensor, config: SamplerConfig, seed: int, counter: Opt
             v.dispose()
 
 
+class SampleOutputs:
+    """Device outputs of one draw in a single int32-sized storage, read back with one copy:
+    token (int32), log-probability (float32), k display ids (int32), k display probabilities
+    (float32)."""
+
+    def __init__(self, k: int):
+        self.k = k
+        kk = max(k, 1)
+        self._buf = Tensor(np.zeros(2 + 2 * kk, np.int32), dtype="int32")
+        st = self._buf.handle.storage
+        view = lambda off, n, dt: Tensor(handle=HipTensorHandle.create_view(st, (n,), dt, (1,), off))  # noqa: E731
+        self.token, self.logprob = view(0, 1, "int32"), view(1, 1, "float32")
+        self.ids, self.probs = view(2, kk, "int32"), view(2 + kk, kk, "float32")
+
+    def read(self) -> SampleResult:
+        kk = max(self.k, 1)
+        raw = self._buf.handle.storage.download(4 * (2 + 2 * kk))
+        w = raw.view(np.int32)
+        f = raw.view(np.float32)
+        return SampleResult(int(w[0]), float(f[1]), [int(i) for i in w[2:2 + self.k]],
+                            f[2 + kk:2 + kk + self.k].copy())
+
+    def dispose(self) -> None:
+        for t in (self.token, self.logprob, self.ids, self.probs, self._buf):
+            t.dispose()
+
+
 def sample(logits: Tensor, config: Optional[SamplerConfig] = None, display_top_k: int = 10, seed: int = 0,
            counter: Union[int, Tensor] = 0) -> SampleResult:
     """sample() (sampling/index.ts:103-243): the token, its log-probability and the display_top_k
     most likely ids with their probabilities.  Greedy (do_sample=False) takes the lowest id of the
     largest logit and reports the unfiltered softmax of logits / temperature, as the reference does."""
     config = config or SamplerConfig()
-    vocab = logits.shape[-1]
-    k = min(display_top_k, vocab)
+    k = min(display_top_k, logits.shape[-1])
     own_ctr = config.do_sample and not isinstance(counter, Tensor)
     ctr = Tensor(np.array([counter], np.int32), dtype="int32") if own_ctr else (
         counter if isinstance(counter, Tensor) else None)
-    outs = [Tensor(handle=HipTensorHandle.create_new(shape, dt))
-            for shape, dt in (((1,), "int32"), ((1,), "float32"), ((max(k, 1),), "int32"), ((max(k, 1),), "float32"))]
-    tokT, lpT, didsT, dprobsT = outs
+    out = SampleOutputs(k)
     try:
-        sample_device(logits, config, seed, ctr, tokT, k, lpT, didsT, dprobsT)
-        token = int(tokT.numpy()[0])
-        log_prob = float(lpT.numpy()[0])
-        ids = [int(i) for i in didsT.numpy()[:k]]
-        probs = dprobsT.numpy()[:k].astype(np.float32)
+        sample_device(logits, config, seed, ctr, out.token, k, out.logprob, out.ids, out.probs)
+        return out.read()
     finally:
-        for t in outs:
-            t.dispose()
+        out.dispose()
         if own_ctr:
             ctr.dispose()
-    return SampleResult(token, log_prob, ids, probs)
 
 
 def sample_greedy(logits: Tensor, display_top_k: int = 10) -> SampleResult:

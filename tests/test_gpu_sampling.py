@@ -165,15 +165,16 @@ def test_generate_stream_sampled_steps_follow_reference(hip, monkeypatch):
     cfg, w, model = _small_model()
     prompt = syn.randint(6, (40,), 0, cfg.vocab_size)
     seen = []
-    real = S.sample
+    real = S.sample_device
 
-    def spy(logits, config=None, display_top_k=10, seed=0, counter=0):
-        seen.append((logits.numpy().reshape(-1).copy(), seed, counter))
-        return real(logits, config, display_top_k, seed, counter)
+    def spy(logits, config, seed, counter, *args, **kw):
+        # eager steps only (use_graph=False): the logits and the counter as the draw reads them
+        seen.append((logits.numpy().reshape(-1).copy(), seed, int(counter.numpy()[0])))
+        return real(logits, config, seed, counter, *args, **kw)
 
-    monkeypatch.setattr(S, "sample", spy)
+    monkeypatch.setattr(S, "sample_device", spy)
     gc = GeneratorConfig(max_new_tokens=6, temperature=0.8, top_k=50, top_p=0.9, display_top_k=5)
-    steps = _drive(model.generate_stream(prompt, gc, seed=7), overrides={2: 123})
+    steps = _drive(model.generate_stream(prompt, gc, seed=7, use_graph=False), overrides={2: 123})
     model.dispose()
     assert len(steps) == 6 and len(seen) == 6
     fed = [s.token_id for s in steps]
@@ -228,3 +229,56 @@ def test_generate_stream_graph_replay_matches_eager(hip):
     for x, y in zip(a, b):
         assert x.top_k_token_ids == y.top_k_token_ids and np.array_equal(x.top_k_probs, y.top_k_probs)
     assert [s.token_id for s in c] != [s.token_id for s in a]   # another seed, another draw
+    # top-p without top-k: the draw takes the full sort, which stays outside the captured graph
+    gp = GeneratorConfig(max_new_tokens=5, temperature=0.9, top_p=0.8, display_top_k=3)
+    cfg2, w2, model2 = _small_model(seed=12)
+    d = _drive(model2.generate_stream(prompt, gp, seed=5, use_graph=False))
+    e = _drive(model2.generate_stream(prompt, gp, seed=5, use_graph=True))
+    model2.dispose()
+    assert [s.token_id for s in d] == [s.token_id for s in e]
+    assert all(np.array_equal(x.top_k_probs, y.top_k_probs) for x, y in zip(d, e))
+
+
+# ---- the selection path (sorted prefix by LDS bitonic selection) against the full sort ------------
+
+def _both_paths(x, cfg, seed, counter, display_k):
+    outs = []
+    for path in (1, 0):
+        kernels.sample_set_path(path)
+        try:
+            lg = Tensor(x, dtype="float32")
+            outs.append(sample(lg, cfg, display_k, seed=seed, counter=counter))
+            lg.dispose()
+        finally:
+            kernels.sample_set_path(0)
+    return outs
+
+
+@pytest.mark.parametrize("n", [1, 100, 4095, 4096, 4097, 40000, VOCAB])
+def test_selection_path_matches_sort_path_sizes(hip, n):
+    x = _logits(20 + n, n=n, scale=2.5)
+    dk = min(10, n)
+    for cfg in (SamplerConfig(do_sample=False), SamplerConfig(), SamplerConfig(temperature=0.7, top_k=min(50, n)),
+                SamplerConfig(temperature=1.2, top_k=min(20, n), top_p=0.8)):
+        for c in range(3):
+            a, b = _both_paths(x, cfg, 5, c, dk)
+            assert a.top_k_token_ids == b.top_k_token_ids
+            np.testing.assert_allclose(b.top_k_probs, a.top_k_probs, rtol=2e-6, atol=1e-30)
+            _check(x, cfg, 5, c, dk)   # and both against the reference restatement
+
+
+def test_selection_path_limits_and_ties(hip):
+    x = _logits(30, n=50000, scale=1.0)
+    # the longest prefix the selection path builds, and one past it (full sort)
+    for k, dk in ((1024, 10), (1025, 10), (40, 1024), (40, 1025)):
+        _check(x, SamplerConfig(temperature=0.9, top_k=k, top_p=0.97), 3, 1, dk)
+    # all logits equal: the order is the ids, the prefix the lowest ids
+    flat = np.full(20000, 1.5, np.float32)
+    for cfg in (SamplerConfig(do_sample=False), SamplerConfig(top_k=300), SamplerConfig()):
+        res = _check(flat, cfg, 2, 7, 16)
+        assert res.top_k_token_ids == list(range(16))
+    # ties straddling selection chunks: equal maxima at ids in different 4096-id chunks
+    y = _logits(31, n=30000, scale=1.0)
+    y[[29999, 4096, 4095, 12000]] = 9.0
+    res = _check(y, SamplerConfig(top_k=3), 4, 0, 5)
+    assert res.top_k_token_ids[:4] == [4095, 4096, 12000, 29999]
