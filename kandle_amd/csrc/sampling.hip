@@ -21,13 +21,18 @@
 // bits (word 0 >> 8, times 2^-24), with the counter read from device memory so a generation loop can
 // advance it on the device.
 //
+// Running sums.  Sums over a kept set of at most 1024 ids (top-k) run sequentially in f64 in the
+// reference's order, as the JavaScript loops do.  Sums over a larger set (the unfiltered draw, top-p
+// without top-k) run in exact 2^-62 fixed point, in any order; they differ from the reference's
+// sequential f64 sums by rounding only (about 1e-16 per term).  Z and P over large sets are f64 tree
+// sums in a fixed order, so every result is deterministic.
+//
 // Two implementations give the same results.  The selection path (greedy, top-k <= 1024 with or
 // without top-p, the unfiltered draw; display_k <= 1024) builds only the needed prefix of the order
 // by bitonic selection and runs under graph capture.  Top-p without top-k may cut anywhere in the
-// order, so it (and longer prefixes) takes the full-sort path: rocPRIM's stable radix sort, f64
-// block reductions and hipCUB scans; hipCUB may clear its temporary storage with memsets, so that
-// path refuses to run under stream capture.
-#include <hipcub/hipcub.hpp>
+// order, so it (and longer prefixes) takes the full-sort path: rocPRIM's stable radix sort, then
+// the top-p cut and the draw found from the fixed-point block sums; rocPRIM may clear its temporary
+// storage with memsets, so that path refuses to run under stream capture.
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include "common.h"
@@ -121,90 +126,6 @@ __global__ __launch_bounds__(kThreads) void final_sum_kernel(const double* __res
   for (int i = threadIdx.x; i < nb; i += blockDim.x) v += part[i];
   v = block_sum_f64(v, red);
   if (threadIdx.x == 0) *out = v;
-}
-
-// p (sorted order) = f32(e / Z), stored as f64 for the top-p scan.
-// (p may be e itself: each element is read, then overwritten.)
-__global__ void prob_kernel(const float* e, int n, const double* __restrict__ Z, float* p, double* __restrict__ p64) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) {
-    const float pf = (float)((double)e[i] / *Z);
-    p[i] = pf;
-    p64[i] = (double)pf;
-  }
-}
-
-// cut[0] = number of kept sorted positions: the first j < k_eff with cum[j] >= top_p gives j + 1
-// (minimum over threads); k_eff when no position reaches top_p.  cut[0] starts at k_eff.
-__global__ void topp_cut_kernel(const double* __restrict__ cum, int k_eff, double top_p, int* __restrict__ cut) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j < k_eff && cum[j] >= top_p) atomicMin(cut, j + 1);
-}
-
-__global__ void fill_int_kernel(int* __restrict__ p, int v) { *p = v; }
-
-// Per-block f64 sums of the kept p (sorted positions < cut).
-__global__ __launch_bounds__(kThreads) void kept_sum_kernel(const float* __restrict__ p, int n,
-                                                            const int* __restrict__ cut, double* __restrict__ part) {
-  __shared__ double red[kThreads / 64];
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const double v = (i < n && i < *cut) ? (double)p[i] : 0.0;
-  const double s = block_sum_f64(v, red);
-  if (threadIdx.x == 0) part[blockIdx.x] = s;
-}
-
-// q in id order: q[id] = f32(p / P) for kept sorted positions (p itself when P == 0 or when not
-// renormalising), 0 otherwise; also the f64 copy for the id-order scan.
-__global__ void scatter_q_kernel(const float* __restrict__ p, const int32_t* __restrict__ sorted_ids, int n,
-                                 const int* __restrict__ cut, const double* __restrict__ P, int renorm,
-                                 float* __restrict__ q, double* __restrict__ q64) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  const int id = sorted_ids[j];
-  float v = 0.f;
-  if (j < *cut) v = (renorm && *P > 0.0) ? (float)((double)p[j] / *P) : p[j];
-  q[id] = v;
-  q64[id] = (double)v;
-}
-
-// sel[0] = min id with r < cum[id]; sel[1] = max id with q[id] > 0 (the fallback); r from Philox.
-// One atomic per wave: the wave's lowest (highest) qualifying id, found from a ballot.
-__global__ void draw_kernel(const double* __restrict__ cum, const float* __restrict__ q, int n, uint64_t seed,
-                            const int32_t* __restrict__ counter, int* __restrict__ sel) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const int lane = threadIdx.x & 63;
-  uint32_t c[4] = {(uint32_t)*counter, 0u, 0u, 0u};
-  philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
-  const double r = (double)(c[0] >> 8) * (1.0 / 16777216.0);
-  const bool in = i < n;
-  const uint64_t hit = __ballot(in && r < cum[in ? i : 0]);
-  const uint64_t pos = __ballot(in && q[in ? i : 0] > 0.f);
-  const int base = i - lane;
-  if (lane == 0 && hit) atomicMin(&sel[0], base + __ffsll((unsigned long long)hit) - 1);
-  if (lane == 0 && pos) atomicMax(&sel[1], base + 63 - __clzll((unsigned long long)pos));
-}
-
-// token: greedy -> the first id of the order; sampling -> the draw, else the fallback, else 0.
-__global__ void finish_kernel(const int* __restrict__ sel, const float* __restrict__ q,
-                              const int32_t* __restrict__ sorted_ids, int n, int greedy, int display_k,
-                              int32_t* __restrict__ token, float* __restrict__ logprob, int32_t* __restrict__ disp_ids,
-                              float* __restrict__ disp_p) {
-  const int t = threadIdx.x;
-  if (t == 0) {
-    const int tok = greedy ? sorted_ids[0] : (sel[0] < n ? sel[0] : (sel[1] >= 0 ? sel[1] : 0));
-    *token = tok;
-    if (logprob) *logprob = (float)log((double)q[tok] + 1e-10);
-  }
-  for (int j = t; j < display_k; j += blockDim.x) {
-    const int id = sorted_ids[j];
-    if (disp_ids) disp_ids[j] = id;
-    if (disp_p) disp_p[j] = q[id];
-  }
-}
-
-__global__ void init_sel_kernel(int* __restrict__ sel, int n) {
-  sel[0] = n;   // "no id yet" for the min
-  sel[1] = -1;  // "no id yet" for the max
 }
 
 inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
@@ -523,20 +444,25 @@ __global__ __launch_bounds__(kIdThreads) void prob_ids_kernel(float* e, int n, c
 // q_i = f32(p_i / P) in place; per block the exact sum of q in 2^-62 fixed point (the draw's running
 // sum, exact in any order) and the last id with q > 0 (-1 if none).
 constexpr double kFix = 4611686018427387904.0;   // 2^62
+__device__ __forceinline__ unsigned long long fix62(float x) { return (unsigned long long)((double)x * kFix); }
+// (ppart == nullptr: p already holds the final q; only the sums are formed.)
 __global__ __launch_bounds__(kIdThreads) void q_ids_kernel(float* p, int n, const double* __restrict__ ppart, int nb,
                                                            unsigned long long* __restrict__ qfix_sum,
                                                            int* __restrict__ last_pos) {
   __shared__ double red[kIdThreads / 64];
   __shared__ unsigned long long ured[kIdThreads / 64];
   __shared__ int lred[kIdThreads / 64];
-  const double P = sum_parts(ppart, nb, red);
+  const double P = ppart ? sum_parts(ppart, nb, red) : 0.0;
   const int i = blockIdx.x * kIdThreads + threadIdx.x;
   unsigned long long f = 0;
   int last = -1;
   if (i < n) {
-    const float q = P > 0.0 ? (float)((double)p[i] / P) : p[i];
-    p[i] = q;
-    f = (unsigned long long)((double)q * kFix);
+    float q = p[i];
+    if (ppart) {
+      q = P > 0.0 ? (float)((double)q / P) : q;
+      p[i] = q;
+    }
+    f = fix62(q);
     if (q > 0.f) last = i;
   }
 #pragma unroll
@@ -561,75 +487,168 @@ __global__ __launch_bounds__(kIdThreads) void q_ids_kernel(float* p, int n, cons
   }
 }
 
-// The draw over the whole row: the first id whose running fixed-point sum of q exceeds
-// r * 2^62, else the last id with q > 0, else 0; one block of 1024 threads.
+// One block of 1024 threads: over the values load(0 .. count) (nonnegative integers), the first
+// index at which base plus the inclusive running sum exceeds target (STRICT) or reaches it; count
+// if none.  *before gets base plus the running sum ahead of that index (the total if none).  Exact
+// integer sums make the running sum monotone, so the first crossing is unique.  pre: 1024 LDS
+// words, res: one LDS int.  Every thread returns the same values.
+template <bool STRICT, typename Load>
+__device__ int first_crossing(Load load, int count, unsigned long long base, unsigned long long target,
+                              unsigned long long* pre, int* res, unsigned long long* before) {
+  const int t = threadIdx.x;
+  unsigned long long carry = base;
+  int found = -1;
+  for (int c0 = 0; c0 < count && found < 0; c0 += 1024) {
+    const int i = c0 + t;
+    pre[t] = i < count ? load(i) : 0ull;
+    if (t == 0) *res = -1;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {   // inclusive Hillis-Steele scan
+      const unsigned long long v = t >= o ? pre[t - o] : 0ull;
+      __syncthreads();
+      pre[t] += v;
+      __syncthreads();
+    }
+    const unsigned long long incl = carry + pre[t], excl = carry + (t ? pre[t - 1] : 0ull);
+    const bool hit = STRICT ? incl > target : incl >= target;
+    const bool hit_before = STRICT ? excl > target : excl >= target;
+    if (i < count && hit && !hit_before) *res = i;
+    __syncthreads();
+    found = *res;
+    carry += found >= 0 ? (found == c0 ? 0ull : pre[found - c0 - 1]) : pre[1023];
+    __syncthreads();
+  }
+  *before = carry;
+  return found < 0 ? count : found;
+}
+
+// The draw over the whole row in id order (q: kIdThreads-id blocks with fixed-point totals
+// qfix_sum and last positive ids last_pos): the first id whose running fixed-point sum of q exceeds
+// r * 2^62, else the last id with q > 0, else 0.  Greedy: the first id of the order.  Display: the
+// first display_k ids of the order (top keys or sorted ids) with q.  One block of 1024 threads.
 __global__ __launch_bounds__(1024) void draw_ids_kernel(const float* __restrict__ q, int n,
                                                         const unsigned long long* __restrict__ qfix_sum,
-                                                        const int* __restrict__ last_pos, int nb,
-                                                        const uint64_t* __restrict__ top, uint64_t seed,
+                                                        const int* __restrict__ last_pos, int nb, int greedy,
+                                                        const uint64_t* __restrict__ top,
+                                                        const int32_t* __restrict__ sorted_ids, uint64_t seed,
                                                         const int32_t* __restrict__ counter, int display_k,
                                                         int32_t* __restrict__ token, float* __restrict__ logprob,
                                                         int32_t* __restrict__ disp_ids, float* __restrict__ disp_p) {
   __shared__ unsigned long long pre[1024];
-  __shared__ int blk_s, pick_s, last_s;
+  __shared__ int res_s, last_s;
   const int t = threadIdx.x;
-  uint32_t c[4] = {(uint32_t)*counter, 0u, 0u, 0u};
-  philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
-  const unsigned long long R = (unsigned long long)(c[0] >> 8) << 38;   // r * 2^62, exact
-  if (t == 0) {
-    blk_s = nb;
-    pick_s = n;
-    last_s = -1;
-  }
-  // block totals, prefix-summed in chunks of 1024 blocks
-  unsigned long long carry = 0;
-  int blk = -1;
-  for (int b0 = 0; b0 < nb && blk < 0; b0 += 1024) {
-    const int b = b0 + t;
-    pre[t] = b < nb ? qfix_sum[b] : 0ull;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {   // inclusive Hillis-Steele scan (exact integers)
-      const unsigned long long v = t >= o ? pre[t - o] : 0ull;
+  auto order_id = [&](int j) { return top ? key_id(top[j]) : sorted_ids[j]; };
+  int tok = 0;
+  if (greedy) {
+    tok = order_id(0);
+  } else {
+    uint32_t c[4] = {(uint32_t)*counter, 0u, 0u, 0u};
+    philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    const unsigned long long R = (unsigned long long)(c[0] >> 8) << 38;   // r * 2^62, exact
+    unsigned long long carry = 0;
+    const int blk = first_crossing<true>([&](int b) { return qfix_sum[b]; }, nb, 0ull, R, pre, &res_s, &carry);
+    if (blk < nb) {
+      const int base = blk * kIdThreads, cnt = min(kIdThreads, n - base);
+      unsigned long long unused = 0;
+      tok = base + first_crossing<true>([&](int u) { return fix62(q[base + u]); }, cnt, carry, R, pre, &res_s,
+                                        &unused);
+    } else {   // r beyond the total: the last id with q > 0, else 0
+      if (t == 0) last_s = -1;
       __syncthreads();
-      pre[t] += v;
+      int l = -1;
+      for (int b = t; b < nb; b += 1024) l = max(l, last_pos[b]);
+      atomicMax(&last_s, l);
       __syncthreads();
+      tok = last_s >= 0 ? last_s : 0;
     }
-    if (b < nb && carry + pre[t] > R && (t == 0 || carry + pre[t - 1] <= R)) blk_s = b;
-    if (b < nb) atomicMax(&last_s, last_pos[b]);
-    __syncthreads();
-    if (blk_s < nb) {
-      blk = blk_s;
-      carry += blk == b0 ? 0ull : pre[blk - b0 - 1];
-    } else {
-      carry += pre[1023];
-    }
-    __syncthreads();
-  }
-  if (blk >= 0) {
-    // inside block blk: ids blk*kIdThreads + u
-    const int base = blk * kIdThreads;
-    const int i = base + t;
-    pre[t] = (t < kIdThreads && i < n) ? (unsigned long long)((double)q[i] * kFix) : 0ull;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-      const unsigned long long v = t >= o ? pre[t - o] : 0ull;
-      __syncthreads();
-      pre[t] += v;
-      __syncthreads();
-    }
-    if (t < kIdThreads && i < n && carry + pre[t] > R) atomicMin(&pick_s, i);
-    __syncthreads();
   }
   if (t == 0) {
-    const int tok = pick_s < n ? pick_s : (last_s >= 0 ? last_s : 0);
     *token = tok;
     if (logprob) *logprob = (float)log((double)q[tok] + 1e-10);
   }
-  if (t < display_k) {
-    const int id = key_id(top[t]);
-    if (disp_ids) disp_ids[t] = id;
-    if (disp_p) disp_p[t] = q[id];
+  for (int j = t; j < display_k; j += 1024) {
+    const int id = order_id(j);
+    if (disp_ids) disp_ids[j] = id;
+    if (disp_p) disp_p[j] = q[id];
   }
+}
+
+// ---- full-sort path kernels (positions j index the descending order) ----------------------------
+
+// p_j = f32(e_j / Z) in place; per kThreads-position block, over positions j < k_eff, the exact
+// 2^-62 fixed-point sum of p (the top-p search) and the f64 tree sum (the kept mass).
+__global__ __launch_bounds__(kThreads) void prob_sorted_kernel(float* e, int n, int k_eff, const double* __restrict__ Z,
+                                                               unsigned long long* __restrict__ pfix_sum,
+                                                               double* __restrict__ p_sum) {
+  __shared__ double red[kThreads / 64];
+  __shared__ unsigned long long ured[kThreads / 64];
+  const int j = blockIdx.x * kThreads + threadIdx.x;
+  double v = 0.0;
+  unsigned long long f = 0;
+  if (j < n) {
+    const float p = (float)((double)e[j] / *Z);
+    e[j] = p;
+    if (j < k_eff) {
+      v = (double)p;
+      f = fix62(p);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) f += __shfl_xor(f, o, 64);
+  if ((threadIdx.x & 63) == 0) ured[threadIdx.x >> 6] = f;
+  v = block_sum_f64(v, red);   // (its barriers also publish ured)
+  if (threadIdx.x == 0) {
+    unsigned long long tot = 0;
+    for (int w = 0; w < kThreads / 64; ++w) tot += ured[w];
+    pfix_sum[blockIdx.x] = tot;
+    p_sum[blockIdx.x] = v;
+  }
+}
+
+// One block of 1024 threads: cut = 1 + the first position j < k_eff whose running sum of p reaches
+// top_p (k_eff if none, or when top_p >= 1), and the kept mass P = sum of p over j < cut (f64:
+// whole blocks' tree sums, then the partial block, in a fixed order).
+__global__ __launch_bounds__(1024) void cut_kernel(const float* __restrict__ p, int k_eff, double top_p,
+                                                   const unsigned long long* __restrict__ pfix_sum,
+                                                   const double* __restrict__ p_sum, int nb, int* __restrict__ cut_out,
+                                                   double* __restrict__ P_out) {
+  __shared__ unsigned long long pre[1024];
+  __shared__ double red[1024 / 64];
+  __shared__ int res_s;
+  const int t = threadIdx.x;
+  int cut = k_eff;
+  if (top_p < 1.0) {
+    const unsigned long long target = (unsigned long long)ceil(top_p * kFix);
+    unsigned long long carry = 0, unused = 0;
+    const int blk = first_crossing<false>([&](int b) { return pfix_sum[b]; }, nb, 0ull, target, pre, &res_s, &carry);
+    if (blk < nb) {
+      const int base = blk * kThreads, cnt = min(kThreads, k_eff - base);
+      const int j = first_crossing<false>([&](int u) { return fix62(p[base + u]); }, cnt, carry, target, pre, &res_s,
+                                          &unused);
+      if (j < cnt) cut = base + j + 1;
+    }
+  }
+  const int full = cut / kThreads;
+  double v = 0.0;
+  for (int b = t; b < full; b += 1024) v += p_sum[b];
+  for (int j = full * kThreads + t; j < cut; j += 1024) v += (double)p[j];
+  v = block_sum_f64(v, red);
+  if (t == 0) {
+    *cut_out = cut;
+    *P_out = v;
+  }
+}
+
+// q in id order: q[id] = f32(p_j / P) for kept positions j < cut (p itself when P == 0 or when not
+// renormalising), 0 otherwise.
+__global__ void scatter_q_kernel(const float* __restrict__ p, const int32_t* __restrict__ sorted_ids, int n,
+                                 const int* __restrict__ cut, const double* __restrict__ P, int renorm,
+                                 float* __restrict__ q) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  float v = 0.f;
+  if (j < *cut) v = (renorm && *P > 0.0) ? (float)((double)p[j] / *P) : p[j];
+  q[sorted_ids[j]] = v;
 }
 
 // rocPRIM's stable radix sort with its default configuration (for a 151,936-id row: a block sort
@@ -713,8 +732,8 @@ static int sample_selected(const float* logits, int n, int greedy, double inv_t,
     exp_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(logits, n, top, inv_t, 0, e, zpart);
     prob_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(e, n, zpart, nb, ppart);
     q_ids_kernel<<<nb, kIdThreads, 0, stream()>>>(e, n, ppart, nb, qfix, last);
-    draw_ids_kernel<<<1, 1024, 0, stream()>>>(e, n, qfix, last, nb, top, seed, counter, display_k, token_out,
-                                              logprob_out, display_ids, display_probs);
+    draw_ids_kernel<<<1, 1024, 0, stream()>>>(e, n, qfix, last, nb, 0, top, nullptr, seed, counter, display_k,
+                                              token_out, logprob_out, display_ids, display_probs);
   }
   const hipError_t err = hipGetLastError();
   scratch_free(ws);  // stream-ordered: reused only by later work on the same stream
@@ -746,22 +765,20 @@ int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperat
   if (!topp_only && m <= kMaxPrefix && g_sample_path != 1)
     return sample_selected(logits, n, greedy, inv_t, k_eff, top_p, m, seed, counter, token_out, logprob_out,
                            display_k, display_ids, display_probs);
-  // The full-sort path calls rocPRIM / hipCUB, which may clear their temporary storage with
-  // memsets: it is not captured into graphs.
+  // The full-sort path calls rocPRIM's sort, which may clear its temporary storage with memsets:
+  // it is not captured into graphs.
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   KH_CHECK_HIP(hipStreamIsCapturing(stream(), &cap));
   KH_REQUIRE(cap == hipStreamCaptureStatusNone,
              "kh_sample: top-p without top-k, top-k > 1024 or display_k > 1024 is not supported under stream "
              "capture");
 
-  // temporary storage sizes of the hipCUB calls
-  size_t sort_bytes = 0, scan_bytes = 0;
+  size_t sort_bytes = 0;
   KH_CHECK_HIP(sort_desc(nullptr, sort_bytes, nullptr, nullptr, nullptr, nullptr, n, stream()));
-  KH_CHECK_HIP(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, (const double*)nullptr, (double*)nullptr, n,
-                                                stream()));
-  const size_t cub_bytes = sort_bytes > scan_bytes ? sort_bytes : scan_bytes;
-  const size_t sz_f = align256((size_t)n * 4), sz_d = align256((size_t)n * 8);
-  const size_t total = 6 * sz_f + 3 * sz_d + align256((size_t)nb * 8) + 256 + align256(cub_bytes);
+  const int nbi = (n + kIdThreads - 1) / kIdThreads;
+  const size_t sz_f = align256((size_t)n * 4);
+  const size_t total = 6 * sz_f + 3 * align256((size_t)nb * 8) + 2 * align256((size_t)nbi * 8) + 256 +
+                       align256(sort_bytes);
   char* ws = (char*)scratch_alloc(total);
   if (!ws) return KH_ERR_OOM;
   char* cur = ws;
@@ -771,57 +788,32 @@ int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperat
   int32_t* ids = (int32_t*)take(sz_f);
   int32_t* sorted_ids = (int32_t*)take(sz_f);
   float* e = (float*)take(sz_f);          // then p (sorted order), in place
-  double* p64 = (double*)take(sz_d);
-  double* cum = (double*)take(sz_d);      // top-p scan, then the id-order scan
-  double* q64 = (double*)take(sz_d);
+  float* q = (float*)take(sz_f);          // id order
   double* part = (double*)take(align256((size_t)nb * 8));
+  unsigned long long* pfix = (unsigned long long*)take(align256((size_t)nb * 8));
+  double* psum = (double*)take(align256((size_t)nb * 8));
+  unsigned long long* qfix = (unsigned long long*)take(align256((size_t)nbi * 8));
+  int* last = (int*)take(align256((size_t)nbi * 8));
   char* small = take(256);
-  double* Z = (double*)small;             // softmax total, then P
+  double* Z = (double*)small;
   double* P = (double*)(small + 8);
   int* cut = (int*)(small + 16);
-  int* sel = (int*)(small + 24);
-  void* cub_tmp = take(align256(cub_bytes));
-  float* q = (float*)take(sz_f);
+  void* sort_tmp = take(align256(sort_bytes));
 
   hipError_t err = hipSuccess;
   auto ok = [&](hipError_t x) { if (err == hipSuccess) err = x; };
   iota_keys_kernel<<<nb, kThreads, 0, stream()>>>(logits, n, keys, ids);
   ok(hipGetLastError());
   size_t sb = sort_bytes;
-  ok(sort_desc(cub_tmp, sb, keys, sorted_logits, ids, sorted_ids, n, stream()));
+  ok(sort_desc(sort_tmp, sb, keys, sorted_logits, ids, sorted_ids, n, stream()));
   exp_kernel<<<nb, kThreads, 0, stream()>>>(sorted_logits, n, inv_t, greedy, e, part);
   final_sum_kernel<<<1, kThreads, 0, stream()>>>(part, nb, Z);
-  prob_kernel<<<nb, kThreads, 0, stream()>>>(e, n, Z, e, p64);
-  fill_int_kernel<<<1, 1, 0, stream()>>>(cut, k_eff);
-  ok(hipGetLastError());
-  if (greedy) {
-    scatter_q_kernel<<<nb, kThreads, 0, stream()>>>(e, sorted_ids, n, cut, Z, 0, q, q64);
-    finish_kernel<<<1, kThreads, 0, stream()>>>(sel, q, sorted_ids, n, 1, display_k, token_out, logprob_out,
-                                                display_ids, display_probs);
-    ok(hipGetLastError());
-    scratch_free(ws);
-    if (err != hipSuccess) {
-      set_error("kh_sample: launch failed: %s", hipGetErrorString(err));
-      return KH_ERR_HIP;
-    }
-    return KH_OK;
-  }
-  if (top_p < 1.0) {
-    size_t cb = scan_bytes;
-    ok(hipcub::DeviceScan::InclusiveSum(cub_tmp, cb, p64, cum, k_eff, stream()));
-    topp_cut_kernel<<<(k_eff + kThreads - 1) / kThreads, kThreads, 0, stream()>>>(cum, k_eff, top_p, cut);
-    ok(hipGetLastError());
-  }
-  kept_sum_kernel<<<nb, kThreads, 0, stream()>>>(e, n, cut, part);
-  final_sum_kernel<<<1, kThreads, 0, stream()>>>(part, nb, P);
-  scatter_q_kernel<<<nb, kThreads, 0, stream()>>>(e, sorted_ids, n, cut, P, 1, q, q64);
-  ok(hipGetLastError());
-  size_t cb = scan_bytes;
-  ok(hipcub::DeviceScan::InclusiveSum(cub_tmp, cb, q64, cum, n, stream()));
-  init_sel_kernel<<<1, 1, 0, stream()>>>(sel, n);
-  draw_kernel<<<nb, kThreads, 0, stream()>>>(cum, q, n, seed, counter, sel);
-  finish_kernel<<<1, kThreads, 0, stream()>>>(sel, q, sorted_ids, n, 0, display_k, token_out, logprob_out,
-                                              display_ids, display_probs);
+  prob_sorted_kernel<<<nb, kThreads, 0, stream()>>>(e, n, k_eff, Z, pfix, psum);
+  cut_kernel<<<1, 1024, 0, stream()>>>(e, k_eff, greedy ? 1.0 : top_p, pfix, psum, nb, cut, P);
+  scatter_q_kernel<<<nb, kThreads, 0, stream()>>>(e, sorted_ids, n, cut, P, greedy ? 0 : 1, q);
+  q_ids_kernel<<<nbi, kIdThreads, 0, stream()>>>(q, n, nullptr, nbi, qfix, last);
+  draw_ids_kernel<<<1, 1024, 0, stream()>>>(q, n, qfix, last, nbi, greedy, nullptr, sorted_ids, seed, counter,
+                                            display_k, token_out, logprob_out, display_ids, display_probs);
   ok(hipGetLastError());
   scratch_free(ws);  // stream-ordered: reused only by later work on the same stream
   if (err != hipSuccess) {
