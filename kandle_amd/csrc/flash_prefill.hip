@@ -347,7 +347,9 @@ struct Softmax {
         bf16x8 pv;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p = fast_exp2(sc[s][8 * h + e] * c2 - mb);
+          // one v_fma_f32 per score (written out: contraction would fuse m_ref * c2 instead and
+          // leave a separate multiply per score)
+          const float p = fast_exp2(__builtin_fmaf(sc[s][8 * h + e], c2, -mb));
           ps[h] += p;
           pv[e] = (__bf16)p;
         }
