@@ -12,7 +12,7 @@ and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against th
 `--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy|load|sample|stream]
+                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm]
 Prints ONE JSON line.
 """
 import argparse
@@ -238,6 +238,52 @@ def bench_load():
     return {"bytes": nbytes, "load_s": load_s, "tokens_match": toks == rtoks}
 
 
+GEMM_SHAPES = (("qkv", 4096, 1024, "bf16"), ("o_proj", 1024, 2048, "f32"), ("gate_up", 6144, 1024, "bf16"),
+               ("down", 1024, 3072, "f32"))
+
+
+def bench_gemm(steps, warmup, M=512):
+    """The four projection GEMMs of a C5 prefill layer (M = 512 tokens, bf16 weights [N, K], fp32
+    accumulate): y = x W^T, bf16 out for qkv and gate/up, fp32 out plus the fp32 residual (beta = 1)
+    for o_proj and down, as in the model.  Per shape: kh_gemm device time (calls replayed from a
+    graph, as the model's prefill runs them) and TFLOP/s."""
+    import ctypes as C
+
+    from kandle_amd import Tensor, _lib
+
+    out = {}
+    for name, N, K, odt in GEMM_SHAPES:
+        x = bf16_tensor(701, (M, K))
+        w = bf16_tensor(702, (N, K))
+        y = Tensor(np.zeros((M, N), np.float32), dtype="float32" if odt == "f32" else "bfloat16")
+        res = Tensor(np.zeros((M, N), np.float32), dtype="float32") if odt == "f32" else None
+        vp = lambda t: C.c_void_p(t.handle.data_ptr() if t is not None else 0)  # noqa: E731
+        call = lambda: _lib.call("kh_gemm", vp(x), K, vp(w), K, vp(y), N, vp(res), N, vp(None), M, N, K,  # noqa: E731
+                                 C.c_float(1.0), C.c_float(1.0 if res is not None else 0.0), 1, 1,
+                                 0 if odt == "f32" else 1)
+        # Device time: 20 calls captured as one graph and replayed (no host launch cost per call).
+        from kandle_amd.graphs import HipGraph
+
+        call()
+        g = HipGraph()
+        with g.capture():
+            for _ in range(20):
+                call()
+        wall, dev = time_calls(g.replay, max(1, steps // 4), warmup)
+        g.dispose()
+        dev /= 20.0
+        flops = 2.0 * M * N * K
+        out[name] = {"M": M, "N": N, "K": K, "us": round(dev * 1e3, 2),
+                     "TFLOP/s": round(flops / (dev * 1e-3) / 1e12, 1)}
+        for t in (x, w, y, res):
+            if t is not None:
+                t.dispose()
+    tot = sum(v["us"] for v in out.values())
+    out["layer_us"] = round(tot, 2)
+    out["layer_TFLOP/s"] = round(sum(2.0 * M * n * k for _, n, k, _ in GEMM_SHAPES) / (tot * 1e-6) / 1e12, 1)
+    return out
+
+
 def bench_sample(steps, warmup):
     """On-device sampling of one token from a Qwen3 logits row (vocab 151936, float32): kh_sample
     per call for greedy, an unfiltered draw, and temperature 0.7 with top-k 50 and top-p 0.9 (the
@@ -356,8 +402,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream"],
-                    default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream",
+                                       "gemm"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -394,6 +440,9 @@ def main():
     if args.only == "stream":
         log("generate_stream ...")
         res["stream"] = bench_stream()
+    if args.only == "gemm":
+        log("C5 prefill GEMMs ...")
+        res["gemm"] = bench_gemm(args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
@@ -476,6 +525,13 @@ def main():
             line.update({"value": round(1e6 / sm["wall_us"], 1), "unit": "draws/s",
                          "ms_per_step": round(sm["wall_us"] * 1e-3, 4),
                          "config": {"workload": "on-device sampling, T=0.7, top-k 50, top-p 0.9, vocab 151936"}})
+    if "gemm" in res:
+        gm = res["gemm"]
+        line.update({"value": gm["layer_TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": round(gm["layer_us"] * 1e-3, 4),
+                     "config": {"workload": "C5 prefill projection GEMMs of one layer, M=512", **gm},
+                     "roofline": {"bound": "mfma", "achieved": gm["layer_TFLOP/s"], "peak": PEAK_BF16_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": round(gm["layer_TFLOP/s"] / PEAK_BF16_TFLOPS, 4),
+                                  "traffic": None}})
     if "stream" in res:
         st = res["stream"]
         line.update({"value": round(1e3 / st["stream_ms_per_token"], 1), "unit": "tokens/s",

@@ -59,10 +59,31 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 // the counter to zero.
 // =============================================================================================
 constexpr int G_THREADS = 256;
+#ifndef KH_GEMM_PREFETCH
+#define KH_GEMM_PREFETCH 3
+#endif
+constexpr int kGemmPrefetch = KH_GEMM_PREFETCH;   // k-steps of global loads in flight per workgroup
+#ifndef KH_GEMM_T128_MIN
+#define KH_GEMM_T128_MIN 256
+#endif
+#ifndef KH_GEMM_SPLIT128
+#define KH_GEMM_SPLIT128 0
+#endif
+constexpr int kGemmT128Min = KH_GEMM_T128_MIN;   // 128-tiles from this many tiles up
+#ifndef KH_GEMM_SPLIT_TARGET
+#define KH_GEMM_SPLIT_TARGET 512
+#endif
+constexpr int kGemmSplitTarget = KH_GEMM_SPLIT_TARGET;   // split K until about this many workgroups
+constexpr bool kGemmSplit128 = KH_GEMM_SPLIT128;
 constexpr int kMaxSplits = 8;
 constexpr int g_tile(int wt) { return 64 * wt; }
 
-template <typename TO, int WT, int KS, bool SPLIT>
+// PF: k-steps of prefetch in flight (register ring of PF stages; the loop is unrolled by PF so the
+// stage indices are compile-time).  Tiles are numbered column-major (all m tiles of one n tile in a
+// row) and, when the workgroup count is a multiple of 8, dealt to the 8 XCDs in contiguous ranges
+// (the hardware hands workgroup i to XCD i mod 8): each XCD then reads its own columns of B (the
+// weights) into its L2, and only A (the activations) is read by every XCD.
+template <typename TO, int WT, int KS, bool SPLIT, int PF = 1>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
@@ -75,9 +96,12 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ATILE + BTILE)];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, g = lane >> 5;
-  const int tile = SPLIT ? blockIdx.x / splits : blockIdx.x;
-  const int split = SPLIT ? blockIdx.x % splits : 0;
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  int bid = blockIdx.x;
+  if (PF > 1 && (gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  const int tile = SPLIT ? bid / splits : bid;
+  const int split = SPLIT ? bid % splits : 0;
+  const int tiles_m = (M + GM - 1) / GM;
+  const int tm = PF > 1 ? tile % tiles_m : tile / tiles_n, tn = PF > 1 ? tile / tiles_m : tile % tiles_n;
   const int m0 = tm * GM, n0 = tn * GN;
   const int wm = (wave >> 1) * 32 * WT, wn = (wave & 1) * 32 * WT;
   const int kbeg = split * kchunk, kend = min(K, kbeg + kchunk);
@@ -87,29 +111,33 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * 2));
   const auto rb = make_rsrc(B + (int64_t)n0 * ldb, (uint32_t)(((int64_t)(nrows - 1) * ldb + K) * 2));
 
-  // Staging: each of the A and B tiles is GM rows x KS k = GM * CPR chunks of 16 B, CPT per thread.
-  uint4 ast[CPT], bst[CPT];
-  auto load_tile = [&](int kt) {
+  // Staging: each of the A and B tiles is GM rows x KS k = GM * CPR chunks of 16 B, CPT per thread,
+  // in PF register stages.
+  uint4 ast[PF][CPT], bst[PF][CPT];
+  // Byte offsets fit 32 bits (the launcher checks 128 rows of lda / ldb); columns past kend map to
+  // 0xffffffff, past the range, and read zero (K % 8 == 0, so a chunk is all in or all out).  The
+  // loads are branch-free, so the compiler's load counting stays exact across the prefetch ring.
+  auto load_tile = [&](int stg, int kt) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + G_THREADS * i;
       const int row = id / CPR, kc = kt + 8 * (id % CPR);
-      // Columns past kend map past the range (K % 8 == 0, so a chunk is all in or all out).
-      const int64_t ao = kc < kend ? (int64_t)row * lda + kc : (int64_t)1 << 40;
-      const int64_t bo = kc < kend ? (int64_t)row * ldb + kc : (int64_t)1 << 40;
-      ast[i] = buf_load16(ra, (uint32_t)min<int64_t>(ao * 2, 0xffffffffLL));
-      bst[i] = buf_load16(rb, (uint32_t)min<int64_t>(bo * 2, 0xffffffffLL));
+      const bool in = kc < kend;
+      const uint32_t ao = in ? ((uint32_t)row * (uint32_t)lda + (uint32_t)kc) * 2u : 0xffffffffu;
+      const uint32_t bo = in ? ((uint32_t)row * (uint32_t)ldb + (uint32_t)kc) * 2u : 0xffffffffu;
+      ast[stg][i] = buf_load16(ra, ao);
+      bst[stg][i] = buf_load16(rb, bo);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int stg, int buf) {
     uint16_t* as = smem + buf * (ATILE + BTILE);
     uint16_t* bs = as + ATILE;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + G_THREADS * i;
       const int row = id / CPR, kc = 8 * (id % CPR);
-      *reinterpret_cast<uint4*>(as + row * STR + kc) = ast[i];
-      *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[i];
+      *reinterpret_cast<uint4*>(as + row * STR + kc) = ast[stg][i];
+      *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[stg][i];
     }
   };
 
@@ -122,17 +150,13 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
 
   const int nk = kend > kbeg ? (kend - kbeg + KS - 1) / KS : 0;
-  if (nk > 0) {
-    load_tile(kbeg);
-    store_tile(0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int t = 0; t < nk; ++t) {
-    const int buf = t & 1;
-    const bool has_next = t + 1 < nk;
-    if (has_next) load_tile(kbeg + (t + 1) * KS);
-    const uint16_t* as = smem + buf * (ATILE + BTILE);
+  // Step t is in LDS buffer t & 1 and, before that, in register stage t % PF.  Iteration t loads
+  // step t + PF into the stage step t has left, computes step t, then moves step t + 1 (loaded PF - 1
+  // iterations earlier) into the other LDS buffer.  Steps past the end load zeros and are stored
+  // into the idle buffer, so the main loop has no branches between a load and its use.
+  auto step = [&](int t, int u) {
+    load_tile(u, kbeg + (t + PF) * KS);
+    const uint16_t* as = smem + (t & 1) * (ATILE + BTILE);
     const uint16_t* bs = as + ATILE;
 #pragma unroll
     for (int kc = 0; kc < KS / 16; ++kc) {
@@ -148,8 +172,22 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
         for (int b = 0; b < WT; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv[a], av[b], acc[a][b], 0, 0, 0);
     }
-    if (has_next) store_tile(buf ^ 1);
+    store_tile((u + 1) % PF, (t + 1) & 1);
     __syncthreads();
+  };
+  if (nk > 0) {
+#pragma unroll
+    for (int s2 = 0; s2 < PF; ++s2) load_tile(s2, kbeg + s2 * KS);
+    store_tile(0, 0);
+    __syncthreads();
+    int t = 0;
+    for (; t + PF <= nk; t += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) step(t + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < PF; ++u)
+      if (t + u < nk) step(t + u, u);
   }
 
   if constexpr (SPLIT) {
@@ -190,39 +228,43 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   }
 }
 
-// Split-K reduction: one workgroup per output tile, four consecutive outputs per thread and step;
-// all splits' partials are loaded before they are added (in split order), then the epilogue.
+// Split-K reduction: one thread per four consecutive outputs of a tile, so every partial of the
+// whole output is in flight at once; the splits are added in split order, then the epilogue.
 template <typename TO, int GT>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits,
                                                                   TO* C, int64_t ldc, const TO* cin, int64_t ldcin,
                                                                   const TO* __restrict__ bias, int M, int N,
-                                                                  float alpha, float beta, int tiles_n) {
-  const int tile = blockIdx.x;
-  const int m0 = (tile / tiles_n) * GT, n0 = (tile % tiles_n) * GT;
-  const float* tp = part + (int64_t)tile * splits * (GT * GT);
-  const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
-  for (int idx = threadIdx.x * 4; idx < GT * GT; idx += blockDim.x * 4) {
-    const int ml = idx / GT, nl = idx % GT;
-    const int m = m0 + ml, n = n0 + nl;
-    float4 pv[kMaxSplits];
+                                                                  float alpha, float beta, int tiles_n,
+                                                                  int tiles_m_colmajor, int tiles) {
+  // Tile numbering as in the GEMM kernel that wrote the partials: row-major over n tiles, or
+  // column-major (tiles_m_colmajor = the number of m tiles) for the prefetching kernel.
+  constexpr int Q = GT * GT / 4;   // float4 groups per tile
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)tiles * Q) return;
+  const int tile = (int)(gid / Q), idx = (int)(gid % Q) * 4;
+  const int tm = tiles_m_colmajor ? tile % tiles_m_colmajor : tile / tiles_n;
+  const int tn = tiles_m_colmajor ? tile / tiles_m_colmajor : tile % tiles_n;
+  const int ml = idx / GT, nl = idx % GT;
+  const int m = tm * GT + ml, n = tn * GT + nl;
+  if (m >= M || n >= N) return;
+  const float* tp = part + (int64_t)tile * splits * (GT * GT) + idx;
+  float4 pv[kMaxSplits];
 #pragma unroll
-    for (int s2 = 0; s2 < kMaxSplits; ++s2)
-      pv[s2] = s2 < splits ? *reinterpret_cast<const float4*>(tp + (int64_t)s2 * (GT * GT) + idx)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s2 = 0; s2 < kMaxSplits; ++s2)
+    pv[s2] = s2 < splits ? *reinterpret_cast<const float4*>(tp + (int64_t)s2 * (GT * GT))
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s2 = 0; s2 < kMaxSplits; ++s2) {
-      v[0] += pv[s2].x;
-      v[1] += pv[s2].y;
-      v[2] += pv[s2].z;
-      v[3] += pv[s2].w;
-    }
-    if (m >= M || n >= N) continue;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = (n + e < N) ? epilogue<TO>(v[e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
-    store4<TO>(C, (int64_t)m * ldc + n, v, vec, min(4, N - n));
+  for (int s2 = 0; s2 < kMaxSplits; ++s2) {
+    v[0] += pv[s2].x;
+    v[1] += pv[s2].y;
+    v[2] += pv[s2].z;
+    v[3] += pv[s2].w;
   }
+  const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (n + e < N) ? epilogue<TO>(v[e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
+  store4<TO>(C, (int64_t)m * ldc + n, v, vec, min(4, N - n));
 }
 
 // =============================================================================================
@@ -546,20 +588,20 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
     // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the
     // workgroups, and when even those leave CUs idle and K is long, split K over up to 8 workgroups.
     const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-    const int wt = t128 >= 256 ? 2 : 1;
+    const int wt = t128 >= kGemmT128Min ? 2 : 1;
     const int gt = g_tile(wt);
     const int tiles_m = (M + gt - 1) / gt, tiles_n = (N + gt - 1) / gt;
     const int64_t tiles = (int64_t)tiles_m * tiles_n;
     KH_REQUIRE(tiles <= INT32_MAX / 8, "kh_gemm: grid too large");
     int splits = 1;
-    if (wt == 1 && tiles < 256 && K >= 1024) {
-      const int64_t want = 512 / tiles;
+    if (tiles < 256 && K >= 1024 && (wt == 1 || kGemmSplit128)) {
+      const int64_t want = kGemmSplitTarget / tiles;
       splits = want < 1 ? 1 : (want > kMaxSplits ? kMaxSplits : (int)want);
     }
     int kchunk = K;
     float* part = nullptr;
     if (splits > 1) {
-      kchunk = ((K + splits - 1) / splits + 127) / 128 * 128;
+      kchunk = ((K + splits - 1) / splits + 127) / 128 * 128;   // whole k-steps of 64 and 128
       splits = (K + kchunk - 1) / kchunk;
       part = (float*)scratch_alloc((size_t)splits * tiles * gt * gt * sizeof(float));
       if (!part) {
@@ -572,19 +614,25 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
     const bool ks128 = tiles * splits <= 512;
     const int nblk = (int)(tiles * splits);
     if constexpr (is_bf16) {
-      if (wt == 2) {
-        gemm_bf16_nt_kernel<TO, 2, 64, false><<<nblk, G_THREADS, 0, stream()>>>(
+      constexpr int PF = kGemmPrefetch;
+      if (wt == 2 && splits > 1) {
+        gemm_bf16_nt_kernel<TO, 2, 64, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
+            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
+        gemm_splitk_reduce_kernel<TO, 128><<<(int)((tiles * 128 * 128 / 4 + 255) / 256), 256, 0, stream()>>>(
+            part, splits, C, ldc, CI, ldcin, BI, M, N, alpha, beta, tiles_n, PF > 1 ? tiles_m : 0, (int)tiles);
+      } else if (wt == 2) {
+        gemm_bf16_nt_kernel<TO, 2, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
             A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
       } else if (splits > 1) {
-        gemm_bf16_nt_kernel<TO, 1, 128, true><<<nblk, G_THREADS, 0, stream()>>>(
+        gemm_bf16_nt_kernel<TO, 1, 128, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
             A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
-        gemm_splitk_reduce_kernel<TO, 64><<<(int)tiles, 256, 0, stream()>>>(part, splits, C, ldc, CI, ldcin, BI, M,
-                                                                            N, alpha, beta, tiles_n);
+        gemm_splitk_reduce_kernel<TO, 64><<<(int)((tiles * 64 * 64 / 4 + 255) / 256), 256, 0, stream()>>>(
+            part, splits, C, ldc, CI, ldcin, BI, M, N, alpha, beta, tiles_n, PF > 1 ? tiles_m : 0, (int)tiles);
       } else if (ks128) {
-        gemm_bf16_nt_kernel<TO, 1, 128, false><<<nblk, G_THREADS, 0, stream()>>>(
+        gemm_bf16_nt_kernel<TO, 1, 128, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
             A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
       } else {
-        gemm_bf16_nt_kernel<TO, 1, 64, false><<<nblk, G_THREADS, 0, stream()>>>(
+        gemm_bf16_nt_kernel<TO, 1, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
             A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
       }
     }
