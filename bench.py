@@ -12,7 +12,7 @@ and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against th
 `--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm]
+                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv]
 Prints ONE JSON line.
 """
 import argparse
@@ -284,6 +284,52 @@ def bench_gemm(steps, warmup, M=512):
     return out
 
 
+GEMV_SHAPES = (  # (name, N, K, prologue 0 none / 1 RMSNorm / 2 silu*mul, fp32 out with residual)
+    ("qkv", 4096, 1024, 1, False), ("o_proj", 1024, 2048, 0, True), ("gate_up", 6144, 1024, 1, False),
+    ("down", 1024, 3072, 2, True), ("lm_head", 151936, 1024, 1, True), ("launch_floor", 64, 64, 0, False))
+
+
+def bench_gemv(steps, warmup):
+    """The one-row GEMVs of a C5 decode step (bf16 weights [N, K], fp32 accumulate) through
+    kh_gemv_fused with the prologue the model uses, 20 calls captured in a graph and replayed: device
+    time per call and weight GB/s against the HBM roofline.  launch_floor is a 64 x 64 GEMV: the
+    per-kernel cost of a launch inside a graph."""
+    import ctypes as C
+
+    from kandle_amd import Tensor, _lib
+    from kandle_amd.graphs import HipGraph
+
+    out = {}
+    for name, N, K, pro, res in GEMV_SHAPES:
+        w = bf16_tensor(711, (N, K))
+        kx = K if pro != 2 else K
+        x = (Tensor(np.random.default_rng(5).normal(size=kx).astype(np.float32), dtype="float32") if pro == 1
+             else bf16_tensor(712, (kx,)))
+        x2 = bf16_tensor(713, (K,)) if pro == 2 else None
+        nw = bf16_tensor(714, (K,)) if pro == 1 else None
+        y = Tensor(np.zeros(N, np.float32), dtype="float32" if res else "bfloat16")
+        cin = Tensor(np.zeros(N, np.float32), dtype="float32") if res else None
+        vp = lambda t: C.c_void_p(t.handle.data_ptr() if t is not None else 0)  # noqa: E731
+        call = lambda: _lib.call("kh_gemv_fused", pro, vp(x), vp(x2), vp(nw), C.c_float(1e-6), vp(w), K, vp(y),  # noqa
+                                 vp(cin), vp(None), N, K, C.c_float(1.0), C.c_float(1.0 if res else 0.0),
+                                 0 if res else 1)
+        call()
+        g = HipGraph()
+        with g.capture():
+            for _ in range(20):
+                call()
+        _, dev = time_calls(g.replay, max(1, steps // 4), warmup)
+        g.dispose()
+        us = dev * 1e3 / 20.0
+        out[name] = {"N": N, "K": K, "us": round(us, 2), "GB/s": round(2.0 * N * K / (us * 1e-6) / 1e9, 1)}
+        for t in (w, x, x2, nw, y, cin):
+            if t is not None:
+                t.dispose()
+    layer = sum(out[n]["us"] for n in ("qkv", "o_proj", "gate_up", "down"))
+    out["layer_gemv_us"] = round(layer, 2)
+    return out
+
+
 def bench_sample(steps, warmup):
     """On-device sampling of one token from a Qwen3 logits row (vocab 151936, float32): kh_sample
     per call for greedy, an unfiltered draw, and temperature 0.7 with top-k 50 and top-p 0.9 (the
@@ -403,7 +449,7 @@ def main():
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
     ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream",
-                                       "gemm"], default=None)
+                                       "gemm", "gemv"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -443,6 +489,9 @@ def main():
     if args.only == "gemm":
         log("C5 prefill GEMMs ...")
         res["gemm"] = bench_gemm(args.steps, args.warmup)
+    if args.only == "gemv":
+        log("C5 decode GEMVs ...")
+        res["gemv"] = bench_gemv(args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
@@ -532,6 +581,13 @@ def main():
                      "roofline": {"bound": "mfma", "achieved": gm["layer_TFLOP/s"], "peak": PEAK_BF16_TFLOPS,
                                   "unit": "TFLOP/s", "frac": round(gm["layer_TFLOP/s"] / PEAK_BF16_TFLOPS, 4),
                                   "traffic": None}})
+    if "gemv" in res:
+        gv = res["gemv"]
+        lm = gv["lm_head"]
+        line.update({"value": lm["GB/s"], "unit": "GB/s", "ms_per_step": round(gv["layer_gemv_us"] * 1e-3, 4),
+                     "config": {"workload": "C5 decode one-row GEMVs (bf16 weights), graph-replayed", **gv},
+                     "roofline": {"bound": "hbm", "achieved": lm["GB/s"], "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                                  "frac": round(lm["GB/s"] / PEAK_HBM_GBPS, 4), "traffic": None}})
     if "stream" in res:
         st = res["stream"]
         line.update({"value": round(1e3 / st["stream_ms_per_token"], 1), "unit": "tokens/s",

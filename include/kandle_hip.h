@@ -171,6 +171,23 @@ int kh_sample_set_path(int path);
  * reference counterpart (the reference draws with Math.random). */
 int kh_philox4x32_10(uint64_t seed, const uint32_t* counters, int64_t n, uint32_t* out);
 
+/* The attention block of one decode step of one sequence, from the raw q/k/v projection row to the
+ * residual update: qk-norm + RoPE of the q heads and of the new token's k row (per-head RMSNorm with
+ * q_norm_w / k_norm_w and eps, angles float(p) * inv_freq[i]); the new k and v rows written into the
+ * caches at row p = *position; split-K attention of the q heads over cache rows [0, p] (GQA,
+ * scale); the merge; then x += o W_o^T (w_o bf16 [n_out, hq*128] with row stride ldw, x fp32
+ * [n_out]).  qkv: bf16 [hq*128 + 2*hkv*128] (q heads, then k, then v).  Caches bf16 [hkv][max_len]
+ * [128] with element strides cache_strides = {k head, k row, v head, v row}.  The position is read
+ * from device memory, so a captured step replays at every position.  Two kernels (three when the
+ * cache exceeds 8 chunks of 256 keys).  Fuses the decode path of GroupedQueryAttention.forward
+ * (reference: packages/model-utils/src/attention/gqa.ts:246-430: projections, q_norm/k_norm,
+ * RoPE, KV-cache update, SDPA, o_proj; kv-cache.ts:164-212) with the o_proj residual add of
+ * Qwen3DecoderLayer.forward (qwen3/decoder_layer.ts:191-241). */
+int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                              float eps, const int32_t* position, void* k_cache, void* v_cache, int hq, int hkv,
+                              int64_t max_len, const int64_t* cache_strides, float scale, const void* w_o,
+                              int64_t ldw, int64_t n_out, float* x);
+
 /* ------------------------------------------------------------------ hot path ----------------- */
 
 /* y[r, :] = x[r, :] * (1 / sqrt(mean(x[r, :]^2) + eps)) * w[:] (w may be NULL), fp32 math,

@@ -60,6 +60,8 @@ SIGNATURES = {
     "kh_sample": [_vp, _i64, _i, C.c_double, _i, C.c_double, C.c_uint64, _vp, _vp, _vp, _i, _vp, _vp],
     "kh_philox4x32_10": [C.c_uint64, _vp, _i64, _vp],
     "kh_sample_set_path": [_i],
+    "kh_decode_attention_block": [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i64, _vp, _f, _vp, _i64, _i64,
+                                  _vp],
     "kh_graph_begin_capture": [],
     "kh_graph_end_capture": [_vpp],
     "kh_graph_launch": [_vp],

@@ -257,18 +257,71 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
 
 // ---- bf16 decode partials with in-row DPP reductions ------------------------------------------
 
+// The fused decode block merges the split-K partials inside the o_proj GEMV's prologue (every
+// workgroup reads all of them) up to this many 256-key chunks; longer caches use the merge kernel.
+constexpr int kMergeInPrologueMaxChunks = 8;
+
+// The decode step's q/k/v as the fused attention block takes them: raw projection rows (before
+// qk-norm and RoPE) of one sequence whose new token sits at cache position *position.
+struct DecodeFuse {
+  const uint16_t* wq = nullptr;       // q_norm weight [128], bf16
+  const uint16_t* wk = nullptr;       // k_norm weight [128], bf16
+  const float* inv_freq = nullptr;    // RoPE inverse frequencies [64]
+  const int32_t* position = nullptr;  // the new token's position p; the sequence has p + 1 keys
+  const uint16_t* k_new = nullptr;    // raw k rows of the new token [hkv][128]
+  const uint16_t* v_new = nullptr;    // raw v rows [hkv][128]
+  float eps = 0.f;
+};
+
+// RMSNorm (weight w, eps) then RoPE of one 128-wide head row held by the 16 lanes of a DPP row,
+// lane `sub` holding columns 8 sub .. 8 sub + 7 (a[]); cs/sn are the lane's cos/sin.  The same
+// arithmetic, term for term, as qk_norm_rope_kernel: x * (1 / sqrt(mean x^2 + eps)) * w, then
+// (first half) x cos - partner sin, (second half) x cos + partner sin, the partner 64 columns away
+// (lane sub ^ 8, row_ror:8).
+__device__ __forceinline__ void norm_rope_row(float (&a)[8], const float (&wv)[8], const float (&cs)[8],
+                                              const float (&sn)[8], int sub, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += a[j] * a[j];
+  ss = row16_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+  float n[8], pn[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n[j] = (a[j] * inv) * wv[j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pn[j] = dpp_f<0x128>(n[j]);
+  const bool first = sub < 8;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = first ? n[j] * cs[j] + (-pn[j]) * sn[j] : n[j] * cs[j] + pn[j] * sn[j];
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
+  f[0] = lo_bf16(u.x); f[1] = hi_bf16(u.x); f[2] = lo_bf16(u.y); f[3] = hi_bf16(u.y);
+  f[4] = lo_bf16(u.z); f[5] = hi_bf16(u.z); f[6] = lo_bf16(u.w); f[7] = hi_bf16(u.w);
+}
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7]));
+}
+
 // Same unit of work and output as decode_partial_kernel, for bf16: the 16 lanes of a DPP row hold
 // one key row (8 columns each), so a score is an in-lane dot product plus a 4-step DPP row sum, and
 // the 4 rows of a wave (key slots kk) keep separate softmax states (m, l, o) -- no cross-row
 // shuffles.  The 16 states of the workgroup (4 waves x 4 rows) are combined once through LDS.
-template <int G>
+// FUSE (decode attention block, one sequence): Q holds the raw q heads; each workgroup applies
+// qk-norm + RoPE to its G heads (rounded to bf16, as the unfused path stores them).  The wave whose
+// keys include the new token p normalises and rotates that token's k row, writes it and the v row
+// into the caches at row p, and scores it from registers (the stale cache row it loaded is masked):
+// the new key joins the softmax state of the DPP row that owns it, with no data dependence on the
+// cache write.  Only this workgroup reads row p in this launch.
+template <int G, bool FUSE = false>
 __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t* __restrict__ Q,
                                                                   const uint16_t* __restrict__ K,
                                                                   const uint16_t* __restrict__ V,
                                                                   const int32_t* __restrict__ lens, int uniform_len,
                                                                   int max_len, int hq, int hkv, AttnStrides st,
                                                                   float scale, int max_chunks,
-                                                                  float* __restrict__ part) {
+                                                                  float* __restrict__ part, DecodeFuse fz) {
   constexpr int D = 128, NI = 16, KPI = 4, KPW = NI * KPI, CHUNK = DC_WAVES * KPW, NS = DC_WAVES * KPI;
   static_assert(CHUNK == dc_chunk<uint16_t>(), "chunk size shared with the merge");
   __shared__ float red_m[NS][G];
@@ -278,7 +331,14 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
   const int chunk = blockIdx.x;
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
-  const int L = decode_len(lens, uniform_len, b, max_len);
+  int praw = 0;
+  int L;
+  if constexpr (FUSE) {
+    praw = *fz.position;
+    L = praw + 1 < 0 ? 0 : (praw + 1 > max_len ? max_len : praw + 1);
+  } else {
+    L = decode_len(lens, uniform_len, b, max_len);
+  }
   if (chunk * CHUNK >= L) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int sub = lane & 15;  // 16-byte column of the key row
@@ -286,15 +346,19 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
   const int key0 = chunk * CHUNK + w * KPW;
 
   float qv[G][8];
+  uint4 qraw[G], wqr, wkr, knr, vnr, kn;
+  float f0 = 0.f;
+  bool newkey = false;  // FUSE: this lane's DPP row scores the new key from registers
 #pragma unroll
-  for (int gi = 0; gi < G; ++gi) {
-    const uint4 u = *reinterpret_cast<const uint4*>(Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * 8);
-    const uint32_t wq[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qv[gi][2 * e] = lo_bf16(wq[e]) * scale;
-      qv[gi][2 * e + 1] = hi_bf16(wq[e]) * scale;
-    }
+  for (int gi = 0; gi < G; ++gi)
+    qraw[gi] = *reinterpret_cast<const uint4*>(Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * 8);
+  if constexpr (FUSE) {
+    // everything the norm and rotation need is requested before the cache rows (loads return in order)
+    wqr = *reinterpret_cast<const uint4*>(fz.wq + sub * 8);
+    wkr = *reinterpret_cast<const uint4*>(fz.wk + sub * 8);
+    knr = *reinterpret_cast<const uint4*>(fz.k_new + hk * D + sub * 8);
+    vnr = *reinterpret_cast<const uint4*>(fz.v_new + hk * D + sub * 8);
+    f0 = fz.inv_freq[lane];
   }
   // Byte ranges end at the sequence length: keys >= L read as zero.
   const auto rk = make_rsrc(K + b * st.kb + hk * st.kh, (uint32_t)(((int64_t)(L - 1) * st.ks + D) * 2));
@@ -310,12 +374,60 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
     const int key = key0 + it * KPI + kk;
     vr[it] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + sub * 8) * 2));
   }
+  if constexpr (FUSE) {
+    // cos/sin of float(p) * inv_freq[i] for this lane's columns (i = (8 sub + j) mod 64): lane l
+    // evaluates frequency l once and the lanes gather theirs.
+    float c0, s0;
+    sincosf((float)praw * f0, &s0, &c0);
+    float cs[8], sn[8], wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = (8 * sub + j) & 63;
+      cs[j] = __shfl(c0, i, 64);
+      sn[j] = __shfl(s0, i, 64);
+    }
+    unpack8(wqr, wv);
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float a[8];
+      unpack8(qraw[gi], a);
+      norm_rope_row(a, wv, cs, sn, sub, fz.eps);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qv[gi][j] = round_bf16(a[j]) * scale;
+    }
+    // The new key's row, normalised and rotated (every wave computes it: one row), and the DPP row
+    // of this wave that owns key p (if any) writes it and the v row into the caches.
+    const int rel = praw - key0;  // the new key relative to this wave's first key
+    newkey = praw < max_len && rel >= 0 && rel < KPW && kk == (rel & 3);
+    float a[8];
+    unpack8(knr, a);
+    unpack8(wkr, wv);
+    norm_rope_row(a, wv, cs, sn, sub, fz.eps);
+    kn = pack8(a);
+    if (newkey) {
+      uint16_t* kc = const_cast<uint16_t*>(K) + b * st.kb + hk * st.kh + (int64_t)praw * st.ks + sub * 8;
+      uint16_t* vc = const_cast<uint16_t*>(V) + b * st.vb + hk * st.vh + (int64_t)praw * st.vs + sub * 8;
+      *reinterpret_cast<uint4*>(kc) = kn;
+      *reinterpret_cast<uint4*>(vc) = vnr;
+    }
+  } else {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float a[8];
+      unpack8(qraw[gi], a);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qv[gi][j] = a[j] * scale;
+    }
+  }
 
+  // FUSE: cache row p is read stale (this launch writes it) and masked; the new key is scored from
+  // its registers below, as one more key of the DPP row that owns it.
+  const int Lc = FUSE && praw < max_len ? praw : L;
   float sc[G][NI];
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const uint32_t wk[4] = {kr[it].x, kr[it].y, kr[it].z, kr[it].w};
-    const bool valid = key0 + it * KPI + kk < L;
+    const bool valid = key0 + it * KPI + kk < Lc;
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
       float d = 0.f;
@@ -328,14 +440,42 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
       sc[gi][it] = valid ? d : -INFINITY;
     }
   }
+  float sn_new[G];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) sn_new[gi] = -INFINITY;
+  if constexpr (FUSE) {
+    const uint32_t wk[4] = {kn.x, kn.y, kn.z, kn.w};
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d += qv[gi][2 * e] * lo_bf16(wk[e]);
+        d += qv[gi][2 * e + 1] * hi_bf16(wk[e]);
+      }
+      d = row16_sum(d);
+      sn_new[gi] = newkey ? d : -INFINITY;
+    }
+  }
   const int s_id = w * KPI + kk;
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
     float mx = sc[gi][0];
 #pragma unroll
     for (int it = 1; it < NI; ++it) mx = fmaxf(mx, sc[gi][it]);
+    if constexpr (FUSE) mx = fmaxf(mx, sn_new[gi]);
     const float mu = mx == -INFINITY ? 0.f : mx;
     float ls = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (FUSE) {
+      const float p = __expf(sn_new[gi] - mu);
+      ls += p;
+      const uint32_t wv[4] = {vnr.x, vnr.y, vnr.z, vnr.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[2 * e] += p * lo_bf16(wv[e]);
+        o[2 * e + 1] += p * hi_bf16(wv[e]);
+      }
+    }
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const float p = __expf(sc[gi][it] - mu);
@@ -379,10 +519,8 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
 // chunk (running max, denominator and column sum, rescaled when the max grows), and the 8 group
 // states are combined through LDS.
 template <typename T>
-__global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __restrict__ part,
-                                                                const int32_t* __restrict__ lens, int uniform_len,
-                                                                int max_len, int hq, int max_chunks, AttnStrides st,
-                                                                T* __restrict__ O) {
+__device__ __forceinline__ void decode_merge_cols_body(const float* __restrict__ part, int L, int hq, int max_chunks,
+                                                       const AttnStrides& st, T* __restrict__ O) {
   constexpr int D = 128, COLS = 32, NG = 8;
   __shared__ float gm[NG], gl[NG];
   __shared__ float gacc[NG][COLS];
@@ -390,7 +528,6 @@ __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __r
   const int tid = threadIdx.x;
   const int col = tid & (COLS - 1), grp = tid >> 5;
   const int d = cg * COLS + col;
-  const int L = decode_len(lens, uniform_len, b, max_len);
   const int nch = (L + dc_chunk<T>() - 1) / dc_chunk<T>();
   const int64_t row0 = ((int64_t)b * hq + h) * max_chunks;
   const float* po = decode_part_o(part) + row0 * D + d;
@@ -444,6 +581,25 @@ __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __r
   }
 }
 
+template <typename T>
+__global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __restrict__ part,
+                                                                const int32_t* __restrict__ lens, int uniform_len,
+                                                                int max_len, int hq, int max_chunks, AttnStrides st,
+                                                                T* __restrict__ O) {
+  decode_merge_cols_body<T>(part, decode_len(lens, uniform_len, blockIdx.z, max_len), hq, max_chunks, st, O);
+}
+
+// The merge of the fused decode block (one sequence, length *position + 1): the same kernel body
+// with the length taken from the position.
+__global__ __launch_bounds__(256) void decode_merge_cols_pos_kernel(const float* __restrict__ part,
+                                                                   const int32_t* __restrict__ position, int max_len,
+                                                                   int hq, int max_chunks, AttnStrides st,
+                                                                   uint16_t* __restrict__ O) {
+  const int p = *position;
+  const int L = p + 1 < 0 ? 0 : (p + 1 > max_len ? max_len : p + 1);
+  decode_merge_cols_body<uint16_t>(part, L, hq, max_chunks, st, O);
+}
+
 AttnStrides load_strides(const int64_t* s) {
   AttnStrides a;
   a.qb = s[0]; a.qh = s[1]; a.qs = s[2];
@@ -476,7 +632,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   case GG:                                                                                                 \
     if constexpr (sizeof(T) == 2)                                                                          \
       decode_partial_bf16_kernel<GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st, \
-                                                                 scale, max_chunks, part);                 \
+                                                                 scale, max_chunks, part, DecodeFuse{});   \
     else                                                                                                   \
       decode_partial_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st,  \
                                                                 scale, max_chunks, part);                  \
@@ -575,6 +731,83 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   if (dtype == KH_BF16)
     return launch_decode<uint16_t>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
   return launch_decode<float>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
+}
+
+int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                              float eps, const int32_t* position, void* k_cache, void* v_cache, int hq, int hkv,
+                              int64_t max_len, const int64_t* cache_strides, float scale, const void* w_o, int64_t ldw,
+                              int64_t n_out, float* x) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "kh_decode_attention_block: bad head counts %d / %d", hq, hkv);
+  const int G = hq / hkv;
+  KH_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "kh_decode_attention_block: hq/hkv = %d not in {1, 2, 4, 8}", G);
+  KH_REQUIRE(max_len > 0 && max_len <= INT32_MAX && n_out > 0 && n_out <= INT32_MAX,
+             "kh_decode_attention_block: bad extents");
+  KH_REQUIRE(qkv && q_norm_w && k_norm_w && inv_freq && position && k_cache && v_cache && cache_strides && w_o && x,
+             "kh_decode_attention_block: null pointer");
+  const int64_t kh_s = cache_strides[0], ks = cache_strides[1], vh_s = cache_strides[2], vs = cache_strides[3];
+  KH_REQUIRE(aligned16(qkv) && aligned16(q_norm_w) && aligned16(k_norm_w) && aligned16(k_cache) &&
+                 aligned16(v_cache) && kh_s % 8 == 0 && ks % 8 == 0 && vh_s % 8 == 0 && vs % 8 == 0,
+             "kh_decode_attention_block: operands must be 16-byte aligned with 16-byte aligned strides");
+  const int64_t lim = int64_t(1) << 31;
+  KH_REQUIRE((max_len + 256) * ks * 2 < lim && (max_len + 256) * vs * 2 < lim,
+             "kh_decode_attention_block: one head of the cache spans more than 2 GiB");
+  const int ml = (int)max_len;
+  constexpr int CH = 256;  // keys per split-K chunk (dc_chunk<bf16>)
+  const int max_chunks = (ml + CH - 1) / CH;
+  KH_REQUIRE(max_chunks <= 65535, "kh_decode_attention_block: max_len too large");
+  const size_t part_bytes = (size_t)hq * max_chunks * (128 + 2) * sizeof(float);
+  float* part = (float*)scratch_alloc(part_bytes);
+  if (!part) return KH_ERR_OOM;
+  const uint16_t* Q = (const uint16_t*)qkv;
+  AttnStrides st{};
+  st.qh = 128;
+  st.kh = kh_s; st.ks = ks; st.vh = vh_s; st.vs = vs;
+  DecodeFuse fz;
+  fz.wq = (const uint16_t*)q_norm_w;
+  fz.wk = (const uint16_t*)k_norm_w;
+  fz.inv_freq = inv_freq;
+  fz.position = position;
+  fz.k_new = Q + (int64_t)hq * 128;
+  fz.v_new = Q + (int64_t)(hq + hkv) * 128;
+  fz.eps = eps;
+  const uint16_t* K = (const uint16_t*)k_cache;
+  const uint16_t* V = (const uint16_t*)v_cache;
+  const dim3 grid(max_chunks, hkv, 1);
+  switch (G) {
+    case 1: decode_partial_bf16_kernel<1, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+    case 2: decode_partial_bf16_kernel<2, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+    case 4: decode_partial_bf16_kernel<4, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+    default: decode_partial_bf16_kernel<8, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+  }
+  KH_CHECK_LAUNCH();
+  const int K_in = hq * 128;
+  int rc = KH_OK;
+  AttnMerge am;
+  am.position = position;
+  am.hq = hq;
+  am.max_chunks = max_chunks;
+  am.max_len = ml;
+  am.chunk = CH;
+  if (max_chunks <= kMergeInPrologueMaxChunks &&
+      launch_gemv_attn_merge(part, am, (const uint16_t*)w_o, ldw, x, x, (int)n_out, K_in, 1.f, 1.f)) {
+    KH_CHECK_LAUNCH();
+  } else {
+    // long caches: a separate merge into a bf16 row, then the plain GEMV with the residual
+    uint16_t* o = (uint16_t*)scratch_alloc((size_t)K_in * 2);
+    if (!o) {
+      scratch_free(part);
+      return KH_ERR_OOM;
+    }
+    AttnStrides so{};
+    so.oh = 128;
+    decode_merge_cols_pos_kernel<<<dim3(4, hq, 1), 256, 0, stream()>>>(part, position, ml, hq, max_chunks, so, o);
+    KH_CHECK_LAUNCH();
+    rc = kh_gemv_fused(0, o, nullptr, nullptr, 0.f, w_o, ldw, x, x, nullptr, n_out, K_in, 1.f, 1.f, KH_F32);
+    scratch_free(o);
+  }
+  scratch_free(part);  // stream-ordered: reused only by later work on the same stream
+  return rc;
 }
 
 }  // extern "C"

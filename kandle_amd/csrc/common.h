@@ -18,6 +18,16 @@ bool initialized();
 void* scratch_alloc(size_t bytes);
 void scratch_free(void* p);
 
+// Split-K decode attention partials of one sequence as the o_proj GEMV prologue reads them:
+// o[hq][max_chunks][128] floats, then (m, l)[hq][max_chunks]; chunks of `chunk` keys, the sequence
+// length position[0] + 1 clamped to [0, max_len].
+struct AttnMerge {
+  const int32_t* position = nullptr;
+  int hq = 0, max_chunks = 0, max_len = 0, chunk = 0;
+};
+bool launch_gemv_attn_merge(const float* part, const AttnMerge& am, const uint16_t* W, int64_t ldw, float* C,
+                            const float* cin, int N, int K, float alpha, float beta);
+
 #define KH_CHECK_HIP(expr)                                                              \
   do {                                                                                  \
     hipError_t _e = (expr);                                                             \

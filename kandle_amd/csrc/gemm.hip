@@ -360,18 +360,64 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
 //   PRO_NONE      x' = x                               (x bf16)
 //   PRO_RMSNORM   x' = bf16(rms_norm(x, norm_w, eps))  (x fp32 residual row, norm_w bf16)
 //   PRO_SILU_MUL  x' = bf16(silu(x) * x2)              (x, x2 bf16: gate and up halves)
+//   PRO_ATTN_MERGE x' = bf16(split-K decode attention merged)  (x: the fp32 partials of one sequence,
+//                 o[h][chunk][128] then (m, l)[h][chunk]; see AttnMerge)
 // Each workgroup forms x' once in LDS (fp32, zero past k); each wave then owns U weight rows and
 // streams them with raw 16-byte buffer loads, CB chunks of 512 columns per row in flight (rows past
 // n read as zero), and reduces each row across the wave.  Every weight byte is read once.
 // =============================================================================================
-constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2;
+constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2, PRO_ATTN_MERGE = 3;
+constexpr int kAttnMergeMaxChunks = 8;   // split-K chunks the attention-merge prologue accepts
 constexpr int GV_CHUNK = 512;  // columns per wave-wide 16-byte load (64 lanes x 8 bf16)
 
 template <int PRO>
 __device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const uint16_t* x2, const uint16_t* nw,
-                                              float eps, int K, int kpad) {
+                                              float eps, int K, int kpad, const AttnMerge& am) {
   const int tid = threadIdx.x;
-  if constexpr (PRO == PRO_RMSNORM) {
+  if constexpr (PRO == PRO_ATTN_MERGE) {
+    // Thread t merges columns 8 (t mod 16) .. + 7 of head t / 16 (then t + 256, ...): the chunks'
+    // (m, l, o) combined with weights exp(m_c - M), M the largest chunk max.  Up to kAttnMergeMaxChunks
+    // chunks, every load issued before any math (indices past the last chunk clamped, weight 0).
+    constexpr int MC = kAttnMergeMaxChunks;
+    const float* po = (const float*)x;
+    const float2* pml = reinterpret_cast<const float2*>(po + (int64_t)am.hq * am.max_chunks * 128);
+    const int p = *am.position;
+    const int L = p + 1 < 0 ? 0 : (p + 1 > am.max_len ? am.max_len : p + 1);
+    const int nch = (L + am.chunk - 1) / am.chunk;
+    for (int g = tid; g < (kpad >> 3); g += blockDim.x) {
+      const int h = g >> 4, d0 = (g & 15) * 8;
+      float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (h < am.hq && nch > 0) {
+        float2 ml[MC];
+        float4 oa[MC], ob[MC];
+#pragma unroll
+        for (int c = 0; c < MC; ++c) {
+          const int cc = min(c, nch - 1);
+          ml[c] = pml[(int64_t)h * am.max_chunks + cc];
+          const float4* o4 = reinterpret_cast<const float4*>(po + ((int64_t)h * am.max_chunks + cc) * 128 + d0);
+          oa[c] = o4[0];
+          ob[c] = o4[1];
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < MC; ++c)
+          if (c < nch) M = fmaxf(M, ml[c].x);
+        const float mu = M == -INFINITY ? 0.f : M;
+        float Ls = 0.f, t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < MC; ++c) {
+          const float f = c < nch ? __expf(ml[c].x - mu) : 0.f;
+          Ls += ml[c].y * f;
+          t[0] += oa[c].x * f; t[1] += oa[c].y * f; t[2] += oa[c].z * f; t[3] += oa[c].w * f;
+          t[4] += ob[c].x * f; t[5] += ob[c].y * f; t[6] += ob[c].z * f; t[7] += ob[c].w * f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = round_bf16(Ls > 0.f ? t[e] / Ls : 0.f);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[g * 8 + e] = (g * 8 + e) < K ? v[e] : 0.f;
+    }
+  } else if constexpr (PRO == PRO_RMSNORM) {
     // Rows of up to 8 * blockDim elements stay in registers between the two passes.
     constexpr int PR = 8;
     __shared__ float red[4];
@@ -422,7 +468,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, 
                                                     const uint16_t* __restrict__ nw, float eps,
                                                     const uint16_t* __restrict__ W, int64_t ldw, uint32_t w_bytes,
                                                     TO* C, const TO* cin, const TO* __restrict__ bias, int N, int K,
-                                                    int nch, float alpha, float beta) {
+                                                    int nch, float alpha, float beta, AttnMerge am) {
   constexpr int CB = 8 / U;  // 16-byte loads in flight per row per lane
   extern __shared__ float xs[];
   const int lane = threadIdx.x & 63;
@@ -447,7 +493,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, 
   };
   // The first batch is in flight while the workgroup forms x'.
   if (n0 < N) issue(n0, 0);
-  gemv_prologue<PRO>(xs, x, x2, nw, eps, K, nch * GV_CHUNK);
+  gemv_prologue<PRO>(xs, x, x2, nw, eps, K, nch * GV_CHUNK, am);
 
   for (; n0 < N; n0 += stride) {
     float acc[U];
@@ -499,18 +545,19 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, 
 // assumptions (16-byte aligned weight rows, 32-bit byte offsets, x' within 64 KiB of LDS).
 template <int U, int PRO, typename TO>
 void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw,
-              uint32_t w_bytes, TO* C, const TO* cin, const TO* bias, int N, int K, int nch, float alpha, float beta) {
+              uint32_t w_bytes, TO* C, const TO* cin, const TO* bias, int N, int K, int nch, float alpha, float beta,
+              const AttnMerge& am) {
   const int64_t waves = (N + U - 1) / U;
   int64_t grid = (waves + 3) / 4;
   if (grid > 8192) grid = 8192;  // waves then stride over the remaining rows
   const size_t shm = (size_t)nch * GV_CHUNK * sizeof(float);
   gemv1_kernel<U, PRO, TO><<<(int)grid, 256, shm, stream()>>>(x, (const uint16_t*)x2, (const uint16_t*)nw, eps, W,
-                                                              ldw, w_bytes, C, cin, bias, N, K, nch, alpha, beta);
+                                                              ldw, w_bytes, C, cin, bias, N, K, nch, alpha, beta, am);
 }
 
 template <int PRO, typename TO>
 bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw, TO* C,
-                  const TO* cin, const TO* bias, int N, int K, float alpha, float beta) {
+                  const TO* cin, const TO* bias, int N, int K, float alpha, float beta, const AttnMerge& am = {}) {
   if (N <= 0 || K <= 0) return false;
   const int nch = (K + GV_CHUNK - 1) / GV_CHUNK;
   const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
@@ -521,11 +568,11 @@ bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, cons
     return false;
   const uint32_t wb = (uint32_t)w_bytes;
   if (N >= 16384)
-    gemv1_go<4, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta);
+    gemv1_go<4, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   else if (N >= 2048)
-    gemv1_go<2, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta);
+    gemv1_go<2, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   else
-    gemv1_go<1, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta);
+    gemv1_go<1, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   return true;
 }
 
@@ -666,6 +713,17 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
 }
 
 }  // namespace
+
+namespace kh {
+// o_proj of the decode attention block: C = alpha * merge(part) W^T + beta * cin (fp32 out), with
+// the split-K partials merged in every workgroup's prologue.  False when the shapes do not fit.
+bool launch_gemv_attn_merge(const float* part, const AttnMerge& am, const uint16_t* W, int64_t ldw, float* C,
+                            const float* cin, int N, int K, float alpha, float beta) {
+  if (am.max_chunks > kAttnMergeMaxChunks || K != am.hq * 128) return false;
+  return launch_gemv1<PRO_ATTN_MERGE, float>(part, nullptr, nullptr, 0.f, W, ldw, C, cin, nullptr, N, K, alpha, beta,
+                                             am);
+}
+}  // namespace kh
 
 extern "C" {
 

@@ -129,6 +129,36 @@ def decode_attention(q, k_cache, v_cache, seq_lens, output, scale: float) -> Non
     )
 
 
+def decode_attention_block(qkv, params: dict) -> None:
+    """The attention block of one decode step (kh_decode_attention_block): qkv bf16 [1, hq*D + 2*hkv*D]
+    raw projections of the new token; params: q_norm, k_norm (bf16 [D]), inv_freq (fp32 [D/2]), eps,
+    position (int32 [1], device), k_cache / v_cache ([1, hkv, max_len, D] bf16), w_o (bf16
+    [hidden, hq*D]), x (fp32 residual row [1, hidden], updated in place), scale."""
+    kc, vc, wo, x = params["k_cache"], params["v_cache"], params["w_o"], params["x"]
+    _, hkv, max_len, D = kc.shape
+    n_in = qkv.numel
+    hq = (n_in - 2 * hkv * D) // D
+    if D != 128 or hq <= 0 or hq * D + 2 * hkv * D != n_in:
+        raise ValueError(f"decode_attention_block: qkv of {n_in} values does not split into q/k/v heads of 128")
+    for name, h in (("qkv", qkv), ("q_norm", params["q_norm"]), ("k_norm", params["k_norm"]), ("k_cache", kc),
+                    ("v_cache", vc), ("w_o", wo)):
+        if h.dtype != BFLOAT16:
+            raise TypeError(f"decode_attention_block: {name} must be bfloat16")
+    if not qkv.is_contiguous() or x.dtype != FLOAT32 or not x.is_contiguous():
+        raise TypeError("decode_attention_block: qkv (bf16) and x (fp32) must be contiguous")
+    n_out = x.numel
+    if tuple(wo.shape) != (n_out, hq * D) or wo.strides[1] != 1:
+        raise ValueError(f"decode_attention_block: w_o must be [{n_out}, {hq * D}] with contiguous rows")
+    pos = params["position"]
+    if pos.dtype != INT32 or pos.numel < 1:
+        raise TypeError("decode_attention_block: position must be an int32 device tensor")
+    strides = _lib.i64_array([kc.strides[1], kc.strides[2], vc.strides[1], vc.strides[2]])
+    _lib.call("kh_decode_attention_block", _vp(qkv.data_ptr()), _vp(params["q_norm"].data_ptr()),
+              _vp(params["k_norm"].data_ptr()), _vp(params["inv_freq"].data_ptr()), C.c_float(params["eps"]),
+              _vp(pos.data_ptr()), _vp(kc.data_ptr()), _vp(vc.data_ptr()), hq, hkv, max_len, strides,
+              C.c_float(params["scale"]), _vp(wo.data_ptr()), wo.strides[0], n_out, _vp(x.data_ptr()))
+
+
 # ---------------------------------------------------------------------------------------------
 # matmul
 # ---------------------------------------------------------------------------------------------
@@ -608,6 +638,7 @@ def philox4x32_10(seed: int, counters, out) -> None:
 
 KERNELS = {
     "sample": sample,
+    "decode_attention_block": decode_attention_block,
     "flash_attention": flash_attention,
     "decode_attention": decode_attention,
     "matmul": matmul,

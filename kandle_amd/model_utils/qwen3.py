@@ -188,6 +188,9 @@ class Qwen3ForCausalLM:
         self.cache = StaticKVCache(cfg.num_hidden_layers, 1, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
         self.scale = 1.0 / np.sqrt(cfg.head_dim)
         self._prefill_graphs: Dict[int, tuple] = {}   # prompt length -> (graph, ids, positions, logits)
+        # Decode steps run each layer's attention block (qk-norm, RoPE, K/V write, attention, o_proj)
+        # as one library call; False runs the separate launches (the prefill's path at S = 1).
+        self.fused_decode = True
 
     # -- decoder body shared by the prefill and the device-resident decode step -------------------
     @classmethod
@@ -210,48 +213,31 @@ class Qwen3ForCausalLM:
         model.load_result = result
         return model
 
-    def _decoder(self, x: Tensor, S: int, positions: Tensor, attend) -> Tensor:
+    def _decoder(self, x: Tensor, S: int, positions: Tensor, attend, decode_block: bool = False) -> Tensor:
         """Runs every decoder layer over the fp32 residual rows x [S, hidden] in place and returns
         the fp32 logits of the last position [1, vocab].  positions: int32 [S] device tensor
         (RoPE angles and KV-cache rows); attend(layer, q_heads, out_view) writes attention for
         q_heads [1, Hq, S, D] into out_view [1, Hq, S, D].  A single row (decode) runs each norm
-        and the SwiGLU product inside the projection that consumes it (linear_fused)."""
+        and the SwiGLU product inside the projection that consumes it (linear_fused); with
+        decode_block the whole attention block after the QKV projection (qk-norm, RoPE, K/V cache
+        write, attention over rows [0, position], o_proj and the residual add) is one library call
+        (decode_attention_block) and `attend` is not used."""
         cfg = self.cfg
         Hq, Hkv, D, Hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
         nq, nkv, I = Hq * D, Hkv * D, cfg.intermediate_size
         eps = cfg.rms_norm_eps
         one = S == 1
         for li, L in enumerate(self.layers):
-            if one:
+            if one and decode_block:
                 qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
+                self.ops.find("decode_attention_block")(qkv.handle, {
+                    "q_norm": L["q_norm"].handle, "k_norm": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
+                    "eps": eps, "position": positions.handle, "k_cache": self.cache.key_cache[li].handle,
+                    "v_cache": self.cache.value_cache[li].handle, "w_o": L["w_o"].handle, "x": x.handle,
+                    "scale": self.scale})                                                # x += o W_o^T
+                qkv.dispose()
             else:
-                h = F.rms_norm(x, [Hd], L["in_norm"], eps, out_dtype="bfloat16")
-                qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
-                h.dispose()
-            q = _split_heads(qkv, 0, S, Hq, D)
-            k = _split_heads(qkv, nq, S, Hkv, D)
-            v = _split_heads(qkv, nq + nkv, S, Hkv, D)
-            q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
-            # K (normed + rotated) and V land in the cache rows given by `positions`.
-            self.ops.find("rms_norm_rope")(q.handle, k.handle, {
-                "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
-                "positions": positions.handle, "eps": eps, "q_out": q_heads,
-                "k_out": self.cache.key_cache[li].handle, "v": v.handle, "v_out": self.cache.value_cache[li].handle,
-                "cache_positions": True})
-            for t in (q, k, v, qkv):
-                t.dispose()
-            attn = HipTensorHandle.create_new((S, nq), "bfloat16")
-            # [1, Hq, S, D] view of the [S, Hq*D] buffer: o_proj then reads it as a plain matrix.
-            attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
-            attend(li, q_heads, attn_view)
-            attn_view.dispose()
-            q_heads.dispose()
-            attn_t = Tensor(handle=attn)
-            if one:
-                F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
-            else:
-                F.dispatch_matmul(attn_t, L["w_o"], c=x, beta=1.0, out=x, transpose_b=True)
-            attn_t.dispose()
+                self._attention_unfused(li, L, x, S, positions, attend, one)
             if one:
                 gu = F.linear_fused("rms_norm", x, L["w_gu"], L["post_norm"], eps)     # [1, 2I]
             else:
@@ -276,6 +262,44 @@ class Qwen3ForCausalLM:
             xf.dispose()
         last.dispose()
         return logits
+
+    def _attention_unfused(self, li: int, L: dict, x: Tensor, S: int, positions: Tensor, attend, one: bool) -> None:
+        """The attention block of layer li as separate launches: QKV projection, qk-norm + RoPE with
+        the K/V cache write, attend(), o_proj with the residual add into x."""
+        cfg = self.cfg
+        Hq, Hkv, D, Hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
+        nq, nkv = Hq * D, Hkv * D
+        eps = cfg.rms_norm_eps
+        if one:
+            qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
+        else:
+            h = F.rms_norm(x, [Hd], L["in_norm"], eps, out_dtype="bfloat16")
+            qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
+            h.dispose()
+        q = _split_heads(qkv, 0, S, Hq, D)
+        k = _split_heads(qkv, nq, S, Hkv, D)
+        v = _split_heads(qkv, nq + nkv, S, Hkv, D)
+        q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+        # K (normed + rotated) and V land in the cache rows given by `positions`.
+        self.ops.find("rms_norm_rope")(q.handle, k.handle, {
+            "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
+            "positions": positions.handle, "eps": eps, "q_out": q_heads,
+            "k_out": self.cache.key_cache[li].handle, "v": v.handle, "v_out": self.cache.value_cache[li].handle,
+            "cache_positions": True})
+        for t in (q, k, v, qkv):
+            t.dispose()
+        attn = HipTensorHandle.create_new((S, nq), "bfloat16")
+        # [1, Hq, S, D] view of the [S, Hq*D] buffer: o_proj then reads it as a plain matrix.
+        attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
+        attend(li, q_heads, attn_view)
+        attn_view.dispose()
+        q_heads.dispose()
+        attn_t = Tensor(handle=attn)
+        if one:
+            F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
+        else:
+            F.dispatch_matmul(attn_t, L["w_o"], c=x, beta=1.0, out=x, transpose_b=True)
+        attn_t.dispose()
 
     # -- one forward over S new tokens at cache position `pos` -------------------------------------
     def _forward_dev(self, ids: Tensor, positions: Tensor, end: int) -> Tensor:
@@ -343,7 +367,7 @@ class Qwen3ForCausalLM:
                                                self.cache.value_cache[li].handle, st.lens.handle, out_view,
                                                self.scale)
 
-        logits = self._decoder(x, 1, st.pos, attend)
+        logits = self._decoder(x, 1, st.pos, attend, decode_block=self.fused_decode)
         x.dispose()
         return logits
 

@@ -117,3 +117,28 @@ def test_from_pretrained_sharded_checkpoint_matches_in_memory(hip, tmp_path):
         assert np.array_equal(a, b)
     otoks, _ = Qwen3Oracle(cfg, w, max_seq_len=64).generate(prompt, 6)
     assert toks == otoks
+
+
+def test_fused_decode_block_matches_unfused_and_oracle(hip):
+    """The decode step's fused attention block (kh_decode_attention_block: qk-norm + RoPE of q and of
+    the new k row, K/V cache write, split-K attention, merge in the o_proj prologue, residual) against
+    the same step run as separate launches, and both against the oracle; caches past 8 chunks of
+    256 keys take the separate merge."""
+    from oracle.qwen3 import Qwen3Oracle
+
+    for max_seq, prompt_len in ((128, 40), (3000, 2100)):   # prologue merge; merge kernel (9+ chunks)
+        cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
+        w = init_qwen3_weights(cfg, seed=21)
+        prompt = syn.randint(22, (prompt_len,), 0, cfg.vocab_size)
+        out = {}
+        for fused in (True, False):
+            model = Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq)
+            model.fused_decode = fused
+            out[fused] = model.generate(prompt, 6, return_logits=True, use_graph=fused)
+            model.dispose()
+        (ft, fl), (ut, ul) = out[True], out[False]
+        rt, rl = Qwen3Oracle(cfg, w, max_seq_len=max_seq).generate(prompt, 6)
+        for i in range(1, 6):   # decode steps (index 0 is the prefill)
+            assert float(np.max(np.abs(fl[i] - ul[i]))) < 5e-3, (max_seq, i)
+            assert float(np.max(np.abs(fl[i] - rl[i]))) < LOGIT_ATOL, (max_seq, i)
+        assert ft == ut == rt, max_seq
