@@ -440,6 +440,105 @@ def cpu_baseline_prefill(n_slices=1):
                       f"single thread ({dt:.1f} s); host has {os.cpu_count()} cores"}
 
 
+def _one_thread():
+    """Context that limits numpy's BLAS to one thread (the CPU baselines state cores = 1)."""
+    try:
+        from threadpoolctl import threadpool_limits
+        return threadpool_limits(1)
+    except ImportError:  # pragma: no cover
+        import contextlib
+        return contextlib.nullcontext()
+
+
+def cpu_baseline_decode():
+    """C4 at full size on the CPU: the oracle's SDPA (double accumulation, one thread) for each of the
+    8 sequences' single query against its whole cache, fp32 inputs; GB/s of the bf16 K/V bytes the GPU
+    kernel reads (lengths as in bench_decode)."""
+    import oracle
+    from kandle_amd import synthetic as syn
+
+    B, Hq, Hkv, D = 8, 16, 8, 128
+    lens = syn.randint(2024, (B,), 8192, 32769)
+    dt = 0.0
+    for b in range(B):
+        L = int(lens[b])
+        q = syn.normal(3000 + b, (1, Hq, 1, D))
+        k = syn.normal(4000 + b, (1, Hkv, L, D))
+        v = syn.normal(5000 + b, (1, Hkv, L, D))
+        t0 = time.perf_counter()
+        oracle.sdpa(q, k, v)
+        dt += time.perf_counter() - t0
+    nbytes = float(lens.sum()) * Hkv * D * 2 * 2
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"full C4 (sum L = {int(lens.sum())}), oracle SDPA in C, one thread, {dt:.2f} s"}
+
+
+def cpu_baseline_norm():
+    """C2 at full size on the CPU: the oracle's RMSNorm over [8192, 1024] and qk-norm + RoPE over q
+    [8192, 16, 128] and k [8192, 8, 128] (C, one thread); GB/s of the bf16 bytes the GPU kernels move."""
+    import oracle
+    from kandle_amd import synthetic as syn
+
+    T, H, Hq, Hkv, D = 8192, 1024, 16, 8, 128
+    x = syn.normal(501, (T, H))
+    q = syn.normal(502, (T, Hq, D))
+    k = syn.normal(503, (T, Hkv, D))
+    w = syn.uniform(504, (H,), 0.5, 1.5)
+    wq = syn.uniform(505, (D,), 0.5, 1.5)
+    wk = syn.uniform(506, (D,), 0.5, 1.5)
+    inv = oracle.rope_inv_freq(D, 1e6)
+    pos = np.arange(T, dtype=np.int32)
+    t0 = time.perf_counter()
+    oracle.rms_norm(x, w, 1e-6)
+    oracle.qk_norm_rope(q, wq, pos, inv, 1e-6)
+    oracle.qk_norm_rope(k, wk, pos, inv, 1e-6)
+    dt = time.perf_counter() - t0
+    nbytes = 134220288.0
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"full C2 (8192 tokens), oracle in C, one thread, {dt:.2f} s"}
+
+
+def cpu_baseline_model(prompt_len=512, decode_steps=4):
+    """C5 on the CPU, extrapolated: the numpy oracle (one BLAS thread) of ONE decoder layer of the
+    0.6B architecture over the 512-token prompt and `decode_steps` one-token steps after it, times 28
+    layers, plus the lm_head row; tokens/s for prefill and decode."""
+    import dataclasses
+
+    from kandle_amd import synthetic as syn
+    from kandle_amd.model_utils import Qwen3Config, init_qwen3_weights
+    from oracle.qwen3 import Qwen3Oracle
+
+    full = Qwen3Config()
+    cfg = dataclasses.replace(full, num_hidden_layers=1)
+    w = init_qwen3_weights(cfg, seed=7)
+    prompt = syn.randint(8, (prompt_len,), 0, cfg.vocab_size)
+    with _one_thread():
+        ref = Qwen3Oracle(cfg, w, max_seq_len=prompt_len + decode_steps + 1)
+        t0 = time.perf_counter()
+        logits = ref.forward(prompt, 0)
+        t_pre = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        pos = prompt_len
+        for _ in range(decode_steps):
+            logits = ref.forward([int(np.argmax(logits))], pos)
+            pos += 1
+        t_dec = (time.perf_counter() - t0) / decode_steps
+        # lm_head share, measured on its own and not multiplied by the layer count
+        e = ref.embed
+        hrow = np.zeros((1, cfg.hidden_size), np.float32)
+        t0 = time.perf_counter()
+        for _ in range(3):
+            hrow @ e.T
+        t_head = (time.perf_counter() - t0) / 3
+    L = full.num_hidden_layers
+    pre_s = (t_pre - t_head) * L + t_head
+    dec_s = (t_dec - t_head) * L + t_head
+    return {"prefill_tokens_per_s": round(prompt_len / pre_s, 2), "decode_tokens_per_s": round(1.0 / dec_s, 3),
+            "cores": 1, "kind": "port",
+            "sample": f"extrapolated: 1 of 28 layers measured (prefill {t_pre:.2f} s, decode {t_dec * 1e3:.1f} ms/step "
+                      f"incl. lm_head {t_head * 1e3:.1f} ms), numpy oracle, one BLAS thread"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -495,7 +594,15 @@ def main():
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
-        cpu = cpu_baseline_prefill(16)
+        with _one_thread():
+            cpu = cpu_baseline_prefill(16)
+    cpu_more = {}
+    if not args.no_cpu_baseline and args.only is None:
+        log("cpu baselines of C4, C2, C5 ...")
+        with _one_thread():
+            cpu_more["decode"] = cpu_baseline_decode()
+            cpu_more["norm_rope"] = cpu_baseline_norm()
+        cpu_more["model"] = cpu_baseline_model()
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded Philox N(0,1))"}
@@ -594,6 +701,9 @@ def main():
                      "ms_per_step": st["stream_ms_per_token"],
                      "config": {"workload": "C5 Qwen3-0.6B generate_stream, T=0.6 top-k 20 top-p 0.95, 512-token "
                                             "prompt", **st}})
+    for key, val in cpu_more.items():
+        if key in line:
+            line[key]["cpu_baseline"] = val
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 
