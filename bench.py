@@ -12,7 +12,7 @@ and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against th
 `--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv]
+                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv|vendor]
 Prints ONE JSON line.
 """
 import argparse
@@ -330,6 +330,71 @@ def bench_gemv(steps, warmup):
     return out
 
 
+def bench_vendor(steps):
+    """Reference points from the vendor stack in this image, on the same shapes (not part of this
+    backend): torch's scaled_dot_product_attention on C3 (each backend torch offers here, with the
+    KV heads expanded to Hq since GQA is not taken natively), and torch.matmul (hipBLASLt) on the
+    C5 prefill projection GEMMs, 20 calls captured in a CUDA graph and replayed."""
+    import torch
+    import torch.nn.functional as TF
+
+    dev = "cuda"
+    out = {}
+    B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, S, D, device=dev, dtype=torch.bfloat16, generator=g)
+    k = torch.randn(B, Hkv, S, D, device=dev, dtype=torch.bfloat16, generator=g)
+    v = torch.randn(B, Hkv, S, D, device=dev, dtype=torch.bfloat16, generator=g)
+    kk = k.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+    vv = v.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+    flops = 4.0 * B * Hq * S * S * D / 2
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel(be):
+                for _ in range(3):
+                    TF.scaled_dot_product_attention(q, kk, vv, is_causal=True)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(steps):
+                    TF.scaled_dot_product_attention(q, kk, vv, is_causal=True)
+                e1.record()
+                torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            out[f"sdpa_{name}"] = {"ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+        except Exception as ex:  # a backend torch does not offer for these inputs
+            out[f"sdpa_{name}"] = {"unavailable": str(ex)[:160]}
+    gem = {}
+    for name, N, K, _ in GEMM_SHAPES:
+        x = torch.randn(512, K, device=dev, dtype=torch.bfloat16, generator=g)
+        w = torch.randn(N, K, device=dev, dtype=torch.bfloat16, generator=g)
+        s2 = torch.cuda.Stream()
+        s2.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s2):
+            for _ in range(3):
+                x @ w.t()
+        torch.cuda.current_stream().wait_stream(s2)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(20):
+                x @ w.t()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 100 * 1e3
+        gem[name] = {"us": round(us, 2), "TFLOP/s": round(2.0 * 512 * N * K / (us * 1e-6) / 1e12, 1)}
+    gem["layer_us"] = round(sum(v["us"] for v in gem.values()), 2)
+    out["gemm_hipblaslt"] = gem
+    return out
+
+
 def bench_sample(steps, warmup):
     """On-device sampling of one token from a Qwen3 logits row (vocab 151936, float32): kh_sample
     per call for greedy, an unfiltered draw, and temperature 0.7 with top-k 50 and top-p 0.9 (the
@@ -548,17 +613,22 @@ def main():
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
     ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream",
-                                       "gemm", "gemv"], default=None)
+                                       "gemm", "gemv", "vendor"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
 
-    from kandle_amd import HipBackend
-
-    HipBackend.create(0)
     res = {}
+    if args.only == "vendor":
+        # torch carries its own HIP runtime: it must be the only one to open the device in this process
+        log("vendor reference points (torch SDPA, hipBLASLt) ...")
+        res["vendor"] = bench_vendor(args.steps)
+    else:
+        from kandle_amd import HipBackend
+
+        HipBackend.create(0)
     if args.only in (None, "prefill"):
         log("prefill C3 ...")
         res["prefill"] = bench_prefill(args.steps, args.warmup)
@@ -688,6 +758,12 @@ def main():
                      "roofline": {"bound": "mfma", "achieved": gm["layer_TFLOP/s"], "peak": PEAK_BF16_TFLOPS,
                                   "unit": "TFLOP/s", "frac": round(gm["layer_TFLOP/s"] / PEAK_BF16_TFLOPS, 4),
                                   "traffic": None}})
+    if "vendor" in res:
+        vd = res["vendor"]
+        best = max((v.get("TFLOP/s", 0.0) for k2, v in vd.items() if k2.startswith("sdpa_")), default=0.0)
+        line.update({"value": best, "unit": "TFLOP/s", "ms_per_step": None,
+                     "config": {"workload": "vendor stack reference points on C3 and the C5 prefill GEMMs "
+                                            "(torch SDPA, hipBLASLt); not this backend", **vd}})
     if "gemv" in res:
         gv = res["gemv"]
         lm = gv["lm_head"]
