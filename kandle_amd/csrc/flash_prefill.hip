@@ -419,9 +419,10 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
         f32x16 sacc[C::NSUB];
         F.qk(ks + c * C::BNC * FA_KSTR, qreg, sacc);
         F.template mask<CAUSAL>(tc, lk, sacc);
-        // P is computed with the current reference max while the tile max is checked (the two are
-        // independent, so their instructions interleave); a raise, rare after the first tile,
-        // rescales O and l and recomputes P.
+        // Written as P computed with the current reference max, then recomputed after a raise
+        // (rare after the first tile).  The compiler folds the two into one exponentiation after
+        // the max check, so the generated code checks the max (lane-pair exchange included) first
+        // and exponentiates once, in the same basic block as the PV product.
         bf16x8 pk[2 * C::NSUB];
         float ps = sm.exponentiate(sacc, c2, pk);
         if (sm.update(sacc, c2, oacc)) ps = sm.exponentiate(sacc, c2, pk);
