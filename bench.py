@@ -9,10 +9,11 @@ algorithm on a bounded sample as the CPU baseline.
 
 It also runs the full Qwen3-0.6B model of config C5 (512-token prefill, 128 greedy decode steps)
 and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against their rooflines.
-`--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters.
+`--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters; `--only mask` times the
+explicit-mask SDPA route at C3 shapes.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv|vendor]
+                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv|vendor|mask]
 Prints ONE JSON line.
 """
 import argparse
@@ -79,6 +80,34 @@ def bench_prefill(steps, warmup):
         t.dispose()
     o.dispose()
     return {"B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D, "flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+
+def bench_mask(steps, warmup):
+    """C3 shapes with an explicit [S, S] float32 mask (the top-left causal pattern as -inf / 0):
+    the masked route scores every (query, key) pair, so the work is the full 4 B Hq S^2 D."""
+    from kandle_amd import HipTensorHandle, Tensor, kernels
+
+    B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
+    q = bf16_tensor(301, (B, Hq, S, D))
+    k = bf16_tensor(302, (B, Hkv, S, D))
+    v = bf16_tensor(303, (B, Hkv, S, D))
+    m = Tensor(np.where(np.arange(S)[None, :] > np.arange(S)[:, None], -np.inf, 0.0).astype(np.float32))
+    o = HipTensorHandle.create_new((B, Hq, S, D), "bfloat16")
+    scale = 1.0 / np.sqrt(D)
+    fn = lambda: kernels.sdpa_masked(q.handle, k.handle, v.handle, m.handle, o, scale)  # noqa: E731
+    wall_ms, dev_ms = time_calls(fn, steps, warmup)
+    flops = 4.0 * B * Hq * S * S * D
+    out = o.data_async()
+    assert np.all(np.isfinite(out)), "masked prefill produced non-finite values"
+    for t in (q, k, v, m):
+        t.dispose()
+    o.dispose()
+    tf = flops / (dev_ms * 1e-3) / 1e12
+    return {"workload": "C3 shapes with an explicit [4096, 4096] float32 mask (causal pattern), all pairs scored",
+            "flops": flops, "ms": round(dev_ms, 4), "wall_ms": round(wall_ms, 4), "TFLOP/s": round(tf, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4)},
+            "kernel": "flash_fwd_kernel<64, 8, 1, false, true, 1>"}
 
 
 def bench_decode(steps, warmup):
@@ -613,7 +642,7 @@ def main():
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
     ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream",
-                                       "gemm", "gemv", "vendor"], default=None)
+                                       "gemm", "gemv", "vendor", "mask"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -661,6 +690,9 @@ def main():
     if args.only == "gemv":
         log("C5 decode GEMVs ...")
         res["gemv"] = bench_gemv(args.steps, args.warmup)
+    if args.only == "mask":
+        log("explicit-mask SDPA at C3 shapes ...")
+        res["mask"] = bench_mask(args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
@@ -771,6 +803,12 @@ def main():
                      "config": {"workload": "C5 decode one-row GEMVs (bf16 weights), graph-replayed", **gv},
                      "roofline": {"bound": "hbm", "achieved": lm["GB/s"], "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                   "frac": round(lm["GB/s"] / PEAK_HBM_GBPS, 4), "traffic": None}})
+    if "mask" in res:
+        mk = res["mask"]
+        line.update({"value": mk["TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": mk["wall_ms"],
+                     "config": {"workload": mk["workload"], "batch": 4, "q_heads": 16, "kv_heads": 8,
+                                "seq_len": 4096, "head_dim": 128},
+                     "roofline": dict(mk["roofline"], traffic=None, kernel=mk["kernel"], kernel_ms=mk["ms"])})
     if "stream" in res:
         st = res["stream"]
         line.update({"value": round(1e3 / st["stream_ms_per_token"], 1), "unit": "tokens/s",

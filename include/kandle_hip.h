@@ -233,6 +233,23 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o,
                        int batch, int hq, int hkv, int64_t lq, int64_t lk, int d,
                        const int64_t* strides, float scale, int causal, int dtype);
 
+/* Scaled dot-product attention with an explicit additive mask:
+ * O = softmax(scale * Q K^T + mask) V, GQA as kh_flash_attention, no causal masking.  This is the
+ * reference's attnMask route (packages/core/src/dispatch/handlers/composite.ts:279-300: matmul with
+ * alpha = scale, add_Tensor(mask), softmax(-1), matmul), fused into one kernel; the reference has
+ * no kernel for it.  Its softmax (packages/backend-webgpu/src/kernels/normalize/shaderBuilder.ts:
+ * 143-213) starts the row max at f32(-1e38), so a row whose every score is far below -1e38
+ * (e.g. all -inf) is 0 / 0: that row's output is NaN.  The mask (dtype KH_F32 or KH_BF16) is
+ * read as mask[b * mask_strides[0] + h * mask_strides[1] + i * mask_strides[2] + j * mask_strides[3]]
+ * for batch b, query head h, query i, key j: element strides, 0 broadcasts an axis.  q/k/v/o
+ * layouts and `strides` as kh_flash_attention.  bf16 with d == 128 runs the MFMA kernel (a mask
+ * without unit key stride and 16-byte aligned 8-key runs is first packed into a scratch copy);
+ * otherwise the fp32-math kernel (d <= 256). */
+int kh_flash_attention_masked(const void* q, const void* k, const void* v, void* o,
+                              int batch, int hq, int hkv, int64_t lq, int64_t lk, int d,
+                              const int64_t* strides, float scale, const void* mask,
+                              const int64_t* mask_strides, int mask_dtype, int dtype);
+
 /* Decode attention for one query token per sequence against a KV cache with per-sequence
  * lengths seq_lens[b] (device int32, each in [1, max_len]); no mask (the caller turns causal off
  * for 1-token decode, reference packages/model-utils/src/attention/gqa.ts:333-336).

@@ -11,6 +11,14 @@ struct AttnStrides {
   int64_t qb, qh, qs, kb, kh, ks, vb, vh, vs, ob, oh, os;
 };
 
+// Explicit additive attention mask (the reference's attnMask route, composite.ts:279-300).
+struct MaskArgs {
+  int64_t sb, sh, sq, sk;  // element strides over (batch, query head, query, key); 0 broadcasts
+  uint32_t bytes;          // byte extent of the mask: buffer loads past it read 0
+  float inv_scale;         // 1 / scale: the mask joins raw q.k scores as mask / scale
+  float floor_raw;         // the reference softmax's f32(-1e38) max floor in raw q.k units
+};
+
 // True when the bf16 MFMA prefill kernel takes this call (d = 128, G in {1,2,4,8}, 16-byte
 // aligned rows, per-head byte ranges addressable with 32-bit buffer offsets).
 bool flash_prefill_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv,
@@ -19,5 +27,12 @@ bool flash_prefill_supported(const void* q, const void* k, const void* v, const 
 // Launches the prefill kernel on the library stream; returns KH_OK or an error code.
 int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
                               int lq, int lk, const AttnStrides& st, float scale, bool causal);
+
+// The prefill kernel with an additive mask (f32 or bf16, KH_F32 / KH_BF16) instead of causal
+// masking; 64-key stages.  Requires flash_prefill_supported(), ma.sk == 1, every 8-key run of the
+// mask 16-byte aligned (base and sb, sh, sq multiples of 8 elements) and ma.bytes < 2^31.
+int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq,
+                                     int hkv, int lq, int lk, const AttnStrides& st, float scale, const void* mask,
+                                     const MaskArgs& ma, int mask_dtype);
 
 }  // namespace kh

@@ -18,11 +18,17 @@ namespace {
 // per step (lane j scores key k0 + j), fp32 online softmax, each lane accumulates d/64 output
 // columns.  Used for fp32 calls (config C1) and shapes the MFMA kernel does not take.
 // =============================================================================================
+//
+// With a mask M (mdt KH_F32 or KH_BF16; the reference's explicit-mask route, composite.ts:279-300)
+// a score is s = (q . k) * scale + M[b, h, i, j], causal is not applied, the running max starts at
+// f32(-1e38) as in the reference softmax (normalize/shaderBuilder.ts:190-195), and a row whose
+// exponentials sum to 0 stores NaN (0 / 0).
 template <typename T>
 __global__ __launch_bounds__(256) void attn_generic_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                            const T* __restrict__ V, T* __restrict__ O, int batch,
                                                            int hq, int hkv, int lq, int lk, int D, AttnStrides st,
-                                                           float scale, int causal) {
+                                                           float scale, int causal, const void* __restrict__ M,
+                                                           int mdt, MaskArgs ma) {
   __shared__ float qs[4][256];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -40,7 +46,8 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const T* __restrict__
   const T* Kb = K + b * st.kb + hk * st.kh;
   const T* Vb = V + b * st.vb + hk * st.vh;
   const int kend = causal ? min(lk, i + 1) : lk;
-  float m = -INFINITY, l = 0.f;
+  const int64_t mrow = M ? b * ma.sb + h * ma.sh + (int64_t)i * ma.sq : 0;
+  float m = M ? -1e38f : -INFINITY, l = 0.f;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};  // columns lane, lane+64, lane+128, lane+192
   for (int k0 = 0; k0 < kend; k0 += 64) {
     const int key = k0 + lane;
@@ -50,6 +57,11 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const T* __restrict__
       float dot = 0.f;
       for (int d = 0; d < D; ++d) dot += qs[w][d] * Elem<T>::load(kr, d);
       s = dot * scale;
+      if (M) {
+        const int64_t mi = mrow + (int64_t)key * ma.sk;
+        s += mdt == KH_F32 ? static_cast<const float*>(M)[mi]
+                           : bf16_bits_to_f32(static_cast<const uint16_t*>(M)[mi]);
+      }
     }
     const float mx = fmaxf(m, wave_max(s));
     const float alpha = expf(m - mx);
@@ -70,12 +82,28 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const T* __restrict__
     m = mx;
   }
   T* orow = O + b * st.ob + h * st.oh + (int64_t)i * st.os;
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const float inv = l > 0.f ? 1.0f / l : (M ? __builtin_nanf("") : 0.f);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int d = lane + 64 * c;
     if (d < D) Elem<T>::store(orow, d, acc[c] * inv);
   }
+}
+
+// Copies a strided mask into rows of ldm elements (unit key stride, 16-byte aligned 8-key runs)
+// for the MFMA kernel: dst[((b' nh + h') nq + q') ldm + j] = src[b' sb + h' sh + q' sq + j sk] for
+// j < lk, 0 for lk <= j < ldm.  Broadcast axes (stride 0) keep extent 1.
+template <typename T>
+__global__ __launch_bounds__(256) void mask_pack_kernel(const T* __restrict__ src, T* __restrict__ dst, int nh,
+                                                        int nq, int lk, int ldm, int64_t sb, int64_t sh, int64_t sq,
+                                                        int64_t sk, int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int q = (int)(row % nq), h = (int)((row / nq) % nh);
+  const int64_t b = row / ((int64_t)nq * nh);
+  const T* s = src + b * sb + h * sh + (int64_t)q * sq;
+  T* d = dst + row * ldm;
+  for (int j = threadIdx.x & 63; j < ldm; j += 64) d[j] = j < lk ? s[(int64_t)j * sk] : T(0);
 }
 
 // =============================================================================================
@@ -659,6 +687,26 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   return KH_OK;
 }
 
+int launch_generic(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
+                   int d, const AttnStrides& st, float scale, int causal, const void* mask, int mask_dtype,
+                   const MaskArgs& ma, int dtype) {
+  KH_REQUIRE(d <= 256, "kh_flash_attention: head_dim %d > 256 is not supported", d);
+  const int64_t rows = (int64_t)batch * hq * lq;
+  const int64_t grid = (rows + 3) / 4;
+  KH_REQUIRE(grid <= INT32_MAX, "kh_flash_attention: grid too large");
+  if (dtype == KH_BF16)
+    attn_generic_kernel<uint16_t><<<(int)grid, 256, 0, stream()>>>((const uint16_t*)q, (const uint16_t*)k,
+                                                                   (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv,
+                                                                   lq, lk, d, st, scale, causal, mask, mask_dtype,
+                                                                   ma);
+  else
+    attn_generic_kernel<float><<<(int)grid, 256, 0, stream()>>>((const float*)q, (const float*)k, (const float*)v,
+                                                                (float*)o, batch, hq, hkv, lq, lk, d, st, scale,
+                                                                causal, mask, mask_dtype, ma);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -690,21 +738,81 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
   }
   if (dtype == KH_BF16 && lq > 1 && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
     return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, st, scale, causal != 0);
+  return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal, nullptr, 0, MaskArgs{},
+                        dtype);
+}
 
-  KH_REQUIRE(d <= 256, "kh_flash_attention: head_dim %d > 256 is not supported", d);
-  const int64_t rows = (int64_t)batch * hq * lq;
-  const int64_t grid = (rows + 3) / 4;
-  KH_REQUIRE(grid <= INT32_MAX, "kh_flash_attention: grid too large");
-  if (dtype == KH_BF16)
-    attn_generic_kernel<uint16_t><<<(int)grid, 256, 0, stream()>>>((const uint16_t*)q, (const uint16_t*)k,
-                                                                   (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv,
-                                                                   (int)lq, (int)lk, d, st, scale, causal);
-  else
-    attn_generic_kernel<float><<<(int)grid, 256, 0, stream()>>>((const float*)q, (const float*)k, (const float*)v,
-                                                                (float*)o, batch, hq, hkv, (int)lq, (int)lk, d, st,
-                                                                scale, causal);
-  KH_CHECK_LAUNCH();
-  return KH_OK;
+int kh_flash_attention_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
+                              int64_t lq, int64_t lk, int d, const int64_t* strides, float scale, const void* mask,
+                              const int64_t* mask_strides, int mask_dtype, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(batch >= 0 && hq > 0 && hkv > 0 && lq >= 0 && lk >= 0 && d > 0,
+             "kh_flash_attention_masked: bad extents");
+  KH_REQUIRE(hq % hkv == 0, "kh_flash_attention_masked: numHeadsQ (%d) must be divisible by numHeadsKV (%d)", hq,
+             hkv);
+  KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_flash_attention_masked: unsupported dtype %d", dtype);
+  KH_REQUIRE(mask_dtype == KH_BF16 || mask_dtype == KH_F32, "kh_flash_attention_masked: unsupported mask dtype %d",
+             mask_dtype);
+  KH_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX, "kh_flash_attention_masked: sequence too long");
+  if (batch == 0 || lq == 0) return KH_OK;
+  KH_REQUIRE(q && k && v && o && strides && mask && mask_strides, "kh_flash_attention_masked: null pointer");
+  KH_REQUIRE(lk > 0, "kh_flash_attention_masked: the key sequence is empty (softmax over no keys is undefined)");
+  const AttnStrides st = load_strides(strides);
+  MaskArgs ma{};
+  ma.sb = mask_strides[0];
+  ma.sh = mask_strides[1];
+  ma.sq = mask_strides[2];
+  ma.sk = mask_strides[3];
+  ma.inv_scale = 1.0f / scale;
+  // The reference softmax's max floor f32(-1e38) in raw q.k units (scores carry 1 / scale).
+  const double fl = (double)-1e38f / (double)scale;
+  ma.floor_raw = (scale > 0.f && fl >= -(double)FLT_MAX) ? (float)fl : -INFINITY;
+
+  if (!(dtype == KH_BF16 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st)))
+    return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
+
+  // MFMA path: the mask must have a unit key stride and 16-byte aligned 8-key runs; otherwise it is
+  // packed into rows of ldm = lk rounded up to 8 elements (broadcast axes stay broadcast).
+  const int es = mask_dtype == KH_F32 ? 4 : 2;
+  const bool direct = ma.sk == 1 && ((uintptr_t)mask % 16) == 0 && ma.sb % 8 == 0 && ma.sh % 8 == 0 &&
+                      ma.sq % 8 == 0 && ma.sb >= 0 && ma.sh >= 0 && ma.sq >= 0;
+  const void* mp = mask;
+  void* packed = nullptr;
+  int64_t extent;
+  if (direct) {
+    extent = ((int64_t)(batch - 1) * ma.sb + (int64_t)(hq - 1) * ma.sh + (lq - 1) * ma.sq + lk) * es;
+  } else {
+    const int nb = ma.sb ? batch : 1, nh = ma.sh ? hq : 1, nq = ma.sq ? (int)lq : 1;
+    const int ldm = (int)((lk + 7) / 8 * 8);
+    const int64_t rows = (int64_t)nb * nh * nq;
+    extent = rows * ldm * es;
+    KH_REQUIRE(extent < (int64_t(1) << 31), "kh_flash_attention_masked: mask larger than 2 GiB");
+    packed = scratch_alloc((size_t)extent);
+    if (!packed) return KH_ERR_OOM;
+    const int64_t grid = (rows + 3) / 4;
+    KH_REQUIRE(grid <= INT32_MAX, "kh_flash_attention_masked: mask grid too large");
+    if (mask_dtype == KH_F32)
+      mask_pack_kernel<float><<<(int)grid, 256, 0, stream()>>>((const float*)mask, (float*)packed, nh, nq, (int)lk,
+                                                                ldm, ma.sb, ma.sh, ma.sq, ma.sk, rows);
+    else
+      mask_pack_kernel<uint16_t><<<(int)grid, 256, 0, stream()>>>((const uint16_t*)mask, (uint16_t*)packed, nh, nq,
+                                                                   (int)lk, ldm, ma.sb, ma.sh, ma.sq, ma.sk, rows);
+    ma.sb = ma.sb ? (int64_t)nh * nq * ldm : 0;
+    ma.sh = ma.sh ? (int64_t)nq * ldm : 0;
+    ma.sq = ma.sq ? ldm : 0;
+    ma.sk = 1;
+    mp = packed;
+  }
+  int rc = KH_OK;
+  if (extent >= (int64_t(1) << 31)) {
+    rc = launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
+  } else {
+    ma.bytes = (uint32_t)extent;
+    rc = launch_flash_prefill_bf16_masked(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, st, scale, mp, ma,
+                                          mask_dtype);
+  }
+  if (packed) scratch_free(packed);  // stream-ordered: reused only by later work on the same stream
+  return rc;
 }
 
 int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o, const int32_t* seq_lens,

@@ -271,11 +271,63 @@ struct Flash {
       }
     }
   }
-  // O[qi][d] = oacc / l; lane holds d = 32dt + 8(j/4) + 4g + j%4.
+  // Additive mask of a 64-key tile t for this lane's query row (MASKT 1: f32, 2: bf16), held as
+  // four runs of eight keys: run (s, h) = keys 64 t + 32 s + 16 h + 8 g .. + 7, which are the S^T
+  // registers sc[s][8 h .. 8 h + 7].  The mask has a unit key stride and 16-byte aligned 8-key runs
+  // (the entry point packs other masks first).  Rows past lq read row lq - 1 (their output is not
+  // stored); reads past the mask's byte extent return 0 (buffer range check), and keys >= lk are
+  // masked to -inf by apply_mask whatever was read.
+  template <int MASKT>
+  struct MaskRegs {
+    uint4 v[MASKT == 1 ? 8 : 4];
+  };
+  template <int MASKT>
+  __device__ __forceinline__ void load_mask(int t, int lq, __amdgpu_buffer_rsrc_t rm, const MaskArgs& ma,
+                                            MaskRegs<MASKT>& mr) const {
+    constexpr int ES = MASKT == 1 ? 4 : 2;
+    const int64_t rowoff = b * ma.sb + hqi * ma.sh + (int64_t)min(qi, lq - 1) * ma.sq;
+#pragma unroll
+    for (int run = 0; run < 4; ++run) {  // run = 2 s + h
+      const uint32_t off = (uint32_t)((rowoff + t * 64 + 16 * run + 8 * g) * ES);
+      if constexpr (MASKT == 1) {
+        mr.v[2 * run] = buf_load16(rm, off);
+        mr.v[2 * run + 1] = buf_load16(rm, off + 16);
+      } else {
+        mr.v[run] = buf_load16(rm, off);
+      }
+    }
+  }
+  static __device__ __forceinline__ uint32_t comp(const uint4& u, int i) {
+    return i == 0 ? u.x : (i == 1 ? u.y : (i == 2 ? u.z : u.w));
+  }
+  // Scores of tile t become q.k + mask / scale (raw units; the exponent multiplies by scale
+  // log2 e), keys >= lk become -inf.
+  template <int MASKT>
+  __device__ __forceinline__ void apply_mask(int t, int lk, const MaskRegs<MASKT>& mr, float inv_scale,
+                                             f32x16 (&sc)[C::NSUB]) const {
+#pragma unroll
+    for (int s = 0; s < C::NSUB; ++s)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int run = 2 * s + (j >> 3), e = j & 7;
+        uint32_t bits;
+        if constexpr (MASKT == 1)
+          bits = comp(mr.v[2 * run + (e >> 2)], e & 3);
+        else
+          bits = (e & 1) ? (comp(mr.v[run], e >> 1) & 0xffff0000u) : (comp(mr.v[run], e >> 1) << 16);
+        const float mv = __builtin_bit_cast(float, bits);
+        const int key = t * 64 + 32 * s + 16 * (j >> 3) + 8 * g + e;
+        sc[s][j] = key < lk ? __builtin_fmaf(mv, inv_scale, sc[s][j]) : -INFINITY;
+      }
+  }
+  // O[qi][d] = oacc / l; lane holds d = 32dt + 8(j/4) + 4g + j%4.  A row whose sum l is 0 stores
+  // zeros, or NaN with NAN_EMPTY (the reference softmax's 0 / 0 on the explicit-mask route).
+  template <bool NAN_EMPTY = false>
   __device__ __forceinline__ void store_o(uint16_t* O, int lq, float l_run, const f32x16 (&oacc)[4]) const {
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     if (qi < lq) {
       const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+      const bool nan_row = NAN_EMPTY && !(l_tot > 0.f);
       uint16_t* orow = O + b * st.ob + hqi * st.oh + (int64_t)qi * st.os;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
@@ -285,6 +337,7 @@ struct Flash {
           uint2 w;
           w.x = pack_bf16x2(oacc[dt][4 * a + 0] * inv, oacc[dt][4 * a + 1] * inv);
           w.y = pack_bf16x2(oacc[dt][4 * a + 2] * inv, oacc[dt][4 * a + 3] * inv);
+          if (nan_row) w = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
           *reinterpret_cast<uint2*>(orow + d) = w;
         }
     }
@@ -306,8 +359,11 @@ struct Softmax {
 
   // Raises the reference max when this tile needs it (rescaling O and l); true (wave-uniform) if
   // any lane did, in which case P must be recomputed.
+  // floor: the lowest row max (raw units): the reference softmax starts its max at f32(-1e38)
+  // on the explicit-mask route; -inf otherwise.
   template <int NSUB>
-  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4]) {
+  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4],
+                                         float floor = -INFINITY) {
     float m4[NSUB * 4];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
@@ -317,7 +373,7 @@ struct Softmax {
     float mx = m4[0];
 #pragma unroll
     for (int i = 1; i < NSUB * 4; ++i) mx = fmaxf(mx, m4[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(fmaxf(mx, __shfl_xor(mx, 32, 64)), floor);
     // NaN-free by construction (this file is compiled assuming no NaNs, so that fmaxf needs no
     // canonicalisation): a row with nothing unmasked (mx = -inf) never asks for a raise, and
     // m_ref = -inf only before the first raise, where alpha = 2^-inf = 0 clears the empty O and l.
@@ -362,12 +418,15 @@ struct Softmax {
 // =============================================================================================
 // Tile-synchronous kernel.
 // =============================================================================================
-template <int BN, int WAVES, int MINB, bool CAUSAL, bool VTR = false>
+// MASKT: 0 = causal / none as CAUSAL says; 1, 2 = additive f32 / bf16 mask M (64-key tiles, no
+// causal mask, the reference's explicit-mask route).
+template <int BN, int WAVES, int MINB, bool CAUSAL, bool VTR = false, int MASKT = 0>
 __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale,
-    int n_qblocks) {
+    int n_qblocks, const void* __restrict__ M, MaskArgs ma) {
   using C = Cfg<BN, WAVES, VTR>;
+  static_assert(MASKT == 0 || (BN == 64 && !CAUSAL), "masked tiles are 64 keys, without causal masking");
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
   Flash<BN, WAVES, VTR> F;
@@ -405,8 +464,14 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  using MR = typename Flash<BN, WAVES, VTR>::template MaskRegs<MASKT == 0 ? 2 : MASKT>;
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(M, MASKT == 0 ? 0u : ma.bytes);
   for (int t = 0; t < ntiles; ++t) {
     const bool has_next = t + 1 < ntiles;
+    // The mask loads go out before the next tile's K/V prefetch, so that waiting for them never
+    // waits for the prefetch (the vector-memory counter retires in issue order).
+    MR mreg;
+    if constexpr (MASKT != 0) F.template load_mask<MASKT>(t, lq, rm, ma, mreg);
     if (has_next) {
       F.load_k(t + 1, kst);
       load_v(t + 1);
@@ -418,14 +483,17 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
       if (tc < F.wave_tiles) {
         f32x16 sacc[C::NSUB];
         F.qk(ks + c * C::BNC * FA_KSTR, qreg, sacc);
-        F.template mask<CAUSAL>(tc, lk, sacc);
+        if constexpr (MASKT != 0)
+          F.template apply_mask<MASKT>(tc, lk, mreg, ma.inv_scale, sacc);
+        else
+          F.template mask<CAUSAL>(tc, lk, sacc);
         // Written as P computed with the current reference max, then recomputed after a raise
         // (rare after the first tile).  The compiler folds the two into one exponentiation after
         // the max check, so the generated code checks the max (lane-pair exchange included) first
         // and exponentiates once, in the same basic block as the PV product.
         bf16x8 pk[2 * C::NSUB];
         float ps = sm.exponentiate(sacc, c2, pk);
-        if (sm.update(sacc, c2, oacc)) ps = sm.exponentiate(sacc, c2, pk);
+        if (sm.update(sacc, c2, oacc, MASKT != 0 ? ma.floor_raw : -INFINITY)) ps = sm.exponentiate(sacc, c2, pk);
         sm.l_run += ps;
         if constexpr (VTR)
           F.pv_tr(ks + C::KTILE + c * C::BNC * C::VSTR, pk, oacc);
@@ -440,7 +508,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     }
     __syncthreads();
   }
-  F.store_o(O, lq, sm.l_run, oacc);
+  F.template store_o<MASKT != 0>(O, lq, sm.l_run, oacc);
 }
 
 int flash_variant() {
@@ -460,12 +528,13 @@ void launch_sync(bool causal, const void* q, const void* k, const void* v, void*
                  int lq, int lk, const AttnStrides& st, float scale, int nqb, int nblk) {
   const uint16_t *Q = (const uint16_t*)q, *K = (const uint16_t*)k, *V = (const uint16_t*)v;
   uint16_t* O = (uint16_t*)o;
+  const MaskArgs none{};
   if (causal)
     flash_fwd_kernel<BN, WAVES, MINB, true, VTR><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq,
-                                                                                   lk, st, scale, nqb);
+                                                                                   lk, st, scale, nqb, nullptr, none);
   else
-    flash_fwd_kernel<BN, WAVES, MINB, false, VTR><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq,
-                                                                                    lk, st, scale, nqb);
+    flash_fwd_kernel<BN, WAVES, MINB, false, VTR><<<nblk, WAVES * 64, 0, stream()>>>(
+        Q, K, V, O, batch, hq, hkv, lq, lk, st, scale, nqb, nullptr, none);
 }
 
 }  // namespace
@@ -506,6 +575,27 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
     launch_sync<64, 8, 1, true>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
   else
     launch_sync<64, 4, 2>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq,
+                                     int hkv, int lq, int lk, const AttnStrides& st, float scale, const void* mask,
+                                     const MaskArgs& ma, int mask_dtype) {
+  const int G = hq / hkv;
+  const int BMQ = 32 * (8 / G);
+  const int nqb = (lq + BMQ - 1) / BMQ;
+  const int64_t nblk64 = (int64_t)nqb * batch * hkv;
+  KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention_masked: grid too large");
+  const int nblk = (int)nblk64;
+  const uint16_t *Q = (const uint16_t*)q, *K = (const uint16_t*)k, *V = (const uint16_t*)v;
+  uint16_t* O = (uint16_t*)o;
+  if (mask_dtype == KH_F32)
+    flash_fwd_kernel<64, 8, 1, false, true, 1><<<nblk, 512, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk, st,
+                                                                            scale, nqb, mask, ma);
+  else
+    flash_fwd_kernel<64, 8, 1, false, true, 2><<<nblk, 512, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk, st,
+                                                                            scale, nqb, mask, ma);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -50,22 +50,26 @@ def _wrap(h: HipTensorHandle) -> Tensor:
 def scaled_dot_product_attention(query: Tensor, key: Tensor, value: Tensor, attn_mask: Optional[Tensor] = None,
                                  dropout_p: float = 0.0, is_causal: bool = False,
                                  scale: Optional[float] = None, out: Optional[Tensor] = None) -> Tensor:
-    """softmax(scale * Q K^T [+ causal]) V.  q (..., L, E), k (..., S, E), v (..., S, Ev) -> (..., L, Ev).
+    """softmax(scale * Q K^T [+ causal | + attn_mask]) V.  q (..., L, E), k (..., S, E),
+    v (..., S, Ev) -> (..., L, Ev).
 
     Like the reference: dropout_p > 0 is warned about and ignored (inference), the default scale is
-    1/sqrt(E), and the `flash_attention` kernel is found by name."""
+    1/sqrt(E), the `flash_attention` kernel is found by name, and an explicit attn_mask takes the
+    masked route (added to the scaled scores, is_causal ignored, composite.ts:279-300), which this
+    backend runs as the fused `sdpa_masked` kernel instead of matmul -> add -> softmax -> matmul."""
     if dropout_p > 0:
         warnings.warn("SDPA: dropout_p > 0 is not supported in inference mode, ignoring")
     E = query.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(E)
-    if attn_mask is not None:
-        # The reference routes explicit masks to matmul -> add -> softmax -> matmul; this backend
-        # has no softmax kernel on the hot path, so an explicit mask is rejected rather than faked.
-        raise NotImplementedError("scaled_dot_product_attention: explicit attn_mask is not supported by the HIP backend")
     out_shape = tuple(query.shape[:-1]) + (value.shape[-1],)
     output = out.handle if out is not None else _new(query, out_shape)
-    _kernel(query, "flash_attention")(query.handle, key.handle, value.handle, output, float(scale), bool(is_causal))
+    if attn_mask is not None:
+        _kernel(query, "sdpa_masked")(query.handle, key.handle, value.handle, attn_mask.handle, output,
+                                      float(scale))
+    else:
+        _kernel(query, "flash_attention")(query.handle, key.handle, value.handle, output, float(scale),
+                                          bool(is_causal))
     return out if out is not None else _wrap(output)
 
 

@@ -103,6 +103,74 @@ def flash_attention(query, key, value, output, scale: float, is_causal: bool) ->
             t.dispose()
 
 
+def _mask_strides(mask, target) -> list:
+    """Element strides of `mask` broadcast (numpy rules, trailing axes aligned) to the 4-D score
+    shape `target` = [B, Hq, Lq, Lk]; 0 for a broadcast axis.  Shapes that do not broadcast raise,
+    as the reference's add_Tensor does."""
+    shape, strides = list(mask.shape), list(mask.strides)
+    if len(shape) > 4:
+        raise ValueError(f"sdpa_masked: attn_mask has {len(shape)} dims, scores have 4")
+    shape = [1] * (4 - len(shape)) + shape
+    strides = [0] * (4 - len(strides)) + strides
+    out = []
+    for n, st, t in zip(shape, strides, target):
+        if n == t:
+            out.append(st if t > 1 else 0)
+        elif n == 1:
+            out.append(0)
+        else:
+            raise ValueError(f"sdpa_masked: attn_mask shape {tuple(mask.shape)} cannot be broadcast to the "
+                             f"attention scores {tuple(target)}")
+    return out
+
+
+def sdpa_masked(query, key, value, mask, output, scale: float) -> None:
+    """O = softmax(scale * Q K^T + mask) V, the reference's explicit-mask route
+    (packages/core/src/dispatch/handlers/composite.ts:279-300) in one kernel: the mask is added to
+    the scaled scores (broadcast over [B, Hq, Lq, Lk]), causal masking is not applied, and a row
+    whose exponentials sum to 0 (every score far below -1e38, e.g. all -inf) is NaN, as the
+    reference softmax's 0 / 0 (normalize/shaderBuilder.ts:143-213).  GQA as flash_attention."""
+    for name, h in (("query", query), ("key", key), ("value", value), ("output", output)):
+        if h.dtype not in (FLOAT32, BFLOAT16):
+            raise TypeError(f"sdpa_masked: {name} dtype {h.dtype} not supported")
+    if not (query.dtype == key.dtype == value.dtype == output.dtype):
+        raise TypeError("sdpa_masked: query/key/value/output dtypes differ")
+    if mask.dtype not in (FLOAT32, BFLOAT16):
+        raise TypeError(f"sdpa_masked: attn_mask dtype {mask.dtype} not supported (additive float32 or bfloat16)")
+    tmp = []
+    try:
+        hs = []
+        for h in (query, key, value):
+            if not _last_dim_contiguous(h):
+                h = _materialize(h)
+                tmp.append(h)
+            hs.append(h)
+        q, k, v = hs
+        qs, qst = _as_4d(q)
+        ks, kst = _as_4d(k)
+        vs, vst = _as_4d(v)
+        os_, ost = _as_4d(output)
+        B, Hq, Lq, D = qs
+        Bk, Hkv, Lk, Dk = ks
+        if Bk != B or vs[0] != B or Dk != D or vs[1] != Hkv or vs[2] != Lk or vs[3] != D:
+            raise ValueError(f"sdpa_masked: incompatible shapes q{qs} k{ks} v{vs}")
+        if Hq % Hkv != 0:
+            raise ValueError(f"sdpa_masked: numHeadsQ ({Hq}) must be divisible by numHeadsKV ({Hkv})")
+        if tuple(os_) != (B, Hq, Lq, D) or ost[3] != 1:
+            raise ValueError(f"sdpa_masked: output must be [B,Hq,Lq,D] with a contiguous last dim, got {os_}")
+        ms = _mask_strides(mask, (B, Hq, Lq, Lk))
+        strides = _lib.i64_array(qst[:3] + kst[:3] + vst[:3] + ost[:3])
+        _lib.call(
+            "kh_flash_attention_masked",
+            _vp(q.data_ptr()), _vp(k.data_ptr()), _vp(v.data_ptr()), _vp(output.data_ptr()),
+            B, Hq, Hkv, Lq, Lk, D, strides, C.c_float(scale), _vp(mask.data_ptr()), _lib.i64_array(ms),
+            mask.kh_dtype, q.kh_dtype,
+        )
+    finally:
+        for t in tmp:
+            t.dispose()
+
+
 def decode_attention(q, k_cache, v_cache, seq_lens, output, scale: float) -> None:
     """One query token per sequence against [B, Hkv, max_len, D] caches with per-sequence lengths.
 
@@ -640,6 +708,7 @@ KERNELS = {
     "sample": sample,
     "decode_attention_block": decode_attention_block,
     "flash_attention": flash_attention,
+    "sdpa_masked": sdpa_masked,
     "decode_attention": decode_attention,
     "matmul": matmul,
     "mm": matmul,

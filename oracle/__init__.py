@@ -50,6 +50,8 @@ def lib():
         L.or_silu_mul.argtypes = [f32p, C.c_void_p, f32p, i64]
         L.or_linear.argtypes = [f32p, f32p, C.c_void_p, C.c_void_p, f32p, i64, i64, i64, C.c_float, C.c_float]
         L.or_argmax.argtypes = [f32p, i64, i64, i32p]
+        L.or_sdpa_masked.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, i64, i64, C.c_int,
+                                     C.c_float, C.c_void_p, i64, i64, i64, i64, f64p]
         L.or_flash_f32.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, i64, i64, C.c_int, C.c_float,
                                    C.c_int, i64]
         for fn in ("or_f32_to_bf16", "or_bf16_to_f32", "or_sdpa", "or_rms_norm", "or_rope_inv_freq",
@@ -99,6 +101,23 @@ def sdpa(q, k, v, scale=None, causal=False, kv_len=None) -> np.ndarray:
     work = np.zeros(max(Lk, 1), np.float64)
     kl = None if kv_len is None else np.ascontiguousarray(kv_len, dtype=np.int32)
     lib().or_sdpa(q, k, v, o, B, Hq, Hkv, Lq, Lk, D, float(scale), int(bool(causal)), _ptr(kl), work)
+    return o
+
+
+def sdpa_masked(q, k, v, mask, scale=None) -> np.ndarray:
+    """softmax(scale * Q K^T + mask) V with the reference's softmax (row max floored at -1e38, a
+    row summing to 0 gives NaN); mask broadcasts to [B, Hq, Lq, Lk] (numpy rules)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Hq, Lq, D = q.shape
+    _, Hkv, Lk, _ = k.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    m = np.broadcast_to(np.asarray(mask, dtype=np.float32), (B, Hq, Lq, Lk))
+    ms = [st // 4 for st in m.strides]
+    o = np.zeros((B, Hq, Lq, D), np.float32)
+    work = np.zeros(max(Lk, 1), np.float64)
+    lib().or_sdpa_masked(q, k, v, o, B, Hq, Hkv, Lq, Lk, D, float(scale), C.c_void_p(m.ctypes.data),
+                         ms[0], ms[1], ms[2], ms[3], work)
     return o
 
 

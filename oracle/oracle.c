@@ -82,6 +82,55 @@ void or_sdpa(const float* q, const float* k, const float* v, float* o, int B, in
 }
 
 /*
+ * SDPA with an explicit additive mask: the reference's naive route for attnMask
+ * (packages/core/src/dispatch/handlers/composite.ts:279-300), which ignores isCausal:
+ *   W = matmul(q, k^T) * scale            (dispatchMatmul alpha = scale, transposeB),
+ *   W = W + mask                          (add_Tensor with broadcasting),
+ *   P = softmax(W, -1)                    (packages/backend-webgpu/src/kernels/normalize/
+ *                                          shaderBuilder.ts:143-213: the row max starts at
+ *                                          f32(-1e38), p = exp(x - max), P = p / sum p, so a row whose
+ *                                          sum is 0 -- every x <= -1e38 far enough -- is 0/0 = NaN),
+ *   O = matmul(P, v).
+ * GQA as in or_sdpa.  The mask is float32 with element strides (msb, msh, msq, msk) over (batch,
+ * query head, query, key); a stride of 0 broadcasts that axis.  work: Lk doubles.
+ */
+void or_sdpa_masked(const float* q, const float* k, const float* v, float* o, int B, int Hq, int Hkv, int64_t Lq,
+                    int64_t Lk, int D, float scale, const float* mask, int64_t msb, int64_t msh, int64_t msq,
+                    int64_t msk, double* work) {
+  const int G = Hq / Hkv;
+  const double floor_max = (double)(float)-1e38;
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hq; ++h) {
+      const int hk = h / G;
+      const float* kb = k + ((int64_t)b * Hkv + hk) * Lk * D;
+      const float* vb = v + ((int64_t)b * Hkv + hk) * Lk * D;
+      for (int64_t i = 0; i < Lq; ++i) {
+        const float* qi = q + (((int64_t)b * Hq + h) * Lq + i) * D;
+        float* oi = o + (((int64_t)b * Hq + h) * Lq + i) * D;
+        const float* mrow = mask + b * msb + h * msh + i * msq;
+        double m = floor_max;
+        for (int64_t j = 0; j < Lk; ++j) {
+          const float* kj = kb + j * D;
+          double dot = 0.0;
+          for (int d = 0; d < D; ++d) dot += (double)qi[d] * (double)kj[d];
+          work[j] = dot * (double)scale + (double)mrow[j * msk];
+          if (work[j] > m) m = work[j];
+        }
+        double l = 0.0;
+        for (int64_t j = 0; j < Lk; ++j) {
+          work[j] = exp(work[j] - m);
+          l += work[j];
+        }
+        for (int d = 0; d < D; ++d) {
+          double acc = 0.0;
+          for (int64_t j = 0; j < Lk; ++j) acc += work[j] * (double)vb[j * D + d];
+          oi[d] = (float)(acc / l); /* l == 0: 0/0 = NaN, as the reference's softmax */
+        }
+      }
+    }
+}
+
+/*
  * RMSNorm over rows of n: y = x * (1 / sqrt(mean(x^2) + eps)) * w
  * (packages/backend-webgpu/src/kernels/normalize/shaderBuilder.ts:394-411; normalizedShape = trailing
  * dims, packages/backend-webgpu/src/kernels/normalize/executor.ts:280-293).  w may be NULL.

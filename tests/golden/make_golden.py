@@ -13,6 +13,9 @@ checks in tests/test_oracle.py.
     f_i = float32(float32(pos) * inv_freq_i) is the reference's float32 product.
   * silu_mul: torch.nn.functional.silu(g) * u, float64.
   * linear: torch.nn.functional.linear, float64.
+  * sdpam / sdpamb: scaled_dot_product_attention with a float attn_mask (added to the scaled scores),
+    float64: a full [B,H,L,S] mask with -inf entries under GQA, and a broadcast [L,S] mask holding the
+    bottom-right causal pattern of the reference's capture path plus noise.
 
 Run: python tests/golden/make_golden.py   (CPU only; writes the .npz beside this file)
 """
@@ -71,6 +74,28 @@ def main():
     a, wt, b = randn(3, 7), randn(5, 7), randn(5)
     d["lin_a"], d["lin_w"], d["lin_b"] = a.numpy(), wt.numpy(), b.numpy()
     d["lin_y"] = F.linear(a.double(), wt.double(), b.double()).float().numpy()
+
+    # ---- SDPA with an explicit additive float mask (GQA 4/2 heads; a full [B,H,L,S] mask with
+    #      -inf entries, and a broadcast [L,S] bottom-right causal mask on a rectangular case) ----
+    qm, km, vm = randn(2, 4, 9, 16), randn(2, 2, 9, 16), randn(2, 2, 9, 16)
+    mm = randn(2, 4, 9, 9) * 2.0
+    drop = torch.rand(2, 4, 9, 9, generator=g) < 0.3
+    drop[..., 0] = False  # keep one finite score per row
+    mm = mm.masked_fill(drop, float("-inf"))
+    d["sdpam_q"], d["sdpam_k"], d["sdpam_v"], d["sdpam_mask"] = qm.numpy(), km.numpy(), vm.numpy(), mm.numpy()
+    d["sdpam_o"] = F.scaled_dot_product_attention(qm.double(), km.double(), vm.double(), attn_mask=mm.double(),
+                                                   enable_gqa=True).float().numpy()
+    qr, kr, vr = randn(1, 2, 5, 8), randn(1, 2, 11, 8), randn(1, 2, 11, 8)
+    L, S = 5, 11
+    br = torch.zeros(L, S)
+    for i in range(L):
+        for j in range(S):
+            if j > i + (S - L):
+                br[i, j] = float("-inf")
+    br = br + randn(L, S) * 0.5
+    d["sdpamb_q"], d["sdpamb_k"], d["sdpamb_v"], d["sdpamb_mask"] = qr.numpy(), kr.numpy(), vr.numpy(), br.numpy()
+    d["sdpamb_o"] = F.scaled_dot_product_attention(qr.double(), kr.double(), vr.double(),
+                                                   attn_mask=br.double()).float().numpy()
 
     np.savez_compressed(OUT, **d)
     print(f"wrote {OUT} ({len(d)} arrays)")

@@ -94,6 +94,64 @@ def test_sdpa_kv_len_equals_truncation():
     np.testing.assert_allclose(o[1:2], oracle.sdpa(q[1:2], k[1:2], v[1:2]), rtol=1e-6)
 
 
+# ------------------------------------------------------------------------------ SDPA with mask
+def test_sdpa_masked_matches_torch_golden():
+    o = oracle.sdpa_masked(G["sdpam_q"], G["sdpam_k"], G["sdpam_v"], G["sdpam_mask"])
+    np.testing.assert_allclose(o, G["sdpam_o"], rtol=1e-5, atol=1e-6)
+    # broadcast [L, S] mask holding the capture path's bottom-right causal pattern plus noise
+    o = oracle.sdpa_masked(G["sdpamb_q"], G["sdpamb_k"], G["sdpamb_v"], G["sdpamb_mask"])
+    np.testing.assert_allclose(o, G["sdpamb_o"], rtol=1e-5, atol=1e-6)
+
+
+def test_sdpa_masked_invariants():
+    r = np.random.default_rng(5)
+    q, k, v = r.standard_normal((2, 4, 7, 8)), r.standard_normal((2, 2, 7, 8)), r.standard_normal((2, 2, 7, 8))
+    # a zero mask is the unmasked (non-causal) attention
+    np.testing.assert_allclose(oracle.sdpa_masked(q, k, v, np.zeros((7, 7))), oracle.sdpa(q, k, v),
+                               rtol=1e-6, atol=1e-7)
+    # -inf above the diagonal is the top-left causal attention
+    tri = np.where(np.arange(7)[None, :] > np.arange(7)[:, None], -np.inf, 0.0)
+    np.testing.assert_allclose(oracle.sdpa_masked(q, k, v, tri), oracle.sdpa(q, k, v, causal=True),
+                               rtol=1e-6, atol=1e-7)
+    # adding a constant per (batch, head, row) does not change the softmax
+    m = r.standard_normal((2, 4, 7, 7))
+    shift = r.standard_normal((2, 4, 7, 1)) * 5.0
+    np.testing.assert_allclose(oracle.sdpa_masked(q, k, v, m), oracle.sdpa_masked(q, k, v, m + shift),
+                               rtol=1e-5, atol=1e-6)
+    # broadcasting over batch and heads equals the expanded mask
+    m2 = r.standard_normal((7, 7))
+    np.testing.assert_allclose(oracle.sdpa_masked(q, k, v, m2),
+                               oracle.sdpa_masked(q, k, v, np.broadcast_to(m2, (2, 4, 7, 7)).copy()), rtol=1e-6)
+    # explicit scale enters before the mask is added: scale s with mask M equals scale 1 on q*s
+    np.testing.assert_allclose(oracle.sdpa_masked(q, k, v, m, scale=0.3),
+                               oracle.sdpa_masked(q * 0.3, k, v, m, scale=1.0), rtol=1e-5, atol=1e-6)
+
+
+def test_sdpa_masked_brute_force_and_reference_softmax_floor():
+    r = np.random.default_rng(6)
+    q, k, v = r.standard_normal((1, 1, 3, 4)), r.standard_normal((1, 1, 5, 4)), r.standard_normal((1, 1, 5, 4))
+    m = r.standard_normal((3, 5))
+    m[1, 2] = -np.inf
+    o = oracle.sdpa_masked(q, k, v, m, scale=0.5)
+    ref = np.zeros((3, 4))
+    for i in range(3):
+        x = np.array([q[0, 0, i] @ k[0, 0, j] * 0.5 + m[i, j] for j in range(5)])
+        p = np.exp(x - x.max())
+        ref[i] = (p / p.sum()) @ v[0, 0]
+    np.testing.assert_allclose(o[0, 0], ref, rtol=1e-5, atol=1e-6)
+    # The reference softmax starts its max at f32(-1e38) (shaderBuilder.ts:190-195): with q = 0 the
+    # scores are the mask values themselves.
+    z = np.zeros((1, 1, 4, 4))
+    mk = np.array([[-1e38, -1e38, -1e38, -1e38],      # x = max floor: p = 1 each -> mean of V
+                   [-3e38, -3e38, -3e38, -3e38],      # every p underflows: 0 / 0 = NaN
+                   [-1.5e38, -1.2e38, -np.inf, -3e38],  # all below the floor: NaN (a plain softmax picks key 1)
+                   [-np.inf, 0.0, -np.inf, -np.inf]], np.float32)  # one finite key -> that V row
+    o = oracle.sdpa_masked(z, k[:, :, :4], v[:, :, :4], mk)
+    np.testing.assert_allclose(o[0, 0, 0], v[0, 0, :4].mean(axis=0), rtol=1e-6)
+    assert np.all(np.isnan(o[0, 0, 1])) and np.all(np.isnan(o[0, 0, 2]))
+    np.testing.assert_allclose(o[0, 0, 3], v[0, 0, 1], rtol=1e-6)
+
+
 def test_flash_f32_baseline_agrees_with_oracle():
     r = np.random.default_rng(3)
     q, k, v = (r.standard_normal((1, 4, 37, 16)).astype(np.float32), r.standard_normal((1, 2, 37, 16)),
