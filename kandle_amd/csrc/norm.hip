@@ -177,20 +177,21 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   T* kot = ko + b * st.s[9] + kv_row * st.s[10];
   T* vot = vo ? vo + b * st.s[15] + kv_row * st.s[16] : vo;
 
-  // Row steps are processed in batches of NB (the host picks NB = min(4, spw)): every load of a
-  // batch is issued, unconditionally, before any math, so a wave keeps NB * 32 bytes per lane in
-  // flight.  Rows past the end of a partial step or batch load a valid clamped row and store nothing.
+  // Row steps are processed in batches of NB: every load of a batch is issued, unconditionally,
+  // before any math, so a wave keeps NB * 32 bytes per lane in flight.  Rows past the end of a
+  // partial step or batch load a valid clamped row and store nothing.  The host uses NB = 1: at
+  // NB = 3 the kernel needs 142 VGPRs (3 waves per SIMD), at NB = 1 106 (4 waves), and the extra
+  // resident waves hide more latency than the deeper batch (C2: 4.97 -> 5.28 TB/s).
   float cs[8], sn[8];
   // The frequencies are loaded before the rows (loads complete in order, so the angles can then be
   // computed while the row loads are in flight); the weights after them.
-  typename Vec8<T>::Raw rwqa, rwqb, rwka, rwkb;
   float f0 = 0.f, f1 = 0.f;
   if (step0 < qk_steps) {
     if (lane < HALF) f0 = inv_freq[lane];
     if (HALF > 64 && lane + 64 < HALF) f1 = inv_freq[lane + 64];
   }
   for (int base = step0; base < step1; base += NB) {
-    typename Vec8<T>::Raw ra[NB], rc[NB];
+    typename Vec8<T>::Raw ra[NB], rc[NB], rwa[NB], rwb[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int step = min(base + u, step1 - 1);
@@ -198,6 +199,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       if (step < qk_steps) {
         const int r = min(step * RPW + rsub, total_rows - 1);
         src = r < hq ? qt + (int64_t)r * st.s[2] : kt + (int64_t)(r - hq) * st.s[5];
+        // this lane's row weights (q_norm or k_norm), loaded with the row
+        const T* wsrc = r < hq ? wq : wk;
+        rwa[u] = Vec8<T>::ld(wsrc + 8 * t);
+        rwb[u] = Vec8<T>::ld(wsrc + HALF + 8 * t);
       } else {
         const int h = min((step - qk_steps) * RPW + rsub, hkv - 1);
         src = vt + (int64_t)h * st.s[14];
@@ -206,10 +211,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       rc[u] = Vec8<T>::ld(src + HALF + 8 * t);
     }
     if (base == step0 && step0 < qk_steps) {
-      rwqa = Vec8<T>::ld(wq + 8 * t);
-      rwqb = Vec8<T>::ld(wq + HALF + 8 * t);
-      rwka = Vec8<T>::ld(wk + 8 * t);
-      rwkb = Vec8<T>::ld(wk + HALF + 8 * t);
       // Keeps the angle computation below the row loads (the compiler would otherwise hoist it,
       // and its wait for the frequencies, above them).
       asm volatile("" : "+v"(f0), "+v"(f1));
@@ -253,26 +254,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss += a[j] * a[j] + c[j] * c[j];
         ss = group_sum<LPR>(ss);
-        // Weights of this lane's row: whole steps of q rows or of k rows select them uniformly.
         float wa[8], wb[8];
-        if (step * RPW + RPW <= hq) {
-          Vec8<T>::cvt(rwqa, wa);
-          Vec8<T>::cvt(rwqb, wb);
-        } else if (step * RPW >= hq) {
-          Vec8<T>::cvt(rwka, wa);
-          Vec8<T>::cvt(rwkb, wb);
-        } else {
-          float xa[8], xb[8];
-          Vec8<T>::cvt(rwqa, wa);
-          Vec8<T>::cvt(rwqb, wb);
-          Vec8<T>::cvt(rwka, xa);
-          Vec8<T>::cvt(rwkb, xb);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            wa[j] = isq ? wa[j] : xa[j];
-            wb[j] = isq ? wb[j] : xb[j];
-          }
-        }
+        Vec8<T>::cvt(rwa[u], wa);
+        Vec8<T>::cvt(rwb[u], wb);
         if (active) {
           const float inv = 1.0f / sqrtf(ss / (float)D + eps);
           float oa[8], oc[8];
@@ -302,12 +286,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 
 template <typename T, int D, typename... Args>
 void launch_qk_norm_rope_d(int nb, int grid, int block, Args... args) {
-  switch (nb) {
-    case 1: qk_norm_rope_kernel<T, D, 1><<<grid, block, 0, stream()>>>(args...); break;
-    case 2: qk_norm_rope_kernel<T, D, 2><<<grid, block, 0, stream()>>>(args...); break;
-    case 3: qk_norm_rope_kernel<T, D, 3><<<grid, block, 0, stream()>>>(args...); break;
-    default: qk_norm_rope_kernel<T, D, 4><<<grid, block, 0, stream()>>>(args...); break;
-  }
+  (void)nb;  // one row step per load batch (see the kernel)
+  qk_norm_rope_kernel<T, D, 1><<<grid, block, 0, stream()>>>(args...);
 }
 template <typename T, typename... Args>
 void launch_qk_norm_rope(int head_dim, int nb, int grid, int block, Args... args) {
@@ -398,7 +378,7 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out, cons
   const int total_steps = (n_q_heads + n_kv_heads + rpw - 1) / rpw + (v ? (n_kv_heads + rpw - 1) / rpw : 0);
   const int spw = n_tokens >= 2048 ? total_steps : 1;
   const int groups = (total_steps + spw - 1) / spw;
-  const int nb = spw < 4 ? spw : 4;
+  const int nb = 1;
   const int waves = 4;
   const int64_t grid = (n_tokens * groups + waves - 1) / waves;
   KH_REQUIRE(grid * waves <= (int64_t)UINT32_MAX && seq_len <= (int64_t)UINT32_MAX,
