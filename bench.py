@@ -515,8 +515,11 @@ def measured_traffic(workload):
         return None
 
 
-def cpu_baseline_prefill(n_slices=1):
-    """The oracle's float32 port of the reference flash algorithm on n (b, head) slices of C3."""
+def cpu_baseline_prefill(n_slices=1, n_js=4):
+    """The reference flash algorithm on CPU for bounded samples of C3 (full S = 4096, causal):
+    restated in JavaScript and run by Node on n_js (b, head) slices -- the stand-in for Kandle's
+    pure-JS CPU backend, which the reference does not ship -- and the oracle's float32 C port on
+    n_slices.  The JS figure is the baseline when Node is installed; the C figure rides along."""
     import oracle
     from kandle_amd import synthetic as syn
 
@@ -528,10 +531,31 @@ def cpu_baseline_prefill(n_slices=1):
     for _ in range(n_slices):
         oracle.flash_f32(q, k, v, causal=True)
     dt = time.perf_counter() - t0
-    flops = n_slices * 4.0 * S * S * D / 2.0
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{n_slices} of 64 (batch, q-head) slices of C3 at full S=4096, causal, fp32, "
-                      f"single thread ({dt:.1f} s); host has {os.cpu_count()} cores"}
+    slice_flops = 4.0 * S * S * D / 2.0
+    c_port = {"value": n_slices * slice_flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+              "sample": f"C port (oracle/oracle.c), {n_slices} of 64 (batch, q-head) slices of C3 at full S=4096, "
+                        f"causal, fp32, single thread ({dt:.1f} s)"}
+    if not oracle.node_available() or n_js < 1:
+        c_port["sample"] += f"; host has {os.cpu_count()} cores"
+        return c_port
+    qj = syn.normal(611, (1, n_js, S, D))
+    kj = syn.normal(612, (1, n_js, S, D))
+    vj = syn.normal(613, (1, n_js, S, D))
+    _, ms = oracle.flash_js(qj, kj, vj, causal=True)
+    return {"value": n_js * slice_flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"JavaScript restatement of the reference flash algorithm (oracle/js/flash_sdpa.js, Node "
+                      f"{_node_version()}, Br=8 Bc=4 tiles, Float32Array storage) on {n_js} of 64 (batch, q-head) "
+                      f"slices of C3 at full S=4096, causal, single thread ({ms / 1e3:.1f} s); host has "
+                      f"{os.cpu_count()} cores",
+            "c_port": c_port}
+
+
+def _node_version():
+    import subprocess
+    try:
+        return subprocess.run(["node", "--version"], capture_output=True, text=True, timeout=30).stdout.strip()
+    except (OSError, subprocess.SubprocessError):
+        return "?"
 
 
 def _one_thread():
@@ -699,7 +723,7 @@ def main():
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
         log("cpu baseline ...")
         with _one_thread():
-            cpu = cpu_baseline_prefill(16)
+            cpu = cpu_baseline_prefill(8, 4)
     cpu_more = {}
     if not args.no_cpu_baseline and args.only is None:
         log("cpu baselines of C4, C2, C5 ...")

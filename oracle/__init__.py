@@ -134,6 +134,41 @@ def flash_f32(q, k, v, scale=None, causal=False, heads_limit=0) -> np.ndarray:
     return o
 
 
+def node_available() -> bool:
+    """True when a `node` executable runs here (the JS restatement needs it)."""
+    import shutil
+    import subprocess
+    exe = shutil.which("node")
+    if exe is None:
+        return False
+    try:
+        return subprocess.run([exe, "--version"], capture_output=True, timeout=30).returncode == 0
+    except (OSError, subprocess.SubprocessError):
+        return False
+
+
+def flash_js(q, k, v, scale=None, causal=False, heads_limit=0):
+    """The reference flash algorithm restated in JavaScript (oracle/js/flash_sdpa.js), run by Node:
+    (o [B,Hq,Lq,D] float32, wall ms of the computation inside Node).  heads_limit > 0 computes only
+    the first heads_limit (b, h) pairs (a bounded sample; the other rows stay zero)."""
+    import json
+    import subprocess
+    import tempfile
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Hq, Lq, D = q.shape
+    _, Hkv, Lk, _ = k.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "js", "flash_sdpa.js")
+    with tempfile.TemporaryDirectory() as d:
+        for name, a in (("q", q), ("k", k), ("v", v)):
+            a.tofile(os.path.join(d, name + ".f32"))
+        out = subprocess.run(["node", script, d, str(B), str(Hq), str(Hkv), str(Lq), str(Lk), str(D), repr(float(scale)),
+                              "1" if causal else "0", str(int(heads_limit))], capture_output=True, text=True, check=True)
+        o = np.fromfile(os.path.join(d, "o.f32"), dtype=np.float32).reshape(B, Hq, Lq, D)
+    return o, float(json.loads(out.stdout.strip().splitlines()[-1])["ms"])
+
+
 def rms_norm(x, w=None, eps=1e-6) -> np.ndarray:
     x = _f32(x)
     n = x.shape[-1]

@@ -94,6 +94,20 @@ def test_sdpa_kv_len_equals_truncation():
     np.testing.assert_allclose(o[1:2], oracle.sdpa(q[1:2], k[1:2], v[1:2]), rtol=1e-6)
 
 
+@pytest.mark.skipif(not oracle.node_available(), reason="node is not installed")
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_js_matches_oracle_and_torch_golden(causal):
+    """The JavaScript restatement (the CPU baseline's JS leg) against the C oracle on ragged GQA
+    shapes (37 rows: a partial Br = 8 block and Bc = 4 block) and against the torch golden vectors."""
+    r = np.random.default_rng(4)
+    q, k, v = (r.standard_normal((1, 4, 37, 16)).astype(np.float32), r.standard_normal((1, 2, 37, 16)),
+               r.standard_normal((1, 2, 37, 16)))
+    o, _ = oracle.flash_js(q, k, v, causal=causal)
+    np.testing.assert_allclose(o, oracle.sdpa(q, k, v, causal=causal), rtol=1e-5, atol=1e-6)
+    og, _ = oracle.flash_js(G["sdpa_q"], G["sdpa_k"], G["sdpa_v"], causal=causal)
+    np.testing.assert_allclose(og, G[f"sdpa_c{int(causal)}_o"], rtol=1e-5, atol=1e-6)
+
+
 # ------------------------------------------------------------------------------ SDPA with mask
 def test_sdpa_masked_matches_torch_golden():
     o = oracle.sdpa_masked(G["sdpam_q"], G["sdpam_k"], G["sdpam_v"], G["sdpam_mask"])
