@@ -116,6 +116,17 @@ int kh_binary(int op, const void* a, const void* b, void* out, int64_t n, int dt
  * Replaces the `silu` pointwise kernel (reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:299). */
 int kh_silu(const void* x, void* out, int64_t n, int dtype);
 
+/* out[i] = op(x[i]) for contiguous operands, computed in fp32: op 0 = neg, 1 = cos, 2 = sin.
+ * Replaces the `neg`/`cos`/`sin` pointwise iterator kernels that Kandle's composite RoPE calls
+ * (reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:168 neg, :201 sin, :202 cos;
+ * callers packages/model-utils/src/rope.ts:254-255,590-630). */
+int kh_unary(int op, const void* x, void* out, int64_t n, int dtype);
+
+/* out[i] = start + f32(i) * step (f32/bf16) or start + i * step in int32 arithmetic (KH_I32), n
+ * elements.  Replaces the `arange` factory kernel (reference:
+ * packages/backend-webgpu/src/kernels/factory/arangeExecutor.ts:30-80, arangeShaderBuilder.ts:66-78). */
+int kh_arange(void* out, int64_t n, double start, double step, int dtype);
+
 /* out[r, i] = silu(gate[r, i]) * up[r, i] over rows x n, rows strided by the given element strides.
  * Fuses SwiGLUMLP's silu and mul (reference: packages/model-utils/src/mlp/swiglu.ts:119-134;
  * ops.ts:299 silu, :329 mul). */

@@ -104,6 +104,32 @@ __global__ void silu_kernel(const T* __restrict__ x, T* __restrict__ out, int64_
     Elem<T>::store(out, i, silu_ref(Elem<T>::load(x, i)));
 }
 
+// Unary map ops of the pointwise kernels: 0 = neg, 1 = cos, 2 = sin, computed in fp32 and stored
+// in the tensor's dtype (reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:168 neg,
+// :201 sin, :202 cos; WGSL evaluates them in f32).
+template <typename T>
+__global__ void unary_kernel(const T* __restrict__ x, T* __restrict__ out, int64_t n, int op) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = Elem<T>::load(x, i);
+    Elem<T>::store(out, i, op == 0 ? -v : (op == 1 ? cosf(v) : sinf(v)));
+  }
+}
+
+// arange: out[i] = start + f32(i) * step in f32 for floating dtypes, start + i * step in i32 for int32
+// (reference: packages/backend-webgpu/src/kernels/factory/arangeShaderBuilder.ts:66-78).
+template <typename T>
+__global__ void arange_kernel(T* __restrict__ out, int64_t n, float start, float step) {
+#pragma clang fp contract(off)  // the product and the sum round separately (no fma)
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float prod = (float)i * step;
+    Elem<T>::store(out, i, start + prod);
+  }
+}
+__global__ void arange_i32_kernel(int32_t* __restrict__ out, int64_t n, int32_t start, int32_t step) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = (int32_t)((uint32_t)start + (uint32_t)i * (uint32_t)step);  // i32 wrap-around as WGSL
+}
+
 template <typename T>
 __global__ void silu_mul_kernel(const T* __restrict__ g, int64_t gs, const T* __restrict__ u, int64_t us,
                                 T* __restrict__ out, int64_t os, int64_t rows, int64_t n) {
@@ -342,6 +368,39 @@ int kh_silu(const void* x, void* out, int64_t n, int dtype) {
     silu_kernel<uint16_t><<<grid_for(n), kThreads, 0, stream()>>>((const uint16_t*)x, (uint16_t*)out, n);
   else
     KH_REQUIRE(false, "kh_silu: unsupported dtype %d", dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_unary(int op, const void* x, void* out, int64_t n, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(op >= 0 && op <= 2, "kh_unary: unknown op %d", op);
+  KH_REQUIRE(n >= 0, "kh_unary: negative count");
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(x && out, "kh_unary: null pointer");
+  if (dtype == KH_F32)
+    unary_kernel<float><<<grid_for(n), kThreads, 0, stream()>>>((const float*)x, (float*)out, n, op);
+  else if (dtype == KH_BF16)
+    unary_kernel<uint16_t><<<grid_for(n), kThreads, 0, stream()>>>((const uint16_t*)x, (uint16_t*)out, n, op);
+  else
+    KH_REQUIRE(false, "kh_unary: unsupported dtype %d", dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_arange(void* out, int64_t n, double start, double step, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(n >= 0, "kh_arange: negative count");
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(out, "kh_arange: null pointer");
+  if (dtype == KH_F32)
+    arange_kernel<float><<<grid_for(n), kThreads, 0, stream()>>>((float*)out, n, (float)start, (float)step);
+  else if (dtype == KH_BF16)
+    arange_kernel<uint16_t><<<grid_for(n), kThreads, 0, stream()>>>((uint16_t*)out, n, (float)start, (float)step);
+  else if (dtype == KH_I32)
+    arange_i32_kernel<<<grid_for(n), kThreads, 0, stream()>>>((int32_t*)out, n, (int32_t)start, (int32_t)step);
+  else
+    KH_REQUIRE(false, "kh_arange: unsupported dtype %d", dtype);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -245,6 +245,45 @@ def silu(x: Tensor) -> Tensor:
     return _wrap(out)
 
 
+def _map(x: Tensor, name: str) -> Tensor:
+    """A one-input pointwise op found by name (the reference's IteratorHandler route,
+    packages/core/src/dispatch/handlers/iterator.ts:24-135): contiguous input, new output."""
+    hx = x.handle if x.handle.is_contiguous() else _kernel(x, "contiguous")(x.handle, {})
+    out = _new(x, x.shape)
+    try:
+        _kernel(x, name)(TensorIterator([hx], [out]))
+    finally:
+        if hx is not x.handle:
+            hx.dispose()
+    return _wrap(out)
+
+
+def neg(x: Tensor) -> Tensor:
+    return _map(x, "neg")
+
+
+def cos(x: Tensor) -> Tensor:
+    return _map(x, "cos")
+
+
+def sin(x: Tensor) -> Tensor:
+    return _map(x, "sin")
+
+
+def arange(start: float, end: Optional[float] = None, step: float = 1.0, dtype: str = "float32") -> Tensor:
+    """[start, end) with step (arange(n) = [0, n)); n = ceil((end - start) / step) elements, values
+    start + i * step from the `arange` factory kernel."""
+    if end is None:
+        start, end = 0.0, start
+    if step == 0:
+        raise ValueError("arange: step must be nonzero")
+    n = max(0, int(math.ceil((end - start) / step)))
+    from .env import get_backend, get_default_device
+    out = get_backend(get_default_device()).create_tensor_handle((n,), dtype)
+    get_backend(get_default_device()).operators.find("arange")(out, float(start), float(step))
+    return _wrap(out)
+
+
 def silu_mul(gate: Tensor, up: Tensor) -> Tensor:
     out = _new(gate, gate.shape)
     _kernel(gate, "silu_mul")(gate.handle, up.handle, out)

@@ -477,6 +477,33 @@ def sub(it: TensorIterator) -> None:
     _binary(2, it)
 
 
+def _unary(op: int, name: str, it: TensorIterator) -> None:
+    x, o = it.input(0), it.output()
+    if not (x.is_contiguous() and o.is_contiguous()) or x.numel != o.numel or x.dtype != o.dtype:
+        raise ValueError(f"{name}: operands must be contiguous, of equal size and dtype")
+    _lib.call("kh_unary", op, _vp(x.data_ptr()), _vp(o.data_ptr()), o.numel, o.kh_dtype)
+
+
+def neg(it: TensorIterator) -> None:
+    _unary(0, "neg", it)
+
+
+def cos(it: TensorIterator) -> None:
+    _unary(1, "cos", it)
+
+
+def sin(it: TensorIterator) -> None:
+    _unary(2, "sin", it)
+
+
+def arange(output: HipTensorHandle, start: float = 0.0, step: float = 1.0) -> None:
+    """output[i] = start + i * step over the contiguous output (the reference's factory kernel)."""
+    if not output.is_contiguous():
+        raise ValueError("arange: output must be contiguous")
+    _lib.call("kh_arange", _vp(output.data_ptr()), output.numel, C.c_double(start), C.c_double(step),
+              output.kh_dtype)
+
+
 def silu(it: TensorIterator) -> None:
     x, o = it.input(0), it.output()
     if not (x.is_contiguous() and o.is_contiguous()) or x.numel != o.numel:
@@ -718,6 +745,10 @@ KERNELS = {
     "rms_norm": rms_norm,
     "rms_norm_rope": rms_norm_rope,
     "silu": silu,
+    "neg": neg,
+    "cos": cos,
+    "sin": sin,
+    "arange": arange,
     "mul": mul,
     "add": add,
     "sub": sub,
