@@ -74,3 +74,28 @@ def test_view_helpers():
     assert _coalesce([2, 3, 4], [12, 4, 1]) == ([24], [1])
     assert _coalesce([2, 4, 3, 8], [96, 8, 32, 1]) == ([2, 4, 3, 8], [96, 8, 32, 1])
     assert _coalesce([1, 5, 1, 8], [40, 8, 8, 1]) == ([40], [1])
+
+
+def test_mask_strides_follow_numpy_broadcasting():
+    """The explicit-mask route broadcasts attn_mask to the [B, Hq, Lq, Lk] scores by element
+    strides (0 for a broadcast axis), and rejects shapes that do not broadcast, as add_Tensor does
+    (packages/core/src/dispatch/handlers/composite.ts:279-300)."""
+    from types import SimpleNamespace as NS
+    tgt = (2, 4, 5, 7)
+    ms = kernels._mask_strides
+    assert ms(NS(shape=(5, 7), strides=(7, 1)), tgt) == [0, 0, 7, 1]
+    assert ms(NS(shape=(2, 1, 5, 7), strides=(35, 35, 7, 1)), tgt) == [35, 0, 7, 1]
+    assert ms(NS(shape=(2, 4, 5, 7), strides=(140, 35, 7, 1)), tgt) == [140, 35, 7, 1]
+    assert ms(NS(shape=(1, 7), strides=(7, 1)), tgt) == [0, 0, 0, 1]          # one row for all queries
+    assert ms(NS(shape=(7, 5), strides=(1, 7)), (1, 1, 7, 5)) == [0, 0, 1, 7]  # transposed view
+    assert ms(NS(shape=(1, 1, 1, 1), strides=(1, 1, 1, 1)), (1, 1, 1, 1)) == [0, 0, 0, 0]
+    for bad in ((3, 7), (5, 6), (3, 1, 5, 7), (1, 1, 2, 5, 7)):
+        with pytest.raises(ValueError):
+            ms(NS(shape=bad, strides=(1,) * len(bad)), tgt)
+
+
+def test_generic_kernel_names_registered():
+    """Kandle's composite RoPE and factories look these up by name (rope.ts:546-644)."""
+    for name in ("neg", "cos", "sin", "arange", "sdpa_masked", "copy", "copy_", "add", "mul", "index_select",
+                 "argmax", "zeros", "cast", "contiguous"):
+        assert name in kernels.KERNELS, name
