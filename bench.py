@@ -62,7 +62,14 @@ def time_calls(fn, steps, warmup):
     return (t1 - t0) * 1e3 / steps, e0.elapsed_ms(e1) / steps
 
 
-def bench_prefill(steps, warmup):
+# Each prep_* function uploads its inputs and returns run(steps, warmup) -> result dict (the run
+# frees what the prep allocated).  main() prepares every leg first and then runs the GPU legs back
+# to back, the headline last: the GPU reaches its steady clock only after several ms of sustained
+# load (C3 prefill measured 0.34 ms per call over 20 calls after 3 warm-up calls from idle, 0.296 ms
+# once the clock has settled), so the headline is timed at the clock a loaded GPU runs at, with no
+# input generation or CPU work between the legs.
+
+def prep_prefill():
     from kandle_amd import HipTensorHandle, kernels
 
     B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
@@ -71,18 +78,45 @@ def bench_prefill(steps, warmup):
     v = bf16_tensor(303, (B, Hkv, S, D))
     o = HipTensorHandle.create_new((B, Hq, S, D), "bfloat16")
     scale = 1.0 / np.sqrt(D)
-    fn = lambda: kernels.flash_attention(q.handle, k.handle, v.handle, o, scale, True)  # noqa: E731
-    wall_ms, dev_ms = time_calls(fn, steps, warmup)
-    flops = 4.0 * B * Hq * S * S * D / 2.0
-    out = o.data_async()
-    assert np.all(np.isfinite(out)), "prefill produced non-finite values"
-    for t in (q, k, v):
-        t.dispose()
-    o.dispose()
-    return {"B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D, "flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+    def run(steps, warmup):
+        fn = lambda: kernels.flash_attention(q.handle, k.handle, v.handle, o, scale, True)  # noqa: E731
+        wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        flops = 4.0 * B * Hq * S * S * D / 2.0
+        out = o.data_async()
+        assert np.all(np.isfinite(out)), "prefill produced non-finite values"
+        for t in (q, k, v):
+            t.dispose()
+        o.dispose()
+        return {"B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D, "flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms}
+    return run
 
 
-def bench_mask(steps, warmup):
+def prep_c1():
+    """Config C1 on the GPU: SDPA in fp32, B=1, Hq=16, Hkv=8, S=256, D=128, causal, scale 1/sqrt(128)
+    (the LDS-tiled fp32-math kernel)."""
+    from kandle_amd import HipTensorHandle, Tensor, kernels
+    from kandle_amd import synthetic as syn
+
+    B, Hq, Hkv, S, D = 1, 16, 8, 256, 128
+    q = Tensor(syn.normal(11, (B, Hq, S, D)))
+    k = Tensor(syn.normal(12, (B, Hkv, S, D)))
+    v = Tensor(syn.normal(13, (B, Hkv, S, D)))
+    o = HipTensorHandle.create_new((B, Hq, S, D), "float32")
+    scale = 1.0 / np.sqrt(D)
+
+    def run(steps, warmup):
+        fn = lambda: kernels.flash_attention(q.handle, k.handle, v.handle, o, scale, True)  # noqa: E731
+        wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        for t in (q, k, v):
+            t.dispose()
+        o.dispose()
+        flops = 4.0 * B * Hq * S * S * D / 2.0
+        return {"flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms}
+    return run
+
+
+def prep_mask():
     """C3 shapes with an explicit [S, S] float32 mask (the top-left causal pattern as -inf / 0):
     the masked route scores every (query, key) pair, so the work is the full 4 B Hq S^2 D."""
     from kandle_amd import HipTensorHandle, Tensor, kernels
@@ -94,44 +128,58 @@ def bench_mask(steps, warmup):
     m = Tensor(np.where(np.arange(S)[None, :] > np.arange(S)[:, None], -np.inf, 0.0).astype(np.float32))
     o = HipTensorHandle.create_new((B, Hq, S, D), "bfloat16")
     scale = 1.0 / np.sqrt(D)
-    fn = lambda: kernels.sdpa_masked(q.handle, k.handle, v.handle, m.handle, o, scale)  # noqa: E731
-    wall_ms, dev_ms = time_calls(fn, steps, warmup)
-    flops = 4.0 * B * Hq * S * S * D
-    out = o.data_async()
-    assert np.all(np.isfinite(out)), "masked prefill produced non-finite values"
-    for t in (q, k, v, m):
-        t.dispose()
-    o.dispose()
-    tf = flops / (dev_ms * 1e-3) / 1e12
-    return {"workload": "C3 shapes with an explicit [4096, 4096] float32 mask (causal pattern), all pairs scored",
-            "flops": flops, "ms": round(dev_ms, 4), "wall_ms": round(wall_ms, 4), "TFLOP/s": round(tf, 1),
-            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / PEAK_BF16_TFLOPS, 4)},
-            "kernel": "flash_fwd_kernel<64, 8, 1, false, true, 1>"}
+
+    def run(steps, warmup):
+        fn = lambda: kernels.sdpa_masked(q.handle, k.handle, v.handle, m.handle, o, scale)  # noqa: E731
+        wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        flops = 4.0 * B * Hq * S * S * D
+        out = o.data_async()
+        assert np.all(np.isfinite(out)), "masked prefill produced non-finite values"
+        for t in (q, k, v, m):
+            t.dispose()
+        o.dispose()
+        tf = flops / (dev_ms * 1e-3) / 1e12
+        return {"workload": "C3 shapes with an explicit [4096, 4096] float32 mask (causal pattern), all pairs scored",
+                "flops": flops, "ms": round(dev_ms, 4), "wall_ms": round(wall_ms, 4), "TFLOP/s": round(tf, 1),
+                "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tf / PEAK_BF16_TFLOPS, 4)},
+                "kernel": "flash_fwd_kernel<64, 8, 1, false, 1>"}
+    return run
 
 
-def bench_decode(steps, warmup):
-    from kandle_amd import HipTensorHandle, Tensor, kernels
+C4_SHAPE = dict(B=8, Hq=16, Hkv=8, D=128, ML=32768)
+
+
+def c4_lengths():
+    """The per-sequence KV lengths of config C4: 8 draws from U[8192, 32768] (seed 2024)."""
     from kandle_amd import synthetic as syn
+    return syn.randint(2024, (C4_SHAPE["B"],), 8192, 32769)
 
-    B, Hq, Hkv, D, ML = 8, 16, 8, 128, 32768
-    lens = syn.randint(2024, (B,), 8192, 32769)
+
+def prep_decode():
+    from kandle_amd import HipTensorHandle, Tensor, kernels
+
+    B, Hq, Hkv, D, ML = (C4_SHAPE[x] for x in ("B", "Hq", "Hkv", "D", "ML"))
+    lens = c4_lengths()
     q = bf16_tensor(401, (B, Hq, D))
     kc = bf16_tensor(402, (B, Hkv, ML, D))
     vc = bf16_tensor(403, (B, Hkv, ML, D))
     sl = Tensor(lens, dtype="int32")
     o = HipTensorHandle.create_new((B, Hq, D), "bfloat16")
     scale = 1.0 / np.sqrt(D)
-    fn = lambda: kernels.decode_attention(q.handle, kc.handle, vc.handle, sl.handle, o, scale)  # noqa: E731
-    wall_ms, dev_ms = time_calls(fn, steps, warmup)
-    kv_bytes = float(lens.sum()) * Hkv * D * 2 * 2
-    for t in (q, kc, vc, sl):
-        t.dispose()
-    o.dispose()
-    return {"B": B, "sum_len": int(lens.sum()), "bytes": kv_bytes, "wall_ms": wall_ms, "dev_ms": dev_ms}
+
+    def run(steps, warmup):
+        fn = lambda: kernels.decode_attention(q.handle, kc.handle, vc.handle, sl.handle, o, scale)  # noqa: E731
+        wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        kv_bytes = float(lens.sum()) * Hkv * D * 2 * 2
+        for t in (q, kc, vc, sl):
+            t.dispose()
+        o.dispose()
+        return {"B": B, "sum_len": int(lens.sum()), "bytes": kv_bytes, "wall_ms": wall_ms, "dev_ms": dev_ms}
+    return run
 
 
-def bench_norm_rope(steps, warmup):
+def prep_norm_rope():
     from kandle_amd import HipTensorHandle, Tensor, kernels
     from kandle_amd import synthetic as syn
 
@@ -157,12 +205,18 @@ def bench_norm_rope(steps, warmup):
         kernels.rms_norm([x.handle], norm_params)
         kernels.rms_norm_rope(q.handle, k.handle, params)
 
-    wall_ms, dev_ms = time_calls(fn, steps, warmup)
-    bytes_ = 2 * T * H * 2 + H * 2 + 2 * (T * Hq * D + T * Hkv * D) * 2 + 2 * D * 2
-    return {"T": T, "bytes": float(bytes_), "wall_ms": wall_ms, "dev_ms": dev_ms}
+    def run(steps, warmup):
+        wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        bytes_ = 2 * T * H * 2 + H * 2 + 2 * (T * Hq * D + T * Hkv * D) * 2 + 2 * D * 2
+        for t in (x, q, k, w, wq, wk, invt, pos):
+            t.dispose()
+        for h in (y, qo, ko):
+            h.dispose()
+        return {"T": T, "bytes": float(bytes_), "wall_ms": wall_ms, "dev_ms": dev_ms}
+    return run
 
 
-def bench_model(steps, warmup, new_tokens=128, prompt_len=512, use_graph=True):
+def prep_model(new_tokens=128, prompt_len=512, use_graph=True):
     """Config C5: Qwen3-0.6B architecture, random N(0, 0.02) bf16 weights, a 512-token prefill of
     uniform-random ids, then 128 greedy decode steps (the decode step captured once as a HIP graph
     and replayed).  One warm-up generation of 8 tokens precedes the timed one; it runs the prefill
@@ -178,29 +232,32 @@ def bench_model(steps, warmup, new_tokens=128, prompt_len=512, use_graph=True):
     prompt = syn.randint(8, (prompt_len,), 0, cfg.vocab_size)
     model = Qwen3ForCausalLM(cfg, w, max_seq_len=prompt_len + new_tokens)
     del w
-    warm = {}
-    model.generate(prompt, 8, use_graph=use_graph, timing=warm)   # eager prefill (then captured)
-    timing = {}
-    toks = model.generate(prompt, new_tokens, timing=timing, use_graph=use_graph)
-    if not use_graph:  # every step eager: time all of them
-        timing["replay_ms"], timing["replay_steps"] = timing["decode_ms"], new_tokens
-    model.dispose()
-    H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
-    Hq, Hkv, Lyr = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
-    layer_w = H * (Hq + 2 * Hkv) * D + Hq * D * H + 3 * H * I            # projection weights per layer
-    prefill_flops = (2.0 * prompt_len * layer_w * Lyr                      # projections, all rows
-                     + 2.0 * cfg.vocab_size * H                            # lm_head, last row
-                     + Lyr * 4.0 * Hq * prompt_len * prompt_len * D / 2)   # causal attention
-    # bytes a decode step must read: every weight once (tied embedding as lm_head), plus the KV
-    # cache rows attended; the mean attended length over the timed replays
-    weight_bytes = 2.0 * (Lyr * (layer_w + 2 * H + 2 * D) + cfg.vocab_size * H + H)
-    steps_r = timing.get("replay_steps", 0)
-    mean_len = prompt_len + 1 + (new_tokens + 1) / 2.0
-    kv_bytes = Lyr * 2 * Hkv * D * 2 * mean_len
-    return {"prefill_ms": timing["prefill_ms"], "prefill_issue": timing["prefill_issue"],
-            "prefill_eager_ms": warm["prefill_ms"], "prefill_flops": prefill_flops, "prompt_len": prompt_len,
-            "new_tokens": new_tokens, "replay_ms": timing.get("replay_ms"), "replay_steps": steps_r,
-            "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8]}
+
+    def run(steps, warmup):
+        warm = {}
+        model.generate(prompt, 8, use_graph=use_graph, timing=warm)   # eager prefill (then captured)
+        timing = {}
+        toks = model.generate(prompt, new_tokens, timing=timing, use_graph=use_graph)
+        if not use_graph:  # every step eager: time all of them
+            timing["replay_ms"], timing["replay_steps"] = timing["decode_ms"], new_tokens
+        model.dispose()
+        H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+        Hq, Hkv, Lyr = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
+        layer_w = H * (Hq + 2 * Hkv) * D + Hq * D * H + 3 * H * I            # projection weights per layer
+        prefill_flops = (2.0 * prompt_len * layer_w * Lyr                      # projections, all rows
+                         + 2.0 * cfg.vocab_size * H                            # lm_head, last row
+                         + Lyr * 4.0 * Hq * prompt_len * prompt_len * D / 2)   # causal attention
+        # bytes a decode step must read: every weight once (tied embedding as lm_head), plus the KV
+        # cache rows attended; the mean attended length over the timed replays
+        weight_bytes = 2.0 * (Lyr * (layer_w + 2 * H + 2 * D) + cfg.vocab_size * H + H)
+        steps_r = timing.get("replay_steps", 0)
+        mean_len = prompt_len + 1 + (new_tokens + 1) / 2.0
+        kv_bytes = Lyr * 2 * Hkv * D * 2 * mean_len
+        return {"prefill_ms": timing["prefill_ms"], "prefill_issue": timing["prefill_issue"],
+                "prefill_eager_ms": warm["prefill_ms"], "prefill_flops": prefill_flops, "prompt_len": prompt_len,
+                "new_tokens": new_tokens, "replay_ms": timing.get("replay_ms"), "replay_steps": steps_r,
+                "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8]}
+    return run
 
 
 def bench_copy(steps, warmup):
@@ -515,11 +572,28 @@ def measured_traffic(workload):
         return None
 
 
-def cpu_baseline_prefill(n_slices=1, n_js=4):
-    """The reference flash algorithm on CPU for bounded samples of C3 (full S = 4096, causal):
-    restated in JavaScript and run by Node on n_js (b, head) slices -- the stand-in for Kandle's
-    pure-JS CPU backend, which the reference does not ship -- and the oracle's float32 C port on
-    n_slices.  The JS figure is the baseline when Node is installed; the C figure rides along."""
+JS_REPEAT = 5   # timed runs of each JavaScript baseline after one untimed run; the median is reported
+
+
+def _js_leg(op, inputs, args, work, unit, sample, scale_to_full=1.0):
+    """One JavaScript CPU baseline: oracle/js/bench_cpu.js OP run by Node on one thread, one untimed
+    run then JS_REPEAT timed runs; value = work / median time (x scale_to_full for a sample)."""
+    import oracle
+
+    _, runs = oracle.js_bench(op, inputs, args, JS_REPEAT)
+    med = float(np.median(runs))
+    return {"value": round(work * scale_to_full / (med * 1e-3), 6), "unit": unit, "cores": 1, "kind": "port",
+            "runtime": f"JavaScript, Node {_node_version()}, one thread (host has {os.cpu_count()} cores)",
+            "sample": sample + f"; median of {JS_REPEAT} timed runs after 1 warm-up "
+                               f"({', '.join(f'{r / 1e3:.2f}' for r in runs)} s)",
+            "median_s": round(med / 1e3, 4)}
+
+
+def cpu_baseline_prefill():
+    """The reference flash algorithm on CPU for C3, restated in JavaScript and run by Node (the
+    stand-in for Kandle's pure-JS CPU backend, which the reference does not ship): one (batch,
+    q-head) slice at full S = 4096, causal, extrapolated x64 to the whole batch.  The oracle's
+    float32 C port on the same slice rides along."""
     import oracle
     from kandle_amd import synthetic as syn
 
@@ -527,73 +601,75 @@ def cpu_baseline_prefill(n_slices=1, n_js=4):
     q = syn.normal(601, (1, 1, S, D))
     k = syn.normal(602, (1, 1, S, D))
     v = syn.normal(603, (1, 1, S, D))
-    t0 = time.perf_counter()
-    for _ in range(n_slices):
-        oracle.flash_f32(q, k, v, causal=True)
-    dt = time.perf_counter() - t0
     slice_flops = 4.0 * S * S * D / 2.0
-    c_port = {"value": n_slices * slice_flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-              "sample": f"C port (oracle/oracle.c), {n_slices} of 64 (batch, q-head) slices of C3 at full S=4096, "
-                        f"causal, fp32, single thread ({dt:.1f} s)"}
-    if not oracle.node_available() or n_js < 1:
-        c_port["sample"] += f"; host has {os.cpu_count()} cores"
+    t0 = time.perf_counter()
+    oracle.flash_f32(q, k, v, causal=True)
+    dt = time.perf_counter() - t0
+    c_port = {"value": slice_flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+              "sample": f"C port (oracle/oracle.c), 1 of 64 (batch, q-head) slices of C3 at full S=4096, causal, "
+                        f"fp32, single thread ({dt:.2f} s)"}
+    if not oracle.node_available():
+        c_port["sample"] += f"; host has {os.cpu_count()} cores (Node not installed: no JavaScript baseline)"
         return c_port
-    qj = syn.normal(611, (1, n_js, S, D))
-    kj = syn.normal(612, (1, n_js, S, D))
-    vj = syn.normal(613, (1, n_js, S, D))
-    _, ms = oracle.flash_js(qj, kj, vj, causal=True)
-    return {"value": n_js * slice_flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"JavaScript restatement of the reference flash algorithm (oracle/js/flash_sdpa.js, Node "
-                      f"{_node_version()}, Br=8 Bc=4 tiles, Float32Array storage) on {n_js} of 64 (batch, q-head) "
-                      f"slices of C3 at full S=4096, causal, single thread ({ms / 1e3:.1f} s); host has "
-                      f"{os.cpu_count()} cores",
-            "c_port": c_port}
+    js = _js_leg("flash", {"q": q, "k": k, "v": v}, [1, 1, 1, S, S, D, 1.0 / np.sqrt(D), 1, 0],
+                 slice_flops / 1e12, "TFLOP/s",
+                 "JavaScript restatement of the reference flash algorithm (oracle/js/flash_sdpa.js: Br=8 Bc=4 tiles, "
+                 "Float32Array storage) on 1 of the 64 (batch, q-head) slices of C3 at full S=4096, causal; "
+                 "extrapolated x64 (throughput of the slice = throughput of the batch)")
+    js["extrapolated"] = "x64"
+    js["c_port"] = c_port
+    return js
 
 
-def _node_version():
-    import subprocess
-    try:
-        return subprocess.run(["node", "--version"], capture_output=True, text=True, timeout=30).stdout.strip()
-    except (OSError, subprocess.SubprocessError):
-        return "?"
-
-
-def _one_thread():
-    """Context that limits numpy's BLAS to one thread (the CPU baselines state cores = 1)."""
-    try:
-        from threadpoolctl import threadpool_limits
-        return threadpool_limits(1)
-    except ImportError:  # pragma: no cover
-        import contextlib
-        return contextlib.nullcontext()
-
-
-def cpu_baseline_decode():
-    """C4 at full size on the CPU: the oracle's SDPA (double accumulation, one thread) for each of the
-    8 sequences' single query against its whole cache, fp32 inputs; GB/s of the bf16 K/V bytes the GPU
-    kernel reads (lengths as in bench_decode)."""
+def cpu_baseline_c1():
+    """Config C1 at full size in JavaScript: SDPA fp32, B=1, Hq=16, Hkv=8, S=256, D=128, causal."""
     import oracle
     from kandle_amd import synthetic as syn
 
-    B, Hq, Hkv, D = 8, 16, 8, 128
-    lens = syn.randint(2024, (B,), 8192, 32769)
+    if not oracle.node_available():
+        return None
+    B, Hq, Hkv, S, D = 1, 16, 8, 256, 128
+    q = syn.normal(11, (B, Hq, S, D))
+    k = syn.normal(12, (B, Hkv, S, D))
+    v = syn.normal(13, (B, Hkv, S, D))
+    return _js_leg("flash", {"q": q, "k": k, "v": v}, [B, Hq, Hkv, S, S, D, 1.0 / np.sqrt(D), 1, 0],
+                   4.0 * B * Hq * S * S * D / 2.0 / 1e9, "GFLOP/s",
+                   "full C1 (B=1, Hq=16, Hkv=8, S=256, D=128, causal, fp32), oracle/js/flash_sdpa.js")
+
+
+def cpu_baseline_decode():
+    """C4 at full size in JavaScript: one L = 1 SDPA per sequence over its whole cache (the caller's
+    decode step, gqa.ts:333-336), float32 caches; GB/s of the bf16 K/V bytes the GPU kernel reads.
+    Without Node, the oracle's C SDPA (double accumulation) times the same work."""
+    import oracle
+    from kandle_amd import synthetic as syn
+
+    B, Hq, Hkv, D = (C4_SHAPE[x] for x in ("B", "Hq", "Hkv", "D"))
+    lens = c4_lengths()
+    nbytes = float(lens.sum()) * Hkv * D * 2 * 2
+    q = syn.normal(3000, (B, Hq, D))
+    ks = [syn.normal(4000 + b, (Hkv, int(L), D)) for b, L in enumerate(lens)]
+    vs = [syn.normal(5000 + b, (Hkv, int(L), D)) for b, L in enumerate(lens)]
+    if oracle.node_available():
+        inputs = {"q": q}
+        for b in range(B):
+            inputs[f"k_{b}"], inputs[f"v_{b}"] = ks[b], vs[b]
+        return _js_leg("decode", inputs, [Hq, Hkv, D, 1.0 / np.sqrt(D)] + [int(L) for L in lens], nbytes / 1e9, "GB/s",
+                       f"full C4 (sum L = {int(lens.sum())}), oracle/js/flash_sdpa.js with one query per sequence")
     dt = 0.0
     for b in range(B):
-        L = int(lens[b])
-        q = syn.normal(3000 + b, (1, Hq, 1, D))
-        k = syn.normal(4000 + b, (1, Hkv, L, D))
-        v = syn.normal(5000 + b, (1, Hkv, L, D))
         t0 = time.perf_counter()
-        oracle.sdpa(q, k, v)
+        oracle.sdpa(q[b][None, :, None, :], ks[b][None], vs[b][None])
         dt += time.perf_counter() - t0
-    nbytes = float(lens.sum()) * Hkv * D * 2 * 2
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"full C4 (sum L = {int(lens.sum())}), oracle SDPA in C, one thread, {dt:.2f} s"}
+            "sample": f"full C4 (sum L = {int(lens.sum())}), oracle SDPA in C, one thread, {dt:.2f} s "
+                      "(Node not installed: no JavaScript baseline)"}
 
 
 def cpu_baseline_norm():
-    """C2 at full size on the CPU: the oracle's RMSNorm over [8192, 1024] and qk-norm + RoPE over q
-    [8192, 16, 128] and k [8192, 8, 128] (C, one thread); GB/s of the bf16 bytes the GPU kernels move."""
+    """C2 at full size in JavaScript: RMSNorm over [8192, 1024], qk-norm + RoPE over q [8192, 16, 128]
+    and k [8192, 8, 128] (the composite's cos/sin tables included); GB/s of the bf16 bytes the GPU
+    kernels move.  Without Node, the oracle's C functions time the same work."""
     import oracle
     from kandle_amd import synthetic as syn
 
@@ -604,6 +680,11 @@ def cpu_baseline_norm():
     w = syn.uniform(504, (H,), 0.5, 1.5)
     wq = syn.uniform(505, (D,), 0.5, 1.5)
     wk = syn.uniform(506, (D,), 0.5, 1.5)
+    nbytes = 134220288.0
+    if oracle.node_available():
+        return _js_leg("normrope", {"x": x, "q": q, "k": k, "w": w, "wq": wq, "wk": wk},
+                       [T, H, Hq, Hkv, D, 1e-6, 1e6], nbytes / 1e9, "GB/s",
+                       "full C2 (8192 tokens), oracle/js/cpu_ops.js")
     inv = oracle.rope_inv_freq(D, 1e6)
     pos = np.arange(T, dtype=np.int32)
     t0 = time.perf_counter()
@@ -611,9 +692,8 @@ def cpu_baseline_norm():
     oracle.qk_norm_rope(q, wq, pos, inv, 1e-6)
     oracle.qk_norm_rope(k, wk, pos, inv, 1e-6)
     dt = time.perf_counter() - t0
-    nbytes = 134220288.0
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"full C2 (8192 tokens), oracle in C, one thread, {dt:.2f} s"}
+            "sample": f"full C2 (8192 tokens), oracle in C, one thread, {dt:.2f} s (Node not installed)"}
 
 
 def cpu_baseline_model(prompt_len=512, decode_steps=4):
@@ -660,14 +740,14 @@ def cpu_baseline_model(prompt_len=512, decode_steps=4):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # Defaults long enough to time the steady clock: the GPU reaches it after several ms of sustained
-    # load (C3 prefill: 0.34 ms per call over 20 calls after 3 warm-up calls, 0.296 ms over 100 after 20).
+    # Single-leg runs (--only) start from an idle GPU: these defaults time enough calls for its clock
+    # to settle.  The default run times the headline after the other GPU legs.
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
-    ap.add_argument("--only", choices=["prefill", "decode", "norm", "model", "copy", "load", "sample", "stream",
+    ap.add_argument("--only", choices=["prefill", "c1", "decode", "norm", "model", "copy", "load", "sample", "stream",
                                        "gemm", "gemv", "vendor", "mask"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -684,29 +764,39 @@ def main():
         from kandle_amd import HipBackend
 
         HipBackend.create(0)
-    if args.only in (None, "prefill"):
-        log("prefill C3 ...")
-        res["prefill"] = bench_prefill(args.steps, args.warmup)
-    if args.only in (None, "decode"):
-        log("decode C4 ...")
-        res["decode"] = bench_decode(args.steps, args.warmup)
-    if args.only in (None, "norm"):
-        log("norm+rope C2 ...")
-        res["norm"] = bench_norm_rope(args.steps, args.warmup)
+    # Inputs of every GPU leg first (host generation and upload), then the legs back to back with
+    # the headline (C3 prefill) last, then the CPU baselines.
+    legs = []
     if args.only in (None, "model"):
-        log("Qwen3-0.6B C5 ...")
-        res["model"] = bench_model(args.steps, args.warmup, use_graph=not args.eager_decode)
+        log("C5 model weights ...")
+        legs.append(("model", "Qwen3-0.6B C5", prep_model(use_graph=not args.eager_decode)))
+    if args.only in (None, "decode"):
+        legs.append(("decode", "decode C4", prep_decode()))
+    if args.only in (None, "norm"):
+        legs.append(("norm", "norm+rope C2", prep_norm_rope()))
+    if args.only in (None, "c1"):
+        legs.append(("c1", "SDPA fp32 C1", prep_c1()))
+    if args.only == "mask":
+        legs.append(("mask", "explicit-mask SDPA at C3 shapes", prep_mask()))
+    if args.only in (None, "prefill"):
+        legs.append(("prefill", "prefill C3", prep_prefill()))
+    for key, label, run in legs:
+        if key == "prefill" and args.only is None:
+            log("sampling ...")
+            res["sample"] = bench_sample(args.steps, args.warmup)
+        log(f"{label} ...")
+        res[key] = run(args.steps, args.warmup)
+    if args.only == "sample":
+        log("sampling ...")
+        res["sample"] = bench_sample(args.steps, args.warmup)
+        if not args.no_cpu_baseline:
+            res["sample"]["cpu_oracle_us"] = round(cpu_baseline_sample(), 1)
     if args.only == "copy":
         log("copy calibration ...")
         res["copy"] = bench_copy(args.steps, args.warmup)
     if args.only == "load":
         log("checkpoint load ...")
         res["load"] = bench_load()
-    if args.only in (None, "sample"):
-        log("sampling ...")
-        res["sample"] = bench_sample(args.steps, args.warmup)
-        if args.only == "sample" and not args.no_cpu_baseline:
-            res["sample"]["cpu_oracle_us"] = round(cpu_baseline_sample(), 1)
     if args.only == "stream":
         log("generate_stream ...")
         res["stream"] = bench_stream()
@@ -716,15 +806,15 @@ def main():
     if args.only == "gemv":
         log("C5 decode GEMVs ...")
         res["gemv"] = bench_gemv(args.steps, args.warmup)
-    if args.only == "mask":
-        log("explicit-mask SDPA at C3 shapes ...")
-        res["mask"] = bench_mask(args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only in (None, "prefill"):
-        log("cpu baseline ...")
+        log("cpu baseline (C3) ...")
         with _one_thread():
-            cpu = cpu_baseline_prefill(8, 4)
+            cpu = cpu_baseline_prefill()
     cpu_more = {}
+    if not args.no_cpu_baseline and args.only in (None, "c1"):
+        log("cpu baseline (C1) ...")
+        cpu_more["c1"] = cpu_baseline_c1()
     if not args.no_cpu_baseline and args.only is None:
         log("cpu baselines of C4, C2, C5 ...")
         with _one_thread():
@@ -745,7 +835,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                          "traffic": measured_traffic("prefill"),
-                         "kernel": "flash_fwd_kernel<128, 8, 1, true, true, 0>", "kernel_ms": round(p["dev_ms"], 4)},
+                         "kernel": "flash_fwd_kernel<128, 8, 1, true, 0>", "kernel_ms": round(p["dev_ms"], 4)},
         })
     if "decode" in res:
         d = res["decode"]
@@ -770,6 +860,17 @@ def main():
         if "value" not in line:
             line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(n["wall_ms"], 4),
                          "config": {"workload": "C2 norm + rope"}})
+    if "c1" in res:
+        c1 = res["c1"]
+        gf = c1["flops"] / (c1["dev_ms"] * 1e-3) / 1e9
+        line["c1"] = {"workload": "C1 SDPA fp32, B=1, Hq=16, Hkv=8, S=256, D=128, causal (LDS-tiled fp32 kernel)",
+                      "flops": c1["flops"], "ms": round(c1["dev_ms"], 4), "wall_ms": round(c1["wall_ms"], 4),
+                      "GFLOP/s": round(gf, 1),
+                      "roofline": {"bound": "fp32 vector", "achieved": round(gf / 1e3, 3), "peak": 157.3,
+                                   "unit": "TFLOP/s", "frac": round(gf / 1e3 / 157.3, 4), "traffic": None}}
+        if "value" not in line:
+            line.update({"value": round(gf, 1), "unit": "GFLOP/s", "ms_per_step": round(c1["wall_ms"], 4),
+                         "config": {"workload": "C1 SDPA fp32"}})
     if "model" in res:
         m = res["model"]
         p_tps = m["prompt_len"] / (m["prefill_ms"] * 1e-3)

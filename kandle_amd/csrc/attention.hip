@@ -637,9 +637,19 @@ AttnStrides load_strides(const int64_t* s) {
   return a;
 }
 
+// Bytes of split-K partials launch_decode needs: o rows + (m, l) per (sequence, head, chunk).
+template <typename T>
+size_t decode_part_bytes(int batch, int hq, int64_t max_len) {
+  const int64_t max_chunks = (max_len + dc_chunk<T>() - 1) / dc_chunk<T>();
+  return (size_t)batch * hq * max_chunks * (128 + 2) * sizeof(float);
+}
+
+// part_in: the partials buffer (at least decode_part_bytes), or nullptr to take one from the
+// caching allocator for the duration of the call.
 template <typename T>
 int launch_decode(const void* q, const void* k, const void* v, void* o, const int32_t* lens, int uniform_len,
-                  int batch, int hq, int hkv, int64_t max_len, const AttnStrides& st, float scale) {
+                  int batch, int hq, int hkv, int64_t max_len, const AttnStrides& st, float scale,
+                  float* part_in = nullptr) {
   const int G = hq / hkv;
   KH_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "kh_decode_attention: hq/hkv = %d not in {1, 2, 4, 8}", G);
   const int64_t lim = int64_t(1) << 31;
@@ -649,8 +659,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   const int ml = (int)max_len;
   const int max_chunks = (ml + dc_chunk<T>() - 1) / dc_chunk<T>();
   KH_REQUIRE(max_chunks <= 65535 * 64, "kh_decode_attention: max_len too large");
-  const size_t part_bytes = (size_t)batch * hq * max_chunks * (128 + 2) * sizeof(float);  // o rows + (m, l)
-  float* part = (float*)scratch_alloc(part_bytes);
+  float* part = part_in ? part_in : (float*)scratch_alloc(decode_part_bytes<T>(batch, hq, max_len));
   if (!part) return KH_ERR_OOM;
   dim3 grid(max_chunks, hkv, batch);
   const T* Q = (const T*)q;
@@ -679,7 +688,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
                                                                   (T*)o);
     e = hipGetLastError();
   }
-  scratch_free(part);  // stream-ordered: the block is reused only by later work on the same stream
+  if (!part_in) scratch_free(part);  // stream-ordered: the block is reused only by later work on the same stream
   if (e != hipSuccess) {
     set_error("kh_decode_attention: launch failed: %s", hipGetErrorString(e));
     return KH_ERR_HIP;
@@ -736,7 +745,9 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
     if (dtype == KH_BF16) return launch_decode<uint16_t>(q, k, v, o, nullptr, (int)lk, batch, hq, hkv, lk, ds, scale);
     return launch_decode<float>(q, k, v, o, nullptr, (int)lk, batch, hq, hkv, lk, ds, scale);
   }
-  if (dtype == KH_BF16 && lq > 1 && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
+  // The MFMA kernel's softmax takes the raw q.k maximum as its reference, which is only the largest
+  // scaled score for scale > 0; other scales take the generic kernel.
+  if (dtype == KH_BF16 && lq > 1 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
     return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, st, scale, causal != 0);
   return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal, nullptr, 0, MaskArgs{},
                         dtype);
@@ -888,7 +899,8 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
     case 4: decode_partial_bf16_kernel<4, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
     default: decode_partial_bf16_kernel<8, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
   }
-  KH_CHECK_LAUNCH();
+  // Launch errors are recorded, and the scratch blocks returned, before any return.
+  hipError_t e = hipGetLastError();
   const int K_in = hq * 128;
   int rc = KH_OK;
   AttnMerge am;
@@ -897,9 +909,11 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
   am.max_chunks = max_chunks;
   am.max_len = ml;
   am.chunk = CH;
-  if (max_chunks <= kMergeInPrologueMaxChunks &&
-      launch_gemv_attn_merge(part, am, (const uint16_t*)w_o, ldw, x, x, (int)n_out, K_in, 1.f, 1.f)) {
-    KH_CHECK_LAUNCH();
+  if (e != hipSuccess) {
+    // nothing more is launched
+  } else if (max_chunks <= kMergeInPrologueMaxChunks &&
+             launch_gemv_attn_merge(part, am, (const uint16_t*)w_o, ldw, x, x, (int)n_out, K_in, 1.f, 1.f)) {
+    e = hipGetLastError();
   } else {
     // long caches: a separate merge into a bf16 row, then the plain GEMV with the residual
     uint16_t* o = (uint16_t*)scratch_alloc((size_t)K_in * 2);
@@ -910,11 +924,16 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
     AttnStrides so{};
     so.oh = 128;
     decode_merge_cols_pos_kernel<<<dim3(4, hq, 1), 256, 0, stream()>>>(part, position, ml, hq, max_chunks, so, o);
-    KH_CHECK_LAUNCH();
-    rc = kh_gemv_fused(0, o, nullptr, nullptr, 0.f, w_o, ldw, x, x, nullptr, n_out, K_in, 1.f, 1.f, KH_F32);
+    e = hipGetLastError();
+    if (e == hipSuccess)
+      rc = kh_gemv_fused(0, o, nullptr, nullptr, 0.f, w_o, ldw, x, x, nullptr, n_out, K_in, 1.f, 1.f, KH_F32);
     scratch_free(o);
   }
   scratch_free(part);  // stream-ordered: reused only by later work on the same stream
+  if (e != hipSuccess) {
+    set_error("kh_decode_attention_block: launch failed: %s", hipGetErrorString(e));
+    return KH_ERR_HIP;
+  }
   return rc;
 }
 

@@ -5,27 +5,30 @@
 // h / (hq / hkv), online softmax in fp32, O = P V / l.
 //
 // A workgroup of WAVES waves shares one kv head: wave w serves query head g = w / (WAVES/G) of the
-// G query heads that read this kv head (G = hq / hkv) and 32 query rows of a BMQ = 32 * WAVES / G row
-// block.  K/V tiles of BN keys (128 by default) are staged in LDS (double buffered, one barrier per
-// tile) and shared by all waves, which compute them in chunks of 64 keys.
+// G query heads that read this kv head (G = hq / hkv <= WAVES) and 32 query rows of a
+// BMQ = 32 * WAVES / G row block.  K/V tiles of BN keys (128) are staged in LDS (double buffered, one
+// barrier per tile) and shared by all waves, which compute them in chunks of 64 keys.
 //
 // Per wave and chunk, with v_mfma_f32_32x32x16_bf16:
 //   S^T (keys x queries) = K Q^T : A = K rows from LDS, B = Q held in registers for the whole loop.
 //   O^T (d x queries)   += V^T P^T: A = V^T fragments, B = P.
-// Each lane owns one query column: the row max / sum of the softmax are in-lane over 32 scores
+// Each lane owns one query column: the row statistics of the softmax are in-lane over 32 scores
 // plus one exchange with lane ^ 32.  K rows are stored in LDS in the order "swap bits 2 and 3 of
 // the key index", which makes S^T accumulator registers j = 0..7 of lane group g hold keys 8g + j
 // (j = 8..15: keys 16 + 8g + j - 8) -- exactly the B-operand layout of the PV product, so P never
-// leaves registers.
+// leaves registers.  V is staged row-major like K and its V^T operand fragments are read with the
+// gfx950 transposing LDS read (ds_read_b64_tr_b16) at a per-lane base plus compile-time offsets.
+// Global loads are raw buffer loads (out-of-range rows read as zero without a branch).
 //
-// V is staged row-major like K and its V^T operand fragments are read with the gfx950 transposing
-// LDS read (ds_read_b64_tr_b16) at a per-lane base plus compile-time offsets.  (A variant stages V
-// transposed, with the 8-key block index XOR-swizzled by (d / 16) % 8 so that the transposing
-// 4-byte writes and the 16-byte operand reads spread over all LDS banks.)  Global loads are raw
-// buffer loads (out-of-range rows read as zero without a branch).  The softmax uses a thresholded
-// reference max (see Softmax), so the O accumulators are rescaled on a few tiles only.
-#include <cstdlib>
-
+// Softmax of the causal / unmasked route (SoftmaxLog2): the QK^T accumulators start at -m (m: the
+// row's reference maximum, raw q.k units) instead of 0, so the MFMA itself delivers s - m and
+// P = 2^((s - m) scale log2 e) is one multiply and one v_exp_f32 per score.  The reference maximum
+// is the exact row maximum of the first chunk and is raised only when a lane's sum of P over its
+// 32 scores exceeds kSumMax (which bounds every P, all being >= 0): the common path has no row
+// maximum and no lane exchange.  O and l are rescaled together on a raise (O / l does not depend
+// on the reference chosen), and l sums the bf16 P the PV product applies.
+// The explicit-mask route keeps a thresholded maximum (SoftmaxRaw), which reproduces the reference
+// softmax's f32(-1e38) floor and its 0 / 0 rows.
 #include "attention.h"
 
 using namespace kh;
@@ -37,28 +40,24 @@ constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
 constexpr int FA_D = 128;
 constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
-// VTR: V is staged row-major (keys x d, like K) and the PV operand is read with the gfx950
-// transposing LDS read; otherwise V is staged transposed (d x keys).
-template <int BN, int WAVES, bool VTR = false>
+template <int BN, int WAVES>
 struct Cfg {
   static constexpr int THREADS = WAVES * 64;
-  // V row stride (elements).  Row-major: 320 B = 80 dwords = 16 banks (mod 64) apart per row.  The
-  // LDS has 64 banks and serves a transposing read 32 lanes per clock: the two 16-lane groups of a
-  // clock read the same 4 rows at column offsets 8 banks apart, so rows must be 16 banks apart for
-  // the 64 dwords to fall on 64 distinct banks (a 288-byte stride gave 2-way conflicts on 28 % of
-  // the LDS-active cycles).
-  static constexpr int VSTR = VTR ? FA_D + 32 : BN + 8;
+  // V row stride (elements).  320 B = 80 dwords = 16 banks (mod 64) apart per row.  The LDS has 64
+  // banks and serves a transposing read 32 lanes per clock: the two 16-lane groups of a clock read
+  // the same 4 rows at column offsets 8 banks apart, so rows must be 16 banks apart for the 64
+  // dwords to fall on 64 distinct banks (a 288-byte stride gave 2-way conflicts on 28 % of the
+  // LDS-active cycles).
+  static constexpr int VSTR = FA_D + 32;
   static constexpr int KTILE = BN * FA_KSTR;         // elements
-  static constexpr int VTILE = VTR ? BN * VSTR : FA_D * VSTR;  // elements
-  static constexpr int NK = BN * 16 / THREADS;       // 16-byte K chunks per thread per tile
-  static constexpr int PAIRS = THREADS / 16;         // V key pairs staged per pass
-  static constexpr int NVG = BN / (2 * PAIRS);       // V passes per tile (transposed V)
-  // Compute works on 64-key chunks; a staged tile holds NCH of them (transposed V: one).
+  static constexpr int VTILE = BN * VSTR;            // elements
+  static constexpr int NK = BN * 16 / THREADS;       // 16-byte K (and V) chunks per thread per tile
+  // Compute works on 64-key chunks; a staged tile holds NCH of them.
   static constexpr int BNC = 64;
   static constexpr int NCH = BN / BNC;
   static constexpr int NSUB = BNC / 32;              // 32-key S^T subtiles per chunk
-  static_assert(BN % BNC == 0 && (VTR || NCH == 1), "multi-chunk tiles need row-major V");
-  static_assert(NK >= 1 && NVG >= 1, "tile too small for the workgroup");
+  static_assert(BN % BNC == 0, "tiles are whole 64-key chunks");
+  static_assert(NK >= 1, "tile too small for the workgroup");
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -90,9 +89,9 @@ __device__ __forceinline__ void sched_reads_ahead() {
 }
 
 // Shared per-workgroup setup and staging helpers.
-template <int BN, int WAVES, bool VTR = false>
+template <int BN, int WAVES>
 struct Flash {
-  using C = Cfg<BN, WAVES, VTR>;
+  using C = Cfg<BN, WAVES>;
   int G, BMQ, tid, wave, lane, r, g, b, hk, hqi, q0, qw0, qi, ntiles, wave_last_q, wave_tiles, dcol;
   __amdgpu_buffer_rsrc_t rk, rv;
   AttnStrides st;
@@ -139,6 +138,7 @@ struct Flash {
   // while the 32 lanes read 32 consecutive rows (no bank conflicts).
   static __device__ __forceinline__ int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
+  // This lane's Q row: query qi, columns 8 g + 16 c .. + 7 (c = 0..7).
   __device__ __forceinline__ void load_q(const uint16_t* Q, int lq, bf16x8 (&qreg)[8]) const {
     const uint16_t* qh = Q + b * st.qb + hqi * st.qh;
     const auto rq = make_rsrc(qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + FA_D) * 2));
@@ -146,23 +146,21 @@ struct Flash {
 #pragma unroll
     for (int c = 0; c < 8; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
   }
-  // K: chunk id = tid + THREADS i -> key id / 16, d 8 * (id % 16).
-  __device__ __forceinline__ void load_k(int t, uint4 (&kst)[C::NK]) const {
+  // K and V rows: chunk id = tid + THREADS i -> key id / 16, d 8 * (id % 16).
+  __device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rsrc, int64_t rstride, int t,
+                                            uint4 (&stg)[C::NK]) const {
 #pragma unroll
     for (int i = 0; i < C::NK; ++i) {
       const int key = t * BN + ((tid + C::THREADS * i) >> 4);
-      kst[i] = buf_load16(rk, (uint32_t)(((int64_t)key * st.ks + dcol) * 2));
+      stg[i] = buf_load16(rsrc, (uint32_t)(((int64_t)key * rstride + dcol) * 2));
     }
   }
-  // V row-major (VTR): the K chunk pattern, chunk id = tid + THREADS i -> key id / 16, d 8 (id % 16).
-  __device__ __forceinline__ void load_v_rows(int t, uint4 (&vst)[C::NK]) const {
+  __device__ __forceinline__ void store_k(uint16_t* ks, const uint4 (&kst)[C::NK]) const {
 #pragma unroll
-    for (int i = 0; i < C::NK; ++i) {
-      const int key = t * BN + ((tid + C::THREADS * i) >> 4);
-      vst[i] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + dcol) * 2));
-    }
+    for (int i = 0; i < C::NK; ++i)
+      *reinterpret_cast<uint4*>(ks + swap23((tid + C::THREADS * i) >> 4) * FA_KSTR + dcol) = kst[i];
   }
-  __device__ __forceinline__ void store_v_rows(uint16_t* vs, const uint4 (&vst)[C::NK]) const {
+  __device__ __forceinline__ void store_v(uint16_t* vs, const uint4 (&vst)[C::NK]) const {
 #pragma unroll
     for (int i = 0; i < C::NK; ++i)
       *reinterpret_cast<uint4*>(vs + ((tid + C::THREADS * i) >> 4) * C::VSTR + dcol) = vst[i];
@@ -171,7 +169,7 @@ struct Flash {
   // 16 kc + 8 g + e) is two transposing reads: lane l = 16 G + L supplies row 16 kc + 8 g + L / 4
   // (+ 4 for the second read), columns 32 dt + 16 (G & 1) + 4 (L & 3) .. + 3 -- a per-lane base
   // plus compile-time offsets.
-  __device__ __forceinline__ void pv_tr(const uint16_t* vs, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[4]) const {
+  __device__ __forceinline__ void pv(const uint16_t* vs, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[4]) const {
     const int L = lane & 15, Gq = lane >> 4;
     const uint16_t* vbase = vs + (8 * (Gq >> 1) + (L >> 2)) * C::VSTR + 16 * (Gq & 1) + 4 * (L & 3);
     constexpr int KC = 2 * C::NSUB;
@@ -193,41 +191,10 @@ struct Flash {
                                                            oacc[dt], 0, 0, 0);
     sched_reads_ahead<4 * KC, 2>();
   }
-  // V: pass vg stages key pair p = tid / 16 + PAIRS vg (keys 2p, 2p + 1), d 8 * (tid % 16) .. + 8.
-  __device__ __forceinline__ void load_v(int t, uint4 (&vst)[C::NVG][2]) const {
-#pragma unroll
-    for (int vg = 0; vg < C::NVG; ++vg)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int key = t * BN + 2 * ((tid >> 4) + C::PAIRS * vg) + i;
-        vst[vg][i] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + dcol) * 2));
-      }
-  }
-  __device__ __forceinline__ void store_k(uint16_t* ks, const uint4 (&kst)[C::NK]) const {
-#pragma unroll
-    for (int i = 0; i < C::NK; ++i)
-      *reinterpret_cast<uint4*>(ks + swap23((tid + C::THREADS * i) >> 4) * FA_KSTR + dcol) = kst[i];
-  }
-  __device__ __forceinline__ void store_v(uint16_t* vts, const uint4 (&vst)[C::NVG][2]) const {
-    const int swz = (dcol >> 4) & 7;  // rows dcol .. dcol + 7 share (d / 16) % 8
-#pragma unroll
-    for (int vg = 0; vg < C::NVG; ++vg) {
-      const int p = (tid >> 4) + C::PAIRS * vg;
-      const int word = (((p >> 2) ^ swz) << 2) | (p & 3);  // swizzled 8-key block, pair inside it
-      const uint32_t a[4] = {vst[vg][0].x, vst[vg][0].y, vst[vg][0].z, vst[vg][0].w};
-      const uint32_t c[4] = {vst[vg][1].x, vst[vg][1].y, vst[vg][1].z, vst[vg][1].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // row d = dcol + 2e holds (V[2p][d], V[2p+1][d]); row d + 1 likewise
-        const uint32_t lo = (a[e] & 0xffffu) | (c[e] << 16);
-        const uint32_t hi = (a[e] >> 16) | (c[e] & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(vts + (dcol + 2 * e) * C::VSTR + 2 * word) = lo;
-        *reinterpret_cast<uint32_t*>(vts + (dcol + 2 * e + 1) * C::VSTR + 2 * word) = hi;
-      }
-    }
-  }
-  // S^T subtiles of one K tile in LDS.
-  __device__ __forceinline__ void qk(const uint16_t* ks, const bf16x8 (&qreg)[8], f32x16 (&sacc)[C::NSUB]) const {
+  // S^T subtiles of one 64-key chunk in LDS; the accumulators start at cinit (INIT) or 0.
+  template <bool INIT>
+  __device__ __forceinline__ void qk(const uint16_t* ks, const bf16x8 (&qreg)[8], const f32x16& cinit,
+                                     f32x16 (&sacc)[C::NSUB]) const {
     bf16x8 kf[C::NSUB * 8];
 #pragma unroll
     for (int s = 0; s < C::NSUB; ++s) {
@@ -237,14 +204,19 @@ struct Flash {
     }
 #pragma unroll
     for (int s = 0; s < C::NSUB; ++s) {
+      if constexpr (INIT) {
+        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8], qreg[0], cinit, 0, 0, 0);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) sacc[s][j] = 0.f;
+        for (int j = 0; j < 16; ++j) sacc[s][j] = 0.f;
+        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8], qreg[0], sacc[s], 0, 0, 0);
+      }
 #pragma unroll
-      for (int c = 0; c < 8; ++c) sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8 + c], qreg[c], sacc[s], 0, 0, 0);
+      for (int c = 1; c < 8; ++c) sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8 + c], qreg[c], sacc[s], 0, 0, 0);
     }
     sched_reads_ahead<C::NSUB * 8, 1>();
   }
-  // Causal / length mask of tile t (only tiles crossing the diagonal or the sequence end).
+  // Causal / length mask of chunk t (only chunks crossing the diagonal or the sequence end).
   template <bool CAUSAL>
   __device__ __forceinline__ void mask(int t, int lk, f32x16 (&sc)[C::NSUB]) const {
     const int kt = t * C::BNC;  // t counts 64-key compute chunks
@@ -255,20 +227,6 @@ struct Flash {
 #pragma unroll
         for (int j = 0; j < 16; ++j)
           if (32 * s + 16 * (j >> 3) + (j & 7) >= lim) sc[s][j] = -INFINITY;
-    }
-  }
-  // O^T += V^T P^T for one V tile in LDS.
-  __device__ __forceinline__ void pv(const uint16_t* vts, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[4]) const {
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int d = 32 * dt + r;
-      const int swz = (d >> 4) & 7;
-      const uint16_t* vrow = vts + d * C::VSTR;
-#pragma unroll
-      for (int kc = 0; kc < 2 * C::NSUB; ++kc) {
-        const bf16x8 vv = as_bf16x8(*reinterpret_cast<const uint4*>(vrow + 8 * ((2 * kc + g) ^ swz)));
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, pk[kc], oacc[dt], 0, 0, 0);
-      }
     }
   }
   // Additive mask of a 64-key tile t for this lane's query row (MASKT 1: f32, 2: bf16), held as
@@ -344,36 +302,117 @@ struct Flash {
   }
 };
 
-// Online-softmax state of one lane (one query row, half of each tile's keys).
+// Row maximum of a chunk's scores: this lane's 32, then the partner lane (lane ^ 32) that holds
+// the other 32 keys of the same query row.
+template <int NSUB>
+__device__ __forceinline__ float chunk_row_max(const f32x16 (&sc)[NSUB]) {
+  float m4[NSUB * 4];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+    for (int j = 0; j < 16; j += 4)
+      m4[s * 4 + j / 4] = fmaxf(fmaxf(sc[s][j], sc[s][j + 1]), fmaxf(sc[s][j + 2], sc[s][j + 3]));
+  float mx = m4[0];
+#pragma unroll
+  for (int i = 1; i < NSUB * 4; ++i) mx = fmaxf(mx, m4[i]);
+  return fmaxf(mx, __shfl_xor(mx, 32, 64));
+}
+
+// Online softmax of the causal / unmasked route: raw q.k scores relative to the reference maximum m
+// (the QK^T accumulators start at mneg = -m, 0 before the first raise); P = 2^(c (s - m)) with
+// c = scale log2 e.
+constexpr float kSumMax = 4096.f;  // a lane's chunk sum of P above this raises the reference
+
+struct SoftmaxLog2 {
+  float m = -INFINITY;  // reference maximum of this row (raw q.k units); -inf before the first raise
+  float l = 0.f;        // partial denominator of this lane's keys, relative to m
+  f32x16 mneg;          // -m in every register (0 while m = -inf)
+
+  __device__ __forceinline__ SoftmaxLog2() {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mneg[j] = 0.f;
+  }
+  // P = 2^(c sc) as bf16 operands; returns this lane's sum of those bf16 values (two per
+  // v_dot2c_f32_bf16 against (1, 1)): l then sums exactly the weights the PV product applies.
+  template <int NSUB>
+  static __device__ __forceinline__ float exponentiate(const f32x16 (&sc)[NSUB], float c, bf16x8 (&pk)[2 * NSUB]) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    float ps[2 * NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        bf16x8 pv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = (__bf16)fast_exp2(sc[s][8 * h + e] * c);
+        pk[2 * s + h] = pv;
+        const bf16x2 p01 = __builtin_shufflevector(pv, pv, 0, 1), p23 = __builtin_shufflevector(pv, pv, 2, 3);
+        const bf16x2 p45 = __builtin_shufflevector(pv, pv, 4, 5), p67 = __builtin_shufflevector(pv, pv, 6, 7);
+        float sum = __builtin_amdgcn_fdot2_f32_bf16(p01, one, 0.f, false);
+        sum = __builtin_amdgcn_fdot2_f32_bf16(p23, one, sum, false);
+        sum = __builtin_amdgcn_fdot2_f32_bf16(p45, one, sum, false);
+        ps[2 * s + h] = __builtin_amdgcn_fdot2_f32_bf16(p67, one, sum, false);
+      }
+    float t = ps[0];
+#pragma unroll
+    for (int i = 1; i < 2 * NSUB; ++i) t += ps[i];
+    return t;
+  }
+  // True (wave-uniform) if some row of the wave must raise its reference: the first chunk, or a
+  // lane sum above kSumMax (inf included).
+  __device__ __forceinline__ bool need_raise(float ps) const {
+    return __any(m == -INFINITY || !(ps <= kSumMax));
+  }
+  // Raises every row's reference to its exact maximum over the chunk (when higher), shifts the
+  // chunk's scores to the new reference and rescales O and l.  A row with nothing unmasked so far
+  // keeps m = -inf (and P = 0).
+  template <int NSUB>
+  __device__ __forceinline__ void raise(f32x16 (&sc)[NSUB], float c, f32x16 (&oacc)[4]) {
+    const float mx = chunk_row_max(sc);  // relative to m (absolute while m = -inf)
+    float d, alpha;
+    if (m == -INFINITY) {
+      d = mx == -INFINITY ? 0.f : mx;
+      alpha = 0.f;  // O and l are still empty
+      m = mx;
+    } else {
+      d = fmaxf(mx, 0.f);
+      alpha = fast_exp2(-d * c);
+      m += d;
+    }
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sc[s][j] -= d;
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+    const float mn = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mneg[j] = mn;
+  }
+};
+
+// Online softmax of the explicit-mask route, raw q.k units.
 //
 // The exponentials use a reference max m_ref that is raised only when some row's tile max exceeds
-// it by more than kRescaleLog2 (log2 units).  P = 2^((s - m_ref) c2) then stays <= 2^kRescaleLog2
-// (exact in bf16/fp32 like any value <= 1), O and l are rescaled together only on those rare raises,
-// and the final O / l does not depend on the reference chosen.  With a fixed threshold the rescale
-// of the 64 accumulator registers runs on the first tile and then almost never.
+// it by more than kRescaleLog2 (log2 units).  P = 2^((s - m_ref) c2) then stays <= 2^kRescaleLog2,
+// O and l are rescaled together only on those rare raises, and the final O / l does not depend on
+// the reference chosen.
 constexpr float kRescaleLog2 = 8.0f;
 
-struct Softmax {
+struct SoftmaxRaw {
   float m_ref = -INFINITY;  // reference max of raw scores (q . k) for this row
   float l_run = 0.f;        // partial denominator of this lane's keys, relative to m_ref
 
   // Raises the reference max when this tile needs it (rescaling O and l); true (wave-uniform) if
-  // any lane did, in which case P must be recomputed.
-  // floor: the lowest row max (raw units): the reference softmax starts its max at f32(-1e38)
-  // on the explicit-mask route; -inf otherwise.
+  // any lane did, in which case P must be recomputed.  floor: the lowest row max (raw units): the
+  // reference softmax starts its max at f32(-1e38).
   template <int NSUB>
-  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4],
-                                         float floor = -INFINITY) {
-    float m4[NSUB * 4];
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-      for (int j = 0; j < 16; j += 4)
-        m4[s * 4 + j / 4] = fmaxf(fmaxf(sc[s][j], sc[s][j + 1]), fmaxf(sc[s][j + 2], sc[s][j + 3]));
-    float mx = m4[0];
-#pragma unroll
-    for (int i = 1; i < NSUB * 4; ++i) mx = fmaxf(mx, m4[i]);
-    mx = fmaxf(fmaxf(mx, __shfl_xor(mx, 32, 64)), floor);
+  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4], float floor) {
+    const float mx = fmaxf(chunk_row_max(sc), floor);
     // NaN-free by construction (this file is compiled assuming no NaNs, so that fmaxf needs no
     // canonicalisation): a row with nothing unmasked (mx = -inf) never asks for a raise, and
     // m_ref = -inf only before the first raise, where alpha = 2^-inf = 0 clears the empty O and l.
@@ -403,8 +442,7 @@ struct Softmax {
         bf16x8 pv;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          // one v_fma_f32 per score (written out: contraction would fuse m_ref * c2 instead and
-          // leave a separate multiply per score)
+          // one v_fma_f32 per score (written out: contraction would fuse m_ref * c2 instead)
           const float p = fast_exp2(__builtin_fmaf(sc[s][8 * h + e], c2, -mb));
           ps[h] += p;
           pv[e] = (__bf16)p;
@@ -420,51 +458,44 @@ struct Softmax {
 // =============================================================================================
 // MASKT: 0 = causal / none as CAUSAL says; 1, 2 = additive f32 / bf16 mask M (64-key tiles, no
 // causal mask, the reference's explicit-mask route).
-template <int BN, int WAVES, int MINB, bool CAUSAL, bool VTR = false, int MASKT = 0>
+template <int BN, int WAVES, int MINB, bool CAUSAL, int MASKT = 0>
 __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale,
     int n_qblocks, const void* __restrict__ M, MaskArgs ma) {
-  using C = Cfg<BN, WAVES, VTR>;
+  using C = Cfg<BN, WAVES>;
+  using FL = Flash<BN, WAVES>;
   static_assert(MASKT == 0 || (BN == 64 && !CAUSAL), "masked tiles are 64 keys, without causal masking");
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
-  Flash<BN, WAVES, VTR> F;
+  FL F;
   F.init(batch, hq, hkv, lq, lk, st, CAUSAL, n_qblocks, K, V);
+  const float c2 = scale * kLog2e;
   bf16x8 qreg[8];
   F.load_q(Q, lq, qreg);
 
-  // V staging registers: row-major chunks (VTR) or transposing key pairs.
-  using VStage = std::conditional_t<VTR, uint4[C::NK], uint4[C::NVG][2]>;
-  uint4 kst[C::NK];
-  VStage vst;
-  auto load_v = [&](int t) {
-    if constexpr (VTR) F.load_v_rows(t, vst); else F.load_v(t, vst);
-  };
-  auto store_v = [&](uint16_t* vs) {
-    if constexpr (VTR) F.store_v_rows(vs, vst); else F.store_v(vs, vst);
-  };
+  uint4 kst[C::NK], vst[C::NK];
   f32x16 oacc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
-  Softmax sm;
-  const float c2 = scale * kLog2e;
+  SoftmaxLog2 sl;
+  SoftmaxRaw sr;
   const int ntiles = F.ntiles;
 
   if (ntiles > 0) {
-    F.load_k(0, kst);
-    load_v(0);
+    F.load_rows(F.rk, st.ks, 0, kst);
+    F.load_rows(F.rv, st.vs, 0, vst);
     F.store_k(smem, kst);
-    store_v(smem + C::KTILE);
+    F.store_v(smem + C::KTILE, vst);
   }
   // Retire every outstanding load (Q included) before the loop, so the compiler's wait counting
   // inside the loop only ever covers the next tile's prefetch and never stalls QK^T on it.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  using MR = typename Flash<BN, WAVES, VTR>::template MaskRegs<MASKT == 0 ? 2 : MASKT>;
+  using MR = typename FL::template MaskRegs<MASKT == 0 ? 2 : MASKT>;
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(M, MASKT == 0 ? 0u : ma.bytes);
   for (int t = 0; t < ntiles; ++t) {
     const bool has_next = t + 1 < ntiles;
@@ -473,8 +504,8 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     MR mreg;
     if constexpr (MASKT != 0) F.template load_mask<MASKT>(t, lq, rm, ma, mreg);
     if (has_next) {
-      F.load_k(t + 1, kst);
-      load_v(t + 1);
+      F.load_rows(F.rk, st.ks, t + 1, kst);
+      F.load_rows(F.rv, st.vs, t + 1, vst);
     }
     const uint16_t* ks = smem + (t & 1) * STAGE;
 #pragma unroll
@@ -482,59 +513,47 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
       const int tc = t * C::NCH + c;  // 64-key compute chunk
       if (tc < F.wave_tiles) {
         f32x16 sacc[C::NSUB];
-        F.qk(ks + c * C::BNC * FA_KSTR, qreg, sacc);
-        if constexpr (MASKT != 0)
-          F.template apply_mask<MASKT>(tc, lk, mreg, ma.inv_scale, sacc);
-        else
-          F.template mask<CAUSAL>(tc, lk, sacc);
-        // Written as P computed with the current reference max, then recomputed after a raise
-        // (rare after the first tile).  The compiler folds the two into one exponentiation after
-        // the max check, so the generated code checks the max (lane-pair exchange included) first
-        // and exponentiates once, in the same basic block as the PV product.
         bf16x8 pk[2 * C::NSUB];
-        float ps = sm.exponentiate(sacc, c2, pk);
-        if (sm.update(sacc, c2, oacc, MASKT != 0 ? ma.floor_raw : -INFINITY)) ps = sm.exponentiate(sacc, c2, pk);
-        sm.l_run += ps;
-        if constexpr (VTR)
-          F.pv_tr(ks + C::KTILE + c * C::BNC * C::VSTR, pk, oacc);
-        else
-          F.pv(ks + C::KTILE, pk, oacc);
+        if constexpr (MASKT == 0) {
+          F.template qk<true>(ks + c * C::BNC * FA_KSTR, qreg, sl.mneg, sacc);
+          F.template mask<CAUSAL>(tc, lk, sacc);
+          float ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
+          if (sl.need_raise(ps)) {
+            sl.raise(sacc, c2, oacc);
+            ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
+          }
+          sl.l += ps;
+        } else {
+          F.template qk<false>(ks + c * C::BNC * FA_KSTR, qreg, sl.mneg, sacc);
+          F.template apply_mask<MASKT>(tc, lk, mreg, ma.inv_scale, sacc);
+          // Written as P computed with the current reference max, then recomputed after a raise
+          // (rare after the first tile); the compiler folds the two into one exponentiation
+          // after the max check.
+          float ps = sr.exponentiate(sacc, c2, pk);
+          if (sr.update(sacc, c2, oacc, ma.floor_raw)) ps = sr.exponentiate(sacc, c2, pk);
+          sr.l_run += ps;
+        }
+        F.pv(ks + C::KTILE + c * C::BNC * C::VSTR, pk, oacc);
       }
     }
     if (has_next) {
       uint16_t* nxt = smem + ((t + 1) & 1) * STAGE;
       F.store_k(nxt, kst);
-      store_v(nxt + C::KTILE);
+      F.store_v(nxt + C::KTILE, vst);
     }
     __syncthreads();
   }
-  F.template store_o<MASKT != 0>(O, lq, sm.l_run, oacc);
+  F.template store_o<MASKT != 0>(O, lq, MASKT == 0 ? sl.l : sr.l_run, oacc);
 }
 
-int flash_variant() {
-  // 0: 128-key stages, row-major V read with transposing loads (default, fastest measured);
-  // 1: 64-key stages, V staged transposed; 2: 64-key stages, row-major V; 3: as 1 with 4 waves
-  // and two workgroups per CU.  KANDLE_FLASH_VARIANT selects one for sweeps.
-  static int v = [] {
-    const char* e = getenv("KANDLE_FLASH_VARIANT");
-    const int x = e ? atoi(e) : 0;
-    return (x >= 0 && x <= 3) ? x : 0;
-  }();
-  return v;
-}
+constexpr int kWaves = 8;  // waves per workgroup: query rows of 32 * 8 / G, one kv head
 
-template <int BN, int WAVES, int MINB, bool VTR = false>
-void launch_sync(bool causal, const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
-                 int lq, int lk, const AttnStrides& st, float scale, int nqb, int nblk) {
-  const uint16_t *Q = (const uint16_t*)q, *K = (const uint16_t*)k, *V = (const uint16_t*)v;
-  uint16_t* O = (uint16_t*)o;
-  const MaskArgs none{};
-  if (causal)
-    flash_fwd_kernel<BN, WAVES, MINB, true, VTR><<<nblk, WAVES * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq,
-                                                                                   lk, st, scale, nqb, nullptr, none);
-  else
-    flash_fwd_kernel<BN, WAVES, MINB, false, VTR><<<nblk, WAVES * 64, 0, stream()>>>(
-        Q, K, V, O, batch, hq, hkv, lq, lk, st, scale, nqb, nullptr, none);
+template <bool CAUSAL>
+void launch_fwd(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
+                const AttnStrides& st, float scale, int nqb, int nblk) {
+  flash_fwd_kernel<128, kWaves, 1, CAUSAL><<<nblk, kWaves * 64, 0, stream()>>>(
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, lq, lk, st, scale,
+      nqb, nullptr, MaskArgs{});
 }
 
 }  // namespace
@@ -544,7 +563,7 @@ namespace kh {
 bool flash_prefill_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv,
                              int64_t lq, int64_t lk, int d, const AttnStrides& st) {
   const int G = hq / hkv;
-  if (d != FA_D || !(G == 1 || G == 2 || G == 4)) return false;
+  if (d != FA_D || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
   const int64_t s16[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.vb, st.vh, st.vs};
   for (int64_t s : s16)
@@ -560,21 +579,15 @@ bool flash_prefill_supported(const void* q, const void* k, const void* v, const 
 int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
                               int lq, int lk, const AttnStrides& st, float scale, bool causal) {
   const int G = hq / hkv;
-  const int var = flash_variant();
-  const int waves = var == 3 ? 4 : 8;
-  const int BMQ = 32 * (waves / G);
+  const int BMQ = 32 * (kWaves / G);
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
   const int nblk = (int)nblk64;
-  if (var == 0)
-    launch_sync<128, 8, 1, true>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
-  else if (var == 1)
-    launch_sync<64, 8, 1>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
-  else if (var == 2)
-    launch_sync<64, 8, 1, true>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
+  if (causal)
+    launch_fwd<true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
   else
-    launch_sync<64, 4, 2>(causal, q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
+    launch_fwd<false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
@@ -583,7 +596,7 @@ int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v
                                      int hkv, int lq, int lk, const AttnStrides& st, float scale, const void* mask,
                                      const MaskArgs& ma, int mask_dtype) {
   const int G = hq / hkv;
-  const int BMQ = 32 * (8 / G);
+  const int BMQ = 32 * (kWaves / G);
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention_masked: grid too large");
@@ -591,11 +604,11 @@ int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v
   const uint16_t *Q = (const uint16_t*)q, *K = (const uint16_t*)k, *V = (const uint16_t*)v;
   uint16_t* O = (uint16_t*)o;
   if (mask_dtype == KH_F32)
-    flash_fwd_kernel<64, 8, 1, false, true, 1><<<nblk, 512, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk, st,
-                                                                            scale, nqb, mask, ma);
+    flash_fwd_kernel<64, kWaves, 1, false, 1><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
+                                                                                  st, scale, nqb, mask, ma);
   else
-    flash_fwd_kernel<64, 8, 1, false, true, 2><<<nblk, 512, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk, st,
-                                                                            scale, nqb, mask, ma);
+    flash_fwd_kernel<64, kWaves, 1, false, 2><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
+                                                                                  st, scale, nqb, mask, ma);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

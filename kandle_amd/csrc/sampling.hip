@@ -617,7 +617,10 @@ __global__ __launch_bounds__(1024) void cut_kernel(const float* __restrict__ p, 
   __shared__ int res_s;
   const int t = threadIdx.x;
   int cut = k_eff;
-  if (top_p < 1.0) {
+  if (top_p <= 0.0) {
+    // The reference's `cum >= topP` holds at i = 0: exactly the first id is kept.
+    cut = min(1, k_eff);
+  } else if (top_p < 1.0) {
     const unsigned long long target = (unsigned long long)ceil(top_p * kFix);
     unsigned long long carry = 0, unused = 0;
     const int blk = first_crossing<false>([&](int b) { return pfix_sum[b]; }, nb, 0ull, target, pre, &res_s, &carry);

@@ -391,8 +391,9 @@ class Qwen3ForCausalLM:
         """Prefill the prompt, then greedy-decode (for_causal_lm.ts:475-508): max_new_tokens token
         ids, each the lowest-index argmax of the previous logits, after max_new_tokens decode
         forwards as in the reference loop.  The decode steps run on device state; with use_graph
-        the step is captured once and replayed.  return_logits adds the fp32 logits each token was
-        chosen from.  timing (a dict) receives wall times: prefill_ms, decode_ms (all decode steps,
+        the step is captured once and replayed.  return_logits adds the fp32 logits of every forward:
+        the prefill's last position and each of the max_new_tokens decode steps (the last of which
+        follows the last token), max_new_tokens + 1 rows.  timing (a dict) receives wall times: prefill_ms, decode_ms (all decode steps,
         including the eager first step and the capture) and, with a graph, replay_ms over the
         replay_steps = max_new_tokens - 1 replayed steps."""
         from .. import _lib
@@ -417,7 +418,7 @@ class Qwen3ForCausalLM:
             for i in range(N):
                 if not use_graph or i == 0:
                     lg = self._decode_step(st)
-                    if return_logits and i + 1 < N:
+                    if return_logits:
                         all_logits.append(lg.numpy()[0])
                     lg.dispose()
                     if use_graph and N > 1:
@@ -430,7 +431,7 @@ class Qwen3ForCausalLM:
                             t_replay = time.perf_counter()
                 else:
                     graph.replay()
-                    if return_logits and i + 1 < N:
+                    if return_logits:
                         all_logits.append(g_logits.numpy()[0])
             toks = st.log.numpy()[:N].tolist()   # waits for the last step
             t2 = time.perf_counter()

@@ -169,6 +169,24 @@ def flash_js(q, k, v, scale=None, causal=False, heads_limit=0):
     return o, float(json.loads(out.stdout.strip().splitlines()[-1])["ms"])
 
 
+def js_bench(op, inputs, args, repeat=1, outputs=()):
+    """Runs oracle/js/bench_cpu.js OP on float32 inputs {name: array} with numeric ARGS: one untimed
+    run, then `repeat` timed runs on one Node thread.  Returns ({name: float32 array} for the
+    requested output files, [ms of each timed run])."""
+    import json
+    import subprocess
+    import tempfile
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "js", "bench_cpu.js")
+    with tempfile.TemporaryDirectory() as d:
+        for name, a in inputs.items():
+            _f32(a).tofile(os.path.join(d, name + ".f32"))
+        cmd = ["node", script, op, d, str(int(repeat))] + [repr(float(x)) if isinstance(x, float) else str(x)
+                                                           for x in args]
+        out = subprocess.run(cmd, capture_output=True, text=True, check=True)
+        res = {name: np.fromfile(os.path.join(d, name + ".f32"), dtype=np.float32) for name in outputs}
+    return res, [float(x) for x in json.loads(out.stdout.strip().splitlines()[-1])["runs_ms"]]
+
+
 def rms_norm(x, w=None, eps=1e-6) -> np.ndarray:
     x = _f32(x)
     n = x.shape[-1]
@@ -214,6 +232,34 @@ def linear(a, w, cin=None, bias=None, alpha=1.0, beta=0.0) -> np.ndarray:
     bi = None if bias is None else _f32(bias)
     lib().or_linear(a, w, _ptr(ci), _ptr(bi), c, M, N, K, float(alpha), float(beta))
     return c
+
+
+def argmax_workgroup_rule(x, wg=256) -> np.ndarray:
+    """The reference argmax kernel's tie rule, restated for comparison only, by simulating the
+    kernel: thread t of a workgroup of wg threads (a power of two) keeps the first strict maximum of
+    indices t, t + wg, t + 2 wg, ... (packages/backend-webgpu/src/kernels/reduction/
+    argShaderBuilder.ts:214-228); then for stride = wg/2, wg/4, ..., 1 position p < stride takes
+    position p + stride's value only when it is strictly greater (:86-98), and position 0 is the
+    result.  Among tied maxima the result depends on wg and is not the lowest index in general."""
+    x = np.asarray(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    out = np.zeros(x2.shape[0], np.int32)
+    lowest = -np.float32(3.4028234663852886e38)
+    for r, row in enumerate(x2):
+        vals = [lowest] * wg
+        idxs = [0] * wg
+        for t in range(wg):
+            for i in range(t, row.size, wg):
+                if row[i] > vals[t]:
+                    vals[t], idxs[t] = row[i], i
+        stride = wg // 2
+        while stride >= 1:
+            for p in range(stride):
+                if vals[p + stride] > vals[p]:
+                    vals[p], idxs[p] = vals[p + stride], idxs[p + stride]
+            stride //= 2
+        out[r] = idxs[0]
+    return out.reshape(x.shape[:-1])
 
 
 def argmax(x) -> np.ndarray:

@@ -222,10 +222,16 @@ void or_linear(const float* A, const float* W, const float* cin, const float* bi
     }
 }
 
-/* Lowest index among the maxima of each row (greedy rule of sample():
- * packages/model-utils/src/sampling/index.ts:132,138; argmax kernel
- * packages/backend-webgpu/src/kernels/reduction/argShaderBuilder.ts:205-240 uses strict '>' from
- * -FLT_MAX, so NaN never wins and a row with no value above -FLT_MAX yields 0). */
+/* Lowest index among the maxima of each row: the greedy rule of sample()
+ * (packages/model-utils/src/sampling/index.ts:132,138: first id of a stable descending sort).
+ * Values are compared with strict '>' from -FLT_MAX as the reference argmax kernel does
+ * (packages/backend-webgpu/src/kernels/reduction/argShaderBuilder.ts:214-228), so NaN never wins
+ * and a row with no value above -FLT_MAX yields 0.  Ties are NOT resolved as that kernel resolves
+ * them: its thread t scans indices t, t + W, t + 2W, ... (W = the device's workgroup size) and
+ * keeps its first maximum, and its tree reduction (:86-98) lets position p take position
+ * p + stride's value only when strictly greater, so among tied maxima the result depends on W
+ * (W = 4, maxima at 1 and 2: index 2; W = 256, maxima at 1 and 256: index 256).  This restatement
+ * and the GPU kernel use the device-independent lowest-index rule. */
 void or_argmax(const float* x, int64_t rows, int64_t n, int32_t* out) {
   for (int64_t r = 0; r < rows; ++r) {
     float best = -3.4028234663852886e38f;

@@ -95,7 +95,9 @@ class Qwen3Oracle:
         return (xf @ self.embed.T)[0].astype(np.float32)
 
     def generate(self, prompt_ids, max_new_tokens: int):
-        """(token ids, per-step logits) for greedy decoding; argmax keeps the lowest index on ties."""
+        """(token ids, logits of every forward) for greedy decoding; argmax keeps the lowest index on
+        ties.  The logits are the prefill's last position and each decode step's, the last one
+        after the last token: max_new_tokens + 1 rows."""
         logits = self.forward(prompt_ids, 0)
         pos = len(prompt_ids)
         toks, all_logits = [], []
@@ -105,4 +107,5 @@ class Qwen3Oracle:
             toks.append(nxt)
             logits = self.forward([nxt], pos)
             pos += 1
+        all_logits.append(logits)
         return toks, all_logits

@@ -167,26 +167,101 @@ def test_decode_c4_full_size(hip):
         t.dispose()
 
 
-def test_flash_c3_full_size_sampled_rows(hip):
-    """Config C3 at full size (B=4, Hq=16, Hkv=8, S=4096, D=128, causal, bf16): 48 query rows,
-    including the first and last of each sampled head, are checked exactly against the oracle."""
+def test_flash_c3_full_size(hip):
+    """Config C3 at full size (B=4, Hq=16, Hkv=8, S=4096, D=128, causal, bf16): every row of two
+    whole (batch, head) slices (the first and the last, 4096 query rows each, every causal key
+    range), the last 128-row query block of every one of the 64 heads, and 48 sampled rows, each
+    against the oracle on the same inputs."""
     B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
     q, qh = seeded(91, (B, Hq, S, D), "bfloat16")
     k, kh = seeded(92, (B, Hkv, S, D), "bfloat16")
     v, vh = seeded(93, (B, Hkv, S, D), "bfloat16")
     out = _sdpa_gpu(q, k, v, True)
     assert np.all(np.isfinite(out))
+    G = Hq // Hkv
+    worst = 0.0
+    for b, h in [(0, 0), (B - 1, Hq - 1)]:
+        ref = oracle.sdpa(qh[b:b + 1, h:h + 1], kh[b:b + 1, h // G:h // G + 1], vh[b:b + 1, h // G:h // G + 1],
+                          causal=True)
+        err = float(np.max(np.abs(out[b, h] - ref[0, 0])))
+        worst = max(worst, err)
+        assert err < BF16_ATOL, ("slice", b, h, err)
+    # the last query block (128 rows at G = 2) of every one of the 64 heads: rows S - 128 + i see
+    # keys 0 .. S - 128 + i, i.e. an explicit mask of -inf above that diagonal
+    tail = 128
+    tmask = np.where(np.arange(S)[None, :] > (S - tail + np.arange(tail))[:, None], -np.inf, 0.0)
+    ref = oracle.sdpa_masked(qh[:, :, S - tail:], kh, vh, tmask.astype(np.float32))
+    err = float(np.max(np.abs(out[:, :, S - tail:] - ref)))
+    worst = max(worst, err)
+    assert err < BF16_ATOL, ("last block", err)
     r = np.random.default_rng(7)
     rows = [(0, 0, 0), (3, 15, S - 1), (1, 7, 4095), (2, 8, 1)] + [
         (int(r.integers(B)), int(r.integers(Hq)), int(r.integers(S))) for _ in range(44)]
     for b, h, i in rows:
-        hk = h // (Hq // Hkv)
+        hk = h // G
         ref = oracle.sdpa(qh[b:b + 1, h:h + 1, i:i + 1], kh[b:b + 1, hk:hk + 1, :i + 1],
                           vh[b:b + 1, hk:hk + 1, :i + 1])
         err = float(np.max(np.abs(out[b, h, i] - ref[0, 0, 0])))
+        worst = max(worst, err)
         assert err < BF16_ATOL, (b, h, i, err)
+    print(f"C3 max abs error {worst:.4g}")
     for t in (q, k, v):
         t.dispose()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_bf16_growing_scores_raise_reference(hip, causal):
+    """Keys whose norms grow along the sequence (x1 .. x4), so the scores of later key chunks
+    exceed every earlier row maximum by far: the softmax reference is raised in the middle of the
+    key loop (not only on the first chunk), GQA 2, ragged S."""
+    B, Hq, Hkv, S, D = 1, 8, 4, 1000, 128
+    q, qh = seeded(101, (B, Hq, S, D), "bfloat16")
+    kraw = syn.normal(102, (B, Hkv, S, D)) * (1.0 + 3.0 * np.arange(S) / S)[None, None, :, None]
+    kbits, kh = syn.bf16(kraw.astype(np.float32))
+    k = Tensor(kbits, dtype="bfloat16")
+    v, vh = seeded(103, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, causal)
+    ref = oracle.sdpa(qh, kh, vh, causal=causal)
+    err = float(np.max(np.abs(out - ref)))
+    assert err < BF16_ATOL, err
+
+
+def test_flash_bf16_wide_score_range(hip):
+    """q, k ~ N(0, 2^2): scores span about +-40 natural-log units, so exponentials relative to the
+    first chunk's maximum overflow float32 unless the reference is raised; peaked softmax rows."""
+    B, Hq, Hkv, S, D = 1, 4, 2, 700, 128
+    q, qh = seeded(111, (B, Hq, S, D), "bfloat16", std=2.0)
+    k, kh = seeded(112, (B, Hkv, S, D), "bfloat16", std=2.0)
+    v, vh = seeded(113, (B, Hkv, S, D), "bfloat16")
+    for causal in (True, False):
+        out = _sdpa_gpu(q, k, v, causal)
+        assert np.all(np.isfinite(out))
+        err = float(np.max(np.abs(out - oracle.sdpa(qh, kh, vh, causal=causal))))
+        assert err < BF16_ATOL, (causal, err)
+
+
+def test_flash_bf16_negative_scale(hip):
+    """A negative scale (scores multiplied by -0.05) takes the generic kernel and matches the oracle."""
+    q, qh = seeded(121, (1, 4, 200, 128), "bfloat16")
+    k, kh = seeded(122, (1, 2, 200, 128), "bfloat16")
+    v, vh = seeded(123, (1, 2, 200, 128), "bfloat16")
+    for causal in (True, False):
+        out = _sdpa_gpu(q, k, v, causal, scale=-0.05)
+        err = float(np.max(np.abs(out - oracle.sdpa(qh, kh, vh, scale=-0.05, causal=causal))))
+        assert err < BF16_ATOL, (causal, err)
+
+
+def test_flash_bf16_gqa8_c3_shape(hip):
+    """GQA ratio 8 (Hq=16, Hkv=2) at S=2048 through the MFMA kernel (one query head per wave)."""
+    B, Hq, Hkv, S, D = 1, 16, 2, 2048, 128
+    q, qh = seeded(131, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(132, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(133, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    for h in (0, 7, 8, 15):
+        ref = oracle.sdpa(qh[:, h:h + 1], kh[:, h // 8:h // 8 + 1], vh[:, h // 8:h // 8 + 1], causal=True)
+        err = float(np.max(np.abs(out[:, h:h + 1] - ref)))
+        assert err < BF16_ATOL, (h, err)
 
 
 def test_flash_rejects_bad_gqa(hip):

@@ -1,7 +1,8 @@
 """GPU parity of the Qwen3 causal-LM path (config C5) against the CPU oracle.
 
 Bar: greedy token ids identical for the first 32 decode steps of the full Qwen3-0.6B architecture
-(random N(0, 0.02) bf16 weights, 512-token prompt); last-position fp32 logits within 2e-2 absolute.
+(random N(0, 0.02) bf16 weights, 512-token prompt); the fp32 logits each token is chosen from (the
+prefill's last position and every decode step) within 2e-2 absolute.
 """
 import numpy as np
 import pytest
@@ -66,12 +67,19 @@ def test_qwen3_0p6b_greedy_32_steps(hip):
     512-token prefill of uniform-random ids, then greedy decoding compared for 32 steps."""
     cfg = Qwen3Config()
     toks, logits, rtoks, rlogits = _run(cfg, seed=7, prompt_len=512, steps=32, max_seq=1024)
-    err0 = float(np.max(np.abs(logits[0] - rlogits[0])))
-    print(f"\nprefill logits max abs err {err0:.3e}; top-2 margins (oracle) "
-          f"{[round(_margin(r), 4) for r in rlogits[:8]]}", flush=True)
-    assert err0 < LOGIT_ATOL
+    assert len(logits) == len(rlogits) == 33   # the prefill's last position, then one per decode step
+    errs = [float(np.max(np.abs(g - r))) for g, r in zip(logits, rlogits)]
+    margins = [_margin(r) for r in rlogits]
+    print("\nstep  max|dlogit|  top-2 margin (oracle)  token gpu / oracle")
+    for i, (e, mg) in enumerate(zip(errs, margins)):
+        tg = toks[i] if i < len(toks) else None
+        tr = rtoks[i] if i < len(rtoks) else None
+        print(f"{i:4d}  {e:.4e}   {mg:.4f}   {tg} / {tr}", flush=True)
+    print(f"max logit error {max(errs):.4e}; smallest top-2 margin {min(margins):.4f}", flush=True)
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, rtoks)) if a != b), None)
-    assert first_diff is None, (first_diff, toks[first_diff], rtoks[first_diff], _margin(rlogits[first_diff]))
+    assert first_diff is None, (first_diff, toks[first_diff], rtoks[first_diff], margins[first_diff])
+    worst = int(np.argmax(errs))
+    assert errs[worst] < LOGIT_ATOL, (worst, errs[worst])
 
 
 def test_from_pretrained_sharded_checkpoint_matches_in_memory(hip, tmp_path):

@@ -264,6 +264,25 @@ def test_argmax_tie_and_nan_rules():
     assert list(oracle.argmax(x)) == [1, 1, 0]
 
 
+def test_argmax_tie_rule_differs_from_the_reference_kernel_only_on_ties():
+    """The oracle (and the GPU kernel) return the lowest index among tied maxima; the reference's
+    WGSL argmax, simulated thread by thread (oracle.argmax_workgroup_rule), depends on the
+    workgroup size on ties: W = 4 with maxima at 1 and 2 gives 2, W = 256 with maxima at 1 and 256
+    gives 256.  Without ties both rules agree (random rows, several workgroup sizes), and NaN /
+    all -inf rows agree."""
+    t4 = np.array([0.0, 5.0, 5.0, 1.0], np.float32)
+    assert oracle.argmax(t4[None])[0] == 1 and oracle.argmax_workgroup_rule(t4, 4) == 2
+    t = np.zeros(300, np.float32)
+    t[1] = t[256] = 7.0
+    assert oracle.argmax(t[None])[0] == 1 and oracle.argmax_workgroup_rule(t, 256) == 256
+    rng = np.random.default_rng(3)
+    rows = rng.normal(size=(6, 777)).astype(np.float32)
+    for wg in (4, 64, 256):
+        np.testing.assert_array_equal(oracle.argmax_workgroup_rule(rows, wg), oracle.argmax(rows))
+    special = np.array([[np.nan, 1.0, np.nan, 0.5], [-np.inf] * 4], np.float32)
+    np.testing.assert_array_equal(oracle.argmax_workgroup_rule(special, 4), oracle.argmax(special))
+
+
 # ---------------------------------------------------------------------------------------- Qwen3 composition
 def test_qwen3_oracle_matches_transformers_float32():
     """The model oracle without its bf16 rounding points reproduces Hugging Face transformers'
