@@ -572,6 +572,24 @@ def measured_traffic(workload):
         return None
 
 
+def _node_version():
+    import subprocess
+    try:
+        return subprocess.run(["node", "--version"], capture_output=True, text=True, timeout=30).stdout.strip()
+    except (OSError, subprocess.SubprocessError):
+        return "?"
+
+
+def _one_thread():
+    """Context that limits numpy's BLAS to one thread (the CPU baselines state cores = 1)."""
+    try:
+        from threadpoolctl import threadpool_limits
+        return threadpool_limits(1)
+    except ImportError:  # pragma: no cover
+        import contextlib
+        return contextlib.nullcontext()
+
+
 JS_REPEAT = 5   # timed runs of each JavaScript baseline after one untimed run; the median is reported
 
 

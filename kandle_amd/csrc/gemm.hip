@@ -53,28 +53,15 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 // B-operand = A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are
 // raw buffer loads (rows past M / N and columns past the k range read as zero without a branch).
 //
-// SPLIT: S workgroups share one output tile, each summing K / S of the products.  Each writes its
-// fp32 accumulators to a workspace and counts itself in a library counter; the last one adds the S
-// partials in split order (deterministic whichever finishes last), applies the epilogue and resets
-// the counter to zero.
+// SPLIT: S workgroups share one output tile, each summing K / S of the products into fp32
+// partials of its own; gemm_splitk_reduce_kernel then adds the S partials in split order
+// (deterministic whichever workgroup finished last) and applies the epilogue.
 // =============================================================================================
 constexpr int G_THREADS = 256;
-#ifndef KH_GEMM_PREFETCH
-#define KH_GEMM_PREFETCH 3
-#endif
-constexpr int kGemmPrefetch = KH_GEMM_PREFETCH;   // k-steps of global loads in flight per workgroup
-#ifndef KH_GEMM_T128_MIN
-#define KH_GEMM_T128_MIN 256
-#endif
-#ifndef KH_GEMM_SPLIT128
-#define KH_GEMM_SPLIT128 0
-#endif
-constexpr int kGemmT128Min = KH_GEMM_T128_MIN;   // 128-tiles from this many tiles up
-#ifndef KH_GEMM_SPLIT_TARGET
-#define KH_GEMM_SPLIT_TARGET 512
-#endif
-constexpr int kGemmSplitTarget = KH_GEMM_SPLIT_TARGET;   // split K until about this many workgroups
-constexpr bool kGemmSplit128 = KH_GEMM_SPLIT128;
+constexpr int kGemmPrefetch = 3;        // k-steps of global loads in flight per workgroup
+constexpr int kGemmT128Min = 256;       // 128-tiles from this many tiles up
+constexpr int kGemmSplitTarget = 512;   // split K until about this many workgroups
+constexpr bool kGemmSplit128 = false;   // 128-tiles are never split
 constexpr int kMaxSplits = 8;
 constexpr int g_tile(int wt) { return 64 * wt; }
 

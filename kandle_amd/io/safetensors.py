@@ -21,6 +21,7 @@ from __future__ import annotations
 import json
 import mmap
 import os
+import struct
 from dataclasses import dataclass, field
 from typing import Dict, Iterator, Optional, Tuple
 
@@ -45,26 +46,46 @@ SAFETENSORS_DTYPES: Dict[str, Tuple[int, np.dtype, str]] = {
     "BOOL": (1, np.dtype("u1"), "bool"),
 }
 
-MAX_HEADER_SIZE = 100 * 1024 * 1024   # parser.ts:41-44
+# The format caps the JSON header at 100 MB (a guard against hostile length fields).
+MAX_HEADER_SIZE = 100 * 1024 * 1024
+_LEN_FIELD = struct.Struct("<Q")
 
 
 def parse_header_size(first8: bytes) -> int:
-    """Header length from the first 8 bytes (u64 LE); rejects lengths past 2^32 or 100 MB
-    (parser.ts:28-47)."""
-    if len(first8) < 8:
-        raise ValueError("Invalid safetensors: file too small to contain header size")
-    low = int.from_bytes(first8[0:4], "little")
-    high = int.from_bytes(first8[4:8], "little")
-    if high != 0:
-        raise ValueError(f"Header size too large: exceeds safe integer limit (high bytes: {high})")
-    if low > MAX_HEADER_SIZE:
-        raise ValueError(f"Header size exceeds safe limit: {low} bytes (max: {MAX_HEADER_SIZE})")
-    return low
+    """Byte length of the JSON header: the file's first 8 bytes as an unsigned little-endian 64-bit
+    integer, at most MAX_HEADER_SIZE."""
+    if len(first8) < _LEN_FIELD.size:
+        raise ValueError(f"safetensors: {len(first8)} bytes where the 8-byte header length belongs (file too small)")
+    (n,) = _LEN_FIELD.unpack_from(first8)
+    if n > MAX_HEADER_SIZE:
+        raise ValueError(f"safetensors: header length {n} bytes exceeds the format's cap of {MAX_HEADER_SIZE} bytes")
+    return n
 
 
-def _is_tensor_entry(entry) -> bool:
-    return (isinstance(entry, dict) and isinstance(entry.get("dtype"), str) and isinstance(entry.get("shape"), list)
-            and isinstance(entry.get("data_offsets"), list) and len(entry["data_offsets"]) == 2)
+def _tensor_entry(name: str, entry, data_size: int):
+    """(dtype, shape, (begin, end)) of a header entry describing a tensor, checked against the
+    format: a known dtype, non-negative integer dims, and a byte range [begin, end) inside the data
+    area holding exactly numel * element-size bytes.  None for entries that describe no tensor
+    (anything but an object with data_offsets), which are ignored like the reference ignores them."""
+    if not isinstance(entry, dict) or "data_offsets" not in entry:
+        return None
+    st, shape, offs = entry.get("dtype"), entry.get("shape"), entry["data_offsets"]
+    if not isinstance(st, str) or st not in SAFETENSORS_DTYPES:
+        raise ValueError(f"safetensors: tensor {name!r} has dtype {st!r}, which this loader does not read "
+                         f"(it reads {', '.join(SAFETENSORS_DTYPES)})")
+    if not isinstance(shape, list) or not all(isinstance(d, int) and d >= 0 for d in shape):
+        raise ValueError(f"safetensors: tensor {name!r} has shape {shape!r}; a shape is a list of dims >= 0")
+    if not (isinstance(offs, list) and len(offs) == 2 and all(isinstance(o, int) and o >= 0 for o in offs)):
+        raise ValueError(f"safetensors: tensor {name!r} has data_offsets {offs!r}; they are [begin, end] byte offsets")
+    begin, end = offs
+    need = int(np.prod(shape, dtype=np.int64)) * SAFETENSORS_DTYPES[st][0]
+    if end - begin != need:
+        raise ValueError(f"safetensors: tensor {name!r} ({st}, shape {tuple(shape)}) needs {need} bytes but its "
+                         f"data_offsets span {end - begin}")
+    if end > data_size:
+        raise ValueError(f"safetensors: tensor {name!r} occupies bytes [{begin}, {end}) of a {data_size}-byte "
+                         f"data area (the file is truncated or the offsets are wrong)")
+    return st, tuple(shape), (begin, end)
 
 
 @dataclass
@@ -122,41 +143,33 @@ class SafetensorFile:
 
 
 def parse_safetensor_file(path: str) -> SafetensorFile:
-    """Parse the header of one .safetensors file (parser.ts:89-172): header size, JSON, metadata, and
-    for every tensor entry a known dtype and a byte range of exactly numel * element size inside the
-    file.  No tensor bytes are read."""
+    """Reads the header of one .safetensors file (the reference's parser: parser.ts:89-172): the
+    8-byte length, the JSON object, its __metadata__ string map, and every tensor entry checked by
+    _tensor_entry.  No tensor bytes are read."""
     file_size = os.path.getsize(path)
     with open(path, "rb") as fh:
-        header_size = parse_header_size(fh.read(8))
-        if header_size == 0:
-            raise ValueError("Invalid safetensors: header size is 0")
-        raw = fh.read(header_size)
-    if len(raw) < header_size:
-        raise ValueError("Invalid safetensors: header data incomplete")
+        n = parse_header_size(fh.read(_LEN_FIELD.size))
+        if n == 0:
+            raise ValueError("safetensors: empty header (length 0)")
+        raw = fh.read(n)
+    if len(raw) != n:
+        raise ValueError(f"safetensors: the header announces {n} bytes but the file holds {len(raw)} after the "
+                         f"length field (incomplete)")
     try:
         header = json.loads(raw.decode("utf-8"))
     except (UnicodeDecodeError, json.JSONDecodeError) as e:
-        raise ValueError(f"Invalid JSON in safetensors header: {e}") from None
+        raise ValueError(f"safetensors: the header is not valid UTF-8 JSON ({e})") from None
     if not isinstance(header, dict):
-        raise ValueError("Invalid JSON in safetensors header: not an object")
-    meta = header.get("__metadata__") or {}
-    f = SafetensorFile(path=path, metadata={str(k): str(v) for k, v in meta.items()}, data_offset=8 + header_size)
+        raise ValueError(f"safetensors: the header is JSON {type(header).__name__}, not an object")
+    meta = header.pop("__metadata__", None) or {}
+    f = SafetensorFile(path=path, metadata={str(k): str(v) for k, v in meta.items()},
+                       data_offset=_LEN_FIELD.size + n)
     data_size = file_size - f.data_offset
     for name, entry in header.items():
-        if name == "__metadata__" or not _is_tensor_entry(entry):
-            continue
-        st = entry["dtype"]
-        if st not in SAFETENSORS_DTYPES:
-            raise ValueError(f"Unsupported safetensors dtype: {st}")
-        shape = tuple(int(d) for d in entry["shape"])
-        numel = int(np.prod(shape)) if shape else 1
-        b0, b1 = (int(x) for x in entry["data_offsets"])
-        expected = numel * SAFETENSORS_DTYPES[st][0]
-        if numel > 0 and b1 - b0 != expected:
-            raise ValueError(f"Data size mismatch for {name}: expected {expected} bytes, got {b1 - b0} bytes")
-        if b0 < 0 or b1 < b0 or b1 > data_size:
-            raise ValueError(f"Data range of {name} [{b0}, {b1}) lies outside the file's {data_size}-byte data area")
-        f.layers[name] = SafetensorLayer(name, st, SAFETENSORS_DTYPES[st][2], shape, f, (b0, b1))
+        t = _tensor_entry(name, entry, data_size)
+        if t is not None:
+            st, shape, rng = t
+            f.layers[name] = SafetensorLayer(name, st, SAFETENSORS_DTYPES[st][2], shape, f, rng)
     return f
 
 

@@ -23,6 +23,7 @@ read fp32 x and write bf16 h); math inside kernels is fp32.
 from __future__ import annotations
 
 import time
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
@@ -31,6 +32,7 @@ import numpy as np
 from .. import env
 from .. import functional as F
 from .. import synthetic as syn
+from .._lib import KandleHipError
 from ..graphs import HipGraph
 from ..kernels import TensorIterator
 from ..tensor import HipTensorHandle, Tensor
@@ -187,7 +189,11 @@ class Qwen3ForCausalLM:
         self.rope = RotaryEmbedding(cfg.head_dim, cfg.rope_theta)
         self.cache = StaticKVCache(cfg.num_hidden_layers, 1, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
         self.scale = 1.0 / np.sqrt(cfg.head_dim)
-        self._prefill_graphs: Dict[int, tuple] = {}   # prompt length -> (graph, ids, positions, logits)
+        # prompt length -> (graph, ids, positions, logits), least recently used first.  Each captured
+        # prefill keeps its activations (sized by the prompt length) in the graph's private pool, so
+        # at most max_prefill_graphs lengths are kept; the least recently used is disposed first.
+        self._prefill_graphs: "OrderedDict[int, tuple]" = OrderedDict()
+        self.max_prefill_graphs = 4
         # Decode steps run each layer's attention block (qk-norm, RoPE, K/V write, attention, o_proj)
         # as one library call; False runs the separate launches (the prefill's path at S = 1).
         self.fused_decode = True
@@ -342,13 +348,27 @@ class Qwen3ForCausalLM:
         entry = self._prefill_graphs.get(S)
         if entry is None:
             logits = self.forward(prompt_ids, 0)
+            if self.max_prefill_graphs < 1:
+                return logits, True
+            while len(self._prefill_graphs) >= self.max_prefill_graphs:
+                self._dispose_prefill_graph(next(iter(self._prefill_graphs)))
             ids_buf = Tensor(np.zeros(S, np.int32), dtype="int32")
             pos_buf = RotaryEmbedding.get_position_ids(S, 0)
             graph = HipGraph()
-            with graph.capture():
-                g_logits = self._forward_dev(ids_buf, pos_buf, S)
+            try:
+                with graph.capture():
+                    g_logits = self._forward_dev(ids_buf, pos_buf, S)
+            except KandleHipError:
+                # e.g. device memory exhausted inside the capture (where the allocator cannot empty
+                # its cache): drop every captured prefill and keep this prompt's eager result
+                ids_buf.dispose()
+                pos_buf.dispose()
+                for key in list(self._prefill_graphs):
+                    self._dispose_prefill_graph(key)
+                return logits, True
             self._prefill_graphs[S] = (graph, ids_buf, pos_buf, g_logits)
             return logits, True
+        self._prefill_graphs.move_to_end(S)
         graph, ids_buf, _, g_logits = entry
         ids_buf.handle.storage.upload(np.ascontiguousarray(prompt_ids, dtype=np.int32))
         graph.replay()
@@ -524,13 +544,16 @@ class Qwen3ForCausalLM:
             for t in (ids, pos, lens, ctr, state):
                 t.dispose()
 
+    def _dispose_prefill_graph(self, length: int) -> None:
+        graph, ids_buf, pos_buf, g_logits = self._prefill_graphs.pop(length)
+        g_logits.dispose()
+        graph.dispose()
+        ids_buf.dispose()
+        pos_buf.dispose()
+
     def dispose(self) -> None:
-        for graph, ids_buf, pos_buf, g_logits in self._prefill_graphs.values():
-            g_logits.dispose()
-            graph.dispose()
-            ids_buf.dispose()
-            pos_buf.dispose()
-        self._prefill_graphs = {}
+        for key in list(self._prefill_graphs):
+            self._dispose_prefill_graph(key)
         self.cache.dispose()
         heads = [self.lm_head] if self.lm_head is not self.embed else []
         for t in [self.embed, self.final_norm] + heads + [v for L in self.layers for v in L.values()]:

@@ -150,3 +150,31 @@ def test_fused_decode_block_matches_unfused_and_oracle(hip):
             assert float(np.max(np.abs(fl[i] - ul[i]))) < 5e-3, (max_seq, i)
             assert float(np.max(np.abs(fl[i] - rl[i]))) < LOGIT_ATOL, (max_seq, i)
         assert ft == ut == rt, max_seq
+
+
+def test_prefill_graphs_bounded_lru(hip):
+    """Prompts of six lengths with max_prefill_graphs = 2: at most two captured prefills are kept
+    (least recently used disposed), device memory held by the allocator stays bounded instead of
+    growing with every new length, and a length seen again (replayed from its graph) gives the
+    same tokens as its eager run."""
+    from kandle_amd import _lib
+
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
+    w = init_qwen3_weights(cfg, seed=31)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=256)
+    model.max_prefill_graphs = 2
+    held = []
+    first = {}
+    for S in (40, 90, 140, 60, 120, 100, 100):
+        prompt = syn.randint(S, (S,), 0, cfg.vocab_size)
+        toks = model.generate(prompt, 3)
+        first.setdefault(S, toks)
+        assert toks == first[S], S
+        assert len(model._prefill_graphs) <= 2
+        st = _lib.alloc_stats()
+        held.append(st["live_bytes"] + st["cached_bytes"])
+    model.dispose()
+    assert list(model._prefill_graphs) == []
+    # after the pool of two is full (third prompt on), memory may not grow past its early peak by
+    # more than one prompt's activations
+    assert max(held[3:]) <= max(held[:3]) * 1.25, held
