@@ -273,6 +273,18 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                         const int32_t* seq_lens, int batch, int hq, int hkv, int d, int64_t max_len,
                         const int64_t* strides, float scale, int dtype);
 
+/* kh_decode_attention without any device allocation: the same arguments, kernels and results,
+ * with the split-K partials in a file-scope device array of 16 MiB (one per GPU, held until the
+ * process ends, its address taken once at kh_init) instead of the caching allocator.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory during the
+ * call (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Limit: batch * hq * ceil(max_len / 256) * 520 bytes (bf16; ceil(max_len / 64) for f32) must not
+ * exceed 16 MiB (e.g. 8 sequences x 16 heads up to max_len 32768), else KH_ERR_INVALID.  All calls
+ * on one GPU share the array: calls that overlap on one GPU (from another stream) race. */
+int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
+                                const int32_t* seq_lens, int batch, int hq, int hkv, int d, int64_t max_len,
+                                const int64_t* strides, float scale, int dtype);
+
 /* C[m, n] = alpha * sum_k A[m, k] * B'[k, n] + beta * Cin[m, n] (+ bias[n]), fp32 accumulate,
  * where B' = B^T with B stored [n, k] (trans_b = 1, the nn.Linear weight layout) or B' = B stored
  * [k, n] (trans_b = 0).  A and B have `dtype`; C, Cin and bias have `out_dtype` (bf16 inputs may

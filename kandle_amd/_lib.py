@@ -71,6 +71,7 @@ SIGNATURES = {
     "kh_flash_attention": [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i64p, _f, _i, _i],
     "kh_flash_attention_masked": [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i64p, _f, _vp, _i64p, _i, _i],
     "kh_decode_attention": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
+    "kh_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
     "kh_gemm": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _f, _f, _i, _i, _i],
     "kh_gemv_fused": [_i, _vp, _vp, _vp, _f, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _f, _f, _i],
 }

@@ -628,6 +628,19 @@ __global__ __launch_bounds__(256) void decode_merge_cols_pos_kernel(const float*
   decode_merge_cols_body<uint16_t>(part, L, hq, max_chunks, st, O);
 }
 
+// ---- scratch of the allocation-free decode entry point (kh_decode_attention_noalloc) ----------
+// The split-K partials of one call live in this file-scope device array instead of the caching
+// allocator.  Every GPU the library runs on holds its own copy until the process ends; host code
+// uses only the device address hipGetSymbolAddress returns for it (the array's name is a
+// host-side stand-in, not a device address).  Calls on one GPU share the array, so calls that
+// overlap on one GPU (another thread's stream) race; on the library's single stream they are
+// ordered.  Nothing in it needs to start at zero: the merge reads only the chunks this call's
+// partial kernel wrote.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 AttnStrides load_strides(const int64_t* s) {
   AttnStrides a;
   a.qb = s[0]; a.qh = s[1]; a.qs = s[2];
@@ -717,6 +730,21 @@ int launch_generic(const void* q, const void* k, const void* v, void* o, int bat
 }
 
 }  // namespace
+
+namespace kh {
+
+// Called by kh_init with `device` current: records this GPU's address of the scratch array.
+int attention_init(int device) {
+  KH_REQUIRE(device >= 0 && device < kMaxDevices, "kh_init: device %d beyond the %d the library tracks", device,
+             kMaxDevices);
+  void* ptr = nullptr;
+  KH_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  KH_REQUIRE(ptr != nullptr, "kh_init: no device address for the decode scratch array");
+  g_scratch_ptr[device] = ptr;
+  return KH_OK;
+}
+
+}  // namespace kh
 
 extern "C" {
 
@@ -850,6 +878,43 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   if (dtype == KH_BF16)
     return launch_decode<uint16_t>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
   return launch_decode<float>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
+}
+
+int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
+                                const int32_t* seq_lens, int batch, int hq, int hkv, int d, int64_t max_len,
+                                const int64_t* strides, float scale, int dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(batch >= 0 && hq > 0 && hkv > 0 && max_len > 0, "kh_decode_attention_noalloc: bad extents");
+  KH_REQUIRE(hq % hkv == 0, "kh_decode_attention_noalloc: numHeadsQ (%d) must be divisible by numHeadsKV (%d)", hq,
+             hkv);
+  KH_REQUIRE(d == 128, "kh_decode_attention_noalloc: head_dim %d not supported (128 only)", d);
+  KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_decode_attention_noalloc: unsupported dtype %d", dtype);
+  KH_REQUIRE(max_len <= INT32_MAX, "kh_decode_attention_noalloc: max_len too large");
+  if (batch == 0) return KH_OK;
+  KH_REQUIRE(batch <= 65535, "kh_decode_attention_noalloc: batch too large");
+  KH_REQUIRE(q && k_cache && v_cache && o && seq_lens && strides, "kh_decode_attention_noalloc: null pointer");
+  const size_t need = dtype == KH_BF16 ? decode_part_bytes<uint16_t>(batch, hq, max_len)
+                                       : decode_part_bytes<float>(batch, hq, max_len);
+  KH_REQUIRE(need <= kNoAllocScratchBytes,
+             "kh_decode_attention_noalloc: batch %d x %d heads x %lld keys needs %zu bytes of split-K partials, "
+             "more than the %zu-byte scratch array (use kh_decode_attention)",
+             batch, hq, (long long)max_len, need, kNoAllocScratchBytes);
+  const int dev = current_device();
+  KH_REQUIRE(dev >= 0 && dev < kMaxDevices && g_scratch_ptr[dev] != nullptr,
+             "kh_decode_attention_noalloc: the scratch array of device %d has no address (kh_init)", dev);
+  AttnStrides st{};
+  st.qb = strides[0]; st.qh = strides[1]; st.qs = 0;
+  st.kb = strides[2]; st.kh = strides[3]; st.ks = strides[4];
+  st.vb = strides[5]; st.vh = strides[6]; st.vs = strides[7];
+  st.ob = strides[8]; st.oh = strides[9]; st.os = 0;
+  const int64_t vec = dtype == KH_BF16 ? 8 : 4;
+  KH_REQUIRE(aligned16(k_cache) && aligned16(v_cache) && st.kb % vec == 0 && st.kh % vec == 0 && st.ks % vec == 0 &&
+                 st.vb % vec == 0 && st.vh % vec == 0 && st.vs % vec == 0,
+             "kh_decode_attention_noalloc: caches must be 16-byte aligned with 16-byte aligned strides");
+  float* part = (float*)g_scratch_ptr[dev];
+  if (dtype == KH_BF16)
+    return launch_decode<uint16_t>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale, part);
+  return launch_decode<float>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale, part);
 }
 
 int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,

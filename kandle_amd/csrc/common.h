@@ -13,6 +13,8 @@ void set_error(const char* fmt, ...);
 void clear_error();
 hipStream_t stream();  // the library stream; nullptr before kh_init
 bool initialized();
+int current_device();  // the device kh_init selected (-1 before)
+int attention_init(int device);  // kh_init's set-up of attention.hip (device current)
 
 // Internal scratch allocation through the caching allocator (stream-ordered on the library stream).
 void* scratch_alloc(size_t bytes);

@@ -178,6 +178,7 @@ void set_error(const char* fmt, ...) {
 void clear_error() { g_err[0] = 0; }
 hipStream_t stream() { return g_state.stream; }
 bool initialized() { return g_state.init; }
+int current_device() { return g_state.init ? g_state.device : -1; }
 
 void* scratch_alloc(size_t bytes) {
   void* p = nullptr;
@@ -220,6 +221,8 @@ int kh_init(int device) {
     return KH_ERR_INVALID;
   }
   KH_CHECK_HIP(hipSetDevice(device));
+  const int rc = attention_init(device);
+  if (rc != KH_OK) return rc;
   KH_CHECK_HIP(hipStreamCreateWithFlags(&g_state.stream, hipStreamNonBlocking));
   g_state.device = device;
   g_state.init = true;
