@@ -141,6 +141,14 @@ int kh_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64
 int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64_t n_idx, int64_t row_elems,
                     void* out, int dtype, int out_dtype);
 
+/* index_select along any axis: a contiguous table viewed as [outer, n_rows, inner] (the axis of
+ * length n_rows selected), out [outer, n_idx, inner] with out[a, i, :] = table[a, idx[i], :]; an id
+ * outside [0, n_rows) yields zeros.  dtypes as kh_index_select.  Replaces the gather kernel's
+ * index_select for every dim (reference: packages/core/src/dispatch/handlers/gather.ts:121,190;
+ * packages/backend-webgpu/src/kernels/gather/index.ts:14-23). */
+int kh_index_select_dim(const void* table, int64_t outer, int64_t n_rows, int64_t inner, const int32_t* idx,
+                        int64_t n_idx, void* out, int dtype, int out_dtype);
+
 /* out[r] = the lowest index of the maximum of row r (rows x n, contiguous), int32.
  * Replaces argmax (reference: packages/backend-webgpu/src/kernels/reduction/argShaderBuilder.ts:205-240)
  * with the greedy tie rule of sample() (packages/model-utils/src/sampling/index.ts:132,138). */
@@ -297,6 +305,18 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
             const void* cin, int64_t ldcin, const void* bias,
             int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b, int dtype, int out_dtype);
 
+/* h[m, f] = silu(g[m, f]) * u[m, f], g = x W_gate^T and u = x W_up^T (bf16 in, fp32 accumulate,
+ * g and u rounded to bf16 before the product and h rounded to bf16: the values the separate GEMM
+ * and silu*mul produce), for m rows and n_half = intermediate features, from ONE weight w_gu
+ * [2 n_half, k] whose rows interleave gate and up in blocks of 8: rows 16i .. 16i+7 are gate rows
+ * 8i .. 8i+7 and rows 16i+8 .. 16i+15 the matching up rows.  x [m, k] and h [m, n_half] with row
+ * strides ldx / ldh (elements); n_half, k, ldx, ldw multiples of 8; x and w_gu 16-byte aligned.
+ * The [m, 2 n_half] gate/up intermediate is never written.  Fuses SwiGLUMLP's gate and up
+ * projections with silu and mul (reference: packages/model-utils/src/mlp/swiglu.ts:119-134;
+ * packages/backend-webgpu/src/kernels/pointwise/ops.ts:299 silu, :329 mul). */
+int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,
+                   int64_t n_half, int64_t k);
+
 /* One-row projection (decode) with the producing op fused in front of it:
  *   c[j] = alpha * sum_i x'[i] * w[j, i] + beta * cin[j] (+ bias[j]),  j < n, i < k,
  * w bf16 [n, k] with row stride ldw (the nn.Linear weight), c/cin/bias of out_dtype, where x' is
@@ -306,7 +326,10 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
  *               — RMSNorm then linear (reference: packages/core/src/nn/modules/normalization/RMSNorm.ts:92-99;
  *               packages/model-utils/src/qwen3/decoder_layer.ts:191-241);
  *   prologue 2: x' = silu(x) * x2 with x, x2 bf16 [k] (gate and up) — the SwiGLU product then
- *               down_proj (reference: packages/model-utils/src/mlp/swiglu.ts:119-134).
+ *               down_proj (reference: packages/model-utils/src/mlp/swiglu.ts:119-134);
+ *   prologue 3: x'[i] = silu(x[16(i/8) + i%8]) * x[16(i/8) + 8 + i%8] with x bf16 [2k] — the same
+ *               product read from the output of a gate/up projection whose weight interleaves gate
+ *               and up rows in blocks of 8 (kh_gemm_swiglu's layout; k % 8 == 0).
  * Needs k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w and k <= 16384.  cin may alias c. */
 int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps,
                   const void* w, int64_t ldw, void* c, const void* cin, const void* bias,

@@ -52,6 +52,7 @@ SIGNATURES = {
     "kh_silu": [_vp, _vp, _i64, _i],
     "kh_silu_mul": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i],
     "kh_index_select": [_vp, _i64, _vp, _i64, _i64, _vp, _i, _i],
+    "kh_index_select_dim": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i, _i],
     "kh_argmax": [_vp, _i64, _i64, _vp, _i],
     "kh_rms_norm": [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _f, _i, _i],
     "kh_qk_norm_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i, _i, _i, _i64p, _f, _i,
@@ -74,6 +75,7 @@ SIGNATURES = {
     "kh_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
     "kh_gemm": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _f, _f, _i, _i, _i],
     "kh_gemv_fused": [_i, _vp, _vp, _vp, _f, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _f, _f, _i],
+    "kh_gemm_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64],
 }
 
 _lib = None

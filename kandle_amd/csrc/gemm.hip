@@ -70,7 +70,12 @@ constexpr int g_tile(int wt) { return 64 * wt; }
 // row) and, when the workgroup count is a multiple of 8, dealt to the 8 XCDs in contiguous ranges
 // (the hardware hands workgroup i to XCD i mod 8): each XCD then reads its own columns of B (the
 // weights) into its L2, and only A (the activations) is read by every XCD.
-template <typename TO, int WT, int KS, bool SPLIT, int PF = 1>
+// SWIGLU (bf16 output, no split): B's rows interleave the gate and up projections in blocks of 8
+// (rows 16i .. 16i + 7: gate rows 8i .. 8i + 7; rows 16i + 8 .. 16i + 15: the matching up rows), so
+// every lane holds each gate accumulator and its up partner, and the epilogue stores
+// C[m, f] = bf16(silu(bf16(gate)) * bf16(up)) over N / 2 features f -- the values the separate
+// GEMM (bf16 store) and silu*mul kernel produce, without the [M, N] intermediate.
+template <typename TO, int WT, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
@@ -196,6 +201,29 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 
   // Epilogue: acc[a][b] lane holds m = m0 + wm + 32b + r, n = n0 + wn + 32a + 8(j/4) + 4g + j%4.
   const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
+  if constexpr (SWIGLU) {
+    // Register groups q = 0, 2 hold gate rows n0 + wn + 32a + 8q + 4g + e, q + 1 the up rows 8 later:
+    // feature f = (n0 + wn + 32a) / 2 + 4q + 4g + e (q = 0, 2).  N / 2 is a multiple of 8.
+    const int NH = N / 2;
+#pragma unroll
+    for (int b = 0; b < WT; ++b) {
+      const int m = m0 + wm + 32 * b + r;
+      if (m >= M) continue;
+#pragma unroll
+      for (int a = 0; a < WT; ++a)
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+          const int f = (n0 + wn + 32 * a) / 2 + 4 * q + 4 * g;
+          if (f >= NH) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = silu_ref(round_bf16(acc[a][b][4 * q + e])) * round_bf16(acc[a][b][4 * q + 4 + e]);
+          store4<TO>(C, (int64_t)m * ldc + f, v, vec, 4);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int b = 0; b < WT; ++b) {
     const int m = m0 + wm + 32 * b + r;
@@ -347,13 +375,15 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
 //   PRO_NONE      x' = x                               (x bf16)
 //   PRO_RMSNORM   x' = bf16(rms_norm(x, norm_w, eps))  (x fp32 residual row, norm_w bf16)
 //   PRO_SILU_MUL  x' = bf16(silu(x) * x2)              (x, x2 bf16: gate and up halves)
+//   PRO_SILU_MUL_IL x'[i] = bf16(silu(x[16(i/8) + i%8]) * x[16(i/8) + 8 + i%8])  (x bf16 [2k]: the
+//                 gate/up row of a projection whose weight interleaves gate and up rows in blocks of 8)
 //   PRO_ATTN_MERGE x' = bf16(split-K decode attention merged)  (x: the fp32 partials of one sequence,
 //                 o[h][chunk][128] then (m, l)[h][chunk]; see AttnMerge)
 // Each workgroup forms x' once in LDS (fp32, zero past k); each wave then owns U weight rows and
 // streams them with raw 16-byte buffer loads, CB chunks of 512 columns per row in flight (rows past
 // n read as zero), and reduces each row across the wave.  Every weight byte is read once.
 // =============================================================================================
-constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2, PRO_ATTN_MERGE = 3;
+constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2, PRO_SILU_MUL_IL = 3, PRO_ATTN_MERGE = 4;
 constexpr int kAttnMergeMaxChunks = 8;   // split-K chunks the attention-merge prologue accepts
 constexpr int GV_CHUNK = 512;  // columns per wave-wide 16-byte load (64 lanes x 8 bf16)
 
@@ -443,6 +473,12 @@ __device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const ui
     const uint16_t* g = (const uint16_t*)x;
     for (int i = tid; i < kpad; i += blockDim.x)
       xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(g[i])) * bf16_bits_to_f32(x2[i])) : 0.f;
+  } else if constexpr (PRO == PRO_SILU_MUL_IL) {
+    const uint16_t* gu = (const uint16_t*)x;
+    for (int i = tid; i < kpad; i += blockDim.x) {
+      const int gi = 16 * (i >> 3) + (i & 7);
+      xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(gu[gi])) * bf16_bits_to_f32(gu[gi + 8])) : 0.f;
+    }
   } else {
     const uint16_t* xb = (const uint16_t*)x;
     for (int i = tid; i < kpad; i += blockDim.x) xs[i] = i < K ? bf16_bits_to_f32(xb[i]) : 0.f;
@@ -699,6 +735,30 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
   return KH_OK;
 }
 
+// The fused SwiGLU projection: the MFMA tile kernel with the SWIGLU epilogue, tiles chosen as in
+// launch_gemm, never split over K (the epilogue needs whole sums).
+int launch_gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, uint16_t* H, int64_t ldh,
+                       int M, int N, int K) {
+  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  const int wt = t128 >= kGemmT128Min ? 2 : 1;
+  const int gt = g_tile(wt);
+  const int64_t tiles = (int64_t)((M + gt - 1) / gt) * ((N + gt - 1) / gt);
+  KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_swiglu: grid too large");
+  const int tiles_n = (N + gt - 1) / gt, nblk = (int)tiles;
+  constexpr int PF = kGemmPrefetch;
+  if (wt == 2)
+    gemm_bf16_nt_kernel<uint16_t, 2, 64, false, PF, true><<<nblk, G_THREADS, 0, stream()>>>(
+        X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr);
+  else if (tiles <= 512)
+    gemm_bf16_nt_kernel<uint16_t, 1, 128, false, PF, true><<<nblk, G_THREADS, 0, stream()>>>(
+        X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr);
+  else
+    gemm_bf16_nt_kernel<uint16_t, 1, 64, false, PF, true><<<nblk, G_THREADS, 0, stream()>>>(
+        X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
 }  // namespace
 
 namespace kh {
@@ -735,11 +795,30 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
   return launch_gemm<float, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
 }
 
+int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,
+                   int64_t n_half, int64_t k) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(m >= 0 && n_half >= 0 && k > 0 && m <= INT32_MAX && 2 * n_half <= INT32_MAX && k <= INT32_MAX,
+             "kh_gemm_swiglu: bad extents");
+  if (m == 0 || n_half == 0) return KH_OK;
+  KH_REQUIRE(x && w_gu && h, "kh_gemm_swiglu: null pointer");
+  KH_REQUIRE(n_half % 8 == 0, "kh_gemm_swiglu: the intermediate size %lld is not a multiple of 8", (long long)n_half);
+  KH_REQUIRE(k % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= k && ldw >= k && ldh >= n_half,
+             "kh_gemm_swiglu: k and the row strides must be multiples of 8 elements (ldx, ldw >= k, ldh >= n_half)");
+  KH_REQUIRE(aligned16(x) && aligned16(w_gu), "kh_gemm_swiglu: x and w_gu must be 16-byte aligned");
+  const int64_t lim = int64_t(1) << 31;
+  KH_REQUIRE((int64_t)g_tile(2) * ldx * 2 < lim && (int64_t)g_tile(2) * ldw * 2 < lim,
+             "kh_gemm_swiglu: row stride too large");
+  return launch_gemm_swiglu((const uint16_t*)x, ldx, (const uint16_t*)w_gu, ldw, (uint16_t*)h, ldh, (int)m,
+                            (int)(2 * n_half), (int)k);
+}
+
 int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps, const void* w,
                   int64_t ldw, void* c, const void* cin, const void* bias, int64_t n, int64_t k, float alpha,
                   float beta, int out_dtype) {
   KH_REQUIRE_INIT();
-  KH_REQUIRE(prologue >= PRO_NONE && prologue <= PRO_SILU_MUL, "kh_gemv_fused: unknown prologue %d", prologue);
+  KH_REQUIRE(prologue >= PRO_NONE && prologue <= PRO_SILU_MUL_IL, "kh_gemv_fused: unknown prologue %d", prologue);
+  KH_REQUIRE(prologue != PRO_SILU_MUL_IL || k % 8 == 0, "kh_gemv_fused: the interleaved silu*mul prologue needs k %% 8 == 0");
   KH_REQUIRE(n >= 0 && k > 0 && n <= INT32_MAX && k <= INT32_MAX, "kh_gemv_fused: bad extents");
   KH_REQUIRE(out_dtype == KH_BF16 || out_dtype == KH_F32, "kh_gemv_fused: unsupported output dtype %d", out_dtype);
   if (n == 0) return KH_OK;
@@ -756,6 +835,8 @@ int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_
       ok = launch_gemv1<PRO_RMSNORM, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
     else if (prologue == PRO_SILU_MUL)
       ok = launch_gemv1<PRO_SILU_MUL, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+    else if (prologue == PRO_SILU_MUL_IL)
+      ok = launch_gemv1<PRO_SILU_MUL_IL, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
     else
       ok = launch_gemv1<PRO_NONE, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
   };

@@ -166,16 +166,45 @@ __global__ void silu_mul_bf16x8_kernel(const uint16_t* __restrict__ g, int64_t g
 // ---- index_select -------------------------------------------------------------------------
 // Rows of `table` (element type T) gathered into `out` (element type D, converted through fp32);
 // an id outside [0, n_rows) yields a zero row.
+// The table is viewed as [outer, n_rows, row_elems] (outer = 1: rows of an embedding table):
+// out[a, r, :] = table[a, idx[r], :].  Block (r, a-slice) copies one output row of row_elems.
 template <typename T, typename D>
 __global__ void index_select_kernel(const T* __restrict__ table, int64_t n_rows, const int32_t* __restrict__ idx,
-                                    int64_t row_elems, D* __restrict__ out) {
+                                    int64_t row_elems, D* __restrict__ out, int64_t outer, int64_t n_idx) {
   const int64_t r = blockIdx.x;
   const int32_t id = idx[r];
   const bool ok = id >= 0 && id < n_rows;
-  const T* src = table + (ok ? (int64_t)id : 0) * row_elems;
-  D* dst = out + r * row_elems;
-  for (int64_t c = threadIdx.x; c < row_elems; c += blockDim.x)
-    Elem<D>::store(dst, c, ok ? Elem<T>::load(src, c) : 0.0f);
+  for (int64_t a = blockIdx.y; a < outer; a += gridDim.y) {
+    const T* src = table + (a * n_rows + (ok ? (int64_t)id : 0)) * row_elems;
+    D* dst = out + (a * n_idx + r) * row_elems;
+    for (int64_t c = threadIdx.x; c < row_elems; c += blockDim.x)
+      Elem<D>::store(dst, c, ok ? Elem<T>::load(src, c) : 0.0f);
+  }
+}
+
+int launch_index_select(const void* table, int64_t outer, int64_t n_rows, int64_t inner, const int32_t* idx,
+                        int64_t n_idx, void* out, int dtype, int out_dtype, const char* name) {
+  KH_REQUIRE(outer > 0 && n_rows > 0 && n_idx >= 0 && inner > 0, "%s: bad extents", name);
+  if (n_idx == 0) return KH_OK;
+  KH_REQUIRE(n_idx <= INT32_MAX, "%s: too many indices", name);
+  KH_REQUIRE(table && idx && out, "%s: null pointer", name);
+  const dim3 grid((unsigned)n_idx, (unsigned)(outer < 65535 ? outer : 65535)), block(kThreads);
+  if (dtype == KH_BF16 && out_dtype == KH_BF16)
+    index_select_kernel<uint16_t, uint16_t><<<grid, block, 0, stream()>>>((const uint16_t*)table, n_rows, idx, inner,
+                                                                          (uint16_t*)out, outer, n_idx);
+  else if (dtype == KH_BF16 && out_dtype == KH_F32)
+    index_select_kernel<uint16_t, float><<<grid, block, 0, stream()>>>((const uint16_t*)table, n_rows, idx, inner,
+                                                                       (float*)out, outer, n_idx);
+  else if (dtype == KH_F32 && out_dtype == KH_F32)
+    index_select_kernel<float, float><<<grid, block, 0, stream()>>>((const float*)table, n_rows, idx, inner,
+                                                                    (float*)out, outer, n_idx);
+  else if (dtype == KH_F32 && out_dtype == KH_BF16)
+    index_select_kernel<float, uint16_t><<<grid, block, 0, stream()>>>((const float*)table, n_rows, idx, inner,
+                                                                       (uint16_t*)out, outer, n_idx);
+  else
+    KH_REQUIRE(false, "%s: unsupported dtypes (table %d, out %d)", name, dtype, out_dtype);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 // ---- greedy decode bookkeeping (one thread) ------------------------------------------------
@@ -437,27 +466,13 @@ int kh_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64
 int kh_index_select(const void* table, int64_t n_rows, const int32_t* idx, int64_t n_idx, int64_t row_elems,
                     void* out, int dtype, int out_dtype) {
   KH_REQUIRE_INIT();
-  KH_REQUIRE(n_rows > 0 && n_idx >= 0 && row_elems > 0, "kh_index_select: bad extents");
-  if (n_idx == 0) return KH_OK;
-  KH_REQUIRE(n_idx <= INT32_MAX, "kh_index_select: too many indices");
-  KH_REQUIRE(table && idx && out, "kh_index_select: null pointer");
-  const dim3 grid((unsigned)n_idx), block(kThreads);
-  if (dtype == KH_BF16 && out_dtype == KH_BF16)
-    index_select_kernel<uint16_t, uint16_t><<<grid, block, 0, stream()>>>((const uint16_t*)table, n_rows, idx,
-                                                                          row_elems, (uint16_t*)out);
-  else if (dtype == KH_BF16 && out_dtype == KH_F32)
-    index_select_kernel<uint16_t, float><<<grid, block, 0, stream()>>>((const uint16_t*)table, n_rows, idx,
-                                                                       row_elems, (float*)out);
-  else if (dtype == KH_F32 && out_dtype == KH_F32)
-    index_select_kernel<float, float><<<grid, block, 0, stream()>>>((const float*)table, n_rows, idx, row_elems,
-                                                                    (float*)out);
-  else if (dtype == KH_F32 && out_dtype == KH_BF16)
-    index_select_kernel<float, uint16_t><<<grid, block, 0, stream()>>>((const float*)table, n_rows, idx,
-                                                                       row_elems, (uint16_t*)out);
-  else
-    KH_REQUIRE(false, "kh_index_select: unsupported dtypes (table %d, out %d)", dtype, out_dtype);
-  KH_CHECK_LAUNCH();
-  return KH_OK;
+  return launch_index_select(table, 1, n_rows, row_elems, idx, n_idx, out, dtype, out_dtype, "kh_index_select");
+}
+
+int kh_index_select_dim(const void* table, int64_t outer, int64_t n_rows, int64_t inner, const int32_t* idx,
+                        int64_t n_idx, void* out, int dtype, int out_dtype) {
+  KH_REQUIRE_INIT();
+  return launch_index_select(table, outer, n_rows, inner, idx, n_idx, out, dtype, out_dtype, "kh_index_select_dim");
 }
 
 int kh_greedy_advance(const int32_t* next_token, int32_t* position, int32_t* seq_len, int32_t* token_log,

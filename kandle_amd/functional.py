@@ -160,7 +160,8 @@ def linear_fused(prologue: str, x: Tensor, weight: Tensor, norm_weight: Optional
                  out_dtype: Optional[str] = None) -> Tensor:
     """One-row linear with its producer fused in front (decode).  prologue 'rms_norm': x is the
     fp32 residual row and the input is rms_norm(x, norm_weight, eps); 'silu_mul': the input is
-    silu(x) * x2; 'none': the input is x.  With `residual` the result is added into it in place
+    silu(x) * x2; 'silu_mul_interleaved': x is a gate/up row interleaved in blocks of 8 and the
+    input is silu(gate) * up; 'none': the input is x.  With `residual` the result is added into it in place
     (residual += input @ weight^T) and returned; otherwise a new [1, out_features] tensor of
     out_dtype (default bf16)."""
     params = {"eps": eps}
@@ -284,6 +285,14 @@ def arange(start: float, end: Optional[float] = None, step: float = 1.0, dtype: 
     return _wrap(out)
 
 
+def linear_swiglu(input: Tensor, weight_gu: Tensor) -> Tensor:
+    """silu(input W_gate^T) * (input W_up^T) in one launch from the interleaved gate/up weight
+    [2 I, H] (kernels.interleave_gate_up); returns [..., I] bf16 (swiglu.ts:119-134)."""
+    out = _new(input, tuple(input.shape[:-1]) + (weight_gu.shape[0] // 2,), "bfloat16")
+    _kernel(input, "linear_swiglu")(input.handle, weight_gu.handle, out)
+    return _wrap(out)
+
+
 def silu_mul(gate: Tensor, up: Tensor) -> Tensor:
     out = _new(gate, gate.shape)
     _kernel(gate, "silu_mul")(gate.handle, up.handle, out)
@@ -321,11 +330,36 @@ def embedding(input_ids: Tensor, weight: Tensor, out_dtype: Optional[str] = None
     return _wrap(out)
 
 
+def index_select(x: Tensor, dim: int, index: Tensor) -> Tensor:
+    """x with the entries of `index` (int32, 1-d) taken along `dim` (gather.ts:121,190)."""
+    nd = len(x.shape)
+    d = dim + nd if dim < 0 else dim
+    if not 0 <= d < nd or len(index.shape) != 1:
+        raise ValueError("index_select: dim out of range or index not 1-d")
+    ids = index if index.handle.is_contiguous() else contiguous(index)
+    out = _new(x, tuple(x.shape[:d]) + (index.shape[0],) + tuple(x.shape[d + 1:]))
+    _kernel(x, "index_select")(x.handle, ids.handle, {"dim": d}, out)
+    if ids is not index:
+        ids.dispose()
+    return _wrap(out)
+
+
 def argmax(x: Tensor, dim: int = -1) -> Tensor:
-    if dim not in (-1, len(x.shape) - 1):
-        raise NotImplementedError("argmax: only the last dim is implemented")
-    out = _new(x, x.shape[:-1], "int32")
-    _kernel(x, "argmax")(TensorIterator([x.handle], [out]))
+    """Index of the maximum along `dim` (lowest index among maxima), int32, `dim` removed.  A dim
+    other than the last is moved last and materialised contiguous first (the argmax kernel reduces
+    contiguous rows; reference: reduction/argShaderBuilder.ts:59-110 reduces any dim)."""
+    nd = len(x.shape)
+    d = dim + nd if dim < 0 else dim
+    if not 0 <= d < nd:
+        raise ValueError(f"argmax: dim {dim} out of range for a {nd}-d tensor")
+    src = x
+    if d != nd - 1:
+        perm = [i for i in range(nd) if i != d] + [d]
+        src = contiguous(permute(x, perm))
+    out = _new(x, tuple(s for i, s in enumerate(x.shape) if i != d), "int32")
+    _kernel(x, "argmax")(TensorIterator([src.handle], [out]))
+    if src is not x:
+        src.dispose()
     return _wrap(out)
 
 

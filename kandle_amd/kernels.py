@@ -20,6 +20,7 @@ New fused names (no reference schema; the reference composes them from the ops a
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
 
@@ -261,14 +262,25 @@ def matmul(config: MatmulDispatchResult, a: HipTensorHandle, b: HipTensorHandle)
         raise TypeError(f"matmul does not support dtype {a.dtype}")
     if out.dtype != a.dtype and not (a.dtype == BFLOAT16 and out.dtype == FLOAT32):
         raise TypeError(f"matmul: {a.dtype} inputs cannot produce a {out.dtype} output")
-    if config.transpose_a:
-        raise NotImplementedError("matmul: transpose_a is materialised by the dispatcher")
     M, K, N = config.M, config.K, config.N
     tmp = []
     try:
+        if config.transpose_a:
+            # A stored [..., K, M]: op(A) = A^T, materialised as contiguous [..., M, K]
+            a = HipTensorHandle.create_view(a.storage, list(a.shape[:-2]) + [a.shape[-1], a.shape[-2]], a.dtype,
+                                            list(a.strides[:-2]) + [a.strides[-1], a.strides[-2]], a.offset)
+            tmp.append(a)
         A = a if (a.strides[-1] == 1 or K == 1) else _materialize(a)
         if A is not a:
             tmp.append(A)
+        if (not config.transpose_b and len(b.shape) >= 2 and b.strides[-2] == 1 and b.shape[-1] > 1
+                and b.strides[-1] >= K):
+            # B [..., K, N] stored column-major is B^T [..., N, K] stored row-major: use it as the
+            # transposed operand instead of copying (matmulOps.ts:171-181 detects this from strides)
+            b = HipTensorHandle.create_view(b.storage, list(b.shape[:-2]) + [N, K], b.dtype,
+                                            list(b.strides[:-2]) + [b.strides[-1], 1], b.offset)
+            tmp.append(b)
+            config = dataclasses.replace(config, transpose_b=True)
         Bm = b if (b.strides[-1] == 1 or b.shape[-1] == 1) else _materialize(b)
         if Bm is not b:
             tmp.append(Bm)
@@ -589,21 +601,29 @@ def _scatter_rows(src: HipTensorHandle, dst: HipTensorHandle) -> None:
 
 
 def index_select(self_: HipTensorHandle, index: HipTensorHandle, params: dict, output: HipTensorHandle) -> None:
-    """GatherKernelImpl for dim 0 of a contiguous table (embedding lookup)."""
+    """GatherKernelImpl (gather.ts:121,190): output = self_ with the entries of `index` taken along
+    params['dim'] (default 0: rows of an embedding table); output holds self_'s shape with that dim
+    replaced by len(index) (dim 0 also accepts index.shape + self_.shape[1:], the embedding form).
+    A non-contiguous table is materialised first; ids outside the dim give zeros."""
+    nd = len(self_.shape)
     dim = int((params or {}).get("dim", 0))
-    if dim != 0:
-        raise NotImplementedError("index_select: only dim 0 (embedding rows) is implemented")
+    if dim < 0:
+        dim += nd
+    if not 0 <= dim < max(nd, 1):
+        raise ValueError(f"index_select: dim {dim} out of range for a {nd}-d tensor")
     if index.dtype != INT32 or not index.is_contiguous():
         raise TypeError("index_select: index must be a contiguous int32 tensor")
     if not output.is_contiguous() or output.dtype not in (FLOAT32, BFLOAT16) or self_.dtype not in (FLOAT32, BFLOAT16):
         raise TypeError("index_select: table and output must be float tensors; output contiguous")
     t = self_ if self_.is_contiguous() else _materialize(self_)
     try:
-        row = int(np.prod(t.shape[1:])) if len(t.shape) > 1 else 1
-        if output.numel != index.numel * row:
-            raise ValueError("index_select: output must hold len(index) rows of the table")
+        shape = list(t.shape) if nd else [1]
+        outer = int(np.prod(shape[:dim])) if dim else 1
+        inner = int(np.prod(shape[dim + 1:])) if dim + 1 < len(shape) else 1
+        if output.numel != outer * index.numel * inner:
+            raise ValueError("index_select: output must hold len(index) entries along dim")
         _lib.call(
-            "kh_index_select", _vp(t.data_ptr()), t.shape[0], _vp(index.data_ptr()), index.numel, row,
+            "kh_index_select_dim", _vp(t.data_ptr()), outer, shape[dim], inner, _vp(index.data_ptr()), index.numel,
             _vp(output.data_ptr()), t.kh_dtype, output.kh_dtype,
         )
     finally:
@@ -633,7 +653,37 @@ def zeros(output: HipTensorHandle) -> None:
     fill(output, 0.0)
 
 
-GEMV_PROLOGUES = {"none": 0, "rms_norm": 1, "silu_mul": 2}
+GEMV_PROLOGUES = {"none": 0, "rms_norm": 1, "silu_mul": 2, "silu_mul_interleaved": 3}
+
+
+def interleave_gate_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """The fused gate/up weight of linear_swiglu: rows 16i .. 16i + 7 are gate rows 8i .. 8i + 7 and
+    rows 16i + 8 .. 16i + 15 the matching up rows (both [I, H], I % 8 == 0)."""
+    I, H = gate.shape
+    if up.shape != gate.shape or I % 8:
+        raise ValueError("interleave_gate_up: gate and up must share a shape [I, H] with I % 8 == 0")
+    return np.stack([gate.reshape(I // 8, 8, H), up.reshape(I // 8, 8, H)], axis=1).reshape(2 * I, H)
+
+
+def linear_swiglu(x, w_gu, output) -> None:
+    """output [..., I] = silu(x W_gate^T) * (x W_up^T), bf16, from the interleaved weight w_gu [2I, H]
+    (interleave_gate_up); x [..., H] bf16 with contiguous rows.  The gate/up projections, silu and
+    mul of SwiGLUMLP.forward (swiglu.ts:119-134) in one launch (kh_gemm_swiglu)."""
+    two_i, H = w_gu.shape
+    I = two_i // 2
+    if x.dtype != BFLOAT16 or w_gu.dtype != BFLOAT16 or output.dtype != BFLOAT16:
+        raise TypeError("linear_swiglu: bf16 operands only")
+    if x.shape[-1] != H or tuple(output.shape) != tuple(x.shape[:-1]) + (I,):
+        raise ValueError(f"linear_swiglu: x [..., {H}] and output [..., {I}] expected for w_gu {tuple(w_gu.shape)}")
+    if x.strides[-1] != 1 or w_gu.strides[1] != 1 or output.strides[-1] != 1:
+        raise ValueError("linear_swiglu: rows must be contiguous")
+    m = int(np.prod(x.shape[:-1])) if len(x.shape) > 1 else 1
+    if len(x.shape) > 2 and not (x.is_contiguous() and output.is_contiguous()):
+        raise ValueError("linear_swiglu: batched operands must be contiguous")
+    ldx = x.strides[-2] if len(x.shape) >= 2 else H
+    ldh = output.strides[-2] if len(output.shape) >= 2 else I
+    _lib.call("kh_gemm_swiglu", _vp(x.data_ptr()), ldx, _vp(w_gu.data_ptr()), w_gu.strides[0],
+              _vp(output.data_ptr()), ldh, m, I, H)
 
 
 def gemv_fused(prologue: str, x, w, out, params=None) -> None:
@@ -641,7 +691,9 @@ def gemv_fused(prologue: str, x, w, out, params=None) -> None:
     + beta * cin (+ bias) for the bf16 weight W [n, k] (nn.Linear layout), where x' is
       'none'     -> x (bf16 [k]);
       'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row x, rounded to bf16;
-      'silu_mul' -> silu(x) * x2 of the bf16 gate/up rows, rounded to bf16.
+      'silu_mul' -> silu(x) * x2 of the bf16 gate/up rows, rounded to bf16;
+      'silu_mul_interleaved' -> the same product read from one bf16 row [2k] holding gate and up
+                    interleaved in blocks of 8 (the output of a linear with interleave_gate_up's weight).
     params: norm_weight, eps, x2, cin, alpha, beta, bias.  out may alias cin (residual add).
     Fuses RMSNorm.ts:92-99 or swiglu.ts:119-134 into Linear.ts:135-137."""
     params = params or {}
@@ -654,8 +706,9 @@ def gemv_fused(prologue: str, x, w, out, params=None) -> None:
     for h, nm in ((x, "x"), (x2, "x2")):
         if h is None:
             continue
-        if h.dtype != want or h.numel != k or (len(h.shape) > 0 and h.strides[-1] != 1):
-            raise ValueError(f"gemv_fused: {nm} must be one contiguous {want} row of {k} elements")
+        kx = 2 * k if prologue == "silu_mul_interleaved" else k
+        if h.dtype != want or h.numel != kx or (len(h.shape) > 0 and h.strides[-1] != 1):
+            raise ValueError(f"gemv_fused: {nm} must be one contiguous {want} row of {kx} elements")
     if prologue == "silu_mul" and x2 is None:
         raise ValueError("gemv_fused: silu_mul needs x2")
     nw = params.get("norm_weight")
@@ -753,6 +806,7 @@ KERNELS = {
     "add": add,
     "sub": sub,
     "silu_mul": silu_mul,
+    "linear_swiglu": linear_swiglu,
     "copy": copy,
     "contiguous": copy,
     "cast": copy,

@@ -12,8 +12,9 @@ position p:
         the caller turns causal off for 1-token decode, gqa.ts:333-336; GQA is native, no repeat_kv)
   x   = x + o W_o^T                                            (matmul, residual in the epilogue)
   h   = rms_norm(x, post_attention_layernorm)
-  gu  = h W_gu^T                                               [S, 2 I] (gate rows then up rows)
-  x   = x + silu(gu[:, :I]) * gu[:, I:] W_down^T                (silu_mul, matmul + residual)
+  a   = silu(h W_gate^T) * (h W_up^T)                          [S, I] (linear_swiglu: one GEMM over
+        the gate/up weight interleaved in blocks of 8 rows, silu*mul in its epilogue)
+  x   = x + a W_down^T                                          (matmul + residual)
 then x = rms_norm(x, norm) and logits = x[last] E^T in fp32 with the tied embedding E
 (for_causal_lm.ts:121-125, 184-185); greedy = argmax, lowest index among maxima (:475-508).
 The residual stream x is float32 (embedding rows widened on gather; the o_proj and down GEMMs add
@@ -34,7 +35,7 @@ from .. import functional as F
 from .. import synthetic as syn
 from .._lib import KandleHipError
 from ..graphs import HipGraph
-from ..kernels import TensorIterator
+from ..kernels import TensorIterator, interleave_gate_up
 from ..tensor import HipTensorHandle, Tensor
 from .kv_cache import StaticKVCache
 from .rope import RotaryEmbedding
@@ -183,7 +184,9 @@ class Qwen3ForCausalLM:
                 "k_norm": up(w("self_attn.k_norm.weight")),
                 "w_o": up(w("self_attn.o_proj.weight")),
                 "post_norm": up(w("post_attention_layernorm.weight")),
-                "w_gu": up(np.concatenate([w("mlp.gate_proj.weight"), w("mlp.up_proj.weight")], axis=0)),
+                # gate and up rows interleaved in blocks of 8 (kernels.interleave_gate_up): the fused
+                # SwiGLU GEMM's layout, whose decode GEMV output the down projection reads in place
+                "w_gu": up(interleave_gate_up(w("mlp.gate_proj.weight"), w("mlp.up_proj.weight"))),
                 "w_down": up(w("mlp.down_proj.weight")),
             })
         self.rope = RotaryEmbedding(cfg.head_dim, cfg.rope_theta)
@@ -245,20 +248,15 @@ class Qwen3ForCausalLM:
             else:
                 self._attention_unfused(li, L, x, S, positions, attend, one)
             if one:
-                gu = F.linear_fused("rms_norm", x, L["w_gu"], L["post_norm"], eps)     # [1, 2I]
+                gu = F.linear_fused("rms_norm", x, L["w_gu"], L["post_norm"], eps)     # [1, 2I] interleaved
+                F.linear_fused("silu_mul_interleaved", gu, L["w_down"], residual=x)    # x += a W_d^T
+                gu.dispose()
             else:
                 h = F.rms_norm(x, [Hd], L["post_norm"], eps, out_dtype="bfloat16")
-                gu = F.linear(h, L["w_gu"])                                            # [S, 2I]
+                a = F.linear_swiglu(h, L["w_gu"])                                      # [S, I]
                 h.dispose()
-            g, u = F.narrow(gu, 1, 0, I), F.narrow(gu, 1, I, I)
-            if one:
-                F.linear_fused("silu_mul", g, L["w_down"], x2=u, residual=x)           # x += a W_d^T
-            else:
-                a = F.silu_mul(g, u)
                 F.dispatch_matmul(a, L["w_down"], c=x, beta=1.0, out=x, transpose_b=True)
                 a.dispose()
-            for t in (g, u, gu):
-                t.dispose()
         last = F.narrow(x, 0, S - 1, 1)
         if one:
             logits = F.linear_fused("rms_norm", last, self.lm_head, self.final_norm, eps, out_dtype="float32")

@@ -355,6 +355,12 @@ FN(indexSelect, 8)
   void* t = arg_ptr(A, 0); int64_t nr = arg_i64(A, 1); void* idx = arg_ptr(A, 2); int64_t ni = arg_i64(A, 3);
   int64_t re = arg_i64(A, 4); void* o = arg_ptr(A, 5); int dt = arg_int(A, 6); int odt = arg_int(A, 7);
   CALL(kh_index_select(t, nr, (const int32_t*)idx, ni, re, o, dt, odt))
+/* indexSelectDim(table, outer, nRows, inner, idx, nIdx, out, dtype, outDtype) */
+FN(indexSelectDim, 9)
+  void* t = arg_ptr(A, 0); int64_t outer = arg_i64(A, 1); int64_t nr = arg_i64(A, 2); int64_t inner = arg_i64(A, 3);
+  void* idx = arg_ptr(A, 4); int64_t ni = arg_i64(A, 5); void* o = arg_ptr(A, 6); int dt = arg_int(A, 7);
+  int odt = arg_int(A, 8);
+  CALL(kh_index_select_dim(t, outer, nr, inner, (const int32_t*)idx, ni, o, dt, odt))
 FN(argmax, 5)
   void* x = arg_ptr(A, 0); int64_t rows = arg_i64(A, 1); int64_t n = arg_i64(A, 2); void* o = arg_ptr(A, 3);
   int dt = arg_int(A, 4);
@@ -451,6 +457,13 @@ FN(gemm, 17)
   double al = arg_f64(A, 12); double be = arg_f64(A, 13); int tb = arg_flag(A, 14); int dt = arg_int(A, 15);
   int odt = arg_int(A, 16);
   CALL(kh_gemm(a, lda, b, ldb, c, ldc, cin, ldcin, bias, m, n, k, (float)al, (float)be, tb, dt, odt))
+/* gemmSwiglu(x, ldx, wGu, ldw, h, ldh, m, nHalf, k): the SwiGLU gate/up projections with silu * mul
+   in the epilogue (swiglu.ts:119-134), weight rows interleaved in blocks of 8 */
+FN(gemmSwiglu, 9)
+  void* x = arg_ptr(A, 0); int64_t ldx = arg_i64(A, 1); void* w = arg_ptr(A, 2); int64_t ldw = arg_i64(A, 3);
+  void* h = arg_ptr(A, 4); int64_t ldh = arg_i64(A, 5); int64_t m = arg_i64(A, 6); int64_t nh = arg_i64(A, 7);
+  int64_t k = arg_i64(A, 8);
+  CALL(kh_gemm_swiglu(x, ldx, w, ldw, h, ldh, m, nh, k))
 /* gemvFused(prologue, x, x2, normW, eps, w, ldw, c, cin, bias, n, k, alpha, beta, outDtype) */
 FN(gemvFused, 15)
   int pro = arg_int(A, 0); void* x = arg_ptr(A, 1); void* x2 = arg_ptr(A, 2); void* nw = arg_ptr(A, 3);
@@ -469,10 +482,10 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(eventCreate), EXPORT(eventDestroy), EXPORT(eventRecord), EXPORT(eventElapsedMs),
       EXPORT(graphBeginCapture), EXPORT(graphEndCapture), EXPORT(graphLaunch), EXPORT(graphDestroy),
       EXPORT(fill), EXPORT(copyStrided), EXPORT(binary), EXPORT(silu), EXPORT(unary), EXPORT(arange),
-      EXPORT(siluMul), EXPORT(indexSelect), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
+      EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
-      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemvFused),
+      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemvFused),
   };
   napi_define_properties(env, exports, sizeof(d) / sizeof(d[0]), d);
   napi_value v;

@@ -103,3 +103,57 @@ def test_argmax_ties_across_chunks_and_rows(hip):
     xb = syn.bf16(syn.normal(351, (3, 9000)))[1]
     ab = F.argmax(Tensor(xb, dtype="bfloat16")).numpy()
     np.testing.assert_array_equal(ab, oracle.argmax(xb))
+
+
+def test_gemv_interleaved_silu_mul_prologue_matches_split_halves(hip):
+    """Prologue 'silu_mul_interleaved' reads gate/up interleaved in blocks of 8 from one row; it
+    equals prologue 'silu_mul' on the same values split into gate and up rows, bit for bit."""
+    I, N = 3072, 1024
+    g, gh = seeded(330, (1, I), "bfloat16", std=2.0)
+    u, uh = seeded(331, (1, I), "bfloat16", std=2.0)
+    from kandle_amd.kernels import interleave_gate_up
+    gu_vals = interleave_gate_up(gh.reshape(I, 1), uh.reshape(I, 1)).reshape(1, 2 * I)
+    gu = Tensor(syn.bf16(gu_vals)[0], dtype="bfloat16")
+    w, wh = seeded(332, (N, I), "bfloat16", std=0.02)
+    res0 = Tensor(np.zeros((1, N), np.float32))
+    res1 = Tensor(np.zeros((1, N), np.float32))
+    a = F.linear_fused("silu_mul", g, w, x2=u, residual=res0).numpy()
+    b = F.linear_fused("silu_mul_interleaved", gu, w, residual=res1).numpy()
+    assert np.array_equal(a, b)
+    ref = oracle.linear(oracle.bf16_round(oracle.silu_mul(gh, uh)), wh)
+    ok, err = _close_f32(b, ref)
+    assert ok, err
+
+
+@pytest.mark.parametrize("M,I,K", [(512, 3072, 1024), (130, 96, 64), (1, 3072, 1024), (7, 40, 200), (600, 3072, 1024)])
+def test_linear_swiglu_matches_unfused_gemm_and_silu_mul(hip, M, I, K):
+    """kh_gemm_swiglu (gate/up GEMM with silu*mul in the epilogue, interleaved weight) against the
+    unfused sequence -- the GEMM over the plain [gate; up] weight stored in bf16, then silu_mul --
+    bit for bit where that GEMM runs the same MFMA tiles (M > 8), and against the oracle within a
+    bound for one bf16 rounding of g, u and h."""
+    from kandle_amd.kernels import interleave_gate_up
+    x, xh = seeded(340, (M, K), "bfloat16")
+    wg_bits, wg = syn.bf16(syn.normal(341, (I, K), 0.05))
+    wu_bits, wu = syn.bf16(syn.normal(342, (I, K), 0.05))
+    w_cat = Tensor(np.concatenate([wg_bits, wu_bits]), dtype="bfloat16")
+    w_il = Tensor(interleave_gate_up(wg_bits, wu_bits), dtype="bfloat16")
+    fused = F.linear_swiglu(x, w_il).numpy()
+    gu = F.linear(x, w_cat)
+    unfused = F.silu_mul(F.narrow(gu, 1, 0, I), F.narrow(gu, 1, I, I)).numpy()
+    if M > 8:   # the unfused GEMM takes the same MFMA tiles (M <= 8: the one-row / skinny paths)
+        assert np.array_equal(fused.view(np.uint32), unfused.view(np.uint32))
+    g = oracle.bf16_round(oracle.linear(xh, wg)).astype(np.float64)
+    u = oracle.bf16_round(oracle.linear(xh, wu)).astype(np.float64)
+    ref = oracle.silu_mul(g.astype(np.float32), u.astype(np.float32)).astype(np.float64)
+    # g and u are fp32 sums rounded to bf16, so either may sit one bf16 rounding (2^-8 relative) away
+    # from the f64 oracle's; silu' <= 1.1, and h itself is rounded once more.
+    silu = g / (1.0 + np.exp(-np.clip(g, -88, 88)))
+    bound = 2.0 ** -8 * (1.1 * np.abs(g) * np.abs(u) + np.abs(silu) * np.abs(u) + np.abs(ref)) + 1e-6
+    assert np.all(np.abs(fused - ref) <= bound), float(np.max(np.abs(fused - ref) - bound))
+
+
+def test_linear_swiglu_rejects_bad_layouts(hip):
+    x, _ = seeded(350, (4, 64), "bfloat16")
+    w, _ = seeded(351, (2 * 12, 64), "bfloat16")   # intermediate 12: not a multiple of 8
+    with pytest.raises(Exception, match="multiple of 8"):
+        F.linear_swiglu(x, w)

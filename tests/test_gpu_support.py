@@ -156,6 +156,54 @@ def test_matmul_batched_fp32(hip):
     assert max_rel(y, np.einsum("bmk,bkn->bmn", ah.astype(np.float64), bh)) < 1e-5
 
 
+@pytest.mark.parametrize("dim", [0, 1, 2, -1])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_index_select_any_dim(hip, dim, dtype):
+    """index_select along every dim of a 3-d tensor (gather.ts:121,190), ids out of range giving zeros,
+    and a permuted (non-contiguous) source."""
+    x, xh = seeded(60, (5, 7, 9), dtype)
+    n = xh.shape[dim]
+    idx = np.array([n - 1, 0, 2, 2, n, -1], np.int32)
+    out = F.index_select(x, dim, Tensor(idx, dtype="int32")).numpy()
+    ref = np.take(xh, np.clip(idx, 0, n - 1), axis=dim)
+    bad = (idx < 0) | (idx >= n)
+    sl = [slice(None)] * 3
+    sl[dim] = bad
+    ref[tuple(sl)] = 0.0
+    assert np.array_equal(out, ref)
+    xp = F.permute(x, [2, 0, 1])
+    out2 = F.index_select(xp, 1, Tensor(np.array([4, 1], np.int32), dtype="int32")).numpy()
+    assert np.array_equal(out2, np.take(np.transpose(xh, (2, 0, 1)), [4, 1], axis=1))
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2])
+def test_argmax_any_dim(hip, dim):
+    """argmax over a non-last dim (moved last and materialised), lowest index on ties."""
+    xh = np.round(syn.normal(61, (6, 50, 33)) * 2).astype(np.float32)   # many ties
+    out = F.argmax(Tensor(xh), dim).numpy()
+    assert np.array_equal(out, np.argmax(xh, axis=dim).astype(np.int32))
+
+
+def test_matmul_transpose_a_and_detected_transpose_b(hip):
+    """The matmul kernel with config.transpose_a (A stored [K, M]) and with B passed as a transposed
+    view of a row-major [N, K] weight (taken as the transposed operand, not copied), bf16 and fp32."""
+    from kandle_amd import kernels
+    for dtype in ("float32", "bfloat16"):
+        M, K, N = 130, 256, 72
+        at, ath = seeded(62, (K, M), dtype)           # A^T stored
+        w, wh = seeded(63, (N, K), dtype, std=0.05)   # B^T stored, passed as the view w^T [K, N]
+        out = F.dispatch_matmul(at, F.transpose(w, 0, 1), transpose_a=True).numpy()
+        ref = oracle.linear(np.ascontiguousarray(ath.T), wh)
+        tol = 1e-4 if dtype == "float32" else 2e-2
+        assert max_rel(out, ref) < tol, dtype
+        # the kernel called as a dispatcher would with MatmulDispatchResult.transposeA set
+        o = F.zeros((M, N), dtype)
+        cfg = kernels.MatmulDispatchResult(variant="mm", output=o.handle, M=M, K=K, N=N, batch_shape=(),
+                                           batch_size=1, transpose_a=True, transpose_b=True, alpha=1.0, beta=0.0)
+        kernels.matmul(cfg, at.handle, w.handle)
+        assert max_rel(o.numpy(), ref) < tol, dtype
+
+
 def test_allocator_reuses_freed_blocks(hip):
     before = HipBackend.memory_stats()
     t = Tensor(np.zeros(1 << 20, np.float32))
