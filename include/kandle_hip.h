@@ -50,6 +50,12 @@ int kh_device_count(int* count);
 /* Text of the most recent error on the calling thread ("" when none). */
 const char* kh_last_error(void);
 
+/* Debug mode (flags bit 0): every entry point waits for the stream after each kernel it launches
+ * and returns KH_ERR_HIP naming itself if the kernel faulted, instead of the fault surfacing at a
+ * later synchronising call; skipped while a graph capture is open.  0 turns it off (the default).
+ * The reference's knownIssues/shader.md:151-175 proposes the same per-dispatch check for WGSL. */
+int kh_set_debug(int flags);
+
 /* Caching device allocator (size classes, stream-ordered reuse on the single library stream).
  * Replaces WebGPUStorage's GPUBuffer creation/destroy and its buffer pooling
  * (reference: packages/backend-webgpu/src/base/storage.ts:68-106, :114-143). */

@@ -11,6 +11,7 @@ include/kandle_hip.h (libkandle_hip.so, built by `python -m kandle_amd.build`).
 """
 from . import env, functional
 from ._lib import KandleHipError
+from .memory import is_in_tidy_scope, keep, tidy
 from .backend import HipBackend, register_hip_kernels
 from .registry import SimpleOperatorRegistry
 from .tensor import HipStorage, HipTensorHandle, Tensor
@@ -25,4 +26,7 @@ __all__ = [
     "SimpleOperatorRegistry",
     "Tensor",
     "register_hip_kernels",
+    "tidy",
+    "keep",
+    "is_in_tidy_scope",
 ]

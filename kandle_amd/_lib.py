@@ -34,6 +34,7 @@ _vpp = C.POINTER(C.c_void_p)
 SIGNATURES = {
     "kh_init": [_i],
     "kh_device_count": [C.POINTER(C.c_int)],
+    "kh_set_debug": [_i],
     "kh_alloc": [C.POINTER(C.c_void_p), _sz],
     "kh_free": [_vp],
     "kh_empty_cache": [],

@@ -706,6 +706,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
     set_error("kh_decode_attention: launch failed: %s", hipGetErrorString(e));
     return KH_ERR_HIP;
   }
+  KH_DEBUG_SYNC();
   return KH_OK;
 }
 
@@ -999,6 +1000,7 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
     set_error("kh_decode_attention_block: launch failed: %s", hipGetErrorString(e));
     return KH_ERR_HIP;
   }
+  if (rc == KH_OK) KH_DEBUG_SYNC();
   return rc;
 }
 

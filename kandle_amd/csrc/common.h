@@ -56,8 +56,25 @@ bool launch_gemv_attn_merge(const float* part, const AttnMerge& am, const uint16
     }                                                                  \
   } while (0)
 
-// After a launch: report launch-configuration errors immediately.
-#define KH_CHECK_LAUNCH() KH_CHECK_HIP(hipGetLastError())
+// Debug mode (kh_set_debug): after every launch, wait for the stream and report an asynchronous
+// fault at the call that launched the kernel.  Off while a graph capture is open.
+bool debug_sync();
+int debug_check(const char* where, const char* file, int line);
+
+#define KH_DEBUG_SYNC()                                                      \
+  do {                                                                       \
+    if (::kh::debug_sync()) {                                                \
+      const int _rc = ::kh::debug_check(__func__, __FILE__, __LINE__);       \
+      if (_rc != KH_OK) return _rc;                                          \
+    }                                                                        \
+  } while (0)
+
+// After a launch: report launch-configuration errors immediately (and, in debug mode, faults).
+#define KH_CHECK_LAUNCH()                 \
+  do {                                    \
+    KH_CHECK_HIP(hipGetLastError());      \
+    KH_DEBUG_SYNC();                      \
+  } while (0)
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

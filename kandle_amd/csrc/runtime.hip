@@ -26,6 +26,7 @@ struct State {
   int device = -1;
   hipStream_t stream = nullptr;
   GraphObj* capturing = nullptr;  // graph whose stream capture is open
+  int debug = 0;                  // kh_set_debug flags
 };
 State g_state;
 
@@ -180,6 +181,19 @@ hipStream_t stream() { return g_state.stream; }
 bool initialized() { return g_state.init; }
 int current_device() { return g_state.init ? g_state.device : -1; }
 
+bool debug_sync() { return (g_state.debug & 1) != 0 && g_state.capturing == nullptr && g_state.stream != nullptr; }
+
+int debug_check(const char* where, const char* file, int line) {
+  const hipError_t e = hipStreamSynchronize(g_state.stream);
+  const hipError_t e2 = hipGetLastError();
+  if (e != hipSuccess || e2 != hipSuccess) {
+    set_error("%s: a kernel it launched failed on the device: %s (%s:%d; debug mode)", where,
+              hipGetErrorString(e != hipSuccess ? e : e2), file, line);
+    return KH_ERR_HIP;
+  }
+  return KH_OK;
+}
+
 void* scratch_alloc(size_t bytes) {
   void* p = nullptr;
   if (g_alloc.alloc(&p, bytes) != KH_OK) return nullptr;
@@ -230,6 +244,12 @@ int kh_init(int device) {
 }
 
 const char* kh_last_error(void) { return g_err; }
+
+int kh_set_debug(int flags) {
+  KH_REQUIRE(flags >= 0 && flags <= 1, "kh_set_debug: unknown flags %d", flags);
+  g_state.debug = flags;
+  return KH_OK;
+}
 
 int kh_alloc(void** ptr, size_t bytes) {
   KH_REQUIRE_INIT();

@@ -744,6 +744,7 @@ static int sample_selected(const float* logits, int n, int greedy, double inv_t,
     set_error("kh_sample: launch failed: %s", hipGetErrorString(err));
     return KH_ERR_HIP;
   }
+  KH_DEBUG_SYNC();
   return KH_OK;
 }
 
@@ -823,6 +824,7 @@ int kh_sample(const float* logits, int64_t vocab, int do_sample, double temperat
     set_error("kh_sample: launch failed: %s", hipGetErrorString(err));
     return KH_ERR_HIP;
   }
+  KH_DEBUG_SYNC();
   return KH_OK;
 }
 

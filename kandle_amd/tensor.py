@@ -243,6 +243,9 @@ class Tensor:
                 shape = arr.shape
             handle = get_backend("hip").create_tensor_handle(shape, dtype, arr)
         self.handle = handle
+        from .memory import _track
+
+        _track(self)
 
     @property
     def shape(self):

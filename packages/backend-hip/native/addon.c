@@ -220,6 +220,8 @@ static napi_value big_ptr(napi_env env, void* p) {
 /* ---------------------------------------------------------------- runtime ---------------------- */
 FN(init, 1) int dev = arg_int(A, 0); CALL(kh_init(dev))
 
+FN(setDebug, 1) int f = arg_int(A, 0); CALL(kh_set_debug(f))
+
 static napi_value js_deviceCount(napi_env env, napi_callback_info info) {
   (void)info;
   int n = 0;
@@ -477,7 +479,7 @@ FN(gemvFused, 15)
 
 static napi_value module_init(napi_env env, napi_value exports) {
   napi_property_descriptor d[] = {
-      EXPORT(init), EXPORT(deviceCount), EXPORT(lastError), EXPORT(alloc), EXPORT(free), EXPORT(emptyCache),
+      EXPORT(init), EXPORT(deviceCount), EXPORT(lastError), EXPORT(setDebug), EXPORT(alloc), EXPORT(free), EXPORT(emptyCache),
       EXPORT(allocStats), EXPORT(memcpyH2D), EXPORT(memcpyD2H), EXPORT(memcpyD2D), EXPORT(synchronize),
       EXPORT(eventCreate), EXPORT(eventDestroy), EXPORT(eventRecord), EXPORT(eventElapsedMs),
       EXPORT(graphBeginCapture), EXPORT(graphEndCapture), EXPORT(graphLaunch), EXPORT(graphDestroy),

@@ -214,3 +214,29 @@ def test_allocator_reuses_freed_blocks(hip):
     assert after["n_cache_hits"] > before["n_cache_hits"]
     assert after["live_bytes"] == live
     t2.dispose()
+
+
+def test_tidy_returns_intermediate_device_memory(hip):
+    """tidy around real ops: the intermediates' blocks go back to the allocator (live bytes return
+    to the level before the scope plus the returned tensor), the returned and kept tensors stay
+    usable (memory.ts:83-119, :190-193)."""
+    from kandle_amd import _lib, keep, tidy
+
+    x, xh = seeded(70, (256, 256))
+    base = _lib.alloc_stats()["live_bytes"]
+    kept = {}
+
+    def body():
+        y = F.silu(x)                                   # intermediate
+        z = F.add(y, x)                                 # intermediate
+        kept["k"] = keep(F.mul(z, z))
+        return F.mul(z, x)
+
+    out = tidy(body)
+    live = _lib.alloc_stats()["live_bytes"]
+    assert live - base == 2 * 256 * 256 * 4, (live, base)   # the returned and the kept tensor only
+    silu = xh / (1 + np.exp(-np.clip(xh, -88, 88)))
+    np.testing.assert_allclose(out.numpy(), (silu + xh) * xh, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(kept["k"].numpy(), (silu + xh) ** 2, rtol=1e-5, atol=1e-5)
+    out.dispose()
+    kept["k"].dispose()
