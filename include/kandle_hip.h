@@ -323,6 +323,33 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
 int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,
                    int64_t n_half, int64_t k);
 
+/* The split count kh_gemm uses for a bf16 [m, k] x [n, k]^T product with contiguous, 16-byte
+ * aligned operands (1: not split).  A caller that splits the same product with
+ * kh_gemm_splitk_partials and adds the partials in split order reproduces kh_gemm bit for bit. */
+int kh_gemm_split_count(int64_t m, int64_t n, int64_t k, int* splits);
+
+/* The split-K stage of kh_gemm alone: part[s][i][j] (fp32, s < splits, row-major [m, n], split s
+ * at part + s*m*n) = the sum over split s's k range of a[i, :] * b[j, :] (bf16 a [m, k] with row
+ * stride lda, b [n, k] with row stride ldb), k ranges of ceil(k / splits) rounded up to 128.
+ * splits must equal kh_gemm_split_count's count for this shape (and the operands meet the MFMA
+ * path's alignment: 16-byte aligned, k, lda, ldb multiples of 8).  The producer half of the
+ * projection + residual + RMSNorm fusion below (no reference counterpart as a separate step:
+ * it is the matmul of packages/core/src/dispatch/matmulOps.ts:32-125 before its epilogue). */
+int kh_gemm_splitk_partials(const void* a, int64_t lda, const void* b, int64_t ldb, float* part,
+                            int64_t m, int64_t n, int64_t k, int splits);
+
+/* Residual add of split-K partials followed by RMSNorm, one launch:
+ *   x[r, :] = (part[0][r, :] + ... + part[splits-1][r, :]) + x[r, :]    (fp32, summed in split
+ *             order from 0 -- what kh_gemm's split reduction with cin = x, beta = 1 stores)
+ *   y[r, :] = rms_norm(x[r, :]) * w                                       (as kh_rms_norm)
+ * part[s] starts s * split_stride elements after part; x (fp32) and y (out_dtype, bf16 or fp32,
+ * like w) are contiguous [rows, n]; n % 8 == 0, n <= 2048, splits <= 8, 16-byte aligned pointers.
+ * Fuses the residual add after o_proj / down_proj with the RMSNorm that follows it
+ * (reference: packages/model-utils/src/qwen3/decoder_layer.ts:224-238 residual adds;
+ * packages/backend-webgpu/src/kernels/normalize/shaderBuilder.ts:394-411 RMSNorm). */
+int kh_add_rms_norm(const float* part, int splits, int64_t split_stride, float* x, const void* w, void* y,
+                    int64_t rows, int64_t n, float eps, int out_dtype);
+
 /* One-row projection (decode) with the producing op fused in front of it:
  *   c[j] = alpha * sum_i x'[i] * w[j, i] + beta * cin[j] (+ bias[j]),  j < n, i < k,
  * w bf16 [n, k] with row stride ldw (the nn.Linear weight), c/cin/bias of out_dtype, where x' is

@@ -547,11 +547,21 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
 }
 
 constexpr int kWaves = 8;  // waves per workgroup: query rows of 32 * 8 / G, one kv head
+// Short prompts: a grid of fewer than kSmallGrid 8-wave workgroups leaves most CUs idle and its time
+// is the key loop of the last query block.  Such launches use workgroups of kSmallWaves waves over
+// kSmallBN-key tiles instead: BMQ shrinks with the wave count, so there are 8 / kSmallWaves times
+// as many workgroups, and each wave has a SIMD to itself.
+constexpr int kSmallGrid = 256;
+constexpr int kSmallWaves = 4;
+constexpr int kSmallBN = 128;
 
-template <bool CAUSAL>
+template <int BN, int WAVES, bool CAUSAL>
 void launch_fwd(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
-                const AttnStrides& st, float scale, int nqb, int nblk) {
-  flash_fwd_kernel<128, kWaves, 1, CAUSAL><<<nblk, kWaves * 64, 0, stream()>>>(
+                const AttnStrides& st, float scale) {
+  const int BMQ = 32 * (WAVES / (hq / hkv));
+  const int nqb = (lq + BMQ - 1) / BMQ;
+  const int nblk = nqb * batch * hkv;
+  flash_fwd_kernel<BN, WAVES, 1, CAUSAL><<<nblk, WAVES * 64, 0, stream()>>>(
       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, lq, lk, st, scale,
       nqb, nullptr, MaskArgs{});
 }
@@ -583,11 +593,16 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
-  const int nblk = (int)nblk64;
-  if (causal)
-    launch_fwd<true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
-  else
-    launch_fwd<false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, nqb, nblk);
+  if (nblk64 < kSmallGrid && G <= kSmallWaves) {
+    if (causal)
+      launch_fwd<kSmallBN, kSmallWaves, true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+    else
+      launch_fwd<kSmallBN, kSmallWaves, false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  } else if (causal) {
+    launch_fwd<128, kWaves, true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  } else {
+    launch_fwd<128, kWaves, false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  }
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -53,9 +53,10 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 // B-operand = A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are
 // raw buffer loads (rows past M / N and columns past the k range read as zero without a branch).
 //
-// SPLIT: S workgroups share one output tile, each summing K / S of the products into fp32
-// partials of its own; gemm_splitk_reduce_kernel then adds the S partials in split order
-// (deterministic whichever workgroup finished last) and applies the epilogue.
+// SPLIT: S workgroups share one output tile, each summing its K range (kchunk columns, a multiple
+// of 128) of the products into fp32 partials part[split][m][n] (row-major, leading dimension N);
+// gemm_splitk_reduce_kernel -- or a consumer such as kh_add_rms_norm -- then adds the S partials
+// in split order (deterministic whichever workgroup finished last) and applies the epilogue.
 // =============================================================================================
 constexpr int G_THREADS = 256;
 constexpr int kGemmPrefetch = 3;        // k-steps of global loads in flight per workgroup
@@ -183,19 +184,23 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   }
 
   if constexpr (SPLIT) {
-    // Raw fp32 partial of this split: part[tile][split][m - m0][n - n0]; the reduction kernel adds
-    // the splits in order and applies the epilogue.
-    float* mine = part + ((int64_t)tile * splits + split) * (GM * GN);
+    // Raw fp32 partial of this split: part[split][m][n] (N % 4 == 0, so four consecutive n of a
+    // register group are all in range or all out).
+    float* mine = part + (int64_t)split * M * N;
 #pragma unroll
-    for (int b = 0; b < WT; ++b)
+    for (int b = 0; b < WT; ++b) {
+      const int m = m0 + wm + 32 * b + r;
+      if (m >= M) continue;
 #pragma unroll
       for (int a = 0; a < WT; ++a)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int ml = wm + 32 * b + r, nl = wn + 32 * a + 8 * q + 4 * g;
-          *reinterpret_cast<float4*>(mine + ml * GN + nl) =
+          const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
+          if (n >= N) continue;
+          *reinterpret_cast<float4*>(mine + (int64_t)m * N + n) =
               make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
         }
+    }
     return;
   }
 
@@ -243,31 +248,22 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   }
 }
 
-// Split-K reduction: one thread per four consecutive outputs of a tile, so every partial of the
-// whole output is in flight at once; the splits are added in split order, then the epilogue.
-template <typename TO, int GT>
+// Split-K reduction: one thread per four consecutive outputs (N % 4 == 0), so every partial of the
+// whole output is in flight at once; the splits are added in split order from 0, then the epilogue.
+template <typename TO>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits,
                                                                   TO* C, int64_t ldc, const TO* cin, int64_t ldcin,
                                                                   const TO* __restrict__ bias, int M, int N,
-                                                                  float alpha, float beta, int tiles_n,
-                                                                  int tiles_m_colmajor, int tiles) {
-  // Tile numbering as in the GEMM kernel that wrote the partials: row-major over n tiles, or
-  // column-major (tiles_m_colmajor = the number of m tiles) for the prefetching kernel.
-  constexpr int Q = GT * GT / 4;   // float4 groups per tile
+                                                                  float alpha, float beta) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)tiles * Q) return;
-  const int tile = (int)(gid / Q), idx = (int)(gid % Q) * 4;
-  const int tm = tiles_m_colmajor ? tile % tiles_m_colmajor : tile / tiles_n;
-  const int tn = tiles_m_colmajor ? tile / tiles_m_colmajor : tile % tiles_n;
-  const int ml = idx / GT, nl = idx % GT;
-  const int m = tm * GT + ml, n = tn * GT + nl;
-  if (m >= M || n >= N) return;
-  const float* tp = part + (int64_t)tile * splits * (GT * GT) + idx;
+  const int64_t mn = (int64_t)M * N;
+  if (gid * 4 >= mn) return;
+  const int m = (int)(gid * 4 / N), n = (int)(gid * 4 % N);
+  const float* tp = part + gid * 4;
   float4 pv[kMaxSplits];
 #pragma unroll
   for (int s2 = 0; s2 < kMaxSplits; ++s2)
-    pv[s2] = s2 < splits ? *reinterpret_cast<const float4*>(tp + (int64_t)s2 * (GT * GT))
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    pv[s2] = s2 < splits ? *reinterpret_cast<const float4*>(tp + s2 * mn) : make_float4(0.f, 0.f, 0.f, 0.f);
   float v[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s2 = 0; s2 < kMaxSplits; ++s2) {
@@ -278,8 +274,8 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   }
   const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = (n + e < N) ? epilogue<TO>(v[e], alpha, beta, cin, ldcin, bias, m, n + e) : 0.f;
-  store4<TO>(C, (int64_t)m * ldc + n, v, vec, min(4, N - n));
+  for (int e = 0; e < 4; ++e) v[e] = epilogue<TO>(v[e], alpha, beta, cin, ldcin, bias, m, n + e);
+  store4<TO>(C, (int64_t)m * ldc + n, v, vec, 4);
 }
 
 // =============================================================================================
@@ -643,6 +639,70 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
     }
 }
 
+// Launch plan of the MFMA tile kernel for a bf16 [M, K] x [N, K]^T product.
+struct GemmPlan {
+  bool mfma = false;  // the MFMA tile kernel applies (else the skinny or generic kernel)
+  int wt = 1, tiles_m = 0, tiles_n = 0, splits = 1, kchunk = 0;
+  int64_t tiles = 0;
+};
+
+// aligned: both operands start on 16 bytes.
+GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, bool bf16, int trans_b) {
+  GemmPlan p;
+  const int64_t lim = int64_t(1) << 31;
+  if (!(bf16 && trans_b && M > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned &&
+        (int64_t)g_tile(2) * lda * 2 < lim && (int64_t)g_tile(2) * ldb * 2 < lim))
+    return p;
+  p.mfma = true;
+  // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the
+  // workgroups, and when even those leave CUs idle and K is long, split K over up to 8 workgroups.
+  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  p.wt = t128 >= kGemmT128Min ? 2 : 1;
+  const int gt = g_tile(p.wt);
+  p.tiles_m = (M + gt - 1) / gt;
+  p.tiles_n = (N + gt - 1) / gt;
+  p.tiles = (int64_t)p.tiles_m * p.tiles_n;
+  p.kchunk = K;
+  if (p.tiles < 256 && K >= 1024 && N % 4 == 0 && (p.wt == 1 || kGemmSplit128)) {
+    const int64_t want = kGemmSplitTarget / p.tiles;
+    const int splits = want < 1 ? 1 : (want > kMaxSplits ? kMaxSplits : (int)want);
+    if (splits > 1) {
+      p.kchunk = ((K + splits - 1) / splits + 127) / 128 * 128;   // whole k-steps of 64 and 128
+      p.splits = (K + p.kchunk - 1) / p.kchunk;
+    }
+  }
+  return p;
+}
+
+// The MFMA tile kernel for plan p: C (or, with part != nullptr and p.splits > 1, only the fp32
+// partials part[split][m][n]).
+template <typename TO>
+void launch_gemm_tiles(const GemmPlan& p, const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
+                       int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI, int M, int N, int K, float alpha,
+                       float beta, float* part) {
+  constexpr int PF = kGemmPrefetch;
+  const int splits = part ? p.splits : 1;
+  const int nblk = (int)(p.tiles * splits);
+  // k-step 128 doubles the bytes per round trip but also the LDS per workgroup (70 KB: two per
+  // CU); with more than two tiles per CU the 64 k-step's occupancy (four per CU) wins.
+  const bool ks128 = p.tiles * splits <= 512;
+  if (p.wt == 2 && splits > 1)
+    gemm_bf16_nt_kernel<TO, 2, 64, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, splits, p.kchunk, part);
+  else if (p.wt == 2)
+    gemm_bf16_nt_kernel<TO, 2, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, 1, K, nullptr);
+  else if (splits > 1)
+    gemm_bf16_nt_kernel<TO, 1, 128, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, splits, p.kchunk, part);
+  else if (ks128)
+    gemm_bf16_nt_kernel<TO, 1, 128, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, 1, K, nullptr);
+  else
+    gemm_bf16_nt_kernel<TO, 1, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, 1, K, nullptr);
+}
+
 template <typename T, typename TO>
 int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, const void* cin,
                 int64_t ldcin, const void* bias, int M, int N, int K, float alpha, float beta, int trans_b) {
@@ -652,63 +712,22 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
   const TO* CI = (const TO*)cin;
   const TO* BI = (const TO*)bias;
   constexpr bool is_bf16 = sizeof(T) == 2;
-  const int64_t lim = int64_t(1) << 31;
-  if (is_bf16 && trans_b && M > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) &&
-      aligned16(b) && (int64_t)g_tile(2) * lda * 2 < lim && (int64_t)g_tile(2) * ldb * 2 < lim) {
-    // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the
-    // workgroups, and when even those leave CUs idle and K is long, split K over up to 8 workgroups.
-    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-    const int wt = t128 >= kGemmT128Min ? 2 : 1;
-    const int gt = g_tile(wt);
-    const int tiles_m = (M + gt - 1) / gt, tiles_n = (N + gt - 1) / gt;
-    const int64_t tiles = (int64_t)tiles_m * tiles_n;
-    KH_REQUIRE(tiles <= INT32_MAX / 8, "kh_gemm: grid too large");
-    int splits = 1;
-    if (tiles < 256 && K >= 1024 && (wt == 1 || kGemmSplit128)) {
-      const int64_t want = kGemmSplitTarget / tiles;
-      splits = want < 1 ? 1 : (want > kMaxSplits ? kMaxSplits : (int)want);
-    }
-    int kchunk = K;
-    float* part = nullptr;
-    if (splits > 1) {
-      kchunk = ((K + splits - 1) / splits + 127) / 128 * 128;   // whole k-steps of 64 and 128
-      splits = (K + kchunk - 1) / kchunk;
-      part = (float*)scratch_alloc((size_t)splits * tiles * gt * gt * sizeof(float));
-      if (!part) {
-        splits = 1;
-        kchunk = K;
+  const GemmPlan p = gemm_plan(aligned16(a) && aligned16(b), lda, ldb, M, N, K, is_bf16, trans_b);
+  if constexpr (is_bf16) {
+    if (p.mfma) {
+      KH_REQUIRE(p.tiles <= INT32_MAX / 8, "kh_gemm: grid too large");
+      float* part = nullptr;
+      if (p.splits > 1) part = (float*)scratch_alloc((size_t)p.splits * M * N * sizeof(float));
+      launch_gemm_tiles<TO>(p, (const uint16_t*)A, lda, (const uint16_t*)B, ldb, C, ldc, CI, ldcin, BI, M, N, K,
+                            alpha, beta, part);
+      if (part) {
+        gemm_splitk_reduce_kernel<TO><<<(int)(((int64_t)M * N / 4 + 255) / 256), 256, 0, stream()>>>(
+            part, p.splits, C, ldc, CI, ldcin, BI, M, N, alpha, beta);
+        scratch_free(part);  // stream-ordered reuse only
       }
+      KH_CHECK_LAUNCH();
+      return KH_OK;
     }
-    // k-step 128 doubles the bytes per round trip but also the LDS per workgroup (70 KB: two per
-    // CU); with more than two tiles per CU the 64 k-step's occupancy (four per CU) wins.
-    const bool ks128 = tiles * splits <= 512;
-    const int nblk = (int)(tiles * splits);
-    if constexpr (is_bf16) {
-      constexpr int PF = kGemmPrefetch;
-      if (wt == 2 && splits > 1) {
-        gemm_bf16_nt_kernel<TO, 2, 64, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
-            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
-        gemm_splitk_reduce_kernel<TO, 128><<<(int)((tiles * 128 * 128 / 4 + 255) / 256), 256, 0, stream()>>>(
-            part, splits, C, ldc, CI, ldcin, BI, M, N, alpha, beta, tiles_n, PF > 1 ? tiles_m : 0, (int)tiles);
-      } else if (wt == 2) {
-        gemm_bf16_nt_kernel<TO, 2, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
-            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
-      } else if (splits > 1) {
-        gemm_bf16_nt_kernel<TO, 1, 128, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
-            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
-        gemm_splitk_reduce_kernel<TO, 64><<<(int)((tiles * 64 * 64 / 4 + 255) / 256), 256, 0, stream()>>>(
-            part, splits, C, ldc, CI, ldcin, BI, M, N, alpha, beta, tiles_n, PF > 1 ? tiles_m : 0, (int)tiles);
-      } else if (ks128) {
-        gemm_bf16_nt_kernel<TO, 1, 128, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
-            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
-      } else {
-        gemm_bf16_nt_kernel<TO, 1, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
-            A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
-      }
-    }
-    if (part) scratch_free(part);  // stream-ordered reuse only
-    KH_CHECK_LAUNCH();
-    return KH_OK;
   }
   if constexpr (is_bf16) {
     if (trans_b && M == 1) {
@@ -793,6 +812,34 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
   if (dtype == KH_BF16)
     return launch_gemm<uint16_t, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
   return launch_gemm<float, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
+}
+
+int kh_gemm_split_count(int64_t m, int64_t n, int64_t k, int* splits) {
+  KH_REQUIRE(splits != nullptr, "kh_gemm_split_count: null pointer");
+  KH_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX,
+             "kh_gemm_split_count: bad extents");
+  // bf16 operands, contiguous and 16-byte aligned
+  const GemmPlan p = gemm_plan(true, k, k, (int)m, (int)n, (int)k, true, 1);
+  *splits = p.mfma ? p.splits : 1;
+  return KH_OK;
+}
+
+int kh_gemm_splitk_partials(const void* a, int64_t lda, const void* b, int64_t ldb, float* part, int64_t m,
+                            int64_t n, int64_t k, int splits) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(m > 0 && n > 0 && k > 0 && m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX,
+             "kh_gemm_splitk_partials: bad extents");
+  KH_REQUIRE(a && b && part, "kh_gemm_splitk_partials: null pointer");
+  KH_REQUIRE(lda >= k && ldb >= k, "kh_gemm_splitk_partials: leading dimension too small");
+  const GemmPlan p = gemm_plan(aligned16(a) && aligned16(b), lda, ldb, (int)m, (int)n, (int)k, true, 1);
+  KH_REQUIRE(p.mfma && p.splits > 1 && p.splits == splits,
+             "kh_gemm_splitk_partials: this product is not split %d ways (kh_gemm_split_count gives the count; "
+             "operands must be 16-byte aligned with k and the leading dimensions multiples of 8)", splits);
+  KH_REQUIRE(p.tiles <= INT32_MAX / 8, "kh_gemm_splitk_partials: grid too large");
+  launch_gemm_tiles<float>(p, (const uint16_t*)a, lda, (const uint16_t*)b, ldb, nullptr, n, nullptr, 0, nullptr,
+                           (int)m, (int)n, (int)k, 1.f, 0.f, part);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,

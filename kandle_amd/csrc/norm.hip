@@ -5,6 +5,8 @@
 //
 // RMSNorm follows the reference formula exactly: rms = sqrt(sum(x^2)/N + eps), scale = 1/rms,
 // y = (x * scale) * w   (reference: packages/backend-webgpu/src/kernels/normalize/shaderBuilder.ts:394-411).
+#include <type_traits>
+
 #include "common.h"
 
 using namespace kh;
@@ -48,6 +50,42 @@ struct Vec8<float> {
 };
 
 // ---- RMSNorm: one wave per row, row kept in registers (n <= 64 * 8 * CPL) -----------------
+// The row's math once its values v are in registers (lane chunk c holds elements 8 (lane + 64 c)
+// .. + 7): sum of squares, 1 / rms, y = (v * inv) * w.  Shared by the plain and the fused
+// residual kernels, so both round identically.
+template <typename TO, int CPL>
+__device__ __forceinline__ void rms_row(const float (&v)[CPL][8], const typename Vec8<TO>::Raw (&rw)[CPL],
+                                       bool has_w, int lane, int nchunks, int n, float eps, TO* yr) {
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    if (lane + 64 * c < nchunks) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / (float)n + eps);
+  const float inv = 1.0f / rms;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch < nchunks) {
+      float o[8];
+      if (has_w) {
+        float wv[8];
+        Vec8<TO>::cvt(rw[c], wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = (v[c][j] * inv) * wv[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = v[c][j] * inv;
+      }
+      Vec8<TO>::store(yr + ch * 8, o);
+    }
+  }
+}
+
 // x has element type TI; w and y have TO (e.g. a float32 residual stream normalised into bf16).
 // Every load of the row and of the weights is issued before any math (lanes past the row end load
 // the last chunk again and ignore it), so a wave waits for one memory round trip, not one per chunk.
@@ -69,36 +107,57 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(const TI* __restrict_
     for (int c = 0; c < CPL; ++c) rw[c] = Vec8<TO>::ld(w + min(lane + 64 * c, nchunks - 1) * 8);
   }
   float v[CPL][8];
-  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) Vec8<TI>::cvt(rx[c], v[c]);
+  rms_row<TO, CPL>(v, rw, w != nullptr, lane, nchunks, n, eps, y + row * ys);
+}
+
+// ---- Split-K residual add + RMSNorm (kh_add_rms_norm) ----------------------------------------
+// x[row] = (sum over splits s, in order from 0, of part[s][row]) + x[row] -- the fp32 result the
+// GEMM's split reduction with a beta = 1 residual writes -- then y[row] = RMSNorm(x[row]) * w as
+// rms_norm_vec_kernel computes it.  Rows are contiguous (stride n); part[s] starts s * pstride
+// elements after part.
+constexpr int kAddNormMaxSplits = 8;
+template <typename TO, int CPL>
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(const float* __restrict__ part, int splits,
+                                                            int64_t pstride, float* x, const TO* __restrict__ w,
+                                                            TO* __restrict__ y, int64_t rows, int n, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nchunks = n >> 3;
+  float* xr = x + row * n;
+  const float* pr = part + row * n;
+  typename Vec8<float>::Raw rx[CPL], rp[kAddNormMaxSplits][CPL];
+  typename Vec8<TO>::Raw rw[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    Vec8<TI>::cvt(rx[c], v[c]);
-    if (lane + 64 * c < nchunks) {
+    const int off = min(lane + 64 * c, nchunks - 1) * 8;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
-    }
+    for (int s2 = 0; s2 < kAddNormMaxSplits; ++s2)
+      if (s2 < splits) rp[s2][c] = Vec8<float>::ld(pr + s2 * pstride + off);
+    rx[c] = Vec8<float>::ld(xr + off);
+    rw[c] = Vec8<TO>::ld(w + off);
   }
-  ss = wave_sum(ss);
-  const float rms = sqrtf(ss / (float)n + eps);
-  const float inv = 1.0f / rms;
-  TO* yr = y + row * ys;
+  float v[CPL][8];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < nchunks) {
-      float o[8];
-      if (w != nullptr) {
-        float wv[8];
-        Vec8<TO>::cvt(rw[c], wv);
+    float xo[8], pv[8];
+    Vec8<float>::cvt(rx[c], xo);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = (v[c][j] * inv) * wv[j];
-      } else {
+    for (int j = 0; j < 8; ++j) v[c][j] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = v[c][j] * inv;
+    for (int s2 = 0; s2 < kAddNormMaxSplits; ++s2)
+      if (s2 < splits) {
+        Vec8<float>::cvt(rp[s2][c], pv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[c][j] += pv[j];
       }
-      Vec8<TO>::store(yr + ch * 8, o);
-    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[c][j] += xo[j];
+    if (lane + 64 * c < nchunks) Vec8<float>::store(xr + (lane + 64 * c) * 8, v[c]);
   }
+  rms_row<TO, CPL>(v, rw, true, lane, nchunks, n, eps, y + row * n);
 }
 
 // Generic RMSNorm (any n, any alignment): one wave per row, two passes over the row.
@@ -344,6 +403,43 @@ int kh_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* y, int
   if (dtype == KH_BF16 && out_dtype == KH_F32)
     return launch_rms_norm<uint16_t, float>(x, x_row_stride, w, y, y_row_stride, rows, n, eps);
   KH_REQUIRE(false, "kh_rms_norm: unsupported dtypes (in %d, out %d)", dtype, out_dtype);
+}
+
+int kh_add_rms_norm(const float* part, int splits, int64_t split_stride, float* x, const void* w, void* y,
+                    int64_t rows, int64_t n, float eps, int out_dtype) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(rows >= 0 && n > 0, "kh_add_rms_norm: bad extents (rows %lld, n %lld)", (long long)rows, (long long)n);
+  if (rows == 0) return KH_OK;
+  KH_REQUIRE(part && x && w && y, "kh_add_rms_norm: null pointer");
+  KH_REQUIRE(splits >= 1 && splits <= kAddNormMaxSplits, "kh_add_rms_norm: splits %d outside [1, %d]", splits,
+             kAddNormMaxSplits);
+  KH_REQUIRE(split_stride >= rows * n, "kh_add_rms_norm: split_stride below rows * n");
+  KH_REQUIRE(n % 8 == 0 && n <= 64 * 8 * 4 && split_stride % 8 == 0,
+             "kh_add_rms_norm: n must be a multiple of 8 up to 2048 (and split_stride a multiple of 8)");
+  KH_REQUIRE(aligned16(part) && aligned16(x) && aligned16(w) && aligned16(y),
+             "kh_add_rms_norm: pointers must be 16-byte aligned");
+  KH_REQUIRE(out_dtype == KH_BF16 || out_dtype == KH_F32, "kh_add_rms_norm: unsupported output dtype %d", out_dtype);
+  const int waves = 4;
+  const int64_t grid = (rows + waves - 1) / waves;
+  KH_REQUIRE(grid <= INT32_MAX, "kh_add_rms_norm: too many rows");
+  auto run = [&](auto* wp, auto* yp) {
+    using TO = std::remove_const_t<std::remove_pointer_t<decltype(wp)>>;
+    if (n <= 64 * 8)
+      add_rms_norm_kernel<TO, 1><<<(int)grid, 64 * waves, 0, stream()>>>(part, splits, split_stride, x, wp, yp, rows,
+                                                                         (int)n, eps);
+    else if (n <= 64 * 8 * 2)
+      add_rms_norm_kernel<TO, 2><<<(int)grid, 64 * waves, 0, stream()>>>(part, splits, split_stride, x, wp, yp, rows,
+                                                                         (int)n, eps);
+    else
+      add_rms_norm_kernel<TO, 4><<<(int)grid, 64 * waves, 0, stream()>>>(part, splits, split_stride, x, wp, yp, rows,
+                                                                         (int)n, eps);
+  };
+  if (out_dtype == KH_BF16)
+    run((const uint16_t*)w, (uint16_t*)y);
+  else
+    run((const float*)w, (float*)y);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out, const void* v, void* v_out,

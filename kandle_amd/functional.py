@@ -293,6 +293,19 @@ def linear_swiglu(input: Tensor, weight_gu: Tensor) -> Tensor:
     return _wrap(out)
 
 
+def linear_add_rms_norm(input: Tensor, weight: Tensor, residual: Tensor, norm_weight: Tensor, eps: float,
+                        rows=None) -> Tensor:
+    """residual += input W^T in place (fp32) and returns rms_norm(residual) * norm_weight in
+    norm_weight's dtype -- a decoder sub-block's closing projection, its residual add and the next
+    RMSNorm (decoder_layer.ts:224-238, RMSNorm.ts:92-99).  rows = (r0, r1) limits the add and the
+    norm to those residual rows (the result has r1 - r0 rows)."""
+    r0, r1 = rows if rows is not None else (0, residual.shape[0])
+    out = _new(residual, (r1 - r0, residual.shape[1]), norm_weight.dtype)
+    _kernel(input, "linear_add_rms_norm")(input.handle, weight.handle, residual.handle, norm_weight.handle,
+                                          float(eps), out, rows)
+    return _wrap(out)
+
+
 def silu_mul(gate: Tensor, up: Tensor) -> Tensor:
     out = _new(gate, gate.shape)
     _kernel(gate, "silu_mul")(gate.handle, up.handle, out)

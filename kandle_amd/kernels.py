@@ -686,6 +686,57 @@ def linear_swiglu(x, w_gu, output) -> None:
               _vp(output.data_ptr()), ldh, m, I, H)
 
 
+def gemm_split_count(m: int, n: int, k: int) -> int:
+    """The K split kh_gemm uses for a contiguous bf16 [m, k] x [n, k]^T product (1: none)."""
+    out = C.c_int(0)
+    _lib.call("kh_gemm_split_count", int(m), int(n), int(k), C.byref(out))
+    return out.value
+
+
+def linear_add_rms_norm(x, w, residual, norm_weight, eps, output, rows=None) -> None:
+    """residual += x W^T (fp32, in place) and output = rms_norm(residual) * norm_weight: the
+    projection that closes a decoder sub-block, its residual add and the RMSNorm that opens the next
+    (decoder_layer.ts:224-238 with RMSNorm.ts:92-99).  x bf16 [M, K] and w bf16 [N, K] with
+    contiguous rows, residual fp32 [M, N] contiguous, norm_weight [N] and output [R, N] of one dtype
+    (bf16 or fp32).  rows = (r0, r1) restricts the add and the norm to residual rows r0 .. r1 - 1
+    (output has r1 - r0 rows; the other residual rows are left as they were), default all rows.
+    When kh_gemm would split K for this shape, the partials go straight into kh_add_rms_norm
+    (two launches instead of GEMM + split reduction + RMSNorm); the values are those of the
+    separate launches bit for bit either way."""
+    M, K = x.shape
+    N = w.shape[0]
+    r0, r1 = rows if rows is not None else (0, M)
+    if x.dtype != BFLOAT16 or w.dtype != BFLOAT16 or residual.dtype != FLOAT32:
+        raise TypeError("linear_add_rms_norm: bf16 x and w with an fp32 residual expected")
+    if w.shape[1] != K or tuple(residual.shape) != (M, N) or tuple(output.shape) != (r1 - r0, N):
+        raise ValueError("linear_add_rms_norm: shapes do not match")
+    if norm_weight.numel != N or norm_weight.dtype != output.dtype:
+        raise ValueError("linear_add_rms_norm: norm_weight must have N elements and the output dtype")
+    if not (0 <= r0 < r1 <= M):
+        raise ValueError(f"linear_add_rms_norm: bad row range {rows} for {M} rows")
+    for h, nm in ((x, "x"), (w, "w"), (residual, "residual"), (output, "output"), (norm_weight, "norm_weight")):
+        if not h.is_contiguous():
+            raise ValueError(f"linear_add_rms_norm: {nm} must be contiguous")
+    splits = gemm_split_count(M, N, K)
+    aligned = all(h.data_ptr() % 16 == 0 for h in (x, w, residual, output, norm_weight))
+    if splits > 1 and aligned and N % 8 == 0 and N <= 2048:
+        part = HipTensorHandle.create_new((splits, M, N), FLOAT32)
+        try:
+            _lib.call("kh_gemm_splitk_partials", _vp(x.data_ptr()), K, _vp(w.data_ptr()), K, _vp(part.data_ptr()),
+                      M, N, K, splits)
+            _lib.call("kh_add_rms_norm", _vp(part.data_ptr() + r0 * N * 4), splits, M * N,
+                      _vp(residual.data_ptr() + r0 * N * 4), _vp(norm_weight.data_ptr()), _vp(output.data_ptr()),
+                      r1 - r0, N, C.c_float(eps), output.kh_dtype)
+        finally:
+            part.dispose()
+        return
+    _lib.call("kh_gemm", _vp(x.data_ptr()), K, _vp(w.data_ptr()), K, _vp(residual.data_ptr()), N,
+              _vp(residual.data_ptr()), N, None, M, N, K, C.c_float(1.0), C.c_float(1.0), 1, x.kh_dtype,
+              residual.kh_dtype)
+    _lib.call("kh_rms_norm", _vp(residual.data_ptr() + r0 * N * 4), N, _vp(norm_weight.data_ptr()),
+              _vp(output.data_ptr()), N, r1 - r0, N, C.c_float(eps), residual.kh_dtype, output.kh_dtype)
+
+
 def gemv_fused(prologue: str, x, w, out, params=None) -> None:
     """One-row projection with its producer fused in front (decode): out[1, n] = alpha * x' W^T
     + beta * cin (+ bias) for the bf16 weight W [n, k] (nn.Linear layout), where x' is
@@ -807,6 +858,7 @@ KERNELS = {
     "sub": sub,
     "silu_mul": silu_mul,
     "linear_swiglu": linear_swiglu,
+    "linear_add_rms_norm": linear_add_rms_norm,
     "copy": copy,
     "contiguous": copy,
     "cast": copy,

@@ -232,10 +232,15 @@ class Qwen3ForCausalLM:
         write, attention over rows [0, position], o_proj and the residual add) is one library call
         (decode_attention_block) and `attend` is not used."""
         cfg = self.cfg
-        Hq, Hkv, D, Hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
-        nq, nkv, I = Hq * D, Hkv * D, cfg.intermediate_size
+        Hd = cfg.hidden_size
         eps = cfg.rms_norm_eps
         one = S == 1
+        n_layers = len(self.layers)
+        # Multi-token rows: each residual add is fused with the RMSNorm after it
+        # (linear_add_rms_norm), so h -- the normed bf16 input of the next projection -- is carried
+        # from one sub-block to the next; the last down projection normalises only the last row, with
+        # the final norm, for the lm_head.
+        h = None if one else F.rms_norm(x, [Hd], self.layers[0]["in_norm"], eps, out_dtype="bfloat16")
         for li, L in enumerate(self.layers):
             if one and decode_block:
                 qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
@@ -245,41 +250,44 @@ class Qwen3ForCausalLM:
                     "v_cache": self.cache.value_cache[li].handle, "w_o": L["w_o"].handle, "x": x.handle,
                     "scale": self.scale})                                                # x += o W_o^T
                 qkv.dispose()
+            elif one:
+                qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
+                attn_t = self._attention_heads(li, L, qkv, S, positions, attend)
+                F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
+                attn_t.dispose()
             else:
-                self._attention_unfused(li, L, x, S, positions, attend, one)
+                qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
+                h.dispose()
+                attn_t = self._attention_heads(li, L, qkv, S, positions, attend)
+                h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm"], eps)     # x += o W_o^T
+                attn_t.dispose()
             if one:
                 gu = F.linear_fused("rms_norm", x, L["w_gu"], L["post_norm"], eps)     # [1, 2I] interleaved
                 F.linear_fused("silu_mul_interleaved", gu, L["w_down"], residual=x)    # x += a W_d^T
                 gu.dispose()
             else:
-                h = F.rms_norm(x, [Hd], L["post_norm"], eps, out_dtype="bfloat16")
                 a = F.linear_swiglu(h, L["w_gu"])                                      # [S, I]
                 h.dispose()
-                F.dispatch_matmul(a, L["w_down"], c=x, beta=1.0, out=x, transpose_b=True)
+                if li + 1 < n_layers:
+                    h = F.linear_add_rms_norm(a, L["w_down"], x, self.layers[li + 1]["in_norm"], eps)
+                else:
+                    h = F.linear_add_rms_norm(a, L["w_down"], x, self.final_norm, eps, rows=(S - 1, S))
                 a.dispose()
-        last = F.narrow(x, 0, S - 1, 1)
         if one:
+            last = F.narrow(x, 0, S - 1, 1)
             logits = F.linear_fused("rms_norm", last, self.lm_head, self.final_norm, eps, out_dtype="float32")
+            last.dispose()
         else:
-            xf = F.rms_norm(last, [Hd], self.final_norm, eps, out_dtype="bfloat16")
-            logits = F.linear(xf, self.lm_head, out_dtype="float32")                   # [1, vocab] fp32
-            xf.dispose()
-        last.dispose()
+            logits = F.linear(h, self.lm_head, out_dtype="float32")                    # [1, vocab] fp32
+            h.dispose()
         return logits
 
-    def _attention_unfused(self, li: int, L: dict, x: Tensor, S: int, positions: Tensor, attend, one: bool) -> None:
-        """The attention block of layer li as separate launches: QKV projection, qk-norm + RoPE with
-        the K/V cache write, attend(), o_proj with the residual add into x."""
+    def _attention_heads(self, li: int, L: dict, qkv: Tensor, S: int, positions: Tensor, attend) -> Tensor:
+        """The attention of layer li from its QKV projection qkv [S, nq + 2 nkv] (disposed here):
+        qk-norm + RoPE with the K/V cache write, then attend(); returns the heads [S, nq] bf16."""
         cfg = self.cfg
-        Hq, Hkv, D, Hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
+        Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         nq, nkv = Hq * D, Hkv * D
-        eps = cfg.rms_norm_eps
-        if one:
-            qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
-        else:
-            h = F.rms_norm(x, [Hd], L["in_norm"], eps, out_dtype="bfloat16")
-            qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
-            h.dispose()
         q = _split_heads(qkv, 0, S, Hq, D)
         k = _split_heads(qkv, nq, S, Hkv, D)
         v = _split_heads(qkv, nq + nkv, S, Hkv, D)
@@ -287,7 +295,7 @@ class Qwen3ForCausalLM:
         # K (normed + rotated) and V land in the cache rows given by `positions`.
         self.ops.find("rms_norm_rope")(q.handle, k.handle, {
             "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
-            "positions": positions.handle, "eps": eps, "q_out": q_heads,
+            "positions": positions.handle, "eps": cfg.rms_norm_eps, "q_out": q_heads,
             "k_out": self.cache.key_cache[li].handle, "v": v.handle, "v_out": self.cache.value_cache[li].handle,
             "cache_positions": True})
         for t in (q, k, v, qkv):
@@ -298,12 +306,7 @@ class Qwen3ForCausalLM:
         attend(li, q_heads, attn_view)
         attn_view.dispose()
         q_heads.dispose()
-        attn_t = Tensor(handle=attn)
-        if one:
-            F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
-        else:
-            F.dispatch_matmul(attn_t, L["w_o"], c=x, beta=1.0, out=x, transpose_b=True)
-        attn_t.dispose()
+        return Tensor(handle=attn)
 
     # -- one forward over S new tokens at cache position `pos` -------------------------------------
     def _forward_dev(self, ids: Tensor, positions: Tensor, end: int) -> Tensor:

@@ -466,6 +466,32 @@ FN(gemmSwiglu, 9)
   void* h = arg_ptr(A, 4); int64_t ldh = arg_i64(A, 5); int64_t m = arg_i64(A, 6); int64_t nh = arg_i64(A, 7);
   int64_t k = arg_i64(A, 8);
   CALL(kh_gemm_swiglu(x, ldx, w, ldw, h, ldh, m, nh, k))
+/* gemmSplitCount(m, n, k) -> the split count gemm uses for a contiguous bf16 [m, k] x [n, k]^T */
+static napi_value js_gemmSplitCount(napi_env env, napi_callback_info info) {
+  Args A_, *A = &A_;
+  if (!begin(A, env, info, "gemmSplitCount", 3)) return NULL;
+  int64_t m = arg_i64(A, 0), n = arg_i64(A, 1), k = arg_i64(A, 2);
+  if (A->bad) return NULL;
+  int splits = 0;
+  if (kh_gemm_split_count(m, n, k, &splits) != KH_OK) return done(A, KH_ERR_INVALID);
+  napi_value out;
+  napi_create_int32(env, splits, &out);
+  return out;
+}
+/* gemmSplitkPartials(a, lda, b, ldb, part, m, n, k, splits): gemm's split-K stage alone, fp32
+   partials [splits][m][n] */
+FN(gemmSplitkPartials, 9)
+  void* a = arg_ptr(A, 0); int64_t lda = arg_i64(A, 1); void* b = arg_ptr(A, 2); int64_t ldb = arg_i64(A, 3);
+  void* part = arg_ptr(A, 4); int64_t m = arg_i64(A, 5); int64_t n = arg_i64(A, 6); int64_t k = arg_i64(A, 7);
+  int sp = arg_int(A, 8);
+  CALL(kh_gemm_splitk_partials(a, lda, b, ldb, (float*)part, m, n, k, sp))
+/* addRmsNorm(part, splits, splitStride, x, w, y, rows, n, eps, outDtype): x += sum of the partials
+   (residual add, decoder_layer.ts:224-238), then y = rms_norm(x) * w */
+FN(addRmsNorm, 10)
+  void* part = arg_ptr(A, 0); int sp = arg_int(A, 1); int64_t ss = arg_i64(A, 2); void* x = arg_ptr(A, 3);
+  void* w = arg_ptr(A, 4); void* y = arg_ptr(A, 5); int64_t rows = arg_i64(A, 6); int64_t n = arg_i64(A, 7);
+  double eps = arg_f64(A, 8); int odt = arg_int(A, 9);
+  CALL(kh_add_rms_norm((const float*)part, sp, ss, (float*)x, w, y, rows, n, (float)eps, odt))
 /* gemvFused(prologue, x, x2, normW, eps, w, ldw, c, cin, bias, n, k, alpha, beta, outDtype) */
 FN(gemvFused, 15)
   int pro = arg_int(A, 0); void* x = arg_ptr(A, 1); void* x2 = arg_ptr(A, 2); void* nw = arg_ptr(A, 3);
@@ -487,7 +513,8 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
-      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemvFused),
+      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemmSplitCount),
+      EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused),
   };
   napi_define_properties(env, exports, sizeof(d) / sizeof(d[0]), d);
   napi_value v;

@@ -157,3 +157,38 @@ def test_linear_swiglu_rejects_bad_layouts(hip):
     w, _ = seeded(351, (2 * 12, 64), "bfloat16")   # intermediate 12: not a multiple of 8
     with pytest.raises(Exception, match="multiple of 8"):
         F.linear_swiglu(x, w)
+
+
+@pytest.mark.parametrize("M,N,K,rows", [(512, 1024, 2048, None), (512, 1024, 3072, None), (512, 1024, 3072, (511, 512)),
+                                        (130, 1024, 2048, (7, 100)), (600, 1024, 3072, None), (64, 96, 40, None)])
+def test_linear_add_rms_norm_matches_separate_launches(hip, M, N, K, rows):
+    """The projection + residual add + RMSNorm of linear_add_rms_norm (split-K partials summed by
+    kh_add_rms_norm when kh_gemm splits the shape, else kh_gemm then kh_rms_norm) against the
+    separate launches -- kh_gemm with the residual as C (beta = 1), then kh_rms_norm -- bit for bit
+    in both the residual and the normed rows, rows outside `rows` untouched; and against the oracle
+    (fp32 residual within the accumulation-order allowance, the bf16 norm within one rounding)."""
+    from kandle_amd import kernels
+    x, xh = seeded(360, (M, K), "bfloat16")
+    w, wh = seeded(361, (N, K), "bfloat16", std=0.02)
+    nw_bits, nwh = syn.bf16(1.0 + syn.normal(362, (N,), 0.1))
+    nw = Tensor(nw_bits, dtype="bfloat16")
+    r0 = syn.normal(363, (M, N))
+    lo, hi = rows if rows is not None else (0, M)
+    res = Tensor(r0.copy())
+    h = F.linear_add_rms_norm(x, w, res, nw, 1e-6, rows=rows)
+    fused_res, fused_h = res.numpy(), h.numpy()
+    ref_res = Tensor(r0.copy())
+    F.dispatch_matmul(x, w, c=ref_res, beta=1.0, out=ref_res, transpose_b=True)
+    sep_h = F.rms_norm(F.narrow(ref_res, 0, lo, hi - lo), [N], nw, 1e-6, out_dtype="bfloat16").numpy()
+    sep_res = ref_res.numpy()
+    assert fused_h.shape == (hi - lo, N)
+    assert np.array_equal(fused_res[lo:hi].view(np.uint32), sep_res[lo:hi].view(np.uint32))
+    assert np.array_equal(fused_h.view(np.uint32), sep_h.view(np.uint32))
+    assert np.array_equal(fused_res[:lo], r0[:lo]) and np.array_equal(fused_res[hi:], r0[hi:])
+    ref = oracle.linear(xh, wh) + r0
+    ok, err = _close_f32(fused_res[lo:hi], ref[lo:hi])
+    assert ok, err
+    ok, err = _close_bf16(fused_h, oracle.rms_norm(ref[lo:hi], nwh, 1e-6), N)
+    assert ok, err
+    if (M, N, K) == (512, 1024, 2048):
+        assert kernels.gemm_split_count(M, N, K) > 1     # the fused split path is what ran

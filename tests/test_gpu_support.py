@@ -121,19 +121,24 @@ def test_linear_bf16(hip, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(512, 1024, 3072), (100, 520, 2048)])
 def test_linear_split_k_residual_deterministic(hip, M, N, K):
-    """Few output tiles and a long K: workgroups split K and the last one of each tile adds the
-    partials in a fixed order -- fp32 output with the residual added in place, and bit-identical
-    results when run twice."""
+    """Few output tiles and a long K: workgroups split K and the last one of each tile to arrive adds
+    the partials in split order -- fp32 output with the residual added in place; bit-identical
+    results over four runs (the arrival order differs from run to run), with another split GEMM of
+    a different tile count between them (the per-tile arrival counters must be back at zero)."""
     x, xh = seeded(245, (M, K), "bfloat16")
     w, wh = seeded(246, (N, K), "bfloat16", std=0.02)
+    x2, _ = seeded(248, (64, 2048), "bfloat16")
+    w2, _ = seeded(249, (96, 2048), "bfloat16", std=0.02)
     r0 = syn.normal(247, (M, N))
-    outs = []
-    for _ in range(2):
+    outs, others = [], []
+    for _ in range(4):
         r = Tensor(r0.copy())
         F.dispatch_matmul(x, w, c=r, beta=1.0, out=r, transpose_b=True)
         outs.append(r.numpy())
         r.dispose()
-    assert np.array_equal(outs[0], outs[1])
+        others.append(F.dispatch_matmul(x2, w2, transpose_b=True).numpy())
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    assert all(np.array_equal(others[0], o) for o in others[1:])
     ref = oracle.linear(xh, wh) + r0
     assert max_rel(outs[0], ref) < 1e-4
 
