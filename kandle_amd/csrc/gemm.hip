@@ -12,21 +12,14 @@
 #include <type_traits>
 
 #include "common.h"
+#include "gemv.h"
 
 using namespace kh;
+using namespace kh::gemv;
 
 namespace {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-template <typename TO>
-__device__ __forceinline__ float epilogue(float acc, float alpha, float beta, const TO* cin, int64_t ldcin,
-                                          const TO* bias, int64_t m, int64_t n) {
-  float v = alpha * acc;
-  if (cin != nullptr && beta != 0.f) v += beta * Elem<TO>::load(cin, m * ldcin + n);
-  if (bias != nullptr) v += Elem<TO>::load(bias, n);
-  return v;
-}
 
 // Four consecutive outputs of one row, vectorised when the row start allows it.
 template <typename TO>
@@ -61,8 +54,8 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 constexpr int G_THREADS = 256;
 constexpr int kGemmPrefetch = 3;        // k-steps of global loads in flight per workgroup
 constexpr int kGemmT128Min = 256;       // 128-tiles from this many tiles up
-constexpr int kGemmSplitTarget = 512;   // split K until about this many workgroups
-constexpr bool kGemmSplit128 = false;   // 128-tiles are never split
+constexpr int kGemmSplitTarget = 512;   // split K until about this many 64-tile workgroups
+constexpr int kGemmSplitWT = 1;         // tile of split launches: 64 (1) or 128 (2)
 constexpr int kMaxSplits = 8;
 constexpr int g_tile(int wt) { return 64 * wt; }
 
@@ -379,185 +372,21 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
 // streams them with raw 16-byte buffer loads, CB chunks of 512 columns per row in flight (rows past
 // n read as zero), and reduces each row across the wave.  Every weight byte is read once.
 // =============================================================================================
-constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2, PRO_SILU_MUL_IL = 3, PRO_ATTN_MERGE = 4;
-constexpr int kAttnMergeMaxChunks = 8;   // split-K chunks the attention-merge prologue accepts
-constexpr int GV_CHUNK = 512;  // columns per wave-wide 16-byte load (64 lanes x 8 bf16)
-
-template <int PRO>
-__device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const uint16_t* x2, const uint16_t* nw,
-                                              float eps, int K, int kpad, const AttnMerge& am) {
-  const int tid = threadIdx.x;
-  if constexpr (PRO == PRO_ATTN_MERGE) {
-    // Thread t merges columns 8 (t mod 16) .. + 7 of head t / 16 (then t + 256, ...): the chunks'
-    // (m, l, o) combined with weights exp(m_c - M), M the largest chunk max.  Up to kAttnMergeMaxChunks
-    // chunks, every load issued before any math (indices past the last chunk clamped, weight 0).
-    constexpr int MC = kAttnMergeMaxChunks;
-    const float* po = (const float*)x;
-    const float2* pml = reinterpret_cast<const float2*>(po + (int64_t)am.hq * am.max_chunks * 128);
-    const int p = *am.position;
-    const int L = p + 1 < 0 ? 0 : (p + 1 > am.max_len ? am.max_len : p + 1);
-    const int nch = (L + am.chunk - 1) / am.chunk;
-    for (int g = tid; g < (kpad >> 3); g += blockDim.x) {
-      const int h = g >> 4, d0 = (g & 15) * 8;
-      float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (h < am.hq && nch > 0) {
-        float2 ml[MC];
-        float4 oa[MC], ob[MC];
-#pragma unroll
-        for (int c = 0; c < MC; ++c) {
-          const int cc = min(c, nch - 1);
-          ml[c] = pml[(int64_t)h * am.max_chunks + cc];
-          const float4* o4 = reinterpret_cast<const float4*>(po + ((int64_t)h * am.max_chunks + cc) * 128 + d0);
-          oa[c] = o4[0];
-          ob[c] = o4[1];
-        }
-        float M = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < MC; ++c)
-          if (c < nch) M = fmaxf(M, ml[c].x);
-        const float mu = M == -INFINITY ? 0.f : M;
-        float Ls = 0.f, t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < MC; ++c) {
-          const float f = c < nch ? __expf(ml[c].x - mu) : 0.f;
-          Ls += ml[c].y * f;
-          t[0] += oa[c].x * f; t[1] += oa[c].y * f; t[2] += oa[c].z * f; t[3] += oa[c].w * f;
-          t[4] += ob[c].x * f; t[5] += ob[c].y * f; t[6] += ob[c].z * f; t[7] += ob[c].w * f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = round_bf16(Ls > 0.f ? t[e] / Ls : 0.f);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xs[g * 8 + e] = (g * 8 + e) < K ? v[e] : 0.f;
-    }
-  } else if constexpr (PRO == PRO_RMSNORM) {
-    // Rows of up to 8 * blockDim elements stay in registers between the two passes.
-    constexpr int PR = 8;
-    __shared__ float red[4];
-    const float* xf = (const float*)x;
-    const bool in_regs = kpad <= PR * (int)blockDim.x;
-    float xv[PR], wv[PR];
-    float ss = 0.f;
-    if (in_regs) {
-#pragma unroll
-      for (int j = 0; j < PR; ++j) {
-        const int i = tid + j * blockDim.x;
-        xv[j] = i < K ? xf[i] : 0.f;
-        wv[j] = i < K ? bf16_bits_to_f32(nw[i]) : 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < PR; ++j) ss += xv[j] * xv[j];
-    } else {
-      for (int i = tid; i < K; i += blockDim.x) ss += xf[i] * xf[i];
-    }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    ss = red[0] + red[1] + red[2] + red[3];
-    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-    if (in_regs) {
-#pragma unroll
-      for (int j = 0; j < PR; ++j) {
-        const int i = tid + j * blockDim.x;
-        if (i < kpad) xs[i] = i < K ? round_bf16((xv[j] * inv) * wv[j]) : 0.f;
-      }
-    } else {
-      for (int i = tid; i < kpad; i += blockDim.x)
-        xs[i] = i < K ? round_bf16((xf[i] * inv) * bf16_bits_to_f32(nw[i])) : 0.f;
-    }
-  } else if constexpr (PRO == PRO_SILU_MUL) {
-    const uint16_t* g = (const uint16_t*)x;
-    for (int i = tid; i < kpad; i += blockDim.x)
-      xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(g[i])) * bf16_bits_to_f32(x2[i])) : 0.f;
-  } else if constexpr (PRO == PRO_SILU_MUL_IL) {
-    const uint16_t* gu = (const uint16_t*)x;
-    for (int i = tid; i < kpad; i += blockDim.x) {
-      const int gi = 16 * (i >> 3) + (i & 7);
-      xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(gu[gi])) * bf16_bits_to_f32(gu[gi + 8])) : 0.f;
-    }
-  } else {
-    const uint16_t* xb = (const uint16_t*)x;
-    for (int i = tid; i < kpad; i += blockDim.x) xs[i] = i < K ? bf16_bits_to_f32(xb[i]) : 0.f;
-  }
-  __syncthreads();
-}
-
 template <int U, int PRO, typename TO>
 __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, const uint16_t* __restrict__ x2,
                                                     const uint16_t* __restrict__ nw, float eps,
                                                     const uint16_t* __restrict__ W, int64_t ldw, uint32_t w_bytes,
                                                     TO* C, const TO* cin, const TO* __restrict__ bias, int N, int K,
                                                     int nch, float alpha, float beta, AttnMerge am) {
-  constexpr int CB = 8 / U;  // 16-byte loads in flight per row per lane
   extern __shared__ float xs[];
-  const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(W, w_bytes);
-  const int64_t stride = (int64_t)gridDim.x * (blockDim.x >> 6) * U;
-  int64_t n0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + w) * U;
-
-  // Weight loads of batch (row group n, chunks [c0, c0 + CB)); columns past K (row padding when
-  // ldw > K) and rows past N read as zero (offset w_bytes is out of range).
-  uint4 wv[U][CB];
-  auto issue = [&](int64_t n, int c0) {
-#pragma unroll
-    for (int cc = 0; cc < CB; ++cc)
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = c0 + cc;
-        const int k = c * GV_CHUNK + lane * 8;
-        const uint32_t off = k < K ? (uint32_t)(((n + u) * ldw + k) * 2) : w_bytes;
-        wv[u][cc] = c < nch ? buf_load16(rsrc, off) : make_uint4(0, 0, 0, 0);
-      }
-  };
+  GemvRows<U> g;
+  g.init(W, ldw, w_bytes, N, K, nch, (int64_t)blockIdx.x * (blockDim.x >> 6) + w,
+         (int64_t)gridDim.x * (blockDim.x >> 6));
   // The first batch is in flight while the workgroup forms x'.
-  if (n0 < N) issue(n0, 0);
+  g.issue_first();
   gemv_prologue<PRO>(xs, x, x2, nw, eps, K, nch * GV_CHUNK, am);
-
-  for (; n0 < N; n0 += stride) {
-    float acc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += CB) {
-      uint4 cur[U][CB];
-#pragma unroll
-      for (int cc = 0; cc < CB; ++cc)
-#pragma unroll
-        for (int u = 0; u < U; ++u) cur[u][cc] = wv[u][cc];
-      // prefetch the next batch: the rest of this row group, else the next row group
-      if (c0 + CB < nch)
-        issue(n0, c0 + CB);
-      else if (n0 + stride < N)
-        issue(n0 + stride, 0);
-#pragma unroll
-      for (int cc = 0; cc < CB; ++cc) {
-        if (c0 + cc < nch) {
-          const float4* xp = reinterpret_cast<const float4*>(xs + (c0 + cc) * GV_CHUNK + lane * 8);
-          const float4 xa = xp[0], xb = xp[1];
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const uint4 q = cur[u][cc];
-            float s = acc[u];
-            s += lo_bf16(q.x) * xa.x;
-            s += hi_bf16(q.x) * xa.y;
-            s += lo_bf16(q.y) * xa.z;
-            s += hi_bf16(q.y) * xa.w;
-            s += lo_bf16(q.z) * xb.x;
-            s += hi_bf16(q.z) * xb.y;
-            s += lo_bf16(q.w) * xb.z;
-            s += hi_bf16(q.w) * xb.w;
-            acc[u] = s;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float sum = wave_sum(acc[u]);
-      const int64_t n = n0 + u;
-      if (lane == 0 && n < N) Elem<TO>::store(C, n, epilogue<TO>(sum, alpha, beta, cin, 0, bias, 0, n));
-    }
-  }
+  g.template run<TO>(xs, C, cin, bias, alpha, beta);
 }
 
 // Launches gemv1_kernel; returns false (nothing launched) when the operands do not fit its
@@ -654,23 +483,26 @@ GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, 
         (int64_t)g_tile(2) * lda * 2 < lim && (int64_t)g_tile(2) * ldb * 2 < lim))
     return p;
   p.mfma = true;
-  // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the
-  // workgroups, and when even those leave CUs idle and K is long, split K over up to 8 workgroups.
+  // The K split is decided on the 64-tile count, whatever tile then runs it, so a shape's k ranges
+  // -- and with them its sums, bit for bit -- do not depend on the tile: split when 64-tiles would
+  // leave CUs idle and K is long, over up to 8 workgroups per tile.
+  const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-  p.wt = t128 >= kGemmT128Min ? 2 : 1;
-  const int gt = g_tile(p.wt);
-  p.tiles_m = (M + gt - 1) / gt;
-  p.tiles_n = (N + gt - 1) / gt;
-  p.tiles = (int64_t)p.tiles_m * p.tiles_n;
   p.kchunk = K;
-  if (p.tiles < 256 && K >= 1024 && N % 4 == 0 && (p.wt == 1 || kGemmSplit128)) {
-    const int64_t want = kGemmSplitTarget / p.tiles;
+  if (t64 < 256 && K >= 1024 && N % 4 == 0) {
+    const int64_t want = kGemmSplitTarget / t64;
     const int splits = want < 1 ? 1 : (want > kMaxSplits ? kMaxSplits : (int)want);
     if (splits > 1) {
       p.kchunk = ((K + splits - 1) / splits + 127) / 128 * 128;   // whole k-steps of 64 and 128
       p.splits = (K + p.kchunk - 1) / p.kchunk;
     }
   }
+  // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the workgroups.
+  p.wt = p.splits > 1 ? kGemmSplitWT : (t128 >= kGemmT128Min ? 2 : 1);
+  const int gt = g_tile(p.wt);
+  p.tiles_m = (M + gt - 1) / gt;
+  p.tiles_n = (N + gt - 1) / gt;
+  p.tiles = (int64_t)p.tiles_m * p.tiles_n;
   return p;
 }
 
