@@ -14,6 +14,7 @@ void clear_error();
 hipStream_t stream();  // the library stream; nullptr before kh_init
 bool initialized();
 int current_device();  // the device kh_init selected (-1 before)
+int cu_count();        // compute units of that device
 int attention_init(int device);  // kh_init's set-up of attention.hip (device current)
 
 // Internal scratch allocation through the caching allocator (stream-ordered on the library stream).

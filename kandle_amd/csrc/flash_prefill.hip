@@ -37,6 +37,8 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
+constexpr int kPersistWaves = 8;  // waves per workgroup of the persistent causal kernel
+constexpr int kPersistMinItems = 2;  // persistent from this many query blocks per CU up (0: never)
 constexpr int FA_D = 128;
 constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
@@ -94,29 +96,29 @@ struct Flash {
   using C = Cfg<BN, WAVES>;
   int G, BMQ, tid, wave, lane, r, g, b, hk, hqi, q0, qw0, qi, ntiles, wave_last_q, wave_tiles, dcol;
   __amdgpu_buffer_rsrc_t rk, rv;
-  AttnStrides st;
+  // Element strides as 32-bit values (the entry checks they fit): half the scalar registers of
+  // the 64-bit AttnStrides, which the persistent kernel needs for its item bookkeeping.
+  struct Strides32 {
+    int32_t qb, qh, qs, kb, kh, ks, vb, vh, vs, ob, oh, os;
+  } st;
 
-  __device__ __forceinline__ void init(int batch, int hq, int hkv, int lq, int lk, const AttnStrides& s, bool causal,
-                                       int n_qblocks, const uint16_t* K, const uint16_t* V) {
-    st = s;
+  // Per-workgroup fields: lane roles, GQA grouping, strides.
+  __device__ __forceinline__ void setup(int hq, int hkv, const AttnStrides& s) {
+    st = Strides32{(int32_t)s.qb, (int32_t)s.qh, (int32_t)s.qs, (int32_t)s.kb, (int32_t)s.kh, (int32_t)s.ks,
+                   (int32_t)s.vb, (int32_t)s.vh, (int32_t)s.vs, (int32_t)s.ob, (int32_t)s.oh, (int32_t)s.os};
     G = hq / hkv;
-    const int wpg = WAVES / G;
-    BMQ = 32 * wpg;
+    BMQ = 32 * (WAVES / G);
     tid = threadIdx.x;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps derived values scalar
     lane = tid & 63;
     r = lane & 31;
     g = lane >> 5;
-    // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCD i % 8), each XCD
-    // with its own L2.  Renumber so that XCD x runs a contiguous range of logical blocks, ordered
-    // (b, kv head)-major and, inside a head, heaviest (last) query block first: at any time an
-    // XCD's CUs work on one or two heads, whose K/V stay resident in its L2.
-    const int nblk = batch * hkv * n_qblocks;
-    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const int base = nblk / kXcds, extra = nblk % kXcds;  // XCD x runs base + (x < extra) blocks
-    const int logical = xcd * base + min(xcd, extra) + j;
-    const int bh = logical / n_qblocks;
-    const int qblk = n_qblocks - 1 - logical % n_qblocks;
+    dcol = 8 * (tid & 15);
+  }
+  // Per-item fields: query block qblk of (batch, kv head) pair bh.
+  __device__ __forceinline__ void set_item(int bh, int qblk, int hkv, int lq, int lk, bool causal, const uint16_t* K,
+                                           const uint16_t* V) {
+    const int wpg = WAVES / G;
     b = bh / hkv;
     hk = bh % hkv;
     hqi = hk * G + wave / wpg;
@@ -129,18 +131,49 @@ struct Flash {
     const int nchunks = (kv_end + C::BNC - 1) / C::BNC;
     wave_last_q = min(qw0 + 31, lq - 1);
     wave_tiles = qw0 >= lq ? 0 : (causal ? min(nchunks, wave_last_q / C::BNC + 1) : nchunks);
-    rk = make_rsrc(K + b * s.kb + hk * s.kh, (uint32_t)(((int64_t)(lk - 1) * s.ks + FA_D) * 2));
-    rv = make_rsrc(V + b * s.vb + hk * s.vh, (uint32_t)(((int64_t)(lk - 1) * s.vs + FA_D) * 2));
-    dcol = 8 * (tid & 15);
+    rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hk * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + FA_D) * 2));
+    rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hk * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + FA_D) * 2));
+  }
+  __device__ __forceinline__ void init(int batch, int hq, int hkv, int lq, int lk, const AttnStrides& s, bool causal,
+                                       int n_qblocks, const uint16_t* K, const uint16_t* V) {
+    setup(hq, hkv, s);
+    // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCD i % 8), each XCD
+    // with its own L2.  Renumber so that XCD x runs a contiguous range of logical blocks, ordered
+    // (b, kv head)-major and, inside a head, heaviest (last) query block first: at any time an
+    // XCD's CUs work on one or two heads, whose K/V stay resident in its L2.
+    const int nblk = batch * hkv * n_qblocks;
+    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int base = nblk / kXcds, extra = nblk % kXcds;  // XCD x runs base + (x < extra) blocks
+    const int logical = xcd * base + min(xcd, extra) + j;
+    set_item(logical / n_qblocks, n_qblocks - 1 - logical % n_qblocks, hkv, lq, lk, causal, K, V);
   }
   // LDS row of tile key k: bits 2 and 3 of k swapped (an involution), so that lane r of the S^T
   // A operand, which reads LDS row r, holds key swap23(r) -- the order the PV B operand needs --
   // while the 32 lanes read 32 consecutive rows (no bank conflicts).
   static __device__ __forceinline__ int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
+  // Q row of this lane in item (bh, qblk) of another item than the current one (the persistent
+  // kernel's prefetch), from the per-workgroup fields alone.
+  __device__ __forceinline__ void load_q_of(int bh, int qblk, int hkv, const uint16_t* Q, int lq,
+                                            bf16x8 (&qreg)[8]) const {
+    const int wpg = WAVES / G;
+    const int bb = bh / hkv, hqn = (bh % hkv) * G + wave / wpg, qin = qblk * BMQ + (wave % wpg) * 32 + r;
+    const auto rq = make_rsrc(Q + (int64_t)bb * st.qb + (int64_t)hqn * st.qh,
+                              (uint32_t)(((int64_t)(lq - 1) * st.qs + FA_D) * 2));
+    const uint32_t qoff = (uint32_t)(((int64_t)qin * st.qs + 8 * g) * 2);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
+  }
+  // K and V byte ranges of pair bh.
+  __device__ __forceinline__ void kv_rsrc_of(int bh, int hkv, int lk, const uint16_t* K, const uint16_t* V,
+                                             __amdgpu_buffer_rsrc_t& rkn, __amdgpu_buffer_rsrc_t& rvn) const {
+    const int bb = bh / hkv, hh = bh % hkv;
+    rkn = make_rsrc(K + (int64_t)bb * st.kb + (int64_t)hh * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + FA_D) * 2));
+    rvn = make_rsrc(V + (int64_t)bb * st.vb + (int64_t)hh * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + FA_D) * 2));
+  }
   // This lane's Q row: query qi, columns 8 g + 16 c .. + 7 (c = 0..7).
   __device__ __forceinline__ void load_q(const uint16_t* Q, int lq, bf16x8 (&qreg)[8]) const {
-    const uint16_t* qh = Q + b * st.qb + hqi * st.qh;
+    const uint16_t* qh = Q + (int64_t)b * st.qb + (int64_t)hqi * st.qh;
     const auto rq = make_rsrc(qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + FA_D) * 2));
     const uint32_t qoff = (uint32_t)(((int64_t)qi * st.qs + 8 * g) * 2);
 #pragma unroll
@@ -286,7 +319,7 @@ struct Flash {
     if (qi < lq) {
       const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
       const bool nan_row = NAN_EMPTY && !(l_tot > 0.f);
-      uint16_t* orow = O + b * st.ob + hqi * st.oh + (int64_t)qi * st.os;
+      uint16_t* orow = O + (int64_t)b * st.ob + (int64_t)hqi * st.oh + (int64_t)qi * st.os;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -485,8 +518,8 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
   const int ntiles = F.ntiles;
 
   if (ntiles > 0) {
-    F.load_rows(F.rk, st.ks, 0, kst);
-    F.load_rows(F.rv, st.vs, 0, vst);
+    F.load_rows(F.rk, F.st.ks, 0, kst);
+    F.load_rows(F.rv, F.st.vs, 0, vst);
     F.store_k(smem, kst);
     F.store_v(smem + C::KTILE, vst);
   }
@@ -504,8 +537,8 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     MR mreg;
     if constexpr (MASKT != 0) F.template load_mask<MASKT>(t, lq, rm, ma, mreg);
     if (has_next) {
-      F.load_rows(F.rk, st.ks, t + 1, kst);
-      F.load_rows(F.rv, st.vs, t + 1, vst);
+      F.load_rows(F.rk, F.st.ks, t + 1, kst);
+      F.load_rows(F.rv, F.st.vs, t + 1, vst);
     }
     const uint16_t* ks = smem + (t & 1) * STAGE;
 #pragma unroll
@@ -546,6 +579,115 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
   F.template store_o<MASKT != 0>(O, lq, MASKT == 0 ? sl.l : sr.l_run, oacc);
 }
 
+// Persistent form of the causal / unmasked route: one workgroup per CU walks a fixed list of
+// (query block, (batch, kv head)) items, so a CU never waits for a new workgroup to start and load
+// its Q and first K/V tile: the next item's Q and first tile are requested during the current
+// item's last tile.  Items are ranked heaviest first (query block descending) and dealt in a snake
+// (ranks w, 2P - 1 - w, 2P + w, ... to workgroup w of P), which gives every workgroup the same
+// number of tiles when the query blocks of all pairs are uniform (C3: 32 + 17 + 16 + 1 = 66 tiles
+// each).  When P is a multiple of the pair count, the odd passes are mirrored so that a workgroup
+// keeps one (batch, kv head) pair for all its items (its K/V stay in its XCD's L2).  The per-item
+// arithmetic is the tile kernel's, so outputs are identical to it.
+template <bool CAUSAL>
+__global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale, int n_qblocks) {
+  constexpr int BN = 128, WAVES = kPersistWaves;
+  using C = Cfg<BN, WAVES>;
+  using FL = Flash<BN, WAVES>;
+  constexpr int STAGE = C::KTILE + C::VTILE;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+  const int P = gridDim.x, w = blockIdx.x;
+  const int npairs = batch * hkv;
+  const int nitems = npairs * n_qblocks;  // < 2^31 (the launcher checks)
+  const bool mirror = P % npairs == 0;
+  auto item = [&](int k, int& bh, int& qblk) -> bool {
+    const int v = P * k + ((k & 1) ? P - 1 - w : w);
+    if (v >= nitems) return false;
+    const int cls = v / npairs, slot = v - cls * npairs;
+    bh = (mirror && (k & 1)) ? npairs - 1 - slot : slot;
+    qblk = n_qblocks - 1 - cls;
+    return true;
+  };
+  int k = 0, bh = 0, qblk = 0;
+  if (!item(0, bh, qblk)) return;
+  FL F;
+  F.setup(hq, hkv, st);
+  F.set_item(bh, qblk, hkv, lq, lk, CAUSAL, K, V);
+  const float c2 = scale * kLog2e;
+  bf16x8 qreg[8];
+  F.load_q(Q, lq, qreg);
+  uint4 kst[C::NK], vst[C::NK];
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
+  SoftmaxLog2 sl;
+  F.load_rows(F.rk, F.st.ks, 0, kst);
+  F.load_rows(F.rv, F.st.vs, 0, vst);
+  F.store_k(smem, kst);
+  F.store_v(smem + C::KTILE, vst);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int buf = 0;
+  while (true) {
+    int bhn = 0, qbn = 0;
+    const bool more = item(k + 1, bhn, qbn);
+    // A wave's Q registers are free once it has formed its last chunk's scores: the next item's Q
+    // is loaded into them there (at the start for a wave with no rows in this item).
+    if (more && F.wave_tiles == 0) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
+    const int ntiles = F.ntiles;
+    for (int t = 0; t < ntiles; ++t) {
+      const bool next_same = t + 1 < ntiles;
+      if (next_same) {
+        F.load_rows(F.rk, F.st.ks, t + 1, kst);
+        F.load_rows(F.rv, F.st.vs, t + 1, vst);
+      } else if (more) {
+        __amdgpu_buffer_rsrc_t rkn, rvn;
+        F.kv_rsrc_of(bhn, hkv, lk, K, V, rkn, rvn);
+        F.load_rows(rkn, F.st.ks, 0, kst);
+        F.load_rows(rvn, F.st.vs, 0, vst);
+      }
+      const uint16_t* ks = smem + buf * STAGE;
+#pragma unroll
+      for (int c = 0; c < C::NCH; ++c) {
+        const int tc = t * C::NCH + c;  // 64-key compute chunk
+        if (tc < F.wave_tiles) {
+          f32x16 sacc[C::NSUB];
+          bf16x8 pk[2 * C::NSUB];
+          F.template qk<true>(ks + c * C::BNC * FA_KSTR, qreg, sl.mneg, sacc);
+          if (more && tc == F.wave_tiles - 1) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
+          F.template mask<CAUSAL>(tc, lk, sacc);
+          float ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
+          if (sl.need_raise(ps)) {
+            sl.raise(sacc, c2, oacc);
+            ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
+          }
+          sl.l += ps;
+          F.pv(ks + C::KTILE + c * C::BNC * C::VSTR, pk, oacc);
+        }
+      }
+      if (next_same || more) {
+        uint16_t* nxt = smem + (buf ^ 1) * STAGE;
+        F.store_k(nxt, kst);
+        F.store_v(nxt + C::KTILE, vst);
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+    F.template store_o<false>(O, lq, sl.l, oacc);
+    if (!more) break;
+    F.set_item(bhn, qbn, hkv, lq, lk, CAUSAL, K, V);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
+    sl = SoftmaxLog2();
+    ++k;
+  }
+}
+
 constexpr int kWaves = 8;  // waves per workgroup: query rows of 32 * 8 / G, one kv head
 // Short prompts: a grid of fewer than kSmallGrid 8-wave workgroups leaves most CUs idle and its time
 // is the key loop of the last query block.  Such launches use workgroups of kSmallWaves waves over
@@ -575,6 +717,9 @@ bool flash_prefill_supported(const void* q, const void* k, const void* v, const 
   const int G = hq / hkv;
   if (d != FA_D || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
+  const int64_t all[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.vb, st.vh, st.vs, st.ob, st.oh, st.os};
+  for (int64_t s : all)
+    if (s < 0 || s > INT32_MAX) return false;  // the kernels hold strides as 32-bit values
   const int64_t s16[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.vb, st.vh, st.vs};
   for (int64_t s : s16)
     if (s % 8 != 0) return false;
@@ -598,6 +743,12 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
       launch_fwd<kSmallBN, kSmallWaves, true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
     else
       launch_fwd<kSmallBN, kSmallWaves, false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  } else if (causal && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
+    // Enough causal query blocks for every CU to take several: one resident workgroup per CU.
+    static_assert(kPersistWaves == kWaves, "the persistent kernel's query blocks are the tile kernel's");
+    flash_fwd_persistent_kernel<true><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
+        st, scale, nqb);
   } else if (causal) {
     launch_fwd<128, kWaves, true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
   } else {

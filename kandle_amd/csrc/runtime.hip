@@ -27,6 +27,7 @@ struct State {
   hipStream_t stream = nullptr;
   GraphObj* capturing = nullptr;  // graph whose stream capture is open
   int debug = 0;                  // kh_set_debug flags
+  int cus = 0;                    // compute units of the device
 };
 State g_state;
 
@@ -179,6 +180,7 @@ void set_error(const char* fmt, ...) {
 void clear_error() { g_err[0] = 0; }
 hipStream_t stream() { return g_state.stream; }
 bool initialized() { return g_state.init; }
+int cu_count() { return g_state.cus; }
 int current_device() { return g_state.init ? g_state.device : -1; }
 
 bool debug_sync() { return (g_state.debug & 1) != 0 && g_state.capturing == nullptr && g_state.stream != nullptr; }
@@ -235,6 +237,7 @@ int kh_init(int device) {
     return KH_ERR_INVALID;
   }
   KH_CHECK_HIP(hipSetDevice(device));
+  KH_CHECK_HIP(hipDeviceGetAttribute(&g_state.cus, hipDeviceAttributeMultiprocessorCount, device));
   const int rc = attention_init(device);
   if (rc != KH_OK) return rc;
   KH_CHECK_HIP(hipStreamCreateWithFlags(&g_state.stream, hipStreamNonBlocking));
