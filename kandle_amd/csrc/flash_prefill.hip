@@ -39,6 +39,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
 constexpr int kPersistWaves = 8;  // waves per workgroup of the persistent causal kernel
 constexpr int kPersistMinItems = 2;  // persistent from this many query blocks per CU up (0: never)
+constexpr bool kPersistXcdLocal = true;  // XCD-local item order where the shape allows it
 constexpr int FA_D = 128;
 constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
@@ -601,7 +602,21 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
   const int npairs = batch * hkv;
   const int nitems = npairs * n_qblocks;  // < 2^31 (the launcher checks)
   const bool mirror = P % npairs == 0;
+  // XCD-local order, when the shape allows it: the P / 8 workgroups of XCD x (w % 8 = x, local
+  // index j = w / 8) take its npairs / 8 pairs one after another, query block n_qblocks - 1 - j of
+  // the even ones and j of the odd ones (n_qblocks + 1 tiles per two items for every j), so an
+  // XCD's L2 holds about two pairs' K/V at a time.
+  const int ppx = npairs / kXcds;
+  const bool xcd_local = kPersistXcdLocal && P % kXcds == 0 && npairs % kXcds == 0 && ppx % 2 == 0 &&
+                         P / kXcds == n_qblocks;
   auto item = [&](int k, int& bh, int& qblk) -> bool {
+    if (xcd_local) {
+      if (k >= ppx) return false;
+      const int x = w % kXcds, j = w / kXcds;
+      bh = ppx * x + k;
+      qblk = (k & 1) ? j : n_qblocks - 1 - j;
+      return true;
+    }
     const int v = P * k + ((k & 1) ? P - 1 - w : w);
     if (v >= nitems) return false;
     const int cls = v / npairs, slot = v - cls * npairs;
