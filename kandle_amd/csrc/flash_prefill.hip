@@ -40,6 +40,7 @@ constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
 constexpr int kPersistWaves = 8;  // waves per workgroup of the persistent causal kernel
 constexpr int kPersistMinItems = 2;  // persistent from this many query blocks per CU up (0: never)
 constexpr bool kPersistXcdLocal = true;  // XCD-local item order where the shape allows it
+constexpr bool kMirrorSlots = true;      // mirrored row slots for the SIMD's second wave
 constexpr int FA_D = 128;
 constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
@@ -116,6 +117,15 @@ struct Flash {
     g = lane >> 5;
     dcol = 8 * (tid & 15);
   }
+  // 32-row slot of this wave inside its head's query block.  Waves w and w + 4 of an 8-wave
+  // workgroup share a SIMD; the second four take their slots mirrored, so that on the causal
+  // diagonal (where a wave's chunk count grows with its slot) each SIMD pairs a short row block
+  // with a long one.  Only the rows a wave owns change, not any row's arithmetic.
+  __device__ __forceinline__ int row_slot(int wpg) const {
+    const int i = wave % wpg;
+    if (!kMirrorSlots || WAVES != 8 || wave < 4 || wpg == 1) return i;
+    return wpg == 8 ? 11 - i : wpg - 1 - i;
+  }
   // Per-item fields: query block qblk of (batch, kv head) pair bh.
   __device__ __forceinline__ void set_item(int bh, int qblk, int hkv, int lq, int lk, bool causal, const uint16_t* K,
                                            const uint16_t* V) {
@@ -124,7 +134,7 @@ struct Flash {
     hk = bh % hkv;
     hqi = hk * G + wave / wpg;
     q0 = qblk * BMQ;
-    qw0 = q0 + (wave % wpg) * 32;
+    qw0 = q0 + row_slot(wpg) * 32;
     qi = qw0 + r;
     const int kv_end = causal ? min(lk, q0 + BMQ) : lk;
     ntiles = (kv_end + BN - 1) / BN;
@@ -158,7 +168,7 @@ struct Flash {
   __device__ __forceinline__ void load_q_of(int bh, int qblk, int hkv, const uint16_t* Q, int lq,
                                             bf16x8 (&qreg)[8]) const {
     const int wpg = WAVES / G;
-    const int bb = bh / hkv, hqn = (bh % hkv) * G + wave / wpg, qin = qblk * BMQ + (wave % wpg) * 32 + r;
+    const int bb = bh / hkv, hqn = (bh % hkv) * G + wave / wpg, qin = qblk * BMQ + row_slot(wpg) * 32 + r;
     const auto rq = make_rsrc(Q + (int64_t)bb * st.qb + (int64_t)hqn * st.qh,
                               (uint32_t)(((int64_t)(lq - 1) * st.qs + FA_D) * 2));
     const uint32_t qoff = (uint32_t)(((int64_t)qin * st.qs + 8 * g) * 2);
