@@ -19,14 +19,15 @@ struct MaskArgs {
   float floor_raw;         // the reference softmax's f32(-1e38) max floor in raw q.k units
 };
 
-// True when the bf16 MFMA prefill kernel takes this call (d = 128, G in {1,2,4,8}, 16-byte
-// aligned rows, per-head byte ranges addressable with 32-bit buffer offsets).
+// True when the bf16 MFMA prefill kernel takes this call (d = 64 or 128, G in {1,2,4,8}, 16-byte
+// aligned rows, strides below 2^31, per-head byte ranges addressable with 32-bit buffer offsets).
+// The explicit-mask kernel takes d = 128 only.
 bool flash_prefill_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv,
                              int64_t lq, int64_t lk, int d, const AttnStrides& st);
 
 // Launches the prefill kernel on the library stream; returns KH_OK or an error code.
 int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
-                              int lq, int lk, const AttnStrides& st, float scale, bool causal);
+                              int lq, int lk, int d, const AttnStrides& st, float scale, bool causal);
 
 // The prefill kernel with an additive mask (f32 or bf16, KH_F32 / KH_BF16) instead of causal
 // masking; 64-key stages.  Requires flash_prefill_supported(), ma.sk == 1, every 8-key run of the

@@ -777,7 +777,7 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
   // The MFMA kernel's softmax takes the raw q.k maximum as its reference, which is only the largest
   // scaled score for scale > 0; other scales take the generic kernel.
   if (dtype == KH_BF16 && lq > 1 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
-    return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, st, scale, causal != 0);
+    return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
   return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal, nullptr, 0, MaskArgs{},
                         dtype);
 }
@@ -808,7 +808,7 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
   const double fl = (double)-1e38f / (double)scale;
   ma.floor_raw = (scale > 0.f && fl >= -(double)FLT_MAX) ? (float)fl : -INFINITY;
 
-  if (!(dtype == KH_BF16 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st)))
+  if (!(dtype == KH_BF16 && scale > 0.f && d == 128 && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st)))
     return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
 
   // MFMA path: the mask must have a unit key stride and 16-byte aligned 8-key runs; otherwise it is

@@ -41,21 +41,28 @@ constexpr int kPersistWaves = 8;  // waves per workgroup of the persistent causa
 constexpr int kPersistMinItems = 2;  // persistent from this many query blocks per CU up (0: never)
 constexpr bool kPersistXcdLocal = true;  // XCD-local item order where the shape allows it
 constexpr bool kMirrorSlots = true;      // mirrored row slots for the SIMD's second wave
-constexpr int FA_D = 128;
-constexpr int FA_KSTR = FA_D + 8;  // K row stride in LDS (elements): 272 B keeps 16-lane reads conflict-free
 
-template <int BN, int WAVES>
+// D: head dimension, 64 or 128.
+template <int BN, int WAVES, int D = 128>
 struct Cfg {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static constexpr int THREADS = WAVES * 64;
+  // K row stride in LDS (elements): 272 B (D 128) or 144 B (D 64) puts the 16-byte reads of 16
+  // consecutive rows on 64 distinct banks.
+  static constexpr int KSTR = D + 8;
   // V row stride (elements).  320 B = 80 dwords = 16 banks (mod 64) apart per row.  The LDS has 64
   // banks and serves a transposing read 32 lanes per clock: the two 16-lane groups of a clock read
   // the same 4 rows at column offsets 8 banks apart, so rows must be 16 banks apart for the 64
   // dwords to fall on 64 distinct banks (a 288-byte stride gave 2-way conflicts on 28 % of the
-  // LDS-active cycles).
-  static constexpr int VSTR = FA_D + 32;
-  static constexpr int KTILE = BN * FA_KSTR;         // elements
+  // LDS-active cycles).  D 64: 192 B = 48 dwords, rows 16 banks apart the other way round.
+  static constexpr int VSTR = D + 32;
+  static constexpr int KTILE = BN * KSTR;            // elements
   static constexpr int VTILE = BN * VSTR;            // elements
-  static constexpr int NK = BN * 16 / THREADS;       // 16-byte K (and V) chunks per thread per tile
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per K or V row
+  static constexpr int CPR_LOG = D == 128 ? 4 : 3;
+  static constexpr int NK = BN * CPR / THREADS;      // 16-byte K (and V) chunks per thread per tile
+  static constexpr int NQ = D / 16;                  // 16-column MFMA k-steps of q.k (Q registers)
+  static constexpr int ND = D / 32;                  // 32-column output tiles of P V
   // Compute works on 64-key chunks; a staged tile holds NCH of them.
   static constexpr int BNC = 64;
   static constexpr int NCH = BN / BNC;
@@ -93,9 +100,9 @@ __device__ __forceinline__ void sched_reads_ahead() {
 }
 
 // Shared per-workgroup setup and staging helpers.
-template <int BN, int WAVES>
+template <int BN, int WAVES, int D = 128>
 struct Flash {
-  using C = Cfg<BN, WAVES>;
+  using C = Cfg<BN, WAVES, D>;
   int G, BMQ, tid, wave, lane, r, g, b, hk, hqi, q0, qw0, qi, ntiles, wave_last_q, wave_tiles, dcol;
   __amdgpu_buffer_rsrc_t rk, rv;
   // Element strides as 32-bit values (the entry checks they fit): half the scalar registers of
@@ -115,7 +122,7 @@ struct Flash {
     lane = tid & 63;
     r = lane & 31;
     g = lane >> 5;
-    dcol = 8 * (tid & 15);
+    dcol = 8 * (tid & (C::CPR - 1));
   }
   // 32-row slot of this wave inside its head's query block.  Waves w and w + 4 of an 8-wave
   // workgroup share a SIMD; the second four take their slots mirrored, so that on the causal
@@ -142,8 +149,8 @@ struct Flash {
     const int nchunks = (kv_end + C::BNC - 1) / C::BNC;
     wave_last_q = min(qw0 + 31, lq - 1);
     wave_tiles = qw0 >= lq ? 0 : (causal ? min(nchunks, wave_last_q / C::BNC + 1) : nchunks);
-    rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hk * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + FA_D) * 2));
-    rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hk * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + FA_D) * 2));
+    rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hk * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 2));
+    rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hk * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 2));
   }
   __device__ __forceinline__ void init(int batch, int hq, int hkv, int lq, int lk, const AttnStrides& s, bool causal,
                                        int n_qblocks, const uint16_t* K, const uint16_t* V) {
@@ -166,60 +173,60 @@ struct Flash {
   // Q row of this lane in item (bh, qblk) of another item than the current one (the persistent
   // kernel's prefetch), from the per-workgroup fields alone.
   __device__ __forceinline__ void load_q_of(int bh, int qblk, int hkv, const uint16_t* Q, int lq,
-                                            bf16x8 (&qreg)[8]) const {
+                                            bf16x8 (&qreg)[C::NQ]) const {
     const int wpg = WAVES / G;
     const int bb = bh / hkv, hqn = (bh % hkv) * G + wave / wpg, qin = qblk * BMQ + row_slot(wpg) * 32 + r;
     const auto rq = make_rsrc(Q + (int64_t)bb * st.qb + (int64_t)hqn * st.qh,
-                              (uint32_t)(((int64_t)(lq - 1) * st.qs + FA_D) * 2));
+                              (uint32_t)(((int64_t)(lq - 1) * st.qs + D) * 2));
     const uint32_t qoff = (uint32_t)(((int64_t)qin * st.qs + 8 * g) * 2);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
+    for (int c = 0; c < C::NQ; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
   }
   // K and V byte ranges of pair bh.
   __device__ __forceinline__ void kv_rsrc_of(int bh, int hkv, int lk, const uint16_t* K, const uint16_t* V,
                                              __amdgpu_buffer_rsrc_t& rkn, __amdgpu_buffer_rsrc_t& rvn) const {
     const int bb = bh / hkv, hh = bh % hkv;
-    rkn = make_rsrc(K + (int64_t)bb * st.kb + (int64_t)hh * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + FA_D) * 2));
-    rvn = make_rsrc(V + (int64_t)bb * st.vb + (int64_t)hh * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + FA_D) * 2));
+    rkn = make_rsrc(K + (int64_t)bb * st.kb + (int64_t)hh * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 2));
+    rvn = make_rsrc(V + (int64_t)bb * st.vb + (int64_t)hh * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 2));
   }
   // This lane's Q row: query qi, columns 8 g + 16 c .. + 7 (c = 0..7).
-  __device__ __forceinline__ void load_q(const uint16_t* Q, int lq, bf16x8 (&qreg)[8]) const {
+  __device__ __forceinline__ void load_q(const uint16_t* Q, int lq, bf16x8 (&qreg)[C::NQ]) const {
     const uint16_t* qh = Q + (int64_t)b * st.qb + (int64_t)hqi * st.qh;
-    const auto rq = make_rsrc(qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + FA_D) * 2));
+    const auto rq = make_rsrc(qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + D) * 2));
     const uint32_t qoff = (uint32_t)(((int64_t)qi * st.qs + 8 * g) * 2);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
+    for (int c = 0; c < C::NQ; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
   }
   // K and V rows: chunk id = tid + THREADS i -> key id / 16, d 8 * (id % 16).
   __device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rsrc, int64_t rstride, int t,
                                             uint4 (&stg)[C::NK]) const {
 #pragma unroll
     for (int i = 0; i < C::NK; ++i) {
-      const int key = t * BN + ((tid + C::THREADS * i) >> 4);
+      const int key = t * BN + ((tid + C::THREADS * i) >> C::CPR_LOG);
       stg[i] = buf_load16(rsrc, (uint32_t)(((int64_t)key * rstride + dcol) * 2));
     }
   }
   __device__ __forceinline__ void store_k(uint16_t* ks, const uint4 (&kst)[C::NK]) const {
 #pragma unroll
     for (int i = 0; i < C::NK; ++i)
-      *reinterpret_cast<uint4*>(ks + swap23((tid + C::THREADS * i) >> 4) * FA_KSTR + dcol) = kst[i];
+      *reinterpret_cast<uint4*>(ks + swap23((tid + C::THREADS * i) >> C::CPR_LOG) * C::KSTR + dcol) = kst[i];
   }
   __device__ __forceinline__ void store_v(uint16_t* vs, const uint4 (&vst)[C::NK]) const {
 #pragma unroll
     for (int i = 0; i < C::NK; ++i)
-      *reinterpret_cast<uint4*>(vs + ((tid + C::THREADS * i) >> 4) * C::VSTR + dcol) = vst[i];
+      *reinterpret_cast<uint4*>(vs + ((tid + C::THREADS * i) >> C::CPR_LOG) * C::VSTR + dcol) = vst[i];
   }
   // O^T += V^T P^T with V row-major in LDS.  The A operand of chunk kc (lane: d = 32 dt + r, keys
   // 16 kc + 8 g + e) is two transposing reads: lane l = 16 G + L supplies row 16 kc + 8 g + L / 4
   // (+ 4 for the second read), columns 32 dt + 16 (G & 1) + 4 (L & 3) .. + 3 -- a per-lane base
   // plus compile-time offsets.
-  __device__ __forceinline__ void pv(const uint16_t* vs, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[4]) const {
+  __device__ __forceinline__ void pv(const uint16_t* vs, const bf16x8 (&pk)[2 * C::NSUB], f32x16 (&oacc)[C::ND]) const {
     const int L = lane & 15, Gq = lane >> 4;
     const uint16_t* vbase = vs + (8 * (Gq >> 1) + (L >> 2)) * C::VSTR + 16 * (Gq & 1) + 4 * (L & 3);
     constexpr int KC = 2 * C::NSUB;
-    v8i16 af[4 * KC];
+    v8i16 af[C::ND * KC];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
         const uint16_t* p0 = vbase + 16 * kc * C::VSTR + 32 * dt;
@@ -228,37 +235,38 @@ struct Flash {
         af[dt * KC + kc] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
         oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[dt * KC + kc]), pk[kc],
                                                            oacc[dt], 0, 0, 0);
-    sched_reads_ahead<4 * KC, 2>();
+    sched_reads_ahead<C::ND * KC, 2>();
   }
   // S^T subtiles of one 64-key chunk in LDS; the accumulators start at cinit (INIT) or 0.
   template <bool INIT>
-  __device__ __forceinline__ void qk(const uint16_t* ks, const bf16x8 (&qreg)[8], const f32x16& cinit,
+  __device__ __forceinline__ void qk(const uint16_t* ks, const bf16x8 (&qreg)[C::NQ], const f32x16& cinit,
                                      f32x16 (&sacc)[C::NSUB]) const {
-    bf16x8 kf[C::NSUB * 8];
+    bf16x8 kf[C::NSUB * C::NQ];
 #pragma unroll
     for (int s = 0; s < C::NSUB; ++s) {
-      const uint16_t* krp = ks + (32 * s + r) * FA_KSTR + 8 * g;
+      const uint16_t* krp = ks + (32 * s + r) * C::KSTR + 8 * g;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) kf[s * 8 + c] = as_bf16x8(*reinterpret_cast<const uint4*>(krp + 16 * c));
+      for (int c = 0; c < C::NQ; ++c) kf[s * C::NQ + c] = as_bf16x8(*reinterpret_cast<const uint4*>(krp + 16 * c));
     }
 #pragma unroll
     for (int s = 0; s < C::NSUB; ++s) {
       if constexpr (INIT) {
-        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8], qreg[0], cinit, 0, 0, 0);
+        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * C::NQ], qreg[0], cinit, 0, 0, 0);
       } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j) sacc[s][j] = 0.f;
-        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8], qreg[0], sacc[s], 0, 0, 0);
+        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * C::NQ], qreg[0], sacc[s], 0, 0, 0);
       }
 #pragma unroll
-      for (int c = 1; c < 8; ++c) sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * 8 + c], qreg[c], sacc[s], 0, 0, 0);
+      for (int c = 1; c < C::NQ; ++c)
+        sacc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s * C::NQ + c], qreg[c], sacc[s], 0, 0, 0);
     }
-    sched_reads_ahead<C::NSUB * 8, 1>();
+    sched_reads_ahead<C::NSUB * C::NQ, 1>();
   }
   // Causal / length mask of chunk t (only chunks crossing the diagonal or the sequence end).
   template <bool CAUSAL>
@@ -325,14 +333,14 @@ struct Flash {
   // O[qi][d] = oacc / l; lane holds d = 32dt + 8(j/4) + 4g + j%4.  A row whose sum l is 0 stores
   // zeros, or NaN with NAN_EMPTY (the reference softmax's 0 / 0 on the explicit-mask route).
   template <bool NAN_EMPTY = false>
-  __device__ __forceinline__ void store_o(uint16_t* O, int lq, float l_run, const f32x16 (&oacc)[4]) const {
+  __device__ __forceinline__ void store_o(uint16_t* O, int lq, float l_run, const f32x16 (&oacc)[C::ND]) const {
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     if (qi < lq) {
       const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
       const bool nan_row = NAN_EMPTY && !(l_tot > 0.f);
       uint16_t* orow = O + (int64_t)b * st.ob + (int64_t)hqi * st.oh + (int64_t)qi * st.os;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
           const int d = 32 * dt + 8 * a + 4 * g;
@@ -411,8 +419,8 @@ struct SoftmaxLog2 {
   // Raises every row's reference to its exact maximum over the chunk (when higher), shifts the
   // chunk's scores to the new reference and rescales O and l.  A row with nothing unmasked so far
   // keeps m = -inf (and P = 0).
-  template <int NSUB>
-  __device__ __forceinline__ void raise(f32x16 (&sc)[NSUB], float c, f32x16 (&oacc)[4]) {
+  template <int NSUB, int ND>
+  __device__ __forceinline__ void raise(f32x16 (&sc)[NSUB], float c, f32x16 (&oacc)[ND]) {
     const float mx = chunk_row_max(sc);  // relative to m (absolute while m = -inf)
     float d, alpha;
     if (m == -INFINITY) {
@@ -430,7 +438,7 @@ struct SoftmaxLog2 {
       for (int j = 0; j < 16; ++j) sc[s][j] -= d;
     l *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
     const float mn = m == -INFINITY ? 0.f : -m;
@@ -454,8 +462,8 @@ struct SoftmaxRaw {
   // Raises the reference max when this tile needs it (rescaling O and l); true (wave-uniform) if
   // any lane did, in which case P must be recomputed.  floor: the lowest row max (raw units): the
   // reference softmax starts its max at f32(-1e38).
-  template <int NSUB>
-  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[4], float floor) {
+  template <int NSUB, int ND>
+  __device__ __forceinline__ bool update(const f32x16 (&sc)[NSUB], float c2, f32x16 (&oacc)[ND], float floor) {
     const float mx = fmaxf(chunk_row_max(sc), floor);
     // NaN-free by construction (this file is compiled assuming no NaNs, so that fmaxf needs no
     // canonicalisation): a row with nothing unmasked (mx = -inf) never asks for a raise, and
@@ -467,7 +475,7 @@ struct SoftmaxRaw {
       m_ref = m_new;
       l_run *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
       return true;
@@ -502,26 +510,26 @@ struct SoftmaxRaw {
 // =============================================================================================
 // MASKT: 0 = causal / none as CAUSAL says; 1, 2 = additive f32 / bf16 mask M (64-key tiles, no
 // causal mask, the reference's explicit-mask route).
-template <int BN, int WAVES, int MINB, bool CAUSAL, int MASKT = 0>
+template <int BN, int WAVES, int MINB, bool CAUSAL, int MASKT = 0, int D = 128>
 __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale,
     int n_qblocks, const void* __restrict__ M, MaskArgs ma) {
-  using C = Cfg<BN, WAVES>;
-  using FL = Flash<BN, WAVES>;
-  static_assert(MASKT == 0 || (BN == 64 && !CAUSAL), "masked tiles are 64 keys, without causal masking");
+  using C = Cfg<BN, WAVES, D>;
+  using FL = Flash<BN, WAVES, D>;
+  static_assert(MASKT == 0 || (BN == 64 && !CAUSAL && D == 128), "masked tiles are 64 keys, D 128, not causal");
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
   FL F;
   F.init(batch, hq, hkv, lq, lk, st, CAUSAL, n_qblocks, K, V);
   const float c2 = scale * kLog2e;
-  bf16x8 qreg[8];
+  bf16x8 qreg[C::NQ];
   F.load_q(Q, lq, qreg);
 
   uint4 kst[C::NK], vst[C::NK];
-  f32x16 oacc[4];
+  f32x16 oacc[C::ND];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
   SoftmaxLog2 sl;
@@ -559,7 +567,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
         f32x16 sacc[C::NSUB];
         bf16x8 pk[2 * C::NSUB];
         if constexpr (MASKT == 0) {
-          F.template qk<true>(ks + c * C::BNC * FA_KSTR, qreg, sl.mneg, sacc);
+          F.template qk<true>(ks + c * C::BNC * C::KSTR, qreg, sl.mneg, sacc);
           F.template mask<CAUSAL>(tc, lk, sacc);
           float ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
           if (sl.need_raise(ps)) {
@@ -568,7 +576,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
           }
           sl.l += ps;
         } else {
-          F.template qk<false>(ks + c * C::BNC * FA_KSTR, qreg, sl.mneg, sacc);
+          F.template qk<false>(ks + c * C::BNC * C::KSTR, qreg, sl.mneg, sacc);
           F.template apply_mask<MASKT>(tc, lk, mreg, ma.inv_scale, sacc);
           // Written as P computed with the current reference max, then recomputed after a raise
           // (rare after the first tile); the compiler folds the two into one exponentiation
@@ -599,13 +607,13 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
 // each).  When P is a multiple of the pair count, the odd passes are mirrored so that a workgroup
 // keeps one (batch, kv head) pair for all its items (its K/V stay in its XCD's L2).  The per-item
 // arithmetic is the tile kernel's, so outputs are identical to it.
-template <bool CAUSAL>
+template <bool CAUSAL, int D = 128>
 __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale, int n_qblocks) {
   constexpr int BN = 128, WAVES = kPersistWaves;
-  using C = Cfg<BN, WAVES>;
-  using FL = Flash<BN, WAVES>;
+  using C = Cfg<BN, WAVES, D>;
+  using FL = Flash<BN, WAVES, D>;
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
   const int P = gridDim.x, w = blockIdx.x;
@@ -640,12 +648,12 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
   F.setup(hq, hkv, st);
   F.set_item(bh, qblk, hkv, lq, lk, CAUSAL, K, V);
   const float c2 = scale * kLog2e;
-  bf16x8 qreg[8];
+  bf16x8 qreg[C::NQ];
   F.load_q(Q, lq, qreg);
   uint4 kst[C::NK], vst[C::NK];
-  f32x16 oacc[4];
+  f32x16 oacc[C::ND];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
   SoftmaxLog2 sl;
@@ -681,7 +689,7 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
         if (tc < F.wave_tiles) {
           f32x16 sacc[C::NSUB];
           bf16x8 pk[2 * C::NSUB];
-          F.template qk<true>(ks + c * C::BNC * FA_KSTR, qreg, sl.mneg, sacc);
+          F.template qk<true>(ks + c * C::BNC * C::KSTR, qreg, sl.mneg, sacc);
           if (more && tc == F.wave_tiles - 1) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
           F.template mask<CAUSAL>(tc, lk, sacc);
           float ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
@@ -705,7 +713,7 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
     if (!more) break;
     F.set_item(bhn, qbn, hkv, lq, lk, CAUSAL, K, V);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
     sl = SoftmaxLog2();
@@ -722,15 +730,43 @@ constexpr int kSmallGrid = 256;
 constexpr int kSmallWaves = 4;
 constexpr int kSmallBN = 128;
 
-template <int BN, int WAVES, bool CAUSAL>
+template <int BN, int WAVES, bool CAUSAL, int D>
 void launch_fwd(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
                 const AttnStrides& st, float scale) {
   const int BMQ = 32 * (WAVES / (hq / hkv));
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int nblk = nqb * batch * hkv;
-  flash_fwd_kernel<BN, WAVES, 1, CAUSAL><<<nblk, WAVES * 64, 0, stream()>>>(
+  flash_fwd_kernel<BN, WAVES, 1, CAUSAL, 0, D><<<nblk, WAVES * 64, 0, stream()>>>(
       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, lq, lk, st, scale,
       nqb, nullptr, MaskArgs{});
+}
+
+template <int D>
+int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
+                     const AttnStrides& st, float scale, bool causal) {
+  const int G = hq / hkv;
+  const int BMQ = 32 * (kWaves / G);
+  const int nqb = (lq + BMQ - 1) / BMQ;
+  const int64_t nblk64 = (int64_t)nqb * batch * hkv;
+  KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
+  if (nblk64 < kSmallGrid && G <= kSmallWaves) {
+    if (causal)
+      launch_fwd<kSmallBN, kSmallWaves, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+    else
+      launch_fwd<kSmallBN, kSmallWaves, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  } else if (causal && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
+    // Enough causal query blocks for every CU to take several: one resident workgroup per CU.
+    static_assert(kPersistWaves == kWaves, "the persistent kernel's query blocks are the tile kernel's");
+    flash_fwd_persistent_kernel<true, D><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
+        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
+        st, scale, nqb);
+  } else if (causal) {
+    launch_fwd<128, kWaves, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  } else {
+    launch_fwd<128, kWaves, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  }
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 }  // namespace
@@ -740,7 +776,7 @@ namespace kh {
 bool flash_prefill_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv,
                              int64_t lq, int64_t lk, int d, const AttnStrides& st) {
   const int G = hq / hkv;
-  if (d != FA_D || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
+  if (!(d == 64 || d == 128) || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
   const int64_t all[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.vb, st.vh, st.vs, st.ob, st.oh, st.os};
   for (int64_t s : all)
@@ -757,30 +793,9 @@ bool flash_prefill_supported(const void* q, const void* k, const void* v, const 
 }
 
 int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
-                              int lq, int lk, const AttnStrides& st, float scale, bool causal) {
-  const int G = hq / hkv;
-  const int BMQ = 32 * (kWaves / G);
-  const int nqb = (lq + BMQ - 1) / BMQ;
-  const int64_t nblk64 = (int64_t)nqb * batch * hkv;
-  KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
-  if (nblk64 < kSmallGrid && G <= kSmallWaves) {
-    if (causal)
-      launch_fwd<kSmallBN, kSmallWaves, true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
-    else
-      launch_fwd<kSmallBN, kSmallWaves, false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
-  } else if (causal && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
-    // Enough causal query blocks for every CU to take several: one resident workgroup per CU.
-    static_assert(kPersistWaves == kWaves, "the persistent kernel's query blocks are the tile kernel's");
-    flash_fwd_persistent_kernel<true><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
-        st, scale, nqb);
-  } else if (causal) {
-    launch_fwd<128, kWaves, true>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
-  } else {
-    launch_fwd<128, kWaves, false>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
-  }
-  KH_CHECK_LAUNCH();
-  return KH_OK;
+                              int lq, int lk, int d, const AttnStrides& st, float scale, bool causal) {
+  if (d == 64) return launch_prefill_d<64>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, causal);
+  return launch_prefill_d<128>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, causal);
 }
 
 int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq,

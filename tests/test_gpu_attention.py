@@ -50,6 +50,55 @@ def test_flash_bf16_mfma_matches_oracle(hip, B, Hq, Hkv, S, causal):
     assert err < BF16_ATOL, err
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(1, 8, 8, 77), (2, 8, 4, 300), (1, 16, 4, 257), (1, 16, 2, 513),
+                                        (1, 8, 1, 130), (1, 16, 16, 1000)])
+def test_flash_bf16_head_dim_64_matches_oracle(hip, B, Hq, Hkv, S, causal):
+    """head_dim 64 on the MFMA kernel (D-templated tiles: 144-byte K rows, 192-byte V rows, four
+    Q registers, two output tiles per wave), GQA 1, 2, 4 and 8, ragged lengths."""
+    q, qh = seeded(24, (B, Hq, S, 64), "bfloat16")
+    k, kh = seeded(25, (B, Hkv, S, 64), "bfloat16")
+    v, vh = seeded(26, (B, Hkv, S, 64), "bfloat16")
+    out = _sdpa_gpu(q, k, v, causal)
+    ref = oracle.sdpa(qh, kh, vh, causal=causal)
+    err = float(np.max(np.abs(out - ref)))
+    assert err < BF16_ATOL, err
+
+
+def test_flash_bf16_head_dim_64_persistent_path(hip):
+    """head_dim 64 at a size that takes the persistent causal kernel (B=4, Hq=16, Hkv=8, S=2048: 512
+    query blocks on 256 CUs): two whole (batch, head) slices and sampled rows against the oracle,
+    and a call time that only the MFMA kernel reaches (the generic kernel takes hundreds of times
+    longer at this size)."""
+    from kandle_amd import _lib
+    B, Hq, Hkv, S, D = 4, 16, 8, 2048, 64
+    q, qh = seeded(94, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(95, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(96, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    G = Hq // Hkv
+    for b, h in [(0, 0), (B - 1, Hq - 1)]:
+        ref = oracle.sdpa(qh[b:b + 1, h:h + 1], kh[b:b + 1, h // G:h // G + 1], vh[b:b + 1, h // G:h // G + 1],
+                          causal=True)
+        err = float(np.max(np.abs(out[b, h] - ref[0, 0])))
+        assert err < BF16_ATOL, ("slice", b, h, err)
+    r = np.random.default_rng(8)
+    for b, h, i in [(1, 5, S - 1), (2, 9, 0)] + [(int(r.integers(B)), int(r.integers(Hq)), int(r.integers(S)))
+                                                 for _ in range(20)]:
+        hk = h // G
+        ref = oracle.sdpa(qh[b:b + 1, h:h + 1, i:i + 1], kh[b:b + 1, hk:hk + 1, :i + 1],
+                          vh[b:b + 1, hk:hk + 1, :i + 1])
+        err = float(np.max(np.abs(out[b, h, i] - ref[0, 0, 0])))
+        assert err < BF16_ATOL, (b, h, i, err)
+    e0, e1 = _lib.Event(), _lib.Event()
+    e0.record()
+    for _ in range(5):
+        F.scaled_dot_product_attention(q, k, v, is_causal=True).dispose()
+    e1.record()
+    ms = e0.elapsed_ms(e1) / 5
+    assert ms < 2.0, ms   # 2.2e10 FLOP: about 0.03 ms on the MFMA kernel
+
+
 def test_flash_bf16_rectangular_noncausal(hip):
     """Lq != Lk (prefix attention without a mask)."""
     q, qh = seeded(31, (1, 4, 40, 128), "bfloat16")

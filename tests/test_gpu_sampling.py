@@ -112,6 +112,19 @@ def test_small_vocab_ties_and_signed_zero(hip):
     assert res.token_id == 0
 
 
+@pytest.mark.parametrize("top_p", [-0.5, 0.0])
+def test_nonpositive_top_p_keeps_one_token(hip, top_p):
+    """top_p <= 0 keeps exactly the most probable token, as the reference loop does (its running
+    sum passes top_p at the first id, sampling/index.ts:197-215): on the full-sort path (top-p
+    alone) and on the selection path (with top-k), against the oracle."""
+    x = _logits(61)
+    for cfg in (SamplerConfig(temperature=0.8, top_p=top_p), SamplerConfig(temperature=0.8, top_k=50, top_p=top_p)):
+        for seed in (1, 2, 3):
+            res = _check(x, cfg, seed, seed)
+            assert res.token_id == int(np.argmax(x))
+            assert res.log_prob == pytest.approx(0.0, abs=1e-6)
+
+
 def test_counter_read_on_device_and_2d_logits(hip):
     x = _logits(15, n=4096, scale=2.0)
     lg = Tensor(x.reshape(1, -1), dtype="float32")
