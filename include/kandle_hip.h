@@ -249,7 +249,7 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out,
  * (query head h reads kv head h / (hq / hkv)); causal masks key j > query i (top-left aligned).
  * Shapes q [batch, hq, lq, d], k/v [batch, hkv, lk, d], o [batch, hq, lq, d]; `strides` holds 12
  * element strides: q (batch, head, seq), k (…), v (…), o (…); the d axis is contiguous.
- * bf16 with d == 128 runs the MFMA flash kernel; lq == 1 runs split-K decode; otherwise a
+ * bf16 with d == 64 or 128 runs the MFMA flash kernel; lq == 1 runs split-K decode; otherwise a
  * LDS-tiled fp32-math kernel (d <= 256).  Replaces the `flash_attention` kernel
  * (reference signature packages/types/src/backend/register.ts:102-109; semantics
  * packages/backend-webgpu/src/kernels/attention/builder.ts:138-329; called from
