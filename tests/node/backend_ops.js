@@ -1,0 +1,153 @@
+'use strict';
+/*
+ * backend_ops.js — runs kernels through the TypeScript HipBackend (packages/backend-hip, compiled
+ * by strip-types.js into dist/index.js) the way Kandle's dispatcher calls them: registry lookups by
+ * name and the reference kernel signatures.  Test infrastructure: tests/test_gpu_node_backend.py
+ * writes the inputs and checks the outputs against the CPU oracle.
+ *
+ * Usage: node backend_ops.js DIR
+ *   DIR/meta.json holds the shapes; inputs are raw little-endian files (bf16 as uint16 bits, f32,
+ *   int32); outputs are written back as f32 (or int32) files and a JSON summary is printed.
+ */
+const fs = require('fs');
+const path = require('path');
+const { HipBackend } = require(path.join(__dirname, '..', '..', 'packages', 'backend-hip', 'dist', 'index.js'));
+
+const dir = process.argv[2];
+const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
+
+function readU16(name) {
+  const b = fs.readFileSync(path.join(dir, name));
+  return new Uint16Array(b.buffer, b.byteOffset, b.length / 2);
+}
+function readF32(name) {
+  const b = fs.readFileSync(path.join(dir, name));
+  return new Float32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.length));
+}
+function readI32(name) {
+  const b = fs.readFileSync(path.join(dir, name));
+  return new Int32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.length));
+}
+function write(name, arr) {
+  fs.writeFileSync(path.join(dir, name), Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
+}
+
+async function main() {
+  const backend = await HipBackend.create(0);
+  const ops = backend.operators;
+  const t = (shape, dtype, data) => backend.createTensorHandle({ shape, dtype, data });
+  const before = backend.memoryStats();
+
+  // flash_attention(q, k, v, out, scale, isCausal): causal GQA prefill, bf16
+  const f = meta.flash;
+  const q = t([f.B, f.Hq, f.S, f.D], 'bfloat16', readU16('fq'));
+  const k = t([f.B, f.Hkv, f.S, f.D], 'bfloat16', readU16('fk'));
+  const v = t([f.B, f.Hkv, f.S, f.D], 'bfloat16', readU16('fv'));
+  const o = backend.createTensorHandle([f.B, f.Hq, f.S, f.D], 'bfloat16');
+  ops.find('flash_attention')(q, k, v, o, 1 / Math.sqrt(f.D), true);
+  write('fo', await o.dataAsync());
+
+  // sdpa_masked with a [Lq, Lk] f32 additive mask broadcast over batch and heads
+  const mask = t([f.S, f.S], 'float32', readF32('fmask'));
+  const om = backend.createTensorHandle([f.B, f.Hq, f.S, f.D], 'bfloat16');
+  ops.find('sdpa_masked')(q, k, v, mask, om, 1 / Math.sqrt(f.D));
+  write('fmo', await om.dataAsync());
+
+  // rms_norm of an fp32 residual into bf16, with weight
+  const r = meta.norm;
+  const x = t([r.rows, r.n], 'float32', readF32('nx'));
+  const w = t([r.n], 'bfloat16', readU16('nw'));
+  const y = ops.find('rms_norm')([x], { normalizedShape: [r.n], eps: r.eps, weight: w, outDtype: 'bfloat16' });
+  write('ny', await y.dataAsync());
+
+  // matmul: out = a @ b^T + 1 * c (linear with a residual), bf16 in, f32 out
+  const m = meta.mm;
+  const a = t([m.M, m.K], 'bfloat16', readU16('ma'));
+  const b = t([m.N, m.K], 'bfloat16', readU16('mb'));
+  const c = t([m.M, m.N], 'float32', readF32('mc'));
+  const out = backend.createTensorHandle([m.M, m.N], 'float32');
+  ops.find('matmul')({ output: out, M: m.M, K: m.K, N: m.N, batchSize: 1, transposeA: false, transposeB: true,
+                       alpha: 1, beta: 1, inputC: c }, a, b);
+  write('mo', await out.dataAsync());
+
+  // silu_mul, and the iterator kernels silu / mul on a strided (transposed) view
+  const g = t([m.M, m.N], 'float32', readF32('mc'));
+  const u = backend.createTensorHandle({ shape: [m.M, m.N], dtype: 'float32' });
+  ops.find('fill')(u, 0.5);
+  const h = backend.createTensorHandle([m.M, m.N], 'float32');
+  ops.find('silu_mul')(g, u, h);
+  write('sm', await h.dataAsync());
+  const gT = backend.createTensorHandle({ storage: g.storage, shape: [m.N, m.M], dtype: 'float32',
+                                          strides: [1, m.N], offset: 0 });
+  const s1 = backend.createTensorHandle([m.N, m.M], 'float32');
+  ops.find('silu')({ numInputs: 1, output: () => ({ tensorHandle: s1 }), input: () => ({ tensorHandle: gT }) });
+  write('st', await s1.dataAsync());
+  const prod = backend.createTensorHandle([m.N, m.M], 'float32');
+  ops.find('mul')({ numInputs: 2, output: () => ({ tensorHandle: prod }),
+                    input: (i) => ({ tensorHandle: i === 0 ? gT : s1 }) });
+  write('pt', await prod.dataAsync());
+
+  // index_select (embedding rows) and argmax over the last axis
+  const e = meta.emb;
+  const table = t([e.V, e.H], 'bfloat16', readU16('et'));
+  const ids = t([e.n], 'int32', readI32('ei'));
+  const rows = backend.createTensorHandle([e.n, e.H], 'float32');
+  ops.find('index_select')(table, ids, { dim: 0 }, rows);
+  write('eo', await rows.dataAsync());
+  const am = backend.createTensorHandle([m.M], 'int32');
+  ops.find('argmax')(c, am);
+  write('am', await am.dataAsync());
+
+  // neg / cos / sin (the composite RoPE's iterator kernels) and arange
+  const un = {};
+  for (const name of ['neg', 'cos', 'sin']) {
+    un[name] = backend.createTensorHandle([m.M, m.N], 'float32');
+    ops.find(name)({ numInputs: 1, output: () => ({ tensorHandle: un[name] }), input: () => ({ tensorHandle: g }) });
+    write('u_' + name, await un[name].dataAsync());
+  }
+  const ar = backend.createTensorHandle([10], 'float32');
+  ops.find('arange')(ar, 0.5, 2);
+  write('ar', await ar.dataAsync());
+
+  // rms_norm_rope into whole KV caches at device positions (the decode-step cache write)
+  const p = meta.rope;
+  const rq = t([1, p.T, p.Hq, p.D], 'bfloat16', readU16('rq'));
+  const rk = t([1, p.T, p.Hkv, p.D], 'bfloat16', readU16('rk'));
+  const rv = t([1, p.T, p.Hkv, p.D], 'bfloat16', readU16('rv'));
+  const wq = t([p.D], 'bfloat16', readU16('rwq'));
+  const wk = t([p.D], 'bfloat16', readU16('rwk'));
+  const inv = t([p.D / 2], 'float32', readF32('rinv'));
+  const pos = t([p.T], 'int32', readI32('rpos'));
+  const kc = backend.createTensorHandle([1, p.Hkv, p.L, p.D], 'bfloat16');
+  const vc = backend.createTensorHandle([1, p.Hkv, p.L, p.D], 'bfloat16');
+  ops.find('fill')(kc, 7);
+  ops.find('fill')(vc, 7);
+  const qk = ops.find('rms_norm_rope')(rq, rk, { qWeight: wq, kWeight: wk, invFreq: inv, positions: pos, eps: p.eps,
+                                                 kOut: kc, v: rv, vOut: vc, cachePositions: true });
+  write('rqo', await qk[0].dataAsync());
+  write('rkc', await kc.dataAsync());
+  write('rvc', await vc.dataAsync());
+
+  // decode_attention: one token per sequence against ragged cache lengths read from the device
+  const d = meta.decode;
+  const dq = t([d.B, d.Hq, d.D], 'bfloat16', readU16('dq'));
+  const dk = t([d.B, d.Hkv, d.L, d.D], 'bfloat16', readU16('dk'));
+  const dv = t([d.B, d.Hkv, d.L, d.D], 'bfloat16', readU16('dv'));
+  const lens = t([d.B], 'int32', new Int32Array(d.lens));
+  const dout = backend.createTensorHandle([d.B, d.Hq, 1, d.D], 'bfloat16');
+  ops.find('decode_attention')(dq, dk, dv, lens, dout, 1 / Math.sqrt(d.D));
+  write('do', await dout.dataAsync());
+
+  for (const hnd of [q, k, v, o, mask, om, x, w, y, a, b, c, out, g, u, h, gT, s1, prod, table, ids, rows, am,
+                     un.neg, un.cos, un.sin, ar, rq, rk, rv, wq, wk, inv, pos, kc, vc, qk[0], qk[1], dq, dk, dv, lens, dout]) {
+    hnd.dispose();
+  }
+  backend.synchronize();
+  const after = backend.memoryStats();
+  console.log(JSON.stringify({ ok: true, names: ops.names(), liveBefore: before.liveBytes, liveAfter: after.liveBytes }));
+}
+
+main().catch((err) => {
+  console.error(err && err.stack ? err.stack : err);
+  process.exit(1);
+});

@@ -1,0 +1,121 @@
+"""The TypeScript HipBackend (packages/backend-hip/src/index.ts) on the CPU: strip-types.js erases
+its type syntax into JavaScript that the image's Node (v12, no TypeScript compiler) parses and
+loads; the module exports the plugin surface and registers the kernels under the names Kandle's
+dispatcher looks up (packages/types/src/backend/register.ts:128-144).  The stripper itself is
+checked on a snippet of every construct it handles, by running the output.  Skipped without Node
+or the built addon."""
+import json
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "packages", "backend-hip")
+ADDON = os.path.join(PKG, "native", "kandle_hip.node")
+STRIP = os.path.join(PKG, "strip-types.js")
+
+
+def _need_node():
+    if shutil.which("node") is None or not os.path.exists(ADDON):
+        pytest.skip("node or the built addon is not available")
+
+
+def _strip(src_path, out_path):
+    subprocess.run(["node", STRIP, str(src_path), str(out_path)], check=True, capture_output=True, timeout=60)
+
+
+def test_backend_source_strips_to_loadable_javascript(tmp_path):
+    _need_node()
+    out = tmp_path / "index.js"
+    _strip(os.path.join(PKG, "src", "index.ts"), out)
+    chk = subprocess.run(["node", "--check", str(out)], capture_output=True, text=True)
+    assert chk.returncode == 0, chk.stderr
+    # dist/index.js requires ../native/kandle_hip.node relative to itself: load the built copy
+    script = f"""
+      const m = require({json.dumps(os.path.join(PKG, 'dist', 'index.js'))});
+      const reg = new m.SimpleOperatorRegistry();
+      m.registerHipKernels(reg);
+      console.log(JSON.stringify({{exports: Object.keys(m).sort(), names: reg.names().sort(),
+                                  strides: m.contiguousStrides([2, 3, 4]),
+                                  bf16: Array.from(m.toBf16Bits(new Float32Array([1, -2.5, 3.14159, 65504]))),
+                                  back: Array.from(m.fromBf16Bits(new Uint16Array([0x3f80, 0xc020])))}}));"""
+    res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stderr
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    assert {"HipBackend", "HipStorage", "HipTensorHandle", "SimpleOperatorRegistry", "registerHipKernels"} <= set(r["exports"])
+    for name in ("flash_attention", "sdpa_masked", "rms_norm", "matmul", "mm", "bmm", "addmm", "baddbmm", "add",
+                 "mul", "sub", "silu", "silu_mul", "index_select", "argmax", "copy", "contiguous", "cast", "fill", "neg",
+                 "cos", "sin", "arange", "decode_attention", "rms_norm_rope"):
+        assert name in r["names"], name
+    assert r["strides"] == [12, 4, 1]
+    assert r["bf16"] == [0x3F80, 0xC020, 0x4049, 0x4780]   # RNE: 3.14159 -> 0x4049, 65504 -> 65536
+    assert r["back"] == [1.0, -2.5]
+
+
+SNIPPET = r'''
+export type Pair = [number, number];
+type Fn = (a: number, b: number) => number;
+interface Box {
+  value: number;
+  label?: string;
+}
+export interface Wide<T> {
+  items: T[];
+}
+export class Counter<T> {
+  private count: number = 0;
+  readonly name: string;
+  items: Map<string, number> = new Map<string, number>();
+  constructor(name: string, quiet?: boolean) {
+    this.name = name;
+  }
+  add(n: number = 1): number {
+    this.count += n;
+    return this.count;
+  }
+  get total(): number {
+    return this.count;
+  }
+  static make(name: string): Counter<number> {
+    return new Counter<number>(name);
+  }
+}
+export function pick(flag: boolean, a?: number, ...rest: number[]): number | undefined {
+  const obj: { [k: string]: number } = { x: 1, y: flag ? 2 : 3 };
+  const v = (flag ? (a as number) : obj.y) as number;
+  const add: Fn = (p: number, q: number): number => p + q;
+  let s: number = 0;
+  for (const r of rest) s = add(s, r);
+  if (s > 0) { return s; }
+  const t = `sum ${s as number} ${flag ? 'yes: x' : 'no'}`;
+  return t.length > 100 ? undefined : v + obj.x;
+}
+export const twice = (x: number): number => x * 2;
+function lessThan(a: number, b: number): boolean { return a < b && b > a; }
+export { lessThan };
+'''
+
+
+def test_type_stripper_handles_each_construct(tmp_path):
+    _need_node()
+    src = tmp_path / "snippet.ts"
+    src.write_text(SNIPPET)
+    out = tmp_path / "snippet.js"
+    _strip(src, out)
+    js = out.read_text()
+    for leftover in ("interface", "type Pair", "type Fn", ": number", "private", "readonly", " as ", "<string"):
+        assert leftover not in js, (leftover, js)
+    script = f"""
+      const m = require({json.dumps(str(out))});
+      const c = m.Counter.make('k');
+      c.add(); c.add(4);
+      console.log(JSON.stringify({{total: c.total, name: c.name, size: c.items.size,
+                                  p1: m.pick(true, 7), p2: m.pick(false), p3: m.pick(true, 1, 2, 3),
+                                  tw: m.twice(21), lt: m.lessThan(1, 2), keys: Object.keys(m).sort()}}));"""
+    res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, (res.stderr, js)
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    assert r == {"total": 5, "name": "k", "size": 0, "p1": 8, "p2": 4, "p3": 5, "tw": 42, "lt": True,
+                 "keys": ["Counter", "lessThan", "pick", "twice"]}
