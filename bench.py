@@ -120,7 +120,7 @@ def prep_prefill():
 
 def prep_c1():
     """Config C1 on the GPU: SDPA in fp32, B=1, Hq=16, Hkv=8, S=256, D=128, causal, scale 1/sqrt(128)
-    (the LDS-tiled fp32-math kernel)."""
+    (the fp32 MFMA flash kernel)."""
     from kandle_amd import HipTensorHandle, Tensor, kernels
     from kandle_amd import synthetic as syn
 
@@ -939,10 +939,10 @@ def main():
     if "c1" in res:
         c1 = res["c1"]
         gf = c1["flops"] / (c1["dev_ms"] * 1e-3) / 1e9
-        line["c1"] = {"workload": "C1 SDPA fp32, B=1, Hq=16, Hkv=8, S=256, D=128, causal (LDS-tiled fp32 kernel)",
+        line["c1"] = {"workload": "C1 SDPA fp32, B=1, Hq=16, Hkv=8, S=256, D=128, causal (fp32 MFMA flash kernel)",
                       "flops": c1["flops"], "ms": round(c1["dev_ms"], 4), "wall_ms": round(c1["wall_ms"], 4),
                       "GFLOP/s": round(gf, 1),
-                      "roofline": {"bound": "fp32 vector", "achieved": round(gf / 1e3, 3), "peak": 157.3,
+                      "roofline": {"bound": "mfma fp32", "achieved": round(gf / 1e3, 3), "peak": 157.3,
                                    "unit": "TFLOP/s", "frac": round(gf / 1e3 / 157.3, 4), "traffic": None}}
         if "value" not in line:
             line.update({"value": round(gf, 1), "unit": "GFLOP/s", "ms_per_step": round(c1["wall_ms"], 4),

@@ -36,4 +36,14 @@ int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v
                                      int hkv, int lq, int lk, const AttnStrides& st, float scale, const void* mask,
                                      const MaskArgs& ma, int mask_dtype);
 
+// True when the fp32 flash kernel (flash_f32.hip) takes this fp32 call: d in {32, 64, 96, 128},
+// 16-byte aligned q / k / o with strides in multiples of 4 elements, 4-byte aligned v, per-head
+// byte ranges below 2^31.
+bool flash_f32_supported(const void* q, const void* k, const void* v, const void* o, int64_t lq, int64_t lk, int d,
+                         const AttnStrides& st);
+
+// fp32 attention with fp32 MFMA (causal or not, any lq / lk, GQA) on the library stream.
+int launch_flash_f32(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
+                     int d, const AttnStrides& st, float scale, bool causal);
+
 }  // namespace kh

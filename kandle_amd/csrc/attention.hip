@@ -1,5 +1,6 @@
 // Scaled dot-product attention entry points for gfx950: routing to the bf16 MFMA flash prefill
-// (flash_prefill.hip), the split-K decode kernels and a generic fp32-math kernel (this file).
+// (flash_prefill.hip), the fp32 MFMA flash kernel (flash_f32.hip), the split-K decode kernels and a
+// generic fp32-math kernel (this file).
 //
 // Semantics (reference: packages/backend-webgpu/src/kernels/attention/builder.ts:138-329):
 //   S = (Q K^T) * scale, causal masks key j > query i (top-left aligned), GQA query head h reads
@@ -16,7 +17,7 @@ namespace {
 // =============================================================================================
 // Generic attention (f32 or bf16 storage, d <= 256, any lq/lk): one wave per query row, 64 keys
 // per step (lane j scores key k0 + j), fp32 online softmax, each lane accumulates d/64 output
-// columns.  Used for fp32 calls (config C1) and shapes the MFMA kernel does not take.
+// columns.  Used for masked fp32 calls and shapes the MFMA kernels do not take.
 // =============================================================================================
 //
 // With a mask M (mdt KH_F32 or KH_BF16; the reference's explicit-mask route, composite.ts:279-300)
@@ -778,6 +779,8 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
   // scaled score for scale > 0; other scales take the generic kernel.
   if (dtype == KH_BF16 && lq > 1 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
     return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
+  if (dtype == KH_F32 && flash_f32_supported(q, k, v, o, lq, lk, d, st))
+    return launch_flash_f32(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
   return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal, nullptr, 0, MaskArgs{},
                         dtype);
 }

@@ -1,0 +1,245 @@
+// Flash attention in fp32 for gfx950: fp32 storage, fp32 MFMA products and accumulation
+// (v_mfma_f32_32x32x2_f32), online softmax in fp32.  Config C1 (fp32 SDPA) runs here.
+//
+// Semantics as kh_flash_attention (reference: packages/backend-webgpu/src/kernels/attention/
+// builder.ts:138-329): S = (Q K^T) * scale, causal masks key j > query i (top-left aligned), GQA
+// query head h reads kv head h / (hq / hkv), O = softmax(S) V.
+//
+// One workgroup per (batch, query head, block of 32 queries), kF32Waves waves.  Wave w takes the
+// block's 32-key tiles w, w + kF32Waves, ... (with the causal mask only tiles up to the block's
+// last query), so a short prompt still spreads each block over four SIMDs.  Per tile the wave
+// forms S^T = K Q^T in D/2 MFMA steps (step s pairs head-dim element s on lanes 0-31 with s + D/2
+// on lanes 32-63): lane (r, g) = (lane & 31, lane >> 5) then holds query r's scores against keys
+// 8(v/4) + 4g + v%4, v < 16, so a query's maximum and sum are an in-lane reduction plus one
+// exchange with lane r ^ 32.  O^T = V^T P^T follows in 16 MFMA steps per 32 head-dim columns; the
+// probabilities enter as the B operand straight from the score registers (step s uses key
+// 8(s/4) + 4g + s%4, the key that lane's score s belongs to).  All of a lane's outputs belong to one
+// query, so the online-softmax rescale is a per-lane multiply.  At the end the waves' (m, l, O)
+// are combined through LDS, in wave order.
+#include <cmath>
+
+#include "attention.h"
+
+using namespace kh;
+
+namespace {
+
+constexpr int kF32Waves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr uint32_t kOut = 0xffffffffu;  // a byte offset past every buffer range: the load reads 0
+
+__device__ __forceinline__ float buf_load4f(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ float4 buf_load16f(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// c = scale * log2(e): scores are kept in log2 units (softmax by exp2).
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kF32Waves * 64) void flash_f32_kernel(const float* __restrict__ Q,
+                                                                   const float* __restrict__ K,
+                                                                   const float* __restrict__ V, float* __restrict__ O,
+                                                                   int hq, int hkv, int lq, int lk, AttnStrides st,
+                                                                   float c, int nqb) {
+  constexpr int HALF = D / 2, NH4 = HALF / 4, NDB = D / 32;
+  constexpr int OSTR = D + 4;  // LDS row stride (floats) of the wave partial outputs
+  __shared__ float2 ml_s[kF32Waves][32];
+  __shared__ __attribute__((aligned(16))) float o_s[kF32Waves][32 * OSTR];
+
+  const int lane = threadIdx.x & 63, r = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bid = blockIdx.x;
+  const int qb = nqb - 1 - bid % nqb;  // the longest causal blocks start first
+  const int bh = bid / nqb;
+  const int h = bh % hq, b = bh / hq;
+  const int hk = h / (hq / hkv);
+  const int q0 = qb * 32;
+  const int kend = CAUSAL ? min(lk, q0 + 32) : lk;
+  const int nt = (kend + 31) >> 5;
+
+  const float* Qh = Q + (int64_t)b * st.qb + (int64_t)h * st.qh;
+  const float* Kh = K + (int64_t)b * st.kb + (int64_t)hk * st.kh;
+  const float* Vh = V + (int64_t)b * st.vb + (int64_t)hk * st.vh;
+  const auto rq = make_rsrc(Qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + D) * 4));
+  const auto rk = make_rsrc(Kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 4));
+  const auto rv = make_rsrc(Vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 4));
+  const uint32_t qs = (uint32_t)st.qs, ks = (uint32_t)st.ks, vs = (uint32_t)st.vs;
+
+  // This lane's query row, half g of the head dim, pre-scaled (rows past lq read as zero).
+  const int qi = q0 + r;
+  float qv[HALF];
+#pragma unroll
+  for (int i = 0; i < NH4; ++i) {
+    const uint32_t off = qi < lq ? ((uint32_t)qi * qs + g * HALF + 4 * i) * 4u : kOut;
+    const float4 t = buf_load16f(rq, off);
+    qv[4 * i] = t.x * c;
+    qv[4 * i + 1] = t.y * c;
+    qv[4 * i + 2] = t.z * c;
+    qv[4 * i + 3] = t.w * c;
+  }
+  // Key row k0 + r, half g (rows past lk read as zero and are masked).
+  auto load_k = [&](float (&kv)[HALF], int k0) {
+    const int kr = k0 + r;
+#pragma unroll
+    for (int i = 0; i < NH4; ++i) {
+      const uint32_t off = kr < lk ? ((uint32_t)kr * ks + g * HALF + 4 * i) * 4u : kOut;
+      const float4 t = buf_load16f(rk, off);
+      kv[4 * i] = t.x;
+      kv[4 * i + 1] = t.y;
+      kv[4 * i + 2] = t.z;
+      kv[4 * i + 3] = t.w;
+    }
+  };
+  // V[key(s)][32 db + r] for the 16 keys key(s) = k0 + 8(s/4) + 4g + s%4 of the PV steps.
+  auto load_v = [&](float (&vv)[NDB][16], int k0) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int kr = k0 + 8 * (s >> 2) + 4 * g + (s & 3);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 32 * db + r) * 4u : kOut;
+        vv[db][s] = buf_load4f(rv, off);
+      }
+    }
+  };
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) oacc[db][v] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  float kv[HALF];
+  if (w < nt) load_k(kv, w * 32);
+  for (int t = w; t < nt; t += kF32Waves) {
+    const int k0 = t * 32;
+    float vv[NDB][16];
+    load_v(vv, k0);
+    f32x16 sacc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sacc[v] = 0.f;
+#pragma unroll
+    for (int s = 0; s < HALF; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[s], qv[s], sacc, 0, 0, 0);
+    if (t + kF32Waves < nt) load_k(kv, k0 + 32 * kF32Waves);  // next tile's keys, during softmax and PV
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int key = k0 + 8 * (v >> 2) + 4 * g + (v & 3);
+      const bool ok = key < lk && (!CAUSAL || key <= qi);
+      sacc[v] = ok ? sacc[v] : -INFINITY;
+      tmax = fmaxf(tmax, sacc[v]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mn = fmaxf(m, tmax);
+    const float mu = mn == -INFINITY ? 0.f : mn;  // no key seen yet: every weight is exp2(-inf) = 0
+    const float alpha = fast_exp2(m - mu);
+    float ps = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      sacc[v] = fast_exp2(sacc[v] - mu);
+      ps += sacc[v];
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
+#pragma unroll
+      for (int s = 0; s < 16; ++s)
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[db][s], sacc[s], oacc[db], 0, 0, 0);
+    }
+  }
+
+  // Combine the waves: O = sum_w exp2(m_w - M) O_w / sum_w exp2(m_w - M) l_w, M = max_w m_w.
+  if (g == 0) ml_s[w][r] = make_float2(m, l);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4)
+      *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 32 * db + 8 * v4 + 4 * g]) =
+          make_float4(oacc[db][4 * v4], oacc[db][4 * v4 + 1], oacc[db][4 * v4 + 2], oacc[db][4 * v4 + 3]);
+  __syncthreads();
+  constexpr int CPT = D / 8;  // output columns per thread: 8 threads per query
+  const int tq = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * CPT;
+  float2 mlw[kF32Waves];
+  float M = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kF32Waves; ++u) {
+    mlw[u] = ml_s[u][tq];
+    M = fmaxf(M, mlw[u].x);
+  }
+  const float mu = M == -INFINITY ? 0.f : M;
+  float f[kF32Waves], L = 0.f;
+#pragma unroll
+  for (int u = 0; u < kF32Waves; ++u) {
+    f[u] = fast_exp2(mlw[u].x - mu);
+    L += mlw[u].y * f[u];
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int qo = q0 + tq;
+  if (qo < lq) {
+    float* orow = O + (int64_t)b * st.ob + (int64_t)h * st.oh + (int64_t)qo * st.os + c0;
+#pragma unroll
+    for (int j = 0; j < CPT; j += 4) {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+      for (int u = 0; u < kF32Waves; ++u) {
+        const float4 x = *reinterpret_cast<const float4*>(&o_s[u][tq * OSTR + c0 + j]);
+        a0 += x.x * f[u];
+        a1 += x.y * f[u];
+        a2 += x.z * f[u];
+        a3 += x.w * f[u];
+      }
+      *reinterpret_cast<float4*>(orow + j) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
+    }
+  }
+}
+
+template <int D>
+void launch_f32_d(const float* q, const float* k, const float* v, float* o, int grid, int hq, int hkv, int lq, int lk,
+                  const AttnStrides& st, float c, int nqb, bool causal) {
+  if (causal)
+    flash_f32_kernel<D, true><<<grid, kF32Waves * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+  else
+    flash_f32_kernel<D, false><<<grid, kF32Waves * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+}
+
+}  // namespace
+
+namespace kh {
+
+bool flash_f32_supported(const void* q, const void* k, const void* v, const void* o, int64_t lq, int64_t lk, int d,
+                         const AttnStrides& st) {
+  if (!(d == 32 || d == 64 || d == 96 || d == 128)) return false;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(o) || (reinterpret_cast<uintptr_t>(v) & 3u) != 0) return false;
+  const int64_t vec[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.ob, st.oh, st.os};
+  for (int64_t s : vec)
+    if (s < 0 || s % 4 != 0) return false;  // 16-byte q / k loads and o stores
+  if (st.vb < 0 || st.vh < 0 || st.vs < 0) return false;
+  // Offsets within one head are 32-bit byte offsets.
+  const int64_t lim = int64_t(1) << 31;
+  return (lq * st.qs + d) * 4 < lim && (lk * st.ks + d) * 4 < lim && (lk * st.vs + d) * 4 < lim;
+}
+
+int launch_flash_f32(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
+                     int d, const AttnStrides& st, float scale, bool causal) {
+  const int nqb = (lq + 31) / 32;
+  const int64_t grid = (int64_t)batch * hq * nqb;
+  KH_REQUIRE(grid <= INT32_MAX, "kh_flash_attention: grid too large");
+  const float c = scale * kLog2e;
+  const float *Q = (const float*)q, *K = (const float*)k, *V = (const float*)v;
+  float* Out = (float*)o;
+  switch (d) {
+    case 32: launch_f32_d<32>(Q, K, V, Out, (int)grid, hq, hkv, lq, lk, st, c, nqb, causal); break;
+    case 64: launch_f32_d<64>(Q, K, V, Out, (int)grid, hq, hkv, lq, lk, st, c, nqb, causal); break;
+    case 96: launch_f32_d<96>(Q, K, V, Out, (int)grid, hq, hkv, lq, lk, st, c, nqb, causal); break;
+    default: launch_f32_d<128>(Q, K, V, Out, (int)grid, hq, hkv, lq, lk, st, c, nqb, causal); break;
+  }
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+}  // namespace kh

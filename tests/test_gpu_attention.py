@@ -121,13 +121,46 @@ def test_flash_bf16_strided_kv_cache_view(hip):
     assert np.max(np.abs(out - ref)) < BF16_ATOL
 
 
-def test_generic_kernel_fp32_small_dims(hip):
-    """Generic path: fp32, D=64, GQA 6/3, ragged lengths, causal."""
-    q, qh = seeded(51, (2, 6, 33, 64))
-    k, kh = seeded(52, (2, 3, 33, 64))
-    v, vh = seeded(53, (2, 3, 33, 64))
+def test_generic_kernel_fp32_odd_head_dim(hip):
+    """Generic path: fp32 with head_dim 48 (not a multiple of 32), GQA 6/3, ragged lengths, causal."""
+    q, qh = seeded(51, (2, 6, 33, 48))
+    k, kh = seeded(52, (2, 3, 33, 48))
+    v, vh = seeded(53, (2, 3, 33, 48))
     out = _sdpa_gpu(q, k, v, True)
     assert max_rel(out, oracle.sdpa(qh, kh, vh, causal=True)) < F32_RTOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,causal", [
+    (2, 6, 2, 33, 33, 64, True),       # GQA 3, one partial query block
+    (1, 8, 1, 100, 300, 128, False),   # Lq < Lk, GQA 8
+    (1, 4, 4, 300, 100, 96, True),     # Lq > Lk: rows past Lk see every key (top-left mask)
+    (2, 8, 4, 129, 129, 32, False),
+    (1, 4, 2, 1, 64, 128, True),       # one causal query row sees key 0 only
+    (1, 2, 2, 1000, 1000, 128, True),  # eight key tiles per wave in the last blocks
+    (1, 16, 16, 31, 257, 64, False),   # ragged key tile
+])
+def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
+    """fp32 flash kernel (fp32 MFMA, four waves splitting a query block's key tiles, merged in LDS)."""
+    q, qh = seeded(54, (B, Hq, Lq, D))
+    k, kh = seeded(55, (B, Hkv, Lk, D))
+    v, vh = seeded(56, (B, Hkv, Lk, D))
+    out = _sdpa_gpu(q, k, v, causal)
+    assert max_rel(out, oracle.sdpa(qh, kh, vh, causal=causal)) < F32_RTOL
+
+
+def test_flash_f32_strided_views_and_negative_scale(hip):
+    """fp32 kernel on [B, S, H, D] storage read through permuted views (no copy), with a negative
+    scale (the running maximum is taken over scaled scores, so any sign works)."""
+    B, S, Hq, Hkv, D = 2, 150, 8, 2, 64
+    qs, qh = seeded(57, (B, S, Hq, D))
+    ks, kh = seeded(58, (B, S, Hkv, D))
+    vs, vh = seeded(59, (B, S, Hkv, D))
+    perm = (0, 2, 1, 3)
+    for scale, causal in ((None, True), (-0.3, False)):
+        out = _sdpa_gpu(F.permute(qs, perm), F.permute(ks, perm), F.permute(vs, perm), causal, scale=scale)
+        ref = oracle.sdpa(np.transpose(qh, perm), np.transpose(kh, perm), np.transpose(vh, perm),
+                          scale=scale, causal=causal)
+        assert max_rel(out, ref) < F32_RTOL, (scale, causal)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
