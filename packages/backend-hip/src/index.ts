@@ -476,6 +476,179 @@ function argmax(x: HipTensorHandle, out: HipTensorHandle): void {
   xc.dispose();
 }
 
+// copy_(dst, src): in-place copy into a (possibly strided) destination view, e.g. a KV-cache slice
+// (kv-cache.ts:180-188).  The source is made contiguous in the destination dtype first; a strided
+// destination is written one contiguous run of its innermost dims at a time.
+function copyInto(dst: HipTensorHandle, src: HipTensorHandle): void {
+  if (dst.shape.join() !== src.shape.join()) throw new Error(`copy_: shape mismatch [${dst.shape}] vs [${src.shape}]`);
+  if (dst.numel === 0) return;
+  const s = src.isContiguous() && src.dtype === dst.dtype ? materialize(src) : contiguous(src, dst.dtype);
+  const isz = ITEMSIZE[dst.dtype];
+  let k = dst.shape.length;
+  let inner = 1;
+  while (k > 0 && (dst.strides[k - 1] === inner || dst.shape[k - 1] === 1)) {
+    inner *= dst.shape[k - 1];
+    k -= 1;
+  }
+  const outer = dst.shape.slice(0, k);
+  const idx = outer.map(() => 0);
+  const runs = numelOf(outer);
+  for (let n = 0; n < runs; ++n) {
+    let off = dst.offset;
+    for (let i = 0; i < k; ++i) off += idx[i] * dst.strides[i];
+    addon.memcpyD2D(dst.storage.ptr + BigInt(off * isz), s.ptr + BigInt(n * inner * isz), inner * isz);
+    for (let i = k - 1; i >= 0; --i) {
+      idx[i] += 1;
+      if (idx[i] < outer[i]) break;
+      idx[i] = 0;
+    }
+  }
+  s.dispose();
+}
+
+function zeros(out: HipTensorHandle): void {
+  fill(out, 0);
+}
+
+const GEMV_PROLOGUE: { [name: string]: number } = { none: 0, rms_norm: 1, silu_mul: 2, silu_mul_interleaved: 3 };
+
+// gemv_fused(prologue, x, w, out, params): one-row projection (decode) out[1, n] = alpha * x' W^T
+// + beta * cin (+ bias) with the producer of x' fused in front: 'none' x' = x (bf16); 'rms_norm'
+// x' = rms_norm(x, normWeight, eps) of the fp32 residual row; 'silu_mul' x' = silu(x) * x2;
+// 'silu_mul_interleaved' the same product from one gate/up row interleaved in blocks of 8
+// (RMSNorm.ts:92-99 or swiglu.ts:119-134 fused into Linear.ts:135-137).  params: normWeight, eps,
+// x2, cin, bias, alpha, beta; out may alias cin (residual add).
+function gemvFused(prologue: string, x: HipTensorHandle, w: HipTensorHandle, out: HipTensorHandle,
+                   params?: { [key: string]: any }): void {
+  const p = params || {};
+  const code = GEMV_PROLOGUE[prologue];
+  if (code === undefined) throw new Error(`gemv_fused: unknown prologue ${prologue}`);
+  if (w.dtype !== 'bfloat16' || w.shape.length !== 2 || w.strides[1] !== 1)
+    throw new Error('gemv_fused: the weight must be bf16 [n, k] with contiguous rows');
+  const n = w.shape[0], k = w.shape[1];
+  if (out.numel !== n || !out.isContiguous()) throw new Error('gemv_fused: out must be a contiguous row of n elements');
+  const want = prologue === 'rms_norm' ? 'float32' : 'bfloat16';
+  const kx = prologue === 'silu_mul_interleaved' ? 2 * k : k;
+  const x2 = p.x2 as HipTensorHandle | undefined;
+  for (const h of x2 === undefined ? [x] : [x, x2]) {
+    if (h.dtype !== want || h.numel !== kx || !h.isContiguous())
+      throw new Error(`gemv_fused: inputs must be contiguous ${want} rows of ${kx} elements`);
+  }
+  const nw = p.normWeight as HipTensorHandle | undefined;
+  const cin = p.cin as HipTensorHandle | undefined;
+  const bias = p.bias as HipTensorHandle | undefined;
+  const beta = p.beta !== undefined ? (p.beta as number) : cin !== undefined ? 1 : 0;
+  addon.gemvFused(code, x.ptr, x2 === undefined ? null : x2.ptr, nw === undefined ? null : nw.ptr,
+                  p.eps === undefined ? 1e-6 : (p.eps as number), w.ptr, w.strides[0], out.ptr,
+                  cin === undefined ? null : cin.ptr, bias === undefined ? null : bias.ptr, n, k,
+                  p.alpha === undefined ? 1 : (p.alpha as number), beta, out.kh);
+}
+
+// linear_swiglu(x, wGu, output): output [.., I] = silu(x W_gate^T) * (x W_up^T) in bf16 from the
+// gate/up weight [2I, H] interleaved in blocks of 8 rows (swiglu.ts:119-134 in one GEMM).
+function linearSwiglu(x: HipTensorHandle, wGu: HipTensorHandle, out: HipTensorHandle): void {
+  const H = wGu.shape[1], I = wGu.shape[0] / 2;
+  if (x.dtype !== 'bfloat16' || wGu.dtype !== 'bfloat16' || out.dtype !== 'bfloat16')
+    throw new Error('linear_swiglu: bf16 operands only');
+  if (x.shape[x.shape.length - 1] !== H || out.shape[out.shape.length - 1] !== I)
+    throw new Error(`linear_swiglu: x [.., ${H}] and output [.., ${I}] expected`);
+  if (!x.isContiguous() || !out.isContiguous() || wGu.strides[1] !== 1)
+    throw new Error('linear_swiglu: contiguous operands expected');
+  const m = x.numel / H;
+  addon.gemmSwiglu(x.ptr, H, wGu.ptr, wGu.strides[0], out.ptr, I, m, I, H);
+}
+
+// linear_add_rms_norm(x, w, residual, normWeight, eps, output, rows?): residual += x W^T (fp32, in
+// place), then output = rms_norm(residual rows) * normWeight (decoder_layer.ts:224-238 with
+// RMSNorm.ts:92-99).  When the GEMM splits K, its fp32 partials go straight into the fused
+// add + RMSNorm kernel; the values are those of the separate launches bit for bit.
+function linearAddRmsNorm(x: HipTensorHandle, w: HipTensorHandle, residual: HipTensorHandle,
+                          normWeight: HipTensorHandle, eps: number, out: HipTensorHandle, rows?: number[]): void {
+  const M = x.shape[0], K = x.shape[1], N = w.shape[0];
+  const r0 = rows === undefined ? 0 : rows[0], r1 = rows === undefined ? M : rows[1];
+  if (x.dtype !== 'bfloat16' || w.dtype !== 'bfloat16' || residual.dtype !== 'float32')
+    throw new Error('linear_add_rms_norm: bf16 x and w with an fp32 residual expected');
+  if (w.shape[1] !== K || residual.shape.join() !== [M, N].join() || out.shape.join() !== [r1 - r0, N].join())
+    throw new Error('linear_add_rms_norm: shapes do not match');
+  if (normWeight.numel !== N || normWeight.dtype !== out.dtype)
+    throw new Error('linear_add_rms_norm: normWeight must have N elements and the output dtype');
+  if (!(r0 >= 0 && r0 < r1 && r1 <= M)) throw new Error('linear_add_rms_norm: bad row range');
+  for (const h of [x, w, residual, out, normWeight])
+    if (!h.isContiguous()) throw new Error('linear_add_rms_norm: contiguous operands expected');
+  const splits = addon.gemmSplitCount(M, N, K) as number;
+  const aligned = [x, w, residual, out, normWeight].every((h) => h.ptr % 16n === 0n);
+  const rowOff = BigInt(r0 * N * 4);
+  if (splits > 1 && aligned && N % 8 === 0 && N <= 2048) {
+    const part = HipTensorHandle.createNew([splits, M, N], 'float32');
+    addon.gemmSplitkPartials(x.ptr, K, w.ptr, K, part.ptr, M, N, K, splits);
+    addon.addRmsNorm(part.ptr + rowOff, splits, M * N, residual.ptr + rowOff, normWeight.ptr, out.ptr, r1 - r0, N,
+                     eps, out.kh);
+    part.dispose();  // stream ordered: reused only by later work on the same stream
+    return;
+  }
+  addon.gemm(x.ptr, K, w.ptr, K, residual.ptr, N, residual.ptr, N, null, M, N, K, 1, 1, true, x.kh, residual.kh);
+  addon.rmsNorm(residual.ptr + rowOff, N, normWeight.ptr, out.ptr, N, r1 - r0, N, eps, residual.kh, out.kh);
+}
+
+// decode_attention_block(qkv, params): one decode step's attention block after the QKV projection
+// of the new token (gqa.ts:246-430): qk-norm, RoPE at the device position, the K/V cache row write,
+// attention over cache rows [0, position], o_proj and the residual add into x, in two kernels.
+// params: qNorm, kNorm (bf16 [128]), invFreq (fp32 [64]), eps, position (int32 [1]), kCache,
+// vCache ([1, Hkv, maxLen, 128] bf16), wO (bf16 [hidden, Hq * 128]), x (fp32 [1, hidden]), scale.
+function decodeAttentionBlock(qkv: HipTensorHandle, params: { [key: string]: any }): void {
+  const kc = params.kCache as HipTensorHandle, vc = params.vCache as HipTensorHandle;
+  const wo = params.wO as HipTensorHandle, x = params.x as HipTensorHandle;
+  const hkv = kc.shape[1], maxLen = kc.shape[2], D = kc.shape[3];
+  const hq = (qkv.numel - 2 * hkv * D) / D;
+  if (D !== 128 || !(hq > 0) || hq !== Math.floor(hq))
+    throw new Error(`decode_attention_block: qkv of ${qkv.numel} values does not split into heads of 128`);
+  for (const h of [qkv, params.qNorm as HipTensorHandle, params.kNorm as HipTensorHandle, kc, vc, wo])
+    if (h.dtype !== 'bfloat16') throw new Error('decode_attention_block: bf16 operands expected');
+  if (!qkv.isContiguous() || x.dtype !== 'float32' || !x.isContiguous())
+    throw new Error('decode_attention_block: qkv (bf16) and x (fp32) must be contiguous');
+  if (wo.shape.join() !== [x.numel, hq * D].join() || wo.strides[1] !== 1)
+    throw new Error(`decode_attention_block: wO must be [${x.numel}, ${hq * D}] with contiguous rows`);
+  const pos = params.position as HipTensorHandle;
+  if (pos.dtype !== 'int32') throw new Error('decode_attention_block: position must be int32');
+  addon.decodeAttentionBlock(qkv.ptr, (params.qNorm as HipTensorHandle).ptr, (params.kNorm as HipTensorHandle).ptr,
+                             (params.invFreq as HipTensorHandle).ptr, params.eps === undefined ? 1e-6 : params.eps,
+                             pos.ptr, kc.ptr, vc.ptr, hq, hkv, maxLen,
+                             [kc.strides[1], kc.strides[2], vc.strides[1], vc.strides[2]], params.scale as number,
+                             wo.ptr, wo.strides[0], x.numel, x.ptr);
+}
+
+// greedy_advance(nextToken, position, seqLen, tokenLog, logBase): the device-side step of the greedy
+// loop (for_causal_lm.ts:475-508): tokenLog[p + 1 - logBase] = nextToken, position = p + 1,
+// seqLen = p + 2, with p = position[0].  int32 operands.
+function greedyAdvance(nextToken: HipTensorHandle, position: HipTensorHandle, seqLen: HipTensorHandle,
+                       tokenLog: HipTensorHandle, logBase: number): void {
+  for (const h of [nextToken, position, seqLen, tokenLog])
+    if (h.dtype !== 'int32' || !h.isContiguous()) throw new Error('greedy_advance: contiguous int32 operands expected');
+  addon.greedyAdvance(nextToken.ptr, position.ptr, seqLen.ptr, tokenLog.ptr, logBase, tokenLog.numel);
+}
+
+// sample(logits, params): one token from a float32 logits row on the device (sampling/index.ts:
+// 103-243).  params: doSample (true), temperature (1), topK (0 = off), topP (1 = off), seed, counter
+// (int32 [1]: r = philox4x32-10(seed, counter)), displayK (0), and the outputs token (int32 [1]),
+// logprob (float32 [1]), displayIds (int32 [displayK]) and displayProbs (float32 [displayK]).
+function sample(logits: HipTensorHandle, params: { [key: string]: any }): void {
+  if (logits.dtype !== 'float32' || !logits.isContiguous())
+    throw new Error('sample: logits must be a contiguous float32 tensor');
+  const vocab = logits.shape[logits.shape.length - 1];
+  if (logits.numel !== vocab) throw new Error('sample: one row of logits expected');
+  const opt = (name: string): HipTensorHandle | undefined => params[name] as HipTensorHandle | undefined;
+  const ptrOf = (h: HipTensorHandle | undefined): bigint | null => (h === undefined ? null : h.ptr);
+  const doSample = params.doSample === undefined ? true : !!params.doSample;
+  const token = opt('token');
+  if (token === undefined || token.dtype !== 'int32') throw new Error('sample: token must be an int32 tensor');
+  if (doSample && (opt('counter') === undefined || (opt('counter') as HipTensorHandle).dtype !== 'int32'))
+    throw new Error('sample: counter must be an int32 tensor');
+  addon.sample(logits.ptr, vocab, doSample, params.temperature === undefined ? 1 : params.temperature,
+               params.topK || 0, params.topP === undefined ? 1 : params.topP, BigInt(params.seed || 0),
+               ptrOf(opt('counter')), token.ptr, ptrOf(opt('logprob')), params.displayK || 0,
+               ptrOf(opt('displayIds')), ptrOf(opt('displayProbs')));
+}
+
 // copy / contiguous / cast (CopyKernelImpl: (input, options) => handle).
 function copyKernel(input: HipTensorHandle, options: { [key: string]: any }): HipTensorHandle {
   return contiguous(input, options && options.dtype ? (options.dtype as DType) : undefined);
@@ -542,7 +715,15 @@ export function registerHipKernels(reg: SimpleOperatorRegistry): void {
   reg.register('index_select', indexSelect);
   reg.register('argmax', argmax);
   for (const name of ['copy', 'contiguous', 'cast']) reg.register(name, copyKernel);
+  reg.register('copy_', copyInto);
   reg.register('fill', fill);
+  reg.register('zeros', zeros);
+  reg.register('gemv_fused', gemvFused);
+  reg.register('linear_swiglu', linearSwiglu);
+  reg.register('linear_add_rms_norm', linearAddRmsNorm);
+  reg.register('decode_attention_block', decodeAttentionBlock);
+  reg.register('greedy_advance', greedyAdvance);
+  reg.register('sample', sample);
 }
 
 export { contiguousStrides, toBf16Bits, fromBf16Bits };

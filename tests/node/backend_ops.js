@@ -138,13 +138,88 @@ async function main() {
   ops.find('decode_attention')(dq, dk, dv, lens, dout, 1 / Math.sqrt(d.D));
   write('do', await dout.dataAsync());
 
+  // fused decode / prefill ops, compared bit for bit with the Python binding on the same inputs
+  const f2 = meta.fused;
+  const gx = t([f2.gvK], 'float32', readF32('gvx'));
+  const gw = t([f2.gvN, f2.gvK], 'bfloat16', readU16('gvw'));
+  const gn = t([f2.gvK], 'bfloat16', readU16('gvn'));
+  const go = backend.createTensorHandle([1, f2.gvN], 'bfloat16');
+  ops.find('gemv_fused')('rms_norm', gx, gw, go, { normWeight: gn, eps: 1e-6 });
+  write('gvo', await go.dataAsync());
+  const gb = t([f2.gvK], 'bfloat16', readU16('gvb'));
+  const gc = t([1, f2.gvN], 'float32', readF32('gvc'));
+  ops.find('gemv_fused')('none', gb, gw, gc, { cin: gc });
+  write('gvr', await gc.dataAsync());
+
+  const sx = t([f2.swM, f2.swH], 'bfloat16', readU16('swx'));
+  const sg = t([2 * f2.swI, f2.swH], 'bfloat16', readU16('swg'));
+  const so = backend.createTensorHandle([f2.swM, f2.swI], 'bfloat16');
+  ops.find('linear_swiglu')(sx, sg, so);
+  write('swo', await so.dataAsync());
+
+  const lx = t([f2.lM, f2.lK], 'bfloat16', readU16('lax'));
+  const lw = t([f2.lN, f2.lK], 'bfloat16', readU16('law'));
+  const lr = t([f2.lM, f2.lN], 'float32', readF32('lar'));
+  const ln = t([f2.lN], 'bfloat16', readU16('lan'));
+  const lo = backend.createTensorHandle([f2.lM - 1, f2.lN], 'bfloat16');
+  ops.find('linear_add_rms_norm')(lx, lw, lr, ln, 1e-6, lo, [1, f2.lM]);
+  write('lao', await lo.dataAsync());
+  write('lar2', await lr.dataAsync());
+
+  const d2 = meta.block;
+  const bqkv = t([1, (d2.Hq + 2 * d2.Hkv) * 128], 'bfloat16', readU16('bqkv'));
+  const bqn = t([128], 'bfloat16', readU16('bqn'));
+  const bkn = t([128], 'bfloat16', readU16('bkn'));
+  const binv = t([64], 'float32', readF32('binv'));
+  const bpos = t([1], 'int32', new Int32Array([d2.pos]));
+  const bkc = t([1, d2.Hkv, d2.L, 128], 'bfloat16', readU16('bkc'));
+  const bvc = t([1, d2.Hkv, d2.L, 128], 'bfloat16', readU16('bvc'));
+  const bwo = t([d2.hidden, d2.Hq * 128], 'bfloat16', readU16('bwo'));
+  const bx = t([1, d2.hidden], 'float32', readF32('bx'));
+  ops.find('decode_attention_block')(bqkv, { qNorm: bqn, kNorm: bkn, invFreq: binv, eps: 1e-6, position: bpos,
+                                             kCache: bkc, vCache: bvc, wO: bwo, x: bx, scale: 1 / Math.sqrt(128) });
+  write('bxo', await bx.dataAsync());
+  write('bkco', await bkc.dataAsync());
+  write('bvco', await bvc.dataAsync());
+
+  const lg = t([meta.sample.V], 'float32', readF32('slg'));
+  const stok = backend.createTensorHandle([1], 'int32');
+  ops.find('sample')(lg, { doSample: false, token: stok });
+  const greedyTok = (await stok.dataAsync())[0];
+  const sctr = t([1], 'int32', new Int32Array([meta.sample.counter]));
+  const slp = backend.createTensorHandle([1], 'float32');
+  ops.find('sample')(lg, { doSample: true, temperature: 0.8, topK: 50, topP: 0.9, seed: meta.sample.seed,
+                          counter: sctr, token: stok, logprob: slp });
+  const sampledTok = (await stok.dataAsync())[0];
+  const sampledLp = (await slp.dataAsync())[0];
+
+  const nt = t([1], 'int32', new Int32Array([42]));
+  const ps = t([1], 'int32', new Int32Array([5]));
+  const sl = t([1], 'int32', new Int32Array([0]));
+  const lgg = t([10], 'int32', new Int32Array(10));
+  ops.find('greedy_advance')(nt, ps, sl, lgg, 3);
+  const adv = { pos: (await ps.dataAsync())[0], len: (await sl.dataAsync())[0], log: Array.from(await lgg.dataAsync()) };
+
+  const cbuf = t([4, 8], 'float32', new Float32Array(32));
+  const cview = backend.createTensorHandle({ storage: cbuf.storage, shape: [4, 3], dtype: 'float32', strides: [8, 1],
+                                              offset: 2 });
+  const csrc = t([4, 3], 'float32', readF32('cps'));
+  ops.find('copy_')(cview, csrc);
+  write('cpo', await cbuf.dataAsync());
+  const zt = t([10], 'float32', new Float32Array(10).fill(1));
+  ops.find('zeros')(zt);
+  const zsum = Array.from(await zt.dataAsync()).reduce((p2, q2) => p2 + Math.abs(q2), 0);
+
   for (const hnd of [q, k, v, o, mask, om, x, w, y, a, b, c, out, g, u, h, gT, s1, prod, table, ids, rows, am,
-                     un.neg, un.cos, un.sin, ar, rq, rk, rv, wq, wk, inv, pos, kc, vc, qk[0], qk[1], dq, dk, dv, lens, dout]) {
+                     un.neg, un.cos, un.sin, ar, rq, rk, rv, wq, wk, inv, pos, kc, vc, qk[0], qk[1], dq, dk, dv, lens, dout,
+                     gx, gw, gn, go, gb, gc, sx, sg, so, lx, lw, lr, ln, lo, bqkv, bqn, bkn, binv, bpos, bkc, bvc, bwo, bx,
+                     lg, stok, sctr, slp, nt, ps, sl, lgg, cbuf, cview, csrc, zt]) {
     hnd.dispose();
   }
   backend.synchronize();
   const after = backend.memoryStats();
-  console.log(JSON.stringify({ ok: true, names: ops.names(), liveBefore: before.liveBytes, liveAfter: after.liveBytes }));
+  console.log(JSON.stringify({ ok: true, names: ops.names(), liveBefore: before.liveBytes, liveAfter: after.liveBytes,
+                                greedyTok, sampledTok, sampledLp, adv, zsum }));
 }
 
 main().catch((err) => {

@@ -3,10 +3,13 @@ index.ts, stripped to dist/index.js by strip-types.js): tests/node/backend_ops.j
 looks each kernel up in its operator registry by the name Kandle's dispatcher uses and calls it with
 the reference kernel signature — flash_attention, sdpa_masked, rms_norm, matmul (linear plus a
 residual), silu_mul, the iterator kernels silu / mul on a transposed view, index_select, argmax,
-neg / cos / sin, arange, rms_norm_rope writing KV caches at device positions, and decode_attention
-over ragged cache lengths — then disposes every handle.  This test writes the inputs and checks each output against the CPU
+neg / cos / sin, arange, rms_norm_rope writing KV caches at device positions, decode_attention
+over ragged cache lengths, the fused gemv_fused / linear_swiglu / linear_add_rms_norm /
+decode_attention_block, sample, greedy_advance, copy_ into a strided view and zeros — then
+disposes every handle.  This test writes the inputs and checks each output against the CPU
 oracle, and that the backend's live device bytes return to where they started."""
 import json
+import math
 import os
 import shutil
 import subprocess
@@ -83,8 +86,33 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     put_bf16("dq", 27, (dd["B"], dd["Hq"], dd["D"]))
     put_bf16("dk", 28, (dd["B"], dd["Hkv"], dd["L"], dd["D"]))
     put_bf16("dv", 29, (dd["B"], dd["Hkv"], dd["L"], dd["D"]))
+    # fused ops (run again through the Python binding below, on the same inputs)
+    fu = dict(gvN=512, gvK=1024, swM=37, swH=256, swI=96, lM=64, lN=1024, lK=2048)
+    put_f32("gvx", syn.normal(30, (fu["gvK"],), 2.0))
+    put_bf16("gvw", 31, (fu["gvN"], fu["gvK"]), 0.05)
+    put_bf16("gvn", 32, (fu["gvK"],))
+    put_bf16("gvb", 33, (fu["gvK"],))
+    put_f32("gvc", syn.normal(34, (1, fu["gvN"])))
+    put_bf16("swx", 35, (fu["swM"], fu["swH"]))
+    put_bf16("swg", 36, (2 * fu["swI"], fu["swH"]), 0.1)
+    put_bf16("lax", 37, (fu["lM"], fu["lK"]))
+    put_bf16("law", 38, (fu["lN"], fu["lK"]), 0.05)
+    put_f32("lar", syn.normal(39, (fu["lM"], fu["lN"])))
+    put_bf16("lan", 40, (fu["lN"],))
+    blk = dict(Hq=16, Hkv=8, L=64, hidden=1024, pos=20)
+    put_bf16("bqkv", 41, (1, (blk["Hq"] + 2 * blk["Hkv"]) * 128))
+    put_bf16("bqn", 42, (128,))
+    put_bf16("bkn", 43, (128,))
+    put_f32("binv", oracle.rope_inv_freq(128, 1e6))
+    put_bf16("bkc", 44, (1, blk["Hkv"], blk["L"], 128))
+    put_bf16("bvc", 45, (1, blk["Hkv"], blk["L"], 128))
+    put_bf16("bwo", 46, (blk["hidden"], blk["Hq"] * 128), 0.02)
+    put_f32("bx", syn.normal(47, (1, blk["hidden"])))
+    smp = dict(V=1000, seed=1234, counter=7)
+    put_f32("slg", syn.normal(48, (smp["V"],), 3.0))
+    put_f32("cps", syn.normal(49, (4, 3)))
     (tmp_path / "meta.json").write_text(json.dumps({"flash": f, "norm": r, "mm": m, "emb": e, "rope": p,
-                                                    "decode": dd}))
+                                                    "decode": dd, "fused": fu, "block": blk, "sample": smp}))
 
     out = subprocess.run(["node", SCRIPT, str(tmp_path)], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr[-2000:]
@@ -142,3 +170,52 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     ref = oracle.sdpa(A["dq"][:, :, None, :], A["dk"], A["dv"], kv_len=np.array(dd["lens"], np.int32))[:, :, 0, :]
     err = float(np.max(np.abs(do - ref)))
     assert err < 2e-2, ("decode_attention", err)
+
+    # The fused ops: bit for bit what the Python binding computes from the same inputs.
+    from kandle_amd import HipTensorHandle, Tensor, kernels
+
+    T = lambda name, dt="bfloat16": Tensor(A[name], dtype=dt)  # noqa: E731
+    gx, gw, gn, gb, gc = T("gvx", "float32"), T("gvw"), T("gvn"), T("gvb"), T("gvc", "float32")
+    go = HipTensorHandle.create_new((1, fu["gvN"]), "bfloat16")
+    kernels.gemv_fused("rms_norm", gx.handle, gw.handle, go, {"norm_weight": gn.handle, "eps": 1e-6})
+    np.testing.assert_array_equal(f32_file("gvo", (1, fu["gvN"])), go.data_async())
+    kernels.gemv_fused("none", gb.handle, gw.handle, gc.handle, {"cin": gc.handle})
+    np.testing.assert_array_equal(f32_file("gvr", (1, fu["gvN"])), gc.numpy())
+    sx, sg = T("swx"), T("swg")
+    so = HipTensorHandle.create_new((fu["swM"], fu["swI"]), "bfloat16")
+    kernels.linear_swiglu(sx.handle, sg.handle, so)
+    np.testing.assert_array_equal(f32_file("swo", (fu["swM"], fu["swI"])), so.data_async())
+    assert kernels.gemm_split_count(fu["lM"], fu["lN"], fu["lK"]) > 1   # the partials + add-norm route
+    lx, lw, lr, ln = T("lax"), T("law"), T("lar", "float32"), T("lan")
+    lo = HipTensorHandle.create_new((fu["lM"] - 1, fu["lN"]), "bfloat16")
+    kernels.linear_add_rms_norm(lx.handle, lw.handle, lr.handle, ln.handle, 1e-6, lo, rows=(1, fu["lM"]))
+    np.testing.assert_array_equal(f32_file("lao", (fu["lM"] - 1, fu["lN"])), lo.data_async())
+    np.testing.assert_array_equal(f32_file("lar2", (fu["lM"], fu["lN"])), lr.numpy())
+
+    bk, bv, bx = T("bkc"), T("bvc"), T("bx", "float32")
+    bpos = Tensor(np.array([blk["pos"]], np.int32), dtype="int32")
+    kernels.decode_attention_block(T("bqkv").handle, {
+        "q_norm": T("bqn").handle, "k_norm": T("bkn").handle, "inv_freq": T("binv", "float32").handle, "eps": 1e-6,
+        "position": bpos.handle, "k_cache": bk.handle, "v_cache": bv.handle, "w_o": T("bwo").handle,
+        "x": bx.handle, "scale": 1.0 / math.sqrt(128)})
+    np.testing.assert_array_equal(f32_file("bxo", (1, blk["hidden"])), bx.numpy())
+    np.testing.assert_array_equal(f32_file("bkco", bk.shape), bk.numpy())
+    np.testing.assert_array_equal(f32_file("bvco", bv.shape), bv.numpy())
+    assert not np.array_equal(bx.numpy(), A["bx"])                 # the block did add into x
+
+    lg = T("slg", "float32")
+    tok = Tensor(np.zeros(1, np.int32), dtype="int32")
+    kernels.sample(lg.handle, {"do_sample": False, "token": tok.handle})
+    assert res["greedyTok"] == int(tok.numpy()[0]) == int(np.argmax(A["slg"]))
+    ctr = Tensor(np.array([smp["counter"]], np.int32), dtype="int32")
+    lp = Tensor(np.zeros(1, np.float32))
+    kernels.sample(lg.handle, {"do_sample": True, "temperature": 0.8, "top_k": 50, "top_p": 0.9, "seed": smp["seed"],
+                               "counter": ctr.handle, "token": tok.handle, "logprob": lp.handle})
+    assert res["sampledTok"] == int(tok.numpy()[0])
+    assert np.float32(res["sampledLp"]) == lp.numpy()[0]
+
+    assert res["adv"] == {"pos": 6, "len": 7, "log": [0, 0, 0, 42, 0, 0, 0, 0, 0, 0]}
+    buf = np.zeros((4, 8), np.float32)
+    buf[:, 2:5] = A["cps"]
+    np.testing.assert_array_equal(f32_file("cpo", (4, 8)), buf)
+    assert res["zsum"] == 0
