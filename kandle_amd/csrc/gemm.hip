@@ -39,9 +39,11 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 }
 
 // =============================================================================================
-// MFMA tile kernel.  Workgroup tile (64 WT) x (64 WT), k-step KS, 4 waves in a 2 x 2 layout, each
-// wave (32 WT) x (32 WT) = WT x WT tiles of 32 x 32: WT = 2 (128 x 128) for large problems, WT = 1
-// (64 x 64, k-step 128) when 128-tiles would leave CUs idle.  The product is formed as C^T = B A^T
+// MFMA tile kernel.  Workgroup tile (64 WTM) x (64 WTN), k-step KS, 4 waves in a 2 x 2 layout, each
+// wave (32 WTM) x (32 WTN) = WTM x WTN tiles of 32 x 32: 128 x 128 for large problems, smaller
+// tiles when 128-tiles would leave CUs idle.  The tile shape does not change any result: every
+// output element is summed over k in the same 16-wide MFMA steps, in the same order, whatever the
+// tile that holds it.  The product is formed as C^T = B A^T
 // so that each lane owns one m row and 4 consecutive n per register group: A-operand = B rows (n),
 // B-operand = A rows (m), both k-contiguous 16-byte LDS reads.  LDS double buffered; global loads are
 // raw buffer loads (rows past M / N and columns past the k range read as zero without a branch).
@@ -55,7 +57,14 @@ constexpr int G_THREADS = 256;
 constexpr int kGemmPrefetch = 3;        // k-steps of global loads in flight per workgroup
 constexpr int kGemmT128Min = 256;       // 128-tiles from this many tiles up
 constexpr int kGemmSplitTarget = 512;   // split K until about this many 64-tile workgroups
-constexpr int kGemmSplitWT = 1;         // tile of split launches: 64 (1) or 128 (2)
+// Tiles (64 WTM) x (64 WTN) of split launches and of products too small for 128 x 128 tiles.
+// C5 prefill, M = 512 (bench.py --only gemm, three runs): split launches with 128 x 64 tiles (one
+// workgroup per CU) against 64 x 64 (two per CU): o_proj 15.25 -> 14.56 us, down 16.83 -> 15.25 us;
+// the unsplit qkv and gate/up products are 0.5-1.5 us slower with 128 x 64 or 64 x 128 tiles, and
+// a k-step of 128 on the rectangular tiles needs 256 VGPRs + 90 AGPRs and is slower everywhere.
+constexpr int kGemmSplitWTM = 2, kGemmSplitWTN = 1;
+constexpr int kGemmSmallWTM = 1, kGemmSmallWTN = 1;
+constexpr int kGemmRectKS = 64;         // k-step of 128 x 64 and 64 x 128 tiles
 constexpr int kMaxSplits = 8;
 constexpr int g_tile(int wt) { return 64 * wt; }
 
@@ -69,16 +78,18 @@ constexpr int g_tile(int wt) { return 64 * wt; }
 // every lane holds each gate accumulator and its up partner, and the epilogue stores
 // C[m, f] = bf16(silu(bf16(gate)) * bf16(up)) over N / 2 features f -- the values the separate
 // GEMM (bf16 store) and silu*mul kernel produce, without the [M, N] intermediate.
-template <typename TO, int WT, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false>
+template <typename TO, int WTM, int WTN, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
     int tiles_n, int splits, int kchunk, float* __restrict__ part) {
-  constexpr int GM = g_tile(WT), GN = g_tile(WT);
+  constexpr int GM = g_tile(WTM), GN = g_tile(WTN);
   constexpr int STR = KS + 8;  // LDS row stride (elements): 16-byte aligned, breaks bank aliasing
   constexpr int ATILE = GM * STR, BTILE = GN * STR;
   constexpr int CPR = KS / 8;                      // 16-byte chunks per row per k-step
-  constexpr int CPT = GM * CPR / G_THREADS;        // chunks per thread per tile
+  constexpr int CPTA = GM * CPR / G_THREADS;       // chunks per thread per A tile
+  constexpr int CPTB = GN * CPR / G_THREADS;       // chunks per thread per B tile
+  constexpr int CPTM = CPTA > CPTB ? CPTA : CPTB;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ATILE + BTILE)];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, g = lane >> 5;
@@ -89,7 +100,7 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   const int tiles_m = (M + GM - 1) / GM;
   const int tm = PF > 1 ? tile % tiles_m : tile / tiles_n, tn = PF > 1 ? tile / tiles_m : tile % tiles_n;
   const int m0 = tm * GM, n0 = tn * GN;
-  const int wm = (wave >> 1) * 32 * WT, wn = (wave & 1) * 32 * WT;
+  const int wm = (wave >> 1) * 32 * WTM, wn = (wave & 1) * 32 * WTN;
   const int kbeg = split * kchunk, kend = min(K, kbeg + kchunk);
 
   // Byte ranges of this tile's rows; a row past the matrix or a column past the range reads zero.
@@ -97,41 +108,45 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * 2));
   const auto rb = make_rsrc(B + (int64_t)n0 * ldb, (uint32_t)(((int64_t)(nrows - 1) * ldb + K) * 2));
 
-  // Staging: each of the A and B tiles is GM rows x KS k = GM * CPR chunks of 16 B, CPT per thread,
-  // in PF register stages.
-  uint4 ast[PF][CPT], bst[PF][CPT];
+  // Staging: the A (B) tile is GM (GN) rows x KS k = GM * CPR chunks of 16 B, CPTA (CPTB) per
+  // thread, in PF register stages.
+  uint4 ast[PF][CPTA], bst[PF][CPTB];
   // Byte offsets fit 32 bits (the launcher checks 128 rows of lda / ldb); columns past kend map to
   // 0xffffffff, past the range, and read zero (K % 8 == 0, so a chunk is all in or all out).  The
   // loads are branch-free, so the compiler's load counting stays exact across the prefetch ring.
   auto load_tile = [&](int stg, int kt) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
+    for (int i = 0; i < CPTM; ++i) {
       const int id = tid + G_THREADS * i;
       const int row = id / CPR, kc = kt + 8 * (id % CPR);
       const bool in = kc < kend;
-      const uint32_t ao = in ? ((uint32_t)row * (uint32_t)lda + (uint32_t)kc) * 2u : 0xffffffffu;
-      const uint32_t bo = in ? ((uint32_t)row * (uint32_t)ldb + (uint32_t)kc) * 2u : 0xffffffffu;
-      ast[stg][i] = buf_load16(ra, ao);
-      bst[stg][i] = buf_load16(rb, bo);
+      if (i < CPTA) {
+        const uint32_t ao = in ? ((uint32_t)row * (uint32_t)lda + (uint32_t)kc) * 2u : 0xffffffffu;
+        ast[stg][i < CPTA ? i : 0] = buf_load16(ra, ao);
+      }
+      if (i < CPTB) {
+        const uint32_t bo = in ? ((uint32_t)row * (uint32_t)ldb + (uint32_t)kc) * 2u : 0xffffffffu;
+        bst[stg][i < CPTB ? i : 0] = buf_load16(rb, bo);
+      }
     }
   };
   auto store_tile = [&](int stg, int buf) {
     uint16_t* as = smem + buf * (ATILE + BTILE);
     uint16_t* bs = as + ATILE;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
+    for (int i = 0; i < CPTM; ++i) {
       const int id = tid + G_THREADS * i;
       const int row = id / CPR, kc = 8 * (id % CPR);
-      *reinterpret_cast<uint4*>(as + row * STR + kc) = ast[stg][i];
-      *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[stg][i];
+      if (i < CPTA) *reinterpret_cast<uint4*>(as + row * STR + kc) = ast[stg][i < CPTA ? i : 0];
+      if (i < CPTB) *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[stg][i < CPTB ? i : 0];
     }
   };
 
-  f32x16 acc[WT][WT];  // [n tile][m tile]
+  f32x16 acc[WTN][WTM];  // [n tile][m tile]
 #pragma unroll
-  for (int a = 0; a < WT; ++a)
+  for (int a = 0; a < WTN; ++a)
 #pragma unroll
-    for (int b = 0; b < WT; ++b)
+    for (int b = 0; b < WTM; ++b)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
 
@@ -146,16 +161,17 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* bs = as + ATILE;
 #pragma unroll
     for (int kc = 0; kc < KS / 16; ++kc) {
-      bf16x8 av[WT], bv[WT];
+      bf16x8 av[WTM], bv[WTN];
 #pragma unroll
-      for (int i = 0; i < WT; ++i) {
+      for (int i = 0; i < WTM; ++i)
         av[i] = as_bf16x8(*reinterpret_cast<const uint4*>(as + (wm + 32 * i + r) * STR + 16 * kc + 8 * g));
+#pragma unroll
+      for (int i = 0; i < WTN; ++i)
         bv[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn + 32 * i + r) * STR + 16 * kc + 8 * g));
-      }
 #pragma unroll
-      for (int a = 0; a < WT; ++a)
+      for (int a = 0; a < WTN; ++a)
 #pragma unroll
-        for (int b = 0; b < WT; ++b)
+        for (int b = 0; b < WTM; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv[a], av[b], acc[a][b], 0, 0, 0);
     }
     store_tile((u + 1) % PF, (t + 1) & 1);
@@ -181,11 +197,11 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     // register group are all in range or all out).
     float* mine = part + (int64_t)split * M * N;
 #pragma unroll
-    for (int b = 0; b < WT; ++b) {
+    for (int b = 0; b < WTM; ++b) {
       const int m = m0 + wm + 32 * b + r;
       if (m >= M) continue;
 #pragma unroll
-      for (int a = 0; a < WT; ++a)
+      for (int a = 0; a < WTN; ++a)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
@@ -204,11 +220,11 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     // feature f = (n0 + wn + 32a) / 2 + 4q + 4g + e (q = 0, 2).  N / 2 is a multiple of 8.
     const int NH = N / 2;
 #pragma unroll
-    for (int b = 0; b < WT; ++b) {
+    for (int b = 0; b < WTM; ++b) {
       const int m = m0 + wm + 32 * b + r;
       if (m >= M) continue;
 #pragma unroll
-      for (int a = 0; a < WT; ++a)
+      for (int a = 0; a < WTN; ++a)
 #pragma unroll
         for (int q = 0; q < 4; q += 2) {
           const int f = (n0 + wn + 32 * a) / 2 + 4 * q + 4 * g;
@@ -223,11 +239,11 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     return;
   }
 #pragma unroll
-  for (int b = 0; b < WT; ++b) {
+  for (int b = 0; b < WTM; ++b) {
     const int m = m0 + wm + 32 * b + r;
     if (m >= M) continue;
 #pragma unroll
-    for (int a = 0; a < WT; ++a)
+    for (int a = 0; a < WTN; ++a)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
@@ -471,9 +487,20 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
 // Launch plan of the MFMA tile kernel for a bf16 [M, K] x [N, K]^T product.
 struct GemmPlan {
   bool mfma = false;  // the MFMA tile kernel applies (else the skinny or generic kernel)
-  int wt = 1, tiles_m = 0, tiles_n = 0, splits = 1, kchunk = 0;
+  int wtm = 1, wtn = 1, tiles_m = 0, tiles_n = 0, splits = 1, kchunk = 0;
   int64_t tiles = 0;
 };
+
+// Tile (64 wtm) x (64 wtn) of a product that does not split K.
+inline void plain_tile(int M, int N, int& wtm, int& wtn) {
+  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  if (t128 >= kGemmT128Min) {
+    wtm = wtn = 2;
+  } else {
+    wtm = kGemmSmallWTM;
+    wtn = kGemmSmallWTN;
+  }
+}
 
 // aligned: both operands start on 16 bytes.
 GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, bool bf16, int trans_b) {
@@ -497,13 +524,58 @@ GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, 
       p.splits = (K + p.kchunk - 1) / p.kchunk;
     }
   }
-  // 128-tiles when they fill the chip (256 CUs), else 64-tiles (k-step 128) for 4x the workgroups.
-  p.wt = p.splits > 1 ? kGemmSplitWT : (t128 >= kGemmT128Min ? 2 : 1);
-  const int gt = g_tile(p.wt);
-  p.tiles_m = (M + gt - 1) / gt;
-  p.tiles_n = (N + gt - 1) / gt;
+  // 128-tiles when they fill the chip (256 CUs), else smaller tiles for more workgroups.
+  if (p.splits > 1) {
+    p.wtm = kGemmSplitWTM;
+    p.wtn = kGemmSplitWTN;
+  } else {
+    plain_tile(M, N, p.wtm, p.wtn);
+  }
+  (void)t128;
+  p.tiles_m = (M + g_tile(p.wtm) - 1) / g_tile(p.wtm);
+  p.tiles_n = (N + g_tile(p.wtn) - 1) / g_tile(p.wtn);
   p.tiles = (int64_t)p.tiles_m * p.tiles_n;
   return p;
+}
+
+// One launch of the tile kernel with tile (64 WTM) x (64 WTN) and k-step KS.
+template <typename TO, int WTM, int WTN, int KS, bool SWIGLU = false>
+void go_tiles(int nblk, int splits, const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
+              int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI, int M, int N, int K, float alpha, float beta,
+              int tiles_n, int kchunk, float* part) {
+  constexpr int PF = kGemmPrefetch;
+  if (!SWIGLU && splits > 1)
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
+  else
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU><<<nblk, G_THREADS, 0, stream()>>>(
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
+}
+
+// Dispatch on the plan's tile: 128 x 128 with k-step 64; 64 x 64 with k-step 128 when split or
+// with at most two tiles per CU (the 70 KB of LDS of k-step 128 lets two workgroups share a CU;
+// with more tiles the 64 k-step's occupancy, four per CU, wins); 128 x 64 and 64 x 128 with
+// kGemmRectKS.
+template <typename TO, bool SWIGLU = false>
+void launch_tile_shape(int wtm, int wtn, int64_t tiles, int splits, const uint16_t* A, int64_t lda,
+                       const uint16_t* B, int64_t ldb, TO* C, int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI,
+                       int M, int N, int K, float alpha, float beta, int tiles_n, int kchunk, float* part) {
+  const int nblk = (int)(tiles * splits);
+  if (wtm == 2 && wtn == 2)
+    go_tiles<TO, 2, 2, 64, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n,
+                                   kchunk, part);
+  else if (wtm == 2)
+    go_tiles<TO, 2, 1, kGemmRectKS, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                            beta, tiles_n, kchunk, part);
+  else if (wtn == 2)
+    go_tiles<TO, 1, 2, kGemmRectKS, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                            beta, tiles_n, kchunk, part);
+  else if (splits > 1 || tiles * splits <= 512)
+    go_tiles<TO, 1, 1, 128, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
+                                    tiles_n, kchunk, part);
+  else
+    go_tiles<TO, 1, 1, 64, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
+                                   tiles_n, kchunk, part);
 }
 
 // The MFMA tile kernel for plan p: C (or, with part != nullptr and p.splits > 1, only the fp32
@@ -512,27 +584,9 @@ template <typename TO>
 void launch_gemm_tiles(const GemmPlan& p, const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
                        int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI, int M, int N, int K, float alpha,
                        float beta, float* part) {
-  constexpr int PF = kGemmPrefetch;
   const int splits = part ? p.splits : 1;
-  const int nblk = (int)(p.tiles * splits);
-  // k-step 128 doubles the bytes per round trip but also the LDS per workgroup (70 KB: two per
-  // CU); with more than two tiles per CU the 64 k-step's occupancy (four per CU) wins.
-  const bool ks128 = p.tiles * splits <= 512;
-  if (p.wt == 2 && splits > 1)
-    gemm_bf16_nt_kernel<TO, 2, 64, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, splits, p.kchunk, part);
-  else if (p.wt == 2)
-    gemm_bf16_nt_kernel<TO, 2, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, 1, K, nullptr);
-  else if (splits > 1)
-    gemm_bf16_nt_kernel<TO, 1, 128, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, splits, p.kchunk, part);
-  else if (ks128)
-    gemm_bf16_nt_kernel<TO, 1, 128, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, 1, K, nullptr);
-  else
-    gemm_bf16_nt_kernel<TO, 1, 64, false, PF><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, p.tiles_n, 1, K, nullptr);
+  launch_tile_shape<TO>(p.wtm, p.wtn, p.tiles, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
+                        p.tiles_n, p.kchunk, part);
 }
 
 template <typename T, typename TO>
@@ -590,22 +644,13 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
 // launch_gemm, never split over K (the epilogue needs whole sums).
 int launch_gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, uint16_t* H, int64_t ldh,
                        int M, int N, int K) {
-  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-  const int wt = t128 >= kGemmT128Min ? 2 : 1;
-  const int gt = g_tile(wt);
-  const int64_t tiles = (int64_t)((M + gt - 1) / gt) * ((N + gt - 1) / gt);
+  int wtm = 1, wtn = 1;
+  plain_tile(M, N, wtm, wtn);
+  const int tiles_m = (M + g_tile(wtm) - 1) / g_tile(wtm), tiles_n = (N + g_tile(wtn) - 1) / g_tile(wtn);
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
   KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_swiglu: grid too large");
-  const int tiles_n = (N + gt - 1) / gt, nblk = (int)tiles;
-  constexpr int PF = kGemmPrefetch;
-  if (wt == 2)
-    gemm_bf16_nt_kernel<uint16_t, 2, 64, false, PF, true><<<nblk, G_THREADS, 0, stream()>>>(
-        X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr);
-  else if (tiles <= 512)
-    gemm_bf16_nt_kernel<uint16_t, 1, 128, false, PF, true><<<nblk, G_THREADS, 0, stream()>>>(
-        X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr);
-  else
-    gemm_bf16_nt_kernel<uint16_t, 1, 64, false, PF, true><<<nblk, G_THREADS, 0, stream()>>>(
-        X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr);
+  launch_tile_shape<uint16_t, true>(wtm, wtn, tiles, 1, X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f,
+                                    0.f, tiles_n, K, nullptr);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
