@@ -55,6 +55,9 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 // =============================================================================================
 constexpr int G_THREADS = 256;
 constexpr int kGemmPrefetch = 3;        // k-steps of global loads in flight per workgroup
+// Split launches (short k ranges, 128 x 64 tiles): 2 steps in flight (C5 prefill, two runs: o_proj
+// 14.56 -> 14.12 us, down 15.25 -> 14.93 us; the unsplit qkv product is 0.5 us slower at 2).
+constexpr int kGemmSplitPrefetch = 2;
 constexpr int kGemmT128Min = 256;       // 128-tiles from this many tiles up
 constexpr int kGemmSplitTarget = 512;   // split K until about this many 64-tile workgroups
 // Tiles (64 WTM) x (64 WTN) of split launches and of products too small for 128 x 128 tiles.
@@ -545,7 +548,7 @@ void go_tiles(int nblk, int splits, const uint16_t* A, int64_t lda, const uint16
               int tiles_n, int kchunk, float* part) {
   constexpr int PF = kGemmPrefetch;
   if (!SWIGLU && splits > 1)
-    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, PF><<<nblk, G_THREADS, 0, stream()>>>(
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch><<<nblk, G_THREADS, 0, stream()>>>(
         A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
   else
     gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU><<<nblk, G_THREADS, 0, stream()>>>(
@@ -553,8 +556,8 @@ void go_tiles(int nblk, int splits, const uint16_t* A, int64_t lda, const uint16
 }
 
 // Dispatch on the plan's tile: 128 x 128 with k-step 64; 64 x 64 with k-step 128 when split or
-// with at most two tiles per CU (the 70 KB of LDS of k-step 128 lets two workgroups share a CU;
-// with more tiles the 64 k-step's occupancy, four per CU, wins); 128 x 64 and 64 x 128 with
+// with at most one tile per CU, else k-step 64 (C5 prefill qkv, 512 tiles: 11.75 -> 10.9 us with
+// k-step 64; gate/up, 768 tiles: 14.0 -> 16.1 us with k-step 128); 128 x 64 and 64 x 128 with
 // kGemmRectKS.
 template <typename TO, bool SWIGLU = false>
 void launch_tile_shape(int wtm, int wtn, int64_t tiles, int splits, const uint16_t* A, int64_t lda,
@@ -570,7 +573,7 @@ void launch_tile_shape(int wtm, int wtn, int64_t tiles, int splits, const uint16
   else if (wtn == 2)
     go_tiles<TO, 1, 2, kGemmRectKS, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
                                             beta, tiles_n, kchunk, part);
-  else if (splits > 1 || tiles * splits <= 512)
+  else if (splits > 1 || tiles <= 256)
     go_tiles<TO, 1, 1, 128, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
                                     tiles_n, kchunk, part);
   else
