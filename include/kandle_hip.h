@@ -368,6 +368,19 @@ int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_
                   const void* w, int64_t ldw, void* c, const void* cin, const void* bias,
                   int64_t n, int64_t k, float alpha, float beta, int out_dtype);
 
+/* One-row SwiGLU projection (decode): h[f] = silu(g_f) * u_f, f < n_half, bf16 out, where g and u
+ * are the gate and up projections of the activation row x' (prologue 0: x' = x, bf16 [k];
+ * prologue 1: x' = rms_norm(x, norm_w, eps) of the fp32 residual row, as kh_gemv_fused) by the
+ * interleaved gate/up weight w_gu [2 n_half, k] of kh_gemm_swiglu (blocks of 8 rows; row stride
+ * ldw).  g and u are rounded to bf16 before the product and h is rounded to bf16: the values that
+ * kh_gemv_fused's gate/up projection followed by its silu * mul prologue produce, without the
+ * [2 n_half] gate/up row.  Fuses SwiGLUMLP's gate and up projections with silu and mul for one
+ * token (reference: packages/model-utils/src/mlp/swiglu.ts:119-134; RMSNorm before it:
+ * packages/core/src/nn/modules/normalization/RMSNorm.ts:92-99).  Needs n_half % 8 == 0,
+ * k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w_gu and k <= 16384. */
+int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, const void* w_gu, int64_t ldw,
+                   void* h, int64_t n_half, int64_t k);
+
 #ifdef __cplusplus
 }
 #endif

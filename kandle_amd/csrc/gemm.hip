@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
 // streams them with raw 16-byte buffer loads, CB chunks of 512 columns per row in flight (rows past
 // n read as zero), and reduces each row across the wave.  Every weight byte is read once.
 // =============================================================================================
-template <int U, int PRO, typename TO>
+template <int U, int PRO, typename TO, bool PAIR8 = false>
 __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, const uint16_t* __restrict__ x2,
                                                     const uint16_t* __restrict__ nw, float eps,
                                                     const uint16_t* __restrict__ W, int64_t ldw, uint32_t w_bytes,
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, 
                                                     int nch, float alpha, float beta, AttnMerge am) {
   extern __shared__ float xs[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  GemvRows<U> g;
+  GemvRows<U, PAIR8> g;
   g.init(W, ldw, w_bytes, N, K, nch, (int64_t)blockIdx.x * (blockDim.x >> 6) + w,
          (int64_t)gridDim.x * (blockDim.x >> 6));
   // The first batch is in flight while the workgroup forms x'.
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, 
 
 // Launches gemv1_kernel; returns false (nothing launched) when the operands do not fit its
 // assumptions (16-byte aligned weight rows, 32-bit byte offsets, x' within 64 KiB of LDS).
-template <int U, int PRO, typename TO>
+template <int U, int PRO, typename TO, bool PAIR8 = false>
 void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw,
               uint32_t w_bytes, TO* C, const TO* cin, const TO* bias, int N, int K, int nch, float alpha, float beta,
               const AttnMerge& am) {
@@ -418,8 +418,27 @@ void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const ui
   int64_t grid = (waves + 3) / 4;
   if (grid > 8192) grid = 8192;  // waves then stride over the remaining rows
   const size_t shm = (size_t)nch * GV_CHUNK * sizeof(float);
-  gemv1_kernel<U, PRO, TO><<<(int)grid, 256, shm, stream()>>>(x, (const uint16_t*)x2, (const uint16_t*)nw, eps, W,
-                                                              ldw, w_bytes, C, cin, bias, N, K, nch, alpha, beta, am);
+  gemv1_kernel<U, PRO, TO, PAIR8><<<(int)grid, 256, shm, stream()>>>(x, (const uint16_t*)x2, (const uint16_t*)nw, eps,
+                                                                     W, ldw, w_bytes, C, cin, bias, N, K, nch, alpha,
+                                                                     beta, am);
+}
+
+// SwiGLU one-row projection: h[f] = bf16(silu(bf16(gate_f)) * bf16(up_f)) from the interleaved
+// gate/up weight (2 * n_half rows, blocks of 8), one wave per (gate, up) row pair.  False when the
+// operands do not fit (as launch_gemv1).
+template <int PRO>
+bool launch_gemv_swiglu(const void* x, const void* nw, float eps, const uint16_t* W, int64_t ldw, uint16_t* H,
+                        int n_half, int K) {
+  const int N = 2 * n_half;
+  if (n_half <= 0 || n_half % 8 != 0 || K <= 0) return false;
+  const int nch = (K + GV_CHUNK - 1) / GV_CHUNK;
+  const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
+  if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || ((int64_t)(N + 4) * ldw) * 2 >= (int64_t(1) << 32) ||
+      (size_t)nch * GV_CHUNK * sizeof(float) > 64 * 1024)
+    return false;
+  gemv1_go<2, PRO, uint16_t, true>(x, nullptr, nw, eps, W, ldw, (uint32_t)w_bytes, H, nullptr, nullptr, N, K, nch,
+                                   1.f, 0.f, AttnMerge{});
+  return true;
 }
 
 template <int PRO, typename TO>
@@ -738,6 +757,26 @@ int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, vo
              "kh_gemm_swiglu: row stride too large");
   return launch_gemm_swiglu((const uint16_t*)x, ldx, (const uint16_t*)w_gu, ldw, (uint16_t*)h, ldh, (int)m,
                             (int)(2 * n_half), (int)k);
+}
+
+int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, const void* w_gu, int64_t ldw,
+                   void* h, int64_t n_half, int64_t k) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(prologue == PRO_NONE || prologue == PRO_RMSNORM, "kh_gemv_swiglu: prologue must be 0 (none) or 1 (RMSNorm)");
+  KH_REQUIRE(n_half > 0 && k > 0 && 2 * n_half <= INT32_MAX && k <= INT32_MAX, "kh_gemv_swiglu: bad extents");
+  KH_REQUIRE(n_half % 8 == 0, "kh_gemv_swiglu: the intermediate size %lld is not a multiple of 8", (long long)n_half);
+  KH_REQUIRE(x && w_gu && h, "kh_gemv_swiglu: null pointer");
+  KH_REQUIRE(prologue != PRO_RMSNORM || norm_w != nullptr, "kh_gemv_swiglu: the RMSNorm prologue needs norm_w");
+  KH_REQUIRE(ldw >= k, "kh_gemv_swiglu: ldw < k");
+  const bool ok = prologue == PRO_RMSNORM
+                      ? launch_gemv_swiglu<PRO_RMSNORM>(x, norm_w, eps, (const uint16_t*)w_gu, ldw, (uint16_t*)h,
+                                                        (int)n_half, (int)k)
+                      : launch_gemv_swiglu<PRO_NONE>(x, norm_w, eps, (const uint16_t*)w_gu, ldw, (uint16_t*)h,
+                                                     (int)n_half, (int)k);
+  KH_REQUIRE(ok, "kh_gemv_swiglu: unsupported operands (need k %% 8 == 0, ldw %% 8 == 0, a 16-byte aligned weight, "
+                 "k <= 16384 and byte offsets below 4 GiB)");
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps, const void* w,

@@ -130,8 +130,13 @@ __device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const ui
 // issue_first() requests the first batch of weights (it may run long before x' exists); run()
 // streams the rest with the next batch always in flight.  Every caller goes through this code, so
 // a row's sum is formed the same way in every kernel that uses it.
-template <int U>
+// PAIR8 (U = 2, SwiGLU): the weight interleaves gate and up rows in blocks of 8 (rows 16i .. 16i+7
+// gate rows 8i .. 8i+7, rows 16i+8 .. 16i+15 the matching up rows); row group q = n0 / 2 is gate row
+// 16 (q / 8) + q % 8 and its up row 8 later, and the output is feature q:
+// bf16(silu(bf16(gate)) * bf16(up)), the value the silu * mul prologue of the next projection forms.
+template <int U, bool PAIR8 = false>
 struct GemvRows {
+  static_assert(!PAIR8 || U == 2, "paired gate/up rows take two rows per group");
   static constexpr int CB = 8 / U;  // 16-byte loads in flight per row per lane
   __amdgpu_buffer_rsrc_t rsrc;
   int64_t ldw, n0, stride;
@@ -153,6 +158,15 @@ struct GemvRows {
   }
   // Weight loads of batch (row group n, chunks [c0, c0 + CB)); columns past K (row padding when
   // ldw > K) and rows past N read as zero (offset w_bytes is out of range).
+  // Weight row u of row group n.
+  static __device__ __forceinline__ int64_t row_of(int64_t n, int u) {
+    if constexpr (PAIR8) {
+      const int64_t q = n >> 1;
+      return 16 * (q >> 3) + (q & 7) + 8 * u;
+    } else {
+      return n + u;
+    }
+  }
   __device__ __forceinline__ void issue(int64_t n, int c0) {
 #pragma unroll
     for (int cc = 0; cc < CB; ++cc)
@@ -160,7 +174,7 @@ struct GemvRows {
       for (int u = 0; u < U; ++u) {
         const int c = c0 + cc;
         const int k = c * GV_CHUNK + lane * 8;
-        const uint32_t off = k < K ? (uint32_t)(((n + u) * ldw + k) * 2) : w_bytes;
+        const uint32_t off = k < K ? (uint32_t)((row_of(n, u) * ldw + k) * 2) : w_bytes;
         wv[u][cc] = c < nch ? buf_load16(rsrc, off) : make_uint4(0, 0, 0, 0);
       }
   }
@@ -206,11 +220,16 @@ struct GemvRows {
           }
         }
       }
+      if constexpr (PAIR8) {
+        const float gsum = wave_sum(acc[0]), usum = wave_sum(acc[1]);
+        if (lane == 0) Elem<TO>::store(C, n0 >> 1, silu_ref(round_bf16(gsum)) * round_bf16(usum));
+      } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float sum = wave_sum(acc[u]);
-        const int64_t n = n0 + u;
-        if (lane == 0 && n < N) Elem<TO>::store(C, n, epilogue<TO>(sum, alpha, beta, cin, 0, bias, 0, n));
+        for (int u = 0; u < U; ++u) {
+          const float sum = wave_sum(acc[u]);
+          const int64_t n = n0 + u;
+          if (lane == 0 && n < N) Elem<TO>::store(C, n, epilogue<TO>(sum, alpha, beta, cin, 0, bias, 0, n));
+        }
       }
     }
   }

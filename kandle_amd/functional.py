@@ -181,6 +181,19 @@ def linear_fused(prologue: str, x: Tensor, weight: Tensor, norm_weight: Optional
     return _wrap(out)
 
 
+def linear_swiglu_row(prologue: str, x: Tensor, w_gu: Tensor, norm_weight: Optional[Tensor] = None,
+                      eps: float = 1e-6) -> Tensor:
+    """One-row SwiGLU (decode): silu(x' W_gate^T) * (x' W_up^T) as a new bf16 [1, I] tensor from the
+    interleaved gate/up weight [2I, H]; prologue 'rms_norm' (x the fp32 residual row, x' its
+    RMSNorm) or 'none' (x' = x, bf16)."""
+    out = _new(w_gu, (1, w_gu.shape[0] // 2), "bfloat16")
+    params = {"eps": eps}
+    if norm_weight is not None:
+        params["norm_weight"] = norm_weight.handle
+    _kernel(w_gu, "gemv_swiglu")(prologue, x.handle, w_gu.handle, out, params)
+    return _wrap(out)
+
+
 # ---------------------------------------------------------------------------------------------
 # normalisation and pointwise
 # ---------------------------------------------------------------------------------------------

@@ -781,6 +781,33 @@ def gemv_fused(prologue: str, x, w, out, params=None) -> None:
     )
 
 
+def gemv_swiglu(prologue: str, x, w_gu, out, params=None) -> None:
+    """One-row SwiGLU projection (decode): out[1, I] = silu(x' W_gate^T) * (x' W_up^T) in bf16, from
+    the gate/up weight w_gu [2I, H] interleaved in blocks of 8 rows (interleave_gate_up), where x' is
+    'none' -> x (bf16 [H]) or 'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row.
+    Gate and up are rounded to bf16 before the product, as gemv_fused's gate/up row followed by the
+    'silu_mul_interleaved' prologue forms it (swiglu.ts:119-134 for one token).  params:
+    norm_weight, eps."""
+    params = params or {}
+    if prologue not in ("none", "rms_norm"):
+        raise ValueError(f"gemv_swiglu: prologue must be 'none' or 'rms_norm', not {prologue!r}")
+    two_i, k = w_gu.shape
+    n_half = two_i // 2
+    if w_gu.dtype != BFLOAT16 or w_gu.strides[1] != 1:
+        raise TypeError("gemv_swiglu: the weight must be bf16 with contiguous rows")
+    want = FLOAT32 if prologue == "rms_norm" else BFLOAT16
+    if x.dtype != want or x.numel != k or not x.is_contiguous():
+        raise ValueError(f"gemv_swiglu: x must be one contiguous {want} row of {k} elements")
+    if out.dtype != BFLOAT16 or out.numel != n_half or not out.is_contiguous():
+        raise ValueError(f"gemv_swiglu: out must be a contiguous bf16 row of {n_half} elements")
+    nw = params.get("norm_weight")
+    if prologue == "rms_norm" and (nw is None or nw.dtype != BFLOAT16 or nw.numel != k):
+        raise ValueError("gemv_swiglu: rms_norm needs a bf16 norm_weight of k elements")
+    _lib.call("kh_gemv_swiglu", GEMV_PROLOGUES[prologue], _vp(x.data_ptr()),
+              _vp(nw.data_ptr()) if nw is not None else None, C.c_float(float(params.get("eps", 1e-6))),
+              _vp(w_gu.data_ptr()), w_gu.strides[0], _vp(out.data_ptr()), n_half, k)
+
+
 def greedy_advance(next_token, position, seq_len, token_log, log_base: int) -> None:
     """Device-side step of the greedy loop (for_causal_lm.ts:475-508): with p = position[0],
     token_log[p + 1 - log_base] = next_token[0] (when inside the log), position = p + 1,
@@ -867,6 +894,7 @@ KERNELS = {
     "argmax": argmax,
     "greedy_advance": greedy_advance,
     "gemv_fused": gemv_fused,
+    "gemv_swiglu": gemv_swiglu,
     "fill": fill,
     "zeros": zeros,
 }

@@ -262,9 +262,9 @@ class Qwen3ForCausalLM:
                 h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm"], eps)     # x += o W_o^T
                 attn_t.dispose()
             if one:
-                gu = F.linear_fused("rms_norm", x, L["w_gu"], L["post_norm"], eps)     # [1, 2I] interleaved
-                F.linear_fused("silu_mul_interleaved", gu, L["w_down"], residual=x)    # x += a W_d^T
-                gu.dispose()
+                a = F.linear_swiglu_row("rms_norm", x, L["w_gu"], L["post_norm"], eps)  # [1, I] = silu(g) * u
+                F.linear_fused("none", a, L["w_down"], residual=x)                     # x += a W_d^T
+                a.dispose()
             else:
                 a = F.linear_swiglu(h, L["w_gu"])                                      # [S, I]
                 h.dispose()

@@ -500,6 +500,13 @@ FN(gemvFused, 15)
   double al = arg_f64(A, 12); double be = arg_f64(A, 13); int odt = arg_int(A, 14);
   CALL(kh_gemv_fused(pro, x, x2, nw, (float)eps, w, ldw, c, cin, bias, n, k, (float)al, (float)be, odt))
 
+/* gemvSwiglu(prologue, x, normW, eps, wGu, ldw, h, nHalf, k) */
+FN(gemvSwiglu, 9)
+  int pro = arg_int(A, 0); void* x = arg_ptr(A, 1); void* nw = arg_ptr(A, 2); double eps = arg_f64(A, 3);
+  void* w = arg_ptr(A, 4); int64_t ldw = arg_i64(A, 5); void* h = arg_ptr(A, 6); int64_t nh = arg_i64(A, 7);
+  int64_t k = arg_i64(A, 8);
+  CALL(kh_gemv_swiglu(pro, x, nw, (float)eps, w, ldw, h, nh, k))
+
 /* ---------------------------------------------------------------- module ----------------------- */
 #define EXPORT(name) {#name, 0, js_##name, 0, 0, 0, napi_enumerable, 0}
 
@@ -514,7 +521,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
       EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemmSplitCount),
-      EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused),
+      EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused), EXPORT(gemvSwiglu),
   };
   napi_define_properties(env, exports, sizeof(d) / sizeof(d[0]), d);
   napi_value v;

@@ -544,6 +544,25 @@ function gemvFused(prologue: string, x: HipTensorHandle, w: HipTensorHandle, out
                   p.alpha === undefined ? 1 : (p.alpha as number), beta, out.kh);
 }
 
+// gemv_swiglu(prologue, x, wGu, out, params): one-row SwiGLU (decode): out[1, I] = silu(x' W_gate^T)
+// * (x' W_up^T) in bf16 from the gate/up weight interleaved in blocks of 8 rows; prologue 'none'
+// (x' = x, bf16) or 'rms_norm' (x the fp32 residual row; params normWeight, eps).
+function gemvSwiglu(prologue: string, x: HipTensorHandle, wGu: HipTensorHandle, out: HipTensorHandle,
+                    params?: { [key: string]: any }): void {
+  const p = params || {};
+  if (prologue !== 'none' && prologue !== 'rms_norm') throw new Error(`gemv_swiglu: unknown prologue ${prologue}`);
+  const k = wGu.shape[1], nHalf = wGu.shape[0] / 2;
+  if (wGu.dtype !== 'bfloat16' || wGu.strides[1] !== 1) throw new Error('gemv_swiglu: bf16 weight with contiguous rows');
+  const want = prologue === 'rms_norm' ? 'float32' : 'bfloat16';
+  if (x.dtype !== want || x.numel !== k || !x.isContiguous())
+    throw new Error(`gemv_swiglu: x must be a contiguous ${want} row of ${k} elements`);
+  if (out.dtype !== 'bfloat16' || out.numel !== nHalf || !out.isContiguous())
+    throw new Error(`gemv_swiglu: out must be a contiguous bf16 row of ${nHalf} elements`);
+  const nw = p.normWeight as HipTensorHandle | undefined;
+  addon.gemvSwiglu(GEMV_PROLOGUE[prologue], x.ptr, nw === undefined ? null : nw.ptr,
+                   p.eps === undefined ? 1e-6 : (p.eps as number), wGu.ptr, wGu.strides[0], out.ptr, nHalf, k);
+}
+
 // linear_swiglu(x, wGu, output): output [.., I] = silu(x W_gate^T) * (x W_up^T) in bf16 from the
 // gate/up weight [2I, H] interleaved in blocks of 8 rows (swiglu.ts:119-134 in one GEMM).
 function linearSwiglu(x: HipTensorHandle, wGu: HipTensorHandle, out: HipTensorHandle): void {
@@ -719,6 +738,7 @@ export function registerHipKernels(reg: SimpleOperatorRegistry): void {
   reg.register('fill', fill);
   reg.register('zeros', zeros);
   reg.register('gemv_fused', gemvFused);
+  reg.register('gemv_swiglu', gemvSwiglu);
   reg.register('linear_swiglu', linearSwiglu);
   reg.register('linear_add_rms_norm', linearAddRmsNorm);
   reg.register('decode_attention_block', decodeAttentionBlock);

@@ -151,6 +151,10 @@ async function main() {
   ops.find('gemv_fused')('none', gb, gw, gc, { cin: gc });
   write('gvr', await gc.dataAsync());
 
+  const gs = backend.createTensorHandle([1, f2.gvN / 2], 'bfloat16');
+  ops.find('gemv_swiglu')('rms_norm', gx, gw, gs, { normWeight: gn, eps: 1e-6 });
+  write('gvs', await gs.dataAsync());
+
   const sx = t([f2.swM, f2.swH], 'bfloat16', readU16('swx'));
   const sg = t([2 * f2.swI, f2.swH], 'bfloat16', readU16('swg'));
   const so = backend.createTensorHandle([f2.swM, f2.swI], 'bfloat16');
@@ -212,7 +216,7 @@ async function main() {
 
   for (const hnd of [q, k, v, o, mask, om, x, w, y, a, b, c, out, g, u, h, gT, s1, prod, table, ids, rows, am,
                      un.neg, un.cos, un.sin, ar, rq, rk, rv, wq, wk, inv, pos, kc, vc, qk[0], qk[1], dq, dk, dv, lens, dout,
-                     gx, gw, gn, go, gb, gc, sx, sg, so, lx, lw, lr, ln, lo, bqkv, bqn, bkn, binv, bpos, bkc, bvc, bwo, bx,
+                     gx, gw, gn, go, gs, gb, gc, sx, sg, so, lx, lw, lr, ln, lo, bqkv, bqn, bkn, binv, bpos, bkc, bvc, bwo, bx,
                      lg, stok, sctr, slp, nt, ps, sl, lgg, cbuf, cview, csrc, zt]) {
     hnd.dispose();
   }

@@ -125,6 +125,37 @@ def test_gemv_interleaved_silu_mul_prologue_matches_split_halves(hip):
     assert ok, err
 
 
+@pytest.mark.parametrize("prologue", ["rms_norm", "none"])
+@pytest.mark.parametrize("I,K", [(3072, 1024), (64, 256), (8, 520)])
+def test_gemv_swiglu_matches_gate_up_row_and_silu_mul_prologue(hip, prologue, I, K):
+    """kh_gemv_swiglu (one wave per gate/up row pair of the interleaved weight, silu * mul in the
+    epilogue) equals the gate/up projection row (kh_gemv_fused) followed by the interleaved
+    silu * mul, bit for bit; so does the down projection fed from either."""
+    from kandle_amd.kernels import interleave_gate_up
+    N = 1024
+    if prologue == "rms_norm":
+        x = Tensor(syn.normal(340, (1, K), 3.0))
+        nw, _ = seeded(341, (K,), "bfloat16")
+    else:
+        x, _ = seeded(340, (1, K), "bfloat16")
+        nw = None
+    _, gh = seeded(342, (I, K), "bfloat16", std=0.05)
+    _, uh = seeded(343, (I, K), "bfloat16", std=0.05)
+    w_gu = Tensor(syn.bf16(interleave_gate_up(gh, uh))[0], dtype="bfloat16")
+    a = F.linear_swiglu_row(prologue, x, w_gu, nw, 1e-6)
+    gu = F.linear_fused(prologue, x, w_gu, nw, 1e-6)                    # [1, 2I] interleaved
+    gv = gu.numpy().reshape(I // 8, 2, 8)
+    ref = oracle.silu_mul(gv[:, 0].reshape(-1), gv[:, 1].reshape(-1))
+    av = a.numpy().reshape(-1)
+    assert np.all(np.abs(av - ref) <= 2 ** -8 * np.abs(ref) + 1e-30)      # one bf16 rounding
+    w_d, _ = seeded(344, (N, I), "bfloat16", std=0.02)
+    res0 = Tensor(np.ones((1, N), np.float32))
+    res1 = Tensor(np.ones((1, N), np.float32))
+    y0 = F.linear_fused("silu_mul_interleaved", gu, w_d, residual=res0).numpy()
+    y1 = F.linear_fused("none", a, w_d, residual=res1).numpy()
+    np.testing.assert_array_equal(y0, y1)
+
+
 @pytest.mark.parametrize("M,I,K", [(512, 3072, 1024), (130, 96, 64), (1, 3072, 1024), (7, 40, 200), (600, 3072, 1024)])
 def test_linear_swiglu_matches_unfused_gemm_and_silu_mul(hip, M, I, K):
     """kh_gemm_swiglu (gate/up GEMM with silu*mul in the epilogue, interleaved weight) against the

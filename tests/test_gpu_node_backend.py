@@ -5,7 +5,7 @@ the reference kernel signature — flash_attention, sdpa_masked, rms_norm, matmu
 residual), silu_mul, the iterator kernels silu / mul on a transposed view, index_select, argmax,
 neg / cos / sin, arange, rms_norm_rope writing KV caches at device positions, decode_attention
 over ragged cache lengths, the fused gemv_fused / linear_swiglu / linear_add_rms_norm /
-decode_attention_block, sample, greedy_advance, copy_ into a strided view and zeros — then
+gemv_swiglu / decode_attention_block, sample, greedy_advance, copy_ into a strided view and zeros — then
 disposes every handle.  This test writes the inputs and checks each output against the CPU
 oracle, and that the backend's live device bytes return to where they started."""
 import json
@@ -179,6 +179,9 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     go = HipTensorHandle.create_new((1, fu["gvN"]), "bfloat16")
     kernels.gemv_fused("rms_norm", gx.handle, gw.handle, go, {"norm_weight": gn.handle, "eps": 1e-6})
     np.testing.assert_array_equal(f32_file("gvo", (1, fu["gvN"])), go.data_async())
+    gs = HipTensorHandle.create_new((1, fu["gvN"] // 2), "bfloat16")
+    kernels.gemv_swiglu("rms_norm", gx.handle, gw.handle, gs, {"norm_weight": gn.handle, "eps": 1e-6})
+    np.testing.assert_array_equal(f32_file("gvs", (1, fu["gvN"] // 2)), gs.data_async())
     kernels.gemv_fused("none", gb.handle, gw.handle, gc.handle, {"cin": gc.handle})
     np.testing.assert_array_equal(f32_file("gvr", (1, fu["gvN"])), gc.numpy())
     sx, sg = T("swx"), T("swg")
