@@ -5,9 +5,10 @@
 // builder.ts:138-329): S = (Q K^T) * scale, causal masks key j > query i (top-left aligned), GQA
 // query head h reads kv head h / (hq / hkv), O = softmax(S) V.
 //
-// One workgroup per (batch, query head, block of 32 queries), kF32Waves waves.  Wave w takes the
-// block's 32-key tiles w, w + kF32Waves, ... (with the causal mask only tiles up to the block's
-// last query), so a short prompt still spreads each block over four SIMDs.  Per tile the wave
+// One workgroup per (batch, query head, block of 32 queries), NW waves (4, or 8 for grids with
+// fewer than two workgroups per CU).  Wave w takes the block's 32-key tiles w, w + NW, ... (with the
+// causal mask only tiles up to the block's last query), so a short prompt still spreads each block
+// over every SIMD of its CU.  Per tile the wave
 // forms S^T = K Q^T in D/2 MFMA steps (step s pairs head-dim element s on lanes 0-31 with s + D/2
 // on lanes 32-63): lane (r, g) = (lane & 31, lane >> 5) then holds query r's scores against keys
 // 8(v/4) + 4g + v%4, v < 16, so a query's maximum and sum are an in-lane reduction plus one
@@ -24,7 +25,7 @@ using namespace kh;
 
 namespace {
 
-constexpr int kF32Waves = 4;
+constexpr int kF32Waves = 4;  // waves per workgroup of the default (register-prefetching) variant
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kOut = 0xffffffffu;  // a byte offset past every buffer range: the load reads 0
 
@@ -35,17 +36,22 @@ __device__ __forceinline__ float4 buf_load16f(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-// c = scale * log2(e): scores are kept in log2 units (softmax by exp2).
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kF32Waves * 64) void flash_f32_kernel(const float* __restrict__ Q,
+// c = scale * log2(e): scores are kept in log2 units (softmax by exp2).  NW waves per workgroup;
+// with NW = 4 (one wave per SIMD) the next tile's K is loaded during the current tile's softmax and
+// PV and V during QK^T; with NW = 8 (two per SIMD, for short inputs whose blocks would otherwise
+// give each SIMD a chain of tiles; 256 registers per wave) the other wave on the SIMD hides the
+// latency: K loads at the tile start and V after QK^T, into the registers K has left.
+template <int D, bool CAUSAL, int NW = kF32Waves>
+__global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restrict__ Q,
                                                                    const float* __restrict__ K,
                                                                    const float* __restrict__ V, float* __restrict__ O,
                                                                    int hq, int hkv, int lq, int lk, AttnStrides st,
                                                                    float c, int nqb) {
   constexpr int HALF = D / 2, NH4 = HALF / 4, NDB = D / 32;
   constexpr int OSTR = D + 4;  // LDS row stride (floats) of the wave partial outputs
-  __shared__ float2 ml_s[kF32Waves][32];
-  __shared__ __attribute__((aligned(16))) float o_s[kF32Waves][32 * OSTR];
+  constexpr bool PREFETCH_K = NW <= 4;
+  __shared__ float2 ml_s[NW][32];
+  __shared__ __attribute__((aligned(16))) float o_s[NW][32 * OSTR];
 
   const int lane = threadIdx.x & 63, r = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -111,17 +117,19 @@ __global__ __launch_bounds__(kF32Waves * 64) void flash_f32_kernel(const float* 
     for (int v = 0; v < 16; ++v) oacc[db][v] = 0.f;
   float m = -INFINITY, l = 0.f;
   float kv[HALF];
-  if (w < nt) load_k(kv, w * 32);
-  for (int t = w; t < nt; t += kF32Waves) {
+  if (PREFETCH_K && w < nt) load_k(kv, w * 32);
+  for (int t = w; t < nt; t += NW) {
     const int k0 = t * 32;
+    if (!PREFETCH_K) load_k(kv, k0);
     float vv[NDB][16];
-    load_v(vv, k0);
+    if (PREFETCH_K) load_v(vv, k0);  // in flight during QK^T
     f32x16 sacc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sacc[v] = 0.f;
 #pragma unroll
     for (int s = 0; s < HALF; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[s], qv[s], sacc, 0, 0, 0);
-    if (t + kF32Waves < nt) load_k(kv, k0 + 32 * kF32Waves);  // next tile's keys, during softmax and PV
+    if (PREFETCH_K && t + NW < nt) load_k(kv, k0 + 32 * NW);  // next tile's keys, during softmax and PV
+    if (!PREFETCH_K) load_v(vv, k0);  // into the registers K has left
     float tmax = -INFINITY;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -162,19 +170,21 @@ __global__ __launch_bounds__(kF32Waves * 64) void flash_f32_kernel(const float* 
       *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 32 * db + 8 * v4 + 4 * g]) =
           make_float4(oacc[db][4 * v4], oacc[db][4 * v4 + 1], oacc[db][4 * v4 + 2], oacc[db][4 * v4 + 3]);
   __syncthreads();
-  constexpr int CPT = D / 8;  // output columns per thread: 8 threads per query
-  const int tq = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * CPT;
-  float2 mlw[kF32Waves];
+  constexpr int TPQ = NW * 64 / 32;  // threads per query
+  constexpr int CPT = D / TPQ;      // output columns per thread
+  static_assert(CPT % 4 == 0, "whole float4 columns per thread");
+  const int tq = threadIdx.x / TPQ, c0 = (threadIdx.x % TPQ) * CPT;
+  float2 mlw[NW];
   float M = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < kF32Waves; ++u) {
+  for (int u = 0; u < NW; ++u) {
     mlw[u] = ml_s[u][tq];
     M = fmaxf(M, mlw[u].x);
   }
   const float mu = M == -INFINITY ? 0.f : M;
-  float f[kF32Waves], L = 0.f;
+  float f[NW], L = 0.f;
 #pragma unroll
-  for (int u = 0; u < kF32Waves; ++u) {
+  for (int u = 0; u < NW; ++u) {
     f[u] = fast_exp2(mlw[u].x - mu);
     L += mlw[u].y * f[u];
   }
@@ -186,7 +196,7 @@ __global__ __launch_bounds__(kF32Waves * 64) void flash_f32_kernel(const float* 
     for (int j = 0; j < CPT; j += 4) {
       float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-      for (int u = 0; u < kF32Waves; ++u) {
+      for (int u = 0; u < NW; ++u) {
         const float4 x = *reinterpret_cast<const float4*>(&o_s[u][tq * OSTR + c0 + j]);
         a0 += x.x * f[u];
         a1 += x.y * f[u];
@@ -198,13 +208,27 @@ __global__ __launch_bounds__(kF32Waves * 64) void flash_f32_kernel(const float* 
   }
 }
 
+template <int D, int NW>
+void launch_f32_dw(const float* q, const float* k, const float* v, float* o, int grid, int hq, int hkv, int lq,
+                   int lk, const AttnStrides& st, float c, int nqb, bool causal) {
+  if (causal)
+    flash_f32_kernel<D, true, NW><<<grid, NW * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+  else
+    flash_f32_kernel<D, false, NW><<<grid, NW * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+}
+
+// Eight-wave workgroups (two waves per SIMD, the tiles of a block over twice the waves) when the
+// grid leaves CUs without a second workgroup, for head_dim 64 and 128.
 template <int D>
 void launch_f32_d(const float* q, const float* k, const float* v, float* o, int grid, int hq, int hkv, int lq, int lk,
                   const AttnStrides& st, float c, int nqb, bool causal) {
-  if (causal)
-    flash_f32_kernel<D, true><<<grid, kF32Waves * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
-  else
-    flash_f32_kernel<D, false><<<grid, kF32Waves * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+  if constexpr (D == 64 || D == 128) {
+    if (grid < 2 * cu_count()) {
+      launch_f32_dw<D, 8>(q, k, v, o, grid, hq, hkv, lq, lk, st, c, nqb, causal);
+      return;
+    }
+  }
+  launch_f32_dw<D, kF32Waves>(q, k, v, o, grid, hq, hkv, lq, lk, st, c, nqb, causal);
 }
 
 }  // namespace
