@@ -416,7 +416,9 @@ void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const ui
               const AttnMerge& am) {
   const int64_t waves = (N + U - 1) / U;
   int64_t grid = (waves + 3) / 4;
-  if (grid > 8192) grid = 8192;  // waves then stride over the remaining rows
+  // Waves stride over the rows past the first grid: lm_head (151936 rows, 8 per wave) at most 2048
+  // workgroups: 69.5 -> 59.9 us graph-replayed with 4 rows per wave and 8192 workgroups before.
+  if (grid > 2048) grid = 2048;
   const size_t shm = (size_t)nch * GV_CHUNK * sizeof(float);
   gemv1_kernel<U, PRO, TO, PAIR8><<<(int)grid, 256, shm, stream()>>>(x, (const uint16_t*)x2, (const uint16_t*)nw, eps,
                                                                      W, ldw, w_bytes, C, cin, bias, N, K, nch, alpha,
@@ -454,7 +456,7 @@ bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, cons
     return false;
   const uint32_t wb = (uint32_t)w_bytes;
   if (N >= 16384)
-    gemv1_go<4, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
+    gemv1_go<8, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   else if (N >= 2048)
     gemv1_go<2, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   else
