@@ -18,6 +18,7 @@
 #include <stdbool.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "kandle_hip.h"
@@ -253,6 +254,81 @@ static napi_value js_alloc(napi_env env, napi_callback_info info) {
 }
 
 FN(free, 1) void* p = arg_ptr(A, 0); CALL(kh_free(p))
+
+/* Owned device blocks.  allocOwned(bytes) returns an external object that holds the block;
+   freeOwned(ext) returns it to the allocator (once; later calls do nothing), and the object's
+   finalizer -- run by the garbage collector after the object becomes unreachable -- returns a
+   block that was never freed: the safety net of a storage whose dispose() was forgotten (Node 12
+   has no FinalizationRegistry).  ownedPtr(ext) is the block's address as a BigInt. */
+typedef struct {
+  void* p;
+  int live;
+} Owned;
+
+static void owned_finalize(napi_env env, void* data, void* hint) {
+  (void)env;
+  (void)hint;
+  Owned* o = (Owned*)data;
+  if (o->live) kh_free(o->p);
+  free(o);
+}
+
+static Owned* arg_owned(Args* A, size_t i) {
+  void* d = NULL;
+  if (type_of(A, i) != napi_external || napi_get_value_external(A->env, A->v[i], &d) != napi_ok || d == NULL) {
+    type_error(A, i, "an owned block (from allocOwned)");
+    return NULL;
+  }
+  return (Owned*)d;
+}
+
+static napi_value js_allocOwned(napi_env env, napi_callback_info info) {
+  Args A_, *A = &A_;
+  if (!begin(A, env, info, "allocOwned", 1)) return NULL;
+  const int64_t bytes = arg_i64(A, 0);
+  if (A->bad) return NULL;
+  if (bytes < 0) {
+    type_error(A, 0, "a byte count >= 0");
+    return NULL;
+  }
+  void* p = NULL;
+  const int rc = kh_alloc(&p, (size_t)bytes);
+  if (rc != KH_OK) return done(A, rc);
+  Owned* o = (Owned*)malloc(sizeof(Owned));
+  napi_value ext;
+  if (o == NULL) {
+    kh_free(p);
+    napi_throw_error(env, NULL, "kandle_hip.allocOwned: out of host memory");
+    return NULL;
+  }
+  o->p = p;
+  o->live = 1;
+  if (napi_create_external(env, o, owned_finalize, NULL, &ext) != napi_ok) {
+    kh_free(p);
+    free(o);
+    napi_throw_error(env, NULL, "kandle_hip.allocOwned: napi_create_external failed");
+    return NULL;
+  }
+  return ext;
+}
+
+static napi_value js_ownedPtr(napi_env env, napi_callback_info info) {
+  Args A_, *A = &A_;
+  if (!begin(A, env, info, "ownedPtr", 1)) return NULL;
+  Owned* o = arg_owned(A, 0);
+  if (A->bad) return NULL;
+  return big_ptr(env, o->live ? o->p : NULL);
+}
+
+static napi_value js_freeOwned(napi_env env, napi_callback_info info) {
+  Args A_, *A = &A_;
+  if (!begin(A, env, info, "freeOwned", 1)) return NULL;
+  Owned* o = arg_owned(A, 0);
+  if (A->bad) return NULL;
+  if (!o->live) return NULL;
+  o->live = 0;
+  return done(A, kh_free(o->p));
+}
 FN(emptyCache, 0) CALL(kh_empty_cache())
 FN(synchronize, 0) CALL(kh_synchronize())
 
@@ -513,6 +589,7 @@ FN(gemvSwiglu, 9)
 static napi_value module_init(napi_env env, napi_value exports) {
   napi_property_descriptor d[] = {
       EXPORT(init), EXPORT(deviceCount), EXPORT(lastError), EXPORT(setDebug), EXPORT(alloc), EXPORT(free), EXPORT(emptyCache),
+      EXPORT(allocOwned), EXPORT(ownedPtr), EXPORT(freeOwned),
       EXPORT(allocStats), EXPORT(memcpyH2D), EXPORT(memcpyD2H), EXPORT(memcpyD2D), EXPORT(synchronize),
       EXPORT(eventCreate), EXPORT(eventDestroy), EXPORT(eventRecord), EXPORT(eventElapsedMs),
       EXPORT(graphBeginCapture), EXPORT(graphEndCapture), EXPORT(graphLaunch), EXPORT(graphDestroy),

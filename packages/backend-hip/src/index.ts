@@ -91,14 +91,20 @@ function fromBf16Bits(bits: Uint16Array): Float32Array {
 // ---------------------------------------------------------------------------------------------
 let nextId = 1;
 
+// The device block is an addon-owned object: dispose() frees it through the last view's decRef, and
+// a storage that is dropped without dispose() is freed by the object's finalizer when the garbage
+// collector reclaims it (the role of backend-webgpu's FinalizationRegistry, storage.ts:6-14, which
+// Node 12 lacks).
 export class HipStorage {
   ptr: bigint;
   byteLength: number;
   refCount: number;
   id: number;
+  private block: any;
 
   constructor(byteLength: number) {
-    this.ptr = addon.alloc(Math.max(byteLength, 1));
+    this.block = addon.allocOwned(Math.max(byteLength, 1));
+    this.ptr = addon.ownedPtr(this.block);
     this.byteLength = byteLength;
     this.refCount = 1;
     this.id = nextId++;
@@ -111,7 +117,7 @@ export class HipStorage {
   // Returns the block to the library's caching allocator once the last view lets go.
   decRef(): void {
     this.refCount -= 1;
-    if (this.refCount === 0) addon.free(this.ptr);
+    if (this.refCount === 0) addon.freeOwned(this.block);
   }
 }
 
@@ -296,6 +302,7 @@ function rmsNorm(inputs: HipTensorHandle[], params: { [key: string]: any }): Hip
   const n = numelOf(ns);
   const eps = params.eps === undefined ? 1e-5 : (params.eps as number);
   const w = params.weight as HipTensorHandle | undefined;
+  if (params.bias !== undefined && params.bias !== null) throw new Error('rms_norm: bias is not part of RMSNorm');
   const outDtype = (params.out ? (params.out as HipTensorHandle).dtype : (params.outDtype || x.dtype)) as DType;
   const out = (params.out as HipTensorHandle | undefined) || HipTensorHandle.createNew(x.shape, outDtype);
   const rows = x.numel / n;

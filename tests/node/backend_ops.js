@@ -222,8 +222,21 @@ async function main() {
   }
   backend.synchronize();
   const after = backend.memoryStats();
+
+  // A storage dropped without dispose(): the garbage collector's finalizer returns its block.
+  let gcFreed = null;
+  if (typeof global.gc === 'function') {
+    const base = backend.memoryStats().liveBytes;
+    (() => { backend.createTensorHandle([1 << 20], 'float32'); })();   // 4 MiB, never disposed
+    const held = backend.memoryStats().liveBytes - base;
+    for (let i = 0; i < 5 && backend.memoryStats().liveBytes > base; ++i) {
+      global.gc();
+      await new Promise((resolve) => setImmediate(resolve));
+    }
+    gcFreed = { held, left: backend.memoryStats().liveBytes - base };
+  }
   console.log(JSON.stringify({ ok: true, names: ops.names(), liveBefore: before.liveBytes, liveAfter: after.liveBytes,
-                                greedyTok, sampledTok, sampledLp, adv, zsum }));
+                                greedyTok, sampledTok, sampledLp, adv, zsum, gcFreed }));
 }
 
 main().catch((err) => {

@@ -1,13 +1,14 @@
 """Kandle's kernels driven from Node through the TypeScript HipBackend (packages/backend-hip/src/
 index.ts, stripped to dist/index.js by strip-types.js): tests/node/backend_ops.js creates the backend,
 looks each kernel up in its operator registry by the name Kandle's dispatcher uses and calls it with
-the reference kernel signature — flash_attention, sdpa_masked, rms_norm, matmul (linear plus a
+the reference kernel signature -- flash_attention, sdpa_masked, rms_norm, matmul (linear plus a
 residual), silu_mul, the iterator kernels silu / mul on a transposed view, index_select, argmax,
-neg / cos / sin, arange, rms_norm_rope writing KV caches at device positions, decode_attention
-over ragged cache lengths, the fused gemv_fused / linear_swiglu / linear_add_rms_norm /
-gemv_swiglu / decode_attention_block, sample, greedy_advance, copy_ into a strided view and zeros — then
-disposes every handle.  This test writes the inputs and checks each output against the CPU
-oracle, and that the backend's live device bytes return to where they started."""
+neg / cos / sin, arange, rms_norm_rope writing KV caches at device positions, decode_attention over
+ragged cache lengths, the fused gemv_fused / gemv_swiglu / linear_swiglu / linear_add_rms_norm /
+decode_attention_block, sample, greedy_advance, copy_ into a strided view and zeros -- then disposes
+every handle.  This test writes the inputs and checks each output against the CPU oracle (the fused
+ops bit for bit against the Python binding), that the backend's live device bytes return to where
+they started, and that a storage dropped without dispose() is freed by the garbage collector."""
 import json
 import math
 import os
@@ -114,11 +115,12 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     (tmp_path / "meta.json").write_text(json.dumps({"flash": f, "norm": r, "mm": m, "emb": e, "rope": p,
                                                     "decode": dd, "fused": fu, "block": blk, "sample": smp}))
 
-    out = subprocess.run(["node", SCRIPT, str(tmp_path)], capture_output=True, text=True, timeout=300)
+    out = subprocess.run(["node", "--expose-gc", SCRIPT, str(tmp_path)], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr[-2000:]
     res = json.loads(out.stdout.strip().splitlines()[-1])
     assert res["ok"]
     assert res["liveAfter"] == res["liveBefore"], res
+    assert res["gcFreed"]["held"] >= 4 << 20 and res["gcFreed"]["left"] == 0, res["gcFreed"]   # GC safety net
 
     def f32_file(name, shape, dtype=np.float32):
         return np.fromfile(str(tmp_path / name), dtype).reshape(shape)
