@@ -1,0 +1,295 @@
+// Qwen3 causal LM on the HIP backend, host side in TypeScript: the caller of the hot path, written
+// against the backend's operator registry the way Kandle's model code reaches its kernels
+// (packages/model-utils/src/qwen3/{model,decoder_layer,for_causal_lm}.ts, attention/gqa.ts,
+// mlp/swiglu.ts).  It runs the same launches, in the same order, as the Python mirror
+// (kandle_amd/model_utils/qwen3.py), so both produce the same logits bit for bit:
+//
+//   prefill of S tokens (pre-norm decoder layers, decoder_layer.ts:191-241)
+//     x = embed[ids] (fp32 residual stream), h = rms_norm(x, input_layernorm) (bf16)
+//     per layer: qkv = h W_qkv^T (q/k/v rows concatenated); q/k per-head RMSNorm + RoPE, q written
+//       heads-first, k and v written into the KV caches at their positions (rms_norm_rope);
+//       o = causal flash attention over the cache rows [0, S); x += o W_o^T and h = rms_norm(x,
+//       post_attention_layernorm) (linear_add_rms_norm); a = silu(h W_gate^T) * (h W_up^T)
+//       (linear_swiglu, gate/up interleaved in blocks of 8 rows); x += a W_down^T and h = the next
+//       layer's input norm of x (the final norm of the last row after the last layer)
+//     logits = h E^T in fp32 with the tied embedding E (for_causal_lm.ts:121-125, 184-185)
+//   decode step of one token at device position p (greedy loop, for_causal_lm.ts:475-508)
+//     x = embed[token]; per layer: qkv = rms_norm(x) W_qkv^T (gemv_fused); the attention block
+//       (decode_attention_block: qk-norm, RoPE, K/V cache write at p, attention over rows [0, p],
+//       o_proj, residual add); a = silu * mul of rms_norm(x) through the gate/up weight
+//       (gemv_swiglu); x += a W_down^T (gemv_fused)
+//     logits = rms_norm(x) E^T; token = argmax (lowest index); greedy_advance moves p on.
+
+const fs = require('fs');
+
+export interface Qwen3Config {
+  vocabSize: number;
+  hiddenSize: number;
+  intermediateSize: number;
+  numHiddenLayers: number;
+  numAttentionHeads: number;
+  numKeyValueHeads: number;
+  headDim: number;
+  rmsNormEps: number;
+  ropeTheta: number;
+}
+
+export interface SafeTensor {
+  dtype: string;
+  shape: number[];
+  bytes: Buffer;
+}
+
+// A .safetensors file: an 8-byte little-endian header length n, n bytes of JSON mapping each tensor
+// name to {dtype, shape, data_offsets: [begin, end]} (offsets into the data after the header), then
+// the data (the format Kandle's io/safetensor/parser.ts reads).
+export function readSafetensors(file: string): { [name: string]: SafeTensor } {
+  const buf: Buffer = fs.readFileSync(file);
+  if (buf.length < 8) throw new Error(`${file}: not a safetensors file (shorter than its header length)`);
+  const n = Number(buf.readBigUInt64LE(0));
+  if (n <= 0 || 8 + n > buf.length) throw new Error(`${file}: header length ${n} outside the file`);
+  const header = JSON.parse(buf.slice(8, 8 + n).toString('utf8'));
+  const out: { [name: string]: SafeTensor } = {};
+  for (const name of Object.keys(header)) {
+    if (name === '__metadata__') continue;
+    const e = header[name];
+    const b = 8 + n + e.data_offsets[0];
+    const end = 8 + n + e.data_offsets[1];
+    if (end > buf.length || b > end) throw new Error(`${file}: ${name} data outside the file`);
+    out[name] = { dtype: e.dtype, shape: e.shape, bytes: buf.slice(b, end) };
+  }
+  return out;
+}
+
+// bf16 bit patterns of a BF16 tensor (copied: the file's data need not be 2-byte aligned).
+function bf16Bits(t: SafeTensor, name: string): Uint16Array {
+  if (t.dtype !== 'BF16') throw new Error(`${name}: BF16 expected, the file holds ${t.dtype}`);
+  const ab = t.bytes.buffer.slice(t.bytes.byteOffset, t.bytes.byteOffset + t.bytes.length);
+  return new Uint16Array(ab);
+}
+
+function concatRows(parts: Uint16Array[]): Uint16Array {
+  const out = new Uint16Array(parts.reduce((s: number, p: Uint16Array) => s + p.length, 0));
+  let off = 0;
+  for (const p of parts) {
+    out.set(p, off);
+    off += p.length;
+  }
+  return out;
+}
+
+// The gate/up weight of the fused SwiGLU kernels: rows 16i .. 16i + 7 are gate rows 8i .. 8i + 7 and
+// rows 16i + 8 .. 16i + 15 the matching up rows (gate and up [I, H], I % 8 == 0).
+function interleaveGateUp(gate: Uint16Array, up: Uint16Array, I: number, H: number): Uint16Array {
+  if (I % 8 !== 0) throw new Error('interleaveGateUp: the intermediate size must be a multiple of 8');
+  const out = new Uint16Array(2 * I * H);
+  for (let blk = 0; blk < I / 8; ++blk) {
+    out.set(gate.subarray(8 * blk * H, 8 * (blk + 1) * H), 16 * blk * H);
+    out.set(up.subarray(8 * blk * H, 8 * (blk + 1) * H), (16 * blk + 8) * H);
+  }
+  return out;
+}
+
+interface Layer {
+  inNorm: any;
+  wQkv: any;
+  qNorm: any;
+  kNorm: any;
+  wO: any;
+  postNorm: any;
+  wGu: any;
+  wDown: any;
+  kCache: any;
+  vCache: any;
+}
+
+export class Qwen3ForCausalLM {
+  cfg: Qwen3Config;
+  backend: any;
+  ops: any;
+  maxSeqLen: number;
+  embed: any;
+  finalNorm: any;
+  invFreq: any;
+  invFreqHost: Float32Array;
+  layers: Layer[] = [];
+  scale: number;
+
+  // weights: Hugging Face tensor names -> bf16 bit patterns (tied embeddings: the lm_head is the
+  // embedding matrix, for_causal_lm.ts:121-125).
+  constructor(backend: any, cfg: Qwen3Config, weights: { [name: string]: Uint16Array }, maxSeqLen: number) {
+    this.cfg = cfg;
+    this.backend = backend;
+    this.ops = backend.operators;
+    this.maxSeqLen = maxSeqLen;
+    const H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
+    const up = (bits: Uint16Array, shape: number[]): any => backend.createTensorHandle({ shape, dtype: 'bfloat16', data: bits });
+    const w = (name: string): Uint16Array => {
+      const bits = weights[name];
+      if (bits === undefined) throw new Error(`Qwen3ForCausalLM: missing weight ${name}`);
+      return bits;
+    };
+    this.embed = up(w('model.embed_tokens.weight'), [cfg.vocabSize, H]);
+    this.finalNorm = up(w('model.norm.weight'), [H]);
+    const nq = cfg.numAttentionHeads * D, nkv = cfg.numKeyValueHeads * D;
+    for (let i = 0; i < cfg.numHiddenLayers; ++i) {
+      const p = `model.layers.${i}.`;
+      const cacheShape = [1, cfg.numKeyValueHeads, maxSeqLen, D];
+      this.layers.push({
+        inNorm: up(w(p + 'input_layernorm.weight'), [H]),
+        wQkv: up(concatRows([w(p + 'self_attn.q_proj.weight'), w(p + 'self_attn.k_proj.weight'),
+                             w(p + 'self_attn.v_proj.weight')]), [nq + 2 * nkv, H]),
+        qNorm: up(w(p + 'self_attn.q_norm.weight'), [D]),
+        kNorm: up(w(p + 'self_attn.k_norm.weight'), [D]),
+        wO: up(w(p + 'self_attn.o_proj.weight'), [H, nq]),
+        postNorm: up(w(p + 'post_attention_layernorm.weight'), [H]),
+        wGu: up(interleaveGateUp(w(p + 'mlp.gate_proj.weight'), w(p + 'mlp.up_proj.weight'), I, H), [2 * I, H]),
+        wDown: up(w(p + 'mlp.down_proj.weight'), [H, I]),
+        kCache: backend.createTensorHandle(cacheShape, 'bfloat16'),
+        vCache: backend.createTensorHandle(cacheShape, 'bfloat16'),
+      });
+      // zero-filled as StaticKVCache's (kv-cache.ts:106-131): the decode block reads the row it is
+      // about to write with a zero weight, which must not meet a NaN bit pattern
+      const last = this.layers[this.layers.length - 1];
+      this.ops.find('zeros')(last.kCache);
+      this.ops.find('zeros')(last.vCache);
+    }
+    // RotaryEmbedding._computeInvFreqDirect (rope.ts:159-171): 1 / theta^(i / (D/2)) in float64,
+    // stored as float32.
+    const half = D / 2;
+    this.invFreqHost = new Float32Array(half);
+    for (let i = 0; i < half; ++i) this.invFreqHost[i] = 1 / Math.pow(cfg.ropeTheta, i / half);
+    this.invFreq = backend.createTensorHandle({ shape: [half], dtype: 'float32', data: this.invFreqHost });
+    this.scale = 1 / Math.sqrt(D);
+  }
+
+  static fromSafetensors(backend: any, cfg: Qwen3Config, file: string, maxSeqLen: number): Qwen3ForCausalLM {
+    const tensors = readSafetensors(file);
+    const weights: { [name: string]: Uint16Array } = {};
+    for (const name of Object.keys(tensors)) weights[name] = bf16Bits(tensors[name], name);
+    return new Qwen3ForCausalLM(backend, cfg, weights, maxSeqLen);
+  }
+
+  private view(base: any, shape: number[], strides: number[], offset: number): any {
+    return this.backend.createTensorHandle({ storage: base.storage, shape, dtype: base.dtype, strides, offset });
+  }
+
+  // fp32 logits [1, vocab] of the last of the S prompt tokens, written at cache rows [0, S).
+  prefill(promptIds: number[]): any {
+    const cfg = this.cfg, ops = this.ops, be = this.backend;
+    const S = promptIds.length, H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
+    const Hq = cfg.numAttentionHeads, Hkv = cfg.numKeyValueHeads, eps = cfg.rmsNormEps;
+    const nq = Hq * D, nkv = Hkv * D, nqkv = nq + 2 * nkv;
+    if (S < 1 || S > this.maxSeqLen) throw new Error(`prefill: ${S} tokens for a cache of ${this.maxSeqLen}`);
+    const ids = be.createTensorHandle({ shape: [S], dtype: 'int32', data: Int32Array.from(promptIds) });
+    const positions = be.createTensorHandle({ shape: [S], dtype: 'int32', data: Int32Array.from(promptIds, (_: number, i: number) => i) });
+    const x = be.createTensorHandle([S, H], 'float32');
+    ops.find('index_select')(this.embed, ids, { dim: 0 }, x);
+    let h = ops.find('rms_norm')([x], { normalizedShape: [H], eps, weight: this.layers[0].inNorm, outDtype: 'bfloat16' });
+    for (let li = 0; li < this.layers.length; ++li) {
+      const L = this.layers[li];
+      const qkv = be.createTensorHandle([S, nqkv], 'bfloat16');
+      ops.find('matmul')({ output: qkv, M: S, K: H, N: nqkv, batchSize: 1, transposeA: false, transposeB: true,
+                           alpha: 1, beta: 0 }, h, L.wQkv);
+      h.dispose();
+      const heads = (col0: number, nh: number): any => this.view(qkv, [1, S, nh, D], [S * nqkv, nqkv, D, 1], col0);
+      const q = heads(0, Hq), k = heads(nq, Hkv), v = heads(nq + nkv, Hkv);
+      const qh = be.createTensorHandle([1, Hq, S, D], 'bfloat16');
+      ops.find('rms_norm_rope')(q, k, { qWeight: L.qNorm, kWeight: L.kNorm, invFreq: this.invFreq, positions, eps,
+                                        qOut: qh, kOut: L.kCache, v, vOut: L.vCache, cachePositions: true });
+      for (const t of [q, k, v, qkv]) t.dispose();
+      // attention into [1, Hq, S, D] viewed over an [S, Hq D] buffer that o_proj reads as a matrix
+      const attn = be.createTensorHandle([S, nq], 'bfloat16');
+      const attnView = this.view(attn, [1, Hq, S, D], [S * nq, D, nq, 1], 0);
+      const kc = this.view(L.kCache, [1, Hkv, S, D], L.kCache.strides, 0);
+      const vc = this.view(L.vCache, [1, Hkv, S, D], L.vCache.strides, 0);
+      ops.find('flash_attention')(qh, kc, vc, attnView, this.scale, S > 1);
+      for (const t of [attnView, kc, vc, qh]) t.dispose();
+      const h2 = be.createTensorHandle([S, H], 'bfloat16');
+      ops.find('linear_add_rms_norm')(attn, L.wO, x, L.postNorm, eps, h2);
+      attn.dispose();
+      const a = be.createTensorHandle([S, I], 'bfloat16');
+      ops.find('linear_swiglu')(h2, L.wGu, a);
+      h2.dispose();
+      if (li + 1 < this.layers.length) {
+        h = be.createTensorHandle([S, H], 'bfloat16');
+        ops.find('linear_add_rms_norm')(a, L.wDown, x, this.layers[li + 1].inNorm, eps, h);
+      } else {
+        h = be.createTensorHandle([1, H], 'bfloat16');
+        ops.find('linear_add_rms_norm')(a, L.wDown, x, this.finalNorm, eps, h, [S - 1, S]);
+      }
+      a.dispose();
+    }
+    const logits = be.createTensorHandle([1, cfg.vocabSize], 'float32');
+    ops.find('matmul')({ output: logits, M: 1, K: H, N: cfg.vocabSize, batchSize: 1, transposeA: false,
+                         transposeB: true, alpha: 1, beta: 0 }, h, this.embed);
+    for (const t of [h, x, ids, positions]) t.dispose();
+    return logits;
+  }
+
+  // One greedy step on device state: logits of token[0] at position pos[0] (its K/V row written
+  // there), then token = argmax and greedy_advance (log[pos + 1 - base] = token, pos += 1).
+  decodeStep(token: any, pos: any, lens: any, log: any, base: number): any {
+    const cfg = this.cfg, ops = this.ops, be = this.backend;
+    const H = cfg.hiddenSize, I = cfg.intermediateSize, eps = cfg.rmsNormEps;
+    const nqkv = (cfg.numAttentionHeads + 2 * cfg.numKeyValueHeads) * cfg.headDim;
+    const x = be.createTensorHandle([1, H], 'float32');
+    ops.find('index_select')(this.embed, token, { dim: 0 }, x);
+    for (const L of this.layers) {
+      const qkv = be.createTensorHandle([1, nqkv], 'bfloat16');
+      ops.find('gemv_fused')('rms_norm', x, L.wQkv, qkv, { normWeight: L.inNorm, eps });
+      ops.find('decode_attention_block')(qkv, { qNorm: L.qNorm, kNorm: L.kNorm, invFreq: this.invFreq, eps,
+                                                position: pos, kCache: L.kCache, vCache: L.vCache, wO: L.wO, x,
+                                                scale: this.scale });
+      qkv.dispose();
+      const a = be.createTensorHandle([1, I], 'bfloat16');
+      ops.find('gemv_swiglu')('rms_norm', x, L.wGu, a, { normWeight: L.postNorm, eps });
+      ops.find('gemv_fused')('none', a, L.wDown, x, { cin: x });
+      a.dispose();
+    }
+    const logits = be.createTensorHandle([1, cfg.vocabSize], 'float32');
+    ops.find('gemv_fused')('rms_norm', x, this.embed, logits, { normWeight: this.finalNorm, eps });
+    x.dispose();
+    ops.find('argmax')(logits, token);
+    ops.find('greedy_advance')(token, pos, lens, log, base);
+    return logits;
+  }
+
+  // Greedy generation (generateWithKVCache, for_causal_lm.ts:475-508): maxNewTokens token ids, each
+  // the argmax of the previous logits, after maxNewTokens one-token forwards; returns the ids and
+  // the fp32 logits of every forward (the prefill's last position, then each decode step).
+  async generate(promptIds: number[], maxNewTokens: number): Promise<{ tokens: number[]; logits: Float32Array[] }> {
+    const be = this.backend, P = promptIds.length, N = maxNewTokens;
+    if (P + N > this.maxSeqLen) throw new Error(`generate: ${P} + ${N} positions for a cache of ${this.maxSeqLen}`);
+    const logits: Float32Array[] = [];
+    const first = this.prefill(promptIds);
+    logits.push((await first.dataAsync()) as Float32Array);
+    const token = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array(1) });
+    const log = be.createTensorHandle({ shape: [N + 1], dtype: 'int32', data: new Int32Array(N + 1) });
+    this.ops.find('argmax')(first, token);
+    first.dispose();
+    const head = this.view(log, [1], [1], 0);
+    this.ops.find('copy_')(head, token);
+    head.dispose();
+    const pos = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P]) });
+    const lens = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P + 1]) });
+    for (let i = 0; i < N; ++i) {
+      const lg = this.decodeStep(token, pos, lens, log, P);
+      logits.push((await lg.dataAsync()) as Float32Array);
+      lg.dispose();
+    }
+    const tokens = Array.from((await log.dataAsync()) as Int32Array).slice(0, N);
+    for (const t of [token, log, pos, lens]) t.dispose();
+    return { tokens, logits };
+  }
+
+  dispose(): void {
+    for (const L of this.layers) {
+      for (const t of [L.inNorm, L.wQkv, L.qNorm, L.kNorm, L.wO, L.postNorm, L.wGu, L.wDown, L.kCache, L.vCache]) {
+        t.dispose();
+      }
+    }
+    for (const t of [this.embed, this.finalNorm, this.invFreq]) t.dispose();
+    this.layers = [];
+  }
+}

@@ -157,9 +157,12 @@ function stripExpr(t) {
     // class fields at line start: `  name?: T` followed by = or ;
     m = /^\n(\s+)([A-Za-z_$][\w$]*)\??:\s/.exec(t.slice(i));
     if (m) {
-      const e = typeEnd(t, i + m[0].length - 1);
-      const after = skipSpace(t, e);
-      if (t[after] === ';' || t[after] === '=') { out += `\n${m[1]}${m[2]}`; i = e; continue; }
+      // (an object literal continued on a new line, `  key: 1, ...`, is not a field: its value
+      // does not parse as a type followed by ; or =)
+      let e = -1;
+      try { e = typeEnd(t, i + m[0].length - 1); } catch (err) { e = -1; }
+      const after = e < 0 ? -1 : skipSpace(t, e);
+      if (e >= 0 && (t[after] === ';' || t[after] === '=')) { out += `\n${m[1]}${m[2]}`; i = e; continue; }
     }
     // type arguments `name<...>(`
     if (t[i] === '<' && /[\w$]/.test(t[i - 1] || '') && t[i - 1] !== ' ') {

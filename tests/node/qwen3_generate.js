@@ -1,0 +1,38 @@
+'use strict';
+/*
+ * qwen3_generate.js — greedy generation with the TypeScript Qwen3 model (packages/backend-hip/src/
+ * qwen3.ts, stripped into dist/qwen3.js) on the HIP backend.  Test infrastructure:
+ * tests/test_gpu_node_qwen3.py writes the checkpoint and compares the results with the Python model.
+ *
+ * Usage: node qwen3_generate.js DIR
+ *   DIR/meta.json {cfg, prompt, n, maxSeq} and DIR/model.safetensors (bf16); writes DIR/logits.f32
+ *   ((n + 1) rows of vocab fp32 logits) and DIR/inv_freq.f32, and prints a JSON summary.
+ */
+const fs = require('fs');
+const path = require('path');
+const dist = path.join(__dirname, '..', '..', 'packages', 'backend-hip', 'dist');
+const { HipBackend } = require(path.join(dist, 'index.js'));
+const { Qwen3ForCausalLM } = require(path.join(dist, 'qwen3.js'));
+
+async function main() {
+  const dir = process.argv[2];
+  const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
+  const backend = await HipBackend.create(0);
+  const before = backend.memoryStats().liveBytes;
+  const model = Qwen3ForCausalLM.fromSafetensors(backend, meta.cfg, path.join(dir, 'model.safetensors'), meta.maxSeq);
+  const res = await model.generate(meta.prompt, meta.n);
+  const V = meta.cfg.vocabSize;
+  const all = new Float32Array(res.logits.length * V);
+  res.logits.forEach((row, i) => all.set(row, i * V));
+  fs.writeFileSync(path.join(dir, 'logits.f32'), Buffer.from(all.buffer));
+  fs.writeFileSync(path.join(dir, 'inv_freq.f32'), Buffer.from(model.invFreqHost.buffer));
+  model.dispose();
+  backend.synchronize();
+  console.log(JSON.stringify({ tokens: res.tokens, rows: res.logits.length, liveBefore: before,
+                               liveAfter: backend.memoryStats().liveBytes }));
+}
+
+main().catch((err) => {
+  console.error(err && err.stack ? err.stack : err);
+  process.exit(1);
+});

@@ -94,6 +94,11 @@ export function pick(flag: boolean, a?: number, ...rest: number[]): number | und
   return t.length > 100 ? undefined : v + obj.x;
 }
 export const twice = (x: number): number => x * 2;
+export function wrapped(n: number): number {
+  const o = { first: n, second: 2,
+              third: 3 };
+  return o.first + o.second + o.third;
+}
 function lessThan(a: number, b: number): boolean { return a < b && b > a; }
 export { lessThan };
 '''
@@ -114,9 +119,40 @@ def test_type_stripper_handles_each_construct(tmp_path):
       c.add(); c.add(4);
       console.log(JSON.stringify({{total: c.total, name: c.name, size: c.items.size,
                                   p1: m.pick(true, 7), p2: m.pick(false), p3: m.pick(true, 1, 2, 3),
-                                  tw: m.twice(21), lt: m.lessThan(1, 2), keys: Object.keys(m).sort()}}));"""
+                                  tw: m.twice(21), lt: m.lessThan(1, 2), wr: m.wrapped(1),
+                                  keys: Object.keys(m).sort()}}));"""
     res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, (res.stderr, js)
     r = json.loads(res.stdout.strip().splitlines()[-1])
-    assert r == {"total": 5, "name": "k", "size": 0, "p1": 8, "p2": 4, "p3": 5, "tw": 42, "lt": True,
-                 "keys": ["Counter", "lessThan", "pick", "twice"]}
+    assert r == {"total": 5, "name": "k", "size": 0, "p1": 8, "p2": 4, "p3": 5, "tw": 42, "lt": True, "wr": 6,
+                 "keys": ["Counter", "lessThan", "pick", "twice", "wrapped"]}
+
+
+def test_typescript_safetensors_reader(tmp_path):
+    """qwen3.ts's readSafetensors on a file the safetensors package wrote: names, dtypes, shapes and
+    the bytes of every tensor; a truncated file is rejected."""
+    _need_node()
+    import numpy as np
+    torch = pytest.importorskip("torch")
+    from safetensors.torch import save_file
+
+    a = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    b = (np.arange(10, dtype=np.int16) * 37).reshape(5, 2)
+    save_file({"a.weight": torch.from_numpy(a), "b": torch.from_numpy(b).view(torch.bfloat16)},
+              str(tmp_path / "m.safetensors"), metadata={"format": "pt"})
+    (tmp_path / "bad.safetensors").write_bytes((tmp_path / "m.safetensors").read_bytes()[:40])
+    script = f"""
+      const m = require({json.dumps(os.path.join(PKG, 'dist', 'qwen3.js'))});
+      const t = m.readSafetensors({json.dumps(str(tmp_path / 'm.safetensors'))});
+      const out = {{}};
+      for (const k of Object.keys(t)) out[k] = [t[k].dtype, t[k].shape, Array.from(t[k].bytes)];
+      let err = null;
+      try {{ m.readSafetensors({json.dumps(str(tmp_path / 'bad.safetensors'))}); }} catch (e) {{ err = e.message; }}
+      console.log(JSON.stringify({{t: out, err}}));"""
+    res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stderr
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    assert sorted(r["t"]) == ["a.weight", "b"]
+    assert r["t"]["a.weight"][:2] == ["F32", [2, 3, 4]] and bytes(r["t"]["a.weight"][2]) == a.tobytes()
+    assert r["t"]["b"][:2] == ["BF16", [5, 2]] and bytes(r["t"]["b"][2]) == b.tobytes()
+    assert r["err"] is not None and "outside the file" in r["err"]
