@@ -719,6 +719,24 @@ export class HipBackend {
     addon.synchronize();
   }
 
+  // HIP graphs of library launches: between graphBegin() and graphEnd() kernels are recorded instead
+  // of run (allocations made meanwhile belong to the graph until graphDestroy); graphLaunch replays.
+  graphBegin(): void {
+    addon.graphBeginCapture();
+  }
+
+  graphEnd(): bigint {
+    return addon.graphEndCapture() as bigint;
+  }
+
+  graphLaunch(graph: bigint): void {
+    addon.graphLaunch(graph);
+  }
+
+  graphDestroy(graph: bigint): void {
+    addon.graphDestroy(graph);
+  }
+
   memoryStats(): { [key: string]: number } {
     return addon.allocStats();
   }

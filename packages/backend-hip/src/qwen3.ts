@@ -256,14 +256,22 @@ export class Qwen3ForCausalLM {
   }
 
   // Greedy generation (generateWithKVCache, for_causal_lm.ts:475-508): maxNewTokens token ids, each
-  // the argmax of the previous logits, after maxNewTokens one-token forwards; returns the ids and
-  // the fp32 logits of every forward (the prefill's last position, then each decode step).
-  async generate(promptIds: number[], maxNewTokens: number): Promise<{ tokens: number[]; logits: Float32Array[] }> {
+  // the argmax of the previous logits, after maxNewTokens one-token forwards; returns the ids, the
+  // fp32 logits of every forward (the prefill's last position, then each decode step) unless
+  // returnLogits is false, and the wall times.  With useGraph the first decode step runs eagerly
+  // and the step is then captured once as a HIP graph and replayed (every value that changes from
+  // step to step lives in device memory), as the Python model does.
+  async generate(promptIds: number[], maxNewTokens: number, options?: { [key: string]: any }):
+      Promise<{ tokens: number[]; logits: Float32Array[]; prefillMs: number; decodeMs: number; replayMs: number }> {
+    const opt = options || {};
+    const useGraph = !!opt.useGraph;
+    const returnLogits = opt.returnLogits === undefined ? true : !!opt.returnLogits;
     const be = this.backend, P = promptIds.length, N = maxNewTokens;
     if (P + N > this.maxSeqLen) throw new Error(`generate: ${P} + ${N} positions for a cache of ${this.maxSeqLen}`);
     const logits: Float32Array[] = [];
+    const t0 = Date.now();
     const first = this.prefill(promptIds);
-    logits.push((await first.dataAsync()) as Float32Array);
+    if (returnLogits) logits.push((await first.dataAsync()) as Float32Array);
     const token = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array(1) });
     const log = be.createTensorHandle({ shape: [N + 1], dtype: 'int32', data: new Int32Array(N + 1) });
     this.ops.find('argmax')(first, token);
@@ -273,14 +281,41 @@ export class Qwen3ForCausalLM {
     head.dispose();
     const pos = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P]) });
     const lens = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P + 1]) });
-    for (let i = 0; i < N; ++i) {
-      const lg = this.decodeStep(token, pos, lens, log, P);
-      logits.push((await lg.dataAsync()) as Float32Array);
-      lg.dispose();
+    be.synchronize();
+    const t1 = Date.now();
+    let t2 = t1;
+    let graph: bigint | null = null;
+    let gLogits: any = null;
+    let tokens: number[] = [];
+    try {
+      for (let i = 0; i < N; ++i) {
+        if (!useGraph || i === 0) {
+          const lg = this.decodeStep(token, pos, lens, log, P);
+          if (returnLogits) logits.push((await lg.dataAsync()) as Float32Array);
+          lg.dispose();
+          if (useGraph && N > 1) {
+            be.graphBegin();
+            try {
+              gLogits = this.decodeStep(token, pos, lens, log, P);   // recorded, not run
+            } finally {
+              graph = be.graphEnd();
+            }
+            be.synchronize();
+            t2 = Date.now();
+          }
+        } else {
+          be.graphLaunch(graph as bigint);
+          if (returnLogits) logits.push((await gLogits.dataAsync()) as Float32Array);
+        }
+      }
+      tokens = Array.from((await log.dataAsync()) as Int32Array).slice(0, N);
+    } finally {
+      if (gLogits !== null) gLogits.dispose();
+      if (graph !== null) be.graphDestroy(graph);
+      for (const t of [token, log, pos, lens]) t.dispose();
     }
-    const tokens = Array.from((await log.dataAsync()) as Int32Array).slice(0, N);
-    for (const t of [token, log, pos, lens]) t.dispose();
-    return { tokens, logits };
+    const t3 = Date.now();
+    return { tokens, logits, prefillMs: t1 - t0, decodeMs: t3 - t1, replayMs: useGraph && N > 1 ? t3 - t2 : 0 };
   }
 
   dispose(): void {

@@ -5,8 +5,9 @@
  * tests/test_gpu_node_qwen3.py writes the checkpoint and compares the results with the Python model.
  *
  * Usage: node qwen3_generate.js DIR
- *   DIR/meta.json {cfg, prompt, n, maxSeq} and DIR/model.safetensors (bf16); writes DIR/logits.f32
- *   ((n + 1) rows of vocab fp32 logits) and DIR/inv_freq.f32, and prints a JSON summary.
+ *   DIR/meta.json {cfg, prompt, n, maxSeq} and DIR/model.safetensors (bf16); generates eagerly and
+ *   then with HIP-graph replay of the decode step, writes DIR/logits.f32 and DIR/logits_graph.f32
+ *   ((n + 1) rows of vocab fp32 logits each) and DIR/inv_freq.f32, and prints a JSON summary.
  */
 const fs = require('fs');
 const path = require('path');
@@ -20,15 +21,22 @@ async function main() {
   const backend = await HipBackend.create(0);
   const before = backend.memoryStats().liveBytes;
   const model = Qwen3ForCausalLM.fromSafetensors(backend, meta.cfg, path.join(dir, 'model.safetensors'), meta.maxSeq);
-  const res = await model.generate(meta.prompt, meta.n);
   const V = meta.cfg.vocabSize;
-  const all = new Float32Array(res.logits.length * V);
-  res.logits.forEach((row, i) => all.set(row, i * V));
-  fs.writeFileSync(path.join(dir, 'logits.f32'), Buffer.from(all.buffer));
+  const save = (name, rows) => {
+    const all = new Float32Array(rows.length * V);
+    rows.forEach((row, i) => all.set(row, i * V));
+    fs.writeFileSync(path.join(dir, name), Buffer.from(all.buffer));
+  };
+  const res = await model.generate(meta.prompt, meta.n);
+  save('logits.f32', res.logits);
+  // the same generation with the decode step captured once and replayed as a HIP graph
+  const resG = await model.generate(meta.prompt, meta.n, { useGraph: true });
+  save('logits_graph.f32', resG.logits);
   fs.writeFileSync(path.join(dir, 'inv_freq.f32'), Buffer.from(model.invFreqHost.buffer));
   model.dispose();
   backend.synchronize();
-  console.log(JSON.stringify({ tokens: res.tokens, rows: res.logits.length, liveBefore: before,
+  console.log(JSON.stringify({ tokens: res.tokens, tokensGraph: resG.tokens, rows: res.logits.length,
+                               rowsGraph: resG.logits.length, replayMs: resG.replayMs, liveBefore: before,
                                liveAfter: backend.memoryStats().liveBytes }));
 }
 

@@ -1,10 +1,11 @@
 """The TypeScript Qwen3 model (packages/backend-hip/src/qwen3.ts) generating from Node: a 2-layer
 Qwen3 with the 0.6B's layer shapes (hidden 1024, 16/8 heads of 128, MLP 3072; vocab 4096) is written
 as a bf16 safetensors checkpoint; tests/node/qwen3_generate.js reads it, runs the prefill of a
-40-token prompt and 8 greedy decode steps through the backend's registry kernels, and writes every
-forward's logits.  The Python model (kandle_amd.model_utils.qwen3) on the same weights must give the
-same tokens and the same logits bit for bit -- both hosts issue the same launches -- and the same
-RoPE inverse frequencies; every device byte the TS model allocated is returned."""
+40-token prompt and 8 greedy decode steps through the backend's registry kernels and writes every
+forward's logits, then generates again with the decode step captured as a HIP graph and replayed.
+The Python model (kandle_amd.model_utils.qwen3) on the same weights must give the same tokens and
+the same logits bit for bit -- both hosts issue the same launches, eagerly or replayed -- and the
+same RoPE inverse frequencies; every device byte the TS model allocated is returned."""
 import json
 import os
 import shutil
@@ -70,3 +71,7 @@ def test_typescript_qwen3_generation_matches_python_model(hip, tmp_path):
     assert res["tokens"] == list(toks)
     assert np.all(np.isfinite(ts_logits))
     np.testing.assert_array_equal(ts_logits, np.stack(logits))
+    # graph replay of the decode step issues the same launches: identical tokens and logits
+    assert res["tokensGraph"] == list(toks) and res["rowsGraph"] == N + 1
+    np.testing.assert_array_equal(
+        np.fromfile(str(tmp_path / "logits_graph.f32"), np.float32).reshape(N + 1, cfg.vocab_size), ts_logits)
