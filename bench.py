@@ -366,11 +366,12 @@ GEMM_SHAPES = (("qkv", 4096, 1024, "bf16"), ("o_proj", 1024, 2048, "f32"), ("gat
                ("down", 1024, 3072, "f32"))
 
 
-def bench_gemm(steps, warmup, M=512):
+def bench_gemm(steps, warmup, M=512, eager=False):
     """The four projection GEMMs of a C5 prefill layer (M = 512 tokens, bf16 weights [N, K], fp32
     accumulate): y = x W^T, bf16 out for qkv and gate/up, fp32 out plus the fp32 residual (beta = 1)
     for o_proj and down, as in the model.  Per shape: kh_gemm device time (calls replayed from a
-    graph, as the model's prefill runs them) and TFLOP/s."""
+    graph, as the model's prefill runs them; with eager, launched one by one from the host, the form
+    a kernel tracer or counter run takes) and TFLOP/s."""
     import ctypes as C
 
     from kandle_amd import Tensor, _lib
@@ -393,13 +394,16 @@ def bench_gemm(steps, warmup, M=512):
         from kandle_amd.graphs import HipGraph
 
         call()
-        g = HipGraph()
-        with g.capture():
-            for _ in range(20):
-                call()
-        wall, dev = time_calls(g.replay, max(1, steps // 4), warmup)
-        g.dispose()
-        dev /= 20.0
+        if eager:
+            wall, dev = time_calls(call, steps, warmup)
+        else:
+            g = HipGraph()
+            with g.capture():
+                for _ in range(20):
+                    call()
+            wall, dev = time_calls(g.replay, max(1, steps // 4), warmup)
+            g.dispose()
+            dev /= 20.0
         flops = 2.0 * M * N * K
         out[name] = {"M": M, "N": N, "K": K, "us": round(dev * 1e3, 2),
                      "TFLOP/s": round(flops / (dev * 1e-3) / 1e12, 1)}
@@ -807,6 +811,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
+    ap.add_argument("--eager-gemm", action="store_true",
+                    help="--only gemm: launch each GEMM from the host instead of replaying a HIP graph")
     ap.add_argument("--only", choices=["prefill", "c1", "decode", "norm", "model", "copy", "load", "sample", "stream",
                                        "gemm", "gemv", "vendor", "mask"], default=None)
     args = ap.parse_args()
@@ -878,7 +884,7 @@ def main():
         res["stream"] = bench_stream()
     if args.only == "gemm":
         log("C5 prefill GEMMs ...")
-        res["gemm"] = bench_gemm(args.steps, args.warmup)
+        res["gemm"] = bench_gemm(args.steps, args.warmup, eager=args.eager_gemm)
     if args.only == "gemv":
         log("C5 decode GEMVs ...")
         res["gemv"] = bench_gemv(args.steps, args.warmup)
