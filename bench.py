@@ -252,7 +252,62 @@ def prep_norm_rope():
     return run
 
 
-def prep_model(new_tokens=128, prompt_len=512, use_graph=True):
+TS_EXAMPLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "packages", "backend-hip", "examples",
+                          "generate.js")
+
+
+def _ts_host_ready():
+    """Node, the built N-API addon and the stripped TypeScript model are all present."""
+    import shutil
+
+    pkg = os.path.dirname(os.path.dirname(TS_EXAMPLE))
+    return (shutil.which("node") is not None and os.path.exists(os.path.join(pkg, "native", "kandle_hip.node"))
+            and all(os.path.exists(os.path.join(pkg, "dist", m + ".js")) for m in ("index", "qwen3")))
+
+
+def _write_ts_inputs(cfg, weights, prompt):
+    """The C5 weights, a Hugging Face style config and the prompt ids in a temporary directory, the
+    input of packages/backend-hip/examples/generate.js."""
+    import tempfile
+
+    from kandle_amd.io import save_safetensors
+
+    d = tempfile.mkdtemp(prefix="kandle_c5_")
+    save_safetensors(os.path.join(d, "model.safetensors"), weights)
+    hf = {"vocab_size": cfg.vocab_size, "hidden_size": cfg.hidden_size, "intermediate_size": cfg.intermediate_size,
+          "num_hidden_layers": cfg.num_hidden_layers, "num_attention_heads": cfg.num_attention_heads,
+          "num_key_value_heads": cfg.num_key_value_heads, "head_dim": cfg.head_dim, "rms_norm_eps": cfg.rms_norm_eps,
+          "rope_theta": cfg.rope_theta, "tie_word_embeddings": True}
+    with open(os.path.join(d, "config.json"), "w") as f:
+        json.dump(hf, f)
+    with open(os.path.join(d, "prompt.json"), "w") as f:
+        json.dump([int(t) for t in prompt], f)
+    return d
+
+
+def _run_ts_host(d, new_tokens, py_tokens):
+    """C5 generation driven from Node through the TypeScript model and the N-API addon: one warm-up
+    generation of 8 tokens (captures the prefill and decode graphs), then the timed one.  Its tokens
+    must equal the Python host's."""
+    import shutil
+    import subprocess
+
+    try:
+        out = subprocess.run(["node", TS_EXAMPLE, os.path.join(d, "config.json"), os.path.join(d, "model.safetensors"),
+                              os.path.join(d, "prompt.json"), str(new_tokens)], capture_output=True, text=True,
+                             timeout=300)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    if out.returncode != 0:
+        raise RuntimeError(f"TypeScript host generation failed: {out.stderr[-2000:]}")
+    r = json.loads(out.stdout.strip().splitlines()[-1])
+    toks = r.pop("tokens")
+    r["tokens_match_python_host"] = toks == [int(t) for t in py_tokens]
+    r["first_tokens"] = toks[:8]
+    return r
+
+
+def prep_model(new_tokens=128, prompt_len=512, use_graph=True, ts_host=False):
     """Config C5: Qwen3-0.6B architecture, random N(0, 0.02) bf16 weights, a 512-token prefill of
     uniform-random ids, then 128 greedy decode steps (the decode step captured once as a HIP graph
     and replayed).  One warm-up generation of 8 tokens precedes the timed one; it runs the prefill
@@ -267,6 +322,7 @@ def prep_model(new_tokens=128, prompt_len=512, use_graph=True):
     log(f"model weights generated in {time.perf_counter() - t0:.1f} s")
     prompt = syn.randint(8, (prompt_len,), 0, cfg.vocab_size)
     model = Qwen3ForCausalLM(cfg, w, max_seq_len=prompt_len + new_tokens)
+    ts_dir = _write_ts_inputs(cfg, w, prompt) if ts_host else None
     del w
 
     def run(steps, warmup):
@@ -277,6 +333,7 @@ def prep_model(new_tokens=128, prompt_len=512, use_graph=True):
         if not use_graph:  # every step eager: time all of them
             timing["replay_ms"], timing["replay_steps"] = timing["decode_ms"], new_tokens
         model.dispose()
+        ts = _run_ts_host(ts_dir, new_tokens, toks) if ts_dir is not None else None
         H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
         Hq, Hkv, Lyr = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
         layer_w = H * (Hq + 2 * Hkv) * D + Hq * D * H + 3 * H * I            # projection weights per layer
@@ -292,7 +349,8 @@ def prep_model(new_tokens=128, prompt_len=512, use_graph=True):
         return {"prefill_ms": timing["prefill_ms"], "prefill_issue": timing["prefill_issue"],
                 "prefill_eager_ms": warm["prefill_ms"], "prefill_flops": prefill_flops, "prompt_len": prompt_len,
                 "new_tokens": new_tokens, "replay_ms": timing.get("replay_ms"), "replay_steps": steps_r,
-                "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8]}
+                "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8],
+                "ts_host": ts}
     return run
 
 
@@ -811,6 +869,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="C5: issue every decode step's kernels from the host instead of replaying a HIP graph")
+    ap.add_argument("--no-ts-host", action="store_true",
+                    help="C5: skip the generation driven from Node through the TypeScript model")
     ap.add_argument("--eager-gemm", action="store_true",
                     help="--only gemm: launch each GEMM from the host instead of replaying a HIP graph")
     ap.add_argument("--only", choices=["prefill", "c1", "decode", "norm", "model", "copy", "load", "sample", "stream",
@@ -835,7 +895,12 @@ def main():
     legs = []
     if args.only in (None, "model"):
         log("C5 model weights ...")
-        legs.append(("model", "Qwen3-0.6B C5", prep_model(use_graph=not args.eager_decode)))
+        ts_host = not args.no_ts_host and _ts_host_ready()
+        if not ts_host:
+            log("C5 from the TypeScript host: skipped (" + ("--no-ts-host" if args.no_ts_host else
+                "node, the N-API addon or the stripped TypeScript is missing: run __graft_entry__.build()") + ")")
+        legs.append(("model", "Qwen3-0.6B C5", prep_model(use_graph=not args.eager_decode,
+                                                          ts_host=ts_host and not args.eager_decode)))
     if args.only in (None, "decode"):
         legs.append(("decode", "decode C4", prep_decode()))
     if args.only in (None, "norm"):
@@ -972,6 +1037,16 @@ def main():
             "decode_issue": "eager" if args.eager_decode else "hip graph replay",
             "prefill_issue": m["prefill_issue"], "prefill_eager_ms": round(m["prefill_eager_ms"], 3),
             "first_tokens": m["tokens"]}
+        if m.get("ts_host") is not None:
+            t = m["ts_host"]
+            line["model"]["ts_host"] = {
+                "workload": "the same generation driven from Node (packages/backend-hip/examples/generate.js: the "
+                            "TypeScript Qwen3 model over the N-API addon)",
+                "prefill_ms": round(t["prefill_ms"], 3), "prefill_issue": "hip graph replay",
+                "prefill_eager_ms": round(t["prefill_eager_ms"], 3) if t["prefill_eager_ms"] is not None else None,
+                "decode_tokens_per_s": round(t["decode_tokens_per_s"], 1), "decode_steps_timed": t["decode_steps_timed"],
+                "decode_issue": t["issue"], "load_ms": round(t["load_ms"], 1),
+                "tokens_match_python_host": t["tokens_match_python_host"], "first_tokens": t["first_tokens"]}
         if "value" not in line:
             line.update({"value": round(1e3 / d_ms, 1), "unit": "tokens/s", "ms_per_step": round(d_ms, 4),
                          "config": {"workload": "C5 Qwen3-0.6B greedy decode"}})

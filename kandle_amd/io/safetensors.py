@@ -269,3 +269,35 @@ def tensor_from_safetensor_layer(layer: SafetensorLayer, dtype: Optional[str] = 
 
     target = dtype or layer.dtype
     return Tensor(np.ascontiguousarray(host_array(layer, target)), dtype=target)
+
+
+def save_safetensors(path: str, tensors: Dict[str, np.ndarray], dtypes: Optional[Dict[str, str]] = None,
+                     metadata: Optional[Dict[str, str]] = None) -> None:
+    """Writes `tensors` (name -> host array) as one .safetensors file.  A uint16 array is stored as
+    BF16 bit patterns unless `dtypes` names another safetensors dtype for it; other arrays as their
+    own dtype (float32 -> F32, int32 -> I32, ...).  Tensors are laid out back to back in name order
+    (the format allows no gaps in the data area) after a JSON header padded with spaces to a
+    multiple of 8 bytes."""
+    by_numpy = {np.dtype(v[1]).str: k for k, v in SAFETENSORS_DTYPES.items() if k not in ("BF16", "BOOL")}
+    header: Dict[str, object] = {}
+    if metadata:
+        header["__metadata__"] = {str(k): str(v) for k, v in metadata.items()}
+    arrays = []
+    offset = 0
+    for name in sorted(tensors):
+        arr = np.ascontiguousarray(tensors[name])
+        st = (dtypes or {}).get(name) or ("BF16" if arr.dtype == np.uint16 else by_numpy.get(arr.dtype.str))
+        if st not in SAFETENSORS_DTYPES:
+            raise ValueError(f"save_safetensors: {name} has dtype {arr.dtype}, which has no safetensors dtype")
+        if arr.dtype.itemsize != SAFETENSORS_DTYPES[st][0]:
+            raise ValueError(f"save_safetensors: {name} ({arr.dtype}) does not match {st}")
+        header[name] = {"dtype": st, "shape": [int(d) for d in arr.shape], "data_offsets": [offset, offset + arr.nbytes]}
+        arrays.append(arr)
+        offset += arr.nbytes
+    text = json.dumps(header, separators=(",", ":")).encode("utf-8")
+    text += b" " * ((-len(text)) % 8)
+    with open(path, "wb") as f:
+        f.write(_LEN_FIELD.pack(len(text)))
+        f.write(text)
+        for arr in arrays:
+            f.write(arr.tobytes())

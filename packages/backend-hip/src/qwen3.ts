@@ -21,6 +21,7 @@
 //     logits = rms_norm(x) E^T; token = argmax (lowest index); greedy_advance moves p on.
 
 const fs = require('fs');
+const { performance } = require('perf_hooks');  // wall times in ms, sub-millisecond resolution
 
 export interface Qwen3Config {
   vocabSize: number;
@@ -103,6 +104,13 @@ interface Layer {
   vCache: any;
 }
 
+interface PrefillGraph {
+  graph: bigint;
+  ids: any;        // device token ids the graph reads (uploaded before each replay)
+  positions: any;  // 0 .. S-1
+  logits: any;     // fp32 [1, vocab], written by each replay
+}
+
 export class Qwen3ForCausalLM {
   cfg: Qwen3Config;
   backend: any;
@@ -114,6 +122,10 @@ export class Qwen3ForCausalLM {
   invFreqHost: Float32Array;
   layers: Layer[] = [];
   scale: number;
+  // Captured prefills by prompt length (generate with useGraph), least recently used first; at most
+  // maxPrefillGraphs are kept, each holding its activations and logits until dropped.
+  prefillGraphs: Map<number, PrefillGraph> = new Map();
+  maxPrefillGraphs: number = 4;
 
   // weights: Hugging Face tensor names -> bf16 bit patterns (tied embeddings: the lm_head is the
   // embedding matrix, for_causal_lm.ts:121-125).
@@ -176,13 +188,26 @@ export class Qwen3ForCausalLM {
 
   // fp32 logits [1, vocab] of the last of the S prompt tokens, written at cache rows [0, S).
   prefill(promptIds: number[]): any {
-    const cfg = this.cfg, ops = this.ops, be = this.backend;
-    const S = promptIds.length, H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
-    const Hq = cfg.numAttentionHeads, Hkv = cfg.numKeyValueHeads, eps = cfg.rmsNormEps;
-    const nq = Hq * D, nkv = Hkv * D, nqkv = nq + 2 * nkv;
+    const S = promptIds.length;
     if (S < 1 || S > this.maxSeqLen) throw new Error(`prefill: ${S} tokens for a cache of ${this.maxSeqLen}`);
+    const be = this.backend;
     const ids = be.createTensorHandle({ shape: [S], dtype: 'int32', data: Int32Array.from(promptIds) });
     const positions = be.createTensorHandle({ shape: [S], dtype: 'int32', data: Int32Array.from(promptIds, (_: number, i: number) => i) });
+    try {
+      return this.prefillFrom(ids, positions, S);
+    } finally {
+      ids.dispose();
+      positions.dispose();
+    }
+  }
+
+  // The prefill over device-resident token ids and positions (int32 [S]): every launch reads its
+  // inputs from device memory, so the same sequence can be captured as a graph and replayed.
+  prefillFrom(ids: any, positions: any, S: number): any {
+    const cfg = this.cfg, ops = this.ops, be = this.backend;
+    const H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
+    const Hq = cfg.numAttentionHeads, Hkv = cfg.numKeyValueHeads, eps = cfg.rmsNormEps;
+    const nq = Hq * D, nkv = Hkv * D, nqkv = nq + 2 * nkv;
     const x = be.createTensorHandle([S, H], 'float32');
     ops.find('index_select')(this.embed, ids, { dim: 0 }, x);
     let h = ops.find('rms_norm')([x], { normalizedShape: [H], eps, weight: this.layers[0].inNorm, outDtype: 'bfloat16' });
@@ -223,8 +248,55 @@ export class Qwen3ForCausalLM {
     const logits = be.createTensorHandle([1, cfg.vocabSize], 'float32');
     ops.find('matmul')({ output: logits, M: 1, K: H, N: cfg.vocabSize, batchSize: 1, transposeA: false,
                          transposeB: true, alpha: 1, beta: 0 }, h, this.embed);
-    for (const t of [h, x, ids, positions]) t.dispose();
+    for (const t of [h, x]) t.dispose();
     return logits;
+  }
+
+  // The prompt's logits and whether the caller owns (disposes) them.  With useGraph the first
+  // prompt of a given length runs eagerly and the same launches are then captured over a device ids
+  // buffer; a later prompt of that length uploads its ids and replays (the logits then belong to the
+  // graph), as the Python model does.
+  private prefillLogits(promptIds: number[], useGraph: boolean): { logits: any; owned: boolean } {
+    const S = promptIds.length, be = this.backend;
+    if (!useGraph) return { logits: this.prefill(promptIds), owned: true };
+    const entry = this.prefillGraphs.get(S);
+    if (entry !== undefined) {
+      entry.ids.upload(Int32Array.from(promptIds));
+      be.graphLaunch(entry.graph);
+      this.prefillGraphs.delete(S);  // most recently used last
+      this.prefillGraphs.set(S, entry);
+      return { logits: entry.logits, owned: false };
+    }
+    const logits = this.prefill(promptIds);
+    if (this.maxPrefillGraphs < 1) return { logits, owned: true };
+    while (this.prefillGraphs.size >= this.maxPrefillGraphs) this.dropPrefillGraph(this.prefillGraphs.keys().next().value);
+    const ids = be.createTensorHandle({ shape: [S], dtype: 'int32', data: new Int32Array(S) });
+    const positions = be.createTensorHandle({ shape: [S], dtype: 'int32', data: Int32Array.from(promptIds, (_: number, i: number) => i) });
+    let gLogits: any = null;
+    be.graphBegin();
+    try {
+      gLogits = this.prefillFrom(ids, positions, S);   // recorded, not run
+    } catch (err) {
+      try {
+        be.graphDestroy(be.graphEnd());
+      } catch (endErr) {
+        // the capture failed as a whole; nothing left to destroy
+      }
+      ids.dispose();
+      positions.dispose();
+      throw err;
+    }
+    const graph = be.graphEnd();
+    this.prefillGraphs.set(S, { graph, ids, positions, logits: gLogits });
+    return { logits, owned: true };
+  }
+
+  private dropPrefillGraph(S: number): void {
+    const e = this.prefillGraphs.get(S);
+    if (e === undefined) return;
+    this.prefillGraphs.delete(S);
+    for (const t of [e.logits, e.ids, e.positions]) t.dispose();
+    this.backend.graphDestroy(e.graph);
   }
 
   // One greedy step on device state: logits of token[0] at position pos[0] (its K/V row written
@@ -258,9 +330,10 @@ export class Qwen3ForCausalLM {
   // Greedy generation (generateWithKVCache, for_causal_lm.ts:475-508): maxNewTokens token ids, each
   // the argmax of the previous logits, after maxNewTokens one-token forwards; returns the ids, the
   // fp32 logits of every forward (the prefill's last position, then each decode step) unless
-  // returnLogits is false, and the wall times.  With useGraph the first decode step runs eagerly
-  // and the step is then captured once as a HIP graph and replayed (every value that changes from
-  // step to step lives in device memory), as the Python model does.
+  // returnLogits is false, and the wall times.  With useGraph the prefill is replayed from a graph
+  // captured for its prompt length when there is one (prefillLogits), and the first decode step runs
+  // eagerly, after which the step is captured once as a HIP graph and replayed (every value that
+  // changes from step to step lives in device memory), as the Python model does.
   async generate(promptIds: number[], maxNewTokens: number, options?: { [key: string]: any }):
       Promise<{ tokens: number[]; logits: Float32Array[]; prefillMs: number; decodeMs: number; replayMs: number }> {
     const opt = options || {};
@@ -269,20 +342,21 @@ export class Qwen3ForCausalLM {
     const be = this.backend, P = promptIds.length, N = maxNewTokens;
     if (P + N > this.maxSeqLen) throw new Error(`generate: ${P} + ${N} positions for a cache of ${this.maxSeqLen}`);
     const logits: Float32Array[] = [];
-    const t0 = Date.now();
-    const first = this.prefill(promptIds);
+    const t0 = performance.now();
+    const pre = this.prefillLogits(promptIds, useGraph);
+    const first = pre.logits;
     if (returnLogits) logits.push((await first.dataAsync()) as Float32Array);
     const token = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array(1) });
     const log = be.createTensorHandle({ shape: [N + 1], dtype: 'int32', data: new Int32Array(N + 1) });
     this.ops.find('argmax')(first, token);
-    first.dispose();
+    if (pre.owned) first.dispose();
     const head = this.view(log, [1], [1], 0);
     this.ops.find('copy_')(head, token);
     head.dispose();
     const pos = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P]) });
     const lens = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P + 1]) });
     be.synchronize();
-    const t1 = Date.now();
+    const t1 = performance.now();
     let t2 = t1;
     let graph: bigint | null = null;
     let gLogits: any = null;
@@ -301,7 +375,7 @@ export class Qwen3ForCausalLM {
               graph = be.graphEnd();
             }
             be.synchronize();
-            t2 = Date.now();
+            t2 = performance.now();
           }
         } else {
           be.graphLaunch(graph as bigint);
@@ -314,11 +388,12 @@ export class Qwen3ForCausalLM {
       if (graph !== null) be.graphDestroy(graph);
       for (const t of [token, log, pos, lens]) t.dispose();
     }
-    const t3 = Date.now();
+    const t3 = performance.now();
     return { tokens, logits, prefillMs: t1 - t0, decodeMs: t3 - t1, replayMs: useGraph && N > 1 ? t3 - t2 : 0 };
   }
 
   dispose(): void {
+    for (const S of Array.from(this.prefillGraphs.keys())) this.dropPrefillGraph(S);
     for (const L of this.layers) {
       for (const t of [L.inNorm, L.wQkv, L.qNorm, L.kNorm, L.wO, L.postNorm, L.wGu, L.wDown, L.kCache, L.vCache]) {
         t.dispose();

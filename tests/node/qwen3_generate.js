@@ -5,9 +5,10 @@
  * tests/test_gpu_node_qwen3.py writes the checkpoint and compares the results with the Python model.
  *
  * Usage: node qwen3_generate.js DIR
- *   DIR/meta.json {cfg, prompt, n, maxSeq} and DIR/model.safetensors (bf16); generates eagerly and
- *   then with HIP-graph replay of the decode step, writes DIR/logits.f32 and DIR/logits_graph.f32
- *   ((n + 1) rows of vocab fp32 logits each) and DIR/inv_freq.f32, and prints a JSON summary.
+ *   DIR/meta.json {cfg, prompt, n, maxSeq} and DIR/model.safetensors (bf16); generates eagerly, then
+ *   twice with HIP graphs (decode step replayed; the second time the prefill too), writes
+ *   DIR/logits.f32, DIR/logits_graph.f32 and DIR/logits_graph2.f32 ((n + 1) rows of vocab fp32
+ *   logits each) and DIR/inv_freq.f32, and prints a JSON summary.
  */
 const fs = require('fs');
 const path = require('path');
@@ -29,15 +30,21 @@ async function main() {
   };
   const res = await model.generate(meta.prompt, meta.n);
   save('logits.f32', res.logits);
-  // the same generation with the decode step captured once and replayed as a HIP graph
+  // the same generation with the decode step captured once and replayed as a HIP graph (the prefill
+  // runs eagerly and is captured for this prompt length) ...
   const resG = await model.generate(meta.prompt, meta.n, { useGraph: true });
   save('logits_graph.f32', resG.logits);
+  // ... and again, now with the prefill replayed from its graph too
+  const resG2 = await model.generate(meta.prompt, meta.n, { useGraph: true });
+  save('logits_graph2.f32', resG2.logits);
   fs.writeFileSync(path.join(dir, 'inv_freq.f32'), Buffer.from(model.invFreqHost.buffer));
+  const prefillGraphs = Array.from(model.prefillGraphs.keys());   // captured prompt lengths
   model.dispose();
   backend.synchronize();
-  console.log(JSON.stringify({ tokens: res.tokens, tokensGraph: resG.tokens, rows: res.logits.length,
-                               rowsGraph: resG.logits.length, replayMs: resG.replayMs, liveBefore: before,
-                               liveAfter: backend.memoryStats().liveBytes }));
+  console.log(JSON.stringify({ tokens: res.tokens, tokensGraph: resG.tokens, tokensGraph2: resG2.tokens,
+                               rows: res.logits.length, rowsGraph: resG.logits.length, rowsGraph2: resG2.logits.length,
+                               prefillGraphs, replayMs: resG.replayMs,
+                               liveBefore: before, liveAfter: backend.memoryStats().liveBytes }));
 }
 
 main().catch((err) => {

@@ -2,7 +2,8 @@
 Qwen3 with the 0.6B's layer shapes (hidden 1024, 16/8 heads of 128, MLP 3072; vocab 4096) is written
 as a bf16 safetensors checkpoint; tests/node/qwen3_generate.js reads it, runs the prefill of a
 40-token prompt and 8 greedy decode steps through the backend's registry kernels and writes every
-forward's logits, then generates again with the decode step captured as a HIP graph and replayed.
+forward's logits, then generates twice more with HIP graphs: the decode step captured and replayed,
+and the second time the prefill replayed from the graph captured for its prompt length.
 The Python model (kandle_amd.model_utils.qwen3) on the same weights must give the same tokens and
 the same logits bit for bit -- both hosts issue the same launches, eagerly or replayed -- and the
 same RoPE inverse frequencies; every device byte the TS model allocated is returned."""
@@ -71,7 +72,11 @@ def test_typescript_qwen3_generation_matches_python_model(hip, tmp_path):
     assert res["tokens"] == list(toks)
     assert np.all(np.isfinite(ts_logits))
     np.testing.assert_array_equal(ts_logits, np.stack(logits))
-    # graph replay of the decode step issues the same launches: identical tokens and logits
+    # graph replay of the decode step, then of the prefill as well, issues the same launches:
+    # identical tokens and logits
     assert res["tokensGraph"] == list(toks) and res["rowsGraph"] == N + 1
-    np.testing.assert_array_equal(
-        np.fromfile(str(tmp_path / "logits_graph.f32"), np.float32).reshape(N + 1, cfg.vocab_size), ts_logits)
+    assert res["tokensGraph2"] == list(toks) and res["rowsGraph2"] == N + 1
+    assert res["prefillGraphs"] == [len(prompt)]
+    for name in ("logits_graph.f32", "logits_graph2.f32"):
+        np.testing.assert_array_equal(np.fromfile(str(tmp_path / name), np.float32).reshape(N + 1, cfg.vocab_size),
+                                      ts_logits)

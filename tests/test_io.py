@@ -198,3 +198,35 @@ def test_qwen3_config_from_hf_json(tmp_path):
     with open(tmp_path / "config.json", "w") as fh:
         json.dump(d, fh)
     assert Qwen3Config.from_json_file(str(tmp_path / "config.json")) == Qwen3Config()
+
+
+def test_save_safetensors_round_trip(tmp_path):
+    """save_safetensors writes what both this loader and the safetensors package read back
+    bit for bit: bf16 bit patterns, float32, int32, an empty tensor and the metadata map, with the
+    header padded to 8 bytes and no gaps in the data area."""
+    from safetensors.torch import load_file
+
+    from kandle_amd.io import save_safetensors
+
+    rng = np.random.default_rng(5)
+    t = {"w.bf16": rng.integers(0, 1 << 16, (7, 5), dtype=np.uint16),
+         "b.f32": rng.standard_normal(9).astype(np.float32),
+         "ids.i32": np.array([3, -1, 151935], np.int32),
+         "empty": np.zeros((0, 4), np.float32)}
+    p = str(tmp_path / "m.safetensors")
+    save_safetensors(p, t, metadata={"format": "pt"})
+    with open(p, "rb") as f:
+        n = parse_header_size(f.read(8))
+    assert n % 8 == 0
+    g = load_safetensor(p)
+    assert g.metadata == {"format": "pt"}
+    want = {"w.bf16": "bfloat16", "b.f32": "float32", "ids.i32": "int32", "empty": "float32"}
+    for k, v in t.items():
+        np.testing.assert_array_equal(host_array(g.layers[k], want[k]), v)
+    r = load_file(p)
+    assert r["w.bf16"].dtype == torch.bfloat16
+    np.testing.assert_array_equal(r["w.bf16"].view(torch.int16).numpy().view(np.uint16), t["w.bf16"])
+    np.testing.assert_array_equal(r["b.f32"].numpy(), t["b.f32"])
+    np.testing.assert_array_equal(r["ids.i32"].numpy(), t["ids.i32"])
+    with pytest.raises(ValueError, match="no safetensors dtype"):
+        save_safetensors(str(tmp_path / "bad.safetensors"), {"x": np.zeros(2, np.complex64)})

@@ -156,3 +156,23 @@ def test_typescript_safetensors_reader(tmp_path):
     assert r["t"]["a.weight"][:2] == ["F32", [2, 3, 4]] and bytes(r["t"]["a.weight"][2]) == a.tobytes()
     assert r["t"]["b"][:2] == ["BF16", [5, 2]] and bytes(r["t"]["b"][2]) == b.tobytes()
     assert r["err"] is not None and "outside the file" in r["err"]
+
+
+def test_generate_example_checks_and_prints_usage(tmp_path):
+    """packages/backend-hip/examples/generate.js (the Node generation CLI that bench.py drives on the
+    GPU box) parses, and without its four arguments prints its usage and exits with status 2 before
+    touching a device; the stripped Qwen3 module it loads exports the model and the reader."""
+    _need_node()
+    out = tmp_path / "qwen3.js"
+    _strip(os.path.join(PKG, "src", "qwen3.ts"), out)
+    for js in (str(out), os.path.join(PKG, "examples", "generate.js")):
+        chk = subprocess.run(["node", "--check", js], capture_output=True, text=True)
+        assert chk.returncode == 0, (js, chk.stderr)
+    res = subprocess.run(["node", os.path.join(PKG, "examples", "generate.js")], capture_output=True, text=True,
+                         timeout=60)
+    assert res.returncode == 2 and "usage: node examples/generate.js CONFIG.json MODEL.safetensors" in res.stderr
+    script = f"const m = require({json.dumps(os.path.join(PKG, 'dist', 'qwen3.js'))}); " \
+             "console.log(JSON.stringify(Object.keys(m).sort()));"
+    r = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert {"Qwen3ForCausalLM", "readSafetensors"} <= set(json.loads(r.stdout.strip().splitlines()[-1]))
