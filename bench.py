@@ -819,9 +819,36 @@ def cpu_baseline_norm():
 
 
 def cpu_baseline_model(prompt_len=512, decode_steps=4):
-    """C5 on the CPU, extrapolated: the numpy oracle (one BLAS thread) of ONE decoder layer of the
-    0.6B architecture over the 512-token prompt and `decode_steps` one-token steps after it, times 28
-    layers, plus the lm_head row; tokens/s for prefill and decode."""
+    """C5 on the CPU, extrapolated from ONE decoder layer of the 0.6B architecture over the 512-token
+    prompt and `decode_steps` one-token steps after it: times 28 layers, plus the lm_head row, as
+    tokens/s for prefill and decode.  The leg reported is the JavaScript restatement run by Node on
+    one thread (oracle/js/qwen3_cpu.js, checked against the numpy oracle in tests/test_oracle_js.py);
+    the numpy oracle (one BLAS thread) rides along as "numpy_oracle"."""
+    import oracle
+
+    js = None
+    if oracle.node_available():
+        from kandle_amd.model_utils import Qwen3Config
+
+        t = oracle.js_qwen3_timing(Qwen3Config(), prompt_len, decode_steps)
+        L = Qwen3Config().num_hidden_layers
+        pre_s = ((t["prefill_ms"] - t["head_ms"]) * L + t["head_ms"]) * 1e-3
+        dec_s = ((t["decode_ms"] - t["head_ms"]) * L + t["head_ms"]) * 1e-3
+        js = {"prefill_tokens_per_s": round(prompt_len / pre_s, 3), "decode_tokens_per_s": round(1.0 / dec_s, 4),
+              "cores": 1, "kind": "port",
+              "runtime": f"JavaScript, Node {_node_version()}, one thread (host has {os.cpu_count()} cores)",
+              "sample": f"extrapolated x28 layers: 1 layer measured once (prefill of {prompt_len} tokens "
+                        f"{t['prefill_ms'] / 1e3:.2f} s, decode {t['decode_ms']:.0f} ms/step over {decode_steps} "
+                        f"steps, both incl. the lm_head row {t['head_ms']:.0f} ms, counted once)"}
+    npy = _cpu_baseline_model_numpy(prompt_len, decode_steps)
+    if js is None:
+        return npy
+    js["numpy_oracle"] = npy
+    return js
+
+
+def _cpu_baseline_model_numpy(prompt_len=512, decode_steps=4):
+    """The numpy oracle (one BLAS thread) of one decoder layer, extrapolated as cpu_baseline_model."""
     import dataclasses
 
     from kandle_amd import synthetic as syn

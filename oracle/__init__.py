@@ -187,6 +187,21 @@ def js_bench(op, inputs, args, repeat=1, outputs=()):
     return res, [float(x) for x in json.loads(out.stdout.strip().splitlines()[-1])["runs_ms"]]
 
 
+def js_qwen3_timing(cfg, prompt_len: int, decode_steps: int, seed: int = 7) -> dict:
+    """oracle/js/bench_cpu.js qwen3: ONE decoder layer of `cfg`'s shapes (seeded weights) in Node on
+    one thread -- the prefill of prompt_len ids, then decode_steps greedy one-token forwards, and the
+    lm_head row alone.  Returns {"prefill_ms", "decode_ms" (per step), "head_ms", "last_token"}."""
+    import json
+    import subprocess
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "js", "bench_cpu.js")
+    args = [cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+            cfg.vocab_size, int(prompt_len), int(decode_steps), repr(float(cfg.rms_norm_eps)),
+            repr(float(cfg.rope_theta)), int(seed)]
+    out = subprocess.run(["node", script, "qwen3", ".", "1"] + [str(a) for a in args], capture_output=True,
+                         text=True, check=True)
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
 def rms_norm(x, w=None, eps=1e-6) -> np.ndarray:
     x = _f32(x)
     n = x.shape[-1]

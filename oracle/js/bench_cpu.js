@@ -10,6 +10,11 @@
  *            issues it for a one-token decode step (packages/model-utils/src/attention/gqa.ts:333-336)
  *   normrope DIR REPEAT T Hid Hq Hkv D eps theta                 (x.f32 [T,Hid], q.f32 [T,Hq,D],
  *            k.f32 [T,Hkv,D], w.f32, wq.f32, wk.f32 -> y.f32, qo.f32, ko.f32); positions 0..T-1
+ *   qwen3    DIR REPEAT Hid I Hq Hkv D vocab S steps eps theta seed  (qwen3_cpu.js: ONE decoder layer
+ *            of seeded weights, uniform in +-0.035 (std 0.02), norms 1): the S-token prefill of seeded
+ *            ids, then `steps` greedy one-token forwards, and the lm_head row alone; REPEAT is
+ *            ignored (one pass, no untimed run: a prefill layer takes seconds) and the op prints
+ *            {"prefill_ms", "decode_ms" (per step), "head_ms"} instead of runs_ms
  * Runs the op once untimed, then REPEAT timed runs (performance.now from perf_hooks: Node 12 has no
  * global performance), writes the last run's outputs and prints {"runs_ms": [...]}.
  */
@@ -18,6 +23,7 @@ const path = require('path');
 const perf = require('perf_hooks').performance;
 const flash = require('./flash_sdpa.js');
 const ops = require('./cpu_ops.js');
+const qwen3 = require('./qwen3_cpu.js');
 
 function readF32(dir, name) {
   const buf = fs.readFileSync(path.join(dir, name));
@@ -88,6 +94,53 @@ function main() {
     writeF32(dir, 'y.f32', y);
     writeF32(dir, 'qo.f32', qo);
     writeF32(dir, 'ko.f32', ko);
+  } else if (op === 'qwen3') {
+    const cfg = { hiddenSize: p[0], intermediateSize: p[1], numAttentionHeads: p[2], numKeyValueHeads: p[3],
+                  headDim: p[4], vocabSize: p[5], numHiddenLayers: 1, rmsNormEps: p[8], ropeTheta: p[9] };
+    const S = p[6], steps = p[7];
+    let st = (p[10] >>> 0) || 1;
+    const rnd = function () {  // xorshift32, uniform in [0, 1)
+      st ^= st << 13; st >>>= 0; st ^= st >>> 17; st ^= st << 5; st >>>= 0;
+      return st / 4294967296;
+    };
+    const fill = function (n, ones) {
+      const a = new Float32Array(n);
+      for (let i = 0; i < n; i++) a[i] = ones ? 1 : (rnd() * 2 - 1) * 0.035;
+      return a;
+    };
+    const Hd = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
+    const nq = cfg.numAttentionHeads * D, nkv = cfg.numKeyValueHeads * D;
+    const pre = 'model.layers.0.';
+    const w = {
+      'model.embed_tokens.weight': fill(cfg.vocabSize * Hd), 'model.norm.weight': fill(Hd, true),
+    };
+    w[pre + 'input_layernorm.weight'] = fill(Hd, true);
+    w[pre + 'post_attention_layernorm.weight'] = fill(Hd, true);
+    w[pre + 'self_attn.q_norm.weight'] = fill(D, true);
+    w[pre + 'self_attn.k_norm.weight'] = fill(D, true);
+    w[pre + 'self_attn.q_proj.weight'] = fill(nq * Hd);
+    w[pre + 'self_attn.k_proj.weight'] = fill(nkv * Hd);
+    w[pre + 'self_attn.v_proj.weight'] = fill(nkv * Hd);
+    w[pre + 'self_attn.o_proj.weight'] = fill(Hd * nq);
+    w[pre + 'mlp.gate_proj.weight'] = fill(I * Hd);
+    w[pre + 'mlp.up_proj.weight'] = fill(I * Hd);
+    w[pre + 'mlp.down_proj.weight'] = fill(Hd * I);
+    const model = new qwen3.Qwen3Cpu(cfg, w, S + steps + 1);
+    const ids = [];
+    for (let i = 0; i < S; i++) ids.push(Math.floor(rnd() * cfg.vocabSize));
+    let t0 = perf.now();
+    let logits = model.forward(ids, 0);
+    const prefillMs = perf.now() - t0;
+    t0 = perf.now();
+    for (let i = 0; i < steps; i++) logits = model.forward([qwen3.argmax(logits)], S + i);
+    const decodeMs = (perf.now() - t0) / steps;
+    const row = fill(Hd, true);
+    t0 = perf.now();
+    for (let i = 0; i < 3; i++) model.lmHead(row);
+    const headMs = (perf.now() - t0) / 3;
+    process.stdout.write(JSON.stringify({ prefill_ms: prefillMs, decode_ms: decodeMs, head_ms: headMs,
+                                          last_token: qwen3.argmax(logits) }) + '\n');
+    return;
   } else {
     process.stderr.write('unknown op ' + op + '\n');
     process.exit(2);
