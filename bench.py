@@ -326,14 +326,20 @@ def prep_model(new_tokens=128, prompt_len=512, use_graph=True, ts_host=False):
     del w
 
     def run(steps, warmup):
-        warm = {}
-        model.generate(prompt, 8, use_graph=use_graph, timing=warm)   # eager prefill (then captured)
-        timing = {}
-        toks = model.generate(prompt, new_tokens, timing=timing, use_graph=use_graph)
+        try:
+            warm = {}
+            model.generate(prompt, 8, use_graph=use_graph, timing=warm)   # eager prefill (then captured)
+            timing = {}
+            toks = model.generate(prompt, new_tokens, timing=timing, use_graph=use_graph)
+        except BaseException:
+            if ts_dir is not None:   # the checkpoint written for the TypeScript host (1.2 GB)
+                import shutil
+                shutil.rmtree(ts_dir, ignore_errors=True)
+            raise
         if not use_graph:  # every step eager: time all of them
             timing["replay_ms"], timing["replay_steps"] = timing["decode_ms"], new_tokens
         model.dispose()
-        ts = _run_ts_host(ts_dir, new_tokens, toks) if ts_dir is not None else None
+        ts = _run_ts_host(ts_dir, new_tokens, toks) if ts_dir is not None else None   # removes ts_dir
         H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
         Hq, Hkv, Lyr = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
         layer_w = H * (Hq + 2 * Hkv) * D + Hq * D * H + 3 * H * I            # projection weights per layer
