@@ -323,6 +323,28 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
 int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,
                    int64_t n_half, int64_t k);
 
+/* The QKV projection of a prefill fused with qk-norm, RoPE and the KV-cache write:
+ *   qkv[t, :] = x[t, :] W^T      (bf16 x [M, k] with row stride ldx, M = n_batch * seq_len tokens;
+ *                                 w_qkv [(hq + 2 hkv) * 128, k] with row stride ldw: the q heads'
+ *                                 rows, then the k heads', then the v heads'; fp32 accumulate,
+ *                                 each value rounded to bf16 as kh_gemm stores it)
+ * then, per token t (batch b = t / seq_len, index s = t % seq_len, position p = positions[t]) and
+ * head row, exactly as kh_qk_norm_rope on that bf16 output: q rows normed with wq and rotated,
+ * written at q_out + b*st[0] + s*st[1] + h*st[2]; k rows normed with wk and rotated, written at
+ * k_out + b*st[3] + row*st[4] + h*st[5]; v rows unchanged at v_out + b*st[6] + row*st[7] + h*st[8],
+ * where row = p when kv_cache_len > 0 (positions outside [0, kv_cache_len) write no K/V row) and
+ * row = s otherwise (`strides` holds these 9 element strides, multiples of 8).  head_dim must be
+ * 128; operands 16-byte aligned; k, ldx, ldw multiples of 8.  The [M, (hq + 2 hkv) * 128]
+ * projection output is never written.  Each output sums over all of k: the values kh_gemm followed
+ * by kh_qk_norm_rope produce whenever kh_gemm runs its MFMA tiles unsplit (M > 8 and
+ * kh_gemm_split_count() == 1).  Fuses GroupedQueryAttention's q/k/v projections with
+ * q_norm / k_norm, RoPE and the cache update (reference: packages/model-utils/src/attention/
+ * gqa.ts:269-309; rope.ts:546-644; kv-cache.ts:164-212); no single reference kernel. */
+int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
+                         int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim, const void* wq,
+                         const void* wk, const float* inv_freq, const int32_t* positions, void* q_out, void* k_out,
+                         void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len);
+
 /* The split count kh_gemm uses for a bf16 [m, k] x [n, k]^T product with contiguous, 16-byte
  * aligned operands (1: not split).  A caller that splits the same product with
  * kh_gemm_splitk_partials and adds the partials in split order reproduces kh_gemm bit for bit. */

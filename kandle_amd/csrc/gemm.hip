@@ -13,6 +13,7 @@
 
 #include "common.h"
 #include "gemv.h"
+#include "qk_rope.h"
 
 using namespace kh;
 using namespace kh::gemv;
@@ -81,11 +82,32 @@ constexpr int g_tile(int wt) { return 64 * wt; }
 // every lane holds each gate accumulator and its up partner, and the epilogue stores
 // C[m, f] = bf16(silu(bf16(gate)) * bf16(up)) over N / 2 features f -- the values the separate
 // GEMM (bf16 store) and silu*mul kernel produce, without the [M, N] intermediate.
-template <typename TO, int WTM, int WTN, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false>
+// QKNR (bf16, 64 x 128 tiles, no split): the QKV projection of a prefill, whose output columns are
+// head rows of 128 (the q heads, then the k heads, then the v heads).  The epilogue stages the
+// tile, rounded to bf16 as the plain GEMM stores it, in LDS and reads it back one head row per
+// group of 8 lanes -- qk_norm_rope_kernel's layout -- to apply qk-norm + RoPE to q and k rows with
+// the same arithmetic (qk_norm_rope_row) and write q rows to q_out and k / v rows into the KV cache,
+// so the [M, N] projection output is never written.
+struct QknrArgs {
+  const uint16_t* wq = nullptr;       // q_norm / k_norm weights [128], bf16
+  const uint16_t* wk = nullptr;
+  const float* inv_freq = nullptr;    // [64]
+  const int32_t* positions = nullptr; // [M]: RoPE position (and, with kv_cache_len > 0, cache row)
+  uint16_t* q_out = nullptr;
+  uint16_t* k_out = nullptr;
+  uint16_t* v_out = nullptr;
+  int64_t s[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};  // (batch, seq, head) element strides of q_out, k_out, v_out
+  int hq = 0, hkv = 0;
+  uint32_t seq_len = 1;               // token m is (batch m / seq_len, index m % seq_len)
+  float eps = 0.f;
+  int64_t kv_cache_len = 0;           // > 0: K/V rows at positions[m] (outside [0, len): not written)
+};
+
+template <typename TO, int WTM, int WTN, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false, bool QKNR = false>
 __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
-    int tiles_n, int splits, int kchunk, float* __restrict__ part) {
+    int tiles_n, int splits, int kchunk, float* __restrict__ part, QknrArgs qa) {
   constexpr int GM = g_tile(WTM), GN = g_tile(WTN);
   constexpr int STR = KS + 8;  // LDS row stride (elements): 16-byte aligned, breaks bank aliasing
   constexpr int ATILE = GM * STR, BTILE = GN * STR;
@@ -217,6 +239,67 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   }
 
   // Epilogue: acc[a][b] lane holds m = m0 + wm + 32b + r, n = n0 + wn + 32a + 8(j/4) + 4g + j%4.
+  if constexpr (QKNR) {
+    static_assert(sizeof(TO) == 2 && WTM == 1 && WTN == 2 && !SPLIT && !SWIGLU, "QKNR: bf16 64 x 128 tiles");
+    constexpr int TSTR = 128 + 8;  // staged row stride (elements): 272 B, 16-byte aligned rows
+    static_assert(GM * TSTR <= 2 * (ATILE + BTILE), "the staged tile fits the k loop's LDS");
+    // Every wave has passed the k loop's last barrier: its LDS is free.
+    uint16_t* tile = smem;
+#pragma unroll
+    for (int a = 0; a < WTN; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint2 w;
+        w.x = pack_bf16x2(acc[a][0][4 * q], acc[a][0][4 * q + 1]);
+        w.y = pack_bf16x2(acc[a][0][4 * q + 2], acc[a][0][4 * q + 3]);
+        *reinterpret_cast<uint2*>(tile + (wm + r) * TSTR + wn + 32 * a + 8 * q + 4 * g) = w;
+      }
+    __syncthreads();
+    const int hd = n0 / 128;                      // q heads, then k heads, then v heads
+    const int t8 = lane & 7, rs = lane >> 3;      // 8 lanes per head row, 8 rows per wave step
+    const bool is_q = hd < qa.hq, is_k = !is_q && hd < qa.hq + qa.hkv;
+    float wa[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, wb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float f[8];
+    if (is_q || is_k) {
+      const uint16_t* wn8 = is_q ? qa.wq : qa.wk;
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(wn8 + 8 * t8), wa);
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(wn8 + 64 + 8 * t8), wb);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[j] = qa.inv_freq[8 * t8 + j];
+    }
+    const bool cache_mode = qa.kv_cache_len > 0;
+#pragma unroll
+    for (int st = 0; st < GM / 32; ++st) {
+      const int row = wave * (GM / 4) + st * 8 + rs;
+      const int m = m0 + row;
+      const bool live = m < M;
+      float a8[8], c8[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(tile + row * TSTR + 8 * t8), a8);
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(tile + row * TSTR + 64 + 8 * t8), c8);
+      const int32_t ipos = live ? qa.positions[m] : 0;
+      const uint32_t bi = live ? (uint32_t)m / qa.seq_len : 0u, si = live ? (uint32_t)m - bi * qa.seq_len : 0u;
+      const int64_t kv_row = cache_mode ? (int64_t)ipos : (int64_t)si;
+      const bool kv_ok = !cache_mode || (ipos >= 0 && (int64_t)ipos < qa.kv_cache_len);
+      if (is_q || is_k) {
+        float cs[8], sn[8], oa[8], oc[8];
+        const float pos = (float)ipos;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sincosf(pos * f[j], &sn[j], &cs[j]);
+        qk_norm_rope_row<128>(a8, c8, wa, wb, cs, sn, qa.eps, oa, oc);
+        if (live && (is_q || kv_ok)) {
+          uint16_t* dst = is_q ? qa.q_out + bi * qa.s[0] + si * qa.s[1] + (int64_t)hd * qa.s[2]
+                               : qa.k_out + bi * qa.s[3] + kv_row * qa.s[4] + (int64_t)(hd - qa.hq) * qa.s[5];
+          *reinterpret_cast<uint4*>(dst + 8 * t8) = pack_bf16x8(oa);
+          *reinterpret_cast<uint4*>(dst + 64 + 8 * t8) = pack_bf16x8(oc);
+        }
+      } else if (live && kv_ok) {
+        uint16_t* dst = qa.v_out + bi * qa.s[6] + kv_row * qa.s[7] + (int64_t)(hd - qa.hq - qa.hkv) * qa.s[8];
+        *reinterpret_cast<uint4*>(dst + 8 * t8) = *reinterpret_cast<const uint4*>(tile + row * TSTR + 8 * t8);
+        *reinterpret_cast<uint4*>(dst + 64 + 8 * t8) = *reinterpret_cast<const uint4*>(tile + row * TSTR + 64 + 8 * t8);
+      }
+    }
+    return;
+  }
   const bool vec = ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TO) - 1)) == 0) && ((ldc & 3) == 0);
   if constexpr (SWIGLU) {
     // Register groups q = 0, 2 hold gate rows n0 + wn + 32a + 8q + 4g + e, q + 1 the up rows 8 later:
@@ -570,10 +653,10 @@ void go_tiles(int nblk, int splits, const uint16_t* A, int64_t lda, const uint16
   constexpr int PF = kGemmPrefetch;
   if (!SWIGLU && splits > 1)
     gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part);
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part, QknrArgs{});
   else
     gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU><<<nblk, G_THREADS, 0, stream()>>>(
-        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr);
+        A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr, QknrArgs{});
 }
 
 // Dispatch on the plan's tile: 128 x 128 with k-step 64; 64 x 64 with k-step 128 when split or
@@ -679,6 +762,19 @@ int launch_gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_
   return KH_OK;
 }
 
+// The fused QKV projection: 64 x 128 tiles (one head row of 128 per tile column), never split.
+int launch_gemm_qk_norm_rope(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, int M, int N, int K,
+                             const QknrArgs& qa) {
+  const int tiles_m = (M + 63) / 64, tiles_n = N / 128;
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_qk_norm_rope: grid too large");
+  gemm_bf16_nt_kernel<uint16_t, 1, 2, kGemmRectKS, false, kGemmPrefetch, false, true><<<(int)tiles, G_THREADS, 0,
+                                                                                          stream()>>>(
+      X, ldx, W, ldw, nullptr, 0, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr, qa);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
 }  // namespace
 
 namespace kh {
@@ -759,6 +855,48 @@ int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, vo
              "kh_gemm_swiglu: row stride too large");
   return launch_gemm_swiglu((const uint16_t*)x, ldx, (const uint16_t*)w_gu, ldw, (uint16_t*)h, ldh, (int)m,
                             (int)(2 * n_half), (int)k);
+}
+
+int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
+                         int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim, const void* wq,
+                         const void* wk, const float* inv_freq, const int32_t* positions, void* q_out, void* k_out,
+                         void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(n_batch >= 0 && seq_len >= 0 && k > 0 && k <= INT32_MAX && kv_cache_len >= 0,
+             "kh_gemm_qk_norm_rope: bad extents");
+  KH_REQUIRE(head_dim == 128, "kh_gemm_qk_norm_rope: head_dim %d (the fused projection takes 128)", head_dim);
+  KH_REQUIRE(n_q_heads > 0 && n_kv_heads > 0, "kh_gemm_qk_norm_rope: head counts must be positive");
+  const int64_t M = n_batch * seq_len, N = (int64_t)(n_q_heads + 2 * n_kv_heads) * 128;
+  KH_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && seq_len <= (int64_t)UINT32_MAX, "kh_gemm_qk_norm_rope: too large");
+  if (M == 0) return KH_OK;
+  KH_REQUIRE(x && w_qkv && wq && wk && inv_freq && positions && q_out && k_out && v_out && strides,
+             "kh_gemm_qk_norm_rope: null pointer");
+  KH_REQUIRE(k % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= k && ldw >= k,
+             "kh_gemm_qk_norm_rope: k and the row strides must be multiples of 8 elements (ldx, ldw >= k)");
+  const void* al[] = {x, w_qkv, wq, wk, q_out, k_out, v_out};
+  for (const void* p : al) KH_REQUIRE(aligned16(p), "kh_gemm_qk_norm_rope: operands must be 16-byte aligned");
+  const int64_t lim = int64_t(1) << 31;
+  KH_REQUIRE((int64_t)g_tile(2) * ldx * 2 < lim && (int64_t)g_tile(2) * ldw * 2 < lim,
+             "kh_gemm_qk_norm_rope: row stride too large");
+  QknrArgs qa;
+  for (int i = 0; i < 9; ++i) {
+    KH_REQUIRE(strides[i] % 8 == 0, "kh_gemm_qk_norm_rope: stride %d (%lld) breaks 16-byte alignment", i,
+               (long long)strides[i]);
+    qa.s[i] = strides[i];
+  }
+  qa.wq = (const uint16_t*)wq;
+  qa.wk = (const uint16_t*)wk;
+  qa.inv_freq = inv_freq;
+  qa.positions = positions;
+  qa.q_out = (uint16_t*)q_out;
+  qa.k_out = (uint16_t*)k_out;
+  qa.v_out = (uint16_t*)v_out;
+  qa.hq = n_q_heads;
+  qa.hkv = n_kv_heads;
+  qa.seq_len = (uint32_t)(seq_len > 0 ? seq_len : 1);
+  qa.eps = eps;
+  qa.kv_cache_len = kv_cache_len;
+  return launch_gemm_qk_norm_rope((const uint16_t*)x, ldx, (const uint16_t*)w_qkv, ldw, (int)M, (int)N, (int)k, qa);
 }
 
 int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, const void* w_gu, int64_t ldw,

@@ -8,6 +8,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "qk_rope.h"
 
 using namespace kh;
 
@@ -309,23 +310,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
         const int r = step * RPW + rsub;
         const bool isq = r < hq;
         const bool active = r < total_rows && (isq || kv_ok);
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss += a[j] * a[j] + c[j] * c[j];
-        ss = group_sum<LPR>(ss);
         float wa[8], wb[8];
         Vec8<T>::cvt(rwa[u], wa);
         Vec8<T>::cvt(rwb[u], wb);
+        float oa[8], oc[8];
+        qk_norm_rope_row<D>(a, c, wa, wb, cs, sn, eps, oa, oc);
         if (active) {
-          const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-          float oa[8], oc[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float na = (a[j] * inv) * wa[j];
-            const float nc = (c[j] * inv) * wb[j];
-            oa[j] = na * cs[j] + (-nc) * sn[j];
-            oc[j] = nc * cs[j] + na * sn[j];
-          }
           T* dst = isq ? qot + (int64_t)r * st.s[8] : kot + (int64_t)(r - hq) * st.s[11];
           Vec8<T>::store(dst + 8 * t, oa);
           Vec8<T>::store(dst + HALF + 8 * t, oc);

@@ -686,6 +686,46 @@ def linear_swiglu(x, w_gu, output) -> None:
               _vp(output.data_ptr()), ldh, m, I, H)
 
 
+def linear_qk_norm_rope(x, w_qkv, params) -> None:
+    """The QKV projection of a multi-token chunk fused with qk-norm, RoPE and the K/V cache write
+    (kh_gemm_qk_norm_rope): x [S, H] bf16 (contiguous rows), w_qkv [(Hq + 2 Hkv) D, H] (q, k, v
+    projection rows concatenated), D = 128.  params: q_weight, k_weight ([D] bf16), inv_freq
+    (float32 [D/2]), positions (int32 [S]), eps, q_out ([1, Hq, S, D] or any [1, Hq, S, D] view with
+    a contiguous head dim), k_out / v_out (the KV caches [1, Hkv, max_seq, D]; token t lands in row
+    positions[t], rows outside the cache write nothing).  The same values as linear() followed by
+    rms_norm_rope(..., cache_positions=True) (gqa.ts:269-309, rope.ts:546-644,
+    kv-cache.ts:164-212), without the [S, (Hq + 2 Hkv) D] projection output."""
+    q_out, k_out, v_out = params["q_out"], params["k_out"], params["v_out"]
+    _, Hq, S, D = q_out.shape
+    _, Hkv, L, _ = k_out.shape
+    N, H = w_qkv.shape
+    if D != 128 or N != (Hq + 2 * Hkv) * D:
+        raise ValueError(f"linear_qk_norm_rope: head_dim 128 and w_qkv [(Hq + 2 Hkv) D, H] expected, got D = {D}, "
+                         f"w_qkv {tuple(w_qkv.shape)} for Hq = {Hq}, Hkv = {Hkv}")
+    if tuple(x.shape) != (S, H) or x.strides[-1] != 1 or w_qkv.strides[1] != 1:
+        raise ValueError(f"linear_qk_norm_rope: x [{S}, {H}] with contiguous rows expected, got {tuple(x.shape)}")
+    if any(t.dtype != BFLOAT16 for t in (x, w_qkv, q_out, k_out, v_out)):
+        raise TypeError("linear_qk_norm_rope: bf16 operands only")
+    if tuple(v_out.shape) != tuple(k_out.shape):
+        raise ValueError("linear_qk_norm_rope: K and V caches must have the same shape")
+    pos, inv_freq = params["positions"], params["inv_freq"]
+    if pos.dtype != INT32 or pos.numel != S:
+        raise ValueError("linear_qk_norm_rope: positions must be int32 with S entries")
+    if inv_freq.dtype != FLOAT32 or inv_freq.numel != D // 2:
+        raise ValueError("linear_qk_norm_rope: inv_freq must be float32 [D/2]")
+    for t in (q_out, k_out, v_out):
+        if t.strides[-1] != 1:
+            raise ValueError("linear_qk_norm_rope: head_dim must be contiguous")
+    # (batch, seq, head) strides of the heads-first outputs
+    st = []
+    for t in (q_out, k_out, v_out):
+        st += [t.strides[0], t.strides[2], t.strides[1]]
+    _lib.call("kh_gemm_qk_norm_rope", _vp(x.data_ptr()), x.strides[0], _vp(w_qkv.data_ptr()), w_qkv.strides[0], 1,
+              S, H, Hq, Hkv, D, _vp(params["q_weight"].data_ptr()), _vp(params["k_weight"].data_ptr()),
+              _vp(inv_freq.data_ptr()), _vp(pos.data_ptr()), _vp(q_out.data_ptr()), _vp(k_out.data_ptr()),
+              _vp(v_out.data_ptr()), _lib.i64_array(st), C.c_float(float(params.get("eps", 1e-6))), L)
+
+
 def gemm_split_count(m: int, n: int, k: int) -> int:
     """The K split kh_gemm uses for a contiguous bf16 [m, k] x [n, k]^T product (1: none)."""
     out = C.c_int(0)
@@ -885,6 +925,7 @@ KERNELS = {
     "sub": sub,
     "silu_mul": silu_mul,
     "linear_swiglu": linear_swiglu,
+    "linear_qk_norm_rope": linear_qk_norm_rope,
     "linear_add_rms_norm": linear_add_rms_norm,
     "copy": copy,
     "contiguous": copy,

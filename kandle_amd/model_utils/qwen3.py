@@ -34,6 +34,7 @@ from .. import env
 from .. import functional as F
 from .. import synthetic as syn
 from .._lib import KandleHipError
+from ..kernels import gemm_split_count
 from ..graphs import HipGraph
 from ..kernels import TensorIterator, interleave_gate_up
 from ..tensor import HipTensorHandle, Tensor
@@ -200,6 +201,10 @@ class Qwen3ForCausalLM:
         # Decode steps run each layer's attention block (qk-norm, RoPE, K/V write, attention, o_proj)
         # as one library call; False runs the separate launches (the prefill's path at S = 1).
         self.fused_decode = True
+        # Chunks whose QKV projection kh_gemm would run on MFMA tiles without a K split run it with
+        # qk-norm, RoPE and the K/V cache write in its epilogue (linear_qk_norm_rope, head_dim 128;
+        # the same values); False always runs the projection and rms_norm_rope as two launches.
+        self.fused_qkv_rope = cfg.head_dim == 128
 
     # -- decoder body shared by the prefill and the device-resident decode step -------------------
     @classmethod
@@ -241,6 +246,11 @@ class Qwen3ForCausalLM:
         # from one sub-block to the next; the last down projection normalises only the last row, with
         # the final norm, for the lm_head.
         h = None if one else F.rms_norm(x, [Hd], self.layers[0]["in_norm"], eps, out_dtype="bfloat16")
+        # The fused QKV projection sums each output over all of K, as kh_gemm does when it takes
+        # its MFMA tiles (more than 8 rows) without splitting K: only then are the values the same.
+        nqkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+        fuse_qkv = (self.fused_qkv_rope and not one and S > 8
+                    and gemm_split_count(S, nqkv, Hd) == 1)
         for li, L in enumerate(self.layers):
             if one and decode_block:
                 qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
@@ -254,6 +264,11 @@ class Qwen3ForCausalLM:
                 qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
                 attn_t = self._attention_heads(li, L, qkv, S, positions, attend)
                 F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
+                attn_t.dispose()
+            elif fuse_qkv:
+                attn_t = self._attention_heads_fused(li, L, h, S, positions, attend)   # q/k/v from h
+                h.dispose()
+                h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm"], eps)     # x += o W_o^T
                 attn_t.dispose()
             else:
                 qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
@@ -281,6 +296,25 @@ class Qwen3ForCausalLM:
             logits = F.linear(h, self.lm_head, out_dtype="float32")                    # [1, vocab] fp32
             h.dispose()
         return logits
+
+    def _attention_heads_fused(self, li: int, L: dict, h: Tensor, S: int, positions: Tensor, attend) -> Tensor:
+        """As _attention_heads from the normed rows h [S, hidden] instead of their projection: one
+        launch projects q/k/v and applies qk-norm + RoPE with the K/V cache write
+        (linear_qk_norm_rope), then attend(); returns the heads [S, nq] bf16."""
+        cfg = self.cfg
+        Hq, D = cfg.num_attention_heads, cfg.head_dim
+        nq = Hq * D
+        q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+        self.ops.find("linear_qk_norm_rope")(h.handle, L["w_qkv"].handle, {
+            "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
+            "positions": positions.handle, "eps": cfg.rms_norm_eps, "q_out": q_heads,
+            "k_out": self.cache.key_cache[li].handle, "v_out": self.cache.value_cache[li].handle})
+        attn = HipTensorHandle.create_new((S, nq), "bfloat16")
+        attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
+        attend(li, q_heads, attn_view)
+        attn_view.dispose()
+        q_heads.dispose()
+        return Tensor(handle=attn)
 
     def _attention_heads(self, li: int, L: dict, qkv: Tensor, S: int, positions: Tensor, attend) -> Tensor:
         """The attention of layer li from its QKV projection qkv [S, nq + 2 nkv] (disposed here):

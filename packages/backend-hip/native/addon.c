@@ -542,6 +542,20 @@ FN(gemmSwiglu, 9)
   void* h = arg_ptr(A, 4); int64_t ldh = arg_i64(A, 5); int64_t m = arg_i64(A, 6); int64_t nh = arg_i64(A, 7);
   int64_t k = arg_i64(A, 8);
   CALL(kh_gemm_swiglu(x, ldx, w, ldw, h, ldh, m, nh, k))
+/* gemmQkNormRope(x, ldx, wQkv, ldw, nBatch, seqLen, k, hq, hkv, headDim, wq, wk, invFreq, positions,
+   qOut, kOut, vOut, strides[9], eps, kvCacheLen): the QKV projection with qk-norm, RoPE and the K/V
+   cache write in its epilogue (gqa.ts:269-309, rope.ts:546-644, kv-cache.ts:164-212) */
+FN(gemmQkNormRope, 20)
+  int64_t st[9];
+  void* x = arg_ptr(A, 0); int64_t ldx = arg_i64(A, 1); void* w = arg_ptr(A, 2); int64_t ldw = arg_i64(A, 3);
+  int64_t nb = arg_i64(A, 4); int64_t sl = arg_i64(A, 5); int64_t k = arg_i64(A, 6);
+  int hq = arg_int(A, 7); int hkv = arg_int(A, 8); int hd = arg_int(A, 9);
+  void* wq = arg_ptr(A, 10); void* wk = arg_ptr(A, 11); void* inv = arg_ptr(A, 12); void* pos = arg_ptr(A, 13);
+  void* qo = arg_ptr(A, 14); void* ko = arg_ptr(A, 15); void* vo = arg_ptr(A, 16);
+  arg_list(A, 17, st, 9);
+  double eps = arg_f64(A, 18); int64_t kvl = arg_i64(A, 19);
+  CALL(kh_gemm_qk_norm_rope(x, ldx, w, ldw, nb, sl, k, hq, hkv, hd, wq, wk, (const float*)inv, (const int32_t*)pos,
+                            qo, ko, vo, st, (float)eps, kvl))
 /* gemmSplitCount(m, n, k) -> the split count gemm uses for a contiguous bf16 [m, k] x [n, k]^T */
 static napi_value js_gemmSplitCount(napi_env env, napi_callback_info info) {
   Args A_, *A = &A_;
@@ -597,7 +611,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
-      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemmSplitCount),
+      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemmQkNormRope), EXPORT(gemmSplitCount),
       EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused), EXPORT(gemvSwiglu),
   };
   napi_define_properties(env, exports, sizeof(d) / sizeof(d[0]), d);

@@ -584,6 +584,32 @@ function linearSwiglu(x: HipTensorHandle, wGu: HipTensorHandle, out: HipTensorHa
   addon.gemmSwiglu(x.ptr, H, wGu.ptr, wGu.strides[0], out.ptr, I, m, I, H);
 }
 
+// linear_qk_norm_rope(x, wQkv, params): the QKV projection of a chunk of S tokens with qk-norm, RoPE
+// and the K/V cache write in its epilogue (gqa.ts:269-309, rope.ts:546-644, kv-cache.ts:164-212);
+// x [S, H] bf16, wQkv [(Hq + 2 Hkv) 128, H]; params: qWeight, kWeight, invFreq, positions (int32 [S]),
+// eps, qOut ([1, Hq, S, 128]), kOut / vOut (the caches [1, Hkv, maxSeq, 128], token t at row
+// positions[t]).  The values of matmul followed by rms_norm_rope with cachePositions.
+function linearQkNormRope(x: HipTensorHandle, wQkv: HipTensorHandle, p: { [key: string]: any }): void {
+  const qOut: HipTensorHandle = p.qOut;
+  const kOut: HipTensorHandle = p.kOut;
+  const vOut: HipTensorHandle = p.vOut;
+  const Hq = qOut.shape[1], S = qOut.shape[2], D = qOut.shape[3], Hkv = kOut.shape[1], L = kOut.shape[2];
+  const H = wQkv.shape[1];
+  if (D !== 128 || wQkv.shape[0] !== (Hq + 2 * Hkv) * D)
+    throw new Error('linear_qk_norm_rope: head_dim 128 and wQkv [(Hq + 2 Hkv) D, H] expected');
+  if (x.shape.join() !== [S, H].join() || x.strides[1] !== 1 || wQkv.strides[1] !== 1)
+    throw new Error(`linear_qk_norm_rope: x [${S}, ${H}] with contiguous rows expected`);
+  for (const t of [x, wQkv, qOut, kOut, vOut]) {
+    if (t.dtype !== 'bfloat16') throw new Error('linear_qk_norm_rope: bf16 operands only');
+  }
+  if (vOut.shape.join() !== kOut.shape.join()) throw new Error('linear_qk_norm_rope: K and V caches differ in shape');
+  const st: number[] = [];
+  for (const t of [qOut, kOut, vOut]) st.push(t.strides[0], t.strides[2], t.strides[1]);
+  addon.gemmQkNormRope(x.ptr, x.strides[0], wQkv.ptr, wQkv.strides[0], 1, S, H, Hq, Hkv, D, p.qWeight.ptr,
+                       p.kWeight.ptr, p.invFreq.ptr, p.positions.ptr, qOut.ptr, kOut.ptr, vOut.ptr, st,
+                       p.eps === undefined ? 1e-6 : p.eps, L);
+}
+
 // linear_add_rms_norm(x, w, residual, normWeight, eps, output, rows?): residual += x W^T (fp32, in
 // place), then output = rms_norm(residual rows) * normWeight (decoder_layer.ts:224-238 with
 // RMSNorm.ts:92-99).  When the GEMM splits K, its fp32 partials go straight into the fused
@@ -737,6 +763,11 @@ export class HipBackend {
     addon.graphDestroy(graph);
   }
 
+  // The K split matmul (kh_gemm) uses for a contiguous bf16 [m, k] x [n, k]^T product (1: none).
+  gemmSplitCount(m: number, n: number, k: number): number {
+    return addon.gemmSplitCount(m, n, k);
+  }
+
   memoryStats(): { [key: string]: number } {
     return addon.allocStats();
   }
@@ -765,6 +796,7 @@ export function registerHipKernels(reg: SimpleOperatorRegistry): void {
   reg.register('gemv_fused', gemvFused);
   reg.register('gemv_swiglu', gemvSwiglu);
   reg.register('linear_swiglu', linearSwiglu);
+  reg.register('linear_qk_norm_rope', linearQkNormRope);
   reg.register('linear_add_rms_norm', linearAddRmsNorm);
   reg.register('decode_attention_block', decodeAttentionBlock);
   reg.register('greedy_advance', greedyAdvance);

@@ -209,20 +209,31 @@ export class Qwen3ForCausalLM {
     const Hq = cfg.numAttentionHeads, Hkv = cfg.numKeyValueHeads, eps = cfg.rmsNormEps;
     const nq = Hq * D, nkv = Hkv * D, nqkv = nq + 2 * nkv;
     const x = be.createTensorHandle([S, H], 'float32');
+    // the fused QKV projection sums over all of K, as matmul does on MFMA tiles (more than 8 rows)
+    // when it does not split K
+    const fuseQkv = D === 128 && S > 8 && be.gemmSplitCount(S, nqkv, H) === 1;
     ops.find('index_select')(this.embed, ids, { dim: 0 }, x);
     let h = ops.find('rms_norm')([x], { normalizedShape: [H], eps, weight: this.layers[0].inNorm, outDtype: 'bfloat16' });
     for (let li = 0; li < this.layers.length; ++li) {
       const L = this.layers[li];
-      const qkv = be.createTensorHandle([S, nqkv], 'bfloat16');
-      ops.find('matmul')({ output: qkv, M: S, K: H, N: nqkv, batchSize: 1, transposeA: false, transposeB: true,
-                           alpha: 1, beta: 0 }, h, L.wQkv);
-      h.dispose();
-      const heads = (col0: number, nh: number): any => this.view(qkv, [1, S, nh, D], [S * nqkv, nqkv, D, 1], col0);
-      const q = heads(0, Hq), k = heads(nq, Hkv), v = heads(nq + nkv, Hkv);
       const qh = be.createTensorHandle([1, Hq, S, D], 'bfloat16');
-      ops.find('rms_norm_rope')(q, k, { qWeight: L.qNorm, kWeight: L.kNorm, invFreq: this.invFreq, positions, eps,
-                                        qOut: qh, kOut: L.kCache, v, vOut: L.vCache, cachePositions: true });
-      for (const t of [q, k, v, qkv]) t.dispose();
+      if (fuseQkv) {
+        // the projection with qk-norm, RoPE and the cache write in its epilogue: the same values as
+        // the two launches below when their projection is not split over K
+        ops.find('linear_qk_norm_rope')(h, L.wQkv, { qWeight: L.qNorm, kWeight: L.kNorm, invFreq: this.invFreq,
+                                                     positions, eps, qOut: qh, kOut: L.kCache, vOut: L.vCache });
+        h.dispose();
+      } else {
+        const qkv = be.createTensorHandle([S, nqkv], 'bfloat16');
+        ops.find('matmul')({ output: qkv, M: S, K: H, N: nqkv, batchSize: 1, transposeA: false, transposeB: true,
+                             alpha: 1, beta: 0 }, h, L.wQkv);
+        h.dispose();
+        const heads = (col0: number, nh: number): any => this.view(qkv, [1, S, nh, D], [S * nqkv, nqkv, D, 1], col0);
+        const q = heads(0, Hq), k = heads(nq, Hkv), v = heads(nq + nkv, Hkv);
+        ops.find('rms_norm_rope')(q, k, { qWeight: L.qNorm, kWeight: L.kNorm, invFreq: this.invFreq, positions, eps,
+                                          qOut: qh, kOut: L.kCache, v, vOut: L.vCache, cachePositions: true });
+        for (const t of [q, k, v, qkv]) t.dispose();
+      }
       // attention into [1, Hq, S, D] viewed over an [S, Hq D] buffer that o_proj reads as a matrix
       const attn = be.createTensorHandle([S, nq], 'bfloat16');
       const attnView = this.view(attn, [1, Hq, S, D], [S * nq, D, nq, 1], 0);

@@ -223,3 +223,64 @@ def test_linear_add_rms_norm_matches_separate_launches(hip, M, N, K, rows):
     assert ok, err
     if (M, N, K) == (512, 1024, 2048):
         assert kernels.gemm_split_count(M, N, K) > 1     # the fused split path is what ran
+
+
+@pytest.mark.parametrize("S,H,Hq,Hkv,L,pos0", [(512, 1024, 16, 8, 640, 0), (200, 1024, 16, 8, 204, 10),
+                                              (40, 256, 4, 2, 64, 30), (9, 256, 4, 2, 64, 60)])
+def test_linear_qk_norm_rope_matches_projection_then_rms_norm_rope(hip, S, H, Hq, Hkv, L, pos0):
+    """kh_gemm_qk_norm_rope (QKV projection with qk-norm, RoPE and the K/V cache write in its
+    epilogue) against the two launches it replaces -- kh_gemm into [S, (Hq + 2 Hkv) 128], then
+    kh_qk_norm_rope with cache addressing -- bit for bit in q and in both whole caches, on shapes
+    kh_gemm does not split over K (where the model fuses); a ragged last tile (200 rows); positions
+    past the cache (pos0 + S > L) write no K/V row, as in the unfused kernel."""
+    from kandle_amd import kernels
+    from kandle_amd.tensor import HipTensorHandle
+
+    D = 128
+    N = (Hq + 2 * Hkv) * D
+    assert kernels.gemm_split_count(S, N, H) == 1
+    x, _ = seeded(360, (S, H), "bfloat16")
+    w, _ = seeded(361, (N, H), "bfloat16", std=0.05)
+    wq = Tensor(syn.bf16(syn.uniform(362, (D,), 0.5, 1.5))[0], dtype="bfloat16")
+    wk = Tensor(syn.bf16(syn.uniform(363, (D,), 0.5, 1.5))[0], dtype="bfloat16")
+    inv = Tensor(oracle.rope_inv_freq(D, 1e6))
+    pos = Tensor(np.arange(pos0, pos0 + S, dtype=np.int32), dtype="int32")
+    cache0 = syn.bf16(syn.normal(364, (1, Hkv, L, D)))[0]    # rows the launches must leave alone
+
+    def caches():
+        return (Tensor(cache0.copy(), dtype="bfloat16"), Tensor(cache0.copy(), dtype="bfloat16"))
+
+    # unfused: the projection, then qk-norm + RoPE with the cache write
+    qkv = F.linear(x, w)
+    k1, v1 = caches()
+    q1 = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+
+    def heads(col, n):
+        return HipTensorHandle.create_view(qkv.handle.storage, (1, S, n, D), "bfloat16", (S * N, N, D, 1), col)
+
+    kernels.rms_norm_rope(heads(0, Hq), heads(Hq * D, Hkv), {
+        "q_weight": wq.handle, "k_weight": wk.handle, "inv_freq": inv.handle, "positions": pos.handle, "eps": 1e-6,
+        "q_out": q1, "k_out": k1.handle, "v": heads((Hq + Hkv) * D, Hkv), "v_out": v1.handle, "cache_positions": True})
+    # fused
+    k2, v2 = caches()
+    q2 = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+    kernels.linear_qk_norm_rope(x.handle, w.handle, {
+        "q_weight": wq.handle, "k_weight": wk.handle, "inv_freq": inv.handle, "positions": pos.handle, "eps": 1e-6,
+        "q_out": q2, "k_out": k2.handle, "v_out": v2.handle})
+    for a, b in ((Tensor(handle=q1), Tensor(handle=q2)), (k1, k2), (v1, v2)):
+        assert np.array_equal(a.numpy().view(np.uint32), b.numpy().view(np.uint32))
+    if pos0 + S > L:   # rows past the cache were not written
+        assert np.array_equal(k2.numpy()[:, :, :pos0].view(np.uint32),
+                              oracle.from_bf16_bits(cache0[:, :, :pos0]).view(np.uint32))
+
+
+def test_linear_qk_norm_rope_rejects_bad_shapes(hip):
+    from kandle_amd import kernels
+    from kandle_amd.tensor import HipTensorHandle
+
+    x, _ = seeded(370, (16, 64), "bfloat16")
+    w, _ = seeded(371, (4 * 64, 64), "bfloat16")   # head_dim 64: not fused
+    q = HipTensorHandle.create_new((1, 2, 16, 64), "bfloat16")
+    kc = HipTensorHandle.create_new((1, 1, 32, 64), "bfloat16")
+    with pytest.raises(ValueError, match="head_dim 128"):
+        kernels.linear_qk_norm_rope(x.handle, w.handle, {"q_out": q, "k_out": kc, "v_out": kc})

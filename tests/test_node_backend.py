@@ -48,7 +48,7 @@ def test_backend_source_strips_to_loadable_javascript(tmp_path):
     for name in ("flash_attention", "sdpa_masked", "rms_norm", "matmul", "mm", "bmm", "addmm", "baddbmm", "add",
                  "mul", "sub", "silu", "silu_mul", "index_select", "argmax", "copy", "contiguous", "cast", "fill", "neg",
                  "cos", "sin", "arange", "decode_attention", "rms_norm_rope", "copy_", "zeros", "gemv_fused", "gemv_swiglu",
-                 "linear_swiglu", "linear_add_rms_norm", "decode_attention_block", "greedy_advance", "sample"):
+                 "linear_swiglu", "linear_qk_norm_rope", "linear_add_rms_norm", "decode_attention_block", "greedy_advance", "sample"):
         assert name in r["names"], name
     assert r["strides"] == [12, 4, 1]
     assert r["bf16"] == [0x3F80, 0xC020, 0x4049, 0x4780]   # RNE: 3.14159 -> 0x4049, 65504 -> 65536
