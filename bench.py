@@ -700,6 +700,7 @@ def _one_thread():
         return contextlib.nullcontext()
 
 
+MASK_LEAD_WARMUP = 40  # warm-up calls of the explicit-mask leg that leads the headline
 JS_REPEAT = 5   # timed runs of each JavaScript baseline after one untimed run; the median is reported
 
 
@@ -957,9 +958,12 @@ def main():
             # calls 2-5, 0.36 ms for calls 6-20, then 0.278 ms after about 150 calls; a constant
             # cycle count per call, profiles/flash_prefill_c3.md).  The headline itself is still W
             # warm-up calls, a synchronisation, then K timed calls and a synchronisation.
+            # The mask leg takes at least MASK_LEAD_WARMUP warm-up calls (~0.9 ms each), so that with
+            # its timed calls some 50 ms of load precede the headline at any --steps / --warmup.
             log("explicit-mask SDPA at C3 shapes, leading the headline ...")
             handle = {}
-            lead = lambda: handle.setdefault("h", lead_mask.enqueue(args.steps, args.warmup))  # noqa: E731
+            lead = lambda: handle.setdefault("h", lead_mask.enqueue(  # noqa: E731
+                args.steps, max(args.warmup, MASK_LEAD_WARMUP)))
             log(f"{label} ...")
             res[key] = run(args.steps, args.warmup, lead=lead)
             res["mask"] = lead_mask.result(finish_timed(handle["h"]))
