@@ -183,6 +183,18 @@ async function main() {
   ops.find('decode_attention_block')(bqkv, { qNorm: bqn, kNorm: bkn, invFreq: binv, eps: 1e-6, position: bpos,
                                              kCache: bkc, vCache: bvc, wO: bwo, x: bx, scale: 1 / Math.sqrt(128) });
   write('bxo', await bx.dataAsync());
+  // the prefill QKV projection with qk-norm, RoPE and the cache write (positions run past the cache)
+  const qx = t([d2.qS, d2.hidden], 'bfloat16', readU16('qx'));
+  const qw = t([(d2.Hq + 2 * d2.Hkv) * 128, d2.hidden], 'bfloat16', readU16('qw'));
+  const qpos = t([d2.qS], 'int32', Int32Array.from({ length: d2.qS }, (_, i) => d2.qPos0 + i));
+  const qkc = t([1, d2.Hkv, d2.L, 128], 'bfloat16', readU16('bkc'));
+  const qvc = t([1, d2.Hkv, d2.L, 128], 'bfloat16', readU16('bvc'));
+  const qq = backend.createTensorHandle([1, d2.Hq, d2.qS, 128], 'bfloat16');
+  ops.find('linear_qk_norm_rope')(qx, qw, { qWeight: bqn, kWeight: bkn, invFreq: binv, positions: qpos, eps: 1e-6,
+                                            qOut: qq, kOut: qkc, vOut: qvc });
+  write('qqo', await qq.dataAsync());
+  write('qkco', await qkc.dataAsync());
+  write('qvco', await qvc.dataAsync());
   write('bkco', await bkc.dataAsync());
   write('bvco', await bvc.dataAsync());
 
@@ -217,6 +229,7 @@ async function main() {
   for (const hnd of [q, k, v, o, mask, om, x, w, y, a, b, c, out, g, u, h, gT, s1, prod, table, ids, rows, am,
                      un.neg, un.cos, un.sin, ar, rq, rk, rv, wq, wk, inv, pos, kc, vc, qk[0], qk[1], dq, dk, dv, lens, dout,
                      gx, gw, gn, go, gs, gb, gc, sx, sg, so, lx, lw, lr, ln, lo, bqkv, bqn, bkn, binv, bpos, bkc, bvc, bwo, bx,
+                     qx, qw, qpos, qkc, qvc, qq,
                      lg, stok, sctr, slp, nt, ps, sl, lgg, cbuf, cview, csrc, zt]) {
     hnd.dispose();
   }

@@ -4,7 +4,7 @@ looks each kernel up in its operator registry by the name Kandle's dispatcher us
 the reference kernel signature -- flash_attention, sdpa_masked, rms_norm, matmul (linear plus a
 residual), silu_mul, the iterator kernels silu / mul on a transposed view, index_select, argmax,
 neg / cos / sin, arange, rms_norm_rope writing KV caches at device positions, decode_attention over
-ragged cache lengths, the fused gemv_fused / gemv_swiglu / linear_swiglu / linear_add_rms_norm /
+ragged cache lengths, the fused gemv_fused / gemv_swiglu / linear_swiglu / linear_qk_norm_rope / linear_add_rms_norm /
 decode_attention_block, sample, greedy_advance, copy_ into a strided view and zeros -- then disposes
 every handle.  This test writes the inputs and checks each output against the CPU oracle (the fused
 ops bit for bit against the Python binding), that the backend's live device bytes return to where
@@ -100,7 +100,7 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     put_bf16("law", 38, (fu["lN"], fu["lK"]), 0.05)
     put_f32("lar", syn.normal(39, (fu["lM"], fu["lN"])))
     put_bf16("lan", 40, (fu["lN"],))
-    blk = dict(Hq=16, Hkv=8, L=64, hidden=1024, pos=20)
+    blk = dict(Hq=16, Hkv=8, L=64, hidden=1024, pos=20, qS=40, qPos0=30)
     put_bf16("bqkv", 41, (1, (blk["Hq"] + 2 * blk["Hkv"]) * 128))
     put_bf16("bqn", 42, (128,))
     put_bf16("bkn", 43, (128,))
@@ -109,6 +109,8 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     put_bf16("bvc", 45, (1, blk["Hkv"], blk["L"], 128))
     put_bf16("bwo", 46, (blk["hidden"], blk["Hq"] * 128), 0.02)
     put_f32("bx", syn.normal(47, (1, blk["hidden"])))
+    put_bf16("qx", 50, (blk["qS"], blk["hidden"]))
+    put_bf16("qw", 51, ((blk["Hq"] + 2 * blk["Hkv"]) * 128, blk["hidden"]), 0.05)
     smp = dict(V=1000, seed=1234, counter=7)
     put_f32("slg", syn.normal(48, (smp["V"],), 3.0))
     put_f32("cps", syn.normal(49, (4, 3)))
@@ -207,6 +209,17 @@ def test_typescript_backend_runs_registered_kernels(hip, tmp_path):
     np.testing.assert_array_equal(f32_file("bkco", bk.shape), bk.numpy())
     np.testing.assert_array_equal(f32_file("bvco", bv.shape), bv.numpy())
     assert not np.array_equal(bx.numpy(), A["bx"])                 # the block did add into x
+
+    qpos = Tensor(np.arange(blk["qPos0"], blk["qPos0"] + blk["qS"], dtype=np.int32), dtype="int32")
+    qkc, qvc = T("bkc"), T("bvc")
+    qq = HipTensorHandle.create_new((1, blk["Hq"], blk["qS"], 128), "bfloat16")
+    kernels.linear_qk_norm_rope(T("qx").handle, T("qw").handle, {
+        "q_weight": T("bqn").handle, "k_weight": T("bkn").handle, "inv_freq": T("binv", "float32").handle,
+        "positions": qpos.handle, "eps": 1e-6, "q_out": qq, "k_out": qkc.handle, "v_out": qvc.handle})
+    np.testing.assert_array_equal(f32_file("qqo", (1, blk["Hq"], blk["qS"], 128)), qq.data_async())
+    np.testing.assert_array_equal(f32_file("qkco", qkc.shape), qkc.numpy())
+    np.testing.assert_array_equal(f32_file("qvco", qvc.shape), qvc.numpy())
+    assert not np.array_equal(qkc.numpy(), A["bkc"])               # rows 30..63 were written
 
     lg = T("slg", "float32")
     tok = Tensor(np.zeros(1, np.int32), dtype="int32")
