@@ -188,12 +188,12 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int key = key0 + it * KPI + kk;
-    kr[it] = buf_load16(rk, (uint32_t)(((int64_t)key * st.ks + sub * EPL) * sizeof(T)));
+    kr[it] = buf_load16_nt(rk, (uint32_t)(((int64_t)key * st.ks + sub * EPL) * sizeof(T)));
   }
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int key = key0 + it * KPI + kk;
-    vr[it] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + sub * EPL) * sizeof(T)));
+    vr[it] = buf_load16_nt(rv, (uint32_t)(((int64_t)key * st.vs + sub * EPL) * sizeof(T)));
   }
 
   auto unpack = [](const uint4& u, float (&f)[EPL]) {
@@ -396,12 +396,12 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int key = key0 + it * KPI + kk;
-    kr[it] = buf_load16(rk, (uint32_t)(((int64_t)key * st.ks + sub * 8) * 2));
+    kr[it] = buf_load16_nt(rk, (uint32_t)(((int64_t)key * st.ks + sub * 8) * 2));
   }
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int key = key0 + it * KPI + kk;
-    vr[it] = buf_load16(rv, (uint32_t)(((int64_t)key * st.vs + sub * 8) * 2));
+    vr[it] = buf_load16_nt(rv, (uint32_t)(((int64_t)key * st.vs + sub * 8) * 2));
   }
   if constexpr (FUSE) {
     // cos/sin of float(p) * inv_freq[i] for this lane's columns (i = (8 sub + j) mod 64): lane l

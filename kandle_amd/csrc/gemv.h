@@ -175,7 +175,7 @@ struct GemvRows {
         const int c = c0 + cc;
         const int k = c * GV_CHUNK + lane * 8;
         const uint32_t off = k < K ? (uint32_t)((row_of(n, u) * ldw + k) * 2) : w_bytes;
-        wv[u][cc] = c < nch ? buf_load16(rsrc, off) : make_uint4(0, 0, 0, 0);
+        wv[u][cc] = c < nch ? buf_load16_nt(rsrc, off) : make_uint4(0, 0, 0, 0);  // every weight byte once
       }
   }
   __device__ __forceinline__ void issue_first() {
