@@ -151,7 +151,8 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
       }
       if (i < CPTB) {
         const uint32_t bo = in ? ((uint32_t)row * (uint32_t)ldb + (uint32_t)kc) * 2u : 0xffffffffu;
-        bst[stg][i < CPTB ? i : 0] = buf_load16(rb, bo);
+        // B (the weights) with the non-temporal hint: C5 prefill 2.413-2.428 -> 2.396-2.402 ms
+        bst[stg][i < CPTB ? i : 0] = buf_load16_nt(rb, bo);
       }
     }
   };
