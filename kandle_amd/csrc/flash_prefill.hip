@@ -734,11 +734,12 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
 
 constexpr int kWaves = 8;  // waves per workgroup: query rows of 32 * 8 / G, one kv head
 // Short prompts: a grid of fewer than kSmallGrid 8-wave workgroups leaves most CUs idle and its time
-// is the key loop of the last query block.  Such launches use workgroups of kSmallWaves waves over
-// kSmallBN-key tiles instead: BMQ shrinks with the wave count, so there are 8 / kSmallWaves times
-// as many workgroups, and each wave has a SIMD to itself.
+// is the key loop of the last query block.  Such launches use workgroups of max(G, 2) waves (G <= 4)
+// over kSmallBN-key tiles instead: one 32-row slot per query head, so there are 8 / waves times as
+// many workgroups, and each wave has a SIMD to itself.  C5 prefill (S = 512, G = 2): 2-wave
+// workgroups (128 of them) 2.392 -> 2.355 ms over 28 layers against 4-wave (64); 64-key tiles
+// measured the same as 128-key ones.
 constexpr int kSmallGrid = 256;
-constexpr int kSmallWaves = 4;
 constexpr int kSmallBN = 128;
 
 template <int BN, int WAVES, bool CAUSAL, int D>
@@ -760,11 +761,16 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
-  if (nblk64 < kSmallGrid && G <= kSmallWaves) {
+  if (nblk64 < kSmallGrid && G <= 2) {
     if (causal)
-      launch_fwd<kSmallBN, kSmallWaves, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+      launch_fwd<kSmallBN, 2, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
     else
-      launch_fwd<kSmallBN, kSmallWaves, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+      launch_fwd<kSmallBN, 2, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+  } else if (nblk64 < kSmallGrid && G == 4) {
+    if (causal)
+      launch_fwd<kSmallBN, 4, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+    else
+      launch_fwd<kSmallBN, 4, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
   } else if (causal && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
     // Enough causal query blocks for every CU to take several: one resident workgroup per CU.
     static_assert(kPersistWaves == kWaves, "the persistent kernel's query blocks are the tile kernel's");
