@@ -285,7 +285,7 @@ def _write_ts_inputs(cfg, weights, prompt):
     return d
 
 
-def _run_ts_host(d, new_tokens, py_tokens):
+def _run_ts_host(d, new_tokens, py_tokens, activations="float32"):
     """C5 generation driven from Node through the TypeScript model and the N-API addon: one warm-up
     generation of 8 tokens (captures the prefill and decode graphs), then the timed one.  Its tokens
     must equal the Python host's."""
@@ -294,8 +294,8 @@ def _run_ts_host(d, new_tokens, py_tokens):
 
     try:
         out = subprocess.run(["node", TS_EXAMPLE, os.path.join(d, "config.json"), os.path.join(d, "model.safetensors"),
-                              os.path.join(d, "prompt.json"), str(new_tokens)], capture_output=True, text=True,
-                             timeout=300)
+                              os.path.join(d, "prompt.json"), str(new_tokens), "--activations", activations],
+                             capture_output=True, text=True, timeout=300)
     finally:
         shutil.rmtree(d, ignore_errors=True)
     if out.returncode != 0:
@@ -307,23 +307,31 @@ def _run_ts_host(d, new_tokens, py_tokens):
     return r
 
 
-def prep_model(new_tokens=128, prompt_len=512, use_graph=True, ts_host=False):
-    """Config C5: Qwen3-0.6B architecture, random N(0, 0.02) bf16 weights, a 512-token prefill of
-    uniform-random ids, then 128 greedy decode steps (the decode step captured once as a HIP graph
-    and replayed).  One warm-up generation of 8 tokens precedes the timed one; it runs the prefill
-    eagerly (reported as prefill_eager_ms) and captures it, so the timed prefill is a graph replay,
-    as in a server that captures one prefill graph per prompt-length bucket."""
-    from kandle_amd.model_utils import Qwen3Config, Qwen3ForCausalLM, init_qwen3_weights
-    from kandle_amd import synthetic as syn
+def c5_weights():
+    """(config, weights) of C5: Qwen3-0.6B architecture, random N(0, 0.02) bf16 weights (seed 7)."""
+    from kandle_amd.model_utils import Qwen3Config, init_qwen3_weights
 
     cfg = Qwen3Config()
     t0 = time.perf_counter()
     w = init_qwen3_weights(cfg, seed=7)
     log(f"model weights generated in {time.perf_counter() - t0:.1f} s")
+    return cfg, w
+
+
+def prep_model(cfg, w, new_tokens=128, prompt_len=512, use_graph=True, ts_host=False, activations="float32"):
+    """Config C5: Qwen3-0.6B architecture, random N(0, 0.02) bf16 weights, a 512-token prefill of
+    uniform-random ids, then 128 greedy decode steps (the decode step captured once as a HIP graph
+    and replayed), with the given activation dtype (float32: the reference's arithmetic;
+    bfloat16: activations rounded to bf16 between kernels).  One warm-up generation of 8 tokens
+    precedes the timed one; it runs the prefill eagerly (reported as prefill_eager_ms) and
+    captures it, so the timed prefill is a graph replay, as in a server that captures one prefill
+    graph per prompt-length bucket."""
+    from kandle_amd.model_utils import Qwen3ForCausalLM
+    from kandle_amd import synthetic as syn
+
     prompt = syn.randint(8, (prompt_len,), 0, cfg.vocab_size)
-    model = Qwen3ForCausalLM(cfg, w, max_seq_len=prompt_len + new_tokens)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=prompt_len + new_tokens, activations=activations)
     ts_dir = _write_ts_inputs(cfg, w, prompt) if ts_host else None
-    del w
 
     def run(steps, warmup):
         try:
@@ -339,7 +347,7 @@ def prep_model(new_tokens=128, prompt_len=512, use_graph=True, ts_host=False):
         if not use_graph:  # every step eager: time all of them
             timing["replay_ms"], timing["replay_steps"] = timing["decode_ms"], new_tokens
         model.dispose()
-        ts = _run_ts_host(ts_dir, new_tokens, toks) if ts_dir is not None else None   # removes ts_dir
+        ts = _run_ts_host(ts_dir, new_tokens, toks, activations) if ts_dir is not None else None   # removes ts_dir
         H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
         Hq, Hkv, Lyr = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
         layer_w = H * (Hq + 2 * Hkv) * D + Hq * D * H + 3 * H * I            # projection weights per layer
@@ -351,8 +359,8 @@ def prep_model(new_tokens=128, prompt_len=512, use_graph=True, ts_host=False):
         weight_bytes = 2.0 * (Lyr * (layer_w + 2 * H + 2 * D) + cfg.vocab_size * H + H)
         steps_r = timing.get("replay_steps", 0)
         mean_len = prompt_len + 1 + (new_tokens + 1) / 2.0
-        kv_bytes = Lyr * 2 * Hkv * D * 2 * mean_len
-        return {"prefill_ms": timing["prefill_ms"], "prefill_issue": timing["prefill_issue"],
+        kv_bytes = Lyr * 2 * Hkv * D * (4 if activations == "float32" else 2) * mean_len
+        return {"activations": activations, "prefill_ms": timing["prefill_ms"], "prefill_issue": timing["prefill_issue"],
                 "prefill_eager_ms": warm["prefill_ms"], "prefill_flops": prefill_flops, "prompt_len": prompt_len,
                 "new_tokens": new_tokens, "replay_ms": timing.get("replay_ms"), "replay_steps": steps_r,
                 "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8],
@@ -430,30 +438,35 @@ GEMM_SHAPES = (("qkv", 4096, 1024, "bf16"), ("o_proj", 1024, 2048, "f32"), ("gat
                ("down", 1024, 3072, "f32"))
 
 
-def bench_gemm(steps, warmup, M=512, eager=False):
+def bench_gemm(steps, warmup, M=512, eager=False, act="bfloat16"):
     """The four projection GEMMs of a C5 prefill layer (M = 512 tokens, bf16 weights [N, K], fp32
-    accumulate): y = x W^T, bf16 out for qkv and gate/up, fp32 out plus the fp32 residual (beta = 1)
-    for o_proj and down, as in the model.  Per shape: kh_gemm device time (calls replayed from a
-    graph, as the model's prefill runs them; with eager, launched one by one from the host, the form
-    a kernel tracer or counter run takes) and TFLOP/s."""
+    accumulate): y = x W^T, the activation dtype out for qkv and gate/up, fp32 out plus the fp32
+    residual (beta = 1) for o_proj and down, as in the model.  act: the activations' dtype
+    (bfloat16, or float32: x fp32, split into bf16 hi + lo on the MFMA tiles).  Per shape: device
+    time (calls replayed from a graph, as the model's prefill runs them; with eager, launched one by
+    one from the host, the form a kernel tracer or counter run takes) and TFLOP/s of the algorithmic
+    2 M N K."""
     import ctypes as C
 
     from kandle_amd import Tensor, _lib
 
+    f32 = act == "float32"
+    a_code = 0 if f32 else 1
     out = {}
     for name, N, K, odt in GEMM_SHAPES:
-        x = bf16_tensor(701, (M, K))
+        x = Tensor(np.random.default_rng(701).normal(size=(M, K)).astype(np.float32)) if f32 else \
+            bf16_tensor(701, (M, K))
         w = bf16_tensor(702, (N, K))
         ny = N // 2 if odt == "swiglu" else N
-        y = Tensor(np.zeros((M, ny), np.float32), dtype="float32" if odt == "f32" else "bfloat16")
+        y = Tensor(np.zeros((M, ny), np.float32), dtype="float32" if (odt == "f32" or f32) else "bfloat16")
         res = Tensor(np.zeros((M, N), np.float32), dtype="float32") if odt == "f32" else None
         vp = lambda t: C.c_void_p(t.handle.data_ptr() if t is not None else 0)  # noqa: E731
         if odt == "swiglu":
-            call = lambda: _lib.call("kh_gemm_swiglu", vp(x), K, vp(w), K, vp(y), ny, M, ny, K)  # noqa: E731
+            call = lambda: _lib.call("kh_gemm_swiglu", vp(x), K, vp(w), K, vp(y), ny, M, ny, K, a_code)  # noqa: E731
         else:
-            call = lambda: _lib.call("kh_gemm", vp(x), K, vp(w), K, vp(y), N, vp(res), N, vp(None), M, N, K,  # noqa: E731
-                                     C.c_float(1.0), C.c_float(1.0 if res is not None else 0.0), 1, 1,
-                                     0 if odt == "f32" else 1)
+            call = lambda: _lib.call("kh_gemm_ex", vp(x), K, a_code, vp(w), K, 1, vp(y), N, vp(res), N,  # noqa: E731
+                                     vp(None), M, N, K, C.c_float(1.0), C.c_float(1.0 if res is not None else 0.0), 1,
+                                     0 if (odt == "f32" or f32) else 1)
         # Device time: 20 calls captured as one graph and replayed (no host launch cost per call).
         from kandle_amd.graphs import HipGraph
 
@@ -475,6 +488,7 @@ def bench_gemm(steps, warmup, M=512, eager=False):
             if t is not None:
                 t.dispose()
     tot = sum(v["us"] for v in out.values())
+    out["activations"] = act
     out["layer_us"] = round(tot, 2)
     out["layer_TFLOP/s"] = round(sum(2.0 * M * n * k for _, n, k, _ in GEMM_SHAPES) / (tot * 1e-6) / 1e12, 1)
     return out
@@ -508,7 +522,7 @@ def bench_gemv(steps, warmup):
         vp = lambda t: C.c_void_p(t.handle.data_ptr() if t is not None else 0)  # noqa: E731
         call = lambda: _lib.call("kh_gemv_fused", pro, vp(x), vp(x2), vp(nw), C.c_float(1e-6), vp(w), K, vp(y),  # noqa
                                  vp(cin), vp(None), N, K, C.c_float(1.0), C.c_float(1.0 if res else 0.0),
-                                 0 if res else 1)
+                                 0 if res else 1, 1)
         call()
         g = HipGraph()
         with g.capture():
@@ -933,8 +947,15 @@ def main():
         if not ts_host:
             log("C5 from the TypeScript host: skipped (" + ("--no-ts-host" if args.no_ts_host else
                 "node, the N-API addon or the stripped TypeScript is missing: run __graft_entry__.build()") + ")")
-        legs.append(("model", "Qwen3-0.6B C5", prep_model(use_graph=not args.eager_decode,
-                                                          ts_host=ts_host and not args.eager_decode)))
+        cfg5, w5 = c5_weights()
+        # float32 activations (the reference's arithmetic, the C5 parity mode) and, as a separately
+        # labelled line, bfloat16 activations
+        legs.append(("model", "Qwen3-0.6B C5 (float32 activations)",
+                     prep_model(cfg5, w5, use_graph=not args.eager_decode, ts_host=ts_host and not args.eager_decode,
+                                activations="float32")))
+        legs.append(("model_bf16", "Qwen3-0.6B C5 (bfloat16 activations)",
+                     prep_model(cfg5, w5, use_graph=not args.eager_decode, activations="bfloat16")))
+        del w5
     if args.only in (None, "decode"):
         legs.append(("decode", "decode C4", prep_decode()))
     if args.only in (None, "norm"):
@@ -987,6 +1008,7 @@ def main():
     if args.only == "gemm":
         log("C5 prefill GEMMs ...")
         res["gemm"] = bench_gemm(args.steps, args.warmup, eager=args.eager_gemm)
+        res["gemm_f32"] = bench_gemm(args.steps, args.warmup, eager=args.eager_gemm, act="float32")
     if args.only == "gemv":
         log("C5 decode GEMVs ...")
         res["gemv"] = bench_gemv(args.steps, args.warmup)
@@ -1055,28 +1077,34 @@ def main():
         if "value" not in line:
             line.update({"value": round(gf, 1), "unit": "GFLOP/s", "ms_per_step": round(c1["wall_ms"], 4),
                          "config": {"workload": "C1 SDPA fp32"}})
-    if "model" in res:
-        m = res["model"]
+    for mkey in ("model", "model_bf16"):
+        if mkey not in res:
+            continue
+        m = res[mkey]
         p_tps = m["prompt_len"] / (m["prefill_ms"] * 1e-3)
         p_tf = m["prefill_flops"] / (m["prefill_ms"] * 1e-3) / 1e12
         d_ms = m["replay_ms"] / m["replay_steps"]
         d_gbps = m["step_bytes"] / (d_ms * 1e-3) / 1e9
-        line["model"] = {
+        line[mkey] = {
             "workload": "C5 Qwen3-0.6B (28 layers, hidden 1024, 16/8 heads, vocab 151936, random bf16 weights): "
                         f"{m['prompt_len']}-token prefill + {m['new_tokens']} greedy decode steps",
+            "activations": m["activations"] + (" (the reference's float32 arithmetic; bf16 weights, fp32 "
+                                               "activations and KV cache)" if m["activations"] == "float32" else
+                                               " (activations and KV cache rounded to bf16 between kernels)"),
             "prefill_ms": round(m["prefill_ms"], 3), "prefill_tokens_per_s": round(p_tps, 1),
             "prefill": {"bound": "mfma", "achieved": round(p_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(p_tf / PEAK_BF16_TFLOPS, 4), "flops": m["prefill_flops"]},
             "decode_ms_per_token": round(d_ms, 4), "decode_tokens_per_s": round(1e3 / d_ms, 1),
             "decode": {"bound": "hbm", "achieved": round(d_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                       "frac": round(d_gbps / PEAK_HBM_GBPS, 4), "bytes_per_step": m["step_bytes"]},
+                       "frac": round(d_gbps / PEAK_HBM_GBPS, 4),
+                       "bytes_per_step": m["step_bytes"]},
             "decode_steps_timed": m["replay_steps"], "decode_total_ms": round(m["decode_ms"], 3),
             "decode_issue": "eager" if args.eager_decode else "hip graph replay",
             "prefill_issue": m["prefill_issue"], "prefill_eager_ms": round(m["prefill_eager_ms"], 3),
             "first_tokens": m["tokens"]}
         if m.get("ts_host") is not None:
             t = m["ts_host"]
-            line["model"]["ts_host"] = {
+            line[mkey]["ts_host"] = {
                 "workload": "the same generation driven from Node (packages/backend-hip/examples/generate.js: the "
                             "TypeScript Qwen3 model over the N-API addon)",
                 "prefill_ms": round(t["prefill_ms"], 3), "prefill_issue": "hip graph replay",
@@ -1107,7 +1135,8 @@ def main():
     if "gemm" in res:
         gm = res["gemm"]
         line.update({"value": gm["layer_TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": round(gm["layer_us"] * 1e-3, 4),
-                     "config": {"workload": "C5 prefill projection GEMMs of one layer, M=512", **gm},
+                     "config": {"workload": "C5 prefill projection GEMMs of one layer, M=512", **gm,
+                                **({"float32_activations": res["gemm_f32"]} if "gemm_f32" in res else {})},
                      "roofline": {"bound": "mfma", "achieved": gm["layer_TFLOP/s"], "peak": PEAK_BF16_TFLOPS,
                                   "unit": "TFLOP/s", "frac": round(gm["layer_TFLOP/s"] / PEAK_BF16_TFLOPS, 4),
                                   "traffic": None}})

@@ -198,20 +198,23 @@ int kh_philox4x32_10(uint64_t seed, const uint32_t* counters, int64_t n, uint32_
 
 /* The attention block of one decode step of one sequence, from the raw q/k/v projection row to the
  * residual update: qk-norm + RoPE of the q heads and of the new token's k row (per-head RMSNorm with
- * q_norm_w / k_norm_w and eps, angles float(p) * inv_freq[i]); the new k and v rows written into the
- * caches at row p = *position; split-K attention of the q heads over cache rows [0, p] (GQA,
- * scale); the merge; then x += o W_o^T (w_o bf16 [n_out, hq*128] with row stride ldw, x fp32
- * [n_out]).  qkv: bf16 [hq*128 + 2*hkv*128] (q heads, then k, then v).  Caches bf16 [hkv][max_len]
- * [128] with element strides cache_strides = {k head, k row, v head, v row}.  The position is read
- * from device memory, so a captured step replays at every position.  Two kernels (three when the
- * cache exceeds 8 chunks of 256 keys).  Fuses the decode path of GroupedQueryAttention.forward
+ * q_norm_w / k_norm_w (bf16 [128]) and eps, angles float(p) * inv_freq[i]); the new k and v rows
+ * written into the caches at row p = *position; split-K attention of the q heads over cache rows
+ * [0, p] (GQA, scale); the merge; then x += o W_o^T (w_o bf16 [n_out, hq*128] with row stride ldw,
+ * x fp32 [n_out]).  qkv: [hq*128 + 2*hkv*128] (q heads, then k, then v) and the caches
+ * [hkv][max_len][128] (element strides cache_strides = {k head, k row, v head, v row}) have `dtype`:
+ * KH_BF16 (q and the new k row rounded to bf16 after RoPE, the merged row rounded to bf16 before
+ * o_proj, as the unfused launches store them) or KH_F32 (every value kept in fp32: the reference's
+ * float32 activations).  The position is read from device memory, so a captured step replays at
+ * every position.  Two kernels (three when the cache exceeds 8 split-K chunks: 256 keys each for
+ * bf16, 128 for fp32).  Fuses the decode path of GroupedQueryAttention.forward
  * (reference: packages/model-utils/src/attention/gqa.ts:246-430: projections, q_norm/k_norm,
  * RoPE, KV-cache update, SDPA, o_proj; kv-cache.ts:164-212) with the o_proj residual add of
  * Qwen3DecoderLayer.forward (qwen3/decoder_layer.ts:191-241). */
 int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                               float eps, const int32_t* position, void* k_cache, void* v_cache, int hq, int hkv,
                               int64_t max_len, const int64_t* cache_strides, float scale, const void* w_o,
-                              int64_t ldw, int64_t n_out, float* x);
+                              int64_t ldw, int64_t n_out, float* x, int dtype);
 
 /* ------------------------------------------------------------------ hot path ----------------- */
 
@@ -311,9 +314,22 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
             const void* cin, int64_t ldcin, const void* bias,
             int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b, int dtype, int out_dtype);
 
-/* h[m, f] = silu(g[m, f]) * u[m, f], g = x W_gate^T and u = x W_up^T (bf16 in, fp32 accumulate,
- * g and u rounded to bf16 before the product and h rounded to bf16: the values the separate GEMM
- * and silu*mul produce), for m rows and n_half = intermediate features, from ONE weight w_gu
+/* kh_gemm with A and B of their own dtypes.  Beyond kh_gemm's pairs it takes a float32 A with a
+ * bfloat16 B (float32 C, Cin, bias): the reference's float32 matmul of float32 activations by
+ * bfloat16 checkpoint weights, which the reference widens to float32 on load
+ * (packages/core/src/io/safetensor/dtypes.ts:17-31), without widening them.  With trans_b = 1 and
+ * m > 8 the MFMA tiles split each A value into bfloat16 hi = bf16(a) and lo = bf16(a - hi) and
+ * accumulate W hi + W lo in fp32 (relative error of each product 2^-17 or less); one-row and
+ * skinny products multiply in fp32.  A bfloat16 A with a float32 B is refused.  Same matmul
+ * contract as kh_gemm (reference: packages/core/src/dispatch/matmulOps.ts:32-125, :408-496). */
+int kh_gemm_ex(const void* a, int64_t lda, int a_dtype, const void* b, int64_t ldb, int b_dtype, void* c,
+               int64_t ldc, const void* cin, int64_t ldcin, const void* bias, int64_t m, int64_t n, int64_t k,
+               float alpha, float beta, int trans_b, int out_dtype);
+
+/* h[m, f] = silu(g[m, f]) * u[m, f], g = x W_gate^T and u = x W_up^T (x_dtype KH_BF16: bf16 x,
+ * fp32 accumulate, g and u rounded to bf16 before the product and h rounded to bf16 -- the values
+ * the separate GEMM and silu*mul produce; KH_F32: fp32 x split as kh_gemm_ex does, g, u and h kept
+ * in fp32, h fp32), for m rows and n_half = intermediate features, from ONE weight w_gu
  * [2 n_half, k] whose rows interleave gate and up in blocks of 8: rows 16i .. 16i+7 are gate rows
  * 8i .. 8i+7 and rows 16i+8 .. 16i+15 the matching up rows.  x [m, k] and h [m, n_half] with row
  * strides ldx / ldh (elements); n_half, k, ldx, ldw multiples of 8; x and w_gu 16-byte aligned.
@@ -321,7 +337,7 @@ int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int
  * projections with silu and mul (reference: packages/model-utils/src/mlp/swiglu.ts:119-134;
  * packages/backend-webgpu/src/kernels/pointwise/ops.ts:299 silu, :329 mul). */
 int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,
-                   int64_t n_half, int64_t k);
+                   int64_t n_half, int64_t k, int x_dtype);
 
 /* The QKV projection of a prefill fused with qk-norm, RoPE and the KV-cache write:
  *   qkv[t, :] = x[t, :] W^T      (bf16 x [M, k] with row stride ldx, M = n_batch * seq_len tokens;
@@ -333,8 +349,10 @@ int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, vo
  * written at q_out + b*st[0] + s*st[1] + h*st[2]; k rows normed with wk and rotated, written at
  * k_out + b*st[3] + row*st[4] + h*st[5]; v rows unchanged at v_out + b*st[6] + row*st[7] + h*st[8],
  * where row = p when kv_cache_len > 0 (positions outside [0, kv_cache_len) write no K/V row) and
- * row = s otherwise (`strides` holds these 9 element strides, multiples of 8).  head_dim must be
- * 128; operands 16-byte aligned; k, ldx, ldw multiples of 8.  The [M, (hq + 2 hkv) * 128]
+ * row = s otherwise (`strides` holds these 9 element strides, 16-byte multiples).  `dtype` is that
+ * of x, q_out and the caches: KH_BF16 as described, or KH_F32 (x split as kh_gemm_ex does, the
+ * projection kept in fp32 -- not rounded -- before qk-norm and RoPE, fp32 rows written).  head_dim
+ * must be 128; operands 16-byte aligned; k, ldx, ldw multiples of 8.  The [M, (hq + 2 hkv) * 128]
  * projection output is never written.  Each output sums over all of k: the values kh_gemm followed
  * by kh_qk_norm_rope produce whenever kh_gemm runs its MFMA tiles unsplit (M > 8 and
  * kh_gemm_split_count() == 1).  Fuses GroupedQueryAttention's q/k/v projections with
@@ -343,22 +361,23 @@ int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, vo
 int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
                          int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim, const void* wq,
                          const void* wk, const float* inv_freq, const int32_t* positions, void* q_out, void* k_out,
-                         void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len);
+                         void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len, int dtype);
 
-/* The split count kh_gemm uses for a bf16 [m, k] x [n, k]^T product with contiguous, 16-byte
- * aligned operands (1: not split).  A caller that splits the same product with
+/* The split count kh_gemm uses for a [m, k] x [n, k]^T product with bf16 weights and contiguous,
+ * 16-byte aligned operands, whether A is bf16 or fp32 (1: not split).  A caller that splits the same product with
  * kh_gemm_splitk_partials and adds the partials in split order reproduces kh_gemm bit for bit. */
 int kh_gemm_split_count(int64_t m, int64_t n, int64_t k, int* splits);
 
 /* The split-K stage of kh_gemm alone: part[s][i][j] (fp32, s < splits, row-major [m, n], split s
  * at part + s*m*n) = the sum over split s's k range of a[i, :] * b[j, :] (bf16 a [m, k] with row
- * stride lda, b [n, k] with row stride ldb), k ranges of ceil(k / splits) rounded up to 128.
+ * stride lda -- or fp32 a with a_dtype KH_F32, split as kh_gemm_ex does -- and b [n, k] with row
+ * stride ldb), k ranges of ceil(k / splits) rounded up to 128.
  * splits must equal kh_gemm_split_count's count for this shape (and the operands meet the MFMA
  * path's alignment: 16-byte aligned, k, lda, ldb multiples of 8).  The producer half of the
  * projection + residual + RMSNorm fusion below (no reference counterpart as a separate step:
  * it is the matmul of packages/core/src/dispatch/matmulOps.ts:32-125 before its epilogue). */
 int kh_gemm_splitk_partials(const void* a, int64_t lda, const void* b, int64_t ldb, float* part,
-                            int64_t m, int64_t n, int64_t k, int splits);
+                            int64_t m, int64_t n, int64_t k, int splits, int a_dtype);
 
 /* Residual add of split-K partials followed by RMSNorm, one launch:
  *   x[r, :] = (part[0][r, :] + ... + part[splits-1][r, :]) + x[r, :]    (fp32, summed in split
@@ -375,7 +394,8 @@ int kh_add_rms_norm(const float* part, int splits, int64_t split_stride, float* 
 /* One-row projection (decode) with the producing op fused in front of it:
  *   c[j] = alpha * sum_i x'[i] * w[j, i] + beta * cin[j] (+ bias[j]),  j < n, i < k,
  * w bf16 [n, k] with row stride ldw (the nn.Linear weight), c/cin/bias of out_dtype, where x' is
- * the activation row exactly as the unfused producer would have stored it (rounded to bf16):
+ * the activation row exactly as the unfused producer would have stored it: with x_dtype KH_BF16
+ * rounded to bf16 (and x, x2 below bf16), with x_dtype KH_F32 kept in fp32 (x, x2 fp32):
  *   prologue 0: x' = x (bf16 [k]) — plain linear (reference: packages/core/src/nn/modules/linear/Linear.ts:135-137);
  *   prologue 1: x' = rms_norm(x, norm_w, eps) with x the fp32 residual row [k] and norm_w bf16 [k]
  *               — RMSNorm then linear (reference: packages/core/src/nn/modules/normalization/RMSNorm.ts:92-99;
@@ -388,20 +408,21 @@ int kh_add_rms_norm(const float* part, int splits, int64_t split_stride, float* 
  * Needs k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w and k <= 16384.  cin may alias c. */
 int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps,
                   const void* w, int64_t ldw, void* c, const void* cin, const void* bias,
-                  int64_t n, int64_t k, float alpha, float beta, int out_dtype);
+                  int64_t n, int64_t k, float alpha, float beta, int out_dtype, int x_dtype);
 
 /* One-row SwiGLU projection (decode): h[f] = silu(g_f) * u_f, f < n_half, bf16 out, where g and u
  * are the gate and up projections of the activation row x' (prologue 0: x' = x, bf16 [k];
  * prologue 1: x' = rms_norm(x, norm_w, eps) of the fp32 residual row, as kh_gemv_fused) by the
  * interleaved gate/up weight w_gu [2 n_half, k] of kh_gemm_swiglu (blocks of 8 rows; row stride
- * ldw).  g and u are rounded to bf16 before the product and h is rounded to bf16: the values that
- * kh_gemv_fused's gate/up projection followed by its silu * mul prologue produce, without the
- * [2 n_half] gate/up row.  Fuses SwiGLUMLP's gate and up projections with silu and mul for one
+ * ldw).  x_dtype KH_BF16: x bf16 (prologue 0), g and u rounded to bf16 before the product and h
+ * stored as bf16 -- the values that kh_gemv_fused's gate/up projection followed by its silu * mul
+ * prologue produce, without the [2 n_half] gate/up row; KH_F32: x fp32 (prologue 0), x', g, u
+ * and h kept in fp32, h fp32.  Fuses SwiGLUMLP's gate and up projections with silu and mul for one
  * token (reference: packages/model-utils/src/mlp/swiglu.ts:119-134; RMSNorm before it:
  * packages/core/src/nn/modules/normalization/RMSNorm.ts:92-99).  Needs n_half % 8 == 0,
  * k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w_gu and k <= 16384. */
 int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, const void* w_gu, int64_t ldw,
-                   void* h, int64_t n_half, int64_t k);
+                   void* h, int64_t n_half, int64_t k, int x_dtype);
 
 #ifdef __cplusplus
 }

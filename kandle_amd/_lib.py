@@ -63,7 +63,7 @@ SIGNATURES = {
     "kh_philox4x32_10": [C.c_uint64, _vp, _i64, _vp],
     "kh_sample_set_path": [_i],
     "kh_decode_attention_block": [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i64, _vp, _f, _vp, _i64, _i64,
-                                  _vp],
+                                  _vp, _i],
     "kh_graph_begin_capture": [],
     "kh_graph_end_capture": [_vpp],
     "kh_graph_launch": [_vp],
@@ -75,13 +75,14 @@ SIGNATURES = {
     "kh_decode_attention": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
     "kh_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
     "kh_gemm": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _f, _f, _i, _i, _i],
-    "kh_gemv_fused": [_i, _vp, _vp, _vp, _f, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _f, _f, _i],
-    "kh_gemv_swiglu": [_i, _vp, _vp, _f, _vp, _i64, _vp, _i64, _i64],
-    "kh_gemm_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64],
+    "kh_gemm_ex": [_vp, _i64, _i, _vp, _i64, _i, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _f, _f, _i, _i],
+    "kh_gemv_fused": [_i, _vp, _vp, _vp, _f, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _f, _f, _i, _i],
+    "kh_gemv_swiglu": [_i, _vp, _vp, _f, _vp, _i64, _vp, _i64, _i64, _i],
+    "kh_gemm_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i],
     "kh_gemm_qk_norm_rope": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                             _i64p, _f, _i64],
+                             _i64p, _f, _i64, _i],
     "kh_gemm_split_count": [_i64, _i64, _i64, C.POINTER(C.c_int)],
-    "kh_gemm_splitk_partials": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i],
+    "kh_gemm_splitk_partials": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i, _i],
     "kh_add_rms_norm": [_vp, _i, _i64, _vp, _vp, _vp, _i64, _i64, _f, _i],
 }
 

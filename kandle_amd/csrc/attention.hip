@@ -8,6 +8,8 @@
 #include <cfloat>
 #include <cmath>
 
+#include <type_traits>
+
 #include "attention.h"
 
 using namespace kh;
@@ -297,8 +299,8 @@ struct DecodeFuse {
   const uint16_t* wk = nullptr;       // k_norm weight [128], bf16
   const float* inv_freq = nullptr;    // RoPE inverse frequencies [64]
   const int32_t* position = nullptr;  // the new token's position p; the sequence has p + 1 keys
-  const uint16_t* k_new = nullptr;    // raw k rows of the new token [hkv][128]
-  const uint16_t* v_new = nullptr;    // raw v rows [hkv][128]
+  const void* k_new = nullptr;        // raw k rows of the new token [hkv][128] (the caches' type)
+  const void* v_new = nullptr;        // raw v rows [hkv][128]
   float eps = 0.f;
 };
 
@@ -333,26 +335,68 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
                     pack_bf16x2(f[6], f[7]));
 }
 
-// Same unit of work and output as decode_partial_kernel, for bf16: the 16 lanes of a DPP row hold
-// one key row (8 columns each), so a score is an in-lane dot product plus a 4-step DPP row sum, and
-// the 4 rows of a wave (key slots kk) keep separate softmax states (m, l, o) -- no cross-row
-// shuffles.  The 16 states of the workgroup (4 waves x 4 rows) are combined once through LDS.
+// Eight consecutive elements of a row as raw 16-byte words: one for bf16, two for fp32.
+template <typename T>
+struct Row8 {
+  static constexpr int NV = (int)sizeof(T) / 2;
+  uint4 u[NV];
+  __device__ __forceinline__ void to_f32(float (&f)[8]) const {
+    if constexpr (NV == 1) {
+      unpack8(u[0], f);
+    } else {
+      f[0] = __uint_as_float(u[0].x); f[1] = __uint_as_float(u[0].y);
+      f[2] = __uint_as_float(u[0].z); f[3] = __uint_as_float(u[0].w);
+      f[4] = __uint_as_float(u[1].x); f[5] = __uint_as_float(u[1].y);
+      f[6] = __uint_as_float(u[1].z); f[7] = __uint_as_float(u[1].w);
+    }
+  }
+  // the row as T stores it: rounded to bf16, or the fp32 values
+  __device__ __forceinline__ void from_f32(const float (&f)[8]) {
+    if constexpr (NV == 1) {
+      u[0] = pack8(f);
+    } else {
+      u[0] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+      u[1] = make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7]));
+    }
+  }
+  __device__ __forceinline__ void load(const T* p) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) u[i] = reinterpret_cast<const uint4*>(p)[i];
+  }
+  __device__ __forceinline__ void store(T* p) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) reinterpret_cast<uint4*>(p)[i] = u[i];
+  }
+  // raw buffer loads (non-temporal) at byte offset off of range r
+  __device__ __forceinline__ void load_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) u[i] = buf_load16_nt(r, off + 16u * i);
+  }
+};
+
+// Same unit of work and output as decode_partial_kernel: the 16 lanes of a DPP row hold one key
+// row (8 columns each: one 16-byte load for bf16, two for fp32), so a score is an in-lane dot
+// product plus a 4-step DPP row sum, and the 4 rows of a wave (key slots kk) keep separate softmax
+// states (m, l, o) -- no cross-row shuffles.  The 16 states of the workgroup (4 waves x 4 rows)
+// are combined once through LDS.  A wave covers 16 key rows per slot with bf16 (64 keys, chunks
+// of 256) and 8 with fp32 (32 keys, chunks of 128), so both keep 16 KiB of K and V in flight.
 // FUSE (decode attention block, one sequence): Q holds the raw q heads; each workgroup applies
-// qk-norm + RoPE to its G heads (rounded to bf16, as the unfused path stores them).  The wave whose
-// keys include the new token p normalises and rotates that token's k row, writes it and the v row
-// into the caches at row p, and scores it from registers (the stale cache row it loaded is masked):
-// the new key joins the softmax state of the DPP row that owns it, with no data dependence on the
-// cache write.  Only this workgroup reads row p in this launch.
-template <int G, bool FUSE = false>
-__global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t* __restrict__ Q,
-                                                                  const uint16_t* __restrict__ K,
-                                                                  const uint16_t* __restrict__ V,
+// qk-norm + RoPE to its G heads (rounded to bf16 as the unfused path stores them, or kept in fp32
+// with fp32 caches).  The wave whose keys include the new token p normalises and rotates that
+// token's k row, writes it and the v row into the caches at row p, and scores it from registers
+// (the stale cache row it loaded is masked): the new key joins the softmax state of the DPP row
+// that owns it, with no data dependence on the cache write.  Only this workgroup reads row p in
+// this launch.
+template <typename T, int G, bool FUSE = false>
+__global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                                                                  const T* __restrict__ V,
                                                                   const int32_t* __restrict__ lens, int uniform_len,
                                                                   int max_len, int hq, int hkv, AttnStrides st,
                                                                   float scale, int max_chunks,
                                                                   float* __restrict__ part, DecodeFuse fz) {
-  constexpr int D = 128, NI = 16, KPI = 4, KPW = NI * KPI, CHUNK = DC_WAVES * KPW, NS = DC_WAVES * KPI;
-  static_assert(CHUNK == dc_chunk<uint16_t>(), "chunk size shared with the merge");
+  constexpr bool F32 = sizeof(T) == 4;
+  constexpr int D = 128, NI = F32 ? 8 : 16, KPI = 4, KPW = NI * KPI, CHUNK = DC_WAVES * KPW, NS = DC_WAVES * KPI;
+  static_assert(CHUNK == dc_chunk<T>(), "chunk size shared with the merge");
   __shared__ float red_m[NS][G];
   __shared__ float red_l[NS][G];
   __shared__ float red_o[NS][G][D];
@@ -370,38 +414,38 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
   }
   if (chunk * CHUNK >= L) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int sub = lane & 15;  // 16-byte column of the key row
+  const int sub = lane & 15;  // 8-column group of the key row
   const int kk = lane >> 4;   // key slot (DPP row) inside a load instruction
   const int key0 = chunk * CHUNK + w * KPW;
 
   float qv[G][8];
-  uint4 qraw[G], wqr, wkr, knr, vnr, kn;
+  Row8<T> qraw[G], knr, vnr, kn;
+  uint4 wqr, wkr;
   float f0 = 0.f;
   bool newkey = false;  // FUSE: this lane's DPP row scores the new key from registers
 #pragma unroll
-  for (int gi = 0; gi < G; ++gi)
-    qraw[gi] = *reinterpret_cast<const uint4*>(Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * 8);
+  for (int gi = 0; gi < G; ++gi) qraw[gi].load(Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * 8);
   if constexpr (FUSE) {
     // everything the norm and rotation need is requested before the cache rows (loads return in order)
     wqr = *reinterpret_cast<const uint4*>(fz.wq + sub * 8);
     wkr = *reinterpret_cast<const uint4*>(fz.wk + sub * 8);
-    knr = *reinterpret_cast<const uint4*>(fz.k_new + hk * D + sub * 8);
-    vnr = *reinterpret_cast<const uint4*>(fz.v_new + hk * D + sub * 8);
+    knr.load((const T*)fz.k_new + hk * D + sub * 8);
+    vnr.load((const T*)fz.v_new + hk * D + sub * 8);
     f0 = fz.inv_freq[lane];
   }
   // Byte ranges end at the sequence length: keys >= L read as zero.
-  const auto rk = make_rsrc(K + b * st.kb + hk * st.kh, (uint32_t)(((int64_t)(L - 1) * st.ks + D) * 2));
-  const auto rv = make_rsrc(V + b * st.vb + hk * st.vh, (uint32_t)(((int64_t)(L - 1) * st.vs + D) * 2));
-  uint4 kr[NI], vr[NI];
+  const auto rk = make_rsrc(K + b * st.kb + hk * st.kh, (uint32_t)(((int64_t)(L - 1) * st.ks + D) * sizeof(T)));
+  const auto rv = make_rsrc(V + b * st.vb + hk * st.vh, (uint32_t)(((int64_t)(L - 1) * st.vs + D) * sizeof(T)));
+  Row8<T> kr[NI], vr[NI];
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int key = key0 + it * KPI + kk;
-    kr[it] = buf_load16_nt(rk, (uint32_t)(((int64_t)key * st.ks + sub * 8) * 2));
+    kr[it].load_nt(rk, (uint32_t)(((int64_t)key * st.ks + sub * 8) * sizeof(T)));
   }
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int key = key0 + it * KPI + kk;
-    vr[it] = buf_load16_nt(rv, (uint32_t)(((int64_t)key * st.vs + sub * 8) * 2));
+    vr[it].load_nt(rv, (uint32_t)(((int64_t)key * st.vs + sub * 8) * sizeof(T)));
   }
   if constexpr (FUSE) {
     // cos/sin of float(p) * inv_freq[i] for this lane's columns (i = (8 sub + j) mod 64): lane l
@@ -419,31 +463,31 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
       float a[8];
-      unpack8(qraw[gi], a);
+      qraw[gi].to_f32(a);
       norm_rope_row(a, wv, cs, sn, sub, fz.eps);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qv[gi][j] = round_bf16(a[j]) * scale;
+      for (int j = 0; j < 8; ++j) qv[gi][j] = (F32 ? a[j] : round_bf16(a[j])) * scale;
     }
     // The new key's row, normalised and rotated (every wave computes it: one row), and the DPP row
     // of this wave that owns key p (if any) writes it and the v row into the caches.
     const int rel = praw - key0;  // the new key relative to this wave's first key
     newkey = praw < max_len && rel >= 0 && rel < KPW && kk == (rel & 3);
     float a[8];
-    unpack8(knr, a);
+    knr.to_f32(a);
     unpack8(wkr, wv);
     norm_rope_row(a, wv, cs, sn, sub, fz.eps);
-    kn = pack8(a);
+    kn.from_f32(a);
     if (newkey) {
-      uint16_t* kc = const_cast<uint16_t*>(K) + b * st.kb + hk * st.kh + (int64_t)praw * st.ks + sub * 8;
-      uint16_t* vc = const_cast<uint16_t*>(V) + b * st.vb + hk * st.vh + (int64_t)praw * st.vs + sub * 8;
-      *reinterpret_cast<uint4*>(kc) = kn;
-      *reinterpret_cast<uint4*>(vc) = vnr;
+      T* kc = const_cast<T*>(K) + b * st.kb + hk * st.kh + (int64_t)praw * st.ks + sub * 8;
+      T* vc = const_cast<T*>(V) + b * st.vb + hk * st.vh + (int64_t)praw * st.vs + sub * 8;
+      kn.store(kc);
+      vnr.store(vc);
     }
   } else {
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
       float a[8];
-      unpack8(qraw[gi], a);
+      qraw[gi].to_f32(a);
 #pragma unroll
       for (int j = 0; j < 8; ++j) qv[gi][j] = a[j] * scale;
     }
@@ -455,16 +499,14 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
   float sc[G][NI];
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const uint32_t wk[4] = {kr[it].x, kr[it].y, kr[it].z, kr[it].w};
+    float kf[8];
+    kr[it].to_f32(kf);
     const bool valid = key0 + it * KPI + kk < Lc;
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
       float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        d += qv[gi][2 * e] * lo_bf16(wk[e]);
-        d += qv[gi][2 * e + 1] * hi_bf16(wk[e]);
-      }
+      for (int j = 0; j < 8; ++j) d += qv[gi][j] * kf[j];
       d = row16_sum(d);
       sc[gi][it] = valid ? d : -INFINITY;
     }
@@ -473,15 +515,13 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) sn_new[gi] = -INFINITY;
   if constexpr (FUSE) {
-    const uint32_t wk[4] = {kn.x, kn.y, kn.z, kn.w};
+    float kf[8];
+    kn.to_f32(kf);
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
       float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        d += qv[gi][2 * e] * lo_bf16(wk[e]);
-        d += qv[gi][2 * e + 1] * hi_bf16(wk[e]);
-      }
+      for (int j = 0; j < 8; ++j) d += qv[gi][j] * kf[j];
       d = row16_sum(d);
       sn_new[gi] = newkey ? d : -INFINITY;
     }
@@ -498,23 +538,19 @@ __global__ __launch_bounds__(256) void decode_partial_bf16_kernel(const uint16_t
     if constexpr (FUSE) {
       const float p = __expf(sn_new[gi] - mu);
       ls += p;
-      const uint32_t wv[4] = {vnr.x, vnr.y, vnr.z, vnr.w};
+      float vf[8];
+      vnr.to_f32(vf);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[2 * e] += p * lo_bf16(wv[e]);
-        o[2 * e + 1] += p * hi_bf16(wv[e]);
-      }
+      for (int j = 0; j < 8; ++j) o[j] += p * vf[j];
     }
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const float p = __expf(sc[gi][it] - mu);
       ls += p;
-      const uint32_t wv[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+      float vf[8];
+      vr[it].to_f32(vf);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[2 * e] += p * lo_bf16(wv[e]);
-        o[2 * e + 1] += p * hi_bf16(wv[e]);
-      }
+      for (int j = 0; j < 8; ++j) o[j] += p * vf[j];
     }
     if (sub == 0) {
       red_m[s_id][gi] = mx;
@@ -620,13 +656,14 @@ __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __r
 
 // The merge of the fused decode block (one sequence, length *position + 1): the same kernel body
 // with the length taken from the position.
+template <typename T>
 __global__ __launch_bounds__(256) void decode_merge_cols_pos_kernel(const float* __restrict__ part,
                                                                    const int32_t* __restrict__ position, int max_len,
                                                                    int hq, int max_chunks, AttnStrides st,
-                                                                   uint16_t* __restrict__ O) {
+                                                                   T* __restrict__ O) {
   const int p = *position;
   const int L = p + 1 < 0 ? 0 : (p + 1 > max_len ? max_len : p + 1);
-  decode_merge_cols_body<uint16_t>(part, L, hq, max_chunks, st, O);
+  decode_merge_cols_body<T>(part, L, hq, max_chunks, st, O);
 }
 
 // ---- scratch of the allocation-free decode entry point (kh_decode_attention_noalloc) ----------
@@ -682,8 +719,9 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
 #define KH_DECODE_CASE(GG)                                                                                 \
   case GG:                                                                                                 \
     if constexpr (sizeof(T) == 2)                                                                          \
-      decode_partial_bf16_kernel<GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st, \
-                                                                 scale, max_chunks, part, DecodeFuse{});   \
+      decode_partial_rows_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv,  \
+                                                                    st, scale, max_chunks, part,           \
+                                                                    DecodeFuse{});                         \
     else                                                                                                   \
       decode_partial_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st,  \
                                                                 scale, max_chunks, part);                  \
@@ -924,30 +962,32 @@ int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* 
 int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                               float eps, const int32_t* position, void* k_cache, void* v_cache, int hq, int hkv,
                               int64_t max_len, const int64_t* cache_strides, float scale, const void* w_o, int64_t ldw,
-                              int64_t n_out, float* x) {
+                              int64_t n_out, float* x, int dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "kh_decode_attention_block: bad head counts %d / %d", hq, hkv);
   const int G = hq / hkv;
   KH_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "kh_decode_attention_block: hq/hkv = %d not in {1, 2, 4, 8}", G);
+  KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_decode_attention_block: unsupported dtype %d", dtype);
   KH_REQUIRE(max_len > 0 && max_len <= INT32_MAX && n_out > 0 && n_out <= INT32_MAX,
              "kh_decode_attention_block: bad extents");
   KH_REQUIRE(qkv && q_norm_w && k_norm_w && inv_freq && position && k_cache && v_cache && cache_strides && w_o && x,
              "kh_decode_attention_block: null pointer");
+  const bool f32 = dtype == KH_F32;
+  const int64_t eb = f32 ? 4 : 2, vec = 16 / eb;
   const int64_t kh_s = cache_strides[0], ks = cache_strides[1], vh_s = cache_strides[2], vs = cache_strides[3];
   KH_REQUIRE(aligned16(qkv) && aligned16(q_norm_w) && aligned16(k_norm_w) && aligned16(k_cache) &&
-                 aligned16(v_cache) && kh_s % 8 == 0 && ks % 8 == 0 && vh_s % 8 == 0 && vs % 8 == 0,
+                 aligned16(v_cache) && kh_s % vec == 0 && ks % vec == 0 && vh_s % vec == 0 && vs % vec == 0,
              "kh_decode_attention_block: operands must be 16-byte aligned with 16-byte aligned strides");
   const int64_t lim = int64_t(1) << 31;
-  KH_REQUIRE((max_len + 256) * ks * 2 < lim && (max_len + 256) * vs * 2 < lim,
+  KH_REQUIRE((max_len + 256) * ks * eb < lim && (max_len + 256) * vs * eb < lim,
              "kh_decode_attention_block: one head of the cache spans more than 2 GiB");
   const int ml = (int)max_len;
-  constexpr int CH = 256;  // keys per split-K chunk (dc_chunk<bf16>)
+  const int CH = f32 ? dc_chunk<float>() : dc_chunk<uint16_t>();  // keys per split-K chunk
   const int max_chunks = (ml + CH - 1) / CH;
   KH_REQUIRE(max_chunks <= 65535, "kh_decode_attention_block: max_len too large");
   const size_t part_bytes = (size_t)hq * max_chunks * (128 + 2) * sizeof(float);
   float* part = (float*)scratch_alloc(part_bytes);
   if (!part) return KH_ERR_OOM;
-  const uint16_t* Q = (const uint16_t*)qkv;
   AttnStrides st{};
   st.qh = 128;
   st.kh = kh_s; st.ks = ks; st.vh = vh_s; st.vs = vs;
@@ -956,18 +996,26 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
   fz.wk = (const uint16_t*)k_norm_w;
   fz.inv_freq = inv_freq;
   fz.position = position;
-  fz.k_new = Q + (int64_t)hq * 128;
-  fz.v_new = Q + (int64_t)(hq + hkv) * 128;
+  fz.k_new = (const char*)qkv + (int64_t)hq * 128 * eb;
+  fz.v_new = (const char*)qkv + (int64_t)(hq + hkv) * 128 * eb;
   fz.eps = eps;
-  const uint16_t* K = (const uint16_t*)k_cache;
-  const uint16_t* V = (const uint16_t*)v_cache;
   const dim3 grid(max_chunks, hkv, 1);
-  switch (G) {
-    case 1: decode_partial_bf16_kernel<1, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-    case 2: decode_partial_bf16_kernel<2, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-    case 4: decode_partial_bf16_kernel<4, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-    default: decode_partial_bf16_kernel<8, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-  }
+  auto partial = [&](auto* tp) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    const T* Q = (const T*)qkv;
+    const T* K = (const T*)k_cache;
+    const T* V = (const T*)v_cache;
+    switch (G) {
+      case 1: decode_partial_rows_kernel<T, 1, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+      case 2: decode_partial_rows_kernel<T, 2, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+      case 4: decode_partial_rows_kernel<T, 4, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+      default: decode_partial_rows_kernel<T, 8, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+    }
+  };
+  if (f32)
+    partial((float*)nullptr);
+  else
+    partial((uint16_t*)nullptr);
   // Launch errors are recorded, and the scratch blocks returned, before any return.
   hipError_t e = hipGetLastError();
   const int K_in = hq * 128;
@@ -981,21 +1029,26 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
   if (e != hipSuccess) {
     // nothing more is launched
   } else if (max_chunks <= kMergeInPrologueMaxChunks &&
-             launch_gemv_attn_merge(part, am, (const uint16_t*)w_o, ldw, x, x, (int)n_out, K_in, 1.f, 1.f)) {
+             launch_gemv_attn_merge(part, am, (const uint16_t*)w_o, ldw, x, x, (int)n_out, K_in, 1.f, 1.f, f32)) {
     e = hipGetLastError();
   } else {
-    // long caches: a separate merge into a bf16 row, then the plain GEMV with the residual
-    uint16_t* o = (uint16_t*)scratch_alloc((size_t)K_in * 2);
+    // long caches: a separate merge into a row of the caches' type, then the plain GEMV with the residual
+    void* o = scratch_alloc((size_t)K_in * eb);
     if (!o) {
       scratch_free(part);
       return KH_ERR_OOM;
     }
     AttnStrides so{};
     so.oh = 128;
-    decode_merge_cols_pos_kernel<<<dim3(4, hq, 1), 256, 0, stream()>>>(part, position, ml, hq, max_chunks, so, o);
+    if (f32)
+      decode_merge_cols_pos_kernel<float><<<dim3(4, hq, 1), 256, 0, stream()>>>(part, position, ml, hq, max_chunks, so,
+                                                                                (float*)o);
+    else
+      decode_merge_cols_pos_kernel<uint16_t><<<dim3(4, hq, 1), 256, 0, stream()>>>(part, position, ml, hq, max_chunks,
+                                                                                   so, (uint16_t*)o);
     e = hipGetLastError();
     if (e == hipSuccess)
-      rc = kh_gemv_fused(0, o, nullptr, nullptr, 0.f, w_o, ldw, x, x, nullptr, n_out, K_in, 1.f, 1.f, KH_F32);
+      rc = kh_gemv_fused(0, o, nullptr, nullptr, 0.f, w_o, ldw, x, x, nullptr, n_out, K_in, 1.f, 1.f, KH_F32, dtype);
     scratch_free(o);
   }
   scratch_free(part);  // stream-ordered: reused only by later work on the same stream

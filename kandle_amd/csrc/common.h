@@ -29,7 +29,7 @@ struct AttnMerge {
   int hq = 0, max_chunks = 0, max_len = 0, chunk = 0;
 };
 bool launch_gemv_attn_merge(const float* part, const AttnMerge& am, const uint16_t* W, int64_t ldw, float* C,
-                            const float* cin, int N, int K, float alpha, float beta);
+                            const float* cin, int N, int K, float alpha, float beta, bool exact);
 
 #define KH_CHECK_HIP(expr)                                                              \
   do {                                                                                  \

@@ -93,9 +93,9 @@ struct QknrArgs {
   const uint16_t* wk = nullptr;
   const float* inv_freq = nullptr;    // [64]
   const int32_t* positions = nullptr; // [M]: RoPE position (and, with kv_cache_len > 0, cache row)
-  uint16_t* q_out = nullptr;
-  uint16_t* k_out = nullptr;
-  uint16_t* v_out = nullptr;
+  void* q_out = nullptr;              // the activations' type: bf16, or fp32 with fp32 activations
+  void* k_out = nullptr;
+  void* v_out = nullptr;
   int64_t s[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};  // (batch, seq, head) element strides of q_out, k_out, v_out
   int hq = 0, hkv = 0;
   uint32_t seq_len = 1;               // token m is (batch m / seq_len, index m % seq_len)
@@ -103,19 +103,41 @@ struct QknrArgs {
   int64_t kv_cache_len = 0;           // > 0: K/V rows at positions[m] (outside [0, len): not written)
 };
 
-template <typename TO, int WTM, int WTN, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false, bool QKNR = false>
-__global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
-    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
+// TA = float (fp32 activations, the reference's float32 arithmetic): A is read as fp32 and each
+// value a is split into bf16 hi = bf16(a) and lo = bf16(a - hi) (a - hi is exact in fp32) when the
+// tile is copied to LDS, as two planes; every k-step then runs two MFMAs into the same accumulator,
+// W * hi and W * lo.  The weights are exactly bf16, so each product is W * a up to the 2^-17
+// relative error of hi + lo, fp32 accumulate; the epilogues keep their fp32 values (no bf16
+// rounding of the SwiGLU operands or of the qk-norm + RoPE input) and store fp32.
+// LDS bytes of the k loop (two stages of the A planes and the B tile): two workgroups per CU when
+// they fit the CU's 160 KiB, else one.
+template <typename TA, int WTM, int WTN, int KS>
+constexpr int gemm_lds_bytes() {
+  return 2 * ((sizeof(TA) == 4 ? 2 : 1) * g_tile(WTM) + g_tile(WTN)) * (KS + 8) * 2;
+}
+template <typename TA, int WTM, int WTN, int KS>
+constexpr int gemm_min_blocks() {
+  return 2 * gemm_lds_bytes<TA, WTM, WTN, KS>() <= 160 * 1024 ? 2 : 1;
+}
+
+template <typename TO, int WTM, int WTN, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false, bool QKNR = false,
+          typename TA = uint16_t>
+__global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) void gemm_bf16_nt_kernel(
+    const TA* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
     int tiles_n, int splits, int kchunk, float* __restrict__ part, QknrArgs qa) {
+  constexpr bool AF = std::is_same<TA, float>::value;
   constexpr int GM = g_tile(WTM), GN = g_tile(WTN);
   constexpr int STR = KS + 8;  // LDS row stride (elements): 16-byte aligned, breaks bank aliasing
-  constexpr int ATILE = GM * STR, BTILE = GN * STR;
-  constexpr int CPR = KS / 8;                      // 16-byte chunks per row per k-step
-  constexpr int CPTA = GM * CPR / G_THREADS;       // chunks per thread per A tile
+  constexpr int APL = AF ? 2 : 1;                  // A planes in LDS: bf16, or hi and lo
+  constexpr int ATILE = GM * STR, BTILE = GN * STR, ASTG = APL * ATILE;
+  constexpr int AE = 16 / (int)sizeof(TA);         // A elements per 16-byte chunk
+  constexpr int CPR = KS / 8;                      // 16-byte chunks per B row per k-step
+  constexpr int CPRA = KS / AE;                    // 16-byte chunks per A row per k-step
+  constexpr int CPTA = GM * CPRA / G_THREADS;      // chunks per thread per A tile
   constexpr int CPTB = GN * CPR / G_THREADS;       // chunks per thread per B tile
   constexpr int CPTM = CPTA > CPTB ? CPTA : CPTB;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ATILE + BTILE)];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ASTG + BTILE)];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, g = lane >> 5;
   int bid = blockIdx.x;
@@ -130,7 +152,7 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 
   // Byte ranges of this tile's rows; a row past the matrix or a column past the range reads zero.
   const int mrows = min(GM, M - m0), nrows = min(GN, N - n0);
-  const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * 2));
+  const auto ra = make_rsrc(A + (int64_t)m0 * lda, (uint32_t)(((int64_t)(mrows - 1) * lda + K) * sizeof(TA)));
   const auto rb = make_rsrc(B + (int64_t)n0 * ldb, (uint32_t)(((int64_t)(nrows - 1) * ldb + K) * 2));
 
   // Staging: the A (B) tile is GM (GN) rows x KS k = GM * CPR chunks of 16 B, CPTA (CPTB) per
@@ -143,13 +165,15 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 #pragma unroll
     for (int i = 0; i < CPTM; ++i) {
       const int id = tid + G_THREADS * i;
-      const int row = id / CPR, kc = kt + 8 * (id % CPR);
-      const bool in = kc < kend;
       if (i < CPTA) {
-        const uint32_t ao = in ? ((uint32_t)row * (uint32_t)lda + (uint32_t)kc) * 2u : 0xffffffffu;
+        const int row = id / CPRA, kc = kt + AE * (id % CPRA);
+        const uint32_t ao =
+            kc < kend ? ((uint32_t)row * (uint32_t)lda + (uint32_t)kc) * (uint32_t)sizeof(TA) : 0xffffffffu;
         ast[stg][i < CPTA ? i : 0] = buf_load16(ra, ao);
       }
       if (i < CPTB) {
+        const int row = id / CPR, kc = kt + 8 * (id % CPR);
+        const bool in = kc < kend;
         const uint32_t bo = in ? ((uint32_t)row * (uint32_t)ldb + (uint32_t)kc) * 2u : 0xffffffffu;
         // B (the weights) with the non-temporal hint: C5 prefill 2.413-2.428 -> 2.396-2.402 ms
         bst[stg][i < CPTB ? i : 0] = buf_load16_nt(rb, bo);
@@ -157,14 +181,30 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
     }
   };
   auto store_tile = [&](int stg, int buf) {
-    uint16_t* as = smem + buf * (ATILE + BTILE);
-    uint16_t* bs = as + ATILE;
+    uint16_t* as = smem + buf * (ASTG + BTILE);
+    uint16_t* bs = as + ASTG;
 #pragma unroll
     for (int i = 0; i < CPTM; ++i) {
       const int id = tid + G_THREADS * i;
-      const int row = id / CPR, kc = 8 * (id % CPR);
-      if (i < CPTA) *reinterpret_cast<uint4*>(as + row * STR + kc) = ast[stg][i < CPTA ? i : 0];
-      if (i < CPTB) *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[stg][i < CPTB ? i : 0];
+      if (i < CPTA) {
+        const int row = id / CPRA, kc = AE * (id % CPRA);
+        const uint4 v = ast[stg][i < CPTA ? i : 0];
+        if constexpr (AF) {
+          // four fp32 values -> bf16 hi (plane 0) and lo = bf16(a - hi) (plane 1)
+          const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+          const uint32_t h01 = pack_bf16x2(f[0], f[1]), h23 = pack_bf16x2(f[2], f[3]);
+          const uint32_t l01 = pack_bf16x2(f[0] - lo_bf16(h01), f[1] - hi_bf16(h01));
+          const uint32_t l23 = pack_bf16x2(f[2] - lo_bf16(h23), f[3] - hi_bf16(h23));
+          *reinterpret_cast<uint2*>(as + row * STR + kc) = make_uint2(h01, h23);
+          *reinterpret_cast<uint2*>(as + ATILE + row * STR + kc) = make_uint2(l01, l23);
+        } else {
+          *reinterpret_cast<uint4*>(as + row * STR + kc) = v;
+        }
+      }
+      if (i < CPTB) {
+        const int row = id / CPR, kc = 8 * (id % CPR);
+        *reinterpret_cast<uint4*>(bs + row * STR + kc) = bst[stg][i < CPTB ? i : 0];
+      }
     }
   };
 
@@ -183,14 +223,17 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
   // into the idle buffer, so the main loop has no branches between a load and its use.
   auto step = [&](int t, int u) {
     load_tile(u, kbeg + (t + PF) * KS);
-    const uint16_t* as = smem + (t & 1) * (ATILE + BTILE);
-    const uint16_t* bs = as + ATILE;
+    const uint16_t* as = smem + (t & 1) * (ASTG + BTILE);
+    const uint16_t* bs = as + ASTG;
 #pragma unroll
     for (int kc = 0; kc < KS / 16; ++kc) {
-      bf16x8 av[WTM], bv[WTN];
+      bf16x8 av[APL][WTM], bv[WTN];
 #pragma unroll
-      for (int i = 0; i < WTM; ++i)
-        av[i] = as_bf16x8(*reinterpret_cast<const uint4*>(as + (wm + 32 * i + r) * STR + 16 * kc + 8 * g));
+      for (int pl = 0; pl < APL; ++pl)
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+          av[pl][i] = as_bf16x8(
+              *reinterpret_cast<const uint4*>(as + pl * ATILE + (wm + 32 * i + r) * STR + 16 * kc + 8 * g));
 #pragma unroll
       for (int i = 0; i < WTN; ++i)
         bv[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn + 32 * i + r) * STR + 16 * kc + 8 * g));
@@ -198,7 +241,9 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
       for (int a = 0; a < WTN; ++a)
 #pragma unroll
         for (int b = 0; b < WTM; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv[a], av[b], acc[a][b], 0, 0, 0);
+#pragma unroll
+          for (int pl = 0; pl < APL; ++pl)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv[a], av[pl][b], acc[a][b], 0, 0, 0);
     }
     store_tile((u + 1) % PF, (t + 1) & 1);
     __syncthreads();
@@ -241,21 +286,47 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
 
   // Epilogue: acc[a][b] lane holds m = m0 + wm + 32b + r, n = n0 + wn + 32a + 8(j/4) + 4g + j%4.
   if constexpr (QKNR) {
-    static_assert(sizeof(TO) == 2 && WTM == 1 && WTN == 2 && !SPLIT && !SWIGLU, "QKNR: bf16 64 x 128 tiles");
-    constexpr int TSTR = 128 + 8;  // staged row stride (elements): 272 B, 16-byte aligned rows
-    static_assert(GM * TSTR <= 2 * (ATILE + BTILE), "the staged tile fits the k loop's LDS");
-    // Every wave has passed the k loop's last barrier: its LDS is free.
-    uint16_t* tile = smem;
+    static_assert(sizeof(TO) == sizeof(TA) && WTM == 1 && WTN == 2 && !SPLIT && !SWIGLU,
+                  "QKNR: 64 x 128 tiles, output of the activations' type");
+    // Staged row stride (elements of TA): 272 B (bf16) or 528 B (fp32), 16-byte aligned rows.
+    constexpr int TSTR = 128 + 16 / (int)sizeof(TA);
+    static_assert(GM * TSTR * (int)sizeof(TA) <= 2 * (ASTG + BTILE) * 2, "the staged tile fits the k loop's LDS");
+    // Every wave has passed the k loop's last barrier: its LDS is free.  The tile is staged as the
+    // plain GEMM would store it: rounded to bf16, or fp32 with fp32 activations.
+    TA* tile = reinterpret_cast<TA*>(smem);
 #pragma unroll
     for (int a = 0; a < WTN; ++a)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        uint2 w;
-        w.x = pack_bf16x2(acc[a][0][4 * q], acc[a][0][4 * q + 1]);
-        w.y = pack_bf16x2(acc[a][0][4 * q + 2], acc[a][0][4 * q + 3]);
-        *reinterpret_cast<uint2*>(tile + (wm + r) * TSTR + wn + 32 * a + 8 * q + 4 * g) = w;
+        TA* dst = tile + (wm + r) * TSTR + wn + 32 * a + 8 * q + 4 * g;
+        if constexpr (AF) {
+          *reinterpret_cast<float4*>(dst) =
+              make_float4(acc[a][0][4 * q], acc[a][0][4 * q + 1], acc[a][0][4 * q + 2], acc[a][0][4 * q + 3]);
+        } else {
+          uint2 w;
+          w.x = pack_bf16x2(acc[a][0][4 * q], acc[a][0][4 * q + 1]);
+          w.y = pack_bf16x2(acc[a][0][4 * q + 2], acc[a][0][4 * q + 3]);
+          *reinterpret_cast<uint2*>(dst) = w;
+        }
       }
     __syncthreads();
+    // 8 elements of TA at p (16 or 32 bytes) <-> 8 floats
+    auto ld8 = [](const TA* p, float (&v)[8]) {
+      if constexpr (AF) {
+        const float4 x0 = reinterpret_cast<const float4*>(p)[0], x1 = reinterpret_cast<const float4*>(p)[1];
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+      } else {
+        unpack_bf16x8(*reinterpret_cast<const uint4*>(p), v);
+      }
+    };
+    auto st8 = [](TA* p, const float (&v)[8]) {
+      if constexpr (AF) {
+        reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+      } else {
+        *reinterpret_cast<uint4*>(p) = pack_bf16x8(v);
+      }
+    };
     const int hd = n0 / 128;                      // q heads, then k heads, then v heads
     const int t8 = lane & 7, rs = lane >> 3;      // 8 lanes per head row, 8 rows per wave step
     const bool is_q = hd < qa.hq, is_k = !is_q && hd < qa.hq + qa.hkv;
@@ -275,8 +346,8 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
       const int m = m0 + row;
       const bool live = m < M;
       float a8[8], c8[8];
-      unpack_bf16x8(*reinterpret_cast<const uint4*>(tile + row * TSTR + 8 * t8), a8);
-      unpack_bf16x8(*reinterpret_cast<const uint4*>(tile + row * TSTR + 64 + 8 * t8), c8);
+      ld8(tile + row * TSTR + 8 * t8, a8);
+      ld8(tile + row * TSTR + 64 + 8 * t8, c8);
       const int32_t ipos = live ? qa.positions[m] : 0;
       const uint32_t bi = live ? (uint32_t)m / qa.seq_len : 0u, si = live ? (uint32_t)m - bi * qa.seq_len : 0u;
       const int64_t kv_row = cache_mode ? (int64_t)ipos : (int64_t)si;
@@ -288,15 +359,15 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
         for (int j = 0; j < 8; ++j) sincosf(pos * f[j], &sn[j], &cs[j]);
         qk_norm_rope_row<128>(a8, c8, wa, wb, cs, sn, qa.eps, oa, oc);
         if (live && (is_q || kv_ok)) {
-          uint16_t* dst = is_q ? qa.q_out + bi * qa.s[0] + si * qa.s[1] + (int64_t)hd * qa.s[2]
-                               : qa.k_out + bi * qa.s[3] + kv_row * qa.s[4] + (int64_t)(hd - qa.hq) * qa.s[5];
-          *reinterpret_cast<uint4*>(dst + 8 * t8) = pack_bf16x8(oa);
-          *reinterpret_cast<uint4*>(dst + 64 + 8 * t8) = pack_bf16x8(oc);
+          TA* dst = is_q ? (TA*)qa.q_out + bi * qa.s[0] + si * qa.s[1] + (int64_t)hd * qa.s[2]
+                         : (TA*)qa.k_out + bi * qa.s[3] + kv_row * qa.s[4] + (int64_t)(hd - qa.hq) * qa.s[5];
+          st8(dst + 8 * t8, oa);
+          st8(dst + 64 + 8 * t8, oc);
         }
       } else if (live && kv_ok) {
-        uint16_t* dst = qa.v_out + bi * qa.s[6] + kv_row * qa.s[7] + (int64_t)(hd - qa.hq - qa.hkv) * qa.s[8];
-        *reinterpret_cast<uint4*>(dst + 8 * t8) = *reinterpret_cast<const uint4*>(tile + row * TSTR + 8 * t8);
-        *reinterpret_cast<uint4*>(dst + 64 + 8 * t8) = *reinterpret_cast<const uint4*>(tile + row * TSTR + 64 + 8 * t8);
+        TA* dst = (TA*)qa.v_out + bi * qa.s[6] + kv_row * qa.s[7] + (int64_t)(hd - qa.hq - qa.hkv) * qa.s[8];
+        st8(dst + 8 * t8, a8);
+        st8(dst + 64 + 8 * t8, c8);
       }
     }
     return;
@@ -318,8 +389,12 @@ __global__ __launch_bounds__(G_THREADS, 2) void gemm_bf16_nt_kernel(
           if (f >= NH) continue;
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            v[e] = silu_ref(round_bf16(acc[a][b][4 * q + e])) * round_bf16(acc[a][b][4 * q + 4 + e]);
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (AF)
+              v[e] = silu_ref(acc[a][b][4 * q + e]) * acc[a][b][4 * q + 4 + e];
+            else
+              v[e] = silu_ref(round_bf16(acc[a][b][4 * q + e])) * round_bf16(acc[a][b][4 * q + 4 + e]);
+          }
           store4<TO>(C, (int64_t)m * ldc + f, v, vec, 4);
         }
     }
@@ -381,15 +456,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 constexpr int SK_MAXM = 8;
 constexpr int SK_ROWS_PER_WAVE = 4;  // weight rows in flight per wave step
 
-template <typename T, typename TO>
-__global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
+template <typename TA, typename T, typename TO>
+__global__ __launch_bounds__(256) void gemv_nt_kernel(const TA* __restrict__ A, int64_t lda, const T* __restrict__ B,
                                                       int64_t ldb, TO* C, int64_t ldc, const TO* cin, int64_t ldcin,
                                                       const TO* __restrict__ bias, int M, int N, int K, float alpha,
                                                       float beta) {
   extern __shared__ float xs[];  // [M][K] fp32
   for (int i = threadIdx.x; i < M * K; i += blockDim.x) {
     const int mm = i / K, kk = i % K;
-    xs[i] = Elem<T>::load(A, (int64_t)mm * lda + kk);
+    xs[i] = Elem<TA>::load(A, (int64_t)mm * lda + kk);
   }
   __syncthreads();
   constexpr int EPL = 16 / sizeof(T);
@@ -475,26 +550,26 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(const T* __restrict__ A, i
 // streams them with raw 16-byte buffer loads, CB chunks of 512 columns per row in flight (rows past
 // n read as zero), and reduces each row across the wave.  Every weight byte is read once.
 // =============================================================================================
-template <int U, int PRO, typename TO, bool PAIR8 = false>
-__global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, const uint16_t* __restrict__ x2,
+template <int U, int PRO, typename TO, bool PAIR8 = false, bool EX = false>
+__global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, const void* __restrict__ x2,
                                                     const uint16_t* __restrict__ nw, float eps,
                                                     const uint16_t* __restrict__ W, int64_t ldw, uint32_t w_bytes,
                                                     TO* C, const TO* cin, const TO* __restrict__ bias, int N, int K,
                                                     int nch, float alpha, float beta, AttnMerge am) {
   extern __shared__ float xs[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  GemvRows<U, PAIR8> g;
+  GemvRows<U, PAIR8, EX> g;
   g.init(W, ldw, w_bytes, N, K, nch, (int64_t)blockIdx.x * (blockDim.x >> 6) + w,
          (int64_t)gridDim.x * (blockDim.x >> 6));
   // The first batch is in flight while the workgroup forms x'.
   g.issue_first();
-  gemv_prologue<PRO>(xs, x, x2, nw, eps, K, nch * GV_CHUNK, am);
+  gemv_prologue<PRO, EX>(xs, x, x2, nw, eps, K, nch * GV_CHUNK, am);
   g.template run<TO>(xs, C, cin, bias, alpha, beta);
 }
 
 // Launches gemv1_kernel; returns false (nothing launched) when the operands do not fit its
 // assumptions (16-byte aligned weight rows, 32-bit byte offsets, x' within 64 KiB of LDS).
-template <int U, int PRO, typename TO, bool PAIR8 = false>
+template <int U, int PRO, typename TO, bool PAIR8 = false, bool EX = false>
 void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw,
               uint32_t w_bytes, TO* C, const TO* cin, const TO* bias, int N, int K, int nch, float alpha, float beta,
               const AttnMerge& am) {
@@ -504,47 +579,54 @@ void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const ui
   // workgroups: 69.5 -> 59.9 us graph-replayed with 4 rows per wave and 8192 workgroups before.
   if (grid > 2048) grid = 2048;
   const size_t shm = (size_t)nch * GV_CHUNK * sizeof(float);
-  gemv1_kernel<U, PRO, TO, PAIR8><<<(int)grid, 256, shm, stream()>>>(x, (const uint16_t*)x2, (const uint16_t*)nw, eps,
-                                                                     W, ldw, w_bytes, C, cin, bias, N, K, nch, alpha,
-                                                                     beta, am);
+  gemv1_kernel<U, PRO, TO, PAIR8, EX><<<(int)grid, 256, shm, stream()>>>(x, x2, (const uint16_t*)nw, eps, W, ldw,
+                                                                         w_bytes, C, cin, bias, N, K, nch, alpha,
+                                                                         beta, am);
 }
 
-// SwiGLU one-row projection: h[f] = bf16(silu(bf16(gate_f)) * bf16(up_f)) from the interleaved
-// gate/up weight (2 * n_half rows, blocks of 8), one wave per (gate, up) row pair.  False when the
-// operands do not fit (as launch_gemv1).
-template <int PRO>
-bool launch_gemv_swiglu(const void* x, const void* nw, float eps, const uint16_t* W, int64_t ldw, uint16_t* H,
+// The weight rows a one-row projection may address fit 32-bit byte offsets: row groups start below
+// N and hold U rows, so the largest row index formed is N - 1 + U - 1 (rows at or past N are never
+// stored, and the buffer range reads them as zero).
+inline bool gemv_offsets_fit(int N, int U, int64_t ldw) {
+  return ((int64_t)(N + U) * ldw) * 2 < (int64_t(1) << 32);
+}
+
+// SwiGLU one-row projection: h[f] = bf16(silu(bf16(gate_f)) * bf16(up_f)) (EX: silu(gate_f) * up_f in
+// fp32, TO float) from the interleaved gate/up weight (2 * n_half rows, blocks of 8), one wave per
+// (gate, up) row pair.  False when the operands do not fit (as launch_gemv1).
+template <int PRO, bool EX = false, typename TO = uint16_t>
+bool launch_gemv_swiglu(const void* x, const void* nw, float eps, const uint16_t* W, int64_t ldw, TO* H,
                         int n_half, int K) {
   const int N = 2 * n_half;
   if (n_half <= 0 || n_half % 8 != 0 || K <= 0) return false;
   const int nch = (K + GV_CHUNK - 1) / GV_CHUNK;
   const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
-  if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || ((int64_t)(N + 4) * ldw) * 2 >= (int64_t(1) << 32) ||
+  // a pair of row group q addresses rows up to 16 (q / 8) + q % 8 + 8 < N + 8
+  if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || !gemv_offsets_fit(N, 8, ldw) ||
       (size_t)nch * GV_CHUNK * sizeof(float) > 64 * 1024)
     return false;
-  gemv1_go<2, PRO, uint16_t, true>(x, nullptr, nw, eps, W, ldw, (uint32_t)w_bytes, H, nullptr, nullptr, N, K, nch,
-                                   1.f, 0.f, AttnMerge{});
+  gemv1_go<2, PRO, TO, true, EX>(x, nullptr, nw, eps, W, ldw, (uint32_t)w_bytes, H, nullptr, nullptr, N, K, nch, 1.f,
+                                 0.f, AttnMerge{});
   return true;
 }
 
-template <int PRO, typename TO>
+template <int PRO, typename TO, bool EX = false>
 bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw, TO* C,
                   const TO* cin, const TO* bias, int N, int K, float alpha, float beta, const AttnMerge& am = {}) {
   if (N <= 0 || K <= 0) return false;
   const int nch = (K + GV_CHUNK - 1) / GV_CHUNK;
   const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
-  // largest offset formed: a row index up to N + 3 (rows past N read as zero)
-  const int64_t max_off = ((int64_t)(N + 4) * ldw) * 2;
-  if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || max_off >= (int64_t(1) << 32) ||
+  const int U = N >= 16384 ? 8 : (N >= 2048 ? 2 : 1);
+  if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || !gemv_offsets_fit(N, U, ldw) ||
       (size_t)nch * GV_CHUNK * sizeof(float) > 64 * 1024)
     return false;
   const uint32_t wb = (uint32_t)w_bytes;
-  if (N >= 16384)
-    gemv1_go<8, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
-  else if (N >= 2048)
-    gemv1_go<2, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
+  if (U == 8)
+    gemv1_go<8, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
+  else if (U == 2)
+    gemv1_go<2, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   else
-    gemv1_go<1, PRO, TO>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
+    gemv1_go<1, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
   return true;
 }
 
@@ -552,8 +634,8 @@ bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, cons
 // Generic tiled kernel (f32 or bf16 storage, trans_b 0/1): 16 x 16 threads, 64 x 64 tile, each
 // thread 4 x 4 outputs, fp32 math.
 // =============================================================================================
-template <typename T, typename TO>
-__global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__ A, int64_t lda,
+template <typename TA, typename T, typename TO>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(const TA* __restrict__ A, int64_t lda,
                                                            const T* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
                                                            const TO* cin, int64_t ldcin, const TO* __restrict__ bias,
                                                            int M, int N, int K, float alpha, float beta, int trans_b) {
@@ -566,7 +648,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
     for (int i = threadIdx.x; i < 16 * 64; i += 256) {
       const int kk = i / 64, mm = i % 64;
       const int gm = m0 + mm, gk = k0 + kk;
-      As[kk][mm] = (gm < M && gk < K) ? Elem<T>::load(A, (int64_t)gm * lda + gk) : 0.f;
+      As[kk][mm] = (gm < M && gk < K) ? Elem<TA>::load(A, (int64_t)gm * lda + gk) : 0.f;
       const int gn = n0 + mm;
       float bv = 0.f;
       if (gn < N && gk < K)
@@ -610,12 +692,14 @@ inline void plain_tile(int M, int N, int& wtm, int& wtn) {
   }
 }
 
-// aligned: both operands start on 16 bytes.
-GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, bool bf16, int trans_b) {
+// aligned: both operands start on 16 bytes.  bf16: bf16 weights B with bf16 (a_bytes 2) or fp32
+// (a_bytes 4, split into hi + lo) activations A.
+GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, bool bf16, int trans_b,
+                   int a_bytes = 2) {
   GemmPlan p;
   const int64_t lim = int64_t(1) << 31;
   if (!(bf16 && trans_b && M > SK_MAXM && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned &&
-        (int64_t)g_tile(2) * lda * 2 < lim && (int64_t)g_tile(2) * ldb * 2 < lim))
+        (int64_t)g_tile(2) * lda * a_bytes < lim && (int64_t)g_tile(2) * ldb * 2 < lim))
     return p;
   p.mfma = true;
   // The K split is decided on the 64-tile count, whatever tile then runs it, so a shape's k ranges
@@ -647,73 +731,77 @@ GemmPlan gemm_plan(bool aligned, int64_t lda, int64_t ldb, int M, int N, int K, 
 }
 
 // One launch of the tile kernel with tile (64 WTM) x (64 WTN) and k-step KS.
-template <typename TO, int WTM, int WTN, int KS, bool SWIGLU = false>
-void go_tiles(int nblk, int splits, const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
+template <typename TO, int WTM, int WTN, int KS, bool SWIGLU = false, typename TA = uint16_t>
+void go_tiles(int nblk, int splits, const TA* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
               int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI, int M, int N, int K, float alpha, float beta,
               int tiles_n, int kchunk, float* part) {
-  constexpr int PF = kGemmPrefetch;
+  // fp32 activations hold twice the A chunks per stage: two stages in flight keep the ring in registers
+  constexpr int PF = std::is_same<TA, float>::value ? 2 : kGemmPrefetch;
   if (!SWIGLU && splits > 1)
-    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch><<<nblk, G_THREADS, 0, stream()>>>(
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch, false, false, TA><<<nblk, G_THREADS, 0,
+                                                                                        stream()>>>(
         A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part, QknrArgs{});
   else
-    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU><<<nblk, G_THREADS, 0, stream()>>>(
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU, false, TA><<<nblk, G_THREADS, 0, stream()>>>(
         A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr, QknrArgs{});
 }
 
 // Dispatch on the plan's tile: 128 x 128 with k-step 64; 64 x 64 with k-step 128 when split or
 // with at most one tile per CU, else k-step 64 (C5 prefill qkv, 512 tiles: 11.75 -> 10.9 us with
 // k-step 64; gate/up, 768 tiles: 14.0 -> 16.1 us with k-step 128); 128 x 64 and 64 x 128 with
-// kGemmRectKS.
-template <typename TO, bool SWIGLU = false>
-void launch_tile_shape(int wtm, int wtn, int64_t tiles, int splits, const uint16_t* A, int64_t lda,
+// kGemmRectKS.  fp32 activations (TA float: two LDS planes of A) keep a k-step of 64 on 64 x 64
+// tiles, so that two workgroups still fit a CU's LDS.
+template <typename TO, bool SWIGLU = false, typename TA = uint16_t>
+void launch_tile_shape(int wtm, int wtn, int64_t tiles, int splits, const TA* A, int64_t lda,
                        const uint16_t* B, int64_t ldb, TO* C, int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI,
                        int M, int N, int K, float alpha, float beta, int tiles_n, int kchunk, float* part) {
+  constexpr bool AF = std::is_same<TA, float>::value;
   const int nblk = (int)(tiles * splits);
   if (wtm == 2 && wtn == 2)
-    go_tiles<TO, 2, 2, 64, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n,
-                                   kchunk, part);
+    go_tiles<TO, 2, 2, 64, SWIGLU, TA>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
+                                       tiles_n, kchunk, part);
   else if (wtm == 2)
-    go_tiles<TO, 2, 1, kGemmRectKS, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
-                                            beta, tiles_n, kchunk, part);
+    go_tiles<TO, 2, 1, kGemmRectKS, SWIGLU, TA>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                                beta, tiles_n, kchunk, part);
   else if (wtn == 2)
-    go_tiles<TO, 1, 2, kGemmRectKS, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
-                                            beta, tiles_n, kchunk, part);
-  else if (splits > 1 || tiles <= 256)
-    go_tiles<TO, 1, 1, 128, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
-                                    tiles_n, kchunk, part);
+    go_tiles<TO, 1, 2, kGemmRectKS, SWIGLU, TA>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                                beta, tiles_n, kchunk, part);
+  else if (!AF && (splits > 1 || tiles <= 256))
+    go_tiles<TO, 1, 1, AF ? 64 : 128, SWIGLU, TA>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                                  beta, tiles_n, kchunk, part);
   else
-    go_tiles<TO, 1, 1, 64, SWIGLU>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
-                                   tiles_n, kchunk, part);
+    go_tiles<TO, 1, 1, 64, SWIGLU, TA>(nblk, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
+                                       tiles_n, kchunk, part);
 }
 
 // The MFMA tile kernel for plan p: C (or, with part != nullptr and p.splits > 1, only the fp32
 // partials part[split][m][n]).
-template <typename TO>
-void launch_gemm_tiles(const GemmPlan& p, const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
+template <typename TO, typename TA = uint16_t>
+void launch_gemm_tiles(const GemmPlan& p, const TA* A, int64_t lda, const uint16_t* B, int64_t ldb, TO* C,
                        int64_t ldc, const TO* CI, int64_t ldcin, const TO* BI, int M, int N, int K, float alpha,
                        float beta, float* part) {
   const int splits = part ? p.splits : 1;
-  launch_tile_shape<TO>(p.wtm, p.wtn, p.tiles, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
-                        p.tiles_n, p.kchunk, part);
+  launch_tile_shape<TO, false, TA>(p.wtm, p.wtn, p.tiles, splits, A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K,
+                                   alpha, beta, p.tiles_n, p.kchunk, part);
 }
 
-template <typename T, typename TO>
+// A has element type TA, B has T (bf16 weights may meet fp32 activations: TA float, T uint16_t).
+template <typename TA, typename T, typename TO>
 int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, const void* cin,
                 int64_t ldcin, const void* bias, int M, int N, int K, float alpha, float beta, int trans_b) {
-  const T* A = (const T*)a;
+  const TA* A = (const TA*)a;
   const T* B = (const T*)b;
   TO* C = (TO*)c;
   const TO* CI = (const TO*)cin;
   const TO* BI = (const TO*)bias;
-  constexpr bool is_bf16 = sizeof(T) == 2;
-  const GemmPlan p = gemm_plan(aligned16(a) && aligned16(b), lda, ldb, M, N, K, is_bf16, trans_b);
-  if constexpr (is_bf16) {
+  constexpr bool w_bf16 = sizeof(T) == 2;
+  const GemmPlan p = gemm_plan(aligned16(a) && aligned16(b), lda, ldb, M, N, K, w_bf16, trans_b, (int)sizeof(TA));
+  if constexpr (w_bf16) {
     if (p.mfma) {
       KH_REQUIRE(p.tiles <= INT32_MAX / 8, "kh_gemm: grid too large");
       float* part = nullptr;
       if (p.splits > 1) part = (float*)scratch_alloc((size_t)p.splits * M * N * sizeof(float));
-      launch_gemm_tiles<TO>(p, (const uint16_t*)A, lda, (const uint16_t*)B, ldb, C, ldc, CI, ldcin, BI, M, N, K,
-                            alpha, beta, part);
+      launch_gemm_tiles<TO, TA>(p, A, lda, (const uint16_t*)B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, part);
       if (part) {
         gemm_splitk_reduce_kernel<TO><<<(int)(((int64_t)M * N / 4 + 255) / 256), 256, 0, stream()>>>(
             part, p.splits, C, ldc, CI, ldcin, BI, M, N, alpha, beta);
@@ -722,10 +810,10 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
       KH_CHECK_LAUNCH();
       return KH_OK;
     }
-  }
-  if constexpr (is_bf16) {
     if (trans_b && M == 1) {
-      if (launch_gemv1<PRO_NONE, TO>(a, nullptr, nullptr, 0.f, B, ldb, C, CI, BI, N, K, alpha, beta)) {
+      constexpr bool EX = std::is_same<TA, float>::value;
+      if (launch_gemv1<PRO_NONE, TO, EX>(a, nullptr, nullptr, 0.f, (const uint16_t*)B, ldb, C, CI, BI, N, K, alpha,
+                                         beta)) {
         KH_CHECK_LAUNCH();
         return KH_OK;
       }
@@ -736,41 +824,45 @@ int launch_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
     int grid = (waves_needed + 3) / 4;
     if (grid > 4096) grid = 4096;
     const size_t shm = (size_t)M * K * sizeof(float);
-    gemv_nt_kernel<T, TO><<<grid, 256, shm, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta);
+    gemv_nt_kernel<TA, T, TO><<<grid, 256, shm, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                                            beta);
     KH_CHECK_LAUNCH();
     return KH_OK;
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64);
   KH_REQUIRE(grid.y <= 65535, "kh_gemm: m too large for the generic kernel");
-  gemm_generic_kernel<T, TO><<<grid, 256, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta,
-                                                         trans_b);
+  gemm_generic_kernel<TA, T, TO><<<grid, 256, 0, stream()>>>(A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha,
+                                                             beta, trans_b);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
 
 // The fused SwiGLU projection: the MFMA tile kernel with the SWIGLU epilogue, tiles chosen as in
-// launch_gemm, never split over K (the epilogue needs whole sums).
-int launch_gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, uint16_t* H, int64_t ldh,
-                       int M, int N, int K) {
+// launch_gemm, never split over K (the epilogue needs whole sums).  TA = TO: bf16, or fp32
+// activations in and out.
+template <typename TA>
+int launch_gemm_swiglu(const TA* X, int64_t ldx, const uint16_t* W, int64_t ldw, TA* H, int64_t ldh, int M, int N,
+                       int K) {
   int wtm = 1, wtn = 1;
   plain_tile(M, N, wtm, wtn);
   const int tiles_m = (M + g_tile(wtm) - 1) / g_tile(wtm), tiles_n = (N + g_tile(wtn) - 1) / g_tile(wtn);
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_swiglu: grid too large");
-  launch_tile_shape<uint16_t, true>(wtm, wtn, tiles, 1, X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f,
-                                    0.f, tiles_n, K, nullptr);
+  launch_tile_shape<TA, true, TA>(wtm, wtn, tiles, 1, X, ldx, W, ldw, H, ldh, nullptr, 0, nullptr, M, N, K, 1.f, 0.f,
+                                  tiles_n, K, nullptr);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
 
 // The fused QKV projection: 64 x 128 tiles (one head row of 128 per tile column), never split.
-int launch_gemm_qk_norm_rope(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, int M, int N, int K,
+template <typename TA>
+int launch_gemm_qk_norm_rope(const TA* X, int64_t ldx, const uint16_t* W, int64_t ldw, int M, int N, int K,
                              const QknrArgs& qa) {
   const int tiles_m = (M + 63) / 64, tiles_n = N / 128;
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_qk_norm_rope: grid too large");
-  gemm_bf16_nt_kernel<uint16_t, 1, 2, kGemmRectKS, false, kGemmPrefetch, false, true><<<(int)tiles, G_THREADS, 0,
-                                                                                          stream()>>>(
+  constexpr int PF = std::is_same<TA, float>::value ? 2 : kGemmPrefetch;
+  gemm_bf16_nt_kernel<TA, 1, 2, kGemmRectKS, false, PF, false, true, TA><<<(int)tiles, G_THREADS, 0, stream()>>>(
       X, ldx, W, ldw, nullptr, 0, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr, qa);
   KH_CHECK_LAUNCH();
   return KH_OK;
@@ -780,10 +872,14 @@ int launch_gemm_qk_norm_rope(const uint16_t* X, int64_t ldx, const uint16_t* W, 
 
 namespace kh {
 // o_proj of the decode attention block: C = alpha * merge(part) W^T + beta * cin (fp32 out), with
-// the split-K partials merged in every workgroup's prologue.  False when the shapes do not fit.
+// the split-K partials merged in every workgroup's prologue (exact: the merged row kept in fp32,
+// else rounded to bf16 as the unfused path stores it).  False when the shapes do not fit.
 bool launch_gemv_attn_merge(const float* part, const AttnMerge& am, const uint16_t* W, int64_t ldw, float* C,
-                            const float* cin, int N, int K, float alpha, float beta) {
+                            const float* cin, int N, int K, float alpha, float beta, bool exact) {
   if (am.max_chunks > kAttnMergeMaxChunks || K != am.hq * 128) return false;
+  if (exact)
+    return launch_gemv1<PRO_ATTN_MERGE, float, true>(part, nullptr, nullptr, 0.f, W, ldw, C, cin, nullptr, N, K,
+                                                     alpha, beta, am);
   return launch_gemv1<PRO_ATTN_MERGE, float>(part, nullptr, nullptr, 0.f, W, ldw, C, cin, nullptr, N, K, alpha, beta,
                                              am);
 }
@@ -791,60 +887,82 @@ bool launch_gemv_attn_merge(const float* part, const AttnMerge& am, const uint16
 
 extern "C" {
 
-int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, const void* cin,
-            int64_t ldcin, const void* bias, int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b,
-            int dtype, int out_dtype) {
+int kh_gemm_ex(const void* a, int64_t lda, int a_dtype, const void* b, int64_t ldb, int b_dtype, void* c,
+               int64_t ldc, const void* cin, int64_t ldcin, const void* bias, int64_t m, int64_t n, int64_t k,
+               float alpha, float beta, int trans_b, int out_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(m >= 0 && n >= 0 && k >= 0, "kh_gemm: negative extent");
   KH_REQUIRE(m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX, "kh_gemm: extent too large");
-  KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_gemm: unsupported dtype %d", dtype);
+  KH_REQUIRE(a_dtype == KH_BF16 || a_dtype == KH_F32, "kh_gemm: unsupported dtype %d", a_dtype);
+  KH_REQUIRE(b_dtype == KH_BF16 || b_dtype == KH_F32, "kh_gemm: unsupported dtype %d", b_dtype);
+  KH_REQUIRE(!(a_dtype == KH_BF16 && b_dtype == KH_F32),
+             "kh_gemm: a bfloat16 A with a float32 B is not supported (float32 A with bfloat16 B is)");
   KH_REQUIRE(out_dtype == KH_BF16 || out_dtype == KH_F32, "kh_gemm: unsupported output dtype %d", out_dtype);
-  KH_REQUIRE(!(dtype == KH_F32 && out_dtype == KH_BF16), "kh_gemm: fp32 inputs with a bf16 output are not supported");
+  KH_REQUIRE(!(a_dtype == KH_F32 && out_dtype == KH_BF16),
+             "kh_gemm: fp32 inputs with a bf16 output are not supported");
   if (m == 0 || n == 0) return KH_OK;
   KH_REQUIRE(a && b && c, "kh_gemm: null pointer");
   KH_REQUIRE(lda >= k && ldc >= n && (trans_b ? ldb >= k : ldb >= n), "kh_gemm: leading dimension too small");
   KH_REQUIRE(cin == nullptr || ldcin >= n, "kh_gemm: ldcin too small");
   const int M = (int)m, N = (int)n, K = (int)k;
-  if (dtype == KH_BF16 && out_dtype == KH_BF16)
-    return launch_gemm<uint16_t, uint16_t>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
-  if (dtype == KH_BF16)
-    return launch_gemm<uint16_t, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
-  return launch_gemm<float, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
+  if (a_dtype == KH_BF16 && out_dtype == KH_BF16)
+    return launch_gemm<uint16_t, uint16_t, uint16_t>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta,
+                                                     trans_b);
+  if (a_dtype == KH_BF16)
+    return launch_gemm<uint16_t, uint16_t, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta,
+                                                  trans_b);
+  if (b_dtype == KH_BF16)
+    return launch_gemm<float, uint16_t, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta,
+                                               trans_b);
+  return launch_gemm<float, float, float>(a, lda, b, ldb, c, ldc, cin, ldcin, bias, M, N, K, alpha, beta, trans_b);
+}
+
+int kh_gemm(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, const void* cin,
+            int64_t ldcin, const void* bias, int64_t m, int64_t n, int64_t k, float alpha, float beta, int trans_b,
+            int dtype, int out_dtype) {
+  return kh_gemm_ex(a, lda, dtype, b, ldb, dtype, c, ldc, cin, ldcin, bias, m, n, k, alpha, beta, trans_b, out_dtype);
 }
 
 int kh_gemm_split_count(int64_t m, int64_t n, int64_t k, int* splits) {
   KH_REQUIRE(splits != nullptr, "kh_gemm_split_count: null pointer");
   KH_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX,
              "kh_gemm_split_count: bad extents");
-  // bf16 operands, contiguous and 16-byte aligned
+  // bf16 weights, contiguous and 16-byte aligned operands (the split does not depend on A's type)
   const GemmPlan p = gemm_plan(true, k, k, (int)m, (int)n, (int)k, true, 1);
   *splits = p.mfma ? p.splits : 1;
   return KH_OK;
 }
 
 int kh_gemm_splitk_partials(const void* a, int64_t lda, const void* b, int64_t ldb, float* part, int64_t m,
-                            int64_t n, int64_t k, int splits) {
+                            int64_t n, int64_t k, int splits, int a_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(m > 0 && n > 0 && k > 0 && m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX,
              "kh_gemm_splitk_partials: bad extents");
   KH_REQUIRE(a && b && part, "kh_gemm_splitk_partials: null pointer");
   KH_REQUIRE(lda >= k && ldb >= k, "kh_gemm_splitk_partials: leading dimension too small");
-  const GemmPlan p = gemm_plan(aligned16(a) && aligned16(b), lda, ldb, (int)m, (int)n, (int)k, true, 1);
+  KH_REQUIRE(a_dtype == KH_BF16 || a_dtype == KH_F32, "kh_gemm_splitk_partials: unsupported dtype %d", a_dtype);
+  const int ab = a_dtype == KH_F32 ? 4 : 2;
+  const GemmPlan p = gemm_plan(aligned16(a) && aligned16(b), lda, ldb, (int)m, (int)n, (int)k, true, 1, ab);
   KH_REQUIRE(p.mfma && p.splits > 1 && p.splits == splits,
              "kh_gemm_splitk_partials: this product is not split %d ways (kh_gemm_split_count gives the count; "
              "operands must be 16-byte aligned with k and the leading dimensions multiples of 8)", splits);
   KH_REQUIRE(p.tiles <= INT32_MAX / 8, "kh_gemm_splitk_partials: grid too large");
-  launch_gemm_tiles<float>(p, (const uint16_t*)a, lda, (const uint16_t*)b, ldb, nullptr, n, nullptr, 0, nullptr,
-                           (int)m, (int)n, (int)k, 1.f, 0.f, part);
+  if (a_dtype == KH_F32)
+    launch_gemm_tiles<float, float>(p, (const float*)a, lda, (const uint16_t*)b, ldb, nullptr, n, nullptr, 0, nullptr,
+                                    (int)m, (int)n, (int)k, 1.f, 0.f, part);
+  else
+    launch_gemm_tiles<float>(p, (const uint16_t*)a, lda, (const uint16_t*)b, ldb, nullptr, n, nullptr, 0, nullptr,
+                             (int)m, (int)n, (int)k, 1.f, 0.f, part);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
 
 int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, void* h, int64_t ldh, int64_t m,
-                   int64_t n_half, int64_t k) {
+                   int64_t n_half, int64_t k, int x_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(m >= 0 && n_half >= 0 && k > 0 && m <= INT32_MAX && 2 * n_half <= INT32_MAX && k <= INT32_MAX,
              "kh_gemm_swiglu: bad extents");
+  KH_REQUIRE(x_dtype == KH_BF16 || x_dtype == KH_F32, "kh_gemm_swiglu: unsupported dtype %d", x_dtype);
   if (m == 0 || n_half == 0) return KH_OK;
   KH_REQUIRE(x && w_gu && h, "kh_gemm_swiglu: null pointer");
   KH_REQUIRE(n_half % 8 == 0, "kh_gemm_swiglu: the intermediate size %lld is not a multiple of 8", (long long)n_half);
@@ -852,21 +970,26 @@ int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, vo
              "kh_gemm_swiglu: k and the row strides must be multiples of 8 elements (ldx, ldw >= k, ldh >= n_half)");
   KH_REQUIRE(aligned16(x) && aligned16(w_gu), "kh_gemm_swiglu: x and w_gu must be 16-byte aligned");
   const int64_t lim = int64_t(1) << 31;
-  KH_REQUIRE((int64_t)g_tile(2) * ldx * 2 < lim && (int64_t)g_tile(2) * ldw * 2 < lim,
+  const int xb = x_dtype == KH_F32 ? 4 : 2;
+  KH_REQUIRE((int64_t)g_tile(2) * ldx * xb < lim && (int64_t)g_tile(2) * ldw * 2 < lim,
              "kh_gemm_swiglu: row stride too large");
-  return launch_gemm_swiglu((const uint16_t*)x, ldx, (const uint16_t*)w_gu, ldw, (uint16_t*)h, ldh, (int)m,
-                            (int)(2 * n_half), (int)k);
+  if (x_dtype == KH_F32)
+    return launch_gemm_swiglu<float>((const float*)x, ldx, (const uint16_t*)w_gu, ldw, (float*)h, ldh, (int)m,
+                                     (int)(2 * n_half), (int)k);
+  return launch_gemm_swiglu<uint16_t>((const uint16_t*)x, ldx, (const uint16_t*)w_gu, ldw, (uint16_t*)h, ldh, (int)m,
+                                      (int)(2 * n_half), (int)k);
 }
 
 int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
                          int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim, const void* wq,
                          const void* wk, const float* inv_freq, const int32_t* positions, void* q_out, void* k_out,
-                         void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len) {
+                         void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len, int dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(n_batch >= 0 && seq_len >= 0 && k > 0 && k <= INT32_MAX && kv_cache_len >= 0,
              "kh_gemm_qk_norm_rope: bad extents");
   KH_REQUIRE(head_dim == 128, "kh_gemm_qk_norm_rope: head_dim %d (the fused projection takes 128)", head_dim);
   KH_REQUIRE(n_q_heads > 0 && n_kv_heads > 0, "kh_gemm_qk_norm_rope: head counts must be positive");
+  KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_gemm_qk_norm_rope: unsupported dtype %d", dtype);
   const int64_t M = n_batch * seq_len, N = (int64_t)(n_q_heads + 2 * n_kv_heads) * 128;
   KH_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && seq_len <= (int64_t)UINT32_MAX, "kh_gemm_qk_norm_rope: too large");
   if (M == 0) return KH_OK;
@@ -877,11 +1000,13 @@ int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t 
   const void* al[] = {x, w_qkv, wq, wk, q_out, k_out, v_out};
   for (const void* p : al) KH_REQUIRE(aligned16(p), "kh_gemm_qk_norm_rope: operands must be 16-byte aligned");
   const int64_t lim = int64_t(1) << 31;
-  KH_REQUIRE((int64_t)g_tile(2) * ldx * 2 < lim && (int64_t)g_tile(2) * ldw * 2 < lim,
+  const int xb = dtype == KH_F32 ? 4 : 2;
+  KH_REQUIRE((int64_t)g_tile(2) * ldx * xb < lim && (int64_t)g_tile(2) * ldw * 2 < lim,
              "kh_gemm_qk_norm_rope: row stride too large");
   QknrArgs qa;
+  const int64_t vec = 16 / xb;
   for (int i = 0; i < 9; ++i) {
-    KH_REQUIRE(strides[i] % 8 == 0, "kh_gemm_qk_norm_rope: stride %d (%lld) breaks 16-byte alignment", i,
+    KH_REQUIRE(strides[i] % vec == 0, "kh_gemm_qk_norm_rope: stride %d (%lld) breaks 16-byte alignment", i,
                (long long)strides[i]);
     qa.s[i] = strides[i];
   }
@@ -889,31 +1014,40 @@ int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t 
   qa.wk = (const uint16_t*)wk;
   qa.inv_freq = inv_freq;
   qa.positions = positions;
-  qa.q_out = (uint16_t*)q_out;
-  qa.k_out = (uint16_t*)k_out;
-  qa.v_out = (uint16_t*)v_out;
+  qa.q_out = q_out;
+  qa.k_out = k_out;
+  qa.v_out = v_out;
   qa.hq = n_q_heads;
   qa.hkv = n_kv_heads;
   qa.seq_len = (uint32_t)(seq_len > 0 ? seq_len : 1);
   qa.eps = eps;
   qa.kv_cache_len = kv_cache_len;
-  return launch_gemm_qk_norm_rope((const uint16_t*)x, ldx, (const uint16_t*)w_qkv, ldw, (int)M, (int)N, (int)k, qa);
+  if (dtype == KH_F32)
+    return launch_gemm_qk_norm_rope<float>((const float*)x, ldx, (const uint16_t*)w_qkv, ldw, (int)M, (int)N, (int)k,
+                                           qa);
+  return launch_gemm_qk_norm_rope<uint16_t>((const uint16_t*)x, ldx, (const uint16_t*)w_qkv, ldw, (int)M, (int)N,
+                                            (int)k, qa);
 }
 
 int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, const void* w_gu, int64_t ldw,
-                   void* h, int64_t n_half, int64_t k) {
+                   void* h, int64_t n_half, int64_t k, int x_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(prologue == PRO_NONE || prologue == PRO_RMSNORM, "kh_gemv_swiglu: prologue must be 0 (none) or 1 (RMSNorm)");
+  KH_REQUIRE(x_dtype == KH_BF16 || x_dtype == KH_F32, "kh_gemv_swiglu: unsupported dtype %d", x_dtype);
   KH_REQUIRE(n_half > 0 && k > 0 && 2 * n_half <= INT32_MAX && k <= INT32_MAX, "kh_gemv_swiglu: bad extents");
   KH_REQUIRE(n_half % 8 == 0, "kh_gemv_swiglu: the intermediate size %lld is not a multiple of 8", (long long)n_half);
   KH_REQUIRE(x && w_gu && h, "kh_gemv_swiglu: null pointer");
   KH_REQUIRE(prologue != PRO_RMSNORM || norm_w != nullptr, "kh_gemv_swiglu: the RMSNorm prologue needs norm_w");
   KH_REQUIRE(ldw >= k, "kh_gemv_swiglu: ldw < k");
-  const bool ok = prologue == PRO_RMSNORM
-                      ? launch_gemv_swiglu<PRO_RMSNORM>(x, norm_w, eps, (const uint16_t*)w_gu, ldw, (uint16_t*)h,
-                                                        (int)n_half, (int)k)
-                      : launch_gemv_swiglu<PRO_NONE>(x, norm_w, eps, (const uint16_t*)w_gu, ldw, (uint16_t*)h,
-                                                     (int)n_half, (int)k);
+  const uint16_t* W = (const uint16_t*)w_gu;
+  const int NH = (int)n_half, K = (int)k;
+  bool ok;
+  if (x_dtype == KH_F32)
+    ok = prologue == PRO_RMSNORM ? launch_gemv_swiglu<PRO_RMSNORM, true, float>(x, norm_w, eps, W, ldw, (float*)h, NH, K)
+                                 : launch_gemv_swiglu<PRO_NONE, true, float>(x, norm_w, eps, W, ldw, (float*)h, NH, K);
+  else
+    ok = prologue == PRO_RMSNORM ? launch_gemv_swiglu<PRO_RMSNORM>(x, norm_w, eps, W, ldw, (uint16_t*)h, NH, K)
+                                 : launch_gemv_swiglu<PRO_NONE>(x, norm_w, eps, W, ldw, (uint16_t*)h, NH, K);
   KH_REQUIRE(ok, "kh_gemv_swiglu: unsupported operands (need k %% 8 == 0, ldw %% 8 == 0, a 16-byte aligned weight, "
                  "k <= 16384 and byte offsets below 4 GiB)");
   KH_CHECK_LAUNCH();
@@ -922,12 +1056,13 @@ int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, c
 
 int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps, const void* w,
                   int64_t ldw, void* c, const void* cin, const void* bias, int64_t n, int64_t k, float alpha,
-                  float beta, int out_dtype) {
+                  float beta, int out_dtype, int x_dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(prologue >= PRO_NONE && prologue <= PRO_SILU_MUL_IL, "kh_gemv_fused: unknown prologue %d", prologue);
   KH_REQUIRE(prologue != PRO_SILU_MUL_IL || k % 8 == 0, "kh_gemv_fused: the interleaved silu*mul prologue needs k %% 8 == 0");
   KH_REQUIRE(n >= 0 && k > 0 && n <= INT32_MAX && k <= INT32_MAX, "kh_gemv_fused: bad extents");
   KH_REQUIRE(out_dtype == KH_BF16 || out_dtype == KH_F32, "kh_gemv_fused: unsupported output dtype %d", out_dtype);
+  KH_REQUIRE(x_dtype == KH_BF16 || x_dtype == KH_F32, "kh_gemv_fused: unsupported activation dtype %d", x_dtype);
   if (n == 0) return KH_OK;
   KH_REQUIRE(x && w && c, "kh_gemv_fused: null pointer");
   KH_REQUIRE(prologue != PRO_RMSNORM || norm_w != nullptr, "kh_gemv_fused: the RMSNorm prologue needs norm_w");
@@ -936,21 +1071,27 @@ int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_
   const int N = (int)n, K = (int)k;
   const uint16_t* W = (const uint16_t*)w;
   bool ok = false;
-  auto run = [&](auto* C, auto* CI, auto* BI) {
+  auto run = [&](auto* C, auto* CI, auto* BI, auto ex) {
     using TO = std::remove_const_t<std::remove_pointer_t<decltype(CI)>>;
+    constexpr bool EX = decltype(ex)::value;
     if (prologue == PRO_RMSNORM)
-      ok = launch_gemv1<PRO_RMSNORM, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+      ok = launch_gemv1<PRO_RMSNORM, TO, EX>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
     else if (prologue == PRO_SILU_MUL)
-      ok = launch_gemv1<PRO_SILU_MUL, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+      ok = launch_gemv1<PRO_SILU_MUL, TO, EX>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
     else if (prologue == PRO_SILU_MUL_IL)
-      ok = launch_gemv1<PRO_SILU_MUL_IL, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+      ok = launch_gemv1<PRO_SILU_MUL_IL, TO, EX>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
     else
-      ok = launch_gemv1<PRO_NONE, TO>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
+      ok = launch_gemv1<PRO_NONE, TO, EX>(x, x2, norm_w, eps, W, ldw, C, CI, BI, N, K, alpha, beta);
   };
-  if (out_dtype == KH_F32)
-    run((float*)c, (const float*)cin, (const float*)bias);
+  const bool exact = x_dtype == KH_F32;
+  if (out_dtype == KH_F32 && exact)
+    run((float*)c, (const float*)cin, (const float*)bias, std::true_type{});
+  else if (out_dtype == KH_F32)
+    run((float*)c, (const float*)cin, (const float*)bias, std::false_type{});
+  else if (exact)
+    run((uint16_t*)c, (const uint16_t*)cin, (const uint16_t*)bias, std::true_type{});
   else
-    run((uint16_t*)c, (const uint16_t*)cin, (const uint16_t*)bias);
+    run((uint16_t*)c, (const uint16_t*)cin, (const uint16_t*)bias, std::false_type{});
   KH_REQUIRE(ok, "kh_gemv_fused: unsupported operands (need k %% 8 == 0, ldw %% 8 == 0, a 16-byte aligned weight, "
                  "k <= 16384 and byte offsets below 4 GiB)");
   KH_CHECK_LAUNCH();

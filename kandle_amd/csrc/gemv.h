@@ -3,6 +3,8 @@
 // the weight-row streamer.  Header-only device code (each translation unit gets its own copy).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace kh {
@@ -23,10 +25,16 @@ constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2, PRO_SILU_MUL_IL =
 constexpr int kAttnMergeMaxChunks = 8;   // split-K chunks the attention-merge prologue accepts
 constexpr int GV_CHUNK = 512;  // columns per wave-wide 16-byte load (64 lanes x 8 bf16)
 
-template <int PRO>
-__device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const uint16_t* x2, const uint16_t* nw,
+// EX (exact): x' keeps the fp32 value of every element instead of rounding it to bf16, and the
+// inputs of prologues 0, 2 and 3 (x, x2) are fp32 instead of bf16 -- the float32 activations of
+// the reference's arithmetic.
+template <int PRO, bool EX = false>
+__device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const void* x2v, const uint16_t* nw,
                                               float eps, int K, int kpad, const AttnMerge& am) {
   const int tid = threadIdx.x;
+  // x' as stored by the producer: rounded to bf16, or kept whole (EX)
+  auto rnd = [](float v) { return EX ? v : round_bf16(v); };
+  using TX = std::conditional_t<EX, float, uint16_t>;
   if constexpr (PRO == PRO_ATTN_MERGE) {
     // Thread t merges columns 8 (t mod 16) .. + 7 of head t / 16 (then t + 256, ...): the chunks'
     // (m, l, o) combined with weights exp(m_c - M), M the largest chunk max.  Up to kAttnMergeMaxChunks
@@ -66,7 +74,7 @@ __device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const ui
             t[4] += ob[c].x * f; t[5] += ob[c].y * f; t[6] += ob[c].z * f; t[7] += ob[c].w * f;
           }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = round_bf16(Ls > 0.f ? t[e] / Ls : 0.f);
+          for (int e = 0; e < 8; ++e) v[e] = rnd(Ls > 0.f ? t[e] / Ls : 0.f);
         }
       }
 #pragma unroll
@@ -101,25 +109,26 @@ __device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const ui
 #pragma unroll
       for (int j = 0; j < PR; ++j) {
         const int i = tid + j * blockDim.x;
-        if (i < kpad) xs[i] = i < K ? round_bf16((xv[j] * inv) * wv[j]) : 0.f;
+        if (i < kpad) xs[i] = i < K ? rnd((xv[j] * inv) * wv[j]) : 0.f;
       }
     } else {
       for (int i = tid; i < kpad; i += blockDim.x)
-        xs[i] = i < K ? round_bf16((xf[i] * inv) * bf16_bits_to_f32(nw[i])) : 0.f;
+        xs[i] = i < K ? rnd((xf[i] * inv) * bf16_bits_to_f32(nw[i])) : 0.f;
     }
   } else if constexpr (PRO == PRO_SILU_MUL) {
-    const uint16_t* g = (const uint16_t*)x;
+    const TX* g = (const TX*)x;
+    const TX* x2 = (const TX*)x2v;
     for (int i = tid; i < kpad; i += blockDim.x)
-      xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(g[i])) * bf16_bits_to_f32(x2[i])) : 0.f;
+      xs[i] = i < K ? rnd(silu_ref(Elem<TX>::load(g, i)) * Elem<TX>::load(x2, i)) : 0.f;
   } else if constexpr (PRO == PRO_SILU_MUL_IL) {
-    const uint16_t* gu = (const uint16_t*)x;
+    const TX* gu = (const TX*)x;
     for (int i = tid; i < kpad; i += blockDim.x) {
       const int gi = 16 * (i >> 3) + (i & 7);
-      xs[i] = i < K ? round_bf16(silu_ref(bf16_bits_to_f32(gu[gi])) * bf16_bits_to_f32(gu[gi + 8])) : 0.f;
+      xs[i] = i < K ? rnd(silu_ref(Elem<TX>::load(gu, gi)) * Elem<TX>::load(gu, gi + 8)) : 0.f;
     }
   } else {
-    const uint16_t* xb = (const uint16_t*)x;
-    for (int i = tid; i < kpad; i += blockDim.x) xs[i] = i < K ? bf16_bits_to_f32(xb[i]) : 0.f;
+    const TX* xb = (const TX*)x;
+    for (int i = tid; i < kpad; i += blockDim.x) xs[i] = i < K ? Elem<TX>::load(xb, i) : 0.f;
   }
   __syncthreads();
 }
@@ -133,8 +142,9 @@ __device__ __forceinline__ void gemv_prologue(float* xs, const void* x, const ui
 // PAIR8 (U = 2, SwiGLU): the weight interleaves gate and up rows in blocks of 8 (rows 16i .. 16i+7
 // gate rows 8i .. 8i+7, rows 16i+8 .. 16i+15 the matching up rows); row group q = n0 / 2 is gate row
 // 16 (q / 8) + q % 8 and its up row 8 later, and the output is feature q:
-// bf16(silu(bf16(gate)) * bf16(up)), the value the silu * mul prologue of the next projection forms.
-template <int U, bool PAIR8 = false>
+// bf16(silu(bf16(gate)) * bf16(up)), the value the silu * mul prologue of the next projection forms
+// (EX: silu(gate) * up of the fp32 sums, unrounded).
+template <int U, bool PAIR8 = false, bool EX = false>
 struct GemvRows {
   static_assert(!PAIR8 || U == 2, "paired gate/up rows take two rows per group");
   static constexpr int CB = 8 / U;  // 16-byte loads in flight per row per lane
@@ -222,7 +232,12 @@ struct GemvRows {
       }
       if constexpr (PAIR8) {
         const float gsum = wave_sum(acc[0]), usum = wave_sum(acc[1]);
-        if (lane == 0) Elem<TO>::store(C, n0 >> 1, silu_ref(round_bf16(gsum)) * round_bf16(usum));
+        if (lane == 0) {
+          if constexpr (EX)
+            Elem<TO>::store(C, n0 >> 1, silu_ref(gsum) * usum);
+          else
+            Elem<TO>::store(C, n0 >> 1, silu_ref(round_bf16(gsum)) * round_bf16(usum));
+        }
       } else {
 #pragma unroll
         for (int u = 0; u < U; ++u) {

@@ -157,14 +157,15 @@ def linear(input: Tensor, weight: Tensor, bias: Optional[Tensor] = None, out_dty
 
 def linear_fused(prologue: str, x: Tensor, weight: Tensor, norm_weight: Optional[Tensor] = None,
                  eps: float = 1e-6, x2: Optional[Tensor] = None, residual: Optional[Tensor] = None,
-                 out_dtype: Optional[str] = None) -> Tensor:
+                 out_dtype: Optional[str] = None, act_dtype: str = "bfloat16") -> Tensor:
     """One-row linear with its producer fused in front (decode).  prologue 'rms_norm': x is the
     fp32 residual row and the input is rms_norm(x, norm_weight, eps); 'silu_mul': the input is
     silu(x) * x2; 'silu_mul_interleaved': x is a gate/up row interleaved in blocks of 8 and the
-    input is silu(gate) * up; 'none': the input is x.  With `residual` the result is added into it in place
-    (residual += input @ weight^T) and returned; otherwise a new [1, out_features] tensor of
-    out_dtype (default bf16)."""
-    params = {"eps": eps}
+    input is silu(gate) * up; 'none': the input is x.  act_dtype is the activations' dtype: bfloat16
+    (the input rounded to bf16 as the unfused producer stores it) or float32 (kept in fp32).  With
+    `residual` the result is added into it in place (residual += input @ weight^T) and returned;
+    otherwise a new [1, out_features] tensor of out_dtype (default act_dtype)."""
+    params = {"eps": eps, "act_dtype": act_dtype}
     if norm_weight is not None:
         params["norm_weight"] = norm_weight.handle
     if x2 is not None:
@@ -174,7 +175,7 @@ def linear_fused(prologue: str, x: Tensor, weight: Tensor, norm_weight: Optional
         params["beta"] = 1.0
         out = residual.handle
     else:
-        out = _new(weight, (1, weight.shape[0]), out_dtype or "bfloat16")
+        out = _new(weight, (1, weight.shape[0]), out_dtype or act_dtype)
     _kernel(weight, "gemv_fused")(prologue, x.handle, weight.handle, out, params)
     if residual is not None:
         return residual
@@ -182,11 +183,12 @@ def linear_fused(prologue: str, x: Tensor, weight: Tensor, norm_weight: Optional
 
 
 def linear_swiglu_row(prologue: str, x: Tensor, w_gu: Tensor, norm_weight: Optional[Tensor] = None,
-                      eps: float = 1e-6) -> Tensor:
-    """One-row SwiGLU (decode): silu(x' W_gate^T) * (x' W_up^T) as a new bf16 [1, I] tensor from the
-    interleaved gate/up weight [2I, H]; prologue 'rms_norm' (x the fp32 residual row, x' its
-    RMSNorm) or 'none' (x' = x, bf16)."""
-    out = _new(w_gu, (1, w_gu.shape[0] // 2), "bfloat16")
+                      eps: float = 1e-6, act_dtype: str = "bfloat16") -> Tensor:
+    """One-row SwiGLU (decode): silu(x' W_gate^T) * (x' W_up^T) as a new [1, I] tensor of act_dtype
+    (bfloat16: x', gate and up rounded to bf16; float32: all kept in fp32) from the interleaved
+    gate/up weight [2I, H]; prologue 'rms_norm' (x the fp32 residual row, x' its RMSNorm) or 'none'
+    (x' = x, of act_dtype)."""
+    out = _new(w_gu, (1, w_gu.shape[0] // 2), act_dtype)
     params = {"eps": eps}
     if norm_weight is not None:
         params["norm_weight"] = norm_weight.handle
@@ -300,8 +302,9 @@ def arange(start: float, end: Optional[float] = None, step: float = 1.0, dtype: 
 
 def linear_swiglu(input: Tensor, weight_gu: Tensor) -> Tensor:
     """silu(input W_gate^T) * (input W_up^T) in one launch from the interleaved gate/up weight
-    [2 I, H] (kernels.interleave_gate_up); returns [..., I] bf16 (swiglu.ts:119-134)."""
-    out = _new(input, tuple(input.shape[:-1]) + (weight_gu.shape[0] // 2,), "bfloat16")
+    [2 I, H] (kernels.interleave_gate_up); returns [..., I] of input's dtype (bf16, or float32 with
+    float32 activations) (swiglu.ts:119-134)."""
+    out = _new(input, tuple(input.shape[:-1]) + (weight_gu.shape[0] // 2,), input.dtype)
     _kernel(input, "linear_swiglu")(input.handle, weight_gu.handle, out)
     return _wrap(out)
 

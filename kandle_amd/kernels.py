@@ -27,7 +27,7 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import _lib
-from .dtypes import BFLOAT16, FLOAT32, INT32
+from .dtypes import BFLOAT16, FLOAT32, INT32, KH_CODE
 from .tensor import HipTensorHandle, copy_into, contiguous_strides
 
 _vp = C.c_void_p
@@ -199,22 +199,28 @@ def decode_attention(q, k_cache, v_cache, seq_lens, output, scale: float) -> Non
 
 
 def decode_attention_block(qkv, params: dict) -> None:
-    """The attention block of one decode step (kh_decode_attention_block): qkv bf16 [1, hq*D + 2*hkv*D]
+    """The attention block of one decode step (kh_decode_attention_block): qkv [1, hq*D + 2*hkv*D]
     raw projections of the new token; params: q_norm, k_norm (bf16 [D]), inv_freq (fp32 [D/2]), eps,
-    position (int32 [1], device), k_cache / v_cache ([1, hkv, max_len, D] bf16), w_o (bf16
-    [hidden, hq*D]), x (fp32 residual row [1, hidden], updated in place), scale."""
+    position (int32 [1], device), k_cache / v_cache ([1, hkv, max_len, D], qkv's dtype), w_o (bf16
+    [hidden, hq*D]), x (fp32 residual row [1, hidden], updated in place), scale.  qkv and the caches
+    are bfloat16 (values rounded to bf16 where the unfused launches store them) or float32 (every
+    activation kept in fp32)."""
     kc, vc, wo, x = params["k_cache"], params["v_cache"], params["w_o"], params["x"]
     _, hkv, max_len, D = kc.shape
     n_in = qkv.numel
     hq = (n_in - 2 * hkv * D) // D
     if D != 128 or hq <= 0 or hq * D + 2 * hkv * D != n_in:
         raise ValueError(f"decode_attention_block: qkv of {n_in} values does not split into q/k/v heads of 128")
-    for name, h in (("qkv", qkv), ("q_norm", params["q_norm"]), ("k_norm", params["k_norm"]), ("k_cache", kc),
-                    ("v_cache", vc), ("w_o", wo)):
+    if qkv.dtype not in (FLOAT32, BFLOAT16):
+        raise TypeError("decode_attention_block: qkv must be float32 or bfloat16")
+    for name, h in (("k_cache", kc), ("v_cache", vc)):
+        if h.dtype != qkv.dtype:
+            raise TypeError(f"decode_attention_block: {name} must have qkv's dtype {qkv.dtype}")
+    for name, h in (("q_norm", params["q_norm"]), ("k_norm", params["k_norm"]), ("w_o", wo)):
         if h.dtype != BFLOAT16:
             raise TypeError(f"decode_attention_block: {name} must be bfloat16")
     if not qkv.is_contiguous() or x.dtype != FLOAT32 or not x.is_contiguous():
-        raise TypeError("decode_attention_block: qkv (bf16) and x (fp32) must be contiguous")
+        raise TypeError("decode_attention_block: qkv and x (fp32) must be contiguous")
     n_out = x.numel
     if tuple(wo.shape) != (n_out, hq * D) or wo.strides[1] != 1:
         raise ValueError(f"decode_attention_block: w_o must be [{n_out}, {hq * D}] with contiguous rows")
@@ -225,7 +231,7 @@ def decode_attention_block(qkv, params: dict) -> None:
     _lib.call("kh_decode_attention_block", _vp(qkv.data_ptr()), _vp(params["q_norm"].data_ptr()),
               _vp(params["k_norm"].data_ptr()), _vp(params["inv_freq"].data_ptr()), C.c_float(params["eps"]),
               _vp(pos.data_ptr()), _vp(kc.data_ptr()), _vp(vc.data_ptr()), hq, hkv, max_len, strides,
-              C.c_float(params["scale"]), _vp(wo.data_ptr()), wo.strides[0], n_out, _vp(x.data_ptr()))
+              C.c_float(params["scale"]), _vp(wo.data_ptr()), wo.strides[0], n_out, _vp(x.data_ptr()), qkv.kh_dtype)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -254,9 +260,13 @@ class MatmulDispatchResult:
 def matmul(config: MatmulDispatchResult, a: HipTensorHandle, b: HipTensorHandle) -> None:
     """out[..., M, N] = alpha * A[..., M, K] op(B) + beta * C (+ bias), one GEMM per batch entry.
 
-    `b` is [..., K, N] (transpose_b False) or [..., N, K] (transpose_b True, the nn.Linear weight)."""
+    `b` is [..., K, N] (transpose_b False) or [..., N, K] (transpose_b True, the nn.Linear weight).
+    Operands share a dtype (float32 or bfloat16), except that float32 activations may meet bfloat16
+    weights: the reference's float32 matmul of a checkpoint it widens to float32 on load
+    (io/safetensor/dtypes.ts:17-31), computed from the bf16 weights directly (kh_gemm_ex)."""
     out = config.output
-    if a.dtype != b.dtype:
+    mixed = a.dtype == FLOAT32 and b.dtype == BFLOAT16
+    if a.dtype != b.dtype and not mixed:
         raise TypeError(f"matmul: dtype mismatch {a.dtype} vs {b.dtype}")
     if a.dtype not in (FLOAT32, BFLOAT16):
         raise TypeError(f"matmul does not support dtype {a.dtype}")
@@ -321,7 +331,7 @@ def _batch_offsets(h: HipTensorHandle, batch_shape, mat_dims: int):
 
 def _gemm_call(A, lda, Bm, out, N, config, rows, a_off, b_off, c_off):
     K = config.K
-    isz = A.itemsize
+    isz, bsz = A.itemsize, Bm.itemsize
     osz = out.itemsize
     # [.., N, K] (transpose_b) or [.., K, N]: either way the row stride of the stored matrix.
     ldb = Bm.strides[-2] if len(Bm.shape) >= 2 else Bm.shape[-1]
@@ -338,14 +348,13 @@ def _gemm_call(A, lda, Bm, out, N, config, rows, a_off, b_off, c_off):
         bias_ptr = config.bias.data_ptr()
     lda_eff = lda if lda else K
     _lib.call(
-        "kh_gemm",
-        _vp(A.data_ptr() + a_off * isz), lda_eff,
-        _vp(Bm.data_ptr() + b_off * isz), ldb,
+        "kh_gemm_ex",
+        _vp(A.data_ptr() + a_off * isz), lda_eff, A.kh_dtype,
+        _vp(Bm.data_ptr() + b_off * bsz), ldb, Bm.kh_dtype,
         _vp(out.data_ptr() + c_off * osz), N,
         _vp(cin_ptr) if cin_ptr else None, ldcin,
         _vp(bias_ptr) if bias_ptr else None,
-        rows, N, K, C.c_float(config.alpha), C.c_float(config.beta), int(bool(config.transpose_b)), A.kh_dtype,
-        out.kh_dtype,
+        rows, N, K, C.c_float(config.alpha), C.c_float(config.beta), int(bool(config.transpose_b)), out.kh_dtype,
     )
 
 
@@ -666,13 +675,14 @@ def interleave_gate_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
 
 
 def linear_swiglu(x, w_gu, output) -> None:
-    """output [..., I] = silu(x W_gate^T) * (x W_up^T), bf16, from the interleaved weight w_gu [2I, H]
-    (interleave_gate_up); x [..., H] bf16 with contiguous rows.  The gate/up projections, silu and
-    mul of SwiGLUMLP.forward (swiglu.ts:119-134) in one launch (kh_gemm_swiglu)."""
+    """output [..., I] = silu(x W_gate^T) * (x W_up^T) from the interleaved bf16 weight w_gu [2I, H]
+    (interleave_gate_up); x [..., H] with contiguous rows, x and output bf16 (gate, up and the
+    product rounded to bf16) or float32 (all kept in fp32).  The gate/up projections, silu and mul
+    of SwiGLUMLP.forward (swiglu.ts:119-134) in one launch (kh_gemm_swiglu)."""
     two_i, H = w_gu.shape
     I = two_i // 2
-    if x.dtype != BFLOAT16 or w_gu.dtype != BFLOAT16 or output.dtype != BFLOAT16:
-        raise TypeError("linear_swiglu: bf16 operands only")
+    if x.dtype not in (BFLOAT16, FLOAT32) or w_gu.dtype != BFLOAT16 or output.dtype != x.dtype:
+        raise TypeError("linear_swiglu: a bf16 weight with bf16 or float32 x and output of x's dtype expected")
     if x.shape[-1] != H or tuple(output.shape) != tuple(x.shape[:-1]) + (I,):
         raise ValueError(f"linear_swiglu: x [..., {H}] and output [..., {I}] expected for w_gu {tuple(w_gu.shape)}")
     if x.strides[-1] != 1 or w_gu.strides[1] != 1 or output.strides[-1] != 1:
@@ -683,13 +693,14 @@ def linear_swiglu(x, w_gu, output) -> None:
     ldx = x.strides[-2] if len(x.shape) >= 2 else H
     ldh = output.strides[-2] if len(output.shape) >= 2 else I
     _lib.call("kh_gemm_swiglu", _vp(x.data_ptr()), ldx, _vp(w_gu.data_ptr()), w_gu.strides[0],
-              _vp(output.data_ptr()), ldh, m, I, H)
+              _vp(output.data_ptr()), ldh, m, I, H, x.kh_dtype)
 
 
 def linear_qk_norm_rope(x, w_qkv, params) -> None:
     """The QKV projection of a multi-token chunk fused with qk-norm, RoPE and the K/V cache write
-    (kh_gemm_qk_norm_rope): x [S, H] bf16 (contiguous rows), w_qkv [(Hq + 2 Hkv) D, H] (q, k, v
-    projection rows concatenated), D = 128.  params: q_weight, k_weight ([D] bf16), inv_freq
+    (kh_gemm_qk_norm_rope): x [S, H] bf16 or float32 (contiguous rows; q_out and the caches of the
+    same dtype), w_qkv [(Hq + 2 Hkv) D, H] bf16 (q, k, v projection rows concatenated), D = 128.
+    params: q_weight, k_weight ([D] bf16), inv_freq
     (float32 [D/2]), positions (int32 [S]), eps, q_out ([1, Hq, S, D] or any [1, Hq, S, D] view with
     a contiguous head dim), k_out / v_out (the KV caches [1, Hkv, max_seq, D]; token t lands in row
     positions[t], rows outside the cache write nothing).  The same values as linear() followed by
@@ -704,8 +715,10 @@ def linear_qk_norm_rope(x, w_qkv, params) -> None:
                          f"w_qkv {tuple(w_qkv.shape)} for Hq = {Hq}, Hkv = {Hkv}")
     if tuple(x.shape) != (S, H) or x.strides[-1] != 1 or w_qkv.strides[1] != 1:
         raise ValueError(f"linear_qk_norm_rope: x [{S}, {H}] with contiguous rows expected, got {tuple(x.shape)}")
-    if any(t.dtype != BFLOAT16 for t in (x, w_qkv, q_out, k_out, v_out)):
-        raise TypeError("linear_qk_norm_rope: bf16 operands only")
+    if x.dtype not in (BFLOAT16, FLOAT32) or any(t.dtype != x.dtype for t in (q_out, k_out, v_out)):
+        raise TypeError("linear_qk_norm_rope: x, q_out and the caches must share a dtype (bf16 or float32)")
+    if w_qkv.dtype != BFLOAT16 or params["q_weight"].dtype != BFLOAT16 or params["k_weight"].dtype != BFLOAT16:
+        raise TypeError("linear_qk_norm_rope: the projection and norm weights must be bfloat16")
     if tuple(v_out.shape) != tuple(k_out.shape):
         raise ValueError("linear_qk_norm_rope: K and V caches must have the same shape")
     pos, inv_freq = params["positions"], params["inv_freq"]
@@ -723,7 +736,7 @@ def linear_qk_norm_rope(x, w_qkv, params) -> None:
     _lib.call("kh_gemm_qk_norm_rope", _vp(x.data_ptr()), x.strides[0], _vp(w_qkv.data_ptr()), w_qkv.strides[0], 1,
               S, H, Hq, Hkv, D, _vp(params["q_weight"].data_ptr()), _vp(params["k_weight"].data_ptr()),
               _vp(inv_freq.data_ptr()), _vp(pos.data_ptr()), _vp(q_out.data_ptr()), _vp(k_out.data_ptr()),
-              _vp(v_out.data_ptr()), _lib.i64_array(st), C.c_float(float(params.get("eps", 1e-6))), L)
+              _vp(v_out.data_ptr()), _lib.i64_array(st), C.c_float(float(params.get("eps", 1e-6))), L, x.kh_dtype)
 
 
 def gemm_split_count(m: int, n: int, k: int) -> int:
@@ -736,9 +749,9 @@ def gemm_split_count(m: int, n: int, k: int) -> int:
 def linear_add_rms_norm(x, w, residual, norm_weight, eps, output, rows=None) -> None:
     """residual += x W^T (fp32, in place) and output = rms_norm(residual) * norm_weight: the
     projection that closes a decoder sub-block, its residual add and the RMSNorm that opens the next
-    (decoder_layer.ts:224-238 with RMSNorm.ts:92-99).  x bf16 [M, K] and w bf16 [N, K] with
-    contiguous rows, residual fp32 [M, N] contiguous, norm_weight [N] and output [R, N] of one dtype
-    (bf16 or fp32).  rows = (r0, r1) restricts the add and the norm to residual rows r0 .. r1 - 1
+    (decoder_layer.ts:224-238 with RMSNorm.ts:92-99).  x [M, K] (bf16, or float32 activations) and w
+    bf16 [N, K] with contiguous rows, residual fp32 [M, N] contiguous, norm_weight [N] and output
+    [R, N] of one dtype (bf16 or fp32).  rows = (r0, r1) restricts the add and the norm to residual rows r0 .. r1 - 1
     (output has r1 - r0 rows; the other residual rows are left as they were), default all rows.
     When kh_gemm would split K for this shape, the partials go straight into kh_add_rms_norm
     (two launches instead of GEMM + split reduction + RMSNorm); the values are those of the
@@ -746,8 +759,8 @@ def linear_add_rms_norm(x, w, residual, norm_weight, eps, output, rows=None) -> 
     M, K = x.shape
     N = w.shape[0]
     r0, r1 = rows if rows is not None else (0, M)
-    if x.dtype != BFLOAT16 or w.dtype != BFLOAT16 or residual.dtype != FLOAT32:
-        raise TypeError("linear_add_rms_norm: bf16 x and w with an fp32 residual expected")
+    if x.dtype not in (BFLOAT16, FLOAT32) or w.dtype != BFLOAT16 or residual.dtype != FLOAT32:
+        raise TypeError("linear_add_rms_norm: bf16 or float32 x and a bf16 w with an fp32 residual expected")
     if w.shape[1] != K or tuple(residual.shape) != (M, N) or tuple(output.shape) != (r1 - r0, N):
         raise ValueError("linear_add_rms_norm: shapes do not match")
     if norm_weight.numel != N or norm_weight.dtype != output.dtype:
@@ -763,16 +776,16 @@ def linear_add_rms_norm(x, w, residual, norm_weight, eps, output, rows=None) -> 
         part = HipTensorHandle.create_new((splits, M, N), FLOAT32)
         try:
             _lib.call("kh_gemm_splitk_partials", _vp(x.data_ptr()), K, _vp(w.data_ptr()), K, _vp(part.data_ptr()),
-                      M, N, K, splits)
+                      M, N, K, splits, x.kh_dtype)
             _lib.call("kh_add_rms_norm", _vp(part.data_ptr() + r0 * N * 4), splits, M * N,
                       _vp(residual.data_ptr() + r0 * N * 4), _vp(norm_weight.data_ptr()), _vp(output.data_ptr()),
                       r1 - r0, N, C.c_float(eps), output.kh_dtype)
         finally:
             part.dispose()
         return
-    _lib.call("kh_gemm", _vp(x.data_ptr()), K, _vp(w.data_ptr()), K, _vp(residual.data_ptr()), N,
-              _vp(residual.data_ptr()), N, None, M, N, K, C.c_float(1.0), C.c_float(1.0), 1, x.kh_dtype,
-              residual.kh_dtype)
+    _lib.call("kh_gemm_ex", _vp(x.data_ptr()), K, x.kh_dtype, _vp(w.data_ptr()), K, w.kh_dtype,
+              _vp(residual.data_ptr()), N, _vp(residual.data_ptr()), N, None, M, N, K, C.c_float(1.0), C.c_float(1.0),
+              1, residual.kh_dtype)
     _lib.call("kh_rms_norm", _vp(residual.data_ptr() + r0 * N * 4), N, _vp(norm_weight.data_ptr()),
               _vp(output.data_ptr()), N, r1 - r0, N, C.c_float(eps), residual.kh_dtype, output.kh_dtype)
 
@@ -780,19 +793,24 @@ def linear_add_rms_norm(x, w, residual, norm_weight, eps, output, rows=None) -> 
 def gemv_fused(prologue: str, x, w, out, params=None) -> None:
     """One-row projection with its producer fused in front (decode): out[1, n] = alpha * x' W^T
     + beta * cin (+ bias) for the bf16 weight W [n, k] (nn.Linear layout), where x' is
-      'none'     -> x (bf16 [k]);
-      'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row x, rounded to bf16;
-      'silu_mul' -> silu(x) * x2 of the bf16 gate/up rows, rounded to bf16;
-      'silu_mul_interleaved' -> the same product read from one bf16 row [2k] holding gate and up
+      'none'     -> x ([k]);
+      'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row x;
+      'silu_mul' -> silu(x) * x2 of the gate/up rows;
+      'silu_mul_interleaved' -> the same product read from one row [2k] holding gate and up
                     interleaved in blocks of 8 (the output of a linear with interleave_gate_up's weight).
-    params: norm_weight, eps, x2, cin, alpha, beta, bias.  out may alias cin (residual add).
+    params: act_dtype (the activations' dtype, default bfloat16: x' rounded to bf16 and x, x2 of
+    'none' / 'silu_mul*' bf16; float32: x' kept in fp32 and x, x2 float32), norm_weight, eps, x2,
+    cin, alpha, beta, bias.  out may alias cin (residual add).
     Fuses RMSNorm.ts:92-99 or swiglu.ts:119-134 into Linear.ts:135-137."""
     params = params or {}
     code = GEMV_PROLOGUES[prologue]
     n, k = w.shape
     if w.dtype != BFLOAT16 or w.strides[1] != 1:
         raise TypeError("gemv_fused: the weight must be bf16 with contiguous rows")
-    want = FLOAT32 if prologue == "rms_norm" else BFLOAT16
+    act = params.get("act_dtype") or BFLOAT16
+    if act not in (BFLOAT16, FLOAT32):
+        raise TypeError(f"gemv_fused: act_dtype must be bfloat16 or float32, not {act}")
+    want = FLOAT32 if prologue == "rms_norm" else act
     x2 = params.get("x2")
     for h, nm in ((x, "x"), (x2, "x2")):
         if h is None:
@@ -817,17 +835,18 @@ def gemv_fused(prologue: str, x, w, out, params=None) -> None:
         _vp(nw.data_ptr()) if nw is not None else None, C.c_float(float(params.get("eps", 1e-6))),
         _vp(w.data_ptr()), w.strides[0], _vp(out.data_ptr()), _vp(cin.data_ptr()) if cin is not None else None,
         _vp(bias.data_ptr()) if bias is not None else None, n, k, C.c_float(float(params.get("alpha", 1.0))),
-        C.c_float(beta), out.kh_dtype,
+        C.c_float(beta), out.kh_dtype, KH_CODE[act],
     )
 
 
 def gemv_swiglu(prologue: str, x, w_gu, out, params=None) -> None:
-    """One-row SwiGLU projection (decode): out[1, I] = silu(x' W_gate^T) * (x' W_up^T) in bf16, from
-    the gate/up weight w_gu [2I, H] interleaved in blocks of 8 rows (interleave_gate_up), where x' is
-    'none' -> x (bf16 [H]) or 'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row.
-    Gate and up are rounded to bf16 before the product, as gemv_fused's gate/up row followed by the
-    'silu_mul_interleaved' prologue forms it (swiglu.ts:119-134 for one token).  params:
-    norm_weight, eps."""
+    """One-row SwiGLU projection (decode): out[1, I] = silu(x' W_gate^T) * (x' W_up^T), from the
+    gate/up weight w_gu [2I, H] interleaved in blocks of 8 rows (interleave_gate_up), where x' is
+    'none' -> x ([H]) or 'rms_norm' -> rms_norm(x, norm_weight, eps) of the fp32 residual row.
+    out's dtype is the activations': bfloat16 (x' and gate and up rounded to bf16 before the
+    product, as gemv_fused's gate/up row followed by the 'silu_mul_interleaved' prologue forms it;
+    x of 'none' bf16) or float32 (all kept in fp32; x of 'none' float32) (swiglu.ts:119-134 for
+    one token).  params: norm_weight, eps."""
     params = params or {}
     if prologue not in ("none", "rms_norm"):
         raise ValueError(f"gemv_swiglu: prologue must be 'none' or 'rms_norm', not {prologue!r}")
@@ -835,17 +854,18 @@ def gemv_swiglu(prologue: str, x, w_gu, out, params=None) -> None:
     n_half = two_i // 2
     if w_gu.dtype != BFLOAT16 or w_gu.strides[1] != 1:
         raise TypeError("gemv_swiglu: the weight must be bf16 with contiguous rows")
-    want = FLOAT32 if prologue == "rms_norm" else BFLOAT16
+    act = out.dtype
+    if act not in (BFLOAT16, FLOAT32) or out.numel != n_half or not out.is_contiguous():
+        raise ValueError(f"gemv_swiglu: out must be a contiguous bf16 or float32 row of {n_half} elements")
+    want = FLOAT32 if prologue == "rms_norm" else act
     if x.dtype != want or x.numel != k or not x.is_contiguous():
         raise ValueError(f"gemv_swiglu: x must be one contiguous {want} row of {k} elements")
-    if out.dtype != BFLOAT16 or out.numel != n_half or not out.is_contiguous():
-        raise ValueError(f"gemv_swiglu: out must be a contiguous bf16 row of {n_half} elements")
     nw = params.get("norm_weight")
     if prologue == "rms_norm" and (nw is None or nw.dtype != BFLOAT16 or nw.numel != k):
         raise ValueError("gemv_swiglu: rms_norm needs a bf16 norm_weight of k elements")
     _lib.call("kh_gemv_swiglu", GEMV_PROLOGUES[prologue], _vp(x.data_ptr()),
               _vp(nw.data_ptr()) if nw is not None else None, C.c_float(float(params.get("eps", 1e-6))),
-              _vp(w_gu.data_ptr()), w_gu.strides[0], _vp(out.data_ptr()), n_half, k)
+              _vp(w_gu.data_ptr()), w_gu.strides[0], _vp(out.data_ptr()), n_half, k, out.kh_dtype)
 
 
 def greedy_advance(next_token, position, seq_len, token_log, log_base: int) -> None:

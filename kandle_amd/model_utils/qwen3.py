@@ -18,8 +18,14 @@ position p:
 then x = rms_norm(x, norm) and logits = x[last] E^T in fp32 with the tied embedding E
 (for_causal_lm.ts:121-125, 184-185); greedy = argmax, lowest index among maxima (:475-508).
 The residual stream x is float32 (embedding rows widened on gather; the o_proj and down GEMMs add
-into it in their fp32 epilogue); every other activation is stored in bf16 between kernels (the norms
-read fp32 x and write bf16 h); math inside kernels is fp32.
+into it in their fp32 epilogue).  The other activations (h, q/k/v, the K/V cache, attention
+output, the SwiGLU product) are stored between kernels in the model's activation dtype:
+  "float32" (default): every activation in fp32, as the reference computes (its bf16 checkpoints
+      are widened to float32 on load, io/safetensor/dtypes.ts:17-31, and every op runs in f32);
+      the weights stay bf16 in HBM and the MFMA GEMMs take each fp32 activation as a bf16 hi + lo
+      pair (kh_gemm_ex), the decode GEMVs multiply in fp32, attention runs in fp32;
+  "bfloat16": rounded to bf16 at each store (half the activation bytes, the fastest path).
+Math inside kernels is fp32 either way.
 """
 from __future__ import annotations
 
@@ -162,10 +168,17 @@ def qwen3_weights_from_safetensor(group, cfg: Qwen3Config, strict: bool = True, 
     return weights, LoadStateDictResult(loaded, missing, unexpected)
 
 
+ACTIVATION_DTYPES = ("float32", "bfloat16")
+
+
 class Qwen3ForCausalLM:
-    def __init__(self, cfg: Qwen3Config, weights: Dict[str, np.ndarray], max_seq_len: int = 1024):
+    def __init__(self, cfg: Qwen3Config, weights: Dict[str, np.ndarray], max_seq_len: int = 1024,
+                 activations: str = "float32"):
+        if activations not in ACTIVATION_DTYPES:
+            raise ValueError(f"activations must be one of {ACTIVATION_DTYPES}, not {activations!r}")
         self.cfg = cfg
         self.max_seq_len = max_seq_len
+        self.act = activations
         self.ops = env.get_backend("hip").operators
         up = lambda a: Tensor(a, dtype="bfloat16")  # noqa: E731  (uint16 bits -> bf16 tensor)
         self.embed = up(weights["model.embed_tokens.weight"])
@@ -190,8 +203,17 @@ class Qwen3ForCausalLM:
                 "w_gu": up(interleave_gate_up(w("mlp.gate_proj.weight"), w("mlp.up_proj.weight"))),
                 "w_down": up(w("mlp.down_proj.weight")),
             })
+        # Norm weights in the activation dtype for the kernels whose weight shares the output's
+        # dtype (rms_norm, linear_add_rms_norm, rms_norm_rope): with float32 activations, the
+        # bf16 values widened exactly (as the reference widens its checkpoint).
+        f32 = lambda t: F.cast(t, "float32")  # noqa: E731
+        for L in self.layers:
+            for k in ("in_norm", "post_norm", "q_norm", "k_norm"):
+                L[k + "_a"] = f32(L[k]) if self.act == "float32" else L[k]
+        self.final_norm_a = f32(self.final_norm) if self.act == "float32" else self.final_norm
         self.rope = RotaryEmbedding(cfg.head_dim, cfg.rope_theta)
-        self.cache = StaticKVCache(cfg.num_hidden_layers, 1, cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
+        self.cache = StaticKVCache(cfg.num_hidden_layers, 1, cfg.num_key_value_heads, max_seq_len, cfg.head_dim,
+                                   dtype=self.act)
         self.scale = 1.0 / np.sqrt(cfg.head_dim)
         # prompt length -> (graph, ids, positions, logits), least recently used first.  Each captured
         # prefill keeps its activations (sized by the prompt length) in the graph's private pool, so
@@ -209,7 +231,7 @@ class Qwen3ForCausalLM:
     # -- decoder body shared by the prefill and the device-resident decode step -------------------
     @classmethod
     def from_pretrained(cls, path: str, max_seq_len: int = 1024, cfg: Optional[Qwen3Config] = None,
-                        strict: bool = True) -> "Qwen3ForCausalLM":
+                        strict: bool = True, activations: str = "float32") -> "Qwen3ForCausalLM":
         """A model from a Hugging Face-layout checkpoint: `path` is a directory holding config.json and
         model.safetensors (or model.safetensors.index.json and its shards), or a .safetensors /
         index file with `cfg` given.  Weights go to the device as bf16 without an fp32 copy."""
@@ -222,7 +244,7 @@ class Qwen3ForCausalLM:
             cfg = Qwen3Config.from_json_file(os.path.join(root, "config.json"))
         with load_safetensor(path) as group:
             weights, result = qwen3_weights_from_safetensor(group, cfg, strict=strict)
-            model = cls(cfg, weights, max_seq_len=max_seq_len)
+            model = cls(cfg, weights, max_seq_len=max_seq_len, activations=activations)
             del weights   # views of the memory maps: released before the files close
         model.load_result = result
         return model
@@ -239,13 +261,14 @@ class Qwen3ForCausalLM:
         cfg = self.cfg
         Hd = cfg.hidden_size
         eps = cfg.rms_norm_eps
+        act = self.act
         one = S == 1
         n_layers = len(self.layers)
         # Multi-token rows: each residual add is fused with the RMSNorm after it
-        # (linear_add_rms_norm), so h -- the normed bf16 input of the next projection -- is carried
-        # from one sub-block to the next; the last down projection normalises only the last row, with
-        # the final norm, for the lm_head.
-        h = None if one else F.rms_norm(x, [Hd], self.layers[0]["in_norm"], eps, out_dtype="bfloat16")
+        # (linear_add_rms_norm), so h -- the normed input of the next projection, in the activation
+        # dtype -- is carried from one sub-block to the next; the last down projection normalises
+        # only the last row, with the final norm, for the lm_head.
+        h = None if one else F.rms_norm(x, [Hd], self.layers[0]["in_norm_a"], eps, out_dtype=act)
         # The fused QKV projection sums each output over all of K, as kh_gemm does when it takes
         # its MFMA tiles (more than 8 rows) without splitting K: only then are the values the same.
         nqkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
@@ -253,7 +276,7 @@ class Qwen3ForCausalLM:
                     and gemm_split_count(S, nqkv, Hd) == 1)
         for li, L in enumerate(self.layers):
             if one and decode_block:
-                qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
+                qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps, act_dtype=act)  # [1, nq + 2 nkv]
                 self.ops.find("decode_attention_block")(qkv.handle, {
                     "q_norm": L["q_norm"].handle, "k_norm": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
                     "eps": eps, "position": positions.handle, "k_cache": self.cache.key_cache[li].handle,
@@ -261,36 +284,38 @@ class Qwen3ForCausalLM:
                     "scale": self.scale})                                                # x += o W_o^T
                 qkv.dispose()
             elif one:
-                qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps)     # [1, nq + 2 nkv]
+                qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps, act_dtype=act)  # [1, nq + 2 nkv]
                 attn_t = self._attention_heads(li, L, qkv, S, positions, attend)
-                F.linear_fused("none", attn_t, L["w_o"], residual=x)                    # x += o W_o^T
+                F.linear_fused("none", attn_t, L["w_o"], residual=x, act_dtype=act)     # x += o W_o^T
                 attn_t.dispose()
             elif fuse_qkv:
                 attn_t = self._attention_heads_fused(li, L, h, S, positions, attend)   # q/k/v from h
                 h.dispose()
-                h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm"], eps)     # x += o W_o^T
+                h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm_a"], eps)   # x += o W_o^T
                 attn_t.dispose()
             else:
                 qkv = F.linear(h, L["w_qkv"])                                          # [S, nq + 2 nkv]
                 h.dispose()
                 attn_t = self._attention_heads(li, L, qkv, S, positions, attend)
-                h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm"], eps)     # x += o W_o^T
+                h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm_a"], eps)   # x += o W_o^T
                 attn_t.dispose()
             if one:
-                a = F.linear_swiglu_row("rms_norm", x, L["w_gu"], L["post_norm"], eps)  # [1, I] = silu(g) * u
-                F.linear_fused("none", a, L["w_down"], residual=x)                     # x += a W_d^T
+                a = F.linear_swiglu_row("rms_norm", x, L["w_gu"], L["post_norm"], eps,
+                                        act_dtype=act)                                 # [1, I] = silu(g) * u
+                F.linear_fused("none", a, L["w_down"], residual=x, act_dtype=act)      # x += a W_d^T
                 a.dispose()
             else:
                 a = F.linear_swiglu(h, L["w_gu"])                                      # [S, I]
                 h.dispose()
                 if li + 1 < n_layers:
-                    h = F.linear_add_rms_norm(a, L["w_down"], x, self.layers[li + 1]["in_norm"], eps)
+                    h = F.linear_add_rms_norm(a, L["w_down"], x, self.layers[li + 1]["in_norm_a"], eps)
                 else:
-                    h = F.linear_add_rms_norm(a, L["w_down"], x, self.final_norm, eps, rows=(S - 1, S))
+                    h = F.linear_add_rms_norm(a, L["w_down"], x, self.final_norm_a, eps, rows=(S - 1, S))
                 a.dispose()
         if one:
             last = F.narrow(x, 0, S - 1, 1)
-            logits = F.linear_fused("rms_norm", last, self.lm_head, self.final_norm, eps, out_dtype="float32")
+            logits = F.linear_fused("rms_norm", last, self.lm_head, self.final_norm, eps, out_dtype="float32",
+                                    act_dtype=act)
             last.dispose()
         else:
             logits = F.linear(h, self.lm_head, out_dtype="float32")                    # [1, vocab] fp32
@@ -304,13 +329,13 @@ class Qwen3ForCausalLM:
         cfg = self.cfg
         Hq, D = cfg.num_attention_heads, cfg.head_dim
         nq = Hq * D
-        q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+        q_heads = HipTensorHandle.create_new((1, Hq, S, D), self.act)
         self.ops.find("linear_qk_norm_rope")(h.handle, L["w_qkv"].handle, {
             "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
             "positions": positions.handle, "eps": cfg.rms_norm_eps, "q_out": q_heads,
             "k_out": self.cache.key_cache[li].handle, "v_out": self.cache.value_cache[li].handle})
-        attn = HipTensorHandle.create_new((S, nq), "bfloat16")
-        attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
+        attn = HipTensorHandle.create_new((S, nq), self.act)
+        attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), self.act, (S * nq, D, nq, 1), 0)
         attend(li, q_heads, attn_view)
         attn_view.dispose()
         q_heads.dispose()
@@ -325,18 +350,18 @@ class Qwen3ForCausalLM:
         q = _split_heads(qkv, 0, S, Hq, D)
         k = _split_heads(qkv, nq, S, Hkv, D)
         v = _split_heads(qkv, nq + nkv, S, Hkv, D)
-        q_heads = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+        q_heads = HipTensorHandle.create_new((1, Hq, S, D), self.act)
         # K (normed + rotated) and V land in the cache rows given by `positions`.
         self.ops.find("rms_norm_rope")(q.handle, k.handle, {
-            "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
+            "q_weight": L["q_norm_a"].handle, "k_weight": L["k_norm_a"].handle, "inv_freq": self.rope.inv_freq.handle,
             "positions": positions.handle, "eps": cfg.rms_norm_eps, "q_out": q_heads,
             "k_out": self.cache.key_cache[li].handle, "v": v.handle, "v_out": self.cache.value_cache[li].handle,
             "cache_positions": True})
         for t in (q, k, v, qkv):
             t.dispose()
-        attn = HipTensorHandle.create_new((S, nq), "bfloat16")
+        attn = HipTensorHandle.create_new((S, nq), self.act)
         # [1, Hq, S, D] view of the [S, Hq*D] buffer: o_proj then reads it as a plain matrix.
-        attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), "bfloat16", (S * nq, D, nq, 1), 0)
+        attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), self.act, (S * nq, D, nq, 1), 0)
         attend(li, q_heads, attn_view)
         attn_view.dispose()
         q_heads.dispose()
@@ -591,7 +616,12 @@ class Qwen3ForCausalLM:
             self._dispose_prefill_graph(key)
         self.cache.dispose()
         heads = [self.lm_head] if self.lm_head is not self.embed else []
-        for t in [self.embed, self.final_norm] + heads + [v for L in self.layers for v in L.values()]:
+        extra = [self.final_norm_a] if self.final_norm_a is not self.final_norm else []
+        owned = {}
+        for L in self.layers:
+            for v in L.values():
+                owned[id(v)] = v   # the *_a norm entries alias the bf16 ones with bf16 activations
+        for t in [self.embed, self.final_norm] + heads + extra + list(owned.values()):
             t.dispose()
 
 

@@ -21,13 +21,23 @@ import numpy as np
 from . import bf16_round, from_bf16_bits, qk_norm_rope, rms_norm, rope_inv_freq
 
 
+ROUNDING_POINTS = ("norm", "qkv", "qk_rope", "attn", "gate_up", "act", "final_norm")
+
+
 class Qwen3Oracle:
     """exact=True drops the bf16 rounding points (every intermediate stays float32/float64): the
-    form checked against an independent float32 implementation of the architecture."""
+    form checked against an independent float32 implementation of the architecture.  `rounding`
+    names the points that are rounded to bf16 (a subset of ROUNDING_POINTS; default: all of them
+    unless exact)."""
 
-    def __init__(self, cfg, weights_bits, max_seq_len: int = 1024, exact: bool = False):
+    def __init__(self, cfg, weights_bits, max_seq_len: int = 1024, exact: bool = False, rounding=None):
         self.cfg = cfg
-        self.r = (lambda a: np.asarray(a, np.float32)) if exact else bf16_round  # noqa: E731
+        if rounding is None:
+            rounding = () if exact else ROUNDING_POINTS
+        unknown = set(rounding) - set(ROUNDING_POINTS)
+        if unknown:
+            raise ValueError(f"unknown rounding points {sorted(unknown)}")
+        self.rounding = frozenset(rounding)
         f = lambda n: from_bf16_bits(weights_bits[n])  # noqa: E731
         self.embed = f("model.embed_tokens.weight")
         self.final_norm = f("model.norm.weight")
@@ -44,6 +54,10 @@ class Qwen3Oracle:
         Hkv, D = cfg.num_key_value_heads, cfg.head_dim
         self.k_cache = [np.zeros((Hkv, max_seq_len, D), np.float32) for _ in range(cfg.num_hidden_layers)]
         self.v_cache = [np.zeros((Hkv, max_seq_len, D), np.float32) for _ in range(cfg.num_hidden_layers)]
+
+    def r(self, a, point: str):
+        """a as float32, rounded to bf16 when `point` is one of the active rounding points."""
+        return bf16_round(a) if point in self.rounding else np.asarray(a, np.float32)
 
     @staticmethod
     def _sdpa(q, k, v, scale, causal):
@@ -72,26 +86,26 @@ class Qwen3Oracle:
         x = self.embed[np.asarray(ids)].astype(np.float32)                    # fp32 residual [S, Hd]
         positions = np.arange(pos, end, dtype=np.int32)
         for li, L in enumerate(self.layers):
-            h = self.r(rms_norm(x, L["in_norm"], eps))
-            q = self.r(h @ L["q"].T).reshape(S, Hq, D)
-            k = self.r(h @ L["k"].T).reshape(S, Hkv, D)
-            v = self.r(h @ L["v"].T).reshape(S, Hkv, D)
-            qh = self.r(qk_norm_rope(q, L["q_norm"], positions, self.inv_freq, eps)).transpose(1, 0, 2)
-            kh = self.r(qk_norm_rope(k, L["k_norm"], positions, self.inv_freq, eps)).transpose(1, 0, 2)
+            h = self.r(rms_norm(x, L["in_norm"], eps), "norm")
+            q = self.r(h @ L["q"].T, "qkv").reshape(S, Hq, D)
+            k = self.r(h @ L["k"].T, "qkv").reshape(S, Hkv, D)
+            v = self.r(h @ L["v"].T, "qkv").reshape(S, Hkv, D)
+            qh = self.r(qk_norm_rope(q, L["q_norm"], positions, self.inv_freq, eps), "qk_rope").transpose(1, 0, 2)
+            kh = self.r(qk_norm_rope(k, L["k_norm"], positions, self.inv_freq, eps), "qk_rope").transpose(1, 0, 2)
             self.k_cache[li][:, pos:end] = kh
             self.v_cache[li][:, pos:end] = v.transpose(1, 0, 2)
             o = self._sdpa(qh, self.k_cache[li][:, :end], self.v_cache[li][:, :end], 1.0 / np.sqrt(D), S > 1)
-            o = self.r(o.transpose(1, 0, 2).reshape(S, Hq * D).astype(np.float32))
+            o = self.r(o.transpose(1, 0, 2).reshape(S, Hq * D), "attn")
             x = (x + (o @ L["o"].T)).astype(np.float32)
-            h = self.r(rms_norm(x, L["post_norm"], eps))
+            h = self.r(rms_norm(x, L["post_norm"], eps), "norm")
             g = h @ L["gate"].T
             u = h @ L["up"].T
-            g = self.r(g)
-            u = self.r(u)
+            g = self.r(g, "gate_up")
+            u = self.r(u, "gate_up")
             c = np.clip(g.astype(np.float64), -88.0, 88.0)
-            a = self.r((g / (1.0 + np.exp(-c)) * u).astype(np.float32))
+            a = self.r(g / (1.0 + np.exp(-c)) * u, "act")
             x = (x + (a @ L["down"].T)).astype(np.float32)
-        xf = self.r(rms_norm(x[-1:], self.final_norm, eps))
+        xf = self.r(rms_norm(x[-1:], self.final_norm, eps), "final_norm")
         return (xf @ self.embed.T)[0].astype(np.float32)
 
     def generate(self, prompt_ids, max_new_tokens: int):

@@ -12,6 +12,7 @@
  *   --eager            issue every launch from the host (default: prefill and decode step replayed
  *                      from HIP graphs)
  *   --warmup N         tokens of the untimed warm-up generation (default 8; it captures the graphs)
+ *   --activations A    float32 (default: the reference's float32 arithmetic) or bfloat16
  * Prints one JSON line: the generated token ids, prefill_ms and decode tokens/s of the timed run.
  */
 const fs = require('fs');
@@ -42,21 +43,26 @@ function configFrom(hf) {
 
 async function main() {
   const argv = process.argv.slice(2);
-  const pos = argv.filter((a, i) => !a.startsWith('--') && !(i > 0 && argv[i - 1] === '--warmup'));
+  const pos = argv.filter((a, i) => !a.startsWith('--') &&
+                                    !(i > 0 && (argv[i - 1] === '--warmup' || argv[i - 1] === '--activations')));
   if (pos.length !== 4) {
-    console.error('usage: node examples/generate.js CONFIG.json MODEL.safetensors PROMPT_IDS.json NEW_TOKENS [--eager] [--warmup N]');
+    console.error('usage: node examples/generate.js CONFIG.json MODEL.safetensors PROMPT_IDS.json NEW_TOKENS ' +
+                  '[--eager] [--warmup N] [--activations float32|bfloat16]');
     process.exit(2);
   }
   const [cfgPath, modelPath, idsPath, nStr] = pos;
   const useGraph = !argv.includes('--eager');
   const wi = argv.indexOf('--warmup');
   const warmup = wi >= 0 ? parseInt(argv[wi + 1], 10) : 8;
+  const ai = argv.indexOf('--activations');
+  const activations = ai >= 0 ? argv[ai + 1] : 'float32';
   const N = parseInt(nStr, 10);
   const cfg = configFrom(JSON.parse(fs.readFileSync(cfgPath, 'utf8')));
   const prompt = JSON.parse(fs.readFileSync(idsPath, 'utf8'));
   const backend = await HipBackend.create(0);
   const t0 = performance.now();
-  const model = Qwen3ForCausalLM.fromSafetensors(backend, cfg, modelPath, prompt.length + Math.max(N, warmup));
+  const model = Qwen3ForCausalLM.fromSafetensors(backend, cfg, modelPath, prompt.length + Math.max(N, warmup),
+                                                 activations);
   const loadMs = performance.now() - t0;
   try {
     let warm = null;
@@ -73,6 +79,7 @@ async function main() {
       decode_tokens_per_s: decodeWindowMs > 0 ? (replaySteps * 1000) / decodeWindowMs : null,
       decode_steps_timed: replaySteps,
       issue: useGraph ? 'hip graph replay' : 'eager',
+      activations,
     }));
   } finally {
     model.dispose();

@@ -23,7 +23,7 @@
 
 #include "kandle_hip.h"
 
-#define MAX_ARGS 20
+#define MAX_ARGS 24
 #define MAX_LIST 32
 
 typedef struct {
@@ -185,6 +185,13 @@ static bool begin(Args* A, napi_env env, napi_callback_info info, const char* fn
   A->bad = false;
   A->n = MAX_ARGS;
   napi_get_cb_info(env, info, &A->n, A->v, NULL, NULL);
+  /* napi reports the count the caller passed, which may exceed the capacity of v: only the first
+     MAX_ARGS values were stored, so reads past them must see "no argument" */
+  if (A->n > MAX_ARGS) A->n = MAX_ARGS;
+  if (want > MAX_ARGS) {
+    napi_throw_error(env, NULL, "kandle_hip: a binding declares more arguments than MAX_ARGS");
+    return false;
+  }
   if (A->n < want) {
     char msg[128];
     snprintf(msg, sizeof msg, "kandle_hip.%s: expected %zu arguments, got %zu", fn, want, A->n);
@@ -461,16 +468,16 @@ FN(philox4x32_10, 4)
   uint64_t seed = arg_u64(A, 0); void* c = arg_ptr(A, 1); int64_t n = arg_i64(A, 2); void* o = arg_ptr(A, 3);
   CALL(kh_philox4x32_10(seed, (const uint32_t*)c, n, (uint32_t*)o))
 /* decodeAttentionBlock(qkv, qNormW, kNormW, invFreq, eps, position, kCache, vCache, hq, hkv, maxLen,
-                        cacheStrides[4], scale, wO, ldw, nOut, x) */
-FN(decodeAttentionBlock, 17)
+                        cacheStrides[4], scale, wO, ldw, nOut, x, dtype) */
+FN(decodeAttentionBlock, 18)
   int64_t cs[4];
   void* qkv = arg_ptr(A, 0); void* qn = arg_ptr(A, 1); void* kn = arg_ptr(A, 2); void* inv = arg_ptr(A, 3);
   double eps = arg_f64(A, 4); void* pos = arg_ptr(A, 5); void* kc = arg_ptr(A, 6); void* vc = arg_ptr(A, 7);
   int hq = arg_int(A, 8); int hkv = arg_int(A, 9); int64_t ml = arg_i64(A, 10); arg_list(A, 11, cs, 4);
   double sc = arg_f64(A, 12); void* wo = arg_ptr(A, 13); int64_t ldw = arg_i64(A, 14); int64_t no = arg_i64(A, 15);
-  void* x = arg_ptr(A, 16);
+  void* x = arg_ptr(A, 16); int dt = arg_int(A, 17);
   CALL(kh_decode_attention_block(qkv, qn, kn, (const float*)inv, (float)eps, (const int32_t*)pos, kc, vc, hq, hkv,
-                                 ml, cs, (float)sc, wo, ldw, no, (float*)x))
+                                 ml, cs, (float)sc, wo, ldw, no, (float*)x, dt))
 
 /* ---------------------------------------------------------------- hot path --------------------- */
 /* rmsNorm(x, xRowStride, w, y, yRowStride, rows, n, eps, dtype, outDtype) */
@@ -535,17 +542,26 @@ FN(gemm, 17)
   double al = arg_f64(A, 12); double be = arg_f64(A, 13); int tb = arg_flag(A, 14); int dt = arg_int(A, 15);
   int odt = arg_int(A, 16);
   CALL(kh_gemm(a, lda, b, ldb, c, ldc, cin, ldcin, bias, m, n, k, (float)al, (float)be, tb, dt, odt))
-/* gemmSwiglu(x, ldx, wGu, ldw, h, ldh, m, nHalf, k): the SwiGLU gate/up projections with silu * mul
-   in the epilogue (swiglu.ts:119-134), weight rows interleaved in blocks of 8 */
-FN(gemmSwiglu, 9)
+/* gemmEx(a, lda, aDtype, b, ldb, bDtype, c, ldc, cin, ldcin, bias, m, n, k, alpha, beta, transB, outDtype):
+   gemm with A and B of their own dtypes (float32 activations by bfloat16 weights) */
+FN(gemmEx, 18)
+  void* a = arg_ptr(A, 0); int64_t lda = arg_i64(A, 1); int adt = arg_int(A, 2); void* b = arg_ptr(A, 3);
+  int64_t ldb = arg_i64(A, 4); int bdt = arg_int(A, 5); void* c = arg_ptr(A, 6); int64_t ldc = arg_i64(A, 7);
+  void* cin = arg_ptr(A, 8); int64_t ldcin = arg_i64(A, 9); void* bias = arg_ptr(A, 10); int64_t m = arg_i64(A, 11);
+  int64_t n = arg_i64(A, 12); int64_t k = arg_i64(A, 13); double al = arg_f64(A, 14); double be = arg_f64(A, 15);
+  int tb = arg_flag(A, 16); int odt = arg_int(A, 17);
+  CALL(kh_gemm_ex(a, lda, adt, b, ldb, bdt, c, ldc, cin, ldcin, bias, m, n, k, (float)al, (float)be, tb, odt))
+/* gemmSwiglu(x, ldx, wGu, ldw, h, ldh, m, nHalf, k, xDtype): the SwiGLU gate/up projections with
+   silu * mul in the epilogue (swiglu.ts:119-134), weight rows interleaved in blocks of 8 */
+FN(gemmSwiglu, 10)
   void* x = arg_ptr(A, 0); int64_t ldx = arg_i64(A, 1); void* w = arg_ptr(A, 2); int64_t ldw = arg_i64(A, 3);
   void* h = arg_ptr(A, 4); int64_t ldh = arg_i64(A, 5); int64_t m = arg_i64(A, 6); int64_t nh = arg_i64(A, 7);
-  int64_t k = arg_i64(A, 8);
-  CALL(kh_gemm_swiglu(x, ldx, w, ldw, h, ldh, m, nh, k))
+  int64_t k = arg_i64(A, 8); int xdt = arg_int(A, 9);
+  CALL(kh_gemm_swiglu(x, ldx, w, ldw, h, ldh, m, nh, k, xdt))
 /* gemmQkNormRope(x, ldx, wQkv, ldw, nBatch, seqLen, k, hq, hkv, headDim, wq, wk, invFreq, positions,
-   qOut, kOut, vOut, strides[9], eps, kvCacheLen): the QKV projection with qk-norm, RoPE and the K/V
-   cache write in its epilogue (gqa.ts:269-309, rope.ts:546-644, kv-cache.ts:164-212) */
-FN(gemmQkNormRope, 20)
+   qOut, kOut, vOut, strides[9], eps, kvCacheLen, dtype): the QKV projection with qk-norm, RoPE and the
+   K/V cache write in its epilogue (gqa.ts:269-309, rope.ts:546-644, kv-cache.ts:164-212) */
+FN(gemmQkNormRope, 21)
   int64_t st[9];
   void* x = arg_ptr(A, 0); int64_t ldx = arg_i64(A, 1); void* w = arg_ptr(A, 2); int64_t ldw = arg_i64(A, 3);
   int64_t nb = arg_i64(A, 4); int64_t sl = arg_i64(A, 5); int64_t k = arg_i64(A, 6);
@@ -553,9 +569,9 @@ FN(gemmQkNormRope, 20)
   void* wq = arg_ptr(A, 10); void* wk = arg_ptr(A, 11); void* inv = arg_ptr(A, 12); void* pos = arg_ptr(A, 13);
   void* qo = arg_ptr(A, 14); void* ko = arg_ptr(A, 15); void* vo = arg_ptr(A, 16);
   arg_list(A, 17, st, 9);
-  double eps = arg_f64(A, 18); int64_t kvl = arg_i64(A, 19);
+  double eps = arg_f64(A, 18); int64_t kvl = arg_i64(A, 19); int dt = arg_int(A, 20);
   CALL(kh_gemm_qk_norm_rope(x, ldx, w, ldw, nb, sl, k, hq, hkv, hd, wq, wk, (const float*)inv, (const int32_t*)pos,
-                            qo, ko, vo, st, (float)eps, kvl))
+                            qo, ko, vo, st, (float)eps, kvl, dt))
 /* gemmSplitCount(m, n, k) -> the split count gemm uses for a contiguous bf16 [m, k] x [n, k]^T */
 static napi_value js_gemmSplitCount(napi_env env, napi_callback_info info) {
   Args A_, *A = &A_;
@@ -568,13 +584,13 @@ static napi_value js_gemmSplitCount(napi_env env, napi_callback_info info) {
   napi_create_int32(env, splits, &out);
   return out;
 }
-/* gemmSplitkPartials(a, lda, b, ldb, part, m, n, k, splits): gemm's split-K stage alone, fp32
+/* gemmSplitkPartials(a, lda, b, ldb, part, m, n, k, splits, aDtype): gemm's split-K stage alone, fp32
    partials [splits][m][n] */
-FN(gemmSplitkPartials, 9)
+FN(gemmSplitkPartials, 10)
   void* a = arg_ptr(A, 0); int64_t lda = arg_i64(A, 1); void* b = arg_ptr(A, 2); int64_t ldb = arg_i64(A, 3);
   void* part = arg_ptr(A, 4); int64_t m = arg_i64(A, 5); int64_t n = arg_i64(A, 6); int64_t k = arg_i64(A, 7);
-  int sp = arg_int(A, 8);
-  CALL(kh_gemm_splitk_partials(a, lda, b, ldb, (float*)part, m, n, k, sp))
+  int sp = arg_int(A, 8); int adt = arg_int(A, 9);
+  CALL(kh_gemm_splitk_partials(a, lda, b, ldb, (float*)part, m, n, k, sp, adt))
 /* addRmsNorm(part, splits, splitStride, x, w, y, rows, n, eps, outDtype): x += sum of the partials
    (residual add, decoder_layer.ts:224-238), then y = rms_norm(x) * w */
 FN(addRmsNorm, 10)
@@ -582,20 +598,20 @@ FN(addRmsNorm, 10)
   void* w = arg_ptr(A, 4); void* y = arg_ptr(A, 5); int64_t rows = arg_i64(A, 6); int64_t n = arg_i64(A, 7);
   double eps = arg_f64(A, 8); int odt = arg_int(A, 9);
   CALL(kh_add_rms_norm((const float*)part, sp, ss, (float*)x, w, y, rows, n, (float)eps, odt))
-/* gemvFused(prologue, x, x2, normW, eps, w, ldw, c, cin, bias, n, k, alpha, beta, outDtype) */
-FN(gemvFused, 15)
+/* gemvFused(prologue, x, x2, normW, eps, w, ldw, c, cin, bias, n, k, alpha, beta, outDtype, xDtype) */
+FN(gemvFused, 16)
   int pro = arg_int(A, 0); void* x = arg_ptr(A, 1); void* x2 = arg_ptr(A, 2); void* nw = arg_ptr(A, 3);
   double eps = arg_f64(A, 4); void* w = arg_ptr(A, 5); int64_t ldw = arg_i64(A, 6); void* c = arg_ptr(A, 7);
   void* cin = arg_ptr(A, 8); void* bias = arg_ptr(A, 9); int64_t n = arg_i64(A, 10); int64_t k = arg_i64(A, 11);
-  double al = arg_f64(A, 12); double be = arg_f64(A, 13); int odt = arg_int(A, 14);
-  CALL(kh_gemv_fused(pro, x, x2, nw, (float)eps, w, ldw, c, cin, bias, n, k, (float)al, (float)be, odt))
+  double al = arg_f64(A, 12); double be = arg_f64(A, 13); int odt = arg_int(A, 14); int xdt = arg_int(A, 15);
+  CALL(kh_gemv_fused(pro, x, x2, nw, (float)eps, w, ldw, c, cin, bias, n, k, (float)al, (float)be, odt, xdt))
 
-/* gemvSwiglu(prologue, x, normW, eps, wGu, ldw, h, nHalf, k) */
-FN(gemvSwiglu, 9)
+/* gemvSwiglu(prologue, x, normW, eps, wGu, ldw, h, nHalf, k, xDtype) */
+FN(gemvSwiglu, 10)
   int pro = arg_int(A, 0); void* x = arg_ptr(A, 1); void* nw = arg_ptr(A, 2); double eps = arg_f64(A, 3);
   void* w = arg_ptr(A, 4); int64_t ldw = arg_i64(A, 5); void* h = arg_ptr(A, 6); int64_t nh = arg_i64(A, 7);
-  int64_t k = arg_i64(A, 8);
-  CALL(kh_gemv_swiglu(pro, x, nw, (float)eps, w, ldw, h, nh, k))
+  int64_t k = arg_i64(A, 8); int xdt = arg_int(A, 9);
+  CALL(kh_gemv_swiglu(pro, x, nw, (float)eps, w, ldw, h, nh, k, xdt))
 
 /* ---------------------------------------------------------------- module ----------------------- */
 #define EXPORT(name) {#name, 0, js_##name, 0, 0, 0, napi_enumerable, 0}
@@ -611,7 +627,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
-      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmSwiglu), EXPORT(gemmQkNormRope), EXPORT(gemmSplitCount),
+      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmEx), EXPORT(gemmSwiglu), EXPORT(gemmQkNormRope), EXPORT(gemmSplitCount),
       EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused), EXPORT(gemvSwiglu),
   };
   napi_define_properties(env, exports, sizeof(d) / sizeof(d[0]), d);

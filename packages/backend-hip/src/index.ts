@@ -330,8 +330,8 @@ function matmul(config: MatmulConfig, a: HipTensorHandle, b: HipTensorHandle): v
     const bPtr = bc.ptr + BigInt((bBatched ? i * N * K : 0) * ITEMSIZE[bc.dtype]);
     const oPtr = out.ptr + BigInt(i * M * N * ITEMSIZE[out.dtype]);
     const cPtr = c === undefined ? null : c.ptr + BigInt((c.numel === batch * M * N ? i * M * N : 0) * ITEMSIZE[c.dtype]);
-    addon.gemm(aPtr, K, bPtr, config.transposeB ? K : N, oPtr, N, cPtr, N, null, M, N, K, config.alpha,
-               config.beta, config.transposeB, ac.kh, out.kh);
+    addon.gemmEx(aPtr, K, ac.kh, bPtr, config.transposeB ? K : N, bc.kh, oPtr, N, cPtr, N, null, M, N, K,
+                 config.alpha, config.beta, config.transposeB, out.kh);
   }
   ac.dispose();
   bc.dispose();
@@ -520,10 +520,12 @@ function zeros(out: HipTensorHandle): void {
 const GEMV_PROLOGUE: { [name: string]: number } = { none: 0, rms_norm: 1, silu_mul: 2, silu_mul_interleaved: 3 };
 
 // gemv_fused(prologue, x, w, out, params): one-row projection (decode) out[1, n] = alpha * x' W^T
-// + beta * cin (+ bias) with the producer of x' fused in front: 'none' x' = x (bf16); 'rms_norm'
+// + beta * cin (+ bias) with the producer of x' fused in front: 'none' x' = x; 'rms_norm'
 // x' = rms_norm(x, normWeight, eps) of the fp32 residual row; 'silu_mul' x' = silu(x) * x2;
 // 'silu_mul_interleaved' the same product from one gate/up row interleaved in blocks of 8
-// (RMSNorm.ts:92-99 or swiglu.ts:119-134 fused into Linear.ts:135-137).  params: normWeight, eps,
+// (RMSNorm.ts:92-99 or swiglu.ts:119-134 fused into Linear.ts:135-137).  params: actDtype (the
+// activations' dtype: 'bfloat16', the default, rounds x' to bf16 and takes bf16 x / x2 for
+// 'none' / 'silu_mul*'; 'float32' keeps x' in fp32 and takes float32 x / x2), normWeight, eps,
 // x2, cin, bias, alpha, beta; out may alias cin (residual add).
 function gemvFused(prologue: string, x: HipTensorHandle, w: HipTensorHandle, out: HipTensorHandle,
                    params?: { [key: string]: any }): void {
@@ -534,7 +536,9 @@ function gemvFused(prologue: string, x: HipTensorHandle, w: HipTensorHandle, out
     throw new Error('gemv_fused: the weight must be bf16 [n, k] with contiguous rows');
   const n = w.shape[0], k = w.shape[1];
   if (out.numel !== n || !out.isContiguous()) throw new Error('gemv_fused: out must be a contiguous row of n elements');
-  const want = prologue === 'rms_norm' ? 'float32' : 'bfloat16';
+  const act = (p.actDtype || 'bfloat16') as DType;
+  if (act !== 'bfloat16' && act !== 'float32') throw new Error('gemv_fused: actDtype must be bfloat16 or float32');
+  const want = prologue === 'rms_norm' ? 'float32' : act;
   const kx = prologue === 'silu_mul_interleaved' ? 2 * k : k;
   const x2 = p.x2 as HipTensorHandle | undefined;
   for (const h of x2 === undefined ? [x] : [x, x2]) {
@@ -548,45 +552,49 @@ function gemvFused(prologue: string, x: HipTensorHandle, w: HipTensorHandle, out
   addon.gemvFused(code, x.ptr, x2 === undefined ? null : x2.ptr, nw === undefined ? null : nw.ptr,
                   p.eps === undefined ? 1e-6 : (p.eps as number), w.ptr, w.strides[0], out.ptr,
                   cin === undefined ? null : cin.ptr, bias === undefined ? null : bias.ptr, n, k,
-                  p.alpha === undefined ? 1 : (p.alpha as number), beta, out.kh);
+                  p.alpha === undefined ? 1 : (p.alpha as number), beta, out.kh, DTYPE_CODE[act]);
 }
 
 // gemv_swiglu(prologue, x, wGu, out, params): one-row SwiGLU (decode): out[1, I] = silu(x' W_gate^T)
-// * (x' W_up^T) in bf16 from the gate/up weight interleaved in blocks of 8 rows; prologue 'none'
-// (x' = x, bf16) or 'rms_norm' (x the fp32 residual row; params normWeight, eps).
+// * (x' W_up^T) from the gate/up weight interleaved in blocks of 8 rows; out's dtype is the
+// activations' (bf16: x', gate and up rounded to bf16; float32: kept in fp32); prologue 'none'
+// (x' = x, of out's dtype) or 'rms_norm' (x the fp32 residual row; params normWeight, eps).
 function gemvSwiglu(prologue: string, x: HipTensorHandle, wGu: HipTensorHandle, out: HipTensorHandle,
                     params?: { [key: string]: any }): void {
   const p = params || {};
   if (prologue !== 'none' && prologue !== 'rms_norm') throw new Error(`gemv_swiglu: unknown prologue ${prologue}`);
   const k = wGu.shape[1], nHalf = wGu.shape[0] / 2;
   if (wGu.dtype !== 'bfloat16' || wGu.strides[1] !== 1) throw new Error('gemv_swiglu: bf16 weight with contiguous rows');
-  const want = prologue === 'rms_norm' ? 'float32' : 'bfloat16';
+  if ((out.dtype !== 'bfloat16' && out.dtype !== 'float32') || out.numel !== nHalf || !out.isContiguous())
+    throw new Error(`gemv_swiglu: out must be a contiguous bf16 or float32 row of ${nHalf} elements`);
+  const want = prologue === 'rms_norm' ? 'float32' : out.dtype;
   if (x.dtype !== want || x.numel !== k || !x.isContiguous())
     throw new Error(`gemv_swiglu: x must be a contiguous ${want} row of ${k} elements`);
-  if (out.dtype !== 'bfloat16' || out.numel !== nHalf || !out.isContiguous())
-    throw new Error(`gemv_swiglu: out must be a contiguous bf16 row of ${nHalf} elements`);
   const nw = p.normWeight as HipTensorHandle | undefined;
   addon.gemvSwiglu(GEMV_PROLOGUE[prologue], x.ptr, nw === undefined ? null : nw.ptr,
-                   p.eps === undefined ? 1e-6 : (p.eps as number), wGu.ptr, wGu.strides[0], out.ptr, nHalf, k);
+                   p.eps === undefined ? 1e-6 : (p.eps as number), wGu.ptr, wGu.strides[0], out.ptr, nHalf, k,
+                   out.kh);
 }
 
-// linear_swiglu(x, wGu, output): output [.., I] = silu(x W_gate^T) * (x W_up^T) in bf16 from the
-// gate/up weight [2I, H] interleaved in blocks of 8 rows (swiglu.ts:119-134 in one GEMM).
+// linear_swiglu(x, wGu, output): output [.., I] = silu(x W_gate^T) * (x W_up^T) from the bf16
+// gate/up weight [2I, H] interleaved in blocks of 8 rows (swiglu.ts:119-134 in one GEMM); x and
+// output bf16 (gate, up and the product rounded to bf16) or float32 (kept in fp32).
 function linearSwiglu(x: HipTensorHandle, wGu: HipTensorHandle, out: HipTensorHandle): void {
   const H = wGu.shape[1], I = wGu.shape[0] / 2;
-  if (x.dtype !== 'bfloat16' || wGu.dtype !== 'bfloat16' || out.dtype !== 'bfloat16')
-    throw new Error('linear_swiglu: bf16 operands only');
+  if ((x.dtype !== 'bfloat16' && x.dtype !== 'float32') || wGu.dtype !== 'bfloat16' || out.dtype !== x.dtype)
+    throw new Error('linear_swiglu: a bf16 weight with bf16 or float32 x and output of x\'s dtype expected');
   if (x.shape[x.shape.length - 1] !== H || out.shape[out.shape.length - 1] !== I)
     throw new Error(`linear_swiglu: x [.., ${H}] and output [.., ${I}] expected`);
   if (!x.isContiguous() || !out.isContiguous() || wGu.strides[1] !== 1)
     throw new Error('linear_swiglu: contiguous operands expected');
   const m = x.numel / H;
-  addon.gemmSwiglu(x.ptr, H, wGu.ptr, wGu.strides[0], out.ptr, I, m, I, H);
+  addon.gemmSwiglu(x.ptr, H, wGu.ptr, wGu.strides[0], out.ptr, I, m, I, H, x.kh);
 }
 
 // linear_qk_norm_rope(x, wQkv, params): the QKV projection of a chunk of S tokens with qk-norm, RoPE
 // and the K/V cache write in its epilogue (gqa.ts:269-309, rope.ts:546-644, kv-cache.ts:164-212);
-// x [S, H] bf16, wQkv [(Hq + 2 Hkv) 128, H]; params: qWeight, kWeight, invFreq, positions (int32 [S]),
+// x [S, H] bf16 or float32 (qOut and the caches of x's dtype), wQkv [(Hq + 2 Hkv) 128, H] bf16;
+// params: qWeight, kWeight (bf16), invFreq, positions (int32 [S]),
 // eps, qOut ([1, Hq, S, 128]), kOut / vOut (the caches [1, Hkv, maxSeq, 128], token t at row
 // positions[t]).  The values of matmul followed by rms_norm_rope with cachePositions.
 function linearQkNormRope(x: HipTensorHandle, wQkv: HipTensorHandle, p: { [key: string]: any }): void {
@@ -599,15 +607,17 @@ function linearQkNormRope(x: HipTensorHandle, wQkv: HipTensorHandle, p: { [key: 
     throw new Error('linear_qk_norm_rope: head_dim 128 and wQkv [(Hq + 2 Hkv) D, H] expected');
   if (x.shape.join() !== [S, H].join() || x.strides[1] !== 1 || wQkv.strides[1] !== 1)
     throw new Error(`linear_qk_norm_rope: x [${S}, ${H}] with contiguous rows expected`);
-  for (const t of [x, wQkv, qOut, kOut, vOut]) {
-    if (t.dtype !== 'bfloat16') throw new Error('linear_qk_norm_rope: bf16 operands only');
+  if (x.dtype !== 'bfloat16' && x.dtype !== 'float32') throw new Error('linear_qk_norm_rope: bf16 or float32 x expected');
+  for (const t of [qOut, kOut, vOut]) {
+    if (t.dtype !== x.dtype) throw new Error('linear_qk_norm_rope: qOut and the caches must have x\'s dtype');
   }
+  if (wQkv.dtype !== 'bfloat16') throw new Error('linear_qk_norm_rope: the projection weight must be bf16');
   if (vOut.shape.join() !== kOut.shape.join()) throw new Error('linear_qk_norm_rope: K and V caches differ in shape');
   const st: number[] = [];
   for (const t of [qOut, kOut, vOut]) st.push(t.strides[0], t.strides[2], t.strides[1]);
   addon.gemmQkNormRope(x.ptr, x.strides[0], wQkv.ptr, wQkv.strides[0], 1, S, H, Hq, Hkv, D, p.qWeight.ptr,
                        p.kWeight.ptr, p.invFreq.ptr, p.positions.ptr, qOut.ptr, kOut.ptr, vOut.ptr, st,
-                       p.eps === undefined ? 1e-6 : p.eps, L);
+                       p.eps === undefined ? 1e-6 : p.eps, L, x.kh);
 }
 
 // linear_add_rms_norm(x, w, residual, normWeight, eps, output, rows?): residual += x W^T (fp32, in
@@ -618,8 +628,8 @@ function linearAddRmsNorm(x: HipTensorHandle, w: HipTensorHandle, residual: HipT
                           normWeight: HipTensorHandle, eps: number, out: HipTensorHandle, rows?: number[]): void {
   const M = x.shape[0], K = x.shape[1], N = w.shape[0];
   const r0 = rows === undefined ? 0 : rows[0], r1 = rows === undefined ? M : rows[1];
-  if (x.dtype !== 'bfloat16' || w.dtype !== 'bfloat16' || residual.dtype !== 'float32')
-    throw new Error('linear_add_rms_norm: bf16 x and w with an fp32 residual expected');
+  if ((x.dtype !== 'bfloat16' && x.dtype !== 'float32') || w.dtype !== 'bfloat16' || residual.dtype !== 'float32')
+    throw new Error('linear_add_rms_norm: bf16 or float32 x and a bf16 w with an fp32 residual expected');
   if (w.shape[1] !== K || residual.shape.join() !== [M, N].join() || out.shape.join() !== [r1 - r0, N].join())
     throw new Error('linear_add_rms_norm: shapes do not match');
   if (normWeight.numel !== N || normWeight.dtype !== out.dtype)
@@ -632,13 +642,14 @@ function linearAddRmsNorm(x: HipTensorHandle, w: HipTensorHandle, residual: HipT
   const rowOff = BigInt(r0 * N * 4);
   if (splits > 1 && aligned && N % 8 === 0 && N <= 2048) {
     const part = HipTensorHandle.createNew([splits, M, N], 'float32');
-    addon.gemmSplitkPartials(x.ptr, K, w.ptr, K, part.ptr, M, N, K, splits);
+    addon.gemmSplitkPartials(x.ptr, K, w.ptr, K, part.ptr, M, N, K, splits, x.kh);
     addon.addRmsNorm(part.ptr + rowOff, splits, M * N, residual.ptr + rowOff, normWeight.ptr, out.ptr, r1 - r0, N,
                      eps, out.kh);
     part.dispose();  // stream ordered: reused only by later work on the same stream
     return;
   }
-  addon.gemm(x.ptr, K, w.ptr, K, residual.ptr, N, residual.ptr, N, null, M, N, K, 1, 1, true, x.kh, residual.kh);
+  addon.gemmEx(x.ptr, K, x.kh, w.ptr, K, w.kh, residual.ptr, N, residual.ptr, N, null, M, N, K, 1, 1, true,
+               residual.kh);
   addon.rmsNorm(residual.ptr + rowOff, N, normWeight.ptr, out.ptr, N, r1 - r0, N, eps, residual.kh, out.kh);
 }
 
@@ -646,7 +657,8 @@ function linearAddRmsNorm(x: HipTensorHandle, w: HipTensorHandle, residual: HipT
 // of the new token (gqa.ts:246-430): qk-norm, RoPE at the device position, the K/V cache row write,
 // attention over cache rows [0, position], o_proj and the residual add into x, in two kernels.
 // params: qNorm, kNorm (bf16 [128]), invFreq (fp32 [64]), eps, position (int32 [1]), kCache,
-// vCache ([1, Hkv, maxLen, 128] bf16), wO (bf16 [hidden, Hq * 128]), x (fp32 [1, hidden]), scale.
+// vCache ([1, Hkv, maxLen, 128] of qkv's dtype: bf16, or float32 activations), wO (bf16
+// [hidden, Hq * 128]), x (fp32 [1, hidden]), scale.
 function decodeAttentionBlock(qkv: HipTensorHandle, params: { [key: string]: any }): void {
   const kc = params.kCache as HipTensorHandle, vc = params.vCache as HipTensorHandle;
   const wo = params.wO as HipTensorHandle, x = params.x as HipTensorHandle;
@@ -654,10 +666,13 @@ function decodeAttentionBlock(qkv: HipTensorHandle, params: { [key: string]: any
   const hq = (qkv.numel - 2 * hkv * D) / D;
   if (D !== 128 || !(hq > 0) || hq !== Math.floor(hq))
     throw new Error(`decode_attention_block: qkv of ${qkv.numel} values does not split into heads of 128`);
-  for (const h of [qkv, params.qNorm as HipTensorHandle, params.kNorm as HipTensorHandle, kc, vc, wo])
-    if (h.dtype !== 'bfloat16') throw new Error('decode_attention_block: bf16 operands expected');
+  for (const h of [params.qNorm as HipTensorHandle, params.kNorm as HipTensorHandle, wo])
+    if (h.dtype !== 'bfloat16') throw new Error('decode_attention_block: bf16 norm and projection weights expected');
+  if (qkv.dtype !== 'bfloat16' && qkv.dtype !== 'float32') throw new Error('decode_attention_block: bf16 or float32 qkv');
+  for (const h of [kc, vc])
+    if (h.dtype !== qkv.dtype) throw new Error('decode_attention_block: the caches must have qkv\'s dtype');
   if (!qkv.isContiguous() || x.dtype !== 'float32' || !x.isContiguous())
-    throw new Error('decode_attention_block: qkv (bf16) and x (fp32) must be contiguous');
+    throw new Error('decode_attention_block: qkv and x (fp32) must be contiguous');
   if (wo.shape.join() !== [x.numel, hq * D].join() || wo.strides[1] !== 1)
     throw new Error(`decode_attention_block: wO must be [${x.numel}, ${hq * D}] with contiguous rows`);
   const pos = params.position as HipTensorHandle;
@@ -666,7 +681,7 @@ function decodeAttentionBlock(qkv: HipTensorHandle, params: { [key: string]: any
                              (params.invFreq as HipTensorHandle).ptr, params.eps === undefined ? 1e-6 : params.eps,
                              pos.ptr, kc.ptr, vc.ptr, hq, hkv, maxLen,
                              [kc.strides[1], kc.strides[2], vc.strides[1], vc.strides[2]], params.scale as number,
-                             wo.ptr, wo.strides[0], x.numel, x.ptr);
+                             wo.ptr, wo.strides[0], x.numel, x.ptr, qkv.kh);
 }
 
 // greedy_advance(nextToken, position, seqLen, tokenLog, logBase): the device-side step of the greedy

@@ -5,7 +5,7 @@
 // (kandle_amd/model_utils/qwen3.py), so both produce the same logits bit for bit:
 //
 //   prefill of S tokens (pre-norm decoder layers, decoder_layer.ts:191-241)
-//     x = embed[ids] (fp32 residual stream), h = rms_norm(x, input_layernorm) (bf16)
+//     x = embed[ids] (fp32 residual stream), h = rms_norm(x, input_layernorm) (activation dtype)
 //     per layer: qkv = h W_qkv^T (q/k/v rows concatenated); q/k per-head RMSNorm + RoPE, q written
 //       heads-first, k and v written into the KV caches at their positions (rms_norm_rope);
 //       o = causal flash attention over the cache rows [0, S); x += o W_o^T and h = rms_norm(x,
@@ -19,6 +19,12 @@
 //       o_proj, residual add); a = silu * mul of rms_norm(x) through the gate/up weight
 //       (gemv_swiglu); x += a W_down^T (gemv_fused)
 //     logits = rms_norm(x) E^T; token = argmax (lowest index); greedy_advance moves p on.
+//
+// Activations other than x (h, q/k/v, the K/V caches, attention output, the SwiGLU product) are
+// stored in the model's activation dtype: 'float32' (the default; every op in fp32 as the
+// reference computes, its bf16 checkpoint widened to float32 on load, io/safetensor/dtypes.ts:17-31:
+// the weights stay bf16 and the kernels multiply fp32 activations by them) or 'bfloat16' (rounded to
+// bf16 at each store: the fastest path).
 
 const fs = require('fs');
 const { performance } = require('perf_hooks');  // wall times in ms, sub-millisecond resolution
@@ -69,6 +75,13 @@ function bf16Bits(t: SafeTensor, name: string): Uint16Array {
   return new Uint16Array(ab);
 }
 
+// bf16 bit patterns widened exactly to float32 (the reference's BF16 load, dtypes.ts:82-94).
+function widenBf16(bits: Uint16Array): Float32Array {
+  const u = new Uint32Array(bits.length);
+  for (let i = 0; i < bits.length; ++i) u[i] = bits[i] << 16;
+  return new Float32Array(u.buffer);
+}
+
 function concatRows(parts: Uint16Array[]): Uint16Array {
   const out = new Uint16Array(parts.reduce((s: number, p: Uint16Array) => s + p.length, 0));
   let off = 0;
@@ -98,6 +111,12 @@ interface Layer {
   kNorm: any;
   wO: any;
   postNorm: any;
+  // the norm weights in the activation dtype, for the kernels whose weight shares the output's
+  // dtype (rms_norm, linear_add_rms_norm, rms_norm_rope); the bf16 handles above with bf16 activations
+  inNormA: any;
+  postNormA: any;
+  qNormA: any;
+  kNormA: any;
   wGu: any;
   wDown: any;
   kCache: any;
@@ -118,6 +137,8 @@ export class Qwen3ForCausalLM {
   maxSeqLen: number;
   embed: any;
   finalNorm: any;
+  finalNormA: any;
+  act: string;
   invFreq: any;
   invFreqHost: Float32Array;
   layers: Layer[] = [];
@@ -129,13 +150,20 @@ export class Qwen3ForCausalLM {
 
   // weights: Hugging Face tensor names -> bf16 bit patterns (tied embeddings: the lm_head is the
   // embedding matrix, for_causal_lm.ts:121-125).
-  constructor(backend: any, cfg: Qwen3Config, weights: { [name: string]: Uint16Array }, maxSeqLen: number) {
+  constructor(backend: any, cfg: Qwen3Config, weights: { [name: string]: Uint16Array }, maxSeqLen: number,
+              activations?: string) {
     this.cfg = cfg;
     this.backend = backend;
     this.ops = backend.operators;
     this.maxSeqLen = maxSeqLen;
+    this.act = activations === undefined ? 'float32' : activations;
+    if (this.act !== 'float32' && this.act !== 'bfloat16')
+      throw new Error(`Qwen3ForCausalLM: activations must be float32 or bfloat16, not ${this.act}`);
     const H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
     const up = (bits: Uint16Array, shape: number[]): any => backend.createTensorHandle({ shape, dtype: 'bfloat16', data: bits });
+    // a norm weight in the activation dtype (exactly widened for float32 activations)
+    const upA = (bits: Uint16Array, shape: number[], bf: any): any =>
+      this.act === 'float32' ? backend.createTensorHandle({ shape, dtype: 'float32', data: widenBf16(bits) }) : bf;
     const w = (name: string): Uint16Array => {
       const bits = weights[name];
       if (bits === undefined) throw new Error(`Qwen3ForCausalLM: missing weight ${name}`);
@@ -143,22 +171,31 @@ export class Qwen3ForCausalLM {
     };
     this.embed = up(w('model.embed_tokens.weight'), [cfg.vocabSize, H]);
     this.finalNorm = up(w('model.norm.weight'), [H]);
+    this.finalNormA = upA(w('model.norm.weight'), [H], this.finalNorm);
     const nq = cfg.numAttentionHeads * D, nkv = cfg.numKeyValueHeads * D;
     for (let i = 0; i < cfg.numHiddenLayers; ++i) {
       const p = `model.layers.${i}.`;
       const cacheShape = [1, cfg.numKeyValueHeads, maxSeqLen, D];
+      const inNorm = up(w(p + 'input_layernorm.weight'), [H]);
+      const postNorm = up(w(p + 'post_attention_layernorm.weight'), [H]);
+      const qNorm = up(w(p + 'self_attn.q_norm.weight'), [D]);
+      const kNorm = up(w(p + 'self_attn.k_norm.weight'), [D]);
       this.layers.push({
-        inNorm: up(w(p + 'input_layernorm.weight'), [H]),
+        inNorm,
         wQkv: up(concatRows([w(p + 'self_attn.q_proj.weight'), w(p + 'self_attn.k_proj.weight'),
                              w(p + 'self_attn.v_proj.weight')]), [nq + 2 * nkv, H]),
-        qNorm: up(w(p + 'self_attn.q_norm.weight'), [D]),
-        kNorm: up(w(p + 'self_attn.k_norm.weight'), [D]),
+        qNorm,
+        kNorm,
         wO: up(w(p + 'self_attn.o_proj.weight'), [H, nq]),
-        postNorm: up(w(p + 'post_attention_layernorm.weight'), [H]),
+        postNorm,
+        inNormA: upA(w(p + 'input_layernorm.weight'), [H], inNorm),
+        postNormA: upA(w(p + 'post_attention_layernorm.weight'), [H], postNorm),
+        qNormA: upA(w(p + 'self_attn.q_norm.weight'), [D], qNorm),
+        kNormA: upA(w(p + 'self_attn.k_norm.weight'), [D], kNorm),
         wGu: up(interleaveGateUp(w(p + 'mlp.gate_proj.weight'), w(p + 'mlp.up_proj.weight'), I, H), [2 * I, H]),
         wDown: up(w(p + 'mlp.down_proj.weight'), [H, I]),
-        kCache: backend.createTensorHandle(cacheShape, 'bfloat16'),
-        vCache: backend.createTensorHandle(cacheShape, 'bfloat16'),
+        kCache: backend.createTensorHandle(cacheShape, this.act),
+        vCache: backend.createTensorHandle(cacheShape, this.act),
       });
       // zero-filled as StaticKVCache's (kv-cache.ts:106-131): the decode block reads the row it is
       // about to write with a zero weight, which must not meet a NaN bit pattern
@@ -175,11 +212,12 @@ export class Qwen3ForCausalLM {
     this.scale = 1 / Math.sqrt(D);
   }
 
-  static fromSafetensors(backend: any, cfg: Qwen3Config, file: string, maxSeqLen: number): Qwen3ForCausalLM {
+  static fromSafetensors(backend: any, cfg: Qwen3Config, file: string, maxSeqLen: number,
+                         activations?: string): Qwen3ForCausalLM {
     const tensors = readSafetensors(file);
     const weights: { [name: string]: Uint16Array } = {};
     for (const name of Object.keys(tensors)) weights[name] = bf16Bits(tensors[name], name);
-    return new Qwen3ForCausalLM(backend, cfg, weights, maxSeqLen);
+    return new Qwen3ForCausalLM(backend, cfg, weights, maxSeqLen, activations);
   }
 
   private view(base: any, shape: number[], strides: number[], offset: number): any {
@@ -208,15 +246,16 @@ export class Qwen3ForCausalLM {
     const H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
     const Hq = cfg.numAttentionHeads, Hkv = cfg.numKeyValueHeads, eps = cfg.rmsNormEps;
     const nq = Hq * D, nkv = Hkv * D, nqkv = nq + 2 * nkv;
+    const act = this.act;
     const x = be.createTensorHandle([S, H], 'float32');
     // the fused QKV projection sums over all of K, as matmul does on MFMA tiles (more than 8 rows)
     // when it does not split K
     const fuseQkv = D === 128 && S > 8 && be.gemmSplitCount(S, nqkv, H) === 1;
     ops.find('index_select')(this.embed, ids, { dim: 0 }, x);
-    let h = ops.find('rms_norm')([x], { normalizedShape: [H], eps, weight: this.layers[0].inNorm, outDtype: 'bfloat16' });
+    let h = ops.find('rms_norm')([x], { normalizedShape: [H], eps, weight: this.layers[0].inNormA, outDtype: act });
     for (let li = 0; li < this.layers.length; ++li) {
       const L = this.layers[li];
-      const qh = be.createTensorHandle([1, Hq, S, D], 'bfloat16');
+      const qh = be.createTensorHandle([1, Hq, S, D], act);
       if (fuseQkv) {
         // the projection with qk-norm, RoPE and the cache write in its epilogue: the same values as
         // the two launches below when their projection is not split over K
@@ -224,35 +263,35 @@ export class Qwen3ForCausalLM {
                                                      positions, eps, qOut: qh, kOut: L.kCache, vOut: L.vCache });
         h.dispose();
       } else {
-        const qkv = be.createTensorHandle([S, nqkv], 'bfloat16');
+        const qkv = be.createTensorHandle([S, nqkv], act);
         ops.find('matmul')({ output: qkv, M: S, K: H, N: nqkv, batchSize: 1, transposeA: false, transposeB: true,
                              alpha: 1, beta: 0 }, h, L.wQkv);
         h.dispose();
         const heads = (col0: number, nh: number): any => this.view(qkv, [1, S, nh, D], [S * nqkv, nqkv, D, 1], col0);
         const q = heads(0, Hq), k = heads(nq, Hkv), v = heads(nq + nkv, Hkv);
-        ops.find('rms_norm_rope')(q, k, { qWeight: L.qNorm, kWeight: L.kNorm, invFreq: this.invFreq, positions, eps,
+        ops.find('rms_norm_rope')(q, k, { qWeight: L.qNormA, kWeight: L.kNormA, invFreq: this.invFreq, positions, eps,
                                           qOut: qh, kOut: L.kCache, v, vOut: L.vCache, cachePositions: true });
         for (const t of [q, k, v, qkv]) t.dispose();
       }
       // attention into [1, Hq, S, D] viewed over an [S, Hq D] buffer that o_proj reads as a matrix
-      const attn = be.createTensorHandle([S, nq], 'bfloat16');
+      const attn = be.createTensorHandle([S, nq], act);
       const attnView = this.view(attn, [1, Hq, S, D], [S * nq, D, nq, 1], 0);
       const kc = this.view(L.kCache, [1, Hkv, S, D], L.kCache.strides, 0);
       const vc = this.view(L.vCache, [1, Hkv, S, D], L.vCache.strides, 0);
       ops.find('flash_attention')(qh, kc, vc, attnView, this.scale, S > 1);
       for (const t of [attnView, kc, vc, qh]) t.dispose();
-      const h2 = be.createTensorHandle([S, H], 'bfloat16');
-      ops.find('linear_add_rms_norm')(attn, L.wO, x, L.postNorm, eps, h2);
+      const h2 = be.createTensorHandle([S, H], act);
+      ops.find('linear_add_rms_norm')(attn, L.wO, x, L.postNormA, eps, h2);
       attn.dispose();
-      const a = be.createTensorHandle([S, I], 'bfloat16');
+      const a = be.createTensorHandle([S, I], act);
       ops.find('linear_swiglu')(h2, L.wGu, a);
       h2.dispose();
       if (li + 1 < this.layers.length) {
-        h = be.createTensorHandle([S, H], 'bfloat16');
-        ops.find('linear_add_rms_norm')(a, L.wDown, x, this.layers[li + 1].inNorm, eps, h);
+        h = be.createTensorHandle([S, H], act);
+        ops.find('linear_add_rms_norm')(a, L.wDown, x, this.layers[li + 1].inNormA, eps, h);
       } else {
-        h = be.createTensorHandle([1, H], 'bfloat16');
-        ops.find('linear_add_rms_norm')(a, L.wDown, x, this.finalNorm, eps, h, [S - 1, S]);
+        h = be.createTensorHandle([1, H], act);
+        ops.find('linear_add_rms_norm')(a, L.wDown, x, this.finalNormA, eps, h, [S - 1, S]);
       }
       a.dispose();
     }
@@ -316,22 +355,23 @@ export class Qwen3ForCausalLM {
     const cfg = this.cfg, ops = this.ops, be = this.backend;
     const H = cfg.hiddenSize, I = cfg.intermediateSize, eps = cfg.rmsNormEps;
     const nqkv = (cfg.numAttentionHeads + 2 * cfg.numKeyValueHeads) * cfg.headDim;
+    const act = this.act;
     const x = be.createTensorHandle([1, H], 'float32');
     ops.find('index_select')(this.embed, token, { dim: 0 }, x);
     for (const L of this.layers) {
-      const qkv = be.createTensorHandle([1, nqkv], 'bfloat16');
-      ops.find('gemv_fused')('rms_norm', x, L.wQkv, qkv, { normWeight: L.inNorm, eps });
+      const qkv = be.createTensorHandle([1, nqkv], act);
+      ops.find('gemv_fused')('rms_norm', x, L.wQkv, qkv, { normWeight: L.inNorm, eps, actDtype: act });
       ops.find('decode_attention_block')(qkv, { qNorm: L.qNorm, kNorm: L.kNorm, invFreq: this.invFreq, eps,
                                                 position: pos, kCache: L.kCache, vCache: L.vCache, wO: L.wO, x,
                                                 scale: this.scale });
       qkv.dispose();
-      const a = be.createTensorHandle([1, I], 'bfloat16');
+      const a = be.createTensorHandle([1, I], act);
       ops.find('gemv_swiglu')('rms_norm', x, L.wGu, a, { normWeight: L.postNorm, eps });
-      ops.find('gemv_fused')('none', a, L.wDown, x, { cin: x });
+      ops.find('gemv_fused')('none', a, L.wDown, x, { cin: x, actDtype: act });
       a.dispose();
     }
     const logits = be.createTensorHandle([1, cfg.vocabSize], 'float32');
-    ops.find('gemv_fused')('rms_norm', x, this.embed, logits, { normWeight: this.finalNorm, eps });
+    ops.find('gemv_fused')('rms_norm', x, this.embed, logits, { normWeight: this.finalNorm, eps, actDtype: act });
     x.dispose();
     ops.find('argmax')(logits, token);
     ops.find('greedy_advance')(token, pos, lens, log, base);
@@ -409,8 +449,10 @@ export class Qwen3ForCausalLM {
       for (const t of [L.inNorm, L.wQkv, L.qNorm, L.kNorm, L.wO, L.postNorm, L.wGu, L.wDown, L.kCache, L.vCache]) {
         t.dispose();
       }
+      if (this.act === 'float32') for (const t of [L.inNormA, L.postNormA, L.qNormA, L.kNormA]) t.dispose();
     }
     for (const t of [this.embed, this.finalNorm, this.invFreq]) t.dispose();
+    if (this.finalNormA !== this.finalNorm) this.finalNormA.dispose();
     this.layers = [];
   }
 }

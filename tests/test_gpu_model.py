@@ -3,6 +3,13 @@
 Bar: greedy token ids identical for the first 32 decode steps of the full Qwen3-0.6B architecture
 (random N(0, 0.02) bf16 weights, 512-token prompt); the fp32 logits each token is chosen from (the
 prefill's last position and every decode step) within 2e-2 absolute.
+
+The reference computes in float32 throughout (bf16 checkpoints are widened to float32 on load,
+packages/core/src/io/safetensor/dtypes.ts:17-31), so the model's default float32 activations are
+checked against the oracle without rounding points (Qwen3Oracle(exact=True), itself pinned to
+transformers' float32 Qwen3).  The bfloat16-activation mode is checked against the oracle that
+rounds to bf16 where the GPU stores (its kernel-level check); its distance from the float32 oracle
+is printed, not asserted (about 0.02: one bf16 rounding per stored activation through 28 layers).
 """
 import numpy as np
 import pytest
@@ -14,27 +21,45 @@ from oracle.qwen3 import Qwen3Oracle
 pytestmark = pytest.mark.gpu
 
 LOGIT_ATOL = 2e-2
+ACTS = ("float32", "bfloat16")
+
+_EXACT = {}   # (seed, prompt_len, steps) -> float32 oracle (tokens, logits): computed once per session
 
 
-def _run(cfg, seed, prompt_len, steps, max_seq):
-    w = init_qwen3_weights(cfg, seed=seed)
-    prompt = syn.randint(seed + 1, (prompt_len,), 0, cfg.vocab_size)
-    model = Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq)
+def _weights_prompt(cfg, seed, prompt_len):
+    return init_qwen3_weights(cfg, seed=seed), syn.randint(seed + 1, (prompt_len,), 0, cfg.vocab_size)
+
+
+def _oracle(cfg, w, prompt, steps, max_seq, act):
+    """The oracle matching the activation dtype: exact float32, or bf16 rounding points."""
+    return Qwen3Oracle(cfg, w, max_seq_len=max_seq, exact=act == "float32").generate(prompt, steps)
+
+
+def _exact(cfg, w, prompt, steps, max_seq, seed):
+    key = (seed, len(prompt), steps, cfg.num_hidden_layers, cfg.vocab_size)
+    if key not in _EXACT:
+        _EXACT[key] = Qwen3Oracle(cfg, w, max_seq_len=max_seq, exact=True).generate(prompt, steps)
+    return _EXACT[key]
+
+
+def _run(cfg, seed, prompt_len, steps, max_seq, act="float32"):
+    w, prompt = _weights_prompt(cfg, seed, prompt_len)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq, activations=act)
     toks, logits = model.generate(prompt, steps, return_logits=True)
     model.dispose()
-    ref = Qwen3Oracle(cfg, w, max_seq_len=max_seq)
-    rtoks, rlogits = ref.generate(prompt, steps)
+    rtoks, rlogits = _oracle(cfg, w, prompt, steps, max_seq, act)
     return toks, logits, rtoks, rlogits
 
 
-def test_decode_graph_replays_match_eager(hip):
+@pytest.mark.parametrize("act", ACTS)
+def test_decode_graph_replays_match_eager(hip, act):
     """The captured decode step, replayed with readbacks (host syncs) between replays, and the
     captured prefill, replayed on a second generation, give the same logits bit for bit as the
     same launches run eagerly, and the oracle's tokens."""
     cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
     w = init_qwen3_weights(cfg, seed=5)
     prompt = syn.randint(6, (40,), 0, cfg.vocab_size)
-    model = Qwen3ForCausalLM(cfg, w, max_seq_len=64)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=64, activations=act)
     etoks, elog = model.generate(prompt, 6, return_logits=True, use_graph=False)
     gtoks, glog = model.generate(prompt, 6, return_logits=True, use_graph=True)     # captures the prefill
     g2toks, g2log = model.generate(prompt, 6, return_logits=True, use_graph=True)   # replays it
@@ -42,7 +67,7 @@ def test_decode_graph_replays_match_eager(hip):
     assert etoks == gtoks == g2toks
     for i, (a, b, c) in enumerate(zip(elog, glog, g2log)):
         assert np.array_equal(a, b) and np.array_equal(a, c), i
-    rtoks, _ = Qwen3Oracle(cfg, w, max_seq_len=64).generate(prompt, 6)
+    rtoks, _ = _oracle(cfg, w, prompt, 6, 64, act)
     assert gtoks == rtoks
 
 
@@ -51,35 +76,78 @@ def _margin(logits):
     return float(top2[1] - top2[0])
 
 
-def test_small_qwen3_prefill_and_decode(hip):
+@pytest.mark.parametrize("act", ACTS)
+def test_small_qwen3_prefill_and_decode(hip, act):
     """2 layers, vocab 4096: logits of the prefill and of 8 decode steps, and the tokens."""
     cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
-    toks, logits, rtoks, rlogits = _run(cfg, seed=3, prompt_len=77, steps=8, max_seq=128)
+    toks, logits, rtoks, rlogits = _run(cfg, seed=3, prompt_len=77, steps=8, max_seq=128, act=act)
     for i, (g, r) in enumerate(zip(logits, rlogits)):
         err = float(np.max(np.abs(g - r)))
         assert err < LOGIT_ATOL, (i, err)
     assert toks == rtoks
 
 
-@pytest.mark.timeout(600)
-def test_qwen3_0p6b_greedy_32_steps(hip):
-    """Config C5: 28 layers, hidden 1024, 16/8 heads, MLP 3072, vocab 151936, tied embeddings;
-    512-token prefill of uniform-random ids, then greedy decoding compared for 32 steps."""
+def _c5_check(act, seed, prompt_len, steps=32, max_seq=1024):
+    """Greedy C5 generation with `act` activations against the float32 oracle (and, for bf16, the
+    bf16-rounding oracle): per-step logit error, the float32 oracle's top-2 margin and the tokens
+    are printed; returns (errors vs the asserted oracle, tokens, oracle tokens, margins)."""
     cfg = Qwen3Config()
-    toks, logits, rtoks, rlogits = _run(cfg, seed=7, prompt_len=512, steps=32, max_seq=1024)
-    assert len(logits) == len(rlogits) == 33   # the prefill's last position, then one per decode step
+    w, prompt = _weights_prompt(cfg, seed, prompt_len)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq, activations=act)
+    toks, logits = model.generate(prompt, steps, return_logits=True)
+    model.dispose()
+    etoks, elogits = _exact(cfg, w, prompt, steps, max_seq, seed)
+    if act == "float32":
+        rtoks, rlogits = etoks, elogits
+    else:
+        rtoks, rlogits = _oracle(cfg, w, prompt, steps, max_seq, act)
+    assert len(logits) == len(rlogits) == steps + 1   # the prefill's last position, then one per step
     errs = [float(np.max(np.abs(g - r))) for g, r in zip(logits, rlogits)]
-    margins = [_margin(r) for r in rlogits]
-    print("\nstep  max|dlogit|  top-2 margin (oracle)  token gpu / oracle")
-    for i, (e, mg) in enumerate(zip(errs, margins)):
+    eerrs = [float(np.max(np.abs(g - r))) for g, r in zip(logits, elogits)]
+    margins = [_margin(r) for r in elogits]
+    print(f"\nC5 seed {seed}, {prompt_len}-token prompt, {act} activations")
+    print("step  |d| vs asserted oracle  |d| vs float32 oracle  top-2 margin (float32)  token gpu / oracle")
+    for i, (e, ee, mg) in enumerate(zip(errs, eerrs, margins)):
         tg = toks[i] if i < len(toks) else None
         tr = rtoks[i] if i < len(rtoks) else None
-        print(f"{i:4d}  {e:.4e}   {mg:.4f}   {tg} / {tr}", flush=True)
-    print(f"max logit error {max(errs):.4e}; smallest top-2 margin {min(margins):.4f}", flush=True)
+        print(f"{i:4d}  {e:.4e}   {ee:.4e}   {mg:.4f}   {tg} / {tr}", flush=True)
+    print(f"max logit error {max(errs):.4e} (vs float32 oracle {max(eerrs):.4e}); smallest top-2 margin "
+          f"{min(margins):.4f}", flush=True)
+    return errs, toks, rtoks, margins
+
+
+@pytest.mark.timeout(600)
+def test_qwen3_0p6b_greedy_32_steps(hip):
+    """Config C5 with float32 activations against the float32 oracle: 28 layers, hidden 1024, 16/8
+    heads, MLP 3072, vocab 151936, tied embeddings; 512-token prefill of uniform-random ids, then 32
+    greedy steps: all 32 tokens identical and all 33 logit vectors within 2e-2 (the smallest top-2
+    margin on this seed is 0.0019, at step 29)."""
+    errs, toks, rtoks, margins = _c5_check("float32", seed=7, prompt_len=512)
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, rtoks)) if a != b), None)
     assert first_diff is None, (first_diff, toks[first_diff], rtoks[first_diff], margins[first_diff])
     worst = int(np.argmax(errs))
     assert errs[worst] < LOGIT_ATOL, (worst, errs[worst])
+
+
+@pytest.mark.timeout(600)
+def test_qwen3_0p6b_greedy_32_steps_second_seed_300_tokens(hip):
+    """C5 with float32 activations on a second (weights, prompt) seed and a 300-token prompt, which
+    takes the non-persistent flash kernel shape and other GEMM tilings: 32 tokens identical to the
+    float32 oracle, 33 logit vectors within 2e-2."""
+    errs, toks, rtoks, margins = _c5_check("float32", seed=17, prompt_len=300)
+    first_diff = next((i for i, (a, b) in enumerate(zip(toks, rtoks)) if a != b), None)
+    assert first_diff is None, (first_diff, toks[first_diff], rtoks[first_diff], margins[first_diff])
+    assert max(errs) < LOGIT_ATOL, max(errs)
+
+
+@pytest.mark.timeout(600)
+def test_qwen3_0p6b_bf16_activations_vs_rounding_oracle(hip):
+    """The bfloat16-activation mode against the oracle that rounds where the GPU stores (kernel-level
+    parity of the bf16 path): tokens identical to that oracle for 32 steps, logits within 2e-2."""
+    errs, toks, rtoks, margins = _c5_check("bfloat16", seed=7, prompt_len=512)
+    first_diff = next((i for i, (a, b) in enumerate(zip(toks, rtoks)) if a != b), None)
+    assert first_diff is None, (first_diff, toks[first_diff], rtoks[first_diff])
+    assert max(errs) < LOGIT_ATOL, max(errs)
 
 
 def test_from_pretrained_sharded_checkpoint_matches_in_memory(hip, tmp_path):
@@ -123,29 +191,29 @@ def test_from_pretrained_sharded_checkpoint_matches_in_memory(hip, tmp_path):
     assert toks == rtoks
     for a, b in zip(logits, rlogits):
         assert np.array_equal(a, b)
-    otoks, _ = Qwen3Oracle(cfg, w, max_seq_len=64).generate(prompt, 6)
+    otoks, _ = Qwen3Oracle(cfg, w, max_seq_len=64, exact=True).generate(prompt, 6)
     assert toks == otoks
 
 
-def test_fused_decode_block_matches_unfused_and_oracle(hip):
+@pytest.mark.parametrize("act", ACTS)
+def test_fused_decode_block_matches_unfused_and_oracle(hip, act):
     """The decode step's fused attention block (kh_decode_attention_block: qk-norm + RoPE of q and of
     the new k row, K/V cache write, split-K attention, merge in the o_proj prologue, residual) against
     the same step run as separate launches, and both against the oracle; caches past 8 chunks of
     256 keys take the separate merge."""
-    from oracle.qwen3 import Qwen3Oracle
-
-    for max_seq, prompt_len in ((128, 40), (3000, 2100)):   # prologue merge; merge kernel (9+ chunks)
+    # prologue merge; merge kernel (9+ chunks: 256 keys each for bf16, 128 for float32)
+    for max_seq, prompt_len in ((128, 40), (3000, 2100)):
         cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
         w = init_qwen3_weights(cfg, seed=21)
         prompt = syn.randint(22, (prompt_len,), 0, cfg.vocab_size)
         out = {}
         for fused in (True, False):
-            model = Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq)
+            model = Qwen3ForCausalLM(cfg, w, max_seq_len=max_seq, activations=act)
             model.fused_decode = fused
             out[fused] = model.generate(prompt, 6, return_logits=True, use_graph=fused)
             model.dispose()
         (ft, fl), (ut, ul) = out[True], out[False]
-        rt, rl = Qwen3Oracle(cfg, w, max_seq_len=max_seq).generate(prompt, 6)
+        rt, rl = _oracle(cfg, w, prompt, 6, max_seq, act)
         for i in range(1, 6):   # decode steps (index 0 is the prefill)
             assert float(np.max(np.abs(fl[i] - ul[i]))) < 5e-3, (max_seq, i)
             assert float(np.max(np.abs(fl[i] - rl[i]))) < LOGIT_ATOL, (max_seq, i)

@@ -192,7 +192,7 @@ def test_generate_stream_sampled_steps_follow_reference(hip, monkeypatch):
     assert len(steps) == 6 and len(seen) == 6
     fed = [s.token_id for s in steps]
     fed[2] = 123
-    ref = Qwen3Oracle(cfg, w, max_seq_len=96)
+    ref = Qwen3Oracle(cfg, w, max_seq_len=96, exact=True)
     rl = ref.forward(prompt, 0)
     for i, (st, (lg, seed, ctr)) in enumerate(zip(steps, seen)):
         assert (seed, ctr) == (7, i) and st.cache_position == 40 + i and st.generated_count == i + 1
