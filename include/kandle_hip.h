@@ -113,6 +113,38 @@ int kh_fill(void* dst, int64_t n, float value, int dtype);
 int kh_copy_strided(const void* src, int64_t src_offset, void* dst, int ndim, const int64_t* shape,
                     const int64_t* src_strides, int dtype_src, int dtype_dst);
 
+/* Ops of kh_map_strided. */
+#define KH_MAP_COPY 0    /* out = a (cast to out's dtype) */
+#define KH_MAP_ADD 1     /* out = a + s0 * b   (s0: add's alpha) */
+#define KH_MAP_SUB 2     /* out = a - s0 * b   (s0: sub's alpha) */
+#define KH_MAP_MUL 3     /* out = a * b */
+#define KH_MAP_DIV 4     /* out = a / b */
+#define KH_MAP_NEG 5     /* out = -a */
+#define KH_MAP_COS 6     /* out = cos(a) */
+#define KH_MAP_SIN 7     /* out = sin(a) */
+#define KH_MAP_SILU 8    /* out = a / (1 + exp(-clamp(a, -88, 88))) */
+#define KH_MAP_FILL 9    /* out = s0 */
+#define KH_MAP_ARANGE 10 /* out = s0 + f32(i) * s1, i the element's row-major index in `shape` */
+
+/* An elementwise op over the index space `shape` (ndim <= 8) in which every operand is addressed by
+ * its own element strides from its pointer (the view's first element; a stride of 0 broadcasts an
+ * axis, negative strides walk backwards): out[idx . out_strides] = op(a[idx . a_strides],
+ * b[idx . b_strides]).  This is Kandle's iterator kernel contract (ITensorIterator operands carry
+ * broadcast-aligned element strides and offsets: reference packages/types/src/tensor.ts:282-378,
+ * built by packages/core/src/dispatch/TensorIterator.ts:660-725 computeBroadcastStrides) and
+ * replaces the strided pointwise executor (packages/backend-webgpu/src/kernels/pointwise/
+ * executor.ts:60-130) and the copy / cast / contiguous / clone / copy_ kernels (kernels/copy/
+ * index.ts:13-33, called from packages/core/src/dispatch/handlers/copy.ts:175-206), the zeros /
+ * full fills (handlers/factory.ts:50-61) and arange (kernels/factory/arangeExecutor.ts:37-44).
+ * Math is fp32 with float (f32 or bf16) outputs, int32 two's-complement with an int32 output (copy
+ * casts floats by truncation toward zero, saturated, NaN -> 0); inputs of any of the three dtypes.
+ * Operands not used by the op may be NULL.  Nothing is read or written outside the element offsets
+ * the strides give: the caller checks they lie in its buffers.  The output must not overlap an input
+ * except element for element (identical strides). */
+int kh_map_strided(int op, int ndim, const int64_t* shape, void* out, const int64_t* out_strides, int out_dtype,
+                   const void* a, const int64_t* a_strides, int a_dtype, const void* b, const int64_t* b_strides,
+                   int b_dtype, double s0, double s1);
+
 /* out[i] = a[i] (op) b[i] for contiguous same-shape operands; op 0 = add, 1 = mul, 2 = sub.
  * Replaces the `add`/`mul`/`sub` pointwise iterator kernels for the contiguous case
  * (reference: packages/backend-webgpu/src/kernels/pointwise/ops.ts:329 mul, :437 add). */

@@ -50,6 +50,7 @@ SIGNATURES = {
     "kh_fill": [_vp, _i64, _f, _i],
     "kh_copy_strided": [_vp, _i64, _vp, _i, _i64p, _i64p, _i, _i],
     "kh_binary": [_i, _vp, _vp, _vp, _i64, _i],
+    "kh_map_strided": [_i, _i, _i64p, _vp, _i64p, _i, _vp, _i64p, _i, _vp, _i64p, _i, C.c_double, C.c_double],
     "kh_silu": [_vp, _vp, _i64, _i],
     "kh_silu_mul": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i],
     "kh_index_select": [_vp, _i64, _vp, _i64, _i64, _vp, _i, _i],

@@ -66,6 +66,92 @@ __global__ void copy_strided_i32_kernel(const int32_t* __restrict__ src, int64_t
   }
 }
 
+// ---- N-D strided map: the iterator kernels (kh_map_strided) -----------------------------------
+// One output element per thread step; the element's offset in every operand is formed from its
+// coordinates in the (coalesced) index space and that operand's element strides, so broadcast
+// operands (stride 0), permuted and sliced views and strided outputs need no materialised copy.
+constexpr int kMapMaxDims = 8;
+struct MapDesc {
+  int ndim;
+  int64_t shape[kMapMaxDims];
+  int64_t so[kMapMaxDims], sa[kMapMaxDims], sb[kMapMaxDims];
+};
+
+__device__ __forceinline__ float map_ld_f(const void* p, int64_t i, int dt) {
+  if (dt == KH_F32) return reinterpret_cast<const float*>(p)[i];
+  if (dt == KH_BF16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  return (float)reinterpret_cast<const int32_t*>(p)[i];
+}
+// int32 view of an element: ints as they are, floats truncated toward zero and saturated (NaN 0),
+// the float -> i32 conversion of WGSL's i32(f).
+__device__ __forceinline__ int32_t map_ld_i(const void* p, int64_t i, int dt) {
+  if (dt == KH_I32) return reinterpret_cast<const int32_t*>(p)[i];
+  const float f = map_ld_f(p, i, dt);
+  if (!(f == f)) return 0;
+  if (f >= 2147483647.f) return INT32_MAX;
+  if (f <= -2147483648.f) return INT32_MIN;
+  return (int32_t)f;
+}
+__device__ __forceinline__ void map_st_f(void* p, int64_t i, int dt, float v) {
+  if (dt == KH_F32)
+    reinterpret_cast<float*>(p)[i] = v;
+  else
+    reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+// INT: int32 output with int32 arithmetic (copy / add / sub / mul / neg / fill / arange, two's
+// complement wrap-around as WGSL's i32); otherwise fp32 math stored in the output's float dtype.
+template <bool INT>
+__global__ void map_strided_kernel(int op, MapDesc d, int64_t n, void* out, int odt, const void* a, int adt,
+                                   const void* b, int bdt, float s0, float s1, int32_t i0, int32_t i1) {
+#pragma clang fp contract(off)  // arange's product and sum round separately, as the WGSL kernel's
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t rem = i, oo = 0, oa = 0, ob = 0;
+    for (int k = d.ndim - 1; k >= 0; --k) {
+      const int64_t c = rem % d.shape[k];
+      rem /= d.shape[k];
+      oo += c * d.so[k];
+      oa += c * d.sa[k];
+      ob += c * d.sb[k];
+    }
+    if constexpr (INT) {
+      int32_t v = 0;
+      switch (op) {
+        case KH_MAP_COPY: v = map_ld_i(a, oa, adt); break;
+        case KH_MAP_ADD: v = (int32_t)((uint32_t)map_ld_i(a, oa, adt) + (uint32_t)i0 * (uint32_t)map_ld_i(b, ob, bdt)); break;
+        case KH_MAP_SUB: v = (int32_t)((uint32_t)map_ld_i(a, oa, adt) - (uint32_t)i0 * (uint32_t)map_ld_i(b, ob, bdt)); break;
+        case KH_MAP_MUL: v = (int32_t)((uint32_t)map_ld_i(a, oa, adt) * (uint32_t)map_ld_i(b, ob, bdt)); break;
+        case KH_MAP_NEG: v = (int32_t)(0u - (uint32_t)map_ld_i(a, oa, adt)); break;
+        case KH_MAP_FILL: v = i0; break;
+        case KH_MAP_ARANGE: v = (int32_t)((uint32_t)i0 + (uint32_t)i * (uint32_t)i1); break;
+        default: break;
+      }
+      reinterpret_cast<int32_t*>(out)[oo] = v;
+    } else {
+      float v = 0.f;
+      switch (op) {
+        case KH_MAP_COPY: v = map_ld_f(a, oa, adt); break;
+        case KH_MAP_ADD: v = map_ld_f(a, oa, adt) + s0 * map_ld_f(b, ob, bdt); break;
+        case KH_MAP_SUB: v = map_ld_f(a, oa, adt) - s0 * map_ld_f(b, ob, bdt); break;
+        case KH_MAP_MUL: v = map_ld_f(a, oa, adt) * map_ld_f(b, ob, bdt); break;
+        case KH_MAP_DIV: v = map_ld_f(a, oa, adt) / map_ld_f(b, ob, bdt); break;
+        case KH_MAP_NEG: v = -map_ld_f(a, oa, adt); break;
+        case KH_MAP_COS: v = cosf(map_ld_f(a, oa, adt)); break;
+        case KH_MAP_SIN: v = sinf(map_ld_f(a, oa, adt)); break;
+        case KH_MAP_SILU: v = silu_ref(map_ld_f(a, oa, adt)); break;
+        case KH_MAP_FILL: v = s0; break;
+        case KH_MAP_ARANGE: {
+          const float prod = (float)i * s1;
+          v = s0 + prod;
+          break;
+        }
+        default: break;
+      }
+      map_st_f(out, oo, odt, v);
+    }
+  }
+}
+
 // ---- binary / unary ---------------------------------------------------------------------------
 __device__ __forceinline__ float apply_binary(int op, float a, float b) {
   return op == 0 ? a + b : (op == 1 ? a * b : a - b);
@@ -360,6 +446,79 @@ int kh_copy_strided(const void* src, int64_t src_offset, void* dst, int ndim, co
   } else {
     KH_REQUIRE(false, "kh_copy_strided: unsupported dtypes %d -> %d", dtype_src, dtype_dst);
   }
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
+int kh_map_strided(int op, int ndim, const int64_t* shape, void* out, const int64_t* out_strides, int out_dtype,
+                   const void* a, const int64_t* a_strides, int a_dtype, const void* b, const int64_t* b_strides,
+                   int b_dtype, double s0, double s1) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(op >= KH_MAP_COPY && op <= KH_MAP_ARANGE, "kh_map_strided: unknown op %d", op);
+  KH_REQUIRE(ndim >= 0 && ndim <= kMapMaxDims, "kh_map_strided: ndim %d outside [0, %d]", ndim, kMapMaxDims);
+  KH_REQUIRE(ndim == 0 || shape != nullptr, "kh_map_strided: null shape");
+  const int nin = op == KH_MAP_FILL || op == KH_MAP_ARANGE
+                      ? 0
+                      : (op == KH_MAP_ADD || op == KH_MAP_SUB || op == KH_MAP_MUL || op == KH_MAP_DIV ? 2 : 1);
+  auto dtype_ok = [](int dt) { return dt == KH_F32 || dt == KH_BF16 || dt == KH_I32; };
+  KH_REQUIRE(dtype_ok(out_dtype), "kh_map_strided: unsupported output dtype %d", out_dtype);
+  KH_REQUIRE(nin < 1 || dtype_ok(a_dtype), "kh_map_strided: unsupported dtype %d of a", a_dtype);
+  KH_REQUIRE(nin < 2 || dtype_ok(b_dtype), "kh_map_strided: unsupported dtype %d of b", b_dtype);
+  const bool int_out = out_dtype == KH_I32;
+  // int32 outputs take integer arithmetic (copy casts any dtype; the arithmetic ops need int32 inputs);
+  // division and the transcendental ops produce floats
+  KH_REQUIRE(!int_out || op == KH_MAP_COPY || op == KH_MAP_FILL || op == KH_MAP_ARANGE ||
+                 ((op == KH_MAP_ADD || op == KH_MAP_SUB || op == KH_MAP_MUL || op == KH_MAP_NEG) &&
+                  a_dtype == KH_I32 && (nin < 2 || b_dtype == KH_I32)),
+             "kh_map_strided: op %d has no int32 form for these operands", op);
+  int64_t n = 1;
+  for (int k = 0; k < ndim; ++k) {
+    KH_REQUIRE(shape[k] >= 0, "kh_map_strided: negative extent");
+    n *= shape[k];
+  }
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(out && (ndim == 0 || out_strides), "kh_map_strided: null output");
+  KH_REQUIRE(nin < 1 || (a && (ndim == 0 || a_strides)), "kh_map_strided: null operand a");
+  KH_REQUIRE(nin < 2 || (b && (ndim == 0 || b_strides)), "kh_map_strided: null operand b");
+  // Coalesce: drop extent-1 axes, then merge axis k into k + 1 wherever every operand steps
+  // through k exactly as through a whole row of k + 1 (stride[k] == stride[k + 1] * shape[k + 1]).
+  MapDesc d{};
+  d.ndim = 0;
+  for (int k = 0; k < ndim; ++k) {
+    if (shape[k] == 1) continue;
+    const int j = d.ndim++;
+    d.shape[j] = shape[k];
+    d.so[j] = out_strides[k];
+    d.sa[j] = nin >= 1 ? a_strides[k] : 0;
+    d.sb[j] = nin >= 2 ? b_strides[k] : 0;
+  }
+  int m = 0;
+  for (int k = 0; k < d.ndim; ++k) {
+    if (m > 0 && d.so[m - 1] == d.so[k] * d.shape[k] && d.sa[m - 1] == d.sa[k] * d.shape[k] &&
+        d.sb[m - 1] == d.sb[k] * d.shape[k]) {
+      d.shape[m - 1] *= d.shape[k];
+      d.so[m - 1] = d.so[k];
+      d.sa[m - 1] = d.sa[k];
+      d.sb[m - 1] = d.sb[k];
+    } else {
+      d.shape[m] = d.shape[k];
+      d.so[m] = d.so[k];
+      d.sa[m] = d.sa[k];
+      d.sb[m] = d.sb[k];
+      ++m;
+    }
+  }
+  d.ndim = m;
+  const int g = grid_for(n);
+  const float f0 = (float)s0, f1 = (float)s1;
+  const int32_t i0 = (int32_t)(int64_t)s0, i1 = (int32_t)(int64_t)s1;
+  // add / sub scale b by alpha (s0): 1 when the caller has none
+  if (int_out)
+    map_strided_kernel<true><<<g, kThreads, 0, stream()>>>(op, d, n, out, out_dtype, a, a_dtype, b, b_dtype, f0, f1,
+                                                           i0, i1);
+  else
+    map_strided_kernel<false><<<g, kThreads, 0, stream()>>>(op, d, n, out, out_dtype, a, a_dtype, b, b_dtype, f0,
+                                                            f1, i0, i1);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -208,70 +208,43 @@ def rms_norm(input: Tensor, normalized_shape: Sequence[int], weight: Optional[Te
     return _wrap(_kernel(input, "rms_norm")([input.handle], params))
 
 
-def _broadcast_pair(a: Tensor, b: Tensor):
-    shape = tuple(np.broadcast_shapes(tuple(a.shape), tuple(b.shape)))
-    ha = a.handle if tuple(a.shape) == shape and a.handle.is_contiguous() else _materialize_expand(a, shape)
-    hb = b.handle if tuple(b.shape) == shape and b.handle.is_contiguous() else _materialize_expand(b, shape)
-    return shape, ha, hb
+def _binary(name: str, a: Tensor, b: Tensor, alpha: Optional[float] = None) -> Tensor:
+    """A binary map op through its iterator kernel (handlers/iterator.ts:24-135): broadcast and
+    strided operands are read in place through their iterator strides; the result is a new tensor
+    of the promoted dtype."""
+    it = TensorIterator.binary_op(a.handle, b.handle, scalar_args=None if alpha is None else {"alpha": alpha})
+    _kernel(a, name)(it)
+    return _wrap(it.output().tensor_handle)
 
 
-def _materialize_expand(t: Tensor, shape) -> HipTensorHandle:
-    v = expand(t, shape) if tuple(t.shape) != tuple(shape) else t
-    h = _kernel(t, "contiguous")(v.handle, {})
-    if v is not t:
-        v.dispose()
-    return h
-
-
-def _binary(name: str, a: Tensor, b: Tensor) -> Tensor:
-    if a.dtype != b.dtype:
-        raise TypeError(f"{name}: dtype mismatch {a.dtype} vs {b.dtype}")
-    shape, ha, hb = _broadcast_pair(a, b)
-    out = _new(a, shape)
-    try:
-        _kernel(a, name)(TensorIterator([ha, hb], [out]))
-    finally:
-        if ha is not a.handle:
-            ha.dispose()
-        if hb is not b.handle:
-            hb.dispose()
-    return _wrap(out)
-
-
-def add(a: Tensor, b: Tensor) -> Tensor:
-    return _binary("add", a, b)
+def add(a: Tensor, b: Tensor, alpha: Optional[float] = None) -> Tensor:
+    """a + alpha * b (ops.ts:437)."""
+    return _binary("add", a, b, alpha)
 
 
 def mul(a: Tensor, b: Tensor) -> Tensor:
     return _binary("mul", a, b)
 
 
-def sub(a: Tensor, b: Tensor) -> Tensor:
-    return _binary("sub", a, b)
+def sub(a: Tensor, b: Tensor, alpha: Optional[float] = None) -> Tensor:
+    return _binary("sub", a, b, alpha)
 
 
-def silu(x: Tensor) -> Tensor:
-    hx = x.handle if x.handle.is_contiguous() else _kernel(x, "contiguous")(x.handle, {})
-    out = _new(x, x.shape)
-    try:
-        _kernel(x, "silu")(TensorIterator([hx], [out]))
-    finally:
-        if hx is not x.handle:
-            hx.dispose()
-    return _wrap(out)
+def div(a: Tensor, b: Tensor) -> Tensor:
+    return _binary("div", a, b)
 
 
 def _map(x: Tensor, name: str) -> Tensor:
     """A one-input pointwise op found by name (the reference's IteratorHandler route,
-    packages/core/src/dispatch/handlers/iterator.ts:24-135): contiguous input, new output."""
-    hx = x.handle if x.handle.is_contiguous() else _kernel(x, "contiguous")(x.handle, {})
-    out = _new(x, x.shape)
-    try:
-        _kernel(x, name)(TensorIterator([hx], [out]))
-    finally:
-        if hx is not x.handle:
-            hx.dispose()
-    return _wrap(out)
+    packages/core/src/dispatch/handlers/iterator.ts:24-135): the input read through its strides,
+    a new output."""
+    it = TensorIterator.unary_op(x.handle)
+    _kernel(x, name)(it)
+    return _wrap(it.output().tensor_handle)
+
+
+def silu(x: Tensor) -> Tensor:
+    return _map(x, "silu")
 
 
 def neg(x: Tensor) -> Tensor:
@@ -295,9 +268,10 @@ def arange(start: float, end: Optional[float] = None, step: float = 1.0, dtype: 
         raise ValueError("arange: step must be nonzero")
     n = max(0, int(math.ceil((end - start) / step)))
     from .env import get_backend, get_default_device
-    out = get_backend(get_default_device()).create_tensor_handle((n,), dtype)
-    get_backend(get_default_device()).operators.find("arange")(out, float(start), float(step))
-    return _wrap(out)
+    it = TensorIterator.nullary_op((n,), dtype, scalar_args={"start": float(start), "end": float(end),
+                                                             "step": float(step)})
+    get_backend(get_default_device()).operators.find("arange")(it)
+    return _wrap(it.output().tensor_handle)
 
 
 def linear_swiglu(input: Tensor, weight_gu: Tensor) -> Tensor:
@@ -336,15 +310,32 @@ def contiguous(x: Tensor) -> Tensor:
     if x.handle.is_contiguous():
         x.handle.storage.inc_ref()
         return _wrap(HipTensorHandle(x.handle.storage, x.shape, x.dtype, x.strides, x.offset))
-    return _wrap(_kernel(x, "contiguous")(x.handle, {}))
+    out = _new(x, x.shape)
+    _kernel(x, "contiguous")(TensorIterator.unary_op(x.handle, out))
+    return _wrap(out)
 
 
 def cast(x: Tensor, dtype: str) -> Tensor:
-    return _wrap(_kernel(x, "cast")(x.handle, {"target_dtype": dtype}))
+    """x in another dtype (handlers/copy.ts cast: the same tensor when the dtype matches)."""
+    if x.dtype == dtype:
+        x.handle.storage.inc_ref()
+        return _wrap(HipTensorHandle(x.handle.storage, x.shape, x.dtype, x.strides, x.offset))
+    out = _new(x, x.shape, dtype)
+    _kernel(x, "cast")(TensorIterator.unary_op(x.handle, out))
+    return _wrap(out)
+
+
+def clone(x: Tensor) -> Tensor:
+    out = _new(x, x.shape)
+    _kernel(x, "clone")(TensorIterator.unary_op(x.handle, out))
+    return _wrap(out)
 
 
 def copy_(dst: Tensor, src: Tensor) -> Tensor:
-    _kernel(dst, "copy_")(dst.handle, src.handle)
+    """dst (any view) takes src's values (handlers/copy.ts copyInplace: shapes must match)."""
+    if tuple(dst.shape) != tuple(src.shape):
+        raise ValueError(f"copy_: shape mismatch {tuple(dst.shape)} vs {tuple(src.shape)}")
+    _kernel(dst, "copy_")(TensorIterator.unary_op(src.handle, dst.handle))
     return dst
 
 
@@ -373,30 +364,24 @@ def index_select(x: Tensor, dim: int, index: Tensor) -> Tensor:
     return _wrap(out)
 
 
-def argmax(x: Tensor, dim: int = -1) -> Tensor:
-    """Index of the maximum along `dim` (lowest index among maxima), int32, `dim` removed.  A dim
-    other than the last is moved last and materialised contiguous first (the argmax kernel reduces
-    contiguous rows; reference: reduction/argShaderBuilder.ts:59-110 reduces any dim)."""
+def argmax(x: Tensor, dim: Optional[int] = -1, keepdim: bool = False) -> Tensor:
+    """Index of the maximum along `dim` (all elements when None), lowest index among maxima, int32,
+    through the reduction iterator (handlers/iterator.ts buildReduceIterator; the kernel reads the
+    input through its strides, reduction/argShaderBuilder.ts:205-240 reduces any dim)."""
     nd = len(x.shape)
-    d = dim + nd if dim < 0 else dim
-    if not 0 <= d < nd:
+    axes = None if dim is None else [dim]
+    if axes is not None and not -nd <= dim < nd:
         raise ValueError(f"argmax: dim {dim} out of range for a {nd}-d tensor")
-    src = x
-    if d != nd - 1:
-        perm = [i for i in range(nd) if i != d] + [d]
-        src = contiguous(permute(x, perm))
-    out = _new(x, tuple(s for i, s in enumerate(x.shape) if i != d), "int32")
-    _kernel(x, "argmax")(TensorIterator([src.handle], [out]))
-    if src is not x:
-        src.dispose()
-    return _wrap(out)
+    it = TensorIterator.reduction_op(x.handle, axes, keepdim, out_dtype="int32")
+    _kernel(x, "argmax")(it)
+    return _wrap(it.output().tensor_handle)
 
 
 def zeros(shape, dtype: str = "float32") -> Tensor:
-    b = env.get_backend("hip")
-    h = b.create_tensor_handle(tuple(shape), dtype)
-    b.operators.find("zeros")(h)
-    return _wrap(h)
+    """The zeros factory (handlers/factory.ts:50-61): a nullary iterator over a new tensor."""
+    it = TensorIterator.nullary_op(tuple(shape), dtype)
+    env.get_backend("hip").operators.find("zeros")(it)
+    return _wrap(it.output().tensor_handle)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -28,7 +28,7 @@ import numpy as np
 
 from . import _lib
 from .dtypes import BFLOAT16, FLOAT32, INT32, KH_CODE
-from .tensor import HipTensorHandle, copy_into, contiguous_strides
+from .tensor import HipTensorHandle, check_extent, copy_into, contiguous_strides
 
 _vp = C.c_void_p
 
@@ -462,74 +462,238 @@ def rms_norm_rope(q, k, params):
 
 
 # ---------------------------------------------------------------------------------------------
-# pointwise (iterator kernels for the same-shape contiguous case the dispatcher prepares)
+# Iterators: the operand geometry Kandle's dispatcher hands an iterator kernel
+# (packages/core/src/dispatch/TensorIterator.ts), and the kernels that consume it
 # ---------------------------------------------------------------------------------------------
+def broadcast_strides(shape, strides, target) -> tuple:
+    """computeBroadcastStrides (packages/utils/src/shape.ts:57-100): the strides of a view of
+    shape / strides read at every index of `target` (right-aligned; 0 on new axes and on broadcast
+    extents of 1)."""
+    if len(target) < len(shape):
+        raise ValueError("broadcast: the target shape has fewer dimensions")
+    out = [0] * len(target)
+    for i in range(len(target)):
+        si = len(shape) - len(target) + i
+        if si < 0:
+            continue
+        if shape[si] == target[i]:
+            out[i] = strides[si]
+        elif shape[si] != 1:
+            raise ValueError(f"broadcast: {tuple(shape)} does not broadcast to {tuple(target)}")
+    return tuple(out)
+
+
+def _promote(dtypes) -> str:
+    """The dtype an elementwise op computes and stores in: float32 over bfloat16, floats over int32."""
+    if FLOAT32 in dtypes:
+        return FLOAT32
+    if BFLOAT16 in dtypes:
+        return BFLOAT16
+    return INT32
+
+
 @dataclass
+class IteratorOperand:
+    """TensorIteratorOperand (packages/types/src/tensor.ts:282-378): strides are element strides
+    aligned to the iterator's output shape (0 on broadcast axes), or for a reduction input to its
+    kept axes with reduction_strides over the reduced ones; offset is in elements."""
+
+    tensor_handle: HipTensorHandle
+    dtype: str
+    shape: tuple
+    strides: tuple
+    offset: int
+    is_output: bool
+    reduction_strides: Optional[tuple] = None
+
+
 class TensorIterator:
-    """Minimal stand-in for ITensorIterator (packages/types/src/tensor.ts:395-569): the dispatcher
-    broadcasts / materialises so every operand is contiguous with the output's shape."""
+    """ITensorIterator (packages/types/src/tensor.ts:395-569) over this backend's handles, built as
+    Kandle's TensorIterator factories build one (TensorIterator.ts: build / unaryOp / binaryOp /
+    nullaryOp / reductionOp): outputs first, input strides aligned to the output shape, scalar
+    arguments (get_scalar_args).  TensorIterator(inputs, outputs) is the elementwise form (the
+    inputs broadcast to the first output's shape)."""
 
-    inputs: list
-    outputs: list
+    def __init__(self, inputs, outputs, scalar_args: Optional[dict] = None, _operands=None, _shapes=None,
+                 _reduction=None):
+        if _operands is None:
+            out = outputs[0]
+            shape = tuple(out.shape)
+            ops = [IteratorOperand(o, o.dtype, tuple(o.shape), tuple(o.strides), o.offset, True) for o in outputs]
+            ops += [IteratorOperand(h, h.dtype, tuple(h.shape), broadcast_strides(h.shape, h.strides, shape), h.offset,
+                                    False) for h in inputs]
+            _operands, _shapes = ops, (shape, shape)
+        self.operands = list(_operands)
+        self.num_outputs = len(outputs)
+        self.num_inputs = len(self.operands) - self.num_outputs
+        self.input_shape, self.output_shape = _shapes
+        self.output_numel = int(np.prod(self.output_shape)) if self.output_shape else 1
+        axes, keep = _reduction if _reduction is not None else ((), False)
+        self.reduction_axes = tuple(axes)
+        self.is_reduction = bool(axes)
+        self.keep_dims = bool(keep)
+        self.reduction_shape = tuple(self.input_shape[a] for a in self.reduction_axes)
+        self._scalars = dict(scalar_args or {})
 
-    def input(self, i: int = 0) -> HipTensorHandle:
-        return self.inputs[i]
+    def output(self, i: int = 0) -> IteratorOperand:
+        return self.operands[i]
 
-    def output(self, i: int = 0) -> HipTensorHandle:
-        return self.outputs[i]
+    def input(self, i: int = 0) -> IteratorOperand:
+        return self.operands[self.num_outputs + i]
+
+    def set_scalar_args(self, args: dict) -> None:
+        self._scalars = dict(args)
+
+    def get_scalar_args(self) -> dict:
+        return dict(self._scalars)
+
+    def get_scalar_arg(self, name: str):
+        return self._scalars.get(name)
+
+    # -- factories ----------------------------------------------------------------------------
+    @classmethod
+    def build(cls, inputs, output: Optional[HipTensorHandle] = None, out_dtype: Optional[str] = None,
+              scalar_args: Optional[dict] = None) -> "TensorIterator":
+        """Elementwise: the inputs broadcast to one shape; the output (allocated, in out_dtype or the
+        promoted input dtype, when not given) has that shape."""
+        if output is None:
+            shape = tuple(np.broadcast_shapes(*[tuple(h.shape) for h in inputs])) if inputs else ()
+            output = HipTensorHandle.create_new(shape, out_dtype or _promote([h.dtype for h in inputs]))
+        else:
+            np.broadcast_shapes(tuple(output.shape), *[tuple(h.shape) for h in inputs])
+        return cls(list(inputs), [output], scalar_args)
+
+    @classmethod
+    def unary_op(cls, x, output=None, scalar_args=None) -> "TensorIterator":
+        return cls.build([x], output, scalar_args=scalar_args)
+
+    @classmethod
+    def binary_op(cls, a, b, output=None, scalar_args=None) -> "TensorIterator":
+        return cls.build([a, b], output, scalar_args=scalar_args)
+
+    @classmethod
+    def nullary_op(cls, shape, dtype: str, output: Optional[HipTensorHandle] = None,
+                   scalar_args: Optional[dict] = None) -> "TensorIterator":
+        """A factory's iterator: no inputs, a new contiguous output of shape and dtype (or `output`)."""
+        out = output if output is not None else HipTensorHandle.create_new(tuple(shape), dtype)
+        return cls([], [out], scalar_args)
+
+    @classmethod
+    def reduction_op(cls, x: HipTensorHandle, axes=None, keep_dims: bool = False,
+                     output: Optional[HipTensorHandle] = None, out_dtype: Optional[str] = None,
+                     scalar_args: Optional[dict] = None) -> "TensorIterator":
+        """A reduction over `axes` (all axes when None or empty): the output holds the kept axes (and
+        extent-1 reduced axes with keep_dims); the input's strides split into the kept axes' and the
+        reduced axes' (reduction_strides), as splitStridesForReduction does."""
+        nd = len(x.shape)
+        red = sorted(range(nd)) if not axes else sorted(a + nd if a < 0 else a for a in axes)
+        if any(not 0 <= a < nd for a in red):
+            raise ValueError(f"reduction: axis out of range for a {nd}-d tensor")
+        kept = [i for i in range(nd) if i not in red]
+        out_shape = tuple(1 if i in red else x.shape[i] for i in range(nd)) if keep_dims else \
+            tuple(x.shape[i] for i in kept)
+        out = output if output is not None else HipTensorHandle.create_new(out_shape, out_dtype or x.dtype)
+        if out.numel != (int(np.prod(out_shape)) if out_shape else 1):
+            raise ValueError(f"reduction: output {tuple(out.shape)} for a result of {out_shape}")
+        ops = [IteratorOperand(out, out.dtype, tuple(out.shape), tuple(out.strides), out.offset, True),
+               IteratorOperand(x, x.dtype, tuple(x.shape), tuple(x.strides[i] for i in kept), x.offset, False,
+                               tuple(x.strides[i] for i in red))]
+        return cls(None, [out], scalar_args, _operands=ops, _shapes=(tuple(x.shape), out_shape),
+                   _reduction=(red, keep_dims))
 
 
-def _binary(op: int, it: TensorIterator) -> None:
-    a, b, o = it.input(0), it.input(1), it.output()
-    if not (a.numel == b.numel == o.numel) or not (a.is_contiguous() and b.is_contiguous() and o.is_contiguous()):
-        raise ValueError("binary kernel: operands must be contiguous and of equal size")
-    _lib.call("kh_binary", op, _vp(a.data_ptr()), _vp(b.data_ptr()), _vp(o.data_ptr()), o.numel, o.kh_dtype)
+def _operand_geometry(op, shape, is_output: bool, name: str):
+    """(device pointer, strides over `shape`, dtype code) of an iterator operand: the strides the
+    dispatcher aligned (or, for an operand without them, its handle broadcast to `shape`), checked to
+    stay inside its storage.  A bare handle is taken as an operand with its own geometry."""
+    h = op.tensor_handle if isinstance(op, IteratorOperand) else op
+    dtype = op.dtype if isinstance(op, IteratorOperand) else h.dtype
+    if dtype != h.dtype:
+        raise TypeError(f"{name}: operand dtype {dtype} differs from its handle's {h.dtype}")
+    offset = op.offset if isinstance(op, IteratorOperand) else h.offset
+    st = op.strides if isinstance(op, IteratorOperand) and len(op.strides) == len(shape) else \
+        broadcast_strides(h.shape, h.strides, shape)
+    if is_output and any(n > 1 and s == 0 for n, s in zip(shape, st)):
+        raise ValueError(f"{name}: the output broadcasts an axis")
+    check_extent(h.storage, shape, st, offset, dtype, f"{name} operand")
+    return h.storage.ptr + offset * h.itemsize, tuple(st), KH_CODE[dtype]
 
 
-def add(it: TensorIterator) -> None:
-    _binary(0, it)
+MAP_OPS = {"copy": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "neg": 5, "cos": 6, "sin": 7, "silu": 8, "fill": 9,
+           "arange": 10}
+_MAP_NIN = {0: 1, 1: 2, 2: 2, 3: 2, 4: 2, 5: 1, 6: 1, 7: 1, 8: 1, 9: 0, 10: 0}
 
 
-def mul(it: TensorIterator) -> None:
-    _binary(1, it)
+def map_strided(op: int, shape, out, a=None, b=None, s0: float = 0.0, s1: float = 0.0, name: str = "map") -> None:
+    """kh_map_strided over `shape`: out and the inputs are IteratorOperands (or handles read with
+    their own strides broadcast to `shape`)."""
+    shape = tuple(int(n) for n in shape)
+    if len(shape) > 8:
+        raise ValueError(f"{name}: at most 8 dimensions")
+    po, so, do = _operand_geometry(out, shape, True, name)
+    args = [op, len(shape), _lib.i64_array(shape or [1]), _vp(po), _lib.i64_array(so or [1]), do]
+    for x in (a, b):
+        if x is None:
+            args += [None, None, 0]
+        else:
+            px, sx, dx = _operand_geometry(x, shape, False, name)
+            args += [_vp(px), _lib.i64_array(sx or [1]), dx]
+    _lib.call("kh_map_strided", *args, C.c_double(s0), C.c_double(s1))
 
 
-def sub(it: TensorIterator) -> None:
-    _binary(2, it)
+def _map_kernel(name: str, op: int, scalars=None):
+    """An iterator kernel (register.ts:9: (iter) => None, the output preallocated as
+    iter.output().tensor_handle) over kh_map_strided: inputs read through their strides, broadcast
+    included; the output written through its own (a view for copy_).  scalars(args) -> (s0, s1)
+    from the iterator's scalar arguments: add / sub alpha (default 1), a fill value, arange's start
+    and step (arangeExecutor.ts:37-44)."""
+    nin = _MAP_NIN[op]
+
+    def kernel(it: TensorIterator) -> None:
+        if it.num_inputs < nin:
+            raise ValueError(f"{name}: {nin} inputs expected")
+        s0, s1 = scalars(it.get_scalar_args()) if scalars is not None else (0.0, 0.0)
+        map_strided(op, it.output_shape, it.output(0), it.input(0) if nin >= 1 else None,
+                    it.input(1) if nin >= 2 else None, s0, s1, name)
+
+    kernel.__name__ = name
+    return kernel
 
 
-def _unary(op: int, name: str, it: TensorIterator) -> None:
-    x, o = it.input(0), it.output()
-    if not (x.is_contiguous() and o.is_contiguous()) or x.numel != o.numel or x.dtype != o.dtype:
-        raise ValueError(f"{name}: operands must be contiguous, of equal size and dtype")
-    _lib.call("kh_unary", op, _vp(x.data_ptr()), _vp(o.data_ptr()), o.numel, o.kh_dtype)
+def _alpha(sc):
+    return float(sc.get("alpha", 1.0)), 0.0
 
 
-def neg(it: TensorIterator) -> None:
-    _unary(0, "neg", it)
+add = _map_kernel("add", MAP_OPS["add"], _alpha)
+sub = _map_kernel("sub", MAP_OPS["sub"], _alpha)
+mul = _map_kernel("mul", MAP_OPS["mul"])
+div = _map_kernel("div", MAP_OPS["div"])
+neg = _map_kernel("neg", MAP_OPS["neg"])
+cos = _map_kernel("cos", MAP_OPS["cos"])
+sin = _map_kernel("sin", MAP_OPS["sin"])
+silu = _map_kernel("silu", MAP_OPS["silu"])
+# copy / cast / contiguous / clone / copy_ are one kernel: the output (possibly a strided view, or a
+# new tensor in the target dtype) takes the input's values (copy/index.ts:13-33, handlers/copy.ts)
+copy = _map_kernel("copy", MAP_OPS["copy"])
+cast = _map_kernel("cast", MAP_OPS["copy"])
+contiguous = _map_kernel("contiguous", MAP_OPS["copy"])
+clone = _map_kernel("clone", MAP_OPS["copy"])
+copy_ = _map_kernel("copy_", MAP_OPS["copy"])
+zeros = _map_kernel("zeros", MAP_OPS["fill"], lambda sc: (0.0, 0.0))
+ones = _map_kernel("ones", MAP_OPS["fill"], lambda sc: (1.0, 0.0))
+full = _map_kernel("full", MAP_OPS["fill"],
+                   lambda sc: (float(sc["fill_value"] if "fill_value" in sc else sc["fillValue"]), 0.0))
+arange = _map_kernel("arange", MAP_OPS["arange"],
+                     lambda sc: (float(sc.get("start", 0.0)), float(sc.get("step", 1.0))))
 
 
-def cos(it: TensorIterator) -> None:
-    _unary(1, "cos", it)
+def empty(it: TensorIterator) -> None:
+    """empty: the output is left as allocated."""
 
 
-def sin(it: TensorIterator) -> None:
-    _unary(2, "sin", it)
-
-
-def arange(output: HipTensorHandle, start: float = 0.0, step: float = 1.0) -> None:
-    """output[i] = start + i * step over the contiguous output (the reference's factory kernel)."""
-    if not output.is_contiguous():
-        raise ValueError("arange: output must be contiguous")
-    _lib.call("kh_arange", _vp(output.data_ptr()), output.numel, C.c_double(start), C.c_double(step),
-              output.kh_dtype)
-
-
-def silu(it: TensorIterator) -> None:
-    x, o = it.input(0), it.output()
-    if not (x.is_contiguous() and o.is_contiguous()) or x.numel != o.numel:
-        raise ValueError("silu: operands must be contiguous and of equal size")
-    _lib.call("kh_silu", _vp(x.data_ptr()), _vp(o.data_ptr()), o.numel, o.kh_dtype)
+def fill(output: HipTensorHandle, value: float) -> None:
+    """Every element of `output` (any view) set to value."""
+    map_strided(MAP_OPS["fill"], output.shape, output, s0=float(value), name="fill")
 
 
 def silu_mul(gate: HipTensorHandle, up: HipTensorHandle, output: HipTensorHandle) -> None:
@@ -564,51 +728,6 @@ def silu_mul(gate: HipTensorHandle, up: HipTensorHandle, output: HipTensorHandle
 # ---------------------------------------------------------------------------------------------
 # copy / gather / argmax / factory
 # ---------------------------------------------------------------------------------------------
-def copy(input: HipTensorHandle, options: dict) -> HipTensorHandle:
-    """CopyKernelImpl: contiguous copy of any view, casting to options['target_dtype'] if given."""
-    target = (options or {}).get("target_dtype") or input.dtype
-    out = HipTensorHandle.create_new(input.shape, target)
-    copy_into(input, out)
-    return out
-
-
-def copy_(dst: HipTensorHandle, src: HipTensorHandle) -> None:
-    """In-place copy into a (possibly strided) destination view, e.g. a KV-cache slice
-    (packages/model-utils/src/kv-cache.ts:180-188).  The destination's last dim must be contiguous and
-    its rows evenly described by (batch, head, seq) strides; the source is materialised first."""
-    if dst.shape != src.shape:
-        raise ValueError(f"copy_: shape mismatch {dst.shape} vs {src.shape}")
-    if dst.is_contiguous():
-        copy_into(src, dst)
-        return
-    s = src if (src.is_contiguous() and src.dtype == dst.dtype) else _materialize(src, dst.dtype)
-    try:
-        # Scatter: copy row-blocks of the contiguous source into the strided destination with
-        # strided copies whose *source* is the destination layout read backwards is not expressible;
-        # instead treat the destination as the "source view" of a gather from a contiguous buffer.
-        _scatter_rows(s, dst)
-    finally:
-        if s is not src:
-            s.dispose()
-
-
-def _scatter_rows(src: HipTensorHandle, dst: HipTensorHandle) -> None:
-    # A strided destination is written one contiguous run of its innermost dims at a time.
-    shape, strides = list(dst.shape), list(dst.strides)
-    inner = 1
-    k = len(shape)
-    while k > 0 and strides[k - 1] == inner:
-        inner *= shape[k - 1]
-        k -= 1
-    outer_shape = shape[:k]
-    isz = dst.itemsize
-    for n, idx in enumerate(np.ndindex(*outer_shape) if outer_shape else [()]):
-        off = dst.offset + sum(i * st for i, st in zip(idx, strides[:k]))
-        _lib.call(
-            "kh_memcpy_d2d", _vp(dst.storage.ptr + off * isz), _vp(src.data_ptr() + n * inner * isz), inner * isz
-        )
-
-
 def index_select(self_: HipTensorHandle, index: HipTensorHandle, params: dict, output: HipTensorHandle) -> None:
     """GatherKernelImpl (gather.ts:121,190): output = self_ with the entries of `index` taken along
     params['dim'] (default 0: rows of an embedding table); output holds self_'s shape with that dim
@@ -641,25 +760,42 @@ def index_select(self_: HipTensorHandle, index: HipTensorHandle, params: dict, o
 
 
 def argmax(it: TensorIterator) -> None:
-    """Row-wise argmax over the last dim (lowest index among maxima), int32 output."""
-    x, o = it.input(0), it.output()
-    xs = x if x.is_contiguous() else _materialize(x)
+    """argmax (reduction/index.ts:20-22; argShaderBuilder.ts:205-240) over the iterator's reduction
+    axes (the dispatcher's dim; all axes without one, or the scalar argument 'dim'): the input's
+    rows are gathered into [kept, reduced] order with one strided copy and each row's maximum taken
+    with the lowest index among maxima (sampling/index.ts:132,138; NaN never wins), int32 output."""
+    x = it.input(0).tensor_handle
+    nd = len(x.shape)
+    if it.is_reduction:
+        axes = list(it.reduction_axes)
+    else:
+        dim = it.get_scalar_arg("dim")
+        axes = list(range(nd)) if dim is None else [int(dim[0] if isinstance(dim, (list, tuple)) else dim)]
+    axes = [a + nd if a < 0 else a for a in axes]
+    if any(not 0 <= a < nd for a in axes):
+        raise ValueError(f"argmax: axis out of range for a {nd}-d tensor")
+    kept = [i for i in range(nd) if i not in axes]
+    perm = kept + axes
+    R = int(np.prod([x.shape[a] for a in axes])) if axes else 1
+    P = int(np.prod([x.shape[i] for i in kept])) if kept else 1
+    if R == 0:
+        raise ValueError("argmax: reduction over an empty axis")
+    out = it.output(0)
+    if out.tensor_handle.dtype != INT32:
+        raise TypeError("argmax: the output must be int32")
+    if it.output_numel != P:
+        raise ValueError(f"argmax: an output of {tuple(it.output_shape)} for {P} rows")
+    pshape = tuple(x.shape[i] for i in perm)
+    rows = HipTensorHandle.create_new(pshape, x.dtype)
+    idx = HipTensorHandle.create_new(tuple(it.output_shape), INT32)
     try:
-        n = x.shape[-1]
-        _lib.call("kh_argmax", _vp(xs.data_ptr()), xs.numel // n, n, _vp(o.data_ptr()), xs.kh_dtype)
+        src = IteratorOperand(x, x.dtype, pshape, tuple(x.strides[i] for i in perm), x.offset, False)
+        map_strided(MAP_OPS["copy"], pshape, rows, src, name="argmax")
+        _lib.call("kh_argmax", _vp(rows.data_ptr()), P, R, _vp(idx.data_ptr()), rows.kh_dtype)
+        map_strided(MAP_OPS["copy"], it.output_shape, out, idx, name="argmax")
     finally:
-        if xs is not x:
-            xs.dispose()
-
-
-def fill(output: HipTensorHandle, value: float) -> None:
-    if not output.is_contiguous():
-        raise ValueError("fill: output must be contiguous")
-    _lib.call("kh_fill", _vp(output.data_ptr()), output.numel, C.c_float(value), output.kh_dtype)
-
-
-def zeros(output: HipTensorHandle) -> None:
-    fill(output, 0.0)
+        rows.dispose()
+        idx.dispose()
 
 
 GEMV_PROLOGUES = {"none": 0, "rms_norm": 1, "silu_mul": 2, "silu_mul_interleaved": 3}
@@ -948,14 +1084,18 @@ KERNELS = {
     "linear_qk_norm_rope": linear_qk_norm_rope,
     "linear_add_rms_norm": linear_add_rms_norm,
     "copy": copy,
-    "contiguous": copy,
-    "cast": copy,
+    "contiguous": contiguous,
+    "cast": cast,
+    "clone": clone,
     "copy_": copy_,
+    "div": div,
+    "ones": ones,
+    "full": full,
+    "empty": empty,
     "index_select": index_select,
     "argmax": argmax,
     "greedy_advance": greedy_advance,
     "gemv_fused": gemv_fused,
     "gemv_swiglu": gemv_swiglu,
-    "fill": fill,
     "zeros": zeros,
 }

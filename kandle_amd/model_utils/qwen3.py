@@ -456,7 +456,7 @@ class Qwen3ForCausalLM:
         overwrites st.ids, and greedy_advance logs it and moves st.pos / st.lens on.  Returns the
         step's fp32 logits [1, vocab]."""
         logits = self._step_logits(st)
-        self.ops.find("argmax")(TensorIterator([logits.handle], [st.ids.handle]))
+        self.ops.find("argmax")(TensorIterator.reduction_op(logits.handle, [-1], False, st.ids.handle))
         self.ops.find("greedy_advance")(st.ids.handle, st.pos.handle, st.lens.handle, st.log.handle, st.base)
         return logits
 
@@ -672,7 +672,7 @@ class DecodeState:
         """State after the prefill: ids = argmax(prefill logits) (also log[0]), pos = prompt_len."""
         ids = F.zeros((1,), "int32")
         log = F.zeros((cap,), "int32")
-        ops.find("argmax")(TensorIterator([prefill_logits.handle], [ids.handle]))
+        ops.find("argmax")(TensorIterator.reduction_op(prefill_logits.handle, [-1], False, ids.handle))
         head = F.narrow(log, 0, 0, 1)
         F.copy_(head, ids)
         head.dispose()

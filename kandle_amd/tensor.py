@@ -83,6 +83,29 @@ class HipStorage:
         return buf
 
 
+def check_extent(storage: "HipStorage", shape, strides, offset: int, dtype: str, what: str = "view") -> None:
+    """Refuse a view whose element offsets (offset + sum of index * stride over `shape`) leave its
+    storage: every kernel addresses device memory from these numbers."""
+    if int(offset) != offset or offset < 0:
+        raise ValueError(f"{what}: offset {offset} is not a non-negative integer")
+    if len(strides) != len(shape):
+        raise ValueError(f"{what}: {len(strides)} strides for a {len(shape)}-d shape")
+    lo = hi = int(offset)
+    for n, st in zip(shape, strides):
+        if n < 0:
+            raise ValueError(f"{what}: negative extent {n}")
+        if n == 0:
+            return
+        span = (int(n) - 1) * int(st)
+        if span < 0:
+            lo += span
+        else:
+            hi += span
+    capacity = storage.nbytes // ITEMSIZE[dtype]
+    if lo < 0 or hi >= capacity:
+        raise ValueError(f"{what}: reaches elements [{lo}, {hi}] of a storage holding {capacity}")
+
+
 class HipTensorHandle:
     """Shape / dtype / element strides / element offset over a HipStorage."""
 
@@ -94,6 +117,7 @@ class HipTensorHandle:
         self.dtype = check_dtype(dtype)
         self.strides = tuple(int(s) for s in (strides if strides is not None else contiguous_strides(self.shape)))
         self.offset = int(offset)
+        check_extent(storage, self.shape, self.strides, self.offset, self.dtype)
         self.id = next(_ids)
         self._disposed = False
 

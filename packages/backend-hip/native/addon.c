@@ -145,6 +145,22 @@ static const int64_t* arg_list(Args* A, size_t i, int64_t* out, uint32_t n) {
   return out;
 }
 
+/* An array of at most `max` integers: returns its length, or -1 after a TypeError. */
+static int arg_list_upto(Args* A, size_t i, int64_t* out, uint32_t max) {
+  bool is_array = false;
+  if (i < A->n) napi_is_array(A->env, A->v[i], &is_array);
+  uint32_t len = 0;
+  if (is_array) napi_get_array_length(A->env, A->v[i], &len);
+  if (!is_array || len > max || max > MAX_LIST) {
+    char want[64];
+    snprintf(want, sizeof want, "an array of at most %u integers", max);
+    type_error(A, i, want);
+    return -1;
+  }
+  arg_list(A, i, out, len);
+  return A->bad ? -1 : (int)len;
+}
+
 /* The bytes of an ArrayBuffer or of a typed array's view. */
 static void* arg_host(Args* A, size_t i, size_t* len) {
   *len = 0;
@@ -479,6 +495,27 @@ FN(decodeAttentionBlock, 18)
   CALL(kh_decode_attention_block(qkv, qn, kn, (const float*)inv, (float)eps, (const int32_t*)pos, kc, vc, hq, hkv,
                                  ml, cs, (float)sc, wo, ldw, no, (float*)x, dt))
 
+/* mapStrided(op, shape[], out, outStrides[], outDtype, a, aStrides[], aDtype, b, bStrides[], bDtype, s0, s1):
+   an elementwise op over `shape` with every operand addressed by its own element strides (Kandle's
+   iterator kernel contract, tensor.ts:282-378); a / b may be null when the op does not read them */
+FN(mapStrided, 13)
+  int64_t sh[MAX_LIST], so[MAX_LIST], sa[MAX_LIST], sb[MAX_LIST];
+  int op = arg_int(A, 0);
+  const int nd = arg_list_upto(A, 1, sh, 8);
+  const uint32_t n = nd < 0 ? 0 : (uint32_t)nd;
+  void* o = arg_ptr(A, 2);
+  arg_list(A, 3, so, n);
+  int odt = arg_int(A, 4);
+  void* a = arg_ptr(A, 5);
+  if (a != NULL) arg_list(A, 6, sa, n);
+  int adt = arg_int(A, 7);
+  void* b = arg_ptr(A, 8);
+  if (b != NULL) arg_list(A, 9, sb, n);
+  int bdt = arg_int(A, 10);
+  double s0 = arg_f64(A, 11), s1 = arg_f64(A, 12);
+  CALL(kh_map_strided(op, (int)n, sh, o, so, odt, a, a != NULL ? sa : NULL, adt, b, b != NULL ? sb : NULL, bdt, s0,
+                      s1))
+
 /* ---------------------------------------------------------------- hot path --------------------- */
 /* rmsNorm(x, xRowStride, w, y, yRowStride, rows, n, eps, dtype, outDtype) */
 FN(rmsNorm, 10)
@@ -623,7 +660,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(allocStats), EXPORT(memcpyH2D), EXPORT(memcpyD2H), EXPORT(memcpyD2D), EXPORT(synchronize),
       EXPORT(eventCreate), EXPORT(eventDestroy), EXPORT(eventRecord), EXPORT(eventElapsedMs),
       EXPORT(graphBeginCapture), EXPORT(graphEndCapture), EXPORT(graphLaunch), EXPORT(graphDestroy),
-      EXPORT(fill), EXPORT(copyStrided), EXPORT(binary), EXPORT(silu), EXPORT(unary), EXPORT(arange),
+      EXPORT(fill), EXPORT(copyStrided), EXPORT(mapStrided), EXPORT(binary), EXPORT(silu), EXPORT(unary), EXPORT(arange),
       EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),

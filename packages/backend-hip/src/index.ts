@@ -18,9 +18,11 @@ const addon = require(path.join(__dirname, '..', 'native', 'kandle_hip.node'));
 // Types mirrored from @kandle/types (tensor.ts:6-55, backend/index.ts:9-55, register.ts:9-144,
 // matmulOps.ts:32-125); only the members this backend reads or provides.
 // ---------------------------------------------------------------------------------------------
-export type DType = 'float32' | 'bfloat16' | 'int32';
+// int64 is stored as int32 on the device, as backend-webgpu stores it (base/DTypeResolver.ts:331-350:
+// uploads narrow BigInt64 values to i32, downloads widen them back to BigInt64Array).
+export type DType = 'float32' | 'bfloat16' | 'int32' | 'int64';
 export type Shape = number[];
-type TypedData = Float32Array | Int32Array | Uint16Array;
+type TypedData = Float32Array | Int32Array | Uint16Array | BigInt64Array;
 type KernelFn = (...args: any[]) => any;
 
 export interface CreateTensorOptions {
@@ -45,18 +47,36 @@ export interface MatmulConfig {
   inputC?: HipTensorHandle;
 }
 
+// TensorIteratorOperand / ITensorIterator (types/src/tensor.ts:282-569): what an iterator kernel
+// reads.  strides are element strides aligned to outputShape (0 on broadcast axes) and offset is in
+// elements; for a reduction input, strides cover the kept axes and reductionStrides the reduced ones.
 export interface IteratorOperand {
   tensorHandle: HipTensorHandle;
+  dtype?: DType;
+  shape?: readonly number[];
+  strides?: readonly number[];
+  offset?: number;
+  isOutput?: boolean;
+  reductionStrides?: readonly number[];
 }
 
 export interface TensorIterator {
   numInputs: number;
+  numOutputs?: number;
+  inputShape?: readonly number[];
+  outputShape?: readonly number[];
+  outputNumel?: number;
+  isReduction?: boolean;
+  reductionAxes?: readonly number[];
+  reductionShape?: readonly number[];
+  keepDims?: boolean;
   output(idx?: number): IteratorOperand;
-  input(idx: number): IteratorOperand;
+  input(idx?: number): IteratorOperand;
+  getScalarArgs?(): { [key: string]: any };
 }
 
-const DTYPE_CODE: { [name: string]: number } = { float32: 0, bfloat16: 1, int32: 2 };
-const ITEMSIZE: { [name: string]: number } = { float32: 4, bfloat16: 2, int32: 4 };
+const DTYPE_CODE: { [name: string]: number } = { float32: 0, bfloat16: 1, int32: 2, int64: 2 };
+const ITEMSIZE: { [name: string]: number } = { float32: 4, bfloat16: 2, int32: 4, int64: 4 };
 
 function contiguousStrides(shape: Shape): number[] {
   const strides = new Array(shape.length).fill(1);
@@ -133,6 +153,8 @@ export class HipTensorHandle {
 
   constructor(storage: HipStorage, shape: Shape, dtype: DType, strides: number[], offset: number) {
     if (!(dtype in DTYPE_CODE)) throw new TypeError(`backend-hip: unsupported dtype ${dtype}`);
+    if (strides.length !== shape.length) throw new Error(`backend-hip: ${strides.length} strides for a ${shape.length}-d shape`);
+    checkExtent(storage, shape, strides, offset, dtype, 'view');
     this.storage = storage;
     this.shape = shape.slice();
     this.dtype = dtype;
@@ -179,6 +201,11 @@ export class HipTensorHandle {
       host = data instanceof Uint16Array ? data : toBf16Bits(Float32Array.from(data as number[]));
     } else if (this.dtype === 'int32') {
       host = data instanceof Int32Array ? data : Int32Array.from(data as number[]);
+    } else if (this.dtype === 'int64') {
+      // narrowed to the int32 storage (DTypeResolver.ts:331-340)
+      const src = data as any;
+      host = new Int32Array(src.length);
+      for (let i = 0; i < src.length; ++i) (host as Int32Array)[i] = Number(src[i]);
     } else {
       host = data instanceof Float32Array ? data : Float32Array.from(data as number[]);
     }
@@ -186,11 +213,12 @@ export class HipTensorHandle {
     addon.memcpyH2D(this.ptr, host);
   }
 
-  // Logical contiguous values (bf16 widened to float32), after the stream's pending work.
-  dataAsync(): Promise<Float32Array | Int32Array> {
+  // Logical contiguous values (bf16 widened to float32, int64 widened to BigInt64Array from its
+  // int32 storage), after the stream's pending work.
+  dataAsync(): Promise<Float32Array | Int32Array | BigInt64Array> {
     const src = this.isContiguous() ? this : contiguous(this);
     const n = this.numel;
-    let out: Float32Array | Int32Array;
+    let out: Float32Array | Int32Array | BigInt64Array;
     if (this.dtype === 'bfloat16') {
       const bits = new Uint16Array(n);
       addon.memcpyD2H(bits, src.ptr);
@@ -198,6 +226,11 @@ export class HipTensorHandle {
     } else if (this.dtype === 'int32') {
       out = new Int32Array(n);
       addon.memcpyD2H(out, src.ptr);
+    } else if (this.dtype === 'int64') {
+      const narrow = new Int32Array(n);
+      addon.memcpyD2H(narrow, src.ptr);
+      out = new BigInt64Array(n);
+      for (let i = 0; i < n; ++i) (out as BigInt64Array)[i] = BigInt(narrow[i]);
     } else {
       out = new Float32Array(n);
       addon.memcpyD2H(out, src.ptr);
@@ -211,6 +244,25 @@ export class HipTensorHandle {
     this.isDisposed = true;
     this.storage.decRef();
   }
+}
+
+// The element offsets a view of `shape` with `strides` from `offset` reaches must lie inside its
+// storage: every kernel addresses memory from these numbers, so a view running past the block (or
+// before it) is refused here rather than read or written on the device.
+function checkExtent(storage: HipStorage, shape: readonly number[], strides: readonly number[], offset: number,
+                     dtype: string, what: string): void {
+  if (!Number.isInteger(offset) || offset < 0) throw new Error(`backend-hip: ${what} offset ${offset} is not a non-negative integer`);
+  let lo = offset, hi = offset, empty = false;
+  for (let i = 0; i < shape.length; ++i) {
+    if (!Number.isInteger(shape[i]) || shape[i] < 0) throw new Error(`backend-hip: ${what} extent ${shape[i]} is invalid`);
+    if (shape[i] === 0) empty = true;
+    const span = (shape[i] - 1) * strides[i];
+    if (span < 0) lo += span; else hi += span;
+  }
+  if (empty) return;
+  const capacity = Math.floor(storage.byteLength / ITEMSIZE[dtype]);
+  if (lo < 0 || hi >= capacity)
+    throw new Error(`backend-hip: ${what} reaches elements [${lo}, ${hi}] of a storage holding ${capacity}`);
 }
 
 function viewOf(base: HipTensorHandle, shape: Shape, strides: number[], offset: number): HipTensorHandle {
@@ -313,12 +365,23 @@ function rmsNorm(inputs: HipTensorHandle[], params: { [key: string]: any }): Hip
   return out;
 }
 
-// matmul(config, a, b) — out = alpha * a @ op(b) + beta * inputC (matmulOps.ts:32-125, 486-493).
-// a [..., M, K] and out [..., M, N] row-major; b [N, K] with transposeB (nn.Linear weights) or
-// [K, N]; batches loop over the leading dims of a (b shared or batched alike).
+// matmul(config, a, b) — out = alpha * op(a) @ op(b) + beta * inputC (matmulOps.ts:32-125, 486-493).
+// op(a) [..., M, K]: a itself, or with transposeA a stored [..., K, M] (the dispatcher's transpose
+// detection from strides, matmulOps.ts:171-181), materialised as [..., M, K]; out [..., M, N]
+// row-major; b [N, K] with transposeB (nn.Linear weights) or [K, N]; batches loop over the leading
+// dims of a (b shared or batched alike).  float32 activations may meet bfloat16 weights.
 function matmul(config: MatmulConfig, a: HipTensorHandle, b: HipTensorHandle): void {
-  if (config.transposeA) throw new Error('backend-hip matmul: transposeA operands must be materialised first');
-  const ac = materialize(a);
+  let at = a;
+  if (config.transposeA) {
+    const nd = a.shape.length;
+    if (nd < 2) throw new Error('matmul: transposeA needs a matrix');
+    const sh = a.shape.slice(), st = a.strides.slice();
+    [sh[nd - 2], sh[nd - 1]] = [sh[nd - 1], sh[nd - 2]];
+    [st[nd - 2], st[nd - 1]] = [st[nd - 1], st[nd - 2]];
+    at = viewOf(a, sh, st, a.offset);
+  }
+  const ac = materialize(at);
+  if (at !== a) at.dispose();
   const bc = materialize(b);
   const out = config.output;
   const M = config.M, N = config.N, K = config.K;
@@ -338,54 +401,247 @@ function matmul(config: MatmulConfig, a: HipTensorHandle, b: HipTensorHandle): v
   if (c !== undefined) c.dispose();
 }
 
-function sameShapeContiguous(hs: HipTensorHandle[], name: string): void {
-  for (const h of hs) {
-    if (h.numel !== hs[0].numel) throw new Error(`${name}: broadcasting operands must be expanded first`);
+// ---------------------------------------------------------------------------------------------
+// Iterators: the operand geometry Kandle's dispatcher hands an iterator kernel
+// (core/src/dispatch/TensorIterator.ts), and the kernels that consume it
+// ---------------------------------------------------------------------------------------------
+
+// computeBroadcastStrides (utils/src/shape.ts:57-100): the strides of a view of `shape` / `strides`
+// read at every index of `target` (right-aligned; 0 on new axes and on broadcast extents of 1).
+function broadcastStrides(shape: readonly number[], strides: readonly number[], target: readonly number[]): number[] {
+  if (target.length < shape.length) throw new Error('broadcast: the target shape has fewer dimensions');
+  const out: number[] = new Array(target.length).fill(0);
+  for (let i = 0; i < target.length; ++i) {
+    const si = shape.length - target.length + i;
+    if (si < 0) continue;
+    if (shape[si] === target[i]) out[i] = strides[si];
+    else if (shape[si] !== 1) throw new Error(`broadcast: [${shape}] does not broadcast to [${target}]`);
+  }
+  return out;
+}
+
+function broadcastShapes(shapes: readonly (readonly number[])[]): number[] {
+  let nd = 0;
+  for (const sh of shapes) nd = Math.max(nd, sh.length);
+  const out: number[] = new Array(nd).fill(1);
+  for (const sh of shapes) {
+    for (let i = 0; i < sh.length; ++i) {
+      const j = nd - sh.length + i;
+      if (sh[i] === out[j] || sh[i] === 1) continue;
+      if (out[j] !== 1) throw new Error(`broadcast: shapes ${shapes.map((x) => '[' + x + ']').join(', ')} do not broadcast`);
+      out[j] = sh[i];
+    }
+  }
+  return out;
+}
+
+// The dtype an elementwise op computes and stores in (the dispatcher's type promotion, reduced to
+// this backend's dtypes): float32 over bfloat16, floats over integers.
+function promoteTypes(dtypes: readonly DType[]): DType {
+  if (dtypes.indexOf('float32') >= 0) return 'float32';
+  if (dtypes.indexOf('bfloat16') >= 0) return 'bfloat16';
+  if (dtypes.indexOf('int64') >= 0) return 'int64';
+  return 'int32';
+}
+
+// An ITensorIterator over this backend's handles, built the way Kandle's TensorIterator factories
+// build one (unaryOp / binaryOp / nullaryOp / reductionOp / build, TensorIterator.ts): outputs first,
+// input strides aligned to the output shape, outputs allocated when not given, scalar arguments.
+export class HipTensorIterator implements TensorIterator {
+  readonly inputShape: number[];
+  readonly outputShape: number[];
+  readonly outputNumel: number;
+  readonly operands: IteratorOperand[];
+  readonly numOutputs: number;
+  readonly numInputs: number;
+  readonly isReduction: boolean;
+  readonly reductionAxes: number[];
+  readonly reductionShape: number[];
+  readonly keepDims: boolean;
+  private scalarArgs: { [key: string]: any } = {};
+
+  private constructor(inputShape: number[], outputShape: number[], operands: IteratorOperand[], numOutputs: number,
+                      reductionAxes: number[], keepDims: boolean) {
+    this.inputShape = inputShape;
+    this.outputShape = outputShape;
+    this.outputNumel = numelOf(outputShape);
+    this.operands = operands;
+    this.numOutputs = numOutputs;
+    this.numInputs = operands.length - numOutputs;
+    this.isReduction = reductionAxes.length > 0;
+    this.reductionAxes = reductionAxes;
+    this.reductionShape = reductionAxes.map((a) => inputShape[a]);
+    this.keepDims = keepDims;
+  }
+
+  output(idx: number = 0): IteratorOperand {
+    return this.operands[idx];
+  }
+
+  input(idx: number = 0): IteratorOperand {
+    return this.operands[this.numOutputs + idx];
+  }
+
+  setScalarArgs(args: { [key: string]: any }): void {
+    this.scalarArgs = Object.assign({}, args);
+  }
+
+  getScalarArgs(): { [key: string]: any } {
+    return Object.assign({}, this.scalarArgs);
+  }
+
+  getScalarArg(name: string): any {
+    return this.scalarArgs[name];
+  }
+
+  private static operand(h: HipTensorHandle, strides: readonly number[], isOutput: boolean): IteratorOperand {
+    return { tensorHandle: h, dtype: h.dtype, shape: h.shape, strides: strides.slice(), offset: h.offset, isOutput };
+  }
+
+  // An elementwise iterator: the inputs broadcast to one shape; the output (allocated in outDtype,
+  // default the promoted input dtype, when not given) has that shape.
+  static build(inputs: HipTensorHandle[], output?: HipTensorHandle, outDtype?: DType): HipTensorIterator {
+    const shape = output !== undefined ? output.shape.slice() : broadcastShapes(inputs.map((h) => h.shape));
+    if (output !== undefined) broadcastShapes([output.shape as readonly number[]].concat(inputs.map((h) => h.shape)));
+    const out = output !== undefined ? output
+      : HipTensorHandle.createNew(shape, outDtype || promoteTypes(inputs.map((h) => h.dtype)));
+    const ops = [HipTensorIterator.operand(out, out.strides, true)].concat(
+      inputs.map((h) => HipTensorIterator.operand(h, broadcastStrides(h.shape, h.strides, shape), false)));
+    return new HipTensorIterator(shape, shape, ops, 1, [], false);
+  }
+
+  static unaryOp(x: HipTensorHandle, output?: HipTensorHandle): HipTensorIterator {
+    return HipTensorIterator.build([x], output);
+  }
+
+  static binaryOp(a: HipTensorHandle, b: HipTensorHandle, output?: HipTensorHandle): HipTensorIterator {
+    return HipTensorIterator.build([a, b], output);
+  }
+
+  // A factory's iterator: no inputs, a new contiguous output of `shape` and `dtype`, or `output`.
+  static nullaryOp(shape: number[], dtype: DType, output?: HipTensorHandle): HipTensorIterator {
+    const out = output !== undefined ? output : HipTensorHandle.createNew(shape, dtype);
+    return new HipTensorIterator(out.shape.slice(), out.shape.slice(),
+                                 [HipTensorIterator.operand(out, out.strides, true)], 1, [], false);
+  }
+
+  // A reduction over `axes` (all axes when empty or undefined): the output has the kept axes (and
+  // extent-1 reduced axes with keepDims); the input's strides split into the kept axes' and the
+  // reduced axes' (reductionStrides), as splitStridesForReduction does.
+  static reductionOp(x: HipTensorHandle, axes: number[] | undefined, keepDims: boolean, output?: HipTensorHandle,
+                     outDtype?: DType): HipTensorIterator {
+    const nd = x.shape.length;
+    const red = (axes === undefined || axes.length === 0 ? x.shape.map((_: number, i: number) => i)
+      : axes.map((a) => (a < 0 ? a + nd : a))).sort((p, q) => p - q);
+    for (const a of red) if (a < 0 || a >= nd) throw new Error(`reduction: axis out of range for a ${nd}-d tensor`);
+    const kept = x.shape.map((_: number, i: number) => i).filter((i: number) => red.indexOf(i) < 0);
+    const outShape = keepDims ? x.shape.map((e: number, i: number) => (red.indexOf(i) >= 0 ? 1 : e))
+      : kept.map((i: number) => x.shape[i]);
+    const out = output !== undefined ? output : HipTensorHandle.createNew(outShape, outDtype || x.dtype);
+    if (out.numel !== numelOf(outShape)) throw new Error(`reduction: output [${out.shape}] for a result of [${outShape}]`);
+    const inOp = HipTensorIterator.operand(x, kept.map((i: number) => x.strides[i]), false);
+    inOp.reductionStrides = red.map((i: number) => x.strides[i]);
+    return new HipTensorIterator(x.shape.slice(), outShape, [HipTensorIterator.operand(out, out.strides, true), inOp],
+                                 1, red, keepDims);
   }
 }
 
-const BINARY_OP: { [name: string]: number } = { add: 0, mul: 1, sub: 2 };
+// Device address, element strides over `shape` and dtype code of an iterator operand: the strides
+// the dispatcher aligned (or, when an operand carries none, the handle's own broadcast to `shape`)
+// and the element offset, checked to stay inside the operand's storage.
+function operandGeometry(op: IteratorOperand, shape: readonly number[], isOutput: boolean, name: string):
+    { ptr: bigint; strides: number[]; kh: number } {
+  const h = op.tensorHandle;
+  const dtype = (op.dtype || h.dtype) as DType;
+  if (dtype !== h.dtype) throw new Error(`${name}: operand dtype ${dtype} differs from its handle's ${h.dtype}`);
+  const offset = op.offset === undefined ? h.offset : op.offset;
+  const strides = op.strides !== undefined && op.strides.length === shape.length ? op.strides.slice()
+    : broadcastStrides(h.shape, h.strides, shape);
+  if (isOutput) {
+    for (let i = 0; i < shape.length; ++i)
+      if (shape[i] > 1 && strides[i] === 0) throw new Error(`${name}: the output broadcasts axis ${i}`);
+  }
+  checkExtent(h.storage, shape, strides, offset, dtype, `${name} operand`);
+  return { ptr: h.storage.ptr + BigInt(offset * ITEMSIZE[dtype]), strides, kh: DTYPE_CODE[dtype] };
+}
 
-// Pointwise iterator kernels (register.ts:9; ops.ts:299 silu, :329 mul, :437 add): same-shape
-// operands, materialised when strided; the output is preallocated by the dispatcher.
-function binaryKernel(name: string): KernelFn {
+function iteratorShape(iter: TensorIterator): number[] {
+  return (iter.outputShape !== undefined ? iter.outputShape : iter.output(0).tensorHandle.shape).slice();
+}
+
+function scalarArgsOf(iter: TensorIterator): { [key: string]: any } {
+  return iter.getScalarArgs !== undefined ? iter.getScalarArgs() : {};
+}
+
+// kh_map_strided op codes (include/kandle_hip.h)
+const MAP = { copy: 0, add: 1, sub: 2, mul: 3, div: 4, neg: 5, cos: 6, sin: 7, silu: 8, fill: 9, arange: 10 };
+
+// An iterator kernel over kh_map_strided (register.ts:9: (iter) => void, the output preallocated in
+// iter.output().tensorHandle): `nin` inputs read through their strides, broadcast included, the
+// output written through its own strides (a view for copy_, channels-last for contiguous).  s0/s1
+// come from the op's scalar arguments: add/sub alpha (ops.ts:437; default 1), a fill value,
+// arange's start and step (arangeExecutor.ts:37-44).
+function mapKernel(name: string, op: number, nin: number,
+                   scalars?: (sc: { [key: string]: any }) => number[]): KernelFn {
   return (iter: TensorIterator): void => {
-    const out = iter.output().tensorHandle;
-    const a = materialize(iter.input(0).tensorHandle);
-    const b = materialize(iter.input(1).tensorHandle);
-    sameShapeContiguous([out, a, b], name);
-    addon.binary(BINARY_OP[name], a.ptr, b.ptr, out.ptr, out.numel, out.kh);
-    a.dispose();
-    b.dispose();
+    const shape = iteratorShape(iter);
+    if (shape.length > 8) throw new Error(`${name}: at most 8 dimensions`);
+    if (iter.numInputs < nin) throw new Error(`${name}: ${nin} inputs expected`);
+    const o = operandGeometry(iter.output(0), shape, true, name);
+    const a = nin >= 1 ? operandGeometry(iter.input(0), shape, false, name) : null;
+    const b = nin >= 2 ? operandGeometry(iter.input(1), shape, false, name) : null;
+    const sv = scalars === undefined ? [0, 0] : scalars(scalarArgsOf(iter));
+    addon.mapStrided(op, shape, o.ptr, o.strides, o.kh, a === null ? null : a.ptr, a === null ? [] : a.strides,
+                     a === null ? 0 : a.kh, b === null ? null : b.ptr, b === null ? [] : b.strides,
+                     b === null ? 0 : b.kh, sv[0], sv[1]);
   };
 }
 
-function silu(iter: TensorIterator): void {
-  const out = iter.output().tensorHandle;
-  const x = materialize(iter.input(0).tensorHandle);
-  sameShapeContiguous([out, x], 'silu');
-  addon.silu(x.ptr, out.ptr, out.numel, out.kh);
-  x.dispose();
+function alphaOf(sc: { [key: string]: any }): number[] {
+  return [sc.alpha === undefined ? 1 : Number(sc.alpha), 0];
 }
 
-const UNARY_OP: { [name: string]: number } = { neg: 0, cos: 1, sin: 2 };
-
-// neg / cos / sin: what Kandle's composite RoPE (rope.ts:546-644) looks up besides mul and add.
-function unaryKernel(name: string): KernelFn {
-  return (iter: TensorIterator): void => {
-    const out = iter.output().tensorHandle;
-    const x = materialize(iter.input(0).tensorHandle);
-    sameShapeContiguous([out, x], name);
-    if (x.dtype !== out.dtype) throw new Error(`${name}: input and output dtypes differ`);
-    addon.unary(UNARY_OP[name], x.ptr, out.ptr, out.numel, out.kh);
-    x.dispose();
-  };
-}
-
-// arange(output, start, step): output[i] = start + i * step (the factory kernel the RoPE tables use).
-function arange(out: HipTensorHandle, start?: number, step?: number): void {
-  if (!out.isContiguous()) throw new Error('arange: contiguous output expected');
-  addon.arange(out.ptr, out.numel, start === undefined ? 0 : start, step === undefined ? 1 : step, out.kh);
+// argmax(iter): a reduction iterator (reduction/index.ts:20-22; argShaderBuilder.ts:205-240) over
+// iter.reductionAxes (the dispatcher's dim; all axes when it has none): the input is gathered into
+// [kept, reduced] rows (one strided copy) and each row's maximum found with the lowest index among
+// maxima (sampling/index.ts:132,138; NaN never wins); indices are stored as int32 (an int64 output
+// included, as backend-webgpu stores it).
+function argmaxKernel(iter: TensorIterator): void {
+  const x = iter.input(0).tensorHandle;
+  const nd = x.shape.length;
+  let axes: number[];
+  if (iter.reductionAxes !== undefined && iter.reductionAxes.length > 0) {
+    axes = iter.reductionAxes.slice();
+  } else {
+    const dim = scalarArgsOf(iter).dim;
+    axes = dim === undefined || dim === null ? x.shape.map((_: number, i: number) => i)
+      : [Array.isArray(dim) ? dim[0] : (dim as number)];
+  }
+  axes = axes.map((a) => (a < 0 ? a + nd : a));
+  for (const a of axes) if (!(a >= 0 && a < nd)) throw new Error(`argmax: axis out of range for a ${nd}-d tensor`);
+  const kept = x.shape.map((_: number, i: number) => i).filter((i: number) => axes.indexOf(i) < 0);
+  const perm = kept.concat(axes);
+  if (perm.length > 8) throw new Error('argmax: at most 8 dimensions');
+  const R = numelOf(axes.map((i) => x.shape[i]));
+  const P = numelOf(kept.map((i) => x.shape[i]));
+  if (R === 0) throw new Error('argmax: reduction over an empty axis');
+  const out = iter.output(0);
+  const dt = out.tensorHandle.dtype;
+  if (dt !== 'int32' && dt !== 'int64') throw new Error('argmax: the output must be an integer tensor');
+  const oshape = iteratorShape(iter);
+  if (numelOf(oshape) !== P) throw new Error(`argmax: an output of [${oshape}] for ${P} rows`);
+  // the input's rows in [kept..., reduced...] order
+  const pshape = perm.map((i) => x.shape[i]);
+  const g = operandGeometry({ tensorHandle: x, strides: perm.map((i) => x.strides[i]), offset: x.offset }, pshape,
+                            false, 'argmax');
+  const rows = HipTensorHandle.createNew(pshape, x.dtype);
+  addon.mapStrided(MAP.copy, pshape, rows.ptr, rows.strides, rows.kh, g.ptr, g.strides, g.kh, null, [], 0, 0, 0);
+  const og = operandGeometry(out, oshape, true, 'argmax');
+  const idx = HipTensorHandle.createNew(oshape, 'int32');
+  addon.argmax(rows.ptr, P, R, idx.ptr, rows.kh);
+  addon.mapStrided(MAP.copy, oshape, og.ptr, og.strides, og.kh, idx.ptr, idx.strides, idx.kh, null, [], 0, 0, 0);
+  idx.dispose();
+  rows.dispose();
 }
 
 // decode_attention(query, kCache, vCache, seqLens, output, scale): one query token per sequence
@@ -473,48 +729,6 @@ function indexSelect(self: HipTensorHandle, index: HipTensorHandle, params: { [k
   addon.indexSelectDim(t.ptr, outer, t.shape[dim], inner, idx.ptr, idx.numel, output.ptr, t.kh, output.kh);
   t.dispose();
   idx.dispose();
-}
-
-// argmax over the last axis of x into int32 out (lowest index among maxima, NaN never wins).
-function argmax(x: HipTensorHandle, out: HipTensorHandle): void {
-  const xc = materialize(x);
-  const n = xc.shape[xc.shape.length - 1];
-  addon.argmax(xc.ptr, xc.numel / n, n, out.ptr, xc.kh);
-  xc.dispose();
-}
-
-// copy_(dst, src): in-place copy into a (possibly strided) destination view, e.g. a KV-cache slice
-// (kv-cache.ts:180-188).  The source is made contiguous in the destination dtype first; a strided
-// destination is written one contiguous run of its innermost dims at a time.
-function copyInto(dst: HipTensorHandle, src: HipTensorHandle): void {
-  if (dst.shape.join() !== src.shape.join()) throw new Error(`copy_: shape mismatch [${dst.shape}] vs [${src.shape}]`);
-  if (dst.numel === 0) return;
-  const s = src.isContiguous() && src.dtype === dst.dtype ? materialize(src) : contiguous(src, dst.dtype);
-  const isz = ITEMSIZE[dst.dtype];
-  let k = dst.shape.length;
-  let inner = 1;
-  while (k > 0 && (dst.strides[k - 1] === inner || dst.shape[k - 1] === 1)) {
-    inner *= dst.shape[k - 1];
-    k -= 1;
-  }
-  const outer = dst.shape.slice(0, k);
-  const idx = outer.map(() => 0);
-  const runs = numelOf(outer);
-  for (let n = 0; n < runs; ++n) {
-    let off = dst.offset;
-    for (let i = 0; i < k; ++i) off += idx[i] * dst.strides[i];
-    addon.memcpyD2D(dst.storage.ptr + BigInt(off * isz), s.ptr + BigInt(n * inner * isz), inner * isz);
-    for (let i = k - 1; i >= 0; --i) {
-      idx[i] += 1;
-      if (idx[i] < outer[i]) break;
-      idx[i] = 0;
-    }
-  }
-  s.dispose();
-}
-
-function zeros(out: HipTensorHandle): void {
-  fill(out, 0);
 }
 
 const GEMV_PROLOGUE: { [name: string]: number } = { none: 0, rms_norm: 1, silu_mul: 2, silu_mul_interleaved: 3 };
@@ -716,16 +930,6 @@ function sample(logits: HipTensorHandle, params: { [key: string]: any }): void {
                ptrOf(opt('displayIds')), ptrOf(opt('displayProbs')));
 }
 
-// copy / contiguous / cast (CopyKernelImpl: (input, options) => handle).
-function copyKernel(input: HipTensorHandle, options: { [key: string]: any }): HipTensorHandle {
-  return contiguous(input, options && options.dtype ? (options.dtype as DType) : undefined);
-}
-
-function fill(out: HipTensorHandle, value: number): void {
-  if (!out.isContiguous()) throw new Error('fill: contiguous output expected');
-  addon.fill(out.ptr, out.numel, value, out.kh);
-}
-
 // ---------------------------------------------------------------------------------------------
 // The backend (backend-webgpu/src/index.ts:15-87 surface)
 // ---------------------------------------------------------------------------------------------
@@ -793,21 +997,27 @@ export function registerHipKernels(reg: SimpleOperatorRegistry): void {
   reg.register('sdpa_masked', sdpaMasked);
   reg.register('rms_norm', rmsNorm);
   for (const name of ['matmul', 'mm', 'bmm', 'addmm', 'baddbmm']) reg.register(name, matmul);
-  reg.register('add', binaryKernel('add'));
-  reg.register('mul', binaryKernel('mul'));
-  reg.register('sub', binaryKernel('sub'));
-  reg.register('silu', silu);
-  for (const name of ['neg', 'cos', 'sin']) reg.register(name, unaryKernel(name));
-  reg.register('arange', arange);
+  // Iterator kernels, (iter: ITensorIterator) => void with broadcast / strided operands
+  // (register.ts:9; pointwise ops.ts:168-437, copy/index.ts:13-33, factory/index.ts:27-29,
+  // reduction/index.ts:20-22): the output is iter.output().tensorHandle.
+  reg.register('add', mapKernel('add', MAP.add, 2, alphaOf));
+  reg.register('sub', mapKernel('sub', MAP.sub, 2, alphaOf));
+  reg.register('mul', mapKernel('mul', MAP.mul, 2));
+  reg.register('div', mapKernel('div', MAP.div, 2));
+  for (const name of ['neg', 'cos', 'sin', 'silu']) reg.register(name, mapKernel(name, (MAP as any)[name], 1));
+  for (const name of ['copy', 'cast', 'contiguous', 'clone', 'copy_']) reg.register(name, mapKernel(name, MAP.copy, 1));
+  reg.register('zeros', mapKernel('zeros', MAP.fill, 0, () => [0, 0]));
+  reg.register('ones', mapKernel('ones', MAP.fill, 0, () => [1, 0]));
+  reg.register('full', mapKernel('full', MAP.fill, 0, (sc: { [key: string]: any }) =>
+    [Number(sc.fill_value !== undefined ? sc.fill_value : sc.fillValue), 0]));
+  reg.register('empty', (_iter: TensorIterator): void => undefined);
+  reg.register('arange', mapKernel('arange', MAP.arange, 0, (sc: { [key: string]: any }) =>
+    [sc.start === undefined ? 0 : Number(sc.start), sc.step === undefined ? 1 : Number(sc.step)]));
+  reg.register('argmax', argmaxKernel);
   reg.register('decode_attention', decodeAttention);
   reg.register('rms_norm_rope', rmsNormRope);
   reg.register('silu_mul', siluMul);
   reg.register('index_select', indexSelect);
-  reg.register('argmax', argmax);
-  for (const name of ['copy', 'contiguous', 'cast']) reg.register(name, copyKernel);
-  reg.register('copy_', copyInto);
-  reg.register('fill', fill);
-  reg.register('zeros', zeros);
   reg.register('gemv_fused', gemvFused);
   reg.register('gemv_swiglu', gemvSwiglu);
   reg.register('linear_swiglu', linearSwiglu);

@@ -27,7 +27,10 @@
 // bf16 at each store: the fastest path).
 
 const fs = require('fs');
+const path = require('path');
 const { performance } = require('perf_hooks');  // wall times in ms, sub-millisecond resolution
+// the iterators Kandle's dispatcher builds for the factory, copy and reduction kernels
+const { HipTensorIterator } = require(path.join(__dirname, 'index.js'));
 
 export interface Qwen3Config {
   vocabSize: number;
@@ -200,8 +203,7 @@ export class Qwen3ForCausalLM {
       // zero-filled as StaticKVCache's (kv-cache.ts:106-131): the decode block reads the row it is
       // about to write with a zero weight, which must not meet a NaN bit pattern
       const last = this.layers[this.layers.length - 1];
-      this.ops.find('zeros')(last.kCache);
-      this.ops.find('zeros')(last.vCache);
+      for (const c of [last.kCache, last.vCache]) this.ops.find('zeros')(HipTensorIterator.nullaryOp(c.shape, c.dtype, c));
     }
     // RotaryEmbedding._computeInvFreqDirect (rope.ts:159-171): 1 / theta^(i / (D/2)) in float64,
     // stored as float32.
@@ -373,7 +375,7 @@ export class Qwen3ForCausalLM {
     const logits = be.createTensorHandle([1, cfg.vocabSize], 'float32');
     ops.find('gemv_fused')('rms_norm', x, this.embed, logits, { normWeight: this.finalNorm, eps, actDtype: act });
     x.dispose();
-    ops.find('argmax')(logits, token);
+    ops.find('argmax')(HipTensorIterator.reductionOp(logits, [-1], false, token));
     ops.find('greedy_advance')(token, pos, lens, log, base);
     return logits;
   }
@@ -399,10 +401,10 @@ export class Qwen3ForCausalLM {
     if (returnLogits) logits.push((await first.dataAsync()) as Float32Array);
     const token = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array(1) });
     const log = be.createTensorHandle({ shape: [N + 1], dtype: 'int32', data: new Int32Array(N + 1) });
-    this.ops.find('argmax')(first, token);
+    this.ops.find('argmax')(HipTensorIterator.reductionOp(first, [-1], false, token));
     if (pre.owned) first.dispose();
     const head = this.view(log, [1], [1], 0);
-    this.ops.find('copy_')(head, token);
+    this.ops.find('copy_')(HipTensorIterator.unaryOp(token, head));
     head.dispose();
     const pos = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P]) });
     const lens = be.createTensorHandle({ shape: [1], dtype: 'int32', data: new Int32Array([P + 1]) });

@@ -8,7 +8,8 @@
  *     declarations and class fields, where T is a union of names with type arguments and array
  *     suffixes, string literals, object types `{ ... }` or parenthesised types;
  *   - `x as T` casts, type arguments `name<...>(`, and the modifiers private / public / protected /
- *     readonly, and the type parameters of `class Name<T>`;
+ *     readonly, the type operator `readonly T[]`, the type parameters of `class Name<T>` and its
+ *     `implements A, B` clause;
  *   - `export` on classes, functions, `const` and `export { ... }` lists (collected into
  *     module.exports).
  * Strings, template literals and comments are copied untouched.  Anything outside the subset is
@@ -71,14 +72,17 @@ function typeEnd(s, i) {
     else if (s[j] === "'" || s[j] === '"') j = skipNonCode(s, j);
     else {
       const m = /^[A-Za-z_$][\w$.]*/.exec(s.slice(j));
-      if (!m) throw new Error(`strip-types: no type at ${j}: ${s.slice(j, j + 30)}`);
+      if (!m) throw new Error(`strip-types: no type at ${j}: ${s.slice(Math.max(0, j - 60), j + 30)}`);
       j += m[0].length;
+      // `readonly T[]`: the operator, then the type it applies to
+      if (m[0] === 'readonly' && /\s/.test(s[j])) { j = skipSpace(s, j); continue; }
       if (s[j] === '<') j = matchClose(s, j) + 1;
     }
     while (s[j] === '[' && s[j + 1] === ']') j += 2;
     const k = skipSpace(s, j);
     if ((s[k] === '|' && s[k + 1] !== '|') || (s[k] === '&' && s[k + 1] !== '&')) { j = skipSpace(s, k + 1); continue; }
-    if (s[k] === '=' && s[k + 1] === '>' && s[skipSpace(s, i)] === '(') { j = typeEnd(s, k + 2); continue; }
+    // a function type `(a: T) => R`: its return type ends the type
+    if (s[k] === '=' && s[k + 1] === '>' && s[skipSpace(s, i)] === '(') return typeEnd(s, k + 2);
     return j;
   }
 }
@@ -145,6 +149,15 @@ function stripExpr(t) {
     if (m && !/[\w$]/.test(t[i - 1] || '')) {
       out += m[0].slice(0, -1);
       i = typeEnd(t, i + m[0].length);
+      continue;
+    }
+    // `class Name<T> extends Base<U> implements A, B {`: type parameters, type arguments and the
+    // implements clause go
+    m = /^(class\s+[A-Za-z_$][\w$]*)(\s*<[^{]*?>)?(\s+extends\s+[A-Za-z_$][\w$.]*)?(\s*<[^{]*?>)?\s+implements\s+[^{]*\{/
+      .exec(t.slice(i));
+    if (m && !/[\w$]/.test(t[i - 1] || '')) {
+      out += m[1] + (m[3] || '') + ' {';
+      i += m[0].length;
       continue;
     }
     // type parameters of a class: `class Name<T, U>`

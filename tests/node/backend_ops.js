@@ -11,7 +11,8 @@
  */
 const fs = require('fs');
 const path = require('path');
-const { HipBackend } = require(path.join(__dirname, '..', '..', 'packages', 'backend-hip', 'dist', 'index.js'));
+const { HipBackend, HipTensorIterator } = require(path.join(__dirname, '..', '..', 'packages', 'backend-hip', 'dist',
+                                                             'index.js'));
 
 const dir = process.argv[2];
 const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
@@ -30,6 +31,13 @@ function readI32(name) {
 }
 function write(name, arr) {
   fs.writeFileSync(path.join(dir, name), Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
+}
+
+// full(fill_value) into an existing handle: the nullary iterator of handlers/factory.ts:50-61
+function fullIter(h, value) {
+  const it = HipTensorIterator.nullaryOp(h.shape, h.dtype, h);
+  it.setScalarArgs({ fill_value: value });
+  return it;
 }
 
 async function main() {
@@ -73,7 +81,7 @@ async function main() {
   // silu_mul, and the iterator kernels silu / mul on a strided (transposed) view
   const g = t([m.M, m.N], 'float32', readF32('mc'));
   const u = backend.createTensorHandle({ shape: [m.M, m.N], dtype: 'float32' });
-  ops.find('fill')(u, 0.5);
+  ops.find('full')(fullIter(u, 0.5));
   const h = backend.createTensorHandle([m.M, m.N], 'float32');
   ops.find('silu_mul')(g, u, h);
   write('sm', await h.dataAsync());
@@ -95,7 +103,7 @@ async function main() {
   ops.find('index_select')(table, ids, { dim: 0 }, rows);
   write('eo', await rows.dataAsync());
   const am = backend.createTensorHandle([m.M], 'int32');
-  ops.find('argmax')(c, am);
+  ops.find('argmax')(HipTensorIterator.reductionOp(c, [-1], false, am));
   write('am', await am.dataAsync());
 
   // neg / cos / sin (the composite RoPE's iterator kernels) and arange
@@ -106,7 +114,9 @@ async function main() {
     write('u_' + name, await un[name].dataAsync());
   }
   const ar = backend.createTensorHandle([10], 'float32');
-  ops.find('arange')(ar, 0.5, 2);
+  const arIt = HipTensorIterator.nullaryOp([10], 'float32', ar);
+  arIt.setScalarArgs({ start: 0.5, end: 20.5, step: 2 });
+  ops.find('arange')(arIt);
   write('ar', await ar.dataAsync());
 
   // rms_norm_rope into whole KV caches at device positions (the decode-step cache write)
@@ -120,8 +130,8 @@ async function main() {
   const pos = t([p.T], 'int32', readI32('rpos'));
   const kc = backend.createTensorHandle([1, p.Hkv, p.L, p.D], 'bfloat16');
   const vc = backend.createTensorHandle([1, p.Hkv, p.L, p.D], 'bfloat16');
-  ops.find('fill')(kc, 7);
-  ops.find('fill')(vc, 7);
+  ops.find('full')(fullIter(kc, 7));
+  ops.find('full')(fullIter(vc, 7));
   const qk = ops.find('rms_norm_rope')(rq, rk, { qWeight: wq, kWeight: wk, invFreq: inv, positions: pos, eps: p.eps,
                                                  kOut: kc, v: rv, vOut: vc, cachePositions: true });
   write('rqo', await qk[0].dataAsync());
@@ -220,10 +230,10 @@ async function main() {
   const cview = backend.createTensorHandle({ storage: cbuf.storage, shape: [4, 3], dtype: 'float32', strides: [8, 1],
                                               offset: 2 });
   const csrc = t([4, 3], 'float32', readF32('cps'));
-  ops.find('copy_')(cview, csrc);
+  ops.find('copy_')(HipTensorIterator.unaryOp(csrc, cview));
   write('cpo', await cbuf.dataAsync());
   const zt = t([10], 'float32', new Float32Array(10).fill(1));
-  ops.find('zeros')(zt);
+  ops.find('zeros')(HipTensorIterator.nullaryOp(zt.shape, zt.dtype, zt));
   const zsum = Array.from(await zt.dataAsync()).reduce((p2, q2) => p2 + Math.abs(q2), 0);
 
   for (const hnd of [q, k, v, o, mask, om, x, w, y, a, b, c, out, g, u, h, gT, s1, prod, table, ids, rows, am,

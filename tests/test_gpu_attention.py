@@ -254,8 +254,10 @@ def test_decode_c4_full_size(hip):
 def test_flash_c3_full_size(hip):
     """Config C3 at full size (B=4, Hq=16, Hkv=8, S=4096, D=128, causal, bf16): every row of two
     whole (batch, head) slices (the first and the last, 4096 query rows each, every causal key
-    range), the last 128-row query block of every one of the 64 heads, and 48 sampled rows, each
-    against the oracle on the same inputs."""
+    range), the last 128-row query block of every one of the 64 heads, one row of every
+    (batch, head, 128-row query block) -- 2048 rows, so every work item of the persistent kernel's
+    schedule and both heads of each kv pair are checked, at a row offset that moves through the
+    block's wave slots -- and 48 sampled rows, each against the oracle on the same inputs."""
     B, Hq, Hkv, S, D = 4, 16, 8, 4096, 128
     q, qh = seeded(91, (B, Hq, S, D), "bfloat16")
     k, kh = seeded(92, (B, Hkv, S, D), "bfloat16")
@@ -278,6 +280,19 @@ def test_flash_c3_full_size(hip):
     err = float(np.max(np.abs(out[:, :, S - tail:] - ref)))
     worst = max(worst, err)
     assert err < BF16_ATOL, ("last block", err)
+    # one row per (b, h, 128-row block): row blk * 128 + (7 blk + 5 h + 3 b) mod 128, the causal
+    # limit of each row as an explicit -inf mask
+    nblk = S // 128
+    for b in range(B):
+        for h in range(Hq):
+            hk = h // G
+            rows_bh = np.array([blk * 128 + (7 * blk + 5 * h + 3 * b) % 128 for blk in range(nblk)])
+            bmask = np.where(np.arange(S)[None, :] > rows_bh[:, None], -np.inf, 0.0).astype(np.float32)
+            ref = oracle.sdpa_masked(qh[b:b + 1, h:h + 1, rows_bh], kh[b:b + 1, hk:hk + 1],
+                                     vh[b:b + 1, hk:hk + 1], bmask)
+            err = float(np.max(np.abs(out[b, h, rows_bh] - ref[0, 0])))
+            worst = max(worst, err)
+            assert err < BF16_ATOL, ("block rows", b, h, err)
     r = np.random.default_rng(7)
     rows = [(0, 0, 0), (3, 15, S - 1), (1, 7, 4095), (2, 8, 1)] + [
         (int(r.integers(B)), int(r.integers(Hq)), int(r.integers(S))) for _ in range(44)]

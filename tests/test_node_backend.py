@@ -44,11 +44,13 @@ def test_backend_source_strips_to_loadable_javascript(tmp_path):
     res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, res.stderr
     r = json.loads(res.stdout.strip().splitlines()[-1])
-    assert {"HipBackend", "HipStorage", "HipTensorHandle", "SimpleOperatorRegistry", "registerHipKernels"} <= set(r["exports"])
+    assert {"HipBackend", "HipStorage", "HipTensorHandle", "HipTensorIterator", "SimpleOperatorRegistry",
+            "registerHipKernels"} <= set(r["exports"])
     for name in ("flash_attention", "sdpa_masked", "rms_norm", "matmul", "mm", "bmm", "addmm", "baddbmm", "add",
-                 "mul", "sub", "silu", "silu_mul", "index_select", "argmax", "copy", "contiguous", "cast", "fill", "neg",
-                 "cos", "sin", "arange", "decode_attention", "rms_norm_rope", "copy_", "zeros", "gemv_fused", "gemv_swiglu",
-                 "linear_swiglu", "linear_qk_norm_rope", "linear_add_rms_norm", "decode_attention_block", "greedy_advance", "sample"):
+                 "mul", "sub", "div", "silu", "silu_mul", "index_select", "argmax", "copy", "contiguous", "cast", "clone",
+                 "copy_", "zeros", "ones", "full", "empty", "neg", "cos", "sin", "arange", "decode_attention",
+                 "rms_norm_rope", "gemv_fused", "gemv_swiglu", "linear_swiglu", "linear_qk_norm_rope",
+                 "linear_add_rms_norm", "decode_attention_block", "greedy_advance", "sample"):
         assert name in r["names"], name
     assert r["strides"] == [12, 4, 1]
     assert r["bf16"] == [0x3F80, 0xC020, 0x4049, 0x4780]   # RNE: 3.14159 -> 0x4049, 65504 -> 65536
@@ -65,7 +67,10 @@ interface Box {
 export interface Wide<T> {
   items: T[];
 }
-export class Counter<T> {
+interface Named {
+  name: string;
+}
+export class Counter<T> implements Named {
   private count: number = 0;
   readonly name: string;
   items: Map<string, number> = new Map<string, number>();
@@ -94,6 +99,11 @@ export function pick(flag: boolean, a?: number, ...rest: number[]): number | und
   return t.length > 100 ? undefined : v + obj.x;
 }
 export const twice = (x: number): number => x * 2;
+export function longest(xs: readonly (readonly number[])[], f?: (sc: { [k: string]: any }) => number[]): number {
+  let best = 0;
+  for (const x of xs) best = Math.max(best, x.length);
+  return f === undefined ? best : best + f({ k: 1 })[0];
+}
 export function wrapped(n: number): number {
   const o = { first: n, second: 2,
               third: 3 };
@@ -111,7 +121,8 @@ def test_type_stripper_handles_each_construct(tmp_path):
     out = tmp_path / "snippet.js"
     _strip(src, out)
     js = out.read_text()
-    for leftover in ("interface", "type Pair", "type Fn", ": number", "private", "readonly", " as ", "<string"):
+    for leftover in ("interface", "implements", "type Pair", "type Fn", ": number", "private", "readonly", " as ",
+                     "<string"):
         assert leftover not in js, (leftover, js)
     script = f"""
       const m = require({json.dumps(str(out))});
@@ -120,12 +131,13 @@ def test_type_stripper_handles_each_construct(tmp_path):
       console.log(JSON.stringify({{total: c.total, name: c.name, size: c.items.size,
                                   p1: m.pick(true, 7), p2: m.pick(false), p3: m.pick(true, 1, 2, 3),
                                   tw: m.twice(21), lt: m.lessThan(1, 2), wr: m.wrapped(1),
+                                  lg: m.longest([[1, 2], [3]]), lg2: m.longest([[1]], (o) => [o.k + 1]),
                                   keys: Object.keys(m).sort()}}));"""
     res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, (res.stderr, js)
     r = json.loads(res.stdout.strip().splitlines()[-1])
     assert r == {"total": 5, "name": "k", "size": 0, "p1": 8, "p2": 4, "p3": 5, "tw": 42, "lt": True, "wr": 6,
-                 "keys": ["Counter", "lessThan", "pick", "twice", "wrapped"]}
+                 "lg": 2, "lg2": 3, "keys": ["Counter", "lessThan", "longest", "pick", "twice", "wrapped"]}
 
 
 def test_typescript_safetensors_reader(tmp_path):
