@@ -56,6 +56,12 @@ const char* kh_last_error(void);
  * The reference's knownIssues/shader.md:151-175 proposes the same per-dispatch check for WGSL. */
 int kh_set_debug(int flags);
 
+/* 1 while a graph capture (kh_graph_begin_capture) is open on the library stream, else 0.  Host
+ * code that reads device memory after a kernel (debug mode's NaN/Inf scan) skips the read then:
+ * the runtime refuses copies into a stream under capture.  No counterpart in the reference (WebGPU
+ * has no graph capture). */
+int kh_is_capturing(void);
+
 /* Caching device allocator (size classes, stream-ordered reuse on the single library stream).
  * Replaces WebGPUStorage's GPUBuffer creation/destroy and its buffer pooling
  * (reference: packages/backend-webgpu/src/base/storage.ts:68-106, :114-143). */

@@ -35,6 +35,7 @@ SIGNATURES = {
     "kh_init": [_i],
     "kh_device_count": [C.POINTER(C.c_int)],
     "kh_set_debug": [_i],
+    "kh_is_capturing": [],
     "kh_alloc": [C.POINTER(C.c_void_p), _sz],
     "kh_free": [_vp],
     "kh_empty_cache": [],
@@ -118,6 +119,11 @@ def check(rc: int, what: str = "") -> None:
 def call(name: str, *args) -> None:
     """Call an entry point and raise on a non-zero return code."""
     check(getattr(load(), name)(*args), name)
+
+
+def is_capturing() -> bool:
+    """True while a graph capture is open on the library stream (kh_is_capturing)."""
+    return bool(load().kh_is_capturing())
 
 
 def i64_array(values) -> C.Array:

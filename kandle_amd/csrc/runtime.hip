@@ -254,6 +254,8 @@ int kh_set_debug(int flags) {
   return KH_OK;
 }
 
+int kh_is_capturing(void) { return g_state.capturing != nullptr ? 1 : 0; }
+
 int kh_alloc(void** ptr, size_t bytes) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(ptr != nullptr, "kh_alloc: null output pointer");

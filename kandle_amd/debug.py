@@ -5,6 +5,8 @@ reports a device fault at the call that launched it) and wraps every kernel regi
 backend so that, after it returns, its floating-point outputs are copied to the host and checked
 for NaN/Inf; the first kernel producing one raises KandleHipError naming it.  disable() restores
 both.  It costs a synchronisation and a readback per kernel: a debugging aid, not for timing.
+Kernels recorded into a HIP graph (generate(use_graph=True)) are not scanned: while the capture is
+open they have not run, and a replay launches the whole graph without calling the host wrappers.
 The reference proposes the same per-dispatch check (knownIssues/shader.md:151-175); its kernels
 run asynchronously on WebGPU and a fault or a NaN surfaces only at the next readback.
 """
@@ -49,7 +51,9 @@ def _outputs(name: str, args, kwargs, ret):
 def _wrap(name: str, fn: Callable) -> Callable:
     def checked(*args, **kwargs):
         ret = fn(*args, **kwargs)
-        if _state["check_finite"]:
+        # under graph capture the kernels are only recorded: nothing has run and the runtime
+        # refuses the readback, so the scan is skipped (replays are not scanned)
+        if _state["check_finite"] and not _lib.is_capturing():
             for o in _outputs(name, args, kwargs, ret):
                 vals = o.data_async()
                 if not np.all(np.isfinite(vals)):

@@ -19,6 +19,7 @@ memory map, and copied to the device without a host-side conversion.
 from __future__ import annotations
 
 import json
+import math
 import mmap
 import os
 import struct
@@ -78,7 +79,7 @@ def _tensor_entry(name: str, entry, data_size: int):
     if not (isinstance(offs, list) and len(offs) == 2 and all(isinstance(o, int) and o >= 0 for o in offs)):
         raise ValueError(f"safetensors: tensor {name!r} has data_offsets {offs!r}; they are [begin, end] byte offsets")
     begin, end = offs
-    need = int(np.prod(shape, dtype=np.int64)) * SAFETENSORS_DTYPES[st][0]
+    need = math.prod(shape) * SAFETENSORS_DTYPES[st][0]      # Python ints: no wrap on hostile shapes
     if end - begin != need:
         raise ValueError(f"safetensors: tensor {name!r} ({st}, shape {tuple(shape)}) needs {need} bytes but its "
                          f"data_offsets span {end - begin}")
@@ -161,7 +162,11 @@ def parse_safetensor_file(path: str) -> SafetensorFile:
         raise ValueError(f"safetensors: the header is not valid UTF-8 JSON ({e})") from None
     if not isinstance(header, dict):
         raise ValueError(f"safetensors: the header is JSON {type(header).__name__}, not an object")
-    meta = header.pop("__metadata__", None) or {}
+    meta = header.pop("__metadata__", None)
+    if meta is None:
+        meta = {}
+    if not isinstance(meta, dict) or not all(isinstance(v, str) for v in meta.values()):
+        raise ValueError("safetensors: __metadata__ must be an object mapping strings to strings")
     f = SafetensorFile(path=path, metadata={str(k): str(v) for k, v in meta.items()},
                        data_offset=_LEN_FIELD.size + n)
     data_size = file_size - f.data_offset

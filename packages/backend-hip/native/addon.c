@@ -255,6 +255,13 @@ static napi_value js_deviceCount(napi_env env, napi_callback_info info) {
   return out;
 }
 
+static napi_value js_isCapturing(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value out;
+  napi_get_boolean(env, kh_is_capturing() != 0, &out);
+  return out;
+}
+
 static napi_value js_lastError(napi_env env, napi_callback_info info) {
   (void)info;
   napi_value out;
@@ -282,8 +289,13 @@ FN(free, 1) void* p = arg_ptr(A, 0); CALL(kh_free(p))
    freeOwned(ext) returns it to the allocator (once; later calls do nothing), and the object's
    finalizer -- run by the garbage collector after the object becomes unreachable -- returns a
    block that was never freed: the safety net of a storage whose dispose() was forgotten (Node 12
-   has no FinalizationRegistry).  ownedPtr(ext) is the block's address as a BigInt. */
+   has no FinalizationRegistry).  ownedPtr(ext) is the block's address as a BigInt.
+   An external made elsewhere (another addon) is told apart by the tag and the self pointer
+   written at creation: Node 12 has no napi_type_tag_object. */
+#define OWNED_TAG 0x6b68426c6f636b31ULL /* "khBlock1" */
 typedef struct {
+  uint64_t tag;
+  const void* self;
   void* p;
   int live;
 } Owned;
@@ -293,12 +305,14 @@ static void owned_finalize(napi_env env, void* data, void* hint) {
   (void)hint;
   Owned* o = (Owned*)data;
   if (o->live) kh_free(o->p);
+  o->tag = 0;
   free(o);
 }
 
 static Owned* arg_owned(Args* A, size_t i) {
   void* d = NULL;
-  if (type_of(A, i) != napi_external || napi_get_value_external(A->env, A->v[i], &d) != napi_ok || d == NULL) {
+  if (type_of(A, i) != napi_external || napi_get_value_external(A->env, A->v[i], &d) != napi_ok || d == NULL ||
+      ((Owned*)d)->tag != OWNED_TAG || ((Owned*)d)->self != d) {
     type_error(A, i, "an owned block (from allocOwned)");
     return NULL;
   }
@@ -324,6 +338,8 @@ static napi_value js_allocOwned(napi_env env, napi_callback_info info) {
     napi_throw_error(env, NULL, "kandle_hip.allocOwned: out of host memory");
     return NULL;
   }
+  o->tag = OWNED_TAG;
+  o->self = o;
   o->p = p;
   o->live = 1;
   if (napi_create_external(env, o, owned_finalize, NULL, &ext) != napi_ok) {
@@ -655,7 +671,7 @@ FN(gemvSwiglu, 10)
 
 static napi_value module_init(napi_env env, napi_value exports) {
   napi_property_descriptor d[] = {
-      EXPORT(init), EXPORT(deviceCount), EXPORT(lastError), EXPORT(setDebug), EXPORT(alloc), EXPORT(free), EXPORT(emptyCache),
+      EXPORT(init), EXPORT(deviceCount), EXPORT(lastError), EXPORT(setDebug), EXPORT(isCapturing), EXPORT(alloc), EXPORT(free), EXPORT(emptyCache),
       EXPORT(allocOwned), EXPORT(ownedPtr), EXPORT(freeOwned),
       EXPORT(allocStats), EXPORT(memcpyH2D), EXPORT(memcpyD2H), EXPORT(memcpyD2D), EXPORT(synchronize),
       EXPORT(eventCreate), EXPORT(eventDestroy), EXPORT(eventRecord), EXPORT(eventElapsedMs),

@@ -36,3 +36,29 @@ def test_debug_mode_flags_non_finite_outputs(hip):
     vb2 = Tensor(bad, dtype="bfloat16")
     out = F.scaled_dot_product_attention(q, k, vb2, is_causal=True).numpy()
     assert np.isnan(out).any()
+
+
+def test_debug_mode_with_graph_capture(hip):
+    """Debug mode with generate(use_graph=True): the kernels recorded while the prefill and decode
+    graphs are captured are not scanned (they have not run; the runtime refuses a readback into a
+    capturing stream), and the tokens and logits equal those of an eager generation with debug mode
+    off."""
+    from kandle_amd import synthetic as syn
+    from kandle_amd.model_utils import Qwen3Config, Qwen3ForCausalLM, init_qwen3_weights
+
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
+    w = init_qwen3_weights(cfg, seed=5)
+    prompt = syn.randint(6, (24,), 0, cfg.vocab_size)
+    model = Qwen3ForCausalLM(cfg, w, max_seq_len=48)
+    try:
+        debug.enable()
+        try:
+            toks, log = model.generate(prompt, 4, return_logits=True, use_graph=True)   # captures both graphs
+        finally:
+            debug.disable()
+        ref_toks, ref_log = model.generate(prompt, 4, return_logits=True, use_graph=False)
+    finally:
+        model.dispose()
+    assert toks == ref_toks
+    for a, b in zip(log, ref_log):
+        assert np.array_equal(a, b)

@@ -121,10 +121,10 @@ def test_linear_bf16(hip, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(512, 1024, 3072), (100, 520, 2048)])
 def test_linear_split_k_residual_deterministic(hip, M, N, K):
-    """Few output tiles and a long K: workgroups split K and the last one of each tile to arrive adds
-    the partials in split order -- fp32 output with the residual added in place; bit-identical
-    results over four runs (the arrival order differs from run to run), with another split GEMM of
-    a different tile count between them (the per-tile arrival counters must be back at zero)."""
+    """Few output tiles and a long K: workgroups split K and write fp32 partials, and a second
+    kernel adds them in split order to the residual in place -- bit-identical results over four
+    runs, with another split GEMM of a different tile count between them (the partial buffer is
+    reused with another layout)."""
     x, xh = seeded(245, (M, K), "bfloat16")
     w, wh = seeded(246, (N, K), "bfloat16", std=0.02)
     x2, _ = seeded(248, (64, 2048), "bfloat16")

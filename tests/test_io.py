@@ -96,6 +96,15 @@ def test_header_checks(tmp_path):
     _raw_file(p, b"[1, 2]")
     with pytest.raises(ValueError, match="not an object"):
         parse_safetensor_file(p)
+    # hostile shapes: a product past 2^64 (no int64 wrap to 0 bytes), a dim past 2^63
+    for shape in ([2 ** 62, 4], [2 ** 64 + 1]):
+        _raw_file(p, json.dumps({"w": {"dtype": "F32", "shape": shape, "data_offsets": [0, 0]}}).encode())
+        with pytest.raises(ValueError, match="needs"):
+            parse_safetensor_file(p)
+    for meta in ([1, 2], "text", {"k": 3}):
+        _raw_file(p, json.dumps({"__metadata__": meta}).encode())
+        with pytest.raises(ValueError, match="__metadata__ must be an object"):
+            parse_safetensor_file(p)
     # entries that describe no tensor (no data_offsets) are skipped, as in the reference
     hdr = json.dumps({"__metadata__": {"k": "v"}, "junk": 3, "w": {"dtype": "I32", "shape": [], "data_offsets": [0, 4]}}).encode()
     _raw_file(p, hdr, struct.pack("<i", -5))

@@ -54,6 +54,9 @@ def test_addon_errors_and_device_count():
       try {{ a.flashAttention(1n, 2n); }} catch (e) {{ res.arity = [e.constructor.name, e.message]; }}
       try {{ a.fill('x', 1, 0, 0); }} catch (e) {{ res.type = [e.constructor.name, e.message]; }}
       try {{ a.copyStrided(0n, 0, 0n, [1, 2, 3, 4, 5, 6, 7], [1], 0, 0); }} catch (e) {{ res.list = e.message; }}
+      // freeOwned / ownedPtr take only blocks from allocOwned
+      try {{ a.freeOwned({{}}); }} catch (e) {{ res.owned = [e.constructor.name, e.message]; }}
+      res.capturing = a.isCapturing();
       // the longest bindings: every argument reaches the C call (which then reports the missing
       // init), and surplus arguments past the binding's capacity are ignored, never read
       const qknr = [16n, 8, 32n, 8, 1, 4, 8, 1, 1, 128, 48n, 64n, 80n, 96n, 112n, 128n, 144n,
@@ -71,6 +74,8 @@ def test_addon_errors_and_device_count():
     assert r["arity"] == ["TypeError", "kandle_hip.flashAttention: expected 14 arguments, got 2"]
     assert r["type"][0] == "TypeError" and "argument 0 must be a device pointer" in r["type"][1]
     assert "at most 6 extents" in r["list"]
+    assert r["owned"][0] == "TypeError" and "an owned block" in r["owned"][1]
+    assert r["capturing"] is False
     if r["n"] == 0:
         for key in ("long", "surplus", "ex"):
             assert r[key][0] == "Error" and "kh_init has not been called" in r[key][1], (key, r[key])
