@@ -576,10 +576,20 @@ def bench_vendor(steps):
             out[f"sdpa_{name}"] = {"ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
         except Exception as ex:  # a backend torch does not offer for these inputs
             out[f"sdpa_{name}"] = {"unavailable": str(ex)[:160]}
+    out["gemm_hipblaslt"] = _vendor_gemms(torch, dev, g, torch.bfloat16)
+    # the reference's own arithmetic: float32 activations times float32 weights (the bf16 weights
+    # widened on load), as torch.matmul runs it in float32
+    out["gemm_hipblaslt_f32"] = _vendor_gemms(torch, dev, g, torch.float32)
+    return out
+
+
+def _vendor_gemms(torch, dev, g, dtype):
+    """torch.matmul (hipBLASLt / rocBLAS) on the C5 prefill projection shapes in `dtype`: x [512, K]
+    times w [N, K] transposed, 20 calls captured in a graph and replayed 5 times."""
     gem = {}
     for name, N, K, _ in GEMM_SHAPES:
-        x = torch.randn(512, K, device=dev, dtype=torch.bfloat16, generator=g)
-        w = torch.randn(N, K, device=dev, dtype=torch.bfloat16, generator=g)
+        x = torch.randn(512, K, device=dev, dtype=dtype, generator=g)
+        w = torch.randn(N, K, device=dev, dtype=dtype, generator=g)
         s2 = torch.cuda.Stream()
         s2.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s2):
@@ -601,8 +611,8 @@ def bench_vendor(steps):
         us = e0.elapsed_time(e1) / 100 * 1e3
         gem[name] = {"us": round(us, 2), "TFLOP/s": round(2.0 * 512 * N * K / (us * 1e-6) / 1e12, 1)}
     gem["layer_us"] = round(sum(v["us"] for v in gem.values()), 2)
-    out["gemm_hipblaslt"] = gem
-    return out
+    gem["dtype"] = str(dtype).replace("torch.", "")
+    return gem
 
 
 def bench_sample(steps, warmup):

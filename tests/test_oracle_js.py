@@ -86,3 +86,57 @@ def test_js_qwen3_matches_numpy_oracle(tmp_path):
     assert scale > 0.1
     err = float(np.max(np.abs(got - want)))
     assert err < 1e-4 * scale, (err, scale)
+
+
+OPS = os.path.join(ROOT, "oracle", "js", "cpu_ops.js")
+OPS_DRIVER = r"""
+const fs = require('fs');
+const path = require('path');
+const ops = require(process.argv[1]);                    // node -e SCRIPT OPS DIR
+const dir = process.argv[2];
+const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
+const rd = (n) => { const b = fs.readFileSync(path.join(dir, n)); return new Float32Array(b.buffer, b.byteOffset, b.byteLength / 4); };
+const { T, H, D, N, eps, theta } = meta;
+const x = rd('x'), wx = rd('wx'), q = rd('q'), wq = rd('wq');
+const y = new Float32Array(T * N);
+ops.rmsNorm(x, 0, wx, y, 0, T, N, eps);
+const inv = ops.ropeInvFreq(D, theta);
+const tab = ops.ropeTables(Int32Array.from(meta.pos), inv, D);
+const qo = new Float32Array(T * H * D);
+ops.qkNormRope(q, wq, qo, T, H, D, tab, eps);
+fs.writeFileSync(path.join(dir, 'y'), Buffer.from(y.buffer));
+fs.writeFileSync(path.join(dir, 'qo'), Buffer.from(qo.buffer));
+fs.writeFileSync(path.join(dir, 'inv'), Buffer.from(inv.buffer));
+console.log('ok');
+"""
+
+
+def test_js_cpu_ops_match_c_oracle(tmp_path):
+    """oracle/js/cpu_ops.js (the C2 CPU baseline's RMSNorm and qk-norm + RoPE) at C2's head_dim 128
+    and hidden 1024 against the C oracle's or_rms_norm / or_rope_inv_freq / or_qk_norm_rope on the
+    same inputs: to float32 rounding (1e-5 of the output scale; positions up to 4000, so the angles
+    reach thousands of radians)."""
+    import oracle
+
+    if shutil.which("node") is None:
+        pytest.skip("node is not available")
+    T, H, D, N, eps, theta = 9, 3, 128, 1024, 1e-6, 1e6
+    x = syn.normal(31, (T, N), 3.0)
+    wx = syn.uniform(32, (N,), 0.5, 1.5)
+    q = syn.normal(33, (T, H, D), 2.0)
+    wq = syn.uniform(34, (D,), 0.5, 1.5)
+    pos = [0, 1, 2, 17, 255, 511, 1000, 2999, 4000]
+    for name, arr in (("x", x), ("wx", wx), ("q", q), ("wq", wq)):
+        np.ascontiguousarray(arr, np.float32).tofile(str(tmp_path / name))
+    (tmp_path / "meta.json").write_text(json.dumps({"T": T, "H": H, "D": D, "N": N, "eps": eps, "theta": theta,
+                                                    "pos": pos}))
+    out = subprocess.run(["node", "-e", OPS_DRIVER, OPS, str(tmp_path)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr[-2000:]
+    inv = np.fromfile(str(tmp_path / "inv"), np.float32)
+    assert np.array_equal(inv, oracle.rope_inv_freq(D, theta))
+    y = np.fromfile(str(tmp_path / "y"), np.float32).reshape(T, N)
+    ry = oracle.rms_norm(x, wx, eps)
+    assert float(np.max(np.abs(y - ry))) <= 1e-5 * float(np.max(np.abs(ry)))
+    qo = np.fromfile(str(tmp_path / "qo"), np.float32).reshape(T, H, D)
+    rq = oracle.qk_norm_rope(q, wq, np.array(pos, np.int32), inv, eps)
+    assert float(np.max(np.abs(qo - rq))) <= 1e-5 * float(np.max(np.abs(rq)))
