@@ -134,11 +134,16 @@ def prep_c1():
     def run(steps, warmup):
         fn = lambda: kernels.flash_attention(q.handle, k.handle, v.handle, o, scale, True)  # noqa: E731
         wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        # the same call in split-bf16 form (kh_flash_attention_split: three bf16 MFMAs per product,
+        # within about 2^-15 of the fp32 products), the float32-activation model's prefill attention
+        fs = lambda: kernels.flash_attention_split(q.handle, k.handle, v.handle, o, scale, True)  # noqa: E731
+        split_wall, split_dev = time_calls(fs, steps, warmup)
         for t in (q, k, v):
             t.dispose()
         o.dispose()
         flops = 4.0 * B * Hq * S * S * D / 2.0
-        return {"flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms}
+        return {"flops": flops, "wall_ms": wall_ms, "dev_ms": dev_ms, "split_wall_ms": split_wall,
+                "split_dev_ms": split_dev}
     return run
 
 
@@ -1090,6 +1095,15 @@ def main():
                       "GFLOP/s": round(gf, 1),
                       "roofline": {"bound": "mfma fp32", "achieved": round(gf / 1e3, 3), "peak": 157.3,
                                    "unit": "TFLOP/s", "frac": round(gf / 1e3 / 157.3, 4), "traffic": None}}
+        if "split_dev_ms" in c1:
+            sg = c1["flops"] / (c1["split_dev_ms"] * 1e-3) / 1e9
+            line["c1"]["split_bf16"] = {
+                "what": "the same call as kh_flash_attention_split: fp32 operands as bf16 hi + lo, three bf16 MFMAs "
+                        "per product (within about 2^-15 of the fp32 products)",
+                "ms": round(c1["split_dev_ms"], 4), "wall_ms": round(c1["split_wall_ms"], 4), "GFLOP/s": round(sg, 1),
+                "roofline": {"bound": "mfma bf16, 3 products per fp32 product", "achieved": round(3 * sg / 1e3, 2),
+                             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(3 * sg / 1e3 / PEAK_BF16_TFLOPS, 4), "traffic": None}}
         if "value" not in line:
             line.update({"value": round(gf, 1), "unit": "GFLOP/s", "ms_per_step": round(c1["wall_ms"], 4),
                          "config": {"workload": "C1 SDPA fp32"}})

@@ -290,14 +290,26 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out,
  * (query head h reads kv head h / (hq / hkv)); causal masks key j > query i (top-left aligned).
  * Shapes q [batch, hq, lq, d], k/v [batch, hkv, lk, d], o [batch, hq, lq, d]; `strides` holds 12
  * element strides: q (batch, head, seq), k (…), v (…), o (…); the d axis is contiguous.
- * bf16 with d == 64 or 128 runs the MFMA flash kernel; lq == 1 runs split-K decode; otherwise a
- * LDS-tiled fp32-math kernel (d <= 256).  Replaces the `flash_attention` kernel
+ * bf16 with d == 64 or 128 runs the MFMA flash kernel; fp32 with d in {32, 64, 96, 128} the fp32
+ * MFMA flash kernel; lq == 1 runs split-K decode; otherwise a LDS-tiled fp32-math kernel
+ * (d <= 256).  Replaces the `flash_attention` kernel
  * (reference signature packages/types/src/backend/register.ts:102-109; semantics
  * packages/backend-webgpu/src/kernels/attention/builder.ts:138-329; called from
  * packages/core/src/dispatch/handlers/composite.ts:312-316). */
 int kh_flash_attention(const void* q, const void* k, const void* v, void* o,
                        int batch, int hq, int hkv, int64_t lq, int64_t lk, int d,
                        const int64_t* strides, float scale, int causal, int dtype);
+
+/* kh_flash_attention for fp32 q / k / v / o in split-bf16 form: every fp32 operand value x is
+ * taken as hi = bf16(x) plus lo = bf16(x - hi) and every product as three bf16 MFMAs (hi*hi +
+ * hi*lo + lo*hi, fp32 accumulate), so S = Q K^T and O = P V are each within about 2^-15 relative
+ * of the fp32 products (l sums the fp32 P) at a sixth of the fp32 MFMA's cycles.  Taken for
+ * d == 128 (any GQA ratio), scale > 0, lq > 1, 16-byte aligned rows with strides in multiples of
+ * 4 elements; any other call runs kh_flash_attention's fp32 route.  Causal and not.  The float32-activation Qwen3 prefill's attention: the reference's f32 attention
+ * (packages/backend-webgpu/src/kernels/attention/builder.ts:138-329) within the error above. */
+int kh_flash_attention_split(const void* q, const void* k, const void* v, void* o,
+                             int batch, int hq, int hkv, int64_t lq, int64_t lk, int d,
+                             const int64_t* strides, float scale, int causal);
 
 /* Scaled dot-product attention with an explicit additive mask:
  * O = softmax(scale * Q K^T + mask) V, GQA as kh_flash_attention, no causal masking.  This is the

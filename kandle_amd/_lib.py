@@ -73,6 +73,7 @@ SIGNATURES = {
     "kh_unary": [_i, _vp, _vp, _i64, _i],
     "kh_arange": [_vp, _i64, C.c_double, C.c_double, _i],
     "kh_flash_attention": [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i64p, _f, _i, _i],
+    "kh_flash_attention_split": [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i64p, _f, _i],
     "kh_flash_attention_masked": [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i64p, _f, _vp, _i64p, _i, _i],
     "kh_decode_attention": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],
     "kh_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i64, _i64p, _f, _i],

@@ -46,4 +46,15 @@ bool flash_f32_supported(const void* q, const void* k, const void* v, const void
 int launch_flash_f32(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
                      int d, const AttnStrides& st, float scale, bool causal);
 
+// True when the split-bf16 fp32 kernel takes this fp32 call: head_dim 128 (any GQA ratio), scale >
+// 0, 16-byte aligned rows with strides in multiples of 4 elements below 2^31, per-head byte ranges
+// below 2^31.
+bool flash_split_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv, int64_t lq,
+                           int64_t lk, int d, const AttnStrides& st, float scale);
+
+// fp32 attention with each fp32 operand split into bf16 hi + lo and every product as three bf16
+// MFMAs (about 2^-15 relative of the fp32 products), causal or not, on the library stream.
+int launch_flash_split_f32(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq,
+                           int lk, const AttnStrides& st, float scale, bool causal);
+
 }  // namespace kh

@@ -823,6 +823,23 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
                         dtype);
 }
 
+int kh_flash_attention_split(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
+                             int64_t lq, int64_t lk, int d, const int64_t* strides, float scale, int causal) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(batch >= 0 && hq > 0 && hkv > 0 && lq >= 0 && lk >= 0 && d > 0, "kh_flash_attention_split: bad extents");
+  KH_REQUIRE(hq % hkv == 0, "kh_flash_attention_split: numHeadsQ (%d) must be divisible by numHeadsKV (%d)", hq,
+             hkv);
+  KH_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX, "kh_flash_attention_split: sequence too long");
+  if (batch == 0 || lq == 0) return KH_OK;
+  KH_REQUIRE(q && k && v && o && strides, "kh_flash_attention_split: null pointer");
+  KH_REQUIRE(lk > 0, "kh_flash_attention_split: the key sequence is empty (softmax over no keys is undefined)");
+  const AttnStrides st = load_strides(strides);
+  if (lq > 1 && flash_split_supported(q, k, v, o, hq, hkv, lq, lk, d, st, scale))
+    return launch_flash_split_f32(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, st, scale, causal != 0);
+  // outside the split kernel's shapes: the fp32 route of kh_flash_attention
+  return kh_flash_attention(q, k, v, o, batch, hq, hkv, lq, lk, d, strides, scale, causal, KH_F32);
+}
+
 int kh_flash_attention_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,
                               int64_t lq, int64_t lk, int d, const int64_t* strides, float scale, const void* mask,
                               const int64_t* mask_strides, int mask_dtype, int dtype) {

@@ -786,6 +786,272 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
   return KH_OK;
 }
 
+// =============================================================================================
+// fp32 attention in split-bf16 form (the float32-activation prefill).
+// =============================================================================================
+// Q, K, V and O are fp32, head_dim 128, any GQA ratio.  Every operand value x is carried as two
+// bf16 values, hi = bf16(x) and lo = bf16(x - hi) (x - hi is exact in fp32, and |x - hi - lo| <=
+// 2^-16 |x|), and every product as three v_mfma_f32_32x32x16_bf16 into one fp32 accumulator,
+// hi * hi + hi * lo + lo * hi (lo * lo, below 2^-16 of the product, is dropped): S^T = K Q^T and
+// O^T += V^T P^T each within about 2^-15 of the fp32 products, in 96 MFMA cycles per 16-wide
+// k-step where the fp32 MFMA takes 512.  P is split the same way after the exponential; l sums
+// the fp32 P.
+//
+// A workgroup is (batch, query head, 32-row query block) with four waves, one per SIMD; wave w
+// takes the block's 32-key chunks w, w + 4, w + 8, ... (causal: up to the block's last row), so
+// the longest block's chain is a quarter of its keys.  A chunk is used by one wave only, so a wave
+// loads its operands straight from memory into registers in the MFMA layouts and splits them
+// there -- the next chunk's K during the whole current chunk, the next V once PV has consumed the
+// current one -- with no LDS staging and no barrier:
+//  - K (the A operand of S^T): lane (r, g) reads key row swap23(r) of the chunk, columns
+//    16 c + 8 g .. + 7 -- 64 contiguous bytes of a row per lane pair and k-step.  swap23 (bits 2
+//    and 3 of the key index exchanged) makes accumulator registers j = 0..7 of lane group g hold
+//    keys 8 g + j and j = 8..15 keys 16 + 8 g + j - 8, the B-operand layout of the PV product.
+//  - V^T (the A operand of O^T): lane (r, g) needs V[16 kc + 8 g + e][32 dt + r], e = 0..7: one
+//    4-byte load per e, the 32 lanes of a group reading 128 contiguous bytes of one key row.
+// The four waves' (m, l, O) are merged through LDS at the end by wave 0, in wave order.  Softmax
+// as SoftmaxLog2 (the QK^T accumulators start at -m; the reference is raised when a lane's sum of
+// P exceeds kSumMax).
+// Measured and not kept: converting K and V once per call into bf16 hi / lo planes (V transposed)
+// in a separate launch, so that the attention loop only loads ready operands -- C1 13.3 -> 20.2 us
+// and C5's prefill 3.23 -> 3.42 ms: the extra dependent launch costs more than the conversion.
+constexpr int kSplitWaves = 4;
+using FL128 = Flash<128, 8, 128>;  // for its swap23 and 32-bit strides
+using SplitStrides = FL128::Strides32;
+
+// Four floats -> their bf16 hi parts and the bf16 of the remainders, as two 8-byte rows.
+__device__ __forceinline__ void split4(const uint4& x, uint2& hi, uint2& lo) {
+  const float a = __uint_as_float(x.x), b = __uint_as_float(x.y), c = __uint_as_float(x.z), d = __uint_as_float(x.w);
+  hi.x = pack_bf16x2(a, b);
+  hi.y = pack_bf16x2(c, d);
+  lo.x = pack_bf16x2(a - __uint_as_float(hi.x << 16), b - __uint_as_float(hi.x & 0xffff0000u));
+  lo.y = pack_bf16x2(c - __uint_as_float(hi.y << 16), d - __uint_as_float(hi.y & 0xffff0000u));
+}
+// Eight floats (as two loads) -> hi and lo bf16x8 operands.
+__device__ __forceinline__ void split8(const uint4& x0, const uint4& x1, bf16x8& hi, bf16x8& lo) {
+  uint2 h0, l0, h1, l1;
+  split4(x0, h0, l0);
+  split4(x1, h1, l1);
+  hi = __builtin_bit_cast(bf16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+  lo = __builtin_bit_cast(bf16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+}
+
+// One 32-key chunk's operands of one wave, as loaded: K rows (8 k-steps of two 16-byte loads) and
+// V^T elements (4 column tiles x 2 key steps x 8 keys).
+struct SplitK {
+  uint4 k[16];
+};
+struct SplitV {
+  uint32_t v[64];
+};
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V, float* __restrict__ O,
+    int hq, int ratio, int lq, int lk, SplitStrides st, float scale, int n_qblocks) {
+  constexpr int D = 128, NQ = D / 16, ND = D / 32;
+  __shared__ __attribute__((aligned(16))) float part[(kSplitWaves - 1) * 66 * 64];  // [wave - 1][66][lane]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, r = lane & 31, g = lane >> 5;
+  // Workgroups go to the 8 XCDs round-robin (workgroup i on XCD i % 8), each with its own L2.
+  // When the grid divides by 8, XCD x runs a contiguous range of logical blocks -- whole query
+  // heads, so a kv head's K / V are read into one L2 and reused there -- heaviest (last) query
+  // block of a head first.
+  int logical = blockIdx.x;
+  if (gridDim.x % kXcds == 0) logical = (blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
+  const int qblk = n_qblocks - 1 - logical % n_qblocks, bh = logical / n_qblocks;
+  const int b = bh / hq, h = bh % hq, hk = h / ratio;
+  const int q0 = qblk * 32, qi = q0 + r;
+  const int kv_end = CAUSAL ? min(lk, q0 + 32) : lk;
+  const int nchunks = (kv_end + 31) / 32;
+  const float c2 = scale * kLog2e;
+
+  // This lane's Q row (query qi, columns 16 c + 8 g .. + 7) as hi and lo operands.
+  bf16x8 qh[NQ], ql[NQ];
+  {
+    const auto rq = make_rsrc(Q + (int64_t)b * st.qb + (int64_t)h * st.qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + D) * 4));
+    const uint32_t qoff = (uint32_t)(((int64_t)qi * st.qs + 8 * g) * 4);
+#pragma unroll
+    for (int c = 0; c < NQ; ++c) split8(buf_load16(rq, qoff + 64 * c), buf_load16(rq, qoff + 64 * c + 16), qh[c], ql[c]);
+  }
+  const auto rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hk * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 4));
+  const auto rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hk * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 4));
+  const int krow = FL128::swap23(r);
+  auto load_k = [&](int tc, SplitK& ch) {
+    const uint32_t ko = (uint32_t)(((int64_t)(32 * tc + krow) * st.ks + 8 * g) * 4);
+#pragma unroll
+    for (int c = 0; c < NQ; ++c) {
+      ch.k[2 * c] = buf_load16(rk, ko + 64 * c);
+      ch.k[2 * c + 1] = buf_load16(rk, ko + 64 * c + 16);
+    }
+  };
+  auto load_v = [&](int tc, SplitV& ch) {
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          ch.v[16 * dt + 8 * kc + e] =
+              buf_load4(rv, (uint32_t)(((int64_t)(32 * tc + 16 * kc + 8 * g + e) * st.vs + 32 * dt + r) * 4));
+  };
+
+  f32x16 oacc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.f;
+  SoftmaxLog2 sl;
+  // QK^T, mask and softmax of chunk tc; P (hi, lo) out
+  auto scores = [&](int tc, const SplitK& ch, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
+    f32x16 sacc[1];
+    {
+      f32x16 acc = sl.mneg;
+#pragma unroll
+      for (int c = 0; c < NQ; ++c) {
+        bf16x8 kh8, kl8;
+        split8(ch.k[2 * c], ch.k[2 * c + 1], kh8, kl8);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh8, qh[c], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh8, ql[c], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl8, qh[c], acc, 0, 0, 0);
+      }
+      sacc[0] = acc;
+    }
+    // causal / length mask (keys 32 tc + 8 g + (j & 7) + 16 (j >> 3) of this lane)
+    const int kb = 32 * tc;
+    if (kb + 32 > lk || (CAUSAL && kb + 31 > q0)) {
+      const int lim = (CAUSAL ? min(lk, qi + 1) : lk) - kb - 8 * g;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (16 * (j >> 3) + (j & 7) >= lim) sacc[0][j] = -INFINITY;
+    }
+    // P = 2^(c2 (s - m)) in fp32, split into bf16 hi and lo operands; returns this lane's fp32 sum
+    auto exponentiate = [&]() -> float {
+      float sum = 0.f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pv[e] = fast_exp2(sacc[0][8 * hh + e] * c2);
+          sum += pv[e];
+        }
+        split8(make_uint4(__float_as_uint(pv[0]), __float_as_uint(pv[1]), __float_as_uint(pv[2]), __float_as_uint(pv[3])),
+               make_uint4(__float_as_uint(pv[4]), __float_as_uint(pv[5]), __float_as_uint(pv[6]), __float_as_uint(pv[7])),
+               ph[hh], pl[hh]);
+      }
+      return sum;
+    };
+    float ps = exponentiate();
+    if (sl.need_raise(ps)) {
+      sl.raise(sacc, c2, oacc);
+      ps = exponentiate();
+    }
+    sl.l += ps;
+  };
+  // O^T += V^T P^T over the chunk's two 16-key steps
+  auto pv = [&](const SplitV& ch, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const uint32_t* vv = ch.v + 16 * dt + 8 * kc;
+        bf16x8 vh8, vl8;
+        split8(make_uint4(vv[0], vv[1], vv[2], vv[3]), make_uint4(vv[4], vv[5], vv[6], vv[7]), vh8, vl8);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh8, ph[kc], oacc[dt], 0, 0, 0);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh8, pl[kc], oacc[dt], 0, 0, 0);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl8, ph[kc], oacc[dt], 0, 0, 0);
+      }
+  };
+  // This wave's chunks wave, wave + 4, ...: K in two register sets (the next chunk's K loads during
+  // the whole current chunk), V in one (the next chunk's V loads once PV has consumed the current
+  // one, and lands during the next QK^T and softmax).
+  {
+    SplitK ka, kb;
+    SplitV vv;
+    int tc = wave;
+    if (tc < nchunks) {
+      load_k(tc, ka);
+      load_v(tc, vv);
+    }
+    while (tc < nchunks) {
+      const int nx = tc + kSplitWaves;
+      if (nx < nchunks) load_k(nx, kb);
+      {
+        bf16x8 ph[2], pl[2];
+        scores(tc, ka, ph, pl);
+        pv(vv, ph, pl);
+      }
+      if (nx < nchunks) load_v(nx, vv);
+      tc = nx;
+      if (tc >= nchunks) break;
+      const int nx2 = tc + kSplitWaves;
+      if (nx2 < nchunks) load_k(nx2, ka);
+      {
+        bf16x8 ph[2], pl[2];
+        scores(tc, kb, ph, pl);
+        pv(vv, ph, pl);
+      }
+      if (nx2 < nchunks) load_v(nx2, vv);
+      tc = nx2;
+    }
+  }
+  // Merge: waves 1..3 write (m, l, O) to LDS; wave 0 combines them in wave order.
+  float l = sl.l;
+  if (wave > 0) {
+    float* p = part + (wave - 1) * 66 * 64 + lane;
+    p[0] = sl.m;
+    p[64] = l;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) p[(2 + 16 * dt + j) * 64] = oacc[dt][j];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  float mo[kSplitWaves];
+  mo[0] = sl.m;
+#pragma unroll
+  for (int w2 = 1; w2 < kSplitWaves; ++w2) mo[w2] = part[(w2 - 1) * 66 * 64 + lane];
+  float mt = mo[0];
+#pragma unroll
+  for (int w2 = 1; w2 < kSplitWaves; ++w2) mt = fmaxf(mt, mo[w2]);
+  // a wave with no unmasked key has m = -inf and adds nothing (its l and O are 0)
+  const float a0 = mo[0] == -INFINITY ? 0.f : fast_exp2((mo[0] - mt) * c2);
+  l *= a0;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[dt][j] *= a0;
+#pragma unroll
+  for (int w2 = 1; w2 < kSplitWaves; ++w2) {
+    const float* p = part + (w2 - 1) * 66 * 64 + lane;
+    const float a = mo[w2] == -INFINITY ? 0.f : fast_exp2((mo[w2] - mt) * c2);
+    l += a * p[64];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[dt][j] += a * p[(2 + 16 * dt + j) * 64];
+  }
+  // O[qi][d] = O / l; lane holds d = 32 dt + 8 a + 4 g .. + 3 (l: this lane's keys plus lane ^ 32's)
+  const float l_tot = l + __shfl_xor(l, 32, 64);
+  if (qi < lq) {
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    float* orow = O + (int64_t)b * st.ob + (int64_t)h * st.oh + (int64_t)qi * st.os;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<float4*>(orow + 32 * dt + 8 * a + 4 * g) =
+            make_float4(oacc[dt][4 * a] * inv, oacc[dt][4 * a + 1] * inv, oacc[dt][4 * a + 2] * inv,
+                        oacc[dt][4 * a + 3] * inv);
+  }
+}
+
 }  // namespace
 
 namespace kh {
@@ -807,6 +1073,38 @@ bool flash_prefill_supported(const void* q, const void* k, const void* v, const 
   // (Tiles are prefetched up to two ahead: keys up to lk + 383 are addressed and read as zero.)
   if ((lq + 512) * st.qs * 2 >= lim || (lk + 512) * st.ks * 2 >= lim || (lk + 512) * st.vs * 2 >= lim) return false;
   return true;
+}
+
+bool flash_split_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv, int64_t lq,
+                           int64_t lk, int d, const AttnStrides& st, float scale) {
+  (void)hq;
+  (void)hkv;
+  if (d != 128 || !(scale > 0.f)) return false;
+  if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
+  const int64_t all[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.vb, st.vh, st.vs, st.ob, st.oh, st.os};
+  for (int64_t s : all)
+    if (s < 0 || s > INT32_MAX || s % 4 != 0) return false;  // 16-byte rows, 32-bit strides
+  const int64_t lim = int64_t(1) << 31;
+  return (lq * st.qs + d) * 4 < lim && (lk * st.ks + d) * 4 < lim && (lk * st.vs + d) * 4 < lim;
+}
+
+int launch_flash_split_f32(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq,
+                           int lk, const AttnStrides& st, float scale, bool causal) {
+  const int nqb = (lq + 31) / 32;
+  const int64_t grid = (int64_t)nqb * batch * hq;
+  KH_REQUIRE(grid <= INT32_MAX, "kh_flash_attention_split: grid too large");
+  const SplitStrides s32{(int32_t)st.qb, (int32_t)st.qh, (int32_t)st.qs, (int32_t)st.kb, (int32_t)st.kh, (int32_t)st.ks,
+                         (int32_t)st.vb, (int32_t)st.vh, (int32_t)st.vs, (int32_t)st.ob, (int32_t)st.oh, (int32_t)st.os};
+  const float *Q = (const float*)q, *K = (const float*)k, *V = (const float*)v;
+  float* O = (float*)o;
+  if (causal)
+    flash_split_kernel<true><<<(int)grid, kSplitWaves * 64, 0, stream()>>>(Q, K, V, O, hq, hq / hkv, lq, lk, s32, scale,
+                                                                          nqb);
+  else
+    flash_split_kernel<false><<<(int)grid, kSplitWaves * 64, 0, stream()>>>(Q, K, V, O, hq, hq / hkv, lq, lk, s32,
+                                                                           scale, nqb);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
 }
 
 int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv,

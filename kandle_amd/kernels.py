@@ -65,6 +65,18 @@ def _as_4d(h: HipTensorHandle):
 # ---------------------------------------------------------------------------------------------
 def flash_attention(query, key, value, output, scale: float, is_causal: bool) -> None:
     """O = softmax(scale * Q K^T + causal) V with native GQA; output preallocated by the caller."""
+    _flash(query, key, value, output, scale, is_causal, split=False)
+
+
+def flash_attention_split(query, key, value, output, scale: float, is_causal: bool) -> None:
+    """flash_attention's signature for fp32 operands, computed in split-bf16 form (each fp32 value as
+    bf16 hi + lo, every product as three bf16 MFMAs: within about 2^-15 relative of the fp32
+    products; kh_flash_attention_split): the float32-activation prefill's attention.  Shapes the
+    split kernel does not take run the fp32 kernel."""
+    _flash(query, key, value, output, scale, is_causal, split=True)
+
+
+def _flash(query, key, value, output, scale: float, is_causal: bool, split: bool) -> None:
     for name, h in (("query", query), ("key", key), ("value", value), ("output", output)):
         if h.dtype not in (FLOAT32, BFLOAT16):
             raise TypeError(f"flash_attention: {name} dtype {h.dtype} not supported")
@@ -94,11 +106,14 @@ def flash_attention(query, key, value, output, scale: float, is_causal: bool) ->
         if tuple(os_) != (B, Hq, Lq, D) or ost[3] != 1:
             raise ValueError(f"flash_attention: output must be [B,Hq,Lq,D] with a contiguous last dim, got {os_}")
         strides = _lib.i64_array(qst[:3] + kst[:3] + vst[:3] + ost[:3])
-        _lib.call(
-            "kh_flash_attention",
-            _vp(q.data_ptr()), _vp(k.data_ptr()), _vp(v.data_ptr()), _vp(output.data_ptr()),
-            B, Hq, Hkv, Lq, Lk, D, strides, C.c_float(scale), int(bool(is_causal)), q.kh_dtype,
-        )
+        args = (_vp(q.data_ptr()), _vp(k.data_ptr()), _vp(v.data_ptr()), _vp(output.data_ptr()),
+                B, Hq, Hkv, Lq, Lk, D, strides, C.c_float(scale), int(bool(is_causal)))
+        if split:
+            if q.dtype != FLOAT32:
+                raise TypeError("flash_attention_split: float32 operands expected")
+            _lib.call("kh_flash_attention_split", *args)
+        else:
+            _lib.call("kh_flash_attention", *args, q.kh_dtype)
     finally:
         for t in tmp:
             t.dispose()
@@ -1062,6 +1077,7 @@ KERNELS = {
     "sample": sample,
     "decode_attention_block": decode_attention_block,
     "flash_attention": flash_attention,
+    "flash_attention_split": flash_attention_split,
     "sdpa_masked": sdpa_masked,
     "decode_attention": decode_attention,
     "matmul": matmul,

@@ -173,12 +173,20 @@ ACTIVATION_DTYPES = ("float32", "bfloat16")
 
 class Qwen3ForCausalLM:
     def __init__(self, cfg: Qwen3Config, weights: Dict[str, np.ndarray], max_seq_len: int = 1024,
-                 activations: str = "float32"):
+                 activations: str = "float32", f32_attention: str = "split"):
+        """activations: "float32" (the reference's f32 arithmetic over bf16 weights) or "bfloat16"
+        (activations and KV caches rounded to bf16).  f32_attention (float32 mode): "split" runs the
+        prefill attention as three bf16 MFMAs per product on hi/lo operands (flash_attention_split,
+        within about 2^-15 of the fp32 products), "fp32" on the fp32 MFMA (flash_attention)."""
         if activations not in ACTIVATION_DTYPES:
             raise ValueError(f"activations must be one of {ACTIVATION_DTYPES}, not {activations!r}")
+        if f32_attention not in ("split", "fp32"):
+            raise ValueError(f"f32_attention must be 'split' or 'fp32', not {f32_attention!r}")
         self.cfg = cfg
         self.max_seq_len = max_seq_len
         self.act = activations
+        self._flash_name = "flash_attention_split" if (activations == "float32" and f32_attention == "split") \
+            else "flash_attention"
         self.ops = env.get_backend("hip").operators
         up = lambda a: Tensor(a, dtype="bfloat16")  # noqa: E731  (uint16 bits -> bf16 tensor)
         self.embed = up(weights["model.embed_tokens.weight"])
@@ -231,7 +239,8 @@ class Qwen3ForCausalLM:
     # -- decoder body shared by the prefill and the device-resident decode step -------------------
     @classmethod
     def from_pretrained(cls, path: str, max_seq_len: int = 1024, cfg: Optional[Qwen3Config] = None,
-                        strict: bool = True, activations: str = "float32") -> "Qwen3ForCausalLM":
+                        strict: bool = True, activations: str = "float32",
+                        f32_attention: str = "split") -> "Qwen3ForCausalLM":
         """A model from a Hugging Face-layout checkpoint: `path` is a directory holding config.json and
         model.safetensors (or model.safetensors.index.json and its shards), or a .safetensors /
         index file with `cfg` given.  Weights go to the device as bf16 without an fp32 copy."""
@@ -244,7 +253,7 @@ class Qwen3ForCausalLM:
             cfg = Qwen3Config.from_json_file(os.path.join(root, "config.json"))
         with load_safetensor(path) as group:
             weights, result = qwen3_weights_from_safetensor(group, cfg, strict=strict)
-            model = cls(cfg, weights, max_seq_len=max_seq_len, activations=activations)
+            model = cls(cfg, weights, max_seq_len=max_seq_len, activations=activations, f32_attention=f32_attention)
             del weights   # views of the memory maps: released before the files close
         model.load_result = result
         return model
@@ -377,7 +386,7 @@ class Qwen3ForCausalLM:
         def attend(li, q_heads, out_view):
             kc, vc = self.cache.valid_slices(li, end)
             # causal for a multi-token chunk; off for one new token (gqa.ts:333-336)
-            self.ops.find("flash_attention")(q_heads, kc.handle, vc.handle, out_view, self.scale, S > 1)
+            self.ops.find(self._flash_name)(q_heads, kc.handle, vc.handle, out_view, self.scale, S > 1)
             kc.dispose()
             vc.dispose()
 

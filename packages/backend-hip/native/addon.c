@@ -561,6 +561,15 @@ FN(flashAttention, 14)
   int64_t lk = arg_i64(A, 8); int d = arg_int(A, 9); arg_list(A, 10, st, 12); double sc = arg_f64(A, 11);
   int causal = arg_flag(A, 12); int dt = arg_int(A, 13);
   CALL(kh_flash_attention(q, k, v, o, b, hq, hkv, lq, lk, d, st, (float)sc, causal, dt))
+/* flashAttentionSplit(q, k, v, o, batch, hq, hkv, lq, lk, d, strides[12], scale, causal): fp32
+   attention in split-bf16 form (kh_flash_attention_split) */
+FN(flashAttentionSplit, 13)
+  int64_t st[12];
+  void* q = arg_ptr(A, 0); void* k = arg_ptr(A, 1); void* v = arg_ptr(A, 2); void* o = arg_ptr(A, 3);
+  int b = arg_int(A, 4); int hq = arg_int(A, 5); int hkv = arg_int(A, 6); int64_t lq = arg_i64(A, 7);
+  int64_t lk = arg_i64(A, 8); int d = arg_int(A, 9); arg_list(A, 10, st, 12); double sc = arg_f64(A, 11);
+  int causal = arg_flag(A, 12);
+  CALL(kh_flash_attention_split(q, k, v, o, b, hq, hkv, lq, lk, d, st, (float)sc, causal))
 /* flashAttentionMasked(q, k, v, o, batch, hq, hkv, lq, lk, d, strides[12], scale, mask, maskStrides[4],
                         maskDtype, dtype): the attnMask route of composite.ts:279-300 in one call */
 FN(flashAttentionMasked, 16)
@@ -679,7 +688,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(fill), EXPORT(copyStrided), EXPORT(mapStrided), EXPORT(binary), EXPORT(silu), EXPORT(unary), EXPORT(arange),
       EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
-      EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
+      EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionSplit), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
       EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmEx), EXPORT(gemmSwiglu), EXPORT(gemmQkNormRope), EXPORT(gemmSplitCount),
       EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused), EXPORT(gemvSwiglu),
   };

@@ -328,6 +328,19 @@ function flashAttention(q: HipTensorHandle, k: HipTensorHandle, v: HipTensorHand
                        q.shape[3], st, scale, isCausal, q.kh);
 }
 
+// flash_attention_split(query, key, value, output, scale, isCausal): flash_attention's signature for
+// fp32 operands in split-bf16 form (each fp32 value as bf16 hi + lo, every product as three bf16
+// MFMAs, within about 2^-15 relative of the fp32 products); the float32-activation prefill's
+// attention.  Shapes the split kernel does not take run the fp32 kernel.
+function flashAttentionSplit(q: HipTensorHandle, k: HipTensorHandle, v: HipTensorHandle, out: HipTensorHandle,
+                             scale: number, isCausal: boolean): void {
+  if (q.dtype !== 'float32' || k.dtype !== 'float32' || v.dtype !== 'float32' || out.dtype !== 'float32')
+    throw new Error('flash_attention_split: float32 operands expected');
+  const st = bhlStrides(q, 'query').concat(bhlStrides(k, 'key'), bhlStrides(v, 'value'), bhlStrides(out, 'output'));
+  addon.flashAttentionSplit(q.ptr, k.ptr, v.ptr, out.ptr, q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2],
+                            q.shape[3], st, scale, isCausal);
+}
+
 // sdpa_masked(query, key, value, mask, output, scale): the attnMask route of composite.ts:279-300 in
 // one kernel; the mask broadcasts to [B, Hq, Lq, Lk] (a stride of 0 on a broadcast axis).
 function sdpaMasked(q: HipTensorHandle, k: HipTensorHandle, v: HipTensorHandle, mask: HipTensorHandle,
@@ -994,6 +1007,7 @@ export class HipBackend {
 
 export function registerHipKernels(reg: SimpleOperatorRegistry): void {
   reg.register('flash_attention', flashAttention);
+  reg.register('flash_attention_split', flashAttentionSplit);
   reg.register('sdpa_masked', sdpaMasked);
   reg.register('rms_norm', rmsNorm);
   for (const name of ['matmul', 'mm', 'bmm', 'addmm', 'baddbmm']) reg.register(name, matmul);

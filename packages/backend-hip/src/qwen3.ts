@@ -142,6 +142,7 @@ export class Qwen3ForCausalLM {
   finalNorm: any;
   finalNormA: any;
   act: string;
+  flashName: string;
   invFreq: any;
   invFreqHost: Float32Array;
   layers: Layer[] = [];
@@ -154,7 +155,7 @@ export class Qwen3ForCausalLM {
   // weights: Hugging Face tensor names -> bf16 bit patterns (tied embeddings: the lm_head is the
   // embedding matrix, for_causal_lm.ts:121-125).
   constructor(backend: any, cfg: Qwen3Config, weights: { [name: string]: Uint16Array }, maxSeqLen: number,
-              activations?: string) {
+              activations?: string, f32Attention?: string) {
     this.cfg = cfg;
     this.backend = backend;
     this.ops = backend.operators;
@@ -162,6 +163,11 @@ export class Qwen3ForCausalLM {
     this.act = activations === undefined ? 'float32' : activations;
     if (this.act !== 'float32' && this.act !== 'bfloat16')
       throw new Error(`Qwen3ForCausalLM: activations must be float32 or bfloat16, not ${this.act}`);
+    // float32 activations: the prefill attention in split-bf16 form ('split', the default) or on the
+    // fp32 MFMA ('fp32'), as the Python model's f32_attention
+    const fa = f32Attention === undefined ? 'split' : f32Attention;
+    if (fa !== 'split' && fa !== 'fp32') throw new Error(`Qwen3ForCausalLM: f32Attention must be split or fp32, not ${fa}`);
+    this.flashName = this.act === 'float32' && fa === 'split' ? 'flash_attention_split' : 'flash_attention';
     const H = cfg.hiddenSize, I = cfg.intermediateSize, D = cfg.headDim;
     const up = (bits: Uint16Array, shape: number[]): any => backend.createTensorHandle({ shape, dtype: 'bfloat16', data: bits });
     // a norm weight in the activation dtype (exactly widened for float32 activations)
@@ -215,11 +221,11 @@ export class Qwen3ForCausalLM {
   }
 
   static fromSafetensors(backend: any, cfg: Qwen3Config, file: string, maxSeqLen: number,
-                         activations?: string): Qwen3ForCausalLM {
+                         activations?: string, f32Attention?: string): Qwen3ForCausalLM {
     const tensors = readSafetensors(file);
     const weights: { [name: string]: Uint16Array } = {};
     for (const name of Object.keys(tensors)) weights[name] = bf16Bits(tensors[name], name);
-    return new Qwen3ForCausalLM(backend, cfg, weights, maxSeqLen, activations);
+    return new Qwen3ForCausalLM(backend, cfg, weights, maxSeqLen, activations, f32Attention);
   }
 
   private view(base: any, shape: number[], strides: number[], offset: number): any {
@@ -280,7 +286,7 @@ export class Qwen3ForCausalLM {
       const attnView = this.view(attn, [1, Hq, S, D], [S * nq, D, nq, 1], 0);
       const kc = this.view(L.kCache, [1, Hkv, S, D], L.kCache.strides, 0);
       const vc = this.view(L.vCache, [1, Hkv, S, D], L.vCache.strides, 0);
-      ops.find('flash_attention')(qh, kc, vc, attnView, this.scale, S > 1);
+      ops.find(this.flashName)(qh, kc, vc, attnView, this.scale, S > 1);
       for (const t of [attnView, kc, vc, qh]) t.dispose();
       const h2 = be.createTensorHandle([S, H], act);
       ops.find('linear_add_rms_norm')(attn, L.wO, x, L.postNormA, eps, h2);
