@@ -844,7 +844,12 @@ template <typename TA>
 int launch_gemm_swiglu(const TA* X, int64_t ldx, const uint16_t* W, int64_t ldw, TA* H, int64_t ldh, int M, int N,
                        int K) {
   int wtm = 1, wtn = 1;
-  plain_tile(M, N, wtm, wtn);
+  // fp32 activations (two MFMAs per k-step) take 64 x 128 tiles: C5 gate/up 27.0-27.3 -> 23.7-23.8 us
+  // (128 x 64: 36.2 us); bf16 keeps the plain choice.  The tile never changes a sum.
+  if constexpr (std::is_same<TA, float>::value)
+    wtn = 2;
+  else
+    plain_tile(M, N, wtm, wtn);
   const int tiles_m = (M + g_tile(wtm) - 1) / g_tile(wtm), tiles_n = (N + g_tile(wtn) - 1) / g_tile(wtn);
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_swiglu: grid too large");
