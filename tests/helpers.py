@@ -23,3 +23,15 @@ def max_rel(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def assert_close_elem(a, b, rtol=1e-4, atol=1e-5, what=""):
+    """Element-wise |a - b| <= rtol * |b| + atol (atol: the floor for elements near zero, where an
+    fp32 sum's absolute error dominates), reporting the worst element."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    excess = np.abs(a - b) - (rtol * np.abs(b) + atol)
+    i = int(np.argmax(excess))
+    assert excess.flat[i] <= 0, (f"{what}: element {np.unravel_index(i, b.shape)} differs by "
+                                 f"{abs(a.flat[i] - b.flat[i]):.3e} (value {b.flat[i]:.4e}; "
+                                 f"bound {rtol * abs(b.flat[i]) + atol:.3e})")

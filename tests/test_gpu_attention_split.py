@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import max_rel, seeded
+from helpers import assert_close_elem, max_rel, seeded
 from kandle_amd import HipTensorHandle, Tensor, kernels
 
 pytestmark = pytest.mark.gpu
@@ -88,6 +88,8 @@ def test_split_attention_matches_emulation_and_fp32(hip, B, Hq, Hkv, Lq, Lk, cau
     print(f"[split attention] {B, Hq, Hkv, Lq, Lk, causal}: vs emulation {e_emu:.2e}, vs fp32 {e_f32:.2e}")
     assert e_emu < EMU_RTOL
     assert e_f32 < F32_RTOL
+    assert_close_elem(out, oracle.sdpa(qv, kv, vv, scale=scale, causal=causal), rtol=4e-4, atol=4e-5,
+                      what="split vs fp32")
 
 
 def test_split_attention_softmax_raises_and_strided_views(hip):
