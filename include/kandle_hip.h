@@ -413,6 +413,23 @@ int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t 
                          const void* wk, const float* inv_freq, const int32_t* positions, void* q_out, void* k_out,
                          void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len, int dtype);
 
+/* kh_gemm_qk_norm_rope with the RoPE angles read from rope_table (kh_rope_table's layout, rows
+ * indexed by the projection's row m = batch * seq_len + index, 16-byte aligned) instead of
+ * evaluated per head tile; rope_table == NULL is kh_gemm_qk_norm_rope.  The table holds the same
+ * values the tile would compute, so the outputs are identical.  No reference counterpart (the
+ * reference builds its cos / sin tables per forward in rope.ts:193-255). */
+int kh_gemm_qk_norm_rope_table(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
+                               int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim,
+                               const void* wq, const void* wk, const float* inv_freq, const int32_t* positions,
+                               void* q_out, void* k_out, void* v_out, const int64_t* strides, float eps,
+                               int64_t kv_cache_len, int dtype, const float* rope_table);
+
+/* RoPE angle table for n tokens: out[2 (t half + i)] = cos(float(positions[t]) * inv_freq[i]) and
+ * out[2 (t half + i) + 1] = sin(...), i < half, fp32 -- the reference's f32 angle product and
+ * cos / sin (packages/model-utils/src/rope.ts:193-255), once per forward for every layer's fused
+ * QKV projection (kh_gemm_qk_norm_rope_table). */
+int kh_rope_table(const int32_t* positions, int64_t n, const float* inv_freq, int half, float* out);
+
 /* The split count kh_gemm uses for a [m, k] x [n, k]^T product with bf16 weights and contiguous,
  * 16-byte aligned operands, whether A is bf16 or fp32 (1: not split).  A caller that splits the same product with
  * kh_gemm_splitk_partials and adds the partials in split order reproduces kh_gemm bit for bit. */

@@ -84,6 +84,9 @@ SIGNATURES = {
     "kh_gemm_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i],
     "kh_gemm_qk_norm_rope": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                              _i64p, _f, _i64, _i],
+    "kh_gemm_qk_norm_rope_table": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _vp, _i64p, _f, _i64, _i, _vp],
+    "kh_rope_table": [_vp, _i64, _vp, _i, _vp],
     "kh_gemm_split_count": [_i64, _i64, _i64, C.POINTER(C.c_int)],
     "kh_gemm_splitk_partials": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i, _i],
     "kh_add_rms_norm": [_vp, _i, _i64, _vp, _vp, _vp, _i64, _i64, _f, _i],

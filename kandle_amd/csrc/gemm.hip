@@ -104,6 +104,9 @@ struct QknrArgs {
   uint32_t seq_len = 1;               // token m is (batch m / seq_len, index m % seq_len)
   float eps = 0.f;
   int64_t kv_cache_len = 0;           // > 0: K/V rows at positions[m] (outside [0, len): not written)
+  // Optional [M][64][2] (cos, sin) of float(positions[m]) * inv_freq[i] (rope_table_kernel, the same
+  // expression): read instead of evaluating sincosf in every head tile.
+  const float* rope_cs = nullptr;
 };
 
 // TA = float (fp32 activations, the reference's float32 arithmetic): A is read as fp32 and each
@@ -357,9 +360,21 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
       const bool kv_ok = !cache_mode || (ipos >= 0 && (int64_t)ipos < qa.kv_cache_len);
       if (is_q || is_k) {
         float cs[8], sn[8], oa[8], oc[8];
-        const float pos = (float)ipos;
+        if (qa.rope_cs != nullptr) {
+          const float4* t4 = reinterpret_cast<const float4*>(qa.rope_cs + ((int64_t)(live ? m : 0) * 64 + 8 * t8) * 2);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sincosf(pos * f[j], &sn[j], &cs[j]);
+          for (int j = 0; j < 4; ++j) {
+            const float4 v = t4[j];
+            cs[2 * j] = v.x;
+            sn[2 * j] = v.y;
+            cs[2 * j + 1] = v.z;
+            sn[2 * j + 1] = v.w;
+          }
+        } else {
+          const float pos = (float)ipos;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sincosf(pos * f[j], &sn[j], &cs[j]);
+        }
         qk_norm_rope_row<128>(a8, c8, wa, wb, cs, sn, qa.eps, oa, oc);
         if (live && (is_q || kv_ok)) {
           TA* dst = is_q ? (TA*)qa.q_out + bi * qa.s[0] + si * qa.s[1] + (int64_t)hd * qa.s[2]
@@ -988,10 +1003,48 @@ int kh_gemm_swiglu(const void* x, int64_t ldx, const void* w_gu, int64_t ldw, vo
                                       (int)(2 * n_half), (int)k);
 }
 
+// cos / sin of float(positions[t]) * inv_freq[i] for n tokens and `half` frequencies, interleaved
+// (cos, sin) per (t, i): the angles of every qk-norm + RoPE head tile of a prefill, evaluated once.
+__global__ __launch_bounds__(256) void rope_table_kernel(const int32_t* __restrict__ positions, int64_t n,
+                                                         const float* __restrict__ inv_freq, int half,
+                                                         float* __restrict__ out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n * half; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / half;
+    const float pos = (float)positions[t];
+    float sn, cs;
+    sincosf(pos * inv_freq[i - t * half], &sn, &cs);
+    out[2 * i] = cs;
+    out[2 * i + 1] = sn;
+  }
+}
+
+int kh_rope_table(const int32_t* positions, int64_t n, const float* inv_freq, int half, float* out) {
+  KH_REQUIRE_INIT();
+  KH_REQUIRE(n >= 0 && half > 0 && half <= 4096, "kh_rope_table: bad extents");
+  if (n == 0) return KH_OK;
+  KH_REQUIRE(positions && inv_freq && out, "kh_rope_table: null pointer");
+  const int64_t total = n * half;
+  const int64_t want = (total + 255) / 256;
+  const int grid = (int)(want < 4096 ? want : 4096);
+  rope_table_kernel<<<grid, 256, 0, stream()>>>(positions, n, inv_freq, half, out);
+  KH_CHECK_LAUNCH();
+  return KH_OK;
+}
+
 int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
                          int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim, const void* wq,
                          const void* wk, const float* inv_freq, const int32_t* positions, void* q_out, void* k_out,
                          void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len, int dtype) {
+  return kh_gemm_qk_norm_rope_table(x, ldx, w_qkv, ldw, n_batch, seq_len, k, n_q_heads, n_kv_heads, head_dim, wq, wk,
+                                    inv_freq, positions, q_out, k_out, v_out, strides, eps, kv_cache_len, dtype,
+                                    nullptr);
+}
+
+int kh_gemm_qk_norm_rope_table(const void* x, int64_t ldx, const void* w_qkv, int64_t ldw, int64_t n_batch,
+                               int64_t seq_len, int64_t k, int n_q_heads, int n_kv_heads, int head_dim, const void* wq,
+                               const void* wk, const float* inv_freq, const int32_t* positions, void* q_out,
+                               void* k_out, void* v_out, const int64_t* strides, float eps, int64_t kv_cache_len,
+                               int dtype, const float* rope_table) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(n_batch >= 0 && seq_len >= 0 && k > 0 && k <= INT32_MAX && kv_cache_len >= 0,
              "kh_gemm_qk_norm_rope: bad extents");
@@ -1030,6 +1083,8 @@ int kh_gemm_qk_norm_rope(const void* x, int64_t ldx, const void* w_qkv, int64_t 
   qa.seq_len = (uint32_t)(seq_len > 0 ? seq_len : 1);
   qa.eps = eps;
   qa.kv_cache_len = kv_cache_len;
+  KH_REQUIRE(rope_table == nullptr || aligned16(rope_table), "kh_gemm_qk_norm_rope: rope_table must be 16-byte aligned");
+  qa.rope_cs = rope_table;
   if (dtype == KH_F32)
     return launch_gemm_qk_norm_rope<float>((const float*)x, ldx, (const uint16_t*)w_qkv, ldw, (int)M, (int)N, (int)k,
                                            qa);

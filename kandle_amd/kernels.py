@@ -884,10 +884,32 @@ def linear_qk_norm_rope(x, w_qkv, params) -> None:
     st = []
     for t in (q_out, k_out, v_out):
         st += [t.strides[0], t.strides[2], t.strides[1]]
-    _lib.call("kh_gemm_qk_norm_rope", _vp(x.data_ptr()), x.strides[0], _vp(w_qkv.data_ptr()), w_qkv.strides[0], 1,
-              S, H, Hq, Hkv, D, _vp(params["q_weight"].data_ptr()), _vp(params["k_weight"].data_ptr()),
-              _vp(inv_freq.data_ptr()), _vp(pos.data_ptr()), _vp(q_out.data_ptr()), _vp(k_out.data_ptr()),
-              _vp(v_out.data_ptr()), _lib.i64_array(st), C.c_float(float(params.get("eps", 1e-6))), L, x.kh_dtype)
+    table = params.get("rope_table")
+    if table is not None and (table.dtype != FLOAT32 or table.numel != S * D or not table.is_contiguous()):
+        raise ValueError("linear_qk_norm_rope: rope_table must be rope_table(positions, inv_freq): float32 [S, D/2, 2]")
+    _lib.call("kh_gemm_qk_norm_rope_table", _vp(x.data_ptr()), x.strides[0], _vp(w_qkv.data_ptr()),
+              w_qkv.strides[0], 1, S, H, Hq, Hkv, D, _vp(params["q_weight"].data_ptr()),
+              _vp(params["k_weight"].data_ptr()), _vp(inv_freq.data_ptr()), _vp(pos.data_ptr()),
+              _vp(q_out.data_ptr()), _vp(k_out.data_ptr()), _vp(v_out.data_ptr()), _lib.i64_array(st),
+              C.c_float(float(params.get("eps", 1e-6))), L, x.kh_dtype,
+              _vp(table.data_ptr() if table is not None else None))
+
+
+def rope_table(positions: HipTensorHandle, inv_freq: HipTensorHandle,
+               output: Optional[HipTensorHandle] = None) -> HipTensorHandle:
+    """The RoPE angles of a chunk once per forward (kh_rope_table): output [S, D/2, 2] float32 =
+    (cos, sin) of float(positions[t]) * inv_freq[i] (rope.ts:193-255); linear_qk_norm_rope reads it
+    (params["rope_table"]) in every layer instead of evaluating the angles in each head tile."""
+    if positions.dtype != INT32 or not positions.is_contiguous():
+        raise TypeError("rope_table: positions must be a contiguous int32 tensor")
+    if inv_freq.dtype != FLOAT32 or not inv_freq.is_contiguous():
+        raise TypeError("rope_table: inv_freq must be a contiguous float32 tensor")
+    S, half = positions.numel, inv_freq.numel
+    out = output if output is not None else HipTensorHandle.create_new((S, half, 2), FLOAT32)
+    if out.dtype != FLOAT32 or out.numel != S * half * 2 or not out.is_contiguous():
+        raise ValueError("rope_table: output must be a contiguous float32 [S, D/2, 2] tensor")
+    _lib.call("kh_rope_table", _vp(positions.data_ptr()), S, _vp(inv_freq.data_ptr()), half, _vp(out.data_ptr()))
+    return out
 
 
 def gemm_split_count(m: int, n: int, k: int) -> int:
@@ -1098,6 +1120,7 @@ KERNELS = {
     "silu_mul": silu_mul,
     "linear_swiglu": linear_swiglu,
     "linear_qk_norm_rope": linear_qk_norm_rope,
+    "rope_table": rope_table,
     "linear_add_rms_norm": linear_add_rms_norm,
     "copy": copy,
     "contiguous": contiguous,

@@ -283,6 +283,8 @@ class Qwen3ForCausalLM:
         nqkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
         fuse_qkv = (self.fused_qkv_rope and not one and S > 8
                     and gemm_split_count(S, nqkv, Hd) == 1)
+        # the RoPE angles of these positions, once for every layer's fused projection
+        rope_tab = self.ops.find("rope_table")(positions.handle, self.rope.inv_freq.handle) if fuse_qkv else None
         for li, L in enumerate(self.layers):
             if one and decode_block:
                 qkv = F.linear_fused("rms_norm", x, L["w_qkv"], L["in_norm"], eps, act_dtype=act)  # [1, nq + 2 nkv]
@@ -298,7 +300,7 @@ class Qwen3ForCausalLM:
                 F.linear_fused("none", attn_t, L["w_o"], residual=x, act_dtype=act)     # x += o W_o^T
                 attn_t.dispose()
             elif fuse_qkv:
-                attn_t = self._attention_heads_fused(li, L, h, S, positions, attend)   # q/k/v from h
+                attn_t = self._attention_heads_fused(li, L, h, S, positions, attend, rope_tab)
                 h.dispose()
                 h = F.linear_add_rms_norm(attn_t, L["w_o"], x, L["post_norm_a"], eps)   # x += o W_o^T
                 attn_t.dispose()
@@ -321,6 +323,8 @@ class Qwen3ForCausalLM:
                 else:
                     h = F.linear_add_rms_norm(a, L["w_down"], x, self.final_norm_a, eps, rows=(S - 1, S))
                 a.dispose()
+        if rope_tab is not None:
+            rope_tab.dispose()
         if one:
             last = F.narrow(x, 0, S - 1, 1)
             logits = F.linear_fused("rms_norm", last, self.lm_head, self.final_norm, eps, out_dtype="float32",
@@ -331,10 +335,12 @@ class Qwen3ForCausalLM:
             h.dispose()
         return logits
 
-    def _attention_heads_fused(self, li: int, L: dict, h: Tensor, S: int, positions: Tensor, attend) -> Tensor:
+    def _attention_heads_fused(self, li: int, L: dict, h: Tensor, S: int, positions: Tensor, attend,
+                               rope_tab=None) -> Tensor:
         """As _attention_heads from the normed rows h [S, hidden] instead of their projection: one
         launch projects q/k/v and applies qk-norm + RoPE with the K/V cache write
-        (linear_qk_norm_rope), then attend(); returns the heads [S, nq] bf16."""
+        (linear_qk_norm_rope; the angles from rope_tab when given), then attend(); returns the
+        heads [S, nq] in the activation dtype."""
         cfg = self.cfg
         Hq, D = cfg.num_attention_heads, cfg.head_dim
         nq = Hq * D
@@ -342,7 +348,8 @@ class Qwen3ForCausalLM:
         self.ops.find("linear_qk_norm_rope")(h.handle, L["w_qkv"].handle, {
             "q_weight": L["q_norm"].handle, "k_weight": L["k_norm"].handle, "inv_freq": self.rope.inv_freq.handle,
             "positions": positions.handle, "eps": cfg.rms_norm_eps, "q_out": q_heads,
-            "k_out": self.cache.key_cache[li].handle, "v_out": self.cache.value_cache[li].handle})
+            "k_out": self.cache.key_cache[li].handle, "v_out": self.cache.value_cache[li].handle,
+            "rope_table": rope_tab})
         attn = HipTensorHandle.create_new((S, nq), self.act)
         attn_view = HipTensorHandle.create_view(attn.storage, (1, Hq, S, D), self.act, (S * nq, D, nq, 1), 0)
         attend(li, q_heads, attn_view)

@@ -634,6 +634,24 @@ FN(gemmQkNormRope, 21)
   double eps = arg_f64(A, 18); int64_t kvl = arg_i64(A, 19); int dt = arg_int(A, 20);
   CALL(kh_gemm_qk_norm_rope(x, ldx, w, ldw, nb, sl, k, hq, hkv, hd, wq, wk, (const float*)inv, (const int32_t*)pos,
                             qo, ko, vo, st, (float)eps, kvl, dt))
+/* gemmQkNormRopeTable(..., dtype, ropeTable): gemmQkNormRope with the RoPE angles read from a
+   ropeTable table (null: computed per tile) */
+FN(gemmQkNormRopeTable, 22)
+  int64_t st[9];
+  void* x = arg_ptr(A, 0); int64_t ldx = arg_i64(A, 1); void* w = arg_ptr(A, 2); int64_t ldw = arg_i64(A, 3);
+  int64_t nb = arg_i64(A, 4); int64_t sl = arg_i64(A, 5); int64_t k = arg_i64(A, 6);
+  int hq = arg_int(A, 7); int hkv = arg_int(A, 8); int hd = arg_int(A, 9);
+  void* wq = arg_ptr(A, 10); void* wk = arg_ptr(A, 11); void* inv = arg_ptr(A, 12); void* pos = arg_ptr(A, 13);
+  void* qo = arg_ptr(A, 14); void* ko = arg_ptr(A, 15); void* vo = arg_ptr(A, 16);
+  arg_list(A, 17, st, 9);
+  double eps = arg_f64(A, 18); int64_t kvl = arg_i64(A, 19); int dt = arg_int(A, 20); void* tab = arg_ptr(A, 21);
+  CALL(kh_gemm_qk_norm_rope_table(x, ldx, w, ldw, nb, sl, k, hq, hkv, hd, wq, wk, (const float*)inv,
+                                  (const int32_t*)pos, qo, ko, vo, st, (float)eps, kvl, dt, (const float*)tab))
+/* ropeTable(positions, n, invFreq, half, out): (cos, sin) of float(positions[t]) * invFreq[i] */
+FN(ropeTable, 5)
+  void* pos = arg_ptr(A, 0); int64_t n = arg_i64(A, 1); void* inv = arg_ptr(A, 2); int half = arg_int(A, 3);
+  void* out = arg_ptr(A, 4);
+  CALL(kh_rope_table((const int32_t*)pos, n, (const float*)inv, half, (float*)out))
 /* gemmSplitCount(m, n, k) -> the split count gemm uses for a contiguous bf16 [m, k] x [n, k]^T */
 static napi_value js_gemmSplitCount(napi_env env, napi_callback_info info) {
   Args A_, *A = &A_;
@@ -689,7 +707,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       EXPORT(siluMul), EXPORT(indexSelect), EXPORT(indexSelectDim), EXPORT(argmax), EXPORT(greedyAdvance), EXPORT(sample),
       EXPORT(sampleSetPath), EXPORT(philox4x32_10), EXPORT(decodeAttentionBlock), EXPORT(rmsNorm),
       EXPORT(qkNormRope), EXPORT(flashAttention), EXPORT(flashAttentionSplit), EXPORT(flashAttentionMasked), EXPORT(decodeAttention),
-      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmEx), EXPORT(gemmSwiglu), EXPORT(gemmQkNormRope), EXPORT(gemmSplitCount),
+      EXPORT(decodeAttentionNoalloc), EXPORT(gemm), EXPORT(gemmEx), EXPORT(gemmSwiglu), EXPORT(gemmQkNormRope), EXPORT(gemmQkNormRopeTable), EXPORT(ropeTable), EXPORT(gemmSplitCount),
       EXPORT(gemmSplitkPartials), EXPORT(addRmsNorm), EXPORT(gemvFused), EXPORT(gemvSwiglu),
   };
   napi_define_properties(env, exports, sizeof(d) / sizeof(d[0]), d);

@@ -842,9 +842,26 @@ function linearQkNormRope(x: HipTensorHandle, wQkv: HipTensorHandle, p: { [key: 
   if (vOut.shape.join() !== kOut.shape.join()) throw new Error('linear_qk_norm_rope: K and V caches differ in shape');
   const st: number[] = [];
   for (const t of [qOut, kOut, vOut]) st.push(t.strides[0], t.strides[2], t.strides[1]);
-  addon.gemmQkNormRope(x.ptr, x.strides[0], wQkv.ptr, wQkv.strides[0], 1, S, H, Hq, Hkv, D, p.qWeight.ptr,
-                       p.kWeight.ptr, p.invFreq.ptr, p.positions.ptr, qOut.ptr, kOut.ptr, vOut.ptr, st,
-                       p.eps === undefined ? 1e-6 : p.eps, L, x.kh);
+  const tab = p.ropeTable as HipTensorHandle | undefined;
+  if (tab !== undefined && (tab.dtype !== 'float32' || tab.numel !== S * D || !tab.isContiguous()))
+    throw new Error('linear_qk_norm_rope: ropeTable must be rope_table(positions, invFreq): float32 [S, D/2, 2]');
+  addon.gemmQkNormRopeTable(x.ptr, x.strides[0], wQkv.ptr, wQkv.strides[0], 1, S, H, Hq, Hkv, D, p.qWeight.ptr,
+                            p.kWeight.ptr, p.invFreq.ptr, p.positions.ptr, qOut.ptr, kOut.ptr, vOut.ptr, st,
+                            p.eps === undefined ? 1e-6 : p.eps, L, x.kh, tab === undefined ? null : tab.ptr);
+}
+
+// rope_table(positions, invFreq, output?): the RoPE angles of a chunk once per forward, [S, D/2, 2]
+// float32 (cos, sin) of float(positions[t]) * invFreq[i] (rope.ts:193-255); linear_qk_norm_rope
+// reads it (params.ropeTable) in every layer instead of evaluating the angles in each head tile.
+function ropeTable(positions: HipTensorHandle, invFreq: HipTensorHandle, output?: HipTensorHandle): HipTensorHandle {
+  if (positions.dtype !== 'int32' || !positions.isContiguous()) throw new Error('rope_table: contiguous int32 positions expected');
+  if (invFreq.dtype !== 'float32' || !invFreq.isContiguous()) throw new Error('rope_table: contiguous float32 invFreq expected');
+  const S = positions.numel, half = invFreq.numel;
+  const out = output || HipTensorHandle.createNew([S, half, 2], 'float32');
+  if (out.dtype !== 'float32' || out.numel !== S * half * 2 || !out.isContiguous())
+    throw new Error('rope_table: output must be a contiguous float32 [S, D/2, 2] tensor');
+  addon.ropeTable(positions.ptr, S, invFreq.ptr, half, out.ptr);
+  return out;
 }
 
 // linear_add_rms_norm(x, w, residual, normWeight, eps, output, rows?): residual += x W^T (fp32, in
@@ -1036,6 +1053,7 @@ export function registerHipKernels(reg: SimpleOperatorRegistry): void {
   reg.register('gemv_swiglu', gemvSwiglu);
   reg.register('linear_swiglu', linearSwiglu);
   reg.register('linear_qk_norm_rope', linearQkNormRope);
+  reg.register('rope_table', ropeTable);
   reg.register('linear_add_rms_norm', linearAddRmsNorm);
   reg.register('decode_attention_block', decodeAttentionBlock);
   reg.register('greedy_advance', greedyAdvance);

@@ -261,6 +261,8 @@ export class Qwen3ForCausalLM {
     const fuseQkv = D === 128 && S > 8 && be.gemmSplitCount(S, nqkv, H) === 1;
     ops.find('index_select')(this.embed, ids, { dim: 0 }, x);
     let h = ops.find('rms_norm')([x], { normalizedShape: [H], eps, weight: this.layers[0].inNormA, outDtype: act });
+    // the RoPE angles of these positions, once for every layer's fused projection
+    const ropeTab = fuseQkv ? ops.find('rope_table')(positions, this.invFreq) : undefined;
     for (let li = 0; li < this.layers.length; ++li) {
       const L = this.layers[li];
       const qh = be.createTensorHandle([1, Hq, S, D], act);
@@ -268,7 +270,8 @@ export class Qwen3ForCausalLM {
         // the projection with qk-norm, RoPE and the cache write in its epilogue: the same values as
         // the two launches below when their projection is not split over K
         ops.find('linear_qk_norm_rope')(h, L.wQkv, { qWeight: L.qNorm, kWeight: L.kNorm, invFreq: this.invFreq,
-                                                     positions, eps, qOut: qh, kOut: L.kCache, vOut: L.vCache });
+                                                     positions, eps, qOut: qh, kOut: L.kCache, vOut: L.vCache,
+                                                     ropeTable: ropeTab });
         h.dispose();
       } else {
         const qkv = be.createTensorHandle([S, nqkv], act);
@@ -303,6 +306,7 @@ export class Qwen3ForCausalLM {
       }
       a.dispose();
     }
+    if (ropeTab !== undefined) ropeTab.dispose();
     const logits = be.createTensorHandle([1, cfg.vocabSize], 'float32');
     ops.find('matmul')({ output: logits, M: 1, K: H, N: cfg.vocabSize, batchSize: 1, transposeA: false,
                          transposeB: true, alpha: 1, beta: 0 }, h, this.embed);

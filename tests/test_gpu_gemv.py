@@ -229,8 +229,9 @@ def test_linear_add_rms_norm_matches_separate_launches(hip, M, N, K, rows):
                                               (40, 256, 4, 2, 64, 30), (9, 256, 4, 2, 64, 60)])
 def test_linear_qk_norm_rope_matches_projection_then_rms_norm_rope(hip, S, H, Hq, Hkv, L, pos0):
     """kh_gemm_qk_norm_rope (QKV projection with qk-norm, RoPE and the K/V cache write in its
-    epilogue) against the two launches it replaces -- kh_gemm into [S, (Hq + 2 Hkv) 128], then
-    kh_qk_norm_rope with cache addressing -- bit for bit in q and in both whole caches, on shapes
+    epilogue; again with the angles from kh_rope_table) against the two launches it replaces --
+    kh_gemm into [S, (Hq + 2 Hkv) 128], then kh_qk_norm_rope with cache addressing -- bit for bit
+    in q and in both whole caches, on shapes
     kh_gemm does not split over K (where the model fuses); a ragged last tile (200 rows); positions
     past the cache (pos0 + S > L) write no K/V row, as in the unfused kernel."""
     from kandle_amd import kernels
@@ -269,6 +270,21 @@ def test_linear_qk_norm_rope_matches_projection_then_rms_norm_rope(hip, S, H, Hq
         "q_out": q2, "k_out": k2.handle, "v_out": v2.handle})
     for a, b in ((Tensor(handle=q1), Tensor(handle=q2)), (k1, k2), (v1, v2)):
         assert np.array_equal(a.numpy().view(np.uint32), b.numpy().view(np.uint32))
+    # fused, the angles read from the per-forward table (kh_rope_table): the same bits again
+    tab = kernels.rope_table(pos.handle, inv.handle)
+    angles = np.arange(pos0, pos0 + S, dtype=np.float32)[:, None] * inv.numpy()[None, :]   # f32 products
+    t = tab.data_async()
+    assert t.shape == (S, D // 2, 2)
+    assert np.max(np.abs(t[..., 0] - np.cos(angles.astype(np.float64)))) < 2e-6
+    assert np.max(np.abs(t[..., 1] - np.sin(angles.astype(np.float64)))) < 2e-6
+    k3, v3 = caches()
+    q3 = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+    kernels.linear_qk_norm_rope(x.handle, w.handle, {
+        "q_weight": wq.handle, "k_weight": wk.handle, "inv_freq": inv.handle, "positions": pos.handle, "eps": 1e-6,
+        "q_out": q3, "k_out": k3.handle, "v_out": v3.handle, "rope_table": tab})
+    for a, b in ((Tensor(handle=q1), Tensor(handle=q3)), (k1, k3), (v1, v3)):
+        assert np.array_equal(a.numpy().view(np.uint32), b.numpy().view(np.uint32))
+    tab.dispose()
     if pos0 + S > L:   # rows past the cache were not written
         assert np.array_equal(k2.numpy()[:, :, :pos0].view(np.uint32),
                               oracle.from_bf16_bits(cache0[:, :, :pos0]).view(np.uint32))

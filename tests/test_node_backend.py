@@ -46,7 +46,7 @@ def test_backend_source_strips_to_loadable_javascript(tmp_path):
     r = json.loads(res.stdout.strip().splitlines()[-1])
     assert {"HipBackend", "HipStorage", "HipTensorHandle", "HipTensorIterator", "SimpleOperatorRegistry",
             "registerHipKernels"} <= set(r["exports"])
-    for name in ("flash_attention", "flash_attention_split", "sdpa_masked", "rms_norm", "matmul", "mm", "bmm", "addmm", "baddbmm", "add",
+    for name in ("flash_attention", "flash_attention_split", "rope_table", "sdpa_masked", "rms_norm", "matmul", "mm", "bmm", "addmm", "baddbmm", "add",
                  "mul", "sub", "div", "silu", "silu_mul", "index_select", "argmax", "copy", "contiguous", "cast", "clone",
                  "copy_", "zeros", "ones", "full", "empty", "neg", "cos", "sin", "arange", "decode_attention",
                  "rms_norm_rope", "gemv_fused", "gemv_swiglu", "linear_swiglu", "linear_qk_norm_rope",
