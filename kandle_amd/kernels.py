@@ -800,6 +800,13 @@ def argmax(it: TensorIterator) -> None:
         raise TypeError("argmax: the output must be int32")
     if it.output_numel != P:
         raise ValueError(f"argmax: an output of {tuple(it.output_shape)} for {P} rows")
+    # rows already contiguous in [kept, reduced] order (the last axis of a contiguous input) into a
+    # contiguous int32 output: one launch, no gather or copy
+    o = out.tensor_handle if isinstance(out, IteratorOperand) else out
+    if axes == list(range(len(kept), nd)) and x.is_contiguous() and o.is_contiguous() and o.numel == P and \
+            (not isinstance(out, IteratorOperand) or out.offset == o.offset):
+        _lib.call("kh_argmax", _vp(x.data_ptr()), P, R, _vp(o.data_ptr()), x.kh_dtype)
+        return
     pshape = tuple(x.shape[i] for i in perm)
     rows = HipTensorHandle.create_new(pshape, x.dtype)
     idx = HipTensorHandle.create_new(tuple(it.output_shape), INT32)

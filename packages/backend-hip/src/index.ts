@@ -643,6 +643,15 @@ function argmaxKernel(iter: TensorIterator): void {
   if (dt !== 'int32' && dt !== 'int64') throw new Error('argmax: the output must be an integer tensor');
   const oshape = iteratorShape(iter);
   if (numelOf(oshape) !== P) throw new Error(`argmax: an output of [${oshape}] for ${P} rows`);
+  // rows already contiguous in [kept, reduced] order (the last axes of a contiguous input) into a
+  // contiguous output: one launch, no gather or copy
+  const oh = out.tensorHandle;
+  const trailing = axes.slice().sort((p, q) => p - q).every((a: number, i: number) => a === kept.length + i);
+  if (trailing && x.isContiguous() && oh.isContiguous() && oh.numel === P &&
+      (out.offset === undefined || out.offset === oh.offset)) {
+    addon.argmax(x.ptr, P, R, oh.ptr, x.kh);
+    return;
+  }
   // the input's rows in [kept..., reduced...] order
   const pshape = perm.map((i) => x.shape[i]);
   const g = operandGeometry({ tensorHandle: x, strides: perm.map((i) => x.strides[i]), offset: x.offset }, pshape,
