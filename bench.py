@@ -213,10 +213,24 @@ def prep_decode():
         fn = lambda: kernels.decode_attention(q.handle, kc.handle, vc.handle, sl.handle, o, scale)  # noqa: E731
         wall_ms, dev_ms = time_calls(fn, steps, warmup)
         kv_bytes = float(lens.sum()) * Hkv * D * 2 * 2
-        for t in (q, kc, vc, sl):
+        # Head dim 64 over the same K/V bytes: the caches' storage read as [B, Hkv, 2 ML, 64] rows
+        # (a view, no copy) with twice the C4 lengths.
+        D64 = 64
+        q64 = bf16_tensor(404, (B, Hq, D64))
+        sl64 = Tensor((2 * lens).astype(np.int32), dtype="int32")
+        o64 = HipTensorHandle.create_new((B, Hq, D64), "bfloat16")
+        st64 = (Hkv * 2 * ML * D64, 2 * ML * D64, D64, 1)
+        kc64 = HipTensorHandle.create_view(kc.handle.storage, (B, Hkv, 2 * ML, D64), "bfloat16", st64, 0)
+        vc64 = HipTensorHandle.create_view(vc.handle.storage, (B, Hkv, 2 * ML, D64), "bfloat16", st64, 0)
+        fn64 = lambda: kernels.decode_attention(q64.handle, kc64, vc64, sl64.handle, o64,  # noqa: E731
+                                                1.0 / np.sqrt(D64))
+        wall64, dev64 = time_calls(fn64, steps, warmup)
+        for t in (q, kc, vc, sl, q64, sl64):
             t.dispose()
-        o.dispose()
-        return {"B": B, "sum_len": int(lens.sum()), "bytes": kv_bytes, "wall_ms": wall_ms, "dev_ms": dev_ms}
+        for h in (o, o64, kc64, vc64):
+            h.dispose()
+        return {"B": B, "sum_len": int(lens.sum()), "bytes": kv_bytes, "wall_ms": wall_ms, "dev_ms": dev_ms,
+                "d64": {"sum_len": int(2 * lens.sum()), "wall_ms": wall64, "dev_ms": dev64}}
     return run
 
 
@@ -1073,6 +1087,11 @@ def main():
                           "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
                                        "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
                                        "traffic": measured_traffic("decode")}}
+        d64 = d["d64"]
+        line["decode"]["head_dim_64"] = {
+            "workload": "B=8, Hq=16, Hkv=8, D=64, L = 2 x the C4 lengths (the same K/V bytes)",
+            "sum_len": d64["sum_len"], "ms": round(d64["dev_ms"], 4),
+            "GB/s": round(d["bytes"] / (d64["dev_ms"] * 1e-3) / 1e9, 1)}
         if "value" not in line:
             line.update({"value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(d["wall_ms"], 4),
                          "config": {"workload": "C4 decode attention"}})

@@ -291,7 +291,8 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out,
  * Shapes q [batch, hq, lq, d], k/v [batch, hkv, lk, d], o [batch, hq, lq, d]; `strides` holds 12
  * element strides: q (batch, head, seq), k (…), v (…), o (…); the d axis is contiguous.
  * bf16 with d == 64 or 128 runs the MFMA flash kernel; fp32 with d in {32, 64, 96, 128} the fp32
- * MFMA flash kernel; lq == 1 runs split-K decode; otherwise a LDS-tiled fp32-math kernel
+ * MFMA flash kernel; lq == 1 without causal masking, d == 64 or 128, GQA ratio 1, 2, 4 or 8 and
+ * 16-byte aligned q / k / v rows runs split-K decode; otherwise a LDS-tiled fp32-math kernel
  * (d <= 256).  Replaces the `flash_attention` kernel
  * (reference signature packages/types/src/backend/register.ts:102-109; semantics
  * packages/backend-webgpu/src/kernels/attention/builder.ts:138-329; called from
@@ -333,7 +334,8 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
  * for 1-token decode, reference packages/model-utils/src/attention/gqa.ts:333-336).
  * q [batch, hq, d], o [batch, hq, d] (strides: batch, head), caches [batch, hkv, max_len, d]
  * (strides: batch, head, seq).  `strides` holds 10 values: q (b, h), k (b, h, s), v (b, h, s),
- * o (b, h).  Split-K over the sequence with a log-sum-exp merge; bf16 or f32.
+ * o (b, h).  Split-K over the sequence with a log-sum-exp merge; bf16 or f32; d == 64 or 128;
+ * hq / hkv in {1, 2, 4, 8}; q and the caches 16-byte aligned with strides in 16-byte units.
  * Varlen extension of flash_attention for StaticKVCache views
  * (reference: packages/model-utils/src/kv-cache.ts:197-211; register.ts:102-109). */
 int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
@@ -345,8 +347,9 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
  * process ends, its address taken once at kh_init) instead of the caching allocator.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory during the
  * call (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Limit: batch * hq * ceil(max_len / 256) * 520 bytes (bf16; ceil(max_len / 64) for f32) must not
- * exceed 16 MiB (e.g. 8 sequences x 16 heads up to max_len 32768), else KH_ERR_INVALID.  All calls
+ * Limit: batch * hq * ceil(max_len / C) * (d + 2) * 4 bytes, C = 256 keys (bf16, d == 128), 128
+ * (f32, 128), 512 (bf16, 64) or 256 (f32, 64), must not exceed 16 MiB (e.g. 8 sequences x 16
+ * heads up to max_len 32768 in bf16 at d == 128), else KH_ERR_INVALID.  All calls
  * on one GPU share the array: calls that overlap on one GPU (from another stream) race. */
 int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
                                 const int32_t* seq_lens, int batch, int hq, int hkv, int d, int64_t max_len,

@@ -123,8 +123,10 @@ constexpr int DC_WAVES = 4;
 // Keys per wave per unit: 16 load instructions of 16 B per lane for K and for V in both dtypes.
 template <typename T>
 constexpr int dc_kpw() { return sizeof(T) == 2 ? 64 : 32; }
-template <typename T>
-constexpr int dc_chunk() { return DC_WAVES * dc_kpw<T>(); }
+// Keys per split-K chunk.  Head dim 64 halves the bytes of a key row, so a chunk holds twice the
+// keys and moves the same 64 KiB of K (and of V) per workgroup.
+template <typename T, int DH = 128>
+constexpr int dc_chunk() { return DC_WAVES * dc_kpw<T>() * (128 / DH); }
 
 // Key count of sequence b: seq_lens[b] (or the uniform length when seq_lens is NULL), clamped to
 // [0, max_len] so that a bad device-side length can never index past the cache.
@@ -133,33 +135,38 @@ __device__ __forceinline__ int decode_len(const int32_t* lens, int uniform_len, 
   return L < 0 ? 0 : (L > max_len ? max_len : L);
 }
 
-// Split-K partials: the column sums o of a (sequence, query head, chunk) as one 512-byte row, so the
-// merge reads whole 128-byte lines of it, and the (max, denominator) pairs in an array of their own.
-// Both kernels run on a grid whose z extent is the batch.
+// Split-K partials: the column sums o of a (sequence, query head, chunk) as one row of DH floats
+// (512 bytes at head dim 128), so the merge reads whole 128-byte lines of it, and the (max,
+// denominator) pairs in an array of their own.  Both kernels run on a grid whose z extent is the
+// batch.
 __device__ __forceinline__ float* decode_part_o(float* part) { return part; }
 __device__ __forceinline__ const float* decode_part_o(const float* part) { return part; }
+template <int DH = 128>
 __device__ __forceinline__ float2* decode_part_ml(float* part, int hq, int max_chunks) {
-  return reinterpret_cast<float2*>(part + (int64_t)gridDim.z * hq * max_chunks * 128);
+  return reinterpret_cast<float2*>(part + (int64_t)gridDim.z * hq * max_chunks * DH);
 }
+template <int DH = 128>
 __device__ __forceinline__ const float2* decode_part_ml(const float* part, int hq, int max_chunks) {
-  return reinterpret_cast<const float2*>(part + (int64_t)gridDim.z * hq * max_chunks * 128);
+  return reinterpret_cast<const float2*>(part + (int64_t)gridDim.z * hq * max_chunks * DH);
 }
 
-template <typename T, int G>
+template <typename T, int G, int DH = 128>
 __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                              const T* __restrict__ V, const int32_t* __restrict__ lens,
                                                              int uniform_len, int max_len, int hq, int hkv,
                                                              AttnStrides st, float scale, int max_chunks,
                                                              float* __restrict__ part) {
-  // Layout of `part` (decode_part_o / decode_part_ml): o[b][hq][max_chunks][128] floats, then
+  // Layout of `part` (decode_part_o / decode_part_ml): o[b][hq][max_chunks][DH] floats, then
   // (m, l)[b][hq][max_chunks] float pairs; valid chunks only.  decode_merge_cols_kernel combines them.
-  constexpr int D = 128;
+  // Head dim 64 halves the lanes of a key row and doubles the keys of a chunk.
+  constexpr int D = DH;
   constexpr int EPL = 16 / (int)sizeof(T);            // elements per 16-byte load
-  constexpr int LPK = D / EPL;                        // lanes per key row (16 bf16, 32 f32)
-  constexpr int KPI = 64 / LPK;                       // keys per load instruction (4 bf16, 2 f32)
-  constexpr int KPW = dc_kpw<T>();
-  constexpr int CHUNK = dc_chunk<T>();
+  constexpr int LPK = D / EPL;                        // lanes per key row (16 bf16, 32 f32 at D = 128)
+  constexpr int KPI = 64 / LPK;                       // keys per load instruction (4 bf16, 2 f32 at 128)
+  constexpr int KPW = dc_kpw<T>() * (128 / DH);
+  constexpr int CHUNK = dc_chunk<T, DH>();
   constexpr int NI = KPW / KPI;                       // load instructions per wave (16)
+  static_assert(DH == 128 || DH == 64, "head dim 64 or 128");
   __shared__ float red_m[DC_WAVES][G];
   __shared__ float red_l[DC_WAVES][G];
   __shared__ float red_o[DC_WAVES][G][D];
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
       Os += red_o[ww][gi][d] * f;
     }
     const int64_t row = ((int64_t)b * hq + hk * G + gi) * max_chunks + chunk;
-    if (d == 0) decode_part_ml(part, hq, max_chunks)[row] = make_float2(M, Ls);
+    if (d == 0) decode_part_ml<DH>(part, hq, max_chunks)[row] = make_float2(M, Ls);
     decode_part_o(part)[row * D + d] = Os;
   }
 }
@@ -380,6 +387,9 @@ struct Row8 {
 // states (m, l, o) -- no cross-row shuffles.  The 16 states of the workgroup (4 waves x 4 rows)
 // are combined once through LDS.  A wave covers 16 key rows per slot with bf16 (64 keys, chunks
 // of 256) and 8 with fp32 (32 keys, chunks of 128), so both keep 16 KiB of K and V in flight.
+// Head dim DH = 64: 8 lanes (half a DPP row) hold a key row and sum by a 3-step DPP reduction, so
+// a load instruction covers 8 keys, a wave 128 (bf16) or 64 (fp32) and the workgroup keeps 32
+// softmax states; the bytes in flight per lane are the same as at 128.
 // FUSE (decode attention block, one sequence): Q holds the raw q heads; each workgroup applies
 // qk-norm + RoPE to its G heads (rounded to bf16 as the unfused path stores them, or kept in fp32
 // with fp32 caches).  The wave whose keys include the new token p normalises and rotates that
@@ -387,7 +397,7 @@ struct Row8 {
 // (the stale cache row it loaded is masked): the new key joins the softmax state of the DPP row
 // that owns it, with no data dependence on the cache write.  Only this workgroup reads row p in
 // this launch.
-template <typename T, int G, bool FUSE = false>
+template <typename T, int G, bool FUSE = false, int DH = 128>
 __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                                   const T* __restrict__ V,
                                                                   const int32_t* __restrict__ lens, int uniform_len,
@@ -395,8 +405,10 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
                                                                   float scale, int max_chunks,
                                                                   float* __restrict__ part, DecodeFuse fz) {
   constexpr bool F32 = sizeof(T) == 4;
-  constexpr int D = 128, NI = F32 ? 8 : 16, KPI = 4, KPW = NI * KPI, CHUNK = DC_WAVES * KPW, NS = DC_WAVES * KPI;
-  static_assert(CHUNK == dc_chunk<T>(), "chunk size shared with the merge");
+  static_assert(DH == 128 || (DH == 64 && !FUSE), "head dim 128, or 64 without the fused block");
+  constexpr int D = DH, LPR = D / 8, NI = F32 ? 8 : 16, KPI = 64 / LPR, KPW = NI * KPI, CHUNK = DC_WAVES * KPW,
+                NS = DC_WAVES * KPI;
+  static_assert(CHUNK == dc_chunk<T, DH>(), "chunk size shared with the merge");
   __shared__ float red_m[NS][G];
   __shared__ float red_l[NS][G];
   __shared__ float red_o[NS][G][D];
@@ -414,8 +426,8 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
   }
   if (chunk * CHUNK >= L) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int sub = lane & 15;  // 8-column group of the key row
-  const int kk = lane >> 4;   // key slot (DPP row) inside a load instruction
+  const int sub = lane & (LPR - 1);  // 8-column group of the key row
+  const int kk = lane / LPR;         // key slot (group of LPR lanes) inside a load instruction
   const int key0 = chunk * CHUNK + w * KPW;
 
   float qv[G][8];
@@ -471,7 +483,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
     // The new key's row, normalised and rotated (every wave computes it: one row), and the DPP row
     // of this wave that owns key p (if any) writes it and the v row into the caches.
     const int rel = praw - key0;  // the new key relative to this wave's first key
-    newkey = praw < max_len && rel >= 0 && rel < KPW && kk == (rel & 3);
+    newkey = praw < max_len && rel >= 0 && rel < KPW && kk == (rel & (KPI - 1));
     float a[8];
     knr.to_f32(a);
     unpack8(wkr, wv);
@@ -507,7 +519,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
       float d = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) d += qv[gi][j] * kf[j];
-      d = row16_sum(d);
+      d = group_sum<LPR>(d);
       sc[gi][it] = valid ? d : -INFINITY;
     }
   }
@@ -522,7 +534,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
       float d = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) d += qv[gi][j] * kf[j];
-      d = row16_sum(d);
+      d = group_sum<LPR>(d);
       sn_new[gi] = newkey ? d : -INFINITY;
     }
   }
@@ -574,7 +586,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
       Os += red_o[s2][gi][d] * f;
     }
     const int64_t row = ((int64_t)b * hq + hk * G + gi) * max_chunks + chunk;
-    if (d == 0) decode_part_ml(part, hq, max_chunks)[row] = make_float2(M, Ls);
+    if (d == 0) decode_part_ml<DH>(part, hq, max_chunks)[row] = make_float2(M, Ls);
     decode_part_o(part)[row * D + d] = Os;
   }
 }
@@ -582,21 +594,21 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
 // Merge by column groups: workgroup (cg, h, b) produces columns 32 cg .. 32 cg + 31 of query head
 // h.  8 groups of 32 threads (one per column) each run one online log-sum-exp pass over every 8th
 // chunk (running max, denominator and column sum, rescaled when the max grows), and the 8 group
-// states are combined through LDS.
-template <typename T>
+// states are combined through LDS.  The grid's x extent is DH / 32.
+template <typename T, int DH = 128>
 __device__ __forceinline__ void decode_merge_cols_body(const float* __restrict__ part, int L, int hq, int max_chunks,
                                                        const AttnStrides& st, T* __restrict__ O) {
-  constexpr int D = 128, COLS = 32, NG = 8;
+  constexpr int D = DH, COLS = 32, NG = 8;
   __shared__ float gm[NG], gl[NG];
   __shared__ float gacc[NG][COLS];
   const int cg = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int col = tid & (COLS - 1), grp = tid >> 5;
   const int d = cg * COLS + col;
-  const int nch = (L + dc_chunk<T>() - 1) / dc_chunk<T>();
+  const int nch = (L + dc_chunk<T, DH>() - 1) / dc_chunk<T, DH>();
   const int64_t row0 = ((int64_t)b * hq + h) * max_chunks;
   const float* po = decode_part_o(part) + row0 * D + d;
-  const float2* pml = decode_part_ml(part, hq, max_chunks) + row0;
+  const float2* pml = decode_part_ml<DH>(part, hq, max_chunks) + row0;
 
   float m = -INFINITY, l = 0.f, acc = 0.f;
   // Fold chunk (mc, lc, oc) into the running state.
@@ -646,12 +658,12 @@ __device__ __forceinline__ void decode_merge_cols_body(const float* __restrict__
   }
 }
 
-template <typename T>
+template <typename T, int DH = 128>
 __global__ __launch_bounds__(256) void decode_merge_cols_kernel(const float* __restrict__ part,
                                                                 const int32_t* __restrict__ lens, int uniform_len,
                                                                 int max_len, int hq, int max_chunks, AttnStrides st,
                                                                 T* __restrict__ O) {
-  decode_merge_cols_body<T>(part, decode_len(lens, uniform_len, blockIdx.z, max_len), hq, max_chunks, st, O);
+  decode_merge_cols_body<T, DH>(part, decode_len(lens, uniform_len, blockIdx.z, max_len), hq, max_chunks, st, O);
 }
 
 // The merge of the fused decode block (one sequence, length *position + 1): the same kernel body
@@ -689,41 +701,47 @@ AttnStrides load_strides(const int64_t* s) {
 }
 
 // Bytes of split-K partials launch_decode needs: o rows + (m, l) per (sequence, head, chunk).
-template <typename T>
+template <typename T, int DH = 128>
 size_t decode_part_bytes(int batch, int hq, int64_t max_len) {
-  const int64_t max_chunks = (max_len + dc_chunk<T>() - 1) / dc_chunk<T>();
-  return (size_t)batch * hq * max_chunks * (128 + 2) * sizeof(float);
+  const int64_t max_chunks = (max_len + dc_chunk<T, DH>() - 1) / dc_chunk<T, DH>();
+  return (size_t)batch * hq * max_chunks * (DH + 2) * sizeof(float);
+}
+
+size_t decode_part_bytes_for(int dtype, int d, int batch, int hq, int64_t max_len) {
+  if (dtype == KH_BF16)
+    return d == 64 ? decode_part_bytes<uint16_t, 64>(batch, hq, max_len) : decode_part_bytes<uint16_t>(batch, hq, max_len);
+  return d == 64 ? decode_part_bytes<float, 64>(batch, hq, max_len) : decode_part_bytes<float>(batch, hq, max_len);
 }
 
 // part_in: the partials buffer (at least decode_part_bytes), or nullptr to take one from the
 // caching allocator for the duration of the call.
-template <typename T>
+template <typename T, int DH = 128>
 int launch_decode(const void* q, const void* k, const void* v, void* o, const int32_t* lens, int uniform_len,
                   int batch, int hq, int hkv, int64_t max_len, const AttnStrides& st, float scale,
                   float* part_in = nullptr) {
   const int G = hq / hkv;
   KH_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "kh_decode_attention: hq/hkv = %d not in {1, 2, 4, 8}", G);
   const int64_t lim = int64_t(1) << 31;
-  KH_REQUIRE((max_len + dc_chunk<T>()) * st.ks * (int64_t)sizeof(T) < lim &&
-                 (max_len + dc_chunk<T>()) * st.vs * (int64_t)sizeof(T) < lim,
+  constexpr int CH = dc_chunk<T, DH>();
+  KH_REQUIRE((max_len + CH) * st.ks * (int64_t)sizeof(T) < lim && (max_len + CH) * st.vs * (int64_t)sizeof(T) < lim,
              "kh_decode_attention: one head of the cache spans more than 2 GiB");
   const int ml = (int)max_len;
-  const int max_chunks = (ml + dc_chunk<T>() - 1) / dc_chunk<T>();
+  const int max_chunks = (ml + CH - 1) / CH;
   KH_REQUIRE(max_chunks <= 65535 * 64, "kh_decode_attention: max_len too large");
-  float* part = part_in ? part_in : (float*)scratch_alloc(decode_part_bytes<T>(batch, hq, max_len));
+  float* part = part_in ? part_in : (float*)scratch_alloc(decode_part_bytes<T, DH>(batch, hq, max_len));
   if (!part) return KH_ERR_OOM;
   dim3 grid(max_chunks, hkv, batch);
   const T* Q = (const T*)q;
   const T* K = (const T*)k;
   const T* V = (const T*)v;
+  // bf16 takes the DPP-row kernel, fp32 the shuffle one (each measured the faster for its type).
 #define KH_DECODE_CASE(GG)                                                                                 \
   case GG:                                                                                                 \
     if constexpr (sizeof(T) == 2)                                                                          \
-      decode_partial_rows_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv,  \
-                                                                    st, scale, max_chunks, part,           \
-                                                                    DecodeFuse{});                         \
+      decode_partial_rows_kernel<T, GG, false, DH><<<grid, 256, 0, stream()>>>(                            \
+          Q, K, V, lens, uniform_len, ml, hq, hkv, st, scale, max_chunks, part, DecodeFuse{});             \
     else                                                                                                   \
-      decode_partial_kernel<T, GG><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st,  \
+      decode_partial_kernel<T, GG, DH><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st,  \
                                                                 scale, max_chunks, part);                  \
     break;
   switch (G) {
@@ -735,9 +753,8 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
 #undef KH_DECODE_CASE
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
-    decode_merge_cols_kernel<T><<<dim3(4, hq, batch), 256, 0, stream()>>>(part, lens, uniform_len, ml, hq,
-                                                                          max_chunks, st,
-                                                                  (T*)o);
+    decode_merge_cols_kernel<T, DH><<<dim3(DH / 32, hq, batch), 256, 0, stream()>>>(part, lens, uniform_len, ml,
+                                                                                    hq, max_chunks, st, (T*)o);
     e = hipGetLastError();
   }
   if (!part_in) scratch_free(part);  // stream-ordered: the block is reused only by later work on the same stream
@@ -747,6 +764,27 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   }
   KH_DEBUG_SYNC();
   return KH_OK;
+}
+
+// launch_decode for the element type `dtype` and head dim d (64 or 128).
+int launch_decode_for(int dtype, int d, const void* q, const void* k, const void* v, void* o, const int32_t* lens,
+                      int uniform_len, int batch, int hq, int hkv, int64_t max_len, const AttnStrides& st,
+                      float scale, float* part_in = nullptr) {
+  if (dtype == KH_BF16)
+    return d == 64 ? launch_decode<uint16_t, 64>(q, k, v, o, lens, uniform_len, batch, hq, hkv, max_len, st, scale,
+                                                 part_in)
+                   : launch_decode<uint16_t>(q, k, v, o, lens, uniform_len, batch, hq, hkv, max_len, st, scale,
+                                             part_in);
+  return d == 64 ? launch_decode<float, 64>(q, k, v, o, lens, uniform_len, batch, hq, hkv, max_len, st, scale, part_in)
+                 : launch_decode<float>(q, k, v, o, lens, uniform_len, batch, hq, hkv, max_len, st, scale, part_in);
+}
+
+// q, the caches and their batch / head / row strides on 16-byte boundaries (the decode kernels
+// read 16-byte words of q, K and V rows).
+bool decode_aligned(const void* q, const void* k, const void* v, const AttnStrides& st, int dtype) {
+  const int64_t vec = dtype == KH_BF16 ? 8 : 4;
+  return aligned16(q) && aligned16(k) && aligned16(v) && st.qb % vec == 0 && st.qh % vec == 0 && st.kb % vec == 0 &&
+         st.kh % vec == 0 && st.ks % vec == 0 && st.vb % vec == 0 && st.vh % vec == 0 && st.vs % vec == 0;
 }
 
 int launch_generic(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
@@ -802,16 +840,13 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
   KH_REQUIRE(lk > 0, "kh_flash_attention: the key sequence is empty (softmax over no keys is undefined)");
 
   // One query row, no mask: split-K decode over the keys (the caller's 1-token decode step).
-  const int64_t vec = dtype == KH_BF16 ? 8 : 4;
-  const bool decode_ok = lq == 1 && !causal && d == 128 && (G == 1 || G == 2 || G == 4 || G == 8) && aligned16(k) &&
-                         aligned16(v) && st.kb % vec == 0 && st.kh % vec == 0 && st.ks % vec == 0 &&
-                         st.vb % vec == 0 && st.vh % vec == 0 && st.vs % vec == 0;
+  const bool decode_ok = lq == 1 && !causal && (d == 128 || d == 64) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+                         batch <= 65535 && decode_aligned(q, k, v, st, dtype);
   if (decode_ok) {
     AttnStrides ds = st;
     ds.qs = 0;
     ds.os = 0;
-    if (dtype == KH_BF16) return launch_decode<uint16_t>(q, k, v, o, nullptr, (int)lk, batch, hq, hkv, lk, ds, scale);
-    return launch_decode<float>(q, k, v, o, nullptr, (int)lk, batch, hq, hkv, lk, ds, scale);
+    return launch_decode_for(dtype, d, q, k, v, o, nullptr, (int)lk, batch, hq, hkv, lk, ds, scale);
   }
   // The MFMA kernel's softmax takes the raw q.k maximum as its reference, which is only the largest
   // scaled score for scale > 0; other scales take the generic kernel.
@@ -919,7 +954,7 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   KH_REQUIRE_INIT();
   KH_REQUIRE(batch >= 0 && hq > 0 && hkv > 0 && max_len > 0, "kh_decode_attention: bad extents");
   KH_REQUIRE(hq % hkv == 0, "kh_decode_attention: numHeadsQ (%d) must be divisible by numHeadsKV (%d)", hq, hkv);
-  KH_REQUIRE(d == 128, "kh_decode_attention: head_dim %d not supported (128 only)", d);
+  KH_REQUIRE(d == 128 || d == 64, "kh_decode_attention: head_dim %d not supported (64 or 128)", d);
   KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_decode_attention: unsupported dtype %d", dtype);
   KH_REQUIRE(max_len <= INT32_MAX, "kh_decode_attention: max_len too large");
   if (batch == 0) return KH_OK;
@@ -930,13 +965,9 @@ int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   st.kb = strides[2]; st.kh = strides[3]; st.ks = strides[4];
   st.vb = strides[5]; st.vh = strides[6]; st.vs = strides[7];
   st.ob = strides[8]; st.oh = strides[9]; st.os = 0;
-  const int64_t vec = dtype == KH_BF16 ? 8 : 4;
-  KH_REQUIRE(aligned16(k_cache) && aligned16(v_cache) && st.kb % vec == 0 && st.kh % vec == 0 && st.ks % vec == 0 &&
-                 st.vb % vec == 0 && st.vh % vec == 0 && st.vs % vec == 0,
-             "kh_decode_attention: caches must be 16-byte aligned with 16-byte aligned strides");
-  if (dtype == KH_BF16)
-    return launch_decode<uint16_t>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
-  return launch_decode<float>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
+  KH_REQUIRE(decode_aligned(q, k_cache, v_cache, st, dtype),
+             "kh_decode_attention: q and the caches must be 16-byte aligned with 16-byte aligned strides");
+  return launch_decode_for(dtype, d, q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale);
 }
 
 int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
@@ -946,14 +977,13 @@ int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* 
   KH_REQUIRE(batch >= 0 && hq > 0 && hkv > 0 && max_len > 0, "kh_decode_attention_noalloc: bad extents");
   KH_REQUIRE(hq % hkv == 0, "kh_decode_attention_noalloc: numHeadsQ (%d) must be divisible by numHeadsKV (%d)", hq,
              hkv);
-  KH_REQUIRE(d == 128, "kh_decode_attention_noalloc: head_dim %d not supported (128 only)", d);
+  KH_REQUIRE(d == 128 || d == 64, "kh_decode_attention_noalloc: head_dim %d not supported (64 or 128)", d);
   KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_decode_attention_noalloc: unsupported dtype %d", dtype);
   KH_REQUIRE(max_len <= INT32_MAX, "kh_decode_attention_noalloc: max_len too large");
   if (batch == 0) return KH_OK;
   KH_REQUIRE(batch <= 65535, "kh_decode_attention_noalloc: batch too large");
   KH_REQUIRE(q && k_cache && v_cache && o && seq_lens && strides, "kh_decode_attention_noalloc: null pointer");
-  const size_t need = dtype == KH_BF16 ? decode_part_bytes<uint16_t>(batch, hq, max_len)
-                                       : decode_part_bytes<float>(batch, hq, max_len);
+  const size_t need = decode_part_bytes_for(dtype, d, batch, hq, max_len);
   KH_REQUIRE(need <= kNoAllocScratchBytes,
              "kh_decode_attention_noalloc: batch %d x %d heads x %lld keys needs %zu bytes of split-K partials, "
              "more than the %zu-byte scratch array (use kh_decode_attention)",
@@ -966,14 +996,10 @@ int kh_decode_attention_noalloc(const void* q, const void* k_cache, const void* 
   st.kb = strides[2]; st.kh = strides[3]; st.ks = strides[4];
   st.vb = strides[5]; st.vh = strides[6]; st.vs = strides[7];
   st.ob = strides[8]; st.oh = strides[9]; st.os = 0;
-  const int64_t vec = dtype == KH_BF16 ? 8 : 4;
-  KH_REQUIRE(aligned16(k_cache) && aligned16(v_cache) && st.kb % vec == 0 && st.kh % vec == 0 && st.ks % vec == 0 &&
-                 st.vb % vec == 0 && st.vh % vec == 0 && st.vs % vec == 0,
-             "kh_decode_attention_noalloc: caches must be 16-byte aligned with 16-byte aligned strides");
+  KH_REQUIRE(decode_aligned(q, k_cache, v_cache, st, dtype),
+             "kh_decode_attention_noalloc: q and the caches must be 16-byte aligned with 16-byte aligned strides");
   float* part = (float*)g_scratch_ptr[dev];
-  if (dtype == KH_BF16)
-    return launch_decode<uint16_t>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale, part);
-  return launch_decode<float>(q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale, part);
+  return launch_decode_for(dtype, d, q, k_cache, v_cache, o, seq_lens, 0, batch, hq, hkv, max_len, st, scale, part);
 }
 
 int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,

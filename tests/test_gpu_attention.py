@@ -256,6 +256,45 @@ def test_decode_c4_full_size(hip):
         t.dispose()
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (8, 4), (16, 4), (16, 2)])
+def test_decode_head_dim_64_matches_oracle(hip, dtype, Hq, Hkv):
+    """Head dim 64 (8 lanes per key row; 512-key chunks in bf16, 256 in fp32): lengths on and off
+    the chunk edges, an empty sequence (zeros) and a one-key one, GQA 1/2/4/8; repeatable."""
+    lens = np.array([0, 1, 255, 256, 512, 513, 1999], np.int32)
+    B, D, ML = len(lens), 64, 2000
+    q, qh = seeded(85, (B, Hq, D), dtype)
+    kc, kch = seeded(86, (B, Hkv, ML, D), dtype)
+    vc, vch = seeded(87, (B, Hkv, ML, D), dtype)
+    sl = Tensor(lens, dtype="int32")
+    outs = [F.decode_attention(q, kc, vc, sl).numpy() for _ in range(2)]
+    assert np.array_equal(outs[0], outs[1])
+    assert np.all(outs[0][0] == 0.0)
+    ref = oracle.sdpa(qh[1:, :, None, :], kch[1:], vch[1:], kv_len=lens[1:])[:, :, 0, :]
+    if dtype == "float32":
+        assert max_rel(outs[0][1:], ref) < F32_RTOL
+        assert_close_elem(outs[0][1:], ref, what="decode D=64 fp32")
+    else:
+        assert np.max(np.abs(outs[0][1:] - ref)) < BF16_ATOL
+    for t in (q, kc, vc, sl):
+        t.dispose()
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_sdpa_single_query_head_dim_64_routes_to_decode(hip, dtype):
+    """Lq = 1 at head dim 64 through the SDPA entry point (the split-K decode kernels)."""
+    q, qh = seeded(88, (2, 8, 1, 64), dtype)
+    k, kh = seeded(89, (2, 2, 1300, 64), dtype)
+    v, vh = seeded(90, (2, 2, 1300, 64), dtype)
+    out = _sdpa_gpu(q, k, v, False)
+    ref = oracle.sdpa(qh, kh, vh)
+    if dtype == "float32":
+        assert max_rel(out, ref) < F32_RTOL
+        assert_close_elem(out, ref, what="sdpa Lq=1 D=64 fp32")
+    else:
+        assert np.max(np.abs(out - ref)) < BF16_ATOL
+
+
 def test_flash_c3_full_size(hip):
     """Config C3 at full size (B=4, Hq=16, Hkv=8, S=4096, D=128, causal, bf16): every row of two
     whole (batch, head) slices (the first and the last, 4096 query rows each, every causal key

@@ -30,26 +30,28 @@ def _stats():
     return s.live_bytes, s.cached_bytes, s.n_device_allocs, s.n_cache_hits
 
 
-@pytest.mark.parametrize("dtype,cases", [
-    ("bfloat16", [(8, 16, 8, 32768, 2024), (2, 16, 2, 1500, 7)]),   # the C4 shape, then a smaller call
-    ("float32", [(4, 16, 8, 4096, 31), (1, 8, 8, 300, 37)])])
-def test_noalloc_decode_matches_allocating_entry_point(hip, dtype, cases):
+@pytest.mark.parametrize("dtype,D,cases", [
+    ("bfloat16", 128, [(8, 16, 8, 32768, 2024), (2, 16, 2, 1500, 7)]),   # the C4 shape, then a smaller call
+    ("float32", 128, [(4, 16, 8, 4096, 31), (1, 8, 8, 300, 37)]),
+    ("bfloat16", 64, [(4, 16, 4, 5000, 41), (1, 8, 8, 700, 43)]),        # head dim 64: 512-key chunks
+    ("float32", 64, [(2, 16, 2, 3000, 47), (1, 4, 4, 200, 53)])])
+def test_noalloc_decode_matches_allocating_entry_point(hip, dtype, D, cases):
     for B, Hq, Hkv, ML, seed in cases:
         lens = syn.randint(seed, (B,), 1, ML + 1)
-        q, _ = seeded(seed + 1, (B, Hq, 128), dtype)
-        kc, _ = seeded(seed + 2, (B, Hkv, ML, 128), dtype)
-        vc, _ = seeded(seed + 3, (B, Hkv, ML, 128), dtype)
+        q, _ = seeded(seed + 1, (B, Hq, D), dtype)
+        kc, _ = seeded(seed + 2, (B, Hkv, ML, D), dtype)
+        vc, _ = seeded(seed + 3, (B, Hkv, ML, D), dtype)
         sl = Tensor(lens, dtype="int32")
-        o_ref = HipTensorHandle.create_new((B, Hq, 128), dtype)
-        o_na = HipTensorHandle.create_new((B, Hq, 128), dtype)
-        _lib.call("kh_decode_attention", *_args(q, kc, vc, o_ref, sl, 1 / np.sqrt(128)))
+        o_ref = HipTensorHandle.create_new((B, Hq, D), dtype)
+        o_na = HipTensorHandle.create_new((B, Hq, D), dtype)
+        _lib.call("kh_decode_attention", *_args(q, kc, vc, o_ref, sl, 1 / np.sqrt(D)))
         _lib.synchronize()
         before = _stats()
-        _lib.call("kh_decode_attention_noalloc", *_args(q, kc, vc, o_na, sl, 1 / np.sqrt(128)))
+        _lib.call("kh_decode_attention_noalloc", *_args(q, kc, vc, o_na, sl, 1 / np.sqrt(D)))
         _lib.synchronize()
         assert _stats() == before, "the allocation-free entry point touched the caching allocator"
         a, b = o_ref.data_async(), o_na.data_async()
-        assert np.all(np.isfinite(a)) and np.array_equal(a.view(np.uint32), b.view(np.uint32)), (dtype, B, ML)
+        assert np.all(np.isfinite(a)) and np.array_equal(a.view(np.uint32), b.view(np.uint32)), (dtype, D, B, ML)
         for t in (q, kc, vc, sl):
             t.dispose()
         o_ref.dispose()
