@@ -16,7 +16,8 @@
 // probabilities enter as the B operand straight from the score registers (step s uses key
 // 8(s/4) + 4g + s%4, the key that lane's score s belongs to).  All of a lane's outputs belong to one
 // query, so the online-softmax rescale is a per-lane multiply.  At the end the waves' (m, l, O)
-// are combined through LDS, in wave order.
+// are combined through LDS, in wave order.  Inputs at head dim 128 whose 32-query blocks give
+// fewer workgroups than CUs take 16-query blocks (flash_f32_q16_kernel, below).
 #include <cmath>
 
 #include "attention.h"
@@ -208,6 +209,184 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restr
   }
 }
 
+// 16-query blocks for inputs whose 32-query blocks give fewer workgroups than CUs (C1: 16 heads x 8
+// blocks = 128 workgroups on 256 CUs): twice the workgroups and half of the heaviest block's MFMA
+// work, which bounds the call.  Same online softmax with v_mfma_f32_16x16x4_f32: per 32-key tile
+// the wave forms S^T = K Q^T as two 16-key blocks kb in D/4 steps (step s pairs head-dim element
+// j D/4 + s of lane group j = lane >> 4), so lane (r, j) = (lane & 15, lane >> 4) holds query r's
+// scores against keys 16 kb + 4 j + i (i < 4): a query's maximum and sum are an in-lane reduction
+// plus exchanges with lanes ^ 16 and ^ 32.  O^T = V^T P^T follows in 8 steps per 16 head-dim
+// columns; step (kb, i) takes key 16 kb + 4 j + i from lane group j, the score that lane holds in
+// its register (kb, i).  Every output of a lane belongs to query r (columns 16 db + 4 j + i).
+// Eight waves (two per SIMD) split a block's tiles; K loads at the tile start, V during QK^T.
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(NW * 64) void flash_f32_q16_kernel(const float* __restrict__ Q,
+                                                                const float* __restrict__ K,
+                                                                const float* __restrict__ V, float* __restrict__ O,
+                                                                int hq, int hkv, int lq, int lk, AttnStrides st,
+                                                                float c, int nqb) {
+  constexpr int QD = D / 4, NQ4 = QD / 4, NDB = D / 16;
+  constexpr int OSTR = D + 4;  // LDS row stride (floats) of the wave partial outputs
+  __shared__ float2 ml_s[NW][16];
+  __shared__ __attribute__((aligned(16))) float o_s[NW][16 * OSTR];
+
+  const int lane = threadIdx.x & 63, r = lane & 15, j = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bid = blockIdx.x;
+  const int qb = nqb - 1 - bid % nqb;  // the longest causal blocks start first
+  const int bh = bid / nqb;
+  const int h = bh % hq, b = bh / hq;
+  const int hk = h / (hq / hkv);
+  const int q0 = qb * 16;
+  const int kend = CAUSAL ? min(lk, q0 + 16) : lk;
+  const int nt = (kend + 31) >> 5;
+
+  const float* Qh = Q + (int64_t)b * st.qb + (int64_t)h * st.qh;
+  const float* Kh = K + (int64_t)b * st.kb + (int64_t)hk * st.kh;
+  const float* Vh = V + (int64_t)b * st.vb + (int64_t)hk * st.vh;
+  const auto rq = make_rsrc(Qh, (uint32_t)(((int64_t)(lq - 1) * st.qs + D) * 4));
+  const auto rk = make_rsrc(Kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 4));
+  const auto rv = make_rsrc(Vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 4));
+  const uint32_t qs = (uint32_t)st.qs, ks = (uint32_t)st.ks, vs = (uint32_t)st.vs;
+
+  // This lane's query row, quarter j of the head dim, pre-scaled (rows past lq read as zero).
+  const int qi = q0 + r;
+  float qv[QD];
+#pragma unroll
+  for (int i = 0; i < NQ4; ++i) {
+    const uint32_t off = qi < lq ? ((uint32_t)qi * qs + j * QD + 4 * i) * 4u : kOut;
+    const float4 t = buf_load16f(rq, off);
+    qv[4 * i] = t.x * c;
+    qv[4 * i + 1] = t.y * c;
+    qv[4 * i + 2] = t.z * c;
+    qv[4 * i + 3] = t.w * c;
+  }
+
+  f32x4 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) oacc[db][v] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  for (int t = w; t < nt; t += NW) {
+    const int k0 = t * 32;
+    // Key rows k0 + 16 kb + r, quarter j (rows past lk read as zero and are masked).
+    float kv[2][QD];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kr = k0 + 16 * kb + r;
+#pragma unroll
+      for (int i = 0; i < NQ4; ++i) {
+        const uint32_t off = kr < lk ? ((uint32_t)kr * ks + j * QD + 4 * i) * 4u : kOut;
+        const float4 x = buf_load16f(rk, off);
+        kv[kb][4 * i] = x.x;
+        kv[kb][4 * i + 1] = x.y;
+        kv[kb][4 * i + 2] = x.z;
+        kv[kb][4 * i + 3] = x.w;
+      }
+    }
+    // V[key(s)][16 db + r] for the keys key(s) = k0 + 16 (s / 4) + 4 j + s % 4 of the PV steps,
+    // requested before QK^T so that they arrive during it.
+    float vv[NDB][8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int kr = k0 + 16 * (s >> 2) + 4 * j + (s & 3);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 16 * db + r) * 4u : kOut;
+        vv[db][s] = buf_load4f(rv, off);
+      }
+    }
+    f32x4 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sacc[kb][v] = 0.f;
+#pragma unroll
+      for (int s = 0; s < QD; ++s) sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kb][s], qv[s], sacc[kb], 0, 0, 0);
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = k0 + 16 * kb + 4 * j + i;
+        const bool ok = key < lk && (!CAUSAL || key <= qi);
+        sacc[kb][i] = ok ? sacc[kb][i] : -INFINITY;
+        tmax = fmaxf(tmax, sacc[kb][i]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mn = fmaxf(m, tmax);
+    const float mu = mn == -INFINITY ? 0.f : mn;  // no key seen yet: every weight is exp2(-inf) = 0
+    const float alpha = fast_exp2(m - mu);
+    float ps = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sacc[kb][i] = fast_exp2(sacc[kb][i] - mu);
+        ps += sacc[kb][i];
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) oacc[db][v] *= alpha;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[db][s], sacc[s >> 2][s & 3], oacc[db], 0, 0, 0);
+    }
+  }
+
+  // Combine the waves: O = sum_w exp2(m_w - M) O_w / sum_w exp2(m_w - M) l_w, M = max_w m_w.
+  if (j == 0) ml_s[w][r] = make_float2(m, l);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 16 * db + 4 * j]) =
+        make_float4(oacc[db][0], oacc[db][1], oacc[db][2], oacc[db][3]);
+  __syncthreads();
+  constexpr int TPQ = NW * 64 / 16;  // threads per query
+  constexpr int CPT = D / TPQ;       // output columns per thread
+  static_assert(CPT % 4 == 0, "whole float4 columns per thread");
+  const int tq = threadIdx.x / TPQ, c0 = (threadIdx.x % TPQ) * CPT;
+  float2 mlw[NW];
+  float M = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < NW; ++u) {
+    mlw[u] = ml_s[u][tq];
+    M = fmaxf(M, mlw[u].x);
+  }
+  const float mu = M == -INFINITY ? 0.f : M;
+  float f[NW], L = 0.f;
+#pragma unroll
+  for (int u = 0; u < NW; ++u) {
+    f[u] = fast_exp2(mlw[u].x - mu);
+    L += mlw[u].y * f[u];
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int qo = q0 + tq;
+  if (qo < lq) {
+    float* orow = O + (int64_t)b * st.ob + (int64_t)h * st.oh + (int64_t)qo * st.os + c0;
+#pragma unroll
+    for (int jj = 0; jj < CPT; jj += 4) {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+      for (int u = 0; u < NW; ++u) {
+        const float4 x = *reinterpret_cast<const float4*>(&o_s[u][tq * OSTR + c0 + jj]);
+        a0 += x.x * f[u];
+        a1 += x.y * f[u];
+        a2 += x.z * f[u];
+        a3 += x.w * f[u];
+      }
+      *reinterpret_cast<float4*>(orow + jj) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
+    }
+  }
+}
+
 template <int D, int NW>
 void launch_f32_dw(const float* q, const float* k, const float* v, float* o, int grid, int hq, int hkv, int lq,
                    int lk, const AttnStrides& st, float c, int nqb, bool causal) {
@@ -256,6 +435,19 @@ int launch_flash_f32(const void* q, const void* k, const void* v, void* o, int b
   const float c = scale * kLog2e;
   const float *Q = (const float*)q, *K = (const float*)k, *V = (const float*)v;
   float* Out = (float*)o;
+  if (d == 128 && grid < cu_count()) {
+    // fewer 32-query blocks than CUs: 16-query blocks (twice the workgroups)
+    const int nqb16 = (lq + 15) / 16;
+    const int grid16 = (int)(grid / nqb * nqb16);
+    if (causal)
+      flash_f32_q16_kernel<128, true, 8><<<grid16, 8 * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c,
+                                                                             nqb16);
+    else
+      flash_f32_q16_kernel<128, false, 8><<<grid16, 8 * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c,
+                                                                              nqb16);
+    KH_CHECK_LAUNCH();
+    return KH_OK;
+  }
   switch (d) {
     case 32: launch_f32_d<32>(Q, K, V, Out, (int)grid, hq, hkv, lq, lk, st, c, nqb, causal); break;
     case 64: launch_f32_d<64>(Q, K, V, Out, (int)grid, hq, hkv, lq, lk, st, c, nqb, causal); break;

@@ -142,10 +142,12 @@ def test_generic_kernel_fp32_odd_head_dim(hip):
     (1, 2, 2, 1000, 1000, 128, True),  # eight key tiles per wave in the last blocks
     (1, 16, 16, 31, 257, 64, False),   # ragged key tile
     (2, 16, 8, 512, 512, 128, True),   # 512 workgroups: the four-wave variant (the others: eight)
+    (1, 8, 8, 400, 400, 128, True),    # 104 blocks of 32 queries: 16-query blocks, a partial last one
 ])
 def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
     """fp32 flash kernel (fp32 MFMA; four or, on small grids, eight waves splitting a query block's
-    key tiles, merged in LDS)."""
+    key tiles, merged in LDS).  At D = 128 a grid of fewer 32-query blocks than CUs takes 16-query
+    blocks (C1 and the D = 128 cases here but the 512-workgroup one)."""
     q, qh = seeded(54, (B, Hq, Lq, D))
     k, kh = seeded(55, (B, Hkv, Lk, D))
     v, vh = seeded(56, (B, Hkv, Lk, D))
@@ -155,10 +157,12 @@ def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
     assert_close_elem(out, ref, what="fp32 flash")
 
 
-def test_flash_f32_strided_views_and_negative_scale(hip):
+@pytest.mark.parametrize("D", [64, 128])
+def test_flash_f32_strided_views_and_negative_scale(hip, D):
     """fp32 kernel on [B, S, H, D] storage read through permuted views (no copy), with a negative
-    scale (the running maximum is taken over scaled scores, so any sign works)."""
-    B, S, Hq, Hkv, D = 2, 150, 8, 2, 64
+    scale (the running maximum is taken over scaled scores, so any sign works).  D = 128 here runs
+    the 16-query-block kernel (80 blocks of 32 queries: fewer than the CUs)."""
+    B, S, Hq, Hkv = 2, 150, 8, 2
     qs, qh = seeded(57, (B, S, Hq, D))
     ks, kh = seeded(58, (B, S, Hkv, D))
     vs, vh = seeded(59, (B, S, Hkv, D))
