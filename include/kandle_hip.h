@@ -238,7 +238,7 @@ int kh_philox4x32_10(uint64_t seed, const uint32_t* counters, int64_t n, uint32_
  * residual update: qk-norm + RoPE of the q heads and of the new token's k row (per-head RMSNorm with
  * q_norm_w / k_norm_w (bf16 [128]) and eps, angles float(p) * inv_freq[i]); the new k and v rows
  * written into the caches at row p = *position; split-K attention of the q heads over cache rows
- * [0, p] (GQA, scale); the merge; then x += o W_o^T (w_o bf16 [n_out, hq*128] with row stride ldw,
+ * [0, p] (GQA, any ratio hq / hkv, scale); the merge; then x += o W_o^T (w_o bf16 [n_out, hq*128] with row stride ldw,
  * x fp32 [n_out]).  qkv: [hq*128 + 2*hkv*128] (q heads, then k, then v) and the caches
  * [hkv][max_len][128] (element strides cache_strides = {k head, k row, v head, v row}) have `dtype`:
  * KH_BF16 (q and the new k row rounded to bf16 after RoPE, the merged row rounded to bf16 before
@@ -291,8 +291,8 @@ int kh_qk_norm_rope(const void* q, const void* k, void* q_out, void* k_out,
  * Shapes q [batch, hq, lq, d], k/v [batch, hkv, lk, d], o [batch, hq, lq, d]; `strides` holds 12
  * element strides: q (batch, head, seq), k (…), v (…), o (…); the d axis is contiguous.
  * bf16 with d == 64 or 128 runs the MFMA flash kernel; fp32 with d in {32, 64, 96, 128} the fp32
- * MFMA flash kernel; lq == 1 without causal masking, d == 64 or 128, GQA ratio 1, 2, 4 or 8 and
- * 16-byte aligned q / k / v rows runs split-K decode; otherwise a LDS-tiled fp32-math kernel
+ * MFMA flash kernel; lq == 1 without causal masking, d == 64 or 128 and 16-byte aligned q / k / v
+ * rows runs split-K decode; any GQA ratio hq / hkv on every route; otherwise a LDS-tiled fp32-math kernel
  * (d <= 256).  Replaces the `flash_attention` kernel
  * (reference signature packages/types/src/backend/register.ts:102-109; semantics
  * packages/backend-webgpu/src/kernels/attention/builder.ts:138-329; called from
@@ -335,7 +335,7 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
  * q [batch, hq, d], o [batch, hq, d] (strides: batch, head), caches [batch, hkv, max_len, d]
  * (strides: batch, head, seq).  `strides` holds 10 values: q (b, h), k (b, h, s), v (b, h, s),
  * o (b, h).  Split-K over the sequence with a log-sum-exp merge; bf16 or f32; d == 64 or 128;
- * hq / hkv in {1, 2, 4, 8}; q and the caches 16-byte aligned with strides in 16-byte units.
+ * any GQA ratio; q and the caches 16-byte aligned with strides in 16-byte units.
  * Varlen extension of flash_attention for StaticKVCache views
  * (reference: packages/model-utils/src/kv-cache.ts:197-211; register.ts:102-109). */
 int kh_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,

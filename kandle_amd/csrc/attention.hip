@@ -153,7 +153,7 @@ __device__ __forceinline__ const float2* decode_part_ml(const float* part, int h
 template <typename T, int G, int DH = 128>
 __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                              const T* __restrict__ V, const int32_t* __restrict__ lens,
-                                                             int uniform_len, int max_len, int hq, int hkv,
+                                                             int uniform_len, int max_len, int hq, int nsub,
                                                              AttnStrides st, float scale, int max_chunks,
                                                              float* __restrict__ part) {
   // Layout of `part` (decode_part_o / decode_part_ml): o[b][hq][max_chunks][DH] floats, then
@@ -172,7 +172,8 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
   __shared__ float red_o[DC_WAVES][G][D];
 
   const int chunk = blockIdx.x;
-  const int hk = blockIdx.y;
+  const int vg = blockIdx.y;      // group of G query heads: vg G .. vg G + G - 1
+  const int hk = vg / nsub;       // their kv head (nsub groups per kv head)
   const int b = blockIdx.z;
   const int L = decode_len(lens, uniform_len, b, max_len);
   if (chunk * CHUNK >= L) return;
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
   float qv[G][EPL];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
-    const T* qr = Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * EPL;
+    const T* qr = Q + b * st.qb + (int64_t)(vg * G + gi) * st.qh + sub * EPL;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) qv[gi][e] = Elem<T>::load(qr, e) * scale;
   }
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const T* __restrict
       Ls += red_l[ww][gi] * f;
       Os += red_o[ww][gi][d] * f;
     }
-    const int64_t row = ((int64_t)b * hq + hk * G + gi) * max_chunks + chunk;
+    const int64_t row = ((int64_t)b * hq + vg * G + gi) * max_chunks + chunk;
     if (d == 0) decode_part_ml<DH>(part, hq, max_chunks)[row] = make_float2(M, Ls);
     decode_part_o(part)[row * D + d] = Os;
   }
@@ -396,12 +397,15 @@ struct Row8 {
 // token's k row, writes it and the v row into the caches at row p, and scores it from registers
 // (the stale cache row it loaded is masked): the new key joins the softmax state of the DPP row
 // that owns it, with no data dependence on the cache write.  Only this workgroup reads row p in
-// this launch.
+// this launch (when a kv head's query heads span several groups, each group's workgroup scores
+// row p from its own registers and only the first group's writes it).
+// Both decode kernels take G query heads per workgroup; blockIdx.y is the group, and a kv head
+// whose ratio hq / hkv is above 8 (or not a multiple of the G chosen) is served by nsub groups.
 template <typename T, int G, bool FUSE = false, int DH = 128>
 __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                                   const T* __restrict__ V,
                                                                   const int32_t* __restrict__ lens, int uniform_len,
-                                                                  int max_len, int hq, int hkv, AttnStrides st,
+                                                                  int max_len, int hq, int nsub, AttnStrides st,
                                                                   float scale, int max_chunks,
                                                                   float* __restrict__ part, DecodeFuse fz) {
   constexpr bool F32 = sizeof(T) == 4;
@@ -414,7 +418,8 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
   __shared__ float red_o[NS][G][D];
 
   const int chunk = blockIdx.x;
-  const int hk = blockIdx.y;
+  const int vg = blockIdx.y;      // group of G query heads: vg G .. vg G + G - 1
+  const int hk = vg / nsub;       // their kv head (nsub groups per kv head)
   const int b = blockIdx.z;
   int praw = 0;
   int L;
@@ -436,7 +441,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
   float f0 = 0.f;
   bool newkey = false;  // FUSE: this lane's DPP row scores the new key from registers
 #pragma unroll
-  for (int gi = 0; gi < G; ++gi) qraw[gi].load(Q + b * st.qb + (int64_t)(hk * G + gi) * st.qh + sub * 8);
+  for (int gi = 0; gi < G; ++gi) qraw[gi].load(Q + b * st.qb + (int64_t)(vg * G + gi) * st.qh + sub * 8);
   if constexpr (FUSE) {
     // everything the norm and rotation need is requested before the cache rows (loads return in order)
     wqr = *reinterpret_cast<const uint4*>(fz.wq + sub * 8);
@@ -489,7 +494,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
     unpack8(wkr, wv);
     norm_rope_row(a, wv, cs, sn, sub, fz.eps);
     kn.from_f32(a);
-    if (newkey) {
+    if (newkey && vg % nsub == 0) {  // the first group of the kv head writes the cache rows
       T* kc = const_cast<T*>(K) + b * st.kb + hk * st.kh + (int64_t)praw * st.ks + sub * 8;
       T* vc = const_cast<T*>(V) + b * st.vb + hk * st.vh + (int64_t)praw * st.vs + sub * 8;
       kn.store(kc);
@@ -585,7 +590,7 @@ __global__ __launch_bounds__(256) void decode_partial_rows_kernel(const T* __res
       Ls += red_l[s2][gi] * f;
       Os += red_o[s2][gi][d] * f;
     }
-    const int64_t row = ((int64_t)b * hq + hk * G + gi) * max_chunks + chunk;
+    const int64_t row = ((int64_t)b * hq + vg * G + gi) * max_chunks + chunk;
     if (d == 0) decode_part_ml<DH>(part, hq, max_chunks)[row] = make_float2(M, Ls);
     decode_part_o(part)[row * D + d] = Os;
   }
@@ -713,14 +718,23 @@ size_t decode_part_bytes_for(int dtype, int d, int batch, int hq, int64_t max_le
   return d == 64 ? decode_part_bytes<float, 64>(batch, hq, max_len) : decode_part_bytes<float>(batch, hq, max_len);
 }
 
+// Query heads per decode workgroup for GQA ratio G: G itself up to 8, else its largest divisor
+// up to 8 (G / that many workgroups then share each kv head's chunk, each reading its K/V rows).
+inline int decode_group_heads(int G) {
+  if (G <= 8) return G;
+  int gc = 8;
+  while (G % gc != 0) --gc;
+  return gc;
+}
+
 // part_in: the partials buffer (at least decode_part_bytes), or nullptr to take one from the
 // caching allocator for the duration of the call.
 template <typename T, int DH = 128>
 int launch_decode(const void* q, const void* k, const void* v, void* o, const int32_t* lens, int uniform_len,
                   int batch, int hq, int hkv, int64_t max_len, const AttnStrides& st, float scale,
                   float* part_in = nullptr) {
-  const int G = hq / hkv;
-  KH_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "kh_decode_attention: hq/hkv = %d not in {1, 2, 4, 8}", G);
+  const int GC = decode_group_heads(hq / hkv), nsub = hq / hkv / GC;
+  KH_REQUIRE((int64_t)hkv * nsub <= 65535, "kh_decode_attention: %d query heads need too many workgroup groups", hq);
   const int64_t lim = int64_t(1) << 31;
   constexpr int CH = dc_chunk<T, DH>();
   KH_REQUIRE((max_len + CH) * st.ks * (int64_t)sizeof(T) < lim && (max_len + CH) * st.vs * (int64_t)sizeof(T) < lim,
@@ -730,7 +744,7 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   KH_REQUIRE(max_chunks <= 65535 * 64, "kh_decode_attention: max_len too large");
   float* part = part_in ? part_in : (float*)scratch_alloc(decode_part_bytes<T, DH>(batch, hq, max_len));
   if (!part) return KH_ERR_OOM;
-  dim3 grid(max_chunks, hkv, batch);
+  dim3 grid(max_chunks, hkv * nsub, batch);
   const T* Q = (const T*)q;
   const T* K = (const T*)k;
   const T* V = (const T*)v;
@@ -739,15 +753,19 @@ int launch_decode(const void* q, const void* k, const void* v, void* o, const in
   case GG:                                                                                                 \
     if constexpr (sizeof(T) == 2)                                                                          \
       decode_partial_rows_kernel<T, GG, false, DH><<<grid, 256, 0, stream()>>>(                            \
-          Q, K, V, lens, uniform_len, ml, hq, hkv, st, scale, max_chunks, part, DecodeFuse{});             \
+          Q, K, V, lens, uniform_len, ml, hq, nsub, st, scale, max_chunks, part, DecodeFuse{});            \
     else                                                                                                   \
-      decode_partial_kernel<T, GG, DH><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, hkv, st,  \
+      decode_partial_kernel<T, GG, DH><<<grid, 256, 0, stream()>>>(Q, K, V, lens, uniform_len, ml, hq, nsub, st, \
                                                                 scale, max_chunks, part);                  \
     break;
-  switch (G) {
+  switch (GC) {
     KH_DECODE_CASE(1)
     KH_DECODE_CASE(2)
+    KH_DECODE_CASE(3)
     KH_DECODE_CASE(4)
+    KH_DECODE_CASE(5)
+    KH_DECODE_CASE(6)
+    KH_DECODE_CASE(7)
     KH_DECODE_CASE(8)
   }
 #undef KH_DECODE_CASE
@@ -836,12 +854,11 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
   if (batch == 0 || lq == 0) return KH_OK;
   KH_REQUIRE(q && k && v && o && strides, "kh_flash_attention: null pointer");
   const AttnStrides st = load_strides(strides);
-  const int G = hq / hkv;
   KH_REQUIRE(lk > 0, "kh_flash_attention: the key sequence is empty (softmax over no keys is undefined)");
 
   // One query row, no mask: split-K decode over the keys (the caller's 1-token decode step).
-  const bool decode_ok = lq == 1 && !causal && (d == 128 || d == 64) && (G == 1 || G == 2 || G == 4 || G == 8) &&
-                         batch <= 65535 && decode_aligned(q, k, v, st, dtype);
+  const bool decode_ok = lq == 1 && !causal && (d == 128 || d == 64) && batch <= 65535 &&
+                         decode_aligned(q, k, v, st, dtype);
   if (decode_ok) {
     AttnStrides ds = st;
     ds.qs = 0;
@@ -1008,8 +1025,9 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
                               int64_t n_out, float* x, int dtype) {
   KH_REQUIRE_INIT();
   KH_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "kh_decode_attention_block: bad head counts %d / %d", hq, hkv);
-  const int G = hq / hkv;
-  KH_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "kh_decode_attention_block: hq/hkv = %d not in {1, 2, 4, 8}", G);
+  const int GC = decode_group_heads(hq / hkv), nsub = hq / hkv / GC;
+  KH_REQUIRE((int64_t)hkv * nsub <= 65535, "kh_decode_attention_block: %d query heads need too many workgroup groups",
+             hq);
   KH_REQUIRE(dtype == KH_BF16 || dtype == KH_F32, "kh_decode_attention_block: unsupported dtype %d", dtype);
   KH_REQUIRE(max_len > 0 && max_len <= INT32_MAX && n_out > 0 && n_out <= INT32_MAX,
              "kh_decode_attention_block: bad extents");
@@ -1042,18 +1060,28 @@ int kh_decode_attention_block(const void* qkv, const void* q_norm_w, const void*
   fz.k_new = (const char*)qkv + (int64_t)hq * 128 * eb;
   fz.v_new = (const char*)qkv + (int64_t)(hq + hkv) * 128 * eb;
   fz.eps = eps;
-  const dim3 grid(max_chunks, hkv, 1);
+  const dim3 grid(max_chunks, hkv * nsub, 1);
   auto partial = [&](auto* tp) {
     using T = std::remove_pointer_t<decltype(tp)>;
     const T* Q = (const T*)qkv;
     const T* K = (const T*)k_cache;
     const T* V = (const T*)v_cache;
-    switch (G) {
-      case 1: decode_partial_rows_kernel<T, 1, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-      case 2: decode_partial_rows_kernel<T, 2, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-      case 4: decode_partial_rows_kernel<T, 4, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
-      default: decode_partial_rows_kernel<T, 8, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, hkv, st, scale, max_chunks, part, fz); break;
+#define KH_BLOCK_CASE(GG)                                                                                   \
+  case GG:                                                                                                  \
+    decode_partial_rows_kernel<T, GG, true><<<grid, 256, 0, stream()>>>(Q, K, V, nullptr, 0, ml, hq, nsub, st,  \
+                                                                        scale, max_chunks, part, fz);        \
+    break;
+    switch (GC) {
+      KH_BLOCK_CASE(1)
+      KH_BLOCK_CASE(2)
+      KH_BLOCK_CASE(3)
+      KH_BLOCK_CASE(4)
+      KH_BLOCK_CASE(5)
+      KH_BLOCK_CASE(6)
+      KH_BLOCK_CASE(7)
+      KH_BLOCK_CASE(8)
     }
+#undef KH_BLOCK_CASE
   };
   if (f32)
     partial((float*)nullptr);

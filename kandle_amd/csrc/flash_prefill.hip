@@ -140,9 +140,10 @@ struct Flash {
     if (!kMirrorSlots || WAVES != 8 || wave < 4 || wpg == 1) return i;
     return wpg == 8 ? 11 - i : wpg - 1 - i;
   }
-  // Per-item fields: query block qblk of (batch, kv head) pair bh.
+  // Per-item fields: query block qblk of (batch, kv head) pair bh.  With kvsub > 1 the "kv heads"
+  // are groups of G query heads, kvsub of them reading each real kv head (hk / kvsub).
   __device__ __forceinline__ void set_item(int bh, int qblk, int hkv, int lq, int lk, bool causal, const uint16_t* K,
-                                           const uint16_t* V) {
+                                           const uint16_t* V, int kvsub = 1) {
     const int wpg = WAVES / G;
     b = bh / hkv;
     hk = bh % hkv;
@@ -156,11 +157,12 @@ struct Flash {
     const int nchunks = (kv_end + C::BNC - 1) / C::BNC;
     wave_last_q = min(qw0 + 31, lq - 1);
     wave_tiles = qw0 >= lq ? 0 : (causal ? min(nchunks, wave_last_q / C::BNC + 1) : nchunks);
-    rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hk * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 2));
-    rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hk * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 2));
+    const int hkr = hk / kvsub;
+    rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hkr * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 2));
+    rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hkr * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 2));
   }
   __device__ __forceinline__ void init(int batch, int hq, int hkv, int lq, int lk, const AttnStrides& s, bool causal,
-                                       int n_qblocks, const uint16_t* K, const uint16_t* V) {
+                                       int n_qblocks, const uint16_t* K, const uint16_t* V, int kvsub = 1) {
     setup(hq, hkv, s);
     // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCD i % 8), each XCD
     // with its own L2.  Renumber so that XCD x runs a contiguous range of logical blocks, ordered
@@ -170,7 +172,7 @@ struct Flash {
     const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
     const int base = nblk / kXcds, extra = nblk % kXcds;  // XCD x runs base + (x < extra) blocks
     const int logical = xcd * base + min(xcd, extra) + j;
-    set_item(logical / n_qblocks, n_qblocks - 1 - logical % n_qblocks, hkv, lq, lk, causal, K, V);
+    set_item(logical / n_qblocks, n_qblocks - 1 - logical % n_qblocks, hkv, lq, lk, causal, K, V, kvsub);
   }
   // LDS row of tile key k: bits 2 and 3 of k swapped (an involution), so that lane r of the S^T
   // A operand, which reads LDS row r, holds key swap23(r) -- the order the PV B operand needs --
@@ -525,14 +527,14 @@ template <int BN, int WAVES, int MINB, bool CAUSAL, int MASKT = 0, int D = 128>
 __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale,
-    int n_qblocks, const void* __restrict__ M, MaskArgs ma) {
+    int n_qblocks, const void* __restrict__ M, MaskArgs ma, int kvsub) {
   using C = Cfg<BN, WAVES, D>;
   using FL = Flash<BN, WAVES, D>;
   static_assert(MASKT == 0 || (BN == 64 && !CAUSAL && D == 128), "masked tiles are 64 keys, D 128, not causal");
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
   FL F;
-  F.init(batch, hq, hkv, lq, lk, st, CAUSAL, n_qblocks, K, V);
+  F.init(batch, hq, hkv, lq, lk, st, CAUSAL, n_qblocks, K, V, kvsub);
   const float c2 = scale * kLog2e;
   bf16x8 qreg[C::NQ];
   F.load_q(Q, lq, qreg);
@@ -742,45 +744,60 @@ constexpr int kWaves = 8;  // waves per workgroup: query rows of 32 * 8 / G, one
 constexpr int kSmallGrid = 256;
 constexpr int kSmallBN = 128;
 
+// hkv here counts groups of hq / hkv query heads sharing K/V tiles; with kvsub > 1 they are
+// sub-groups, kvsub of them per real kv head (see prefill_groups).
 template <int BN, int WAVES, bool CAUSAL, int D>
 void launch_fwd(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
-                const AttnStrides& st, float scale) {
+                const AttnStrides& st, float scale, int kvsub) {
   const int BMQ = 32 * (WAVES / (hq / hkv));
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int nblk = nqb * batch * hkv;
   flash_fwd_kernel<BN, WAVES, 1, CAUSAL, 0, D><<<nblk, WAVES * 64, 0, stream()>>>(
       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, lq, lk, st, scale,
-      nqb, nullptr, MaskArgs{});
+      nqb, nullptr, MaskArgs{}, kvsub);
+}
+
+// The tile kernels serve G = 1, 2, 4 or 8 query heads per kv head.  Another ratio R is served in
+// groups of G = the largest of 8, 4, 2, 1 dividing R: kvsub = R / G groups per kv head, each a
+// "kv head" of the launch (hkv * kvsub of them) that reads real kv head group / kvsub.
+struct PrefillGroups {
+  int G, kvsub, hkv;
+};
+inline PrefillGroups prefill_groups(int hq, int hkv) {
+  const int R = hq / hkv;
+  const int G = R % 8 == 0 ? 8 : (R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1));
+  return PrefillGroups{G, R / G, hkv * (R / G)};
 }
 
 template <int D>
-int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int lq, int lk,
-                     const AttnStrides& st, float scale, bool causal) {
-  const int G = hq / hkv;
+int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv_real, int lq,
+                     int lk, const AttnStrides& st, float scale, bool causal) {
+  const PrefillGroups pg = prefill_groups(hq, hkv_real);
+  const int G = pg.G, kvsub = pg.kvsub, hkv = pg.hkv;
   const int BMQ = 32 * (kWaves / G);
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
   if (nblk64 < kSmallGrid && G <= 2) {
     if (causal)
-      launch_fwd<kSmallBN, 2, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+      launch_fwd<kSmallBN, 2, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
     else
-      launch_fwd<kSmallBN, 2, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+      launch_fwd<kSmallBN, 2, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
   } else if (nblk64 < kSmallGrid && G == 4) {
     if (causal)
-      launch_fwd<kSmallBN, 4, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+      launch_fwd<kSmallBN, 4, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
     else
-      launch_fwd<kSmallBN, 4, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
-  } else if (causal && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
+      launch_fwd<kSmallBN, 4, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
+  } else if (causal && kvsub == 1 && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
     // Enough causal query blocks for every CU to take several: one resident workgroup per CU.
     static_assert(kPersistWaves == kWaves, "the persistent kernel's query blocks are the tile kernel's");
     flash_fwd_persistent_kernel<true, D><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
         (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
         st, scale, nqb);
   } else if (causal) {
-    launch_fwd<128, kWaves, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+    launch_fwd<128, kWaves, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
   } else {
-    launch_fwd<128, kWaves, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale);
+    launch_fwd<128, kWaves, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
   }
   KH_CHECK_LAUNCH();
   return KH_OK;
@@ -1058,8 +1075,9 @@ namespace kh {
 
 bool flash_prefill_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv,
                              int64_t lq, int64_t lk, int d, const AttnStrides& st) {
-  const int G = hq / hkv;
-  if (!(d == 64 || d == 128) || !(G == 1 || G == 2 || G == 4 || G == 8)) return false;
+  (void)hq;
+  (void)hkv;
+  if (!(d == 64 || d == 128)) return false;  // any GQA ratio (prefill_groups)
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
   const int64_t all[] = {st.qb, st.qh, st.qs, st.kb, st.kh, st.ks, st.vb, st.vh, st.vs, st.ob, st.oh, st.os};
   for (int64_t s : all)
@@ -1114,9 +1132,10 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
 }
 
 int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq,
-                                     int hkv, int lq, int lk, const AttnStrides& st, float scale, const void* mask,
-                                     const MaskArgs& ma, int mask_dtype) {
-  const int G = hq / hkv;
+                                     int hkv_real, int lq, int lk, const AttnStrides& st, float scale,
+                                     const void* mask, const MaskArgs& ma, int mask_dtype) {
+  const PrefillGroups pg = prefill_groups(hq, hkv_real);
+  const int G = pg.G, kvsub = pg.kvsub, hkv = pg.hkv;
   const int BMQ = 32 * (kWaves / G);
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
@@ -1126,10 +1145,10 @@ int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v
   uint16_t* O = (uint16_t*)o;
   if (mask_dtype == KH_F32)
     flash_fwd_kernel<64, kWaves, 1, false, 1><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
-                                                                                  st, scale, nqb, mask, ma);
+                                                                                  st, scale, nqb, mask, ma, kvsub);
   else
     flash_fwd_kernel<64, kWaves, 1, false, 2><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
-                                                                                  st, scale, nqb, mask, ma);
+                                                                                  st, scale, nqb, mask, ma, kvsub);
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -299,6 +299,63 @@ def test_sdpa_single_query_head_dim_64_routes_to_decode(hip, dtype):
         assert np.max(np.abs(out - ref)) < BF16_ATOL
 
 
+# GQA ratios other than 1, 2, 4, 8 (e.g. Qwen3-14B: 40 / 8 = 5): decode serves them as groups of
+# up to 8 query heads per workgroup (several groups per kv head above 8), the bf16 flash kernels as
+# groups of 8, 4, 2 or 1 heads (the largest dividing the ratio).
+@pytest.mark.parametrize("Hq,Hkv,dtype,D", [
+    (6, 2, "bfloat16", 128), (10, 2, "bfloat16", 128), (12, 2, "bfloat16", 128), (14, 2, "bfloat16", 128),
+    (16, 1, "bfloat16", 128),   # ratio 16: two groups of 8 per kv head
+    (24, 2, "bfloat16", 128),   # ratio 12: two groups of 6
+    (11, 1, "bfloat16", 128),   # ratio 11: one group of 11 would exceed 8: eleven groups of one
+    (10, 2, "float32", 128), (24, 2, "float32", 128), (14, 2, "bfloat16", 64), (10, 2, "float32", 64),
+])
+def test_decode_any_gqa_ratio(hip, Hq, Hkv, dtype, D):
+    lens = np.array([1, 300, 777], np.int32)
+    B, ML = len(lens), 800
+    q, qh = seeded(91, (B, Hq, D), dtype)
+    kc, kch = seeded(92, (B, Hkv, ML, D), dtype)
+    vc, vch = seeded(93, (B, Hkv, ML, D), dtype)
+    sl = Tensor(lens, dtype="int32")
+    o = F.decode_attention(q, kc, vc, sl).numpy()
+    ref = oracle.sdpa(qh[:, :, None, :], kch, vch, kv_len=lens)[:, :, 0, :]
+    if dtype == "float32":
+        assert max_rel(o, ref) < F32_RTOL
+        assert_close_elem(o, ref, what="decode any GQA fp32")
+    else:
+        assert np.max(np.abs(o - ref)) < BF16_ATOL
+    for t in (q, kc, vc, sl):
+        t.dispose()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [
+    (1, 6, 2, 300, 128),    # ratio 3: groups of 1 (2-wave tiles)
+    (1, 10, 2, 257, 128),   # ratio 5
+    (2, 12, 2, 200, 64),    # ratio 6: groups of 2
+    (1, 16, 1, 130, 128),   # ratio 16: groups of 8
+    (2, 24, 2, 600, 128),   # ratio 12: groups of 4 (4-wave tiles)
+])
+def test_flash_bf16_any_gqa_ratio(hip, B, Hq, Hkv, S, D, causal):
+    q, qh = seeded(94, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(95, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(96, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, causal)
+    assert np.max(np.abs(out - oracle.sdpa(qh, kh, vh, causal=causal))) < BF16_ATOL
+
+
+def test_flash_bf16_gqa_3_eight_wave_tiles(hip):
+    """Ratio 3 on a grid of 384 query blocks: the eight-wave tile kernel (the persistent causal kernel
+    takes ratios 1, 2, 4 and 8 only)."""
+    B, Hq, Hkv, S, D = 2, 24, 8, 2048, 64
+    q, qh = seeded(97, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(98, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(99, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    assert np.max(np.abs(out - oracle.sdpa(qh, kh, vh, causal=True))) < BF16_ATOL
+    for t in (q, k, v):
+        t.dispose()
+
+
 def test_flash_c3_full_size(hip):
     """Config C3 at full size (B=4, Hq=16, Hkv=8, S=4096, D=128, causal, bf16): every row of two
     whole (batch, head) slices (the first and the last, 4096 query rows each, every causal key

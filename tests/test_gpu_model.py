@@ -87,6 +87,20 @@ def test_small_qwen3_prefill_and_decode(hip, act):
     assert toks == rtoks
 
 
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("heads,kv_heads", [(6, 2), (10, 2), (16, 1)])
+def test_small_qwen3_any_gqa_ratio(hip, act, heads, kv_heads):
+    """GQA ratios 3, 5 (as Qwen3-14B's 40 / 8) and 16: the fused QKV projection, the prefill
+    attention, the fused decode attention block and the replayed decode step against the oracle."""
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2, num_attention_heads=heads,
+                      num_key_value_heads=kv_heads)
+    toks, logits, rtoks, rlogits = _run(cfg, seed=9, prompt_len=60, steps=6, max_seq=128, act=act)
+    for i, (g, r) in enumerate(zip(logits, rlogits)):
+        err = float(np.max(np.abs(g - r)))
+        assert err < LOGIT_ATOL, (i, err)
+    assert toks == rtoks
+
+
 def _c5_check(act, seed, prompt_len, steps=32, max_seq=1024):
     """Greedy C5 generation with `act` activations against the float32 oracle (and, for bf16, the
     bf16-rounding oracle): per-step logit error, the float32 oracle's top-2 margin and the tokens
