@@ -229,8 +229,9 @@ class Qwen3ForCausalLM:
         self._prefill_graphs: "OrderedDict[int, tuple]" = OrderedDict()
         self.max_prefill_graphs = 4
         # Decode steps run each layer's attention block (qk-norm, RoPE, K/V write, attention, o_proj)
-        # as one library call; False runs the separate launches (the prefill's path at S = 1).
-        self.fused_decode = True
+        # as one library call (head_dim 128); False runs the separate launches (the prefill's path
+        # at S = 1).
+        self.fused_decode = cfg.head_dim == 128
         # Chunks whose QKV projection kh_gemm would run on MFMA tiles without a K split run it with
         # qk-norm, RoPE and the K/V cache write in its epilogue (linear_qk_norm_rope, head_dim 128;
         # the same values); False always runs the projection and rms_norm_rope as two launches.

@@ -16,7 +16,8 @@
 //   decode step of one token at device position p (greedy loop, for_causal_lm.ts:475-508)
 //     x = embed[token]; per layer: qkv = rms_norm(x) W_qkv^T (gemv_fused); the attention block
 //       (decode_attention_block: qk-norm, RoPE, K/V cache write at p, attention over rows [0, p],
-//       o_proj, residual add); a = silu * mul of rms_norm(x) through the gate/up weight
+//       o_proj, residual add; head_dim 128 -- other head dims run rms_norm_rope, decode_attention
+//       and the o_proj gemv_fused); a = silu * mul of rms_norm(x) through the gate/up weight
 //       (gemv_swiglu); x += a W_down^T (gemv_fused)
 //     logits = rms_norm(x) E^T; token = argmax (lowest index); greedy_advance moves p on.
 //
@@ -143,6 +144,9 @@ export class Qwen3ForCausalLM {
   finalNormA: any;
   act: string;
   flashName: string;
+  // decode steps run each layer's attention block as one decode_attention_block call (head_dim
+  // 128); false runs rms_norm_rope, decode_attention and the o_proj GEMV
+  fusedDecode: boolean;
   invFreq: any;
   invFreqHost: Float32Array;
   layers: Layer[] = [];
@@ -218,6 +222,7 @@ export class Qwen3ForCausalLM {
     for (let i = 0; i < half; ++i) this.invFreqHost[i] = 1 / Math.pow(cfg.ropeTheta, i / half);
     this.invFreq = backend.createTensorHandle({ shape: [half], dtype: 'float32', data: this.invFreqHost });
     this.scale = 1 / Math.sqrt(D);
+    this.fusedDecode = D === 128;
   }
 
   static fromSafetensors(backend: any, cfg: Qwen3Config, file: string, maxSeqLen: number,
@@ -365,17 +370,34 @@ export class Qwen3ForCausalLM {
   // there), then token = argmax and greedy_advance (log[pos + 1 - base] = token, pos += 1).
   decodeStep(token: any, pos: any, lens: any, log: any, base: number): any {
     const cfg = this.cfg, ops = this.ops, be = this.backend;
-    const H = cfg.hiddenSize, I = cfg.intermediateSize, eps = cfg.rmsNormEps;
-    const nqkv = (cfg.numAttentionHeads + 2 * cfg.numKeyValueHeads) * cfg.headDim;
+    const H = cfg.hiddenSize, I = cfg.intermediateSize, eps = cfg.rmsNormEps, D = cfg.headDim;
+    const Hq = cfg.numAttentionHeads, Hkv = cfg.numKeyValueHeads;
+    const nq = Hq * D, nkv = Hkv * D, nqkv = nq + 2 * nkv;
     const act = this.act;
     const x = be.createTensorHandle([1, H], 'float32');
     ops.find('index_select')(this.embed, token, { dim: 0 }, x);
     for (const L of this.layers) {
       const qkv = be.createTensorHandle([1, nqkv], act);
       ops.find('gemv_fused')('rms_norm', x, L.wQkv, qkv, { normWeight: L.inNorm, eps, actDtype: act });
-      ops.find('decode_attention_block')(qkv, { qNorm: L.qNorm, kNorm: L.kNorm, invFreq: this.invFreq, eps,
-                                                position: pos, kCache: L.kCache, vCache: L.vCache, wO: L.wO, x,
-                                                scale: this.scale });
+      if (this.fusedDecode) {
+        ops.find('decode_attention_block')(qkv, { qNorm: L.qNorm, kNorm: L.kNorm, invFreq: this.invFreq, eps,
+                                                  position: pos, kCache: L.kCache, vCache: L.vCache, wO: L.wO, x,
+                                                  scale: this.scale });
+      } else {
+        // qk-norm + RoPE at position p with the K/V rows written into the caches there, the one
+        // query against cache rows [0, p], then x += o W_o^T
+        const heads = (col0: number, nh: number): any => this.view(qkv, [1, 1, nh, D], [nqkv, nqkv, D, 1], col0);
+        const q = heads(0, Hq), k = heads(nq, Hkv), v = heads(nq + nkv, Hkv);
+        const qh = be.createTensorHandle([1, Hq, 1, D], act);
+        ops.find('rms_norm_rope')(q, k, { qWeight: L.qNormA, kWeight: L.kNormA, invFreq: this.invFreq, positions: pos,
+                                          eps, qOut: qh, kOut: L.kCache, v, vOut: L.vCache, cachePositions: true });
+        for (const t of [q, k, v]) t.dispose();
+        const attn = be.createTensorHandle([1, nq], act);
+        const attnView = this.view(attn, [1, Hq, 1, D], [nq, D, D, 1], 0);
+        ops.find('decode_attention')(qh, L.kCache, L.vCache, lens, attnView, this.scale);
+        ops.find('gemv_fused')('none', attn, L.wO, x, { cin: x, actDtype: act });
+        for (const t of [attnView, attn, qh]) t.dispose();
+      }
       qkv.dispose();
       const a = be.createTensorHandle([1, I], act);
       ops.find('gemv_swiglu')('rms_norm', x, L.wGu, a, { normWeight: L.postNorm, eps });

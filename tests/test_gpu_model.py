@@ -88,12 +88,14 @@ def test_small_qwen3_prefill_and_decode(hip, act):
 
 
 @pytest.mark.parametrize("act", ACTS)
-@pytest.mark.parametrize("heads,kv_heads", [(6, 2), (10, 2), (16, 1)])
-def test_small_qwen3_any_gqa_ratio(hip, act, heads, kv_heads):
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(6, 2, 128), (10, 2, 128), (16, 1, 128), (16, 8, 64)])
+def test_small_qwen3_any_gqa_ratio(hip, act, heads, kv_heads, head_dim):
     """GQA ratios 3, 5 (as Qwen3-14B's 40 / 8) and 16: the fused QKV projection, the prefill
-    attention, the fused decode attention block and the replayed decode step against the oracle."""
+    attention, the fused decode attention block and the replayed decode step against the oracle;
+    head dim 64: the projection, qk-norm + RoPE and the decode step's attention as separate
+    launches."""
     cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2, num_attention_heads=heads,
-                      num_key_value_heads=kv_heads)
+                      num_key_value_heads=kv_heads, head_dim=head_dim)
     toks, logits, rtoks, rlogits = _run(cfg, seed=9, prompt_len=60, steps=6, max_seq=128, act=act)
     for i, (g, r) in enumerate(zip(logits, rlogits)):
         err = float(np.max(np.abs(g - r)))

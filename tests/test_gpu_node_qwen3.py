@@ -35,14 +35,20 @@ def _ensure_dist():
             subprocess.run(["node", os.path.join(PKG, "strip-types.js"), src, dist], check=True, timeout=60)
 
 
-def test_typescript_qwen3_generation_matches_python_model(hip, tmp_path):
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [
+    (16, 8, 128),   # the 0.6B's attention shapes
+    (10, 2, 128),   # GQA ratio 5
+    (16, 8, 64),    # head dim 64: the decode step's attention as separate launches
+])
+def test_typescript_qwen3_generation_matches_python_model(hip, tmp_path, heads, kv_heads, head_dim):
     if shutil.which("node") is None or not os.path.exists(ADDON):
         pytest.skip("node or the built addon is not available")
     torch = pytest.importorskip("torch")
     from safetensors.torch import save_file
 
     _ensure_dist()
-    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2, num_attention_heads=heads, num_key_value_heads=kv_heads,
+                      head_dim=head_dim)
     w = init_qwen3_weights(cfg, seed=13)
     for i, name in enumerate(sorted(k for k in w if k.endswith("norm.weight"))):   # norms other than 1
         w[name] = syn.bf16(syn.uniform(500 + i, w[name].shape, 0.5, 1.5))[0]
