@@ -475,7 +475,7 @@ int kh_add_rms_norm(const float* part, int splits, int64_t split_stride, float* 
  *   prologue 3: x'[i] = silu(x[16(i/8) + i%8]) * x[16(i/8) + 8 + i%8] with x bf16 [2k] — the same
  *               product read from the output of a gate/up projection whose weight interleaves gate
  *               and up rows in blocks of 8 (kh_gemm_swiglu's layout; k % 8 == 0).
- * Needs k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w and k <= 16384.  cin may alias c. */
+ * Needs k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w and k <= 32768.  cin may alias c. */
 int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_w, float eps,
                   const void* w, int64_t ldw, void* c, const void* cin, const void* bias,
                   int64_t n, int64_t k, float alpha, float beta, int out_dtype, int x_dtype);
@@ -490,7 +490,7 @@ int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_
  * and h kept in fp32, h fp32.  Fuses SwiGLUMLP's gate and up projections with silu and mul for one
  * token (reference: packages/model-utils/src/mlp/swiglu.ts:119-134; RMSNorm before it:
  * packages/core/src/nn/modules/normalization/RMSNorm.ts:92-99).  Needs n_half % 8 == 0,
- * k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w_gu and k <= 16384. */
+ * k % 8 == 0, ldw % 8 == 0, a 16-byte aligned w_gu and k <= 32768. */
 int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, const void* w_gu, int64_t ldw,
                    void* h, int64_t n_half, int64_t k, int x_dtype);
 

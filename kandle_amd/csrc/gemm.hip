@@ -585,10 +585,15 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const void* __restrict__ x, 
   g.template run<TO>(xs, C, cin, bias, alpha, beta);
 }
 
+// x' is staged in LDS as fp32: k <= 32768 (128 KiB of the CU's 160 KiB; above 64 KiB one
+// workgroup per CU, the size of the down projections of 14B- and 32B-class models).
+constexpr size_t kGemvMaxLds = 128 * 1024;
+
 // Launches gemv1_kernel; returns false (nothing launched) when the operands do not fit its
-// assumptions (16-byte aligned weight rows, 32-bit byte offsets, x' within 64 KiB of LDS).
+// assumptions (16-byte aligned weight rows, 32-bit byte offsets, x' within kGemvMaxLds of LDS) or
+// the runtime refuses the workgroup's LDS size.
 template <int U, int PRO, typename TO, bool PAIR8 = false, bool EX = false>
-void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw,
+bool gemv1_go(const void* x, const void* x2, const void* nw, float eps, const uint16_t* W, int64_t ldw,
               uint32_t w_bytes, TO* C, const TO* cin, const TO* bias, int N, int K, int nch, float alpha, float beta,
               const AttnMerge& am) {
   const int64_t waves = (N + U - 1) / U;
@@ -597,9 +602,17 @@ void gemv1_go(const void* x, const void* x2, const void* nw, float eps, const ui
   // workgroups: 69.5 -> 59.9 us graph-replayed with 4 rows per wave and 8192 workgroups before.
   if (grid > 2048) grid = 2048;
   const size_t shm = (size_t)nch * GV_CHUNK * sizeof(float);
+  if (shm > 64 * 1024) {
+    // dynamic LDS above 64 KiB is opted into once per kernel instantiation
+    static const bool raised = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv1_kernel<U, PRO, TO, PAIR8, EX>),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)kGemvMaxLds) == hipSuccess;
+    if (!raised) return false;
+  }
   gemv1_kernel<U, PRO, TO, PAIR8, EX><<<(int)grid, 256, shm, stream()>>>(x, x2, (const uint16_t*)nw, eps, W, ldw,
                                                                          w_bytes, C, cin, bias, N, K, nch, alpha,
                                                                          beta, am);
+  return true;
 }
 
 // The weight rows a one-row projection may address fit 32-bit byte offsets: row groups start below
@@ -621,11 +634,10 @@ bool launch_gemv_swiglu(const void* x, const void* nw, float eps, const uint16_t
   const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
   // a pair of row group q addresses rows up to 16 (q / 8) + q % 8 + 8 < N + 8
   if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || !gemv_offsets_fit(N, 8, ldw) ||
-      (size_t)nch * GV_CHUNK * sizeof(float) > 64 * 1024)
+      (size_t)nch * GV_CHUNK * sizeof(float) > kGemvMaxLds)
     return false;
-  gemv1_go<2, PRO, TO, true, EX>(x, nullptr, nw, eps, W, ldw, (uint32_t)w_bytes, H, nullptr, nullptr, N, K, nch, 1.f,
-                                 0.f, AttnMerge{});
-  return true;
+  return gemv1_go<2, PRO, TO, true, EX>(x, nullptr, nw, eps, W, ldw, (uint32_t)w_bytes, H, nullptr, nullptr, N, K, nch,
+                                        1.f, 0.f, AttnMerge{});
 }
 
 template <int PRO, typename TO, bool EX = false>
@@ -636,16 +648,12 @@ bool launch_gemv1(const void* x, const void* x2, const void* nw, float eps, cons
   const int64_t w_bytes = ((int64_t)(N - 1) * ldw + K) * 2;
   const int U = N >= 16384 ? 8 : (N >= 2048 ? 2 : 1);
   if (K % 8 != 0 || ldw % 8 != 0 || !aligned16(W) || !gemv_offsets_fit(N, U, ldw) ||
-      (size_t)nch * GV_CHUNK * sizeof(float) > 64 * 1024)
+      (size_t)nch * GV_CHUNK * sizeof(float) > kGemvMaxLds)
     return false;
   const uint32_t wb = (uint32_t)w_bytes;
-  if (U == 8)
-    gemv1_go<8, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
-  else if (U == 2)
-    gemv1_go<2, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
-  else
-    gemv1_go<1, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
-  return true;
+  if (U == 8) return gemv1_go<8, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
+  if (U == 2) return gemv1_go<2, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
+  return gemv1_go<1, PRO, TO, false, EX>(x, x2, nw, eps, W, ldw, wb, C, cin, bias, N, K, nch, alpha, beta, am);
 }
 
 // =============================================================================================
@@ -1112,7 +1120,7 @@ int kh_gemv_swiglu(int prologue, const void* x, const void* norm_w, float eps, c
     ok = prologue == PRO_RMSNORM ? launch_gemv_swiglu<PRO_RMSNORM>(x, norm_w, eps, W, ldw, (uint16_t*)h, NH, K)
                                  : launch_gemv_swiglu<PRO_NONE>(x, norm_w, eps, W, ldw, (uint16_t*)h, NH, K);
   KH_REQUIRE(ok, "kh_gemv_swiglu: unsupported operands (need k %% 8 == 0, ldw %% 8 == 0, a 16-byte aligned weight, "
-                 "k <= 16384 and byte offsets below 4 GiB)");
+                 "k <= 32768 and byte offsets below 4 GiB)");
   KH_CHECK_LAUNCH();
   return KH_OK;
 }
@@ -1156,7 +1164,7 @@ int kh_gemv_fused(int prologue, const void* x, const void* x2, const void* norm_
   else
     run((uint16_t*)c, (const uint16_t*)cin, (const uint16_t*)bias, std::false_type{});
   KH_REQUIRE(ok, "kh_gemv_fused: unsupported operands (need k %% 8 == 0, ldw %% 8 == 0, a 16-byte aligned weight, "
-                 "k <= 16384 and byte offsets below 4 GiB)");
+                 "k <= 32768 and byte offsets below 4 GiB)");
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -37,6 +37,28 @@ def test_gemv_plain_bf16(hip, N, K):
     assert ok, err
 
 
+@pytest.mark.parametrize("N,K", [(300, 17408), (1000, 25600), (64, 32768)])
+def test_gemv_long_rows(hip, N, K):
+    """Rows longer than 16384 (the down projections of 14B- and 32B-class models: intermediate sizes
+    17408 and 25600): x' staged in more than 64 KiB of LDS; fp32 residual row out, bf16 weights."""
+    x, xh = seeded(305, (1, K), "bfloat16")
+    w, wh = seeded(306, (N, K), "bfloat16", std=0.02)
+    y = F.linear_fused("none", x, w).numpy()
+    ok, err = _close_bf16(y, oracle.linear(xh, wh), K)
+    assert ok, err
+    r, rh = seeded(307, (1, N))
+    F.linear_fused("none", x, w, residual=r)          # r += x W^T, fp32
+    ok, err = _close_f32(r.numpy(), rh + oracle.linear(xh, wh))
+    assert ok, err
+
+
+def test_gemv_rejects_rows_past_32768(hip):
+    x, _ = seeded(308, (1, 32776), "bfloat16")
+    w, _ = seeded(309, (8, 32776), "bfloat16")
+    with pytest.raises(Exception, match="32768"):
+        F.linear_fused("none", x, w)
+
+
 def test_gemv_rms_norm_prologue_matches_unfused(hip):
     K, N = 1024, 4096
     x, xh = seeded(310, (1, K), std=3.0)                    # fp32 residual row

@@ -103,6 +103,25 @@ def test_small_qwen3_any_gqa_ratio(hip, act, heads, kv_heads, head_dim):
     assert toks == rtoks
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("hidden,inter,heads,kv_heads", [
+    (2560, 9728, 32, 8),    # Qwen3-4B's layer widths
+    (5120, 17408, 40, 8),   # Qwen3-14B's: GQA 5, down-projection rows of 17408
+])
+def test_wide_qwen3_layer(hip, hidden, inter, heads, kv_heads):
+    """One decoder layer at the widths of larger Qwen3 models (vocab 4096), float32 activations:
+    prefill and decode logits and tokens against the float32 oracle.  (The bfloat16-activation
+    mode's distance from its rounding oracle grows with the widths -- 0.023 at hidden 2560 -- so
+    its bar is checked at the 0.6B widths only.)"""
+    cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=1, hidden_size=hidden, intermediate_size=inter,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads)
+    toks, logits, rtoks, rlogits = _run(cfg, seed=3, prompt_len=24, steps=4, max_seq=64, act="float32")
+    for i, (g, r) in enumerate(zip(logits, rlogits)):
+        err = float(np.max(np.abs(g - r)))
+        assert err < LOGIT_ATOL, (i, err)
+    assert toks == rtoks
+
+
 def _c5_check(act, seed, prompt_len, steps=32, max_seq=1024):
     """Greedy C5 generation with `act` activations against the float32 oracle (and, for bf16, the
     bf16-rounding oracle): per-step logit error, the float32 oracle's top-2 margin and the tokens
