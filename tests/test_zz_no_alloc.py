@@ -34,7 +34,8 @@ def _stats():
     ("bfloat16", 128, [(8, 16, 8, 32768, 2024), (2, 16, 2, 1500, 7)]),   # the C4 shape, then a smaller call
     ("float32", 128, [(4, 16, 8, 4096, 31), (1, 8, 8, 300, 37)]),
     ("bfloat16", 64, [(4, 16, 4, 5000, 41), (1, 8, 8, 700, 43)]),        # head dim 64: 512-key chunks
-    ("float32", 64, [(2, 16, 2, 3000, 47), (1, 4, 4, 200, 53)])])
+    ("float32", 64, [(2, 16, 2, 3000, 47), (1, 4, 4, 200, 53)]),
+    ("bfloat16", 128, [(2, 10, 2, 3000, 61), (1, 24, 2, 500, 67)])])      # GQA 5, then 12 (2 groups of 6)
 def test_noalloc_decode_matches_allocating_entry_point(hip, dtype, D, cases):
     for B, Hq, Hkv, ML, seed in cases:
         lens = syn.randint(seed, (B,), 1, ML + 1)
