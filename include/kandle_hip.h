@@ -321,7 +321,7 @@ int kh_flash_attention_split(const void* q, const void* k, const void* v, void* 
  * (e.g. all -inf) is 0 / 0: that row's output is NaN.  The mask (dtype KH_F32 or KH_BF16) is
  * read as mask[b * mask_strides[0] + h * mask_strides[1] + i * mask_strides[2] + j * mask_strides[3]]
  * for batch b, query head h, query i, key j: element strides, 0 broadcasts an axis.  q/k/v/o
- * layouts and `strides` as kh_flash_attention.  bf16 with d == 128 runs the MFMA kernel (a mask
+ * layouts and `strides` as kh_flash_attention.  bf16 with d == 64 or 128 runs the MFMA kernel (a mask
  * without unit key stride and 16-byte aligned 8-key runs is first packed into a scratch copy);
  * otherwise the fp32-math kernel (d <= 256). */
 int kh_flash_attention_masked(const void* q, const void* k, const void* v, void* o,

@@ -19,9 +19,8 @@ struct MaskArgs {
   float floor_raw;         // the reference softmax's f32(-1e38) max floor in raw q.k units
 };
 
-// True when the bf16 MFMA prefill kernel takes this call (d = 64 or 128, G in {1,2,4,8}, 16-byte
+// True when the bf16 MFMA prefill kernel takes this call (d = 64 or 128, any GQA ratio, 16-byte
 // aligned rows, strides below 2^31, per-head byte ranges addressable with 32-bit buffer offsets).
-// The explicit-mask kernel takes d = 128 only.
 bool flash_prefill_supported(const void* q, const void* k, const void* v, const void* o, int hq, int hkv,
                              int64_t lq, int64_t lk, int d, const AttnStrides& st);
 
@@ -33,8 +32,8 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
 // masking; 64-key stages.  Requires flash_prefill_supported(), ma.sk == 1, every 8-key run of the
 // mask 16-byte aligned (base and sb, sh, sq multiples of 8 elements) and ma.bytes < 2^31.
 int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq,
-                                     int hkv, int lq, int lk, const AttnStrides& st, float scale, const void* mask,
-                                     const MaskArgs& ma, int mask_dtype);
+                                     int hkv, int lq, int lk, int d, const AttnStrides& st, float scale,
+                                     const void* mask, const MaskArgs& ma, int mask_dtype);
 
 // True when the fp32 flash kernel (flash_f32.hip) takes this fp32 call: d in {32, 64, 96, 128},
 // 16-byte aligned q / k / o with strides in multiples of 4 elements, 4-byte aligned v, per-head

@@ -918,7 +918,7 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
   const double fl = (double)-1e38f / (double)scale;
   ma.floor_raw = (scale > 0.f && fl >= -(double)FLT_MAX) ? (float)fl : -INFINITY;
 
-  if (!(dtype == KH_BF16 && scale > 0.f && d == 128 && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st)))
+  if (!(dtype == KH_BF16 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st)))
     return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
 
   // MFMA path: the mask must have a unit key stride and 16-byte aligned 8-key runs; otherwise it is
@@ -958,7 +958,7 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
     rc = launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
   } else {
     ma.bytes = (uint32_t)extent;
-    rc = launch_flash_prefill_bf16_masked(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, st, scale, mp, ma,
+    rc = launch_flash_prefill_bf16_masked(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, mp, ma,
                                           mask_dtype);
   }
   if (packed) scratch_free(packed);  // stream-ordered: reused only by later work on the same stream

@@ -530,7 +530,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
     int n_qblocks, const void* __restrict__ M, MaskArgs ma, int kvsub) {
   using C = Cfg<BN, WAVES, D>;
   using FL = Flash<BN, WAVES, D>;
-  static_assert(MASKT == 0 || (BN == 64 && !CAUSAL && D == 128), "masked tiles are 64 keys, D 128, not causal");
+  static_assert(MASKT == 0 || (BN == 64 && !CAUSAL), "masked tiles are 64 keys, not causal");
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
   FL F;
@@ -1132,7 +1132,7 @@ int launch_flash_prefill_bf16(const void* q, const void* k, const void* v, void*
 }
 
 int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v, void* o, int batch, int hq,
-                                     int hkv_real, int lq, int lk, const AttnStrides& st, float scale,
+                                     int hkv_real, int lq, int lk, int d, const AttnStrides& st, float scale,
                                      const void* mask, const MaskArgs& ma, int mask_dtype) {
   const PrefillGroups pg = prefill_groups(hq, hkv_real);
   const int G = pg.G, kvsub = pg.kvsub, hkv = pg.hkv;
@@ -1143,12 +1143,21 @@ int launch_flash_prefill_bf16_masked(const void* q, const void* k, const void* v
   const int nblk = (int)nblk64;
   const uint16_t *Q = (const uint16_t*)q, *K = (const uint16_t*)k, *V = (const uint16_t*)v;
   uint16_t* O = (uint16_t*)o;
-  if (mask_dtype == KH_F32)
-    flash_fwd_kernel<64, kWaves, 1, false, 1><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
-                                                                                  st, scale, nqb, mask, ma, kvsub);
-  else
-    flash_fwd_kernel<64, kWaves, 1, false, 2><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, lk,
-                                                                                  st, scale, nqb, mask, ma, kvsub);
+#define KH_MASKED_LAUNCH(MT, DD)                                                                               \
+  flash_fwd_kernel<64, kWaves, 1, false, MT, DD><<<nblk, kWaves * 64, 0, stream()>>>(Q, K, V, O, batch, hq, hkv, lq, \
+                                                                                     lk, st, scale, nqb, mask, ma, kvsub)
+  if (d == 64) {
+    if (mask_dtype == KH_F32)
+      KH_MASKED_LAUNCH(1, 64);
+    else
+      KH_MASKED_LAUNCH(2, 64);
+  } else {
+    if (mask_dtype == KH_F32)
+      KH_MASKED_LAUNCH(1, 128);
+    else
+      KH_MASKED_LAUNCH(2, 128);
+  }
+#undef KH_MASKED_LAUNCH
   KH_CHECK_LAUNCH();
   return KH_OK;
 }

@@ -36,15 +36,16 @@ def _mask(seed, shape, drop=0.25, std=2.0):
     return m.astype(np.float32)
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,L,S", [(2, 8, 4, 128, 128), (1, 4, 2, 77, 77), (1, 8, 8, 40, 300),
-                                          (1, 4, 1, 1, 200), (1, 6, 2, 100, 128), (2, 10, 1, 64, 200)])
-def test_mfma_full_mask_matches_oracle(hip, B, Hq, Hkv, L, S):
-    """bf16 q/k/v, D = 128 (MFMA kernel), a full [B, Hq, L, S] float32 mask with -inf entries;
+@pytest.mark.parametrize("B,Hq,Hkv,L,S,D", [(2, 8, 4, 128, 128, 128), (1, 4, 2, 77, 77, 128), (1, 8, 8, 40, 300, 128),
+                                            (1, 4, 1, 1, 200, 128), (1, 6, 2, 100, 128, 128), (2, 10, 1, 64, 200, 128),
+                                            (2, 8, 4, 128, 128, 64), (1, 6, 2, 77, 300, 64)])
+def test_mfma_full_mask_matches_oracle(hip, B, Hq, Hkv, L, S, D):
+    """bf16 q/k/v, D = 128 or 64 (MFMA kernel), a full [B, Hq, L, S] float32 mask with -inf entries;
     ragged S (77, 300) takes the packed-mask path, S = 128 reads the mask in place; L = 1 is a
     decode-shaped call; GQA 3 and 10 run as groups of one query head per workgroup."""
-    q, qh = seeded(101, (B, Hq, L, 128), "bfloat16")
-    k, kh = seeded(102, (B, Hkv, S, 128), "bfloat16")
-    v, vh = seeded(103, (B, Hkv, S, 128), "bfloat16")
+    q, qh = seeded(101, (B, Hq, L, D), "bfloat16")
+    k, kh = seeded(102, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(103, (B, Hkv, S, D), "bfloat16")
     m = _mask(104, (B, Hq, L, S))
     out = _run(q, k, v, dev(m))
     ref = oracle.sdpa_masked(qh, kh, vh, m)
