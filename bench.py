@@ -10,10 +10,11 @@ algorithm on a bounded sample as the CPU baseline.
 It also runs the full Qwen3-0.6B model of config C5 (512-token prefill, 128 greedy decode steps)
 and reports prefill tokens/s and TFLOP/s and decode tokens/s and GB/s against their rooflines.
 `--only copy` runs the 1 GiB copy that calibrates the HBM traffic counters; `--only mask` times the
-explicit-mask SDPA route at C3 shapes.
+explicit-mask SDPA route at C3 shapes; `--only prefill_b1` the causal prefill of one sequence at
+512 to 4096 tokens.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv|vendor|mask]
+                    [--only prefill|decode|norm|model|copy|load|sample|stream|gemm|gemv|vendor|mask|prefill_b1]
 Prints ONE JSON line.
 """
 import argparse
@@ -385,6 +386,30 @@ def prep_model(cfg, w, new_tokens=128, prompt_len=512, use_graph=True, ts_host=F
                 "decode_ms": timing["decode_ms"], "step_bytes": weight_bytes + kv_bytes, "tokens": toks[:8],
                 "ts_host": ts}
     return run
+
+
+def bench_prefill_one_sequence(steps, warmup):
+    """Causal bf16 flash prefill of ONE sequence (B = 1, Hq = 16, Hkv = 8, D = 128) at several prompt
+    lengths: the shapes whose query blocks are too few to fill the CUs as C3's four sequences do
+    (the key-split persistent form runs S >= 1024)."""
+    from kandle_amd import HipTensorHandle, kernels
+
+    out = {}
+    Hq, Hkv, D = 16, 8, 128
+    for S in (512, 1024, 2048, 4096):
+        q = bf16_tensor(311, (1, Hq, S, D))
+        k = bf16_tensor(312, (1, Hkv, S, D))
+        v = bf16_tensor(313, (1, Hkv, S, D))
+        o = HipTensorHandle.create_new((1, Hq, S, D), "bfloat16")
+        fn = lambda: kernels.flash_attention(q.handle, k.handle, v.handle, o, 1.0 / np.sqrt(D), True)  # noqa: E731
+        wall_ms, dev_ms = time_calls(fn, steps, warmup)
+        flops = 4.0 * Hq * S * S * D / 2.0
+        tf = flops / (dev_ms * 1e-3) / 1e12
+        out[f"S{S}"] = {"ms": round(dev_ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        for t in (q, k, v):
+            t.dispose()
+        o.dispose()
+    return out
 
 
 def bench_copy(steps, warmup):
@@ -951,7 +976,7 @@ def main():
     ap.add_argument("--eager-gemm", action="store_true",
                     help="--only gemm: launch each GEMM from the host instead of replaying a HIP graph")
     ap.add_argument("--only", choices=["prefill", "c1", "decode", "norm", "model", "copy", "load", "sample", "stream",
-                                       "gemm", "gemv", "vendor", "mask"], default=None)
+                                       "gemm", "gemv", "vendor", "mask", "prefill_b1"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -1026,6 +1051,9 @@ def main():
         res["sample"] = bench_sample(args.steps, args.warmup)
         if not args.no_cpu_baseline:
             res["sample"]["cpu_oracle_us"] = round(cpu_baseline_sample(), 1)
+    if args.only == "prefill_b1":
+        log("one-sequence causal prefill ...")
+        res["prefill_b1"] = bench_prefill_one_sequence(args.steps, args.warmup)
     if args.only == "copy":
         log("copy calibration ...")
         res["copy"] = bench_copy(args.steps, args.warmup)
@@ -1181,6 +1209,10 @@ def main():
             line.update({"value": round(1e6 / sm["wall_us"], 1), "unit": "draws/s",
                          "ms_per_step": round(sm["wall_us"] * 1e-3, 4),
                          "config": {"workload": "on-device sampling, T=0.7, top-k 50, top-p 0.9, vocab 151936"}})
+    if "prefill_b1" in res:
+        pb = res["prefill_b1"]
+        line.update({"value": pb["S4096"]["TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": pb["S4096"]["ms"],
+                     "config": {"workload": "causal bf16 flash prefill of one sequence, Hq=16, Hkv=8, D=128", **pb}})
     if "gemm" in res:
         gm = res["gemm"]
         line.update({"value": gm["layer_TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": round(gm["layer_us"] * 1e-3, 4),

@@ -107,10 +107,16 @@ __device__ __forceinline__ void mfma_block_begin() { __builtin_amdgcn_s_setprio(
 __device__ __forceinline__ void mfma_block_end() { __builtin_amdgcn_s_setprio(0); }
 
 // Shared per-workgroup setup and staging helpers.
-template <int BN, int WAVES, int D = 128>
+// KSPLIT = 2 (the persistent kernel's key-split form): waves w and w + WAVES / 2 own the same rows
+// and take the even and the odd 64-key chunk of every tile (key half khalf = w / SW), so an item
+// holds SW / G row slots per query head, half the rows of the KSPLIT = 1 form.
+template <int BN, int WAVES, int D = 128, int KSPLIT = 1>
 struct Flash {
   using C = Cfg<BN, WAVES, D>;
+  static_assert(KSPLIT == 1 || (KSPLIT == 2 && WAVES == 8 && C::NCH == 2), "key halves: 8 waves, 2 chunks per tile");
+  static constexpr int SW = WAVES / KSPLIT;  // waves holding an item's row slots
   int G, BMQ, tid, wave, lane, r, g, b, hk, hqi, q0, qw0, qi, ntiles, wave_last_q, wave_tiles, dcol;
+  int khalf = 0, half_last = -1;  // KSPLIT = 2: this wave's key half and its last chunk (-1: none)
   __amdgpu_buffer_rsrc_t rk, rv;
   // Element strides as 32-bit values (the entry checks they fit): half the scalar registers of
   // the 64-bit AttnStrides, which the persistent kernel needs for its item bookkeeping.
@@ -123,31 +129,40 @@ struct Flash {
     st = Strides32{(int32_t)s.qb, (int32_t)s.qh, (int32_t)s.qs, (int32_t)s.kb, (int32_t)s.kh, (int32_t)s.ks,
                    (int32_t)s.vb, (int32_t)s.vh, (int32_t)s.vs, (int32_t)s.ob, (int32_t)s.oh, (int32_t)s.os};
     G = hq / hkv;
-    BMQ = 32 * (WAVES / G);
+    BMQ = 32 * (SW / G);
     tid = threadIdx.x;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps derived values scalar
     lane = tid & 63;
     r = lane & 31;
     g = lane >> 5;
     dcol = 8 * (tid & (C::CPR - 1));
+    if constexpr (KSPLIT == 2) khalf = wave / SW;
+  }
+  // The wave's row-slot index among the SW waves that hold an item's rows.
+  __device__ __forceinline__ int swave() const {
+    if constexpr (KSPLIT == 1)
+      return wave;
+    else
+      return wave % SW;
   }
   // 32-row slot of this wave inside its head's query block.  Waves w and w + 4 of an 8-wave
   // workgroup share a SIMD; the second four take their slots mirrored, so that on the causal
   // diagonal (where a wave's chunk count grows with its slot) each SIMD pairs a short row block
   // with a long one.  Only the rows a wave owns change, not any row's arithmetic.
   __device__ __forceinline__ int row_slot(int wpg) const {
-    const int i = wave % wpg;
-    if (!kMirrorSlots || WAVES != 8 || wave < 4 || wpg == 1) return i;
+    const int i = swave() % wpg;
+    // (KSPLIT = 2: the SIMD's second wave is the other key half of the same slot)
+    if (!kMirrorSlots || WAVES != 8 || KSPLIT != 1 || wave < 4 || wpg == 1) return i;
     return wpg == 8 ? 11 - i : wpg - 1 - i;
   }
   // Per-item fields: query block qblk of (batch, kv head) pair bh.  With kvsub > 1 the "kv heads"
   // are groups of G query heads, kvsub of them reading each real kv head (hk / kvsub).
   __device__ __forceinline__ void set_item(int bh, int qblk, int hkv, int lq, int lk, bool causal, const uint16_t* K,
                                            const uint16_t* V, int kvsub = 1) {
-    const int wpg = WAVES / G;
+    const int wpg = SW / G;
     b = bh / hkv;
     hk = bh % hkv;
-    hqi = hk * G + wave / wpg;
+    hqi = hk * G + swave() / wpg;
     q0 = qblk * BMQ;
     qw0 = q0 + row_slot(wpg) * 32;
     qi = qw0 + r;
@@ -157,6 +172,7 @@ struct Flash {
     const int nchunks = (kv_end + C::BNC - 1) / C::BNC;
     wave_last_q = min(qw0 + 31, lq - 1);
     wave_tiles = qw0 >= lq ? 0 : (causal ? min(nchunks, wave_last_q / C::BNC + 1) : nchunks);
+    if constexpr (KSPLIT == 2) half_last = wave_tiles > khalf ? khalf + 2 * ((wave_tiles - 1 - khalf) / 2) : -1;
     const int hkr = hk / kvsub;
     rk = make_rsrc(K + (int64_t)b * st.kb + (int64_t)hkr * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 2));
     rv = make_rsrc(V + (int64_t)b * st.vb + (int64_t)hkr * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 2));
@@ -183,8 +199,8 @@ struct Flash {
   // kernel's prefetch), from the per-workgroup fields alone.
   __device__ __forceinline__ void load_q_of(int bh, int qblk, int hkv, const uint16_t* Q, int lq,
                                             bf16x8 (&qreg)[C::NQ]) const {
-    const int wpg = WAVES / G;
-    const int bb = bh / hkv, hqn = (bh % hkv) * G + wave / wpg, qin = qblk * BMQ + row_slot(wpg) * 32 + r;
+    const int wpg = SW / G;
+    const int bb = bh / hkv, hqn = (bh % hkv) * G + swave() / wpg, qin = qblk * BMQ + row_slot(wpg) * 32 + r;
     const auto rq = make_rsrc(Q + (int64_t)bb * st.qb + (int64_t)hqn * st.qh,
                               (uint32_t)(((int64_t)(lq - 1) * st.qs + D) * 2));
     const uint32_t qoff = (uint32_t)(((int64_t)qin * st.qs + 8 * g) * 2);
@@ -620,13 +636,18 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
 // each).  When P is a multiple of the pair count, the odd passes are mirrored so that a workgroup
 // keeps one (batch, kv head) pair for all its items (its K/V stay in its XCD's L2).  The per-item
 // arithmetic is the tile kernel's, so outputs are identical to it.
-template <bool CAUSAL, int D = 128>
+// KSPLIT = 2 (one sequence of a few thousand tokens: too few 128-row items to pair): items of half
+// the rows, each row slot held by two waves that take the even and the odd 64-key chunk of every
+// tile; at the end of an item the two halves' (m, l, O) merge through the staging buffer the loop
+// left free, and the first half stores the rows.  Its sums are grouped differently from the
+// KSPLIT = 1 form, so its outputs differ from it within the rounding of the split.
+template <bool CAUSAL, int D = 128, int KSPLIT = 1>
 __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale, int n_qblocks) {
   constexpr int BN = 128, WAVES = kPersistWaves;
   using C = Cfg<BN, WAVES, D>;
-  using FL = Flash<BN, WAVES, D>;
+  using FL = Flash<BN, WAVES, D, KSPLIT>;
   constexpr int STAGE = C::KTILE + C::VTILE;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
   const int P = gridDim.x, w = blockIdx.x;
@@ -682,7 +703,7 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
     const bool more = item(k + 1, bhn, qbn);
     // A wave's Q registers are free once it has formed its last chunk's scores: the next item's Q
     // is loaded into them there (at the start for a wave with no rows in this item).
-    if (more && F.wave_tiles == 0) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
+    if (more && (KSPLIT == 1 ? F.wave_tiles == 0 : F.half_last < 0)) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
     const int ntiles = F.ntiles;
     for (int t = 0; t < ntiles; ++t) {
       const bool next_same = t + 1 < ntiles;
@@ -699,11 +720,11 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
 #pragma unroll
       for (int c = 0; c < C::NCH; ++c) {
         const int tc = t * C::NCH + c;  // 64-key compute chunk
-        if (tc < F.wave_tiles) {
+        if (tc < F.wave_tiles && (KSPLIT == 1 || c == F.khalf)) {
           f32x16 sacc[C::NSUB];
           bf16x8 pk[2 * C::NSUB];
           F.template qk<true>(ks + c * C::BNC * C::KSTR, qreg, sl.mneg, sacc);
-          if (more && tc == F.wave_tiles - 1) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
+          if (more && tc == (KSPLIT == 1 ? F.wave_tiles - 1 : F.half_last)) F.load_q_of(bhn, qbn, hkv, Q, lq, qreg);
           F.template mask<CAUSAL>(tc, lk, sacc);
           float ps = SoftmaxLog2::exponentiate(sacc, c2, pk);
           if (sl.need_raise(ps)) {
@@ -722,7 +743,39 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
       __syncthreads();
       buf ^= 1;
     }
-    F.template store_o<false>(O, lq, sl.l, oacc);
+    if constexpr (KSPLIT == 1) {
+      F.template store_o<false>(O, lq, sl.l, oacc);
+    } else {
+      // Merge the two key halves of each row slot: the second writes (m, l, O) per lane into the
+      // free staging buffer (the other holds the next item's first tile), the first combines them
+      // with the log-sum-exp rule and stores the rows.  The last barrier keeps the buffer until
+      // every read is done: the next item's second tile is staged there.
+      constexpr int MS = 2 + 16 * C::ND;  // floats per lane
+      static_assert(WAVES / 2 * MS * 64 * 4 <= STAGE * 2, "the merge fits a staging buffer");
+      float* mp = reinterpret_cast<float*>(smem + (buf ^ 1) * STAGE) + F.swave() * MS * 64 + F.lane;
+      if (F.khalf == 1) {
+        mp[0] = sl.m;
+        mp[64] = sl.l;
+#pragma unroll
+        for (int dt = 0; dt < C::ND; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) mp[(2 + 16 * dt + j) * 64] = oacc[dt][j];
+      }
+      __syncthreads();
+      if (F.khalf == 0) {
+        const float m1 = mp[0], l1 = mp[64];
+        const float mt = fmaxf(sl.m, m1);
+        // a half with no unmasked key has m = -inf and adds nothing (its l and O are 0)
+        const float a0 = sl.m == -INFINITY ? 0.f : fast_exp2((sl.m - mt) * c2);
+        const float a1 = m1 == -INFINITY ? 0.f : fast_exp2((m1 - mt) * c2);
+#pragma unroll
+        for (int dt = 0; dt < C::ND; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) oacc[dt][j] = oacc[dt][j] * a0 + mp[(2 + 16 * dt + j) * 64] * a1;
+        F.template store_o<false>(O, lq, sl.l * a0 + l1 * a1, oacc);
+      }
+      __syncthreads();
+    }
     if (!more) break;
     F.set_item(bhn, qbn, hkv, lq, lk, CAUSAL, K, V);
 #pragma unroll
@@ -778,6 +831,22 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
+  if (causal && kvsub == 1 && G <= 4 && kPersistMinItems > 0 && nblk64 < (int64_t)kPersistMinItems * cu_count()) {
+    // Too few 128-row items to pair heavy with light ones (one sequence of a few thousand tokens:
+    // 256 items of very unequal length on 256 CUs): the key-split persistent form, whose items
+    // hold half the rows, when that gives at least half the CUs one (B = 1, 16 / 8 heads: S = 4096
+    // 117.6 -> 103.0 us, 2048 63.4 -> 42.1, 1024 30.1 -> 24.6; shorter prompts keep the small
+    // workgroups below).
+    const int BMQ2 = 32 * (kPersistWaves / 2 / G);
+    const int nqb2 = (lq + BMQ2 - 1) / BMQ2;
+    if ((int64_t)nqb2 * batch * hkv >= cu_count() / 2) {
+      flash_fwd_persistent_kernel<true, D, 2><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
+          (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq,
+          (int)lk, st, scale, nqb2);
+      KH_CHECK_LAUNCH();
+      return KH_OK;
+    }
+  }
   if (nblk64 < kSmallGrid && G <= 2) {
     if (causal)
       launch_fwd<kSmallBN, 2, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);

@@ -413,6 +413,52 @@ def test_flash_c3_full_size(hip):
         t.dispose()
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [
+    (1, 16, 8, 4096, 128),   # one sequence: 512 items of 64 rows, two per CU, heaviest with lightest
+    (1, 16, 8, 2048, 128),   # 256 items, one per CU
+    (1, 16, 8, 1024, 128),   # 128 items: half the CUs
+    (1, 8, 8, 4096, 128),    # GQA 1: 128-row items
+    (1, 16, 4, 4096, 128),   # GQA 4: 32-row items
+    (1, 16, 8, 3000, 128),   # ragged last item
+    (1, 16, 8, 4096, 64),
+])
+def test_flash_bf16_key_split_persistent(hip, B, Hq, Hkv, S, D):
+    """Causal prefill of one long sequence (too few 128-row items to pair on the CUs) runs the
+    key-split persistent form: two waves per row slot take alternate 64-key chunks and merge their
+    (m, l, O).  Checked: the first and last heads' whole slices, one row of every (head, 64-row
+    item) at an offset that moves through the item's row slots, and every head's last 64 rows."""
+    q, qh = seeded(131, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(132, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(133, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    assert np.all(np.isfinite(out))
+    G = Hq // Hkv
+    worst = 0.0
+    for h in (0, Hq - 1):
+        ref = oracle.sdpa(qh[:, h:h + 1], kh[:, h // G:h // G + 1], vh[:, h // G:h // G + 1], causal=True)
+        err = float(np.max(np.abs(out[:, h] - ref[:, 0])))
+        worst = max(worst, err)
+        assert err < BF16_ATOL, ("slice", h, err)
+    tail = 64
+    tmask = np.where(np.arange(S)[None, :] > (S - tail + np.arange(tail))[:, None], -np.inf, 0.0).astype(np.float32)
+    ref = oracle.sdpa_masked(qh[:, :, S - tail:], kh, vh, tmask)
+    err = float(np.max(np.abs(out[:, :, S - tail:] - ref)))
+    worst = max(worst, err)
+    assert err < BF16_ATOL, ("last rows", err)
+    nblk = (S + 63) // 64
+    for h in range(Hq):
+        hk = h // G
+        rows = np.array([min(blk * 64 + (7 * blk + 5 * h) % 64, S - 1) for blk in range(nblk)])
+        bmask = np.where(np.arange(S)[None, :] > rows[:, None], -np.inf, 0.0).astype(np.float32)
+        ref = oracle.sdpa_masked(qh[:, h:h + 1, rows], kh[:, hk:hk + 1], vh[:, hk:hk + 1], bmask)
+        err = float(np.max(np.abs(out[:, h, rows] - ref[:, 0])))
+        worst = max(worst, err)
+        assert err < BF16_ATOL, ("item rows", h, err)
+    print(f"key-split persistent {B, Hq, Hkv, S, D}: max abs error {worst:.4g}")
+    for t in (q, k, v):
+        t.dispose()
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_bf16_growing_scores_raise_reference(hip, causal):
     """Keys whose norms grow along the sequence (x1 .. x4), so the scores of later key chunks
