@@ -29,6 +29,8 @@
 // on the reference chosen), and l sums the bf16 P the PV product applies.
 // The explicit-mask route keeps a thresholded maximum (SoftmaxRaw), which reproduces the reference
 // softmax's f32(-1e38) floor and its 0 / 0 rows.
+#include <type_traits>
+
 #include "attention.h"
 
 using namespace kh;
@@ -207,10 +209,11 @@ struct Flash {
 #pragma unroll
     for (int c = 0; c < C::NQ; ++c) qreg[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c));
   }
-  // K and V byte ranges of pair bh.
+  // K and V byte ranges of pair bh (kvsub as set_item).
   __device__ __forceinline__ void kv_rsrc_of(int bh, int hkv, int lk, const uint16_t* K, const uint16_t* V,
-                                             __amdgpu_buffer_rsrc_t& rkn, __amdgpu_buffer_rsrc_t& rvn) const {
-    const int bb = bh / hkv, hh = bh % hkv;
+                                             __amdgpu_buffer_rsrc_t& rkn, __amdgpu_buffer_rsrc_t& rvn,
+                                             int kvsub = 1) const {
+    const int bb = bh / hkv, hh = (bh % hkv) / kvsub;
     rkn = make_rsrc(K + (int64_t)bb * st.kb + (int64_t)hh * st.kh, (uint32_t)(((int64_t)(lk - 1) * st.ks + D) * 2));
     rvn = make_rsrc(V + (int64_t)bb * st.vb + (int64_t)hh * st.vh, (uint32_t)(((int64_t)(lk - 1) * st.vs + D) * 2));
   }
@@ -641,10 +644,13 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void flash_fwd_kernel(
 // tile; at the end of an item the two halves' (m, l, O) merge through the staging buffer the loop
 // left free, and the first half stores the rows.  Its sums are grouped differently from the
 // KSPLIT = 1 form, so its outputs differ from it within the rounding of the split.
-template <bool CAUSAL, int D = 128, int KSPLIT = 1>
+// GROUPS: hkv counts groups of G query heads, kvsub of them per real kv head (a GQA ratio other than
+// 1, 2, 4, 8, as the tile kernel's kvsub); without it kvsub is ignored.
+template <bool CAUSAL, int D = 128, int KSPLIT = 1, bool GROUPS = false>
 __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale, int n_qblocks) {
+    uint16_t* __restrict__ O, int batch, int hq, int hkv, int lq, int lk, AttnStrides st, float scale, int n_qblocks,
+    int kvsub) {
   constexpr int BN = 128, WAVES = kPersistWaves;
   using C = Cfg<BN, WAVES, D>;
   using FL = Flash<BN, WAVES, D, KSPLIT>;
@@ -680,7 +686,7 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
   if (!item(0, bh, qblk)) return;
   FL F;
   F.setup(hq, hkv, st);
-  F.set_item(bh, qblk, hkv, lq, lk, CAUSAL, K, V);
+  F.set_item(bh, qblk, hkv, lq, lk, CAUSAL, K, V, GROUPS ? kvsub : 1);
   const float c2 = scale * kLog2e;
   bf16x8 qreg[C::NQ];
   F.load_q(Q, lq, qreg);
@@ -712,7 +718,7 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
         F.load_rows(F.rv, F.st.vs, t + 1, vst);
       } else if (more) {
         __amdgpu_buffer_rsrc_t rkn, rvn;
-        F.kv_rsrc_of(bhn, hkv, lk, K, V, rkn, rvn);
+        F.kv_rsrc_of(bhn, hkv, lk, K, V, rkn, rvn, GROUPS ? kvsub : 1);
         F.load_rows(rkn, F.st.ks, 0, kst);
         F.load_rows(rvn, F.st.vs, 0, vst);
       }
@@ -777,7 +783,7 @@ __global__ __launch_bounds__(kPersistWaves * 64, 1) void flash_fwd_persistent_ke
       __syncthreads();
     }
     if (!more) break;
-    F.set_item(bhn, qbn, hkv, lq, lk, CAUSAL, K, V);
+    F.set_item(bhn, qbn, hkv, lq, lk, CAUSAL, K, V, GROUPS ? kvsub : 1);
 #pragma unroll
     for (int dt = 0; dt < C::ND; ++dt)
 #pragma unroll
@@ -831,7 +837,19 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
   const int nqb = (lq + BMQ - 1) / BMQ;
   const int64_t nblk64 = (int64_t)nqb * batch * hkv;
   KH_REQUIRE(nblk64 <= INT32_MAX, "kh_flash_attention: grid too large");
-  if (causal && kvsub == 1 && G <= 4 && kPersistMinItems > 0 && nblk64 < (int64_t)kPersistMinItems * cu_count()) {
+  // The persistent forms (one resident workgroup per CU); GROUPS instantiations serve kvsub > 1.
+  auto persist = [&](auto ksplit, int n_qb) {
+    constexpr int KSP = decltype(ksplit)::value;
+    if (kvsub > 1)
+      flash_fwd_persistent_kernel<true, D, KSP, true><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
+          (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
+          st, scale, n_qb, kvsub);
+    else
+      flash_fwd_persistent_kernel<true, D, KSP, false><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
+          (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
+          st, scale, n_qb, 1);
+  };
+  if (causal && G <= 4 && kPersistMinItems > 0 && nblk64 < (int64_t)kPersistMinItems * cu_count()) {
     // Too few 128-row items to pair heavy with light ones (one sequence of a few thousand tokens:
     // 256 items of very unequal length on 256 CUs): the key-split persistent form, whose items
     // hold half the rows, when that gives at least half the CUs one (B = 1, 16 / 8 heads: S = 4096
@@ -840,9 +858,7 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
     const int BMQ2 = 32 * (kPersistWaves / 2 / G);
     const int nqb2 = (lq + BMQ2 - 1) / BMQ2;
     if ((int64_t)nqb2 * batch * hkv >= cu_count() / 2) {
-      flash_fwd_persistent_kernel<true, D, 2><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
-          (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq,
-          (int)lk, st, scale, nqb2);
+      persist(std::integral_constant<int, 2>{}, nqb2);
       KH_CHECK_LAUNCH();
       return KH_OK;
     }
@@ -857,12 +873,10 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
       launch_fwd<kSmallBN, 4, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
     else
       launch_fwd<kSmallBN, 4, false, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
-  } else if (causal && kvsub == 1 && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
+  } else if (causal && kPersistMinItems > 0 && nblk64 >= (int64_t)kPersistMinItems * cu_count()) {
     // Enough causal query blocks for every CU to take several: one resident workgroup per CU.
     static_assert(kPersistWaves == kWaves, "the persistent kernel's query blocks are the tile kernel's");
-    flash_fwd_persistent_kernel<true, D><<<cu_count(), kPersistWaves * 64, 0, stream()>>>(
-        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, batch, hq, hkv, (int)lq, (int)lk,
-        st, scale, nqb);
+    persist(std::integral_constant<int, 1>{}, nqb);
   } else if (causal) {
     launch_fwd<128, kWaves, true, D>(q, k, v, o, batch, hq, hkv, lq, lk, st, scale, kvsub);
   } else {

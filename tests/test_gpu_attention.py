@@ -427,6 +427,21 @@ def test_flash_bf16_key_split_persistent(hip, B, Hq, Hkv, S, D):
     key-split persistent form: two waves per row slot take alternate 64-key chunks and merge their
     (m, l, O).  Checked: the first and last heads' whole slices, one row of every (head, 64-row
     item) at an offset that moves through the item's row slots, and every head's last 64 rows."""
+    _check_long_causal(B, Hq, Hkv, S, D, "key-split persistent")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S", [
+    (1, 40, 8, 4096),   # ratio 5 (Qwen3-14B's heads): 640 items, the persistent form over groups of 1
+    (1, 24, 8, 2048),   # ratio 3: the key-split form over groups of 1
+    (2, 12, 2, 4096),   # ratio 6: the key-split form over groups of 2
+])
+def test_flash_bf16_persistent_other_gqa_ratios(hip, B, Hq, Hkv, S):
+    """Long causal prefills at GQA ratios other than 1, 2, 4, 8 run the persistent forms over groups
+    of query heads (several groups per kv head); checked as the key-split test."""
+    _check_long_causal(B, Hq, Hkv, S, 128, "persistent, GQA groups")
+
+
+def _check_long_causal(B, Hq, Hkv, S, D, what):
     q, qh = seeded(131, (B, Hq, S, D), "bfloat16")
     k, kh = seeded(132, (B, Hkv, S, D), "bfloat16")
     v, vh = seeded(133, (B, Hkv, S, D), "bfloat16")
@@ -454,7 +469,7 @@ def test_flash_bf16_key_split_persistent(hip, B, Hq, Hkv, S, D):
         err = float(np.max(np.abs(out[:, h, rows] - ref[:, 0])))
         worst = max(worst, err)
         assert err < BF16_ATOL, ("item rows", h, err)
-    print(f"key-split persistent {B, Hq, Hkv, S, D}: max abs error {worst:.4g}")
+    print(f"{what} {B, Hq, Hkv, S, D}: max abs error {worst:.4g}")
     for t in (q, k, v):
         t.dispose()
 
