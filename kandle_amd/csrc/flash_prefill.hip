@@ -1,4 +1,10 @@
-// bf16 causal / non-causal GQA flash-attention prefill for gfx950, head_dim 128.
+// bf16 causal / non-causal GQA flash-attention prefill for gfx950, head_dim 64 or 128, and the
+// split-bf16 fp32 attention of the float32-activation model.
+//
+// Launch forms of the bf16 kernel (launch_prefill_d): the tile kernel (one workgroup per query
+// block, 8 waves, or 2-4 waves on small grids); the persistent form for causal inputs with at least
+// two 128-row items per CU (C3); its key-split form for one or two long sequences (too few items to
+// pair); GQA ratios other than 1, 2, 4, 8 as groups of query heads on all of them.
 //
 // Semantics follow the reference kernel (packages/backend-webgpu/src/kernels/attention/builder.ts:138-329):
 // score = (q . k) * scale, key j > query i masked when causal (top-left), query head h reads kv head
