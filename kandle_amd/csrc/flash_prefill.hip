@@ -913,8 +913,13 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
 //    16 c + 8 g .. + 7 -- 64 contiguous bytes of a row per lane pair and k-step.  swap23 (bits 2
 //    and 3 of the key index exchanged) makes accumulator registers j = 0..7 of lane group g hold
 //    keys 8 g + j and j = 8..15 keys 16 + 8 g + j - 8, the B-operand layout of the PV product.
-//  - V^T (the A operand of O^T): lane (r, g) needs V[16 kc + 8 g + e][32 dt + r], e = 0..7: one
-//    4-byte load per e, the 32 lanes of a group reading 128 contiguous bytes of one key row.
+//  - V^T (the A operand of O^T): row m of output tile dt is column d = 4 m + dt (a permutation
+//    of the rows, which changes no sum), so lane (r, g) needs V[16 kc + 8 g + e][4 r + dt] for
+//    dt = 0..3 -- one 16-byte load per key e = 0..7, the 32 lanes of a group reading 512
+//    contiguous bytes of one key row -- and the four tiles' accumulator registers j form 16
+//    contiguous output bytes.  (4-byte loads along 32 dt + r took four times the load
+//    instructions, and with 80 loads per chunk the wave stalled at issue on the 63 loads the
+//    counter tracks: C5's attention 19.3 -> 18.2 us per layer, outputs bit-identical.)
 // The four waves' (m, l, O) are merged through LDS at the end by wave 0, in wave order.  Softmax
 // as SoftmaxLog2 (the QK^T accumulators start at -m; the reference is raised when a lane's sum of
 // P exceeds kSumMax).
@@ -941,18 +946,23 @@ __device__ __forceinline__ void split8(const uint4& x0, const uint4& x1, bf16x8&
   hi = __builtin_bit_cast(bf16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
   lo = __builtin_bit_cast(bf16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
 }
-__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
-}
 
 // One 32-key chunk's operands of one wave, as loaded: K rows (8 k-steps of two 16-byte loads) and
-// V^T elements (4 column tiles x 2 key steps x 8 keys).
+// V rows (2 key steps x 8 keys, columns 4 r .. 4 r + 3 of each).
 struct SplitK {
   uint4 k[16];
 };
 struct SplitV {
-  uint32_t v[64];
+  uint4 v[16];
 };
+// Word i (compile-time) of a 16-byte load.
+template <int I>
+__device__ __forceinline__ uint32_t word(const uint4& u) {
+  if constexpr (I == 0) return u.x;
+  else if constexpr (I == 1) return u.y;
+  else if constexpr (I == 2) return u.z;
+  else return u.w;
+}
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
@@ -997,13 +1007,10 @@ __global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
   };
   auto load_v = [&](int tc, SplitV& ch) {
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
+    for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          ch.v[16 * dt + 8 * kc + e] =
-              buf_load4(rv, (uint32_t)(((int64_t)(32 * tc + 16 * kc + 8 * g + e) * st.vs + 32 * dt + r) * 4));
+      for (int e = 0; e < 8; ++e)
+        ch.v[8 * kc + e] = buf_load16(rv, (uint32_t)(((int64_t)(32 * tc + 16 * kc + 8 * g + e) * st.vs + 4 * r) * 4));
   };
 
   f32x16 oacc[ND];
@@ -1059,19 +1066,26 @@ __global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
     }
     sl.l += ps;
   };
-  // O^T += V^T P^T over the chunk's two 16-key steps
+  // O^T += V^T P^T over the chunk's two 16-key steps; tile dt's A row m is column d = 4 m + dt
+  auto pv_tile = [&](auto dt_c, const SplitV& ch, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
+    constexpr int DT = decltype(dt_c)::value;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const uint4* vv = ch.v + 8 * kc;
+      bf16x8 vh8, vl8;
+      split8(make_uint4(word<DT>(vv[0]), word<DT>(vv[1]), word<DT>(vv[2]), word<DT>(vv[3])),
+             make_uint4(word<DT>(vv[4]), word<DT>(vv[5]), word<DT>(vv[6]), word<DT>(vv[7])), vh8, vl8);
+      oacc[DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh8, ph[kc], oacc[DT], 0, 0, 0);
+      oacc[DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh8, pl[kc], oacc[DT], 0, 0, 0);
+      oacc[DT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl8, ph[kc], oacc[DT], 0, 0, 0);
+    }
+  };
   auto pv = [&](const SplitV& ch, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const uint32_t* vv = ch.v + 16 * dt + 8 * kc;
-        bf16x8 vh8, vl8;
-        split8(make_uint4(vv[0], vv[1], vv[2], vv[3]), make_uint4(vv[4], vv[5], vv[6], vv[7]), vh8, vl8);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh8, ph[kc], oacc[dt], 0, 0, 0);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh8, pl[kc], oacc[dt], 0, 0, 0);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl8, ph[kc], oacc[dt], 0, 0, 0);
-      }
+    static_assert(ND == 4, "four output tiles");
+    pv_tile(std::integral_constant<int, 0>{}, ch, ph, pl);
+    pv_tile(std::integral_constant<int, 1>{}, ch, ph, pl);
+    pv_tile(std::integral_constant<int, 2>{}, ch, ph, pl);
+    pv_tile(std::integral_constant<int, 3>{}, ch, ph, pl);
   };
   // This wave's chunks wave, wave + 4, ...: K in two register sets (the next chunk's K loads during
   // the whole current chunk), V in one (the next chunk's V loads once PV has consumed the current
@@ -1143,18 +1157,19 @@ __global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
 #pragma unroll
       for (int j = 0; j < 16; ++j) oacc[dt][j] += a * p[(2 + 16 * dt + j) * 64];
   }
-  // O[qi][d] = O / l; lane holds d = 32 dt + 8 a + 4 g .. + 3 (l: this lane's keys plus lane ^ 32's)
+  // O[qi][d] = O / l (l: this lane's keys plus lane ^ 32's).  Register j = 4 a + i of tile dt holds
+  // A row m = 8 a + 4 g + i, i.e. d = 4 m + dt: the four tiles' registers j form 16 contiguous bytes.
   const float l_tot = l + __shfl_xor(l, 32, 64);
   if (qi < lq) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     float* orow = O + (int64_t)b * st.ob + (int64_t)h * st.oh + (int64_t)qi * st.os;
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<float4*>(orow + 32 * dt + 8 * a + 4 * g) =
-            make_float4(oacc[dt][4 * a] * inv, oacc[dt][4 * a + 1] * inv, oacc[dt][4 * a + 2] * inv,
-                        oacc[dt][4 * a + 3] * inv);
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(orow + 4 * (8 * a + 4 * g + i)) =
+            make_float4(oacc[0][4 * a + i] * inv, oacc[1][4 * a + i] * inv, oacc[2][4 * a + i] * inv,
+                        oacc[3][4 * a + i] * inv);
   }
 }
 
