@@ -42,7 +42,11 @@ __device__ __forceinline__ float4 buf_load16f(__amdgpu_buffer_rsrc_t r, uint32_t
 // PV and V during QK^T; with NW = 8 (two per SIMD, for short inputs whose blocks would otherwise
 // give each SIMD a chain of tiles; 256 registers per wave) the other wave on the SIMD hides the
 // latency: K loads at the tile start and V after QK^T, into the registers K has left.
-template <int D, bool CAUSAL, int NW = kF32Waves>
+// V16 (head dim 128, V rows 16-byte aligned): row m of output block db is head-dim column 4 m + db
+// instead of 32 db + m -- a permutation of the MFMA rows, which changes no sum -- so the V^T
+// operands of one key for the four blocks are 16 contiguous bytes of its row: one 16-byte load per
+// key instead of four 4-byte ones.
+template <int D, bool CAUSAL, int NW = kF32Waves, bool V16 = false>
 __global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restrict__ Q,
                                                                    const float* __restrict__ K,
                                                                    const float* __restrict__ V, float* __restrict__ O,
@@ -98,15 +102,25 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restr
       kv[4 * i + 3] = t.w;
     }
   };
-  // V[key(s)][32 db + r] for the 16 keys key(s) = k0 + 8(s/4) + 4g + s%4 of the PV steps.
+  // V[key(s)][32 db + r] (V16: [4 r + db]) for the 16 keys key(s) = k0 + 8(s/4) + 4g + s%4 of the
+  // PV steps.
   auto load_v = [&](float (&vv)[NDB][16], int k0) {
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const int kr = k0 + 8 * (s >> 2) + 4 * g + (s & 3);
+      if constexpr (V16) {
+        static_assert(NDB == 4, "one 16-byte load per key");
+        const float4 x = buf_load16f(rv, kr < lk ? ((uint32_t)kr * vs + 4 * r) * 4u : kOut);
+        vv[0][s] = x.x;
+        vv[1][s] = x.y;
+        vv[2][s] = x.z;
+        vv[3][s] = x.w;
+      } else {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 32 * db + r) * 4u : kOut;
-        vv[db][s] = buf_load4f(rv, off);
+        for (int db = 0; db < NDB; ++db) {
+          const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 32 * db + r) * 4u : kOut;
+          vv[db][s] = buf_load4f(rv, off);
+        }
       }
     }
   };
@@ -163,13 +177,22 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restr
   }
 
   // Combine the waves: O = sum_w exp2(m_w - M) O_w / sum_w exp2(m_w - M) l_w, M = max_w m_w.
+  // Register v of block db holds MFMA row 8 (v / 4) + 4 g + v % 4: column 32 db + that row, or
+  // with V16 4 (that row) + db (the four blocks' registers v are then 16 contiguous bytes).
   if (g == 0) ml_s[w][r] = make_float2(m, l);
+  if constexpr (V16) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+    for (int v = 0; v < 16; ++v)
+      *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 4 * (8 * (v >> 2) + 4 * g + (v & 3))]) =
+          make_float4(oacc[0][v], oacc[1][v], oacc[2][v], oacc[3][v]);
+  } else {
 #pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4)
-      *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 32 * db + 8 * v4 + 4 * g]) =
-          make_float4(oacc[db][4 * v4], oacc[db][4 * v4 + 1], oacc[db][4 * v4 + 2], oacc[db][4 * v4 + 3]);
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4)
+        *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 32 * db + 8 * v4 + 4 * g]) =
+            make_float4(oacc[db][4 * v4], oacc[db][4 * v4 + 1], oacc[db][4 * v4 + 2], oacc[db][4 * v4 + 3]);
+  }
   __syncthreads();
   constexpr int TPQ = NW * 64 / 32;  // threads per query
   constexpr int CPT = D / TPQ;      // output columns per thread
@@ -219,7 +242,12 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restr
 // columns; step (kb, i) takes key 16 kb + 4 j + i from lane group j, the score that lane holds in
 // its register (kb, i).  Every output of a lane belongs to query r (columns 16 db + 4 j + i).
 // Eight waves (two per SIMD) split a block's tiles; K loads at the tile start, V during QK^T.
-template <int D, bool CAUSAL, int NW>
+// V16 (V rows 16-byte aligned): row m of output block db is head-dim column 8 m + db instead of
+// 16 db + m -- a permutation of the MFMA rows, which changes no sum -- so the V^T operands of one
+// key for all eight blocks are 32 contiguous bytes of its row: two 16-byte loads per key instead
+// of eight 4-byte ones, and a tile's loads fit the 63 a wave's load counter tracks (16 K + 64 V
+// 4-byte loads did not, and the wave stalled at issue).
+template <int D, bool CAUSAL, int NW, bool V16 = false>
 __global__ __launch_bounds__(NW * 64) void flash_f32_q16_kernel(const float* __restrict__ Q,
                                                                 const float* __restrict__ K,
                                                                 const float* __restrict__ V, float* __restrict__ O,
@@ -291,10 +319,18 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_q16_kernel(const float* __r
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int kr = k0 + 16 * (s >> 2) + 4 * j + (s & 3);
+      if constexpr (V16) {
+        static_assert(NDB == 8, "two 16-byte loads per key");
+        const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 8 * r) * 4u : kOut;
+        const float4 x0 = buf_load16f(rv, off), x1 = buf_load16f(rv, off == kOut ? kOut : off + 16);
+        vv[0][s] = x0.x; vv[1][s] = x0.y; vv[2][s] = x0.z; vv[3][s] = x0.w;
+        vv[4][s] = x1.x; vv[5][s] = x1.y; vv[6][s] = x1.z; vv[7][s] = x1.w;
+      } else {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 16 * db + r) * 4u : kOut;
-        vv[db][s] = buf_load4f(rv, off);
+        for (int db = 0; db < NDB; ++db) {
+          const uint32_t off = kr < lk ? ((uint32_t)kr * vs + 16 * db + r) * 4u : kOut;
+          vv[db][s] = buf_load4f(rv, off);
+        }
       }
     }
     f32x4 sacc[2];
@@ -343,11 +379,23 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_q16_kernel(const float* __r
   }
 
   // Combine the waves: O = sum_w exp2(m_w - M) O_w / sum_w exp2(m_w - M) l_w, M = max_w m_w.
+  // Register i of block db holds MFMA row 4 j + i: column 16 db + 4 j + i, or with V16
+  // 8 (4 j + i) + db (the eight blocks' registers i are then 32 contiguous columns).
   if (j == 0) ml_s[w][r] = make_float2(m, l);
+  if constexpr (V16) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
-    *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 16 * db + 4 * j]) =
-        make_float4(oacc[db][0], oacc[db][1], oacc[db][2], oacc[db][3]);
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 32 * j + 8 * i]) =
+          make_float4(oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]);
+      *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 32 * j + 8 * i + 4]) =
+          make_float4(oacc[4][i], oacc[5][i], oacc[6][i], oacc[7][i]);
+    }
+  } else {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      *reinterpret_cast<float4*>(&o_s[w][r * OSTR + 16 * db + 4 * j]) =
+          make_float4(oacc[db][0], oacc[db][1], oacc[db][2], oacc[db][3]);
+  }
   __syncthreads();
   constexpr int TPQ = NW * 64 / 16;  // threads per query
   constexpr int CPT = D / TPQ;       // output columns per thread
@@ -390,6 +438,15 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_q16_kernel(const float* __r
 template <int D, int NW>
 void launch_f32_dw(const float* q, const float* k, const float* v, float* o, int grid, int hq, int hkv, int lq,
                    int lk, const AttnStrides& st, float c, int nqb, bool causal) {
+  if constexpr (D == 128) {
+    if (aligned16(v) && st.vb % 4 == 0 && st.vh % 4 == 0 && st.vs % 4 == 0) {
+      if (causal)
+        flash_f32_kernel<D, true, NW, true><<<grid, NW * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+      else
+        flash_f32_kernel<D, false, NW, true><<<grid, NW * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
+      return;
+    }
+  }
   if (causal)
     flash_f32_kernel<D, true, NW><<<grid, NW * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
   else
@@ -439,12 +496,17 @@ int launch_flash_f32(const void* q, const void* k, const void* v, void* o, int b
     // fewer 32-query blocks than CUs: 16-query blocks (twice the workgroups)
     const int nqb16 = (lq + 15) / 16;
     const int grid16 = (int)(grid / nqb * nqb16);
-    if (causal)
-      flash_f32_q16_kernel<128, true, 8><<<grid16, 8 * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c,
-                                                                             nqb16);
-    else
-      flash_f32_q16_kernel<128, false, 8><<<grid16, 8 * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c,
-                                                                              nqb16);
+    const bool v16 = aligned16(v) && st.vb % 4 == 0 && st.vh % 4 == 0 && st.vs % 4 == 0;
+#define KH_Q16(CAUSAL, V16) \
+  flash_f32_q16_kernel<128, CAUSAL, 8, V16><<<grid16, 8 * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c, nqb16)
+    if (causal) {
+      if (v16) KH_Q16(true, true);
+      else KH_Q16(true, false);
+    } else {
+      if (v16) KH_Q16(false, true);
+      else KH_Q16(false, false);
+    }
+#undef KH_Q16
     KH_CHECK_LAUNCH();
     return KH_OK;
   }

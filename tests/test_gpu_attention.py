@@ -142,6 +142,7 @@ def test_generic_kernel_fp32_odd_head_dim(hip):
     (1, 2, 2, 1000, 1000, 128, True),  # eight key tiles per wave in the last blocks
     (1, 16, 16, 31, 257, 64, False),   # ragged key tile
     (2, 16, 8, 512, 512, 128, True),   # 512 workgroups: the four-wave variant (the others: eight)
+    (1, 16, 8, 512, 512, 128, True),   # 256 workgroups: eight waves, 32-query blocks
     (1, 8, 8, 400, 400, 128, True),    # 104 blocks of 32 queries: 16-query blocks, a partial last one
 ])
 def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
