@@ -907,8 +907,8 @@ int launch_prefill_d(const void* q, const void* k, const void* v, void* o, int b
 // takes the block's 32-key chunks w, w + 4, w + 8, ... (causal: up to the block's last row), so
 // the longest block's chain is a quarter of its keys.  A chunk is used by one wave only, so a wave
 // loads its operands straight from memory into registers in the MFMA layouts and splits them
-// there -- the next chunk's K during the whole current chunk, the next V once PV has consumed the
-// current one -- with no LDS staging and no barrier:
+// there -- the next chunk's K once QK^T has consumed the current one, the next V once PV has --
+// with no LDS staging and no barrier:
 //  - K (the A operand of S^T): lane (r, g) reads key row swap23(r) of the chunk, columns
 //    16 c + 8 g .. + 7 -- 64 contiguous bytes of a row per lane pair and k-step.  swap23 (bits 2
 //    and 3 of the key index exchanged) makes accumulator registers j = 0..7 of lane group g hold
@@ -1087,37 +1087,29 @@ __global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
     pv_tile(std::integral_constant<int, 2>{}, ch, ph, pl);
     pv_tile(std::integral_constant<int, 3>{}, ch, ph, pl);
   };
-  // This wave's chunks wave, wave + 4, ...: K in two register sets (the next chunk's K loads during
-  // the whole current chunk), V in one (the next chunk's V loads once PV has consumed the current
-  // one, and lands during the next QK^T and softmax).
+  // This wave's chunks wave, wave + 4, ...: one register set each for K and V.  The next chunk's K
+  // loads once QK^T has consumed the current one (and lands during the softmax and PV), the next
+  // V once PV has (landing during the next QK^T and softmax).  One loop body, not unrolled: the
+  // instruction cache starts cold at every launch, and each first pass through unrolled code waits
+  // on its fetches.  (K in two register sets, the next chunk's K loading during the whole current
+  // chunk, needs the body twice: C5-shape call 17.6 -> 18.2 us, 32-key call 7.4 -> 8.1 us.)
   {
-    SplitK ka, kb;
+    SplitK ka;
     SplitV vv;
     int tc = wave;
     if (tc < nchunks) {
       load_k(tc, ka);
       load_v(tc, vv);
     }
+#pragma unroll 1
     while (tc < nchunks) {
       const int nx = tc + kSplitWaves;
-      if (nx < nchunks) load_k(nx, kb);
-      {
-        bf16x8 ph[2], pl[2];
-        scores(tc, ka, ph, pl);
-        pv(vv, ph, pl);
-      }
+      bf16x8 ph[2], pl[2];
+      scores(tc, ka, ph, pl);
+      if (nx < nchunks) load_k(nx, ka);
+      pv(vv, ph, pl);
       if (nx < nchunks) load_v(nx, vv);
       tc = nx;
-      if (tc >= nchunks) break;
-      const int nx2 = tc + kSplitWaves;
-      if (nx2 < nchunks) load_k(nx2, ka);
-      {
-        bf16x8 ph[2], pl[2];
-        scores(tc, kb, ph, pl);
-        pv(vv, ph, pl);
-      }
-      if (nx2 < nchunks) load_v(nx2, vv);
-      tc = nx2;
     }
   }
   // Merge: waves 1..3 write (m, l, O) to LDS; wave 0 combines them in wave order.
