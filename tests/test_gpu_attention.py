@@ -442,10 +442,14 @@ def test_flash_bf16_persistent_other_gqa_ratios(hip, B, Hq, Hkv, S):
     _check_long_causal(B, Hq, Hkv, S, 128, "persistent, GQA groups")
 
 
-def _check_long_causal(B, Hq, Hkv, S, D, what):
+def _check_long_causal(B, Hq, Hkv, S, D, what, Lk=None):
+    """Causal bf16 prefill of S queries over Lk keys (default S; top-left mask: key j > query i is
+    masked): two whole (b, h) slices, the last 64 rows of every head and one row of every 64-row
+    block of every head, against the oracle."""
+    Lk = S if Lk is None else Lk
     q, qh = seeded(131, (B, Hq, S, D), "bfloat16")
-    k, kh = seeded(132, (B, Hkv, S, D), "bfloat16")
-    v, vh = seeded(133, (B, Hkv, S, D), "bfloat16")
+    k, kh = seeded(132, (B, Hkv, Lk, D), "bfloat16")
+    v, vh = seeded(133, (B, Hkv, Lk, D), "bfloat16")
     out = _sdpa_gpu(q, k, v, True)
     assert np.all(np.isfinite(out))
     G = Hq // Hkv
@@ -456,7 +460,7 @@ def _check_long_causal(B, Hq, Hkv, S, D, what):
         worst = max(worst, err)
         assert err < BF16_ATOL, ("slice", h, err)
     tail = 64
-    tmask = np.where(np.arange(S)[None, :] > (S - tail + np.arange(tail))[:, None], -np.inf, 0.0).astype(np.float32)
+    tmask = np.where(np.arange(Lk)[None, :] > (S - tail + np.arange(tail))[:, None], -np.inf, 0.0).astype(np.float32)
     ref = oracle.sdpa_masked(qh[:, :, S - tail:], kh, vh, tmask)
     err = float(np.max(np.abs(out[:, :, S - tail:] - ref)))
     worst = max(worst, err)
@@ -465,14 +469,26 @@ def _check_long_causal(B, Hq, Hkv, S, D, what):
     for h in range(Hq):
         hk = h // G
         rows = np.array([min(blk * 64 + (7 * blk + 5 * h) % 64, S - 1) for blk in range(nblk)])
-        bmask = np.where(np.arange(S)[None, :] > rows[:, None], -np.inf, 0.0).astype(np.float32)
+        bmask = np.where(np.arange(Lk)[None, :] > rows[:, None], -np.inf, 0.0).astype(np.float32)
         ref = oracle.sdpa_masked(qh[:, h:h + 1, rows], kh[:, hk:hk + 1], vh[:, hk:hk + 1], bmask)
         err = float(np.max(np.abs(out[:, h, rows] - ref[:, 0])))
         worst = max(worst, err)
         assert err < BF16_ATOL, ("item rows", h, err)
-    print(f"{what} {B, Hq, Hkv, S, D}: max abs error {worst:.4g}")
+    print(f"{what} {B, Hq, Hkv, S, Lk, D}: max abs error {worst:.4g}")
     for t in (q, k, v):
         t.dispose()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,Lk", [
+    (4, 16, 8, 4096, 4600),   # persistent form; keys past the last query are never visible
+    (4, 16, 8, 4096, 3000),   # persistent form; queries 3000 .. 4095 see every key
+    (1, 16, 8, 4096, 3500),   # key-split form
+    (1, 16, 8, 2000, 4096),   # key-split form, more keys than queries
+])
+def test_flash_bf16_persistent_causal_unequal_lengths(hip, B, Hq, Hkv, S, Lk):
+    """The persistent and key-split causal forms with query and key lengths that differ (the
+    reference's causal mask is top-left: query i sees keys 0 .. i whatever the key length)."""
+    _check_long_causal(B, Hq, Hkv, S, 128, "persistent, unequal lengths", Lk=Lk)
 
 
 @pytest.mark.parametrize("causal", [True, False])
