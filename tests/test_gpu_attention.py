@@ -158,6 +158,33 @@ def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
     assert_close_elem(out, ref, what="fp32 flash")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,S", [
+    (1, 8, 8, 200),    # 16-query blocks
+    (2, 16, 8, 512),   # 32-query blocks, four waves
+])
+def test_flash_f32_v_rows_not_16_byte_aligned(hip, B, Hq, Hkv, S):
+    """V read through a view one element into its storage: its rows are 4- but not 16-byte
+    aligned, so the fp32 kernels take 4-byte V loads along the head dim instead of the 16-byte
+    loads of permuted output rows; same results as the aligned call."""
+    from kandle_amd import HipTensorHandle
+    D = 128
+    q, qh = seeded(141, (B, Hq, S, D))
+    k, kh = seeded(142, (B, Hkv, S, D))
+    vflat = syn.normal(143, (B * Hkv * S * D + 1,)).astype(np.float32)
+    vbuf = Tensor(vflat)
+    v = Tensor(handle=HipTensorHandle.create_view(vbuf.handle.storage, (B, Hkv, S, D), "float32",
+                                                  (Hkv * S * D, S * D, D, 1), 1))
+    vh = vflat[1:].reshape(B, Hkv, S, D)
+    out = _sdpa_gpu(q, k, v, True)
+    ref = oracle.sdpa(qh, kh, vh, causal=True)
+    assert max_rel(out, ref) < F32_RTOL
+    assert_close_elem(out, ref, what="fp32 flash, unaligned V")
+    va = Tensor(np.ascontiguousarray(vh))
+    assert np.array_equal(out, _sdpa_gpu(q, k, va, True))  # the two load forms sum identically
+    for t in (q, k, v, vbuf, va):
+        t.dispose()
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_flash_f32_strided_views_and_negative_scale(hip, D):
     """fp32 kernel on [B, S, H, D] storage read through permuted views (no copy), with a negative
