@@ -1089,10 +1089,10 @@ __global__ __launch_bounds__(kSplitWaves * 64, 1) void flash_split_kernel(
   };
   // This wave's chunks wave, wave + 4, ...: one register set each for K and V.  The next chunk's K
   // loads once QK^T has consumed the current one (and lands during the softmax and PV), the next
-  // V once PV has (landing during the next QK^T and softmax).  One loop body, not unrolled: the
-  // instruction cache starts cold at every launch, and each first pass through unrolled code waits
-  // on its fetches.  (K in two register sets, the next chunk's K loading during the whole current
-  // chunk, needs the body twice: C5-shape call 17.6 -> 18.2 us, 32-key call 7.4 -> 8.1 us.)
+  // V once PV has (landing during the next QK^T and softmax).  One loop body, not unrolled: a
+  // wave's first pass through each copy of unrolled code waits on instruction fetches.  (K in two
+  // register sets, the next chunk's K loading during the whole current chunk, needs the body twice:
+  // C5-shape call 17.6 -> 18.2 us, 32-key call 7.4 -> 8.1 us.)
   {
     SplitK ka;
     SplitV vv;
