@@ -518,6 +518,33 @@ def test_flash_bf16_persistent_causal_unequal_lengths(hip, B, Hq, Hkv, S, Lk):
     _check_long_causal(B, Hq, Hkv, S, 128, "persistent, unequal lengths", Lk=Lk)
 
 
+def test_flash_bf16_persistent_16k_tokens(hip):
+    """One 16384-token causal prefill (16/8 heads, 1024 items: the persistent form) -- long-sequence
+    offsets and item lists; the last 64 rows of every head and one row per 256-row block of every
+    head against the oracle."""
+    B, Hq, Hkv, S, D = 1, 16, 8, 16384, 128
+    q, qh = seeded(151, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(152, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(153, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    assert np.all(np.isfinite(out))
+    G = Hq // Hkv
+    tail = 64
+    tmask = np.where(np.arange(S)[None, :] > (S - tail + np.arange(tail))[:, None], -np.inf, 0.0).astype(np.float32)
+    err = float(np.max(np.abs(out[:, :, S - tail:] - oracle.sdpa_masked(qh[:, :, S - tail:], kh, vh, tmask))))
+    assert err < BF16_ATOL, ("last rows", err)
+    for h in range(Hq):
+        rows = np.array([blk * 256 + (37 * blk + 11 * h) % 256 for blk in range(S // 256)])
+        bmask = np.where(np.arange(S)[None, :] > rows[:, None], -np.inf, 0.0).astype(np.float32)
+        ref = oracle.sdpa_masked(qh[:, h:h + 1, rows], kh[:, h // G:h // G + 1], vh[:, h // G:h // G + 1], bmask)
+        e = float(np.max(np.abs(out[:, h, rows] - ref[:, 0])))
+        assert e < BF16_ATOL, ("sampled rows", h, e)
+        err = max(err, e)
+    print(f"persistent 16k: max abs error {err:.4g}")
+    for t in (q, k, v):
+        t.dispose()
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_bf16_growing_scores_raise_reference(hip, causal):
     """Keys whose norms grow along the sequence (x1 .. x4), so the scores of later key chunks

@@ -115,6 +115,26 @@ def test_split_attention_softmax_raises_and_strided_views(hip):
     assert max_rel(out, oracle.sdpa(qp, kp, vp, scale=scale, causal=True)) < F32_RTOL
 
 
+def test_split_attention_8k_tokens(hip):
+    """An 8192-token causal call (8/4 heads): long-sequence offsets; the last 32 rows of every head
+    and one row per 256-row block of every head against the fp32 oracle."""
+    B, Hq, Hkv, S, D = 1, 8, 4, 8192, 128
+    q, qv = seeded(83, (B, Hq, S, D))
+    k, kv = seeded(84, (B, Hkv, S, D))
+    v, vv = seeded(85, (B, Hkv, S, D))
+    scale = 1.0 / np.sqrt(D)
+    out = _run(q, k, v, True, scale)
+    assert np.all(np.isfinite(out))
+    G = Hq // Hkv
+    for h in range(Hq):
+        rows = np.concatenate([np.array([blk * 256 + (29 * blk + 7 * h) % 256 for blk in range(S // 256)]),
+                               np.arange(S - 32, S)])
+        mask = np.where(np.arange(S)[None, :] > rows[:, None], -np.inf, 0.0).astype(np.float32)
+        ref = oracle.sdpa_masked(qv[:, h:h + 1, rows], kv[:, h // G:h // G + 1], vv[:, h // G:h // G + 1], mask,
+                                 scale=scale)
+        assert max_rel(out[:, h:h + 1, rows], ref) < F32_RTOL, h
+
+
 def test_split_attention_gqa_8(hip):
     """GQA 8 (query head h reads kv head h / 8)."""
     q, qv = seeded(80, (1, 16, 130, 128))
