@@ -27,6 +27,7 @@ using namespace kh;
 namespace {
 
 constexpr int kF32Waves = 4;  // waves per workgroup of the default (register-prefetching) variant
+constexpr int kQ16Waves = 4;  // waves per workgroup of the 16-query-block kernel
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kOut = 0xffffffffu;  // a byte offset past every buffer range: the load reads 0
 
@@ -241,7 +242,8 @@ __global__ __launch_bounds__(NW * 64) void flash_f32_kernel(const float* __restr
 // plus exchanges with lanes ^ 16 and ^ 32.  O^T = V^T P^T follows in 8 steps per 16 head-dim
 // columns; step (kb, i) takes key 16 kb + 4 j + i from lane group j, the score that lane holds in
 // its register (kb, i).  Every output of a lane belongs to query r (columns 16 db + 4 j + i).
-// Eight waves (two per SIMD) split a block's tiles; K loads at the tile start, V during QK^T.
+// NW waves split a block's tiles (kQ16Waves: four, one per SIMD; eight, two per SIMD, took C1
+// 11.1 -> 11.5 us once V loads were 16 bytes wide); K loads at the tile start, V during QK^T.
 // V16 (V rows 16-byte aligned): row m of output block db is head-dim column 8 m + db instead of
 // 16 db + m -- a permutation of the MFMA rows, which changes no sum -- so the V^T operands of one
 // key for all eight blocks are 32 contiguous bytes of its row: two 16-byte loads per key instead
@@ -498,7 +500,7 @@ int launch_flash_f32(const void* q, const void* k, const void* v, void* o, int b
     const int grid16 = (int)(grid / nqb * nqb16);
     const bool v16 = aligned16(v) && st.vb % 4 == 0 && st.vh % 4 == 0 && st.vs % 4 == 0;
 #define KH_Q16(CAUSAL, V16) \
-  flash_f32_q16_kernel<128, CAUSAL, 8, V16><<<grid16, 8 * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c, nqb16)
+  flash_f32_q16_kernel<128, CAUSAL, kQ16Waves, V16><<<grid16, kQ16Waves * 64, 0, stream()>>>(Q, K, V, Out, hq, hkv, lq, lk, st, c, nqb16)
     if (causal) {
       if (v16) KH_Q16(true, true);
       else KH_Q16(true, false);
