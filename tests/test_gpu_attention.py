@@ -144,6 +144,8 @@ def test_generic_kernel_fp32_odd_head_dim(hip):
     (2, 16, 8, 512, 512, 128, True),   # 512 workgroups: the four-wave 32-query variant
     (1, 16, 8, 512, 512, 128, True),   # 256 workgroups: eight waves, 32-query blocks
     (1, 8, 8, 400, 400, 128, True),    # 104 blocks of 32 queries: 16-query blocks, a partial last one
+    (1, 8, 4, 300, 120, 128, True),    # 16-query blocks, Lq > Lk (rows past Lk see every key)
+    (2, 6, 2, 33, 500, 128, True),     # 16-query blocks, Lq < Lk, GQA 3, a partial last block
 ])
 def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
     """fp32 flash kernel (fp32 MFMA; four or, on small grids, eight waves splitting a query block's
