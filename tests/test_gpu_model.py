@@ -234,10 +234,11 @@ def test_from_pretrained_sharded_checkpoint_matches_in_memory(hip, tmp_path):
 def test_fused_decode_block_matches_unfused_and_oracle(hip, act):
     """The decode step's fused attention block (kh_decode_attention_block: qk-norm + RoPE of q and of
     the new k row, K/V cache write, split-K attention, merge in the o_proj prologue, residual) against
-    the same step run as separate launches, and both against the oracle; caches past 8 chunks of
-    256 keys take the separate merge."""
-    # prologue merge; merge kernel (9+ chunks: 256 keys each for bf16, 128 for float32)
-    for max_seq, prompt_len in ((128, 40), (3000, 2100)):
+    the same step run as separate launches, and both against the oracle; caches past 8 chunks
+    (256 keys each with bf16 caches, 128 with float32) take the separate merge."""
+    # prologue merge (few chunks; with float32, 7 chunks); merge kernel (12 bf16 / 24 float32 chunks)
+    cases = ((128, 40), (800, 600), (3000, 2100)) if act == "float32" else ((128, 40), (3000, 2100))
+    for max_seq, prompt_len in cases:
         cfg = Qwen3Config(vocab_size=4096, num_hidden_layers=2)
         w = init_qwen3_weights(cfg, seed=21)
         prompt = syn.randint(22, (prompt_len,), 0, cfg.vocab_size)
