@@ -1104,7 +1104,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                          "traffic": measured_traffic("prefill"),
-                         "kernel": "flash_fwd_persistent_kernel<true>", "kernel_ms": round(p["dev_ms"], 4)},
+                         "kernel": "flash_fwd_persistent_kernel<true, 128, 1, false>", "kernel_ms": round(p["dev_ms"], 4)},
         })
     if "decode" in res:
         d = res["decode"]
