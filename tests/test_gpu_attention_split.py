@@ -73,6 +73,8 @@ def _run(q, k, v, causal, scale):
     (1, 8, 8, 300, 100, True),     # Lq > Lk: rows past Lk see every key
     (1, 4, 2, 77, 77, False),
     (2, 8, 8, 33, 1000, False),    # many stages, one query block
+    (1, 16, 1, 130, 130, True),    # GQA 16 (one kv head for all query heads)
+    (1, 12, 4, 200, 200, True),    # GQA 3
 ])
 def test_split_attention_matches_emulation_and_fp32(hip, B, Hq, Hkv, Lq, Lk, causal):
     D = 128
