@@ -73,6 +73,11 @@ constexpr int kGemmSplitF32WTM = 1, kGemmSplitF32WTN = 2;
 constexpr int kGemmSmallWTM = 1, kGemmSmallWTN = 1;
 constexpr int kGemmRectKS = 64;         // k-step of 128 x 64 and 64 x 128 tiles
 constexpr int kMaxSplits = 8;
+// Waves per workgroup of the fp32-activation launches on 64 x 128 tiles: 2 x 4 waves of 32 x 32, two
+// per SIMD, so that one wave's hi / lo split of A and LDS traffic overlaps the other's MFMAs (C5
+// prefill, float32: GEMMs 77.3-78.0 -> 75.2-75.8 us per layer, the whole prefill 2.87-2.90 ->
+// 2.75-2.77 ms; 4 = 2 x 2 waves of 32 x 64).  Each output's k-steps and their order are unchanged.
+constexpr int kGemmF32Waves = 8;
 constexpr int g_tile(int wt) { return 64 * wt; }
 
 // PF: k-steps of prefetch in flight (register ring of PF stages; the loop is unrolled by PF so the
@@ -127,21 +132,25 @@ constexpr int gemm_min_blocks() {
 }
 
 template <typename TO, int WTM, int WTN, int KS, bool SPLIT, int PF = 1, bool SWIGLU = false, bool QKNR = false,
-          typename TA = uint16_t>
-__global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) void gemm_bf16_nt_kernel(
+          typename TA = uint16_t, int NW = 4>
+__global__ __launch_bounds__(NW * 64, (gemm_min_blocks<TA, WTM, WTN, KS>())) void gemm_bf16_nt_kernel(
     const TA* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb, TO* C, int64_t ldc,
     const TO* cin, int64_t ldcin, const TO* __restrict__ bias, int M, int N, int K, float alpha, float beta,
     int tiles_n, int splits, int kchunk, float* __restrict__ part, QknrArgs qa) {
   constexpr bool AF = std::is_same<TA, float>::value;
   constexpr int GM = g_tile(WTM), GN = g_tile(WTN);
+  // NW waves in a 2 x NW/2 layout, each (32 WTM) x (32 AN): AN = WTN with four waves, WTN / 2 with
+  // eight (two per SIMD).
+  constexpr int NT = NW * 64, NWN = NW / 2, AN = 4 * WTN / NW;
+  static_assert(NW == 4 || (NW == 8 && WTN % 2 == 0), "four waves, or eight on tiles of even WTN");
   constexpr int STR = KS + 8;  // LDS row stride (elements): 16-byte aligned, breaks bank aliasing
   constexpr int APL = AF ? 2 : 1;                  // A planes in LDS: bf16, or hi and lo
   constexpr int ATILE = GM * STR, BTILE = GN * STR, ASTG = APL * ATILE;
   constexpr int AE = 16 / (int)sizeof(TA);         // A elements per 16-byte chunk
   constexpr int CPR = KS / 8;                      // 16-byte chunks per B row per k-step
   constexpr int CPRA = KS / AE;                    // 16-byte chunks per A row per k-step
-  constexpr int CPTA = GM * CPRA / G_THREADS;      // chunks per thread per A tile
-  constexpr int CPTB = GN * CPR / G_THREADS;       // chunks per thread per B tile
+  constexpr int CPTA = GM * CPRA / NT;             // chunks per thread per A tile
+  constexpr int CPTB = GN * CPR / NT;              // chunks per thread per B tile
   constexpr int CPTM = CPTA > CPTB ? CPTA : CPTB;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (ASTG + BTILE)];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
   const int tiles_m = (M + GM - 1) / GM;
   const int tm = PF > 1 ? tile % tiles_m : tile / tiles_n, tn = PF > 1 ? tile / tiles_m : tile % tiles_n;
   const int m0 = tm * GM, n0 = tn * GN;
-  const int wm = (wave >> 1) * 32 * WTM, wn = (wave & 1) * 32 * WTN;
+  const int wm = (wave / NWN) * 32 * WTM, wn = (wave % NWN) * 32 * AN;
   const int kbeg = split * kchunk, kend = min(K, kbeg + kchunk);
 
   // Byte ranges of this tile's rows; a row past the matrix or a column past the range reads zero.
@@ -170,7 +179,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
   auto load_tile = [&](int stg, int kt) {
 #pragma unroll
     for (int i = 0; i < CPTM; ++i) {
-      const int id = tid + G_THREADS * i;
+      const int id = tid + NT * i;
       if (i < CPTA) {
         const int row = id / CPRA, kc = kt + AE * (id % CPRA);
         const uint32_t ao =
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
     uint16_t* bs = as + ASTG;
 #pragma unroll
     for (int i = 0; i < CPTM; ++i) {
-      const int id = tid + G_THREADS * i;
+      const int id = tid + NT * i;
       if (i < CPTA) {
         const int row = id / CPRA, kc = AE * (id % CPRA);
         const uint4 v = ast[stg][i < CPTA ? i : 0];
@@ -214,9 +223,9 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
     }
   };
 
-  f32x16 acc[WTN][WTM];  // [n tile][m tile]
+  f32x16 acc[AN][WTM];  // [n tile][m tile]
 #pragma unroll
-  for (int a = 0; a < WTN; ++a)
+  for (int a = 0; a < AN; ++a)
 #pragma unroll
     for (int b = 0; b < WTM; ++b)
 #pragma unroll
@@ -233,7 +242,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
     const uint16_t* bs = as + ASTG;
 #pragma unroll
     for (int kc = 0; kc < KS / 16; ++kc) {
-      bf16x8 av[APL][WTM], bv[WTN];
+      bf16x8 av[APL][WTM], bv[AN];
 #pragma unroll
       for (int pl = 0; pl < APL; ++pl)
 #pragma unroll
@@ -241,10 +250,10 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
           av[pl][i] = as_bf16x8(
               *reinterpret_cast<const uint4*>(as + pl * ATILE + (wm + 32 * i + r) * STR + 16 * kc + 8 * g));
 #pragma unroll
-      for (int i = 0; i < WTN; ++i)
+      for (int i = 0; i < AN; ++i)
         bv[i] = as_bf16x8(*reinterpret_cast<const uint4*>(bs + (wn + 32 * i + r) * STR + 16 * kc + 8 * g));
 #pragma unroll
-      for (int a = 0; a < WTN; ++a)
+      for (int a = 0; a < AN; ++a)
 #pragma unroll
         for (int b = 0; b < WTM; ++b)
 #pragma unroll
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
       const int m = m0 + wm + 32 * b + r;
       if (m >= M) continue;
 #pragma unroll
-      for (int a = 0; a < WTN; ++a)
+      for (int a = 0; a < AN; ++a)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
     // plain GEMM would store it: rounded to bf16, or fp32 with fp32 activations.
     TA* tile = reinterpret_cast<TA*>(smem);
 #pragma unroll
-    for (int a = 0; a < WTN; ++a)
+    for (int a = 0; a < AN; ++a)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         TA* dst = tile + (wm + r) * TSTR + wn + 32 * a + 8 * q + 4 * g;
@@ -347,8 +356,8 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
     }
     const bool cache_mode = qa.kv_cache_len > 0;
 #pragma unroll
-    for (int st = 0; st < GM / 32; ++st) {
-      const int row = wave * (GM / 4) + st * 8 + rs;
+    for (int st = 0; st < GM / (8 * NW); ++st) {
+      const int row = wave * (GM / NW) + st * 8 + rs;
       const int m = m0 + row;
       const bool live = m < M;
       float a8[8], c8[8];
@@ -400,7 +409,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
       const int m = m0 + wm + 32 * b + r;
       if (m >= M) continue;
 #pragma unroll
-      for (int a = 0; a < WTN; ++a)
+      for (int a = 0; a < AN; ++a)
 #pragma unroll
         for (int q = 0; q < 4; q += 2) {
           const int f = (n0 + wn + 32 * a) / 2 + 4 * q + 4 * g;
@@ -423,7 +432,7 @@ __global__ __launch_bounds__(G_THREADS, (gemm_min_blocks<TA, WTM, WTN, KS>())) v
     const int m = m0 + wm + 32 * b + r;
     if (m >= M) continue;
 #pragma unroll
-    for (int a = 0; a < WTN; ++a)
+    for (int a = 0; a < AN; ++a)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn + 32 * a + 8 * q + 4 * g;
@@ -763,12 +772,13 @@ void go_tiles(int nblk, int splits, const TA* A, int64_t lda, const uint16_t* B,
               int tiles_n, int kchunk, float* part) {
   // fp32 activations hold twice the A chunks per stage: two stages in flight keep the ring in registers
   constexpr int PF = std::is_same<TA, float>::value ? 2 : kGemmPrefetch;
+  constexpr int NW = std::is_same<TA, float>::value && WTN == 2 ? kGemmF32Waves : 4;
   if (!SWIGLU && splits > 1)
-    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch, false, false, TA><<<nblk, G_THREADS, 0,
-                                                                                        stream()>>>(
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch, false, false, TA, NW><<<nblk, NW * 64, 0,
+                                                                                            stream()>>>(
         A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, splits, kchunk, part, QknrArgs{});
   else
-    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU, false, TA><<<nblk, G_THREADS, 0, stream()>>>(
+    gemm_bf16_nt_kernel<TO, WTM, WTN, KS, false, PF, SWIGLU, false, TA, NW><<<nblk, NW * 64, 0, stream()>>>(
         A, lda, B, ldb, C, ldc, CI, ldcin, BI, M, N, K, alpha, beta, tiles_n, 1, K, nullptr, QknrArgs{});
 }
 
@@ -893,7 +903,8 @@ int launch_gemm_qk_norm_rope(const TA* X, int64_t ldx, const uint16_t* W, int64_
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_qk_norm_rope: grid too large");
   constexpr int PF = std::is_same<TA, float>::value ? 2 : kGemmPrefetch;
-  gemm_bf16_nt_kernel<TA, 1, 2, kGemmRectKS, false, PF, false, true, TA><<<(int)tiles, G_THREADS, 0, stream()>>>(
+  constexpr int NW = std::is_same<TA, float>::value ? kGemmF32Waves : 4;
+  gemm_bf16_nt_kernel<TA, 1, 2, kGemmRectKS, false, PF, false, true, TA, NW><<<(int)tiles, NW * 64, 0, stream()>>>(
       X, ldx, W, ldw, nullptr, 0, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr, qa);
   KH_CHECK_LAUNCH();
   return KH_OK;
