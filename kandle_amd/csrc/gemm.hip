@@ -41,7 +41,8 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 
 // =============================================================================================
 // MFMA tile kernel.  Workgroup tile (64 WTM) x (64 WTN), k-step KS, 4 waves in a 2 x 2 layout, each
-// wave (32 WTM) x (32 WTN) = WTM x WTN tiles of 32 x 32: 128 x 128 for large problems, smaller
+// wave (32 WTM) x (32 WTN) = WTM x WTN tiles of 32 x 32 (64 x 128 tiles: 8 waves in 2 x 4, each
+// 32 x 32; gemm_waves): 128 x 128 for large problems, smaller
 // tiles when 128-tiles would leave CUs idle.  The tile shape does not change any result: every
 // output element is summed over k in the same 16-wide MFMA steps, in the same order, whatever the
 // tile that holds it.  The product is formed as C^T = B A^T
@@ -54,7 +55,6 @@ __device__ __forceinline__ void store4(TO* C, int64_t off, const float (&v)[4], 
 // gemm_splitk_reduce_kernel -- or a consumer such as kh_add_rms_norm -- then adds the S partials
 // in split order (deterministic whichever workgroup finished last) and applies the epilogue.
 // =============================================================================================
-constexpr int G_THREADS = 256;
 constexpr int kGemmPrefetch = 3;        // k-steps of global loads in flight per workgroup
 // Split launches (short k ranges, 128 x 64 tiles): 2 steps in flight (C5 prefill, two runs: o_proj
 // 14.56 -> 14.12 us, down 15.25 -> 14.93 us; the unsplit qkv product is 0.5 us slower at 2).
@@ -73,11 +73,14 @@ constexpr int kGemmSplitF32WTM = 1, kGemmSplitF32WTN = 2;
 constexpr int kGemmSmallWTM = 1, kGemmSmallWTN = 1;
 constexpr int kGemmRectKS = 64;         // k-step of 128 x 64 and 64 x 128 tiles
 constexpr int kMaxSplits = 8;
-// Waves per workgroup of the fp32-activation launches on 64 x 128 tiles: 2 x 4 waves of 32 x 32, two
-// per SIMD, so that one wave's hi / lo split of A and LDS traffic overlaps the other's MFMAs (C5
-// prefill, float32: GEMMs 77.3-78.0 -> 75.2-75.8 us per layer, the whole prefill 2.87-2.90 ->
-// 2.75-2.77 ms; 4 = 2 x 2 waves of 32 x 64).  Each output's k-steps and their order are unchanged.
-constexpr int kGemmF32Waves = 8;
+// Waves per workgroup on 64 x 128 tiles: 2 x 4 waves of 32 x 32, two per SIMD, so that one wave's
+// LDS traffic (and with fp32 activations its hi / lo split of A) overlaps the other's MFMAs.  C5
+// prefill, alternating builds on one box: float32 activations 2.87-2.90 -> 2.75-2.77 ms (GEMMs
+// 77.3-78.0 -> 75.2-75.8 us per layer), bf16 2.363-2.367 -> 2.316-2.332 ms.  Other tiles keep four
+// waves of (32 WTM) x (32 WTN).  Each output's k-steps and their order are unchanged.
+constexpr int kGemmWaves64x128 = 8;
+template <int WTM, int WTN>
+constexpr int gemm_waves() { return WTM == 1 && WTN == 2 ? kGemmWaves64x128 : 4; }
 constexpr int g_tile(int wt) { return 64 * wt; }
 
 // PF: k-steps of prefetch in flight (register ring of PF stages; the loop is unrolled by PF so the
@@ -772,7 +775,7 @@ void go_tiles(int nblk, int splits, const TA* A, int64_t lda, const uint16_t* B,
               int tiles_n, int kchunk, float* part) {
   // fp32 activations hold twice the A chunks per stage: two stages in flight keep the ring in registers
   constexpr int PF = std::is_same<TA, float>::value ? 2 : kGemmPrefetch;
-  constexpr int NW = std::is_same<TA, float>::value && WTN == 2 ? kGemmF32Waves : 4;
+  constexpr int NW = gemm_waves<WTM, WTN>();
   if (!SWIGLU && splits > 1)
     gemm_bf16_nt_kernel<TO, WTM, WTN, KS, true, kGemmSplitPrefetch, false, false, TA, NW><<<nblk, NW * 64, 0,
                                                                                             stream()>>>(
@@ -903,7 +906,7 @@ int launch_gemm_qk_norm_rope(const TA* X, int64_t ldx, const uint16_t* W, int64_
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   KH_REQUIRE(tiles <= INT32_MAX, "kh_gemm_qk_norm_rope: grid too large");
   constexpr int PF = std::is_same<TA, float>::value ? 2 : kGemmPrefetch;
-  constexpr int NW = std::is_same<TA, float>::value ? kGemmF32Waves : 4;
+  constexpr int NW = gemm_waves<1, 2>();
   gemm_bf16_nt_kernel<TA, 1, 2, kGemmRectKS, false, PF, false, true, TA, NW><<<(int)tiles, NW * 64, 0, stream()>>>(
       X, ldx, W, ldw, nullptr, 0, nullptr, 0, nullptr, M, N, K, 1.f, 0.f, tiles_n, 1, K, nullptr, qa);
   KH_CHECK_LAUNCH();
