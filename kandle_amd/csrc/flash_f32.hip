@@ -5,8 +5,8 @@
 // builder.ts:138-329): S = (Q K^T) * scale, causal masks key j > query i (top-left aligned), GQA
 // query head h reads kv head h / (hq / hkv), O = softmax(S) V.
 //
-// One workgroup per (batch, query head, block of 32 queries), NW waves (4, or 8 for grids with
-// fewer than two workgroups per CU).  Wave w takes the block's 32-key tiles w, w + NW, ... (with the
+// One workgroup per (batch, query head, block of 32 queries), NW waves (8 at head_dim 128; at 64, 8
+// for grids with fewer than two workgroups per CU; else 4).  Wave w takes the block's 32-key tiles w, w + NW, ... (with the
 // causal mask only tiles up to the block's last query), so a short prompt still spreads each block
 // over every SIMD of its CU.  Per tile the wave
 // forms S^T = K Q^T in D/2 MFMA steps (step s pairs head-dim element s on lanes 0-31 with s + D/2
@@ -455,13 +455,15 @@ void launch_f32_dw(const float* q, const float* k, const float* v, float* o, int
     flash_f32_kernel<D, false, NW><<<grid, NW * 64, 0, stream()>>>(q, k, v, o, hq, hkv, lq, lk, st, c, nqb);
 }
 
-// Eight-wave workgroups (two waves per SIMD, the tiles of a block over twice the waves) when the
-// grid leaves CUs without a second workgroup, for head_dim 64 and 128.
+// Eight-wave workgroups (two waves per SIMD, the tiles of a block over twice the waves): always at
+// head_dim 128 (with 16-byte V loads, grids of 512 and 2048 workgroups too: B=2, 16/8 heads, S=512
+// 53.3 -> 50.6 us; B=4, S=1024 347.5 -> 326.3 us), and at 64 when the grid leaves CUs without a
+// second workgroup.
 template <int D>
 void launch_f32_d(const float* q, const float* k, const float* v, float* o, int grid, int hq, int hkv, int lq, int lk,
                   const AttnStrides& st, float c, int nqb, bool causal) {
   if constexpr (D == 64 || D == 128) {
-    if (grid < 2 * cu_count()) {
+    if (D == 128 || grid < 2 * cu_count()) {
       launch_f32_dw<D, 8>(q, k, v, o, grid, hq, hkv, lq, lk, st, c, nqb, causal);
       return;
     }

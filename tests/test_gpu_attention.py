@@ -141,16 +141,17 @@ def test_generic_kernel_fp32_odd_head_dim(hip):
     (1, 4, 2, 1, 64, 128, True),       # one causal query row sees key 0 only
     (1, 2, 2, 1000, 1000, 128, True),  # eight key tiles per wave in the last blocks
     (1, 16, 16, 31, 257, 64, False),   # ragged key tile
-    (2, 16, 8, 512, 512, 128, True),   # 512 workgroups: the four-wave 32-query variant
+    (2, 16, 8, 512, 512, 128, True),   # 512 workgroups of 32 queries
     (1, 16, 8, 512, 512, 128, True),   # 256 workgroups: eight waves, 32-query blocks
     (1, 8, 8, 400, 400, 128, True),    # 104 blocks of 32 queries: 16-query blocks, a partial last one
     (1, 8, 4, 300, 120, 128, True),    # 16-query blocks, Lq > Lk (rows past Lk see every key)
     (2, 6, 2, 33, 500, 128, True),     # 16-query blocks, Lq < Lk, GQA 3, a partial last block
 ])
 def test_flash_f32_mfma_matches_oracle(hip, B, Hq, Hkv, Lq, Lk, D, causal):
-    """fp32 flash kernel (fp32 MFMA; four or, on small grids, eight waves splitting a query block's
-    key tiles, merged in LDS).  At D = 128 a grid of fewer 32-query blocks than CUs takes 16-query
-    blocks with four waves (C1 and the D = 128 cases here but the 512- and 256-workgroup ones)."""
+    """fp32 flash kernel (fp32 MFMA; waves splitting a query block's key tiles, merged in LDS: eight
+    at D = 128, four or, on small grids, eight at the other head dims).  At D = 128 a grid of fewer
+    32-query blocks than CUs takes 16-query blocks with four waves (C1 and the D = 128 cases here
+    but the 512- and 256-workgroup ones)."""
     q, qh = seeded(54, (B, Hq, Lq, D))
     k, kh = seeded(55, (B, Hkv, Lk, D))
     v, vh = seeded(56, (B, Hkv, Lk, D))
