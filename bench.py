@@ -391,12 +391,14 @@ def prep_model(cfg, w, new_tokens=128, prompt_len=512, use_graph=True, ts_host=F
 def bench_prefill_one_sequence(steps, warmup):
     """Causal bf16 flash prefill of ONE sequence (B = 1, Hq = 16, Hkv = 8, D = 128) at several prompt
     lengths: the shapes whose query blocks are too few to fill the CUs as C3's four sequences do
-    (the key-split persistent form runs S >= 1024)."""
+    (the key-split persistent form runs S >= 1024), and at S = 4096 two head dims the kernel has no
+    tiles for (96, 80: staged as zero-padded 128-column rows; FLOPs counted at the true D)."""
     from kandle_amd import HipTensorHandle, kernels
 
     out = {}
-    Hq, Hkv, D = 16, 8, 128
-    for S in (512, 1024, 2048, 4096):
+    Hq, Hkv = 16, 8
+    # D = 96 and 80: head dims without tiles of their own, run on rows staged with zero padding to 128.
+    for S, D in ((512, 128), (1024, 128), (2048, 128), (4096, 128), (4096, 96), (4096, 80)):
         q = bf16_tensor(311, (1, Hq, S, D))
         k = bf16_tensor(312, (1, Hkv, S, D))
         v = bf16_tensor(313, (1, Hkv, S, D))
@@ -405,7 +407,8 @@ def bench_prefill_one_sequence(steps, warmup):
         wall_ms, dev_ms = time_calls(fn, steps, warmup)
         flops = 4.0 * Hq * S * S * D / 2.0
         tf = flops / (dev_ms * 1e-3) / 1e12
-        out[f"S{S}"] = {"ms": round(dev_ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        key = f"S{S}" if D == 128 else f"S{S}_D{D}_staged"
+        out[key] = {"ms": round(dev_ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
         for t in (q, k, v):
             t.dispose()
         o.dispose()

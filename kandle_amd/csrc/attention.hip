@@ -109,6 +109,21 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const T* __restrict__ sr
   for (int j = threadIdx.x & 63; j < ldm; j += 64) d[j] = j < lk ? s[(int64_t)j * sk] : T(0);
 }
 
+// The inverse copy for an attention output staged in rows of ld elements:
+// dst[b' sb + h' sh + q' sq + j] = src[((b' nh + h') nq + q') ld + j] for j < d (unit column stride).
+template <typename T>
+__global__ __launch_bounds__(256) void rows_unpack_kernel(const T* __restrict__ src, T* __restrict__ dst, int nh,
+                                                          int nq, int d, int ld, int64_t sb, int64_t sh, int64_t sq,
+                                                          int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int q = (int)(row % nq), h = (int)((row / nq) % nh);
+  const int64_t b = row / ((int64_t)nq * nh);
+  T* o = dst + b * sb + h * sh + (int64_t)q * sq;
+  const T* s = src + row * ld;
+  for (int j = threadIdx.x & 63; j < d; j += 64) o[j] = s[j];
+}
+
 // =============================================================================================
 // Split-K decode: one query token per sequence, per-sequence KV length.
 //
@@ -844,6 +859,71 @@ int attention_init(int device) {
 
 extern "C" {
 
+// bf16 calls the MFMA prefill kernel has no tiles or layout for -- head dims below 128 other than
+// 64, or views it cannot read in place (unaligned pointers or strides) -- run it on staged copies:
+// Q, K and V are copied into contiguous rows of dp = 64 or 128 elements whose columns past d are
+// zero, so each q.k sum is the sum over the d columns plus exact zeros, and the output's columns
+// past d (P times zero V columns) are dropped when the rows are copied into the caller's o.  The
+// scale stays the caller's.  Staging costs one read and one write of Q, K, V and O.
+namespace {
+struct StagedAttn {
+  void* block = nullptr;
+  uint16_t *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+  AttnStrides st{};
+  int dp = 0;
+};
+
+// Returns KH_OK with p.block set when staged, KH_OK with p.block null when the staged shapes are
+// outside the kernel's limits too (the caller takes the generic kernel), or an error.
+int stage_attn_bf16(StagedAttn& p, const void* q, const void* k, const void* v, int batch, int hq, int hkv,
+                    int64_t lq, int64_t lk, int d, const AttnStrides& st) {
+  p = StagedAttn{};
+  if (d > 128) return KH_OK;
+  const int dp = d <= 64 ? 64 : 128;
+  const int64_t rq = (int64_t)batch * hq * lq, rk = (int64_t)batch * hkv * lk;
+  AttnStrides ps{};
+  ps.qb = ps.ob = hq * lq * dp;
+  ps.qh = ps.oh = lq * dp;
+  ps.qs = ps.os = dp;
+  ps.kb = ps.vb = hkv * lk * dp;
+  ps.kh = ps.vh = lk * dp;
+  ps.ks = ps.vs = dp;
+  const void* a16 = reinterpret_cast<const void*>(uintptr_t(256));  // the block's parts are 256-byte aligned
+  if (!flash_prefill_supported(a16, a16, a16, a16, hq, hkv, lq, lk, dp, ps)) return KH_OK;
+  if ((rq + 3) / 4 > INT32_MAX || (rk + 3) / 4 > INT32_MAX) return KH_OK;
+  const size_t bq = (size_t)rq * dp * 2, bk = (size_t)rk * dp * 2;  // multiples of 128 bytes
+  const size_t align = 256, oq = (bq + align - 1) / align * align, ok = (bk + align - 1) / align * align;
+  p.block = scratch_alloc(2 * oq + 2 * ok);
+  if (!p.block) return KH_ERR_OOM;
+  char* base = static_cast<char*>(p.block);
+  p.q = reinterpret_cast<uint16_t*>(base);
+  p.k = reinterpret_cast<uint16_t*>(base + oq);
+  p.v = reinterpret_cast<uint16_t*>(base + oq + ok);
+  p.o = reinterpret_cast<uint16_t*>(base + oq + 2 * ok);
+  p.st = ps;
+  p.dp = dp;
+  mask_pack_kernel<uint16_t><<<(int)((rq + 3) / 4), 256, 0, stream()>>>(
+      static_cast<const uint16_t*>(q), p.q, hq, (int)lq, d, dp, st.qb, st.qh, st.qs, 1, rq);
+  mask_pack_kernel<uint16_t><<<(int)((rk + 3) / 4), 256, 0, stream()>>>(
+      static_cast<const uint16_t*>(k), p.k, hkv, (int)lk, d, dp, st.kb, st.kh, st.ks, 1, rk);
+  mask_pack_kernel<uint16_t><<<(int)((rk + 3) / 4), 256, 0, stream()>>>(
+      static_cast<const uint16_t*>(v), p.v, hkv, (int)lk, d, dp, st.vb, st.vh, st.vs, 1, rk);
+  return KH_OK;
+}
+
+// Copies the staged output into the caller's o (after a successful launch) and releases the block.
+int unstage_attn_bf16(StagedAttn& p, int rc, void* o, int batch, int hq, int64_t lq, int d, const AttnStrides& st) {
+  if (rc == KH_OK) {
+    const int64_t rq = (int64_t)batch * hq * lq;
+    rows_unpack_kernel<uint16_t><<<(int)((rq + 3) / 4), 256, 0, stream()>>>(p.o, static_cast<uint16_t*>(o), hq,
+                                                                            (int)lq, d, p.dp, st.ob, st.oh, st.os, rq);
+  }
+  scratch_free(p.block);  // stream-ordered: reused only by later work on the same stream
+  p.block = nullptr;
+  return rc;
+}
+}  // namespace
+
 int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int batch, int hq, int hkv, int64_t lq,
                        int64_t lk, int d, const int64_t* strides, float scale, int causal, int dtype) {
   KH_REQUIRE_INIT();
@@ -867,8 +947,18 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
   }
   // The MFMA kernel's softmax takes the raw q.k maximum as its reference, which is only the largest
   // scaled score for scale > 0; other scales take the generic kernel.
-  if (dtype == KH_BF16 && lq > 1 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
-    return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
+  if (dtype == KH_BF16 && lq > 1 && scale > 0.f) {
+    if (flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
+      return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
+    StagedAttn p;
+    const int rs = stage_attn_bf16(p, q, k, v, batch, hq, hkv, lq, lk, d, st);
+    if (rs != KH_OK) return rs;
+    if (p.block) {
+      const int rc = launch_flash_prefill_bf16(p.q, p.k, p.v, p.o, batch, hq, hkv, (int)lq, (int)lk, p.dp, p.st,
+                                               scale, causal != 0);
+      return unstage_attn_bf16(p, rc, o, batch, hq, lq, d, st);
+    }
+  }
   if (dtype == KH_F32 && flash_f32_supported(q, k, v, o, lq, lk, d, st))
     return launch_flash_f32(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
   return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal, nullptr, 0, MaskArgs{},
@@ -918,7 +1008,11 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
   const double fl = (double)-1e38f / (double)scale;
   ma.floor_raw = (scale > 0.f && fl >= -(double)FLT_MAX) ? (float)fl : -INFINITY;
 
-  if (!(dtype == KH_BF16 && scale > 0.f && flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st)))
+  if (!(dtype == KH_BF16 && scale > 0.f))
+    return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
+  // Q, K and V the kernel cannot read in place are staged (stage_attn_bf16) once the mask is ready.
+  const bool direct_qkv = flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st);
+  if (!direct_qkv && d > 128)
     return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
 
   // MFMA path: the mask must have a unit key stride and 16-byte aligned 8-key runs; otherwise it is
@@ -954,12 +1048,27 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
     mp = packed;
   }
   int rc = KH_OK;
-  if (extent >= (int64_t(1) << 31)) {
-    rc = launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
+  StagedAttn sp;
+  if (extent < (int64_t(1) << 31) && !direct_qkv) rc = stage_attn_bf16(sp, q, k, v, batch, hq, hkv, lq, lk, d, st);
+  if (rc != KH_OK) {
+  } else if (extent >= (int64_t(1) << 31) || (!direct_qkv && !sp.block)) {
+    // The generic kernel reads the caller's mask (its strides, not the packed copy's).
+    MaskArgs mg = ma;
+    mg.sb = mask_strides[0];
+    mg.sh = mask_strides[1];
+    mg.sq = mask_strides[2];
+    mg.sk = mask_strides[3];
+    rc = launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, mg, dtype);
   } else {
     ma.bytes = (uint32_t)extent;
-    rc = launch_flash_prefill_bf16_masked(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, mp, ma,
-                                          mask_dtype);
+    if (sp.block)
+      rc = unstage_attn_bf16(sp,
+                             launch_flash_prefill_bf16_masked(sp.q, sp.k, sp.v, sp.o, batch, hq, hkv, (int)lq, (int)lk,
+                                                              sp.dp, sp.st, scale, mp, ma, mask_dtype),
+                             o, batch, hq, lq, d, st);
+    else
+      rc = launch_flash_prefill_bf16_masked(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, mp, ma,
+                                            mask_dtype);
   }
   if (packed) scratch_free(packed);  // stream-ordered: reused only by later work on the same stream
   return rc;

@@ -124,6 +124,47 @@ def test_flash_bf16_strided_kv_cache_view(hip):
     assert np.max(np.abs(out - ref)) < BF16_ATOL
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 8, 4, 300, 96), (2, 4, 2, 130, 80), (1, 8, 8, 257, 32),
+                                          (1, 16, 8, 512, 112), (1, 4, 1, 77, 48), (1, 8, 2, 1000, 72),
+                                          (2, 16, 8, 640, 120)])
+def test_flash_bf16_staged_head_dims(hip, B, Hq, Hkv, S, D, causal):
+    """Head dims below 128 other than 64 run the MFMA kernel on copies of Q, K and V whose rows are
+    zero-padded to 64 or 128 columns (the zero columns add exact zeros to every q.k sum; the output's
+    extra columns are dropped). The scale stays 1/sqrt(D)."""
+    q, qh = seeded(61, (B, Hq, S, D), "bfloat16")
+    k, kh = seeded(62, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(63, (B, Hkv, S, D), "bfloat16")
+    out = _sdpa_gpu(q, k, v, causal)
+    ref = oracle.sdpa(qh, kh, vh, causal=causal)
+    assert out.shape == ref.shape
+    err = float(np.max(np.abs(out - ref)))
+    assert err < BF16_ATOL, (D, err)
+
+
+@pytest.mark.parametrize("D,off", [(128, 1), (128, 4), (64, 3)])
+def test_flash_bf16_unaligned_views_staged(hip, D, off):
+    """Views the MFMA kernel cannot read in place (the head-dim slice [off:off + D] of wider rows: the
+    base pointer is not 16-byte aligned) are staged into contiguous rows."""
+    W = D + 8
+    qw, qwh = seeded(64, (1, 8, 200, W), "bfloat16")
+    kw, kwh = seeded(65, (1, 4, 200, W), "bfloat16")
+    vw, vwh = seeded(66, (1, 4, 200, W), "bfloat16")
+    q, k, v = (F.narrow(t, 3, off, D) for t in (qw, kw, vw))
+    out = _sdpa_gpu(q, k, v, True)
+    ref = oracle.sdpa(qwh[..., off:off + D], kwh[..., off:off + D], vwh[..., off:off + D], causal=True)
+    assert np.max(np.abs(out - ref)) < BF16_ATOL
+
+
+def test_flash_bf16_head_dim_256_generic(hip):
+    """Head dim 256 (above the MFMA kernel's 128) stays on the generic kernel, same tolerance."""
+    q, qh = seeded(67, (1, 4, 100, 256), "bfloat16")
+    k, kh = seeded(68, (1, 2, 100, 256), "bfloat16")
+    v, vh = seeded(69, (1, 2, 100, 256), "bfloat16")
+    out = _sdpa_gpu(q, k, v, True)
+    assert np.max(np.abs(out - oracle.sdpa(qh, kh, vh, causal=True))) < BF16_ATOL
+
+
 def test_generic_kernel_fp32_odd_head_dim(hip):
     """Generic path: fp32 with head_dim 48 (not a multiple of 32), GQA 6/3, ragged lengths, causal."""
     q, qh = seeded(51, (2, 6, 33, 48))

@@ -140,3 +140,16 @@ def test_mask_errors(hip):
         F.scaled_dot_product_attention(q, k, k, attn_mask=dev(np.zeros((3, 8), np.float32)))
     with pytest.raises(TypeError, match="attn_mask dtype"):
         F.scaled_dot_product_attention(q, k, k, attn_mask=dev(np.zeros((8, 8), np.int32), "int32"))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,S,D", [(1, 8, 4, 100, 300, 96), (2, 4, 2, 77, 77, 48), (1, 4, 4, 128, 128, 80)])
+def test_mfma_mask_staged_head_dims(hip, B, Hq, Hkv, L, S, D):
+    """Head dims without MFMA tiles: Q, K and V are staged as rows zero-padded to 64 or 128 columns
+    and the masked MFMA kernel runs on them (the packed-mask path for S = 77 and 300)."""
+    q, qh = seeded(111, (B, Hq, L, D), "bfloat16")
+    k, kh = seeded(112, (B, Hkv, S, D), "bfloat16")
+    v, vh = seeded(113, (B, Hkv, S, D), "bfloat16")
+    m = _mask(114, (B, Hq, L, S))
+    out = _run(q, k, v, dev(m))
+    ref = oracle.sdpa_masked(qh, kh, vh, m)
+    assert np.max(np.abs(out - ref)) < BF16_ATOL
