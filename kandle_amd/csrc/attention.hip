@@ -109,19 +109,49 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const T* __restrict__ sr
   for (int j = threadIdx.x & 63; j < ldm; j += 64) d[j] = j < lk ? s[(int64_t)j * sk] : T(0);
 }
 
-// The inverse copy for an attention output staged in rows of ld elements:
-// dst[b' sb + h' sh + q' sq + j] = src[((b' nh + h') nq + q') ld + j] for j < d (unit column stride).
-template <typename T>
-__global__ __launch_bounds__(256) void rows_unpack_kernel(const T* __restrict__ src, T* __restrict__ dst, int nh,
-                                                          int nq, int d, int ld, int64_t sb, int64_t sh, int64_t sq,
-                                                          int64_t rows) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Attention operands staged in rows of ld elements (ld a multiple of 8, rows 16-byte aligned), from
+// and back to strided views with a unit column stride and any alignment.  Thread i handles 8
+// consecutive elements of one row with one 16-byte access on the staged side and element accesses
+// on the caller's side.
+// rows_pad_kernel: dst[((b' nh + h') nq + q') ld + j] = src[b' sb + h' sh + q' sq + j] for j < d, 0 for
+// d <= j < ld.
+__global__ __launch_bounds__(256) void rows_pad_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                       int nh, int nq, int d, int ld, int64_t sb, int64_t sh,
+                                                       int64_t sq, int64_t rows) {
+  const int per_row = ld >> 3;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = i / per_row;
   if (row >= rows) return;
+  const int j0 = (int)(i - row * per_row) * 8;
   const int q = (int)(row % nq), h = (int)((row / nq) % nh);
   const int64_t b = row / ((int64_t)nq * nh);
-  T* o = dst + b * sb + h * sh + (int64_t)q * sq;
-  const T* s = src + row * ld;
-  for (int j = threadIdx.x & 63; j < d; j += 64) o[j] = s[j];
+  const uint16_t* s = src + b * sb + h * sh + (int64_t)q * sq;
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = j0 + 2 * e < d ? s[j0 + 2 * e] : 0u, hi = j0 + 2 * e + 1 < d ? s[j0 + 2 * e + 1] : 0u;
+    w[e] = lo | (hi << 16);
+  }
+  *reinterpret_cast<uint4*>(dst + row * ld + j0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// rows_unpack_kernel: dst[b' sb + h' sh + q' sq + j] = src[((b' nh + h') nq + q') ld + j] for j < d.
+__global__ __launch_bounds__(256) void rows_unpack_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                          int nh, int nq, int d, int ld, int64_t sb, int64_t sh,
+                                                          int64_t sq, int64_t rows) {
+  const int per_row = (d + 7) >> 3;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = i / per_row;
+  if (row >= rows) return;
+  const int j0 = (int)(i - row * per_row) * 8;
+  const int q = (int)(row % nq), h = (int)((row / nq) % nh);
+  const int64_t b = row / ((int64_t)nq * nh);
+  uint16_t* o = dst + b * sb + h * sh + (int64_t)q * sq;
+  const uint4 v = *reinterpret_cast<const uint4*>(src + row * ld + j0);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (j0 + e < d) o[j0 + e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
 }
 
 // =============================================================================================
@@ -890,7 +920,8 @@ int stage_attn_bf16(StagedAttn& p, const void* q, const void* k, const void* v, 
   ps.ks = ps.vs = dp;
   const void* a16 = reinterpret_cast<const void*>(uintptr_t(256));  // the block's parts are 256-byte aligned
   if (!flash_prefill_supported(a16, a16, a16, a16, hq, hkv, lq, lk, dp, ps)) return KH_OK;
-  if ((rq + 3) / 4 > INT32_MAX || (rk + 3) / 4 > INT32_MAX) return KH_OK;
+  const int per = dp / 8;  // threads per staged row
+  if ((rq * per + 255) / 256 > INT32_MAX || (rk * per + 255) / 256 > INT32_MAX) return KH_OK;
   const size_t bq = (size_t)rq * dp * 2, bk = (size_t)rk * dp * 2;  // multiples of 128 bytes
   const size_t align = 256, oq = (bq + align - 1) / align * align, ok = (bk + align - 1) / align * align;
   p.block = scratch_alloc(2 * oq + 2 * ok);
@@ -902,12 +933,13 @@ int stage_attn_bf16(StagedAttn& p, const void* q, const void* k, const void* v, 
   p.o = reinterpret_cast<uint16_t*>(base + oq + 2 * ok);
   p.st = ps;
   p.dp = dp;
-  mask_pack_kernel<uint16_t><<<(int)((rq + 3) / 4), 256, 0, stream()>>>(
-      static_cast<const uint16_t*>(q), p.q, hq, (int)lq, d, dp, st.qb, st.qh, st.qs, 1, rq);
-  mask_pack_kernel<uint16_t><<<(int)((rk + 3) / 4), 256, 0, stream()>>>(
-      static_cast<const uint16_t*>(k), p.k, hkv, (int)lk, d, dp, st.kb, st.kh, st.ks, 1, rk);
-  mask_pack_kernel<uint16_t><<<(int)((rk + 3) / 4), 256, 0, stream()>>>(
-      static_cast<const uint16_t*>(v), p.v, hkv, (int)lk, d, dp, st.vb, st.vh, st.vs, 1, rk);
+  const int gq = (int)((rq * per + 255) / 256), gk = (int)((rk * per + 255) / 256);
+  rows_pad_kernel<<<gq, 256, 0, stream()>>>(static_cast<const uint16_t*>(q), p.q, hq, (int)lq, d, dp, st.qb, st.qh,
+                                            st.qs, rq);
+  rows_pad_kernel<<<gk, 256, 0, stream()>>>(static_cast<const uint16_t*>(k), p.k, hkv, (int)lk, d, dp, st.kb, st.kh,
+                                            st.ks, rk);
+  rows_pad_kernel<<<gk, 256, 0, stream()>>>(static_cast<const uint16_t*>(v), p.v, hkv, (int)lk, d, dp, st.vb, st.vh,
+                                            st.vs, rk);
   return KH_OK;
 }
 
@@ -915,8 +947,9 @@ int stage_attn_bf16(StagedAttn& p, const void* q, const void* k, const void* v, 
 int unstage_attn_bf16(StagedAttn& p, int rc, void* o, int batch, int hq, int64_t lq, int d, const AttnStrides& st) {
   if (rc == KH_OK) {
     const int64_t rq = (int64_t)batch * hq * lq;
-    rows_unpack_kernel<uint16_t><<<(int)((rq + 3) / 4), 256, 0, stream()>>>(p.o, static_cast<uint16_t*>(o), hq,
-                                                                            (int)lq, d, p.dp, st.ob, st.oh, st.os, rq);
+    const int64_t grid = (rq * ((d + 7) / 8) + 255) / 256;  // <= the staging grid, checked at staging
+    rows_unpack_kernel<<<(int)grid, 256, 0, stream()>>>(p.o, static_cast<uint16_t*>(o), hq, (int)lq, d, p.dp, st.ob,
+                                                        st.oh, st.os, rq);
   }
   scratch_free(p.block);  // stream-ordered: reused only by later work on the same stream
   p.block = nullptr;
