@@ -109,49 +109,56 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const T* __restrict__ sr
   for (int j = threadIdx.x & 63; j < ldm; j += 64) d[j] = j < lk ? s[(int64_t)j * sk] : T(0);
 }
 
-// Attention operands staged in rows of ld elements (ld a multiple of 8, rows 16-byte aligned), from
-// and back to strided views with a unit column stride and any alignment.  Thread i handles 8
-// consecutive elements of one row with one 16-byte access on the staged side and element accesses
-// on the caller's side.
+// Attention operands staged in rows of ld elements (rows of a multiple of 16 bytes, 16-byte aligned),
+// from and back to strided views with a unit column stride and any alignment.  Thread i handles
+// the 16 bytes of V = 16 / sizeof(T) consecutive elements of one row with one 16-byte access on the
+// staged side and element accesses on the caller's side.
 // rows_pad_kernel: dst[((b' nh + h') nq + q') ld + j] = src[b' sb + h' sh + q' sq + j] for j < d, 0 for
 // d <= j < ld.
-__global__ __launch_bounds__(256) void rows_pad_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                                       int nh, int nq, int d, int ld, int64_t sb, int64_t sh,
-                                                       int64_t sq, int64_t rows) {
-  const int per_row = ld >> 3;
+template <typename T>
+__global__ __launch_bounds__(256) void rows_pad_kernel(const T* __restrict__ src, T* __restrict__ dst, int nh, int nq,
+                                                       int d, int ld, int64_t sb, int64_t sh, int64_t sq,
+                                                       int64_t rows) {
+  constexpr int V = 16 / sizeof(T);
+  const int per_row = ld / V;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = i / per_row;
   if (row >= rows) return;
-  const int j0 = (int)(i - row * per_row) * 8;
+  const int j0 = (int)(i - row * per_row) * V;
   const int q = (int)(row % nq), h = (int)((row / nq) % nh);
   const int64_t b = row / ((int64_t)nq * nh);
-  const uint16_t* s = src + b * sb + h * sh + (int64_t)q * sq;
-  uint32_t w[4];
+  const T* s = src + b * sb + h * sh + (int64_t)q * sq;
+  union {
+    T e[V];
+    uint4 u;
+  } w;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t lo = j0 + 2 * e < d ? s[j0 + 2 * e] : 0u, hi = j0 + 2 * e + 1 < d ? s[j0 + 2 * e + 1] : 0u;
-    w[e] = lo | (hi << 16);
-  }
-  *reinterpret_cast<uint4*>(dst + row * ld + j0) = make_uint4(w[0], w[1], w[2], w[3]);
+  for (int e = 0; e < V; ++e) w.e[e] = j0 + e < d ? s[j0 + e] : T(0);
+  *reinterpret_cast<uint4*>(dst + row * ld + j0) = w.u;
 }
 
 // rows_unpack_kernel: dst[b' sb + h' sh + q' sq + j] = src[((b' nh + h') nq + q') ld + j] for j < d.
-__global__ __launch_bounds__(256) void rows_unpack_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                                          int nh, int nq, int d, int ld, int64_t sb, int64_t sh,
-                                                          int64_t sq, int64_t rows) {
-  const int per_row = (d + 7) >> 3;
+template <typename T>
+__global__ __launch_bounds__(256) void rows_unpack_kernel(const T* __restrict__ src, T* __restrict__ dst, int nh,
+                                                          int nq, int d, int ld, int64_t sb, int64_t sh, int64_t sq,
+                                                          int64_t rows) {
+  constexpr int V = 16 / sizeof(T);
+  const int per_row = (d + V - 1) / V;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = i / per_row;
   if (row >= rows) return;
-  const int j0 = (int)(i - row * per_row) * 8;
+  const int j0 = (int)(i - row * per_row) * V;
   const int q = (int)(row % nq), h = (int)((row / nq) % nh);
   const int64_t b = row / ((int64_t)nq * nh);
-  uint16_t* o = dst + b * sb + h * sh + (int64_t)q * sq;
-  const uint4 v = *reinterpret_cast<const uint4*>(src + row * ld + j0);
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  T* o = dst + b * sb + h * sh + (int64_t)q * sq;
+  union {
+    T e[V];
+    uint4 u;
+  } w;
+  w.u = *reinterpret_cast<const uint4*>(src + row * ld + j0);
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if (j0 + e < d) o[j0 + e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+  for (int e = 0; e < V; ++e)
+    if (j0 + e < d) o[j0 + e] = w.e[e];
 }
 
 // =============================================================================================
@@ -889,27 +896,42 @@ int attention_init(int device) {
 
 extern "C" {
 
-// bf16 calls the MFMA prefill kernel has no tiles or layout for -- head dims below 128 other than
-// 64, or views it cannot read in place (unaligned pointers or strides) -- run it on staged copies:
-// Q, K and V are copied into contiguous rows of dp = 64 or 128 elements whose columns past d are
-// zero, so each q.k sum is the sum over the d columns plus exact zeros, and the output's columns
-// past d (P times zero V columns) are dropped when the rows are copied into the caller's o.  The
-// scale stays the caller's.  Staging costs one read and one write of Q, K, V and O.
+// Calls the MFMA attention kernels have no tiles or layout for -- bf16 head dims below 128 other
+// than 64, fp32 head dims other than 32, 64, 96 and 128 up to 128, or views a kernel cannot read in
+// place (unaligned pointers or strides) -- run them on staged copies: Q, K and V are copied into
+// contiguous rows of dp elements (bf16: 64 or 128; fp32: the next multiple of 32) whose columns past
+// d are zero, so each q.k sum is the sum over the d columns plus exact zeros, and the output's
+// columns past d (P times zero V columns) are dropped when the rows are copied into the caller's o.
+// The scale stays the caller's.  Staging costs one read and one write of Q, K, V and O.
 namespace {
 struct StagedAttn {
   void* block = nullptr;
-  uint16_t *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+  void *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
   AttnStrides st{};
   int dp = 0;
 };
 
+void launch_rows_pad(bool f32, const void* src, void* dst, int nh, int64_t n, int d, int dp, int64_t sb, int64_t sh,
+                     int64_t ss, int64_t rows) {
+  const int64_t grid = (rows * (dp * (f32 ? 4 : 2) / 16) + 255) / 256;
+  if (f32)
+    rows_pad_kernel<float><<<(int)grid, 256, 0, stream()>>>(static_cast<const float*>(src), static_cast<float*>(dst),
+                                                            nh, (int)n, d, dp, sb, sh, ss, rows);
+  else
+    rows_pad_kernel<uint16_t><<<(int)grid, 256, 0, stream()>>>(static_cast<const uint16_t*>(src),
+                                                               static_cast<uint16_t*>(dst), nh, (int)n, d, dp, sb, sh,
+                                                               ss, rows);
+}
+
 // Returns KH_OK with p.block set when staged, KH_OK with p.block null when the staged shapes are
 // outside the kernel's limits too (the caller takes the generic kernel), or an error.
-int stage_attn_bf16(StagedAttn& p, const void* q, const void* k, const void* v, int batch, int hq, int hkv,
-                    int64_t lq, int64_t lk, int d, const AttnStrides& st) {
+int stage_attn(StagedAttn& p, int dtype, const void* q, const void* k, const void* v, int batch, int hq, int hkv,
+               int64_t lq, int64_t lk, int d, const AttnStrides& st) {
   p = StagedAttn{};
   if (d > 128) return KH_OK;
-  const int dp = d <= 64 ? 64 : 128;
+  const bool f32 = dtype == KH_F32;
+  const int es = f32 ? 4 : 2;
+  const int dp = f32 ? (d + 31) / 32 * 32 : (d <= 64 ? 64 : 128);
   const int64_t rq = (int64_t)batch * hq * lq, rk = (int64_t)batch * hkv * lk;
   AttnStrides ps{};
   ps.qb = ps.ob = hq * lq * dp;
@@ -919,37 +941,42 @@ int stage_attn_bf16(StagedAttn& p, const void* q, const void* k, const void* v, 
   ps.kh = ps.vh = lk * dp;
   ps.ks = ps.vs = dp;
   const void* a16 = reinterpret_cast<const void*>(uintptr_t(256));  // the block's parts are 256-byte aligned
-  if (!flash_prefill_supported(a16, a16, a16, a16, hq, hkv, lq, lk, dp, ps)) return KH_OK;
-  const int per = dp / 8;  // threads per staged row
+  if (f32 ? !flash_f32_supported(a16, a16, a16, a16, lq, lk, dp, ps)
+          : !flash_prefill_supported(a16, a16, a16, a16, hq, hkv, lq, lk, dp, ps))
+    return KH_OK;
+  const int64_t per = dp * es / 16;  // threads per staged row
   if ((rq * per + 255) / 256 > INT32_MAX || (rk * per + 255) / 256 > INT32_MAX) return KH_OK;
-  const size_t bq = (size_t)rq * dp * 2, bk = (size_t)rk * dp * 2;  // multiples of 128 bytes
+  const size_t bq = (size_t)rq * dp * es, bk = (size_t)rk * dp * es;  // multiples of 64 bytes
   const size_t align = 256, oq = (bq + align - 1) / align * align, ok = (bk + align - 1) / align * align;
   p.block = scratch_alloc(2 * oq + 2 * ok);
   if (!p.block) return KH_ERR_OOM;
   char* base = static_cast<char*>(p.block);
-  p.q = reinterpret_cast<uint16_t*>(base);
-  p.k = reinterpret_cast<uint16_t*>(base + oq);
-  p.v = reinterpret_cast<uint16_t*>(base + oq + ok);
-  p.o = reinterpret_cast<uint16_t*>(base + oq + 2 * ok);
+  p.q = base;
+  p.k = base + oq;
+  p.v = base + oq + ok;
+  p.o = base + oq + 2 * ok;
   p.st = ps;
   p.dp = dp;
-  const int gq = (int)((rq * per + 255) / 256), gk = (int)((rk * per + 255) / 256);
-  rows_pad_kernel<<<gq, 256, 0, stream()>>>(static_cast<const uint16_t*>(q), p.q, hq, (int)lq, d, dp, st.qb, st.qh,
-                                            st.qs, rq);
-  rows_pad_kernel<<<gk, 256, 0, stream()>>>(static_cast<const uint16_t*>(k), p.k, hkv, (int)lk, d, dp, st.kb, st.kh,
-                                            st.ks, rk);
-  rows_pad_kernel<<<gk, 256, 0, stream()>>>(static_cast<const uint16_t*>(v), p.v, hkv, (int)lk, d, dp, st.vb, st.vh,
-                                            st.vs, rk);
+  launch_rows_pad(f32, q, p.q, hq, lq, d, dp, st.qb, st.qh, st.qs, rq);
+  launch_rows_pad(f32, k, p.k, hkv, lk, d, dp, st.kb, st.kh, st.ks, rk);
+  launch_rows_pad(f32, v, p.v, hkv, lk, d, dp, st.vb, st.vh, st.vs, rk);
   return KH_OK;
 }
 
 // Copies the staged output into the caller's o (after a successful launch) and releases the block.
-int unstage_attn_bf16(StagedAttn& p, int rc, void* o, int batch, int hq, int64_t lq, int d, const AttnStrides& st) {
+int unstage_attn(StagedAttn& p, int rc, int dtype, void* o, int batch, int hq, int64_t lq, int d,
+                 const AttnStrides& st) {
   if (rc == KH_OK) {
     const int64_t rq = (int64_t)batch * hq * lq;
-    const int64_t grid = (rq * ((d + 7) / 8) + 255) / 256;  // <= the staging grid, checked at staging
-    rows_unpack_kernel<<<(int)grid, 256, 0, stream()>>>(p.o, static_cast<uint16_t*>(o), hq, (int)lq, d, p.dp, st.ob,
-                                                        st.oh, st.os, rq);
+    const int V = dtype == KH_F32 ? 4 : 8;
+    const int64_t grid = (rq * ((d + V - 1) / V) + 255) / 256;  // <= the staging grid, checked at staging
+    if (dtype == KH_F32)
+      rows_unpack_kernel<float><<<(int)grid, 256, 0, stream()>>>(static_cast<const float*>(p.o), static_cast<float*>(o),
+                                                                 hq, (int)lq, d, p.dp, st.ob, st.oh, st.os, rq);
+    else
+      rows_unpack_kernel<uint16_t><<<(int)grid, 256, 0, stream()>>>(static_cast<const uint16_t*>(p.o),
+                                                                    static_cast<uint16_t*>(o), hq, (int)lq, d, p.dp,
+                                                                    st.ob, st.oh, st.os, rq);
   }
   scratch_free(p.block);  // stream-ordered: reused only by later work on the same stream
   p.block = nullptr;
@@ -984,16 +1011,26 @@ int kh_flash_attention(const void* q, const void* k, const void* v, void* o, int
     if (flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st))
       return launch_flash_prefill_bf16(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
     StagedAttn p;
-    const int rs = stage_attn_bf16(p, q, k, v, batch, hq, hkv, lq, lk, d, st);
+    const int rs = stage_attn(p, KH_BF16, q, k, v, batch, hq, hkv, lq, lk, d, st);
     if (rs != KH_OK) return rs;
     if (p.block) {
       const int rc = launch_flash_prefill_bf16(p.q, p.k, p.v, p.o, batch, hq, hkv, (int)lq, (int)lk, p.dp, p.st,
                                                scale, causal != 0);
-      return unstage_attn_bf16(p, rc, o, batch, hq, lq, d, st);
+      return unstage_attn(p, rc, KH_BF16, o, batch, hq, lq, d, st);
     }
   }
-  if (dtype == KH_F32 && flash_f32_supported(q, k, v, o, lq, lk, d, st))
-    return launch_flash_f32(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
+  if (dtype == KH_F32) {
+    if (flash_f32_supported(q, k, v, o, lq, lk, d, st))
+      return launch_flash_f32(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal != 0);
+    StagedAttn p;
+    const int rs = stage_attn(p, KH_F32, q, k, v, batch, hq, hkv, lq, lk, d, st);
+    if (rs != KH_OK) return rs;
+    if (p.block) {
+      const int rc = launch_flash_f32(p.q, p.k, p.v, p.o, batch, hq, hkv, (int)lq, (int)lk, p.dp, p.st, scale,
+                                      causal != 0);
+      return unstage_attn(p, rc, KH_F32, o, batch, hq, lq, d, st);
+    }
+  }
   return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, causal, nullptr, 0, MaskArgs{},
                         dtype);
 }
@@ -1043,7 +1080,7 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
 
   if (!(dtype == KH_BF16 && scale > 0.f))
     return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
-  // Q, K and V the kernel cannot read in place are staged (stage_attn_bf16) once the mask is ready.
+  // Q, K and V the kernel cannot read in place are staged (stage_attn) once the mask is ready.
   const bool direct_qkv = flash_prefill_supported(q, k, v, o, hq, hkv, lq, lk, d, st);
   if (!direct_qkv && d > 128)
     return launch_generic(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, 0, mask, mask_dtype, ma, dtype);
@@ -1082,7 +1119,7 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
   }
   int rc = KH_OK;
   StagedAttn sp;
-  if (extent < (int64_t(1) << 31) && !direct_qkv) rc = stage_attn_bf16(sp, q, k, v, batch, hq, hkv, lq, lk, d, st);
+  if (extent < (int64_t(1) << 31) && !direct_qkv) rc = stage_attn(sp, KH_BF16, q, k, v, batch, hq, hkv, lq, lk, d, st);
   if (rc != KH_OK) {
   } else if (extent >= (int64_t(1) << 31) || (!direct_qkv && !sp.block)) {
     // The generic kernel reads the caller's mask (its strides, not the packed copy's).
@@ -1095,10 +1132,10 @@ int kh_flash_attention_masked(const void* q, const void* k, const void* v, void*
   } else {
     ma.bytes = (uint32_t)extent;
     if (sp.block)
-      rc = unstage_attn_bf16(sp,
-                             launch_flash_prefill_bf16_masked(sp.q, sp.k, sp.v, sp.o, batch, hq, hkv, (int)lq, (int)lk,
-                                                              sp.dp, sp.st, scale, mp, ma, mask_dtype),
-                             o, batch, hq, lq, d, st);
+      rc = unstage_attn(sp,
+                        launch_flash_prefill_bf16_masked(sp.q, sp.k, sp.v, sp.o, batch, hq, hkv, (int)lq, (int)lk,
+                                                         sp.dp, sp.st, scale, mp, ma, mask_dtype),
+                        KH_BF16, o, batch, hq, lq, d, st);
     else
       rc = launch_flash_prefill_bf16_masked(q, k, v, o, batch, hq, hkv, (int)lq, (int)lk, d, st, scale, mp, ma,
                                             mask_dtype);

@@ -166,12 +166,48 @@ def test_flash_bf16_head_dim_256_generic(hip):
 
 
 def test_generic_kernel_fp32_odd_head_dim(hip):
-    """Generic path: fp32 with head_dim 48 (not a multiple of 32), GQA 6/3, ragged lengths, causal."""
+    """fp32 with head_dim 48 (not a multiple of 32; staged to 64 for the fp32 MFMA kernel), GQA 6/3,
+    ragged lengths, causal."""
     q, qh = seeded(51, (2, 6, 33, 48))
     k, kh = seeded(52, (2, 3, 33, 48))
     v, vh = seeded(53, (2, 3, 33, 48))
     out = _sdpa_gpu(q, k, v, True)
     assert max_rel(out, oracle.sdpa(qh, kh, vh, causal=True)) < F32_RTOL
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 8, 4, 300, 80), (2, 4, 2, 130, 112), (1, 8, 8, 77, 8),
+                                          (1, 16, 8, 256, 48), (1, 4, 1, 513, 100)])
+def test_flash_f32_staged_head_dims(hip, B, Hq, Hkv, S, D, causal):
+    """fp32 head dims the fp32 MFMA kernel has no tiles for run it on copies of Q, K and V whose rows
+    are zero-padded to the next multiple of 32 columns; fp32 tolerance normwise and per element."""
+    q, qh = seeded(71, (B, Hq, S, D))
+    k, kh = seeded(72, (B, Hkv, S, D))
+    v, vh = seeded(73, (B, Hkv, S, D))
+    out = _sdpa_gpu(q, k, v, causal)
+    ref = oracle.sdpa(qh, kh, vh, causal=causal)
+    assert max_rel(out, ref) < F32_RTOL
+    assert_close_elem(out, ref, what=f"staged fp32 D={D}")
+
+
+def test_flash_f32_unaligned_view_and_wide_head_dim(hip):
+    """An fp32 view whose base pointer is not 16-byte aligned (head-dim slice [1:65]) is staged; head
+    dim 160 (above 128) runs the generic kernel."""
+    qw, qwh = seeded(74, (1, 8, 150, 72))
+    kw, kwh = seeded(75, (1, 4, 150, 72))
+    vw, vwh = seeded(76, (1, 4, 150, 72))
+    q, k, v = (F.narrow(t, 3, 1, 64) for t in (qw, kw, vw))
+    out = _sdpa_gpu(q, k, v, True)
+    ref = oracle.sdpa(qwh[..., 1:65], kwh[..., 1:65], vwh[..., 1:65], causal=True)
+    assert max_rel(out, ref) < F32_RTOL
+    assert_close_elem(out, ref, what="unaligned fp32 view")
+    q, qh = seeded(77, (1, 4, 90, 160))
+    k, kh = seeded(78, (1, 2, 90, 160))
+    v, vh = seeded(79, (1, 2, 90, 160))
+    out = _sdpa_gpu(q, k, v, False)
+    ref = oracle.sdpa(qh, kh, vh, causal=False)
+    assert max_rel(out, ref) < F32_RTOL
+    assert_close_elem(out, ref, what="fp32 D=160")
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,causal", [
